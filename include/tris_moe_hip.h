@@ -1,0 +1,213 @@
+/*
+ * tris_moe_hip.h — C ABI of the MI355X (gfx950) TriS-MoE grouped expert
+ * dequant-GEMM library (libtris_moe_hip.so).
+ *
+ * Every entry point takes plain device pointers (fp16 data as uint16_t bit
+ * patterns), sizes and a hipStream_t passed as void*; nothing here depends on
+ * torch.  All kernels run on the given stream and no entry point
+ * synchronises the device.  Return value: 0 on success, a negative
+ * TRIS_ERR_* code otherwise; tris_last_error() then describes the failure
+ * (thread-local, valid until the next failing call on the same thread).
+ *
+ * Each declaration names the reference interface it replaces
+ * (paths relative to the TriS-MoE checkout):
+ *   TriSMoE_cuda.cpp  = AutoGPTQ/autogptq_extension/TriSMoE/TriSMoE_cuda.cpp
+ *   kernel.cu         = AutoGPTQ/autogptq_extension/TriSMoE/TriSMoE_cuda_kernel.cu
+ *   qlinear_cuda.py   = AutoGPTQ/auto_gptq/nn_modules/qlinear/qlinear_cuda.py
+ */
+#ifndef TRIS_MOE_HIP_H_
+#define TRIS_MOE_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TRIS_COMPACT3_KERNEL_ABI_VERSION 2
+
+#define TRIS_OK 0
+#define TRIS_ERR_INVALID (-1) /* argument / shape contract violated (the reference's TORCH_CHECK) */
+#define TRIS_ERR_HIP (-2)     /* a HIP runtime call or kernel launch failed */
+
+/*
+ * One projection's stacked grouped compact3 payload, as produced by
+ * build_grouped_precomputed_payload (qlinear_cuda.py:1512-1636); shapes
+ * (E experts, K = rank, N = outfeatures, G groups):
+ *   qweight1               int32 [E, ceil(K/32), N]
+ *   qweight2_sparse        int32 [E, qweight2_sparse_rows, N]   (zero padded)
+ *   qweight2_sparse_prefix int32 [E, ceil(K/32)+1]
+ *   q_gmap_gr_words        int32 [E, gr_words_stride]           (zero padded)
+ *   q_gmap_gr_offsets      int32 [E, nblk+1]
+ *   q_gmap_gr_meta         int32 [E, nblk], nblk = ceil(ceil(K/32)/2)*ceil(N/64)
+ *   c_map                  int32 [E, ceil(K/32)]
+ *   g_idx                  int32 [E, K]
+ *   col_pack3              int64 [E, K]
+ *   row_pack3              int64 [E, N, G]
+ *   output_scale           fp16  [E, N]  (read only if has_output_scale)
+ *   bias                   fp16  [E, N]  (read only if has_bias)
+ * The q_gmap_gr_* pointers may be NULL for the *_predecoded entry points.
+ */
+typedef struct tris_compact3_payload {
+  int32_t num_experts;
+  int32_t rank;
+  int32_t outfeatures;
+  int32_t num_groups;
+  int32_t qweight2_sparse_rows;
+  int32_t gr_words_stride;
+  const int32_t* qweight1;
+  const int32_t* qweight2_sparse;
+  const int32_t* qweight2_sparse_prefix;
+  const int32_t* q_gmap_gr_words;
+  const int32_t* q_gmap_gr_offsets;
+  const int32_t* q_gmap_gr_meta;
+  const int32_t* c_map;
+  const int32_t* g_idx;
+  const int64_t* col_pack3;
+  const int64_t* row_pack3;
+  const uint16_t* output_scale;
+  const uint16_t* bias;
+  int32_t has_output_scale;
+  int32_t has_bias;
+  int32_t use_uniform_k64_groups; /* every 64-column tile lies in one group (kernel.cu:830-853) */
+} tris_compact3_payload;
+
+/* Module attribute TRIS_COMPACT3_KERNEL_ABI_VERSION (TriSMoE_cuda.cpp:1139). Returns 2. */
+int tris_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* tris_last_error(void);
+
+/*
+ * Offline block-GR encoder (host, CPU): replaces QuantLinear._pack_block_gr_gmap_tensor
+ * (qlinear_cuda.py:3793-3859) and tools/rewrite_runtime_min_checkpoint.py:252-347
+ * (pack_block_gr_gmap_tensor with k_min/k_max bounds, force_raw).
+ * packed: host int32 [packed_rows, outfeatures]; words_out capacity must be
+ * >= nblk*128 (words_capacity); offsets_out [nblk+1]; meta_out [nblk].
+ * Returns the number of words written (>= 0) or a negative error code.
+ */
+int64_t tris_gr_encode(const int32_t* packed, int32_t packed_rows, int32_t outfeatures, int32_t k_min,
+                       int32_t k_max, int32_t force_raw, int32_t* words_out, int64_t words_capacity,
+                       int32_t* offsets_out, int32_t* meta_out);
+
+/*
+ * Device route builder: replaces build_grouped_route (TriSMoE_cuda.cpp:741-793;
+ * Python fallback qlinear_cuda.py:1301-1378) without its device->host sync.
+ * selected_experts int64 [num_tokens, top_k].  Outputs (device):
+ *   perm, grouped_token_indices, grouped_slots  int64 [R], R = num_tokens*top_k
+ *     (perm is the stable argsort of the flattened expert ids)
+ *   grouped_expert_ids int32 [R]
+ *   expert_ids         int32 [num_experts]   active experts ascending, then -1
+ *   segment_offsets    int32 [num_experts+1] valid prefix [num_active+1], rest = R
+ *   problem_offsets    int32 [num_experts+1] prefix of ceil(len/m_tile), rest = total
+ *   counts             int32 [2] = {num_active, total_problem_tiles}
+ * Expert ids outside [0, num_experts) are an error reported through counts[0] = -1.
+ */
+int tris_build_grouped_route(const int64_t* selected_experts, int32_t num_tokens, int32_t top_k,
+                             int32_t num_experts, int32_t m_tile, int64_t* perm,
+                             int64_t* grouped_token_indices, int64_t* grouped_slots,
+                             int32_t* grouped_expert_ids, int32_t* expert_ids, int32_t* segment_offsets,
+                             int32_t* problem_offsets, int32_t* counts, void* stream);
+
+/*
+ * Grouped expert GEMM with in-kernel block-GR decode: replaces
+ * compact3_tris_precomputed_grouped_forward_block_gr (TriSMoE_cuda.cpp:1018-1063,
+ * kernel.cu:9768-10213).  output[r, n] = fp16(sum_k hidden[r,k] * W_e[n,k]
+ * (* output_scale[e,n]) (+ bias[e,n])) for row r of segment s, e = expert_ids[s]
+ * (e < 0, and e >= num_experts, give zero rows).  hidden fp16 [batch, rank];
+ * output fp16 [batch, N]: rows inside segments are written, others untouched.  total_problem_tiles is the host copy of the route's
+ * tile count (m_tile 4); it only bounds the launch.
+ */
+int tris_grouped_forward_block_gr(const uint16_t* hidden, int32_t batch, const int32_t* expert_ids,
+                                  const int32_t* segment_offsets, const int32_t* problem_offsets,
+                                  int32_t num_segments, int64_t total_problem_tiles,
+                                  const tris_compact3_payload* payload, uint16_t* output, void* stream);
+
+/* Gate/up pair in one launch: replaces compact3_tris_precomputed_grouped_dual_forward_block_gr
+ * (TriSMoE_cuda.cpp:1065-1136, kernel.cu:10214-10779). */
+int tris_grouped_dual_forward_block_gr(const uint16_t* hidden_a, const uint16_t* hidden_b, int32_t batch,
+                                       const int32_t* expert_ids, const int32_t* segment_offsets,
+                                       const int32_t* problem_offsets, int32_t num_segments,
+                                       int64_t total_problem_tiles, const tris_compact3_payload* payload_a,
+                                       const tris_compact3_payload* payload_b, uint16_t* output_a,
+                                       uint16_t* output_b, void* stream);
+
+/*
+ * Decode every GR block of the listed experts: replaces
+ * compact3_tris_precomputed_grouped_block_gr_predecode (TriSMoE_cuda.cpp:836-853,
+ * kernel.cu:4683-4718, host :8980-9029).  decoded int32 [num_active, nblk, 128];
+ * an expert id outside [0, num_experts) gives zero blocks.
+ */
+int tris_grouped_block_gr_predecode(int32_t* decoded, const int32_t* expert_ids, int32_t num_active,
+                                    const int32_t* q_gmap_gr_words, const int32_t* q_gmap_gr_offsets,
+                                    const int32_t* q_gmap_gr_meta, int32_t num_experts, int32_t words_stride,
+                                    int32_t packed_rows, int32_t outfeatures, void* stream);
+
+/*
+ * Grouped GEMM reading predecoded split bitmaps: replaces
+ * compact3_tris_precomputed_grouped_forward_block_gr_predecoded (TriSMoE_cuda.cpp:855-889,
+ * kernel.cu:4720-4885).  decoded is indexed by segment (the predecode of
+ * expert_ids).  As in the reference, no output scale or bias is applied.
+ */
+int tris_grouped_forward_block_gr_predecoded(const uint16_t* hidden, int32_t batch, const int32_t* expert_ids,
+                                             const int32_t* segment_offsets, const int32_t* problem_offsets,
+                                             int32_t num_segments, int64_t total_problem_tiles,
+                                             const int32_t* decoded, const tris_compact3_payload* payload,
+                                             uint16_t* output, void* stream);
+
+/* Dual variant: replaces compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded
+ * (TriSMoE_cuda.cpp:922-974, kernel.cu:5094-5380). */
+int tris_grouped_dual_forward_block_gr_predecoded(const uint16_t* hidden_a, const uint16_t* hidden_b,
+                                                  int32_t batch, const int32_t* expert_ids,
+                                                  const int32_t* segment_offsets, const int32_t* problem_offsets,
+                                                  int32_t num_segments, int64_t total_problem_tiles,
+                                                  const int32_t* decoded_a, const int32_t* decoded_b,
+                                                  const tris_compact3_payload* payload_a,
+                                                  const tris_compact3_payload* payload_b, uint16_t* output_a,
+                                                  uint16_t* output_b, void* stream);
+
+/*
+ * Dequantise the listed experts to dense fp16 weights [num, N, rank]
+ * (verification kernel; the product GEMMs never write weights).  Replaces the
+ * reference's CPU dequant QuantLinear._dequantize_compact3_matrix
+ * (qlinear_cuda.py:4200-4236) with the GPU per-weight formula of
+ * kernel.cu:665-774 and row-pack selection :830-853.  Uses the GR bitmap.
+ */
+int tris_compact3_dequant(const tris_compact3_payload* payload, const int32_t* expert_ids, int32_t num,
+                          uint16_t* weights, void* stream);
+
+/*
+ * Decode the listed experts' GR bitmaps into the dense packed layout
+ * int32 [num, ceil(rank/32), N] (verification kernel; inverse of the encoder's
+ * block gather, qlinear_cuda.py:3810-3822 / kernel.cu:481-502).
+ */
+int tris_gr_decode_dense(const int32_t* q_gmap_gr_words, const int32_t* q_gmap_gr_offsets,
+                         const int32_t* q_gmap_gr_meta, int32_t num_experts, int32_t words_stride,
+                         const int32_t* expert_ids, int32_t num, int32_t packed_rows, int32_t outfeatures,
+                         int32_t* dense, void* stream);
+
+/*
+ * Shared backbone projection: replaces QuantLinear.compute_shared_hidden's fp16
+ * branch (qlinear_cuda.py:4454-4502: F.linear(x * s_in, SV)).  x fp16 [tokens, in];
+ * sv fp16 [rank, in]; in_scale fp16 [in] or NULL (applied as fp16(x*s) when
+ * ns_mode == 1, :4477-4480); out fp16 [tokens, rank]; fp32 accumulation.
+ * row_index int64 [tokens] or NULL gathers x rows (x[row_index[t]]), fusing the
+ * reference's index_select (modeling_mixtral.py:467).  x, sv and in_scale must
+ * be 16-byte aligned.  workspace: device memory of
+ * tris_backbone_workspace_bytes(tokens, in, rank) bytes, zero-filled before
+ * its first use; every call leaves it zero-filled again (per-tile counters)
+ * apart from scratch partial sums.  Calls sharing a workspace must not overlap.
+ */
+int tris_backbone_linear(const uint16_t* x, int32_t tokens, int32_t in_features, const int64_t* row_index,
+                         const uint16_t* sv, int32_t rank, const uint16_t* in_scale, uint16_t* out,
+                         void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace size for tris_backbone_linear (no reference counterpart: cuBLAS
+ * owns its workspace). */
+int64_t tris_backbone_workspace_bytes(int32_t tokens, int32_t in_features, int32_t rank);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRIS_MOE_HIP_H_ */

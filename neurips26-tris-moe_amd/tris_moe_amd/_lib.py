@@ -1,0 +1,107 @@
+"""ctypes binding of libtris_moe_hip.so (the C ABI declared in include/tris_moe_hip.h).
+
+The library is built in place by ``make -C neurips26-tris-moe_amd`` (or
+``__graft_entry__.build()``).  Loading fails loudly: there is no CPU or torch
+fallback for any entry point.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+PKG_ROOT = Path(__file__).resolve().parent.parent
+LIB_PATH = Path(os.environ.get("TRIS_MOE_HIP_LIB", PKG_ROOT / "libtris_moe_hip.so"))
+
+TRIS_COMPACT3_KERNEL_ABI_VERSION = 2
+
+
+class TrisExtensionUnavailable(ImportError):
+    """The HIP library is missing or incompatible."""
+
+
+class TrisPayload(ctypes.Structure):
+    """Mirror of struct tris_compact3_payload."""
+
+    _fields_ = [
+        ("num_experts", ctypes.c_int32),
+        ("rank", ctypes.c_int32),
+        ("outfeatures", ctypes.c_int32),
+        ("num_groups", ctypes.c_int32),
+        ("qweight2_sparse_rows", ctypes.c_int32),
+        ("gr_words_stride", ctypes.c_int32),
+        ("qweight1", ctypes.c_void_p),
+        ("qweight2_sparse", ctypes.c_void_p),
+        ("qweight2_sparse_prefix", ctypes.c_void_p),
+        ("q_gmap_gr_words", ctypes.c_void_p),
+        ("q_gmap_gr_offsets", ctypes.c_void_p),
+        ("q_gmap_gr_meta", ctypes.c_void_p),
+        ("c_map", ctypes.c_void_p),
+        ("g_idx", ctypes.c_void_p),
+        ("col_pack3", ctypes.c_void_p),
+        ("row_pack3", ctypes.c_void_p),
+        ("output_scale", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("has_output_scale", ctypes.c_int32),
+        ("has_bias", ctypes.c_int32),
+        ("use_uniform_k64_groups", ctypes.c_int32),
+    ]
+
+
+# name -> (restype, argtypes)
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+_PAY = ctypes.POINTER(TrisPayload)
+SIGNATURES = {
+    "tris_abi_version": (ctypes.c_int, []),
+    "tris_last_error": (ctypes.c_char_p, []),
+    "tris_gr_encode": (_I64, [_P, _I32, _I32, _I32, _I32, _I32, _P, _I64, _P, _P]),
+    "tris_build_grouped_route": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "tris_grouped_forward_block_gr": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I32, _I64, _PAY, _P, _P]),
+    "tris_grouped_dual_forward_block_gr": (ctypes.c_int, [_P, _P, _I32, _P, _P, _P, _I32, _I64, _PAY, _PAY, _P, _P, _P]),
+    "tris_grouped_block_gr_predecode": (ctypes.c_int, [_P, _P, _I32, _P, _P, _P, _I32, _I32, _I32, _I32, _P]),
+    "tris_grouped_forward_block_gr_predecoded": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I32, _I64, _P, _PAY, _P, _P]),
+    "tris_grouped_dual_forward_block_gr_predecoded": (
+        ctypes.c_int, [_P, _P, _I32, _P, _P, _P, _I32, _I64, _P, _P, _PAY, _PAY, _P, _P, _P]),
+    "tris_compact3_dequant": (ctypes.c_int, [_PAY, _P, _I32, _P, _P]),
+    "tris_gr_decode_dense": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _P, _I32, _I32, _I32, _P, _P]),
+    "tris_backbone_linear": (ctypes.c_int, [_P, _I32, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P]),
+    "tris_backbone_workspace_bytes": (_I64, [_I32, _I32, _I32]),
+}
+
+_lib = None
+
+
+def load():
+    """Load and type the HIP library (cached).  Raises TrisExtensionUnavailable."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise TrisExtensionUnavailable(
+            f"TriS HIP library not found at {LIB_PATH}; build it with `make -C {PKG_ROOT}` "
+            "(there is no CPU fallback)"
+        )
+    lib = ctypes.CDLL(str(LIB_PATH))
+    missing = [name for name in SIGNATURES if not hasattr(lib, name)]
+    if missing:
+        raise TrisExtensionUnavailable(f"{LIB_PATH} lacks entry points {missing}; rebuild it")
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    version = lib.tris_abi_version()
+    if version != TRIS_COMPACT3_KERNEL_ABI_VERSION:
+        raise TrisExtensionUnavailable(
+            f"{LIB_PATH}: compact3 ABI {version}, expected {TRIS_COMPACT3_KERNEL_ABI_VERSION}")
+    _lib = lib
+    return lib
+
+
+def check(rc: int, what: str):
+    """Turn a negative C-ABI return code into RuntimeError (the reference's TORCH_CHECK)."""
+    if rc < 0:
+        msg = load().tris_last_error().decode("utf-8", "replace")
+        raise RuntimeError(f"{what}: {msg}")
+    return rc

@@ -1,0 +1,477 @@
+"""Drop-in for the reference's native module ``autogptq_TriS_cuda`` on the grouped expert path.
+
+Every function keeps the pybind name, argument order and defaults of
+``TriSMoE_cuda.cpp:1138-1430`` for the grouped block-GR path and returns
+freshly allocated torch tensors exactly as the reference does, but computes
+through the gfx950 HIP kernels of libtris_moe_hip.so (C ABI, via ctypes).
+Argument contracts mirror the reference's ``CHECK_*`` / ``TORCH_CHECK``
+macros (``TriSMoE_cuda_kernel.cu:49-54``, ``:9789-9842``) and raise
+``RuntimeError`` like them.  All work is enqueued on torch's current stream of
+the input's device.
+
+The non-expert compact3 linears (``compact3_linear_forward``,
+``compact3_qkv_linear_forward``, ``compact3_dual_linear_forward``) are outside
+this library's scope; they exist so that the reference's ABI probe
+(``qlinear_cuda.py:14-37``) accepts the module, and raise RuntimeError, which
+the reference's callers treat as "kernel unavailable".
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import TRIS_COMPACT3_KERNEL_ABI_VERSION, TrisPayload  # noqa: F401
+
+BLOCK_GR_TILE_K = 64
+BLOCK_GR_TILE_OUT = 64
+BLOCK_GR_PACKED_ROWS = 2
+BLOCK_GR_WORDS_PER_BLOCK = 128
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ptr(t):
+    if t is None or t.numel() == 0:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _check_cuda(name, t, dtype, dims=None, device=None):
+    if not isinstance(t, torch.Tensor):
+        raise RuntimeError(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{name} must be a CUDA tensor")
+    if device is not None and t.device != device:
+        raise RuntimeError(f"{name} must be on {device}")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+    if t.dtype != dtype:
+        raise RuntimeError(f"{name} must be {dtype}")
+    if dims is not None and t.dim() != dims:
+        raise RuntimeError(f"{name} must be {dims}D")
+
+
+def _host_tiles(total_problem_tiles) -> int:
+    if isinstance(total_problem_tiles, torch.Tensor):
+        if total_problem_tiles.device.type != "cpu":
+            raise RuntimeError("total_problem_tiles must be a CPU tensor")
+        if total_problem_tiles.numel() != 1:
+            raise RuntimeError("total_problem_tiles must contain one value")
+        return int(total_problem_tiles.reshape(-1)[0].item())
+    return int(total_problem_tiles)
+
+
+def _num_gr_blocks(packed_rows: int, outfeatures: int) -> int:
+    return -(-packed_rows // BLOCK_GR_PACKED_ROWS) * -(-outfeatures // BLOCK_GR_TILE_OUT)
+
+
+def make_payload_struct(rank, qweight1, qweight2_sparse, qweight2_sparse_prefix, q_gmap_gr_words, q_gmap_gr_offsets,
+                        q_gmap_gr_meta, c_map, g_idx, col_pack3, row_pack3, output_scale, has_output_scale, bias,
+                        has_bias, use_uniform_k64_groups, device, need_gr=True, who="grouped payload"):
+    """Validate one projection's stacked payload (kernel.cu:9789-9842) and pack the C descriptor."""
+    _check_cuda("qweight1", qweight1, torch.int32, 3, device)
+    _check_cuda("qweight2_sparse", qweight2_sparse, torch.int32, 3, device)
+    _check_cuda("qweight2_sparse_prefix", qweight2_sparse_prefix, torch.int32, 2, device)
+    _check_cuda("c_map", c_map, torch.int32, 2, device)
+    _check_cuda("g_idx", g_idx, torch.int32, 2, device)
+    _check_cuda("col_pack3", col_pack3, torch.int64, 2, device)
+    _check_cuda("row_pack3", row_pack3, torch.int64, 3, device)
+    num_experts = int(qweight1.size(0))
+    packed_rows = (rank + 31) // 32
+    outfeatures = int(qweight1.size(2))
+    num_groups = int(row_pack3.size(2))
+    nblk = _num_gr_blocks(packed_rows, outfeatures)
+    if int(qweight1.size(1)) != packed_rows:
+        raise RuntimeError(f"{who}: qweight1 packed height mismatch")
+    if int(qweight2_sparse.size(0)) != num_experts or int(qweight2_sparse.size(2)) != outfeatures:
+        raise RuntimeError(f"{who}: qweight2_sparse shape mismatch")
+    if tuple(qweight2_sparse_prefix.shape) != (num_experts, packed_rows + 1):
+        raise RuntimeError(f"{who}: qweight2 prefix mismatch")
+    if tuple(c_map.shape) != (num_experts, packed_rows):
+        raise RuntimeError(f"{who}: c_map mismatch")
+    if tuple(g_idx.shape) != (num_experts, rank):
+        raise RuntimeError(f"{who}: g_idx mismatch")
+    if tuple(col_pack3.shape) != (num_experts, rank):
+        raise RuntimeError(f"{who}: col_pack3 mismatch")
+    if int(row_pack3.size(0)) != num_experts or int(row_pack3.size(1)) != outfeatures:
+        raise RuntimeError(f"{who}: row_pack3 mismatch")
+    words_stride = 0
+    if need_gr:
+        _check_cuda("q_gmap_gr_words", q_gmap_gr_words, torch.int32, 2, device)
+        _check_cuda("q_gmap_gr_offsets", q_gmap_gr_offsets, torch.int32, 2, device)
+        _check_cuda("q_gmap_gr_meta", q_gmap_gr_meta, torch.int32, 2, device)
+        if (int(q_gmap_gr_words.size(0)) != num_experts or int(q_gmap_gr_offsets.size(0)) != num_experts
+                or int(q_gmap_gr_meta.size(0)) != num_experts):
+            raise RuntimeError(f"{who}: block-GR expert mismatch")
+        if int(q_gmap_gr_offsets.size(1)) != nblk + 1:
+            raise RuntimeError(f"{who}: q_gmap_gr_offsets shape mismatch")
+        if int(q_gmap_gr_meta.size(1)) != nblk:
+            raise RuntimeError(f"{who}: q_gmap_gr_meta shape mismatch")
+        words_stride = int(q_gmap_gr_words.size(1))
+    if has_output_scale:
+        _check_cuda("output_scale", output_scale, torch.float16, 2, device)
+        if tuple(output_scale.shape) != (num_experts, outfeatures):
+            raise RuntimeError(f"{who}: output_scale mismatch")
+    if has_bias:
+        _check_cuda("bias", bias, torch.float16, 2, device)
+        if tuple(bias.shape) != (num_experts, outfeatures):
+            raise RuntimeError(f"{who}: bias mismatch")
+    s = TrisPayload()
+    s.num_experts = num_experts
+    s.rank = rank
+    s.outfeatures = outfeatures
+    s.num_groups = num_groups
+    s.qweight2_sparse_rows = int(qweight2_sparse.size(1))
+    s.gr_words_stride = words_stride
+    s.qweight1 = qweight1.data_ptr()
+    s.qweight2_sparse = qweight2_sparse.data_ptr() if qweight2_sparse.numel() else None
+    s.qweight2_sparse_prefix = qweight2_sparse_prefix.data_ptr()
+    if need_gr:
+        s.q_gmap_gr_words = q_gmap_gr_words.data_ptr() if q_gmap_gr_words.numel() else None
+        s.q_gmap_gr_offsets = q_gmap_gr_offsets.data_ptr()
+        s.q_gmap_gr_meta = q_gmap_gr_meta.data_ptr() if q_gmap_gr_meta.numel() else None
+    s.c_map = c_map.data_ptr()
+    s.g_idx = g_idx.data_ptr()
+    s.col_pack3 = col_pack3.data_ptr()
+    s.row_pack3 = row_pack3.data_ptr() if row_pack3.numel() else None
+    s.output_scale = output_scale.data_ptr() if has_output_scale else None
+    s.bias = bias.data_ptr() if has_bias else None
+    s.has_output_scale = int(bool(has_output_scale))
+    s.has_bias = int(bool(has_bias))
+    s.use_uniform_k64_groups = int(bool(use_uniform_k64_groups))
+    return s
+
+
+def _check_route(hidden, expert_ids, segment_offsets, problem_offsets):
+    _check_cuda("hidden", hidden, torch.float16, 2)
+    dev = hidden.device
+    _check_cuda("expert_ids", expert_ids, torch.int32, 1, dev)
+    _check_cuda("segment_offsets", segment_offsets, torch.int32, 1, dev)
+    _check_cuda("problem_offsets", problem_offsets, torch.int32, 1, dev)
+    if segment_offsets.size(0) != expert_ids.size(0) + 1:
+        raise RuntimeError("segment_offsets must be 1D [segments + 1]")
+    if problem_offsets.size(0) != expert_ids.size(0) + 1:
+        raise RuntimeError("problem_offsets must be 1D [segments + 1]")
+
+
+# ------------------------------------------------------------------ route
+def build_grouped_route(selected_experts: torch.Tensor, num_experts: int, m_tile: int):
+    """TriSMoE_cuda.cpp:741-793: returns [perm, grouped_token_indices, grouped_slots, expert_ids,
+    segment_offsets, problem_offsets, total_problem_tiles(CPU int64 [1])].
+
+    The kernels build everything on the device; as in the reference, one
+    device->host copy fetches the active-expert and tile counts to size the
+    returned tensors.  ``build_grouped_route_device`` skips that copy."""
+    out = build_grouped_route_device(selected_experts, num_experts, m_tile)
+    counts = out["counts"].to("cpu")
+    num_active, total = int(counts[0]), int(counts[1])
+    if num_active < 0:
+        raise RuntimeError("selected_experts contains an expert id outside [0, num_experts)")
+    return [
+        out["perm"],
+        out["grouped_token_indices"],
+        out["grouped_slots"],
+        out["expert_ids"][:num_active].contiguous(),
+        out["segment_offsets"][: num_active + 1].contiguous(),
+        out["problem_offsets"][: num_active + 1].contiguous(),
+        torch.tensor([total], dtype=torch.int64),
+    ]
+
+
+def build_grouped_route_device(selected_experts: torch.Tensor, num_experts: int, m_tile: int = 4) -> dict:
+    """Route metadata padded to num_experts segments, with no host synchronisation."""
+    if not isinstance(selected_experts, torch.Tensor) or selected_experts.device.type != "cuda":
+        raise RuntimeError("selected_experts must be a CUDA tensor")
+    if selected_experts.dim() != 2:
+        raise RuntimeError("selected_experts must be 2D [tokens, top_k]")
+    if num_experts < 0:
+        raise RuntimeError("num_experts must be non-negative")
+    if m_tile <= 0:
+        raise RuntimeError("m_tile must be positive")
+    sel = selected_experts.contiguous().to(torch.int64)
+    dev = sel.device
+    t, k = int(sel.size(0)), int(sel.size(1))
+    r = t * k
+    long_opts = dict(device=dev, dtype=torch.int64)
+    int_opts = dict(device=dev, dtype=torch.int32)
+    perm = torch.empty(r, **long_opts)
+    gti = torch.empty(r, **long_opts)
+    gsl = torch.empty(r, **long_opts)
+    gexp = torch.empty(r, **int_opts)
+    expert_ids = torch.empty(max(num_experts, 0), **int_opts)
+    seg = torch.empty(num_experts + 1, **int_opts)
+    prob = torch.empty(num_experts + 1, **int_opts)
+    counts = torch.empty(2, **int_opts)
+    lib = _lib.load()
+    _lib.check(lib.tris_build_grouped_route(_ptr(sel), t, k, num_experts, m_tile, _ptr(perm), _ptr(gti), _ptr(gsl),
+                                            _ptr(gexp), _ptr(expert_ids), _ptr(seg), _ptr(prob), _ptr(counts),
+                                            _stream(sel)), "build_grouped_route")
+    return {"perm": perm, "grouped_token_indices": gti, "grouped_slots": gsl, "grouped_expert_ids": gexp,
+            "expert_ids": expert_ids, "segment_offsets": seg, "problem_offsets": prob, "counts": counts}
+
+
+# ----------------------------------------------------------- grouped GEMMs
+def compact3_tris_precomputed_grouped_forward_block_gr(hidden, expert_ids, segment_offsets, problem_offsets,
+                                                       total_problem_tiles, qweight1, qweight2_sparse,
+                                                       qweight2_sparse_prefix, q_gmap_gr_words, q_gmap_gr_offsets,
+                                                       q_gmap_gr_meta, c_map, g_idx, col_pack3, row_pack3,
+                                                       output_scale, has_output_scale, bias, has_bias,
+                                                       use_uniform_k64_groups=False):
+    """TriSMoE_cuda.cpp:1018-1063 -> tris_grouped_forward_block_gr."""
+    _check_route(hidden, expert_ids, segment_offsets, problem_offsets)
+    total = _host_tiles(total_problem_tiles)
+    rank = int(hidden.size(1))
+    pay = make_payload_struct(rank, qweight1, qweight2_sparse, qweight2_sparse_prefix, q_gmap_gr_words,
+                              q_gmap_gr_offsets, q_gmap_gr_meta, c_map, g_idx, col_pack3, row_pack3, output_scale,
+                              has_output_scale, bias, has_bias, use_uniform_k64_groups, hidden.device)
+    out = torch.zeros((hidden.size(0), pay.outfeatures), dtype=torch.float16, device=hidden.device)
+    _lib.check(_lib.load().tris_grouped_forward_block_gr(
+        _ptr(hidden), int(hidden.size(0)), _ptr(expert_ids), _ptr(segment_offsets), _ptr(problem_offsets),
+        int(expert_ids.size(0)), total, ctypes.byref(pay), _ptr(out), _stream(hidden)),
+        "compact3_tris_precomputed_grouped_forward_block_gr")
+    return out
+
+
+def compact3_tris_precomputed_grouped_dual_forward_block_gr(
+        hidden_a, hidden_b, expert_ids, segment_offsets, problem_offsets, total_problem_tiles,
+        qweight1_a, qweight2_sparse_a, qweight2_sparse_prefix_a, q_gmap_gr_words_a, q_gmap_gr_offsets_a,
+        q_gmap_gr_meta_a, c_map_a, g_idx_a, col_pack3_a, row_pack3_a, output_scale_a, has_output_scale_a, bias_a,
+        qweight1_b, qweight2_sparse_b, qweight2_sparse_prefix_b, q_gmap_gr_words_b, q_gmap_gr_offsets_b,
+        q_gmap_gr_meta_b, c_map_b, g_idx_b, col_pack3_b, row_pack3_b, output_scale_b, has_output_scale_b, bias_b,
+        use_uniform_k64_groups=False):
+    """TriSMoE_cuda.cpp:1065-1136 -> tris_grouped_dual_forward_block_gr.  has_bias = bias.numel() > 0
+    (kernel.cu:10330-10331)."""
+    _check_route(hidden_a, expert_ids, segment_offsets, problem_offsets)
+    _check_cuda("hidden_b", hidden_b, torch.float16, 2, hidden_a.device)
+    if hidden_b.size(0) != hidden_a.size(0):
+        raise RuntimeError("hidden_a/hidden_b batch mismatch")
+    total = _host_tiles(total_problem_tiles)
+    has_bias_a = isinstance(bias_a, torch.Tensor) and bias_a.numel() > 0
+    has_bias_b = isinstance(bias_b, torch.Tensor) and bias_b.numel() > 0
+    pa = make_payload_struct(int(hidden_a.size(1)), qweight1_a, qweight2_sparse_a, qweight2_sparse_prefix_a,
+                             q_gmap_gr_words_a, q_gmap_gr_offsets_a, q_gmap_gr_meta_a, c_map_a, g_idx_a, col_pack3_a,
+                             row_pack3_a, output_scale_a, has_output_scale_a, bias_a, has_bias_a,
+                             use_uniform_k64_groups, hidden_a.device, who="grouped payload a")
+    pb = make_payload_struct(int(hidden_b.size(1)), qweight1_b, qweight2_sparse_b, qweight2_sparse_prefix_b,
+                             q_gmap_gr_words_b, q_gmap_gr_offsets_b, q_gmap_gr_meta_b, c_map_b, g_idx_b, col_pack3_b,
+                             row_pack3_b, output_scale_b, has_output_scale_b, bias_b, has_bias_b,
+                             use_uniform_k64_groups, hidden_a.device, who="grouped payload b")
+    out_a = torch.zeros((hidden_a.size(0), pa.outfeatures), dtype=torch.float16, device=hidden_a.device)
+    out_b = torch.zeros((hidden_b.size(0), pb.outfeatures), dtype=torch.float16, device=hidden_a.device)
+    _lib.check(_lib.load().tris_grouped_dual_forward_block_gr(
+        _ptr(hidden_a), _ptr(hidden_b), int(hidden_a.size(0)), _ptr(expert_ids), _ptr(segment_offsets),
+        _ptr(problem_offsets), int(expert_ids.size(0)), total, ctypes.byref(pa), ctypes.byref(pb), _ptr(out_a),
+        _ptr(out_b), _stream(hidden_a)), "compact3_tris_precomputed_grouped_dual_forward_block_gr")
+    return [out_a, out_b]
+
+
+def compact3_tris_precomputed_grouped_block_gr_predecode(decoded_q_gmap_words, expert_ids, q_gmap_gr_words,
+                                                         q_gmap_gr_offsets, q_gmap_gr_meta, packed_rows, outfeatures):
+    """TriSMoE_cuda.cpp:836-853 (kernel.cu:8980-9029): decode into the caller's buffer and return it."""
+    _check_cuda("decoded_q_gmap_words", decoded_q_gmap_words, torch.int32, None)
+    dev = decoded_q_gmap_words.device
+    _check_cuda("expert_ids", expert_ids, torch.int32, 1, dev)
+    _check_cuda("q_gmap_gr_words", q_gmap_gr_words, torch.int32, 2, dev)
+    _check_cuda("q_gmap_gr_offsets", q_gmap_gr_offsets, torch.int32, 2, dev)
+    _check_cuda("q_gmap_gr_meta", q_gmap_gr_meta, torch.int32, 2, dev)
+    nblk = _num_gr_blocks(int(packed_rows), int(outfeatures))
+    num_active = int(expert_ids.size(0))
+    if decoded_q_gmap_words.numel() != num_active * nblk * BLOCK_GR_WORDS_PER_BLOCK:
+        raise RuntimeError("decoded_q_gmap_words must hold [active, blocks, 128] words")
+    if int(q_gmap_gr_offsets.size(1)) != nblk + 1 or int(q_gmap_gr_meta.size(1)) != nblk:
+        raise RuntimeError("q_gmap_gr_offsets/meta shape mismatch")
+    words = q_gmap_gr_words
+    if words.numel() == 0:
+        words = torch.zeros((max(int(q_gmap_gr_offsets.size(0)), 1), 1), dtype=torch.int32, device=dev)
+    _lib.check(_lib.load().tris_grouped_block_gr_predecode(
+        _ptr(decoded_q_gmap_words), _ptr(expert_ids), num_active, _ptr(words), _ptr(q_gmap_gr_offsets),
+        _ptr(q_gmap_gr_meta), int(q_gmap_gr_offsets.size(0)), int(words.size(1)), int(packed_rows),
+        int(outfeatures), _stream(decoded_q_gmap_words)),
+        "compact3_tris_precomputed_grouped_block_gr_predecode")
+    return decoded_q_gmap_words
+
+
+def compact3_tris_precomputed_grouped_forward_block_gr_predecoded(hidden, expert_ids, segment_offsets,
+                                                                  problem_offsets, total_problem_tiles,
+                                                                  decoded_q_gmap_words, qweight1, qweight2_sparse,
+                                                                  qweight2_sparse_prefix, c_map, g_idx, col_pack3,
+                                                                  row_pack3, use_uniform_k64_groups=False):
+    """TriSMoE_cuda.cpp:855-889 (no output scale / bias, as the reference's NoScaleNoBias kernel)."""
+    _check_route(hidden, expert_ids, segment_offsets, problem_offsets)
+    total = _host_tiles(total_problem_tiles)
+    pay = make_payload_struct(int(hidden.size(1)), qweight1, qweight2_sparse, qweight2_sparse_prefix, None, None,
+                              None, c_map, g_idx, col_pack3, row_pack3, None, False, None, False,
+                              use_uniform_k64_groups, hidden.device, need_gr=False)
+    _check_predecoded(decoded_q_gmap_words, expert_ids, pay, hidden.device)
+    out = torch.zeros((hidden.size(0), pay.outfeatures), dtype=torch.float16, device=hidden.device)
+    _lib.check(_lib.load().tris_grouped_forward_block_gr_predecoded(
+        _ptr(hidden), int(hidden.size(0)), _ptr(expert_ids), _ptr(segment_offsets), _ptr(problem_offsets),
+        int(expert_ids.size(0)), total, _ptr(decoded_q_gmap_words), ctypes.byref(pay), _ptr(out), _stream(hidden)),
+        "compact3_tris_precomputed_grouped_forward_block_gr_predecoded")
+    return out
+
+
+def _check_predecoded(decoded, expert_ids, pay, device):
+    _check_cuda("decoded_q_gmap_words", decoded, torch.int32, None, device)
+    nblk = _num_gr_blocks((pay.rank + 31) // 32, pay.outfeatures)
+    if decoded.numel() < int(expert_ids.size(0)) * nblk * BLOCK_GR_WORDS_PER_BLOCK:
+        raise RuntimeError("decoded_q_gmap_words is smaller than [segments, blocks, 128]")
+
+
+def compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
+        hidden_a, hidden_b, expert_ids, segment_offsets, problem_offsets, total_problem_tiles,
+        decoded_q_gmap_words_a, qweight1_a, qweight2_sparse_a, qweight2_sparse_prefix_a, c_map_a, g_idx_a,
+        col_pack3_a, row_pack3_a, decoded_q_gmap_words_b, qweight1_b, qweight2_sparse_b, qweight2_sparse_prefix_b,
+        c_map_b, g_idx_b, col_pack3_b, row_pack3_b, use_uniform_k64_groups=False):
+    """TriSMoE_cuda.cpp:922-974."""
+    _check_route(hidden_a, expert_ids, segment_offsets, problem_offsets)
+    _check_cuda("hidden_b", hidden_b, torch.float16, 2, hidden_a.device)
+    total = _host_tiles(total_problem_tiles)
+    pa = make_payload_struct(int(hidden_a.size(1)), qweight1_a, qweight2_sparse_a, qweight2_sparse_prefix_a, None,
+                             None, None, c_map_a, g_idx_a, col_pack3_a, row_pack3_a, None, False, None, False,
+                             use_uniform_k64_groups, hidden_a.device, need_gr=False, who="grouped payload a")
+    pb = make_payload_struct(int(hidden_b.size(1)), qweight1_b, qweight2_sparse_b, qweight2_sparse_prefix_b, None,
+                             None, None, c_map_b, g_idx_b, col_pack3_b, row_pack3_b, None, False, None, False,
+                             use_uniform_k64_groups, hidden_a.device, need_gr=False, who="grouped payload b")
+    _check_predecoded(decoded_q_gmap_words_a, expert_ids, pa, hidden_a.device)
+    _check_predecoded(decoded_q_gmap_words_b, expert_ids, pb, hidden_a.device)
+    out_a = torch.zeros((hidden_a.size(0), pa.outfeatures), dtype=torch.float16, device=hidden_a.device)
+    out_b = torch.zeros((hidden_b.size(0), pb.outfeatures), dtype=torch.float16, device=hidden_a.device)
+    _lib.check(_lib.load().tris_grouped_dual_forward_block_gr_predecoded(
+        _ptr(hidden_a), _ptr(hidden_b), int(hidden_a.size(0)), _ptr(expert_ids), _ptr(segment_offsets),
+        _ptr(problem_offsets), int(expert_ids.size(0)), total, _ptr(decoded_q_gmap_words_a),
+        _ptr(decoded_q_gmap_words_b), ctypes.byref(pa), ctypes.byref(pb), _ptr(out_a), _ptr(out_b),
+        _stream(hidden_a)), "compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded")
+    return [out_a, out_b]
+
+
+def _segments_total(segment_offsets) -> int:
+    return int(segment_offsets.numel()) - 1
+
+
+def compact3_tris_precomputed_grouped_forward_block_gr_predecoded_hybrid(
+        hidden, expert_ids, segment_offsets, full_problem_offsets, full_problem_tiles, tail_problem_offsets,
+        tail_problem_tiles, decoded_q_gmap_words, qweight1, qweight2_sparse, qweight2_sparse_prefix, c_map, g_idx,
+        col_pack3, row_pack3, use_uniform_k64_groups=False):
+    """TriSMoE_cuda.cpp:891-920.  The reference splits full 16-row tiles (tensor cores) from tail
+    tiles; here one kernel covers every row of every segment, so the split metadata only bounds
+    the launch and the result is the predecoded GEMM."""
+    total = _host_tiles(full_problem_tiles) + _host_tiles(tail_problem_tiles) + _segments_total(segment_offsets)
+    return compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
+        hidden, expert_ids, segment_offsets, full_problem_offsets, total, decoded_q_gmap_words, qweight1,
+        qweight2_sparse, qweight2_sparse_prefix, c_map, g_idx, col_pack3, row_pack3, use_uniform_k64_groups)
+
+
+def compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded_hybrid(
+        hidden_a, hidden_b, expert_ids, segment_offsets, full_problem_offsets, full_problem_tiles,
+        tail_problem_offsets, tail_problem_tiles, decoded_q_gmap_words_a, qweight1_a, qweight2_sparse_a,
+        qweight2_sparse_prefix_a, c_map_a, g_idx_a, col_pack3_a, row_pack3_a, decoded_q_gmap_words_b, qweight1_b,
+        qweight2_sparse_b, qweight2_sparse_prefix_b, c_map_b, g_idx_b, col_pack3_b, row_pack3_b,
+        use_uniform_k64_groups=False):
+    """TriSMoE_cuda.cpp:976-1016 (see the single-projection hybrid)."""
+    total = _host_tiles(full_problem_tiles) + _host_tiles(tail_problem_tiles) + _segments_total(segment_offsets)
+    return compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
+        hidden_a, hidden_b, expert_ids, segment_offsets, full_problem_offsets, total, decoded_q_gmap_words_a,
+        qweight1_a, qweight2_sparse_a, qweight2_sparse_prefix_a, c_map_a, g_idx_a, col_pack3_a, row_pack3_a,
+        decoded_q_gmap_words_b, qweight1_b, qweight2_sparse_b, qweight2_sparse_prefix_b, c_map_b, g_idx_b,
+        col_pack3_b, row_pack3_b, use_uniform_k64_groups)
+
+
+def _out_of_scope(name):
+    def fn(*args, **kwargs):
+        raise RuntimeError(f"{name}: non-expert compact3 linears are not provided by the TriS-MoE HIP library")
+    fn.__name__ = name
+    return fn
+
+
+compact3_linear_forward = _out_of_scope("compact3_linear_forward")
+compact3_qkv_linear_forward = _out_of_scope("compact3_qkv_linear_forward")
+compact3_dual_linear_forward = _out_of_scope("compact3_dual_linear_forward")
+
+
+# ---------------------------------------------- verification / helper entry points
+def compact3_dequant(payload_tensors: dict, rank: int, expert_ids: torch.Tensor, use_uniform_k64_groups=False):
+    """Dense fp16 weights [num, N, rank] of the listed experts (GPU verification kernel)."""
+    dev = expert_ids.device
+    pay = make_payload_struct(rank, payload_tensors["qweight1"], payload_tensors["qweight2_sparse"],
+                              payload_tensors["qweight2_sparse_prefix"], payload_tensors["q_gmap_gr_words"],
+                              payload_tensors["q_gmap_gr_offsets"], payload_tensors["q_gmap_gr_meta"],
+                              payload_tensors["c_map"], payload_tensors["g_idx"], payload_tensors["col_pack3"],
+                              payload_tensors["row_pack3"], None, False, None, False, use_uniform_k64_groups, dev)
+    ids = expert_ids.to(torch.int32).contiguous()
+    out = torch.empty((ids.numel(), pay.outfeatures, rank), dtype=torch.float16, device=dev)
+    _lib.check(_lib.load().tris_compact3_dequant(ctypes.byref(pay), _ptr(ids), ids.numel(), _ptr(out), _stream(ids)),
+               "tris_compact3_dequant")
+    return out
+
+
+def gr_decode_dense(q_gmap_gr_words, q_gmap_gr_offsets, q_gmap_gr_meta, expert_ids, packed_rows, outfeatures):
+    """Dense packed split bitmaps [num, packed_rows, N] int32 of the listed experts."""
+    dev = q_gmap_gr_offsets.device
+    ids = expert_ids.to(torch.int32).contiguous()
+    words = q_gmap_gr_words
+    if words.numel() == 0:
+        words = torch.zeros((max(int(q_gmap_gr_offsets.size(0)), 1), 1), dtype=torch.int32, device=dev)
+    out = torch.zeros((ids.numel(), packed_rows, outfeatures), dtype=torch.int32, device=dev)
+    _lib.check(_lib.load().tris_gr_decode_dense(_ptr(words), _ptr(q_gmap_gr_offsets), _ptr(q_gmap_gr_meta),
+                                                int(q_gmap_gr_offsets.size(0)), int(words.size(1)), _ptr(ids),
+                                                ids.numel(), packed_rows, outfeatures, _ptr(out), _stream(ids)),
+               "tris_gr_decode_dense")
+    return out
+
+
+_WORKSPACES: dict = {}
+
+
+def backbone_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Zero-filled per-device workspace for the backbone kernel (kept zeroed by the kernel)."""
+    key = (device.type, device.index)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def backbone_linear(x: torch.Tensor, sv: torch.Tensor, in_scale: torch.Tensor | None = None,
+                    row_index: torch.Tensor | None = None) -> torch.Tensor:
+    """hidden = fp16(x[row_index] * in_scale) @ sv^T with fp32 accumulation (compute_shared_hidden)."""
+    _check_cuda("x", x, torch.float16, 2)
+    _check_cuda("shared_sv", sv, torch.float16, 2, x.device)
+    if sv.size(1) != x.size(1):
+        raise RuntimeError("shared_sv in-features mismatch")
+    tokens = int(row_index.numel()) if row_index is not None else int(x.size(0))
+    if row_index is not None:
+        _check_cuda("row_index", row_index, torch.int64, 1, x.device)
+    if in_scale is not None:
+        _check_cuda("in_scale", in_scale, torch.float16, 1, x.device)
+    rank, in_f = int(sv.size(0)), int(sv.size(1))
+    out = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
+    lib = _lib.load()
+    need = int(lib.tris_backbone_workspace_bytes(tokens, in_f, rank))
+    ws = backbone_workspace(x.device, need)
+    _lib.check(lib.tris_backbone_linear(_ptr(x), tokens, in_f, _ptr(row_index), _ptr(sv), rank, _ptr(in_scale),
+                                        _ptr(out), _ptr(ws), int(ws.numel()), _stream(x)), "tris_backbone_linear")
+    return out
+
+
+def gr_encode(packed, k_min: int = 0, k_max: int = 7, force_raw: bool = False):
+    """Host block-GR encoder: int32 [packed_rows, N] (numpy or CPU tensor) -> (words, offsets, meta) int32 numpy."""
+    import numpy as np
+
+    arr = np.ascontiguousarray(packed.cpu().numpy() if isinstance(packed, torch.Tensor) else packed, dtype=np.int32)
+    rows, n = arr.shape
+    nblk = _num_gr_blocks(rows, n)
+    words = np.zeros(max(nblk * BLOCK_GR_WORDS_PER_BLOCK, 1), dtype=np.int32)
+    offsets = np.zeros(nblk + 1, dtype=np.int32)
+    meta = np.zeros(nblk, dtype=np.int32)
+    lib = _lib.load()
+    total = lib.tris_gr_encode(arr.ctypes.data_as(ctypes.c_void_p), rows, n, k_min, k_max, int(force_raw),
+                               words.ctypes.data_as(ctypes.c_void_p), words.size,
+                               offsets.ctypes.data_as(ctypes.c_void_p), meta.ctypes.data_as(ctypes.c_void_p))
+    _lib.check(int(total), "tris_gr_encode")
+    return words[:total].copy(), offsets, meta

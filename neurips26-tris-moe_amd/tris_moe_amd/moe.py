@@ -1,0 +1,120 @@
+"""Sparse MoE block on the grouped expert path (``modeling_mixtral.py:406-608``).
+
+``TrisSparseMoeBlock.forward(hidden_states) -> (out, router_logits)`` keeps the
+reference block's signature and dataflow: router softmax (fp32) -> top-k ->
+optional renormalisation (Mixtral/Qwen always, OLMoE when ``norm_topk_prob``,
+``modeling_olmoe.py:1053-1058``) -> bf16 -> fp16 cast of the kernel input
+(``:83-90``) -> grouped route -> shared backbones -> grouped gate/up pair ->
+SiLU * up -> down backbone -> grouped down -> routing-weighted scatter-add in
+the output dtype.  An optional always-on fp16 shared expert (A3B-class
+layers) is added unrouted.
+
+``grouped_moe_forward`` is the same computation with every size fixed by the
+input shape (route metadata padded to num_experts segments, launch bounds
+from the routed-row count), so it runs without host synchronisation and can
+be captured in a HIP graph; ``TrisSparseMoeBlock`` uses it too.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import ext
+from .qlinear import GROUPED_SEGMENT_M_TILE
+
+
+def route_topk(router_logits: torch.Tensor, top_k: int, renormalize: bool):
+    """modeling_mixtral.py:548-551."""
+    weights = F.softmax(router_logits, dim=1, dtype=torch.float)
+    weights, selected = torch.topk(weights, top_k, dim=-1)
+    if renormalize:
+        weights = weights / weights.sum(dim=-1, keepdim=True)
+    return weights, selected
+
+
+def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, selected_experts: torch.Tensor,
+                        payloads: dict, backbones: dict, num_experts: int, output_dtype=torch.bfloat16,
+                        shared_expert=None) -> torch.Tensor:
+    """The grouped MoE layer on the HIP kernels with no host synchronisation.
+
+    x16 fp16 [T, H]; routing_weights [T, k] (cast to fp16 as in modeling_mixtral.py:555);
+    selected_experts int64 [T, k]; payloads {gate, up, down} device payload dicts;
+    backbones {gate, up, down} fp16 [rank, in].  Returns [T, H] in output_dtype."""
+    T, H = int(x16.size(0)), int(x16.size(1))
+    k = int(selected_experts.size(1))
+    R = T * k
+    final = torch.zeros((T, H), dtype=output_dtype, device=x16.device)
+    if R == 0:
+        return final
+    route = ext.build_grouped_route_device(selected_experts, num_experts, GROUPED_SEGMENT_M_TILE)
+    gti = route["grouped_token_indices"]
+    gsl = route["grouped_slots"]
+    expert_ids = route["expert_ids"]
+    seg = route["segment_offsets"]
+    prob = route["problem_offsets"]
+    # Launch bound only: every padded segment past the active ones is empty.
+    tile_bound = R // GROUPED_SEGMENT_M_TILE + min(num_experts, R) + 1
+    hid_g = ext.backbone_linear(x16, backbones["gate"], row_index=gti)
+    hid_u = ext.backbone_linear(x16, backbones["up"], row_index=gti)
+    pg, pu, pd = payloads["gate"], payloads["up"], payloads["down"]
+    uniform = bool(pg.get("_compact3_k64_groups_uniform", False) and pu.get("_compact3_k64_groups_uniform", False))
+    empty = x16.new_empty((0, 0))
+    g_out, u_out = ext.compact3_tris_precomputed_grouped_dual_forward_block_gr(
+        hid_g, hid_u, expert_ids, seg, prob, tile_bound,
+        pg["qweight1"], pg["qweight2_sparse"], pg["qweight2_sparse_prefix"], pg["q_gmap_gr_words"],
+        pg["q_gmap_gr_offsets"], pg["q_gmap_gr_meta"], pg["c_map"], pg["g_idx"], pg["col_pack3"], pg["row_pack3"],
+        pg["output_scale"], bool(pg["has_output_scale"]), pg["bias"] if pg["has_bias"] else empty,
+        pu["qweight1"], pu["qweight2_sparse"], pu["qweight2_sparse_prefix"], pu["q_gmap_gr_words"],
+        pu["q_gmap_gr_offsets"], pu["q_gmap_gr_meta"], pu["c_map"], pu["g_idx"], pu["col_pack3"], pu["row_pack3"],
+        pu["output_scale"], bool(pu["has_output_scale"]), pu["bias"] if pu["has_bias"] else empty, uniform)
+    mlp = F.silu(g_out) * u_out
+    hid_d = ext.backbone_linear(mlp, backbones["down"])
+    d_out = ext.compact3_tris_precomputed_grouped_forward_block_gr(
+        hid_d, expert_ids, seg, prob, tile_bound,
+        pd["qweight1"], pd["qweight2_sparse"], pd["qweight2_sparse_prefix"], pd["q_gmap_gr_words"],
+        pd["q_gmap_gr_offsets"], pd["q_gmap_gr_meta"], pd["c_map"], pd["g_idx"], pd["col_pack3"], pd["row_pack3"],
+        pd["output_scale"], bool(pd["has_output_scale"]), pd["bias"] if pd["has_bias"] else empty,
+        bool(pd["has_bias"]), bool(pd.get("_compact3_k64_groups_uniform", False)))
+    w16 = routing_weights.to(torch.float16)
+    contrib = (d_out * w16[gti, gsl].unsqueeze(-1)).to(output_dtype)
+    final.index_add_(0, gti, contrib)
+    if shared_expert is not None:
+        wg, wu, wd = shared_expert
+        final = final + F.linear(F.silu(F.linear(x16, wg)) * F.linear(x16, wu), wd).to(output_dtype)
+    return final
+
+
+class TrisSparseMoeBlock(nn.Module):
+    """Grouped-expert sparse MoE block (MixtralSparseMoeBlock / OlmoeSparseMoeBlock shape)."""
+
+    def __init__(self, hidden_size: int, num_experts: int, top_k: int, payloads: dict, backbones: dict,
+                 router_weight: torch.Tensor | None = None, renormalize: bool = True, shared_expert=None):
+        super().__init__()
+        self.hidden_dim = hidden_size
+        self.num_experts = num_experts
+        self.top_k = top_k
+        self.renormalize = renormalize
+        self.gate = nn.Linear(hidden_size, num_experts, bias=False)
+        if router_weight is not None:
+            self.gate.weight.data = router_weight
+        self.payloads = payloads
+        self.backbones = backbones
+        self.shared_expert = shared_expert
+
+    def forward_routed(self, hidden_states: torch.Tensor, router_logits: torch.Tensor) -> torch.Tensor:
+        """The block after the router: [T, H] activations and [T, E] logits -> [T, H]."""
+        output_dtype = hidden_states.dtype
+        weights, selected = route_topk(router_logits, self.top_k, self.renormalize)
+        x16 = hidden_states.to(torch.float16) if hidden_states.dtype == torch.bfloat16 else hidden_states
+        if x16.dtype != torch.float16 or x16.device.type != "cuda":
+            raise RuntimeError("grouped expert kernels require CUDA float16/bfloat16 hidden states")
+        return grouped_moe_forward(x16.contiguous(), weights, selected, self.payloads, self.backbones,
+                                   self.num_experts, output_dtype, self.shared_expert)
+
+    def forward(self, hidden_states: torch.Tensor):
+        batch, seq, hidden = hidden_states.shape
+        flat = hidden_states.view(-1, hidden)
+        router_logits = self.gate(flat)
+        out = self.forward_routed(flat, router_logits)
+        return out.reshape(batch, seq, hidden), router_logits

@@ -1,0 +1,501 @@
+"""Grouped expert runtime with the reference's Python API (``qlinear_cuda.py``), on the HIP library.
+
+Mirrors, for the grouped block-GR expert path:
+
+* ``build_grouped_route`` (``qlinear_cuda.py:1301-1378``) and its empty route
+  (``:1242-1255``);
+* ``run_grouped_structured_expert_forward`` (``:2131-2335``) and
+  ``run_grouped_structured_expert_pair_forward`` (``:2338-2634``);
+* ``build_grouped_precomputed_payload`` / payload resolution (``:1512-1682``);
+* ``ExpertSharedMatrix`` + ``QuantLinear`` in expert_compact3 mode (mode 5):
+  ``compute_shared_hidden`` (``:4454-4502``), ``forward_from_precomputed_hidden``
+  (``:4504-4560``), ``can_precompute_shared`` (``:4451``), block-GR packing
+  ``_pack_block_gr_gmap_tensor`` (``:3793-3859``).
+
+Differences that are deliberate: no CPU/dequant fallback (a missing HIP
+library raises ``TrisExtensionUnavailable``); the route's segment order within
+an expert is the stable flat order; the launch policy is this library's
+(fused GR decode for decode-sized segments, predecode + predecoded GEMM when
+segments are long), with no split-K since each workgroup covers all of K.
+Matrix-mode null-space compensation (``ns_mode == 2``) is not provided.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+import torch.nn as nn
+
+from . import ext
+from .packing import num_gr_blocks
+
+GROUPED_SEGMENT_M_TILE = 4
+BLOCK_GR_TILE_K = 64
+BLOCK_GR_TILE_OUT = 64
+BLOCK_GR_PACKED_ROWS = 2
+BLOCK_GR_WORDS_PER_BLOCK = 128
+BLOCK_GR_META_RAW_FLAG = 1 << 4
+BLOCK_GR_META_ONE_COUNT_SHIFT = 8
+BLOCK_GR_MAX_K = 7
+# Rows per segment above which the predecoded GEMM (one decode per block) beats
+# in-kernel decode (one decode per 16-row tile).
+PREDECODE_MIN_ROWS_PER_SEGMENT = 32
+_PREDECODE_MAX_BYTES = 256 * 1024 * 1024
+
+PAYLOAD_TENSOR_KEYS = ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "q_gmap_gr_words",
+                       "q_gmap_gr_offsets", "q_gmap_gr_meta", "c_map", "g_idx", "col_pack3", "row_pack3",
+                       "output_scale", "bias")
+
+
+# ------------------------------------------------------------------ payloads
+def payload_to_device(payload: dict, device, dtype=torch.float16) -> dict:
+    """Host (numpy) stacked payload -> device tensors with the reference's dtypes."""
+    out = {}
+    for key, val in payload.items():
+        if isinstance(val, np.ndarray):
+            if key in ("output_scale", "bias"):
+                out[key] = torch.from_numpy(np.ascontiguousarray(val)).to(device=device, dtype=dtype)
+            elif val.dtype == np.int64:
+                out[key] = torch.from_numpy(np.ascontiguousarray(val)).to(device=device, dtype=torch.int64)
+            else:
+                out[key] = torch.from_numpy(np.ascontiguousarray(val).astype(np.int32)).to(device=device)
+        else:
+            out[key] = val
+    return out
+
+
+def _payload_has_output_scale(payload: dict) -> bool:
+    scale = payload.get("output_scale")
+    if not isinstance(scale, torch.Tensor) or scale.numel() == 0:
+        return False
+    if "has_output_scale" in payload:
+        return bool(payload["has_output_scale"])
+    return not bool(torch.all(scale == 1).item())
+
+
+def _normalize_scalars(payload: dict) -> dict:
+    """Scalars stored as 1-element tensors become Python values (grouped_payload_sidecar.py:168-190)."""
+    for key in ("is_compact3", "compact3_use_block_gr", "has_output_scale", "has_bias", "_compact3_k64_groups_uniform"):
+        val = payload.get(key)
+        if isinstance(val, torch.Tensor) and val.numel() == 1:
+            payload[key] = bool(val.reshape(-1)[0].item())
+    return payload
+
+
+def _k64_uniform(payload: dict) -> bool:
+    if "_compact3_k64_groups_uniform" not in payload:
+        g = payload["g_idx"]
+        rank = int(g.size(1))
+        first = g[:, (torch.arange(rank, device=g.device) // 64) * 64]
+        payload["_compact3_k64_groups_uniform"] = bool(torch.equal(first, g))
+    return bool(payload["_compact3_k64_groups_uniform"])
+
+
+def resolve_grouped_precomputed_payload(payload_or_modules, device, dtype):
+    """qlinear_cuda.py:1639-1682: validate a payload dict or stack it from modules."""
+    if isinstance(payload_or_modules, dict):
+        payload = _normalize_scalars(payload_or_modules)
+        for key in ("is_compact3", "qweight1", "c_map", "g_idx", "output_scale", "has_bias"):
+            if key not in payload:
+                return None
+        if payload["qweight1"].device != torch.device(device) or payload["output_scale"].dtype != dtype:
+            return None
+        if not payload["is_compact3"] or not payload.get("compact3_use_block_gr", False):
+            return None
+        for key in ("qweight2_sparse", "qweight2_sparse_prefix", "q_gmap_gr_words", "q_gmap_gr_offsets",
+                    "q_gmap_gr_meta", "col_pack3", "row_pack3"):
+            if key not in payload:
+                return None
+        payload["has_output_scale"] = _payload_has_output_scale(payload)
+        _k64_uniform(payload)
+        return payload
+    return build_grouped_precomputed_payload(payload_or_modules, device, dtype)
+
+
+# --------------------------------------------------------------------- route
+def _empty_grouped_route(device):
+    empty_int = torch.empty((0,), device=device, dtype=torch.int32)
+    empty_long = torch.empty((0,), device=device, dtype=torch.long)
+    return {
+        "perm": empty_long,
+        "grouped_token_indices": empty_long,
+        "grouped_slots": empty_long,
+        "grouped_expert_ids": empty_int,
+        "expert_ids": empty_int,
+        "segment_offsets": torch.zeros((1,), device=device, dtype=torch.int32),
+        "problem_offsets": torch.zeros((1,), device=device, dtype=torch.int32),
+        "total_problem_tiles": torch.zeros((1,), device="cpu", dtype=torch.int64),
+        "total_problem_tiles_host": 0,
+    }
+
+
+def build_grouped_route(selected_experts: torch.Tensor, num_experts: int, m_tile: int = GROUPED_SEGMENT_M_TILE):
+    """qlinear_cuda.py:1301-1378 on the device route kernels.  Returns None for a non-2D input and
+    the empty route for an empty input or m_tile <= 0, as the reference does."""
+    if selected_experts.dim() != 2:
+        return None
+    if m_tile <= 0 or selected_experts.numel() == 0:
+        return _empty_grouped_route(selected_experts.device)
+    route = ext.build_grouped_route_device(selected_experts, int(num_experts), int(m_tile))
+    counts = route["counts"].to("cpu")
+    num_active, total = int(counts[0]), int(counts[1])
+    if num_active < 0:
+        raise RuntimeError("build_grouped_route: expert id outside [0, num_experts)")
+    return {
+        "perm": route["perm"],
+        "grouped_token_indices": route["grouped_token_indices"],
+        "grouped_slots": route["grouped_slots"],
+        "grouped_expert_ids": route["grouped_expert_ids"],
+        "expert_ids": route["expert_ids"][:num_active].contiguous(),
+        "segment_offsets": route["segment_offsets"][: num_active + 1].contiguous(),
+        "problem_offsets": route["problem_offsets"][: num_active + 1].contiguous(),
+        "total_problem_tiles": torch.tensor([total], dtype=torch.int64),
+        "total_problem_tiles_host": total,
+    }
+
+
+def _route_total_problem_tiles_host(route) -> int:
+    if "total_problem_tiles_host" in route:
+        return int(route["total_problem_tiles_host"])
+    return int(route["total_problem_tiles"].reshape(-1)[0].item())
+
+
+def _coerce_grouped_route(route_or_lengths, device, expert_ids=None):
+    """qlinear_cuda.py:1385-1406: a route dict, or per-expert segment lengths."""
+    if isinstance(route_or_lengths, dict):
+        return route_or_lengths
+    lengths = torch.as_tensor(route_or_lengths, dtype=torch.long).cpu()
+    if lengths.numel() == 0 or bool((lengths < 0).any()):
+        return _empty_grouped_route(device)
+    ids = (torch.arange(lengths.numel(), dtype=torch.int32) if expert_ids is None
+           else torch.as_tensor(expert_ids, dtype=torch.int32).cpu())
+    if ids.numel() != lengths.numel():
+        return _empty_grouped_route(device)
+    seg = torch.cat([torch.zeros(1, dtype=torch.long), torch.cumsum(lengths, 0)])
+    prob = torch.cat([torch.zeros(1, dtype=torch.long),
+                      torch.cumsum((lengths + GROUPED_SEGMENT_M_TILE - 1) // GROUPED_SEGMENT_M_TILE, 0)])
+    return {
+        "perm": torch.empty(0, dtype=torch.long, device=device),
+        "grouped_token_indices": torch.empty(0, dtype=torch.long, device=device),
+        "grouped_slots": torch.empty(0, dtype=torch.long, device=device),
+        "grouped_expert_ids": torch.repeat_interleave(ids, lengths).to(device=device, dtype=torch.int32),
+        "expert_ids": ids.to(device=device),
+        "segment_offsets": seg.to(device=device, dtype=torch.int32),
+        "problem_offsets": prob.to(device=device, dtype=torch.int32),
+        "total_problem_tiles": prob[-1:].to(torch.int64),
+        "total_problem_tiles_host": int(prob[-1]),
+    }
+
+
+# ------------------------------------------------------------ grouped forward
+def _use_predecode(batch: int, num_segments: int, payload: dict, has_scale: bool, has_bias: bool) -> bool:
+    if has_scale or has_bias or num_segments == 0:
+        return False
+    if batch < PREDECODE_MIN_ROWS_PER_SEGMENT * num_segments:
+        return False
+    rank = int(payload["g_idx"].size(1))
+    n = int(payload["qweight1"].size(2))
+    return num_segments * num_gr_blocks(rank, n) * BLOCK_GR_WORDS_PER_BLOCK * 4 <= _PREDECODE_MAX_BYTES
+
+
+def _predecode(payload: dict, route: dict, rank: int, n: int) -> torch.Tensor:
+    ids = route["expert_ids"]
+    nblk = num_gr_blocks(rank, n)
+    buf = torch.empty((ids.numel(), nblk, BLOCK_GR_WORDS_PER_BLOCK), dtype=torch.int32, device=ids.device)
+    return ext.compact3_tris_precomputed_grouped_block_gr_predecode(
+        buf, ids, payload["q_gmap_gr_words"], payload["q_gmap_gr_offsets"], payload["q_gmap_gr_meta"],
+        (rank + 31) // 32, n)
+
+
+def _check_ns_payload(ns_payload):
+    if ns_payload is None or isinstance(ns_payload, (list, tuple)):
+        return
+    if isinstance(ns_payload, dict) and ns_payload.get("ns_mode", "none") in ("matrix", 2):
+        raise NotImplementedError("matrix-mode null-space compensation is not provided by the TriS-MoE HIP library")
+
+
+def run_grouped_structured_expert_forward(payload_or_modules, hidden_grouped: torch.Tensor, x_grouped: torch.Tensor,
+                                          grouped_route_or_segment_lengths, expert_modules=None, expert_ids=None,
+                                          ns_payload=None, prefer_ns_fused_decode: bool = False):
+    """qlinear_cuda.py:2131-2335.  Returns fp16 [R, N] or None when the inputs are outside the
+    kernel contract (non-CUDA / non-fp16 / shape mismatch), as the reference does."""
+    if hidden_grouped.device.type != "cuda" or hidden_grouped.dtype != torch.float16:
+        return None
+    if x_grouped.device != hidden_grouped.device or x_grouped.dtype != hidden_grouped.dtype:
+        return None
+    if hidden_grouped.dim() != 2 or x_grouped.dim() != 2 or hidden_grouped.size(0) != x_grouped.size(0):
+        return None
+    route = _coerce_grouped_route(grouped_route_or_segment_lengths, hidden_grouped.device, expert_ids)
+    gti = route.get("grouped_token_indices")
+    if gti is not None and gti.numel() not in (0, hidden_grouped.size(0)):
+        return None
+    payload = resolve_grouped_precomputed_payload(payload_or_modules, hidden_grouped.device, hidden_grouped.dtype)
+    if payload is None:
+        return None
+    _check_ns_payload(ns_payload)
+    if expert_modules is None and not isinstance(payload_or_modules, dict):
+        expert_modules = payload_or_modules
+    defer_bias = bool(payload["has_bias"]) and (ns_payload is not None or expert_modules is not None)
+    has_bias_arg = bool(payload["has_bias"]) and not defer_bias
+    bias_arg = payload["bias"] if has_bias_arg else hidden_grouped.new_empty((0, 0))
+    has_scale = _payload_has_output_scale(payload)
+    batch = int(hidden_grouped.size(0))
+    rank = int(hidden_grouped.size(1))
+    n = int(payload["qweight1"].size(2))
+    total = _route_total_problem_tiles_host(route)
+    uniform = _k64_uniform(payload)
+    hidden_c = hidden_grouped.contiguous()
+    if _use_predecode(batch, int(route["expert_ids"].numel()), payload, has_scale, has_bias_arg):
+        decoded = _predecode(payload, route, rank, n)
+        out = ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
+            hidden_c, route["expert_ids"], route["segment_offsets"], route["problem_offsets"], total, decoded,
+            payload["qweight1"], payload["qweight2_sparse"], payload["qweight2_sparse_prefix"], payload["c_map"],
+            payload["g_idx"], payload["col_pack3"], payload["row_pack3"], uniform)
+    else:
+        out = ext.compact3_tris_precomputed_grouped_forward_block_gr(
+            hidden_c, route["expert_ids"], route["segment_offsets"], route["problem_offsets"], total,
+            payload["qweight1"], payload["qweight2_sparse"], payload["qweight2_sparse_prefix"],
+            payload["q_gmap_gr_words"], payload["q_gmap_gr_offsets"], payload["q_gmap_gr_meta"], payload["c_map"],
+            payload["g_idx"], payload["col_pack3"], payload["row_pack3"], payload["output_scale"], has_scale,
+            bias_arg, has_bias_arg, uniform)
+    if defer_bias:
+        out.add_(payload["bias"].index_select(0, route["grouped_expert_ids"].to(dtype=torch.long)))
+    return out
+
+
+def run_grouped_structured_expert_pair_forward(payload_or_modules_a, payload_or_modules_b, hidden_a_grouped,
+                                               hidden_b_grouped, x_grouped, grouped_route_or_segment_lengths,
+                                               expert_modules_a=None, expert_modules_b=None, expert_ids=None,
+                                               ns_payload_a=None, ns_payload_b=None):
+    """qlinear_cuda.py:2338-2634: gate and up projections sharing one route, one launch.
+    Returns (out_a, out_b) or (None, None) outside the kernel contract."""
+    for h in (hidden_a_grouped, hidden_b_grouped):
+        if h.device.type != "cuda" or h.dtype != torch.float16 or h.dim() != 2:
+            return None, None
+    if hidden_a_grouped.size(0) != hidden_b_grouped.size(0) or x_grouped.size(0) != hidden_a_grouped.size(0):
+        return None, None
+    route = _coerce_grouped_route(grouped_route_or_segment_lengths, hidden_a_grouped.device, expert_ids)
+    pa = resolve_grouped_precomputed_payload(payload_or_modules_a, hidden_a_grouped.device, hidden_a_grouped.dtype)
+    pb = resolve_grouped_precomputed_payload(payload_or_modules_b, hidden_b_grouped.device, hidden_b_grouped.dtype)
+    if pa is None or pb is None:
+        return None, None
+    _check_ns_payload(ns_payload_a)
+    _check_ns_payload(ns_payload_b)
+    if expert_modules_a is None and not isinstance(payload_or_modules_a, dict):
+        expert_modules_a = payload_or_modules_a
+    if expert_modules_b is None and not isinstance(payload_or_modules_b, dict):
+        expert_modules_b = payload_or_modules_b
+    defer_a = bool(pa["has_bias"]) and (ns_payload_a is not None or expert_modules_a is not None)
+    defer_b = bool(pb["has_bias"]) and (ns_payload_b is not None or expert_modules_b is not None)
+    empty = hidden_a_grouped.new_empty((0, 0))
+    bias_a = pa["bias"] if pa["has_bias"] and not defer_a else empty
+    bias_b = pb["bias"] if pb["has_bias"] and not defer_b else empty
+    scale_a = _payload_has_output_scale(pa)
+    scale_b = _payload_has_output_scale(pb)
+    batch = int(hidden_a_grouped.size(0))
+    total = _route_total_problem_tiles_host(route)
+    uniform = _k64_uniform(pa) and _k64_uniform(pb)
+    nseg = int(route["expert_ids"].numel())
+    ha = hidden_a_grouped.contiguous()
+    hb = hidden_b_grouped.contiguous()
+    if (_use_predecode(batch, nseg, pa, scale_a, bias_a.numel() > 0)
+            and _use_predecode(batch, nseg, pb, scale_b, bias_b.numel() > 0)):
+        da = _predecode(pa, route, int(ha.size(1)), int(pa["qweight1"].size(2)))
+        db = _predecode(pb, route, int(hb.size(1)), int(pb["qweight1"].size(2)))
+        out_a, out_b = ext.compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
+            ha, hb, route["expert_ids"], route["segment_offsets"], route["problem_offsets"], total,
+            da, pa["qweight1"], pa["qweight2_sparse"], pa["qweight2_sparse_prefix"], pa["c_map"], pa["g_idx"],
+            pa["col_pack3"], pa["row_pack3"], db, pb["qweight1"], pb["qweight2_sparse"],
+            pb["qweight2_sparse_prefix"], pb["c_map"], pb["g_idx"], pb["col_pack3"], pb["row_pack3"], uniform)
+    else:
+        out_a, out_b = ext.compact3_tris_precomputed_grouped_dual_forward_block_gr(
+            ha, hb, route["expert_ids"], route["segment_offsets"], route["problem_offsets"], total,
+            pa["qweight1"], pa["qweight2_sparse"], pa["qweight2_sparse_prefix"], pa["q_gmap_gr_words"],
+            pa["q_gmap_gr_offsets"], pa["q_gmap_gr_meta"], pa["c_map"], pa["g_idx"], pa["col_pack3"],
+            pa["row_pack3"], pa["output_scale"], scale_a, bias_a,
+            pb["qweight1"], pb["qweight2_sparse"], pb["qweight2_sparse_prefix"], pb["q_gmap_gr_words"],
+            pb["q_gmap_gr_offsets"], pb["q_gmap_gr_meta"], pb["c_map"], pb["g_idx"], pb["col_pack3"],
+            pb["row_pack3"], pb["output_scale"], scale_b, bias_b, uniform)
+    gexp = route["grouped_expert_ids"].to(dtype=torch.long)
+    if defer_a:
+        out_a.add_(pa["bias"].index_select(0, gexp))
+    if defer_b:
+        out_b.add_(pb["bias"].index_select(0, gexp))
+    return out_a, out_b
+
+
+# --------------------------------------------------------------- modules
+def pack_block_gr_gmap_tensor(packed: torch.Tensor, force_raw: bool = False, fixed_k=None, k_min=None, k_max=None):
+    """tools/rewrite_runtime_min_checkpoint.py:252-347 (and QuantLinear._pack_block_gr_gmap_tensor):
+    dense packed split bitmap [packed_rows, N] -> (words, offsets, meta) int32 tensors on packed.device."""
+    if fixed_k is not None:
+        if k_min is not None or k_max is not None:
+            raise ValueError("--blockgr-k cannot be combined with --blockgr-k-min/--blockgr-k-max")
+        if not 0 <= fixed_k <= BLOCK_GR_MAX_K:
+            raise ValueError(f"--blockgr-k must be in [0, {BLOCK_GR_MAX_K}], got {fixed_k}")
+        lo, hi = fixed_k, fixed_k
+    elif k_min is None and k_max is None:
+        lo, hi = 0, BLOCK_GR_MAX_K
+    elif k_min is None or k_max is None:
+        raise ValueError("--blockgr-k-min and --blockgr-k-max must be provided together")
+    else:
+        if not 0 <= k_min <= k_max <= BLOCK_GR_MAX_K:
+            raise ValueError(f"--blockgr-k-min/--blockgr-k-max must satisfy 0 <= min <= max <= {BLOCK_GR_MAX_K}")
+        lo, hi = k_min, k_max
+    if packed.numel() == 0:
+        empty = torch.zeros((0,), dtype=torch.int32, device=packed.device)
+        return empty, empty, empty
+    words, offsets, meta = ext.gr_encode(packed.detach().to("cpu", torch.int32), lo, hi, force_raw)
+    dev = packed.device
+    return (torch.from_numpy(words).to(dev), torch.from_numpy(offsets).to(dev), torch.from_numpy(meta).to(dev))
+
+
+class ExpertSharedMatrix(nn.Module):
+    """qlinear_cuda.py:2787-2968: the shared backbone SV [rank, in] of one (layer, projection)."""
+
+    def __init__(self, shared_sv: torch.Tensor):
+        super().__init__()
+        self.register_buffer("shared_sv", shared_sv.contiguous())
+
+    def get_shared_sv(self, device, dtype):
+        sv = self.shared_sv
+        if sv.device != torch.device(device) or sv.dtype != dtype:
+            sv = sv.to(device=device, dtype=dtype).contiguous()
+        return sv
+
+
+class QuantLinear(nn.Module):
+    """Expert compact3 linear (mode 5) with its shared backbone: W = B_e . SV.
+
+    Holds one expert's packed tensors (``expert_*`` buffers, qlinear_cuda.py:2971+) and its
+    block-GR split bitmap; ``forward(x) = forward_from_precomputed_hidden(compute_shared_hidden(x), x)``.
+    """
+
+    QUANT_TYPE = "hip"
+
+    def __init__(self, infeatures: int, outfeatures: int, rank: int, shared: ExpertSharedMatrix, bias=None,
+                 expert_input_scale=None):
+        super().__init__()
+        self.infeatures = infeatures
+        self.outfeatures = outfeatures
+        self.rank = rank
+        self._shared_matrix_module = shared
+        self._mode_host = 5
+        self._ns_mode_host = 1 if expert_input_scale is not None else 0
+        self.register_buffer("expert_input_scale", expert_input_scale)
+        self.register_buffer("bias", bias)
+        self.register_buffer("ns_vector_row", torch.ones(outfeatures, dtype=torch.float16))
+
+    def load_expert_payload(self, tensors: dict):
+        """Set the expert_* buffers from one expert's packed tensors (host numpy or torch)."""
+        for key in ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx", "col_pack3",
+                    "row_pack3"):
+            val = tensors[key]
+            t = torch.as_tensor(np.ascontiguousarray(val)) if isinstance(val, np.ndarray) else val
+            self.register_buffer("expert_" + key, t.clone())
+        if "gmap_dense" in tensors:
+            dense = torch.as_tensor(np.ascontiguousarray(tensors["gmap_dense"]))
+            words, offsets, meta = pack_block_gr_gmap_tensor(dense)
+        else:
+            words, offsets, meta = (torch.as_tensor(tensors[k]) for k in ("q_gmap_gr_words", "q_gmap_gr_offsets",
+                                                                           "q_gmap_gr_meta"))
+        self.register_buffer("expert_q_gmap_gr_words", words)
+        self.register_buffer("expert_q_gmap_gr_offsets", offsets)
+        self.register_buffer("expert_q_gmap_gr_meta", meta)
+        return self
+
+    def can_precompute_shared(self) -> bool:
+        return self._mode_host == 5 and self._shared_matrix_module is not None
+
+    def compute_shared_hidden(self, x: torch.Tensor):
+        """hidden = (x * s_in) . SV^T (qlinear_cuda.py:4454-4502, fp16 backbone branch)."""
+        if not self.can_precompute_shared():
+            return None
+        shape = x.shape[:-1]
+        xb = x.reshape(-1, x.shape[-1]).contiguous()
+        sv = self._shared_matrix_module.get_shared_sv(xb.device, xb.dtype)
+        if xb.shape[0] == 0:
+            return xb.new_empty((0, sv.shape[0])).reshape(shape + (sv.shape[0],))
+        scale = None
+        if self._ns_mode_host == 1:
+            scale = self.expert_input_scale.to(device=xb.device, dtype=xb.dtype).contiguous()
+        hidden = ext.backbone_linear(xb, sv, in_scale=scale)
+        return hidden.reshape(shape + (hidden.shape[-1],))
+
+    def _single_payload(self, device, dtype) -> dict:
+        key = (str(device), dtype)
+        cache = getattr(self, "_payload_cache", None)
+        if cache is not None and cache[0] == key:
+            return cache[1]
+        payload = build_grouped_precomputed_payload([self], device, dtype)
+        self._payload_cache = (key, payload)
+        return payload
+
+    def forward_from_precomputed_hidden(self, hidden: torch.Tensor, x_base: torch.Tensor):
+        """qlinear_cuda.py:4504-4560 for one expert: a one-segment grouped call."""
+        out_shape = hidden.shape[:-1] + (self.outfeatures,)
+        hf = hidden.reshape(-1, hidden.shape[-1]).contiguous()
+        xf = x_base.reshape(-1, x_base.shape[-1]).contiguous()
+        if hf.shape[0] == 0:
+            return hf.new_empty((0, self.outfeatures)).reshape(out_shape)
+        payload = self._single_payload(hf.device, hf.dtype)
+        # ns_vector_row is the payload's output_scale, applied in the kernel epilogue.
+        out = run_grouped_structured_expert_forward(payload, hf, xf, [hf.shape[0]])
+        if out is None:
+            raise RuntimeError("QuantLinear.forward_from_precomputed_hidden: grouped kernel rejected the inputs")
+        return out.reshape(out_shape)
+
+    def forward(self, x: torch.Tensor):
+        hidden = self.compute_shared_hidden(x)
+        return self.forward_from_precomputed_hidden(hidden, x)
+
+
+def build_grouped_precomputed_payload(modules, device, dtype):
+    """qlinear_cuda.py:1512-1636: stack per-expert buffers (zero-padding ragged qweight2_sparse and
+    GR words) into the grouped payload dict."""
+    if len(modules) == 0:
+        return None
+    for m in modules:
+        if not isinstance(m, QuantLinear) or m._mode_host != 5:
+            return None
+    dev = torch.device(device)
+
+    def stack(name, dt=torch.int32, pad_rows=False, pad_cols=False):
+        ts = [getattr(m, "expert_" + name).to(device=dev, dtype=dt) for m in modules]
+        if pad_rows:
+            rows = max(int(t.shape[0]) for t in ts)
+            ts = [torch.nn.functional.pad(t, (0, 0, 0, rows - int(t.shape[0]))) for t in ts]
+        if pad_cols:
+            cols = max(int(t.shape[0]) for t in ts)
+            ts = [torch.nn.functional.pad(t, (0, cols - int(t.shape[0]))) for t in ts]
+        return torch.stack(ts, 0).contiguous()
+
+    output_scale = torch.stack([m.ns_vector_row.to(device=dev, dtype=dtype) for m in modules], 0).contiguous()
+    if output_scale.numel() > 0 and bool(torch.all(output_scale == 0).item()):
+        output_scale = torch.ones_like(output_scale)
+    has_bias = any(m.bias is not None for m in modules)
+    bias = None
+    if has_bias:
+        bias = torch.stack([m.bias.to(device=dev, dtype=dtype) if m.bias is not None
+                            else torch.zeros(m.outfeatures, device=dev, dtype=dtype) for m in modules], 0)
+    payload = {
+        "is_compact3": True,
+        "qweight1": stack("qweight1"),
+        "qweight2_sparse": stack("qweight2_sparse", pad_rows=True),
+        "qweight2_sparse_prefix": stack("qweight2_sparse_prefix"),
+        "compact3_use_block_gr": True,
+        "q_gmap_gr_words": stack("q_gmap_gr_words", pad_cols=True),
+        "q_gmap_gr_offsets": stack("q_gmap_gr_offsets"),
+        "q_gmap_gr_meta": stack("q_gmap_gr_meta"),
+        "c_map": stack("c_map"),
+        "g_idx": stack("g_idx"),
+        "col_pack3": stack("col_pack3", torch.int64),
+        "row_pack3": stack("row_pack3", torch.int64),
+        "output_scale": output_scale,
+        "has_output_scale": not bool(torch.all(output_scale == 1).item()),
+        "bias": bias,
+        "has_bias": has_bias,
+    }
+    _k64_uniform(payload)
+    return payload

@@ -1,0 +1,430 @@
+"""CPU oracle for the TriS-MoE grouped expert dequant-GEMM path.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this package, and only as the
+checker (or the timed CPU baseline), never as the product path.  The product
+(``neurips26-tris-moe_amd``) never imports it and fails loudly when its HIP
+library is missing.
+
+Parts and the reference code each one restates (paths relative to the
+reference checkout):
+
+* GR codec (C, ``tris_oracle.c``): encoder ``qlinear_cuda.py:3763-3859`` /
+  ``tools/rewrite_runtime_min_checkpoint.py:170-347``; decoder
+  ``TriSMoE_cuda_kernel.cu:321-502``; predecode layout ``:4683-4718``.
+* Bit packing (numpy): ``utils/pack_utils.py:6-64``.
+* Compact3 weight reconstruction (numpy, exact IEEE fp16):
+  ``TriSMoE_cuda_kernel.cu:665-774`` (per-weight formula) and ``:830-853``
+  (row-pack group selection); agrees with the CPU fallback
+  ``qlinear_cuda.py:4200-4236`` for finite scale products.
+* Grouped GEMM + epilogue (numpy, fp32 accumulation of the exact fp16 weights):
+  ``TriSMoE_cuda_kernel.cu:4500-4681`` (segment kernel arithmetic and
+  epilogue), segment search ``:3874-3904``.
+* Route metadata (numpy): ``TriSMoE_cuda.cpp:741-793`` /
+  ``qlinear_cuda.py:1301-1378``.
+* MoE block (numpy): ``modeling_mixtral.py:406-608`` (grouped forward) and
+  ``modeling_olmoe.py:1053-1058`` (optional top-k renormalisation).
+
+How each part is pinned (see tests/test_oracle_*.py): hand-derived
+known-answer GR blocks, closed-form Rice lengths and k choice, encode/decode
+round trips on random and edge-case bitmaps, agreement of the reference's
+two decoder paths (general and k==3); fp16 products checked against integer
+significand arithmetic; the dequantised matrix checked against the reference
+CPU formula (masks and per-term products, ``qlinear_cuda.py:4213-4236``);
+routes by brute force; layer output against a float64 dense evaluation.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "libtris_oracle.so"
+
+GR_TILE_OUT = 64
+GR_PACKED_ROWS = 2
+GR_WORDS = 128
+GR_META_RAW = 16
+GR_META_ONES_SHIFT = 8
+GR_MAX_K = 7
+
+_lib = None
+
+
+def _load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not _LIB_PATH.exists():
+        raise RuntimeError(
+            f"oracle library {_LIB_PATH} is missing; build it with `make -C oracle` "
+            "(or __graft_entry__.build())"
+        )
+    lib = ctypes.CDLL(str(_LIB_PATH))
+    P = ctypes.c_void_p
+    i32 = ctypes.c_int
+    lib.orc_gr_encode.restype = ctypes.c_int64
+    lib.orc_gr_encode.argtypes = [P, i32, i32, i32, i32, i32, P, P, P]
+    lib.orc_rice_bits.restype = ctypes.c_int64
+    lib.orc_rice_bits.argtypes = [P, i32, i32]
+    lib.orc_rice_encode.restype = i32
+    lib.orc_rice_encode.argtypes = [P, i32, i32, P, i32]
+    lib.orc_gr_decode_block_impl.restype = None
+    lib.orc_gr_decode_block_impl.argtypes = [P, P, P, i32, i32, P]
+    lib.orc_gr_decode_dense.restype = None
+    lib.orc_gr_decode_dense.argtypes = [P, P, P, i32, i32, P]
+    lib.orc_gr_predecode.restype = None
+    lib.orc_gr_predecode.argtypes = [P, P, P, i32, i32, P, i32, P]
+    _lib = lib
+    return lib
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a), dtype=np.int32)
+
+
+def num_gr_blocks(packed_rows: int, n: int) -> int:
+    return -(-packed_rows // GR_PACKED_ROWS) * -(-n // GR_TILE_OUT)
+
+
+# ----------------------------------------------------------------- GR codec
+def gr_encode(packed, kmin: int = 0, kmax: int = GR_MAX_K, force_raw: bool = False):
+    """Dense packed bitmap [packed_rows, n] int32 -> (words, offsets, meta)."""
+    packed = _i32(packed)
+    rows, n = packed.shape
+    nblk = num_gr_blocks(rows, n)
+    words = np.zeros(max(nblk * GR_WORDS, 1), dtype=np.int32)
+    offsets = np.zeros(nblk + 1, dtype=np.int32)
+    meta = np.zeros(nblk, dtype=np.int32)
+    total = _load().orc_gr_encode(_ptr(packed), rows, n, kmin, kmax, int(force_raw), _ptr(words), _ptr(offsets), _ptr(meta))
+    return words[:total].copy(), offsets, meta
+
+
+def rice_bits(runs, k: int) -> int:
+    runs = _i32(runs)
+    return int(_load().orc_rice_bits(_ptr(runs), runs.size, k))
+
+
+def rice_encode(runs, k: int) -> np.ndarray:
+    runs = _i32(runs)
+    cap = int(rice_bits(runs, k) + 31) // 32 + 1
+    out = np.zeros(cap, dtype=np.uint32)
+    nw = _load().orc_rice_encode(_ptr(runs), runs.size, k, _ptr(out), cap)
+    return out[:nw].copy()
+
+
+def gr_decode_block(words, offsets, meta, block_idx: int, k3_fast_path: bool = True) -> np.ndarray:
+    words, offsets, meta = _i32(words), _i32(offsets), _i32(meta)
+    if words.size == 0:
+        words = np.zeros(1, dtype=np.int32)
+    out = np.zeros(GR_WORDS, dtype=np.uint32)
+    _load().orc_gr_decode_block_impl(_ptr(words), _ptr(offsets), _ptr(meta), block_idx, int(k3_fast_path), _ptr(out))
+    return out
+
+
+def gr_decode_dense(words, offsets, meta, packed_rows: int, n: int) -> np.ndarray:
+    words, offsets, meta = _i32(words), _i32(offsets), _i32(meta)
+    if words.size == 0:
+        words = np.zeros(1, dtype=np.int32)
+    dense = np.zeros((packed_rows, n), dtype=np.int32)
+    _load().orc_gr_decode_dense(_ptr(words), _ptr(offsets), _ptr(meta), packed_rows, n, _ptr(dense))
+    return dense
+
+
+def gr_predecode(words2d, offsets2d, meta2d, expert_ids, nblk: int) -> np.ndarray:
+    """[E, Wmax] stacked payload -> [A, nblk, 128] int32 (reference predecode layout)."""
+    words2d, offsets2d, meta2d, expert_ids = _i32(words2d), _i32(offsets2d), _i32(meta2d), _i32(expert_ids)
+    stride = words2d.shape[1] if words2d.ndim == 2 else 0
+    if words2d.size == 0:
+        words2d = np.zeros((1, 1), dtype=np.int32)
+    out = np.zeros((expert_ids.size, nblk, GR_WORDS), dtype=np.int32)
+    _load().orc_gr_predecode(_ptr(words2d), _ptr(offsets2d), _ptr(meta2d), stride, nblk, _ptr(expert_ids), expert_ids.size, _ptr(out))
+    return out
+
+
+# ------------------------------------------------------------- bit packing
+def pack_bool_vector(values) -> np.ndarray:
+    """pack_utils.py:6-16: bit i of word i//32."""
+    v = np.asarray(values, dtype=bool).ravel()
+    nwords = -(-v.size // 32)
+    padded = np.zeros(nwords * 32, dtype=np.uint64)
+    padded[: v.size] = v
+    shifts = np.arange(32, dtype=np.uint64)
+    words = (padded.reshape(nwords, 32) << shifts).sum(axis=1).astype(np.uint32)
+    return words.view(np.int32)
+
+
+def pack_bool_matrix(matrix) -> np.ndarray:
+    """pack_utils.py:19-29: [rows=N, cols=K] bool -> [ceil(K/32), N] int32, bit k&31."""
+    m = np.asarray(matrix, dtype=bool)
+    n, k = m.shape
+    nwords = -(-k // 32)
+    padded = np.zeros((nwords * 32, n), dtype=np.uint64)
+    padded[:k] = m.T
+    shifts = np.arange(32, dtype=np.uint64).reshape(1, 32, 1)
+    words = (padded.reshape(nwords, 32, n) << shifts).sum(axis=1).astype(np.uint32)
+    return words.view(np.int32)
+
+
+def unpack_bool_matrix(packed, ncols: int) -> np.ndarray:
+    """Inverse of pack_bool_matrix -> [N, ncols] bool."""
+    p = np.asarray(packed).astype(np.uint32)
+    rows, n = p.shape
+    bits = (p[:, None, :] >> np.arange(32, dtype=np.uint32).reshape(1, 32, 1)) & 1
+    return bits.reshape(rows * 32, n)[:ncols].T.astype(bool)
+
+
+def unpack_bool_vector(packed, ncols: int) -> np.ndarray:
+    p = np.asarray(packed).astype(np.uint32).ravel()
+    bits = (p[:, None] >> np.arange(32, dtype=np.uint32)) & 1
+    return bits.reshape(-1)[:ncols].astype(bool)
+
+
+def sparse_prefix(active_cols) -> np.ndarray:
+    """pack_utils.py:39-52: prefix[r] = #active columns with k < 32r."""
+    a = np.asarray(active_cols, dtype=bool).ravel()
+    rows = -(-a.size // 32)
+    padded = np.zeros(rows * 32, dtype=np.int64)
+    padded[: a.size] = a
+    return np.concatenate([[0], np.cumsum(padded.reshape(rows, 32).sum(axis=1))]).astype(np.int32)
+
+
+def pack_sparse_bool_matrix(matrix, active_cols) -> np.ndarray:
+    """pack_utils.py:32-36: pack only the active columns (compacted)."""
+    m = np.asarray(matrix, dtype=bool)
+    a = np.asarray(active_cols, dtype=bool)
+    if a.size == 0 or not a.any():
+        return np.zeros((0, m.shape[0]), dtype=np.int32)
+    return pack_bool_matrix(m[:, a])
+
+
+def pack_half4(first, second, third, fourth) -> np.ndarray:
+    """pack_utils.py:55-64: four fp16 halves at bits 0/16/32/48 of an int64."""
+    def bits(x):
+        return np.asarray(x, dtype=np.float16).view(np.uint16).astype(np.uint64)
+    out = bits(first) | (bits(second) << np.uint64(16)) | (bits(third) << np.uint64(32)) | (bits(fourth) << np.uint64(48))
+    return out.view(np.int64)
+
+
+def unpack_half4(packed):
+    p = np.asarray(packed).view(np.uint64) if np.asarray(packed).dtype == np.int64 else np.asarray(packed, dtype=np.int64).view(np.uint64)
+    return tuple(((p >> np.uint64(s)) & np.uint64(0xFFFF)).astype(np.uint16).view(np.float16) for s in (0, 16, 32, 48))
+
+
+# ----------------------------------------------------- compact3 dequant
+def f16_mul(a, b) -> np.ndarray:
+    """IEEE fp16 product, round to nearest even (exact in fp32, then one rounding)."""
+    return (np.asarray(a, dtype=np.float16).astype(np.float32) * np.asarray(b, dtype=np.float16).astype(np.float32)).astype(np.float16)
+
+
+def f16_add(a, b) -> np.ndarray:
+    """IEEE fp16 sum, round to nearest even (fp32 has 24 >= 2*11+2 bits, so the double rounding is innocuous)."""
+    return (np.asarray(a, dtype=np.float16).astype(np.float32) + np.asarray(b, dtype=np.float16).astype(np.float32)).astype(np.float16)
+
+
+def dequant_compact3(qweight1, qweight2_sparse, qweight2_sparse_prefix, gmap_dense, c_map, g_idx, col_pack3, row_pack3,
+                     rank: int, uniform_k64_groups: bool = False) -> np.ndarray:
+    """Exact fp16 weights [N, rank] of one expert (TriSMoE_cuda_kernel.cu:665-774, :830-853).
+
+    gmap_dense is the dense packed split bitmap [ceil(rank/32), N] (GR-decoded).
+    With uniform_k64_groups every k of a 64-wide tile uses the group of the
+    tile's first column (select_compact3_row_pack<true>); otherwise each k
+    uses g_idx[k], and an out-of-range group gives a zero row pack.
+    """
+    q1 = np.asarray(qweight1).astype(np.uint32)
+    n = q1.shape[1]
+    K = rank
+    ks = np.arange(K)
+    rows = ks >> 5
+    bits = (ks & 31).astype(np.uint32)
+    cmap_w = np.asarray(c_map).astype(np.uint32).ravel()
+    salient = ((cmap_w[rows] >> bits) & 1).astype(bool)                      # [K]
+    sign1 = ((q1[rows, :] >> bits[:, None]) & 1).astype(bool).T                # [N, K]
+    gm = np.asarray(gmap_dense).astype(np.uint32)
+    large = ((gm[rows, :] >> bits[:, None]) & 1).astype(bool).T                # [N, K]
+
+    # qweight2 sparse index: prefix[k/32] + popc(c_map_word & low_mask(k&31))  (kernel.cu:599-616)
+    low = np.where(bits == 0, np.uint32(0), (np.uint32(1) << bits) - np.uint32(1)).astype(np.uint32)
+    masked = cmap_w[rows] & low
+    popc = np.array([bin(int(v)).count("1") for v in masked], dtype=np.int64)
+    sidx = np.asarray(qweight2_sparse_prefix).astype(np.int64)[rows] + popc   # [K]
+    q2 = np.asarray(qweight2_sparse).astype(np.uint32)
+    sign2 = np.zeros((n, K), dtype=bool)
+    sal_k = np.nonzero(salient)[0]
+    if sal_k.size:
+        srow = sidx[sal_k] >> 5
+        sbit = (sidx[sal_k] & 31).astype(np.uint32)
+        sign2[:, sal_k] = ((q2[srow, :] >> sbit[:, None]) & 1).astype(bool).T
+
+    gi = np.asarray(g_idx).astype(np.int64).ravel()
+    if uniform_k64_groups:
+        gi = gi[(ks // 64) * 64]
+    rp = np.asarray(row_pack3).astype(np.int64)                                  # [N, G]
+    G = rp.shape[1]
+    valid = (gi >= 0) & (gi < G)
+    rpk = np.where(valid[None, :], rp[:, np.clip(gi, 0, max(G - 1, 0))] if G > 0 else 0, 0)  # [N, K]
+    r0, r1, r2, r3 = unpack_half4(rpk)
+    c0, c1, c2, c3 = unpack_half4(np.asarray(col_pack3).astype(np.int64).ravel())
+
+    t1 = f16_mul(c0[None, :], r0)
+    t1 = np.where(sign1, t1, -t1)
+    t2 = f16_mul(c1[None, :], r1)
+    t2 = np.where(sign2, t2, -t2)
+    w_sal = f16_add(t1, t2)
+    w_ns = np.where(large, f16_mul(c2[None, :], r2), f16_mul(c3[None, :], r3))
+    w_ns = np.where(sign1, w_ns, -w_ns)
+    return np.where(salient[None, :], w_sal, w_ns).astype(np.float16)
+
+
+def expert_slice(payload: dict, e: int) -> dict:
+    return {k: (v[e] if isinstance(v, np.ndarray) and v.ndim >= 1 and k != "__scalar__" else v) for k, v in payload.items()}
+
+
+def dequant_grouped_expert(payload: dict, e: int, uniform_k64_groups: bool | None = None) -> np.ndarray:
+    """Decode the expert's GR bitmap and reconstruct its fp16 weights [N, rank]."""
+    rank = int(payload["g_idx"].shape[1])
+    n = int(payload["qweight1"].shape[2])
+    packed_rows = -(-rank // 32)
+    nblk = num_gr_blocks(packed_rows, n)
+    gmap = gr_decode_dense(payload["q_gmap_gr_words"][e], payload["q_gmap_gr_offsets"][e][: nblk + 1],
+                           payload["q_gmap_gr_meta"][e][:nblk], packed_rows, n)
+    if uniform_k64_groups is None:
+        uniform_k64_groups = bool(payload.get("_compact3_k64_groups_uniform", False))
+    return dequant_compact3(payload["qweight1"][e], payload["qweight2_sparse"][e], payload["qweight2_sparse_prefix"][e],
+                            gmap, payload["c_map"][e], payload["g_idx"][e], payload["col_pack3"][e], payload["row_pack3"][e],
+                            rank, uniform_k64_groups)
+
+
+# --------------------------------------------------------- grouped GEMM
+def grouped_forward(payload: dict, hidden, expert_ids, segment_offsets, uniform_k64_groups: bool | None = None,
+                    weight_cache: dict | None = None) -> np.ndarray:
+    """out[R, N] fp16: per segment, fp32-accumulated hidden @ W_e^T, then the
+    reference epilogue fp16(acc * scale + bias) (TriSMoE_cuda_kernel.cu:4662-4680).
+    Segments with a negative expert slot produce zeros."""
+    hidden = np.asarray(hidden, dtype=np.float16)
+    n = int(payload["qweight1"].shape[2])
+    out = np.zeros((hidden.shape[0], n), dtype=np.float16)
+    has_scale = bool(payload.get("has_output_scale", False))
+    has_bias = bool(payload.get("has_bias", False))
+    seg = np.asarray(segment_offsets).astype(np.int64)
+    cache = weight_cache if weight_cache is not None else {}
+    for s, e in enumerate(np.asarray(expert_ids).astype(np.int64)):
+        r0, r1 = int(seg[s]), int(seg[s + 1])
+        if r1 <= r0:
+            continue
+        if e < 0:
+            out[r0:r1] = 0
+            continue
+        if e not in cache:
+            cache[e] = dequant_grouped_expert(payload, int(e), uniform_k64_groups).astype(np.float32)
+        acc = hidden[r0:r1].astype(np.float32) @ cache[e].T
+        if has_scale:
+            acc = acc * np.asarray(payload["output_scale"][e], dtype=np.float16).astype(np.float32)[None, :]
+        if has_bias:
+            acc = acc + np.asarray(payload["bias"][e], dtype=np.float16).astype(np.float32)[None, :]
+        out[r0:r1] = acc.astype(np.float16)
+    return out
+
+
+# ------------------------------------------------------------------ route
+def build_route(selected_experts, num_experts: int, m_tile: int = 4) -> dict:
+    """TriSMoE_cuda.cpp:741-793.  The permutation is the stable argsort of the
+    flattened expert ids (the reference uses an unstable sort; any order within
+    a segment gives the same per-row results, so stability is this oracle's
+    choice and the product path is required to match it)."""
+    sel = np.asarray(selected_experts).astype(np.int64)
+    t, k = sel.shape
+    flat = sel.reshape(-1)
+    perm = np.argsort(flat, kind="stable").astype(np.int64)
+    grouped = flat[perm]
+    counts = np.bincount(grouped, minlength=num_experts) if flat.size else np.zeros(num_experts, dtype=np.int64)
+    active = np.nonzero(counts > 0)[0]
+    seg_len = counts[active]
+    seg = np.concatenate([[0], np.cumsum(seg_len)]).astype(np.int32)
+    prob = np.concatenate([[0], np.cumsum((seg_len + m_tile - 1) // m_tile)]).astype(np.int64)
+    return {
+        "perm": perm,
+        "grouped_token_indices": perm // max(k, 1),
+        "grouped_slots": perm % max(k, 1),
+        "grouped_expert_ids": grouped.astype(np.int32),
+        "expert_ids": active.astype(np.int32),
+        "segment_offsets": seg,
+        "problem_offsets": prob.astype(np.int32),
+        "total_problem_tiles": int(prob[-1]),
+    }
+
+
+# ---------------------------------------------------------------- MoE block
+def silu_f16(x) -> np.ndarray:
+    x32 = np.asarray(x, dtype=np.float16).astype(np.float32)
+    return (x32 / (1.0 + np.exp(-x32))).astype(np.float16)
+
+
+def linear_f16(x, w) -> np.ndarray:
+    """fp16 F.linear with fp32 accumulation: fp16(x @ w^T)."""
+    return (np.asarray(x, dtype=np.float16).astype(np.float32) @ np.asarray(w, dtype=np.float16).astype(np.float32).T).astype(np.float16)
+
+
+def route_topk(router_logits, top_k: int, renormalize: bool = True):
+    """softmax(fp32) -> top-k -> optional renorm (modeling_mixtral.py:548-551)."""
+    lg = np.asarray(router_logits, dtype=np.float32)
+    p = np.exp(lg - lg.max(axis=1, keepdims=True))
+    p = p / p.sum(axis=1, keepdims=True)
+    idx = np.argsort(-p, axis=1, kind="stable")[:, :top_k]
+    w = np.take_along_axis(p, idx, axis=1)
+    if renormalize:
+        w = w / w.sum(axis=1, keepdims=True)
+    return w.astype(np.float32), idx.astype(np.int64)
+
+
+def moe_layer(x_f16, routing_weights, selected_experts, payloads: dict, backbones: dict, num_experts: int,
+              shared_expert=None, weight_caches: dict | None = None) -> np.ndarray:
+    """Grouped MoE block (modeling_mixtral.py:406-537) with fp16 tensors between
+    stages and fp32 accumulation inside every product; returns fp32 [T, H]
+    (the caller rounds to the output dtype).
+
+    payloads: {"gate","up","down"} stacked grouped payloads; backbones: the
+    matching fp16 shared matrices SV [rank, in].  routing_weights are cast to
+    fp16 as the reference does (modeling_mixtral.py:555).  shared_expert, if
+    given, is (w_gate [I,H], w_up [I,H], w_down [H,I]) fp16 added unrouted.
+    """
+    caches = weight_caches if weight_caches is not None else {"gate": {}, "up": {}, "down": {}}
+    x = np.asarray(x_f16, dtype=np.float16)
+    t = x.shape[0]
+    route = build_route(selected_experts, num_experts)
+    gti = route["grouped_token_indices"]
+    gsl = route["grouped_slots"]
+    rw16 = np.asarray(routing_weights, dtype=np.float32).astype(np.float16)
+    x_g = x[gti]
+    hid_g = linear_f16(x, backbones["gate"])[gti]
+    hid_u = linear_f16(x, backbones["up"])[gti]
+    g_out = grouped_forward(payloads["gate"], hid_g, route["expert_ids"], route["segment_offsets"], weight_cache=caches["gate"])
+    u_out = grouped_forward(payloads["up"], hid_u, route["expert_ids"], route["segment_offsets"], weight_cache=caches["up"])
+    mlp = (silu_f16(g_out).astype(np.float32) * u_out.astype(np.float32)).astype(np.float16)
+    hid_d = linear_f16(mlp, backbones["down"])
+    d_out = grouped_forward(payloads["down"], hid_d, route["expert_ids"], route["segment_offsets"], weight_cache=caches["down"])
+    contrib = (d_out.astype(np.float32) * rw16[gti, gsl].astype(np.float32)[:, None]).astype(np.float16)
+    out = np.zeros((t, x.shape[1]), dtype=np.float32)
+    np.add.at(out, gti, contrib.astype(np.float32))
+    del x_g
+    if shared_expert is not None:
+        wg, wu, wd = shared_expert
+        sg = linear_f16(x, wg)
+        su = linear_f16(x, wu)
+        smlp = (silu_f16(sg).astype(np.float32) * su.astype(np.float32)).astype(np.float16)
+        out = out + linear_f16(smlp, wd).astype(np.float32)
+    return out
+
+
+def bf16_round(x) -> np.ndarray:
+    """fp32 -> bf16 (round to nearest even) -> fp32, for comparing bf16 outputs."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return rounded.astype(np.uint32).view(np.float32)

@@ -1,0 +1,390 @@
+"""GPU parity of the HIP path against the CPU oracle (run on the MI355X box: -m gpu).
+
+Integer work (GR decode, predecode, route, dequantised fp16 weights) must be
+bit-exact; fp16 GEMM outputs and layer outputs must be within
+max-abs 2e-2 and relative-L2 1e-3 of the oracle.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from gr_cases import (block_from_positions, case_expected_words, case_positions, load_known_answers,
+                      multi_block_dense, random_bitmap, structured_bitmap)
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+REL_L2 = 1e-3
+
+
+def note(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def assert_close(got, want, what):
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    assert np.isfinite(got).all(), what
+    err = got - want
+    max_abs = float(np.abs(err).max()) if err.size else 0.0
+    denom = float(np.linalg.norm(want))
+    rel = float(np.linalg.norm(err)) / denom if denom > 0 else float(np.linalg.norm(err))
+    assert max_abs <= MAX_ABS and rel <= REL_L2, f"{what}: max_abs={max_abs:.3g} rel_l2={rel:.3g}"
+
+
+def t_i32(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(dev)
+
+
+def stacked_gr(oracle_mod, denses):
+    coded = [oracle_mod.gr_encode(d) for d in denses]
+    width = max(1, max(c[0].size for c in coded))
+    words = np.zeros((len(denses), width), dtype=np.int32)
+    for e, c in enumerate(coded):
+        words[e, : c[0].size] = c[0]
+    return words, np.stack([c[1] for c in coded]), np.stack([c[2] for c in coded])
+
+
+# --------------------------------------------------------------- GR decode
+def test_gr_decode_known_answers(tris, oracle_mod, cuda):
+    ext = tris["ext"]
+    kats = load_known_answers()
+    for case in kats["single_block"]:
+        note(f"gr kat {case['name']}")
+        dense = block_from_positions(case_positions(case))
+        words = case_expected_words(case, dense)
+        if words.size == 0:
+            words = np.zeros(1, dtype=np.int32)
+        got = ext.gr_decode_dense(t_i32(words[None], cuda), t_i32([[0, case_expected_words(case, dense).size]], cuda),
+                                  t_i32([[case["meta"]]], cuda), t_i32([0], cuda), 2, 64)
+        np.testing.assert_array_equal(got[0].cpu().numpy(), dense, err_msg=case["name"])
+    for case in kats["multi_block"]:
+        note(f"gr kat {case['name']}")
+        dense = multi_block_dense(case)
+        got = ext.gr_decode_dense(t_i32([case["words"]], cuda), t_i32([case["offsets"]], cuda),
+                                  t_i32([case["meta"]], cuda), t_i32([0], cuda), case["packed_rows"],
+                                  case["outfeatures"])
+        np.testing.assert_array_equal(got[0].cpu().numpy(), dense)
+
+
+@pytest.mark.parametrize("p", [0.0, 0.05, 0.15, 0.3, 0.6, 0.97])
+def test_gr_decode_random_bit_exact(tris, oracle_mod, cuda, p):
+    note(f"gr random p={p}")
+    rng = np.random.default_rng(int(p * 1000) + 1)
+    shape = (16, 448)
+    denses = [random_bitmap(rng, *shape, p) for _ in range(3)]
+    words, offsets, meta = stacked_gr(oracle_mod, denses)
+    got = tris["ext"].gr_decode_dense(t_i32(words, cuda), t_i32(offsets, cuda), t_i32(meta, cuda),
+                                      t_i32([2, 0, 1, 2], cuda), *shape).cpu().numpy()
+    for i, e in enumerate([2, 0, 1, 2]):
+        np.testing.assert_array_equal(got[i], denses[e])
+
+
+@pytest.mark.parametrize("kind", ["full", "corners", "stripes", "sparse_long_runs"])
+def test_gr_decode_structured_and_padded(tris, oracle_mod, cuda, kind):
+    note(f"gr structured {kind}")
+    dense = structured_bitmap(kind, 9, 131, np.random.default_rng(5))
+    for kmin, kmax in ((0, 7), (3, 3), (7, 7), (0, 0)):
+        words, offsets, meta = stacked_gr(oracle_mod, [dense])
+        if (kmin, kmax) != (0, 7):
+            w, o, m = oracle_mod.gr_encode(dense, kmin, kmax)
+            words, offsets, meta = (w[None] if w.size else np.zeros((1, 1), np.int32)), o[None], m[None]
+        got = tris["ext"].gr_decode_dense(t_i32(words, cuda), t_i32(offsets, cuda), t_i32(meta, cuda),
+                                          t_i32([0], cuda), 9, 131)
+        np.testing.assert_array_equal(got[0].cpu().numpy(), dense)
+
+
+@pytest.mark.parametrize("k", list(range(16)))
+def test_gr_decode_malformed_streams_follow_reference(tris, oracle_mod, cuda, k):
+    """one_count disagreeing with the stream, unterminated runs, stray bits, k > 7: the GPU decoder
+    reproduces the reference decoder exactly (serial rules)."""
+    note(f"gr malformed k={k}")
+    rng = np.random.default_rng(500 + k)
+    nblk = 24
+    words, offsets, meta = [], [0], []
+    for b in range(nblk):
+        nw = int(rng.integers(0, 150))
+        w = rng.integers(-2**31, 2**31, size=nw, dtype=np.int64).astype(np.int32)
+        if b % 3 == 0 and nw:
+            w[-(nw // 2 + 1):] = 0
+        if b % 4 == 1:
+            w = (w & np.int32(0x11111111)).astype(np.int32)
+        words.extend(w.tolist())
+        offsets.append(len(words))
+        meta.append(k | (int(rng.integers(0, 700)) << 8) if b % 7 else 16)
+    words_a = np.asarray(words if words else [0], dtype=np.int32)[None]
+    offsets_a = np.asarray(offsets, dtype=np.int32)[None]
+    meta_a = np.asarray(meta, dtype=np.int32)[None]
+    packed_rows, n = 2 * 4, 64 * 6  # 4 k-blocks x 6 out-blocks = 24 blocks
+    want = oracle_mod.gr_predecode(words_a, offsets_a, meta_a, np.array([0]), nblk)
+    buf = torch.zeros((1, nblk, 128), dtype=torch.int32, device=cuda)
+    got = tris["ext"].compact3_tris_precomputed_grouped_block_gr_predecode(
+        buf, t_i32([0], cuda), t_i32(words_a, cuda), t_i32(offsets_a, cuda), t_i32(meta_a, cuda), packed_rows, n)
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
+
+
+def test_predecode_layout_and_negative_slots(tris, oracle_mod, cuda):
+    note("predecode layout")
+    rng = np.random.default_rng(8)
+    denses = [random_bitmap(rng, 6, 200, 0.15) for _ in range(4)]
+    words, offsets, meta = stacked_gr(oracle_mod, denses)
+    ids = np.array([3, -1, 0, 2], dtype=np.int32)
+    nblk = 3 * 4
+    want = oracle_mod.gr_predecode(words, offsets, meta, ids, nblk)
+    buf = torch.full((4, nblk, 128), 7, dtype=torch.int32, device=cuda)
+    got = tris["ext"].compact3_tris_precomputed_grouped_block_gr_predecode(
+        buf, t_i32(ids, cuda), t_i32(words, cuda), t_i32(offsets, cuda), t_i32(meta, cuda), 6, 200)
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
+
+
+# ------------------------------------------------------------------ dequant
+def make_projection(tris, seed, E, n, k, p=0.15, salient_counts=None, scale=False, bias=False, g_idx=None):
+    syn = tris["synthetic"]
+    rng = syn.rng_for(seed)
+    os_ = rng.uniform(0.5, 1.5, (E, n)).astype(np.float16) if scale else None
+    bs = (rng.standard_normal((E, n)) * 0.1).astype(np.float16) if bias else None
+    return syn.make_projection(rng, E, n, k, p, rng.random(k) + 0.5, tris["ext"].gr_encode,
+                               salient_counts=salient_counts, output_scale=os_, bias=bs, g_idx=g_idx,
+                               keep_dense_gmap=True)
+
+
+DEQUANT_CASES = [
+    dict(E=3, n=128, k=256),
+    dict(E=2, n=100, k=96),                                 # partial out block, K not a multiple of 64
+    dict(E=4, n=64, k=512, salient_counts=[0, 1, 40, 70]),  # ragged qweight2_sparse rows
+    dict(E=2, n=96, k=256, g_idx="alternating"),            # non-uniform groups
+    dict(E=2, n=64, k=128, p=0.9),
+]
+
+
+@pytest.mark.parametrize("case", DEQUANT_CASES, ids=lambda c: "-".join(f"{a}{b}" for a, b in c.items() if a != "salient_counts"))
+def test_dequant_bit_exact(tris, oracle_mod, cuda, case):
+    note(f"dequant {case}")
+    case = dict(case)
+    g_idx = None
+    if case.pop("g_idx", None) == "alternating":
+        g_idx = (np.arange(case["k"]) % 2).astype(np.int32)
+    payload = make_projection(tris, 31, g_idx=g_idx, **case)
+    dev = tris["qlinear"].payload_to_device(payload, cuda)
+    E, k = case["E"], case["k"]
+    ids = torch.tensor([E - 1, -1] + list(range(E)), dtype=torch.int32, device=cuda)
+    for uniform in (False, True):
+        got = tris["ext"].compact3_dequant(dev, k, ids, use_uniform_k64_groups=uniform).cpu().numpy()
+        for i, e in enumerate(ids.tolist()):
+            if e < 0:
+                assert not got[i].any()
+                continue
+            want = oracle_mod.dequant_grouped_expert(payload, e, uniform)
+            np.testing.assert_array_equal(got[i].view(np.uint16), want.view(np.uint16), err_msg=f"expert {e}")
+
+
+# -------------------------------------------------------------------- route
+@pytest.mark.parametrize("t,k,e", [(1, 2, 8), (4, 2, 8), (16, 2, 8), (16, 8, 64), (33, 8, 256), (2048, 2, 8)])
+def test_route_matches_oracle(tris, oracle_mod, cuda, t, k, e):
+    note(f"route t={t} k={k} e={e}")
+    rng = np.random.default_rng(t + k + e)
+    sel = np.stack([rng.choice(e, size=k, replace=False) for _ in range(t)]).astype(np.int64)
+    want = oracle_mod.build_route(sel, e, 4)
+    got = tris["qlinear"].build_grouped_route(torch.from_numpy(sel).to(cuda), e)
+    for key in ("perm", "grouped_token_indices", "grouped_slots", "grouped_expert_ids", "expert_ids",
+                "segment_offsets", "problem_offsets"):
+        np.testing.assert_array_equal(got[key].cpu().numpy(), want[key], err_msg=key)
+    assert got["total_problem_tiles_host"] == want["total_problem_tiles"]
+    assert int(got["total_problem_tiles"][0]) == want["total_problem_tiles"]
+
+
+def test_route_rejects_bad_expert_ids(tris, cuda):
+    note("route bad ids")
+    sel = torch.tensor([[0, 9]], dtype=torch.int64, device=cuda)
+    with pytest.raises(RuntimeError):
+        tris["qlinear"].build_grouped_route(sel, 8)
+
+
+# ----------------------------------------------------------- grouped GEMM
+def oracle_grouped(oracle_mod, payload, hidden, expert_ids, seg, uniform):
+    return oracle_mod.grouped_forward(payload, hidden, expert_ids, seg, uniform)
+
+
+GEMM_CASES = [
+    dict(E=8, n=256, k=512, seg=[1, 0, 1, 0, 0, 0, 0, 0]),              # decode: one row per segment
+    dict(E=4, n=192, k=256, seg=[3, 17, 0, 40]),                         # multi-tile segments, an empty one
+    dict(E=3, n=100, k=96, seg=[5, 2, 9]),                               # ragged shapes
+    dict(E=3, n=128, k=256, seg=[4, 4, 4], scale=True, bias=True),       # epilogue
+    dict(E=2, n=128, k=256, seg=[6, 6], g_idx="alternating"),            # non-uniform groups
+]
+
+
+def _segments(seg_lengths, E, drop=None):
+    ids = [e for e in range(E) if seg_lengths[e] > 0]
+    offs = np.concatenate([[0], np.cumsum([seg_lengths[e] for e in ids])]).astype(np.int32)
+    ids = np.asarray(ids, dtype=np.int32)
+    if drop is not None and ids.size:
+        ids = ids.copy()
+        ids[drop] = -1
+    return ids, offs
+
+
+@pytest.mark.parametrize("case", GEMM_CASES, ids=lambda c: f"E{c['E']}n{c['n']}k{c['k']}" + ("s" if c.get("scale") else ""))
+def test_grouped_forward_block_gr(tris, oracle_mod, cuda, case):
+    note(f"grouped block_gr {case}")
+    case = dict(case)
+    g_idx = None
+    if case.pop("g_idx", None) == "alternating":
+        g_idx = (np.arange(case["k"]) % 2).astype(np.int32)
+    seg_len = case.pop("seg")
+    payload = make_projection(tris, 41, g_idx=g_idx, **case)
+    dev = tris["qlinear"].payload_to_device(payload, cuda)
+    ext = tris["ext"]
+    rows = int(sum(seg_len))
+    rng = np.random.default_rng(3)
+    hidden = (rng.standard_normal((rows, case["k"])) * 1.5).astype(np.float16)
+    for drop in (None, 0):
+        ids, offs = _segments(seg_len, case["E"], drop)
+        prob = np.concatenate([[0], np.cumsum((np.diff(offs) + 3) // 4)]).astype(np.int32)
+        for uniform in ((False, True) if g_idx is None else (False,)):
+            got = ext.compact3_tris_precomputed_grouped_forward_block_gr(
+                torch.from_numpy(hidden).to(cuda), t_i32(ids, cuda), t_i32(offs, cuda), t_i32(prob, cuda),
+                torch.tensor([int(prob[-1])]), dev["qweight1"], dev["qweight2_sparse"], dev["qweight2_sparse_prefix"],
+                dev["q_gmap_gr_words"], dev["q_gmap_gr_offsets"], dev["q_gmap_gr_meta"], dev["c_map"], dev["g_idx"],
+                dev["col_pack3"], dev["row_pack3"], dev["output_scale"], dev["has_output_scale"],
+                dev["bias"] if dev["has_bias"] else torch.empty(0, device=cuda, dtype=torch.float16),
+                dev["has_bias"], uniform).cpu().numpy()
+            want = oracle_grouped(oracle_mod, payload, hidden, ids, offs, uniform)
+            assert_close(got.astype(np.float32), want.astype(np.float32), f"drop={drop} uniform={uniform}")
+
+
+def test_dual_and_predecoded_match(tris, oracle_mod, cuda):
+    note("dual + predecoded")
+    ext = tris["ext"]
+    E, k = 4, 256
+    pa = make_projection(tris, 51, E, 320, k)
+    pb = make_projection(tris, 52, E, 320, k)
+    da = tris["qlinear"].payload_to_device(pa, cuda)
+    db = tris["qlinear"].payload_to_device(pb, cuda)
+    ids, offs = _segments([2, 37, 0, 5], E)
+    prob = np.concatenate([[0], np.cumsum((np.diff(offs) + 3) // 4)]).astype(np.int32)
+    rng = np.random.default_rng(4)
+    rows = int(offs[-1])
+    ha = torch.from_numpy((rng.standard_normal((rows, k)) * 1.5).astype(np.float16)).to(cuda)
+    hb = torch.from_numpy((rng.standard_normal((rows, k)) * 1.5).astype(np.float16)).to(cuda)
+    args = (t_i32(ids, cuda), t_i32(offs, cuda), t_i32(prob, cuda), torch.tensor([int(prob[-1])]))
+    empty = torch.empty(0, device=cuda, dtype=torch.float16)
+
+    def single(d, h):
+        return ext.compact3_tris_precomputed_grouped_forward_block_gr(
+            h, *args, d["qweight1"], d["qweight2_sparse"], d["qweight2_sparse_prefix"], d["q_gmap_gr_words"],
+            d["q_gmap_gr_offsets"], d["q_gmap_gr_meta"], d["c_map"], d["g_idx"], d["col_pack3"], d["row_pack3"],
+            d["output_scale"], False, empty, False, True)
+
+    oa, ob = ext.compact3_tris_precomputed_grouped_dual_forward_block_gr(
+        ha, hb, *args, *[da[x] for x in ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "q_gmap_gr_words",
+                                         "q_gmap_gr_offsets", "q_gmap_gr_meta", "c_map", "g_idx", "col_pack3",
+                                         "row_pack3", "output_scale")], False, empty,
+        *[db[x] for x in ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "q_gmap_gr_words",
+                          "q_gmap_gr_offsets", "q_gmap_gr_meta", "c_map", "g_idx", "col_pack3", "row_pack3",
+                          "output_scale")], False, empty, True)
+    assert torch.equal(oa, single(da, ha)) and torch.equal(ob, single(db, hb))
+    assert_close(oa.cpu().numpy(), oracle_grouped(oracle_mod, pa, ha.cpu().numpy(), ids, offs, True), "dual a")
+    assert_close(ob.cpu().numpy(), oracle_grouped(oracle_mod, pb, hb.cpu().numpy(), ids, offs, True), "dual b")
+    nblk = tris["synthetic"].packing.num_gr_blocks(k, 320)
+    deca = torch.empty((ids.size, nblk, 128), dtype=torch.int32, device=cuda)
+    deca = ext.compact3_tris_precomputed_grouped_block_gr_predecode(
+        deca, t_i32(ids, cuda), da["q_gmap_gr_words"], da["q_gmap_gr_offsets"], da["q_gmap_gr_meta"], k // 32, 320)
+    pre = ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
+        ha, *args, deca, da["qweight1"], da["qweight2_sparse"], da["qweight2_sparse_prefix"], da["c_map"],
+        da["g_idx"], da["col_pack3"], da["row_pack3"], True)
+    assert torch.equal(pre, oa)
+
+
+def test_run_grouped_structured_api(tris, oracle_mod, cuda):
+    """qlinear-level API: route dict, segment-length lists, predecode policy for long segments."""
+    note("run_grouped_structured api")
+    ql = tris["qlinear"]
+    E, k, n = 4, 256, 192
+    payload = make_projection(tris, 61, E, n, k)
+    dev = ql.payload_to_device(payload, cuda)
+    rng = np.random.default_rng(6)
+    for lengths in ([1, 0, 1, 0], [70, 80, 0, 90]):
+        rows = sum(lengths)
+        hidden = torch.from_numpy((rng.standard_normal((rows, k)) * 1.5).astype(np.float16)).to(cuda)
+        out = ql.run_grouped_structured_expert_forward(dev, hidden, hidden, lengths)
+        ids, offs = _segments(lengths, E)
+        want = oracle_grouped(oracle_mod, payload, hidden.cpu().numpy(), ids, offs, True)
+        assert_close(out.cpu().numpy(), want, f"lengths={lengths}")
+    assert ql.run_grouped_structured_expert_forward(dev, hidden.cpu(), hidden.cpu(), lengths) is None
+
+
+# ------------------------------------------------------------------ backbone
+@pytest.mark.parametrize("tokens,in_f,rank", [(1, 4096, 512), (16, 4096, 512), (5, 14336, 512), (37, 2048, 256),
+                                              (4, 1000, 100)])
+def test_backbone_matches_fp32(tris, cuda, tokens, in_f, rank):
+    note(f"backbone T={tokens} in={in_f} rank={rank}")
+    rng = np.random.default_rng(tokens + in_f)
+    x = rng.standard_normal((tokens, in_f)).astype(np.float16)
+    sv = (rng.standard_normal((rank, in_f)) * 0.02).astype(np.float16)
+    want = (x.astype(np.float32) @ sv.astype(np.float32).T).astype(np.float16)
+    xt, st = torch.from_numpy(x).to(cuda), torch.from_numpy(sv).to(cuda)
+    for _ in range(2):  # the second call reuses the self-resetting workspace
+        got = tris["ext"].backbone_linear(xt, st).cpu().numpy()
+        assert_close(got, want, "backbone")
+    idx = torch.from_numpy(rng.integers(0, tokens, 2 * tokens)).to(cuda)
+    got = tris["ext"].backbone_linear(xt, st, row_index=idx).cpu().numpy()
+    assert_close(got, want[idx.cpu().numpy()], "backbone gathered")
+    if in_f % 8 == 0:
+        s = rng.uniform(0.5, 1.5, in_f).astype(np.float16)
+        xs = (x.astype(np.float32) * s.astype(np.float32)).astype(np.float16)
+        want_s = (xs.astype(np.float32) @ sv.astype(np.float32).T).astype(np.float16)
+        got = tris["ext"].backbone_linear(xt, st, in_scale=torch.from_numpy(s).to(cuda)).cpu().numpy()
+        assert_close(got, want_s, "backbone scaled")
+
+
+# --------------------------------------------------------------------- layer
+def _run_layer(tris, oracle_mod, cuda, spec, tokens, seed):
+    syn = tris["synthetic"]
+    ql = tris["qlinear"]
+    layer = syn.make_layer(spec, seed, tris["ext"].gr_encode)
+    inp = syn.make_inputs(spec, tokens, seed + 1, layer["outlier_idx"])
+    payloads = {p: ql.payload_to_device(layer[p], cuda) for p in ("gate", "up", "down")}
+    backbones = {p: torch.from_numpy(layer["backbones"][p]).to(cuda) for p in ("gate", "up", "down")}
+    shared = None
+    if "shared_expert" in layer:
+        shared = tuple(torch.from_numpy(w).to(cuda) for w in layer["shared_expert"])
+    block = tris["moe"].TrisSparseMoeBlock(spec.hidden, spec.num_experts, spec.top_k, payloads, backbones,
+                                           renormalize=spec.renormalize, shared_expert=shared)
+    x = torch.from_numpy(inp["x"]).to(cuda).to(torch.bfloat16)
+    logits = torch.from_numpy(inp["router_logits"]).to(cuda)
+    out = block.forward_routed(x, logits).float().cpu().numpy()
+    w, sel = oracle_mod.route_topk(inp["router_logits"], spec.top_k, spec.renormalize)
+    want = oracle_mod.moe_layer(inp["x"].astype(np.float16), w, sel, {p: layer[p] for p in ("gate", "up", "down")},
+                                layer["backbones"], spec.num_experts, layer.get("shared_expert"))
+    return out, oracle_mod.bf16_round(want)
+
+
+def test_layer_olmoe_c0(tris, oracle_mod, cuda):
+    from tris_moe_amd.configs import C0_OLMOE
+
+    note("layer C0 OLMoE T=16")
+    out, want = _run_layer(tris, oracle_mod, cuda, C0_OLMOE, 16, 1000)
+    assert_close(out, want, "C0 layer")
+
+
+@pytest.mark.parametrize("tokens", [1, 4])
+def test_layer_mixtral_c1_decode(tris, oracle_mod, cuda, tokens):
+    from tris_moe_amd.configs import C1_MIXTRAL_DECODE
+
+    note(f"layer C1 Mixtral T={tokens}")
+    out, want = _run_layer(tris, oracle_mod, cuda, C1_MIXTRAL_DECODE, tokens, 2000 + tokens)
+    assert_close(out, want, f"C1 layer T={tokens}")
+
+
+def test_layer_a3b_c3_with_shared_expert(tris, oracle_mod, cuda):
+    from tris_moe_amd.configs import C3_A3B
+
+    note("layer C3 A3B T=32")
+    out, want = _run_layer(tris, oracle_mod, cuda, C3_A3B, 32, 3000)
+    assert_close(out, want, "C3 layer")

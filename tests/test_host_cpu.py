@@ -1,0 +1,261 @@
+"""CPU-only checks of the product's host side and of the oracle's dequant / route / layer pins.
+
+* the C-ABI library loads and exports every symbol declared in include/tris_moe_hip.h;
+* argument-contract errors come back as RuntimeError without touching a GPU;
+* the product's host GR encoder is bit-identical to the oracle (known answers + random);
+* the product's packing helpers equal the oracle's restatement of pack_utils.py;
+* oracle fp16 arithmetic equals single-rounding float64 arithmetic;
+* the oracle's weight reconstruction equals the reference CPU formula
+  (qlinear_cuda.py:4213-4236, masks and per-term fp16 products in torch CPU half);
+* the oracle's route equals a brute-force grouping;
+* the oracle MoE layer agrees with a float64 evaluation of the same weights.
+"""
+import ctypes
+import math
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from gr_cases import block_from_positions, case_positions, load_known_answers, random_bitmap, structured_bitmap
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "tris_moe_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tris_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_header_symbols(tris):
+    from tris_moe_amd import _lib
+
+    lib = _lib.load()
+    names = declared_functions()
+    assert "tris_grouped_forward_block_gr" in names and len(names) >= 12
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert lib.tris_abi_version() == 2
+
+
+def test_ext_module_passes_reference_abi_probe(tris):
+    """qlinear_cuda.py:14-37 requires these callables and ABI attribute."""
+    ext = tris["ext"]
+    required = ("compact3_linear_forward", "compact3_qkv_linear_forward", "compact3_dual_linear_forward",
+                "compact3_tris_precomputed_grouped_forward_block_gr",
+                "compact3_tris_precomputed_grouped_dual_forward_block_gr",
+                "compact3_tris_precomputed_grouped_block_gr_predecode",
+                "compact3_tris_precomputed_grouped_forward_block_gr_predecoded",
+                "compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded",
+                "compact3_tris_precomputed_grouped_forward_block_gr_predecoded_hybrid",
+                "compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded_hybrid")
+    assert ext.TRIS_COMPACT3_KERNEL_ABI_VERSION == 2
+    for name in required:
+        assert callable(getattr(ext, name)), name
+    with pytest.raises(RuntimeError):
+        ext.compact3_linear_forward()
+
+
+def test_c_abi_argument_errors_without_gpu(tris):
+    from tris_moe_amd import _lib
+
+    lib = _lib.load()
+    rc = lib.tris_build_grouped_route(None, 1, 2, 8, 0, None, None, None, None, None, None, None, None, None)
+    assert rc == -1 and b"m_tile" in lib.tris_last_error()
+    rc = lib.tris_grouped_forward_block_gr(None, 4, None, None, None, 1, 1, None, None, None)
+    assert rc == -1 and b"null payload" in lib.tris_last_error()
+    assert lib.tris_backbone_workspace_bytes(1, 4096, 512) > 0
+    rc = lib.tris_backbone_linear(None, 2, 4096, None, None, 512, None, ctypes.c_void_p(16), None, 0, None)
+    assert rc == -1
+
+
+def test_ext_rejects_cpu_tensors(tris):
+    ext = tris["ext"]
+    with pytest.raises(RuntimeError, match="CUDA"):
+        ext.build_grouped_route(torch.zeros((2, 2), dtype=torch.long), 4, 4)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        ext.backbone_linear(torch.zeros((2, 8), dtype=torch.float16), torch.zeros((4, 8), dtype=torch.float16))
+
+
+@pytest.mark.parametrize("case", load_known_answers()["single_block"], ids=lambda c: c["name"])
+def test_product_encoder_known_answers(tris, oracle_mod, case):
+    dense = block_from_positions(case_positions(case))
+    got = tris["ext"].gr_encode(dense)
+    want = oracle_mod.gr_encode(dense)
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g, w)
+    assert got[2].tolist() == [case["meta"]]
+
+
+@pytest.mark.parametrize("p", [0.0, 0.05, 0.15, 0.3, 0.9])
+@pytest.mark.parametrize("kmin,kmax", [(0, 7), (2, 4), (5, 5)])
+def test_product_encoder_matches_oracle(tris, oracle_mod, p, kmin, kmax):
+    rng = np.random.default_rng(int(p * 100) + kmin * 10 + kmax)
+    dense = random_bitmap(rng, 16, 200, p)
+    got = tris["ext"].gr_encode(dense, kmin, kmax)
+    want = oracle_mod.gr_encode(dense, kmin, kmax)
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g, w)
+
+
+@pytest.mark.parametrize("kind", ["full", "corners", "stripes", "sparse_long_runs"])
+def test_product_encoder_structured(tris, oracle_mod, kind):
+    dense = structured_bitmap(kind, 7, 65, np.random.default_rng(1))
+    for force_raw in (False, True):
+        got = tris["ext"].gr_encode(dense, force_raw=force_raw)
+        want = oracle_mod.gr_encode(dense, force_raw=force_raw)
+        for g, w in zip(got, want):
+            np.testing.assert_array_equal(g, w)
+
+
+def test_product_encoder_rejects_bad_k_bounds(tris):
+    with pytest.raises(RuntimeError, match="k bounds"):
+        tris["ext"].gr_encode(np.zeros((2, 64), dtype=np.int32), 3, 9)
+
+
+def test_product_packing_matches_oracle(oracle_mod):
+    from tris_moe_amd import packing
+
+    rng = np.random.default_rng(2)
+    for n, k in ((5, 7), (64, 512), (33, 100)):
+        m = rng.random((n, k)) < 0.4
+        np.testing.assert_array_equal(packing.pack_bool_matrix(m), oracle_mod.pack_bool_matrix(m))
+        v = rng.random(k) < 0.3
+        np.testing.assert_array_equal(packing.pack_bool_vector(v), oracle_mod.pack_bool_vector(v))
+        np.testing.assert_array_equal(packing.sparse_prefix(v), oracle_mod.sparse_prefix(v))
+        np.testing.assert_array_equal(packing.pack_sparse_bool_matrix(m, v), oracle_mod.pack_sparse_bool_matrix(m, v))
+        h = rng.standard_normal((4, k)).astype(np.float16)
+        np.testing.assert_array_equal(packing.pack_half4(*h), oracle_mod.pack_half4(*h))
+        np.testing.assert_array_equal(oracle_mod.unpack_bool_matrix(oracle_mod.pack_bool_matrix(m), k), m)
+
+
+def test_fp16_arithmetic_single_rounding(oracle_mod):
+    """Products/sums computed via fp32 then rounded equal one rounding of the exact (float64) result."""
+    rng = np.random.default_rng(4)
+    bits = rng.integers(0, 0x7C00, size=(2, 200000), dtype=np.uint16)  # finite non-negative halves
+    sign = rng.integers(0, 2, size=(2, 200000), dtype=np.uint16) << 15
+    a, b = (bits | sign).view(np.float16)
+    exact_mul = (a.astype(np.float64) * b.astype(np.float64)).astype(np.float16)
+    exact_add = (a.astype(np.float64) + b.astype(np.float64)).astype(np.float16)
+    np.testing.assert_array_equal(oracle_mod.f16_mul(a, b).view(np.uint16), exact_mul.view(np.uint16))
+    np.testing.assert_array_equal(oracle_mod.f16_add(a, b).view(np.uint16), exact_add.view(np.uint16))
+
+
+def _reference_cpu_dequant(oracle_mod, ex, gmap_dense, n, k):
+    """qlinear_cuda.py:4213-4236 restated with torch CPU half ops (masks and per-term products)."""
+    half = torch.float16
+    b1 = torch.from_numpy(oracle_mod.unpack_bool_matrix(ex["qweight1"], k)).to(half) * 2 - 1
+    sal = torch.from_numpy(oracle_mod.unpack_bool_vector(ex["c_map"], k))
+    nonsal = ~sal
+    q2 = ex["qweight2_sparse"]
+    b2 = torch.zeros((n, k), dtype=torch.bool)
+    if int(sal.sum()) > 0 and q2.shape[0] > 0:
+        b2[:, sal] = torch.from_numpy(oracle_mod.unpack_bool_matrix(q2, int(sal.sum())))
+    b2 = b2.to(half) * 2 - 1
+    g = torch.from_numpy(oracle_mod.unpack_bool_matrix(gmap_dense, k))
+    cols = [torch.from_numpy(c.astype(np.float16)) for c in oracle_mod.unpack_half4(ex["col_pack3"])]
+    rows = [torch.from_numpy(r.astype(np.float16))[:, torch.from_numpy(ex["g_idx"].astype(np.int64))]
+            for r in oracle_mod.unpack_half4(ex["row_pack3"])]
+    smask = sal.unsqueeze(0).expand(n, -1).to(half)
+    dmask = (nonsal.unsqueeze(0) & g).to(half)
+    nmask = (nonsal.unsqueeze(0) & ~g).to(half)
+    w = torch.zeros((n, k), dtype=half)
+    w += b1 * (rows[0] * cols[0].unsqueeze(0)) * smask
+    w += b2 * (rows[1] * cols[1].unsqueeze(0)) * smask
+    w += b1 * (rows[2] * cols[2].unsqueeze(0)) * dmask
+    w += b1 * (rows[3] * cols[3].unsqueeze(0)) * nmask
+    return w.numpy()
+
+
+@pytest.mark.parametrize("n,k,p", [(64, 128, 0.15), (100, 256, 0.3), (70, 96, 0.05)])
+def test_oracle_dequant_matches_reference_cpu_formula(oracle_mod, n, k, p):
+    from tris_moe_amd import synthetic
+
+    rng = synthetic.rng_for(n * k)
+    sal = synthetic.salient_columns(rng, rng.random(k) + 0.5, math.ceil(0.05 * k))
+    ex = synthetic.make_expert(rng, n, k, p, sal)
+    ours = oracle_mod.dequant_compact3(ex["qweight1"], ex["qweight2_sparse"], ex["qweight2_sparse_prefix"],
+                                       ex["gmap_dense"], ex["c_map"], ex["g_idx"], ex["col_pack3"], ex["row_pack3"], k)
+    ref = _reference_cpu_dequant(oracle_mod, ex, ex["gmap_dense"], n, k)
+    np.testing.assert_array_equal(ours.astype(np.float32), ref.astype(np.float32))  # +0 == -0
+    assert np.isfinite(ours.astype(np.float32)).all()
+
+
+def test_oracle_dequant_group_selection(oracle_mod):
+    """Non-uniform g_idx uses g_idx[k] per column; the uniform fast path uses the 64-column tile's
+    first group; an out-of-range group gives zero weights (kernel.cu:830-853)."""
+    from tris_moe_amd import synthetic
+
+    rng = synthetic.rng_for(77)
+    n, k = 64, 128
+    sal = synthetic.salient_columns(rng, rng.random(k), 7)
+    ex = synthetic.make_expert(rng, n, k, 0.2, sal)
+    args = (ex["qweight1"], ex["qweight2_sparse"], ex["qweight2_sparse_prefix"], ex["gmap_dense"], ex["c_map"])
+    g_perm = (np.arange(k) * 7 % 2).astype(np.int32)          # alternating groups 0/1 within tiles
+    per_k = oracle_mod.dequant_compact3(*args, g_perm, ex["col_pack3"], ex["row_pack3"], k, False)
+    tile = oracle_mod.dequant_compact3(*args, g_perm, ex["col_pack3"], ex["row_pack3"], k, True)
+    only0 = oracle_mod.dequant_compact3(*args, np.zeros(k, np.int32), ex["col_pack3"], ex["row_pack3"], k)
+    only1 = oracle_mod.dequant_compact3(*args, np.ones(k, np.int32), ex["col_pack3"], ex["row_pack3"], k)
+    sel = g_perm.astype(bool)
+    np.testing.assert_array_equal(per_k[:, sel], only1[:, sel])
+    np.testing.assert_array_equal(per_k[:, ~sel], only0[:, ~sel])
+    np.testing.assert_array_equal(tile, only0)               # both tiles start with group 0
+    bad = g_perm.copy()
+    bad[5] = 9
+    w_bad = oracle_mod.dequant_compact3(*args, bad, ex["col_pack3"], ex["row_pack3"], k)
+    assert np.all(w_bad[:, 5].astype(np.float32) == 0)
+
+
+@pytest.mark.parametrize("t,k,e", [(1, 2, 8), (7, 3, 5), (16, 8, 64), (0, 2, 4)])
+def test_oracle_route_brute_force(oracle_mod, t, k, e):
+    rng = np.random.default_rng(t * 100 + k * 10 + e)
+    sel = np.stack([rng.choice(e, size=k, replace=False) for _ in range(t)]) if t else np.zeros((0, k), np.int64)
+    route = oracle_mod.build_route(sel, e, 4)
+    flat = sel.reshape(-1)
+    active = sorted(set(flat.tolist()))
+    assert route["expert_ids"].tolist() == active
+    seg = route["segment_offsets"]
+    for s, ex in enumerate(active):
+        rows = route["perm"][seg[s]:seg[s + 1]]
+        assert sorted(rows.tolist()) == [i for i in range(flat.size) if flat[i] == ex]
+        assert list(rows) == sorted(rows)                      # stable within a segment
+    assert route["problem_offsets"].tolist() == [0] + list(np.cumsum([(int(np.sum(flat == ex)) + 3) // 4 for ex in active]))
+    np.testing.assert_array_equal(route["grouped_token_indices"] * k + route["grouped_slots"], route["perm"])
+
+
+def test_oracle_layer_against_float64(oracle_mod, tris):
+    """The oracle layer (fp16 between stages, fp32 accumulation) stays within the layer tolerance of a
+    float64 evaluation of the same exact weights."""
+    from tris_moe_amd.configs import MoELayerSpec
+
+    spec = MoELayerSpec("tiny", hidden=256, num_experts=4, intermediate=384, top_k=2, rank=128, tokens=(5,))
+    syn = tris["synthetic"]
+    layer = syn.make_layer(spec, 5, oracle_mod.gr_encode)
+    inp = syn.make_inputs(spec, 5, 6, layer["outlier_idx"])
+    w, sel = oracle_mod.route_topk(inp["router_logits"], spec.top_k, spec.renormalize)
+    x16 = inp["x"].astype(np.float16)
+    out = oracle_mod.moe_layer(x16, w, sel, {p: layer[p] for p in ("gate", "up", "down")}, layer["backbones"],
+                               spec.num_experts)
+    # float64 reference: same fp16 weights and inputs, no intermediate rounding
+    sv = {p: layer["backbones"][p].astype(np.float64) for p in ("gate", "up", "down")}
+    ref = np.zeros((5, spec.hidden))
+    w16 = w.astype(np.float16).astype(np.float64)
+    for t in range(5):
+        for s in range(spec.top_k):
+            e = int(sel[t, s])
+            Wg = oracle_mod.dequant_grouped_expert(layer["gate"], e).astype(np.float64)
+            Wu = oracle_mod.dequant_grouped_expert(layer["up"], e).astype(np.float64)
+            Wd = oracle_mod.dequant_grouped_expert(layer["down"], e).astype(np.float64)
+            xv = x16[t].astype(np.float64)
+            g = Wg @ (sv["gate"] @ xv)
+            u = Wu @ (sv["up"] @ xv)
+            m = g / (1 + np.exp(-g)) * u
+            ref[t] += w16[t, s] * (Wd @ (sv["down"] @ m))
+    err = out - ref
+    assert np.abs(err).max() < 2e-2
+    assert np.linalg.norm(err) / np.linalg.norm(ref) < 1e-3
