@@ -101,13 +101,14 @@ int64_t tris_gr_encode(const int32_t* packed, int32_t packed_rows, int32_t outfe
  *   segment_offsets    int32 [num_experts+1] valid prefix [num_active+1], rest = R
  *   problem_offsets    int32 [num_experts+1] prefix of ceil(len/m_tile), rest = total
  *   counts             int32 [2] = {num_active, total_problem_tiles}
+ *   inverse_perm       int32 [R] or NULL: grouped row of flat slot t*top_k + s
  * Expert ids outside [0, num_experts) are an error reported through counts[0] = -1.
  */
 int tris_build_grouped_route(const int64_t* selected_experts, int32_t num_tokens, int32_t top_k,
                              int32_t num_experts, int32_t m_tile, int64_t* perm,
                              int64_t* grouped_token_indices, int64_t* grouped_slots,
                              int32_t* grouped_expert_ids, int32_t* expert_ids, int32_t* segment_offsets,
-                             int32_t* problem_offsets, int32_t* counts, void* stream);
+                             int32_t* problem_offsets, int32_t* counts, int32_t* inverse_perm, void* stream);
 
 /*
  * Grouped expert GEMM with in-kernel block-GR decode: replaces
@@ -193,10 +194,10 @@ int tris_gr_decode_dense(const int32_t* q_gmap_gr_words, const int32_t* q_gmap_g
  * ns_mode == 1, :4477-4480); out fp16 [tokens, rank]; fp32 accumulation.
  * row_index int64 [tokens] or NULL gathers x rows (x[row_index[t]]), fusing the
  * reference's index_select (modeling_mixtral.py:467).  x, sv and in_scale must
- * be 16-byte aligned.  workspace: device memory of
- * tris_backbone_workspace_bytes(tokens, in, rank) bytes, zero-filled before
- * its first use; every call leaves it zero-filled again (per-tile counters)
- * apart from scratch partial sums.  Calls sharing a workspace must not overlap.
+ * be 16-byte aligned.  workspace: device scratch of
+ * tris_backbone_workspace_bytes(tokens, in, rank) bytes (fp32 split-K partial
+ * sums; no initial contents needed).  Calls sharing a workspace on different
+ * streams must not overlap.
  */
 int tris_backbone_linear(const uint16_t* x, int32_t tokens, int32_t in_features, const int64_t* row_index,
                          const uint16_t* sv, int32_t rank, const uint16_t* in_scale, uint16_t* out,
@@ -205,6 +206,19 @@ int tris_backbone_linear(const uint16_t* x, int32_t tokens, int32_t in_features,
 /* Workspace size for tris_backbone_linear (no reference counterpart: cuBLAS
  * owns its workspace). */
 int64_t tris_backbone_workspace_bytes(int32_t tokens, int32_t in_features, int32_t rank);
+
+/*
+ * Routing-weighted combine: replaces final.index_add_(0, grouped_token_indices,
+ * (down_out * routing).to(output_dtype)) (modeling_mixtral.py:529-536).
+ * out[t, :] = bf16( sum_s fp16(expert_out[inverse_perm[t*top_k+s], :] * weights[t, s])
+ *                   (+ shared[t, :]) ), summed in fp32 and rounded once.
+ * expert_out fp16 [R, hidden] (16-byte aligned when hidden % 8 == 0);
+ * inverse_perm int32 [tokens*top_k]; weights fp16 [tokens, top_k];
+ * shared fp16 [tokens, hidden] or NULL; out bf16 [tokens, hidden].
+ */
+int tris_moe_combine(const uint16_t* expert_out, const int32_t* inverse_perm, const uint16_t* weights,
+                     const uint16_t* shared, int32_t tokens, int32_t top_k, int32_t hidden, uint16_t* out,
+                     void* stream);
 
 #ifdef __cplusplus
 }

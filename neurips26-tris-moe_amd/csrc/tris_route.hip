@@ -101,7 +101,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_histogram_kernel(
 __global__ __launch_bounds__(256) void route_scatter_kernel(
     const int64_t* __restrict__ selected, int total, int top_k, int num_experts, const int32_t* __restrict__ expert_ids,
     const int32_t* __restrict__ segment_offsets, int64_t* __restrict__ perm, int64_t* __restrict__ token_idx,
-    int64_t* __restrict__ slots, int32_t* __restrict__ grouped_expert_ids) {
+    int64_t* __restrict__ slots, int32_t* __restrict__ grouped_expert_ids, int32_t* __restrict__ inverse_perm) {
   const int seg = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   if (seg >= num_experts) return;
@@ -119,6 +119,7 @@ __global__ __launch_bounds__(256) void route_scatter_kernel(
       token_idx[dst] = i / top_k;
       slots[dst] = i % top_k;
       grouped_expert_ids[dst] = e;
+      if (inverse_perm != nullptr) inverse_perm[i] = dst;
     }
     pos += __popcll(mask);
   }
@@ -132,7 +133,8 @@ extern "C" int tris_build_grouped_route(const int64_t* selected_experts, int32_t
                                         int32_t num_experts, int32_t m_tile, int64_t* perm,
                                         int64_t* grouped_token_indices, int64_t* grouped_slots,
                                         int32_t* grouped_expert_ids, int32_t* expert_ids, int32_t* segment_offsets,
-                                        int32_t* problem_offsets, int32_t* counts, void* stream) {
+                                        int32_t* problem_offsets, int32_t* counts, int32_t* inverse_perm,
+                                        void* stream) {
   TRIS_REQUIRE(num_tokens >= 0 && top_k >= 0, "build_grouped_route: negative shape");
   TRIS_REQUIRE(num_experts >= 0, "num_experts must be non-negative");
   TRIS_REQUIRE(m_tile > 0, "m_tile must be positive");
@@ -155,6 +157,6 @@ extern "C" int tris_build_grouped_route(const int64_t* selected_experts, int32_t
   const int waves_per_block = 256 / kWave;
   hipLaunchKernelGGL(route_scatter_kernel, dim3(ceil_div(num_experts, waves_per_block)), dim3(256), 0, s,
                      selected_experts, static_cast<int>(total), top_k, num_experts, expert_ids, segment_offsets, perm,
-                     grouped_token_indices, grouped_slots, grouped_expert_ids);
+                     grouped_token_indices, grouped_slots, grouped_expert_ids, inverse_perm);
   return check_launch("route_scatter_kernel");
 }

@@ -57,7 +57,7 @@ SIGNATURES = {
     "tris_abi_version": (ctypes.c_int, []),
     "tris_last_error": (ctypes.c_char_p, []),
     "tris_gr_encode": (_I64, [_P, _I32, _I32, _I32, _I32, _I32, _P, _I64, _P, _P]),
-    "tris_build_grouped_route": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "tris_build_grouped_route": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "tris_grouped_forward_block_gr": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I32, _I64, _PAY, _P, _P]),
     "tris_grouped_dual_forward_block_gr": (ctypes.c_int, [_P, _P, _I32, _P, _P, _P, _I32, _I64, _PAY, _PAY, _P, _P, _P]),
     "tris_grouped_block_gr_predecode": (ctypes.c_int, [_P, _P, _I32, _P, _P, _P, _I32, _I32, _I32, _I32, _P]),
@@ -68,6 +68,7 @@ SIGNATURES = {
     "tris_gr_decode_dense": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _P, _I32, _I32, _I32, _P, _P]),
     "tris_backbone_linear": (ctypes.c_int, [_P, _I32, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P]),
     "tris_backbone_workspace_bytes": (_I64, [_I32, _I32, _I32]),
+    "tris_moe_combine": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _P, _P]),
 }
 
 _lib = None

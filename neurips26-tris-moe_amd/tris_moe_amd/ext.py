@@ -206,12 +206,14 @@ def build_grouped_route_device(selected_experts: torch.Tensor, num_experts: int,
     seg = torch.empty(num_experts + 1, **int_opts)
     prob = torch.empty(num_experts + 1, **int_opts)
     counts = torch.empty(2, **int_opts)
+    inv = torch.empty(r, **int_opts)
     lib = _lib.load()
     _lib.check(lib.tris_build_grouped_route(_ptr(sel), t, k, num_experts, m_tile, _ptr(perm), _ptr(gti), _ptr(gsl),
                                             _ptr(gexp), _ptr(expert_ids), _ptr(seg), _ptr(prob), _ptr(counts),
-                                            _stream(sel)), "build_grouped_route")
+                                            _ptr(inv), _stream(sel)), "build_grouped_route")
     return {"perm": perm, "grouped_token_indices": gti, "grouped_slots": gsl, "grouped_expert_ids": gexp,
-            "expert_ids": expert_ids, "segment_offsets": seg, "problem_offsets": prob, "counts": counts}
+            "expert_ids": expert_ids, "segment_offsets": seg, "problem_offsets": prob, "counts": counts,
+            "inverse_perm": inv}
 
 
 # ----------------------------------------------------------- grouped GEMMs
@@ -456,6 +458,27 @@ def backbone_linear(x: torch.Tensor, sv: torch.Tensor, in_scale: torch.Tensor | 
     ws = backbone_workspace(x.device, need)
     _lib.check(lib.tris_backbone_linear(_ptr(x), tokens, in_f, _ptr(row_index), _ptr(sv), rank, _ptr(in_scale),
                                         _ptr(out), _ptr(ws), int(ws.numel()), _stream(x)), "tris_backbone_linear")
+    return out
+
+
+def moe_combine(expert_out: torch.Tensor, inverse_perm: torch.Tensor, weights: torch.Tensor,
+                shared: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16 [T, H] = sum_s fp16(expert_out[inverse_perm[t, s]] * weights[t, s]) (+ shared), fp32-accumulated."""
+    _check_cuda("expert_out", expert_out, torch.float16, 2)
+    dev = expert_out.device
+    _check_cuda("weights", weights, torch.float16, 2, dev)
+    _check_cuda("inverse_perm", inverse_perm, torch.int32, 1, dev)
+    tokens, top_k = int(weights.size(0)), int(weights.size(1))
+    hidden = int(expert_out.size(1))
+    if inverse_perm.numel() != tokens * top_k:
+        raise RuntimeError("inverse_perm must hold tokens * top_k entries")
+    if shared is not None:
+        _check_cuda("shared", shared, torch.float16, 2, dev)
+        if tuple(shared.shape) != (tokens, hidden):
+            raise RuntimeError("shared must be [tokens, hidden]")
+    out = torch.empty((tokens, hidden), dtype=torch.bfloat16, device=dev)
+    _lib.check(_lib.load().tris_moe_combine(_ptr(expert_out), _ptr(inverse_perm), _ptr(weights), _ptr(shared), tokens,
+                                            top_k, hidden, _ptr(out), _stream(expert_out)), "tris_moe_combine")
     return out
 
 

@@ -44,12 +44,10 @@ def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, select
     T, H = int(x16.size(0)), int(x16.size(1))
     k = int(selected_experts.size(1))
     R = T * k
-    final = torch.zeros((T, H), dtype=output_dtype, device=x16.device)
     if R == 0:
-        return final
+        return torch.zeros((T, H), dtype=output_dtype, device=x16.device)
     route = ext.build_grouped_route_device(selected_experts, num_experts, GROUPED_SEGMENT_M_TILE)
     gti = route["grouped_token_indices"]
-    gsl = route["grouped_slots"]
     expert_ids = route["expert_ids"]
     seg = route["segment_offsets"]
     prob = route["problem_offsets"]
@@ -76,13 +74,13 @@ def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, select
         pd["q_gmap_gr_offsets"], pd["q_gmap_gr_meta"], pd["c_map"], pd["g_idx"], pd["col_pack3"], pd["row_pack3"],
         pd["output_scale"], bool(pd["has_output_scale"]), pd["bias"] if pd["has_bias"] else empty,
         bool(pd["has_bias"]), bool(pd.get("_compact3_k64_groups_uniform", False)))
-    w16 = routing_weights.to(torch.float16)
-    contrib = (d_out * w16[gti, gsl].unsqueeze(-1)).to(output_dtype)
-    final.index_add_(0, gti, contrib)
+    w16 = routing_weights.to(torch.float16).contiguous()
+    shared = None
     if shared_expert is not None:
         wg, wu, wd = shared_expert
-        final = final + F.linear(F.silu(F.linear(x16, wg)) * F.linear(x16, wu), wd).to(output_dtype)
-    return final
+        shared = F.linear(F.silu(F.linear(x16, wg)) * F.linear(x16, wu), wd).contiguous()
+    out = ext.moe_combine(d_out, route["inverse_perm"], w16, shared)
+    return out if output_dtype == torch.bfloat16 else out.to(output_dtype)
 
 
 class TrisSparseMoeBlock(nn.Module):

@@ -65,7 +65,7 @@ def test_c_abi_argument_errors_without_gpu(tris):
     from tris_moe_amd import _lib
 
     lib = _lib.load()
-    rc = lib.tris_build_grouped_route(None, 1, 2, 8, 0, None, None, None, None, None, None, None, None, None)
+    rc = lib.tris_build_grouped_route(None, 1, 2, 8, 0, None, None, None, None, None, None, None, None, None, None)
     assert rc == -1 and b"m_tile" in lib.tris_last_error()
     rc = lib.tris_grouped_forward_block_gr(None, 4, None, None, None, 1, 1, None, None, None)
     assert rc == -1 and b"null payload" in lib.tris_last_error()
