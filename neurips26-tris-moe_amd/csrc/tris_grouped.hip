@@ -442,6 +442,11 @@ int launch_grouped(const uint16_t* hidden_a, const uint16_t* hidden_b, int batch
   return check_launch(who);
 }
 
+int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int batch, const int32_t* expert_ids,
+                        const int32_t* segment_offsets, int num_segments, const int32_t* decoded_a,
+                        const int32_t* decoded_b, const tris_compact3_payload* pa, const tris_compact3_payload* pb,
+                        uint16_t* out_a, uint16_t* out_b, void* stream, const char* who);
+
 }  // namespace tris
 
 using namespace tris;
@@ -483,6 +488,11 @@ extern "C" int tris_grouped_forward_block_gr_predecoded(const uint16_t* hidden, 
   tris_compact3_payload p = *payload;  // the predecoded kernels apply no scale or bias
   p.has_output_scale = 0;
   p.has_bias = 0;
+  if (p.use_uniform_k64_groups) {
+    if (total_problem_tiles <= 0) return TRIS_OK;
+    return launch_grouped_mfma(hidden, nullptr, batch, expert_ids, segment_offsets, num_segments, decoded, nullptr,
+                               &p, nullptr, output, nullptr, stream, "tris_grouped_forward_block_gr_predecoded");
+  }
   return launch_grouped(hidden, nullptr, batch, expert_ids, segment_offsets, num_segments, total_problem_tiles,
                         decoded, nullptr, &p, nullptr, output, nullptr, true, stream,
                         "tris_grouped_forward_block_gr_predecoded");
@@ -502,6 +512,13 @@ extern "C" int tris_grouped_dual_forward_block_gr_predecoded(
   tris_compact3_payload pb = *payload_b;
   pa.has_output_scale = pb.has_output_scale = 0;
   pa.has_bias = pb.has_bias = 0;
+  if (pa.use_uniform_k64_groups && pb.use_uniform_k64_groups) {
+    if (total_problem_tiles <= 0) return TRIS_OK;
+    TRIS_REQUIRE(pa.num_experts == pb.num_experts, "tris_grouped_dual_forward_block_gr_predecoded: expert count mismatch");
+    return launch_grouped_mfma(hidden_a, hidden_b, batch, expert_ids, segment_offsets, num_segments, decoded_a,
+                               decoded_b, &pa, &pb, output_a, output_b, stream,
+                               "tris_grouped_dual_forward_block_gr_predecoded");
+  }
   return launch_grouped(hidden_a, hidden_b, batch, expert_ids, segment_offsets, num_segments, total_problem_tiles,
                         decoded_a, decoded_b, &pa, &pb, output_a, output_b, true, stream,
                         "tris_grouped_dual_forward_block_gr_predecoded");

@@ -1,0 +1,391 @@
+// Grouped compact3 expert GEMM on MFMA for decode-sized segments, reading
+// dense (predecoded) split bitmaps.
+//
+// Arithmetic.  A non-salient weight is w[n,k] = s1 * C_j[k] * R_j[n,g] with
+// j = d if the split bit is set, else nd, s1 = +-1 from qweight1
+// (TriSMoE_cuda_kernel.cu:665-774).  Factoring the per-column factor into the
+// activations, y_j[r,k] = fp16(C_j[k] * x[r,k]), gives
+//   out[r,n] = sum_g R_nd[n,g] * sum_k y_nd[r,k] * s1*(1-g)
+//            + R_d[n,g]  * sum_k y_d[r,k]  * s1*g          (non-salient k)
+//            + sum over salient k of x[r,k] * w_s[n,k]      (exact fp16 weight)
+// so the per-weight work is turning bits into +-1/0 operands.  The fp16
+// roundings differ from the reference's (the per-weight product C_j*R_j is
+// not rounded to fp16; C_j*x is), which stays within the layer tolerance;
+// bit-exact weights are produced by the dequant kernel.
+//
+// MFMA v_mfma_f32_16x16x32_f16: A rows 0-7 are y_nd for up to 8 segment rows,
+// rows 8-15 are y_d for the same rows; B is S = s1 (+-1.0) or X = s1*g
+// (0 or +-1.0).  Lane group kg (lanes 16kg..16kg+15) supplies the 8 columns
+// k = kg + 4i (i = 0..7) of each 32-column packed row, so after one shift the
+// needed sign / split bits sit at nibble positions 4i of a word; OR-ing in the
+// fp4 (e2m1) exponent pattern gives eight fp4 values (+-1.0 = 0b0010 / 0b1010,
+// 0 = 0b0000) that v_cvt_scalef32_pk_f16_fp4 expands two at a time to fp16.
+// The activations are staged in LDS in the same permuted column order.  Per
+// 64-column tile the accumulators are folded with the tile group's row
+// scales: nd rows take R_nd*(A.S - A.X), d rows take R_d*(A.X).  Salient
+// columns (a few per cent) take an exact VALU path with lane = output column.
+//
+// Work decomposition: workgroup = 4 wavefronts = one 64-output tile x one
+// tile of <= 8 rows of one segment x one projection (blockIdx.z); wavefront w
+// takes K columns [128w, 128w+128) of every 512-column chunk and issues all of
+// its global loads for the chunk before computing; the four partial results
+// are reduced through LDS.  Requires each 64-column K tile to lie in a single
+// group (the reference's UniformK64Groups case).
+#include "tris_common.h"
+
+namespace tris {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMfWaves = 4;
+constexpr int kMfThreads = kMfWaves * kWave;
+constexpr int kMfRows = 8;          // segment rows per workgroup tile
+constexpr int kMfChunk = 512;       // K columns staged per pass
+constexpr int kMfWaveK = kMfChunk / kMfWaves;
+constexpr int kMfYStride = kMfChunk + 8;  // fp16 elements per staged row (pad breaks bank aliasing)
+constexpr int kMfPR = kMfWaveK / 32;      // packed rows per wave per chunk
+constexpr int kMfKT = kMfWaveK / kTileK;  // 64-column K tiles per wave per chunk
+
+struct MfmaProj {
+  const uint16_t* hidden;  // [batch, rank]
+  uint16_t* out;           // [batch, N]
+  const int32_t* decoded;  // [num_segments, nblk, 128]
+  tris_compact3_payload p;
+};
+
+struct MfmaArgs {
+  MfmaProj proj[2];
+  const int32_t* expert_ids;
+  const int32_t* segment_offsets;
+  int num_segments;
+};
+
+// Position of column k (0..31) of a packed row in the staged order: lane group
+// k % 4, element k / 4.
+__device__ __forceinline__ int mf_perm32(int k) { return 8 * (k & 3) + (k >> 2); }
+
+// Eight fp4 nibbles -> eight fp16 values (v_cvt_scalef32_pk_f16_fp4, two per byte).
+__device__ __forceinline__ f16x8 fp4x8_to_f16x8(uint32_t nib) {
+  const f16x2 h0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(nib, 1.0f, 0);
+  const f16x2 h1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(nib, 1.0f, 1);
+  const f16x2 h2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(nib, 1.0f, 2);
+  const f16x2 h3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(nib, 1.0f, 3);
+  return f16x8{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+}
+
+// Same mapping as the in-kernel-decode GEMM (tris_grouped.hip).
+__device__ inline bool mf_map_row_tile(const int32_t* __restrict__ seg, int nseg, int tile, int row_tile, int* s_out,
+                                       int* row0_out, int* rc_out) {
+  const int lane = static_cast<int>(__lane_id());
+  int base = 0;
+  for (int c = 0; c < nseg; c += kWave) {
+    const int i = c + lane;
+    int t = 0;
+    if (i < nseg) {
+      const int len = seg[i + 1] - seg[i];
+      t = len > 0 ? (len + row_tile - 1) / row_tile : 0;
+    }
+    int incl = t;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int v = __shfl_up(incl, d);
+      if (lane >= d) incl += v;
+    }
+    const int total = __shfl(incl, kWave - 1);
+    if (tile < base + total) {
+      const uint64_t hit = __ballot(i < nseg && tile < base + incl);
+      const int L = __ffsll(static_cast<unsigned long long>(hit)) - 1;
+      const int excl = __shfl(incl - t, L);
+      const int s = c + L;
+      const int local = tile - base - excl;
+      const int row0 = seg[s] + local * row_tile;
+      const int end = seg[s + 1];
+      *s_out = s;
+      *row0_out = row0;
+      *rc_out = (end - row0) < row_tile ? (end - row0) : row_tile;
+      return true;
+    }
+    base += total;
+  }
+  return false;
+}
+
+template <int kNumProj>
+__global__ __launch_bounds__(kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t ys[16][kMfYStride];
+  __shared__ uint16_t xs_sal[kMfRows][kMfChunk];  // raw fp16 x (natural order) for the salient path
+  __shared__ uint32_t col_sal[kMfChunk];          // s_c1 | s_c2 << 16 per column
+  __shared__ float red[kMfWaves][kMfRows][kWave];
+
+  const MfmaProj& pa = a.proj[kNumProj == 1 ? 0 : blockIdx.z];
+  const tris_compact3_payload& p = pa.p;
+  const int N = p.outfeatures;
+  const int n0 = blockIdx.x * kTileOut;
+  if (n0 >= N) return;
+  int s = 0, row0 = 0, rc = 0;
+  if (!mf_map_row_tile(a.segment_offsets, a.num_segments, blockIdx.y, kMfRows, &s, &row0, &rc)) return;
+
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int e = a.expert_ids[s];
+  uint16_t* out = pa.out;
+  if (e < 0 || e >= p.num_experts) {
+    if (wave == 0 && n0 + lane < N) {
+      for (int r = 0; r < rc; ++r) out[static_cast<int64_t>(row0 + r) * N + n0 + lane] = 0;
+    }
+    return;
+  }
+
+  const int rank = p.rank;
+  const int packed_rows = ceil_div(rank, 32);
+  const int nkb = ceil_div(packed_rows, kGrPackedRows);
+  const int nob = ceil_div(N, kTileOut);
+  const int nblk = nkb * nob;
+  const int ob = blockIdx.x;
+  const int G = p.num_groups;
+  const int32_t* q1_e = p.qweight1 + static_cast<int64_t>(e) * packed_rows * N;
+  const int32_t* q2_e = p.qweight2_sparse + static_cast<int64_t>(e) * p.qweight2_sparse_rows * N;
+  const int32_t* q2p_e = p.qweight2_sparse_prefix + static_cast<int64_t>(e) * (packed_rows + 1);
+  const int32_t* cmap_e = p.c_map + static_cast<int64_t>(e) * packed_rows;
+  const int32_t* gidx_e = p.g_idx + static_cast<int64_t>(e) * rank;
+  const int64_t* col_e = p.col_pack3 + static_cast<int64_t>(e) * rank;
+  const int64_t* row_e = p.row_pack3 + static_cast<int64_t>(e) * N * G;
+  const int32_t* dec_s = pa.decoded + static_cast<int64_t>(s) * nblk * kGrWords;
+  const uint16_t* hid = pa.hidden + static_cast<int64_t>(row0) * rank;
+
+  const int i16 = lane % 16;   // MFMA column within a 16-wide tile / A row
+  const int kg = lane / 16;    // MFMA k group
+  f32x4 tot[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) tot[ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float sal[kMfRows];
+#pragma unroll
+  for (int r = 0; r < kMfRows; ++r) sal[r] = 0.0f;
+  const int n_lane = n0 + lane;           // output column of the salient path
+  const bool nv_lane = n_lane < N;
+
+  for (int kc = 0; kc < rank; kc += kMfChunk) {
+    // ---- issue every global load of this chunk before touching LDS
+    const int pr0 = (kc + wave * kMfWaveK) / 32;
+    uint32_t qw[kMfPR][4], gw[kMfPR][4];
+    uint64_t rp[kMfKT][4];
+    int gt[kMfKT];
+#pragma unroll
+    for (int j = 0; j < kMfPR; ++j) {
+      const int pr = pr0 + j;
+      const int32_t* blk = dec_s + static_cast<int64_t>((pr >> 1) * nob + ob) * kGrWords + (pr & 1) * kTileOut;
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const int n = n0 + 16 * ct + i16;
+        const bool ok = pr < packed_rows && n < N;
+        qw[j][ct] = ok ? static_cast<uint32_t>(q1_e[static_cast<int64_t>(pr) * N + n]) : 0u;
+        gw[j][ct] = ok ? static_cast<uint32_t>(blk[16 * ct + i16]) : 0u;
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kMfKT; ++t) {
+      const int kt = kc + wave * kMfWaveK + t * kTileK;
+      const int g = kt < rank ? gidx_e[kt] : -1;
+      gt[t] = g;
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const int n = n0 + 16 * ct + i16;
+        rp[t][ct] = (g >= 0 && g < G && n < N) ? static_cast<uint64_t>(row_e[static_cast<int64_t>(n) * G + g]) : 0ull;
+      }
+    }
+    // salient-path operands of this wave's range (lane = output column)
+    uint32_t cmw[kMfPR], q1s[kMfPR];
+    int q2p[kMfPR + 1];
+    uint64_t rps[kMfKT];
+#pragma unroll
+    for (int j = 0; j < kMfPR; ++j) {
+      const int pr = pr0 + j;
+      const int nbits = (rank - pr * 32) < 32 ? (rank - pr * 32) : 32;
+      cmw[j] = pr < packed_rows ? (static_cast<uint32_t>(cmap_e[pr]) & low_mask(nbits)) : 0u;
+      q1s[j] = (nv_lane && pr < packed_rows) ? static_cast<uint32_t>(q1_e[static_cast<int64_t>(pr) * N + n_lane]) : 0u;
+      q2p[j] = pr < packed_rows ? q2p_e[pr] : 0;
+    }
+    q2p[kMfPR] = (pr0 + kMfPR) <= packed_rows ? q2p_e[pr0 + kMfPR] : q2p_e[packed_rows];
+#pragma unroll
+    for (int t = 0; t < kMfKT; ++t) {
+      const int g = gt[t];
+      rps[t] = (nv_lane && g >= 0 && g < G) ? static_cast<uint64_t>(row_e[static_cast<int64_t>(n_lane) * G + g]) : 0ull;
+    }
+    const int q2row0 = q2p[0] >> 5;
+    const uint32_t q2w0 = (nv_lane && q2row0 < p.qweight2_sparse_rows && q2p[kMfPR] > q2p[0])
+                              ? static_cast<uint32_t>(q2_e[static_cast<int64_t>(q2row0) * N + n_lane]) : 0u;
+    // staging loads: thread handles columns kc+tid and kc+tid+256 for every row < rc
+    uint64_t cpv[2];
+    uint32_t cmk[2];
+    uint16_t xv[2][kMfRows];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int k = kc + tid + h * kMfThreads;
+      const bool kv = k < rank;
+      cpv[h] = kv ? static_cast<uint64_t>(col_e[k]) : 0ull;
+      cmk[h] = kv ? static_cast<uint32_t>(cmap_e[k >> 5]) : 0u;
+#pragma unroll
+      for (int r = 0; r < kMfRows; ++r) xv[h][r] = (kv && r < rc) ? hid[static_cast<int64_t>(r) * rank + k] : 0;
+    }
+    __syncthreads();  // previous chunk's LDS readers are done
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = tid + h * kMfThreads;
+      const int pj = (j & ~31) + mf_perm32(j & 31);
+      const bool salient = (cmk[h] >> (j & 31)) & 1u;
+      const uint16_t cd = static_cast<uint16_t>(cpv[h] >> 32);
+      const uint16_t cnd = static_cast<uint16_t>(cpv[h] >> 48);
+      col_sal[j] = static_cast<uint32_t>(cpv[h]);
+#pragma unroll
+      for (int r = 0; r < kMfRows; ++r) {
+        const uint16_t x = xv[h][r];
+        ys[r][pj] = salient ? 0 : hmul_bits(cnd, x);
+        ys[kMfRows + r][pj] = salient ? 0 : hmul_bits(cd, x);
+        xs_sal[r][j] = x;
+      }
+    }
+    __syncthreads();
+
+    // ---- MFMA over the wave's K tiles
+#pragma unroll
+    for (int t = 0; t < kMfKT; ++t) {
+      const int kt = kc + wave * kMfWaveK + t * kTileK;
+      if (kt >= rank) break;
+      f32x4 acc_s[4], acc_x[4];
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        acc_s[ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        acc_x[ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+#pragma unroll
+      for (int lpr = 0; lpr < kGrPackedRows; ++lpr) {
+        const int j = 2 * t + lpr;
+        if (pr0 + j >= packed_rows) break;
+        const int kl = (pr0 + j) * 32 - kc;
+        const f16x8 av = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&ys[i16][kl + 8 * kg]));
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+          const uint32_t nq = ((~qw[j][ct]) >> kg) & 0x11111111u;   // 1 = negative
+          const uint32_t gs = (gw[j][ct] >> kg) & 0x11111111u;      // 1 = split bit set
+          const uint32_t snib = (nq << 3) | 0x22222222u;            // +-1.0
+          const uint32_t xnib = ((gs & nq) << 3) | (gs << 1);       // g ? +-1.0 : 0
+          acc_s[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, fp4x8_to_f16x8(snib), acc_s[ct], 0, 0, 0);
+          acc_x[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, fp4x8_to_f16x8(xnib), acc_x[ct], 0, 0, 0);
+        }
+      }
+      // Fold with the tile group's row scales: lane groups 0-1 hold nd rows, 2-3 hold d rows.
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const float r_d = h2f(static_cast<uint16_t>(rp[t][ct] >> 32));
+        const float r_nd = h2f(static_cast<uint16_t>(rp[t][ct] >> 48));
+        const float cs = kg < 2 ? r_nd : 0.0f;
+        const float cx = kg < 2 ? -r_nd : r_d;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) tot[ct][v] += cs * acc_s[ct][v] + cx * acc_x[ct][v];
+      }
+    }
+
+    // ---- salient columns of the wave's range: exact fp16 weights, lane = output column
+#pragma unroll
+    for (int j = 0; j < kMfPR; ++j) {
+      uint32_t m = cmw[j];
+      const int t = j / 2;
+      int sidx = q2p[j];
+      while (m != 0u) {
+        const int b = __builtin_ctz(m);
+        m &= m - 1u;
+        const int kl = (pr0 + j) * 32 + b - kc;
+        uint32_t q2w = q2w0;
+        if ((sidx >> 5) != q2row0) {
+          q2w = nv_lane ? static_cast<uint32_t>(q2_e[static_cast<int64_t>(sidx >> 5) * N + n_lane]) : 0u;
+        }
+        const uint32_t cp = col_sal[kl];
+        uint16_t t1 = hmul_bits(static_cast<uint16_t>(cp), static_cast<uint16_t>(rps[t]));
+        if (!((q1s[j] >> b) & 1u)) t1 ^= 0x8000u;
+        uint16_t t2 = hmul_bits(static_cast<uint16_t>(cp >> 16), static_cast<uint16_t>(rps[t] >> 16));
+        if (!((q2w >> (sidx & 31)) & 1u)) t2 ^= 0x8000u;
+        const float wf = h2f(hadd_bits(t1, t2));
+#pragma unroll
+        for (int r = 0; r < kMfRows; ++r) {
+          if (r < rc) sal[r] = fmaf(h2f(xs_sal[r][kl]), wf, sal[r]);
+        }
+        ++sidx;
+      }
+    }
+  }
+
+  // tot[ct][v] = row 4*(kg%2)+v of the nd (kg<2) or d (kg>=2) part for column 16ct+i16.
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) tot[ct][v] += __shfl_xor(tot[ct][v], 32);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kMfRows; ++r) red[wave][r][lane] = sal[r];
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  if (kg < 2) {
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[wave][4 * kg + v][16 * ct + i16] += tot[ct][v];
+    }
+  }
+  __syncthreads();
+  if (wave == 0 && nv_lane) {
+    const float scale = p.has_output_scale ? h2f(p.output_scale[static_cast<int64_t>(e) * N + n_lane]) : 1.0f;
+    const float bias = p.has_bias ? h2f(p.bias[static_cast<int64_t>(e) * N + n_lane]) : 0.0f;
+    for (int r = 0; r < rc; ++r) {
+      float v = red[0][r][lane] + red[1][r][lane] + red[2][r][lane] + red[3][r][lane];
+      if (p.has_output_scale) v = v * scale;
+      if (p.has_bias) v = v + bias;
+      out[static_cast<int64_t>(row0 + r) * N + n_lane] = f2h_bits(v);
+    }
+  }
+}
+
+int check_payload(const tris_compact3_payload* p, bool need_gr, const char* who);
+
+int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int batch, const int32_t* expert_ids,
+                        const int32_t* segment_offsets, int num_segments, const int32_t* decoded_a,
+                        const int32_t* decoded_b, const tris_compact3_payload* pa, const tris_compact3_payload* pb,
+                        uint16_t* out_a, uint16_t* out_b, void* stream, const char* who) {
+  TRIS_REQUIRE(batch >= 0 && num_segments >= 0, "%s: negative batch or segment count", who);
+  int rc = check_payload(pa, false, who);
+  if (rc) return rc;
+  if (pb) {
+    rc = check_payload(pb, false, who);
+    if (rc) return rc;
+  }
+  if (batch == 0 || num_segments == 0) return TRIS_OK;
+  TRIS_REQUIRE(hidden_a && out_a && expert_ids && segment_offsets && decoded_a, "%s: null pointer", who);
+  TRIS_REQUIRE(!pb || (hidden_b && out_b && decoded_b), "%s: null pointer (second projection)", who);
+  int max_n = 0;
+  for (int i = 0; i < (pb ? 2 : 1); ++i) {
+    const tris_compact3_payload* p = i ? pb : pa;
+    TRIS_REQUIRE(p->num_experts > 0 && p->rank > 0 && p->outfeatures > 0, "%s: empty payload", who);
+    max_n = p->outfeatures > max_n ? p->outfeatures : max_n;
+  }
+  const int64_t tiles = static_cast<int64_t>(batch) / kMfRows + num_segments;
+  TRIS_REQUIRE(tiles <= 2147483647LL, "%s: too many tiles", who);
+  MfmaArgs args{};
+  args.proj[0] = MfmaProj{hidden_a, out_a, decoded_a, *pa};
+  if (pb) args.proj[1] = MfmaProj{hidden_b, out_b, decoded_b, *pb};
+  args.expert_ids = expert_ids;
+  args.segment_offsets = segment_offsets;
+  args.num_segments = num_segments;
+  dim3 grid(ceil_div(max_n, kTileOut), static_cast<unsigned>(tiles), pb ? 2 : 1);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pb) {
+    hipLaunchKernelGGL((grouped_mfma_kernel<2>), grid, dim3(kMfThreads), 0, s, args);
+  } else {
+    hipLaunchKernelGGL((grouped_mfma_kernel<1>), grid, dim3(kMfThreads), 0, s, args);
+  }
+  return check_launch(who);
+}
+
+}  // namespace tris

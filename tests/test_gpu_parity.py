@@ -128,6 +128,27 @@ def test_gr_decode_malformed_streams_follow_reference(tris, oracle_mod, cuda, k)
     np.testing.assert_array_equal(got.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("experts,packed_rows,n", [(1, 64, 3200), (3, 128, 2048), (2, 128, 14336)],
+                         ids=["1600blk", "6144blk", "28672blk"])
+def test_predecode_large_grids(tris, oracle_mod, cuda, experts, packed_rows, n):
+    """Block counts that select each lanes-per-block width of the decoder."""
+    note(f"predecode large E={experts} rows={packed_rows} n={n}")
+    rng = np.random.default_rng(packed_rows + n)
+    denses = [random_bitmap(rng, packed_rows, n, p) for p in (0.15, 0.02, 0.5)[:experts]]
+    words, offsets, meta = stacked_gr(oracle_mod, denses)
+    ids = np.arange(experts, dtype=np.int32)[::-1].copy()
+    nblk = (packed_rows // 2) * (n // 64)
+    want = oracle_mod.gr_predecode(words, offsets, meta, ids, nblk)
+    buf = torch.empty((experts, nblk, 128), dtype=torch.int32, device=cuda)
+    got = tris["ext"].compact3_tris_precomputed_grouped_block_gr_predecode(
+        buf, t_i32(ids, cuda), t_i32(words, cuda), t_i32(offsets, cuda), t_i32(meta, cuda), packed_rows, n)
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
+    dense = tris["ext"].gr_decode_dense(t_i32(words, cuda), t_i32(offsets, cuda), t_i32(meta, cuda),
+                                        t_i32(ids, cuda), packed_rows, n).cpu().numpy()
+    for i, e in enumerate(ids):
+        np.testing.assert_array_equal(dense[i], denses[e])
+
+
 def test_predecode_layout_and_negative_slots(tris, oracle_mod, cuda):
     note("predecode layout")
     rng = np.random.default_rng(8)
@@ -295,10 +316,22 @@ def test_dual_and_predecoded_match(tris, oracle_mod, cuda):
     deca = torch.empty((ids.size, nblk, 128), dtype=torch.int32, device=cuda)
     deca = ext.compact3_tris_precomputed_grouped_block_gr_predecode(
         deca, t_i32(ids, cuda), da["q_gmap_gr_words"], da["q_gmap_gr_offsets"], da["q_gmap_gr_meta"], k // 32, 320)
-    pre = ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
-        ha, *args, deca, da["qweight1"], da["qweight2_sparse"], da["qweight2_sparse_prefix"], da["c_map"],
-        da["g_idx"], da["col_pack3"], da["row_pack3"], True)
-    assert torch.equal(pre, oa)
+    for uniform in (True, False):  # MFMA kernel (factored scales) / exact per-weight kernel
+        pre = ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
+            ha, *args, deca, da["qweight1"], da["qweight2_sparse"], da["qweight2_sparse_prefix"], da["c_map"],
+            da["g_idx"], da["col_pack3"], da["row_pack3"], uniform)
+        assert_close(pre.cpu().numpy(), oracle_grouped(oracle_mod, pa, ha.cpu().numpy(), ids, offs, True),
+                     f"predecoded uniform={uniform}")
+    decb = torch.empty((ids.size, nblk, 128), dtype=torch.int32, device=cuda)
+    decb = ext.compact3_tris_precomputed_grouped_block_gr_predecode(
+        decb, t_i32(ids, cuda), db["q_gmap_gr_words"], db["q_gmap_gr_offsets"], db["q_gmap_gr_meta"], k // 32, 320)
+    pa2, pb2 = ext.compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
+        ha, hb, *args, deca, *[da[x] for x in ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map",
+                                               "g_idx", "col_pack3", "row_pack3")],
+        decb, *[db[x] for x in ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx",
+                                "col_pack3", "row_pack3")], True)
+    assert_close(pa2.cpu().numpy(), oracle_grouped(oracle_mod, pa, ha.cpu().numpy(), ids, offs, True), "dual pre a")
+    assert_close(pb2.cpu().numpy(), oracle_grouped(oracle_mod, pb, hb.cpu().numpy(), ids, offs, True), "dual pre b")
 
 
 def test_run_grouped_structured_api(tris, oracle_mod, cuda):
