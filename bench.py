@@ -5,16 +5,16 @@ Workload: one Mixtral-8x7B-shaped MoE layer at
 decode (hidden 4096, 8 experts, intermediate 14336, top-2, rank-512 fp16
 backbones, binarised compact3 experts with a block-GR split bitmap at
 p = 0.15).  A step is one full layer forward over one decode batch: router
-softmax/top-k, device route, gate/up backbones, fused GR-decode grouped
-gate/up GEMM, SiLU*up, down backbone, grouped down GEMM and the weighted
-scatter-add.  Synthetic seeded data; every step reads a different one of
+softmax/top-k, device route, gate/up backbones, GR predecode of the routed
+experts' split bitmaps (gate, up, down), MFMA grouped gate/up GEMM, SiLU*up,
+down backbone, grouped down GEMM and the weighted scatter-add.  Synthetic seeded data; every step reads a different one of
 --layers identical-content layer copies resident in HBM (so weights come from
 HBM, not the 256 MB last-level cache), with each step captured in a HIP graph.
 
 Prints ONE JSON line.  ``value`` is MoE-layer tokens/s; ``hbm_gbps`` the
 layer's algorithmic bytes / step time; ``roofline`` is for the dominant
-kernel, the fused gate/up grouped GEMM (grouped_gemm_kernel<false, 2>),
-timed live with HIP events on its own stream; ``cpu_baseline`` times the
+kernel, the MFMA gate/up grouped GEMM over predecoded bitmaps
+(grouped_mfma_kernel<2>), timed live with HIP events on its own stream; ``cpu_baseline`` times the
 CPU oracle (GR decode + exact fp16 dequant + fp32 GEMM) on a bounded sample.
 """
 from __future__ import annotations
@@ -136,23 +136,36 @@ def main():
         sweep[f"T{tok}"]["active_experts"] = r["active_experts"]
         log(f"T={tok}: {r['ms_per_step'] * 1e3:.1f} us/step, {r['tokens_per_s']:.0f} tok/s, {r['hbm_gbps']:.0f} GB/s")
 
-    # ---- dominant kernel: fused GR-decode gate/up grouped GEMM, one launch per layer copy
+    # ---- dominant kernel: the MFMA gate/up grouped GEMM over predecoded split bitmaps, one launch
+    # per layer copy, replayed from a graph on its own stream and timed there with HIP events
     x16, logits = main_res["x16"], main_res["logits"]
     w, sel = moe.route_topk(logits, SPEC.top_k, SPEC.renormalize)
     route = ext.build_grouped_route_device(sel, SPEC.num_experts, 4)
     rows = int(sel.numel())
+    slots = min(SPEC.num_experts, rows)
+    eid = route["expert_ids"][:slots]
+    seg = route["segment_offsets"][: slots + 1]
+    prob = route["problem_offsets"][: slots + 1]
     hid_g = ext.backbone_linear(x16, base_backbones["gate"], row_index=route["grouped_token_indices"])
     hid_u = ext.backbone_linear(x16, base_backbones["up"], row_index=route["grouped_token_indices"])
-    tile_bound = rows // 4 + min(SPEC.num_experts, rows) + 1
-    empty = x16.new_empty((0, 0))
-    keys = ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "q_gmap_gr_words", "q_gmap_gr_offsets",
-            "q_gmap_gr_meta", "c_map", "g_idx", "col_pack3", "row_pack3", "output_scale")
+    tile_bound = rows // 4 + slots + 1
+    names = ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx", "col_pack3", "row_pack3")
+    nblk = int(layer["gate"]["q_gmap_gr_meta"].shape[1])
+    decoded = []
+    for pl, _ in copies:
+        pair = []
+        for p in ("gate", "up"):
+            buf = torch.empty((slots, nblk, 128), dtype=torch.int32, device=dev)
+            pair.append(ext.compact3_tris_precomputed_grouped_block_gr_predecode(
+                buf, eid, pl[p]["q_gmap_gr_words"], pl[p]["q_gmap_gr_offsets"], pl[p]["q_gmap_gr_meta"],
+                SPEC.rank // 32, SPEC.intermediate))
+        decoded.append(pair)
 
     def dual(i):
         pl = copies[i][0]
-        return ext.compact3_tris_precomputed_grouped_dual_forward_block_gr(
-            hid_g, hid_u, route["expert_ids"], route["segment_offsets"], route["problem_offsets"], tile_bound,
-            *[pl["gate"][k] for k in keys], False, empty, *[pl["up"][k] for k in keys], False, empty, True)
+        return ext.compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
+            hid_g, hid_u, eid, seg, prob, tile_bound, decoded[i][0], *[pl["gate"][k] for k in names],
+            decoded[i][1], *[pl["up"][k] for k in names], True)
 
     kstream = torch.cuda.Stream(device=dev)
     kstream.wait_stream(torch.cuda.current_stream())
@@ -173,12 +186,12 @@ def main():
         kstream.synchronize()
     kernel_s = ks.elapsed_time(ke) / 1e3 / (args.kernel_reps * len(copies))
     active = main_res["active"]
-    dual_bytes = (synthetic.payload_nbytes(layer["gate"], active) + synthetic.payload_nbytes(layer["up"], active)
+    dual_bytes = (synthetic.predecoded_nbytes(layer["gate"], active) + synthetic.predecoded_nbytes(layer["up"], active)
                   + 2 * rows * SPEC.rank * 2 + 2 * rows * SPEC.intermediate * 2)
     achieved = dual_bytes / kernel_s / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                "kernel": "grouped_gemm_kernel<false, 2> (fused GR decode + dequant gate/up GEMM)",
+                "kernel": "grouped_mfma_kernel<2> (predecoded gate/up grouped GEMM)",
                 "kernel_us": round(kernel_s * 1e6, 2), "bytes_per_launch": int(dual_bytes)}
     log(f"dual GEMM: {kernel_s * 1e6:.1f} us/launch, {achieved:.0f} GB/s algorithmic")
 

@@ -446,6 +446,7 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
                         const int32_t* segment_offsets, int num_segments, const int32_t* decoded_a,
                         const int32_t* decoded_b, const tris_compact3_payload* pa, const tris_compact3_payload* pb,
                         uint16_t* out_a, uint16_t* out_b, void* stream, const char* who);
+bool grouped_mfma_supported(const tris_compact3_payload* p, const uint16_t* hidden);
 
 }  // namespace tris
 
@@ -488,7 +489,7 @@ extern "C" int tris_grouped_forward_block_gr_predecoded(const uint16_t* hidden, 
   tris_compact3_payload p = *payload;  // the predecoded kernels apply no scale or bias
   p.has_output_scale = 0;
   p.has_bias = 0;
-  if (p.use_uniform_k64_groups) {
+  if (grouped_mfma_supported(&p, hidden)) {
     if (total_problem_tiles <= 0) return TRIS_OK;
     return launch_grouped_mfma(hidden, nullptr, batch, expert_ids, segment_offsets, num_segments, decoded, nullptr,
                                &p, nullptr, output, nullptr, stream, "tris_grouped_forward_block_gr_predecoded");
@@ -512,7 +513,7 @@ extern "C" int tris_grouped_dual_forward_block_gr_predecoded(
   tris_compact3_payload pb = *payload_b;
   pa.has_output_scale = pb.has_output_scale = 0;
   pa.has_bias = pb.has_bias = 0;
-  if (pa.use_uniform_k64_groups && pb.use_uniform_k64_groups) {
+  if (grouped_mfma_supported(&pa, hidden_a) && grouped_mfma_supported(&pb, hidden_b)) {
     if (total_problem_tiles <= 0) return TRIS_OK;
     TRIS_REQUIRE(pa.num_experts == pb.num_experts, "tris_grouped_dual_forward_block_gr_predecoded: expert count mismatch");
     return launch_grouped_mfma(hidden_a, hidden_b, batch, expert_ids, segment_offsets, num_segments, decoded_a,

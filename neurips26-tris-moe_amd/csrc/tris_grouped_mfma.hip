@@ -1,32 +1,30 @@
 // Grouped compact3 expert GEMM on MFMA for decode-sized segments, reading
 // dense (predecoded) split bitmaps.
 //
-// Arithmetic.  A non-salient weight is w[n,k] = s1 * C_j[k] * R_j[n,g] with
-// j = d if the split bit is set, else nd, s1 = +-1 from qweight1
-// (TriSMoE_cuda_kernel.cu:665-774).  Factoring the per-column factor into the
-// activations, y_j[r,k] = fp16(C_j[k] * x[r,k]), gives
-//   out[r,n] = sum_g R_nd[n,g] * sum_k y_nd[r,k] * s1*(1-g)
-//            + R_d[n,g]  * sum_k y_d[r,k]  * s1*g          (non-salient k)
-//            + sum over salient k of x[r,k] * w_s[n,k]      (exact fp16 weight)
-// so the per-weight work is turning bits into +-1/0 operands.  The fp16
-// roundings differ from the reference's (the per-weight product C_j*R_j is
-// not rounded to fp16; C_j*x is), which stays within the layer tolerance;
-// bit-exact weights are produced by the dequant kernel.
+// Arithmetic.  Every non-salient weight is the reference's exact fp16 value
+// w[n,k] = s1 * fp16(C_j[k] * R_j[n,g]) with j = d if the split bit is set,
+// else nd, and s1 = +-1 from qweight1 (TriSMoE_cuda_kernel.cu:665-774); the
+// products are formed with packed fp16 multiplies (round to nearest even, as
+// __hmul).  The choice of j and the sign come from the bit planes as two
+// selector pairs sd, sn in {0, +1, -1}: w = fma(sd, P_d, sn * P_nd), exact
+// because one of the two terms is zero.  Salient columns (a few per cent,
+// w = fp16(+-fp16(C0*R0) +- fp16(C1*R1))) take a VALU path with lane = output
+// column and are zero in the MFMA operand.  Products with the activations are
+// exact in fp32 and accumulate in fp32, as in the reference's tensor-core
+// kernel (TriSMoE_cuda_kernel.cu:4889-5093).
 //
-// MFMA v_mfma_f32_16x16x32_f16: A rows 0-7 are y_nd for up to 8 segment rows,
-// rows 8-15 are y_d for the same rows; B is S = s1 (+-1.0) or X = s1*g
-// (0 or +-1.0).  Lane group kg (lanes 16kg..16kg+15) supplies the 8 columns
+// Operand layout (v_mfma_f32_16x16x32_f16): A rows are up to 16 rows of one
+// segment; lane group kg (lanes 16kg..16kg+15) supplies the 8 columns
 // k = kg + 4i (i = 0..7) of each 32-column packed row, so after one shift the
-// needed sign / split bits sit at nibble positions 4i of a word; OR-ing in the
-// fp4 (e2m1) exponent pattern gives eight fp4 values (+-1.0 = 0b0010 / 0b1010,
-// 0 = 0b0000) that v_cvt_scalef32_pk_f16_fp4 expands two at a time to fp16.
-// The activations are staged in LDS in the same permuted column order.  Per
-// 64-column tile the accumulators are folded with the tile group's row
-// scales: nd rows take R_nd*(A.S - A.X), d rows take R_d*(A.X).  Salient
-// columns (a few per cent) take an exact VALU path with lane = output column.
+// sign / split / salient bits of those columns sit at nibble positions 4i of a
+// word.  OR-ing in the fp4 (e2m1) exponent pattern gives eight fp4 selectors
+// (+-1.0 = 0b0010 / 0b1010, 0 = 0b0000) that v_cvt_scalef32_pk_f16_fp4
+// expands two at a time to fp16 pairs.  Activations and the column factors are
+// staged in LDS in the same permuted column order, so each lane reads its 8
+// values with one 16-byte LDS load.
 //
 // Work decomposition: workgroup = 4 wavefronts = one 64-output tile x one
-// tile of <= 8 rows of one segment x one projection (blockIdx.z); wavefront w
+// tile of <= 16 rows of one segment x one projection (blockIdx.z); wavefront w
 // takes K columns [128w, 128w+128) of every 512-column chunk and issues all of
 // its global loads for the chunk before computing; the four partial results
 // are reduced through LDS.  Requires each 64-column K tile to lie in a single
@@ -41,12 +39,13 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMfWaves = 4;
 constexpr int kMfThreads = kMfWaves * kWave;
-constexpr int kMfRows = 8;          // segment rows per workgroup tile
+constexpr int kMfRows = 16;         // segment rows per workgroup tile
 constexpr int kMfChunk = 512;       // K columns staged per pass
 constexpr int kMfWaveK = kMfChunk / kMfWaves;
-constexpr int kMfYStride = kMfChunk + 8;  // fp16 elements per staged row (pad breaks bank aliasing)
+constexpr int kMfXStride = kMfChunk + 8;  // fp16 elements per staged row (pad breaks bank aliasing)
 constexpr int kMfPR = kMfWaveK / 32;      // packed rows per wave per chunk
 constexpr int kMfKT = kMfWaveK / kTileK;  // 64-column K tiles per wave per chunk
+constexpr int kMfRuns = kMfRows * (kMfChunk / 8) / kMfThreads;  // 8-column activation runs per thread
 
 struct MfmaProj {
   const uint16_t* hidden;  // [batch, rank]
@@ -66,14 +65,18 @@ struct MfmaArgs {
 // k % 4, element k / 4.
 __device__ __forceinline__ int mf_perm32(int k) { return 8 * (k & 3) + (k >> 2); }
 
-// Eight fp4 nibbles -> eight fp16 values (v_cvt_scalef32_pk_f16_fp4, two per byte).
-__device__ __forceinline__ f16x8 fp4x8_to_f16x8(uint32_t nib) {
-  const f16x2 h0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(nib, 1.0f, 0);
-  const f16x2 h1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(nib, 1.0f, 1);
-  const f16x2 h2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(nib, 1.0f, 2);
-  const f16x2 h3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(nib, 1.0f, 3);
-  return f16x8{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+// Nibbles 2i, 2i+1 (byte i) of eight fp4 values -> two fp16 (low nibble -> low half).
+__device__ __forceinline__ f16x2 fp4x2_to_f16x2(uint32_t nib, int byte_sel) {
+  switch (byte_sel) {
+    case 0: return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(nib, 1.0f, 0);
+    case 1: return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(nib, 1.0f, 1);
+    case 2: return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(nib, 1.0f, 2);
+    default: return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(nib, 1.0f, 3);
+  }
 }
+
+__device__ __forceinline__ f16x2 u32_as_f16x2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
+__device__ __forceinline__ uint32_t f16x2_as_u32(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
 
 // Same mapping as the in-kernel-decode GEMM (tris_grouped.hip).
 __device__ inline bool mf_map_row_tile(const int32_t* __restrict__ seg, int nseg, int tile, int row_tile, int* s_out,
@@ -114,9 +117,10 @@ __device__ inline bool mf_map_row_tile(const int32_t* __restrict__ seg, int nseg
 
 template <int kNumProj>
 __global__ __launch_bounds__(kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t ys[16][kMfYStride];
-  __shared__ uint16_t xs_sal[kMfRows][kMfChunk];  // raw fp16 x (natural order) for the salient path
-  __shared__ uint32_t col_sal[kMfChunk];          // s_c1 | s_c2 << 16 per column
+  __shared__ __attribute__((aligned(16))) uint16_t xs[kMfRows][kMfXStride];  // activations, staged order
+  __shared__ __attribute__((aligned(16))) uint16_t cds[kMfChunk];            // C_d, staged order
+  __shared__ __attribute__((aligned(16))) uint16_t cns[kMfChunk];            // C_nd, staged order
+  __shared__ uint32_t col_sal[kMfChunk];                                     // C0 | C1 << 16, natural order
   __shared__ float red[kMfWaves][kMfRows][kWave];
 
   const MfmaProj& pa = a.proj[kNumProj == 1 ? 0 : blockIdx.z];
@@ -133,8 +137,9 @@ __global__ __launch_bounds__(kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
   const int e = a.expert_ids[s];
   uint16_t* out = pa.out;
   if (e < 0 || e >= p.num_experts) {
-    if (wave == 0 && n0 + lane < N) {
-      for (int r = 0; r < rc; ++r) out[static_cast<int64_t>(row0 + r) * N + n0 + lane] = 0;
+    for (int idx = tid; idx < rc * kTileOut; idx += kMfThreads) {
+      const int n = n0 + idx % kTileOut;
+      if (n < N) out[static_cast<int64_t>(row0 + idx / kTileOut) * N + n] = 0;
     }
     return;
   }
@@ -217,35 +222,47 @@ __global__ __launch_bounds__(kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
     const int q2row0 = q2p[0] >> 5;
     const uint32_t q2w0 = (nv_lane && q2row0 < p.qweight2_sparse_rows && q2p[kMfPR] > q2p[0])
                               ? static_cast<uint32_t>(q2_e[static_cast<int64_t>(q2row0) * N + n_lane]) : 0u;
-    // staging loads: thread handles columns kc+tid and kc+tid+256 for every row < rc
+    // staging loads: activations as 8-column runs (row idx / 64, run idx % 64; rank is a
+    // multiple of 64, so a run lies wholly inside or outside the matrix), column factors
+    // for columns kc + tid and kc + tid + 256
+    uint4 xv[kMfRuns];
+#pragma unroll
+    for (int h = 0; h < kMfRuns; ++h) {
+      const int idx = tid + h * kMfThreads;
+      const int r = idx / (kMfChunk / 8);
+      const int k = kc + (idx % (kMfChunk / 8)) * 8;
+      xv[h] = (r < rc && k < rank) ? *reinterpret_cast<const uint4*>(hid + static_cast<int64_t>(r) * rank + k)
+                                   : make_uint4(0u, 0u, 0u, 0u);
+    }
     uint64_t cpv[2];
-    uint32_t cmk[2];
-    uint16_t xv[2][kMfRows];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int k = kc + tid + h * kMfThreads;
-      const bool kv = k < rank;
-      cpv[h] = kv ? static_cast<uint64_t>(col_e[k]) : 0ull;
-      cmk[h] = kv ? static_cast<uint32_t>(cmap_e[k >> 5]) : 0u;
-#pragma unroll
-      for (int r = 0; r < kMfRows; ++r) xv[h][r] = (kv && r < rc) ? hid[static_cast<int64_t>(r) * rank + k] : 0;
+      cpv[h] = k < rank ? static_cast<uint64_t>(col_e[k]) : 0ull;
     }
     __syncthreads();  // previous chunk's LDS readers are done
+#pragma unroll
+    for (int h = 0; h < kMfRuns; ++h) {
+      const int idx = tid + h * kMfThreads;
+      const int r = idx / (kMfChunk / 8);
+      const int c = (idx % (kMfChunk / 8)) * 8;  // run start within the chunk (a multiple of 8)
+      // columns c + b and c + b + 4 (b < 4) are neighbours in the staged order
+      const uint32_t w[4] = {xv[h].x, xv[h].y, xv[h].z, xv[h].w};
+      const int base = (c & ~31) + ((c & 31) >> 2);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t lo = (w[b >> 1] >> (16 * (b & 1))) & 0xFFFFu;
+        const uint32_t hi = (w[2 + (b >> 1)] >> (16 * (b & 1))) & 0xFFFFu;
+        *reinterpret_cast<uint32_t*>(&xs[r][base + 8 * b]) = lo | (hi << 16);
+      }
+    }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int j = tid + h * kMfThreads;
       const int pj = (j & ~31) + mf_perm32(j & 31);
-      const bool salient = (cmk[h] >> (j & 31)) & 1u;
-      const uint16_t cd = static_cast<uint16_t>(cpv[h] >> 32);
-      const uint16_t cnd = static_cast<uint16_t>(cpv[h] >> 48);
+      cds[pj] = static_cast<uint16_t>(cpv[h] >> 32);
+      cns[pj] = static_cast<uint16_t>(cpv[h] >> 48);
       col_sal[j] = static_cast<uint32_t>(cpv[h]);
-#pragma unroll
-      for (int r = 0; r < kMfRows; ++r) {
-        const uint16_t x = xv[h][r];
-        ys[r][pj] = salient ? 0 : hmul_bits(cnd, x);
-        ys[kMfRows + r][pj] = salient ? 0 : hmul_bits(cd, x);
-        xs_sal[r][j] = x;
-      }
     }
     __syncthreads();
 
@@ -254,37 +271,43 @@ __global__ __launch_bounds__(kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
     for (int t = 0; t < kMfKT; ++t) {
       const int kt = kc + wave * kMfWaveK + t * kTileK;
       if (kt >= rank) break;
-      f32x4 acc_s[4], acc_x[4];
+      f16x2 rd2[4], rn2[4];
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct) {
-        acc_s[ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        acc_x[ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        const uint32_t d = static_cast<uint32_t>(rp[t][ct] >> 32) & 0xFFFFu;
+        const uint32_t nd = static_cast<uint32_t>(rp[t][ct] >> 48);
+        rd2[ct] = u32_as_f16x2(d | (d << 16));
+        rn2[ct] = u32_as_f16x2(nd | (nd << 16));
       }
 #pragma unroll
       for (int lpr = 0; lpr < kGrPackedRows; ++lpr) {
         const int j = 2 * t + lpr;
         if (pr0 + j >= packed_rows) break;
-        const int kl = (pr0 + j) * 32 - kc;
-        const f16x8 av = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&ys[i16][kl + 8 * kg]));
+        const int kl = (pr0 + j) * 32 - kc + 8 * kg;
+        const f16x8 av = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&xs[i16][kl]));
+        const uint4 cdv = *reinterpret_cast<const uint4*>(&cds[kl]);
+        const uint4 cnv = *reinterpret_cast<const uint4*>(&cns[kl]);
+        const uint32_t cd[4] = {cdv.x, cdv.y, cdv.z, cdv.w};
+        const uint32_t cn[4] = {cnv.x, cnv.y, cnv.z, cnv.w};
+        const uint32_t nsal = (~cmw[j] >> kg) & 0x11111111u;     // 1 = non-salient column
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct) {
-          const uint32_t nq = ((~qw[j][ct]) >> kg) & 0x11111111u;   // 1 = negative
-          const uint32_t gs = (gw[j][ct] >> kg) & 0x11111111u;      // 1 = split bit set
-          const uint32_t snib = (nq << 3) | 0x22222222u;            // +-1.0
-          const uint32_t xnib = ((gs & nq) << 3) | (gs << 1);       // g ? +-1.0 : 0
-          acc_s[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, fp4x8_to_f16x8(snib), acc_s[ct], 0, 0, 0);
-          acc_x[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, fp4x8_to_f16x8(xnib), acc_x[ct], 0, 0, 0);
+          const uint32_t neg = ((~qw[j][ct]) >> kg) & 0x11111111u;   // 1 = negative
+          const uint32_t gd = (gw[j][ct] >> kg) & nsal;               // 1 = d term
+          const uint32_t gn = nsal ^ gd;                              // 1 = nd term
+          const uint32_t sd = (gd << 1) | ((gd & neg) << 3);          // fp4 +-1.0 / 0
+          const uint32_t sn = (gn << 1) | ((gn & neg) << 3);
+          uint32_t b[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const f16x2 pd = u32_as_f16x2(cd[i]) * rd2[ct];
+            const f16x2 pn = u32_as_f16x2(cn[i]) * rn2[ct];
+            const f16x2 tn = fp4x2_to_f16x2(sn, i) * pn;
+            b[i] = f16x2_as_u32(__builtin_elementwise_fma(fp4x2_to_f16x2(sd, i), pd, tn));
+          }
+          const f16x8 bv = __builtin_bit_cast(f16x8, make_uint4(b[0], b[1], b[2], b[3]));
+          tot[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, tot[ct], 0, 0, 0);
         }
-      }
-      // Fold with the tile group's row scales: lane groups 0-1 hold nd rows, 2-3 hold d rows.
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        const float r_d = h2f(static_cast<uint16_t>(rp[t][ct] >> 32));
-        const float r_nd = h2f(static_cast<uint16_t>(rp[t][ct] >> 48));
-        const float cs = kg < 2 ? r_nd : 0.0f;
-        const float cx = kg < 2 ? -r_nd : r_d;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) tot[ct][v] += cs * acc_s[ct][v] + cx * acc_x[ct][v];
       }
     }
 
@@ -308,43 +331,37 @@ __global__ __launch_bounds__(kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
         uint16_t t2 = hmul_bits(static_cast<uint16_t>(cp >> 16), static_cast<uint16_t>(rps[t] >> 16));
         if (!((q2w >> (sidx & 31)) & 1u)) t2 ^= 0x8000u;
         const float wf = h2f(hadd_bits(t1, t2));
+        const int xpos = (kl & ~31) + mf_perm32(kl & 31);
 #pragma unroll
         for (int r = 0; r < kMfRows; ++r) {
-          if (r < rc) sal[r] = fmaf(h2f(xs_sal[r][kl]), wf, sal[r]);
+          if (r < rc) sal[r] = fmaf(h2f(xs[r][xpos]), wf, sal[r]);
         }
         ++sidx;
       }
     }
   }
 
-  // tot[ct][v] = row 4*(kg%2)+v of the nd (kg<2) or d (kg>=2) part for column 16ct+i16.
-#pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-#pragma unroll
-    for (int v = 0; v < 4; ++v) tot[ct][v] += __shfl_xor(tot[ct][v], 32);
-  }
+  // tot[ct][v] = row 4*kg+v, column 16ct+i16.
   __syncthreads();
 #pragma unroll
   for (int r = 0; r < kMfRows; ++r) red[wave][r][lane] = sal[r];
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
   __builtin_amdgcn_wave_barrier();
-  if (kg < 2) {
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
+  for (int ct = 0; ct < 4; ++ct) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) red[wave][4 * kg + v][16 * ct + i16] += tot[ct][v];
-    }
+    for (int v = 0; v < 4; ++v) red[wave][4 * kg + v][16 * ct + i16] += tot[ct][v];
   }
   __syncthreads();
-  if (wave == 0 && nv_lane) {
-    const float scale = p.has_output_scale ? h2f(p.output_scale[static_cast<int64_t>(e) * N + n_lane]) : 1.0f;
-    const float bias = p.has_bias ? h2f(p.bias[static_cast<int64_t>(e) * N + n_lane]) : 0.0f;
-    for (int r = 0; r < rc; ++r) {
-      float v = red[0][r][lane] + red[1][r][lane] + red[2][r][lane] + red[3][r][lane];
-      if (p.has_output_scale) v = v * scale;
-      if (p.has_bias) v = v + bias;
-      out[static_cast<int64_t>(row0 + r) * N + n_lane] = f2h_bits(v);
-    }
+  for (int idx = tid; idx < rc * kTileOut; idx += kMfThreads) {
+    const int r = idx / kTileOut;
+    const int c = idx % kTileOut;
+    const int n = n0 + c;
+    if (n >= N) continue;
+    float v = red[0][r][c] + red[1][r][c] + red[2][r][c] + red[3][r][c];
+    if (p.has_output_scale) v = v * h2f(p.output_scale[static_cast<int64_t>(e) * N + n]);
+    if (p.has_bias) v = v + h2f(p.bias[static_cast<int64_t>(e) * N + n]);
+    out[static_cast<int64_t>(row0 + r) * N + n] = f2h_bits(v);
   }
 }
 
@@ -386,6 +403,14 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
     hipLaunchKernelGGL((grouped_mfma_kernel<1>), grid, dim3(kMfThreads), 0, s, args);
   }
   return check_launch(who);
+}
+
+// True when the MFMA kernel can run this payload: uniform 64-column groups (so
+// a 64-column K tile has one row scale) and a rank that is a whole number of
+// 64-column tiles, with 16-byte aligned activations (8-column loads).
+bool grouped_mfma_supported(const tris_compact3_payload* p, const uint16_t* hidden) {
+  return p != nullptr && p->use_uniform_k64_groups && p->rank > 0 && p->rank % kTileK == 0 &&
+         reinterpret_cast<uintptr_t>(hidden) % 16 == 0;
 }
 
 }  // namespace tris

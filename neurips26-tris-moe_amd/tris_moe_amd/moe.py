@@ -35,12 +35,18 @@ def route_topk(router_logits: torch.Tensor, top_k: int, renormalize: bool):
 
 def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, selected_experts: torch.Tensor,
                         payloads: dict, backbones: dict, num_experts: int, output_dtype=torch.bfloat16,
-                        shared_expert=None) -> torch.Tensor:
+                        shared_expert=None, expert_path: str = "auto") -> torch.Tensor:
     """The grouped MoE layer on the HIP kernels with no host synchronisation.
 
     x16 fp16 [T, H]; routing_weights [T, k] (cast to fp16 as in modeling_mixtral.py:555);
     selected_experts int64 [T, k]; payloads {gate, up, down} device payload dicts;
-    backbones {gate, up, down} fp16 [rank, in].  Returns [T, H] in output_dtype."""
+    backbones {gate, up, down} fp16 [rank, in].  Returns [T, H] in output_dtype.
+
+    expert_path: "predecoded" decodes the split bitmaps once per projection and runs the MFMA
+    grouped GEMMs (needs uniform 64-column groups and no output scale or bias); "fused" decodes
+    inside the exact grouped GEMM; "auto" takes "predecoded" whenever the payloads allow it."""
+    if expert_path not in ("auto", "fused", "predecoded"):
+        raise ValueError(f"unknown expert_path {expert_path!r}")
     T, H = int(x16.size(0)), int(x16.size(1))
     k = int(selected_experts.size(1))
     R = T * k
@@ -57,6 +63,13 @@ def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, select
     hid_u = ext.backbone_linear(x16, backbones["up"], row_index=gti)
     pg, pu, pd = payloads["gate"], payloads["up"], payloads["down"]
     uniform = bool(pg.get("_compact3_k64_groups_uniform", False) and pu.get("_compact3_k64_groups_uniform", False))
+    predecodable = uniform and bool(pd.get("_compact3_k64_groups_uniform", False)) and not any(
+        bool(p["has_output_scale"]) or bool(p["has_bias"]) for p in (pg, pu, pd))
+    if expert_path == "predecoded" and not predecodable:
+        raise RuntimeError("the predecoded expert path needs uniform 64-column groups and no output scale or bias")
+    if predecodable and expert_path != "fused":
+        return _predecoded_moe_forward(x16, routing_weights, route, hid_g, hid_u, payloads, backbones, num_experts,
+                                       R, output_dtype, shared_expert)
     empty = x16.new_empty((0, 0))
     g_out, u_out = ext.compact3_tris_precomputed_grouped_dual_forward_block_gr(
         hid_g, hid_u, expert_ids, seg, prob, tile_bound,
@@ -74,6 +87,10 @@ def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, select
         pd["q_gmap_gr_offsets"], pd["q_gmap_gr_meta"], pd["c_map"], pd["g_idx"], pd["col_pack3"], pd["row_pack3"],
         pd["output_scale"], bool(pd["has_output_scale"]), pd["bias"] if pd["has_bias"] else empty,
         bool(pd["has_bias"]), bool(pd.get("_compact3_k64_groups_uniform", False)))
+    return _combine(x16, d_out, route, routing_weights, output_dtype, shared_expert)
+
+
+def _combine(x16, d_out, route, routing_weights, output_dtype, shared_expert):
     w16 = routing_weights.to(torch.float16).contiguous()
     shared = None
     if shared_expert is not None:
@@ -81,6 +98,36 @@ def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, select
         shared = F.linear(F.silu(F.linear(x16, wg)) * F.linear(x16, wu), wd).contiguous()
     out = ext.moe_combine(d_out, route["inverse_perm"], w16, shared)
     return out if output_dtype == torch.bfloat16 else out.to(output_dtype)
+
+
+def _predecoded_moe_forward(x16, routing_weights, route, hid_g, hid_u, payloads, backbones, num_experts, R,
+                            output_dtype, shared_expert):
+    """Uniform-group payloads without output scale or bias: GR-decode every routed expert's split
+    bitmaps once per projection (TriSMoE_cuda.cpp:836-853), then run the predecoded grouped GEMMs
+    (TriSMoE_cuda.cpp:855-889, 922-974).  Active experts come first in the padded route, so
+    min(num_experts, R) segments cover every routed row and the later segments are empty."""
+    slots = min(num_experts, R)
+    eid = route["expert_ids"][:slots]
+    seg = route["segment_offsets"][: slots + 1]
+    prob = route["problem_offsets"][: slots + 1]
+    tile_bound = R // GROUPED_SEGMENT_M_TILE + slots + 1
+    pg, pu, pd = payloads["gate"], payloads["up"], payloads["down"]
+    decoded = {}
+    for name, p in (("gate", pg), ("up", pu), ("down", pd)):
+        packed_rows, n = int(p["qweight1"].size(1)), int(p["qweight1"].size(2))
+        nblk = ((packed_rows + 1) // 2) * ((n + 63) // 64)
+        buf = torch.empty((slots, nblk, 128), dtype=torch.int32, device=x16.device)
+        decoded[name] = ext.compact3_tris_precomputed_grouped_block_gr_predecode(
+            buf, eid, p["q_gmap_gr_words"], p["q_gmap_gr_offsets"], p["q_gmap_gr_meta"], packed_rows, n)
+    names = ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx", "col_pack3", "row_pack3")
+    g_out, u_out = ext.compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
+        hid_g, hid_u, eid, seg, prob, tile_bound, decoded["gate"], *[pg[k] for k in names], decoded["up"],
+        *[pu[k] for k in names], True)
+    mlp = F.silu(g_out) * u_out
+    hid_d = ext.backbone_linear(mlp, backbones["down"])
+    d_out = ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
+        hid_d, eid, seg, prob, tile_bound, decoded["down"], *[pd[k] for k in names], True)
+    return _combine(x16, d_out, route, routing_weights, output_dtype, shared_expert)
 
 
 class TrisSparseMoeBlock(nn.Module):

@@ -208,3 +208,17 @@ def payload_nbytes(payload: dict, experts=None) -> int:
         total += payload["c_map"][e].nbytes + payload["g_idx"][e].nbytes
         total += payload["col_pack3"][e].nbytes + payload["row_pack3"][e].nbytes
     return int(total)
+
+
+def predecoded_nbytes(payload: dict, experts=None) -> int:
+    """Bytes a predecoded grouped GEMM reads for the listed experts: the payload minus the GR
+    stream (words, offsets, meta) plus the decoded split bitmap (128 words per GR block)."""
+    E = payload["qweight1"].shape[0]
+    ids = list(range(E) if experts is None else experts)
+    nblk = int(payload["q_gmap_gr_meta"].shape[1])
+    total = payload_nbytes(payload, ids)
+    for e in ids:
+        total -= 4 * int(payload["q_gmap_gr_offsets"][e][-1])
+        total -= payload["q_gmap_gr_offsets"][e].nbytes + payload["q_gmap_gr_meta"][e].nbytes
+        total += nblk * 128 * 4
+    return int(total)

@@ -377,7 +377,7 @@ def test_backbone_matches_fp32(tris, cuda, tokens, in_f, rank):
 
 
 # --------------------------------------------------------------------- layer
-def _run_layer(tris, oracle_mod, cuda, spec, tokens, seed):
+def _run_layer(tris, oracle_mod, cuda, spec, tokens, seed, expert_path="auto"):
     syn = tris["synthetic"]
     ql = tris["qlinear"]
     layer = syn.make_layer(spec, seed, tris["ext"].gr_encode)
@@ -391,7 +391,12 @@ def _run_layer(tris, oracle_mod, cuda, spec, tokens, seed):
                                            renormalize=spec.renormalize, shared_expert=shared)
     x = torch.from_numpy(inp["x"]).to(cuda).to(torch.bfloat16)
     logits = torch.from_numpy(inp["router_logits"]).to(cuda)
-    out = block.forward_routed(x, logits).float().cpu().numpy()
+    if expert_path == "auto":
+        out = block.forward_routed(x, logits).float().cpu().numpy()
+    else:
+        wt, st = tris["moe"].route_topk(logits, spec.top_k, spec.renormalize)
+        out = tris["moe"].grouped_moe_forward(x.to(torch.float16), wt, st, payloads, backbones, spec.num_experts,
+                                              torch.bfloat16, shared, expert_path=expert_path).float().cpu().numpy()
     w, sel = oracle_mod.route_topk(inp["router_logits"], spec.top_k, spec.renormalize)
     want = oracle_mod.moe_layer(inp["x"].astype(np.float16), w, sel, {p: layer[p] for p in ("gate", "up", "down")},
                                 layer["backbones"], spec.num_experts, layer.get("shared_expert"))
@@ -406,13 +411,13 @@ def test_layer_olmoe_c0(tris, oracle_mod, cuda):
     assert_close(out, want, "C0 layer")
 
 
-@pytest.mark.parametrize("tokens", [1, 4])
-def test_layer_mixtral_c1_decode(tris, oracle_mod, cuda, tokens):
+@pytest.mark.parametrize("tokens,path", [(1, "auto"), (4, "auto"), (16, "predecoded"), (4, "fused")])
+def test_layer_mixtral_c1_decode(tris, oracle_mod, cuda, tokens, path):
     from tris_moe_amd.configs import C1_MIXTRAL_DECODE
 
-    note(f"layer C1 Mixtral T={tokens}")
-    out, want = _run_layer(tris, oracle_mod, cuda, C1_MIXTRAL_DECODE, tokens, 2000 + tokens)
-    assert_close(out, want, f"C1 layer T={tokens}")
+    note(f"layer C1 Mixtral T={tokens} path={path}")
+    out, want = _run_layer(tris, oracle_mod, cuda, C1_MIXTRAL_DECODE, tokens, 2000 + tokens, path)
+    assert_close(out, want, f"C1 layer T={tokens} {path}")
 
 
 def test_layer_a3b_c3_with_shared_expert(tris, oracle_mod, cuda):
