@@ -8,8 +8,8 @@
 // __hmul).  The choice of j and the sign come from the bit planes as two
 // selector pairs sd, sn in {0, +1, -1}: w = fma(sd, P_d, sn * P_nd), exact
 // because one of the two terms is zero.  Salient columns (a few per cent,
-// w = fp16(+-fp16(C0*R0) +- fp16(C1*R1))) take a VALU path with lane = output
-// column and are zero in the MFMA operand.  Products with the activations are
+// w = fp16(+-fp16(C0*R0) +- fp16(C1*R1))) are zero in that operand and get
+// their own MFMA pass over an LDS table of their exact weights.  Products with the activations are
 // exact in fp32 and accumulate in fp32, as in the reference's tensor-core
 // kernel (TriSMoE_cuda_kernel.cu:4889-5093).
 //
@@ -24,11 +24,17 @@
 // values with one 16-byte LDS load.
 //
 // Work decomposition: workgroup = 4 wavefronts = one 64-output tile x one
-// tile of <= 16 rows of one segment x one projection (blockIdx.z); wavefront w
-// takes K columns [128w, 128w+128) of every 512-column chunk and issues all of
-// its global loads for the chunk before computing; the four partial results
-// are reduced through LDS.  Requires each 64-column K tile to lie in a single
-// group (the reference's UniformK64Groups case).
+// tile of <= 16 rows of one segment x one projection (blockIdx.z).  The
+// workgroup stages the rows' activations and the column factors of a 512-column
+// chunk in LDS once; wavefront w then owns outputs [16w, 16w+16) over the whole
+// chunk, issuing its weight loads (one column per lane, 16 packed rows) before
+// computing, so no partial sums cross wavefronts.  Salient columns are zero in
+// that pass; afterwards each lane writes the exact salient weights of its
+// column (lane group kg takes the salient columns k = kg (mod 4)) into an LDS
+// table, and one or two more MFMA steps multiply the activations gathered at
+// the salient columns by it, into the same fp32 accumulator.  Requires each
+// 64-column K tile to lie in a single group (the reference's UniformK64Groups
+// case) and rank % 64 == 0.
 #include "tris_common.h"
 
 namespace tris {
@@ -41,11 +47,9 @@ constexpr int kMfWaves = 4;
 constexpr int kMfThreads = kMfWaves * kWave;
 constexpr int kMfRows = 16;         // segment rows per workgroup tile
 constexpr int kMfChunk = 512;       // K columns staged per pass
-constexpr int kMfWaveK = kMfChunk / kMfWaves;
 constexpr int kMfXStride = kMfChunk + 8;  // fp16 elements per staged row (pad breaks bank aliasing)
-constexpr int kMfPR = kMfWaveK / 32;      // packed rows per wave per chunk
-constexpr int kMfKT = kMfWaveK / kTileK;  // 64-column K tiles per wave per chunk
-constexpr int kMfRuns = kMfRows * (kMfChunk / 8) / kMfThreads;  // 8-column activation runs per thread
+constexpr int kMfSalWin = 64;             // salient columns per MFMA pass
+constexpr int kMfSalStride = kMfSalWin + 8;
 
 struct MfmaProj {
   const uint16_t* hidden;  // [batch, rank]
@@ -121,7 +125,8 @@ __global__ __launch_bounds__(kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t cds[kMfChunk];            // C_d, staged order
   __shared__ __attribute__((aligned(16))) uint16_t cns[kMfChunk];            // C_nd, staged order
   __shared__ uint32_t col_sal[kMfChunk];                                     // C0 | C1 << 16, natural order
-  __shared__ float red[kMfWaves][kMfRows][kWave];
+  __shared__ uint16_t sal_col[kMfChunk];        // chunk column of the chunk's q-th salient column
+  __shared__ __attribute__((aligned(16))) uint16_t ws[kMfWaves][16][kMfSalStride];  // salient weights
 
   const MfmaProj& pa = a.proj[kNumProj == 1 ? 0 : blockIdx.z];
   const tris_compact3_payload& p = pa.p;
@@ -130,6 +135,9 @@ __global__ __launch_bounds__(kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
   if (n0 >= N) return;
   int s = 0, row0 = 0, rc = 0;
   if (!mf_map_row_tile(a.segment_offsets, a.num_segments, blockIdx.y, kMfRows, &s, &row0, &rc)) return;
+  s = __builtin_amdgcn_readfirstlane(s);  // the mapping is the same in every lane
+  row0 = __builtin_amdgcn_readfirstlane(row0);
+  rc = __builtin_amdgcn_readfirstlane(rc);
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
@@ -151,6 +159,7 @@ __global__ __launch_bounds__(kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
   const int nblk = nkb * nob;
   const int ob = blockIdx.x;
   const int G = p.num_groups;
+  // Per-expert bases; element offsets below stay within 32 bits (checked on the host).
   const int32_t* q1_e = p.qweight1 + static_cast<int64_t>(e) * packed_rows * N;
   const int32_t* q2_e = p.qweight2_sparse + static_cast<int64_t>(e) * p.qweight2_sparse_rows * N;
   const int32_t* q2p_e = p.qweight2_sparse_prefix + static_cast<int64_t>(e) * (packed_rows + 1);
@@ -161,93 +170,53 @@ __global__ __launch_bounds__(kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
   const int32_t* dec_s = pa.decoded + static_cast<int64_t>(s) * nblk * kGrWords;
   const uint16_t* hid = pa.hidden + static_cast<int64_t>(row0) * rank;
 
-  const int i16 = lane % 16;   // MFMA column within a 16-wide tile / A row
-  const int kg = lane / 16;    // MFMA k group
-  f32x4 tot[4];
-#pragma unroll
-  for (int ct = 0; ct < 4; ++ct) tot[ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  float sal[kMfRows];
-#pragma unroll
-  for (int r = 0; r < kMfRows; ++r) sal[r] = 0.0f;
-  const int n_lane = n0 + lane;           // output column of the salient path
-  const bool nv_lane = n_lane < N;
+  const int i16 = lane % 16;   // MFMA column within the wave's 16 outputs / A row
+  const int kg = lane / 16;    // MFMA k group: columns k = kg (mod 4) of every packed row
+  const int n = n0 + 16 * wave + i16;  // this lane's output column
+  const bool nv = n < N;
+  const uint32_t nu = nv ? static_cast<uint32_t>(n) : 0u;
+  f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   for (int kc = 0; kc < rank; kc += kMfChunk) {
-    // ---- issue every global load of this chunk before touching LDS
-    const int pr0 = (kc + wave * kMfWaveK) / 32;
-    uint32_t qw[kMfPR][4], gw[kMfPR][4];
-    uint64_t rp[kMfKT][4];
-    int gt[kMfKT];
+    const int pr0 = kc / 32;
+    const int pr_end = (pr0 + kMfChunk / 32) < packed_rows ? (pr0 + kMfChunk / 32) : packed_rows;
+    // ---- the wave's weight loads for the chunk: 16 packed rows x 1 column per lane
+    uint32_t qw[kMfChunk / 32], gw[kMfChunk / 32];
+    uint64_t rp[kMfChunk / kTileK];
 #pragma unroll
-    for (int j = 0; j < kMfPR; ++j) {
+    for (int j = 0; j < kMfChunk / 32; ++j) {
       const int pr = pr0 + j;
-      const int32_t* blk = dec_s + static_cast<int64_t>((pr >> 1) * nob + ob) * kGrWords + (pr & 1) * kTileOut;
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        const int n = n0 + 16 * ct + i16;
-        const bool ok = pr < packed_rows && n < N;
-        qw[j][ct] = ok ? static_cast<uint32_t>(q1_e[static_cast<int64_t>(pr) * N + n]) : 0u;
-        gw[j][ct] = ok ? static_cast<uint32_t>(blk[16 * ct + i16]) : 0u;
-      }
+      const bool ok = nv && pr < packed_rows;
+      const uint32_t boff = static_cast<uint32_t>(((pr >> 1) * nob + ob) * kGrWords + (pr & 1) * kTileOut +
+                                                  16 * wave + i16);
+      qw[j] = ok ? static_cast<uint32_t>(q1_e[static_cast<uint32_t>(pr) * static_cast<uint32_t>(N) + nu]) : 0u;
+      gw[j] = ok ? static_cast<uint32_t>(dec_s[boff]) : 0u;
     }
 #pragma unroll
-    for (int t = 0; t < kMfKT; ++t) {
-      const int kt = kc + wave * kMfWaveK + t * kTileK;
+    for (int t = 0; t < kMfChunk / kTileK; ++t) {
+      const int kt = kc + t * kTileK;
       const int g = kt < rank ? gidx_e[kt] : -1;
-      gt[t] = g;
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        const int n = n0 + 16 * ct + i16;
-        rp[t][ct] = (g >= 0 && g < G && n < N) ? static_cast<uint64_t>(row_e[static_cast<int64_t>(n) * G + g]) : 0ull;
-      }
+      rp[t] = (nv && g >= 0 && g < G)
+                  ? static_cast<uint64_t>(row_e[nu * static_cast<uint32_t>(G) + static_cast<uint32_t>(g)]) : 0ull;
     }
-    // salient-path operands of this wave's range (lane = output column)
-    uint32_t cmw[kMfPR], q1s[kMfPR];
-    int q2p[kMfPR + 1];
-    uint64_t rps[kMfKT];
-#pragma unroll
-    for (int j = 0; j < kMfPR; ++j) {
-      const int pr = pr0 + j;
-      const int nbits = (rank - pr * 32) < 32 ? (rank - pr * 32) : 32;
-      cmw[j] = pr < packed_rows ? (static_cast<uint32_t>(cmap_e[pr]) & low_mask(nbits)) : 0u;
-      q1s[j] = (nv_lane && pr < packed_rows) ? static_cast<uint32_t>(q1_e[static_cast<int64_t>(pr) * N + n_lane]) : 0u;
-      q2p[j] = pr < packed_rows ? q2p_e[pr] : 0;
-    }
-    q2p[kMfPR] = (pr0 + kMfPR) <= packed_rows ? q2p_e[pr0 + kMfPR] : q2p_e[packed_rows];
-#pragma unroll
-    for (int t = 0; t < kMfKT; ++t) {
-      const int g = gt[t];
-      rps[t] = (nv_lane && g >= 0 && g < G) ? static_cast<uint64_t>(row_e[static_cast<int64_t>(n_lane) * G + g]) : 0ull;
-    }
-    const int q2row0 = q2p[0] >> 5;
-    const uint32_t q2w0 = (nv_lane && q2row0 < p.qweight2_sparse_rows && q2p[kMfPR] > q2p[0])
-                              ? static_cast<uint32_t>(q2_e[static_cast<int64_t>(q2row0) * N + n_lane]) : 0u;
-    // staging loads: activations as 8-column runs (row idx / 64, run idx % 64; rank is a
-    // multiple of 64, so a run lies wholly inside or outside the matrix), column factors
-    // for columns kc + tid and kc + tid + 256
-    uint4 xv[kMfRuns];
-#pragma unroll
-    for (int h = 0; h < kMfRuns; ++h) {
-      const int idx = tid + h * kMfThreads;
-      const int r = idx / (kMfChunk / 8);
-      const int k = kc + (idx % (kMfChunk / 8)) * 8;
-      xv[h] = (r < rc && k < rank) ? *reinterpret_cast<const uint4*>(hid + static_cast<int64_t>(r) * rank + k)
-                                   : make_uint4(0u, 0u, 0u, 0u);
-    }
-    uint64_t cpv[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int k = kc + tid + h * kMfThreads;
-      cpv[h] = k < rank ? static_cast<uint64_t>(col_e[k]) : 0ull;
-    }
+    const int sbase0 = q2p_e[pr0];                // qweight2_sparse index of the chunk's first salient column
+    const int num_sal = q2p_e[pr_end] - sbase0;   // salient columns in the chunk
+    // first qweight2_sparse row of the chunk's salient columns (usually the only one)
+    const int q2row0 = sbase0 >> 5;
+    const uint32_t q2w0 = (nv && num_sal > 0 && q2row0 < p.qweight2_sparse_rows)
+        ? static_cast<uint32_t>(q2_e[static_cast<uint32_t>(q2row0) * static_cast<uint32_t>(N) + nu]) : 0u;
+    // ---- stage activations (rc rows, 8-column runs; rank is a multiple of 64 so a run is
+    // wholly inside or outside the matrix), column factors and the salient column list
     __syncthreads();  // previous chunk's LDS readers are done
-#pragma unroll
-    for (int h = 0; h < kMfRuns; ++h) {
-      const int idx = tid + h * kMfThreads;
+    for (int idx = tid; idx < kMfRows * (kMfChunk / 8); idx += kMfThreads) {
       const int r = idx / (kMfChunk / 8);
       const int c = (idx % (kMfChunk / 8)) * 8;  // run start within the chunk (a multiple of 8)
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (r < rc && kc + c < rank) {
+        v = *reinterpret_cast<const uint4*>(hid + static_cast<uint32_t>(r * rank + kc + c));
+      }
       // columns c + b and c + b + 4 (b < 4) are neighbours in the staged order
-      const uint32_t w[4] = {xv[h].x, xv[h].y, xv[h].z, xv[h].w};
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
       const int base = (c & ~31) + ((c & 31) >> 2);
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
@@ -256,112 +225,140 @@ __global__ __launch_bounds__(kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
         *reinterpret_cast<uint32_t*>(&xs[r][base + 8 * b]) = lo | (hi << 16);
       }
     }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int j = tid + h * kMfThreads;
+    for (int j = tid; j < kMfChunk; j += kMfThreads) {
+      const int k = kc + j;
+      const bool kv = k < rank;
+      const uint64_t cp = kv ? static_cast<uint64_t>(col_e[k]) : 0ull;
       const int pj = (j & ~31) + mf_perm32(j & 31);
-      cds[pj] = static_cast<uint16_t>(cpv[h] >> 32);
-      cns[pj] = static_cast<uint16_t>(cpv[h] >> 48);
-      col_sal[j] = static_cast<uint32_t>(cpv[h]);
+      cds[pj] = static_cast<uint16_t>(cp >> 32);
+      cns[pj] = static_cast<uint16_t>(cp >> 48);
+      col_sal[j] = static_cast<uint32_t>(cp);
+      if (kv) {
+        const int pr = k >> 5;
+        const int bit = k & 31;
+        const int nbits = (rank - pr * 32) < 32 ? (rank - pr * 32) : 32;
+        const uint32_t cmw = static_cast<uint32_t>(cmap_e[pr]) & low_mask(nbits);
+        if ((cmw >> bit) & 1u) sal_col[q2p_e[pr] - sbase0 + __popc(cmw & ((1u << bit) - 1u))] = static_cast<uint16_t>(j);
+      }
     }
     __syncthreads();
 
-    // ---- MFMA over the wave's K tiles
+    // ---- MFMA over the chunk's packed rows (salient columns are zero here)
 #pragma unroll
-    for (int t = 0; t < kMfKT; ++t) {
-      const int kt = kc + wave * kMfWaveK + t * kTileK;
-      if (kt >= rank) break;
-      f16x2 rd2[4], rn2[4];
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        const uint32_t d = static_cast<uint32_t>(rp[t][ct] >> 32) & 0xFFFFu;
-        const uint32_t nd = static_cast<uint32_t>(rp[t][ct] >> 48);
-        rd2[ct] = u32_as_f16x2(d | (d << 16));
-        rn2[ct] = u32_as_f16x2(nd | (nd << 16));
-      }
-#pragma unroll
-      for (int lpr = 0; lpr < kGrPackedRows; ++lpr) {
-        const int j = 2 * t + lpr;
-        if (pr0 + j >= packed_rows) break;
-        const int kl = (pr0 + j) * 32 - kc + 8 * kg;
+    for (int j = 0; j < kMfChunk / 32; ++j) {
+      const int pr = pr0 + j;
+      if (pr < packed_rows) {
+        const int t = j / 2;
+        const uint32_t d = static_cast<uint32_t>(rp[t] >> 32) & 0xFFFFu;
+        const uint32_t nd = static_cast<uint32_t>(rp[t] >> 48);
+        const f16x2 rd2 = u32_as_f16x2(d | (d << 16));
+        const f16x2 rn2 = u32_as_f16x2(nd | (nd << 16));
+        const int kl = j * 32 + 8 * kg;
         const f16x8 av = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&xs[i16][kl]));
         const uint4 cdv = *reinterpret_cast<const uint4*>(&cds[kl]);
         const uint4 cnv = *reinterpret_cast<const uint4*>(&cns[kl]);
         const uint32_t cd[4] = {cdv.x, cdv.y, cdv.z, cdv.w};
         const uint32_t cn[4] = {cnv.x, cnv.y, cnv.z, cnv.w};
-        const uint32_t nsal = (~cmw[j] >> kg) & 0x11111111u;     // 1 = non-salient column
+        const int nbits = (rank - pr * 32) < 32 ? (rank - pr * 32) : 32;
+        const uint32_t cmw = static_cast<uint32_t>(cmap_e[pr]) & low_mask(nbits);  // salient columns
+        const uint32_t nsal = (~cmw >> kg) & 0x11111111u;                          // 1 = non-salient
+        const uint32_t neg = ((~qw[j]) >> kg) & 0x11111111u;                         // 1 = negative
+        const uint32_t gd = (gw[j] >> kg) & nsal;                                    // 1 = d term
+        const uint32_t gn = nsal ^ gd;                                               // 1 = nd term
+        const uint32_t sd = (gd << 1) | ((gd & neg) << 3);                           // fp4 +-1.0 / 0
+        const uint32_t sn = (gn << 1) | ((gn & neg) << 3);
+        uint32_t b[4];
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-          const uint32_t neg = ((~qw[j][ct]) >> kg) & 0x11111111u;   // 1 = negative
-          const uint32_t gd = (gw[j][ct] >> kg) & nsal;               // 1 = d term
-          const uint32_t gn = nsal ^ gd;                              // 1 = nd term
-          const uint32_t sd = (gd << 1) | ((gd & neg) << 3);          // fp4 +-1.0 / 0
-          const uint32_t sn = (gn << 1) | ((gn & neg) << 3);
-          uint32_t b[4];
+        for (int i = 0; i < 4; ++i) {
+          const f16x2 pd = u32_as_f16x2(cd[i]) * rd2;
+          const f16x2 pn = u32_as_f16x2(cn[i]) * rn2;
+          const f16x2 tn = fp4x2_to_f16x2(sn, i) * pn;
+          b[i] = f16x2_as_u32(__builtin_elementwise_fma(fp4x2_to_f16x2(sd, i), pd, tn));
+        }
+        const f16x8 bv = __builtin_bit_cast(f16x8, make_uint4(b[0], b[1], b[2], b[3]));
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
+      }
+    }
+
+    // ---- salient columns, kMfSalWin at a time: each lane writes the exact fp16 weights of its
+    // output column for the salient columns k = kg (mod 4) into ws, then the wave multiplies
+    // the gathered activations by ws on MFMA.
+    for (int w0 = 0; w0 < num_sal; w0 += kMfSalWin) {
+#pragma unroll
+      for (int q = kg * (kMfSalWin / 4); q < (kg + 1) * (kMfSalWin / 4); ++q) ws[wave][i16][q] = 0;
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int j = 0; j < kMfChunk / 32; ++j) {
+        const int pr = pr0 + j;
+        if (pr < packed_rows) {
+          const int t = j / 2;
+          const int nbits = (rank - pr * 32) < 32 ? (rank - pr * 32) : 32;
+          const uint32_t cmw = static_cast<uint32_t>(cmap_e[pr]) & low_mask(nbits);
+          uint32_t m = cmw & (0x11111111u << kg);
+          const int sbase = q2p_e[pr];
+          while (m != 0u) {
+            const int bit = __builtin_ctz(m);
+            m &= m - 1u;
+            const int sidx = sbase + __popc(cmw & ((1u << bit) - 1u));  // qweight2_sparse index
+            const int q = sidx - sbase0 - w0;                            // slot in the window
+            if (q >= 0 && q < kMfSalWin) {
+              uint32_t q2w = q2w0;
+              if ((sidx >> 5) != q2row0) {
+                q2w = nv ? static_cast<uint32_t>(
+                               q2_e[static_cast<uint32_t>(sidx >> 5) * static_cast<uint32_t>(N) + nu]) : 0u;
+              }
+              const uint32_t cp = col_sal[j * 32 + bit];
+              uint16_t t1 = hmul_bits(static_cast<uint16_t>(cp), static_cast<uint16_t>(rp[t]));
+              if (!((qw[j] >> bit) & 1u)) t1 ^= 0x8000u;
+              uint16_t t2 = hmul_bits(static_cast<uint16_t>(cp >> 16), static_cast<uint16_t>(rp[t] >> 16));
+              if (!((q2w >> (sidx & 31)) & 1u)) t2 ^= 0x8000u;
+              ws[wave][i16][q] = hadd_bits(t1, t2);
+            }
+          }
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      const int wn = (num_sal - w0) < kMfSalWin ? (num_sal - w0) : kMfSalWin;
+#pragma unroll
+      for (int blk = 0; blk < kMfSalWin; blk += 32) {
+        if (blk < wn) {
+          uint32_t ap[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const f16x2 pd = u32_as_f16x2(cd[i]) * rd2[ct];
-            const f16x2 pn = u32_as_f16x2(cn[i]) * rn2[ct];
-            const f16x2 tn = fp4x2_to_f16x2(sn, i) * pn;
-            b[i] = f16x2_as_u32(__builtin_elementwise_fma(fp4x2_to_f16x2(sd, i), pd, tn));
+            const int q0 = blk + 8 * kg + 2 * i;
+            uint32_t lo = 0u, hi = 0u;
+            if (q0 < wn) {
+              const int c = sal_col[w0 + q0];
+              lo = xs[i16][(c & ~31) + mf_perm32(c & 31)];
+            }
+            if (q0 + 1 < wn) {
+              const int c = sal_col[w0 + q0 + 1];
+              hi = xs[i16][(c & ~31) + mf_perm32(c & 31)];
+            }
+            ap[i] = lo | (hi << 16);
           }
-          const f16x8 bv = __builtin_bit_cast(f16x8, make_uint4(b[0], b[1], b[2], b[3]));
-          tot[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, tot[ct], 0, 0, 0);
+          const f16x8 av = __builtin_bit_cast(f16x8, make_uint4(ap[0], ap[1], ap[2], ap[3]));
+          const f16x8 bv = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&ws[wave][i16][blk + 8 * kg]));
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
         }
       }
-    }
-
-    // ---- salient columns of the wave's range: exact fp16 weights, lane = output column
-#pragma unroll
-    for (int j = 0; j < kMfPR; ++j) {
-      uint32_t m = cmw[j];
-      const int t = j / 2;
-      int sidx = q2p[j];
-      while (m != 0u) {
-        const int b = __builtin_ctz(m);
-        m &= m - 1u;
-        const int kl = (pr0 + j) * 32 + b - kc;
-        uint32_t q2w = q2w0;
-        if ((sidx >> 5) != q2row0) {
-          q2w = nv_lane ? static_cast<uint32_t>(q2_e[static_cast<int64_t>(sidx >> 5) * N + n_lane]) : 0u;
-        }
-        const uint32_t cp = col_sal[kl];
-        uint16_t t1 = hmul_bits(static_cast<uint16_t>(cp), static_cast<uint16_t>(rps[t]));
-        if (!((q1s[j] >> b) & 1u)) t1 ^= 0x8000u;
-        uint16_t t2 = hmul_bits(static_cast<uint16_t>(cp >> 16), static_cast<uint16_t>(rps[t] >> 16));
-        if (!((q2w >> (sidx & 31)) & 1u)) t2 ^= 0x8000u;
-        const float wf = h2f(hadd_bits(t1, t2));
-        const int xpos = (kl & ~31) + mf_perm32(kl & 31);
-#pragma unroll
-        for (int r = 0; r < kMfRows; ++r) {
-          if (r < rc) sal[r] = fmaf(h2f(xs[r][xpos]), wf, sal[r]);
-        }
-        ++sidx;
-      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
     }
   }
 
-  // tot[ct][v] = row 4*kg+v, column 16ct+i16.
-  __syncthreads();
+  // acc[v] = row 4*kg+v of column n.
+  const float scale = (nv && p.has_output_scale) ? h2f(p.output_scale[static_cast<int64_t>(e) * N + n]) : 1.0f;
+  const float bias = (nv && p.has_bias) ? h2f(p.bias[static_cast<int64_t>(e) * N + n]) : 0.0f;
 #pragma unroll
-  for (int r = 0; r < kMfRows; ++r) red[wave][r][lane] = sal[r];
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-#pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-#pragma unroll
-    for (int v = 0; v < 4; ++v) red[wave][4 * kg + v][16 * ct + i16] += tot[ct][v];
-  }
-  __syncthreads();
-  for (int idx = tid; idx < rc * kTileOut; idx += kMfThreads) {
-    const int r = idx / kTileOut;
-    const int c = idx % kTileOut;
-    const int n = n0 + c;
-    if (n >= N) continue;
-    float v = red[0][r][c] + red[1][r][c] + red[2][r][c] + red[3][r][c];
-    if (p.has_output_scale) v = v * h2f(p.output_scale[static_cast<int64_t>(e) * N + n]);
-    if (p.has_bias) v = v + h2f(p.bias[static_cast<int64_t>(e) * N + n]);
-    out[static_cast<int64_t>(row0 + r) * N + n] = f2h_bits(v);
+  for (int v = 0; v < 4; ++v) {
+    const int r = 4 * kg + v;
+    float x = acc[v];
+    if (p.has_output_scale) x = x * scale;
+    if (p.has_bias) x = x + bias;
+    if (nv && r < rc) out[static_cast<int64_t>(row0 + r) * N + n] = f2h_bits(x);
   }
 }
 

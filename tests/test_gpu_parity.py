@@ -316,7 +316,7 @@ def test_dual_and_predecoded_match(tris, oracle_mod, cuda):
     deca = torch.empty((ids.size, nblk, 128), dtype=torch.int32, device=cuda)
     deca = ext.compact3_tris_precomputed_grouped_block_gr_predecode(
         deca, t_i32(ids, cuda), da["q_gmap_gr_words"], da["q_gmap_gr_offsets"], da["q_gmap_gr_meta"], k // 32, 320)
-    for uniform in (True, False):  # MFMA kernel (factored scales) / exact per-weight kernel
+    for uniform in (True, False):  # MFMA kernel / per-weight VALU kernel
         pre = ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
             ha, *args, deca, da["qweight1"], da["qweight2_sparse"], da["qweight2_sparse_prefix"], da["c_map"],
             da["g_idx"], da["col_pack3"], da["row_pack3"], uniform)
@@ -332,6 +332,37 @@ def test_dual_and_predecoded_match(tris, oracle_mod, cuda):
                                 "col_pack3", "row_pack3")], True)
     assert_close(pa2.cpu().numpy(), oracle_grouped(oracle_mod, pa, ha.cpu().numpy(), ids, offs, True), "dual pre a")
     assert_close(pb2.cpu().numpy(), oracle_grouped(oracle_mod, pb, hb.cpu().numpy(), ids, offs, True), "dual pre b")
+
+
+@pytest.mark.parametrize("rank,n,salient", [(256, 128, None), (512, 192, [0, 40]), (128, 64, [7, 0])])
+def test_predecoded_mfma_one_hot_is_bit_exact(tris, oracle_mod, cuda, rank, n, salient):
+    """With one-hot activation rows the MFMA grouped GEMM returns single dequantised weights, which
+    must equal the reference's fp16 weights bit for bit: every lane group, packed row, split bit,
+    sign and salient column of the operand construction is checked."""
+    note(f"mfma one-hot rank={rank} n={n}")
+    ext = tris["ext"]
+    E = 2
+    pay = make_projection(tris, 70 + rank, E, n, rank, salient_counts=salient)
+    d = tris["qlinear"].payload_to_device(pay, cuda)
+    ids, offs = _segments([rank, rank], E)   # each expert gets `rank` rows: row r of a segment is e_r
+    rows = int(offs[-1])
+    h = np.zeros((rows, rank), dtype=np.float16)
+    for s in range(E):
+        for r in range(rank):
+            h[offs[s] + r, r] = 1.0
+    hd = torch.from_numpy(h).to(cuda)
+    prob = np.concatenate([[0], np.cumsum((np.diff(offs) + 3) // 4)]).astype(np.int32)
+    nblk = tris["synthetic"].packing.num_gr_blocks(rank, n)
+    dec = torch.empty((ids.size, nblk, 128), dtype=torch.int32, device=cuda)
+    ext.compact3_tris_precomputed_grouped_block_gr_predecode(
+        dec, t_i32(ids, cuda), d["q_gmap_gr_words"], d["q_gmap_gr_offsets"], d["q_gmap_gr_meta"], rank // 32, n)
+    got = ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
+        hd, t_i32(ids, cuda), t_i32(offs, cuda), t_i32(prob, cuda), int(prob[-1]), dec, d["qweight1"],
+        d["qweight2_sparse"], d["qweight2_sparse_prefix"], d["c_map"], d["g_idx"], d["col_pack3"], d["row_pack3"],
+        True).cpu().numpy()
+    for s, e in enumerate(ids):
+        w = oracle_mod.dequant_grouped_expert(pay, int(e), True)   # [n, rank] fp16
+        np.testing.assert_array_equal(got[offs[s]:offs[s + 1]].view(np.uint16), w.T.astype(np.float16).view(np.uint16))
 
 
 def test_run_grouped_structured_api(tris, oracle_mod, cuda):
