@@ -168,6 +168,21 @@ int tris_grouped_dual_forward_block_gr_predecoded(const uint16_t* hidden_a, cons
                                                   uint16_t* output_b, void* stream);
 
 /*
+ * Gate/up grouped GEMM over predecoded bitmaps with the SwiGLU product fused
+ * (no reference counterpart: fuses tris_grouped_dual_forward_block_gr_predecoded,
+ * TriSMoE_cuda.cpp:922-974, with act_fn(gate_out) * up_out of
+ * modeling_mixtral.py:496 so the gate and up outputs never reach HBM).
+ * output fp16 [batch, N] = fp16(fp16(silu(g)) * u) with g, u the fp16 outputs
+ * the dual entry point would return.  Requires uniform 64-column groups,
+ * rank % 64 == 0 and 16-byte aligned hidden rows (else TRIS_ERR_INVALID).
+ */
+int tris_grouped_swiglu_forward_block_gr_predecoded(
+    const uint16_t* hidden_gate, const uint16_t* hidden_up, int32_t batch, const int32_t* expert_ids,
+    const int32_t* segment_offsets, const int32_t* problem_offsets, int32_t num_segments, int64_t total_problem_tiles,
+    const int32_t* decoded_gate, const int32_t* decoded_up, const tris_compact3_payload* payload_gate,
+    const tris_compact3_payload* payload_up, uint16_t* output, void* stream);
+
+/*
  * Dequantise the listed experts to dense fp16 weights [num, N, rank]
  * (verification kernel; the product GEMMs never write weights).  Replaces the
  * reference's CPU dequant QuantLinear._dequantize_compact3_matrix
@@ -196,15 +211,27 @@ int tris_gr_decode_dense(const int32_t* q_gmap_gr_words, const int32_t* q_gmap_g
  * reference's index_select (modeling_mixtral.py:467).  x, sv and in_scale must
  * be 16-byte aligned.  workspace: device scratch of
  * tris_backbone_workspace_bytes(tokens, in, rank) bytes (fp32 split-K partial
- * sums; no initial contents needed).  Calls sharing a workspace on different
- * streams must not overlap.
+ * sums; no initial contents needed; may be NULL when that size is 0).  Calls
+ * sharing a workspace on different streams must not overlap.  Deterministic:
+ * the same inputs give the same bits.
  */
 int tris_backbone_linear(const uint16_t* x, int32_t tokens, int32_t in_features, const int64_t* row_index,
                          const uint16_t* sv, int32_t rank, const uint16_t* in_scale, uint16_t* out,
                          void* workspace, int64_t workspace_bytes, void* stream);
 
-/* Workspace size for tris_backbone_linear (no reference counterpart: cuBLAS
- * owns its workspace). */
+/* Two backbone projections of the same gathered rows in one launch (no
+ * reference counterpart: batches the gate and up compute_shared_hidden calls
+ * of a grouped SwiGLU layer, modeling_mixtral.py:467-476, without in_scale).
+ * out_a = x[row_index] . sv_a^T, out_b = x[row_index] . sv_b^T, as two calls
+ * of tris_backbone_linear would give.  workspace: see
+ * tris_backbone_pair_workspace_bytes. */
+int tris_backbone_linear_pair(const uint16_t* x, int32_t tokens, int32_t in_features, const int64_t* row_index,
+                              const uint16_t* sv_a, const uint16_t* sv_b, int32_t rank, uint16_t* out_a,
+                              uint16_t* out_b, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace sizes for tris_backbone_linear / _pair (no reference counterpart:
+ * cuBLAS owns its workspace). */
+int64_t tris_backbone_pair_workspace_bytes(int32_t tokens, int32_t in_features, int32_t rank);
 int64_t tris_backbone_workspace_bytes(int32_t tokens, int32_t in_features, int32_t rank);
 
 /*

@@ -445,7 +445,7 @@ int launch_grouped(const uint16_t* hidden_a, const uint16_t* hidden_b, int batch
 int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int batch, const int32_t* expert_ids,
                         const int32_t* segment_offsets, int num_segments, const int32_t* decoded_a,
                         const int32_t* decoded_b, const tris_compact3_payload* pa, const tris_compact3_payload* pb,
-                        uint16_t* out_a, uint16_t* out_b, void* stream, const char* who);
+                        uint16_t* out_a, uint16_t* out_b, bool swiglu, void* stream, const char* who);
 bool grouped_mfma_supported(const tris_compact3_payload* p, const uint16_t* hidden);
 
 }  // namespace tris
@@ -492,7 +492,7 @@ extern "C" int tris_grouped_forward_block_gr_predecoded(const uint16_t* hidden, 
   if (grouped_mfma_supported(&p, hidden)) {
     if (total_problem_tiles <= 0) return TRIS_OK;
     return launch_grouped_mfma(hidden, nullptr, batch, expert_ids, segment_offsets, num_segments, decoded, nullptr,
-                               &p, nullptr, output, nullptr, stream, "tris_grouped_forward_block_gr_predecoded");
+                               &p, nullptr, output, nullptr, false, stream, "tris_grouped_forward_block_gr_predecoded");
   }
   return launch_grouped(hidden, nullptr, batch, expert_ids, segment_offsets, num_segments, total_problem_tiles,
                         decoded, nullptr, &p, nullptr, output, nullptr, true, stream,
@@ -517,12 +517,35 @@ extern "C" int tris_grouped_dual_forward_block_gr_predecoded(
     if (total_problem_tiles <= 0) return TRIS_OK;
     TRIS_REQUIRE(pa.num_experts == pb.num_experts, "tris_grouped_dual_forward_block_gr_predecoded: expert count mismatch");
     return launch_grouped_mfma(hidden_a, hidden_b, batch, expert_ids, segment_offsets, num_segments, decoded_a,
-                               decoded_b, &pa, &pb, output_a, output_b, stream,
+                               decoded_b, &pa, &pb, output_a, output_b, false, stream,
                                "tris_grouped_dual_forward_block_gr_predecoded");
   }
   return launch_grouped(hidden_a, hidden_b, batch, expert_ids, segment_offsets, num_segments, total_problem_tiles,
                         decoded_a, decoded_b, &pa, &pb, output_a, output_b, true, stream,
                         "tris_grouped_dual_forward_block_gr_predecoded");
+}
+
+extern "C" int tris_grouped_swiglu_forward_block_gr_predecoded(
+    const uint16_t* hidden_gate, const uint16_t* hidden_up, int32_t batch, const int32_t* expert_ids,
+    const int32_t* segment_offsets, const int32_t* problem_offsets, int32_t num_segments, int64_t total_problem_tiles,
+    const int32_t* decoded_gate, const int32_t* decoded_up, const tris_compact3_payload* payload_gate,
+    const tris_compact3_payload* payload_up, uint16_t* output, void* stream) {
+  (void)problem_offsets;
+  if (payload_gate == nullptr || payload_up == nullptr) {
+    set_error("tris_grouped_swiglu_forward_block_gr_predecoded: null payload");
+    return TRIS_ERR_INVALID;
+  }
+  tris_compact3_payload pg = *payload_gate;
+  tris_compact3_payload pu = *payload_up;
+  pg.has_output_scale = pu.has_output_scale = 0;
+  pg.has_bias = pu.has_bias = 0;
+  TRIS_REQUIRE(grouped_mfma_supported(&pg, hidden_gate) && grouped_mfma_supported(&pu, hidden_up),
+               "tris_grouped_swiglu_forward_block_gr_predecoded: needs uniform 64-column groups, rank %% 64 == 0 "
+               "and 16-byte aligned hidden rows");
+  if (total_problem_tiles <= 0) return TRIS_OK;
+  return launch_grouped_mfma(hidden_gate, hidden_up, batch, expert_ids, segment_offsets, num_segments, decoded_gate,
+                             decoded_up, &pg, &pu, output, nullptr, true, stream,
+                             "tris_grouped_swiglu_forward_block_gr_predecoded");
 }
 
 extern "C" int tris_compact3_dequant(const tris_compact3_payload* payload, const int32_t* expert_ids, int32_t num,

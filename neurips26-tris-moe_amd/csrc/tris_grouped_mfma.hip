@@ -119,39 +119,32 @@ __device__ inline bool mf_map_row_tile(const int32_t* __restrict__ seg, int nseg
   return false;
 }
 
-template <int kNumProj>
-__global__ __launch_bounds__(kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t xs[kMfRows][kMfXStride];  // activations, staged order
-  __shared__ __attribute__((aligned(16))) uint16_t cds[kMfChunk];            // C_d, staged order
-  __shared__ __attribute__((aligned(16))) uint16_t cns[kMfChunk];            // C_nd, staged order
-  __shared__ uint32_t col_sal[kMfChunk];                                     // C0 | C1 << 16, natural order
-  __shared__ uint16_t sal_col[kMfChunk];        // chunk column of the chunk's q-th salient column
-  __shared__ __attribute__((aligned(16))) uint16_t ws[kMfWaves][16][kMfSalStride];  // salient weights
+// LDS of one workgroup, shared by the projections it computes one after the other.
+struct MfmaLds {
+  uint16_t (*xs)[kMfXStride];          // activations, staged order
+  uint16_t* cds;                        // C_d, staged order
+  uint16_t* cns;                        // C_nd, staged order
+  uint32_t* col_sal;                    // C0 | C1 << 16, natural order
+  uint16_t* sal_col;                    // chunk column of the chunk's q-th salient column
+  uint16_t (*ws)[16][kMfSalStride];    // per-wave salient weights
+};
 
-  const MfmaProj& pa = a.proj[kNumProj == 1 ? 0 : blockIdx.z];
+// One projection of one workgroup tile: rows [row0, row0 + rc) of segment s
+// (expert e) x output columns [n0, n0 + 64).  Returns the lane's accumulator:
+// rows 4*kg + v, column n0 + 16*wave + lane % 16.
+__device__ __forceinline__ f32x4 mfma_project(const MfmaProj& pa, int s, int row0, int rc, int e, int n0,
+                                              const MfmaLds& L) {
   const tris_compact3_payload& p = pa.p;
   const int N = p.outfeatures;
-  const int n0 = blockIdx.x * kTileOut;
-  if (n0 >= N) return;
-  int s = 0, row0 = 0, rc = 0;
-  if (!mf_map_row_tile(a.segment_offsets, a.num_segments, blockIdx.y, kMfRows, &s, &row0, &rc)) return;
-  s = __builtin_amdgcn_readfirstlane(s);  // the mapping is the same in every lane
-  row0 = __builtin_amdgcn_readfirstlane(row0);
-  rc = __builtin_amdgcn_readfirstlane(rc);
-
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
   const int lane = tid % kWave;
-  const int e = a.expert_ids[s];
-  uint16_t* out = pa.out;
-  if (e < 0 || e >= p.num_experts) {
-    for (int idx = tid; idx < rc * kTileOut; idx += kMfThreads) {
-      const int n = n0 + idx % kTileOut;
-      if (n < N) out[static_cast<int64_t>(row0 + idx / kTileOut) * N + n] = 0;
-    }
-    return;
-  }
-
+  uint16_t (*xs)[kMfXStride] = L.xs;
+  uint16_t* cds = L.cds;
+  uint16_t* cns = L.cns;
+  uint32_t* col_sal = L.col_sal;
+  uint16_t* sal_col = L.sal_col;
+  uint16_t (*ws)[16][kMfSalStride] = L.ws;
   const int rank = p.rank;
   const int packed_rows = ceil_div(rank, 32);
   const int nkb = ceil_div(packed_rows, kGrPackedRows);
@@ -349,16 +342,71 @@ __global__ __launch_bounds__(kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
     }
   }
 
-  // acc[v] = row 4*kg+v of column n.
+  return acc;
+}
+
+// kMode 0: one projection; 1: two projections, blockIdx.z picks one; 2: both
+// projections per workgroup (gate, up) and the output is fp16(silu(g) * u).
+template <int kMode>
+__global__ __launch_bounds__(kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t xs[kMfRows][kMfXStride];
+  __shared__ __attribute__((aligned(16))) uint16_t cds[kMfChunk];
+  __shared__ __attribute__((aligned(16))) uint16_t cns[kMfChunk];
+  __shared__ uint32_t col_sal[kMfChunk];
+  __shared__ uint16_t sal_col[kMfChunk];
+  __shared__ __attribute__((aligned(16))) uint16_t ws[kMfWaves][16][kMfSalStride];
+  const MfmaLds L{xs, cds, cns, col_sal, sal_col, ws};
+
+  const MfmaProj& pa = a.proj[kMode == 1 ? blockIdx.z : 0];
+  const tris_compact3_payload& p = pa.p;
+  const int N = p.outfeatures;
+  const int n0 = blockIdx.x * kTileOut;
+  if (n0 >= N) return;
+  int s = 0, row0 = 0, rc = 0;
+  if (!mf_map_row_tile(a.segment_offsets, a.num_segments, blockIdx.y, kMfRows, &s, &row0, &rc)) return;
+  s = __builtin_amdgcn_readfirstlane(s);  // the mapping is the same in every lane
+  row0 = __builtin_amdgcn_readfirstlane(row0);
+  rc = __builtin_amdgcn_readfirstlane(rc);
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int e = a.expert_ids[s];
+  uint16_t* out = pa.out;
+  if (e < 0 || e >= p.num_experts) {
+    for (int idx = tid; idx < rc * kTileOut; idx += kMfThreads) {
+      const int n = n0 + idx % kTileOut;
+      if (n < N) out[static_cast<int64_t>(row0 + idx / kTileOut) * N + n] = 0;
+    }
+    return;
+  }
+  const f32x4 acc = mfma_project(pa, s, row0, rc, e, n0, L);
+  f32x4 acc_up = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (kMode == 2) acc_up = mfma_project(a.proj[1], s, row0, rc, e, n0, L);
+
+  const int kg = lane / 16;
+  const int n = n0 + 16 * (tid / kWave) + lane % 16;
+  const bool nv = n < N;
   const float scale = (nv && p.has_output_scale) ? h2f(p.output_scale[static_cast<int64_t>(e) * N + n]) : 1.0f;
   const float bias = (nv && p.has_bias) ? h2f(p.bias[static_cast<int64_t>(e) * N + n]) : 0.0f;
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int r = 4 * kg + v;
-    float x = acc[v];
-    if (p.has_output_scale) x = x * scale;
-    if (p.has_bias) x = x + bias;
-    if (nv && r < rc) out[static_cast<int64_t>(row0 + r) * N + n] = f2h_bits(x);
+    if (!nv || r >= rc) continue;
+    uint16_t y;
+    if (kMode == 2) {
+      // g and u rounded to fp16 as the two outputs would be, SiLU in fp32 rounded to fp16, then the
+      // fp16 product (modeling_mixtral.py:496)
+      const float g = h2f(f2h_bits(acc[v]));
+      const float u = h2f(f2h_bits(acc_up[v]));
+      const float sg = h2f(f2h_bits(g / (1.0f + expf(-g))));
+      y = f2h_bits(sg * u);
+    } else {
+      float x = acc[v];
+      if (p.has_output_scale) x = x * scale;
+      if (p.has_bias) x = x + bias;
+      y = f2h_bits(x);
+    }
+    out[static_cast<int64_t>(row0 + r) * N + n] = y;
   }
 }
 
@@ -367,7 +415,7 @@ int check_payload(const tris_compact3_payload* p, bool need_gr, const char* who)
 int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int batch, const int32_t* expert_ids,
                         const int32_t* segment_offsets, int num_segments, const int32_t* decoded_a,
                         const int32_t* decoded_b, const tris_compact3_payload* pa, const tris_compact3_payload* pb,
-                        uint16_t* out_a, uint16_t* out_b, void* stream, const char* who) {
+                        uint16_t* out_a, uint16_t* out_b, bool swiglu, void* stream, const char* who) {
   TRIS_REQUIRE(batch >= 0 && num_segments >= 0, "%s: negative batch or segment count", who);
   int rc = check_payload(pa, false, who);
   if (rc) return rc;
@@ -375,15 +423,18 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
     rc = check_payload(pb, false, who);
     if (rc) return rc;
   }
+  TRIS_REQUIRE(!swiglu || pb != nullptr, "%s: the fused SwiGLU needs two projections", who);
   if (batch == 0 || num_segments == 0) return TRIS_OK;
   TRIS_REQUIRE(hidden_a && out_a && expert_ids && segment_offsets && decoded_a, "%s: null pointer", who);
-  TRIS_REQUIRE(!pb || (hidden_b && out_b && decoded_b), "%s: null pointer (second projection)", who);
+  TRIS_REQUIRE(!pb || (hidden_b && decoded_b && (swiglu || out_b)), "%s: null pointer (second projection)", who);
   int max_n = 0;
   for (int i = 0; i < (pb ? 2 : 1); ++i) {
     const tris_compact3_payload* p = i ? pb : pa;
     TRIS_REQUIRE(p->num_experts > 0 && p->rank > 0 && p->outfeatures > 0, "%s: empty payload", who);
     max_n = p->outfeatures > max_n ? p->outfeatures : max_n;
   }
+  TRIS_REQUIRE(!swiglu || (pa->outfeatures == pb->outfeatures && pa->num_experts == pb->num_experts),
+               "%s: gate and up projections differ in shape", who);
   const int64_t tiles = static_cast<int64_t>(batch) / kMfRows + num_segments;
   TRIS_REQUIRE(tiles <= 2147483647LL, "%s: too many tiles", who);
   MfmaArgs args{};
@@ -392,12 +443,16 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
   args.expert_ids = expert_ids;
   args.segment_offsets = segment_offsets;
   args.num_segments = num_segments;
-  dim3 grid(ceil_div(max_n, kTileOut), static_cast<unsigned>(tiles), pb ? 2 : 1);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (pb) {
+  if (swiglu) {
+    const dim3 grid(ceil_div(max_n, kTileOut), static_cast<unsigned>(tiles), 1);
     hipLaunchKernelGGL((grouped_mfma_kernel<2>), grid, dim3(kMfThreads), 0, s, args);
-  } else {
+  } else if (pb) {
+    const dim3 grid(ceil_div(max_n, kTileOut), static_cast<unsigned>(tiles), 2);
     hipLaunchKernelGGL((grouped_mfma_kernel<1>), grid, dim3(kMfThreads), 0, s, args);
+  } else {
+    const dim3 grid(ceil_div(max_n, kTileOut), static_cast<unsigned>(tiles), 1);
+    hipLaunchKernelGGL((grouped_mfma_kernel<0>), grid, dim3(kMfThreads), 0, s, args);
   }
   return check_launch(who);
 }

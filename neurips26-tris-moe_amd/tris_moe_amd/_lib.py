@@ -64,9 +64,13 @@ SIGNATURES = {
     "tris_grouped_forward_block_gr_predecoded": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I32, _I64, _P, _PAY, _P, _P]),
     "tris_grouped_dual_forward_block_gr_predecoded": (
         ctypes.c_int, [_P, _P, _I32, _P, _P, _P, _I32, _I64, _P, _P, _PAY, _PAY, _P, _P, _P]),
+    "tris_grouped_swiglu_forward_block_gr_predecoded": (
+        ctypes.c_int, [_P, _P, _I32, _P, _P, _P, _I32, _I64, _P, _P, _PAY, _PAY, _P, _P]),
     "tris_compact3_dequant": (ctypes.c_int, [_PAY, _P, _I32, _P, _P]),
     "tris_gr_decode_dense": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _P, _I32, _I32, _I32, _P, _P]),
     "tris_backbone_linear": (ctypes.c_int, [_P, _I32, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P]),
+    "tris_backbone_linear_pair": (ctypes.c_int, [_P, _I32, _I32, _P, _P, _P, _I32, _P, _P, _P, _I64, _P]),
+    "tris_backbone_pair_workspace_bytes": (_I64, [_I32, _I32, _I32]),
     "tris_backbone_workspace_bytes": (_I64, [_I32, _I32, _I32]),
     "tris_moe_combine": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _P, _P]),
 }

@@ -301,19 +301,31 @@ def compact3_tris_precomputed_grouped_forward_block_gr_predecoded(hidden, expert
                                                                   problem_offsets, total_problem_tiles,
                                                                   decoded_q_gmap_words, qweight1, qweight2_sparse,
                                                                   qweight2_sparse_prefix, c_map, g_idx, col_pack3,
-                                                                  row_pack3, use_uniform_k64_groups=False):
-    """TriSMoE_cuda.cpp:855-889 (no output scale / bias, as the reference's NoScaleNoBias kernel)."""
+                                                                  row_pack3, use_uniform_k64_groups=False,
+                                                                  out=None):
+    """TriSMoE_cuda.cpp:855-889 (no output scale / bias, as the reference's NoScaleNoBias kernel).
+    ``out``: optional [rows, N] fp16 buffer; rows outside every segment are left as they are
+    (the default buffer is zero-filled, as the reference's)."""
     _check_route(hidden, expert_ids, segment_offsets, problem_offsets)
     total = _host_tiles(total_problem_tiles)
     pay = make_payload_struct(int(hidden.size(1)), qweight1, qweight2_sparse, qweight2_sparse_prefix, None, None,
                               None, c_map, g_idx, col_pack3, row_pack3, None, False, None, False,
                               use_uniform_k64_groups, hidden.device, need_gr=False)
     _check_predecoded(decoded_q_gmap_words, expert_ids, pay, hidden.device)
-    out = torch.zeros((hidden.size(0), pay.outfeatures), dtype=torch.float16, device=hidden.device)
+    out = _out_buffer(out, hidden.size(0), pay.outfeatures, hidden.device)
     _lib.check(_lib.load().tris_grouped_forward_block_gr_predecoded(
         _ptr(hidden), int(hidden.size(0)), _ptr(expert_ids), _ptr(segment_offsets), _ptr(problem_offsets),
         int(expert_ids.size(0)), total, _ptr(decoded_q_gmap_words), ctypes.byref(pay), _ptr(out), _stream(hidden)),
         "compact3_tris_precomputed_grouped_forward_block_gr_predecoded")
+    return out
+
+
+def _out_buffer(out, rows, cols, device):
+    if out is None:
+        return torch.zeros((rows, cols), dtype=torch.float16, device=device)
+    _check_cuda("out", out, torch.float16, 2, device)
+    if tuple(out.shape) != (int(rows), int(cols)):
+        raise RuntimeError(f"out must be [{int(rows)}, {int(cols)}]")
     return out
 
 
@@ -328,8 +340,8 @@ def compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
         hidden_a, hidden_b, expert_ids, segment_offsets, problem_offsets, total_problem_tiles,
         decoded_q_gmap_words_a, qweight1_a, qweight2_sparse_a, qweight2_sparse_prefix_a, c_map_a, g_idx_a,
         col_pack3_a, row_pack3_a, decoded_q_gmap_words_b, qweight1_b, qweight2_sparse_b, qweight2_sparse_prefix_b,
-        c_map_b, g_idx_b, col_pack3_b, row_pack3_b, use_uniform_k64_groups=False):
-    """TriSMoE_cuda.cpp:922-974."""
+        c_map_b, g_idx_b, col_pack3_b, row_pack3_b, use_uniform_k64_groups=False, out_a=None, out_b=None):
+    """TriSMoE_cuda.cpp:922-974.  ``out_a`` / ``out_b`` as ``out`` of the single-projection call."""
     _check_route(hidden_a, expert_ids, segment_offsets, problem_offsets)
     _check_cuda("hidden_b", hidden_b, torch.float16, 2, hidden_a.device)
     total = _host_tiles(total_problem_tiles)
@@ -341,14 +353,43 @@ def compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
                              use_uniform_k64_groups, hidden_a.device, need_gr=False, who="grouped payload b")
     _check_predecoded(decoded_q_gmap_words_a, expert_ids, pa, hidden_a.device)
     _check_predecoded(decoded_q_gmap_words_b, expert_ids, pb, hidden_a.device)
-    out_a = torch.zeros((hidden_a.size(0), pa.outfeatures), dtype=torch.float16, device=hidden_a.device)
-    out_b = torch.zeros((hidden_b.size(0), pb.outfeatures), dtype=torch.float16, device=hidden_a.device)
+    out_a = _out_buffer(out_a, hidden_a.size(0), pa.outfeatures, hidden_a.device)
+    out_b = _out_buffer(out_b, hidden_b.size(0), pb.outfeatures, hidden_a.device)
     _lib.check(_lib.load().tris_grouped_dual_forward_block_gr_predecoded(
         _ptr(hidden_a), _ptr(hidden_b), int(hidden_a.size(0)), _ptr(expert_ids), _ptr(segment_offsets),
         _ptr(problem_offsets), int(expert_ids.size(0)), total, _ptr(decoded_q_gmap_words_a),
         _ptr(decoded_q_gmap_words_b), ctypes.byref(pa), ctypes.byref(pb), _ptr(out_a), _ptr(out_b),
         _stream(hidden_a)), "compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded")
     return [out_a, out_b]
+
+
+def compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded(
+        hidden_gate, hidden_up, expert_ids, segment_offsets, problem_offsets, total_problem_tiles,
+        decoded_q_gmap_words_gate, qweight1_gate, qweight2_sparse_gate, qweight2_sparse_prefix_gate, c_map_gate,
+        g_idx_gate, col_pack3_gate, row_pack3_gate, decoded_q_gmap_words_up, qweight1_up, qweight2_sparse_up,
+        qweight2_sparse_prefix_up, c_map_up, g_idx_up, col_pack3_up, row_pack3_up, out=None):
+    """fp16(silu(gate) * up) of the dual predecoded GEMM (TriSMoE_cuda.cpp:922-974) fused with the
+    SwiGLU product of modeling_mixtral.py:496 (an extension with no reference entry point; needs
+    uniform 64-column groups)."""
+    _check_route(hidden_gate, expert_ids, segment_offsets, problem_offsets)
+    _check_cuda("hidden_up", hidden_up, torch.float16, 2, hidden_gate.device)
+    total = _host_tiles(total_problem_tiles)
+    pg = make_payload_struct(int(hidden_gate.size(1)), qweight1_gate, qweight2_sparse_gate,
+                             qweight2_sparse_prefix_gate, None, None, None, c_map_gate, g_idx_gate, col_pack3_gate,
+                             row_pack3_gate, None, False, None, False, True, hidden_gate.device, need_gr=False,
+                             who="gate payload")
+    pu = make_payload_struct(int(hidden_up.size(1)), qweight1_up, qweight2_sparse_up, qweight2_sparse_prefix_up,
+                             None, None, None, c_map_up, g_idx_up, col_pack3_up, row_pack3_up, None, False, None,
+                             False, True, hidden_gate.device, need_gr=False, who="up payload")
+    _check_predecoded(decoded_q_gmap_words_gate, expert_ids, pg, hidden_gate.device)
+    _check_predecoded(decoded_q_gmap_words_up, expert_ids, pu, hidden_gate.device)
+    out = _out_buffer(out, hidden_gate.size(0), pg.outfeatures, hidden_gate.device)
+    _lib.check(_lib.load().tris_grouped_swiglu_forward_block_gr_predecoded(
+        _ptr(hidden_gate), _ptr(hidden_up), int(hidden_gate.size(0)), _ptr(expert_ids), _ptr(segment_offsets),
+        _ptr(problem_offsets), int(expert_ids.size(0)), total, _ptr(decoded_q_gmap_words_gate),
+        _ptr(decoded_q_gmap_words_up), ctypes.byref(pg), ctypes.byref(pu), _ptr(out), _stream(hidden_gate)),
+        "compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded")
+    return out
 
 
 def _segments_total(segment_offsets) -> int:
@@ -430,11 +471,12 @@ _WORKSPACES: dict = {}
 
 
 def backbone_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Zero-filled per-device workspace for the backbone kernel (kept zeroed by the kernel)."""
+    """Per-device scratch for the backbone's split-K partial sums (no initial contents needed;
+    calls on one device share it, so they must not overlap on different streams)."""
     key = (device.type, device.index)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
 
@@ -454,11 +496,32 @@ def backbone_linear(x: torch.Tensor, sv: torch.Tensor, in_scale: torch.Tensor | 
     rank, in_f = int(sv.size(0)), int(sv.size(1))
     out = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
     lib = _lib.load()
-    need = int(lib.tris_backbone_workspace_bytes(tokens, in_f, rank))
-    ws = backbone_workspace(x.device, need)
+    ws = backbone_workspace(x.device, int(lib.tris_backbone_workspace_bytes(tokens, in_f, rank)))
     _lib.check(lib.tris_backbone_linear(_ptr(x), tokens, in_f, _ptr(row_index), _ptr(sv), rank, _ptr(in_scale),
                                         _ptr(out), _ptr(ws), int(ws.numel()), _stream(x)), "tris_backbone_linear")
     return out
+
+
+def backbone_linear_pair(x: torch.Tensor, sv_a: torch.Tensor, sv_b: torch.Tensor,
+                         row_index: torch.Tensor | None = None):
+    """(x[row_index] @ sv_a^T, x[row_index] @ sv_b^T) in one launch: the gate and up backbones."""
+    _check_cuda("x", x, torch.float16, 2)
+    _check_cuda("shared_sv_a", sv_a, torch.float16, 2, x.device)
+    _check_cuda("shared_sv_b", sv_b, torch.float16, 2, x.device)
+    if sv_a.shape != sv_b.shape or sv_a.size(1) != x.size(1):
+        raise RuntimeError("backbone pair shape mismatch")
+    tokens = int(row_index.numel()) if row_index is not None else int(x.size(0))
+    if row_index is not None:
+        _check_cuda("row_index", row_index, torch.int64, 1, x.device)
+    rank, in_f = int(sv_a.size(0)), int(sv_a.size(1))
+    out_a = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
+    out_b = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
+    lib = _lib.load()
+    ws = backbone_workspace(x.device, int(lib.tris_backbone_pair_workspace_bytes(tokens, in_f, rank)))
+    _lib.check(lib.tris_backbone_linear_pair(_ptr(x), tokens, in_f, _ptr(row_index), _ptr(sv_a), _ptr(sv_b), rank,
+                                             _ptr(out_a), _ptr(out_b), _ptr(ws), int(ws.numel()), _stream(x)),
+               "tris_backbone_linear_pair")
+    return out_a, out_b
 
 
 def moe_combine(expert_out: torch.Tensor, inverse_perm: torch.Tensor, weights: torch.Tensor,

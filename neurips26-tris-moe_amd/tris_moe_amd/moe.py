@@ -59,8 +59,6 @@ def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, select
     prob = route["problem_offsets"]
     # Launch bound only: every padded segment past the active ones is empty.
     tile_bound = R // GROUPED_SEGMENT_M_TILE + min(num_experts, R) + 1
-    hid_g = ext.backbone_linear(x16, backbones["gate"], row_index=gti)
-    hid_u = ext.backbone_linear(x16, backbones["up"], row_index=gti)
     pg, pu, pd = payloads["gate"], payloads["up"], payloads["down"]
     uniform = bool(pg.get("_compact3_k64_groups_uniform", False) and pu.get("_compact3_k64_groups_uniform", False))
     predecodable = uniform and bool(pd.get("_compact3_k64_groups_uniform", False)) and not any(
@@ -68,8 +66,10 @@ def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, select
     if expert_path == "predecoded" and not predecodable:
         raise RuntimeError("the predecoded expert path needs uniform 64-column groups and no output scale or bias")
     if predecodable and expert_path != "fused":
-        return _predecoded_moe_forward(x16, routing_weights, route, hid_g, hid_u, payloads, backbones, num_experts,
-                                       R, output_dtype, shared_expert)
+        return _predecoded_moe_forward(x16, routing_weights, route, payloads, backbones, num_experts, R,
+                                       output_dtype, shared_expert)
+    hid_g = ext.backbone_linear(x16, backbones["gate"], row_index=gti)
+    hid_u = ext.backbone_linear(x16, backbones["up"], row_index=gti)
     empty = x16.new_empty((0, 0))
     g_out, u_out = ext.compact3_tris_precomputed_grouped_dual_forward_block_gr(
         hid_g, hid_u, expert_ids, seg, prob, tile_bound,
@@ -100,33 +100,63 @@ def _combine(x16, d_out, route, routing_weights, output_dtype, shared_expert):
     return out if output_dtype == torch.bfloat16 else out.to(output_dtype)
 
 
-def _predecoded_moe_forward(x16, routing_weights, route, hid_g, hid_u, payloads, backbones, num_experts, R,
-                            output_dtype, shared_expert):
+def _predecode_buffer(p, slots, device):
+    packed_rows, n = int(p["qweight1"].size(1)), int(p["qweight1"].size(2))
+    nblk = ((packed_rows + 1) // 2) * ((n + 63) // 64)
+    return torch.empty((slots, nblk, 128), dtype=torch.int32, device=device)
+
+
+def _predecode(p, expert_ids, buf):
+    packed_rows, n = int(p["qweight1"].size(1)), int(p["qweight1"].size(2))
+    return ext.compact3_tris_precomputed_grouped_block_gr_predecode(
+        buf, expert_ids, p["q_gmap_gr_words"], p["q_gmap_gr_offsets"], p["q_gmap_gr_meta"], packed_rows, n)
+
+
+_SIDE_STREAMS: dict = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """A second stream per device (default priority) for work that overlaps the main chain."""
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    if key not in _SIDE_STREAMS:
+        _SIDE_STREAMS[key] = torch.cuda.Stream(device=device)
+    return _SIDE_STREAMS[key]
+
+
+def _predecoded_moe_forward(x16, routing_weights, route, payloads, backbones, num_experts, R, output_dtype,
+                            shared_expert):
     """Uniform-group payloads without output scale or bias: GR-decode every routed expert's split
     bitmaps once per projection (TriSMoE_cuda.cpp:836-853), then run the predecoded grouped GEMMs
     (TriSMoE_cuda.cpp:855-889, 922-974).  Active experts come first in the padded route, so
-    min(num_experts, R) segments cover every routed row and the later segments are empty."""
+    min(num_experts, R) segments cover every routed row and the later segments are empty.  The
+    decodes depend only on the route, so they run on a side stream while the gate/up backbones
+    run on the caller's stream."""
     slots = min(num_experts, R)
     eid = route["expert_ids"][:slots]
     seg = route["segment_offsets"][: slots + 1]
     prob = route["problem_offsets"][: slots + 1]
     tile_bound = R // GROUPED_SEGMENT_M_TILE + slots + 1
     pg, pu, pd = payloads["gate"], payloads["up"], payloads["down"]
-    decoded = {}
-    for name, p in (("gate", pg), ("up", pu), ("down", pd)):
-        packed_rows, n = int(p["qweight1"].size(1)), int(p["qweight1"].size(2))
-        nblk = ((packed_rows + 1) // 2) * ((n + 63) // 64)
-        buf = torch.empty((slots, nblk, 128), dtype=torch.int32, device=x16.device)
-        decoded[name] = ext.compact3_tris_precomputed_grouped_block_gr_predecode(
-            buf, eid, p["q_gmap_gr_words"], p["q_gmap_gr_offsets"], p["q_gmap_gr_meta"], packed_rows, n)
+    dev = x16.device
+    bufs = {name: _predecode_buffer(p, slots, dev) for name, p in (("gate", pg), ("up", pu), ("down", pd))}
+    main = torch.cuda.current_stream(dev)
+    side = _side_stream(dev)
+    side.wait_stream(main)
+    with torch.cuda.stream(side):
+        decoded = {name: _predecode(p, eid, bufs[name]) for name, p in (("gate", pg), ("up", pu), ("down", pd))}
+    hid_g, hid_u = ext.backbone_linear_pair(x16, backbones["gate"], backbones["up"],
+                                            row_index=route["grouped_token_indices"])
+    main.wait_stream(side)
     names = ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx", "col_pack3", "row_pack3")
-    g_out, u_out = ext.compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
+    # every routed row lies in a segment, so the outputs need no zero fill
+    mlp = torch.empty((R, int(pg["qweight1"].size(2))), dtype=torch.float16, device=dev)
+    ext.compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded(
         hid_g, hid_u, eid, seg, prob, tile_bound, decoded["gate"], *[pg[k] for k in names], decoded["up"],
-        *[pu[k] for k in names], True)
-    mlp = F.silu(g_out) * u_out
+        *[pu[k] for k in names], out=mlp)
     hid_d = ext.backbone_linear(mlp, backbones["down"])
-    d_out = ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
-        hid_d, eid, seg, prob, tile_bound, decoded["down"], *[pd[k] for k in names], True)
+    d_out = torch.empty((R, int(pd["qweight1"].size(2))), dtype=torch.float16, device=dev)
+    ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
+        hid_d, eid, seg, prob, tile_bound, decoded["down"], *[pd[k] for k in names], True, out=d_out)
     return _combine(x16, d_out, route, routing_weights, output_dtype, shared_expert)
 
 

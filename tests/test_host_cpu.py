@@ -69,9 +69,14 @@ def test_c_abi_argument_errors_without_gpu(tris):
     assert rc == -1 and b"m_tile" in lib.tris_last_error()
     rc = lib.tris_grouped_forward_block_gr(None, 4, None, None, None, 1, 1, None, None, None)
     assert rc == -1 and b"null payload" in lib.tris_last_error()
-    assert lib.tris_backbone_workspace_bytes(1, 4096, 512) > 0
+    assert lib.tris_backbone_workspace_bytes(1, 4096, 512) > 0    # split-K partial sums at decode
+    assert lib.tris_backbone_pair_workspace_bytes(1, 4096, 512) > 0
+    assert lib.tris_backbone_workspace_bytes(4096, 64, 512) == 0  # one slice: no scratch
     rc = lib.tris_backbone_linear(None, 2, 4096, None, None, 512, None, ctypes.c_void_p(16), None, 0, None)
-    assert rc == -1
+    assert rc == -1 and b"null input" in lib.tris_last_error()
+    rc = lib.tris_backbone_linear_pair(None, 2, 4096, None, ctypes.c_void_p(16), None, 512, ctypes.c_void_p(16),
+                                       ctypes.c_void_p(16), None, 0, None)
+    assert rc == -1 and b"null sv_b" in lib.tris_last_error()
 
 
 def test_ext_rejects_cpu_tensors(tris):
