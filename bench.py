@@ -4,16 +4,17 @@
 Workload: one Mixtral-8x7B-shaped MoE layer at
 decode (hidden 4096, 8 experts, intermediate 14336, top-2, rank-512 fp16
 backbones, binarised compact3 experts with a block-GR split bitmap at
-p = 0.15).  A step is one full layer forward over one decode batch: router
-softmax/top-k, device route, gate/up backbones, GR predecode of the routed
-experts' split bitmaps (gate, up, down), MFMA grouped gate/up GEMM, SiLU*up,
-down backbone, grouped down GEMM and the weighted scatter-add.  Synthetic seeded data; every step reads a different one of
+p = 0.15).  A step is one full layer forward over one decode batch from the
+router logits: fused softmax/top-k/route, gate/up backbone pair, GR predecode
+of the routed experts' split bitmaps (gate, up, down in one launch, on a side
+stream), MFMA grouped gate/up GEMM with the SwiGLU product, down backbone,
+grouped down GEMM and the weighted scatter-add.  Synthetic seeded data; every step reads a different one of
 --layers identical-content layer copies resident in HBM (so weights come from
 HBM, not the 256 MB last-level cache), with each step captured in a HIP graph.
 
 Prints ONE JSON line.  ``value`` is MoE-layer tokens/s; ``hbm_gbps`` the
 layer's algorithmic bytes / step time; ``roofline`` is for the dominant
-kernel, the MFMA gate/up grouped GEMM over predecoded bitmaps
+kernel, the MFMA gate/up grouped GEMM + SwiGLU over predecoded bitmaps
 (grouped_mfma_kernel<2>), timed live with HIP events on its own stream; ``cpu_baseline`` times the
 CPU oracle (GR decode + exact fp16 dequant + fp32 GEMM) on a bounded sample.
 """
@@ -91,8 +92,8 @@ def main():
 
         def step(i):
             pl, bb = copies[i % len(copies)]
-            w, sel = moe.route_topk(logits, SPEC.top_k, SPEC.renormalize)
-            return moe.grouped_moe_forward(x16, w, sel, pl, bb, SPEC.num_experts, torch.bfloat16)
+            return moe.grouped_moe_forward_from_logits(x16, logits, SPEC.top_k, SPEC.renormalize, pl, bb,
+                                                       SPEC.num_experts, torch.bfloat16)
 
         for i in range(max(warmup, 1)):
             step(i)
@@ -136,8 +137,8 @@ def main():
         sweep[f"T{tok}"]["active_experts"] = r["active_experts"]
         log(f"T={tok}: {r['ms_per_step'] * 1e3:.1f} us/step, {r['tokens_per_s']:.0f} tok/s, {r['hbm_gbps']:.0f} GB/s")
 
-    # ---- dominant kernel: the MFMA gate/up grouped GEMM over predecoded split bitmaps, one launch
-    # per layer copy, replayed from a graph on its own stream and timed there with HIP events
+    # ---- dominant kernel: the MFMA gate/up grouped GEMM + SwiGLU over predecoded split bitmaps, one
+    # launch per layer copy, replayed from a graph on its own stream and timed there with HIP events
     x16, logits = main_res["x16"], main_res["logits"]
     w, sel = moe.route_topk(logits, SPEC.top_k, SPEC.renormalize)
     route = ext.build_grouped_route_device(sel, SPEC.num_experts, 4)
@@ -161,11 +162,13 @@ def main():
                 SPEC.rank // 32, SPEC.intermediate))
         decoded.append(pair)
 
+    mlp = torch.empty((rows, SPEC.intermediate), dtype=torch.float16, device=dev)
+
     def dual(i):
         pl = copies[i][0]
-        return ext.compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
+        return ext.compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded(
             hid_g, hid_u, eid, seg, prob, tile_bound, decoded[i][0], *[pl["gate"][k] for k in names],
-            decoded[i][1], *[pl["up"][k] for k in names], True)
+            decoded[i][1], *[pl["up"][k] for k in names], out=mlp)
 
     kstream = torch.cuda.Stream(device=dev)
     kstream.wait_stream(torch.cuda.current_stream())
@@ -187,13 +190,13 @@ def main():
     kernel_s = ks.elapsed_time(ke) / 1e3 / (args.kernel_reps * len(copies))
     active = main_res["active"]
     dual_bytes = (synthetic.predecoded_nbytes(layer["gate"], active) + synthetic.predecoded_nbytes(layer["up"], active)
-                  + 2 * rows * SPEC.rank * 2 + 2 * rows * SPEC.intermediate * 2)
+                  + 2 * rows * SPEC.rank * 2 + rows * SPEC.intermediate * 2)
     achieved = dual_bytes / kernel_s / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                "kernel": "grouped_mfma_kernel<2> (predecoded gate/up grouped GEMM)",
+                "kernel": "grouped_mfma_kernel<2> (gate/up grouped GEMM + SwiGLU over predecoded bitmaps)",
                 "kernel_us": round(kernel_s * 1e6, 2), "bytes_per_launch": int(dual_bytes)}
-    log(f"dual GEMM: {kernel_s * 1e6:.1f} us/launch, {achieved:.0f} GB/s algorithmic")
+    log(f"gate/up SwiGLU GEMM: {kernel_s * 1e6:.1f} us/launch, {achieved:.0f} GB/s algorithmic")
 
     cpu = None
     if args.cpu_baseline:

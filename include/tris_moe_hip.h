@@ -111,6 +111,26 @@ int tris_build_grouped_route(const int64_t* selected_experts, int32_t num_tokens
                              int32_t* problem_offsets, int32_t* counts, int32_t* inverse_perm, void* stream);
 
 /*
+ * Router softmax + top-k fused with the grouped route for decode-sized batches
+ * (no reference counterpart: fuses F.softmax(router_logits, dtype=float),
+ * torch.topk, the optional renormalisation and the routing-weight cast of
+ * modeling_mixtral.py:548-555 with tris_build_grouped_route).  One launch.
+ * router_logits fp32 [num_tokens, num_experts]; top-k by probability with ties
+ * to the lower expert id; weights renormalised over the k picks when
+ * renormalize != 0.  routing_weights_f16 fp16 [num_tokens, top_k] (required),
+ * routing_weights_f32 / selected_experts optional (NULL to skip); the route
+ * outputs are those of tris_build_grouped_route (padded to num_experts
+ * segments).  Limits: num_tokens * top_k <= 2048, num_experts <= 1024,
+ * top_k <= 16 (else TRIS_ERR_INVALID: use tris_build_grouped_route).
+ */
+int tris_route_topk_grouped(const float* router_logits, int32_t num_tokens, int32_t num_experts, int32_t top_k,
+                            int32_t renormalize, int32_t m_tile, uint16_t* routing_weights_f16,
+                            float* routing_weights_f32, int64_t* selected_experts, int64_t* perm,
+                            int64_t* grouped_token_indices, int64_t* grouped_slots, int32_t* grouped_expert_ids,
+                            int32_t* expert_ids, int32_t* segment_offsets, int32_t* problem_offsets, int32_t* counts,
+                            int32_t* inverse_perm, void* stream);
+
+/*
  * Grouped expert GEMM with in-kernel block-GR decode: replaces
  * compact3_tris_precomputed_grouped_forward_block_gr (TriSMoE_cuda.cpp:1018-1063,
  * kernel.cu:9768-10213).  output[r, n] = fp16(sum_k hidden[r,k] * W_e[n,k]
@@ -143,6 +163,27 @@ int tris_grouped_block_gr_predecode(int32_t* decoded, const int32_t* expert_ids,
                                     const int32_t* q_gmap_gr_words, const int32_t* q_gmap_gr_offsets,
                                     const int32_t* q_gmap_gr_meta, int32_t num_experts, int32_t words_stride,
                                     int32_t packed_rows, int32_t outfeatures, void* stream);
+
+/* One projection's GR stream for tris_grouped_block_gr_predecode_multi. */
+typedef struct tris_gr_predecode_job {
+  int32_t* decoded;              /* int32 [num_active, nblk, 128] */
+  const int32_t* q_gmap_gr_words;
+  const int32_t* q_gmap_gr_offsets;
+  const int32_t* q_gmap_gr_meta;
+  int32_t num_experts;
+  int32_t words_stride;
+  int32_t packed_rows;
+  int32_t outfeatures;
+} tris_gr_predecode_job;
+
+#define TRIS_MAX_PREDECODE_JOBS 4
+
+/* Predecode of up to TRIS_MAX_PREDECODE_JOBS projections (e.g. gate, up and
+ * down of one layer) for the same routed experts in one launch (no reference
+ * counterpart: batches the per-projection predecode calls, TriSMoE_cuda.cpp:836-853).
+ * Each job's output is what tris_grouped_block_gr_predecode would write. */
+int tris_grouped_block_gr_predecode_multi(const tris_gr_predecode_job* jobs, int32_t num_jobs,
+                                          const int32_t* expert_ids, int32_t num_active, void* stream);
 
 /*
  * Grouped GEMM reading predecoded split bitmaps: replaces

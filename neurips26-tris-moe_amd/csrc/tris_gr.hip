@@ -9,84 +9,112 @@
 // shorten each lane's serial span (latency), fewer cut the shuffle steps, so S
 // is chosen from the block count.
 #include "tris_gr_span.h"
+#include "tris_moe_hip.h"
 
 namespace tris {
 
 constexpr int kSpanThreads = 256;
 
+// One projection's stream; jobs of one launch share the routed expert list.
+struct GrJob {
+  int32_t* out;
+  const int32_t* words;
+  const int32_t* offsets;
+  const int32_t* meta;
+  int num_experts;
+  int words_stride;
+  int nblk;
+  int num_out_blocks;
+  int dense_rows;  // 0: predecode layout [slot][block][128]; else dense [slot][packed_rows][N]
+  int dense_cols;
+};
+
+struct GrJobs {
+  GrJob job[TRIS_MAX_PREDECODE_JOBS];
+};
+
+// grid = (ceil(max nblk / blocks per workgroup), slots, jobs)
 template <int S>
-__global__ __launch_bounds__(kSpanThreads) void gr_decode_span_kernel(
-    int32_t* __restrict__ decoded, const int32_t* __restrict__ expert_ids, const int32_t* __restrict__ num_active_dev,
-    const int32_t* __restrict__ words, const int32_t* __restrict__ offsets, const int32_t* __restrict__ meta,
-    int words_stride, int nblk, int num_experts, int dense_rows, int dense_cols, int num_out_blocks) {
+__global__ __launch_bounds__(kSpanThreads) void gr_decode_span_kernel(GrJobs jobs, const int32_t* __restrict__ expert_ids) {
   constexpr int kBlocksPerWg = kSpanThreads / S;
   __shared__ GrTables tab;
   __shared__ uint32_t outb[kBlocksPerWg][kGrWords];
+  const GrJob& jb = jobs.job[blockIdx.z];
   const int slot = blockIdx.y;
-  if (num_active_dev != nullptr && slot >= *num_active_dev) return;  // uniform over the workgroup
+  const int block0 = blockIdx.x * kBlocksPerWg;
+  if (block0 >= jb.nblk) return;  // uniform over the workgroup
+  const int nblk = jb.nblk;
   const int tid = threadIdx.x;
   const int g = tid / S;
   const int j = tid % S;
-  const int block0 = blockIdx.x * kBlocksPerWg;
   const int block = block0 + g;
   const int expert = expert_ids[slot];
-  const bool evalid = expert >= 0 && expert < num_experts;
+  const bool evalid = expert >= 0 && expert < jb.num_experts;
   GrSpan<S> sp;
-  gr_span_load<S>(sp, evalid ? words + static_cast<int64_t>(expert) * words_stride : nullptr,
-                  evalid ? offsets + static_cast<int64_t>(expert) * (nblk + 1) : nullptr,
-                  evalid ? meta + static_cast<int64_t>(expert) * nblk : nullptr, block, evalid && block < nblk, j);
+  gr_span_load<S>(sp, evalid ? jb.words + static_cast<int64_t>(expert) * jb.words_stride : nullptr,
+                  evalid ? jb.offsets + static_cast<int64_t>(expert) * (nblk + 1) : nullptr,
+                  evalid ? jb.meta + static_cast<int64_t>(expert) * nblk : nullptr, block, evalid && block < nblk, j);
   gr_tables_to_lds(&tab);
   for (int idx = tid; idx < kBlocksPerWg * kGrWords; idx += kSpanThreads) outb[idx / kGrWords][idx % kGrWords] = 0u;
   __syncthreads();
   gr_decode_block_group<S>(sp, &tab, outb[g], j);
   __syncthreads();
-  if (dense_rows == 0) {
-    // predecode layout [slot][block][128]
-    int32_t* dst = decoded + (static_cast<int64_t>(slot) * nblk + block0) * kGrWords;
+  if (jb.dense_rows == 0) {
+    int32_t* dst = jb.out + (static_cast<int64_t>(slot) * nblk + block0) * kGrWords;
     for (int idx = tid; idx < kBlocksPerWg * kGrWords; idx += kSpanThreads) {
       if (block0 + idx / kGrWords < nblk) dst[idx] = static_cast<int32_t>(outb[idx / kGrWords][idx % kGrWords]);
     }
   } else {
-    // dense layout [slot][packed_rows][N]
-    int32_t* dst = decoded + static_cast<int64_t>(slot) * dense_rows * dense_cols;
+    int32_t* dst = jb.out + static_cast<int64_t>(slot) * jb.dense_rows * jb.dense_cols;
     for (int idx = tid; idx < kBlocksPerWg * kGrWords; idx += kSpanThreads) {
       const int b = block0 + idx / kGrWords;
       if (b >= nblk) continue;
       const int w = idx % kGrWords;
-      const int row = (b / num_out_blocks) * kGrPackedRows + w / kTileOut;
-      const int col = (b % num_out_blocks) * kTileOut + w % kTileOut;
-      if (row < dense_rows && col < dense_cols) {
-        dst[static_cast<int64_t>(row) * dense_cols + col] = static_cast<int32_t>(outb[idx / kGrWords][w]);
+      const int row = (b / jb.num_out_blocks) * kGrPackedRows + w / kTileOut;
+      const int col = (b % jb.num_out_blocks) * kTileOut + w % kTileOut;
+      if (row < jb.dense_rows && col < jb.dense_cols) {
+        dst[static_cast<int64_t>(row) * jb.dense_cols + col] = static_cast<int32_t>(outb[idx / kGrWords][w]);
       }
     }
   }
 }
 
-int launch_gr_decode(int32_t* out, const int32_t* expert_ids, const int32_t* num_active_dev, int num_slots,
-                     const int32_t* words, const int32_t* offsets, const int32_t* meta, int num_experts,
-                     int words_stride, int packed_rows, int outfeatures, bool dense, void* stream, const char* who) {
+// Fills job from one projection's arguments; returns the job's block count (0: nothing to do).
+int make_gr_job(GrJob* job, int32_t* out, const int32_t* words, const int32_t* offsets, const int32_t* meta,
+                int num_experts, int words_stride, int packed_rows, int outfeatures, bool dense, const char* who) {
+  TRIS_REQUIRE(packed_rows >= 0 && outfeatures >= 0 && words_stride >= 0 && num_experts >= 0,
+               "%s: negative size", who);
   const int nob = ceil_div(outfeatures, kTileOut);
   const int nblk = ceil_div(packed_rows, kGrPackedRows) * nob;
-  if (num_slots == 0 || nblk == 0) return TRIS_OK;
-  TRIS_REQUIRE(out && expert_ids && offsets && meta && words, "%s: null pointer", who);
+  *job = GrJob{out, words, offsets, meta, num_experts, words_stride, nblk, nob, dense ? packed_rows : 0,
+               dense ? outfeatures : 0};
+  if (nblk == 0) return TRIS_OK;
+  TRIS_REQUIRE(out && offsets && meta && words, "%s: null pointer", who);
+  return TRIS_OK;
+}
+
+int launch_gr_jobs(const GrJobs& jobs, int num_jobs, const int32_t* expert_ids, int num_slots, void* stream,
+                   const char* who) {
+  int max_nblk = 0;
+  int64_t total = 0;
+  for (int q = 0; q < num_jobs; ++q) {
+    max_nblk = jobs.job[q].nblk > max_nblk ? jobs.job[q].nblk : max_nblk;
+    total += static_cast<int64_t>(jobs.job[q].nblk) * num_slots;
+  }
+  if (num_slots == 0 || max_nblk == 0) return TRIS_OK;
+  TRIS_REQUIRE(expert_ids != nullptr, "%s: null expert ids", who);
   TRIS_REQUIRE(num_slots <= 65535, "%s: too many experts (%d)", who, num_slots);
-  const int64_t total = static_cast<int64_t>(nblk) * num_slots;
   const int S = total >= 8192 ? 8 : (total >= 2048 ? 16 : 32);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int dr = dense ? packed_rows : 0;
-  const int dc = dense ? outfeatures : 0;
   if (S == 8) {
-    hipLaunchKernelGGL((gr_decode_span_kernel<8>), dim3(ceil_div(nblk, kSpanThreads / 8), num_slots),
-                       dim3(kSpanThreads), 0, s, out, expert_ids, num_active_dev, words, offsets, meta, words_stride,
-                       nblk, num_experts, dr, dc, nob);
+    hipLaunchKernelGGL((gr_decode_span_kernel<8>), dim3(ceil_div(max_nblk, kSpanThreads / 8), num_slots, num_jobs),
+                       dim3(kSpanThreads), 0, s, jobs, expert_ids);
   } else if (S == 16) {
-    hipLaunchKernelGGL((gr_decode_span_kernel<16>), dim3(ceil_div(nblk, kSpanThreads / 16), num_slots),
-                       dim3(kSpanThreads), 0, s, out, expert_ids, num_active_dev, words, offsets, meta, words_stride,
-                       nblk, num_experts, dr, dc, nob);
+    hipLaunchKernelGGL((gr_decode_span_kernel<16>), dim3(ceil_div(max_nblk, kSpanThreads / 16), num_slots, num_jobs),
+                       dim3(kSpanThreads), 0, s, jobs, expert_ids);
   } else {
-    hipLaunchKernelGGL((gr_decode_span_kernel<32>), dim3(ceil_div(nblk, kSpanThreads / 32), num_slots),
-                       dim3(kSpanThreads), 0, s, out, expert_ids, num_active_dev, words, offsets, meta, words_stride,
-                       nblk, num_experts, dr, dc, nob);
+    hipLaunchKernelGGL((gr_decode_span_kernel<32>), dim3(ceil_div(max_nblk, kSpanThreads / 32), num_slots, num_jobs),
+                       dim3(kSpanThreads), 0, s, jobs, expert_ids);
   }
   return check_launch(who);
 }
@@ -100,19 +128,41 @@ extern "C" int tris_grouped_block_gr_predecode(int32_t* decoded, const int32_t* 
                                                const int32_t* q_gmap_gr_meta, int32_t num_experts,
                                                int32_t words_stride, int32_t packed_rows, int32_t outfeatures,
                                                void* stream) {
-  TRIS_REQUIRE(num_active >= 0 && packed_rows >= 0 && outfeatures >= 0 && words_stride >= 0 && num_experts >= 0,
-               "predecode: negative size");
-  return launch_gr_decode(decoded, expert_ids, nullptr, num_active, q_gmap_gr_words, q_gmap_gr_offsets,
-                          q_gmap_gr_meta, num_experts, words_stride, packed_rows, outfeatures, false, stream,
-                          "tris_grouped_block_gr_predecode");
+  const char* who = "tris_grouped_block_gr_predecode";
+  TRIS_REQUIRE(num_active >= 0, "%s: negative size", who);
+  GrJobs jobs{};
+  int rc = make_gr_job(&jobs.job[0], decoded, q_gmap_gr_words, q_gmap_gr_offsets, q_gmap_gr_meta, num_experts,
+                       words_stride, packed_rows, outfeatures, false, who);
+  if (rc) return rc;
+  return launch_gr_jobs(jobs, 1, expert_ids, num_active, stream, who);
+}
+
+extern "C" int tris_grouped_block_gr_predecode_multi(const tris_gr_predecode_job* jobs, int32_t num_jobs,
+                                                     const int32_t* expert_ids, int32_t num_active, void* stream) {
+  const char* who = "tris_grouped_block_gr_predecode_multi";
+  TRIS_REQUIRE(num_active >= 0, "%s: negative size", who);
+  TRIS_REQUIRE(num_jobs >= 0 && num_jobs <= TRIS_MAX_PREDECODE_JOBS, "%s: %d jobs (at most %d)", who, num_jobs,
+               TRIS_MAX_PREDECODE_JOBS);
+  TRIS_REQUIRE(num_jobs == 0 || jobs != nullptr, "%s: null jobs", who);
+  GrJobs g{};
+  for (int q = 0; q < num_jobs; ++q) {
+    const tris_gr_predecode_job& j = jobs[q];
+    int rc = make_gr_job(&g.job[q], j.decoded, j.q_gmap_gr_words, j.q_gmap_gr_offsets, j.q_gmap_gr_meta,
+                         j.num_experts, j.words_stride, j.packed_rows, j.outfeatures, false, who);
+    if (rc) return rc;
+  }
+  return launch_gr_jobs(g, num_jobs, expert_ids, num_active, stream, who);
 }
 
 extern "C" int tris_gr_decode_dense(const int32_t* q_gmap_gr_words, const int32_t* q_gmap_gr_offsets,
                                     const int32_t* q_gmap_gr_meta, int32_t num_experts, int32_t words_stride,
                                     const int32_t* expert_ids, int32_t num, int32_t packed_rows,
                                     int32_t outfeatures, int32_t* dense, void* stream) {
-  TRIS_REQUIRE(num >= 0 && packed_rows >= 0 && outfeatures >= 0 && words_stride >= 0 && num_experts >= 0,
-               "decode_dense: negative size");
-  return launch_gr_decode(dense, expert_ids, nullptr, num, q_gmap_gr_words, q_gmap_gr_offsets, q_gmap_gr_meta,
-                          num_experts, words_stride, packed_rows, outfeatures, true, stream, "tris_gr_decode_dense");
+  const char* who = "tris_gr_decode_dense";
+  TRIS_REQUIRE(num >= 0, "%s: negative size", who);
+  GrJobs jobs{};
+  int rc = make_gr_job(&jobs.job[0], dense, q_gmap_gr_words, q_gmap_gr_offsets, q_gmap_gr_meta, num_experts,
+                       words_stride, packed_rows, outfeatures, true, who);
+  if (rc) return rc;
+  return launch_gr_jobs(jobs, 1, expert_ids, num, stream, who);
 }

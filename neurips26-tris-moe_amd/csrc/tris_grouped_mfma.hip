@@ -173,7 +173,35 @@ __device__ __forceinline__ f32x4 mfma_project(const MfmaProj& pa, int s, int row
   for (int kc = 0; kc < rank; kc += kMfChunk) {
     const int pr0 = kc / 32;
     const int pr_end = (pr0 + kMfChunk / 32) < packed_rows ? (pr0 + kMfChunk / 32) : packed_rows;
-    // ---- the wave's weight loads for the chunk: 16 packed rows x 1 column per lane
+    // ---- batch 1: the chunk's uniform metadata (group of each 64-column tile, salient words and
+    // prefix per packed row).  Later loads use these in their addresses; loading them first means
+    // the one wait for them does not also wait for the weight loads.
+    // Indices are clamped so that every load is issued unconditionally; validity is applied after.
+    int gt[kMfChunk / kTileK];
+    uint32_t cmw[kMfChunk / 32];
+    int q2p[kMfChunk / 32 + 1];
+#pragma unroll
+    for (int t = 0; t < kMfChunk / kTileK; ++t) {
+      const int kt = kc + t * kTileK;
+      gt[t] = gidx_e[kt < rank ? kt : rank - 1];
+    }
+#pragma unroll
+    for (int j = 0; j < kMfChunk / 32; ++j) {
+      cmw[j] = static_cast<uint32_t>(cmap_e[pr0 + j < packed_rows ? pr0 + j : packed_rows - 1]);
+      q2p[j] = q2p_e[pr0 + j < packed_rows ? pr0 + j : packed_rows];
+    }
+    q2p[kMfChunk / 32] = q2p_e[pr_end];
+#pragma unroll
+    for (int t = 0; t < kMfChunk / kTileK; ++t) {
+      gt[t] = (kc + t * kTileK) < rank ? __builtin_amdgcn_readfirstlane(gt[t]) : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kMfChunk / 32; ++j) {
+      const int pr = pr0 + j;
+      const int nbits = (rank - pr * 32) < 32 ? (rank - pr * 32) : 32;
+      cmw[j] = pr < packed_rows ? (cmw[j] & low_mask(nbits)) : 0u;
+    }
+    // ---- batch 2: the wave's weights (16 packed rows x 1 column per lane) and row scales
     uint32_t qw[kMfChunk / 32], gw[kMfChunk / 32];
     uint64_t rp[kMfChunk / kTileK];
 #pragma unroll
@@ -187,29 +215,49 @@ __device__ __forceinline__ f32x4 mfma_project(const MfmaProj& pa, int s, int row
     }
 #pragma unroll
     for (int t = 0; t < kMfChunk / kTileK; ++t) {
-      const int kt = kc + t * kTileK;
-      const int g = kt < rank ? gidx_e[kt] : -1;
+      const int g = gt[t];
       rp[t] = (nv && g >= 0 && g < G)
                   ? static_cast<uint64_t>(row_e[nu * static_cast<uint32_t>(G) + static_cast<uint32_t>(g)]) : 0ull;
     }
-    const int sbase0 = q2p_e[pr0];                // qweight2_sparse index of the chunk's first salient column
-    const int num_sal = q2p_e[pr_end] - sbase0;   // salient columns in the chunk
+    const int sbase0 = q2p[0];                        // qweight2_sparse index of the chunk's first salient column
+    const int num_sal = q2p[kMfChunk / 32] - sbase0;  // salient columns in the chunk
     // first qweight2_sparse row of the chunk's salient columns (usually the only one)
     const int q2row0 = sbase0 >> 5;
     const uint32_t q2w0 = (nv && num_sal > 0 && q2row0 < p.qweight2_sparse_rows)
         ? static_cast<uint32_t>(q2_e[static_cast<uint32_t>(q2row0) * static_cast<uint32_t>(N) + nu]) : 0u;
-    // ---- stage activations (rc rows, 8-column runs; rank is a multiple of 64 so a run is
-    // wholly inside or outside the matrix), column factors and the salient column list
+    // staging loads, issued with the weight loads: activation runs (row idx / 64, 8-column run
+    // idx % 64; rank is a multiple of 64, so a run is wholly inside or outside the matrix) and,
+    // for columns kc + tid and kc + tid + 256, the column factors, salient word and prefix
+    constexpr int kRuns = kMfRows * (kMfChunk / 8) / kMfThreads;
+    uint4 xv[kRuns];
+#pragma unroll
+    for (int h = 0; h < kRuns; ++h) {
+      const int idx = tid + h * kMfThreads;
+      const int r = idx / (kMfChunk / 8);
+      const int c = (idx % (kMfChunk / 8)) * 8;
+      xv[h] = (r < rc && kc + c < rank) ? *reinterpret_cast<const uint4*>(hid + static_cast<uint32_t>(r * rank + kc + c))
+                                        : make_uint4(0u, 0u, 0u, 0u);
+    }
+    uint64_t cpv[2];
+    uint32_t cmt[2];
+    int q2t[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int k = kc + tid + h * kMfThreads;
+      const bool kv = k < rank;
+      const int pr = kv ? (k >> 5) : 0;
+      cpv[h] = kv ? static_cast<uint64_t>(col_e[k]) : 0ull;
+      cmt[h] = kv ? static_cast<uint32_t>(cmap_e[pr]) : 0u;
+      q2t[h] = kv ? q2p_e[pr] : 0;
+    }
     __syncthreads();  // previous chunk's LDS readers are done
-    for (int idx = tid; idx < kMfRows * (kMfChunk / 8); idx += kMfThreads) {
+#pragma unroll
+    for (int h = 0; h < kRuns; ++h) {
+      const int idx = tid + h * kMfThreads;
       const int r = idx / (kMfChunk / 8);
       const int c = (idx % (kMfChunk / 8)) * 8;  // run start within the chunk (a multiple of 8)
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (r < rc && kc + c < rank) {
-        v = *reinterpret_cast<const uint4*>(hid + static_cast<uint32_t>(r * rank + kc + c));
-      }
       // columns c + b and c + b + 4 (b < 4) are neighbours in the staged order
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+      const uint32_t w[4] = {xv[h].x, xv[h].y, xv[h].z, xv[h].w};
       const int base = (c & ~31) + ((c & 31) >> 2);
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
@@ -218,20 +266,20 @@ __device__ __forceinline__ f32x4 mfma_project(const MfmaProj& pa, int s, int row
         *reinterpret_cast<uint32_t*>(&xs[r][base + 8 * b]) = lo | (hi << 16);
       }
     }
-    for (int j = tid; j < kMfChunk; j += kMfThreads) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = tid + h * kMfThreads;
       const int k = kc + j;
-      const bool kv = k < rank;
-      const uint64_t cp = kv ? static_cast<uint64_t>(col_e[k]) : 0ull;
       const int pj = (j & ~31) + mf_perm32(j & 31);
-      cds[pj] = static_cast<uint16_t>(cp >> 32);
-      cns[pj] = static_cast<uint16_t>(cp >> 48);
-      col_sal[j] = static_cast<uint32_t>(cp);
-      if (kv) {
-        const int pr = k >> 5;
+      cds[pj] = static_cast<uint16_t>(cpv[h] >> 32);
+      cns[pj] = static_cast<uint16_t>(cpv[h] >> 48);
+      col_sal[j] = static_cast<uint32_t>(cpv[h]);
+      if (k < rank) {
         const int bit = k & 31;
+        const int pr = k >> 5;
         const int nbits = (rank - pr * 32) < 32 ? (rank - pr * 32) : 32;
-        const uint32_t cmw = static_cast<uint32_t>(cmap_e[pr]) & low_mask(nbits);
-        if ((cmw >> bit) & 1u) sal_col[q2p_e[pr] - sbase0 + __popc(cmw & ((1u << bit) - 1u))] = static_cast<uint16_t>(j);
+        const uint32_t cm = cmt[h] & low_mask(nbits);
+        if ((cm >> bit) & 1u) sal_col[q2t[h] - sbase0 + __popc(cm & ((1u << bit) - 1u))] = static_cast<uint16_t>(j);
       }
     }
     __syncthreads();
@@ -252,9 +300,7 @@ __device__ __forceinline__ f32x4 mfma_project(const MfmaProj& pa, int s, int row
         const uint4 cnv = *reinterpret_cast<const uint4*>(&cns[kl]);
         const uint32_t cd[4] = {cdv.x, cdv.y, cdv.z, cdv.w};
         const uint32_t cn[4] = {cnv.x, cnv.y, cnv.z, cnv.w};
-        const int nbits = (rank - pr * 32) < 32 ? (rank - pr * 32) : 32;
-        const uint32_t cmw = static_cast<uint32_t>(cmap_e[pr]) & low_mask(nbits);  // salient columns
-        const uint32_t nsal = (~cmw >> kg) & 0x11111111u;                          // 1 = non-salient
+        const uint32_t nsal = (~cmw[j] >> kg) & 0x11111111u;                       // 1 = non-salient
         const uint32_t neg = ((~qw[j]) >> kg) & 0x11111111u;                         // 1 = negative
         const uint32_t gd = (gw[j] >> kg) & nsal;                                    // 1 = d term
         const uint32_t gn = nsal ^ gd;                                               // 1 = nd term
@@ -286,14 +332,12 @@ __device__ __forceinline__ f32x4 mfma_project(const MfmaProj& pa, int s, int row
         const int pr = pr0 + j;
         if (pr < packed_rows) {
           const int t = j / 2;
-          const int nbits = (rank - pr * 32) < 32 ? (rank - pr * 32) : 32;
-          const uint32_t cmw = static_cast<uint32_t>(cmap_e[pr]) & low_mask(nbits);
-          uint32_t m = cmw & (0x11111111u << kg);
-          const int sbase = q2p_e[pr];
+          uint32_t m = cmw[j] & (0x11111111u << kg);
+          const int sbase = q2p[j];
           while (m != 0u) {
             const int bit = __builtin_ctz(m);
             m &= m - 1u;
-            const int sidx = sbase + __popc(cmw & ((1u << bit) - 1u));  // qweight2_sparse index
+            const int sidx = sbase + __popc(cmw[j] & ((1u << bit) - 1u));  // qweight2_sparse index
             const int q = sidx - sbase0 - w0;                            // slot in the window
             if (q >= 0 && q < kMfSalWin) {
               uint32_t q2w = q2w0;
@@ -370,7 +414,7 @@ __global__ __launch_bounds__(kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
-  const int e = a.expert_ids[s];
+  const int e = __builtin_amdgcn_readfirstlane(a.expert_ids[s]);
   uint16_t* out = pa.out;
   if (e < 0 || e >= p.num_experts) {
     for (int idx = tid; idx < rc * kTileOut; idx += kMfThreads) {

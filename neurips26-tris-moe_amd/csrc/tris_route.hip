@@ -11,6 +11,9 @@
 //      counting-sort scatter; each wave scans the flattened expert ids in
 //      64-element chunks and places its expert's entries in flat order using
 //      a ballot and a popcount of the lower lanes.
+// For decode-sized batches route_topk_small_kernel does the router softmax
+// and top-k (modeling_mixtral.py:548-555) and all of the above in one
+// workgroup and one launch.
 #include "tris_common.h"
 
 namespace tris {
@@ -125,6 +128,155 @@ __global__ __launch_bounds__(256) void route_scatter_kernel(
   }
 }
 
+constexpr int kRouteSmallMaxRows = 2048;    // tokens * top_k
+constexpr int kRouteSmallMaxExperts = 1024;
+constexpr int kRouteMaxTopK = 16;
+
+// One workgroup: per token softmax (fp32, max-subtracted, summed in expert
+// order), top-k by probability with ties to the lower expert id (a stable
+// descending sort, as the oracle's argsort), optional renormalisation over the
+// k picks (summed in pick order), fp16 weights; then the histogram, scan and
+// padded outputs of route_histogram_kernel and a stable scatter in which each
+// routed entry counts the earlier entries of its expert.
+__global__ __launch_bounds__(kRouteThreads) void route_topk_small_kernel(
+    const float* __restrict__ logits, int tokens, int num_experts, int top_k, int renormalize, int m_tile,
+    uint16_t* __restrict__ weights16, float* __restrict__ weights32, int64_t* __restrict__ selected,
+    int64_t* __restrict__ perm, int64_t* __restrict__ token_idx, int64_t* __restrict__ slots,
+    int32_t* __restrict__ grouped_expert_ids, int32_t* __restrict__ expert_ids, int32_t* __restrict__ segment_offsets,
+    int32_t* __restrict__ problem_offsets, int32_t* __restrict__ counts, int32_t* __restrict__ inverse_perm) {
+  __shared__ int16_t sel[kRouteSmallMaxRows];
+  __shared__ int cnt[kRouteSmallMaxExperts];
+  __shared__ int seg_of[kRouteSmallMaxExperts];  // first row of each expert's segment
+  __shared__ int scan_active[kRouteThreads];
+  __shared__ int scan_rows[kRouteThreads];
+  __shared__ int scan_tiles[kRouteThreads];
+  const int tid = threadIdx.x;
+  const int total = tokens * top_k;
+  for (int e = tid; e < num_experts; e += kRouteThreads) cnt[e] = 0;
+  __syncthreads();
+  // ---- softmax and top-k, one token per thread
+  for (int t = tid; t < tokens; t += kRouteThreads) {
+    const float* row = logits + static_cast<int64_t>(t) * num_experts;
+    float m = row[0];
+    for (int e = 1; e < num_experts; ++e) m = fmaxf(m, row[e]);
+    float sum = 0.0f;
+    for (int e = 0; e < num_experts; ++e) sum += expf(row[e] - m);
+    float bp[kRouteMaxTopK];
+    int be[kRouteMaxTopK];
+#pragma unroll
+    for (int j = 0; j < kRouteMaxTopK; ++j) {
+      bp[j] = -1.0f;
+      be[j] = -1;
+    }
+    for (int e = 0; e < num_experts; ++e) {
+      const float pe = expf(row[e] - m) / sum;
+      // insert after every kept entry with probability >= pe (earlier experts win ties)
+      if (pe > bp[top_k - 1] || be[top_k - 1] < 0) {
+        float cp = pe;
+        int ce = e;
+        bool shifting = false;  // once placed, every later entry moves down one
+#pragma unroll
+        for (int j = 0; j < kRouteMaxTopK; ++j) {
+          if (j < top_k && (shifting || be[j] < 0 || cp > bp[j])) {
+            const float tp = bp[j];
+            const int te = be[j];
+            bp[j] = cp;
+            be[j] = ce;
+            cp = tp;
+            ce = te;
+            shifting = true;
+          }
+        }
+      }
+    }
+    float denom = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRouteMaxTopK; ++j) {
+      if (j < top_k) denom += bp[j];
+    }
+#pragma unroll
+    for (int j = 0; j < kRouteMaxTopK; ++j) {
+      if (j < top_k) {
+        const float w = renormalize ? bp[j] / denom : bp[j];
+        const int i = t * top_k + j;
+        sel[i] = static_cast<int16_t>(be[j]);
+        if (selected != nullptr) selected[i] = be[j];
+        weights16[i] = f2h_bits(w);
+        if (weights32 != nullptr) weights32[i] = w;
+        atomicAdd(&cnt[be[j]], 1);
+      }
+    }
+  }
+  __syncthreads();
+  // ---- per-expert counts -> compacted active experts, segment and problem offsets
+  const int chunk = (num_experts + kRouteThreads - 1) / kRouteThreads;
+  const int e0 = tid * chunk;
+  const int e1 = (e0 + chunk) < num_experts ? (e0 + chunk) : num_experts;
+  int na = 0, nr = 0, nt = 0;
+  for (int e = e0; e < e1; ++e) {
+    const int c = cnt[e];
+    if (c > 0) {
+      ++na;
+      nr += c;
+      nt += (c + m_tile - 1) / m_tile;
+    }
+  }
+  scan_active[tid] = na;
+  scan_rows[tid] = nr;
+  scan_tiles[tid] = nt;
+  __syncthreads();
+  for (int d = 1; d < kRouteThreads; d <<= 1) {
+    const int va = tid >= d ? scan_active[tid - d] : 0;
+    const int vr = tid >= d ? scan_rows[tid - d] : 0;
+    const int vt = tid >= d ? scan_tiles[tid - d] : 0;
+    __syncthreads();
+    scan_active[tid] += va;
+    scan_rows[tid] += vr;
+    scan_tiles[tid] += vt;
+    __syncthreads();
+  }
+  const int num_active = scan_active[kRouteThreads - 1];
+  const int rows_total = scan_rows[kRouteThreads - 1];
+  const int tiles_total = scan_tiles[kRouteThreads - 1];
+  int a = scan_active[tid] - na;
+  int r = scan_rows[tid] - nr;
+  int tt = scan_tiles[tid] - nt;
+  for (int e = e0; e < e1; ++e) {
+    const int c = cnt[e];
+    seg_of[e] = r;
+    if (c > 0) {
+      expert_ids[a] = e;
+      segment_offsets[a] = r;
+      problem_offsets[a] = tt;
+      ++a;
+      r += c;
+      tt += (c + m_tile - 1) / m_tile;
+    }
+  }
+  for (int j = num_active + tid; j < num_experts; j += kRouteThreads) expert_ids[j] = -1;
+  for (int j = num_active + tid; j <= num_experts; j += kRouteThreads) {
+    segment_offsets[j] = rows_total;
+    problem_offsets[j] = tiles_total;
+  }
+  if (tid == 0) {
+    counts[0] = num_active;
+    counts[1] = tiles_total;
+  }
+  __syncthreads();
+  // ---- stable scatter: an entry's place in its segment = earlier entries of the same expert
+  for (int i = tid; i < total; i += kRouteThreads) {
+    const int e = sel[i];
+    int before = 0;
+    for (int q = 0; q < i; ++q) before += sel[q] == e ? 1 : 0;
+    const int dst = seg_of[e] + before;
+    perm[dst] = i;
+    token_idx[dst] = i / top_k;
+    slots[dst] = i % top_k;
+    grouped_expert_ids[dst] = e;
+    if (inverse_perm != nullptr) inverse_perm[i] = dst;
+  }
+}
+
 }  // namespace tris
 
 using namespace tris;
@@ -159,4 +311,32 @@ extern "C" int tris_build_grouped_route(const int64_t* selected_experts, int32_t
                      selected_experts, static_cast<int>(total), top_k, num_experts, expert_ids, segment_offsets, perm,
                      grouped_token_indices, grouped_slots, grouped_expert_ids, inverse_perm);
   return check_launch("route_scatter_kernel");
+}
+
+extern "C" int tris_route_topk_grouped(const float* router_logits, int32_t num_tokens, int32_t num_experts,
+                                       int32_t top_k, int32_t renormalize, int32_t m_tile,
+                                       uint16_t* routing_weights_f16, float* routing_weights_f32,
+                                       int64_t* selected_experts, int64_t* perm, int64_t* grouped_token_indices,
+                                       int64_t* grouped_slots, int32_t* grouped_expert_ids, int32_t* expert_ids,
+                                       int32_t* segment_offsets, int32_t* problem_offsets, int32_t* counts,
+                                       int32_t* inverse_perm, void* stream) {
+  const char* who = "tris_route_topk_grouped";
+  TRIS_REQUIRE(num_tokens >= 0 && num_experts > 0 && top_k > 0, "%s: bad shape", who);
+  TRIS_REQUIRE(top_k <= num_experts && top_k <= kRouteMaxTopK, "%s: top_k %d (at most %d and num_experts)", who,
+               top_k, kRouteMaxTopK);
+  TRIS_REQUIRE(num_experts <= kRouteSmallMaxExperts, "%s: num_experts %d exceeds %d", who, num_experts,
+               kRouteSmallMaxExperts);
+  TRIS_REQUIRE(static_cast<int64_t>(num_tokens) * top_k <= kRouteSmallMaxRows,
+               "%s: %lld routed rows exceed %d (use tris_build_grouped_route)", who,
+               static_cast<long long>(num_tokens) * top_k, kRouteSmallMaxRows);
+  TRIS_REQUIRE(m_tile > 0, "m_tile must be positive");
+  TRIS_REQUIRE(counts && segment_offsets && problem_offsets && expert_ids, "%s: null output", who);
+  TRIS_REQUIRE(num_tokens == 0 || (router_logits && routing_weights_f16 && perm && grouped_token_indices &&
+                                   grouped_slots && grouped_expert_ids),
+               "%s: null pointer", who);
+  hipLaunchKernelGGL(route_topk_small_kernel, dim3(1), dim3(kRouteThreads), 0, static_cast<hipStream_t>(stream),
+                     router_logits, num_tokens, num_experts, top_k, renormalize, m_tile, routing_weights_f16,
+                     routing_weights_f32, selected_experts, perm, grouped_token_indices, grouped_slots,
+                     grouped_expert_ids, expert_ids, segment_offsets, problem_offsets, counts, inverse_perm);
+  return check_launch(who);
 }

@@ -49,6 +49,23 @@ class TrisPayload(ctypes.Structure):
 
 
 # name -> (restype, argtypes)
+class TrisPredecodeJob(ctypes.Structure):
+    """Mirror of struct tris_gr_predecode_job."""
+
+    _fields_ = [
+        ("decoded", ctypes.c_void_p),
+        ("q_gmap_gr_words", ctypes.c_void_p),
+        ("q_gmap_gr_offsets", ctypes.c_void_p),
+        ("q_gmap_gr_meta", ctypes.c_void_p),
+        ("num_experts", ctypes.c_int32),
+        ("words_stride", ctypes.c_int32),
+        ("packed_rows", ctypes.c_int32),
+        ("outfeatures", ctypes.c_int32),
+    ]
+
+
+MAX_PREDECODE_JOBS = 4
+
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
 _I64 = ctypes.c_int64
@@ -58,9 +75,12 @@ SIGNATURES = {
     "tris_last_error": (ctypes.c_char_p, []),
     "tris_gr_encode": (_I64, [_P, _I32, _I32, _I32, _I32, _I32, _P, _I64, _P, _P]),
     "tris_build_grouped_route": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "tris_route_topk_grouped": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                                _P, _P, _P, _P]),
     "tris_grouped_forward_block_gr": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I32, _I64, _PAY, _P, _P]),
     "tris_grouped_dual_forward_block_gr": (ctypes.c_int, [_P, _P, _I32, _P, _P, _P, _I32, _I64, _PAY, _PAY, _P, _P, _P]),
     "tris_grouped_block_gr_predecode": (ctypes.c_int, [_P, _P, _I32, _P, _P, _P, _I32, _I32, _I32, _I32, _P]),
+    "tris_grouped_block_gr_predecode_multi": (ctypes.c_int, [ctypes.POINTER(TrisPredecodeJob), _I32, _P, _I32, _P]),
     "tris_grouped_forward_block_gr_predecoded": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I32, _I64, _P, _PAY, _P, _P]),
     "tris_grouped_dual_forward_block_gr_predecoded": (
         ctypes.c_int, [_P, _P, _I32, _P, _P, _P, _I32, _I64, _P, _P, _PAY, _PAY, _P, _P, _P]),

@@ -216,6 +216,47 @@ def build_grouped_route_device(selected_experts: torch.Tensor, num_experts: int,
             "inverse_perm": inv}
 
 
+ROUTE_TOPK_MAX_ROWS = 2048     # tokens * top_k for tris_route_topk_grouped
+ROUTE_TOPK_MAX_EXPERTS = 1024
+ROUTE_TOPK_MAX_K = 16
+
+
+def route_topk_grouped(router_logits: torch.Tensor, top_k: int, renormalize: bool, m_tile: int = 4) -> dict:
+    """Router softmax / top-k / renormalisation (modeling_mixtral.py:548-555) and the padded grouped
+    route in one launch, for decode-sized batches (an extension; see build_grouped_route_device).
+    Returns the route dict plus routing_weights_f16 [T, k], routing_weights [T, k] fp32 and
+    selected_experts [T, k] int64."""
+    _check_cuda("router_logits", router_logits, torch.float32, 2)
+    logits = router_logits.contiguous()
+    t, e = int(logits.size(0)), int(logits.size(1))
+    k = int(top_k)
+    if t * k > ROUTE_TOPK_MAX_ROWS or e > ROUTE_TOPK_MAX_EXPERTS or k > ROUTE_TOPK_MAX_K or k > e or k <= 0:
+        raise RuntimeError("route_topk_grouped: batch outside the one-workgroup limits")
+    dev = logits.device
+    r = t * k
+    long_opts = dict(device=dev, dtype=torch.int64)
+    int_opts = dict(device=dev, dtype=torch.int32)
+    w16 = torch.empty((t, k), device=dev, dtype=torch.float16)
+    w32 = torch.empty((t, k), device=dev, dtype=torch.float32)
+    sel = torch.empty((t, k), **long_opts)
+    perm = torch.empty(r, **long_opts)
+    gti = torch.empty(r, **long_opts)
+    gsl = torch.empty(r, **long_opts)
+    gexp = torch.empty(r, **int_opts)
+    expert_ids = torch.empty(e, **int_opts)
+    seg = torch.empty(e + 1, **int_opts)
+    prob = torch.empty(e + 1, **int_opts)
+    counts = torch.empty(2, **int_opts)
+    inv = torch.empty(r, **int_opts)
+    _lib.check(_lib.load().tris_route_topk_grouped(
+        _ptr(logits), t, e, k, int(bool(renormalize)), int(m_tile), _ptr(w16), _ptr(w32), _ptr(sel), _ptr(perm),
+        _ptr(gti), _ptr(gsl), _ptr(gexp), _ptr(expert_ids), _ptr(seg), _ptr(prob), _ptr(counts), _ptr(inv),
+        _stream(logits)), "route_topk_grouped")
+    return {"perm": perm, "grouped_token_indices": gti, "grouped_slots": gsl, "grouped_expert_ids": gexp,
+            "expert_ids": expert_ids, "segment_offsets": seg, "problem_offsets": prob, "counts": counts,
+            "inverse_perm": inv, "routing_weights_f16": w16, "routing_weights": w32, "selected_experts": sel}
+
+
 # ----------------------------------------------------------- grouped GEMMs
 def compact3_tris_precomputed_grouped_forward_block_gr(hidden, expert_ids, segment_offsets, problem_offsets,
                                                        total_problem_tiles, qweight1, qweight2_sparse,
@@ -295,6 +336,39 @@ def compact3_tris_precomputed_grouped_block_gr_predecode(decoded_q_gmap_words, e
         int(outfeatures), _stream(decoded_q_gmap_words)),
         "compact3_tris_precomputed_grouped_block_gr_predecode")
     return decoded_q_gmap_words
+
+
+def grouped_block_gr_predecode_multi(jobs, expert_ids):
+    """Predecode several projections' GR streams for the same routed experts in one launch (an
+    extension batching TriSMoE_cuda.cpp:836-853).  jobs: sequence of (decoded_buffer,
+    q_gmap_gr_words, q_gmap_gr_offsets, q_gmap_gr_meta, packed_rows, outfeatures); each buffer is
+    filled as compact3_tris_precomputed_grouped_block_gr_predecode would fill it and returned."""
+    if len(jobs) > _lib.MAX_PREDECODE_JOBS:
+        raise RuntimeError(f"at most {_lib.MAX_PREDECODE_JOBS} predecode jobs per launch")
+    _check_cuda("expert_ids", expert_ids, torch.int32, 1)
+    dev = expert_ids.device
+    num_active = int(expert_ids.size(0))
+    arr = (_lib.TrisPredecodeJob * max(len(jobs), 1))()
+    keep = []
+    for q, (buf, words, offsets, meta, packed_rows, outfeatures) in enumerate(jobs):
+        _check_cuda("decoded_q_gmap_words", buf, torch.int32, None, dev)
+        _check_cuda("q_gmap_gr_words", words, torch.int32, 2, dev)
+        _check_cuda("q_gmap_gr_offsets", offsets, torch.int32, 2, dev)
+        _check_cuda("q_gmap_gr_meta", meta, torch.int32, 2, dev)
+        nblk = _num_gr_blocks(int(packed_rows), int(outfeatures))
+        if buf.numel() != num_active * nblk * BLOCK_GR_WORDS_PER_BLOCK:
+            raise RuntimeError("decoded_q_gmap_words must hold [active, blocks, 128] words")
+        if int(offsets.size(1)) != nblk + 1 or int(meta.size(1)) != nblk:
+            raise RuntimeError("q_gmap_gr_offsets/meta shape mismatch")
+        if words.numel() == 0:
+            words = torch.zeros((max(int(offsets.size(0)), 1), 1), dtype=torch.int32, device=dev)
+        keep.append(words)
+        arr[q] = _lib.TrisPredecodeJob(_ptr(buf), _ptr(words), _ptr(offsets), _ptr(meta), int(offsets.size(0)),
+                                       int(words.size(1)), int(packed_rows), int(outfeatures))
+    _lib.check(_lib.load().tris_grouped_block_gr_predecode_multi(arr, len(jobs), _ptr(expert_ids), num_active,
+                                                                 _stream(expert_ids)),
+               "grouped_block_gr_predecode_multi")
+    return [j[0] for j in jobs]
 
 
 def compact3_tris_precomputed_grouped_forward_block_gr_predecoded(hidden, expert_ids, segment_offsets,

@@ -45,14 +45,41 @@ def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, select
     expert_path: "predecoded" decodes the split bitmaps once per projection and runs the MFMA
     grouped GEMMs (needs uniform 64-column groups and no output scale or bias); "fused" decodes
     inside the exact grouped GEMM; "auto" takes "predecoded" whenever the payloads allow it."""
-    if expert_path not in ("auto", "fused", "predecoded"):
-        raise ValueError(f"unknown expert_path {expert_path!r}")
     T, H = int(x16.size(0)), int(x16.size(1))
     k = int(selected_experts.size(1))
-    R = T * k
-    if R == 0:
+    if T * k == 0:
         return torch.zeros((T, H), dtype=output_dtype, device=x16.device)
     route = ext.build_grouped_route_device(selected_experts, num_experts, GROUPED_SEGMENT_M_TILE)
+    w16 = routing_weights.to(torch.float16).contiguous()
+    return _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, output_dtype, shared_expert,
+                               expert_path)
+
+
+def grouped_moe_forward_from_logits(x16: torch.Tensor, router_logits: torch.Tensor, top_k: int, renormalize: bool,
+                                    payloads: dict, backbones: dict, num_experts: int,
+                                    output_dtype=torch.bfloat16, shared_expert=None,
+                                    expert_path: str = "auto") -> torch.Tensor:
+    """The layer from router logits: softmax / top-k / renormalisation / route in one kernel when the
+    batch is decode-sized (tris_route_topk_grouped), else route_topk + the two-kernel route."""
+    T, H = int(x16.size(0)), int(x16.size(1))
+    if T * top_k == 0:
+        return torch.zeros((T, H), dtype=output_dtype, device=x16.device)
+    if (router_logits.dtype == torch.float32 and T * top_k <= ext.ROUTE_TOPK_MAX_ROWS
+            and num_experts <= ext.ROUTE_TOPK_MAX_EXPERTS and top_k <= ext.ROUTE_TOPK_MAX_K):
+        route = ext.route_topk_grouped(router_logits, top_k, renormalize, GROUPED_SEGMENT_M_TILE)
+        return _forward_with_route(x16, route["routing_weights_f16"], route, top_k, payloads, backbones,
+                                   num_experts, output_dtype, shared_expert, expert_path)
+    weights, selected = route_topk(router_logits, top_k, renormalize)
+    return grouped_moe_forward(x16, weights, selected, payloads, backbones, num_experts, output_dtype,
+                               shared_expert, expert_path)
+
+
+def _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, output_dtype, shared_expert,
+                        expert_path):
+    if expert_path not in ("auto", "fused", "predecoded"):
+        raise ValueError(f"unknown expert_path {expert_path!r}")
+    T = int(x16.size(0))
+    R = T * k
     gti = route["grouped_token_indices"]
     expert_ids = route["expert_ids"]
     seg = route["segment_offsets"]
@@ -66,10 +93,9 @@ def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, select
     if expert_path == "predecoded" and not predecodable:
         raise RuntimeError("the predecoded expert path needs uniform 64-column groups and no output scale or bias")
     if predecodable and expert_path != "fused":
-        return _predecoded_moe_forward(x16, routing_weights, route, payloads, backbones, num_experts, R,
-                                       output_dtype, shared_expert)
-    hid_g = ext.backbone_linear(x16, backbones["gate"], row_index=gti)
-    hid_u = ext.backbone_linear(x16, backbones["up"], row_index=gti)
+        return _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype,
+                                       shared_expert)
+    hid_g, hid_u = ext.backbone_linear_pair(x16, backbones["gate"], backbones["up"], row_index=gti)
     empty = x16.new_empty((0, 0))
     g_out, u_out = ext.compact3_tris_precomputed_grouped_dual_forward_block_gr(
         hid_g, hid_u, expert_ids, seg, prob, tile_bound,
@@ -87,11 +113,10 @@ def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, select
         pd["q_gmap_gr_offsets"], pd["q_gmap_gr_meta"], pd["c_map"], pd["g_idx"], pd["col_pack3"], pd["row_pack3"],
         pd["output_scale"], bool(pd["has_output_scale"]), pd["bias"] if pd["has_bias"] else empty,
         bool(pd["has_bias"]), bool(pd.get("_compact3_k64_groups_uniform", False)))
-    return _combine(x16, d_out, route, routing_weights, output_dtype, shared_expert)
+    return _combine(x16, d_out, route, w16, output_dtype, shared_expert)
 
 
-def _combine(x16, d_out, route, routing_weights, output_dtype, shared_expert):
-    w16 = routing_weights.to(torch.float16).contiguous()
+def _combine(x16, d_out, route, w16, output_dtype, shared_expert):
     shared = None
     if shared_expert is not None:
         wg, wu, wd = shared_expert
@@ -106,12 +131,6 @@ def _predecode_buffer(p, slots, device):
     return torch.empty((slots, nblk, 128), dtype=torch.int32, device=device)
 
 
-def _predecode(p, expert_ids, buf):
-    packed_rows, n = int(p["qweight1"].size(1)), int(p["qweight1"].size(2))
-    return ext.compact3_tris_precomputed_grouped_block_gr_predecode(
-        buf, expert_ids, p["q_gmap_gr_words"], p["q_gmap_gr_offsets"], p["q_gmap_gr_meta"], packed_rows, n)
-
-
 _SIDE_STREAMS: dict = {}
 
 
@@ -123,8 +142,7 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
     return _SIDE_STREAMS[key]
 
 
-def _predecoded_moe_forward(x16, routing_weights, route, payloads, backbones, num_experts, R, output_dtype,
-                            shared_expert):
+def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype, shared_expert):
     """Uniform-group payloads without output scale or bias: GR-decode every routed expert's split
     bitmaps once per projection (TriSMoE_cuda.cpp:836-853), then run the predecoded grouped GEMMs
     (TriSMoE_cuda.cpp:855-889, 922-974).  Active experts come first in the padded route, so
@@ -143,7 +161,11 @@ def _predecoded_moe_forward(x16, routing_weights, route, payloads, backbones, nu
     side = _side_stream(dev)
     side.wait_stream(main)
     with torch.cuda.stream(side):
-        decoded = {name: _predecode(p, eid, bufs[name]) for name, p in (("gate", pg), ("up", pu), ("down", pd))}
+        order = (("gate", pg), ("up", pu), ("down", pd))
+        ext.grouped_block_gr_predecode_multi(
+            [(bufs[name], p["q_gmap_gr_words"], p["q_gmap_gr_offsets"], p["q_gmap_gr_meta"], int(p["qweight1"].size(1)),
+              int(p["qweight1"].size(2))) for name, p in order], eid)
+        decoded = bufs
     hid_g, hid_u = ext.backbone_linear_pair(x16, backbones["gate"], backbones["up"],
                                             row_index=route["grouped_token_indices"])
     main.wait_stream(side)
@@ -157,7 +179,7 @@ def _predecoded_moe_forward(x16, routing_weights, route, payloads, backbones, nu
     d_out = torch.empty((R, int(pd["qweight1"].size(2))), dtype=torch.float16, device=dev)
     ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
         hid_d, eid, seg, prob, tile_bound, decoded["down"], *[pd[k] for k in names], True, out=d_out)
-    return _combine(x16, d_out, route, routing_weights, output_dtype, shared_expert)
+    return _combine(x16, d_out, route, w16, output_dtype, shared_expert)
 
 
 class TrisSparseMoeBlock(nn.Module):
@@ -180,12 +202,12 @@ class TrisSparseMoeBlock(nn.Module):
     def forward_routed(self, hidden_states: torch.Tensor, router_logits: torch.Tensor) -> torch.Tensor:
         """The block after the router: [T, H] activations and [T, E] logits -> [T, H]."""
         output_dtype = hidden_states.dtype
-        weights, selected = route_topk(router_logits, self.top_k, self.renormalize)
         x16 = hidden_states.to(torch.float16) if hidden_states.dtype == torch.bfloat16 else hidden_states
         if x16.dtype != torch.float16 or x16.device.type != "cuda":
             raise RuntimeError("grouped expert kernels require CUDA float16/bfloat16 hidden states")
-        return grouped_moe_forward(x16.contiguous(), weights, selected, self.payloads, self.backbones,
-                                   self.num_experts, output_dtype, self.shared_expert)
+        return grouped_moe_forward_from_logits(x16.contiguous(), router_logits.float().contiguous(), self.top_k,
+                                               self.renormalize, self.payloads, self.backbones, self.num_experts,
+                                               output_dtype, self.shared_expert)
 
     def forward(self, hidden_states: torch.Tensor):
         batch, seq, hidden = hidden_states.shape

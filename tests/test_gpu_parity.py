@@ -149,6 +149,26 @@ def test_predecode_large_grids(tris, oracle_mod, cuda, experts, packed_rows, n):
         np.testing.assert_array_equal(dense[i], denses[e])
 
 
+def test_predecode_multi_matches_single_calls(tris, oracle_mod, cuda):
+    """Three projections of different block counts in one launch give each projection's single-call
+    result bit for bit (slots with expert -1 give zero blocks)."""
+    note("predecode multi")
+    rng = np.random.default_rng(12)
+    shapes = [(16, 448, 0.15), (16, 448, 0.3), (32, 128, 0.05)]
+    ids = np.array([2, 0, -1], dtype=np.int32)
+    jobs, want = [], []
+    for rows, n, p in shapes:
+        denses = [random_bitmap(rng, rows, n, p) for _ in range(3)]
+        words, offsets, meta = stacked_gr(oracle_mod, denses)
+        nblk = (rows // 2) * ((n + 63) // 64)
+        want.append(oracle_mod.gr_predecode(words, offsets, meta, ids, nblk))
+        buf = torch.full((ids.size, nblk, 128), 7, dtype=torch.int32, device=cuda)
+        jobs.append((buf, t_i32(words, cuda), t_i32(offsets, cuda), t_i32(meta, cuda), rows, n))
+    got = tris["ext"].grouped_block_gr_predecode_multi(jobs, t_i32(ids, cuda))
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g.cpu().numpy(), w)
+
+
 def test_predecode_layout_and_negative_slots(tris, oracle_mod, cuda):
     note("predecode layout")
     rng = np.random.default_rng(8)
@@ -217,6 +237,32 @@ def test_route_matches_oracle(tris, oracle_mod, cuda, t, k, e):
         np.testing.assert_array_equal(got[key].cpu().numpy(), want[key], err_msg=key)
     assert got["total_problem_tiles_host"] == want["total_problem_tiles"]
     assert int(got["total_problem_tiles"][0]) == want["total_problem_tiles"]
+
+
+@pytest.mark.parametrize("t,k,e", [(1, 2, 8), (16, 2, 8), (16, 8, 64), (7, 8, 256), (256, 8, 128)])
+def test_route_topk_fused_matches_oracle(tris, oracle_mod, cuda, t, k, e):
+    """Fused softmax / top-k / route: the selection and the route are exactly the oracle's
+    (stable argsort of the fp32 softmax), weights within one fp16 ulp."""
+    note(f"route topk fused t={t} k={k} e={e}")
+    rng = np.random.default_rng(t * 100 + e)
+    logits = rng.standard_normal((t, e)).astype(np.float32)
+    if t > 1:
+        logits[1, : min(e, 4)] = 0.25  # exact ties among the top experts
+    w, sel = oracle_mod.route_topk(logits, k, True)
+    r = tris["ext"].route_topk_grouped(torch.from_numpy(logits).to(cuda), k, True, 4)
+    np.testing.assert_array_equal(r["selected_experts"].cpu().numpy(), sel)
+    want = oracle_mod.build_route(sel, e, 4)
+    for key in ("perm", "grouped_token_indices", "grouped_slots"):
+        np.testing.assert_array_equal(r[key].cpu().numpy(), np.asarray(want[key]), err_msg=key)
+    na = len(want["expert_ids"])
+    np.testing.assert_array_equal(r["expert_ids"].cpu().numpy()[:na], np.asarray(want["expert_ids"]))
+    np.testing.assert_array_equal(r["segment_offsets"].cpu().numpy()[: na + 1], np.asarray(want["segment_offsets"]))
+    np.testing.assert_allclose(r["routing_weights"].cpu().numpy(), w, rtol=2e-6, atol=1e-7)
+    got16 = r["routing_weights_f16"].cpu().numpy().view(np.int16).astype(np.int32)
+    want16 = w.astype(np.float16).view(np.int16).astype(np.int32)
+    assert np.abs(got16 - want16).max() <= 1
+    inv = r["inverse_perm"].cpu().numpy()
+    np.testing.assert_array_equal(r["perm"].cpu().numpy()[inv], np.arange(t * k))
 
 
 def test_route_rejects_bad_expert_ids(tris, cuda):
