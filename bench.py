@@ -47,6 +47,10 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--cpu-baseline", type=int, default=1)
+    ap.add_argument("--profile-kernel", action="store_true",
+                    help="only run the dominant kernel eagerly --kernel-reps times (a target for rocprofv3 --pmc)")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="only run a device-to-device copy of this many bytes 5 times (counter calibration)")
     return ap.parse_args()
 
 
@@ -62,6 +66,16 @@ def main():
         sys.exit(2)
     import numpy as np
     import torch
+
+    if args.copy_bytes > 0:
+        dev = torch.device("cuda:0")
+        src = torch.ones(args.copy_bytes // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": int(src.numel() * 4), "launches": 5}))
+        return
 
     import tris_moe_amd
     from tris_moe_amd import ext, moe, qlinear, synthetic
@@ -125,6 +139,9 @@ def main():
                 "hbm_gbps": step_bytes / (ms / 1e3) / 1e9, "step_bytes": step_bytes, "expert_bytes": expert_bytes,
                 "active_experts": len(active), "x16": x16, "logits": logits, "active": active}
 
+    if args.profile_kernel:
+        profile_dominant_kernel(args, layer, base_payloads, base_backbones, SPEC, dev)
+        return
     main_res = measure(args.tokens, args.steps, args.warmup)
     log(f"T={args.tokens}: {main_res['ms_per_step'] * 1e3:.1f} us/step, {main_res['tokens_per_s']:.0f} tok/s, "
         f"{main_res['hbm_gbps']:.0f} GB/s")
@@ -193,7 +210,7 @@ def main():
                   + 2 * rows * SPEC.rank * 2 + rows * SPEC.intermediate * 2)
     achieved = dual_bytes / kernel_s / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(args.tokens),
                 "kernel": "grouped_mfma_kernel<2> (gate/up grouped GEMM + SwiGLU over predecoded bitmaps)",
                 "kernel_us": round(kernel_s * 1e6, 2), "bytes_per_launch": int(dual_bytes)}
     log(f"gate/up SwiGLU GEMM: {kernel_s * 1e6:.1f} us/launch, {achieved:.0f} GB/s algorithmic")
@@ -227,6 +244,53 @@ def main():
         "sweep": sweep,
     }
     print(json.dumps(line), flush=True)
+
+
+def measured_traffic(tokens: int):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    runs (scaled by a copy-kernel calibration), or None when no measurement matches this workload."""
+    path = ROOT / "profiles" / f"grouped_mfma_swiglu_mixtral_decode_T{tokens}_traffic.json"
+    try:
+        return int(json.loads(path.read_text())["traffic_bytes"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def profile_dominant_kernel(args, layer, payloads, backbones, spec, dev):
+    """Eager launches of the dominant kernel at the bench workload, for hardware-counter runs."""
+    import torch
+
+    from tris_moe_amd import ext, synthetic
+
+    inp = synthetic.make_inputs(spec, args.tokens, args.seed + args.tokens, layer["outlier_idx"])
+    x16 = torch.from_numpy(inp["x"]).to(dev).to(torch.bfloat16).to(torch.float16)
+    logits = torch.from_numpy(inp["router_logits"]).to(dev)
+    route = ext.route_topk_grouped(logits, spec.top_k, spec.renormalize, 4)
+    rows = args.tokens * spec.top_k
+    slots = min(spec.num_experts, rows)
+    eid = route["expert_ids"][:slots]
+    seg = route["segment_offsets"][: slots + 1]
+    prob = route["problem_offsets"][: slots + 1]
+    hid_g, hid_u = ext.backbone_linear_pair(x16, backbones["gate"], backbones["up"],
+                                            row_index=route["grouped_token_indices"])
+    nblk = int(layer["gate"]["q_gmap_gr_meta"].shape[1])
+    dec = []
+    for p in ("gate", "up"):
+        buf = torch.empty((slots, nblk, 128), dtype=torch.int32, device=dev)
+        dec.append(ext.compact3_tris_precomputed_grouped_block_gr_predecode(
+            buf, eid, payloads[p]["q_gmap_gr_words"], payloads[p]["q_gmap_gr_offsets"],
+            payloads[p]["q_gmap_gr_meta"], spec.rank // 32, spec.intermediate))
+    names = ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx", "col_pack3", "row_pack3")
+    mlp = torch.empty((rows, spec.intermediate), dtype=torch.float16, device=dev)
+    for _ in range(args.kernel_reps):
+        ext.compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded(
+            hid_g, hid_u, eid, seg, prob, rows // 4 + slots + 1, dec[0], *[payloads["gate"][k] for k in names],
+            dec[1], *[payloads["up"][k] for k in names], out=mlp)
+    torch.cuda.synchronize()
+    active = sorted(set(route["selected_experts"].cpu().numpy().reshape(-1).tolist()))
+    nbytes = (synthetic.predecoded_nbytes(layer["gate"], active) + synthetic.predecoded_nbytes(layer["up"], active)
+              + 2 * rows * spec.rank * 2 + rows * spec.intermediate * 2)
+    print(json.dumps({"kernel": "grouped_mfma_kernel<2>", "launches": args.kernel_reps, "bytes_per_launch": nbytes}))
 
 
 def cpu_baseline(layer, res, spec):

@@ -233,6 +233,24 @@ def test_oracle_route_brute_force(oracle_mod, t, k, e):
     np.testing.assert_array_equal(route["grouped_token_indices"] * k + route["grouped_slots"], route["perm"])
 
 
+@pytest.mark.parametrize("t,k,e,renorm", [(5, 2, 8, True), (9, 8, 64, True), (4, 3, 16, False), (3, 1, 4, True)])
+def test_oracle_route_topk_against_float64(oracle_mod, t, k, e, renorm):
+    """softmax -> top-k -> renormalisation (modeling_mixtral.py:548-551): selection equals a brute-force
+    descending order of the float64 softmax with ties to the lower expert id; weights equal the float64
+    values to fp32 precision."""
+    rng = np.random.default_rng(t * 1000 + k * 10 + e)
+    logits = rng.standard_normal((t, e)).astype(np.float32)
+    logits[0, : min(e, 3)] = 1.5                      # exact ties at the top
+    w, sel = oracle_mod.route_topk(logits, k, renorm)
+    p64 = np.exp(logits.astype(np.float64) - logits.max(axis=1, keepdims=True))
+    p64 /= p64.sum(axis=1, keepdims=True)
+    for i in range(t):
+        order = sorted(range(e), key=lambda j: (-p64[i, j], j))[:k]
+        assert sel[i].tolist() == order
+        want = p64[i, order] / (p64[i, order].sum() if renorm else 1.0)
+        np.testing.assert_allclose(w[i], want, rtol=3e-6)
+
+
 def test_oracle_layer_against_float64(oracle_mod, tris):
     """The oracle layer (fp16 between stages, fp32 accumulation) stays within the layer tolerance of a
     float64 evaluation of the same exact weights."""
