@@ -127,11 +127,33 @@ struct MfmaLds {
   uint32_t* col_sal;                    // C0 | C1 << 16, natural order
   uint16_t* sal_col;                    // chunk column of the chunk's q-th salient column
   uint16_t (*ws)[16][kMfSalStride];    // per-wave salient weights
+  uint32_t (*q1l)[kTileOut];           // qweight1 words of the tile's columns, per chunk packed row
+  uint32_t (*r01)[kTileOut];           // R0 | R1 << 16 of the tile's columns, per chunk 64-column tile
 };
+
+constexpr uint32_t kBufferWord3 = 0x00020000;  // raw buffer resource, gfx9 family
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufferWord3);
+}
+// Raw buffer loads: voffset at or past the buffer size returns 0 without a memory access.
+__device__ __forceinline__ uint32_t bload32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+__device__ __forceinline__ uint64_t bload64(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+  return static_cast<uint64_t>(v[0]) | (static_cast<uint64_t>(v[1]) << 32);
+}
+__device__ __forceinline__ uint4 bload128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
 
 // One projection of one workgroup tile: rows [row0, row0 + rc) of segment s
 // (expert e) x output columns [n0, n0 + 64).  Returns the lane's accumulator:
-// rows 4*kg + v, column n0 + 16*wave + lane % 16.
+// rows 4*kg + v, column n0 + 16*wave + lane % 16.  Per-expert tensors are read
+// through raw buffer resources (uniform base, 32-bit lane offsets; element
+// offsets fit in 32 bits, which the host checks).
 __device__ __forceinline__ f32x4 mfma_project(const MfmaProj& pa, int s, int row0, int rc, int e, int n0,
                                               const MfmaLds& L) {
   const tris_compact3_payload& p = pa.p;
@@ -152,34 +174,44 @@ __device__ __forceinline__ f32x4 mfma_project(const MfmaProj& pa, int s, int row
   const int nblk = nkb * nob;
   const int ob = blockIdx.x;
   const int G = p.num_groups;
-  // Per-expert bases; element offsets below stay within 32 bits (checked on the host).
-  const int32_t* q1_e = p.qweight1 + static_cast<int64_t>(e) * packed_rows * N;
-  const int32_t* q2_e = p.qweight2_sparse + static_cast<int64_t>(e) * p.qweight2_sparse_rows * N;
   const int32_t* q2p_e = p.qweight2_sparse_prefix + static_cast<int64_t>(e) * (packed_rows + 1);
   const int32_t* cmap_e = p.c_map + static_cast<int64_t>(e) * packed_rows;
   const int32_t* gidx_e = p.g_idx + static_cast<int64_t>(e) * rank;
-  const int64_t* col_e = p.col_pack3 + static_cast<int64_t>(e) * rank;
-  const int64_t* row_e = p.row_pack3 + static_cast<int64_t>(e) * N * G;
-  const int32_t* dec_s = pa.decoded + static_cast<int64_t>(s) * nblk * kGrWords;
-  const uint16_t* hid = pa.hidden + static_cast<int64_t>(row0) * rank;
+  const uint32_t q1_bytes = static_cast<uint32_t>(packed_rows) * N * 4u;
+  const uint32_t dec_bytes = static_cast<uint32_t>(nblk) * kGrWords * 4u;
+  const uint32_t row_bytes = static_cast<uint32_t>(N) * G * 8u;
+  const uint32_t q2_bytes = static_cast<uint32_t>(p.qweight2_sparse_rows) * N * 4u;
+  const uint32_t col_bytes = static_cast<uint32_t>(rank) * 8u;
+  const uint32_t hid_bytes = static_cast<uint32_t>(rc) * rank * 2u;
+  const __amdgpu_buffer_rsrc_t r_q1 = make_rsrc(p.qweight1 + static_cast<int64_t>(e) * packed_rows * N, q1_bytes);
+  const __amdgpu_buffer_rsrc_t r_dec = make_rsrc(pa.decoded + static_cast<int64_t>(s) * nblk * kGrWords, dec_bytes);
+  const __amdgpu_buffer_rsrc_t r_row = make_rsrc(p.row_pack3 + static_cast<int64_t>(e) * N * G, row_bytes);
+  const __amdgpu_buffer_rsrc_t r_q2 =
+      make_rsrc(p.qweight2_sparse + static_cast<int64_t>(e) * p.qweight2_sparse_rows * N, q2_bytes);
+  const __amdgpu_buffer_rsrc_t r_col = make_rsrc(p.col_pack3 + static_cast<int64_t>(e) * rank, col_bytes);
+  const __amdgpu_buffer_rsrc_t r_hid = make_rsrc(pa.hidden + static_cast<int64_t>(row0) * rank, hid_bytes);
 
   const int i16 = lane % 16;   // MFMA column within the wave's 16 outputs / A row
   const int kg = lane / 16;    // MFMA k group: columns k = kg (mod 4) of every packed row
-  const int n = n0 + 16 * wave + i16;  // this lane's output column
+  const int tc = 16 * wave + i16;      // column within the tile
+  const int n = n0 + tc;               // this lane's output column
   const bool nv = n < N;
-  const uint32_t nu = nv ? static_cast<uint32_t>(n) : 0u;
+  // lane offsets; an invalid column reads past its buffer, which returns 0
+  const uint32_t v_q1 = nv ? static_cast<uint32_t>(n) * 4u : q1_bytes;
+  const uint32_t v_dec = nv ? static_cast<uint32_t>(tc) * 4u : dec_bytes;
+  const uint32_t v_row = nv ? static_cast<uint32_t>(n) * G * 8u : row_bytes;
+  const uint32_t v_q2 = nv ? static_cast<uint32_t>(n) * 4u : q2_bytes;
   f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   for (int kc = 0; kc < rank; kc += kMfChunk) {
     const int pr0 = kc / 32;
-    const int pr_end = (pr0 + kMfChunk / 32) < packed_rows ? (pr0 + kMfChunk / 32) : packed_rows;
+    const int npr = (packed_rows - pr0) < kMfChunk / 32 ? (packed_rows - pr0) : kMfChunk / 32;  // even
+    const int pr_end = pr0 + npr;
     // ---- batch 1: the chunk's uniform metadata (group of each 64-column tile, salient words and
-    // prefix per packed row).  Later loads use these in their addresses; loading them first means
-    // the one wait for them does not also wait for the weight loads.
-    // Indices are clamped so that every load is issued unconditionally; validity is applied after.
+    // prefix per packed row), then the lane's weights, which do not depend on it.  Indices are
+    // clamped so that every load is issued unconditionally; validity is applied afterwards.
     int gt[kMfChunk / kTileK];
     uint32_t cmw[kMfChunk / 32];
-    int q2p[kMfChunk / 32 + 1];
 #pragma unroll
     for (int t = 0; t < kMfChunk / kTileK; ++t) {
       const int kt = kc + t * kTileK;
@@ -187,47 +219,58 @@ __device__ __forceinline__ f32x4 mfma_project(const MfmaProj& pa, int s, int row
     }
 #pragma unroll
     for (int j = 0; j < kMfChunk / 32; ++j) {
-      cmw[j] = static_cast<uint32_t>(cmap_e[pr0 + j < packed_rows ? pr0 + j : packed_rows - 1]);
-      q2p[j] = q2p_e[pr0 + j < packed_rows ? pr0 + j : packed_rows];
+      cmw[j] = static_cast<uint32_t>(cmap_e[j < npr ? pr0 + j : packed_rows - 1]);
     }
-    q2p[kMfChunk / 32] = q2p_e[pr_end];
+    const int q2_first = q2p_e[pr0];
+    const int q2_end = q2p_e[pr_end];
+    // every load below is issued unconditionally (a branch around a load makes the compiler wait
+    // for it at the join): an invalid row or group gets a lane offset past the buffer, which
+    // reads 0, and an in-range uniform offset
+    uint32_t qw[kMfChunk / 32], gw[kMfChunk / 32];
+#pragma unroll
+    for (int j = 0; j < kMfChunk / 32; ++j) {
+      const bool jv = j < npr;  // uniform
+      const uint32_t pr = static_cast<uint32_t>(jv ? pr0 + j : 0);
+      qw[j] = bload32(r_q1, jv ? v_q1 : q1_bytes, pr * N * 4u);
+      gw[j] = bload32(r_dec, jv ? v_dec : dec_bytes,
+                      ((static_cast<uint32_t>(pr >> 1) * nob + ob) * kGrWords + (pr & 1u) * kTileOut) * 4u);
+    }
 #pragma unroll
     for (int t = 0; t < kMfChunk / kTileK; ++t) {
-      gt[t] = (kc + t * kTileK) < rank ? __builtin_amdgcn_readfirstlane(gt[t]) : -1;
+      // an invalid tile's group is made negative (uses the loaded value on every path, so the
+      // compiler does not move its load behind the weight loads)
+      gt[t] = __builtin_amdgcn_readfirstlane(gt[t] | ((kc + t * kTileK) < rank ? 0 : INT32_MIN));
     }
 #pragma unroll
     for (int j = 0; j < kMfChunk / 32; ++j) {
       const int pr = pr0 + j;
       const int nbits = (rank - pr * 32) < 32 ? (rank - pr * 32) : 32;
-      cmw[j] = pr < packed_rows ? (cmw[j] & low_mask(nbits)) : 0u;
+      // uniform; readfirstlane keeps the load where it was issued
+      cmw[j] = __builtin_amdgcn_readfirstlane(cmw[j]) & (j < npr ? low_mask(nbits) : 0u);
     }
-    // ---- batch 2: the wave's weights (16 packed rows x 1 column per lane) and row scales
-    uint32_t qw[kMfChunk / 32], gw[kMfChunk / 32];
+    // ---- batch 2: row scales of each tile's group
     uint64_t rp[kMfChunk / kTileK];
-#pragma unroll
-    for (int j = 0; j < kMfChunk / 32; ++j) {
-      const int pr = pr0 + j;
-      const bool ok = nv && pr < packed_rows;
-      const uint32_t boff = static_cast<uint32_t>(((pr >> 1) * nob + ob) * kGrWords + (pr & 1) * kTileOut +
-                                                  16 * wave + i16);
-      qw[j] = ok ? static_cast<uint32_t>(q1_e[static_cast<uint32_t>(pr) * static_cast<uint32_t>(N) + nu]) : 0u;
-      gw[j] = ok ? static_cast<uint32_t>(dec_s[boff]) : 0u;
-    }
 #pragma unroll
     for (int t = 0; t < kMfChunk / kTileK; ++t) {
       const int g = gt[t];
-      rp[t] = (nv && g >= 0 && g < G)
-                  ? static_cast<uint64_t>(row_e[nu * static_cast<uint32_t>(G) + static_cast<uint32_t>(g)]) : 0ull;
+      const bool gv = g >= 0 && g < G;
+      rp[t] = bload64(r_row, gv ? v_row : row_bytes, static_cast<uint32_t>(gv ? g : 0) * 8u);
     }
-    const int sbase0 = q2p[0];                        // qweight2_sparse index of the chunk's first salient column
-    const int num_sal = q2p[kMfChunk / 32] - sbase0;  // salient columns in the chunk
-    // first qweight2_sparse row of the chunk's salient columns (usually the only one)
+    const int sbase0 = __builtin_amdgcn_readfirstlane(q2_first);  // qweight2_sparse index of the first salient column
+    const int num_sal = __builtin_amdgcn_readfirstlane(q2_end) - sbase0;  // salient columns in the chunk
+    // the first two qweight2_sparse rows of the chunk's salient columns (one window of salient
+    // columns spans at most three)
+    const int q2rows = p.qweight2_sparse_rows;
     const int q2row0 = sbase0 >> 5;
-    const uint32_t q2w0 = (nv && num_sal > 0 && q2row0 < p.qweight2_sparse_rows)
-        ? static_cast<uint32_t>(q2_e[static_cast<uint32_t>(q2row0) * static_cast<uint32_t>(N) + nu]) : 0u;
-    // staging loads, issued with the weight loads: activation runs (row idx / 64, 8-column run
-    // idx % 64; rank is a multiple of 64, so a run is wholly inside or outside the matrix) and,
-    // for columns kc + tid and kc + tid + 256, the column factors, salient word and prefix
+    uint32_t q2w01[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const bool rv = num_sal > 32 * h && q2row0 + h < q2rows;
+      q2w01[h] = bload32(r_q2, rv ? v_q2 : q2_bytes, static_cast<uint32_t>(rv ? q2row0 + h : 0) * N * 4u);
+    }
+    // staging loads: activation runs (row idx / 64, 8-column run idx % 64; rank is a multiple
+    // of 64, so a run is wholly inside or outside the matrix; rows >= rc read past the buffer)
+    // and, for columns kc + tid and kc + tid + 256, the column factors, salient word and prefix
     constexpr int kRuns = kMfRows * (kMfChunk / 8) / kMfThreads;
     uint4 xv[kRuns];
 #pragma unroll
@@ -235,8 +278,8 @@ __device__ __forceinline__ f32x4 mfma_project(const MfmaProj& pa, int s, int row
       const int idx = tid + h * kMfThreads;
       const int r = idx / (kMfChunk / 8);
       const int c = (idx % (kMfChunk / 8)) * 8;
-      xv[h] = (r < rc && kc + c < rank) ? *reinterpret_cast<const uint4*>(hid + static_cast<uint32_t>(r * rank + kc + c))
-                                        : make_uint4(0u, 0u, 0u, 0u);
+      const uint32_t voff = (kc + c < rank) ? static_cast<uint32_t>(r * rank + kc + c) * 2u : hid_bytes;
+      xv[h] = bload128(r_hid, voff, 0u);
     }
     uint64_t cpv[2];
     uint32_t cmt[2];
@@ -246,9 +289,9 @@ __device__ __forceinline__ f32x4 mfma_project(const MfmaProj& pa, int s, int row
       const int k = kc + tid + h * kMfThreads;
       const bool kv = k < rank;
       const int pr = kv ? (k >> 5) : 0;
-      cpv[h] = kv ? static_cast<uint64_t>(col_e[k]) : 0ull;
-      cmt[h] = kv ? static_cast<uint32_t>(cmap_e[pr]) : 0u;
-      q2t[h] = kv ? q2p_e[pr] : 0;
+      cpv[h] = bload64(r_col, kv ? static_cast<uint32_t>(k) * 8u : col_bytes, 0u);
+      cmt[h] = static_cast<uint32_t>(cmap_e[pr]);
+      q2t[h] = q2p_e[pr];
     }
     __syncthreads();  // previous chunk's LDS readers are done
 #pragma unroll
@@ -282,13 +325,19 @@ __device__ __forceinline__ f32x4 mfma_project(const MfmaProj& pa, int s, int row
         if ((cm >> bit) & 1u) sal_col[q2t[h] - sbase0 + __popc(cm & ((1u << bit) - 1u))] = static_cast<uint16_t>(j);
       }
     }
+    // the lane's sign words and R0 | R1, for the salient pass (lane group kg writes every 4th)
+    if (num_sal > 0) {
+#pragma unroll
+      for (int j = 0; j < kMfChunk / 32; j += 4) L.q1l[j + kg][tc] = qw[j + kg];
+#pragma unroll
+      for (int t = 0; t < kMfChunk / kTileK; t += 4) L.r01[t + kg][tc] = static_cast<uint32_t>(rp[t + kg]);
+    }
     __syncthreads();
 
     // ---- MFMA over the chunk's packed rows (salient columns are zero here)
 #pragma unroll
     for (int j = 0; j < kMfChunk / 32; ++j) {
-      const int pr = pr0 + j;
-      if (pr < packed_rows) {
+      if (j < npr) {
         const int t = j / 2;
         const uint32_t d = static_cast<uint32_t>(rp[t] >> 32) & 0xFFFFu;
         const uint32_t nd = static_cast<uint32_t>(rp[t] >> 48);
@@ -319,45 +368,35 @@ __device__ __forceinline__ f32x4 mfma_project(const MfmaProj& pa, int s, int row
       }
     }
 
-    // ---- salient columns, kMfSalWin at a time: each lane writes the exact fp16 weights of its
-    // output column for the salient columns k = kg (mod 4) into ws, then the wave multiplies
-    // the gathered activations by ws on MFMA.
+    // ---- salient columns, kMfSalWin at a time.  Lane group kg writes the exact fp16 weights of
+    // its column for window slots kg, kg + 4, ... into ws (sign word and R0 | R1 from LDS), then
+    // the wave multiplies the activations gathered at those columns by ws on MFMA.
     for (int w0 = 0; w0 < num_sal; w0 += kMfSalWin) {
+      const int wn = (num_sal - w0) < kMfSalWin ? (num_sal - w0) : kMfSalWin;
 #pragma unroll
-      for (int q = kg * (kMfSalWin / 4); q < (kg + 1) * (kMfSalWin / 4); ++q) ws[wave][i16][q] = 0;
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int j = 0; j < kMfChunk / 32; ++j) {
-        const int pr = pr0 + j;
-        if (pr < packed_rows) {
-          const int t = j / 2;
-          uint32_t m = cmw[j] & (0x11111111u << kg);
-          const int sbase = q2p[j];
-          while (m != 0u) {
-            const int bit = __builtin_ctz(m);
-            m &= m - 1u;
-            const int sidx = sbase + __popc(cmw[j] & ((1u << bit) - 1u));  // qweight2_sparse index
-            const int q = sidx - sbase0 - w0;                            // slot in the window
-            if (q >= 0 && q < kMfSalWin) {
-              uint32_t q2w = q2w0;
-              if ((sidx >> 5) != q2row0) {
-                q2w = nv ? static_cast<uint32_t>(
-                               q2_e[static_cast<uint32_t>(sidx >> 5) * static_cast<uint32_t>(N) + nu]) : 0u;
-              }
-              const uint32_t cp = col_sal[j * 32 + bit];
-              uint16_t t1 = hmul_bits(static_cast<uint16_t>(cp), static_cast<uint16_t>(rp[t]));
-              if (!((qw[j] >> bit) & 1u)) t1 ^= 0x8000u;
-              uint16_t t2 = hmul_bits(static_cast<uint16_t>(cp >> 16), static_cast<uint16_t>(rp[t] >> 16));
-              if (!((q2w >> (sidx & 31)) & 1u)) t2 ^= 0x8000u;
-              ws[wave][i16][q] = hadd_bits(t1, t2);
-            }
-          }
+      for (int i = 0; i < kMfSalWin / 4; ++i) {
+        const int q = 4 * i + kg;
+        uint16_t w = 0;
+        if (q < wn) {
+          const int c = sal_col[w0 + q];  // chunk column
+          const int bit = c & 31;
+          const uint32_t w1 = L.q1l[c >> 5][tc];
+          const uint32_t rr = L.r01[c >> 6][tc];
+          const uint32_t cp = col_sal[c];
+          const int sidx = sbase0 + w0 + q;  // qweight2_sparse index
+          const int q2r = (sidx >> 5) - q2row0;
+          uint32_t q2w = q2r == 0 ? q2w01[0] : q2w01[1];
+          if (q2r > 1) q2w = bload32(r_q2, v_q2, static_cast<uint32_t>(sidx >> 5) * N * 4u);
+          uint16_t t1 = hmul_bits(static_cast<uint16_t>(cp), static_cast<uint16_t>(rr));
+          if (!((w1 >> bit) & 1u)) t1 ^= 0x8000u;
+          uint16_t t2 = hmul_bits(static_cast<uint16_t>(cp >> 16), static_cast<uint16_t>(rr >> 16));
+          if (!((q2w >> (sidx & 31)) & 1u)) t2 ^= 0x8000u;
+          w = hadd_bits(t1, t2);
         }
+        ws[wave][i16][q] = w;
       }
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
       __builtin_amdgcn_wave_barrier();
-      const int wn = (num_sal - w0) < kMfSalWin ? (num_sal - w0) : kMfSalWin;
 #pragma unroll
       for (int blk = 0; blk < kMfSalWin; blk += 32) {
         if (blk < wn) {
@@ -385,7 +424,6 @@ __device__ __forceinline__ f32x4 mfma_project(const MfmaProj& pa, int s, int row
       __builtin_amdgcn_wave_barrier();
     }
   }
-
   return acc;
 }
 
@@ -399,7 +437,9 @@ __global__ __launch_bounds__(kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
   __shared__ uint32_t col_sal[kMfChunk];
   __shared__ uint16_t sal_col[kMfChunk];
   __shared__ __attribute__((aligned(16))) uint16_t ws[kMfWaves][16][kMfSalStride];
-  const MfmaLds L{xs, cds, cns, col_sal, sal_col, ws};
+  __shared__ uint32_t q1l[kMfChunk / 32][kTileOut];
+  __shared__ uint32_t r01[kMfChunk / kTileK][kTileOut];
+  const MfmaLds L{xs, cds, cns, col_sal, sal_col, ws, q1l, r01};
 
   const MfmaProj& pa = a.proj[kMode == 1 ? blockIdx.z : 0];
   const tris_compact3_payload& p = pa.p;
@@ -505,8 +545,17 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
 // a 64-column K tile has one row scale) and a rank that is a whole number of
 // 64-column tiles, with 16-byte aligned activations (8-column loads).
 bool grouped_mfma_supported(const tris_compact3_payload* p, const uint16_t* hidden) {
-  return p != nullptr && p->use_uniform_k64_groups && p->rank > 0 && p->rank % kTileK == 0 &&
-         reinterpret_cast<uintptr_t>(hidden) % 16 == 0;
+  if (p == nullptr || !p->use_uniform_k64_groups || p->rank <= 0 || p->rank % kTileK != 0 ||
+      reinterpret_cast<uintptr_t>(hidden) % 16 != 0) {
+    return false;
+  }
+  // the kernel addresses each expert's tensors with 32-bit buffer offsets
+  const int64_t limit = int64_t{1} << 31;
+  const int64_t packed_rows = (p->rank + 31) / 32;
+  const int64_t n = p->outfeatures;
+  return packed_rows * n * 4 < limit && int64_t{p->qweight2_sparse_rows} * n * 4 < limit &&
+         n * p->num_groups * 8 < limit && int64_t{kMfRows} * p->rank * 2 < limit &&
+         ((packed_rows + 1) / 2) * ((n + kTileOut - 1) / kTileOut) * kGrWords * 4 < limit;
 }
 
 }  // namespace tris
