@@ -48,7 +48,7 @@ constexpr int kMfThreads = kMfWaves * kWave;
 constexpr int kMfRows = 16;         // segment rows per workgroup tile
 constexpr int kMfChunk = 512;       // K columns staged per pass
 constexpr int kMfXStride = kMfChunk + 8;  // fp16 elements per staged row (pad breaks bank aliasing)
-constexpr int kMfSalWin = 64;             // salient columns per MFMA pass
+constexpr int kMfSalWin = 32;             // salient columns per MFMA pass
 constexpr int kMfSalStride = kMfSalWin + 8;
 
 struct MfmaProj {
@@ -63,6 +63,8 @@ struct MfmaArgs {
   const int32_t* expert_ids;
   const int32_t* segment_offsets;
   int num_segments;
+  int xs_rows;       // activation rows staged per tile: min(16, batch)
+  int lds_groups;    // row-scale groups the LDS layout is sized for (max over the projections)
 };
 
 // Position of column k (0..31) of a packed row in the staged order: lane group
@@ -82,16 +84,22 @@ __device__ __forceinline__ f16x2 fp4x2_to_f16x2(uint32_t nib, int byte_sel) {
 __device__ __forceinline__ f16x2 u32_as_f16x2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
 __device__ __forceinline__ uint32_t f16x2_as_u32(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
 
-// Same mapping as the in-kernel-decode GEMM (tris_grouped.hip).
-__device__ inline bool mf_map_row_tile(const int32_t* __restrict__ seg, int nseg, int tile, int row_tile, int* s_out,
-                                       int* row0_out, int* rc_out) {
+// Same mapping as the in-kernel-decode GEMM (tris_grouped.hip), plus the segment's expert id, loaded
+// in the same round trip as the segment lengths.
+__device__ inline bool mf_map_row_tile(const int32_t* __restrict__ seg, const int32_t* __restrict__ expert_ids,
+                                       int nseg, int tile, int row_tile, int* s_out, int* row0_out, int* rc_out,
+                                       int* e_out) {
   const int lane = static_cast<int>(__lane_id());
   int base = 0;
   for (int c = 0; c < nseg; c += kWave) {
     const int i = c + lane;
+    const int ic = i < nseg ? i : nseg - 1;
+    const int lo = seg[ic];
+    const int hi = seg[ic + 1];
+    const int ex = expert_ids[ic];
     int t = 0;
     if (i < nseg) {
-      const int len = seg[i + 1] - seg[i];
+      const int len = hi - lo;
       t = len > 0 ? (len + row_tile - 1) / row_tile : 0;
     }
     int incl = t;
@@ -105,13 +113,13 @@ __device__ inline bool mf_map_row_tile(const int32_t* __restrict__ seg, int nseg
       const uint64_t hit = __ballot(i < nseg && tile < base + incl);
       const int L = __ffsll(static_cast<unsigned long long>(hit)) - 1;
       const int excl = __shfl(incl - t, L);
-      const int s = c + L;
       const int local = tile - base - excl;
-      const int row0 = seg[s] + local * row_tile;
-      const int end = seg[s + 1];
-      *s_out = s;
+      const int row0 = __shfl(lo, L) + local * row_tile;
+      const int end = __shfl(hi, L);
+      *s_out = c + L;
       *row0_out = row0;
       *rc_out = (end - row0) < row_tile ? (end - row0) : row_tile;
+      *e_out = __shfl(ex, L);
       return true;
     }
     base += total;
@@ -119,16 +127,131 @@ __device__ inline bool mf_map_row_tile(const int32_t* __restrict__ seg, int nseg
   return false;
 }
 
-// LDS of one workgroup, shared by the projections it computes one after the other.
-struct MfmaLds {
-  uint16_t (*xs)[kMfXStride];          // activations, staged order
-  uint16_t* cds;                        // C_d, staged order
-  uint16_t* cns;                        // C_nd, staged order
-  uint32_t* col_sal;                    // C0 | C1 << 16, natural order
-  uint16_t* sal_col;                    // chunk column of the chunk's q-th salient column
-  uint16_t (*ws)[16][kMfSalStride];    // per-wave salient weights
-  uint32_t (*q1l)[kTileOut];           // qweight1 words of the tile's columns, per chunk packed row
-  uint32_t (*r01)[kTileOut];           // R0 | R1 << 16 of the tile's columns, per chunk 64-column tile
+// Row tiles of the segments (tiles of <= row_tile rows), scanned once: with at most 64 segments the
+// scan stays in registers and mapping a row tile costs no memory access.
+struct MfSegScan {
+  int lo, hi, ex;  // this lane's segment (lane < nseg): row range and expert id
+  int t, incl;     // its row tiles, inclusive prefix over lanes
+  int total;       // row tiles of all segments (the same in every lane)
+};
+
+__device__ inline MfSegScan mf_scan_segments(const int32_t* __restrict__ seg, const int32_t* __restrict__ expert_ids,
+                                             int nseg, int row_tile) {
+  const int lane = static_cast<int>(__lane_id());
+  MfSegScan r;
+  r.total = 0;
+  for (int c = 0; c < nseg; c += kWave) {
+    const int i = c + lane;
+    const int ic = i < nseg ? i : nseg - 1;
+    const int lo = seg[ic];
+    const int hi = seg[ic + 1];
+    const int ex = expert_ids[ic];
+    int t = 0;
+    if (i < nseg) t = hi > lo ? (hi - lo + row_tile - 1) / row_tile : 0;
+    int incl = t;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int v = __shfl_up(incl, d);
+      if (lane >= d) incl += v;
+    }
+    if (c == 0) {
+      r.lo = lo;
+      r.hi = hi;
+      r.ex = ex;
+      r.t = t;
+      r.incl = incl;
+    }
+    r.total += __shfl(incl, kWave - 1);
+  }
+  return r;
+}
+
+// Row tile `tile` (< sc.total) -> segment, first row, row count and expert id.
+__device__ inline void mf_map_scanned(const MfSegScan& sc, const int32_t* __restrict__ seg,
+                                      const int32_t* __restrict__ expert_ids, int nseg, int tile, int row_tile,
+                                      int* s_out, int* row0_out, int* rc_out, int* e_out) {
+  if (nseg <= kWave) {
+    const int lane = static_cast<int>(__lane_id());
+    const uint64_t hit = __ballot(lane < nseg && tile < sc.incl);
+    const int L = __ffsll(static_cast<unsigned long long>(hit)) - 1;
+    const int local = tile - __shfl(sc.incl - sc.t, L);
+    const int row0 = __shfl(sc.lo, L) + local * row_tile;
+    const int end = __shfl(sc.hi, L);
+    *s_out = L;
+    *row0_out = row0;
+    *rc_out = (end - row0) < row_tile ? (end - row0) : row_tile;
+    *e_out = __shfl(sc.ex, L);
+    return;
+  }
+  mf_map_row_tile(seg, expert_ids, nseg, tile, row_tile, s_out, row0_out, rc_out, e_out);
+}
+
+constexpr int kMfPR = kMfChunk / 32;         // packed rows per chunk
+constexpr int kMfTiles = kMfChunk / kTileK;  // 64-column K tiles per chunk
+constexpr int kMfQ1Stride = kTileOut + 1;    // words per staged qweight1 row (odd, so per-lane row reads spread over banks)
+constexpr int kMfMaxGroups = 8;              // the 64 columns x G row-scale block is staged whole
+// One output tile's weight words in LDS: qweight1 [kMfPR][kMfQ1Stride], split words [kMfPR][64],
+// row_pack3 [64][kMfMaxGroups][2] (32-bit words; every piece 16-byte aligned).
+constexpr int kMfTbQ1 = 0;
+constexpr int kMfTbGw = kMfPR * kMfQ1Stride;
+constexpr int kMfTbRs = kMfTbGw + kMfPR * kTileOut;
+constexpr int kMfTbWords = kMfTbRs + kTileOut * kMfMaxGroups * 2;
+static_assert(kMfTbGw % 4 == 0 && kMfTbRs % 4 == 0, "tile buffer pieces must be 16-byte aligned");
+constexpr int kMfCus = 256;  // MI355X compute units
+constexpr int kMfRuns = kMfRows * (kMfChunk / 8) / kMfThreads;  // activation runs per thread of a unit
+
+// Dynamic LDS of one unit (4 wavefronts computing one projection): the chunk's activations and column
+// data (shared by every output tile the workgroup walks), the salient row-scale table and the salient
+// weight table.  Byte offsets, 16-byte aligned pieces.  The per-tile weight words live in two static
+// arrays (double buffering): the copies of the next tile into one overlap the compute from the other,
+// and being distinct objects lets the compiler see that the compute's LDS reads do not wait for them.
+struct MfUnitLayout {
+  int xs, cds, cns, col_sal, sal_col, meta;  // chunk
+  int r01t, ws, bytes;
+};
+
+__host__ __device__ inline int mf_take(int* o, int b) {
+  const int at = *o;
+  *o += (b + 15) & ~15;
+  return at;
+}
+
+__host__ __device__ inline MfUnitLayout mf_unit_layout(int rows, int groups) {
+  MfUnitLayout L;
+  int o = 0;
+  L.xs = mf_take(&o, rows * kMfXStride * 2);
+  L.cds = mf_take(&o, kMfChunk * 2);
+  L.cns = mf_take(&o, kMfChunk * 2);
+  L.col_sal = mf_take(&o, kMfChunk * 4);
+  L.sal_col = mf_take(&o, kMfChunk * 2);
+  L.meta = mf_take(&o, 16 * 4);
+  (void)groups;
+  L.r01t = mf_take(&o, kMfTiles * kTileOut * 4);
+  L.ws = mf_take(&o, kMfWaves * 16 * kMfSalStride * 2);
+  L.bytes = o;
+  return L;
+}
+
+constexpr int kMfExchBytes = kMfThreads * 4 * 4;  // SwiGLU: the up unit's accumulators for the gate unit
+
+// Dynamic LDS of a workgroup with `units` units, and its static (tile buffer) LDS.
+__host__ __device__ inline int mf_lds_bytes(int units, int rows, int groups) {
+  return units * mf_unit_layout(rows, groups).bytes + (units == 2 ? kMfExchBytes : 0);
+}
+constexpr int mf_static_lds_bytes(int units) { return units * 2 * kMfTbWords * 4; }
+
+struct MfChunk {       // a unit's staged chunk
+  uint16_t* xs;        // [rows][kMfXStride] activations, staged column order
+  uint16_t* cds;       // C_d, staged column order (0 for salient columns)
+  uint16_t* cns;       // C_nd, staged column order (0 for salient columns)
+  uint32_t* col_sal;   // C0 | C1 << 16, natural order
+  uint16_t* sal_col;   // chunk column of the chunk's q-th salient column
+  int32_t* meta;       // [t < 8] group of K tile t (-1: none); [8] first salient index; [9] end
+};
+struct MfTileBuf {     // one output tile's weight words
+  uint32_t* q1;        // [kMfPR][kMfQ1Stride] qweight1 words of the tile's 64 columns
+  uint32_t* gw;        // [kMfPR][64] predecoded split words
+  uint32_t* rs;        // [64][G][2] row_pack3: R0 | R1 << 16, R_d | R_nd << 16
 };
 
 constexpr uint32_t kBufferWord3 = 0x00020000;  // raw buffer resource, gfx9 family
@@ -148,353 +271,521 @@ __device__ __forceinline__ uint4 bload128(__amdgpu_buffer_rsrc_t r, uint32_t vof
   const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
+// Buffer loads straight into LDS: lane l's 4 (16) bytes land at dst + 4l (16l); dst is wave-uniform.
+__device__ __forceinline__ void dma32(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 4, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma128(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
+}
 
-// One projection of one workgroup tile: rows [row0, row0 + rc) of segment s
-// (expert e) x output columns [n0, n0 + 64).  Returns the lane's accumulator:
-// rows 4*kg + v, column n0 + 16*wave + lane % 16.  Per-expert tensors are read
-// through raw buffer resources (uniform base, 32-bit lane offsets; element
-// offsets fit in 32 bits, which the host checks).
-__device__ __forceinline__ f32x4 mfma_project(const MfmaProj& pa, int s, int row0, int rc, int e, int n0,
-                                              const MfmaLds& L) {
+// Register-staged loads of a unit's chunk, held between issue and write.
+struct MfRegs {
+  uint4 xv[kMfRuns];  // activation runs: row 4h + wave, 8 columns at lane * 8
+  uint64_t cpv[2];    // col_pack3 of columns kc + utid, kc + utid + 256
+  uint32_t cmt[2];    // their salient words
+  int q2t[2];         // their packed rows' salient prefix
+  int sbase0;         // salient prefix at the chunk's first packed row
+  int32_t mv;         // metadata word (see mf_chunk_issue)
+};
+
+// Issue the register loads of chunk [kc, kc + 512) of one projection for rows [row0, row0 + rc) of
+// expert e.  utid is the thread's index within its unit.  Every load is issued unconditionally (a
+// branch around a load makes the compiler wait for it at the join); invalid lanes get an offset past
+// their buffer, which reads 0.
+__device__ __forceinline__ void mf_chunk_issue(const MfmaProj& pa, int e, int row0, int rc, int kc, int utid,
+                                               MfRegs& R) {
   const tris_compact3_payload& p = pa.p;
-  const int N = p.outfeatures;
-  const int tid = threadIdx.x;
-  const int wave = tid / kWave;
-  const int lane = tid % kWave;
-  uint16_t (*xs)[kMfXStride] = L.xs;
-  uint16_t* cds = L.cds;
-  uint16_t* cns = L.cns;
-  uint32_t* col_sal = L.col_sal;
-  uint16_t* sal_col = L.sal_col;
-  uint16_t (*ws)[16][kMfSalStride] = L.ws;
   const int rank = p.rank;
-  const int packed_rows = ceil_div(rank, 32);
-  const int nkb = ceil_div(packed_rows, kGrPackedRows);
-  const int nob = ceil_div(N, kTileOut);
-  const int nblk = nkb * nob;
-  const int ob = blockIdx.x;
-  const int G = p.num_groups;
-  const int32_t* q2p_e = p.qweight2_sparse_prefix + static_cast<int64_t>(e) * (packed_rows + 1);
-  const int32_t* cmap_e = p.c_map + static_cast<int64_t>(e) * packed_rows;
-  const int32_t* gidx_e = p.g_idx + static_cast<int64_t>(e) * rank;
-  const uint32_t q1_bytes = static_cast<uint32_t>(packed_rows) * N * 4u;
-  const uint32_t dec_bytes = static_cast<uint32_t>(nblk) * kGrWords * 4u;
-  const uint32_t row_bytes = static_cast<uint32_t>(N) * G * 8u;
-  const uint32_t q2_bytes = static_cast<uint32_t>(p.qweight2_sparse_rows) * N * 4u;
-  const uint32_t col_bytes = static_cast<uint32_t>(rank) * 8u;
+  const int wave = __builtin_amdgcn_readfirstlane(utid / kWave);  // wave-uniform
+  const int lane = utid % kWave;
+  const int packed_rows = rank / 32;  // rank % 64 == 0
+  const int pr0 = kc / 32;
+  const int npr = (packed_rows - pr0) < kMfPR ? (packed_rows - pr0) : kMfPR;
   const uint32_t hid_bytes = static_cast<uint32_t>(rc) * rank * 2u;
-  const __amdgpu_buffer_rsrc_t r_q1 = make_rsrc(p.qweight1 + static_cast<int64_t>(e) * packed_rows * N, q1_bytes);
-  const __amdgpu_buffer_rsrc_t r_dec = make_rsrc(pa.decoded + static_cast<int64_t>(s) * nblk * kGrWords, dec_bytes);
-  const __amdgpu_buffer_rsrc_t r_row = make_rsrc(p.row_pack3 + static_cast<int64_t>(e) * N * G, row_bytes);
-  const __amdgpu_buffer_rsrc_t r_q2 =
-      make_rsrc(p.qweight2_sparse + static_cast<int64_t>(e) * p.qweight2_sparse_rows * N, q2_bytes);
-  const __amdgpu_buffer_rsrc_t r_col = make_rsrc(p.col_pack3 + static_cast<int64_t>(e) * rank, col_bytes);
+  const uint32_t col_bytes = static_cast<uint32_t>(rank) * 8u;
   const __amdgpu_buffer_rsrc_t r_hid = make_rsrc(pa.hidden + static_cast<int64_t>(row0) * rank, hid_bytes);
+  const __amdgpu_buffer_rsrc_t r_col = make_rsrc(p.col_pack3 + static_cast<int64_t>(e) * rank, col_bytes);
+  const int32_t* cmap_e = p.c_map + static_cast<int64_t>(e) * packed_rows;
+  const int32_t* q2p_e = p.qweight2_sparse_prefix + static_cast<int64_t>(e) * (packed_rows + 1);
+  const int32_t* gidx_e = p.g_idx + static_cast<int64_t>(e) * rank;
+#pragma unroll
+  for (int h = 0; h < kMfRuns; ++h) {
+    const int r = 4 * h + wave;
+    const int c = lane * 8;
+    const uint32_t voff = (r < rc && kc + c < rank) ? static_cast<uint32_t>(r * rank + kc + c) * 2u : hid_bytes;
+    R.xv[h] = bload128(r_hid, voff, 0u);
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int k = kc + utid + h * kMfThreads;
+    const bool kv = k < rank;
+    const int pr = kv ? (k >> 5) : 0;
+    R.cpv[h] = bload64(r_col, kv ? static_cast<uint32_t>(k) * 8u : col_bytes, 0u);
+    R.cmt[h] = static_cast<uint32_t>(cmap_e[pr]);
+    R.q2t[h] = q2p_e[pr];
+  }
+  R.sbase0 = q2p_e[pr0];
+  // metadata: utid 64..71 -> group of K tile utid - 64; 72 / 73 -> salient prefix at the chunk's
+  // start / end
+  const int32_t* mp = q2p_e + pr0;
+  if (utid >= 64 && utid < 72) {
+    const int kt = kc + (utid - 64) * kTileK;
+    mp = gidx_e + (kt < rank ? kt : rank - 1);
+  } else if (utid == 73) {
+    mp = q2p_e + pr0 + npr;
+  }
+  R.mv = *mp;
+}
 
-  const int i16 = lane % 16;   // MFMA column within the wave's 16 outputs / A row
-  const int kg = lane / 16;    // MFMA k group: columns k = kg (mod 4) of every packed row
-  const int tc = 16 * wave + i16;      // column within the tile
-  const int n = n0 + tc;               // this lane's output column
-  const bool nv = n < N;
-  // lane offsets; an invalid column reads past its buffer, which returns 0
-  const uint32_t v_q1 = nv ? static_cast<uint32_t>(n) * 4u : q1_bytes;
-  const uint32_t v_dec = nv ? static_cast<uint32_t>(tc) * 4u : dec_bytes;
-  const uint32_t v_row = nv ? static_cast<uint32_t>(n) * G * 8u : row_bytes;
-  const uint32_t v_q2 = nv ? static_cast<uint32_t>(n) * 4u : q2_bytes;
-  f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-  for (int kc = 0; kc < rank; kc += kMfChunk) {
-    const int pr0 = kc / 32;
-    const int npr = (packed_rows - pr0) < kMfChunk / 32 ? (packed_rows - pr0) : kMfChunk / 32;  // even
-    const int pr_end = pr0 + npr;
-    // ---- batch 1: the chunk's uniform metadata (group of each 64-column tile, salient words and
-    // prefix per packed row), then the lane's weights, which do not depend on it.  Indices are
-    // clamped so that every load is issued unconditionally; validity is applied afterwards.
-    int gt[kMfChunk / kTileK];
-    uint32_t cmw[kMfChunk / 32];
+// Write a unit's register-staged chunk to LDS (waits for those loads).  Salient columns get zero
+// C_d / C_nd, so the main pass gives them zero weights whatever their selector bits.
+__device__ __forceinline__ void mf_chunk_write(const MfmaProj& pa, int rc, int kc, int utid, const MfChunk& ch,
+                                               const MfRegs& R) {
+  const tris_compact3_payload& p = pa.p;
+  const int rank = p.rank;
+  const int G = p.num_groups;
+  const int wave = __builtin_amdgcn_readfirstlane(utid / kWave);  // wave-uniform
+  const int lane = utid % kWave;
 #pragma unroll
-    for (int t = 0; t < kMfChunk / kTileK; ++t) {
-      const int kt = kc + t * kTileK;
-      gt[t] = gidx_e[kt < rank ? kt : rank - 1];
-    }
-#pragma unroll
-    for (int j = 0; j < kMfChunk / 32; ++j) {
-      cmw[j] = static_cast<uint32_t>(cmap_e[j < npr ? pr0 + j : packed_rows - 1]);
-    }
-    const int q2_first = q2p_e[pr0];
-    const int q2_end = q2p_e[pr_end];
-    // every load below is issued unconditionally (a branch around a load makes the compiler wait
-    // for it at the join): an invalid row or group gets a lane offset past the buffer, which
-    // reads 0, and an in-range uniform offset
-    uint32_t qw[kMfChunk / 32], gw[kMfChunk / 32];
-#pragma unroll
-    for (int j = 0; j < kMfChunk / 32; ++j) {
-      const bool jv = j < npr;  // uniform
-      const uint32_t pr = static_cast<uint32_t>(jv ? pr0 + j : 0);
-      qw[j] = bload32(r_q1, jv ? v_q1 : q1_bytes, pr * N * 4u);
-      gw[j] = bload32(r_dec, jv ? v_dec : dec_bytes,
-                      ((static_cast<uint32_t>(pr >> 1) * nob + ob) * kGrWords + (pr & 1u) * kTileOut) * 4u);
-    }
-#pragma unroll
-    for (int t = 0; t < kMfChunk / kTileK; ++t) {
-      // an invalid tile's group is made negative (uses the loaded value on every path, so the
-      // compiler does not move its load behind the weight loads)
-      gt[t] = __builtin_amdgcn_readfirstlane(gt[t] | ((kc + t * kTileK) < rank ? 0 : INT32_MIN));
-    }
-#pragma unroll
-    for (int j = 0; j < kMfChunk / 32; ++j) {
-      const int pr = pr0 + j;
-      const int nbits = (rank - pr * 32) < 32 ? (rank - pr * 32) : 32;
-      // uniform; readfirstlane keeps the load where it was issued
-      cmw[j] = __builtin_amdgcn_readfirstlane(cmw[j]) & (j < npr ? low_mask(nbits) : 0u);
-    }
-    // ---- batch 2: row scales of each tile's group
-    uint64_t rp[kMfChunk / kTileK];
-#pragma unroll
-    for (int t = 0; t < kMfChunk / kTileK; ++t) {
-      const int g = gt[t];
-      const bool gv = g >= 0 && g < G;
-      rp[t] = bload64(r_row, gv ? v_row : row_bytes, static_cast<uint32_t>(gv ? g : 0) * 8u);
-    }
-    const int sbase0 = __builtin_amdgcn_readfirstlane(q2_first);  // qweight2_sparse index of the first salient column
-    const int num_sal = __builtin_amdgcn_readfirstlane(q2_end) - sbase0;  // salient columns in the chunk
-    // the first two qweight2_sparse rows of the chunk's salient columns (one window of salient
-    // columns spans at most three)
-    const int q2rows = p.qweight2_sparse_rows;
-    const int q2row0 = sbase0 >> 5;
-    uint32_t q2w01[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const bool rv = num_sal > 32 * h && q2row0 + h < q2rows;
-      q2w01[h] = bload32(r_q2, rv ? v_q2 : q2_bytes, static_cast<uint32_t>(rv ? q2row0 + h : 0) * N * 4u);
-    }
-    // staging loads: activation runs (row idx / 64, 8-column run idx % 64; rank is a multiple
-    // of 64, so a run is wholly inside or outside the matrix; rows >= rc read past the buffer)
-    // and, for columns kc + tid and kc + tid + 256, the column factors, salient word and prefix
-    constexpr int kRuns = kMfRows * (kMfChunk / 8) / kMfThreads;
-    uint4 xv[kRuns];
-#pragma unroll
-    for (int h = 0; h < kRuns; ++h) {
-      const int idx = tid + h * kMfThreads;
-      const int r = idx / (kMfChunk / 8);
-      const int c = (idx % (kMfChunk / 8)) * 8;
-      const uint32_t voff = (kc + c < rank) ? static_cast<uint32_t>(r * rank + kc + c) * 2u : hid_bytes;
-      xv[h] = bload128(r_hid, voff, 0u);
-    }
-    uint64_t cpv[2];
-    uint32_t cmt[2];
-    int q2t[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int k = kc + tid + h * kMfThreads;
-      const bool kv = k < rank;
-      const int pr = kv ? (k >> 5) : 0;
-      cpv[h] = bload64(r_col, kv ? static_cast<uint32_t>(k) * 8u : col_bytes, 0u);
-      cmt[h] = static_cast<uint32_t>(cmap_e[pr]);
-      q2t[h] = q2p_e[pr];
-    }
-    __syncthreads();  // previous chunk's LDS readers are done
-#pragma unroll
-    for (int h = 0; h < kRuns; ++h) {
-      const int idx = tid + h * kMfThreads;
-      const int r = idx / (kMfChunk / 8);
-      const int c = (idx % (kMfChunk / 8)) * 8;  // run start within the chunk (a multiple of 8)
+  for (int h = 0; h < kMfRuns; ++h) {
+    const int r = 4 * h + wave;
+    if (r < rc) {  // wave-uniform
+      const int c = lane * 8;  // run start within the chunk (a multiple of 8)
       // columns c + b and c + b + 4 (b < 4) are neighbours in the staged order
-      const uint32_t w[4] = {xv[h].x, xv[h].y, xv[h].z, xv[h].w};
+      const uint32_t w[4] = {R.xv[h].x, R.xv[h].y, R.xv[h].z, R.xv[h].w};
       const int base = (c & ~31) + ((c & 31) >> 2);
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const uint32_t lo = (w[b >> 1] >> (16 * (b & 1))) & 0xFFFFu;
         const uint32_t hi = (w[2 + (b >> 1)] >> (16 * (b & 1))) & 0xFFFFu;
-        *reinterpret_cast<uint32_t*>(&xs[r][base + 8 * b]) = lo | (hi << 16);
+        *reinterpret_cast<uint32_t*>(&ch.xs[r * kMfXStride + base + 8 * b]) = lo | (hi << 16);
       }
     }
+  }
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int j = tid + h * kMfThreads;
-      const int k = kc + j;
-      const int pj = (j & ~31) + mf_perm32(j & 31);
-      cds[pj] = static_cast<uint16_t>(cpv[h] >> 32);
-      cns[pj] = static_cast<uint16_t>(cpv[h] >> 48);
-      col_sal[j] = static_cast<uint32_t>(cpv[h]);
-      if (k < rank) {
-        const int bit = k & 31;
-        const int pr = k >> 5;
-        const int nbits = (rank - pr * 32) < 32 ? (rank - pr * 32) : 32;
-        const uint32_t cm = cmt[h] & low_mask(nbits);
-        if ((cm >> bit) & 1u) sal_col[q2t[h] - sbase0 + __popc(cm & ((1u << bit) - 1u))] = static_cast<uint16_t>(j);
-      }
-    }
-    // the lane's sign words and R0 | R1, for the salient pass (lane group kg writes every 4th)
-    if (num_sal > 0) {
-#pragma unroll
-      for (int j = 0; j < kMfChunk / 32; j += 4) L.q1l[j + kg][tc] = qw[j + kg];
-#pragma unroll
-      for (int t = 0; t < kMfChunk / kTileK; t += 4) L.r01[t + kg][tc] = static_cast<uint32_t>(rp[t + kg]);
-    }
-    __syncthreads();
+  for (int h = 0; h < 2; ++h) {
+    const int j = utid + h * kMfThreads;
+    const int k = kc + j;
+    const int pj = (j & ~31) + mf_perm32(j & 31);
+    const int bit = k & 31;
+    const uint32_t cm = R.cmt[h];
+    const bool sal = k < rank && ((cm >> bit) & 1u);
+    ch.cds[pj] = sal ? static_cast<uint16_t>(0) : static_cast<uint16_t>(R.cpv[h] >> 32);
+    ch.cns[pj] = sal ? static_cast<uint16_t>(0) : static_cast<uint16_t>(R.cpv[h] >> 48);
+    ch.col_sal[j] = static_cast<uint32_t>(R.cpv[h]);
+    if (sal) ch.sal_col[R.q2t[h] - R.sbase0 + __popc(cm & ((1u << bit) - 1u))] = static_cast<uint16_t>(j);
+  }
+  if (utid >= 64 && utid < 72) {
+    const bool tv = kc + (utid - 64) * kTileK < rank && R.mv >= 0 && R.mv < G;
+    ch.meta[utid - 64] = tv ? R.mv : -1;
+  } else if (utid >= 72 && utid < 74) {
+    ch.meta[8 + (utid - 72)] = R.mv;
+  }
+}
 
-    // ---- MFMA over the chunk's packed rows (salient columns are zero here)
+// LDS copies of one output tile's weight words for chunk kc: qweight1 and split words (wave w of the
+// unit copies packed rows w, w + 4, ...) and the 64 x G row-scale block.  Wave-uniform conditions
+// only; the caller waits (s_waitcnt) before reading.
+__device__ __forceinline__ void mf_tile_issue(const MfmaProj& pa, int s, int e, int kc, int ob, int utid,
+                                              const MfTileBuf& tb) {
+  const tris_compact3_payload& p = pa.p;
+  const int N = p.outfeatures;
+  const int rank = p.rank;
+  const int G = p.num_groups;
+  const int wave = __builtin_amdgcn_readfirstlane(utid / kWave);  // wave-uniform
+  const int lane = utid % kWave;
+  const int packed_rows = rank / 32;
+  const int nob = ceil_div(N, kTileOut);
+  const int nblk = (packed_rows / 2) * nob;
+  const int pr0 = kc / 32;
+  const int npr = (packed_rows - pr0) < kMfPR ? (packed_rows - pr0) : kMfPR;
+  const int n0 = ob * kTileOut;
+  const uint32_t q1_bytes = static_cast<uint32_t>(packed_rows) * N * 4u;
+  const __amdgpu_buffer_rsrc_t r_q1 = make_rsrc(p.qweight1 + static_cast<int64_t>(e) * packed_rows * N, q1_bytes);
+  const __amdgpu_buffer_rsrc_t r_dec =
+      make_rsrc(pa.decoded + static_cast<int64_t>(s) * nblk * kGrWords, static_cast<uint32_t>(nblk) * kGrWords * 4u);
+  const int n = n0 + lane;
+  const uint32_t v_q1 = n < N ? static_cast<uint32_t>(n) * 4u : q1_bytes;
 #pragma unroll
-    for (int j = 0; j < kMfChunk / 32; ++j) {
-      if (j < npr) {
-        const int t = j / 2;
-        const uint32_t d = static_cast<uint32_t>(rp[t] >> 32) & 0xFFFFu;
-        const uint32_t nd = static_cast<uint32_t>(rp[t] >> 48);
-        const f16x2 rd2 = u32_as_f16x2(d | (d << 16));
-        const f16x2 rn2 = u32_as_f16x2(nd | (nd << 16));
-        const int kl = j * 32 + 8 * kg;
-        const f16x8 av = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&xs[i16][kl]));
-        const uint4 cdv = *reinterpret_cast<const uint4*>(&cds[kl]);
-        const uint4 cnv = *reinterpret_cast<const uint4*>(&cns[kl]);
-        const uint32_t cd[4] = {cdv.x, cdv.y, cdv.z, cdv.w};
-        const uint32_t cn[4] = {cnv.x, cnv.y, cnv.z, cnv.w};
-        const uint32_t nsal = (~cmw[j] >> kg) & 0x11111111u;                       // 1 = non-salient
-        const uint32_t neg = ((~qw[j]) >> kg) & 0x11111111u;                         // 1 = negative
-        const uint32_t gd = (gw[j] >> kg) & nsal;                                    // 1 = d term
-        const uint32_t gn = nsal ^ gd;                                               // 1 = nd term
-        const uint32_t sd = (gd << 1) | ((gd & neg) << 3);                           // fp4 +-1.0 / 0
-        const uint32_t sn = (gn << 1) | ((gn & neg) << 3);
-        uint32_t b[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const f16x2 pd = u32_as_f16x2(cd[i]) * rd2;
-          const f16x2 pn = u32_as_f16x2(cn[i]) * rn2;
-          const f16x2 tn = fp4x2_to_f16x2(sn, i) * pn;
-          b[i] = f16x2_as_u32(__builtin_elementwise_fma(fp4x2_to_f16x2(sd, i), pd, tn));
-        }
-        const f16x8 bv = __builtin_bit_cast(f16x8, make_uint4(b[0], b[1], b[2], b[3]));
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
-      }
+  for (int jj = 0; jj < kMfPR / kMfWaves; ++jj) {
+    const int j = wave + kMfWaves * jj;
+    if (j < npr) {
+      const uint32_t pr = static_cast<uint32_t>(pr0 + j);
+      dma32(r_q1, tb.q1 + j * kMfQ1Stride, v_q1, pr * N * 4u);
+      dma32(r_dec, tb.gw + j * kTileOut, static_cast<uint32_t>(lane) * 4u,
+            ((((pr >> 1) * nob) + ob) * kGrWords + (pr & 1u) * kTileOut) * 4u);
     }
+  }
+  // row_pack3[e][n0 .. n0 + 63][0 .. G - 1] is one contiguous block; columns >= N read 0
+  const __amdgpu_buffer_rsrc_t r_rs =
+      make_rsrc(p.row_pack3 + (static_cast<int64_t>(e) * N + n0) * G, static_cast<uint32_t>(N - n0) * G * 8u);
+  const int kb = ceil_div(kTileOut * G * 8, 1024);  // <= 4 KiB (G <= kMfMaxGroups)
+  for (int b = wave; b < kb; b += kMfWaves) {
+    dma128(r_rs, reinterpret_cast<unsigned char*>(tb.rs) + b * 1024, static_cast<uint32_t>(b * 1024 + lane * 16), 0u);
+  }
+}
 
-    // ---- salient columns, kMfSalWin at a time.  Lane group kg writes the exact fp16 weights of
-    // its column for window slots kg, kg + 4, ... into ws (sign word and R0 | R1 from LDS), then
-    // the wave multiplies the activations gathered at those columns by ws on MFMA.
-    for (int w0 = 0; w0 < num_sal; w0 += kMfSalWin) {
-      const int wn = (num_sal - w0) < kMfSalWin ? (num_sal - w0) : kMfSalWin;
+// One projection over one staged chunk and output tile [n0, n0 + 64): accumulates rows 4 * kg + v,
+// column n0 + 16 * wave + lane % 16 of x . W^T into acc.  xrow is the staged activation row this
+// lane's A operand reads.
+// The lane's qweight2_sparse words of the chunk's first salient window (a window of kMfSalWin salient
+// columns spans at most two qweight2_sparse rows), for output column n.  Issued before the next tile's
+// LDS copies so that waiting for them does not wait for the copies.
+__device__ __forceinline__ void mf_q2_issue(const MfmaProj& pa, int e, int n, const MfChunk& ch, uint32_t q2w[2]) {
+  const tris_compact3_payload& p = pa.p;
+  const int N = p.outfeatures;
+  const int sbase0 = __builtin_amdgcn_readfirstlane(ch.meta[8]);
+  const int num_sal = __builtin_amdgcn_readfirstlane(ch.meta[9]) - sbase0;
+  const int q2rows = p.qweight2_sparse_rows;
+  const uint32_t q2_bytes = static_cast<uint32_t>(q2rows) * N * 4u;
+  const __amdgpu_buffer_rsrc_t r_q2 = make_rsrc(p.qweight2_sparse + static_cast<int64_t>(e) * q2rows * N, q2_bytes);
+  const uint32_t v_q2 = n < N ? static_cast<uint32_t>(n) * 4u : q2_bytes;
 #pragma unroll
-      for (int i = 0; i < kMfSalWin / 4; ++i) {
-        const int q = 4 * i + kg;
-        uint16_t w = 0;
-        if (q < wn) {
-          const int c = sal_col[w0 + q];  // chunk column
-          const int bit = c & 31;
-          const uint32_t w1 = L.q1l[c >> 5][tc];
-          const uint32_t rr = L.r01[c >> 6][tc];
-          const uint32_t cp = col_sal[c];
-          const int sidx = sbase0 + w0 + q;  // qweight2_sparse index
-          const int q2r = (sidx >> 5) - q2row0;
-          uint32_t q2w = q2r == 0 ? q2w01[0] : q2w01[1];
-          if (q2r > 1) q2w = bload32(r_q2, v_q2, static_cast<uint32_t>(sidx >> 5) * N * 4u);
-          uint16_t t1 = hmul_bits(static_cast<uint16_t>(cp), static_cast<uint16_t>(rr));
-          if (!((w1 >> bit) & 1u)) t1 ^= 0x8000u;
-          uint16_t t2 = hmul_bits(static_cast<uint16_t>(cp >> 16), static_cast<uint16_t>(rr >> 16));
-          if (!((q2w >> (sidx & 31)) & 1u)) t2 ^= 0x8000u;
-          w = hadd_bits(t1, t2);
-        }
-        ws[wave][i16][q] = w;
-      }
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      __builtin_amdgcn_wave_barrier();
+  for (int h = 0; h < 2; ++h) {
+    const int row = (sbase0 >> 5) + h;
+    const bool rv = num_sal > 0 && row < q2rows;
+    q2w[h] = bload32(r_q2, rv ? v_q2 : q2_bytes, static_cast<uint32_t>(rv ? row : 0) * N * 4u);
+  }
+}
+
+__device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, int n0, int xrow, int utid,
+                                            const MfChunk& ch, const MfTileBuf& tb, uint32_t* r01t,
+                                            uint16_t (*ws)[16][kMfSalStride], const uint32_t q2w0[2], f32x4 acc) {
+  const tris_compact3_payload& p = pa.p;
+  const int N = p.outfeatures;
+  const int rank = p.rank;
+  const int G = p.num_groups;
+  const int wave = __builtin_amdgcn_readfirstlane(utid / kWave);  // wave-uniform
+  const int lane = utid % kWave;
+  const int i16 = lane % 16;   // MFMA column within the wave's 16 outputs / A row
+  const int kg = lane / 16;    // MFMA k group: columns k = kg (mod 4) of every packed row
+  const int tc = 16 * wave + i16;
+  const int n = n0 + tc;
+  const int packed_rows = rank / 32;
+  const int pr0 = kc / 32;
+  const int npr = (packed_rows - pr0) < kMfPR ? (packed_rows - pr0) : kMfPR;
+  const uint16_t* xr = ch.xs + xrow * kMfXStride;
+
+  // salient columns of the chunk; the first window's qweight2_sparse words come in q2w0
+  const int sbase0 = __builtin_amdgcn_readfirstlane(ch.meta[8]);
+  const int num_sal = __builtin_amdgcn_readfirstlane(ch.meta[9]) - sbase0;
+  const int q2rows = p.qweight2_sparse_rows;
+  const uint32_t q2_bytes = static_cast<uint32_t>(q2rows) * N * 4u;
+  const __amdgpu_buffer_rsrc_t r_q2 =
+      make_rsrc(p.qweight2_sparse + static_cast<int64_t>(e) * q2rows * N, q2_bytes);
+  const uint32_t v_q2 = n < N ? static_cast<uint32_t>(n) * 4u : q2_bytes;
+  uint32_t q2w[2] = {q2w0[0], q2w0[1]};
+
+  // ---- MFMA over the chunk's packed rows (salient columns have zero factors here).  Per packed row
+  // the lane builds the nibble selectors of its 8 columns k = kg + 4m: bit 1 = this term is used,
+  // bit 3 = negative (shared by both terms; the unused term is a signed zero).  The LDS reads of row
+  // j + 1 are issued before row j is computed.
+  const uint32_t rot = static_cast<uint32_t>(kg - 1) & 31u;  // rotate right: bit kg + 4m -> 4m + 1
+  const uint32_t shl = static_cast<uint32_t>(3 - kg);        // shift left:   bit kg + 4m -> 4m + 3
+  // row scales of each K tile's group for this column: R_d | R_nd << 16, and R0 | R1 << 16 into the
+  // wave's salient table (only this wave reads its columns' entries)
+  uint32_t rdn[kMfTiles];
 #pragma unroll
-      for (int blk = 0; blk < kMfSalWin; blk += 32) {
-        if (blk < wn) {
-          uint32_t ap[4];
+  for (int t = 0; t < kMfTiles; ++t) {
+    const int g = __builtin_amdgcn_readfirstlane(ch.meta[t]);
+    const int gi = (tc * G + (g >= 0 ? g : 0)) * 2;
+    rdn[t] = g >= 0 ? tb.rs[gi + 1] : 0u;
+    if ((t & 3) == kg) r01t[t * kTileOut + tc] = g >= 0 ? tb.rs[gi] : 0u;
+  }
+  struct Row {
+    uint32_t qw, gw;
+    uint4 av, cd, cn;
+  };
+  auto load_row = [&](int j) {
+    Row r;
+    const int kl = j * 32 + 8 * kg;
+    r.qw = tb.q1[j * kMfQ1Stride + tc];
+    r.gw = tb.gw[j * kTileOut + tc];
+    r.av = *reinterpret_cast<const uint4*>(&xr[kl]);
+    r.cd = *reinterpret_cast<const uint4*>(&ch.cds[kl]);
+    r.cn = *reinterpret_cast<const uint4*>(&ch.cns[kl]);
+    return r;
+  };
+  auto row_mfma = [&](const Row& r, uint32_t rs2) {
+    const f16x2 rd2 = u32_as_f16x2(__builtin_amdgcn_perm(rs2, rs2, 0x01000100u));
+    const f16x2 rn2 = u32_as_f16x2(__builtin_amdgcn_perm(rs2, rs2, 0x03020302u));
+    const uint32_t cd[4] = {r.cd.x, r.cd.y, r.cd.z, r.cd.w};
+    const uint32_t cn[4] = {r.cn.x, r.cn.y, r.cn.z, r.cn.w};
+    const uint32_t neg3 = ~(r.qw << shl) & 0x88888888u;
+    const uint32_t sd = (__builtin_rotateright32(r.gw, rot) & 0x22222222u) | neg3;  // d term: fp4 +-1.0, else +-0
+    const uint32_t sn = sd ^ 0x22222222u;                                           // nd term: the others
+    uint32_t b[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int q0 = blk + 8 * kg + 2 * i;
-            uint32_t lo = 0u, hi = 0u;
-            if (q0 < wn) {
-              const int c = sal_col[w0 + q0];
-              lo = xs[i16][(c & ~31) + mf_perm32(c & 31)];
-            }
-            if (q0 + 1 < wn) {
-              const int c = sal_col[w0 + q0 + 1];
-              hi = xs[i16][(c & ~31) + mf_perm32(c & 31)];
-            }
-            ap[i] = lo | (hi << 16);
-          }
-          const f16x8 av = __builtin_bit_cast(f16x8, make_uint4(ap[0], ap[1], ap[2], ap[3]));
-          const f16x8 bv = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&ws[wave][i16][blk + 8 * kg]));
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
-        }
-      }
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      __builtin_amdgcn_wave_barrier();
+    for (int i = 0; i < 4; ++i) {
+      const f16x2 pd = u32_as_f16x2(cd[i]) * rd2;
+      const f16x2 pn = u32_as_f16x2(cn[i]) * rn2;
+      const f16x2 tn = fp4x2_to_f16x2(sn, i) * pn;
+      b[i] = f16x2_as_u32(__builtin_elementwise_fma(fp4x2_to_f16x2(sd, i), pd, tn));
     }
+    const f16x8 bv = __builtin_bit_cast(f16x8, make_uint4(b[0], b[1], b[2], b[3]));
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, r.av), bv, acc, 0, 0, 0);
+  };
+  if (npr == kMfPR) {  // a full chunk
+    Row cur = load_row(0);
+#pragma unroll
+    for (int j = 0; j < kMfPR; ++j) {
+      Row nxt = cur;
+      if (j + 1 < kMfPR) nxt = load_row(j + 1);  // compile-time condition
+      row_mfma(cur, rdn[j / 2]);
+      cur = nxt;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kMfPR; ++j) {
+      if (j < npr) row_mfma(load_row(j), rdn[j / 2]);  // uniform
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();  // r01t written
+
+  // ---- salient columns, kMfSalWin at a time.  Lane group kg writes the exact fp16 weights of its
+  // column for window slots kg, kg + 4, ... into ws (every slot, zero past the window's end, with no
+  // per-slot branch so the LDS reads overlap): w = fp16(+-fp16(C0 * R0) +- fp16(C1 * R1)), both
+  // products in one packed multiply.  Then the wave multiplies the activations gathered at those
+  // columns by ws on MFMA.
+  for (int w0 = 0; w0 < num_sal; w0 += kMfSalWin) {
+    const int wn = (num_sal - w0) < kMfSalWin ? (num_sal - w0) : kMfSalWin;
+    const int q2b = (sbase0 + w0) >> 5;  // qweight2_sparse row of the window's first salient column
+    if (w0 > 0) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const bool rv = q2b + h < q2rows;
+        q2w[h] = bload32(r_q2, rv ? v_q2 : q2_bytes, static_cast<uint32_t>(rv ? q2b + h : 0) * N * 4u);
+      }
+    }
+    uint16_t wv[kMfSalWin / 4];
+#pragma unroll
+    for (int u = 0; u < kMfSalWin / 4; ++u) {
+      const int q = 4 * u + kg;
+      const bool qv = q < wn;
+      const int c = ch.sal_col[w0 + (qv ? q : 0)];  // chunk column
+      const uint32_t w1 = tb.q1[(c >> 5) * kMfQ1Stride + tc];
+      const uint32_t rr = r01t[(c >> 6) * kTileOut + tc];
+      const uint32_t cp = ch.col_sal[c];
+      const int sidx = sbase0 + w0 + q;  // qweight2_sparse index
+      const uint32_t q2 = ((sidx >> 5) - q2b) == 0 ? q2w[0] : q2w[1];
+      // sign bits: positive where the qweight1 / qweight2 bit is set
+      const uint32_t neg = ((~(w1 >> (c & 31)) & 1u) << 15) | ((~(q2 >> (sidx & 31)) & 1u) << 31);
+      const f16x2 t = __builtin_bit_cast(f16x2, f16x2_as_u32(u32_as_f16x2(cp) * u32_as_f16x2(rr)) ^ neg);
+      const _Float16 w = t[0] + t[1];
+      wv[u] = qv ? __builtin_bit_cast(uint16_t, w) : static_cast<uint16_t>(0);
+    }
+#pragma unroll
+    for (int u = 0; u < kMfSalWin / 4; ++u) ws[wave][i16][4 * u + kg] = wv[u];
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    uint32_t ap[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q0 = 8 * kg + 2 * i;
+      uint32_t lo = 0u, hi = 0u;
+      if (q0 < wn) {
+        const int c = ch.sal_col[w0 + q0];
+        lo = xr[(c & ~31) + mf_perm32(c & 31)];
+      }
+      if (q0 + 1 < wn) {
+        const int c = ch.sal_col[w0 + q0 + 1];
+        hi = xr[(c & ~31) + mf_perm32(c & 31)];
+      }
+      ap[i] = lo | (hi << 16);
+    }
+    const f16x8 av = __builtin_bit_cast(f16x8, make_uint4(ap[0], ap[1], ap[2], ap[3]));
+    const f16x8 bv = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&ws[wave][i16][8 * kg]));
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
   }
   return acc;
 }
 
-// kMode 0: one projection; 1: two projections, blockIdx.z picks one; 2: both
-// projections per workgroup (gate, up) and the output is fp16(silu(g) * u).
-template <int kMode>
-__global__ __launch_bounds__(kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t xs[kMfRows][kMfXStride];
-  __shared__ __attribute__((aligned(16))) uint16_t cds[kMfChunk];
-  __shared__ __attribute__((aligned(16))) uint16_t cns[kMfChunk];
-  __shared__ uint32_t col_sal[kMfChunk];
-  __shared__ uint16_t sal_col[kMfChunk];
-  __shared__ __attribute__((aligned(16))) uint16_t ws[kMfWaves][16][kMfSalStride];
-  __shared__ uint32_t q1l[kMfChunk / 32][kTileOut];
-  __shared__ uint32_t r01[kMfChunk / kTileK][kTileOut];
-  const MfmaLds L{xs, cds, cns, col_sal, sal_col, ws, q1l, r01};
-
-  const MfmaProj& pa = a.proj[kMode == 1 ? blockIdx.z : 0];
+// Workgroup = kUnits units of 4 wavefronts.  The grid is sized to what the GPU holds at once, and the
+// workgroups share the (row tile, output tile) pairs evenly: with R row tiles (tiles of <= 16 rows of one
+// segment) and W = gridDim.x workgroups, each row tile gets W / R (or one more) workgroups that split its
+// output tiles into runs; with R > W, workgroup w takes row tiles w, w + W, ... whole.
+// kUnits == 1: one projection (blockIdx.z picks it when two are given, unfused).
+// kUnits == 2: unit 0 computes the gate and unit 1 the up projection of the same tiles, side by side;
+// the output is fp16(silu(g) * u).
+// Along a run the units compute from one weight buffer while the next tile's weight words are copied into
+// the other.  With more than one 512-column chunk (rank > 512) the chunk data is restaged per tile and
+// nothing is prefetched.
+template <int kUnits>
+__global__ __launch_bounds__(kUnits * kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char mf_lds[];
+  const int unit = kUnits == 2 ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kMfThreads) : 0;
+  const int utid = static_cast<int>(threadIdx.x) % kMfThreads;
+  const MfmaProj& pa = a.proj[kUnits == 2 ? unit : blockIdx.z];
   const tris_compact3_payload& p = pa.p;
   const int N = p.outfeatures;
-  const int n0 = blockIdx.x * kTileOut;
-  if (n0 >= N) return;
-  int s = 0, row0 = 0, rc = 0;
-  if (!mf_map_row_tile(a.segment_offsets, a.num_segments, blockIdx.y, kMfRows, &s, &row0, &rc)) return;
+  const int nob = ceil_div(N, kTileOut);
+  const MfSegScan sc = mf_scan_segments(a.segment_offsets, a.expert_ids, a.num_segments, kMfRows);
+  const int R = __builtin_amdgcn_readfirstlane(sc.total);
+  if (R == 0) return;  // no rows
+  const int W = static_cast<int>(gridDim.x);
+  const int w = static_cast<int>(blockIdx.x);
+  int rt_first = w, rt_step = W, ob_lo = 0, ob_hi = nob;
+  if (R <= W) {
+    const int per = W / R;
+    const int extra = W % R;
+    int sub, cnt;
+    if (w < extra * (per + 1)) {
+      rt_first = w / (per + 1);
+      sub = w % (per + 1);
+      cnt = per + 1;
+    } else {
+      rt_first = extra + (w - extra * (per + 1)) / per;
+      sub = (w - extra * (per + 1)) % per;
+      cnt = per;
+    }
+    cnt = cnt < nob ? cnt : nob;
+    if (sub >= cnt) return;  // more workgroups than output tiles for this row tile
+    ob_lo = static_cast<int>(static_cast<int64_t>(sub) * nob / cnt);
+    ob_hi = static_cast<int>(static_cast<int64_t>(sub + 1) * nob / cnt);
+    rt_step = R;  // one row tile
+  }
+  const int lane = utid % kWave;
+  uint16_t* out = kUnits == 2 ? a.proj[0].out : pa.out;
+  const MfUnitLayout L = mf_unit_layout(a.xs_rows, a.lds_groups);
+  unsigned char* base = mf_lds + unit * L.bytes;
+  MfChunk ch;
+  ch.xs = reinterpret_cast<uint16_t*>(base + L.xs);
+  ch.cds = reinterpret_cast<uint16_t*>(base + L.cds);
+  ch.cns = reinterpret_cast<uint16_t*>(base + L.cns);
+  ch.col_sal = reinterpret_cast<uint32_t*>(base + L.col_sal);
+  ch.sal_col = reinterpret_cast<uint16_t*>(base + L.sal_col);
+  ch.meta = reinterpret_cast<int32_t*>(base + L.meta);
+  __shared__ __attribute__((aligned(16))) uint32_t mf_tb0[kUnits][kMfTbWords];
+  __shared__ __attribute__((aligned(16))) uint32_t mf_tb1[kUnits][kMfTbWords];
+  MfTileBuf tb0, tb1;
+  tb0.q1 = &mf_tb0[unit][kMfTbQ1];
+  tb0.gw = &mf_tb0[unit][kMfTbGw];
+  tb0.rs = &mf_tb0[unit][kMfTbRs];
+  tb1.q1 = &mf_tb1[unit][kMfTbQ1];
+  tb1.gw = &mf_tb1[unit][kMfTbGw];
+  tb1.rs = &mf_tb1[unit][kMfTbRs];
+  uint32_t* r01t = reinterpret_cast<uint32_t*>(base + L.r01t);
+  auto ws = reinterpret_cast<uint16_t (*)[16][kMfSalStride]>(base + L.ws);
+  float* exch = reinterpret_cast<float*>(mf_lds + kUnits * L.bytes);
+  // A operand row of this lane: rows >= rc hold stale values and only feed output rows that are not stored
+  const int i16 = lane % 16;
+  const int xrow = i16 < a.xs_rows ? i16 : a.xs_rows - 1;
+  const int rank = p.rank;
+  const bool one_chunk = rank <= kMfChunk;
+  const int kg = lane / 16;
+
+  for (int rt = rt_first; rt < R; rt += rt_step) {
+  int s = 0, row0 = 0, rc = 0, e = -1;
+  mf_map_scanned(sc, a.segment_offsets, a.expert_ids, a.num_segments, rt, kMfRows, &s, &row0, &rc, &e);
   s = __builtin_amdgcn_readfirstlane(s);  // the mapping is the same in every lane
   row0 = __builtin_amdgcn_readfirstlane(row0);
   rc = __builtin_amdgcn_readfirstlane(rc);
-
-  const int tid = threadIdx.x;
-  const int lane = tid % kWave;
-  const int e = __builtin_amdgcn_readfirstlane(a.expert_ids[s]);
-  uint16_t* out = pa.out;
-  if (e < 0 || e >= p.num_experts) {
-    for (int idx = tid; idx < rc * kTileOut; idx += kMfThreads) {
-      const int n = n0 + idx % kTileOut;
-      if (n < N) out[static_cast<int64_t>(row0 + idx / kTileOut) * N + n] = 0;
+  e = __builtin_amdgcn_readfirstlane(e);
+  const int ob_begin = ob_lo;
+  const int ob_end = ob_hi;
+  if (e < 0 || e >= p.num_experts) {  // rows routed to no expert: zero output
+    if (unit == 0) {
+      const int span = (ob_end - ob_begin) * kTileOut;
+      for (int idx = utid; idx < rc * span; idx += kMfThreads) {
+        const int n = ob_begin * kTileOut + idx % span;
+        if (n < N) out[static_cast<int64_t>(row0 + idx / span) * N + n] = 0;
+      }
     }
-    return;
+    continue;
   }
-  const f32x4 acc = mfma_project(pa, s, row0, rc, e, n0, L);
-  f32x4 acc_up = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  if (kMode == 2) acc_up = mfma_project(a.proj[1], s, row0, rc, e, n0, L);
+  if (rt != rt_first) __syncthreads();  // the previous row tile's LDS readers are done
+  {  // chunk 0 and the first tile's weights
+    MfRegs regs;
+    mf_tile_issue(pa, s, e, 0, ob_begin, utid, tb0);
+    mf_chunk_issue(pa, e, row0, rc, 0, utid, regs);
+    mf_chunk_write(pa, rc, 0, utid, ch, regs);
+    __builtin_amdgcn_s_waitcnt(0);  // LDS copies landed (all counters zero)
+    __syncthreads();
+  }
+  // One output tile, computed from `cur`; with one chunk the next tile's words are copied into `nxt`
+  // meanwhile.  Called with the two static buffers in alternation, so every instance knows which
+  // object it reads and which it fills.
+  auto tile = [&](int ob, const MfTileBuf& cur, const MfTileBuf& nxt) {
+    const int n = ob * kTileOut + 16 * (utid / kWave) + i16;
+    uint32_t q2w[2];
+    mf_q2_issue(pa, e, n, ch, q2w);
+    if (one_chunk && ob + 1 < ob_end) mf_tile_issue(pa, s, e, 0, ob + 1, utid, nxt);  // prefetch
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int kc = 0; kc < rank; kc += kMfChunk) {
+      if (!one_chunk && (ob > ob_begin || kc > 0)) {
+        __syncthreads();  // the previous chunk's readers are done
+        MfRegs regs;
+        mf_tile_issue(pa, s, e, kc, ob, utid, cur);
+        mf_chunk_issue(pa, e, row0, rc, kc, utid, regs);
+        mf_chunk_write(pa, rc, kc, utid, ch, regs);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        mf_q2_issue(pa, e, n, ch, q2w);
+      }
+      acc = mf_compute(pa, e, kc, ob * kTileOut, xrow, utid, ch, cur, r01t, ws, q2w, acc);
+    }
 
-  const int kg = lane / 16;
-  const int n = n0 + 16 * (tid / kWave) + lane % 16;
-  const bool nv = n < N;
-  const float scale = (nv && p.has_output_scale) ? h2f(p.output_scale[static_cast<int64_t>(e) * N + n]) : 1.0f;
-  const float bias = (nv && p.has_bias) ? h2f(p.bias[static_cast<int64_t>(e) * N + n]) : 0.0f;
+    const bool nv = n < N;
+    if (kUnits == 2) {
+      if (unit == 1) *reinterpret_cast<f32x4*>(&exch[utid * 4]) = acc;
+      __syncthreads();
+      if (unit == 0) {
+        const f32x4 up = *reinterpret_cast<const f32x4*>(&exch[utid * 4]);
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int r = 4 * kg + v;
-    if (!nv || r >= rc) continue;
-    uint16_t y;
-    if (kMode == 2) {
-      // g and u rounded to fp16 as the two outputs would be, SiLU in fp32 rounded to fp16, then the
-      // fp16 product (modeling_mixtral.py:496)
-      const float g = h2f(f2h_bits(acc[v]));
-      const float u = h2f(f2h_bits(acc_up[v]));
-      const float sg = h2f(f2h_bits(g / (1.0f + expf(-g))));
-      y = f2h_bits(sg * u);
+        for (int v = 0; v < 4; ++v) {
+          const int r = 4 * kg + v;
+          if (!nv || r >= rc) continue;
+          // g and u rounded to fp16 as the two outputs would be, SiLU in fp32 rounded to fp16, then the
+          // fp16 product (modeling_mixtral.py:496)
+          const float g = h2f(f2h_bits(acc[v]));
+          const float u = h2f(f2h_bits(up[v]));
+          const float sg = h2f(f2h_bits(g / (1.0f + expf(-g))));
+          out[static_cast<int64_t>(row0 + r) * N + n] = f2h_bits(sg * u);
+        }
+      }
     } else {
-      float x = acc[v];
-      if (p.has_output_scale) x = x * scale;
-      if (p.has_bias) x = x + bias;
-      y = f2h_bits(x);
+      const float scale = (nv && p.has_output_scale) ? h2f(p.output_scale[static_cast<int64_t>(e) * N + n]) : 1.0f;
+      const float bias = (nv && p.has_bias) ? h2f(p.bias[static_cast<int64_t>(e) * N + n]) : 0.0f;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int r = 4 * kg + v;
+        if (!nv || r >= rc) continue;
+        float x = acc[v];
+        if (p.has_output_scale) x = x * scale;
+        if (p.has_bias) x = x + bias;
+        out[static_cast<int64_t>(row0 + r) * N + n] = f2h_bits(x);
+      }
     }
-    out[static_cast<int64_t>(row0 + r) * N + n] = y;
+    if (one_chunk) {
+      __builtin_amdgcn_s_waitcnt(0);  // the next tile's copies landed
+      __syncthreads();                // and every reader of this tile's buffer (and exch) is done
+    }
+  };
+  for (int ob = ob_begin; ob < ob_end; ob += 2) {
+    tile(ob, tb0, tb1);
+    if (ob + 1 < ob_end) tile(ob + 1, tb1, tb0);
   }
+  }  // row tiles
 }
 
 int check_payload(const tris_compact3_payload* p, bool need_gr, const char* who);
+
+static bool allow_mfma_lds(const void* kernel, int bytes) {
+  static int granted[2] = {0, 0};
+  const int which = kernel == reinterpret_cast<const void*>(&grouped_mfma_kernel<1>) ? 0 : 1;
+  if (bytes <= granted[which]) return true;
+  // Raising the dynamic LDS limit is not a stream operation, so it is safe while a caller captures a graph.
+  if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  granted[which] = bytes;
+  return true;
+}
 
 int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int batch, const int32_t* expert_ids,
                         const int32_t* segment_offsets, int num_segments, const int32_t* decoded_a,
@@ -517,26 +808,44 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
     TRIS_REQUIRE(p->num_experts > 0 && p->rank > 0 && p->outfeatures > 0, "%s: empty payload", who);
     max_n = p->outfeatures > max_n ? p->outfeatures : max_n;
   }
-  TRIS_REQUIRE(!swiglu || (pa->outfeatures == pb->outfeatures && pa->num_experts == pb->num_experts),
+  TRIS_REQUIRE(!swiglu || (pa->outfeatures == pb->outfeatures && pa->num_experts == pb->num_experts &&
+                           pa->rank == pb->rank),
                "%s: gate and up projections differ in shape", who);
-  const int64_t tiles = static_cast<int64_t>(batch) / kMfRows + num_segments;
-  TRIS_REQUIRE(tiles <= 2147483647LL, "%s: too many tiles", who);
   MfmaArgs args{};
   args.proj[0] = MfmaProj{hidden_a, out_a, decoded_a, *pa};
   if (pb) args.proj[1] = MfmaProj{hidden_b, out_b, decoded_b, *pb};
   args.expert_ids = expert_ids;
   args.segment_offsets = segment_offsets;
   args.num_segments = num_segments;
+  args.xs_rows = batch < kMfRows ? batch : kMfRows;
+  args.lds_groups = pa->num_groups;
+  if (pb && pb->num_groups > args.lds_groups) args.lds_groups = pb->num_groups;
+  const int units = swiglu ? 2 : 1;
+  const int lds = mf_lds_bytes(units, args.xs_rows, args.lds_groups);
+  const int lds_total = lds + mf_static_lds_bytes(units);
+  TRIS_REQUIRE(lds_total <= 160 * 1024, "%s: LDS request %d exceeds a CU", who, lds_total);
+  // Workgroups: as many as the GPU holds at once (LDS and about 160 VGPRs per lane, 3 wavefronts per
+  // SIMD, bound them), shared by the projections of an unfused pair.
+  int wgs_per_cu = (160 * 1024) / lds_total;
+  const int by_regs = 3 / units;
+  wgs_per_cu = wgs_per_cu < by_regs ? wgs_per_cu : by_regs;
+  wgs_per_cu = wgs_per_cu > 0 ? wgs_per_cu : 1;
+  const int nproj = (pb && !swiglu) ? 2 : 1;
+  int wgs = (kMfCus * wgs_per_cu) / nproj;
+  // no more than the (row tile, output tile) pairs there can be: row tiles <= batch / 16 + min(segments, batch)
+  const int64_t pairs =
+      (static_cast<int64_t>(batch) / kMfRows + (num_segments < batch ? num_segments : batch)) * ceil_div(max_n, kTileOut);
+  if (pairs < wgs) wgs = static_cast<int>(pairs);
+  const dim3 grid(wgs > 0 ? wgs : 1, 1, nproj);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (swiglu) {
-    const dim3 grid(ceil_div(max_n, kTileOut), static_cast<unsigned>(tiles), 1);
-    hipLaunchKernelGGL((grouped_mfma_kernel<2>), grid, dim3(kMfThreads), 0, s, args);
-  } else if (pb) {
-    const dim3 grid(ceil_div(max_n, kTileOut), static_cast<unsigned>(tiles), 2);
-    hipLaunchKernelGGL((grouped_mfma_kernel<1>), grid, dim3(kMfThreads), 0, s, args);
+    TRIS_REQUIRE(allow_mfma_lds(reinterpret_cast<const void*>(&grouped_mfma_kernel<2>), lds), "%s: %s", who,
+                 "cannot raise the kernel's dynamic LDS limit");
+    hipLaunchKernelGGL((grouped_mfma_kernel<2>), grid, dim3(2 * kMfThreads), lds, s, args);
   } else {
-    const dim3 grid(ceil_div(max_n, kTileOut), static_cast<unsigned>(tiles), 1);
-    hipLaunchKernelGGL((grouped_mfma_kernel<0>), grid, dim3(kMfThreads), 0, s, args);
+    TRIS_REQUIRE(allow_mfma_lds(reinterpret_cast<const void*>(&grouped_mfma_kernel<1>), lds), "%s: %s", who,
+                 "cannot raise the kernel's dynamic LDS limit");
+    hipLaunchKernelGGL((grouped_mfma_kernel<1>), grid, dim3(kMfThreads), lds, s, args);
   }
   return check_launch(who);
 }
@@ -546,7 +855,7 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
 // 64-column tiles, with 16-byte aligned activations (8-column loads).
 bool grouped_mfma_supported(const tris_compact3_payload* p, const uint16_t* hidden) {
   if (p == nullptr || !p->use_uniform_k64_groups || p->rank <= 0 || p->rank % kTileK != 0 ||
-      reinterpret_cast<uintptr_t>(hidden) % 16 != 0) {
+      p->num_groups < 1 || p->num_groups > kMfMaxGroups || reinterpret_cast<uintptr_t>(hidden) % 16 != 0) {
     return false;
   }
   // the kernel addresses each expert's tensors with 32-bit buffer offsets
