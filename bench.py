@@ -14,8 +14,9 @@ HBM, not the 256 MB last-level cache), with each step captured in a HIP graph.
 
 Prints ONE JSON line.  ``value`` is MoE-layer tokens/s; ``hbm_gbps`` the
 layer's algorithmic bytes / step time; ``roofline`` is for the dominant
-kernel, the MFMA gate/up grouped GEMM + SwiGLU over predecoded bitmaps
-(grouped_mfma_kernel<2>), timed live with HIP events on its own stream; ``cpu_baseline`` times the
+kernel, the MFMA gate/up grouped GEMM over predecoded bitmaps that the step runs at this batch
+(grouped_mfma_kernel<1> for gate and up in separate workgroups, or grouped_mfma_kernel<2> with the
+SwiGLU epilogue at <= 4 routed rows), timed live with HIP events on its own stream; ``cpu_baseline`` times the
 CPU oracle (GR decode + exact fp16 dequant + fp32 GEMM) on a bounded sample.
 """
 from __future__ import annotations
@@ -154,8 +155,8 @@ def main():
         sweep[f"T{tok}"]["active_experts"] = r["active_experts"]
         log(f"T={tok}: {r['ms_per_step'] * 1e3:.1f} us/step, {r['tokens_per_s']:.0f} tok/s, {r['hbm_gbps']:.0f} GB/s")
 
-    # ---- dominant kernel: the MFMA gate/up grouped GEMM + SwiGLU over predecoded split bitmaps, one
-    # launch per layer copy, replayed from a graph on its own stream and timed there with HIP events
+    # ---- dominant kernel: the MFMA gate/up grouped GEMM over predecoded split bitmaps that the step runs,
+    # one launch per layer copy, replayed from a graph on its own stream and timed there with HIP events
     x16, logits = main_res["x16"], main_res["logits"]
     w, sel = moe.route_topk(logits, SPEC.top_k, SPEC.renormalize)
     route = ext.build_grouped_route_device(sel, SPEC.num_experts, 4)
@@ -166,8 +167,6 @@ def main():
     prob = route["problem_offsets"][: slots + 1]
     hid_g = ext.backbone_linear(x16, base_backbones["gate"], row_index=route["grouped_token_indices"])
     hid_u = ext.backbone_linear(x16, base_backbones["up"], row_index=route["grouped_token_indices"])
-    tile_bound = rows // 4 + slots + 1
-    names = ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx", "col_pack3", "row_pack3")
     nblk = int(layer["gate"]["q_gmap_gr_meta"].shape[1])
     decoded = []
     for pl, _ in copies:
@@ -179,13 +178,12 @@ def main():
                 SPEC.rank // 32, SPEC.intermediate))
         decoded.append(pair)
 
-    mlp = torch.empty((rows, SPEC.intermediate), dtype=torch.float16, device=dev)
+    active = main_res["active"]
+    launch, kname, kbytes, kind = gateup_kernel(ext, moe, synthetic, layer, rows, active, SPEC, hid_g, hid_u, eid,
+                                                seg, prob, dev)
 
     def dual(i):
-        pl = copies[i][0]
-        return ext.compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded(
-            hid_g, hid_u, eid, seg, prob, tile_bound, decoded[i][0], *[pl["gate"][k] for k in names],
-            decoded[i][1], *[pl["up"][k] for k in names], out=mlp)
+        launch(copies[i][0], decoded[i][0], decoded[i][1])
 
     kstream = torch.cuda.Stream(device=dev)
     kstream.wait_stream(torch.cuda.current_stream())
@@ -205,15 +203,11 @@ def main():
         ke.record(kstream)
         kstream.synchronize()
     kernel_s = ks.elapsed_time(ke) / 1e3 / (args.kernel_reps * len(copies))
-    active = main_res["active"]
-    dual_bytes = (synthetic.predecoded_nbytes(layer["gate"], active) + synthetic.predecoded_nbytes(layer["up"], active)
-                  + 2 * rows * SPEC.rank * 2 + rows * SPEC.intermediate * 2)
-    achieved = dual_bytes / kernel_s / 1e9
+    achieved = kbytes / kernel_s / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(args.tokens),
-                "kernel": "grouped_mfma_kernel<2> (gate/up grouped GEMM + SwiGLU over predecoded bitmaps)",
-                "kernel_us": round(kernel_s * 1e6, 2), "bytes_per_launch": int(dual_bytes)}
-    log(f"gate/up SwiGLU GEMM: {kernel_s * 1e6:.1f} us/launch, {achieved:.0f} GB/s algorithmic")
+                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(args.tokens, kind),
+                "kernel": kname, "kernel_us": round(kernel_s * 1e6, 2), "bytes_per_launch": int(kbytes)}
+    log(f"gate/up grouped GEMM ({kind}): {kernel_s * 1e6:.1f} us/launch, {achieved:.0f} GB/s algorithmic")
 
     cpu = None
     if args.cpu_baseline:
@@ -246,10 +240,42 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def measured_traffic(tokens: int):
+def gateup_kernel(ext, moe, synthetic, layer, rows, active, spec, hid_g, hid_u, eid, seg, prob, dev):
+    """The gate/up grouped GEMM the layer step runs at `rows` routed rows: returns (launch(payloads,
+    decoded_gate, decoded_up), kernel name, algorithmic bytes per launch).  Bytes: the routed experts'
+    payloads with predecoded bitmaps, the two backbone outputs read, the fp16 output(s) written."""
+    import torch
+
+    names = ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx", "col_pack3", "row_pack3")
+    slots = int(eid.numel())
+    tile_bound = rows // 4 + slots + 1
+    weights = synthetic.predecoded_nbytes(layer["gate"], active) + synthetic.predecoded_nbytes(layer["up"], active)
+    if rows <= moe.FUSED_SWIGLU_MAX_ROWS:
+        mlp = torch.empty((rows, spec.intermediate), dtype=torch.float16, device=dev)
+
+        def launch(pl, dg, du):
+            ext.compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded(
+                hid_g, hid_u, eid, seg, prob, tile_bound, dg, *[pl["gate"][k] for k in names], du,
+                *[pl["up"][k] for k in names], out=mlp)
+        name = "grouped_mfma_kernel<2> (gate/up grouped GEMM + SwiGLU epilogue, predecoded bitmaps)"
+        nbytes = weights + 2 * rows * spec.rank * 2 + rows * spec.intermediate * 2
+        return launch, name, nbytes, "swiglu"
+    g = torch.empty((rows, spec.intermediate), dtype=torch.float16, device=dev)
+    u = torch.empty_like(g)
+
+    def launch(pl, dg, du):
+        ext.compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
+            hid_g, hid_u, eid, seg, prob, tile_bound, dg, *[pl["gate"][k] for k in names], du,
+            *[pl["up"][k] for k in names], True, out_a=g, out_b=u)
+    name = "grouped_mfma_kernel<1> (gate and up grouped GEMMs, predecoded bitmaps)"
+    nbytes = weights + 2 * rows * spec.rank * 2 + 2 * rows * spec.intermediate * 2
+    return launch, name, nbytes, "dual"
+
+
+def measured_traffic(tokens: int, kind: str):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
     runs (scaled by a copy-kernel calibration), or None when no measurement matches this workload."""
-    path = ROOT / "profiles" / f"grouped_mfma_swiglu_mixtral_decode_T{tokens}_traffic.json"
+    path = ROOT / "profiles" / f"grouped_mfma_{kind}_mixtral_decode_T{tokens}_traffic.json"
     try:
         return int(json.loads(path.read_text())["traffic_bytes"])
     except (OSError, ValueError, KeyError):
@@ -260,7 +286,7 @@ def profile_dominant_kernel(args, layer, payloads, backbones, spec, dev):
     """Eager launches of the dominant kernel at the bench workload, for hardware-counter runs."""
     import torch
 
-    from tris_moe_amd import ext, synthetic
+    from tris_moe_amd import ext, moe, synthetic
 
     inp = synthetic.make_inputs(spec, args.tokens, args.seed + args.tokens, layer["outlier_idx"])
     x16 = torch.from_numpy(inp["x"]).to(dev).to(torch.bfloat16).to(torch.float16)
@@ -280,17 +306,13 @@ def profile_dominant_kernel(args, layer, payloads, backbones, spec, dev):
         dec.append(ext.compact3_tris_precomputed_grouped_block_gr_predecode(
             buf, eid, payloads[p]["q_gmap_gr_words"], payloads[p]["q_gmap_gr_offsets"],
             payloads[p]["q_gmap_gr_meta"], spec.rank // 32, spec.intermediate))
-    names = ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx", "col_pack3", "row_pack3")
-    mlp = torch.empty((rows, spec.intermediate), dtype=torch.float16, device=dev)
-    for _ in range(args.kernel_reps):
-        ext.compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded(
-            hid_g, hid_u, eid, seg, prob, rows // 4 + slots + 1, dec[0], *[payloads["gate"][k] for k in names],
-            dec[1], *[payloads["up"][k] for k in names], out=mlp)
-    torch.cuda.synchronize()
     active = sorted(set(route["selected_experts"].cpu().numpy().reshape(-1).tolist()))
-    nbytes = (synthetic.predecoded_nbytes(layer["gate"], active) + synthetic.predecoded_nbytes(layer["up"], active)
-              + 2 * rows * spec.rank * 2 + rows * spec.intermediate * 2)
-    print(json.dumps({"kernel": "grouped_mfma_kernel<2>", "launches": args.kernel_reps, "bytes_per_launch": nbytes}))
+    launch, kname, nbytes, kind = gateup_kernel(ext, moe, synthetic, layer, rows, active, spec, hid_g, hid_u, eid,
+                                                seg, prob, dev)
+    for _ in range(args.kernel_reps):
+        launch(payloads, dec[0], dec[1])
+    torch.cuda.synchronize()
+    print(json.dumps({"kernel": kname, "kind": kind, "launches": args.kernel_reps, "bytes_per_launch": nbytes}))
 
 
 def cpu_baseline(layer, res, spec):

@@ -288,6 +288,15 @@ int tris_moe_combine(const uint16_t* expert_out, const int32_t* inverse_perm, co
                      const uint16_t* shared, int32_t tokens, int32_t top_k, int32_t hidden, uint16_t* out,
                      void* stream);
 
+/*
+ * out = act_fn(gate) * up for fp16 tensors of `count` elements (16-byte aligned): SiLU in fp32 rounded
+ * to fp16, then the fp16 product, as the reference's MixtralBlockSparseTop2MLP.forward
+ * (modeling_mixtral.py:496) computes act_fn(w1(x)) * w3(x) on the two fp16 GEMM outputs.  Used after
+ * tris_grouped_dual_forward_block_gr_predecoded; gives the same bits as the fused
+ * tris_grouped_swiglu_forward_block_gr_predecoded.
+ */
+int tris_swiglu_mul(const uint16_t* gate, const uint16_t* up, int64_t count, uint16_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

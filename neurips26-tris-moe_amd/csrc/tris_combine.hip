@@ -59,9 +59,48 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
   }
 }
 
+// out = act_fn(gate) * up, 8 consecutive elements per thread (16-byte loads when aligned).
+__global__ __launch_bounds__(256) void swiglu_mul_kernel(const uint16_t* __restrict__ gate,
+                                                         const uint16_t* __restrict__ up, int64_t count,
+                                                         uint16_t* __restrict__ out) {
+  const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+  if (i0 >= count) return;
+  if (i0 + 8 <= count) {
+    const uint4 gv = *reinterpret_cast<const uint4*>(gate + i0);
+    const uint4 uv = *reinterpret_cast<const uint4*>(up + i0);
+    const uint32_t g[4] = {gv.x, gv.y, gv.z, gv.w};
+    const uint32_t u[4] = {uv.x, uv.y, uv.z, uv.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t lo = swiglu_bits(static_cast<uint16_t>(g[k]), static_cast<uint16_t>(u[k]));
+      const uint32_t hi = swiglu_bits(static_cast<uint16_t>(g[k] >> 16), static_cast<uint16_t>(u[k] >> 16));
+      o[k] = lo | (hi << 16);
+    }
+    *reinterpret_cast<uint4*>(out + i0) = make_uint4(o[0], o[1], o[2], o[3]);
+    return;
+  }
+  for (int64_t i = i0; i < count; ++i) out[i] = swiglu_bits(gate[i], up[i]);
+}
+
 }  // namespace tris
 
 using namespace tris;
+
+extern "C" int tris_swiglu_mul(const uint16_t* gate, const uint16_t* up, int64_t count, uint16_t* out, void* stream) {
+  TRIS_REQUIRE(count >= 0, "tris_swiglu_mul: negative count");
+  if (count == 0) return TRIS_OK;
+  TRIS_REQUIRE(gate && up && out, "tris_swiglu_mul: null pointer");
+  TRIS_REQUIRE(reinterpret_cast<uintptr_t>(gate) % 16 == 0 && reinterpret_cast<uintptr_t>(up) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(out) % 16 == 0,
+               "tris_swiglu_mul: tensors must be 16-byte aligned");
+  const int64_t threads = 256;
+  const int64_t blocks = (count + 8 * threads - 1) / (8 * threads);
+  TRIS_REQUIRE(blocks <= 2147483647LL, "tris_swiglu_mul: too many elements");
+  hipLaunchKernelGGL(swiglu_mul_kernel, dim3(static_cast<unsigned>(blocks)), dim3(threads), 0,
+                     static_cast<hipStream_t>(stream), gate, up, count, out);
+  return check_launch("swiglu_mul_kernel");
+}
 
 extern "C" int tris_moe_combine(const uint16_t* expert_out, const int32_t* inverse_perm, const uint16_t* weights,
                                 const uint16_t* shared, int32_t tokens, int32_t top_k, int32_t hidden,

@@ -41,6 +41,14 @@ __device__ __forceinline__ uint16_t hadd_bits(uint16_t a, uint16_t b) {
   return __half_as_ushort(__hadd(__ushort_as_half(a), __ushort_as_half(b)));
 }
 
+// The reference's gated activation act_fn(g) * u for fp16 g, u (modeling_mixtral.py:496): SiLU in fp32
+// rounded to fp16, then the fp16 product.
+__device__ __forceinline__ uint16_t swiglu_bits(uint16_t g16, uint16_t u16) {
+  const float g = h2f(g16);
+  const float sg = h2f(f2h_bits(g / (1.0f + expf(-g))));
+  return f2h_bits(sg * h2f(u16));
+}
+
 __device__ __forceinline__ uint32_t low_mask(int bits) {
   return bits >= 32 ? 0xFFFFFFFFu : ((1u << bits) - 1u);
 }

@@ -739,12 +739,8 @@ __global__ __launch_bounds__(kUnits * kMfThreads) void grouped_mfma_kernel(MfmaA
         for (int v = 0; v < 4; ++v) {
           const int r = 4 * kg + v;
           if (!nv || r >= rc) continue;
-          // g and u rounded to fp16 as the two outputs would be, SiLU in fp32 rounded to fp16, then the
-          // fp16 product (modeling_mixtral.py:496)
-          const float g = h2f(f2h_bits(acc[v]));
-          const float u = h2f(f2h_bits(up[v]));
-          const float sg = h2f(f2h_bits(g / (1.0f + expf(-g))));
-          out[static_cast<int64_t>(row0 + r) * N + n] = f2h_bits(sg * u);
+          // g and u rounded to fp16 as the two outputs would be
+          out[static_cast<int64_t>(row0 + r) * N + n] = swiglu_bits(f2h_bits(acc[v]), f2h_bits(up[v]));
         }
       }
     } else {

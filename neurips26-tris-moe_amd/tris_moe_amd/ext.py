@@ -619,6 +619,22 @@ def moe_combine(expert_out: torch.Tensor, inverse_perm: torch.Tensor, weights: t
     return out
 
 
+def swiglu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp16 act_fn(gate) * up (modeling_mixtral.py:496): SiLU in fp32 rounded to fp16, then the fp16 product."""
+    _check_cuda("gate", gate, torch.float16, None)
+    _check_cuda("up", up, torch.float16, None, gate.device)
+    if gate.shape != up.shape:
+        raise RuntimeError("gate and up must have the same shape")
+    if out is None:
+        out = torch.empty_like(gate)
+    _check_cuda("out", out, torch.float16, None, gate.device)
+    if out.shape != gate.shape:
+        raise RuntimeError("out must have the shape of gate")
+    _lib.check(_lib.load().tris_swiglu_mul(_ptr(gate), _ptr(up), gate.numel(), _ptr(out), _stream(gate)),
+               "tris_swiglu_mul")
+    return out
+
+
 def gr_encode(packed, k_min: int = 0, k_max: int = 7, force_raw: bool = False):
     """Host block-GR encoder: int32 [packed_rows, N] (numpy or CPU tensor) -> (words, offsets, meta) int32 numpy."""
     import numpy as np

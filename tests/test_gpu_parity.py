@@ -444,6 +444,31 @@ def test_swiglu_fused_matches_dual_then_silu(tris, oracle_mod, cuda):
     want = (oracle_mod.silu_f16(g).astype(np.float32) * u.astype(np.float32)).astype(np.float16)
     ulp = np.abs(fused.view(np.int16).astype(np.int32) - want.view(np.int16).astype(np.int32))
     assert ulp.max() <= 1 and (ulp > 0).mean() < 0.01, (int(ulp.max()), float((ulp > 0).mean()))
+    # the standalone act_fn(g) * u kernel gives the fused kernel's bits exactly
+    sep = ext.swiglu_mul(torch.from_numpy(g).to(cuda), torch.from_numpy(u).to(cuda)).cpu().numpy()
+    np.testing.assert_array_equal(sep.view(np.uint16), fused.view(np.uint16))
+
+
+def test_swiglu_mul_edge_cases(tris, oracle_mod, cuda):
+    """act_fn(g) * u over a ragged length (a 16-byte body and an element-wise tail), zeros, infinities
+    and large magnitudes, against the oracle's fp16 roundings (one ulp allowed for exp)."""
+    note("swiglu_mul edges")
+    ext = tris["ext"]
+    rng = np.random.default_rng(31)
+    count = 1003
+    g = (rng.standard_normal(count) * 6).astype(np.float16)
+    u = (rng.standard_normal(count) * 6).astype(np.float16)
+    g[:6] = np.array([0.0, -0.0, 60000.0, -60000.0, np.inf, -np.inf], dtype=np.float16)
+    u[6:9] = np.array([0.0, 65504.0, -65504.0], dtype=np.float16)
+    gt, ut = torch.from_numpy(g).to(cuda), torch.from_numpy(u).to(cuda)
+    out = ext.swiglu_mul(gt, ut).cpu().numpy()
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = (oracle_mod.silu_f16(g).astype(np.float32) * u.astype(np.float32)).astype(np.float16)
+    fin = np.isfinite(want)
+    np.testing.assert_array_equal(np.isfinite(out), fin)
+    ulp = np.abs(out[fin].view(np.int16).astype(np.int32) - want[fin].view(np.int16).astype(np.int32))
+    assert ulp.max() <= 1, int(ulp.max())
+    assert ext.swiglu_mul(gt[:0], ut[:0]).numel() == 0
 
 
 def test_run_grouped_structured_api(tris, oracle_mod, cuda):
