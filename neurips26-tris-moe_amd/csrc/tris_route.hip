@@ -132,6 +132,168 @@ constexpr int kRouteSmallMaxRows = 2048;    // tokens * top_k
 constexpr int kRouteSmallMaxExperts = 1024;
 constexpr int kRouteMaxTopK = 16;
 
+// Softmax of one token's logits (fp32, max-subtracted, summed in expert order) and its top-k by
+// probability with ties to the lower expert id (a stable descending sort, as the oracle's argsort):
+// bp[j] / be[j] for j < top_k, most probable first.
+__device__ __forceinline__ void route_token_topk(const float* __restrict__ row, int num_experts, int top_k,
+                                                 float bp[kRouteMaxTopK], int be[kRouteMaxTopK]) {
+  float m = row[0];
+  for (int e = 1; e < num_experts; ++e) m = fmaxf(m, row[e]);
+  float sum = 0.0f;
+  for (int e = 0; e < num_experts; ++e) sum += expf(row[e] - m);
+#pragma unroll
+  for (int j = 0; j < kRouteMaxTopK; ++j) {
+    bp[j] = -1.0f;
+    be[j] = -1;
+  }
+  for (int e = 0; e < num_experts; ++e) {
+    const float pe = expf(row[e] - m) / sum;
+    // insert after every kept entry with probability >= pe (earlier experts win ties)
+    if (pe > bp[top_k - 1] || be[top_k - 1] < 0) {
+      float cp = pe;
+      int ce = e;
+      bool shifting = false;  // once placed, every later entry moves down one
+#pragma unroll
+      for (int j = 0; j < kRouteMaxTopK; ++j) {
+        if (j < top_k && (shifting || be[j] < 0 || cp > bp[j])) {
+          const float tp = bp[j];
+          const int te = be[j];
+          bp[j] = cp;
+          be[j] = ce;
+          cp = tp;
+          ce = te;
+          shifting = true;
+        }
+      }
+    }
+  }
+}
+
+// The routing weight of pick j: renormalised over the k picks (summed in pick order) or not.
+__device__ __forceinline__ float route_pick_weight(const float bp[kRouteMaxTopK], int top_k, int renormalize, int j) {
+  float denom = 0.0f;
+#pragma unroll
+  for (int q = 0; q < kRouteMaxTopK; ++q) {
+    if (q < top_k) denom += bp[q];
+  }
+  return renormalize ? bp[j] / denom : bp[j];
+}
+
+constexpr int kRouteWaveMax = 64;  // routed rows and experts of the one-wavefront router
+
+// One wavefront, no barriers, for at most 64 routed rows and 64 experts: lane t < tokens takes token
+// t's softmax and top-k; lane i < tokens * top_k then holds routed entry i (expert sel_i); lane e <
+// num_experts counts its expert by ballots, and prefix sums over lanes give the compacted active
+// experts and their segment / problem offsets; entry i's place in its segment is the number of
+// earlier entries of its expert.  The same outputs as route_topk_small_kernel.
+__global__ __launch_bounds__(kWave) void route_topk_wave_kernel(
+    const float* __restrict__ logits, int tokens, int num_experts, int top_k, int renormalize, int m_tile,
+    uint16_t* __restrict__ weights16, float* __restrict__ weights32, int64_t* __restrict__ selected,
+    int64_t* __restrict__ perm, int64_t* __restrict__ token_idx, int64_t* __restrict__ slots,
+    int32_t* __restrict__ grouped_expert_ids, int32_t* __restrict__ expert_ids, int32_t* __restrict__ segment_offsets,
+    int32_t* __restrict__ problem_offsets, int32_t* __restrict__ counts, int32_t* __restrict__ inverse_perm) {
+  __shared__ float lg[kRouteWaveMax * kRouteWaveMax];  // the logits, [tokens][num_experts]
+  const int lane = static_cast<int>(threadIdx.x);
+  const int total = tokens * top_k;
+  // every load in flight at once (coalesced), then each token reads its row from LDS
+  const int nlog = tokens * num_experts;
+  for (int u0 = 0; u0 < nlog; u0 += 8 * kWave) {  // 8 loads per lane in flight per round
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int idx = u0 + u * kWave + lane;
+      v[u] = logits[idx < nlog ? idx : 0];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int idx = u0 + u * kWave + lane;
+      if (idx < nlog) lg[idx] = v[u];
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  float bp[kRouteMaxTopK];
+  int be[kRouteMaxTopK];
+#pragma unroll
+  for (int j = 0; j < kRouteMaxTopK; ++j) {
+    bp[j] = -1.0f;
+    be[j] = -1;
+  }
+  if (lane < tokens) {
+    route_token_topk(lg + lane * num_experts, num_experts, top_k, bp, be);
+#pragma unroll
+    for (int j = 0; j < kRouteMaxTopK; ++j) {
+      if (j < top_k) {
+        const float w = route_pick_weight(bp, top_k, renormalize, j);
+        const int i = lane * top_k + j;
+        if (selected != nullptr) selected[i] = be[j];
+        weights16[i] = f2h_bits(w);
+        if (weights32 != nullptr) weights32[i] = w;
+      }
+    }
+  }
+  // entry i = t * top_k + j lives in lane t's be[j]
+  int sel_i = -1;
+  {
+    const int t = lane / top_k;
+    const int jj = lane - t * top_k;
+#pragma unroll
+    for (int j = 0; j < kRouteMaxTopK; ++j) {
+      const int v = __shfl(be[j], t < kWave ? t : 0);
+      if (j < top_k && j == jj && lane < total) sel_i = v;
+    }
+  }
+  // per-expert counts (lane e) and each entry's earlier entries of its expert
+  int cnt = 0, before = 0;
+  const uint64_t lower = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+  for (int e = 0; e < num_experts; ++e) {
+    const uint64_t mask = __ballot(sel_i == e);
+    if (lane == e) cnt = __popcll(mask);
+    if (sel_i == e) before = __popcll(mask & lower);
+  }
+  const bool act = lane < num_experts && cnt > 0;
+  const int tiles = act ? (cnt + m_tile - 1) / m_tile : 0;
+  const uint64_t amask = __ballot(act);
+  const int a = __popcll(amask & lower);  // index among active experts
+  int rows_incl = cnt, tiles_incl = tiles;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int vr = __shfl_up(rows_incl, d);
+    const int vt = __shfl_up(tiles_incl, d);
+    if (lane >= d) {
+      rows_incl += vr;
+      tiles_incl += vt;
+    }
+  }
+  const int num_active = __popcll(amask);
+  const int rows_total = __shfl(rows_incl, kWave - 1);
+  const int tiles_total = __shfl(tiles_incl, kWave - 1);
+  const int seg_start = rows_incl - cnt;  // first row of lane e's segment
+  if (act) {
+    expert_ids[a] = lane;
+    segment_offsets[a] = seg_start;
+    problem_offsets[a] = tiles_incl - tiles;
+  }
+  for (int j = num_active + lane; j < num_experts; j += kWave) expert_ids[j] = -1;
+  for (int j = num_active + lane; j <= num_experts; j += kWave) {
+    segment_offsets[j] = rows_total;
+    problem_offsets[j] = tiles_total;
+  }
+  if (lane == 0) {
+    counts[0] = num_active;
+    counts[1] = tiles_total;
+  }
+  const int seg_of = __shfl(seg_start, sel_i >= 0 ? sel_i : 0);
+  if (lane < total) {
+    const int dst = seg_of + before;
+    perm[dst] = lane;
+    token_idx[dst] = lane / top_k;
+    slots[dst] = lane % top_k;
+    grouped_expert_ids[dst] = sel_i;
+    if (inverse_perm != nullptr) inverse_perm[lane] = dst;
+  }
+}
+
 // One workgroup: per token softmax (fp32, max-subtracted, summed in expert
 // order), top-k by probability with ties to the lower expert id (a stable
 // descending sort, as the oracle's argsort), optional renormalisation over the
@@ -156,48 +318,13 @@ __global__ __launch_bounds__(kRouteThreads) void route_topk_small_kernel(
   __syncthreads();
   // ---- softmax and top-k, one token per thread
   for (int t = tid; t < tokens; t += kRouteThreads) {
-    const float* row = logits + static_cast<int64_t>(t) * num_experts;
-    float m = row[0];
-    for (int e = 1; e < num_experts; ++e) m = fmaxf(m, row[e]);
-    float sum = 0.0f;
-    for (int e = 0; e < num_experts; ++e) sum += expf(row[e] - m);
     float bp[kRouteMaxTopK];
     int be[kRouteMaxTopK];
-#pragma unroll
-    for (int j = 0; j < kRouteMaxTopK; ++j) {
-      bp[j] = -1.0f;
-      be[j] = -1;
-    }
-    for (int e = 0; e < num_experts; ++e) {
-      const float pe = expf(row[e] - m) / sum;
-      // insert after every kept entry with probability >= pe (earlier experts win ties)
-      if (pe > bp[top_k - 1] || be[top_k - 1] < 0) {
-        float cp = pe;
-        int ce = e;
-        bool shifting = false;  // once placed, every later entry moves down one
-#pragma unroll
-        for (int j = 0; j < kRouteMaxTopK; ++j) {
-          if (j < top_k && (shifting || be[j] < 0 || cp > bp[j])) {
-            const float tp = bp[j];
-            const int te = be[j];
-            bp[j] = cp;
-            be[j] = ce;
-            cp = tp;
-            ce = te;
-            shifting = true;
-          }
-        }
-      }
-    }
-    float denom = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kRouteMaxTopK; ++j) {
-      if (j < top_k) denom += bp[j];
-    }
+    route_token_topk(logits + static_cast<int64_t>(t) * num_experts, num_experts, top_k, bp, be);
 #pragma unroll
     for (int j = 0; j < kRouteMaxTopK; ++j) {
       if (j < top_k) {
-        const float w = renormalize ? bp[j] / denom : bp[j];
+        const float w = route_pick_weight(bp, top_k, renormalize, j);
         const int i = t * top_k + j;
         sel[i] = static_cast<int16_t>(be[j]);
         if (selected != nullptr) selected[i] = be[j];
@@ -334,6 +461,13 @@ extern "C" int tris_route_topk_grouped(const float* router_logits, int32_t num_t
   TRIS_REQUIRE(num_tokens == 0 || (router_logits && routing_weights_f16 && perm && grouped_token_indices &&
                                    grouped_slots && grouped_expert_ids),
                "%s: null pointer", who);
+  if (static_cast<int64_t>(num_tokens) * top_k <= kRouteWaveMax && num_experts <= kRouteWaveMax) {
+    hipLaunchKernelGGL(route_topk_wave_kernel, dim3(1), dim3(kWave), 0, static_cast<hipStream_t>(stream),
+                       router_logits, num_tokens, num_experts, top_k, renormalize, m_tile, routing_weights_f16,
+                       routing_weights_f32, selected_experts, perm, grouped_token_indices, grouped_slots,
+                       grouped_expert_ids, expert_ids, segment_offsets, problem_offsets, counts, inverse_perm);
+    return check_launch(who);
+  }
   hipLaunchKernelGGL(route_topk_small_kernel, dim3(1), dim3(kRouteThreads), 0, static_cast<hipStream_t>(stream),
                      router_logits, num_tokens, num_experts, top_k, renormalize, m_tile, routing_weights_f16,
                      routing_weights_f32, selected_experts, perm, grouped_token_indices, grouped_slots,

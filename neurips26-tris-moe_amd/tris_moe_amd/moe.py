@@ -166,6 +166,9 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     main = torch.cuda.current_stream(dev)
     side = _side_stream(dev)
     side.wait_stream(main)
+
+    # one launch for the three projections (the persistent GEMMs assume the whole GPU, so nothing runs
+    # beside them)
     with torch.cuda.stream(side):
         order = (("gate", pg), ("up", pu), ("down", pd))
         ext.grouped_block_gr_predecode_multi(

@@ -128,13 +128,14 @@ def test_gr_decode_malformed_streams_follow_reference(tris, oracle_mod, cuda, k)
     np.testing.assert_array_equal(got.cpu().numpy(), want)
 
 
-@pytest.mark.parametrize("experts,packed_rows,n", [(1, 64, 3200), (3, 128, 2048), (2, 128, 14336)],
-                         ids=["1600blk", "6144blk", "28672blk"])
+@pytest.mark.parametrize("experts,packed_rows,n", [(1, 64, 3200), (3, 128, 2048), (2, 128, 14336), (5, 128, 14336)],
+                         ids=["1600blk", "6144blk", "28672blk", "71680blk"])
 def test_predecode_large_grids(tris, oracle_mod, cuda, experts, packed_rows, n):
-    """Block counts that select each lanes-per-block width of the decoder."""
+    """Block counts that select each lanes-per-block width of the decoder (32 lanes up to 8192 blocks,
+    16 up to 65536, 8 above)."""
     note(f"predecode large E={experts} rows={packed_rows} n={n}")
-    rng = np.random.default_rng(packed_rows + n)
-    denses = [random_bitmap(rng, packed_rows, n, p) for p in (0.15, 0.02, 0.5)[:experts]]
+    rng = np.random.default_rng(packed_rows + n + experts)
+    denses = [random_bitmap(rng, packed_rows, n, (0.15, 0.02, 0.5, 0.3, 0.08)[i]) for i in range(experts)]
     words, offsets, meta = stacked_gr(oracle_mod, denses)
     ids = np.arange(experts, dtype=np.int32)[::-1].copy()
     nblk = (packed_rows // 2) * (n // 64)
@@ -239,10 +240,12 @@ def test_route_matches_oracle(tris, oracle_mod, cuda, t, k, e):
     assert int(got["total_problem_tiles"][0]) == want["total_problem_tiles"]
 
 
-@pytest.mark.parametrize("t,k,e", [(1, 2, 8), (16, 2, 8), (16, 8, 64), (7, 8, 256), (256, 8, 128)])
+@pytest.mark.parametrize("t,k,e", [(1, 2, 8), (16, 2, 8), (32, 2, 64), (8, 8, 60), (4, 16, 16), (3, 1, 64),
+                                   (16, 8, 64), (33, 2, 8), (7, 8, 256), (256, 8, 128)])
 def test_route_topk_fused_matches_oracle(tris, oracle_mod, cuda, t, k, e):
     """Fused softmax / top-k / route: the selection and the route are exactly the oracle's
-    (stable argsort of the fp32 softmax), weights within one fp16 ulp."""
+    (stable argsort of the fp32 softmax), weights within one fp16 ulp.  Up to 64 routed rows and 64
+    experts one wavefront does it (the first six cases, at its limits); otherwise one workgroup."""
     note(f"route topk fused t={t} k={k} e={e}")
     rng = np.random.default_rng(t * 100 + e)
     logits = rng.standard_normal((t, e)).astype(np.float32)
@@ -257,6 +260,11 @@ def test_route_topk_fused_matches_oracle(tris, oracle_mod, cuda, t, k, e):
     na = len(want["expert_ids"])
     np.testing.assert_array_equal(r["expert_ids"].cpu().numpy()[:na], np.asarray(want["expert_ids"]))
     np.testing.assert_array_equal(r["segment_offsets"].cpu().numpy()[: na + 1], np.asarray(want["segment_offsets"]))
+    np.testing.assert_array_equal(r["problem_offsets"].cpu().numpy()[: na + 1], np.asarray(want["problem_offsets"]))
+    # padding to num_experts segments: no expert, empty segments at the end
+    assert (r["expert_ids"].cpu().numpy()[na:] == -1).all()
+    assert (r["segment_offsets"].cpu().numpy()[na:] == t * k).all()
+    assert (r["problem_offsets"].cpu().numpy()[na:] == want["problem_offsets"][-1]).all()
     np.testing.assert_allclose(r["routing_weights"].cpu().numpy(), w, rtol=2e-6, atol=1e-7)
     got16 = r["routing_weights_f16"].cpu().numpy().view(np.int16).astype(np.int32)
     want16 = w.astype(np.float16).view(np.int16).astype(np.int32)
