@@ -52,6 +52,10 @@ def parse_args():
                     help="only run the dominant kernel eagerly --kernel-reps times (a target for rocprofv3 --pmc)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run a device-to-device copy of this many bytes 5 times (counter calibration)")
+    ap.add_argument("--streaming", action="store_true",
+                    help="only measure C4: 32 Mixtral layers at T=8 with whole-layer payloads streamed from pinned "
+                         "host memory through two device slots, for p = 0.05, 0.15, 0.30 (one JSON line)")
+    ap.add_argument("--stream-layers", type=int, default=32)
     return ap.parse_args()
 
 
@@ -85,6 +89,9 @@ def main():
     tris_moe_amd.load_library()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.streaming:
+        streaming_bench(args, dev)
+        return
     t0 = time.time()
     layer = synthetic.make_layer(SPEC, args.seed, ext.gr_encode)
     log(f"synthetic layer generated in {time.time() - t0:.1f}s")
@@ -313,6 +320,88 @@ def profile_dominant_kernel(args, layer, payloads, backbones, spec, dev):
         launch(payloads, dec[0], dec[1])
     torch.cuda.synchronize()
     print(json.dumps({"kernel": kname, "kind": kind, "launches": args.kernel_reps, "bytes_per_launch": nbytes}))
+
+
+def streaming_bench(args, dev):
+    """C4: a 32-layer Mixtral MoE stack at T = 8 (each layer's input the previous layer's output) with every
+    layer's compressed payload and backbones streamed from pinned host memory into two device slots, the next
+    layer's copy overlapping the current layer's kernels; against the same stack resident in HBM.  One
+    synthetic layer per split-bitmap density is shared by all 32 layers' host blobs (the copies are real)."""
+    import numpy as np
+    import torch
+
+    from tris_moe_amd import ext, moe, qlinear, streaming, synthetic
+    from tris_moe_amd.configs import C4_DENSITIES, C4_STREAMING as SPEC
+
+    T = SPEC.tokens[0]
+    L = args.stream_layers
+    results = {}
+    for p in C4_DENSITIES:
+        t0 = time.time()
+        layer = synthetic.make_layer(SPEC, args.seed, ext.gr_encode, gmap_p=p)
+        host = [{q: layer[q] for q in streaming.PROJECTIONS} for _ in range(L)]
+        bbs = [layer["backbones"] for _ in range(L)]
+        st = streaming.GroupedPayloadStreamer(host, dev, num_slots=2, backbones=bbs)
+        log(f"C4 p={p}: layer generated and {L} pinned blobs of {st.layer_nbytes(0) / 1e6:.1f} MB packed in "
+            f"{time.time() - t0:.1f}s")
+        inp = synthetic.make_inputs(SPEC, T, args.seed + T, layer["outlier_idx"])
+        x16 = torch.from_numpy(inp["x"]).to(dev).to(torch.bfloat16).to(torch.float16)
+        rng = np.random.default_rng(args.seed)
+        logits = [torch.from_numpy(rng.standard_normal((T, SPEC.num_experts)).astype(np.float32)).to(dev)
+                  for _ in range(L)]
+
+        def timed(fn, reps=3):
+            fn()
+            fn()
+            torch.cuda.synchronize()
+            s_, e_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s_.record()
+            for _ in range(reps):
+                fn()
+            e_.record()
+            torch.cuda.synchronize()
+            return s_.elapsed_time(e_) / reps / 1e3
+
+        stream_s = timed(lambda: streaming.streamed_forward(st, x16, logits, SPEC.top_k, SPEC.renormalize,
+                                                            SPEC.num_experts))
+        # variant: backbones resident (L x 23 MB on the device), only the expert payloads streamed
+        st_e = streaming.GroupedPayloadStreamer(host, dev, num_slots=2, backbones=None)
+        bb_res = [{q: torch.from_numpy(layer["backbones"][q]).to(dev) for q in streaming.PROJECTIONS} for _ in range(L)]
+        stream_e_s = timed(lambda: streaming.streamed_forward(st_e, x16, logits, SPEC.top_k, SPEC.renormalize,
+                                                              SPEC.num_experts, backbones=bb_res))
+        expert_bytes = st_e.layer_nbytes(0)
+        # the same stack resident in HBM: L distinct device copies (so every layer reads HBM, not the cache)
+        pl0 = {q: qlinear.payload_to_device(layer[q], dev) for q in streaming.PROJECTIONS}
+        bb0 = {q: torch.from_numpy(layer["backbones"][q]).to(dev) for q in streaming.PROJECTIONS}
+        pls = [{q: {k: (v.clone() if isinstance(v, torch.Tensor) else v) for k, v in pl0[q].items()}
+                for q in streaming.PROJECTIONS} for _ in range(L)]
+        bbs_dev = [{q: v.clone() for q, v in bb0.items()} for _ in range(L)]
+
+        def resident():
+            x = x16
+            for i in range(L):
+                x = moe.grouped_moe_forward_from_logits(x, logits[i], SPEC.top_k, SPEC.renormalize, pls[i],
+                                                        bbs_dev[i], SPEC.num_experts, torch.bfloat16).to(torch.float16)
+        resident_s = timed(resident)
+        layer_bytes = st.layer_nbytes(0)
+        results[f"p{p}"] = {
+            "tokens_per_s": round(T / stream_s, 1), "ms_per_forward": round(stream_s * 1e3, 3),
+            "resident_ms_per_forward": round(resident_s * 1e3, 3), "layer_bytes": int(layer_bytes),
+            "h2d_gbps": round(L * layer_bytes / stream_s / 1e9, 2),
+            "device_slot_bytes": int(2 * st.slot_bytes), "resident_model_bytes": int(L * layer_bytes),
+            "experts_only": {"tokens_per_s": round(T / stream_e_s, 1), "ms_per_forward": round(stream_e_s * 1e3, 3),
+                             "layer_bytes": int(expert_bytes),
+                             "h2d_gbps": round(L * expert_bytes / stream_e_s / 1e9, 2)}}
+        log(f"C4 p={p}: streamed {stream_s * 1e3:.2f} ms / {L} layers ({T / stream_s:.0f} tok/s, "
+            f"{L * layer_bytes / stream_s / 1e9:.1f} GB/s host-to-device), experts only {stream_e_s * 1e3:.2f} ms, "
+            f"resident {resident_s * 1e3:.2f} ms")
+        del st, st_e, bb_res, host, bbs, pl0, bb0, pls, bbs_dev
+        torch.cuda.synchronize()
+    print(json.dumps({"metric": "C4 MoE-stack tokens/sec with whole-layer payload streaming (pinned host -> 2 "
+                      "device slots), Mixtral-8x7B shape", "unit": "tokens/s", "n_gpus": 1,
+                      "config": {"workload": f"mixtral8x7b_moe_stack_{L}layers_T{T}_streamed", "layers": L,
+                                 "tokens": T, "slots": 2, "data": "synthetic"},
+                      "results": results}), flush=True)
 
 
 def cpu_baseline(layer, res, spec):
