@@ -555,6 +555,19 @@ def backbone_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+# From this many rows on the backbone is a plain dense GEMM better served by the library GEMM (hipBLASLt
+# through F.linear, as the reference's compute_shared_hidden, qlinear_cuda.py:4454-4502); below it, the
+# decode-shaped split-K MFMA kernel of tris_backbone_linear.
+BACKBONE_LIBRARY_MIN_ROWS = 256
+
+
+def _backbone_library(x, svs, in_scale, row_index):
+    xs = x.index_select(0, row_index) if row_index is not None else x
+    if in_scale is not None:
+        xs = xs * in_scale  # fp16 products, as x * ns_col
+    return [torch.nn.functional.linear(xs, sv) for sv in svs]
+
+
 def backbone_linear(x: torch.Tensor, sv: torch.Tensor, in_scale: torch.Tensor | None = None,
                     row_index: torch.Tensor | None = None) -> torch.Tensor:
     """hidden = fp16(x[row_index] * in_scale) @ sv^T with fp32 accumulation (compute_shared_hidden)."""
@@ -568,6 +581,8 @@ def backbone_linear(x: torch.Tensor, sv: torch.Tensor, in_scale: torch.Tensor | 
     if in_scale is not None:
         _check_cuda("in_scale", in_scale, torch.float16, 1, x.device)
     rank, in_f = int(sv.size(0)), int(sv.size(1))
+    if tokens >= BACKBONE_LIBRARY_MIN_ROWS:
+        return _backbone_library(x, (sv,), in_scale, row_index)[0]
     out = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
     lib = _lib.load()
     ws = backbone_workspace(x.device, int(lib.tris_backbone_workspace_bytes(tokens, in_f, rank)))
@@ -588,6 +603,9 @@ def backbone_linear_pair(x: torch.Tensor, sv_a: torch.Tensor, sv_b: torch.Tensor
     if row_index is not None:
         _check_cuda("row_index", row_index, torch.int64, 1, x.device)
     rank, in_f = int(sv_a.size(0)), int(sv_a.size(1))
+    if tokens >= BACKBONE_LIBRARY_MIN_ROWS:
+        out_a, out_b = _backbone_library(x, (sv_a, sv_b), None, row_index)
+        return out_a, out_b
     out_a = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
     out_b = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
     lib = _lib.load()

@@ -499,8 +499,10 @@ def test_run_grouped_structured_api(tris, oracle_mod, cuda):
 
 # ------------------------------------------------------------------ backbone
 @pytest.mark.parametrize("tokens,in_f,rank", [(1, 4096, 512), (16, 4096, 512), (5, 14336, 512), (37, 2048, 256),
-                                              (4, 1000, 100)])
+                                              (4, 1000, 100), (300, 4096, 512)])
 def test_backbone_matches_fp32(tris, cuda, tokens, in_f, rank):
+    """Decode-sized inputs run the split-K MFMA kernel; from ext.BACKBONE_LIBRARY_MIN_ROWS rows (the last
+    case, and its gathered rows) the library GEMM."""
     note(f"backbone T={tokens} in={in_f} rank={rank}")
     rng = np.random.default_rng(tokens + in_f)
     x = rng.standard_normal((tokens, in_f)).astype(np.float16)
@@ -567,6 +569,16 @@ def test_layer_mixtral_c1_decode(tris, oracle_mod, cuda, tokens, path):
     note(f"layer C1 Mixtral T={tokens} path={path}")
     out, want = _run_layer(tris, oracle_mod, cuda, C1_MIXTRAL_DECODE, tokens, 2000 + tokens, path)
     assert_close(out, want, f"C1 layer T={tokens} {path}")
+
+
+def test_layer_mixtral_prefill_shape(tris, oracle_mod, cuda):
+    """C2's layer shape at 160 tokens (320 routed rows): multi-tile segments in the grouped GEMMs and the
+    library GEMM for the backbones."""
+    from tris_moe_amd.configs import C2_MIXTRAL_PREFILL
+
+    note("layer C2 Mixtral prefill shape T=160")
+    out, want = _run_layer(tris, oracle_mod, cuda, C2_MIXTRAL_PREFILL, 160, 4000)
+    assert_close(out, want, "C2-shape layer T=160")
 
 
 def test_layer_a3b_c3_with_shared_expert(tris, oracle_mod, cuda):
