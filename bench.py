@@ -35,6 +35,7 @@ for p in (str(ROOT), str(PKG)):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBPS = 8000.0
+MFMA_FP16_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA, MI355X
 
 
 def parse_args():
@@ -56,6 +57,10 @@ def parse_args():
                     help="only measure C4: 32 Mixtral layers at T=8 with whole-layer payloads streamed from pinned "
                          "host memory through two device slots, for p = 0.05, 0.15, 0.30 (one JSON line)")
     ap.add_argument("--stream-layers", type=int, default=32)
+    ap.add_argument("--prefill", type=int, default=2048,
+                    help="C2 prefill tokens measured into 'prefill' (0 for none)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="measure only the C2 prefill step and print its JSON object")
     return ap.parse_args()
 
 
@@ -150,6 +155,9 @@ def main():
     if args.profile_kernel:
         profile_dominant_kernel(args, layer, base_payloads, base_backbones, SPEC, dev)
         return
+    if args.prefill_only:
+        print(json.dumps(prefill_bench(args, layer, copies, dev)), flush=True)
+        return
     main_res = measure(args.tokens, args.steps, args.warmup)
     log(f"T={args.tokens}: {main_res['ms_per_step'] * 1e3:.1f} us/step, {main_res['tokens_per_s']:.0f} tok/s, "
         f"{main_res['hbm_gbps']:.0f} GB/s")
@@ -216,6 +224,8 @@ def main():
                 "kernel": kname, "kernel_us": round(kernel_s * 1e6, 2), "bytes_per_launch": int(kbytes)}
     log(f"gate/up grouped GEMM ({kind}): {kernel_s * 1e6:.1f} us/launch, {achieved:.0f} GB/s algorithmic")
 
+    prefill = prefill_bench(args, layer, copies, dev) if args.prefill > 0 else None
+
     cpu = None
     if args.cpu_baseline:
         cpu = cpu_baseline(layer, main_res, SPEC)
@@ -243,8 +253,55 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "sweep": sweep,
+        "prefill": prefill,
     }
     print(json.dumps(line), flush=True)
+
+
+def layer_flops_per_token(spec) -> int:
+    """Algorithmic flops of one token through the layer: gate/up backbones, top_k x (gate/up expert GEMMs, down
+    backbone, down expert GEMM)."""
+    h, r, i, k = spec.hidden, spec.rank, spec.intermediate, spec.top_k
+    return 2 * (2 * h * r) + k * (2 * (2 * r * i) + 2 * i * r + 2 * r * h)
+
+
+def prefill_bench(args, layer, copies, dev):
+    """C2: the same layer weights at --prefill tokens with N(0, 1) router logits,
+    one full layer step (eager launches) per layer copy in turn; MFMA-bound, reported against the dense
+    fp16 MFMA peak."""
+    import torch
+
+    from tris_moe_amd import moe, synthetic
+    from tris_moe_amd.configs import C2_MIXTRAL_PREFILL as SPEC2
+
+    T = args.prefill
+    inp = synthetic.make_inputs(SPEC2, T, args.seed + T, layer["outlier_idx"])
+    x16 = torch.from_numpy(inp["x"]).to(dev).to(torch.bfloat16).to(torch.float16)
+    logits = torch.from_numpy(inp["router_logits"]).to(dev)
+
+    def step(i):
+        pl, bb = copies[i % len(copies)]
+        return moe.grouped_moe_forward_from_logits(x16, logits, SPEC2.top_k, SPEC2.renormalize, pl, bb,
+                                                   SPEC2.num_experts, torch.bfloat16)
+
+    for i in range(3):
+        step(i)
+    torch.cuda.synchronize()
+    steps = max(2 * len(copies), 20)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        step(i)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    flops = layer_flops_per_token(SPEC2) * T
+    tflops = flops / (ms / 1e3) / 1e12
+    log(f"prefill T={T}: {ms:.3f} ms/step, {T / (ms / 1e3):.0f} tok/s, {tflops:.1f} TFLOP/s")
+    return {"workload": f"mixtral8x7b_moe_layer_prefill_T{T}", "tokens": T, "steps": steps,
+            "ms_per_step": round(ms, 4), "tokens_per_s": round(T / (ms / 1e3), 1),
+            "tflops": round(tflops, 2), "mfma_peak_tflops": MFMA_FP16_PEAK_TFLOPS,
+            "mfma_frac": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4), "flops_per_token": layer_flops_per_token(SPEC2)}
 
 
 def gateup_kernel(ext, moe, synthetic, layer, rows, active, spec, hid_g, hid_u, eid, seg, prob, dev):

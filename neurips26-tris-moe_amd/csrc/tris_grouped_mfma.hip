@@ -341,7 +341,7 @@ __device__ __forceinline__ void mf_chunk_issue(const MfmaProj& pa, int e, int ro
 // Write a unit's register-staged chunk to LDS (waits for those loads).  Salient columns get zero
 // C_d / C_nd, so the main pass gives them zero weights whatever their selector bits.
 __device__ __forceinline__ void mf_chunk_write(const MfmaProj& pa, int rc, int kc, int utid, const MfChunk& ch,
-                                               const MfRegs& R) {
+                                               const MfRegs& R, bool natural = false) {
   const tris_compact3_payload& p = pa.p;
   const int rank = p.rank;
   const int G = p.num_groups;
@@ -367,7 +367,7 @@ __device__ __forceinline__ void mf_chunk_write(const MfmaProj& pa, int rc, int k
   for (int h = 0; h < 2; ++h) {
     const int j = utid + h * kMfThreads;
     const int k = kc + j;
-    const int pj = (j & ~31) + mf_perm32(j & 31);
+    const int pj = natural ? j : (j & ~31) + mf_perm32(j & 31);
     const int bit = k & 31;
     const uint32_t cm = R.cmt[h];
     const bool sal = k < rank && ((cm >> bit) & 1u);
@@ -429,6 +429,88 @@ __device__ __forceinline__ void mf_tile_issue(const MfmaProj& pa, int s, int e, 
 // One projection over one staged chunk and output tile [n0, n0 + 64): accumulates rows 4 * kg + v,
 // column n0 + 16 * wave + lane % 16 of x . W^T into acc.  xrow is the staged activation row this
 // lane's A operand reads.
+// Exact B operand of the lane's column for packed row j: the 8 weights k = kg + 4m.  Per packed row the
+// lane builds nibble selectors: bit 1 = this term is used, bit 3 = negative (shared by both terms; the
+// unused term is a signed zero); w = fma(sd, fp16(C_d * R_d), sn * fp16(C_nd * R_nd)).
+__device__ __forceinline__ f16x8 mf_row_b(uint32_t qw, uint32_t gw, const uint4& cdv, const uint4& cnv, uint32_t rs2,
+                                          uint32_t shl, uint32_t rot) {
+  const f16x2 rd2 = u32_as_f16x2(__builtin_amdgcn_perm(rs2, rs2, 0x01000100u));
+  const f16x2 rn2 = u32_as_f16x2(__builtin_amdgcn_perm(rs2, rs2, 0x03020302u));
+  const uint32_t cd[4] = {cdv.x, cdv.y, cdv.z, cdv.w};
+  const uint32_t cn[4] = {cnv.x, cnv.y, cnv.z, cnv.w};
+  const uint32_t neg3 = ~(qw << shl) & 0x88888888u;
+  const uint32_t sd = (__builtin_rotateright32(gw, rot) & 0x22222222u) | neg3;  // d term: fp4 +-1.0, else +-0
+  const uint32_t sn = sd ^ 0x22222222u;                                        // nd term: the others
+  uint32_t b[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f16x2 pd = u32_as_f16x2(cd[i]) * rd2;
+    const f16x2 pn = u32_as_f16x2(cn[i]) * rn2;
+    const f16x2 tn = fp4x2_to_f16x2(sn, i) * pn;
+    b[i] = f16x2_as_u32(__builtin_elementwise_fma(fp4x2_to_f16x2(sd, i), pd, tn));
+  }
+  return __builtin_bit_cast(f16x8, make_uint4(b[0], b[1], b[2], b[3]));
+}
+
+// Bit m of b (m < 8) to bit 4m.
+__device__ __forceinline__ uint32_t spread8(uint32_t b) {
+  b = (b | (b << 12)) & 0x000F000Fu;
+  b = (b | (b << 6)) & 0x03030303u;
+  return (b | (b << 3)) & 0x11111111u;
+}
+
+// mf_row_b for the natural column order: the lane's 8 weights are k = 8 kg + m (m < 8), so the A operand is 16
+// contiguous bytes of an activation row.  The selector bits of those columns are byte kg of the packed words,
+// spread to one nibble each.
+__device__ __forceinline__ f16x8 mf_row_b_nat(uint32_t qw, uint32_t gw, const uint4& cdv, const uint4& cnv,
+                                              uint32_t rs2, int kg) {
+  const f16x2 rd2 = u32_as_f16x2(__builtin_amdgcn_perm(rs2, rs2, 0x01000100u));
+  const f16x2 rn2 = u32_as_f16x2(__builtin_amdgcn_perm(rs2, rs2, 0x03020302u));
+  const uint32_t cd[4] = {cdv.x, cdv.y, cdv.z, cdv.w};
+  const uint32_t cn[4] = {cnv.x, cnv.y, cnv.z, cnv.w};
+  const uint32_t q4 = spread8(__builtin_amdgcn_ubfe(qw, 8u * kg, 8u));
+  const uint32_t g4 = spread8(__builtin_amdgcn_ubfe(gw, 8u * kg, 8u));
+  const uint32_t sd = (g4 << 1) | ((q4 ^ 0x11111111u) << 3);  // d term: fp4 +-1.0, else +-0; bit 3 = negative
+  const uint32_t sn = sd ^ 0x22222222u;                        // nd term: the others
+  uint32_t b[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f16x2 pd = u32_as_f16x2(cd[i]) * rd2;
+    const f16x2 pn = u32_as_f16x2(cn[i]) * rn2;
+    const f16x2 tn = fp4x2_to_f16x2(sn, i) * pn;
+    b[i] = f16x2_as_u32(__builtin_elementwise_fma(fp4x2_to_f16x2(sd, i), pd, tn));
+  }
+  return __builtin_bit_cast(f16x8, make_uint4(b[0], b[1], b[2], b[3]));
+}
+
+// Salient window [w0, w0 + wn) of the chunk (wn <= kMfSalWin): lane group kg writes the exact fp16 weights
+// w = fp16(+-fp16(C0 * R0) +- fp16(C1 * R1)) of column tc for window slots kg, kg + 4, ... into its wave's
+// ws row i16 (every slot, zero past wn, with no per-slot branch so the LDS reads overlap).  q2w holds the
+// lane's qweight2_sparse words of rows q2b and q2b + 1 (a window spans at most two).
+__device__ __forceinline__ void mf_salient_weights(const MfChunk& ch, const MfTileBuf& tb, const uint32_t* r01t,
+                                                   int tc, int kg, int wave, int i16, int sbase0, int w0, int wn,
+                                                   int q2b, const uint32_t q2w[2], uint16_t (*ws)[16][kMfSalStride]) {
+  uint16_t wv[kMfSalWin / 4];
+#pragma unroll
+  for (int u = 0; u < kMfSalWin / 4; ++u) {
+    const int q = 4 * u + kg;
+    const bool qv = q < wn;
+    const int c = ch.sal_col[w0 + (qv ? q : 0)];  // chunk column
+    const uint32_t w1 = tb.q1[(c >> 5) * kMfQ1Stride + tc];
+    const uint32_t rr = r01t[(c >> 6) * kTileOut + tc];
+    const uint32_t cp = ch.col_sal[c];
+    const int sidx = sbase0 + w0 + q;  // qweight2_sparse index
+    const uint32_t q2 = ((sidx >> 5) - q2b) == 0 ? q2w[0] : q2w[1];
+    // sign bits: positive where the qweight1 / qweight2 bit is set
+    const uint32_t neg = ((~(w1 >> (c & 31)) & 1u) << 15) | ((~(q2 >> (sidx & 31)) & 1u) << 31);
+    const f16x2 t = __builtin_bit_cast(f16x2, f16x2_as_u32(u32_as_f16x2(cp) * u32_as_f16x2(rr)) ^ neg);
+    const _Float16 w = t[0] + t[1];
+    wv[u] = qv ? __builtin_bit_cast(uint16_t, w) : static_cast<uint16_t>(0);
+  }
+#pragma unroll
+  for (int u = 0; u < kMfSalWin / 4; ++u) ws[wave][i16][4 * u + kg] = wv[u];
+}
+
 // The lane's qweight2_sparse words of the chunk's first salient window (a window of kMfSalWin salient
 // columns spans at most two qweight2_sparse rows), for output column n.  Issued before the next tile's
 // LDS copies so that waiting for them does not wait for the copies.
@@ -508,23 +590,8 @@ __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, i
     return r;
   };
   auto row_mfma = [&](const Row& r, uint32_t rs2) {
-    const f16x2 rd2 = u32_as_f16x2(__builtin_amdgcn_perm(rs2, rs2, 0x01000100u));
-    const f16x2 rn2 = u32_as_f16x2(__builtin_amdgcn_perm(rs2, rs2, 0x03020302u));
-    const uint32_t cd[4] = {r.cd.x, r.cd.y, r.cd.z, r.cd.w};
-    const uint32_t cn[4] = {r.cn.x, r.cn.y, r.cn.z, r.cn.w};
-    const uint32_t neg3 = ~(r.qw << shl) & 0x88888888u;
-    const uint32_t sd = (__builtin_rotateright32(r.gw, rot) & 0x22222222u) | neg3;  // d term: fp4 +-1.0, else +-0
-    const uint32_t sn = sd ^ 0x22222222u;                                           // nd term: the others
-    uint32_t b[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const f16x2 pd = u32_as_f16x2(cd[i]) * rd2;
-      const f16x2 pn = u32_as_f16x2(cn[i]) * rn2;
-      const f16x2 tn = fp4x2_to_f16x2(sn, i) * pn;
-      b[i] = f16x2_as_u32(__builtin_elementwise_fma(fp4x2_to_f16x2(sd, i), pd, tn));
-    }
-    const f16x8 bv = __builtin_bit_cast(f16x8, make_uint4(b[0], b[1], b[2], b[3]));
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, r.av), bv, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, r.av),
+                                                 mf_row_b(r.qw, r.gw, r.cd, r.cn, rs2, shl, rot), acc, 0, 0, 0);
   };
   if (npr == kMfPR) {  // a full chunk
     Row cur = load_row(0);
@@ -559,25 +626,7 @@ __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, i
         q2w[h] = bload32(r_q2, rv ? v_q2 : q2_bytes, static_cast<uint32_t>(rv ? q2b + h : 0) * N * 4u);
       }
     }
-    uint16_t wv[kMfSalWin / 4];
-#pragma unroll
-    for (int u = 0; u < kMfSalWin / 4; ++u) {
-      const int q = 4 * u + kg;
-      const bool qv = q < wn;
-      const int c = ch.sal_col[w0 + (qv ? q : 0)];  // chunk column
-      const uint32_t w1 = tb.q1[(c >> 5) * kMfQ1Stride + tc];
-      const uint32_t rr = r01t[(c >> 6) * kTileOut + tc];
-      const uint32_t cp = ch.col_sal[c];
-      const int sidx = sbase0 + w0 + q;  // qweight2_sparse index
-      const uint32_t q2 = ((sidx >> 5) - q2b) == 0 ? q2w[0] : q2w[1];
-      // sign bits: positive where the qweight1 / qweight2 bit is set
-      const uint32_t neg = ((~(w1 >> (c & 31)) & 1u) << 15) | ((~(q2 >> (sidx & 31)) & 1u) << 31);
-      const f16x2 t = __builtin_bit_cast(f16x2, f16x2_as_u32(u32_as_f16x2(cp) * u32_as_f16x2(rr)) ^ neg);
-      const _Float16 w = t[0] + t[1];
-      wv[u] = qv ? __builtin_bit_cast(uint16_t, w) : static_cast<uint16_t>(0);
-    }
-#pragma unroll
-    for (int u = 0; u < kMfSalWin / 4; ++u) ws[wave][i16][4 * u + kg] = wv[u];
+    mf_salient_weights(ch, tb, r01t, tc, kg, wave, i16, sbase0, w0, wn, q2b, q2w, ws);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
     uint32_t ap[4];
@@ -768,11 +817,422 @@ __global__ __launch_bounds__(kUnits * kMfThreads) void grouped_mfma_kernel(MfmaA
   }  // row tiles
 }
 
+// ----------------------------------------------------------------------------------------------------
+// Weight-stationary variant for long segments (prefill).  A work item is (active segment, 64-column output
+// tile): the unit copies the tile's weight words, builds the exact B operands of its column over the whole
+// K (rank <= 512: 16 packed rows, 4 registers each, plus at most two 32-column salient windows) once, and
+// streams the segment's 16-row activation tiles through them: per row tile 16 + 2 MFMAs per wavefront,
+// with the next row tile's loads in flight meanwhile (two activation buffers).  kUnits == 2 runs the
+// gate and up projections of the same item side by side and writes fp16(silu(g) * u).
+constexpr int kWsSalWindows = 2;  // salient columns per item <= 64
+constexpr int kWsMinRows = 64;    // mean rows per active segment from which the host picks this kernel
+#ifndef TRIS_WS_SUB
+#define TRIS_WS_SUB 1
+#endif
+constexpr int kWsSub = TRIS_WS_SUB;  // output tiles per item
+#ifndef TRIS_WS_READ_AHEAD
+#define TRIS_WS_READ_AHEAD 4
+#endif
+constexpr int kWsReadAhead = TRIS_WS_READ_AHEAD;  // A-operand LDS reads in flight ahead of the MFMAs
+#ifndef TRIS_WS_XDEPTH
+#define TRIS_WS_XDEPTH 1
+#endif
+constexpr int kWsXDepth = TRIS_WS_XDEPTH;  // row tiles of activations in flight in registers (1 or 2)
+static_assert(kWsXDepth == 1 || kWsXDepth == 2, "activation prefetch depth is 1 or 2");
+
+struct MfWsLayout {  // per unit, byte offsets into dynamic LDS
+  int xs[2], cds, cns, col_sal, sal_col, meta, r01t, ws, bytes;
+};
+
+__host__ __device__ inline MfWsLayout mf_ws_layout() {
+  MfWsLayout L;
+  int o = 0;
+  L.xs[0] = mf_take(&o, kMfRows * kMfXStride * 2);
+  L.xs[1] = mf_take(&o, kMfRows * kMfXStride * 2);
+  L.cds = mf_take(&o, kMfChunk * 2);
+  L.cns = mf_take(&o, kMfChunk * 2);
+  L.col_sal = mf_take(&o, kMfChunk * 4);
+  L.sal_col = mf_take(&o, kMfChunk * 2);
+  L.meta = mf_take(&o, 16 * 4);
+  L.r01t = mf_take(&o, kMfTiles * kTileOut * 4);
+  L.ws = mf_take(&o, kMfWaves * 16 * kMfSalStride * 2);
+  L.bytes = o;
+  return L;
+}
+
+__host__ __device__ inline int mf_ws_lds_bytes(int units, int sub) {
+  return units * mf_ws_layout().bytes + (units == 2 ? sub * kMfExchBytes : 0);
+}
+
+// Activation rows [row0, row0 + rc) of the chunk: register loads (issued early) and the permuted LDS write.
+struct WsX {
+  uint4 xv[kMfRuns];
+};
+
+__device__ __forceinline__ void ws_x_issue(const MfmaProj& pa, int row0, int rc, int utid, WsX& X) {
+  const int rank = pa.p.rank;
+  const int wave = utid / kWave;
+  const int lane = utid % kWave;
+  const uint32_t hid_bytes = static_cast<uint32_t>(rc) * rank * 2u;
+  const __amdgpu_buffer_rsrc_t r_hid = make_rsrc(pa.hidden + static_cast<int64_t>(row0) * rank, hid_bytes);
+#pragma unroll
+  for (int h = 0; h < kMfRuns; ++h) {
+    const int r = 4 * h + wave;
+    const int c = lane * 8;
+    const uint32_t voff = (r < rc && c < rank) ? static_cast<uint32_t>(r * rank + c) * 2u : hid_bytes;
+    X.xv[h] = bload128(r_hid, voff, 0u);
+  }
+}
+
+// Writes every staged row in natural column order (rows >= rc get the zeros their loads returned): one
+// 16-byte LDS write per run, a wave's 64 runs one contiguous kilobyte.
+__device__ __forceinline__ void ws_x_write(int utid, uint16_t* xs, const WsX& X) {
+  const int wave = utid / kWave;
+  const int lane = utid % kWave;
+#pragma unroll
+  for (int h = 0; h < kMfRuns; ++h) {
+    const int r = 4 * h + wave;
+    *reinterpret_cast<uint4*>(&xs[r * kMfXStride + lane * 8]) = X.xv[h];
+  }
+}
+
+// Work split: item (segment a, kSub output tiles from tile kSub * i) costs t_a + kWsBuildCost row tiles (t_a:
+// the segment's row tiles; building the B operands costs about kWsBuildCost of them).  Items are ordered
+// segment-major and the workgroup of virtual index v takes those whose cost prefix starts in
+// [v * total / W, (v + 1) * total / W): each lane works out the item range of its segment, so no item list
+// exists anywhere.  Virtual indices are XCD-major: the hardware places workgroup w on XCD w % 8, and each
+// XCD gets a contiguous share of the items, so its L2 holds the activations of about one segment instead
+// of every XCD streaming every segment.
+constexpr int kWsBuildCost = 2;
+constexpr int kXcds = 8;  // MI355X: 8 XCDs (32 CUs and one L2 each)
+
+__device__ __forceinline__ int xcd_major_index(int w, int W) {
+  const int x = w % kXcds;
+  const int q = W / kXcds;
+  const int r = W % kXcds;
+  return x * q + (x < r ? x : r) + w / kXcds;
+}
+
+// kSub output tiles per item: wavefront w computes columns 16 w + (0..15) of each, so one activation read
+// from LDS feeds kSub MFMAs (B operands: 16 packed rows x kSub x 4 registers).  Activations are staged in
+// natural column order (a plain copy) and the B operands built for it (mf_row_b_nat).
+template <int kUnits, int kSub>
+__global__ __launch_bounds__(kUnits * kMfThreads) void grouped_mfma_ws_kernel(MfmaArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char mf_lds[];
+  __shared__ __attribute__((aligned(16))) uint32_t ws_tb[kUnits][kSub][kMfTbWords];
+  const int unit = kUnits == 2 ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kMfThreads) : 0;
+  const int utid = static_cast<int>(threadIdx.x) % kMfThreads;
+  const MfmaProj& pa = a.proj[kUnits == 2 ? unit : blockIdx.z];
+  const tris_compact3_payload& p = pa.p;
+  const int N = p.outfeatures;
+  const int G = p.num_groups;
+  const int nob = ceil_div(N, kTileOut);
+  const int nit = ceil_div(nob, kSub);  // items per segment
+  const int npr = p.rank / 32;          // <= kMfPR: rank <= kMfChunk (host-checked)
+  const int wave = __builtin_amdgcn_readfirstlane(utid / kWave);
+  const int lane = utid % kWave;
+  const int i16 = lane % 16;
+  const int kg = lane / 16;
+  const int tc = 16 * wave + i16;
+  uint16_t* out = kUnits == 2 ? a.proj[0].out : pa.out;
+
+  // segments (<= 64, host-checked): lane i holds segment i
+  const MfSegScan sc = mf_scan_segments(a.segment_offsets, a.expert_ids, a.num_segments, kMfRows);
+  const bool act = static_cast<int>(__lane_id()) < a.num_segments && sc.t > 0;
+  const int u = act ? sc.t + kWsBuildCost : 0;
+  int incl = u;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int v = __shfl_up(incl, d);
+    if (static_cast<int>(__lane_id()) >= d) incl += v;
+  }
+  const int64_t total = static_cast<int64_t>(nit) * __shfl(incl, kWave - 1);
+  const int64_t W = gridDim.x;
+  const int64_t vw = xcd_major_index(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const int64_t lo_w = vw * total / W;
+  const int64_t hi_w = (vw + 1) * total / W;
+  const int64_t base = static_cast<int64_t>(nit) * (incl - u);
+  int it_lo = 0, it_hi = 0;
+  if (act) {
+    const int64_t d0 = lo_w - base, d1 = hi_w - base;
+    it_lo = d0 <= 0 ? 0 : static_cast<int>((d0 + u - 1) / u);
+    it_hi = d1 <= 0 ? 0 : static_cast<int>((d1 + u - 1) / u);
+    it_lo = it_lo < nit ? it_lo : nit;
+    it_hi = it_hi < nit ? it_hi : nit;
+  }
+  uint64_t todo = __ballot(act && it_hi > it_lo);
+
+  const MfWsLayout L = mf_ws_layout();
+  unsigned char* lbase = mf_lds + unit * L.bytes;
+  MfChunk ch;
+  ch.xs = nullptr;
+  ch.cds = reinterpret_cast<uint16_t*>(lbase + L.cds);
+  ch.cns = reinterpret_cast<uint16_t*>(lbase + L.cns);
+  ch.col_sal = reinterpret_cast<uint32_t*>(lbase + L.col_sal);
+  ch.sal_col = reinterpret_cast<uint16_t*>(lbase + L.sal_col);
+  ch.meta = reinterpret_cast<int32_t*>(lbase + L.meta);
+  uint16_t* const xsb0 = reinterpret_cast<uint16_t*>(lbase + L.xs[0]);
+  uint16_t* const xsb1 = reinterpret_cast<uint16_t*>(lbase + L.xs[1]);
+  // column kMfChunk of every staged row stays zero (the activation writes cover columns 0 .. 511): the salient
+  // gather's padding slots read it
+  if (utid < 2 * kMfRows) (utid < kMfRows ? xsb0 : xsb1)[(utid % kMfRows) * kMfXStride + kMfChunk] = 0;
+  uint32_t* r01t = reinterpret_cast<uint32_t*>(lbase + L.r01t);
+  auto ws = reinterpret_cast<uint16_t (*)[16][kMfSalStride]>(lbase + L.ws);
+  float* exch = reinterpret_cast<float*>(mf_lds + kUnits * L.bytes);
+  MfTileBuf tb[kSub];
+#pragma unroll
+  for (int b = 0; b < kSub; ++b) {
+    tb[b].q1 = &ws_tb[unit][b][kMfTbQ1];
+    tb[b].gw = &ws_tb[unit][b][kMfTbGw];
+    tb[b].rs = &ws_tb[unit][b][kMfTbRs];
+  }
+  while (todo != 0) {
+    const int s = __ffsll(static_cast<unsigned long long>(todo)) - 1;  // wave-uniform
+    todo &= todo - 1;
+    const int seg_lo = __builtin_amdgcn_readfirstlane(__shfl(sc.lo, s));
+    const int seg_hi = __builtin_amdgcn_readfirstlane(__shfl(sc.hi, s));
+    const int e = __builtin_amdgcn_readfirstlane(__shfl(sc.ex, s));
+    const int it0 = __builtin_amdgcn_readfirstlane(__shfl(it_lo, s));
+    const int it1 = __builtin_amdgcn_readfirstlane(__shfl(it_hi, s));
+    const int rows = seg_hi - seg_lo;
+    if (e < 0 || e >= p.num_experts) {  // rows routed to no expert: zero output
+      if (unit == 0) {
+        const int n_lo = it0 * kSub * kTileOut;
+        const int n_hi = (it1 * kSub * kTileOut) < N ? it1 * kSub * kTileOut : N;
+        const int span = n_hi - n_lo;
+        for (int idx = utid; idx < rows * span; idx += kMfThreads) {
+          out[static_cast<int64_t>(seg_lo + idx / span) * N + n_lo + idx % span] = 0;
+        }
+      }
+      continue;
+    }
+    const int nrt = ceil_div(rows, kMfRows);
+    for (int it = it0; it < it1; ++it) {
+      const int ob = it * kSub;
+      __syncthreads();  // the previous item's LDS readers are done
+#pragma unroll
+      for (int b = 0; b < kSub; ++b) {
+        if (ob + b < nob) mf_tile_issue(pa, s, e, 0, ob + b, utid, tb[b]);  // uniform; copies into LDS only
+      }
+      if (it == it0) {  // the segment's column data
+        MfRegs regs;
+        mf_chunk_issue(pa, e, seg_lo, 0, 0, utid, regs);  // rc = 0: no activation rows
+        mf_chunk_write(pa, 0, 0, utid, ch, regs, true);  // natural column order
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      int n[kSub];
+      bool nv[kSub];
+#pragma unroll
+      for (int b = 0; b < kSub; ++b) {
+        n[b] = (ob + b) * kTileOut + tc;
+        nv[b] = n[b] < N;
+      }
+      const int sbase0 = __builtin_amdgcn_readfirstlane(ch.meta[8]);
+      const int num_sal = __builtin_amdgcn_readfirstlane(ch.meta[9]) - sbase0;
+      uint32_t q2w[kSub][kWsSalWindows + 1];  // qweight2_sparse words of the rows the windows span
+      {
+        const int q2rows = p.qweight2_sparse_rows;
+        const uint32_t q2_bytes = static_cast<uint32_t>(q2rows) * N * 4u;
+        const __amdgpu_buffer_rsrc_t r_q2 =
+            make_rsrc(p.qweight2_sparse + static_cast<int64_t>(e) * q2rows * N, q2_bytes);
+#pragma unroll
+        for (int b = 0; b < kSub; ++b) {
+          const uint32_t v_q2 = nv[b] ? static_cast<uint32_t>(n[b]) * 4u : q2_bytes;
+#pragma unroll
+          for (int h = 0; h <= kWsSalWindows; ++h) {
+            const int row = (sbase0 >> 5) + h;
+            const bool rv = num_sal > 0 && row < q2rows;
+            q2w[b][h] = bload32(r_q2, rv ? v_q2 : q2_bytes, static_cast<uint32_t>(rv ? row : 0) * N * 4u);
+          }
+        }
+      }
+      // the first two row tiles' activations, in flight while the B operands are built; row tile rt's
+      // registers are X[rt % 2], reloaded with row tile rt + 2 once staged
+      WsX X0, X1;
+      ws_x_issue(pa, seg_lo, rows < kMfRows ? rows : kMfRows, utid, X0);
+      if (kWsXDepth == 2 && nrt > 1) {
+        ws_x_issue(pa, seg_lo + kMfRows, (rows - kMfRows) < kMfRows ? rows - kMfRows : kMfRows, utid, X1);
+      }
+
+      // columns of the salient activations of each window, two 16-bit offsets a word, in the A operand's slot
+      // order (padding slots point at the zero column kMfChunk)
+      uint32_t soff[kWsSalWindows][4];
+#pragma unroll
+      for (int win = 0; win < kWsSalWindows; ++win) {
+        const int w0 = win * kMfSalWin;
+        const int wn = (num_sal - w0) < kMfSalWin ? (num_sal - w0) : kMfSalWin;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int q0 = 8 * kg + 2 * i;
+          uint32_t lo = kMfChunk, hi = kMfChunk;
+          if (q0 < wn) {
+            const int c = ch.sal_col[w0 + q0];
+            lo = static_cast<uint32_t>(c);
+          }
+          if (q0 + 1 < wn) {
+            const int c = ch.sal_col[w0 + q0 + 1];
+            hi = static_cast<uint32_t>(c);
+          }
+          soff[win][i] = lo | (hi << 16);
+        }
+      }
+      // ---- B operands over the whole K, per output tile: the packed rows, then the salient windows (the
+      // row scales R0 | R1 << 16 go through r01t, rewritten per tile)
+      f16x8 bmain[kSub][kMfPR];
+      f16x8 bsal[kSub][kWsSalWindows];
+#pragma unroll
+      for (int b = 0; b < kSub; ++b) {
+#pragma unroll
+        for (int t = 0; t < kMfTiles; ++t) {
+          const int g = __builtin_amdgcn_readfirstlane(ch.meta[t]);
+          const int gi = (tc * G + (g >= 0 ? g : 0)) * 2;
+          const uint32_t rdn = g >= 0 ? tb[b].rs[gi + 1] : 0u;
+          if ((t & 3) == kg) r01t[t * kTileOut + tc] = g >= 0 ? tb[b].rs[gi] : 0u;
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) {
+            const int j = 2 * t + jj;
+            bmain[b][j] = f16x8{};
+            if (j < npr) {  // uniform
+              const int kl = j * 32 + 8 * kg;
+              bmain[b][j] = mf_row_b_nat(tb[b].q1[j * kMfQ1Stride + tc], tb[b].gw[j * kTileOut + tc],
+                                         *reinterpret_cast<const uint4*>(&ch.cds[kl]),
+                                         *reinterpret_cast<const uint4*>(&ch.cns[kl]), rdn, kg);
+            }
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();  // r01t written
+#pragma unroll
+        for (int win = 0; win < kWsSalWindows; ++win) {
+          const int w0 = win * kMfSalWin;
+          const int wn = (num_sal - w0) < kMfSalWin ? (num_sal - w0) : kMfSalWin;
+          bsal[b][win] = f16x8{};
+          if (wn > 0) {  // uniform
+            const int q2b = (sbase0 + w0) >> 5;
+            const uint32_t q2pair[2] = {q2w[b][win], q2w[b][win + 1]};
+            mf_salient_weights(ch, tb[b], r01t, tc, kg, wave, i16, sbase0, w0, wn, q2b, q2pair, ws);
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            bsal[b][win] = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&ws[wave][i16][8 * kg]));
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();  // ws (and, after the last window, r01t) are rewritten next
+          }
+        }
+      }
+
+      // ---- the segment's row tiles through the stationary B operands
+      auto row_tile = [&](int rt, uint16_t* xs, WsX& X) {
+        const int row0 = seg_lo + rt * kMfRows;
+        const int rc = (seg_hi - row0) < kMfRows ? (seg_hi - row0) : kMfRows;
+        ws_x_write(utid, xs, X);
+        __syncthreads();  // staged rows visible; the previous row tile's exch reads are done
+        if (rt + kWsXDepth < nrt) {  // depth 1: X0 is the only register set (both call sites pass it)
+          const int r2 = row0 + kWsXDepth * kMfRows;
+          ws_x_issue(pa, r2, (seg_hi - r2) < kMfRows ? (seg_hi - r2) : kMfRows, utid, X);
+        }
+        const uint16_t* xr = xs + i16 * kMfXStride;
+        f32x4 acc[kSub];
+#pragma unroll
+        for (int b = 0; b < kSub; ++b) acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        // activations at the salient columns of window win (their A operand)
+        auto sal_gather = [&](int win) {
+          uint32_t ap[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = xr[soff[win][i] & 0xFFFFu];
+            const uint32_t hi = xr[soff[win][i] >> 16];
+            ap[i] = lo | (hi << 16);
+          }
+          return __builtin_bit_cast(f16x8, make_uint4(ap[0], ap[1], ap[2], ap[3]));
+        };
+        auto row_mfma = [&](int j) {
+          const f16x8 av = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&xr[j * 32 + 8 * kg]));
+#pragma unroll
+          for (int b = 0; b < kSub; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bmain[b][j], acc[b], 0, 0, 0);
+        };
+        // window 0 always runs (zero weights and the zero column when the chunk has no salient column), so it
+        // joins the main block: its gathers are issued first and its MFMA comes last
+        const f16x8 as0 = sal_gather(0);
+        if (npr == kMfPR) {  // rank 512: no branch between the MFMAs, so the LDS reads run ahead of them
+#pragma unroll
+          for (int j = 0; j < kMfPR; ++j) row_mfma(j);
+#pragma unroll
+          for (int b = 0; b < kSub; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as0, bsal[b][0], acc[b], 0, 0, 0);
+          // schedule: kWsReadAhead A reads, then one MFMA group per further read
+          __builtin_amdgcn_sched_group_barrier(0x100, kWsReadAhead, 0);
+#pragma unroll
+          for (int j = kWsReadAhead; j < kMfPR; ++j) {
+            __builtin_amdgcn_sched_group_barrier(0x008, kSub, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
+          __builtin_amdgcn_sched_group_barrier(0x008, (kWsReadAhead + 1) * kSub, 0);
+        } else {
+#pragma unroll
+          for (int j = 0; j < kMfPR; ++j) {
+            if (j < npr) row_mfma(j);  // uniform
+          }
+#pragma unroll
+          for (int b = 0; b < kSub; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as0, bsal[b][0], acc[b], 0, 0, 0);
+        }
+#pragma unroll
+        for (int win = 1; win < kWsSalWindows; ++win) {
+          if (win * kMfSalWin < num_sal) {  // uniform
+            const f16x8 av = sal_gather(win);
+#pragma unroll
+            for (int b = 0; b < kSub; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bsal[b][win], acc[b], 0, 0, 0);
+          }
+        }
+        if (kUnits == 2) {
+          if (unit == 1) {
+#pragma unroll
+            for (int b = 0; b < kSub; ++b) *reinterpret_cast<f32x4*>(&exch[(b * kMfThreads + utid) * 4]) = acc[b];
+          }
+          __syncthreads();
+          if (unit == 0) {
+#pragma unroll
+            for (int b = 0; b < kSub; ++b) {
+              const f32x4 up = *reinterpret_cast<const f32x4*>(&exch[(b * kMfThreads + utid) * 4]);
+#pragma unroll
+              for (int v = 0; v < 4; ++v) {
+                const int r = 4 * kg + v;
+                if (nv[b] && r < rc) {
+                  out[static_cast<int64_t>(row0 + r) * N + n[b]] = swiglu_bits(f2h_bits(acc[b][v]), f2h_bits(up[v]));
+                }
+              }
+            }
+          }
+        } else {
+#pragma unroll
+          for (int b = 0; b < kSub; ++b) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const int r = 4 * kg + v;
+              if (nv[b] && r < rc) out[static_cast<int64_t>(row0 + r) * N + n[b]] = f2h_bits(acc[b][v]);
+            }
+          }
+        }
+      };
+      // two activation buffers in alternation (distinct objects per call site)
+      for (int rt = 0; rt < nrt; rt += 2) {
+        row_tile(rt, xsb0, X0);
+        if (rt + 1 < nrt) row_tile(rt + 1, xsb1, kWsXDepth == 2 ? X1 : X0);
+      }
+    }
+  }
+}
+
 int check_payload(const tris_compact3_payload* p, bool need_gr, const char* who);
 
 static bool allow_mfma_lds(const void* kernel, int bytes) {
-  static int granted[2] = {0, 0};
-  const int which = kernel == reinterpret_cast<const void*>(&grouped_mfma_kernel<1>) ? 0 : 1;
+  // dynamic LDS granted so far per kernel (the four instantiations of the two kernels)
+  static const void* kernels[4] = {reinterpret_cast<const void*>(&grouped_mfma_kernel<1>),
+                                   reinterpret_cast<const void*>(&grouped_mfma_kernel<2>),
+                                   reinterpret_cast<const void*>(&grouped_mfma_ws_kernel<1, kWsSub>),
+                                   reinterpret_cast<const void*>(&grouped_mfma_ws_kernel<2, kWsSub>)};
+  static int granted[4] = {0, 0, 0, 0};
+  int which = 0;
+  while (which < 3 && kernels[which] != kernel) ++which;
   if (bytes <= granted[which]) return true;
   // Raising the dynamic LDS limit is not a stream operation, so it is safe while a caller captures a graph.
   if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
@@ -781,6 +1241,43 @@ static bool allow_mfma_lds(const void* kernel, int bytes) {
   }
   granted[which] = bytes;
   return true;
+}
+
+// Weight-stationary launch (long segments, one 512-column chunk, <= 64 salient columns per expert):
+// workgroups as the GPU holds at once (the occupancy the compiled kernel allows with this LDS), no more
+// than the items.
+static int launch_grouped_mfma_ws(const MfmaArgs& args, int units, int nproj, int max_n, hipStream_t s,
+                                  const char* who) {
+  const int lds = mf_ws_lds_bytes(units, kWsSub);
+  const int lds_total = lds + units * kWsSub * kMfTbWords * 4;
+  TRIS_REQUIRE(lds_total <= 160 * 1024, "%s: LDS request %d exceeds a CU", who, lds_total);
+  const void* kernel = units == 2 ? reinterpret_cast<const void*>(&grouped_mfma_ws_kernel<2, kWsSub>)
+                                  : reinterpret_cast<const void*>(&grouped_mfma_ws_kernel<1, kWsSub>);
+  TRIS_REQUIRE(allow_mfma_lds(kernel, lds), "%s: %s", who, "cannot raise the kernel's dynamic LDS limit");
+  static int per_cu[2] = {0, 0};  // resident workgroups per CU, per kernel (queried once)
+  int& wgs_per_cu = per_cu[units - 1];
+  if (wgs_per_cu == 0) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel, units * kMfThreads, lds) != hipSuccess) {
+      (void)hipGetLastError();
+      nb = 1;
+    }
+    wgs_per_cu = nb > 0 ? nb : 1;
+  }
+  int wgs = (kMfCus * wgs_per_cu) / nproj;
+  const int64_t items = static_cast<int64_t>(args.num_segments) * ceil_div(ceil_div(max_n, kTileOut), kWsSub);
+  if (items < wgs) wgs = static_cast<int>(items);
+  const dim3 grid(wgs > 0 ? wgs : 1, 1, nproj);
+  if (units == 2) {
+    hipLaunchKernelGGL((grouped_mfma_ws_kernel<2, kWsSub>), grid, dim3(2 * kMfThreads), lds, s, args);
+  } else {
+    hipLaunchKernelGGL((grouped_mfma_ws_kernel<1, kWsSub>), grid, dim3(kMfThreads), lds, s, args);
+  }
+  return check_launch(who);
+}
+
+static bool ws_fits(const tris_compact3_payload* p) {
+  return p->rank <= kMfChunk && p->qweight2_sparse_rows <= kWsSalWindows && !p->has_output_scale && !p->has_bias;
 }
 
 int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int batch, const int32_t* expert_ids,
@@ -817,6 +1314,13 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
   args.lds_groups = pa->num_groups;
   if (pb && pb->num_groups > args.lds_groups) args.lds_groups = pb->num_groups;
   const int units = swiglu ? 2 : 1;
+  const int nproj = (pb && !swiglu) ? 2 : 1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // long segments: keep each output tile's weights in registers and stream the segment's rows through them
+  if (num_segments <= kWave && static_cast<int64_t>(batch) >= static_cast<int64_t>(kWsMinRows) * num_segments &&
+      ws_fits(pa) && (!pb || ws_fits(pb))) {
+    return launch_grouped_mfma_ws(args, units, nproj, max_n, s, who);
+  }
   const int lds = mf_lds_bytes(units, args.xs_rows, args.lds_groups);
   const int lds_total = lds + mf_static_lds_bytes(units);
   TRIS_REQUIRE(lds_total <= 160 * 1024, "%s: LDS request %d exceeds a CU", who, lds_total);
@@ -826,14 +1330,12 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
   const int by_regs = 3 / units;
   wgs_per_cu = wgs_per_cu < by_regs ? wgs_per_cu : by_regs;
   wgs_per_cu = wgs_per_cu > 0 ? wgs_per_cu : 1;
-  const int nproj = (pb && !swiglu) ? 2 : 1;
   int wgs = (kMfCus * wgs_per_cu) / nproj;
   // no more than the (row tile, output tile) pairs there can be: row tiles <= batch / 16 + min(segments, batch)
   const int64_t pairs =
       (static_cast<int64_t>(batch) / kMfRows + (num_segments < batch ? num_segments : batch)) * ceil_div(max_n, kTileOut);
   if (pairs < wgs) wgs = static_cast<int>(pairs);
   const dim3 grid(wgs > 0 ? wgs : 1, 1, nproj);
-  hipStream_t s = static_cast<hipStream_t>(stream);
   if (swiglu) {
     TRIS_REQUIRE(allow_mfma_lds(reinterpret_cast<const void*>(&grouped_mfma_kernel<2>), lds), "%s: %s", who,
                  "cannot raise the kernel's dynamic LDS limit");

@@ -37,6 +37,10 @@ def assert_close(got, want, what):
     assert max_abs <= MAX_ABS and rel <= REL_L2, f"{what}: max_abs={max_abs:.3g} rel_l2={rel:.3g}"
 
 
+def ceil_div(a, b):
+    return (a + b - 1) // b
+
+
 def t_i32(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(dev)
 
@@ -291,6 +295,7 @@ GEMM_CASES = [
     dict(E=3, n=100, k=96, seg=[5, 2, 9]),                               # ragged shapes
     dict(E=3, n=128, k=256, seg=[4, 4, 4], scale=True, bias=True),       # epilogue
     dict(E=2, n=128, k=256, seg=[6, 6], g_idx="alternating"),            # non-uniform groups
+    dict(E=3, n=200, k=512, seg=[130, 0, 75], scale=True, bias=True, salient_counts=[64, 0, 33]),  # long
 ]
 
 
@@ -388,22 +393,29 @@ def test_dual_and_predecoded_match(tris, oracle_mod, cuda):
     assert_close(pb2.cpu().numpy(), oracle_grouped(oracle_mod, pb, hb.cpu().numpy(), ids, offs, True), "dual pre b")
 
 
-@pytest.mark.parametrize("rank,n,salient", [(256, 128, None), (512, 192, [0, 40]), (128, 64, [7, 0])])
-def test_predecoded_mfma_one_hot_is_bit_exact(tris, oracle_mod, cuda, rank, n, salient):
+@pytest.mark.parametrize("split", [None, 16], ids=["whole", "split16"])
+@pytest.mark.parametrize("rank,n,salient", [(256, 128, None), (512, 192, [0, 40]), (128, 64, [7, 0]),
+                                            (512, 136, [64, 17])])
+def test_predecoded_mfma_one_hot_is_bit_exact(tris, oracle_mod, cuda, rank, n, salient, split):
     """With one-hot activation rows the MFMA grouped GEMM returns single dequantised weights, which
     must equal the reference's fp16 weights bit for bit: every lane group, packed row, split bit,
-    sign and salient column of the operand construction is checked."""
-    note(f"mfma one-hot rank={rank} n={n}")
+    sign and salient column of the operand construction is checked.  Each expert gets `rank` rows (row r
+    is e_r), as one segment (long segments: the weight-stationary kernel) or as segments of `split` rows
+    of the same expert (the row-tile kernel)."""
+    note(f"mfma one-hot rank={rank} n={n} split={split}")
     ext = tris["ext"]
     E = 2
     pay = make_projection(tris, 70 + rank, E, n, rank, salient_counts=salient)
     d = tris["qlinear"].payload_to_device(pay, cuda)
-    ids, offs = _segments([rank, rank], E)   # each expert gets `rank` rows: row r of a segment is e_r
-    rows = int(offs[-1])
+    step = rank if split is None else split
+    ids = np.repeat(np.arange(E, dtype=np.int32), ceil_div(rank, step))
+    offs = np.concatenate([[0], np.cumsum([min(step, rank - c) for _ in range(E) for c in range(0, rank, step)])])
+    offs = offs.astype(np.int32)
+    rows = E * rank
     h = np.zeros((rows, rank), dtype=np.float16)
-    for s in range(E):
+    for e in range(E):
         for r in range(rank):
-            h[offs[s] + r, r] = 1.0
+            h[e * rank + r, r] = 1.0
     hd = torch.from_numpy(h).to(cuda)
     prob = np.concatenate([[0], np.cumsum((np.diff(offs) + 3) // 4)]).astype(np.int32)
     nblk = tris["synthetic"].packing.num_gr_blocks(rank, n)
@@ -414,23 +426,55 @@ def test_predecoded_mfma_one_hot_is_bit_exact(tris, oracle_mod, cuda, rank, n, s
         hd, t_i32(ids, cuda), t_i32(offs, cuda), t_i32(prob, cuda), int(prob[-1]), dec, d["qweight1"],
         d["qweight2_sparse"], d["qweight2_sparse_prefix"], d["c_map"], d["g_idx"], d["col_pack3"], d["row_pack3"],
         True).cpu().numpy()
-    for s, e in enumerate(ids):
-        w = oracle_mod.dequant_grouped_expert(pay, int(e), True)   # [n, rank] fp16
-        np.testing.assert_array_equal(got[offs[s]:offs[s + 1]].view(np.uint16), w.T.astype(np.float16).view(np.uint16))
+    for e in range(E):
+        w = oracle_mod.dequant_grouped_expert(pay, e, True)   # [n, rank] fp16
+        np.testing.assert_array_equal(got[e * rank:(e + 1) * rank].view(np.uint16),
+                                      w.T.astype(np.float16).view(np.uint16))
 
 
-def test_swiglu_fused_matches_dual_then_silu(tris, oracle_mod, cuda):
+@pytest.mark.parametrize("drop", [None, 0])
+def test_predecoded_long_segments(tris, oracle_mod, cuda, drop):
+    """Segments of 64 rows and more (the weight-stationary MFMA kernel): ragged N (a partial output tile),
+    rows not a multiple of 16, a full second salient window (64 salient columns) and, with drop=0, a
+    segment routed to no expert (zero rows)."""
+    note(f"predecoded long segments drop={drop}")
+    ext = tris["ext"]
+    E, n, k = 3, 200, 512
+    pay = make_projection(tris, 81, E, n, k, salient_counts=[64, 0, 33])
+    d = tris["qlinear"].payload_to_device(pay, cuda)
+    ids, offs = _segments([130, 0, 75], E, drop)
+    prob = np.concatenate([[0], np.cumsum((np.diff(offs) + 3) // 4)]).astype(np.int32)
+    rng = np.random.default_rng(12)
+    rows = int(offs[-1])
+    h = (rng.standard_normal((rows, k)) * 1.5).astype(np.float16)
+    nblk = tris["synthetic"].packing.num_gr_blocks(k, n)
+    dec = torch.empty((ids.size, nblk, 128), dtype=torch.int32, device=cuda)
+    ext.compact3_tris_precomputed_grouped_block_gr_predecode(
+        dec, t_i32(ids, cuda), d["q_gmap_gr_words"], d["q_gmap_gr_offsets"], d["q_gmap_gr_meta"], k // 32, n)
+    got = ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
+        torch.from_numpy(h).to(cuda), t_i32(ids, cuda), t_i32(offs, cuda), t_i32(prob, cuda), int(prob[-1]), dec,
+        d["qweight1"], d["qweight2_sparse"], d["qweight2_sparse_prefix"], d["c_map"], d["g_idx"], d["col_pack3"],
+        d["row_pack3"], True).cpu().numpy()
+    want = oracle_grouped(oracle_mod, pay, h, ids, offs, True)
+    assert_close(got.astype(np.float32), want.astype(np.float32), f"long segments drop={drop}")
+    if drop is not None:
+        assert not got[offs[drop]:offs[drop + 1]].any()
+
+
+@pytest.mark.parametrize("seg", [[3, 21, 0, 9], [90, 150, 0, 70]], ids=["short", "long"])
+def test_swiglu_fused_matches_dual_then_silu(tris, oracle_mod, cuda, seg):
     """The fused gate/up GEMM + SwiGLU equals silu(g) * u computed from the dual kernel's own fp16
     outputs with the oracle's fp16 roundings; exp may differ in its last fp32 bit from numpy's,
-    so a rare one-ulp difference is allowed."""
-    note("swiglu fused")
+    so a rare one-ulp difference is allowed.  Long segments run the weight-stationary kernel, whose
+    dual outputs are also checked against the oracle."""
+    note(f"swiglu fused seg={seg}")
     ext = tris["ext"]
     E, k, n = 4, 256, 320
     pa = make_projection(tris, 61, E, n, k)
     pb = make_projection(tris, 62, E, n, k)
     da = tris["qlinear"].payload_to_device(pa, cuda)
     db = tris["qlinear"].payload_to_device(pb, cuda)
-    ids, offs = _segments([3, 21, 0, 9], E)
+    ids, offs = _segments(seg, E)
     prob = np.concatenate([[0], np.cumsum((np.diff(offs) + 3) // 4)]).astype(np.int32)
     rng = np.random.default_rng(9)
     rows = int(offs[-1])
@@ -449,6 +493,8 @@ def test_swiglu_fused_matches_dual_then_silu(tris, oracle_mod, cuda):
     fused = ext.compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded(
         ha, hb, *args, dec[0], *[da[x] for x in names], dec[1], *[db[x] for x in names]).cpu().numpy()
     g, u = g.cpu().numpy(), u.cpu().numpy()
+    assert_close(g, oracle_grouped(oracle_mod, pa, ha.cpu().numpy(), ids, offs, True), "dual gate")
+    assert_close(u, oracle_grouped(oracle_mod, pb, hb.cpu().numpy(), ids, offs, True), "dual up")
     want = (oracle_mod.silu_f16(g).astype(np.float32) * u.astype(np.float32)).astype(np.float16)
     ulp = np.abs(fused.view(np.int16).astype(np.int32) - want.view(np.int16).astype(np.int32))
     assert ulp.max() <= 1 and (ulp > 0).mean() < 0.01, (int(ulp.max()), float((ulp > 0).mean()))
@@ -571,14 +617,16 @@ def test_layer_mixtral_c1_decode(tris, oracle_mod, cuda, tokens, path):
     assert_close(out, want, f"C1 layer T={tokens} {path}")
 
 
-def test_layer_mixtral_prefill_shape(tris, oracle_mod, cuda):
-    """C2's layer shape at 160 tokens (320 routed rows): multi-tile segments in the grouped GEMMs and the
-    library GEMM for the backbones."""
+@pytest.mark.parametrize("tokens", [160, 512])
+def test_layer_mixtral_prefill_shape(tris, oracle_mod, cuda, tokens):
+    """C2's layer shape at 160 tokens (320 routed rows: multi-tile segments, the row-tile MFMA kernel) and
+    512 tokens (about 128 rows per expert: the weight-stationary kernel), with the library GEMM for the
+    backbones."""
     from tris_moe_amd.configs import C2_MIXTRAL_PREFILL
 
-    note("layer C2 Mixtral prefill shape T=160")
-    out, want = _run_layer(tris, oracle_mod, cuda, C2_MIXTRAL_PREFILL, 160, 4000)
-    assert_close(out, want, "C2-shape layer T=160")
+    note(f"layer C2 Mixtral prefill shape T={tokens}")
+    out, want = _run_layer(tris, oracle_mod, cuda, C2_MIXTRAL_PREFILL, tokens, 4000 + tokens)
+    assert_close(out, want, f"C2-shape layer T={tokens}")
 
 
 def test_layer_a3b_c3_with_shared_expert(tris, oracle_mod, cuda):
