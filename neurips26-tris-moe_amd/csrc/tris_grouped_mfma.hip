@@ -830,6 +830,11 @@ constexpr int kWsMinRows = 64;    // mean rows per active segment from which the
 #define TRIS_WS_SUB 1
 #endif
 constexpr int kWsSub = TRIS_WS_SUB;  // output tiles per item
+#ifndef TRIS_WS_XSTRIDE
+#define TRIS_WS_XSTRIDE 528
+#endif
+constexpr int kWsXStride = TRIS_WS_XSTRIDE;  // fp16 elements per staged activation row (kMfChunk + zero column + pad)
+static_assert(kWsXStride > kMfChunk && kWsXStride % 8 == 0, "staged rows need the zero column and 16-byte runs");
 #ifndef TRIS_WS_READ_AHEAD
 #define TRIS_WS_READ_AHEAD 4
 #endif
@@ -847,8 +852,8 @@ struct MfWsLayout {  // per unit, byte offsets into dynamic LDS
 __host__ __device__ inline MfWsLayout mf_ws_layout() {
   MfWsLayout L;
   int o = 0;
-  L.xs[0] = mf_take(&o, kMfRows * kMfXStride * 2);
-  L.xs[1] = mf_take(&o, kMfRows * kMfXStride * 2);
+  L.xs[0] = mf_take(&o, kMfRows * kWsXStride * 2);
+  L.xs[1] = mf_take(&o, kMfRows * kWsXStride * 2);
   L.cds = mf_take(&o, kMfChunk * 2);
   L.cns = mf_take(&o, kMfChunk * 2);
   L.col_sal = mf_take(&o, kMfChunk * 4);
@@ -892,7 +897,7 @@ __device__ __forceinline__ void ws_x_write(int utid, uint16_t* xs, const WsX& X)
 #pragma unroll
   for (int h = 0; h < kMfRuns; ++h) {
     const int r = 4 * h + wave;
-    *reinterpret_cast<uint4*>(&xs[r * kMfXStride + lane * 8]) = X.xv[h];
+    *reinterpret_cast<uint4*>(&xs[r * kWsXStride + lane * 8]) = X.xv[h];
   }
 }
 
@@ -975,7 +980,7 @@ __global__ __launch_bounds__(kUnits * kMfThreads) void grouped_mfma_ws_kernel(Mf
   uint16_t* const xsb1 = reinterpret_cast<uint16_t*>(lbase + L.xs[1]);
   // column kMfChunk of every staged row stays zero (the activation writes cover columns 0 .. 511): the salient
   // gather's padding slots read it
-  if (utid < 2 * kMfRows) (utid < kMfRows ? xsb0 : xsb1)[(utid % kMfRows) * kMfXStride + kMfChunk] = 0;
+  if (utid < 2 * kMfRows) (utid < kMfRows ? xsb0 : xsb1)[(utid % kMfRows) * kWsXStride + kMfChunk] = 0;
   uint32_t* r01t = reinterpret_cast<uint32_t*>(lbase + L.r01t);
   auto ws = reinterpret_cast<uint16_t (*)[16][kMfSalStride]>(lbase + L.ws);
   float* exch = reinterpret_cast<float*>(mf_lds + kUnits * L.bytes);
@@ -1131,7 +1136,7 @@ __global__ __launch_bounds__(kUnits * kMfThreads) void grouped_mfma_ws_kernel(Mf
           const int r2 = row0 + kWsXDepth * kMfRows;
           ws_x_issue(pa, r2, (seg_hi - r2) < kMfRows ? (seg_hi - r2) : kMfRows, utid, X);
         }
-        const uint16_t* xr = xs + i16 * kMfXStride;
+        const uint16_t* xr = xs + i16 * kWsXStride;
         f32x4 acc[kSub];
 #pragma unroll
         for (int b = 0; b < kSub; ++b) acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};

@@ -7,10 +7,10 @@
 //   1. route_histogram_kernel (one workgroup): per-expert counts in LDS,
 //      a block scan over experts, compacted active expert ids,
 //      segment_offsets, problem_offsets and {num_active, total_tiles}.
-//   2. route_scatter_kernel (one wavefront per active expert): a stable
-//      counting-sort scatter; each wave scans the flattened expert ids in
-//      64-element chunks and places its expert's entries in flat order using
-//      a ballot and a popcount of the lower lanes.
+//   2. route_scatter_kernel (one workgroup per active expert): a stable
+//      counting-sort scatter; each workgroup scans the flattened expert ids in
+//      1024-element chunks and places its expert's entries in flat order using
+//      ballots, a popcount of the lower lanes and the wave totals in LDS.
 // For decode-sized batches route_topk_small_kernel does the router softmax
 // and top-k (modeling_mixtral.py:548-555) and all of the above in one
 // workgroup and one launch.
@@ -101,30 +101,50 @@ __global__ __launch_bounds__(kRouteThreads) void route_histogram_kernel(
   }
 }
 
-__global__ __launch_bounds__(256) void route_scatter_kernel(
+constexpr int kScatterThreads = 1024;
+constexpr int kScatterWaves = kScatterThreads / kWave;
+
+// One workgroup per segment slot: the flattened expert ids are scanned in chunks of kScatterThreads, each
+// chunk's hits of this expert placed in flat order (ballot within a wave, wave totals through LDS), so a
+// segment's entries keep the order of the flat index as in a stable sort.
+__global__ __launch_bounds__(kScatterThreads) void route_scatter_kernel(
     const int64_t* __restrict__ selected, int total, int top_k, int num_experts, const int32_t* __restrict__ expert_ids,
     const int32_t* __restrict__ segment_offsets, int64_t* __restrict__ perm, int64_t* __restrict__ token_idx,
     int64_t* __restrict__ slots, int32_t* __restrict__ grouped_expert_ids, int32_t* __restrict__ inverse_perm) {
-  const int seg = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
-  const int lane = threadIdx.x % kWave;
+  __shared__ int wave_hits[2][kScatterWaves];
+  const int seg = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
   if (seg >= num_experts) return;
   const int e = expert_ids[seg];
-  if (e < 0) return;
+  if (e < 0) return;  // the whole workgroup: an inactive slot
   int pos = segment_offsets[seg];
   const uint64_t lower = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int c = 0; c < total; c += kWave) {
-    const int i = c + lane;
+  int buf = 0;
+  for (int c = 0; c < total; c += kScatterThreads) {
+    const int i = c + tid;
     const bool hit = i < total && selected[i] == e;
     const uint64_t mask = __ballot(hit);
+    if (lane == 0) wave_hits[buf][wave] = __popcll(mask);
+    __syncthreads();  // (two buffers: the next chunk's writes do not race this chunk's reads)
+    int before = 0, chunk = 0;
+#pragma unroll
+    for (int w = 0; w < kScatterWaves; ++w) {
+      const int h = wave_hits[buf][w];
+      before += w < wave ? h : 0;
+      chunk += h;
+    }
     if (hit) {
-      const int dst = pos + __popcll(mask & lower);
+      const int dst = pos + before + __popcll(mask & lower);
       perm[dst] = i;
       token_idx[dst] = i / top_k;
       slots[dst] = i % top_k;
       grouped_expert_ids[dst] = e;
       if (inverse_perm != nullptr) inverse_perm[i] = dst;
     }
-    pos += __popcll(mask);
+    pos += chunk;
+    buf ^= 1;
   }
 }
 
@@ -433,8 +453,7 @@ extern "C" int tris_build_grouped_route(const int64_t* selected_experts, int32_t
   int rc = check_launch("route_histogram_kernel");
   if (rc) return rc;
   if (total == 0 || num_experts == 0) return TRIS_OK;
-  const int waves_per_block = 256 / kWave;
-  hipLaunchKernelGGL(route_scatter_kernel, dim3(ceil_div(num_experts, waves_per_block)), dim3(256), 0, s,
+  hipLaunchKernelGGL(route_scatter_kernel, dim3(num_experts), dim3(kScatterThreads), 0, s,
                      selected_experts, static_cast<int>(total), top_k, num_experts, expert_ids, segment_offsets, perm,
                      grouped_token_indices, grouped_slots, grouped_expert_ids, inverse_perm);
   return check_launch("route_scatter_kernel");

@@ -562,6 +562,10 @@ BACKBONE_LIBRARY_MIN_ROWS = 256
 
 
 def _backbone_library(x, svs, in_scale, row_index):
+    if row_index is not None and x.size(0) < row_index.numel():
+        # more routed rows than tokens (top-k > 1): project each token once, then gather the projected rows
+        xs = x * in_scale if in_scale is not None else x
+        return [torch.nn.functional.linear(xs, sv).index_select(0, row_index) for sv in svs]
     xs = x.index_select(0, row_index) if row_index is not None else x
     if in_scale is not None:
         xs = xs * in_scale  # fp16 products, as x * ns_col
