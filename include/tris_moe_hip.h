@@ -276,6 +276,46 @@ int64_t tris_backbone_pair_workspace_bytes(int32_t tokens, int32_t in_features, 
 int64_t tris_backbone_workspace_bytes(int32_t tokens, int32_t in_features, int32_t rank);
 
 /*
+ * 4-bit packed backbone matrix (PackedQuantMatrix4bit buffers, qlinear_cuda.py:2637-2786):
+ * SV[r][c] = fp16((q - z) * s) with q = nibble c % 8 (bits 4*(c%8)) of qweight[c / 8][r],
+ * z = nibble r % 8 of qzeros[g][r / 8] plus one, s = scales[g][r], g = g_idx[c]
+ * (the reference's dequantize, :2761-2786).
+ */
+typedef struct tris_packed4_matrix {
+  const int32_t* qweight;  /* int32 [ceil(cols / 8), rows] */
+  const int32_t* qzeros;   /* int32 [num_groups, ceil(rows / 8)] */
+  const uint16_t* scales;  /* fp16 [num_groups, rows] */
+  const int32_t* g_idx;    /* int32 [cols] (may be NULL for the fused projection) */
+  int32_t rows;            /* out features (the backbone rank) */
+  int32_t cols;            /* in features */
+  int32_t num_groups;
+  int32_t group_size;      /* > 0 when g_idx[c] == c / group_size for every c, else 0 */
+} tris_packed4_matrix;
+
+/* Dequantise to fp16 out [rows, cols] (any g_idx): the reference's
+ * PackedQuantMatrix4bit.dequantize (qlinear_cuda.py:2761-2786), bit for bit. */
+int tris_packed4_dequant(const tris_packed4_matrix* w, uint16_t* out, void* stream);
+
+/*
+ * hidden = x[row_index] (* in_scale) . SV^T from the packed matrix without materialising SV: replaces
+ * packed4_linear_forward (TriSMoE_cuda_kernel.cu:8023-8137, called by compute_shared_hidden through
+ * _run_packed_4bit_linear_cuda, qlinear_cuda.py:4487-4494).  Same tiling, split-K and workspace
+ * (tris_backbone_workspace_bytes(tokens, cols, rows)) as tris_backbone_linear; exact fp16 weights
+ * and products, fp32 accumulation (the reference's kernels round products or partial sums to fp16;
+ * results agree within the fp16 tolerance).  Needs uniform groups: group_size > 0, a multiple of 8.
+ */
+int tris_packed4_backbone_linear(const uint16_t* x, int32_t tokens, const int64_t* row_index,
+                                 const tris_packed4_matrix* w, const uint16_t* in_scale, uint16_t* out,
+                                 void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Gate and up packed backbones of the same rows in one launch (no reference counterpart; see
+ * tris_backbone_linear_pair).  Workspace: tris_backbone_pair_workspace_bytes. */
+int tris_packed4_backbone_linear_pair(const uint16_t* x, int32_t tokens, const int64_t* row_index,
+                                      const tris_packed4_matrix* wa, const tris_packed4_matrix* wb,
+                                      uint16_t* out_a, uint16_t* out_b, void* workspace,
+                                      int64_t workspace_bytes, void* stream);
+
+/*
  * Routing-weighted combine: replaces final.index_add_(0, grouped_token_indices,
  * (down_out * routing).to(output_dtype)) (modeling_mixtral.py:529-536).
  * out[t, :] = bf16( sum_s fp16(expert_out[inverse_perm[t*top_k+s], :] * weights[t, s])

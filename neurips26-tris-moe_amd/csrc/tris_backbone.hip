@@ -250,6 +250,272 @@ int launch_backbone(const uint16_t* x, int tokens, int in_features, const int64_
   return check_launch(who);
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// 4-bit packed backbone (PackedQuantMatrix4bit, qlinear_cuda.py:2637-2786): SV[r][c] =
+// fp16((q[c][r] - z[g][r]) * s[g][r]) with q the nibble c % 8 of qweight[c / 8][r], z = nibble r % 8 of
+// qzeros[g][r / 8] plus one, s = scales[g][r], g = g_idx[c] (the reference's dequantize, :2761-2786).
+
+// Nibbles m of a qweight word (8 columns, natural order) to fp16 weights: (1024 + q) - (1024 + z) is exact,
+// and the product with s is rounded once, as the reference's fp16 subtract and multiply.
+__device__ __forceinline__ f16x8 p4_weights(uint32_t w, uint32_t z1024x2, uint32_t s2) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const uint32_t lo = w & 0x0F0F0F0Fu;         // q0, q2, q4, q6 in bytes 0..3
+  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // q1, q3, q5, q7
+  const h2 z = __builtin_bit_cast(h2, z1024x2);
+  const h2 sc = __builtin_bit_cast(h2, s2);
+  uint32_t out[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // halves (q_2i, q_2i+1): byte i of lo, byte i of hi, each under 0x64 (fp16 1024 + q)
+    const uint32_t sel = 0x0C000C00u | (static_cast<uint32_t>(4 + i) << 16) | static_cast<uint32_t>(i);
+    const uint32_t pair = __builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u;
+    out[i] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2, pair) - z) * sc);
+  }
+  return __builtin_bit_cast(f16x8, make_uint4(out[0], out[1], out[2], out[3]));
+}
+
+struct Packed4Proj {
+  const int32_t* qweight;
+  const int32_t* qzeros;
+  const uint16_t* scales;
+  uint16_t* out;
+};
+
+struct Packed4Args {
+  BackboneArgs base;  // x, row_index, in_scale, partials, shapes, slices (proj[].out for the reduce)
+  Packed4Proj proj[2];
+  int packed_cols;    // ceil(in / 8)
+  int qzeros_cols;    // ceil(rank / 8)
+  int group_size;     // a multiple of 8: the 8 columns of a word share a group
+  int num_groups;
+};
+
+// The fp16 backbone kernel's tiling and split-K with the B operand built from packed words: lane (i, kg)
+// of a K step holds the 8 weights of row r0 + i, columns k .. k + 7 (k = step + 8 kg), one qweight word.
+__global__ __launch_bounds__(kBbThreads) void packed4_backbone_kernel(Packed4Args pa) {
+  __shared__ f32x4 red[kBbWaves - 1][kWave];
+  const BackboneArgs& a = pa.base;
+  const int q = blockIdx.z;
+  const Packed4Proj& pj = pa.proj[q];
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int r0 = blockIdx.x * 16;
+  const int slice = blockIdx.y % a.slices;
+  const int t0 = (blockIdx.y / a.slices) * 16;
+  const int i = lane % 16;
+  const int kg = lane / 16;
+
+  const int t = t0 + i;
+  const bool t_valid = t < a.tokens;
+  int64_t xrow = 0;
+  if (t_valid) xrow = a.row_index != nullptr ? a.row_index[t] : t;
+  const uint16_t* xsrc = a.x + xrow * a.in_features;
+  const int r = r0 + i;
+  const bool r_valid = r < a.rank;
+  const int rr = r_valid ? r : 0;
+  const bool scaled = a.in_scale != nullptr;
+  const bool vec = (a.in_features % 8) == 0;
+  const uint32_t zshift = 4u * static_cast<uint32_t>(rr & 7);
+
+  auto weights = [&](int k) {  // k: a multiple of 8
+    const int p = k >> 3;
+    int g = k / pa.group_size;
+    g = g < pa.num_groups ? g : pa.num_groups - 1;
+    uint32_t w = 0u, zw = 0u;
+    uint16_t sh = 0;
+    if (r_valid && p < pa.packed_cols) {
+      w = static_cast<uint32_t>(pj.qweight[static_cast<int64_t>(p) * a.rank + rr]);
+      zw = static_cast<uint32_t>(pj.qzeros[static_cast<int64_t>(g) * pa.qzeros_cols + (rr >> 3)]);
+      sh = pj.scales[static_cast<int64_t>(g) * a.rank + rr];
+    }
+    const uint32_t z = ((zw >> zshift) & 0xFu) + 1u;
+    const uint32_t z2 = (0x6400u | z) * 0x00010001u;
+    const uint32_t s2 = static_cast<uint32_t>(sh) * 0x00010001u;
+    return p4_weights(w, z2, s2);
+  };
+
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int kper = a.slice_k / kBbWaves;
+  const int kbeg0 = slice * a.slice_k + wave * kper;
+  const int kbeg = kbeg0 < a.in_features ? kbeg0 : a.in_features;
+  const int kend = (kbeg0 + kper) < a.in_features ? (kbeg0 + kper) : a.in_features;
+  int k0 = kbeg;
+  if (vec) {
+    for (; k0 + kBbBatch * kBbKStep <= kend; k0 += kBbBatch * kBbKStep) {
+      f16x8 av[kBbBatch], bv[kBbBatch];
+#pragma unroll
+      for (int u = 0; u < kBbBatch; ++u) {
+        const int k = k0 + u * kBbKStep + kg * 8;
+        av[u] = load8_vec(xsrc, k, t_valid);
+        bv[u] = weights(k);
+      }
+      if (scaled) {
+#pragma unroll
+        for (int u = 0; u < kBbBatch; ++u) {
+          av[u] = av[u] * load8_vec(a.in_scale, k0 + u * kBbKStep + kg * 8, true);  // fp16 products, as x * ns_col
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kBbBatch; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[u], bv[u], acc, 0, 0, 0);
+    }
+  }
+  for (; k0 < kend; k0 += kBbKStep) {
+    const int k = k0 + kg * 8;
+    f16x8 av;
+    if (vec && k + 8 <= kend) {
+      av = load8_vec(xsrc, k, t_valid);
+      if (scaled) av = av * load8_vec(a.in_scale, k, true);
+    } else {
+      av = load8_tail(xsrc, k, kend, t_valid);  // columns past the end read 0, so their weights do not count
+      if (scaled) av = av * load8_tail(a.in_scale, k, kend, true);
+    }
+    const f16x8 bv = k < kend ? weights(k) : f16x8{};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
+  }
+  if (wave > 0) red[wave - 1][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 0; w < kBbWaves - 1; ++w) acc += red[w][lane];
+  const int col = r0 + i;
+  if (col >= a.rank) return;
+  if (a.slices == 1) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int tt = t0 + 4 * kg + v;
+      if (tt < a.tokens) pj.out[static_cast<int64_t>(tt) * a.rank + col] = f2h_bits(acc[v]);
+    }
+    return;
+  }
+  float* part = a.partials + (static_cast<int64_t>(q) * a.slices + slice) * a.tokens * a.rank;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int tt = t0 + 4 * kg + v;
+    if (tt < a.tokens) part[static_cast<int64_t>(tt) * a.rank + col] = acc[v];
+  }
+}
+
+// out[r][c] = the dequantised weight, any g_idx: one thread per (row, word), threads along the words of a row
+// so that the 16-byte stores of a row are contiguous.
+__global__ __launch_bounds__(256) void packed4_dequant_kernel(tris_packed4_matrix w, uint16_t* __restrict__ out) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int words = (w.cols + 7) / 8;
+  if (idx >= static_cast<int64_t>(words) * w.rows) return;
+  const int r = static_cast<int>(idx / words);
+  const int p = static_cast<int>(idx % words);
+  const int qzc = (w.rows + 7) / 8;
+  const uint32_t word = static_cast<uint32_t>(w.qweight[static_cast<int64_t>(p) * w.rows + r]);
+  uint16_t h[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const int c = 8 * p + m;
+    h[m] = 0;
+    if (c < w.cols) {
+      int g = w.g_idx[c];
+      g = g < 0 ? 0 : (g >= w.num_groups ? w.num_groups - 1 : g);
+      const uint32_t zw = static_cast<uint32_t>(w.qzeros[static_cast<int64_t>(g) * qzc + (r >> 3)]);
+      const int z = static_cast<int>((zw >> (4 * (r & 7))) & 0xFu) + 1;
+      const int qv = static_cast<int>((word >> (4 * m)) & 0xFu);
+      // (q - z) is a small integer, so the fp32 product is exact and rounds once to fp16
+      h[m] = f2h_bits(static_cast<float>(qv - z) * h2f(w.scales[static_cast<int64_t>(g) * w.rows + r]));
+    }
+  }
+  uint16_t* dst = out + static_cast<int64_t>(r) * w.cols + 8 * p;
+  if (w.cols % 8 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0) {
+    *reinterpret_cast<uint4*>(dst) = make_uint4(h[0] | (uint32_t(h[1]) << 16), h[2] | (uint32_t(h[3]) << 16),
+                                                h[4] | (uint32_t(h[5]) << 16), h[6] | (uint32_t(h[7]) << 16));
+  } else {
+    for (int m = 0; m < 8 && 8 * p + m < w.cols; ++m) dst[m] = h[m];
+  }
+}
+
+static int check_packed4(const tris_packed4_matrix* w, bool fused, const char* who) {
+  TRIS_REQUIRE(w != nullptr, "%s: null matrix", who);
+  TRIS_REQUIRE(w->rows >= 0 && w->cols >= 0 && w->num_groups >= 0, "%s: negative shape", who);
+  if (w->rows == 0 || w->cols == 0) return TRIS_OK;
+  TRIS_REQUIRE(w->num_groups > 0, "%s: no groups", who);
+  TRIS_REQUIRE(w->qweight && w->qzeros && w->scales && (w->g_idx || fused), "%s: null tensor", who);
+  TRIS_REQUIRE(static_cast<int64_t>((w->cols + 7) / 8) * w->rows < (int64_t{1} << 31),
+               "%s: matrix too large", who);
+  if (fused) {
+    TRIS_REQUIRE(w->group_size > 0 && w->group_size % 8 == 0 &&
+                     static_cast<int64_t>(w->group_size) * w->num_groups >= w->cols,
+                 "%s: the fused kernel needs uniform groups of a multiple of 8 columns (g_idx[c] == c / group_size); "
+                 "dequantize with tris_packed4_dequant and use tris_backbone_linear otherwise", who);
+  }
+  return TRIS_OK;
+}
+
+int launch_packed4_backbone(const uint16_t* x, int tokens, const int64_t* row_index, const tris_packed4_matrix* wa,
+                            const tris_packed4_matrix* wb, const uint16_t* in_scale, uint16_t* out_a, uint16_t* out_b,
+                            void* workspace, int64_t workspace_bytes, void* stream, const char* who) {
+  int rc = check_packed4(wa, true, who);
+  if (rc) return rc;
+  if (wb) {
+    rc = check_packed4(wb, true, who);
+    if (rc) return rc;
+    TRIS_REQUIRE(wb->rows == wa->rows && wb->cols == wa->cols, "%s: pair shapes differ", who);
+  }
+  TRIS_REQUIRE(tokens >= 0, "%s: negative tokens", who);
+  const int in_features = wa->cols;
+  const int rank = wa->rows;
+  if (tokens == 0 || rank == 0) return TRIS_OK;
+  TRIS_REQUIRE(out_a != nullptr && (wb == nullptr || out_b != nullptr), "%s: null output", who);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int nproj = wb != nullptr ? 2 : 1;
+  if (in_features == 0) {
+    const int64_t count = static_cast<int64_t>(tokens) * rank;
+    for (int q = 0; q < nproj; ++q) {
+      hipLaunchKernelGGL(fill_zero_u16_kernel, dim3(static_cast<unsigned>((count + 255) / 256)), dim3(256), 0, s,
+                         q ? out_b : out_a, count);
+    }
+    return check_launch("fill_zero_u16_kernel");
+  }
+  TRIS_REQUIRE(x != nullptr, "%s: null input", who);
+  TRIS_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                   (in_scale == nullptr || reinterpret_cast<uintptr_t>(in_scale) % 16 == 0),
+               "%s: x and in_scale must be 16-byte aligned", who);
+  const int slices = backbone_slices(tokens, in_features, rank);
+  const int64_t need = backbone_workspace_bytes(tokens, in_features, rank, nproj);
+  TRIS_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+               "%s: workspace of %lld bytes needed, %lld given", who, static_cast<long long>(need),
+               static_cast<long long>(workspace_bytes));
+  const int token_tiles = ceil_div(tokens, 16);
+  const int row_tiles = ceil_div(rank, 16);
+  TRIS_REQUIRE(static_cast<int64_t>(token_tiles) * slices <= 65535, "%s: too many tokens", who);
+  Packed4Args pa{};
+  BackboneArgs& args = pa.base;
+  args.x = x;
+  args.row_index = row_index;
+  args.in_scale = in_scale;
+  args.proj[0] = BackboneProj{nullptr, out_a};
+  args.proj[1] = BackboneProj{nullptr, out_b};
+  args.partials = static_cast<float*>(workspace);
+  args.tokens = tokens;
+  args.in_features = in_features;
+  args.rank = rank;
+  args.slices = slices;
+  args.slice_k = ceil_div(ceil_div(in_features, slices), kBbWaves * kBbKStep) * kBbWaves * kBbKStep;
+  pa.proj[0] = Packed4Proj{wa->qweight, wa->qzeros, wa->scales, out_a};
+  if (wb) pa.proj[1] = Packed4Proj{wb->qweight, wb->qzeros, wb->scales, out_b};
+  pa.packed_cols = (in_features + 7) / 8;
+  pa.qzeros_cols = (rank + 7) / 8;
+  pa.group_size = wa->group_size;
+  pa.num_groups = wa->num_groups;
+  if (wb) {
+    TRIS_REQUIRE(wb->group_size == wa->group_size && wb->num_groups == wa->num_groups, "%s: pair groups differ", who);
+  }
+  hipLaunchKernelGGL(packed4_backbone_kernel, dim3(row_tiles, token_tiles * slices, nproj), dim3(kBbThreads), 0, s,
+                     pa);
+  rc = check_launch(who);
+  if (rc || slices == 1) return rc;
+  const int64_t count = static_cast<int64_t>(tokens) * rank;
+  hipLaunchKernelGGL(backbone_reduce_kernel, dim3(static_cast<unsigned>((count + 255) / 256), nproj), dim3(256), 0, s,
+                     args);
+  return check_launch(who);
+}
+
 }  // namespace tris
 
 using namespace tris;
@@ -276,4 +542,31 @@ extern "C" int tris_backbone_linear_pair(const uint16_t* x, int32_t tokens, int3
   TRIS_REQUIRE(sv_b != nullptr, "tris_backbone_linear_pair: null sv_b");
   return launch_backbone(x, tokens, in_features, row_index, sv_a, sv_b, rank, nullptr, out_a, out_b, workspace,
                          workspace_bytes, stream, "tris_backbone_linear_pair");
+}
+
+extern "C" int tris_packed4_dequant(const tris_packed4_matrix* w, uint16_t* out, void* stream) {
+  int rc = check_packed4(w, false, "tris_packed4_dequant");
+  if (rc) return rc;
+  if (w->rows == 0 || w->cols == 0) return TRIS_OK;
+  TRIS_REQUIRE(out != nullptr, "tris_packed4_dequant: null output");
+  const int64_t n = static_cast<int64_t>((w->cols + 7) / 8) * w->rows;
+  hipLaunchKernelGGL(packed4_dequant_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), *w, out);
+  return check_launch("tris_packed4_dequant");
+}
+
+extern "C" int tris_packed4_backbone_linear(const uint16_t* x, int32_t tokens, const int64_t* row_index,
+                                            const tris_packed4_matrix* w, const uint16_t* in_scale, uint16_t* out,
+                                            void* workspace, int64_t workspace_bytes, void* stream) {
+  return launch_packed4_backbone(x, tokens, row_index, w, nullptr, in_scale, out, nullptr, workspace, workspace_bytes,
+                                 stream, "tris_packed4_backbone_linear");
+}
+
+extern "C" int tris_packed4_backbone_linear_pair(const uint16_t* x, int32_t tokens, const int64_t* row_index,
+                                                 const tris_packed4_matrix* wa, const tris_packed4_matrix* wb,
+                                                 uint16_t* out_a, uint16_t* out_b, void* workspace,
+                                                 int64_t workspace_bytes, void* stream) {
+  TRIS_REQUIRE(wb != nullptr, "tris_packed4_backbone_linear_pair: null second matrix");
+  return launch_packed4_backbone(x, tokens, row_index, wa, wb, nullptr, out_a, out_b, workspace, workspace_bytes,
+                                 stream, "tris_packed4_backbone_linear_pair");
 }

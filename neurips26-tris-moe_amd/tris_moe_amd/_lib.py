@@ -64,12 +64,28 @@ class TrisPredecodeJob(ctypes.Structure):
     ]
 
 
+class TrisPacked4(ctypes.Structure):
+    """Mirror of struct tris_packed4_matrix."""
+
+    _fields_ = [
+        ("qweight", ctypes.c_void_p),
+        ("qzeros", ctypes.c_void_p),
+        ("scales", ctypes.c_void_p),
+        ("g_idx", ctypes.c_void_p),
+        ("rows", ctypes.c_int32),
+        ("cols", ctypes.c_int32),
+        ("num_groups", ctypes.c_int32),
+        ("group_size", ctypes.c_int32),
+    ]
+
+
 MAX_PREDECODE_JOBS = 4
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
 _I64 = ctypes.c_int64
 _PAY = ctypes.POINTER(TrisPayload)
+_P4 = ctypes.POINTER(TrisPacked4)
 SIGNATURES = {
     "tris_abi_version": (ctypes.c_int, []),
     "tris_last_error": (ctypes.c_char_p, []),
@@ -94,6 +110,9 @@ SIGNATURES = {
     "tris_backbone_workspace_bytes": (_I64, [_I32, _I32, _I32]),
     "tris_moe_combine": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _P, _P]),
     "tris_swiglu_mul": (ctypes.c_int, [_P, _P, _I64, _P, _P]),
+    "tris_packed4_dequant": (ctypes.c_int, [_P4, _P, _P]),
+    "tris_packed4_backbone_linear": (ctypes.c_int, [_P, _I32, _P, _P4, _P, _P, _P, _I64, _P]),
+    "tris_packed4_backbone_linear_pair": (ctypes.c_int, [_P, _I32, _P, _P4, _P4, _P, _P, _P, _I64, _P]),
 }
 
 _lib = None

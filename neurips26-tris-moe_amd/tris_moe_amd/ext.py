@@ -620,6 +620,131 @@ def backbone_linear_pair(x: torch.Tensor, sv_a: torch.Tensor, sv_b: torch.Tensor
     return out_a, out_b
 
 
+# ----------------------------------------------------------------------------------------- 4-bit backbone
+class Packed4Matrix:
+    """Device tensors of one 4-bit packed matrix (PackedQuantMatrix4bit buffers, qlinear_cuda.py:2637-2786):
+    qweight int32 [ceil(cols/8), rows], qzeros int32 [G, ceil(rows/8)], scales fp16 [G, rows], g_idx int32
+    [cols]; group_size > 0 when g_idx[c] == c // group_size (a multiple of 8), else 0."""
+
+    __slots__ = ("qweight", "qzeros", "scales", "g_idx", "rows", "cols", "group_size")
+
+    def __init__(self, qweight, qzeros, scales, g_idx, rows: int, cols: int, group_size: int):
+        self.qweight, self.qzeros, self.scales, self.g_idx = qweight, qzeros, scales, g_idx
+        self.rows, self.cols, self.group_size = int(rows), int(cols), int(group_size)
+
+    def c_struct(self):
+        return _lib.TrisPacked4(_ptr(self.qweight), _ptr(self.qzeros), _ptr(self.scales), _ptr(self.g_idx),
+                                self.rows, self.cols, int(self.scales.size(0)), self.group_size)
+
+
+def uniform_group_size(g_idx) -> int:
+    """The group size when g_idx[c] == c // size for every column and size is a multiple of 8 (one group:
+    cols rounded up to 8), else 0.  Read on the host once per matrix, as the reference's
+    resolve_packed4_fast_config reads g_idx (TriSMoE_cuda_kernel.cu:8044-8048)."""
+    import numpy as np
+
+    g = g_idx.detach().to("cpu").numpy() if isinstance(g_idx, torch.Tensor) else np.asarray(g_idx)
+    g = g.astype(np.int64).reshape(-1)
+    cols = int(g.size)
+    if cols == 0 or g[0] != 0:
+        return 0
+    nz = np.flatnonzero(g != 0)
+    if nz.size == 0:
+        return (cols + 7) // 8 * 8
+    size = int(nz[0])
+    if size % 8 != 0 or not np.array_equal(g, np.arange(cols) // size):
+        return 0
+    return size
+
+
+def _check_packed4(m: Packed4Matrix, device):
+    _check_cuda("qweight", m.qweight, torch.int32, 2, device)
+    _check_cuda("qzeros", m.qzeros, torch.int32, 2, device)
+    _check_cuda("scales", m.scales, torch.float16, 2, device)
+    if m.g_idx is not None:
+        _check_cuda("g_idx", m.g_idx, torch.int32, 1, device)
+    if (m.qweight.size(0) != (m.cols + 7) // 8 or m.qweight.size(1) != m.rows or m.scales.size(1) != m.rows
+            or m.qzeros.size(1) != (m.rows + 7) // 8 or m.qzeros.size(0) != m.scales.size(0)):
+        raise RuntimeError("packed 4-bit matrix: inconsistent qweight / qzeros / scales shapes")
+
+
+def packed4_dequant(m: Packed4Matrix) -> torch.Tensor:
+    """fp16 [rows, cols] = PackedQuantMatrix4bit.dequantize (qlinear_cuda.py:2761-2786), bit for bit."""
+    dev = m.qweight.device
+    _check_packed4(m, dev)
+    if m.g_idx is None:
+        raise RuntimeError("packed4_dequant needs g_idx")
+    out = torch.empty((m.rows, m.cols), dtype=torch.float16, device=dev)
+    st = m.c_struct()
+    _lib.check(_lib.load().tris_packed4_dequant(ctypes.byref(st), _ptr(out), _stream(out)), "tris_packed4_dequant")
+    return out
+
+
+def packed4_backbone_linear(x: torch.Tensor, m: Packed4Matrix, in_scale: torch.Tensor | None = None,
+                            row_index: torch.Tensor | None = None) -> torch.Tensor:
+    """hidden = fp16(x[row_index] * in_scale) . SV^T straight from the packed matrix (uniform groups)."""
+    _check_cuda("x", x, torch.float16, 2)
+    _check_packed4(m, x.device)
+    if x.size(1) != m.cols:
+        raise RuntimeError("packed backbone in-features mismatch")
+    tokens = int(row_index.numel()) if row_index is not None else int(x.size(0))
+    if row_index is not None:
+        _check_cuda("row_index", row_index, torch.int64, 1, x.device)
+    if in_scale is not None:
+        _check_cuda("in_scale", in_scale, torch.float16, 1, x.device)
+    out = torch.empty((tokens, m.rows), dtype=torch.float16, device=x.device)
+    lib = _lib.load()
+    ws = backbone_workspace(x.device, int(lib.tris_backbone_workspace_bytes(tokens, m.cols, m.rows)))
+    st = m.c_struct()
+    _lib.check(lib.tris_packed4_backbone_linear(_ptr(x), tokens, _ptr(row_index), ctypes.byref(st), _ptr(in_scale),
+                                                _ptr(out), _ptr(ws), int(ws.numel()), _stream(x)),
+               "tris_packed4_backbone_linear")
+    return out
+
+
+def packed4_backbone_linear_pair(x: torch.Tensor, ma: Packed4Matrix, mb: Packed4Matrix,
+                                 row_index: torch.Tensor | None = None):
+    """The gate and up packed backbones of the same rows in one launch (same bits as two single calls)."""
+    _check_cuda("x", x, torch.float16, 2)
+    _check_packed4(ma, x.device)
+    _check_packed4(mb, x.device)
+    if x.size(1) != ma.cols or (ma.rows, ma.cols) != (mb.rows, mb.cols):
+        raise RuntimeError("packed backbone pair shape mismatch")
+    tokens = int(row_index.numel()) if row_index is not None else int(x.size(0))
+    if row_index is not None:
+        _check_cuda("row_index", row_index, torch.int64, 1, x.device)
+    out_a = torch.empty((tokens, ma.rows), dtype=torch.float16, device=x.device)
+    out_b = torch.empty((tokens, mb.rows), dtype=torch.float16, device=x.device)
+    lib = _lib.load()
+    ws = backbone_workspace(x.device, int(lib.tris_backbone_pair_workspace_bytes(tokens, ma.cols, ma.rows)))
+    sa, sb = ma.c_struct(), mb.c_struct()
+    _lib.check(lib.tris_packed4_backbone_linear_pair(_ptr(x), tokens, _ptr(row_index), ctypes.byref(sa),
+                                                     ctypes.byref(sb), _ptr(out_a), _ptr(out_b), _ptr(ws),
+                                                     int(ws.numel()), _stream(x)),
+               "tris_packed4_backbone_linear_pair")
+    return out_a, out_b
+
+
+def packed4_linear_forward(input: torch.Tensor, qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor,
+                           g_idx: torch.Tensor, group_size: int | None = None) -> torch.Tensor:
+    """The extension's packed4_linear_forward(input, qweight, qzeros, scales, g_idx) (TriSMoE_cuda.cpp binding
+    of TriSMoE_cuda_kernel.cu:8023-8137): fp16 [batch, cols] -> [batch, rows].  Uniform groups take the fused
+    kernel below BACKBONE_LIBRARY_MIN_ROWS rows; otherwise the matrix is dequantised and projected in fp16
+    (the reference's non-fast kernels and its Python fallback, qlinear_cuda.py:4490-4494).  group_size: the
+    uniform group size if known (else read from g_idx on the host)."""
+    _check_cuda("input", input, torch.float16, 2)
+    cols = int(g_idx.numel())
+    if input.size(1) != cols:
+        raise RuntimeError("packed4_linear_forward: input columns != g_idx length")
+    gs = uniform_group_size(g_idx) if group_size is None else int(group_size)
+    m = Packed4Matrix(qweight, qzeros, scales, g_idx, int(qweight.size(1)), cols, gs)
+    if input.size(0) == 0 or m.rows == 0:
+        return torch.zeros((int(input.size(0)), m.rows), dtype=torch.float16, device=input.device)
+    if gs > 0 and input.size(0) < BACKBONE_LIBRARY_MIN_ROWS:
+        return packed4_backbone_linear(input, m)
+    return backbone_linear(input, packed4_dequant(m))
+
+
 def moe_combine(expert_out: torch.Tensor, inverse_perm: torch.Tensor, weights: torch.Tensor,
                 shared: torch.Tensor | None = None) -> torch.Tensor:
     """bf16 [T, H] = sum_s fp16(expert_out[inverse_perm[t, s]] * weights[t, s]) (+ shared), fp32-accumulated."""

@@ -21,7 +21,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ext
-from .qlinear import GROUPED_SEGMENT_M_TILE
+from .qlinear import GROUPED_SEGMENT_M_TILE, shared_projection, shared_projection_pair
 
 
 def route_topk(router_logits: torch.Tensor, top_k: int, renormalize: bool):
@@ -40,7 +40,8 @@ def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, select
 
     x16 fp16 [T, H]; routing_weights [T, k] (cast to fp16 as in modeling_mixtral.py:555);
     selected_experts int64 [T, k]; payloads {gate, up, down} device payload dicts;
-    backbones {gate, up, down} fp16 [rank, in].  Returns [T, H] in output_dtype.
+    backbones {gate, up, down}: fp16 SV [rank, in] or qlinear.PackedQuantMatrix4bit.  Returns [T, H] in
+    output_dtype.
 
     expert_path: "predecoded" decodes the split bitmaps once per projection and runs the MFMA
     grouped GEMMs (needs uniform 64-column groups and no output scale or bias); "fused" decodes
@@ -95,7 +96,7 @@ def _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, ou
     if predecodable and expert_path != "fused":
         return _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype,
                                        shared_expert)
-    hid_g, hid_u = ext.backbone_linear_pair(x16, backbones["gate"], backbones["up"], row_index=gti)
+    hid_g, hid_u = shared_projection_pair(x16, backbones["gate"], backbones["up"], row_index=gti)
     empty = x16.new_empty((0, 0))
     g_out, u_out = ext.compact3_tris_precomputed_grouped_dual_forward_block_gr(
         hid_g, hid_u, expert_ids, seg, prob, tile_bound,
@@ -106,7 +107,7 @@ def _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, ou
         pu["q_gmap_gr_offsets"], pu["q_gmap_gr_meta"], pu["c_map"], pu["g_idx"], pu["col_pack3"], pu["row_pack3"],
         pu["output_scale"], bool(pu["has_output_scale"]), pu["bias"] if pu["has_bias"] else empty, uniform)
     mlp = F.silu(g_out) * u_out
-    hid_d = ext.backbone_linear(mlp, backbones["down"])
+    hid_d = shared_projection(mlp, backbones["down"])
     d_out = ext.compact3_tris_precomputed_grouped_forward_block_gr(
         hid_d, expert_ids, seg, prob, tile_bound,
         pd["qweight1"], pd["qweight2_sparse"], pd["qweight2_sparse_prefix"], pd["q_gmap_gr_words"],
@@ -175,7 +176,7 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
             [(bufs[name], p["q_gmap_gr_words"], p["q_gmap_gr_offsets"], p["q_gmap_gr_meta"], int(p["qweight1"].size(1)),
               int(p["qweight1"].size(2))) for name, p in order], eid)
         decoded = bufs
-    hid_g, hid_u = ext.backbone_linear_pair(x16, backbones["gate"], backbones["up"],
+    hid_g, hid_u = shared_projection_pair(x16, backbones["gate"], backbones["up"],
                                             row_index=route["grouped_token_indices"])
     main.wait_stream(side)
     names = ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx", "col_pack3", "row_pack3")
@@ -196,7 +197,7 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
             hid_g, hid_u, eid, seg, prob, tile_bound, decoded["gate"], *[pg[k] for k in names], decoded["up"],
             *[pu[k] for k in names], True, out_a=g, out_b=u)
         ext.swiglu_mul(g, u, out=mlp)
-    hid_d = ext.backbone_linear(mlp, backbones["down"])
+    hid_d = shared_projection(mlp, backbones["down"])
     d_out = torch.empty((R, int(pd["qweight1"].size(2))), dtype=torch.float16, device=dev)
     ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
         hid_d, eid, seg, prob, tile_bound, decoded["down"], *[pd[k] for k in names], True, out=d_out)

@@ -351,18 +351,175 @@ def pack_block_gr_gmap_tensor(packed: torch.Tensor, force_raw: bool = False, fix
     return (torch.from_numpy(words).to(dev), torch.from_numpy(offsets).to(dev), torch.from_numpy(meta).to(dev))
 
 
-class ExpertSharedMatrix(nn.Module):
-    """qlinear_cuda.py:2787-2968: the shared backbone SV [rank, in] of one (layer, projection)."""
+class PackedQuantMatrix4bit(nn.Module):
+    """qlinear_cuda.py:2637-2786: a 4-bit packed matrix [rows, cols] (the shared backbone SV of real
+    checkpoints): qweight int32 [ceil(cols/8), rows], qzeros int32 [G, ceil(rows/8)], scales [G, rows],
+    g_idx int32 [cols]; W[r][c] = (q - z) * s (see ``ext.packed4_dequant``).
 
-    def __init__(self, shared_sv: torch.Tensor):
+    ``project`` computes x . W^T on the GPU: the fused 4-bit kernel for uniform groups below
+    ``ext.BACKBONE_LIBRARY_MIN_ROWS`` rows, else the cached dequantised matrix through the fp16 path."""
+
+    def __init__(self, weight_dtype=torch.float16):
         super().__init__()
-        self.register_buffer("shared_sv", shared_sv.contiguous())
+        self.register_buffer("qweight", torch.zeros((0, 0), dtype=torch.int32))
+        self.register_buffer("qzeros", torch.zeros((0, 0), dtype=torch.int32))
+        self.register_buffer("scales", torch.zeros((0, 0), dtype=weight_dtype))
+        self.register_buffer("g_idx", torch.zeros((0,), dtype=torch.int32))
+        self.register_buffer("rows", torch.zeros((), dtype=torch.int32))
+        self.register_buffer("cols", torch.zeros((), dtype=torch.int32))
+        self._rows_host = 0
+        self._cols_host = 0
+        self._group_size = 0
+        self._cached_weight = None
+        self._cached_weight_key = None
+
+    def _apply(self, fn):
+        super()._apply(fn)
+        self.invalidate_cache()
+        return self
+
+    def invalidate_cache(self):
+        self._cached_weight = None
+        self._cached_weight_key = None
+
+    def set_empty(self):
+        self.set_quantized(torch.zeros((0, 0), dtype=torch.int32), torch.zeros((0, 0), dtype=torch.int32),
+                           torch.zeros((0, 0), dtype=self.scales.dtype), torch.zeros((0,), dtype=torch.int32), 0, 0)
+
+    def is_quantized(self) -> bool:
+        return self.qweight.numel() > 0 and self._rows_host > 0 and self._cols_host > 0
+
+    def set_quantized(self, qweight, qzeros, scales, g_idx, rows=None, cols=None):
+        """qlinear_cuda.py:2726-2743; rows default to scales.shape[1], cols to g_idx.numel()."""
+        def as_t(v):
+            return torch.as_tensor(np.ascontiguousarray(v)) if isinstance(v, np.ndarray) else v
+        self.qweight = as_t(qweight).to(torch.int32).contiguous()
+        self.qzeros = as_t(qzeros).to(torch.int32).contiguous()
+        self.scales = as_t(scales).to(dtype=self.scales.dtype).contiguous()
+        self.g_idx = as_t(g_idx).to(torch.int32).contiguous()
+        n_rows = int(rows.item()) if isinstance(rows, torch.Tensor) else rows
+        n_cols = int(cols.item()) if isinstance(cols, torch.Tensor) else cols
+        if n_rows is None:
+            n_rows = self.scales.shape[1] if self.scales.dim() == 2 else 0
+        if n_cols is None:
+            n_cols = self.g_idx.numel()
+        self.rows = torch.tensor(int(n_rows), dtype=torch.int32)
+        self.cols = torch.tensor(int(n_cols), dtype=torch.int32)
+        self._rows_host = int(n_rows)
+        self._cols_host = int(n_cols)
+        self._group_size = ext.uniform_group_size(self.g_idx) if self.g_idx.numel() else 0
+        self.invalidate_cache()
+        return self
+
+    def set_from_payload(self, payload, device=None):
+        """qlinear_cuda.py:2745-2759 (a payload of build_packed_4bit_payload, utils/pack_utils.py:126-180)."""
+        if payload is None or not isinstance(payload, dict) or "qweight" not in payload:
+            self.set_empty()
+            return self
+        self.set_quantized(payload["qweight"], payload["qzeros"], payload["scales"], payload["g_idx"],
+                           payload.get("rows"), payload.get("cols"))
+        if device is not None:
+            self.to(device)
+        return self
+
+    @property
+    def group_size(self) -> int:
+        return self._group_size
+
+    def matrix(self) -> ext.Packed4Matrix:
+        return ext.Packed4Matrix(self.qweight, self.qzeros, self.scales, self.g_idx, self._rows_host,
+                                 self._cols_host, self._group_size)
+
+    def dequantize(self, device, dtype) -> torch.Tensor:
+        """qlinear_cuda.py:2761-2786 on the GPU (fp16: the HIP kernel, bit for bit; cached)."""
+        device = torch.device(device)
+        key = (device.type, device.index, dtype)
+        if self._cached_weight is not None and self._cached_weight_key == key:
+            return self._cached_weight
+        if self._rows_host == 0 or self._cols_host == 0:
+            w = torch.zeros((self._rows_host, self._cols_host), device=device, dtype=dtype)
+        else:
+            if self.qweight.device != device:
+                self.to(device)
+            w = ext.packed4_dequant(self.matrix())
+            if dtype != torch.float16:
+                w = w.to(dtype)
+        self._cached_weight = w
+        self._cached_weight_key = key
+        return w
+
+    def fused_ok(self, tokens: int) -> bool:
+        return self._group_size > 0 and tokens < ext.BACKBONE_LIBRARY_MIN_ROWS
+
+    def project(self, x: torch.Tensor, in_scale: torch.Tensor | None = None,
+                row_index: torch.Tensor | None = None) -> torch.Tensor:
+        """hidden = fp16(x[row_index] * in_scale) . W^T (compute_shared_hidden with a packed SV,
+        qlinear_cuda.py:4487-4494)."""
+        tokens = int(row_index.numel()) if row_index is not None else int(x.size(0))
+        if self.fused_ok(tokens):
+            return ext.packed4_backbone_linear(x, self.matrix(), in_scale=in_scale, row_index=row_index)
+        return ext.backbone_linear(x, self.dequantize(x.device, torch.float16), in_scale=in_scale,
+                                   row_index=row_index)
+
+
+def shared_projection(x: torch.Tensor, sv, in_scale: torch.Tensor | None = None,
+                      row_index: torch.Tensor | None = None) -> torch.Tensor:
+    """The shared backbone of one projection: sv is an fp16 SV [rank, in] or a PackedQuantMatrix4bit."""
+    if isinstance(sv, PackedQuantMatrix4bit):
+        return sv.project(x, in_scale=in_scale, row_index=row_index)
+    return ext.backbone_linear(x, sv, in_scale=in_scale, row_index=row_index)
+
+
+def shared_projection_pair(x: torch.Tensor, sv_a, sv_b, row_index: torch.Tensor | None = None):
+    """Gate and up backbones of the same rows: one launch for two fp16 matrices or two fused-capable packed
+    matrices of one shape, else two projections."""
+    tokens = int(row_index.numel()) if row_index is not None else int(x.size(0))
+    if isinstance(sv_a, torch.Tensor) and isinstance(sv_b, torch.Tensor):
+        return ext.backbone_linear_pair(x, sv_a, sv_b, row_index=row_index)
+    if (isinstance(sv_a, PackedQuantMatrix4bit) and isinstance(sv_b, PackedQuantMatrix4bit)
+            and sv_a.fused_ok(tokens) and sv_b.fused_ok(tokens) and sv_a.group_size == sv_b.group_size
+            and (sv_a._rows_host, sv_a._cols_host) == (sv_b._rows_host, sv_b._cols_host)
+            and sv_a.scales.shape == sv_b.scales.shape):
+        return ext.packed4_backbone_linear_pair(x, sv_a.matrix(), sv_b.matrix(), row_index=row_index)
+    return (shared_projection(x, sv_a, row_index=row_index), shared_projection(x, sv_b, row_index=row_index))
+
+
+class ExpertSharedMatrix(nn.Module):
+    """qlinear_cuda.py:2787-2968: the shared backbone SV [rank, in] of one (layer, projection), either fp16
+    (``shared_sv``) or 4-bit packed (``shared_sv_quant``)."""
+
+    def __init__(self, shared_sv=None):
+        super().__init__()
+        self.register_buffer("shared_sv", torch.zeros((0, 0), dtype=torch.float16))
+        self.shared_sv_quant = PackedQuantMatrix4bit()
+        if shared_sv is not None:
+            self.set_shared_sv(shared_sv)
+
+    def set_shared_sv(self, payload):
+        """qlinear_cuda.py:2944-2953: a packed payload dict (with ``qweight``) or an fp16 matrix."""
+        if isinstance(payload, dict) and "qweight" in payload:
+            self.shared_sv = torch.zeros((0, 0), dtype=torch.float16)
+            self.shared_sv_quant.set_from_payload(payload)  # the payload's tensors keep their device
+        else:
+            self.shared_sv_quant.set_empty()
+            self.shared_sv = torch.as_tensor(payload).to(dtype=torch.float16).contiguous()
+        return self
 
     def get_shared_sv(self, device, dtype):
+        if self.shared_sv_quant.is_quantized():
+            return self.shared_sv_quant.dequantize(device, dtype)
         sv = self.shared_sv
         if sv.device != torch.device(device) or sv.dtype != dtype:
             sv = sv.to(device=device, dtype=dtype).contiguous()
         return sv
+
+    def backbone(self, device):
+        """What shared_projection takes: the packed matrix (moved to device) or the fp16 SV."""
+        if self.shared_sv_quant.is_quantized():
+            if self.shared_sv_quant.qweight.device != torch.device(device):
+                self.shared_sv_quant.to(device)
+            return self.shared_sv_quant
+        return self.get_shared_sv(device, torch.float16)
 
 
 class QuantLinear(nn.Module):
@@ -414,13 +571,14 @@ class QuantLinear(nn.Module):
             return None
         shape = x.shape[:-1]
         xb = x.reshape(-1, x.shape[-1]).contiguous()
-        sv = self._shared_matrix_module.get_shared_sv(xb.device, xb.dtype)
+        sv = self._shared_matrix_module.backbone(xb.device)
+        rank = sv._rows_host if isinstance(sv, PackedQuantMatrix4bit) else sv.shape[0]
         if xb.shape[0] == 0:
-            return xb.new_empty((0, sv.shape[0])).reshape(shape + (sv.shape[0],))
+            return xb.new_empty((0, rank)).reshape(shape + (rank,))
         scale = None
         if self._ns_mode_host == 1:
             scale = self.expert_input_scale.to(device=xb.device, dtype=xb.dtype).contiguous()
-        hidden = ext.backbone_linear(xb, sv, in_scale=scale)
+        hidden = shared_projection(xb, sv, in_scale=scale)
         return hidden.reshape(shape + (hidden.shape[-1],))
 
     def _single_payload(self, device, dtype) -> dict:

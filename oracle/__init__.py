@@ -24,6 +24,9 @@ reference checkout):
   ``qlinear_cuda.py:1301-1378``.
 * MoE block (numpy): ``modeling_mixtral.py:406-608`` (grouped forward) and
   ``modeling_olmoe.py:1053-1058`` (optional top-k renormalisation).
+* 4-bit packed backbone (numpy): producer ``utils/pack_utils.py:126-180``,
+  consumer ``qlinear_cuda.py:2761-2786`` (exact fp16 dequant; the projection
+  is then ``linear_f16`` of the dequantised matrix).
 
 How each part is pinned (see tests/test_oracle_*.py): hand-derived
 known-answer GR blocks, closed-form Rice lengths and k choice, encode/decode
@@ -31,7 +34,9 @@ round trips on random and edge-case bitmaps, agreement of the reference's
 two decoder paths (general and k==3); fp16 products checked against integer
 significand arithmetic; the dequantised matrix checked against the reference
 CPU formula (masks and per-term products, ``qlinear_cuda.py:4213-4236``);
-routes by brute force; layer output against a float64 dense evaluation.
+routes by brute force; layer output against a float64 dense evaluation;
+4-bit packing by hand-derived known answers, the quantisation error bound
+|W - dequant| <= s/2 and the zero-of-0 reads-as-16 convention.
 """
 from __future__ import annotations
 
@@ -421,6 +426,45 @@ def moe_layer(x_f16, routing_weights, selected_experts, payloads: dict, backbone
         smlp = (silu_f16(sg).astype(np.float32) * su.astype(np.float32)).astype(np.float16)
         out = out + linear_f16(smlp, wd).astype(np.float32)
     return out
+
+
+def packed4_build_payload(matrix, scale, zero, g_idx) -> dict:
+    """4-bit packed payload of a float matrix [rows, cols] (utils/pack_utils.py:126-180): q =
+    clamp(round(m / s + z), 0, 15) per column group; qweight [ceil(cols/8), rows] holds column c in nibble
+    c % 8 of word c // 8; qzeros [G, ceil(rows/8)] holds (round(z) - 1) & 0xF in nibble r % 8 (the
+    consumer adds one back, so a zero of 0 reads as 16).  scale / zero are group-major [G, rows]."""
+    m = np.asarray(matrix, dtype=np.float32)
+    rows, cols = m.shape
+    sc = np.asarray(scale, dtype=np.float32)
+    zr = np.asarray(zero, dtype=np.float32)
+    g = np.asarray(g_idx, dtype=np.int64)
+    q = np.clip(np.round(m.T / sc[g] + zr[g]), 0, 15).astype(np.int64)  # [cols, rows]
+    qweight = np.zeros(((cols + 7) // 8, rows), dtype=np.int64)
+    for c in range(cols):
+        qweight[c // 8] |= q[c] << (4 * (c % 8))
+    zint = (np.clip(np.round(zr), 0, 15).astype(np.int64) - 1) & 0xF  # [G, rows]
+    qzeros = np.zeros((zr.shape[0], (rows + 7) // 8), dtype=np.int64)
+    for r in range(rows):
+        qzeros[:, r // 8] |= zint[:, r] << (4 * (r % 8))
+    return {"rows": rows, "cols": cols, "qweight": qweight.astype(np.uint32).view(np.int32),
+            "qzeros": qzeros.astype(np.uint32).view(np.int32), "scales": sc.astype(np.float16),
+            "g_idx": g.astype(np.int32)}
+
+
+def packed4_dequant(qweight, qzeros, scales, g_idx, rows: int, cols: int) -> np.ndarray:
+    """PackedQuantMatrix4bit.dequantize (qlinear_cuda.py:2761-2786) in exact fp16: W[r][c] =
+    fp16(fp16(q - z) * s) with q = nibble c % 8 of qweight[c // 8][r], z = nibble r % 8 of
+    qzeros[g][r // 8] + 1, s = scales[g][r], g = g_idx[c].  Returns fp16 [rows, cols]."""
+    qw = np.asarray(qweight).astype(np.uint32).astype(np.int64)
+    qz = np.asarray(qzeros).astype(np.uint32).astype(np.int64)
+    sc = np.asarray(scales, dtype=np.float16)
+    g = np.asarray(g_idx, dtype=np.int64)[:cols]
+    shifts = 4 * np.arange(8, dtype=np.int64)
+    q = ((qw[:, None, :] >> shifts[None, :, None]) & 0xF).reshape(-1, qw.shape[1])[:cols]   # [cols, rows]
+    z = ((qz[:, :, None] >> shifts[None, None, :]) & 0xF).reshape(qz.shape[0], -1)[:, :rows] + 1  # [G, rows]
+    diff = (q - z[g]).astype(np.float16)          # small integers: exact in fp16
+    w = f16_mul(diff, sc[g])                       # one rounding, as the fp16 multiply
+    return np.ascontiguousarray(w.T)
 
 
 def bf16_round(x) -> np.ndarray:
