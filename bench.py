@@ -59,6 +59,8 @@ def parse_args():
     ap.add_argument("--stream-layers", type=int, default=32)
     ap.add_argument("--prefill", type=int, default=2048,
                     help="C2 prefill tokens measured into 'prefill' (0 for none)")
+    ap.add_argument("--packed4", type=int, default=1,
+                    help="also time the decode step with 4-bit packed backbones into 'packed4_backbones'")
     ap.add_argument("--prefill-only", action="store_true",
                     help="measure only the C2 prefill step and print its JSON object")
     return ap.parse_args()
@@ -112,13 +114,14 @@ def main():
     torch.cuda.synchronize()
     log(f"{args.layers} layer copies resident")
 
-    def measure(tokens: int, steps: int, warmup: int):
+    def measure(tokens: int, steps: int, warmup: int, cps=None, backbone_bytes=None):
+        cps = copies if cps is None else cps
         inp = synthetic.make_inputs(SPEC, tokens, args.seed + tokens, layer["outlier_idx"])
         x16 = torch.from_numpy(inp["x"]).to(dev).to(torch.bfloat16).to(torch.float16)
         logits = torch.from_numpy(inp["router_logits"]).to(dev)
 
         def step(i):
-            pl, bb = copies[i % len(copies)]
+            pl, bb = cps[i % len(cps)]
             return moe.grouped_moe_forward_from_logits(x16, logits, SPEC.top_k, SPEC.renormalize, pl, bb,
                                                        SPEC.num_experts, torch.bfloat16)
 
@@ -126,7 +129,7 @@ def main():
             step(i)
         torch.cuda.synchronize()
         graphs = []
-        for i in range(len(copies)):
+        for i in range(len(cps)):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
                 step(i)
@@ -145,7 +148,8 @@ def main():
         w, sel = moe.route_topk(logits, SPEC.top_k, SPEC.renormalize)
         active = sorted(set(sel.cpu().numpy().reshape(-1).tolist()))
         expert_bytes = sum(synthetic.payload_nbytes(layer[p], active) for p in projs)
-        backbone_bytes = sum(layer["backbones"][p].nbytes for p in projs)
+        if backbone_bytes is None:
+            backbone_bytes = sum(layer["backbones"][p].nbytes for p in projs)
         act_bytes = 2 * tokens * SPEC.hidden * 2
         step_bytes = expert_bytes + backbone_bytes + act_bytes
         return {"tokens": tokens, "ms_per_step": ms, "tokens_per_s": tokens / (ms / 1e3),
@@ -169,6 +173,23 @@ def main():
         sweep[f"T{tok}"] = {k: round(r[k], 3) for k in ("ms_per_step", "tokens_per_s", "hbm_gbps")}
         sweep[f"T{tok}"]["active_experts"] = r["active_experts"]
         log(f"T={tok}: {r['ms_per_step'] * 1e3:.1f} us/step, {r['tokens_per_s']:.0f} tok/s, {r['hbm_gbps']:.0f} GB/s")
+
+    # ---- the same step with 4-bit packed backbones (group 128, as real checkpoints store SV)
+    packed4 = None
+    if args.packed4:
+        from tris_moe_amd import packing
+        from tris_moe_amd.qlinear import PackedQuantMatrix4bit
+
+        pk = {p: packing.pack_4bit(layer["backbones"][p].astype(np.float32), 128) for p in projs}
+        p4_bytes = sum(pk[p][k].nbytes for p in projs for k in ("qweight", "qzeros", "scales", "g_idx"))
+        pcopies = [(pl, {p: PackedQuantMatrix4bit().set_from_payload(pk[p]).to(dev) for p in projs})
+                   for pl, _ in copies]
+        packed4 = {"backbone_bytes": int(p4_bytes), "group_size": 128}
+        for tok in sorted({args.tokens, 1}):
+            r = measure(tok, max(args.steps // 2, 10), args.warmup, pcopies, p4_bytes)
+            packed4[f"T{tok}"] = {k: round(r[k], 3) for k in ("ms_per_step", "tokens_per_s", "hbm_gbps")}
+            log(f"packed4 backbones T={tok}: {r['ms_per_step'] * 1e3:.1f} us/step, {r['tokens_per_s']:.0f} tok/s")
+        del pcopies
 
     # ---- dominant kernel: the MFMA gate/up grouped GEMM over predecoded split bitmaps that the step runs,
     # one launch per layer copy, replayed from a graph on its own stream and timed there with HIP events
@@ -254,6 +275,7 @@ def main():
         "cpu_baseline": cpu,
         "sweep": sweep,
         "prefill": prefill,
+        "packed4_backbones": packed4,
     }
     print(json.dumps(line), flush=True)
 

@@ -70,7 +70,7 @@ def test_quantisation_error_bound(oracle_mod, perm):
     G = int(g_idx.max()) + 1
     lo = np.stack([m[:, g_idx == g].min(axis=1) for g in range(G)])   # [G, rows]
     hi = np.stack([m[:, g_idx == g].max(axis=1) for g in range(G)])
-    scale = ((hi - lo) / 15.0).astype(np.float16).astype(np.float32)
+    scale = ((hi - lo) / 14.0).astype(np.float16).astype(np.float32)   # one step of slack for the zero's rounding
     zero = np.round(-lo / scale)
     assert zero.min() >= 1 and zero.max() <= 15   # standard normal data: min < 0 < max
     pl = oracle_mod.packed4_build_payload(m, scale, zero, g_idx)
@@ -78,7 +78,6 @@ def test_quantisation_error_bound(oracle_mod, perm):
     s_rc = scale[g_idx].T   # [rows, cols]
     err = np.abs(w.astype(np.float32) - m)
     bound = s_rc * 0.5 * (1 + 1e-3) + np.abs(w.astype(np.float32)) * 2.0 ** -11
-    # entries clamped at 0 or 15 sit at most s/2 beyond the range too
     assert (err <= bound + 1e-6).all(), float((err - bound).max())
 
 
@@ -109,3 +108,22 @@ def test_packed_matrix_module_host_state():
     assert sm.shared_sv_quant.is_quantized() and sm.shared_sv.numel() == 0
     sm.set_shared_sv(np.zeros((4, 8), np.float16))
     assert not sm.shared_sv_quant.is_quantized() and tuple(sm.shared_sv.shape) == (4, 8)
+
+
+@pytest.mark.parametrize("rows,cols,group", [(512, 4096, 128), (37, 90, 16), (9, 8, 8)])
+def test_product_packer_matches_producer(oracle_mod, rows, cols, group):
+    """tris_moe_amd.packing.pack_4bit lays its payload out exactly as the oracle's restatement of the
+    reference producer does for the same scales and zeros."""
+    from tris_moe_amd.packing import pack_4bit
+
+    rng = np.random.default_rng(rows + cols)
+    m = (rng.standard_normal((rows, cols)) * 0.1).astype(np.float32)
+    pl = pack_4bit(m, group)
+    z = (((pl["qzeros"].view(np.uint32)[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF)
+         .reshape(pl["qzeros"].shape[0], -1)[:, :rows].astype(np.int64) + 1) & 0xF   # stored z - 1 -> z
+    ref = oracle_mod.packed4_build_payload(m, pl["scales"].astype(np.float32), z.astype(np.float32), pl["g_idx"])
+    for key in ("qweight", "qzeros", "scales", "g_idx"):
+        np.testing.assert_array_equal(pl[key], ref[key], err_msg=key)
+    w = oracle_mod.packed4_dequant(pl["qweight"], pl["qzeros"], pl["scales"], pl["g_idx"], rows, cols)
+    s = pl["scales"].astype(np.float32)[pl["g_idx"]].T
+    assert (np.abs(w.astype(np.float32) - m) <= s * 0.5 * (1 + 1e-3) + np.abs(w.astype(np.float32)) * 2.0 ** -11).all()
