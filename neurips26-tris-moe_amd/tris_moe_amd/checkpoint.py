@@ -1,0 +1,351 @@
+"""Grouped runtime payload checkpoints (safetensors).
+
+Reads and writes the reference's checkpoint layout for the grouped expert path
+(``grouped_payload_sidecar.py:18-135`` key scheme and scalar encoding, ``:160-337``
+decoding, compatibility checks and repair, ``:340-361`` inspection, ``:586-698``
+loading), so that exported TriS-MoE checkpoints load into this build without the
+AutoGPTQ loader:
+
+* expert payloads: ``{layer_prefix}.grouped_payload.{gate|up|down}.{name}`` with
+  ``layer_prefix`` ``model.layers.{i}.block_sparse_moe`` (Mixtral) or
+  ``model.layers.{i}.mlp`` (OLMoE / Qwen-MoE); Python scalars are stored as
+  one-element tensors (bool or int32), ``None`` as an empty tensor; names
+  starting with ``_`` (derived caches) are never written;
+* shared backbones (the ``ExpertSharedMatrix`` banks of a layer,
+  ``modeling/_utils.py:135-177``): ``model.layers.{i}.TriS_shared_{proj}_proj.shared_sv``
+  (fp16 [rank, in]) or ``....shared_sv_quant.{qweight,qzeros,scales,g_idx,rows,cols}``
+  (4-bit packed, ``qlinear_cuda.py:2637-2786``).
+
+Loading returns the stacked payload dicts the grouped kernels take (device
+tensors, scalars as Python values, the uniform-K64 proof taken once).  Payloads
+stored with the sparse split bitmap (``q_gmap_sparse`` + prefix, no block-GR
+words) are converted to block-GR on load: the bitmap is expanded to its dense
+form and GR-coded with this build's encoder (the format the kernels read).
+Null-space compensation payloads (``*_ns`` cache keys) are outside this path and
+are skipped.  Host-side I/O only; nothing here runs on the GPU except the final
+copies.
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import torch
+
+GROUPED_PAYLOAD_SIDECAR_BASENAME = "grouped_runtime_payload.safetensors"
+GROUPED_PAYLOAD_METADATA = {"format": "olmoe_grouped_runtime_payload_v1"}
+GROUPED_PAYLOAD_EMBEDDED_METADATA_KEY = "olmoe_grouped_runtime_payload"
+GROUPED_PRECOMPUTED_KEYS = ("gate", "up", "down")
+GROUPED_QGMAP_PAYLOAD_NAMES = frozenset({"q_gmap_sparse", "q_gmap_sparse_prefix"})
+SCALAR_NAMES = frozenset({"is_compact3", "compact3_use_block_gr", "has_output_scale", "has_bias", "max_ns_rank",
+                          "infeatures", "outfeatures", "group_size"})
+BOOL_NAMES = frozenset({"is_compact3", "compact3_use_block_gr", "has_output_scale", "has_bias"})
+PROJ_MODULE = {"gate": "gate_proj", "up": "up_proj", "down": "down_proj"}
+PACKED4_NAMES = ("qweight", "qzeros", "scales", "g_idx", "rows", "cols")
+MARKER = ".grouped_payload."
+
+
+# ------------------------------------------------------------------------------------------------ names
+def payload_tensor_name(layer_prefix: str, cache_key: str, name: str) -> str:
+    """grouped_payload_sidecar.py:104-105."""
+    return f"{layer_prefix}{MARKER}{cache_key}.{name}"
+
+
+def split_payload_tensor_name(name: str):
+    """(layer_prefix, cache_key, payload_name) of a payload tensor key, else None (:112-122)."""
+    if MARKER not in name:
+        return None
+    layer_prefix, rest = name.split(MARKER, 1)
+    if "." not in rest:
+        return None
+    cache_key, payload_name = rest.split(".", 1)
+    if not cache_key or not payload_name:
+        return None
+    return layer_prefix, cache_key, payload_name
+
+
+def moe_layer_prefix(layer_idx: int, family: str = "mixtral") -> str:
+    """The MoE block of decoder layer i (grouped_payload_sidecar.py:54-80)."""
+    return f"model.layers.{layer_idx}.block_sparse_moe" if family == "mixtral" else f"model.layers.{layer_idx}.mlp"
+
+
+def shared_bank_prefix(layer_idx: int, proj: str) -> str:
+    """The ExpertSharedMatrix of (layer, projection): attribute TriS_shared_{gate|up|down}_proj of the
+    decoder layer (modeling/_utils.py:135-177)."""
+    return f"model.layers.{layer_idx}.TriS_shared_{PROJ_MODULE[proj]}"
+
+
+# ------------------------------------------------------------------------------------------------ write
+def encode_payload_tensor(value):
+    """A payload value as a checkpoint tensor (grouped_payload_sidecar.py:172-184): arrays as they are
+    (0-d made 1-element), bool -> bool [1], int -> int32 [1], None -> empty fp16."""
+    if isinstance(value, torch.Tensor):
+        value = value.detach().to("cpu").contiguous()
+        return value.reshape(1) if value.ndim == 0 else value
+    if isinstance(value, np.ndarray):
+        t = torch.from_numpy(np.ascontiguousarray(value))
+        return t.reshape(1) if t.ndim == 0 else t
+    if value is None:
+        return torch.empty((0,), dtype=torch.float16)
+    if isinstance(value, (bool, np.bool_)):
+        return torch.tensor([bool(value)], dtype=torch.bool)
+    if isinstance(value, (int, np.integer)):
+        return torch.tensor([int(value)], dtype=torch.int32)
+    raise TypeError(f"unsupported grouped payload value {type(value)!r}")
+
+
+def payload_tensors(layer_prefix: str, cache_key: str, payload: dict) -> dict:
+    """Checkpoint tensors of one stacked payload; derived caches (names starting with '_') and the
+    host-only dense split bitmap are left out."""
+    out = {}
+    for name, value in payload.items():
+        if name.startswith("_") or name == "gmap_dense":
+            continue
+        out[payload_tensor_name(layer_prefix, cache_key, name)] = encode_payload_tensor(value)
+    return out
+
+
+def backbone_tensors(layer_idx: int, proj: str, backbone) -> dict:
+    """Checkpoint tensors of one shared backbone: an fp16 SV [rank, in], or a packed 4-bit payload dict
+    (qweight, qzeros, scales, g_idx, rows, cols)."""
+    prefix = shared_bank_prefix(layer_idx, proj)
+    if isinstance(backbone, dict):
+        out = {}
+        for k in PACKED4_NAMES:
+            v = backbone[k]
+            if k in ("rows", "cols"):  # 0-d int32 buffers, as PackedQuantMatrix4bit registers them
+                out[f"{prefix}.shared_sv_quant.{k}"] = torch.tensor(int(v), dtype=torch.int32)
+            else:
+                out[f"{prefix}.shared_sv_quant.{k}"] = encode_payload_tensor(v)
+        return out
+    return {f"{prefix}.shared_sv": encode_payload_tensor(np.asarray(backbone, dtype=np.float16))}
+
+
+def save_grouped_checkpoint(path: str, layers: list, family: str = "mixtral", backbones: list | None = None,
+                            metadata: dict | None = None) -> str:
+    """Write decoder layers' grouped payloads (``layers[i] = {"gate": payload, "up": ..., "down": ...}``,
+    host arrays) and optionally their shared backbones (``backbones[i] = {proj: SV or packed payload}``) in the
+    reference's key scheme, with the sidecar metadata (:542-557)."""
+    from safetensors.torch import save_file
+
+    tensors = {}
+    for i, layer in enumerate(layers):
+        for key in GROUPED_PRECOMPUTED_KEYS:
+            tensors.update(payload_tensors(moe_layer_prefix(i, family), key, layer[key]))
+        if backbones is not None:
+            for proj in GROUPED_PRECOMPUTED_KEYS:
+                tensors.update(backbone_tensors(i, proj, backbones[i][proj]))
+    meta = dict(GROUPED_PAYLOAD_METADATA)
+    if metadata:
+        meta.update({str(k): str(v) for k, v in metadata.items()})
+    os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+    save_file(tensors, path, metadata=meta)
+    return path
+
+
+# ------------------------------------------------------------------------------------------------ repair
+def repair_grouped_payload_tensors(tensors: dict) -> int:
+    """In place: a compact3 payload whose output_scale is all zeros gets ones and has_output_scale False
+    (grouped_payload_sidecar.py:307-337).  Returns the number of payloads repaired."""
+    groups = {}
+    for name in tensors:
+        split = split_payload_tensor_name(name)
+        if split is None or split[1] not in GROUPED_PRECOMPUTED_KEYS:
+            continue
+        groups.setdefault(split[:2], {})[split[2]] = name
+    repaired = 0
+    for names in groups.values():
+        c3, osn = names.get("is_compact3"), names.get("output_scale")
+        if c3 is None or osn is None:
+            continue
+        is_c3, scale = tensors[c3], tensors[osn]
+        if is_c3.numel() == 0 or not bool(is_c3.reshape(-1)[0]) or scale.numel() == 0 or bool((scale != 0).any()):
+            continue
+        tensors[osn] = torch.ones_like(scale)
+        if "has_output_scale" in names:
+            tensors[names["has_output_scale"]] = torch.zeros_like(tensors[names["has_output_scale"]],
+                                                                   dtype=torch.bool)
+        repaired += 1
+    return repaired
+
+
+def sparse_gmap_to_dense(q_gmap_sparse: np.ndarray, prefix: np.ndarray, c_map: np.ndarray, rank: int) -> np.ndarray:
+    """The dense split bitmap (int32 [rank/32, N], zeros at salient columns) of one expert from its sparse
+    form: the j-th non-salient column (k order) has its bits in word j // 32, bit j % 32
+    (TriSMoE_cuda_kernel.cu:619-637; the inverse of pack_sparse_bool_matrix)."""
+    from .packing import pack_bool_matrix
+
+    words = np.asarray(q_gmap_sparse).astype(np.uint32)
+    n = words.shape[1]
+    cm = np.asarray(c_map).astype(np.uint32)
+    salient = ((cm[np.arange(rank) // 32] >> (np.arange(rank) % 32).astype(np.uint32)) & 1).astype(bool)
+    active = np.flatnonzero(~salient)
+    pre = np.asarray(prefix, dtype=np.int64)
+    if active.size and pre.size > 1 and int(pre[-1]) != active.size:
+        raise ValueError(f"q_gmap_sparse_prefix counts {int(pre[-1])} non-salient columns, c_map {active.size}")
+    dense = np.zeros((n, rank), dtype=bool)
+    if active.size:
+        j = np.arange(active.size)
+        dense[:, active] = ((words[j // 32] >> (j % 32).astype(np.uint32)[:, None]) & 1).astype(bool).T
+    return pack_bool_matrix(dense)
+
+
+def _to_block_gr(payload: dict) -> dict:
+    """A sparse-bitmap compact3 payload as block-GR: per expert dense bitmap, GR-coded, stacked with zero
+    padding (qlinear_cuda.py:1551-1601)."""
+    from . import ext
+
+    qs = payload["q_gmap_sparse"].cpu().numpy()
+    pre = payload["q_gmap_sparse_prefix"].cpu().numpy()
+    cmap = payload["c_map"].cpu().numpy()
+    rank = int(payload["g_idx"].shape[1])
+    coded = [ext.gr_encode(sparse_gmap_to_dense(qs[e], pre[e], cmap[e], rank)) for e in range(qs.shape[0])]
+    width = max(c[0].size for c in coded)
+    words = np.zeros((len(coded), width), dtype=np.int32)
+    for e, c in enumerate(coded):
+        words[e, : c[0].size] = c[0]
+    dev = payload["qweight1"].device
+    out = {k: v for k, v in payload.items() if k not in GROUPED_QGMAP_PAYLOAD_NAMES}
+    out["q_gmap_gr_words"] = torch.from_numpy(words).to(dev)
+    out["q_gmap_gr_offsets"] = torch.from_numpy(np.stack([c[1] for c in coded])).to(dev)
+    out["q_gmap_gr_meta"] = torch.from_numpy(np.stack([c[2] for c in coded])).to(dev)
+    out["compact3_use_block_gr"] = True
+    return out
+
+
+def _k64_uniform(g_idx: torch.Tensor) -> bool:
+    """Every 64-column K tile of every expert lies in one group (qlinear_cuda.py:364-381)."""
+    rank = int(g_idx.shape[-1])
+    first = g_idx[..., (torch.arange(rank, device=g_idx.device) // 64) * 64]
+    return bool(torch.equal(first, g_idx))
+
+
+def decode_payload(raw: dict, device, dtype=torch.float16) -> dict | None:
+    """One stacked payload from its checkpoint tensors (grouped_payload_sidecar.py:187-193, 248-304,
+    630-643): floating tensors to ``dtype``, integer tensors to int32/int64 as stored, 1-element scalars to
+    Python values, an all-zero output_scale repaired to ones, empty bias to None, sparse bitmaps converted to
+    block-GR; None when it is not a compact3 payload this path runs."""
+    p = {}
+    for name, t in raw.items():
+        if name in SCALAR_NAMES and t.numel() == 1:
+            v = t.reshape(-1)[0].item()
+            p[name] = bool(v) if name in BOOL_NAMES else int(v)
+        elif t.is_floating_point():
+            p[name] = t.to(device=device, dtype=dtype).contiguous()
+        else:
+            p[name] = t.to(device=device).contiguous()
+    if not p.get("is_compact3", False):
+        return None
+    scale = p.get("output_scale")
+    if isinstance(scale, torch.Tensor) and scale.numel() and not bool((scale != 0).any()):
+        p["output_scale"] = torch.ones_like(scale)
+        p["has_output_scale"] = False
+    bias = p.get("bias")
+    if isinstance(bias, torch.Tensor) and bias.numel() == 0:
+        p["bias"] = None
+        p["has_bias"] = False
+    if not p.get("compact3_use_block_gr", False) or "q_gmap_gr_words" not in p:
+        if not GROUPED_QGMAP_PAYLOAD_NAMES <= set(p):
+            return None
+        p = _to_block_gr(p)
+    for key in ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx", "col_pack3", "row_pack3",
+                "output_scale"):
+        if key not in p:
+            raise ValueError(f"grouped payload lacks {key}")
+    if "has_output_scale" not in p:
+        p["has_output_scale"] = not bool(torch.all(p["output_scale"] == 1).item())
+    p.setdefault("has_bias", p.get("bias") is not None)
+    p["_compact3_k64_groups_uniform"] = _k64_uniform(p["g_idx"])
+    return p
+
+
+# ------------------------------------------------------------------------------------------------ read
+class GroupedCheckpoint:
+    """A safetensors checkpoint (sidecar or full model file) holding grouped payloads and shared banks.
+
+    ``layer_prefixes()`` lists the MoE blocks with payloads; ``load_layer(prefix, device)`` returns
+    ``{"gate", "up", "down"}`` payload dicts; ``load_backbones(i, device)`` the layer's shared backbones (fp16
+    tensors or ``qlinear.PackedQuantMatrix4bit`` modules)."""
+
+    def __init__(self, path: str):
+        from safetensors import safe_open
+
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        self.path = path
+        self._f = safe_open(path, framework="pt", device="cpu")
+        self.metadata = dict(self._f.metadata() or {})
+        self._keys = list(self._f.keys())
+        self._payload_keys = {}
+        for k in self._keys:
+            split = split_payload_tensor_name(k)
+            if split is not None:
+                self._payload_keys.setdefault(split[:2], {})[split[2]] = k
+
+    def keys(self):
+        return list(self._keys)
+
+    def layer_prefixes(self) -> list:
+        def order(prefix):
+            parts = prefix.split(".")
+            return (int(parts[2]) if len(parts) > 2 and parts[2].isdigit() else -1, prefix)
+        return sorted({lp for lp, key in self._payload_keys if key in GROUPED_PRECOMPUTED_KEYS}, key=order)
+
+    def compatibility(self):
+        """(ok, reason) like inspect_grouped_payload_sidecar_compatibility (grouped_payload_sidecar.py:340-361),
+        for the block-GR/sparse compact3 payloads this path loads."""
+        if not self._payload_keys:
+            return False, "checkpoint contains no grouped payload tensors"
+        for (lp, key), names in sorted(self._payload_keys.items()):
+            if key not in GROUPED_PRECOMPUTED_KEYS:
+                continue
+            need = {"is_compact3", "qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx",
+                    "col_pack3", "row_pack3", "output_scale"}
+            gr = {"q_gmap_gr_words", "q_gmap_gr_offsets", "q_gmap_gr_meta"}
+            if not need <= set(names) or not (gr <= set(names) or GROUPED_QGMAP_PAYLOAD_NAMES <= set(names)):
+                return False, f"incomplete grouped payload: {lp}:{key}"
+        return True, None
+
+    def raw_payload(self, layer_prefix: str, cache_key: str) -> dict | None:
+        names = self._payload_keys.get((layer_prefix, cache_key))
+        if names is None:
+            return None
+        return {n: self._f.get_tensor(k) for n, k in names.items()}
+
+    def load_payload(self, layer_prefix: str, cache_key: str, device, dtype=torch.float16) -> dict | None:
+        raw = self.raw_payload(layer_prefix, cache_key)
+        return None if raw is None else decode_payload(raw, device, dtype)
+
+    def load_layer(self, layer_prefix: str, device, dtype=torch.float16) -> dict:
+        out = {}
+        for key in GROUPED_PRECOMPUTED_KEYS:
+            p = self.load_payload(layer_prefix, key, device, dtype)
+            if p is None:
+                raise KeyError(f"{self.path}: no compact3 grouped payload {layer_prefix}:{key}")
+            out[key] = p
+        return out
+
+    def load_layer_numpy(self, layer_prefix: str) -> dict:
+        """load_layer on the host with numpy arrays (the form ``streaming.GroupedPayloadStreamer`` packs into
+        pinned layer blobs)."""
+        layer = self.load_layer(layer_prefix, "cpu")
+        return {proj: {k: (v.numpy() if isinstance(v, torch.Tensor) else v) for k, v in p.items()}
+                for proj, p in layer.items()}
+
+    def load_backbones(self, layer_idx: int, device) -> dict:
+        from .qlinear import PackedQuantMatrix4bit
+
+        out = {}
+        for proj in GROUPED_PRECOMPUTED_KEYS:
+            prefix = shared_bank_prefix(layer_idx, proj)
+            quant = {n: f"{prefix}.shared_sv_quant.{n}" for n in PACKED4_NAMES}
+            if all(k in self._keys for k in quant.values()) and self._f.get_tensor(quant["qweight"]).numel() > 0:
+                t = {n: self._f.get_tensor(k) for n, k in quant.items()}
+                out[proj] = PackedQuantMatrix4bit().set_quantized(
+                    t["qweight"], t["qzeros"], t["scales"].to(torch.float16), t["g_idx"], int(t["rows"].reshape(-1)[0]),
+                    int(t["cols"].reshape(-1)[0])).to(device)
+            elif f"{prefix}.shared_sv" in self._keys:
+                out[proj] = self._f.get_tensor(f"{prefix}.shared_sv").to(device=device, dtype=torch.float16).contiguous()
+            else:
+                raise KeyError(f"{self.path}: no shared backbone {prefix}")
+        return out

@@ -1,0 +1,169 @@
+"""Grouped payload checkpoints (tris_moe_amd.checkpoint): the reference's safetensors key scheme and scalar
+encoding (grouped_payload_sidecar.py:18-135, 172-193), its load-time repair (:248-337), sparse-bitmap payloads
+converted to block-GR, shared backbones (fp16 and 4-bit packed); on the GPU a layer loaded from a checkpoint
+gives the bits of the same layer built in memory."""
+import numpy as np
+import pytest
+import torch
+
+from tris_moe_amd import checkpoint as ck
+from tris_moe_amd.configs import MoELayerSpec
+
+TINY = MoELayerSpec("tiny", hidden=256, num_experts=4, intermediate=384, top_k=2, rank=128, tokens=(3,))
+
+
+def _save(tris, tmp_path, n=2, packed_down=False, family="mixtral"):
+    layers = [tris["synthetic"].make_layer(TINY, 100 + i, tris["ext"].gr_encode) for i in range(n)]
+    bbs = []
+    for L in layers:
+        bb = dict(L["backbones"])
+        if packed_down:
+            from tris_moe_amd.packing import pack_4bit
+            bb["down"] = pack_4bit(bb["down"].astype(np.float32), 64)
+        bbs.append(bb)
+    path = str(tmp_path / ck.GROUPED_PAYLOAD_SIDECAR_BASENAME)
+    ck.save_grouped_checkpoint(path, [{p: L[p] for p in ck.GROUPED_PRECOMPUTED_KEYS} for L in layers], family,
+                               bbs, metadata={"model": "tiny"})
+    return path, layers, bbs
+
+
+def test_key_scheme_and_scalars(tris, tmp_path):
+    from safetensors import safe_open
+
+    path, layers, _ = _save(tris, tmp_path)
+    with safe_open(path, framework="pt") as f:
+        keys = set(f.keys())
+        meta = f.metadata()
+        assert meta["format"] == "olmoe_grouped_runtime_payload_v1" and meta["model"] == "tiny"
+        assert "model.layers.0.block_sparse_moe.grouped_payload.gate.qweight1" in keys
+        assert "model.layers.1.block_sparse_moe.grouped_payload.down.q_gmap_gr_words" in keys
+        assert "model.layers.0.TriS_shared_up_proj.shared_sv" in keys
+        assert not any(k.split(".")[-1].startswith("_") for k in keys)   # derived caches stay out
+        t = f.get_tensor("model.layers.0.block_sparse_moe.grouped_payload.gate.is_compact3")
+        assert t.dtype == torch.bool and tuple(t.shape) == (1,) and bool(t[0])
+        assert f.get_tensor("model.layers.0.block_sparse_moe.grouped_payload.gate.bias").numel() == 0
+    assert ck.split_payload_tensor_name("model.layers.3.mlp.grouped_payload.up_ns.ns_c1_qweight") == \
+        ("model.layers.3.mlp", "up_ns", "ns_c1_qweight")
+    assert ck.split_payload_tensor_name("model.layers.3.mlp.experts.0.w1") is None
+    assert ck.moe_layer_prefix(5, "olmoe") == "model.layers.5.mlp"
+
+
+def test_round_trip_on_host(tris, tmp_path):
+    path, layers, bbs = _save(tris, tmp_path, packed_down=True)
+    c = ck.GroupedCheckpoint(path)
+    assert c.compatibility() == (True, None)
+    assert c.layer_prefixes() == ["model.layers.0.block_sparse_moe", "model.layers.1.block_sparse_moe"]
+    for i, lp in enumerate(c.layer_prefixes()):
+        got = c.load_layer(lp, "cpu")
+        for proj in ck.GROUPED_PRECOMPUTED_KEYS:
+            want = layers[i][proj]
+            for key, val in want.items():
+                if key == "gmap_dense":
+                    continue
+                if isinstance(val, np.ndarray):
+                    np.testing.assert_array_equal(got[proj][key].numpy(), val, err_msg=f"{lp} {proj} {key}")
+                else:
+                    assert got[proj][key] == val, (proj, key)
+        host = c.load_layer_numpy(lp)   # the host form the streaming loader packs
+        for proj in ck.GROUPED_PRECOMPUTED_KEYS:
+            np.testing.assert_array_equal(host[proj]["q_gmap_gr_words"], layers[i][proj]["q_gmap_gr_words"])
+            assert host[proj]["bias"] is None and host[proj]["is_compact3"] is True
+        bb = c.load_backbones(i, "cpu")
+        np.testing.assert_array_equal(bb["gate"].numpy(), bbs[i]["gate"])
+        assert bb["down"].is_quantized() and bb["down"].group_size == 64
+        np.testing.assert_array_equal(bb["down"].qweight.numpy(), bbs[i]["down"]["qweight"])
+
+
+def test_zero_output_scale_is_repaired(tris, tmp_path):
+    """A compact3 payload saved with an all-zero output_scale loads with ones and has_output_scale False,
+    and repair_grouped_payload_tensors fixes the tensors in place (grouped_payload_sidecar.py:248-337)."""
+    layer = tris["synthetic"].make_layer(TINY, 7, tris["ext"].gr_encode)
+    pls = {p: dict(layer[p]) for p in ck.GROUPED_PRECOMPUTED_KEYS}
+    pls["up"]["output_scale"] = np.zeros_like(pls["up"]["output_scale"])
+    pls["up"]["has_output_scale"] = True
+    path = str(tmp_path / "c.safetensors")
+    ck.save_grouped_checkpoint(path, [pls])
+    got = ck.GroupedCheckpoint(path).load_layer("model.layers.0.block_sparse_moe", "cpu")
+    assert got["up"]["has_output_scale"] is False and bool((got["up"]["output_scale"] == 1).all())
+    tensors = ck.payload_tensors("L", "up", pls["up"])
+    assert ck.repair_grouped_payload_tensors(tensors) == 1
+    assert bool((tensors["L.grouped_payload.up.output_scale"] == 1).all())
+    assert not bool(tensors["L.grouped_payload.up.has_output_scale"][0])
+
+
+def test_sparse_bitmap_payload_converts_to_block_gr(tris, tmp_path):
+    """A payload in the sparse split-bitmap format (q_gmap_sparse over the non-salient columns + prefix, no GR
+    words) loads as block-GR with the words this build's encoder gives for the same dense bitmap."""
+    from tris_moe_amd.packing import pack_sparse_bool_matrix, sparse_prefix, pack_bool_matrix
+
+    syn, ext = tris["synthetic"], tris["ext"]
+    layer = syn.make_layer(TINY, 9, ext.gr_encode)
+    rng = np.random.default_rng(1)
+    pls = {}
+    for proj in ck.GROUPED_PRECOMPUTED_KEYS:
+        p = dict(layer[proj])
+        E, _, n = p["qweight1"].shape
+        rank = p["g_idx"].shape[1]
+        sparse, prefix, dense_words = [], [], []
+        for e in range(E):
+            sal = ((p["c_map"][e].astype(np.uint32)[np.arange(rank) // 32] >> (np.arange(rank) % 32).astype(np.uint32))
+                   & 1).astype(bool)
+            dense = (rng.random((n, rank)) < 0.2) & ~sal[None, :]
+            sparse.append(pack_sparse_bool_matrix(dense, ~sal))
+            prefix.append(sparse_prefix(~sal))
+            dense_words.append(pack_bool_matrix(dense))
+        rows = max(s.shape[0] for s in sparse)
+        p["q_gmap_sparse"] = np.stack([np.pad(s, ((0, rows - s.shape[0]), (0, 0))) for s in sparse])
+        p["q_gmap_sparse_prefix"] = np.stack(prefix)
+        for k in ("q_gmap_gr_words", "q_gmap_gr_offsets", "q_gmap_gr_meta"):
+            del p[k]
+        p["compact3_use_block_gr"] = False
+        p["_dense"] = dense_words
+        pls[proj] = p
+    path = str(tmp_path / "sparse.safetensors")
+    ck.save_grouped_checkpoint(path, [pls], family="olmoe")
+    got = ck.GroupedCheckpoint(path).load_layer("model.layers.0.mlp", "cpu")
+    for proj in ck.GROUPED_PRECOMPUTED_KEYS:
+        g = got[proj]
+        assert g["compact3_use_block_gr"] is True and "q_gmap_sparse" not in g
+        for e, dw in enumerate(pls[proj]["_dense"]):
+            words, offsets, meta = ext.gr_encode(dw)
+            np.testing.assert_array_equal(g["q_gmap_gr_offsets"][e].numpy(), offsets)
+            np.testing.assert_array_equal(g["q_gmap_gr_meta"][e].numpy(), meta)
+            np.testing.assert_array_equal(g["q_gmap_gr_words"][e, : words.size].numpy(), words)
+
+
+def test_incomplete_checkpoint_is_reported(tris, tmp_path):
+    from safetensors.torch import save_file
+
+    path = str(tmp_path / "bad.safetensors")
+    save_file({"model.layers.0.mlp.grouped_payload.gate.qweight1": torch.zeros(1, dtype=torch.int32)}, path)
+    ok, reason = ck.GroupedCheckpoint(path).compatibility()
+    assert not ok and "model.layers.0.mlp:gate" in reason
+    save_file({"x": torch.zeros(1)}, path)
+    assert ck.GroupedCheckpoint(path).compatibility()[0] is False
+
+
+@pytest.mark.gpu
+def test_checkpoint_layer_runs_like_memory(tris, cuda, tmp_path):
+    """Two layers loaded from a checkpoint (one with a packed down backbone) give the bits of the same layers
+    built from the in-memory payloads."""
+    print("checkpoint layer", flush=True)
+    path, layers, bbs = _save(tris, tmp_path, packed_down=True)
+    c = ck.GroupedCheckpoint(path)
+    ql, moe = tris["qlinear"], tris["moe"]
+    rng = np.random.default_rng(5)
+    x16 = torch.from_numpy(rng.standard_normal((3, TINY.hidden)).astype(np.float16)).to(cuda)
+    logits = torch.from_numpy(rng.standard_normal((3, TINY.num_experts)).astype(np.float32)).to(cuda)
+    for i, lp in enumerate(c.layer_prefixes()):
+        loaded = c.load_layer(lp, cuda)
+        lbb = c.load_backbones(i, cuda)
+        mem = {p: ql.payload_to_device(layers[i][p], cuda) for p in ck.GROUPED_PRECOMPUTED_KEYS}
+        mbb = {p: torch.from_numpy(bbs[i][p]).to(cuda) for p in ("gate", "up")}
+        mbb["down"] = ql.PackedQuantMatrix4bit().set_from_payload(bbs[i]["down"]).to(cuda)
+        a = moe.grouped_moe_forward_from_logits(x16, logits, TINY.top_k, TINY.renormalize, loaded, lbb,
+                                                TINY.num_experts, torch.bfloat16)
+        b = moe.grouped_moe_forward_from_logits(x16, logits, TINY.top_k, TINY.renormalize, mem, mbb,
+                                                TINY.num_experts, torch.bfloat16)
+        torch.cuda.synchronize()
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), lp
