@@ -316,6 +316,51 @@ int tris_packed4_backbone_linear_pair(const uint16_t* x, int32_t tokens, const i
                                       int64_t workspace_bytes, void* stream);
 
 /*
+ * Matrix-mode null-space compensation payload of one projection (build_grouped_ns_compensation_payload,
+ * qlinear_cuda.py:1734-1872): per expert e two 4-bit packed matrices (PackedQuantMatrix4bit layout),
+ * C2_e [rank_e, in] and C1_e [out, rank_e], concatenated over the experts:
+ *   C2: qweight int32 [ceil(in/8), total_rank], qzeros int32 [ceil(in/group_size), total_rank_words],
+ *       scales fp16 [ceil(in/group_size), total_rank]; expert e's rows start at column
+ *       ns_c2_rank_offsets[e] (qzeros: ns_c2_rank_word_offsets[e]); experts may share a C2.
+ *   C1: qweight int32 [sum ceil(rank_e/8), out] from row ns_c1_rank_word_offsets[e], qzeros int32
+ *       [sum groups_e, ceil(out/8)] and scales fp16 [sum groups_e, out] from row ns_c1_group_offsets[e];
+ *       groups of min(rank_e, group_size) columns.
+ * ns_rank_per_expert[e] == 0: no compensation for expert e.
+ */
+typedef struct tris_ns_payload {
+  const int32_t* ns_rank_per_expert;       /* int32 [E] */
+  const int32_t* ns_c2_rank_offsets;       /* int32 [E] */
+  const int32_t* ns_c2_rank_word_offsets;  /* int32 [E] */
+  const int32_t* ns_c1_rank_word_offsets;  /* int32 [E] */
+  const int32_t* ns_c1_group_offsets;      /* int32 [E] */
+  const int32_t* ns_c2_qweight;
+  const int32_t* ns_c2_qzeros;
+  const uint16_t* ns_c2_scales;
+  const int32_t* ns_c1_qweight;
+  const int32_t* ns_c1_qzeros;
+  const uint16_t* ns_c1_scales;
+  int32_t num_experts;
+  int32_t infeatures;
+  int32_t outfeatures;
+  int32_t max_ns_rank;                     /* <= 512 */
+  int32_t group_size;
+  int32_t total_rank;                      /* ns_c2_qweight / ns_c2_scales columns */
+  int32_t total_rank_words;                /* ns_c2_qzeros columns */
+} tris_ns_payload;
+
+/*
+ * comp[r] = fp16(C1_e . fp16(C2_e . x_grouped[r])) for the rows r of every segment (e = its expert):
+ * replaces grouped_ns_compensation_forward (TriSMoE_cuda_kernel.cu:1208-2145) and, with accumulate != 0,
+ * the caller's out.add_(compensation) (qlinear_cuda.py:2322-2334): out[r] = fp16(out[r] + comp[r]);
+ * with accumulate == 0, out = comp.  x_grouped fp16 [batch, in]; hidden: fp16 workspace
+ * [batch, max_ns_rank] (no initial contents); out fp16 [batch, out].  Exact fp16 weights, fp32 sums.
+ */
+int tris_grouped_ns_compensation_forward(const uint16_t* x_grouped, int32_t batch, const int32_t* expert_ids,
+                                         const int32_t* segment_offsets, int32_t num_segments,
+                                         const tris_ns_payload* ns, uint16_t* hidden, uint16_t* out,
+                                         int32_t accumulate, void* stream);
+
+/*
  * Routing-weighted combine: replaces final.index_add_(0, grouped_token_indices,
  * (down_out * routing).to(output_dtype)) (modeling_mixtral.py:529-536).
  * out[t, :] = bf16( sum_s fp16(expert_out[inverse_perm[t*top_k+s], :] * weights[t, s])

@@ -79,6 +79,31 @@ class TrisPacked4(ctypes.Structure):
     ]
 
 
+class TrisNsPayload(ctypes.Structure):
+    """Mirror of struct tris_ns_payload."""
+
+    _fields_ = [
+        ("ns_rank_per_expert", ctypes.c_void_p),
+        ("ns_c2_rank_offsets", ctypes.c_void_p),
+        ("ns_c2_rank_word_offsets", ctypes.c_void_p),
+        ("ns_c1_rank_word_offsets", ctypes.c_void_p),
+        ("ns_c1_group_offsets", ctypes.c_void_p),
+        ("ns_c2_qweight", ctypes.c_void_p),
+        ("ns_c2_qzeros", ctypes.c_void_p),
+        ("ns_c2_scales", ctypes.c_void_p),
+        ("ns_c1_qweight", ctypes.c_void_p),
+        ("ns_c1_qzeros", ctypes.c_void_p),
+        ("ns_c1_scales", ctypes.c_void_p),
+        ("num_experts", ctypes.c_int32),
+        ("infeatures", ctypes.c_int32),
+        ("outfeatures", ctypes.c_int32),
+        ("max_ns_rank", ctypes.c_int32),
+        ("group_size", ctypes.c_int32),
+        ("total_rank", ctypes.c_int32),
+        ("total_rank_words", ctypes.c_int32),
+    ]
+
+
 MAX_PREDECODE_JOBS = 4
 
 _P = ctypes.c_void_p
@@ -86,6 +111,7 @@ _I32 = ctypes.c_int32
 _I64 = ctypes.c_int64
 _PAY = ctypes.POINTER(TrisPayload)
 _P4 = ctypes.POINTER(TrisPacked4)
+_PNS = ctypes.POINTER(TrisNsPayload)
 SIGNATURES = {
     "tris_abi_version": (ctypes.c_int, []),
     "tris_last_error": (ctypes.c_char_p, []),
@@ -113,6 +139,7 @@ SIGNATURES = {
     "tris_packed4_dequant": (ctypes.c_int, [_P4, _P, _P]),
     "tris_packed4_backbone_linear": (ctypes.c_int, [_P, _I32, _P, _P4, _P, _P, _P, _I64, _P]),
     "tris_packed4_backbone_linear_pair": (ctypes.c_int, [_P, _I32, _P, _P4, _P4, _P, _P, _P, _I64, _P]),
+    "tris_grouped_ns_compensation_forward": (ctypes.c_int, [_P, _I32, _P, _P, _I32, _PNS, _P, _P, _I32, _P]),
 }
 
 _lib = None

@@ -21,9 +21,11 @@ tensors, scalars as Python values, the uniform-K64 proof taken once).  Payloads
 stored with the sparse split bitmap (``q_gmap_sparse`` + prefix, no block-GR
 words) are converted to block-GR on load: the bitmap is expanded to its dense
 form and GR-coded with this build's encoder (the format the kernels read).
-Null-space compensation payloads (``*_ns`` cache keys) are outside this path and
-are skipped.  Host-side I/O only; nothing here runs on the GPU except the final
-copies.
+Matrix-mode null-space payloads (``gate_ns`` / ``up_ns`` / ``down_ns`` cache keys,
+``build_grouped_ns_compensation_payload`` layout) load next to them, checked like
+the reference's ``_sidecar_payload_is_compatible`` (:196-245) and bounds-checked
+before they reach a kernel.  Host-side I/O only; nothing here runs on the GPU
+except the final copies.
 """
 from __future__ import annotations
 
@@ -132,6 +134,8 @@ def save_grouped_checkpoint(path: str, layers: list, family: str = "mixtral", ba
     for i, layer in enumerate(layers):
         for key in GROUPED_PRECOMPUTED_KEYS:
             tensors.update(payload_tensors(moe_layer_prefix(i, family), key, layer[key]))
+            if layer.get(f"{key}_ns") is not None:
+                tensors.update(payload_tensors(moe_layer_prefix(i, family), f"{key}_ns", layer[f"{key}_ns"]))
         if backbones is not None:
             for proj in GROUPED_PRECOMPUTED_KEYS:
                 tensors.update(backbone_tensors(i, proj, backbones[i][proj]))
@@ -291,12 +295,54 @@ class GroupedCheckpoint:
             return (int(parts[2]) if len(parts) > 2 and parts[2].isdigit() else -1, prefix)
         return sorted({lp for lp, key in self._payload_keys if key in GROUPED_PRECOMPUTED_KEYS}, key=order)
 
+    def ns_compatible(self, layer_prefix: str, cache_key: str) -> bool:
+        """grouped_payload_sidecar.py:196-245: every null-space tensor present, offsets one per expert, block
+        shapes consistent with infeatures, outfeatures, group_size and the per-expert ranks."""
+        names = self._payload_keys.get((layer_prefix, cache_key), {})
+        need = ("ns_rank_per_expert", "ns_c2_rank_offsets", "ns_c2_rank_word_offsets", "ns_c1_rank_word_offsets",
+                "ns_c1_group_offsets", "max_ns_rank", "group_size", "infeatures", "outfeatures", "ns_c2_qweight",
+                "ns_c2_qzeros", "ns_c2_scales", "ns_c1_qweight", "ns_c1_qzeros", "ns_c1_scales")
+        if any(n not in names for n in need):
+            return False
+        t = {n: self._f.get_tensor(names[n]) for n in need}
+        scal = {n: int(t[n].reshape(-1)[0]) if t[n].numel() else 0 for n in ("group_size", "infeatures", "outfeatures")}
+        gs, inf, outf = scal["group_size"], scal["infeatures"], scal["outfeatures"]
+        if gs <= 0 or inf < 0 or outf < 0:
+            return False
+        E = int(t["ns_rank_per_expert"].numel())
+        if any(int(t[n].numel()) != E for n in ("ns_c2_rank_offsets", "ns_c2_rank_word_offsets",
+                                               "ns_c1_rank_word_offsets", "ns_c1_group_offsets")):
+            return False
+        if t["ns_c2_qweight"].ndim != 2 or int(t["ns_c2_qweight"].shape[0]) != (inf + 7) // 8:
+            return False
+        if t["ns_c2_qzeros"].ndim != 2 or t["ns_c2_scales"].ndim != 2:
+            return False
+        if int(t["ns_c2_qzeros"].shape[0]) != int(t["ns_c2_scales"].shape[0]) or \
+                int(t["ns_c2_qzeros"].shape[0]) != ((inf + gs - 1) // gs if inf > 0 else 0):
+            return False
+        if t["ns_c1_qweight"].ndim != 2 or int(t["ns_c1_qweight"].shape[1]) != outf:
+            return False
+        if t["ns_c1_qzeros"].ndim != 2 or int(t["ns_c1_qzeros"].shape[1]) != (outf + 7) // 8:
+            return False
+        if t["ns_c1_scales"].ndim != 2 or int(t["ns_c1_scales"].shape[1]) != outf:
+            return False
+        ranks = t["ns_rank_per_expert"].reshape(-1).to(torch.int64)
+        pos = ranks[ranks > 0]
+        words = int(((pos + 7) // 8).sum()) if pos.numel() else 0
+        groups = int(((pos + gs - 1) // gs).sum()) if pos.numel() else 0
+        return (int(t["ns_c1_qweight"].shape[0]) == words and int(t["ns_c1_qzeros"].shape[0]) == groups
+                and int(t["ns_c1_scales"].shape[0]) == groups)
+
     def compatibility(self):
         """(ok, reason) like inspect_grouped_payload_sidecar_compatibility (grouped_payload_sidecar.py:340-361),
         for the block-GR/sparse compact3 payloads this path loads."""
         if not self._payload_keys:
             return False, "checkpoint contains no grouped payload tensors"
         for (lp, key), names in sorted(self._payload_keys.items()):
+            if key.endswith("_ns") and key[:-3] in GROUPED_PRECOMPUTED_KEYS:
+                if not self.ns_compatible(lp, key):
+                    return False, f"incompatible grouped payload: {lp}:{key}"
+                continue
             if key not in GROUPED_PRECOMPUTED_KEYS:
                 continue
             need = {"is_compact3", "qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx",
@@ -316,13 +362,31 @@ class GroupedCheckpoint:
         raw = self.raw_payload(layer_prefix, cache_key)
         return None if raw is None else decode_payload(raw, device, dtype)
 
+    def load_ns_payload(self, layer_prefix: str, cache_key: str, device, dtype=torch.float16) -> dict | None:
+        """The null-space payload of ``cache_key`` (gate / up / down) on the device, or None when the checkpoint
+        has none; raises ValueError when it is present but inconsistent."""
+        from .qlinear import ns_payload_to_device
+
+        key = f"{cache_key}_ns"
+        raw = self.raw_payload(layer_prefix, key)
+        if raw is None:
+            return None
+        if not self.ns_compatible(layer_prefix, key):
+            raise ValueError(f"{self.path}: incompatible null-space payload {layer_prefix}:{key}")
+        host = {n: (int(t.reshape(-1)[0]) if n in SCALAR_NAMES and t.numel() == 1 else t) for n, t in raw.items()}
+        return ns_payload_to_device(host, device, dtype)
+
     def load_layer(self, layer_prefix: str, device, dtype=torch.float16) -> dict:
+        """{"gate", "up", "down"} payloads, plus "gate_ns" / "up_ns" / "down_ns" where the checkpoint has them."""
         out = {}
         for key in GROUPED_PRECOMPUTED_KEYS:
             p = self.load_payload(layer_prefix, key, device, dtype)
             if p is None:
                 raise KeyError(f"{self.path}: no compact3 grouped payload {layer_prefix}:{key}")
             out[key] = p
+            ns = self.load_ns_payload(layer_prefix, key, device, dtype)
+            if ns is not None:
+                out[f"{key}_ns"] = ns
         return out
 
     def load_layer_numpy(self, layer_prefix: str) -> dict:
@@ -330,7 +394,7 @@ class GroupedCheckpoint:
         pinned layer blobs)."""
         layer = self.load_layer(layer_prefix, "cpu")
         return {proj: {k: (v.numpy() if isinstance(v, torch.Tensor) else v) for k, v in p.items()}
-                for proj, p in layer.items()}
+                for proj, p in layer.items() if proj in GROUPED_PRECOMPUTED_KEYS}
 
     def load_backbones(self, layer_idx: int, device) -> dict:
         from .qlinear import PackedQuantMatrix4bit

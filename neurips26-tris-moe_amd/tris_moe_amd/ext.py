@@ -745,6 +745,69 @@ def packed4_linear_forward(input: torch.Tensor, qweight: torch.Tensor, qzeros: t
     return backbone_linear(input, packed4_dequant(m))
 
 
+# ----------------------------------------------------------------- null-space compensation
+NS_PAYLOAD_TENSORS = ("ns_rank_per_expert", "ns_c2_rank_offsets", "ns_c2_rank_word_offsets", "ns_c1_rank_word_offsets",
+                      "ns_c1_group_offsets", "ns_c2_qweight", "ns_c2_qzeros", "ns_c2_scales", "ns_c1_qweight",
+                      "ns_c1_qzeros", "ns_c1_scales")
+
+
+def _ns_struct(ns: dict, infeatures: int, device):
+    for k in ("ns_rank_per_expert", "ns_c2_rank_offsets", "ns_c2_rank_word_offsets", "ns_c1_rank_word_offsets",
+              "ns_c1_group_offsets"):
+        _check_cuda(k, ns[k], torch.int32, 1, device)
+    for k in ("ns_c2_qweight", "ns_c2_qzeros", "ns_c1_qweight", "ns_c1_qzeros"):
+        _check_cuda(k, ns[k], torch.int32, 2, device)
+    for k in ("ns_c2_scales", "ns_c1_scales"):
+        _check_cuda(k, ns[k], torch.float16, 2, device)
+    E = int(ns["ns_rank_per_expert"].numel())
+    if any(int(ns[k].numel()) != E for k in ("ns_c2_rank_offsets", "ns_c2_rank_word_offsets",
+                                             "ns_c1_rank_word_offsets", "ns_c1_group_offsets")):
+        raise RuntimeError("null-space payload: per-expert offset vectors differ in length")
+    if int(ns["ns_c2_qweight"].size(0)) != (infeatures + 7) // 8:
+        raise RuntimeError("null-space payload: ns_c2_qweight rows != ceil(infeatures / 8)")
+    return _lib.TrisNsPayload(*[_ptr(ns[k]) for k in NS_PAYLOAD_TENSORS], E, int(infeatures),
+                              int(ns["ns_c1_scales"].size(1)), int(ns["max_ns_rank"]), int(ns["group_size"]),
+                              int(ns["ns_c2_qweight"].size(1)), int(ns["ns_c2_qzeros"].size(1)))
+
+
+def ns_compensation_apply_(out: torch.Tensor, x_grouped: torch.Tensor, expert_ids: torch.Tensor,
+                           segment_offsets: torch.Tensor, ns: dict, accumulate: bool = True) -> torch.Tensor:
+    """out[r] = fp16(out[r] + C1_e . fp16(C2_e . x_grouped[r])) for every routed row (accumulate), or the
+    compensation alone: the grouped null-space term of run_grouped_structured_expert_forward
+    (qlinear_cuda.py:2322-2334) on the HIP kernels."""
+    _check_cuda("x_grouped", x_grouped, torch.float16, 2)
+    dev = x_grouped.device
+    _check_cuda("out", out, torch.float16, 2, dev)
+    _check_cuda("expert_ids", expert_ids, torch.int32, 1, dev)
+    _check_cuda("segment_offsets", segment_offsets, torch.int32, 1, dev)
+    st = _ns_struct(ns, int(x_grouped.size(1)), dev)
+    batch = int(x_grouped.size(0))
+    if out.size(0) != batch or out.size(1) != st.outfeatures:
+        raise RuntimeError("null-space compensation: out must be [batch, outfeatures]")
+    hidden = torch.empty((batch, max(st.max_ns_rank, 1)), dtype=torch.float16, device=dev)
+    _lib.check(_lib.load().tris_grouped_ns_compensation_forward(
+        _ptr(x_grouped), batch, _ptr(expert_ids), _ptr(segment_offsets), int(expert_ids.numel()), ctypes.byref(st),
+        _ptr(hidden), _ptr(out), int(bool(accumulate)), _stream(x_grouped)), "tris_grouped_ns_compensation_forward")
+    return out
+
+
+def grouped_ns_compensation_forward(x_grouped, expert_ids, segment_offsets, problem_offsets, total_problem_tiles,
+                                    ns_rank_per_expert, ns_c2_rank_offsets, ns_c2_rank_word_offsets,
+                                    ns_c1_rank_word_offsets, ns_c1_group_offsets, ns_c2_qweight, ns_c2_qzeros,
+                                    ns_c2_scales, ns_c1_qweight, ns_c1_qzeros, ns_c1_scales, max_ns_rank: int,
+                                    group_size: int, decode_phase: bool = False) -> torch.Tensor:
+    """The extension's grouped_ns_compensation_forward (TriSMoE_cuda_kernel.cu:1208-2145; called at
+    qlinear_cuda.py:2103-2124): fp16 [batch, out] compensation C1_e . (C2_e . x) per routed row."""
+    ns = {"ns_rank_per_expert": ns_rank_per_expert, "ns_c2_rank_offsets": ns_c2_rank_offsets,
+          "ns_c2_rank_word_offsets": ns_c2_rank_word_offsets, "ns_c1_rank_word_offsets": ns_c1_rank_word_offsets,
+          "ns_c1_group_offsets": ns_c1_group_offsets, "ns_c2_qweight": ns_c2_qweight, "ns_c2_qzeros": ns_c2_qzeros,
+          "ns_c2_scales": ns_c2_scales, "ns_c1_qweight": ns_c1_qweight, "ns_c1_qzeros": ns_c1_qzeros,
+          "ns_c1_scales": ns_c1_scales, "max_ns_rank": int(max_ns_rank), "group_size": int(group_size)}
+    out = torch.empty((int(x_grouped.size(0)), int(ns_c1_scales.size(1))), dtype=torch.float16,
+                      device=x_grouped.device)
+    return ns_compensation_apply_(out, x_grouped, expert_ids, segment_offsets, ns, accumulate=False)
+
+
 def moe_combine(expert_out: torch.Tensor, inverse_perm: torch.Tensor, weights: torch.Tensor,
                 shared: torch.Tensor | None = None) -> torch.Tensor:
     """bf16 [T, H] = sum_s fp16(expert_out[inverse_perm[t, s]] * weights[t, s]) (+ shared), fp32-accumulated."""

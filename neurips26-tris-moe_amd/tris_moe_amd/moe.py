@@ -40,8 +40,9 @@ def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, select
 
     x16 fp16 [T, H]; routing_weights [T, k] (cast to fp16 as in modeling_mixtral.py:555);
     selected_experts int64 [T, k]; payloads {gate, up, down} device payload dicts;
-    backbones {gate, up, down}: fp16 SV [rank, in] or qlinear.PackedQuantMatrix4bit.  Returns [T, H] in
-    output_dtype.
+    backbones {gate, up, down}: fp16 SV [rank, in] or qlinear.PackedQuantMatrix4bit.  payloads may also hold
+    matrix-mode null-space payloads under gate_ns / up_ns / down_ns (``qlinear.build_grouped_ns_payload``
+    format on the device).  Returns [T, H] in output_dtype.
 
     expert_path: "predecoded" decodes the split bitmaps once per projection and runs the MFMA
     grouped GEMMs (needs uniform 64-column groups and no output scale or bias); "fused" decodes
@@ -88,6 +89,7 @@ def _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, ou
     # Launch bound only: every padded segment past the active ones is empty.
     tile_bound = R // GROUPED_SEGMENT_M_TILE + min(num_experts, R) + 1
     pg, pu, pd = payloads["gate"], payloads["up"], payloads["down"]
+    ns = _ns_payloads(payloads)
     uniform = bool(pg.get("_compact3_k64_groups_uniform", False) and pu.get("_compact3_k64_groups_uniform", False))
     predecodable = uniform and bool(pd.get("_compact3_k64_groups_uniform", False)) and not any(
         bool(p["has_output_scale"]) or bool(p["has_bias"]) for p in (pg, pu, pd))
@@ -106,6 +108,11 @@ def _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, ou
         pu["qweight1"], pu["qweight2_sparse"], pu["qweight2_sparse_prefix"], pu["q_gmap_gr_words"],
         pu["q_gmap_gr_offsets"], pu["q_gmap_gr_meta"], pu["c_map"], pu["g_idx"], pu["col_pack3"], pu["row_pack3"],
         pu["output_scale"], bool(pu["has_output_scale"]), pu["bias"] if pu["has_bias"] else empty, uniform)
+    if ns["gate"] is not None or ns["up"] is not None:
+        x_g = x16.index_select(0, gti)
+        for out, key in ((g_out, "gate"), (u_out, "up")):
+            if ns[key] is not None:
+                ext.ns_compensation_apply_(out, x_g, expert_ids, seg, ns[key])
     mlp = F.silu(g_out) * u_out
     hid_d = shared_projection(mlp, backbones["down"])
     d_out = ext.compact3_tris_precomputed_grouped_forward_block_gr(
@@ -114,7 +121,19 @@ def _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, ou
         pd["q_gmap_gr_offsets"], pd["q_gmap_gr_meta"], pd["c_map"], pd["g_idx"], pd["col_pack3"], pd["row_pack3"],
         pd["output_scale"], bool(pd["has_output_scale"]), pd["bias"] if pd["has_bias"] else empty,
         bool(pd["has_bias"]), bool(pd.get("_compact3_k64_groups_uniform", False)))
+    if ns["down"] is not None:
+        ext.ns_compensation_apply_(d_out, mlp, expert_ids, seg, ns["down"])
     return _combine(x16, d_out, route, w16, output_dtype, shared_expert)
+
+
+def _ns_payloads(payloads: dict) -> dict:
+    """The layer's matrix-mode null-space payloads (keys gate_ns, up_ns, down_ns, as the reference's
+    _forward_grouped fetches them, modeling_mixtral.py:437-450, 503-509), None where absent or rank 0."""
+    out = {}
+    for key in ("gate", "up", "down"):
+        ns = payloads.get(f"{key}_ns")
+        out[key] = ns if isinstance(ns, dict) and int(ns.get("max_ns_rank", 0)) > 0 else None
+    return out
 
 
 def _combine(x16, d_out, route, w16, output_dtype, shared_expert):
@@ -162,6 +181,7 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     prob = route["problem_offsets"][: slots + 1]
     tile_bound = R // GROUPED_SEGMENT_M_TILE + slots + 1
     pg, pu, pd = payloads["gate"], payloads["up"], payloads["down"]
+    ns = _ns_payloads(payloads)
     dev = x16.device
     bufs = {name: _predecode_buffer(p, slots, dev) for name, p in (("gate", pg), ("up", pu), ("down", pd))}
     main = torch.cuda.current_stream(dev)
@@ -183,7 +203,7 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     # every routed row lies in a segment, so the outputs need no zero fill
     n_mlp = int(pg["qweight1"].size(2))
     mlp = torch.empty((R, n_mlp), dtype=torch.float16, device=dev)
-    if R <= FUSED_SWIGLU_MAX_ROWS:
+    if R <= FUSED_SWIGLU_MAX_ROWS and ns["gate"] is None and ns["up"] is None:
         # few rows: the gate/up GEMM with act_fn(g) * u in its epilogue (one launch)
         ext.compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded(
             hid_g, hid_u, eid, seg, prob, tile_bound, decoded["gate"], *[pg[k] for k in names], decoded["up"],
@@ -196,11 +216,19 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
         ext.compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
             hid_g, hid_u, eid, seg, prob, tile_bound, decoded["gate"], *[pg[k] for k in names], decoded["up"],
             *[pu[k] for k in names], True, out_a=g, out_b=u)
+        if ns["gate"] is not None or ns["up"] is not None:
+            # the compensation C1 . (C2 . x) joins each projection before act_fn (qlinear_cuda.py:2322-2334)
+            x_g = x16.index_select(0, route["grouped_token_indices"])
+            for out, key in ((g, "gate"), (u, "up")):
+                if ns[key] is not None:
+                    ext.ns_compensation_apply_(out, x_g, eid, seg, ns[key])
         ext.swiglu_mul(g, u, out=mlp)
     hid_d = shared_projection(mlp, backbones["down"])
     d_out = torch.empty((R, int(pd["qweight1"].size(2))), dtype=torch.float16, device=dev)
     ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
         hid_d, eid, seg, prob, tile_bound, decoded["down"], *[pd[k] for k in names], True, out=d_out)
+    if ns["down"] is not None:
+        ext.ns_compensation_apply_(d_out, mlp, eid, seg, ns["down"])
     return _combine(x16, d_out, route, w16, output_dtype, shared_expert)
 
 

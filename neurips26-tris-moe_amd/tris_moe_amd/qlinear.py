@@ -208,11 +208,134 @@ def _predecode(payload: dict, route: dict, rank: int, n: int) -> torch.Tensor:
         (rank + 31) // 32, n)
 
 
-def _check_ns_payload(ns_payload):
+def build_grouped_ns_payload(c2: list, c1: list, infeatures: int, outfeatures: int, group_size: int,
+                             c2_keys: list | None = None) -> dict:
+    """Host assembly of a null-space compensation payload (build_grouped_ns_compensation_payload,
+    qlinear_cuda.py:1734-1872) from per-expert 4-bit packed payloads (``packing.pack_4bit`` dicts or None for
+    an expert without compensation): c2[e] holds C2_e [rank_e, in], c1[e] C1_e [out, rank_e].  C2 blocks are
+    concatenated along their rows (qweight / scales columns), C1 blocks along their packed rank words;
+    experts with equal ``c2_keys[e]`` share one C2 block."""
+    E = len(c2)
+    ranks, c2_off, c2_woff, c1_woff, c1_goff = [], [], [], [], []
+    c2_qw, c2_qz, c2_sc, c1_qw, c1_qz, c1_sc = [], [], [], [], [], []
+    shared = {}
+    tot_rank = tot_words = tot_c1_words = tot_c1_groups = 0
+    in_groups = (infeatures + group_size - 1) // group_size if infeatures > 0 else 0
+    for e in range(E):
+        c1_woff.append(tot_c1_words)
+        c1_goff.append(tot_c1_groups)
+        if c2[e] is None or c1[e] is None:
+            ranks.append(0)
+            c2_off.append(tot_rank)
+            c2_woff.append(tot_words)
+            continue
+        rank = int(c2[e]["rows"])
+        if int(c1[e]["cols"]) != rank or int(c2[e]["cols"]) != infeatures or int(c1[e]["rows"]) != outfeatures:
+            raise ValueError(f"expert {e}: C2 [{c2[e]['rows']}, {c2[e]['cols']}] / C1 [{c1[e]['rows']}, "
+                             f"{c1[e]['cols']}] do not chain {infeatures} -> rank -> {outfeatures}")
+        key = c2_keys[e] if c2_keys is not None else ("local", e)
+        if key in shared:
+            off, woff, r0 = shared[key]
+            if r0 != rank:
+                raise ValueError(f"expert {e}: shared C2 of rank {r0}, expert rank {rank}")
+        else:
+            off, woff = tot_rank, tot_words
+            shared[key] = (off, woff, rank)
+            c2_qw.append(np.asarray(c2[e]["qweight"], np.int32))
+            c2_qz.append(np.asarray(c2[e]["qzeros"], np.int32))
+            c2_sc.append(np.asarray(c2[e]["scales"], np.float16))
+            tot_rank += rank
+            tot_words += int(c2_qz[-1].shape[1])
+        ranks.append(rank)
+        c2_off.append(off)
+        c2_woff.append(woff)
+        c1_qw.append(np.asarray(c1[e]["qweight"], np.int32))
+        c1_qz.append(np.asarray(c1[e]["qzeros"], np.int32))
+        c1_sc.append(np.asarray(c1[e]["scales"], np.float16))
+        tot_c1_words += int(c1_qw[-1].shape[0])
+        tot_c1_groups += int(c1_qz[-1].shape[0])
+    qzc = (outfeatures + 7) // 8
+    return {
+        "ns_rank_per_expert": np.asarray(ranks, np.int32),
+        "ns_c2_rank_offsets": np.asarray(c2_off, np.int32),
+        "ns_c2_rank_word_offsets": np.asarray(c2_woff, np.int32),
+        "ns_c1_rank_word_offsets": np.asarray(c1_woff, np.int32),
+        "ns_c1_group_offsets": np.asarray(c1_goff, np.int32),
+        "max_ns_rank": max(ranks) if ranks else 0,
+        "infeatures": int(infeatures),
+        "outfeatures": int(outfeatures),
+        "group_size": int(group_size),
+        "ns_c2_qweight": np.concatenate(c2_qw, axis=1) if c2_qw else np.zeros(((infeatures + 7) // 8, 0), np.int32),
+        "ns_c2_qzeros": np.concatenate(c2_qz, axis=1) if c2_qz else np.zeros((in_groups, 0), np.int32),
+        "ns_c2_scales": np.concatenate(c2_sc, axis=1) if c2_sc else np.zeros((in_groups, 0), np.float16),
+        "ns_c1_qweight": np.concatenate(c1_qw, axis=0) if c1_qw else np.zeros((0, outfeatures), np.int32),
+        "ns_c1_qzeros": np.concatenate(c1_qz, axis=0) if c1_qz else np.zeros((0, qzc), np.int32),
+        "ns_c1_scales": np.concatenate(c1_sc, axis=0) if c1_sc else np.zeros((0, outfeatures), np.float16),
+    }
+
+
+def validate_ns_payload(ns: dict) -> None:
+    """Host check that every expert's slices lie inside the concatenated blocks (the kernels index them
+    without bounds checks): raises ValueError naming the first expert that does not fit."""
+    def arr(k):
+        v = ns[k]
+        return v.detach().cpu().numpy() if isinstance(v, torch.Tensor) else np.asarray(v)
+    ranks = arr("ns_rank_per_expert").astype(np.int64)
+    infeatures, outfeatures = int(ns["infeatures"]), int(ns["outfeatures"])
+    gs, max_rank = int(ns["group_size"]), int(ns["max_ns_rank"])
+    if max_rank > 0 and gs <= 0:
+        raise ValueError("null-space payload: group_size must be positive")
+    c2w, c2z, c2s = arr("ns_c2_qweight").shape, arr("ns_c2_qzeros").shape, arr("ns_c2_scales").shape
+    c1w, c1z, c1s = arr("ns_c1_qweight").shape, arr("ns_c1_qzeros").shape, arr("ns_c1_scales").shape
+    in_groups = (infeatures + gs - 1) // gs if gs > 0 else 0
+    if max_rank > 0 and (c2w[0] != (infeatures + 7) // 8 or c2z[0] < in_groups or c2s[0] < in_groups
+                         or c1w[1] != outfeatures or c1s[1] != outfeatures or c1z[1] != (outfeatures + 7) // 8):
+        raise ValueError("null-space payload: block shapes do not match infeatures / outfeatures / group_size")
+    off, woff = arr("ns_c2_rank_offsets"), arr("ns_c2_rank_word_offsets")
+    c1wo, c1go = arr("ns_c1_rank_word_offsets"), arr("ns_c1_group_offsets")
+    for e, r in enumerate(ranks):
+        if r <= 0:
+            continue
+        egs = min(int(r), gs)
+        groups = (int(r) + egs - 1) // egs
+        if (r > max_rank or off[e] < 0 or off[e] + r > min(c2w[1], c2s[1]) or woff[e] < 0
+                or woff[e] + (r + 7) // 8 > c2z[1] or c1wo[e] < 0 or c1wo[e] + (r + 7) // 8 > c1w[0]
+                or c1go[e] < 0 or c1go[e] + groups > min(c1z[0], c1s[0])):
+            raise ValueError(f"null-space payload: expert {e} (rank {int(r)}) lies outside the concatenated blocks")
+
+
+def ns_payload_to_device(ns: dict, device, dtype=torch.float16) -> dict:
+    """Host null-space payload -> device tensors (int32, scales in ``dtype``), scalars as Python ints;
+    validated first (validate_ns_payload)."""
+    validate_ns_payload(ns)
+    out = {}
+    for k, v in ns.items():
+        if isinstance(v, (np.ndarray, torch.Tensor)):
+            t = torch.as_tensor(np.ascontiguousarray(v)) if isinstance(v, np.ndarray) else v
+            if t.is_floating_point():
+                out[k] = t.to(device=device, dtype=dtype).contiguous()
+            elif t.numel() == 1 and k in ("max_ns_rank", "infeatures", "outfeatures", "group_size"):
+                out[k] = int(t.reshape(-1)[0].item())
+            else:
+                out[k] = t.to(device=device, dtype=torch.int32).contiguous()
+        else:
+            out[k] = v
+    return out
+
+
+def _resolve_ns_payload(ns_payload):
+    """A device null-space payload with a compensation term, else None.  Module lists carry no matrix-mode
+    compensation in this build (its QuantLinear holds vector-mode scales only), so they give None."""
     if ns_payload is None or isinstance(ns_payload, (list, tuple)):
-        return
-    if isinstance(ns_payload, dict) and ns_payload.get("ns_mode", "none") in ("matrix", 2):
-        raise NotImplementedError("matrix-mode null-space compensation is not provided by the TriS-MoE HIP library")
+        return None
+    if not isinstance(ns_payload, dict) or "ns_rank_per_expert" not in ns_payload:
+        raise RuntimeError("null-space payload lacks ns_rank_per_expert (build_grouped_ns_payload format)")
+    return ns_payload if int(ns_payload["max_ns_rank"]) > 0 else None
+
+
+def _apply_ns(out, x_grouped, route, ns):
+    if ns is not None:
+        ext.ns_compensation_apply_(out, x_grouped.contiguous(), route["expert_ids"], route["segment_offsets"], ns)
 
 
 def run_grouped_structured_expert_forward(payload_or_modules, hidden_grouped: torch.Tensor, x_grouped: torch.Tensor,
@@ -233,7 +356,7 @@ def run_grouped_structured_expert_forward(payload_or_modules, hidden_grouped: to
     payload = resolve_grouped_precomputed_payload(payload_or_modules, hidden_grouped.device, hidden_grouped.dtype)
     if payload is None:
         return None
-    _check_ns_payload(ns_payload)
+    ns = _resolve_ns_payload(ns_payload)
     if expert_modules is None and not isinstance(payload_or_modules, dict):
         expert_modules = payload_or_modules
     defer_bias = bool(payload["has_bias"]) and (ns_payload is not None or expert_modules is not None)
@@ -259,6 +382,7 @@ def run_grouped_structured_expert_forward(payload_or_modules, hidden_grouped: to
             payload["q_gmap_gr_words"], payload["q_gmap_gr_offsets"], payload["q_gmap_gr_meta"], payload["c_map"],
             payload["g_idx"], payload["col_pack3"], payload["row_pack3"], payload["output_scale"], has_scale,
             bias_arg, has_bias_arg, uniform)
+    _apply_ns(out, x_grouped, route, ns)
     if defer_bias:
         out.add_(payload["bias"].index_select(0, route["grouped_expert_ids"].to(dtype=torch.long)))
     return out
@@ -280,8 +404,8 @@ def run_grouped_structured_expert_pair_forward(payload_or_modules_a, payload_or_
     pb = resolve_grouped_precomputed_payload(payload_or_modules_b, hidden_b_grouped.device, hidden_b_grouped.dtype)
     if pa is None or pb is None:
         return None, None
-    _check_ns_payload(ns_payload_a)
-    _check_ns_payload(ns_payload_b)
+    ns_a = _resolve_ns_payload(ns_payload_a)
+    ns_b = _resolve_ns_payload(ns_payload_b)
     if expert_modules_a is None and not isinstance(payload_or_modules_a, dict):
         expert_modules_a = payload_or_modules_a
     if expert_modules_b is None and not isinstance(payload_or_modules_b, dict):
@@ -317,6 +441,8 @@ def run_grouped_structured_expert_pair_forward(payload_or_modules_a, payload_or_
             pb["qweight1"], pb["qweight2_sparse"], pb["qweight2_sparse_prefix"], pb["q_gmap_gr_words"],
             pb["q_gmap_gr_offsets"], pb["q_gmap_gr_meta"], pb["c_map"], pb["g_idx"], pb["col_pack3"],
             pb["row_pack3"], pb["output_scale"], scale_b, bias_b, uniform)
+    _apply_ns(out_a, x_grouped, route, ns_a)
+    _apply_ns(out_b, x_grouped, route, ns_b)
     gexp = route["grouped_expert_ids"].to(dtype=torch.long)
     if defer_a:
         out_a.add_(pa["bias"].index_select(0, gexp))

@@ -222,3 +222,32 @@ def predecoded_nbytes(payload: dict, experts=None) -> int:
         total -= payload["q_gmap_gr_offsets"][e].nbytes + payload["q_gmap_gr_meta"][e].nbytes
         total += nblk * 128 * 4
     return int(total)
+
+
+def make_ns_payload(rng: np.random.Generator, num_experts: int, infeatures: int, outfeatures: int, ranks,
+                    group_size: int = 128, magnitude: float = 0.02, share_c2: bool = False) -> dict:
+    """A matrix-mode null-space compensation payload (host): per expert random C2 [rank, in] and C1
+    [out, rank] of the given magnitude, 4-bit packed (packing.pack_4bit) and concatenated
+    (qlinear.build_grouped_ns_payload); rank 0 gives no compensation; share_c2 makes experts of equal rank
+    share one C2 block."""
+    from .packing import pack_4bit
+    from .qlinear import build_grouped_ns_payload
+
+    c2, c1, keys = [], [], []
+    shared = {}
+    for e in range(num_experts):
+        r = int(ranks[e])
+        if r <= 0:
+            c2.append(None)
+            c1.append(None)
+            keys.append(("none", e))
+            continue
+        if share_c2 and r in shared:
+            c2.append(shared[r])
+        else:
+            blk = pack_4bit(rng.standard_normal((r, infeatures)).astype(np.float32) * magnitude, group_size)
+            shared[r] = blk
+            c2.append(blk)
+        keys.append(("shared", r) if share_c2 else ("local", e))
+        c1.append(pack_4bit(rng.standard_normal((outfeatures, r)).astype(np.float32) * magnitude, min(r, group_size)))
+    return build_grouped_ns_payload(c2, c1, infeatures, outfeatures, group_size, c2_keys=keys)

@@ -24,6 +24,9 @@ reference checkout):
   ``qlinear_cuda.py:1301-1378``.
 * MoE block (numpy): ``modeling_mixtral.py:406-608`` (grouped forward) and
   ``modeling_olmoe.py:1053-1058`` (optional top-k renormalisation).
+* Null-space compensation (numpy): payload slicing
+  ``qlinear_cuda.py:1734-1872`` / ``TriSMoE_cuda_kernel.cu:1208-1505``, the
+  fallback product ``qlinear_cuda.py:1943-1946``.
 * 4-bit packed backbone (numpy): producer ``utils/pack_utils.py:126-180``,
   consumer ``qlinear_cuda.py:2761-2786`` (exact fp16 dequant; the projection
   is then ``linear_f16`` of the dequantised matrix).
@@ -390,7 +393,7 @@ def route_topk(router_logits, top_k: int, renormalize: bool = True):
 
 
 def moe_layer(x_f16, routing_weights, selected_experts, payloads: dict, backbones: dict, num_experts: int,
-              shared_expert=None, weight_caches: dict | None = None) -> np.ndarray:
+              shared_expert=None, weight_caches: dict | None = None, ns_payloads: dict | None = None) -> np.ndarray:
     """Grouped MoE block (modeling_mixtral.py:406-537) with fp16 tensors between
     stages and fp32 accumulation inside every product; returns fp32 [T, H]
     (the caller rounds to the output dtype).
@@ -412,9 +415,17 @@ def moe_layer(x_f16, routing_weights, selected_experts, payloads: dict, backbone
     hid_u = linear_f16(x, backbones["up"])[gti]
     g_out = grouped_forward(payloads["gate"], hid_g, route["expert_ids"], route["segment_offsets"], weight_cache=caches["gate"])
     u_out = grouped_forward(payloads["up"], hid_u, route["expert_ids"], route["segment_offsets"], weight_cache=caches["up"])
+    ns_payloads = ns_payloads or {}
+    # matrix-mode null-space terms join each projection's output with an fp16 add (qlinear_cuda.py:2322-2334)
+    if ns_payloads.get("gate") is not None:
+        g_out = f16_add(g_out, ns_compensation(x_g, ns_payloads["gate"], route["expert_ids"], route["segment_offsets"]))
+    if ns_payloads.get("up") is not None:
+        u_out = f16_add(u_out, ns_compensation(x_g, ns_payloads["up"], route["expert_ids"], route["segment_offsets"]))
     mlp = (silu_f16(g_out).astype(np.float32) * u_out.astype(np.float32)).astype(np.float16)
     hid_d = linear_f16(mlp, backbones["down"])
     d_out = grouped_forward(payloads["down"], hid_d, route["expert_ids"], route["segment_offsets"], weight_cache=caches["down"])
+    if ns_payloads.get("down") is not None:
+        d_out = f16_add(d_out, ns_compensation(mlp, ns_payloads["down"], route["expert_ids"], route["segment_offsets"]))
     contrib = (d_out.astype(np.float32) * rw16[gti, gsl].astype(np.float32)[:, None]).astype(np.float16)
     out = np.zeros((t, x.shape[1]), dtype=np.float32)
     np.add.at(out, gti, contrib.astype(np.float32))
@@ -465,6 +476,43 @@ def packed4_dequant(qweight, qzeros, scales, g_idx, rows: int, cols: int) -> np.
     diff = (q - z[g]).astype(np.float16)          # small integers: exact in fp16
     w = f16_mul(diff, sc[g])                       # one rounding, as the fp16 multiply
     return np.ascontiguousarray(w.T)
+
+
+def ns_expert_matrices(ns: dict, e: int):
+    """Expert e's null-space matrices (C2 fp16 [rank, in], C1 fp16 [out, rank]) from a grouped payload
+    (build_grouped_ns_compensation_payload layout, qlinear_cuda.py:1734-1872), or None when its rank is 0:
+    C2 is a column slice of the concatenated C2 blocks, C1 a row slice of the C1 blocks, whose groups hold
+    min(rank, group_size) columns (TriSMoE_cuda_kernel.cu:1398-1505)."""
+    rank = int(ns["ns_rank_per_expert"][e])
+    if rank <= 0:
+        return None
+    infeatures, outfeatures, gs = int(ns["infeatures"]), int(ns["outfeatures"]), int(ns["group_size"])
+    off, woff = int(ns["ns_c2_rank_offsets"][e]), int(ns["ns_c2_rank_word_offsets"][e])
+    words = (rank + 7) // 8
+    c2 = packed4_dequant(ns["ns_c2_qweight"][:, off:off + rank], ns["ns_c2_qzeros"][:, woff:woff + words],
+                         ns["ns_c2_scales"][:, off:off + rank], np.arange(infeatures) // gs, rank, infeatures)
+    egs = min(rank, gs)
+    ng = (rank + egs - 1) // egs
+    wo, go = int(ns["ns_c1_rank_word_offsets"][e]), int(ns["ns_c1_group_offsets"][e])
+    c1 = packed4_dequant(ns["ns_c1_qweight"][wo:wo + words], ns["ns_c1_qzeros"][go:go + ng],
+                         ns["ns_c1_scales"][go:go + ng], np.arange(rank) // egs, outfeatures, rank)
+    return c2, c1
+
+
+def ns_compensation(x_grouped, ns: dict, expert_ids, segment_offsets) -> np.ndarray:
+    """fp16 [R, out] = F.linear(F.linear(x_seg, C2_e), C1_e) per segment: the reference's own fallback of the
+    grouped compensation (qlinear_cuda.py:1943-1946), fp32-accumulated, fp16 between the two products."""
+    x = np.asarray(x_grouped, dtype=np.float16)
+    out = np.zeros((x.shape[0], int(ns["outfeatures"])), dtype=np.float16)
+    seg = np.asarray(segment_offsets)
+    for s, e in enumerate(np.asarray(expert_ids)):
+        lo, hi = int(seg[s]), int(seg[s + 1])
+        if hi <= lo or e < 0 or e >= len(ns["ns_rank_per_expert"]):
+            continue
+        m = ns_expert_matrices(ns, int(e))
+        if m is not None:
+            out[lo:hi] = linear_f16(linear_f16(x[lo:hi], m[0]), m[1])
+    return out
 
 
 def bf16_round(x) -> np.ndarray:

@@ -133,6 +133,35 @@ def test_sparse_bitmap_payload_converts_to_block_gr(tris, tmp_path):
             np.testing.assert_array_equal(g["q_gmap_gr_words"][e, : words.size].numpy(), words)
 
 
+def test_null_space_payloads_round_trip(tris, tmp_path):
+    """gate_ns / up_ns / down_ns payloads are written under their cache keys, pass the compatibility check and
+    load back with the same tensors and Python scalars; an inconsistent one is refused."""
+    from safetensors.torch import load_file, save_file
+
+    syn = tris["synthetic"]
+    layer = syn.make_layer(TINY, 11, tris["ext"].gr_encode)
+    rng = np.random.default_rng(0)
+    pls = {p: layer[p] for p in ck.GROUPED_PRECOMPUTED_KEYS}
+    pls["gate_ns"] = syn.make_ns_payload(rng, 4, TINY.hidden, TINY.intermediate, [8, 0, 16, 8], 64)
+    pls["down_ns"] = syn.make_ns_payload(rng, 4, TINY.intermediate, TINY.hidden, [0, 0, 0, 0], 64)
+    path = str(tmp_path / "ns.safetensors")
+    ck.save_grouped_checkpoint(path, [pls])
+    c = ck.GroupedCheckpoint(path)
+    assert c.compatibility() == (True, None)
+    got = c.load_layer("model.layers.0.block_sparse_moe", "cpu")
+    assert "up_ns" not in got and got["gate_ns"]["max_ns_rank"] == 16 and got["down_ns"]["max_ns_rank"] == 0
+    for k in ("ns_c2_qweight", "ns_c1_scales", "ns_c1_group_offsets"):
+        np.testing.assert_array_equal(got["gate_ns"][k].numpy(), pls["gate_ns"][k])
+    tensors = load_file(path)
+    tensors["model.layers.0.block_sparse_moe.grouped_payload.gate_ns.ns_c1_qweight"] = torch.zeros((1, TINY.intermediate),
+                                                                                                 dtype=torch.int32)
+    save_file(tensors, path)
+    c = ck.GroupedCheckpoint(path)
+    assert c.compatibility()[0] is False
+    with pytest.raises(ValueError, match="gate_ns"):
+        c.load_layer("model.layers.0.block_sparse_moe", "cpu")
+
+
 def test_incomplete_checkpoint_is_reported(tris, tmp_path):
     from safetensors.torch import save_file
 

@@ -1,0 +1,151 @@
+"""Matrix-mode null-space compensation (grouped C1_e . (C2_e . x) per routed row, qlinear_cuda.py:1734-2336):
+the payload layout on the host against the oracle's slicing, and on the GPU the kernels and a Mixtral layer
+with gate/up/down compensation against the oracle."""
+import numpy as np
+import pytest
+import torch
+
+from tris_moe_amd import qlinear, synthetic
+from tris_moe_amd.packing import pack_4bit
+
+
+def _blocks(rng, ranks, infeatures, outfeatures, gs):
+    c2 = [None if r == 0 else pack_4bit(rng.standard_normal((r, infeatures)).astype(np.float32) * 0.05, gs)
+          for r in ranks]
+    c1 = [None if r == 0 else pack_4bit(rng.standard_normal((outfeatures, r)).astype(np.float32) * 0.05, min(r, gs))
+          for r in ranks]
+    return c2, c1
+
+
+@pytest.mark.parametrize("ranks,gs", [([8, 0, 24, 16], 64), ([40, 3, 0], 16), ([0, 0], 32)])
+def test_payload_layout_round_trip(oracle_mod, ranks, gs):
+    """build_grouped_ns_payload concatenates per-expert blocks so that the oracle's per-expert slices
+    (offsets, word offsets, C1 groups of min(rank, group_size)) dequantise to each expert's own matrices."""
+    rng = np.random.default_rng(len(ranks) + gs)
+    infeatures, outfeatures = 200, 72
+    c2, c1 = _blocks(rng, ranks, infeatures, outfeatures, gs)
+    ns = qlinear.build_grouped_ns_payload(c2, c1, infeatures, outfeatures, gs)
+    assert ns["max_ns_rank"] == max(ranks) and ns["ns_rank_per_expert"].tolist() == ranks
+    for e, r in enumerate(ranks):
+        m = oracle_mod.ns_expert_matrices(ns, e)
+        if r == 0:
+            assert m is None
+            continue
+        w2 = oracle_mod.packed4_dequant(c2[e]["qweight"], c2[e]["qzeros"], c2[e]["scales"], c2[e]["g_idx"], r,
+                                        infeatures)
+        w1 = oracle_mod.packed4_dequant(c1[e]["qweight"], c1[e]["qzeros"], c1[e]["scales"], c1[e]["g_idx"],
+                                        outfeatures, r)
+        np.testing.assert_array_equal(m[0], w2)
+        np.testing.assert_array_equal(m[1], w1)
+
+
+def test_shared_c2_blocks(oracle_mod):
+    """Experts with one C2 key share its block (one copy, equal offsets), each with its own C1."""
+    rng = np.random.default_rng(2)
+    ns = synthetic.make_ns_payload(rng, 4, 128, 64, [16, 16, 8, 16], group_size=32, share_c2=True)
+    off = ns["ns_c2_rank_offsets"].tolist()
+    assert off[0] == off[1] == off[3] != off[2]
+    assert ns["ns_c2_qweight"].shape[1] == 16 + 8
+    m0, m1 = oracle_mod.ns_expert_matrices(ns, 0), oracle_mod.ns_expert_matrices(ns, 1)
+    np.testing.assert_array_equal(m0[0], m1[0])
+    assert not np.array_equal(m0[1], m1[1])
+
+
+def test_out_of_range_slices_are_rejected():
+    rng = np.random.default_rng(4)
+    ns = synthetic.make_ns_payload(rng, 3, 64, 32, [8, 16, 8], group_size=32)
+    qlinear.validate_ns_payload(ns)
+    bad = dict(ns, ns_c2_rank_offsets=ns["ns_c2_rank_offsets"] + np.asarray([0, 0, 20], np.int32))
+    with pytest.raises(ValueError, match="expert 2"):
+        qlinear.validate_ns_payload(bad)
+    bad = dict(ns, ns_c1_group_offsets=ns["ns_c1_group_offsets"] + np.asarray([0, 9, 0], np.int32))
+    with pytest.raises(ValueError, match="expert 1"):
+        qlinear.validate_ns_payload(bad)
+
+
+def test_chain_mismatch_is_rejected():
+    rng = np.random.default_rng(3)
+    c2, c1 = _blocks(rng, [8], 64, 32, 32)
+    c1[0] = pack_4bit(np.zeros((32, 16), np.float32), 16)
+    with pytest.raises(ValueError, match="do not chain"):
+        qlinear.build_grouped_ns_payload(c2, c1, 64, 32, 32)
+
+
+# ------------------------------------------------------------------------------------------------ GPU
+def _dev_ns(ns, dev):
+    return qlinear.ns_payload_to_device(ns, dev)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_compensation_kernel_matches_oracle(tris, oracle_mod, cuda, accumulate):
+    """Ragged segments, an empty segment, a segment routed to no expert, a rank-0 expert and a rank above
+    one C2 workgroup (64): comp (or out + comp) within tolerance of the oracle, untouched rows exact."""
+    from test_gpu_parity import assert_close, note
+
+    note(f"ns compensation accumulate={accumulate}")
+    ext = tris["ext"]
+    rng = np.random.default_rng(7)
+    E, infeatures, outfeatures = 5, 512, 320
+    ns = synthetic.make_ns_payload(rng, E, infeatures, outfeatures, [16, 0, 72, 8, 24], group_size=128,
+                                   magnitude=0.05)
+    ids = np.asarray([2, 0, 1, -1, 4, 3], np.int32)
+    lens = [37, 5, 9, 4, 0, 17]
+    offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    R = int(offs[-1])
+    x = (rng.standard_normal((R, infeatures)) * 1.5).astype(np.float16)
+    base = (rng.standard_normal((R, outfeatures))).astype(np.float16)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    dns = _dev_ns(ns, cuda)
+    out = t(base).clone()
+    ext.ns_compensation_apply_(out, t(x), t(ids), t(offs), dns, accumulate=accumulate)
+    comp = oracle_mod.ns_compensation(x, ns, ids, offs)
+    want = oracle_mod.f16_add(base, comp) if accumulate else comp
+    got = out.cpu().numpy()
+    assert_close(got, want, "ns compensation")
+    untouched = np.r_[offs[3]:offs[4]]   # the segment with no expert: comp = 0
+    if accumulate:
+        np.testing.assert_array_equal(got[untouched], base[untouched])
+    else:
+        assert not got[untouched].any()
+    api = ext.grouped_ns_compensation_forward(
+        t(x), t(ids), t(offs), t(offs), 0, *[dns[k] for k in ext.NS_PAYLOAD_TENSORS], dns["max_ns_rank"],
+        dns["group_size"])
+    assert_close(api.cpu().numpy(), comp, "grouped_ns_compensation_forward")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tokens", [2, 16, 160])
+def test_layer_with_ns_compensation(tris, oracle_mod, cuda, tokens):
+    """A Mixtral-shaped layer (smaller intermediate) with gate/up/down null-space payloads: the fused-SwiGLU
+    size (2 tokens), the dual path (16) and multi-tile segments (160) against the oracle layer."""
+    from test_gpu_parity import assert_close, note
+    from tris_moe_amd.configs import MoELayerSpec
+
+    note(f"layer with ns T={tokens}")
+    spec = MoELayerSpec("ns", hidden=1024, num_experts=8, intermediate=1536, top_k=2, rank=256, tokens=(tokens,))
+    syn, ql = tris["synthetic"], tris["qlinear"]
+    layer = syn.make_layer(spec, 8100 + tokens, tris["ext"].gr_encode)
+    inp = syn.make_inputs(spec, tokens, 8101 + tokens, layer["outlier_idx"])
+    rng = np.random.default_rng(tokens)
+    ranks = rng.integers(0, 48, spec.num_experts)
+    ns_host = {"gate": syn.make_ns_payload(rng, 8, spec.hidden, spec.intermediate, ranks, 128, magnitude=0.03),
+               "up": syn.make_ns_payload(rng, 8, spec.hidden, spec.intermediate, ranks, 128, magnitude=0.03),
+               "down": syn.make_ns_payload(rng, 8, spec.intermediate, spec.hidden, ranks, 128, magnitude=0.03)}
+    payloads = {p: ql.payload_to_device(layer[p], cuda) for p in ("gate", "up", "down")}
+    for p in ("gate", "up", "down"):
+        payloads[f"{p}_ns"] = ql.ns_payload_to_device(ns_host[p], cuda)
+    backbones = {p: torch.from_numpy(layer["backbones"][p]).to(cuda) for p in ("gate", "up", "down")}
+    block = tris["moe"].TrisSparseMoeBlock(spec.hidden, spec.num_experts, spec.top_k, payloads, backbones,
+                                           renormalize=spec.renormalize)
+    x = torch.from_numpy(inp["x"]).to(cuda).to(torch.bfloat16)
+    out = block.forward_routed(x, torch.from_numpy(inp["router_logits"]).to(cuda)).float().cpu().numpy()
+    w, sel = oracle_mod.route_topk(inp["router_logits"], spec.top_k, spec.renormalize)
+    want = oracle_mod.moe_layer(inp["x"].astype(np.float16), w, sel, {p: layer[p] for p in ("gate", "up", "down")},
+                                layer["backbones"], spec.num_experts, ns_payloads=ns_host)
+    without = oracle_mod.moe_layer(inp["x"].astype(np.float16), w, sel, {p: layer[p] for p in ("gate", "up", "down")},
+                                   layer["backbones"], spec.num_experts)
+    # the compensation moves the output beyond the tolerance, so leaving it out could not pass (larger
+    # magnitudes make C1 . C2 dominate the layer and its bf16 rounding)
+    assert np.abs(want - without).max() > 0.02
+    assert_close(out, oracle_mod.bf16_round(want), f"layer with ns T={tokens}")
