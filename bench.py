@@ -61,6 +61,8 @@ def parse_args():
                     help="C2 prefill tokens measured into 'prefill' (0 for none)")
     ap.add_argument("--packed4", type=int, default=1,
                     help="also time the decode step with 4-bit packed backbones into 'packed4_backbones'")
+    ap.add_argument("--ns", type=int, default=1,
+                    help="also time the decode step with null-space compensation into 'ns_compensation'")
     ap.add_argument("--prefill-only", action="store_true",
                     help="measure only the C2 prefill step and print its JSON object")
     return ap.parse_args()
@@ -191,6 +193,25 @@ def main():
             log(f"packed4 backbones T={tok}: {r['ms_per_step'] * 1e3:.1f} us/step, {r['tokens_per_s']:.0f} tok/s")
         del pcopies
 
+    # ---- the same step with matrix-mode null-space compensation on every projection (rank 32 per expert)
+    ns_line = None
+    if args.ns:
+        from tris_moe_amd import qlinear as ql
+
+        rng = np.random.default_rng(args.seed)
+        ranks = [32] * SPEC.num_experts
+        ns_host = {"gate": synthetic.make_ns_payload(rng, SPEC.num_experts, SPEC.hidden, SPEC.intermediate, ranks),
+                   "up": synthetic.make_ns_payload(rng, SPEC.num_experts, SPEC.hidden, SPEC.intermediate, ranks),
+                   "down": synthetic.make_ns_payload(rng, SPEC.num_experts, SPEC.intermediate, SPEC.hidden, ranks)}
+        ns_dev = {f"{p}_ns": ql.ns_payload_to_device(ns_host[p], dev) for p in projs}
+        ncopies = [(dict(pl, **ns_dev), bb) for pl, bb in copies]
+        ns_line = {"rank_per_expert": 32}
+        for tok in sorted({args.tokens, 1}):
+            r = measure(tok, max(args.steps // 2, 10), args.warmup, ncopies)
+            ns_line[f"T{tok}"] = {k: round(r[k], 3) for k in ("ms_per_step", "tokens_per_s")}
+            log(f"ns compensation T={tok}: {r['ms_per_step'] * 1e3:.1f} us/step, {r['tokens_per_s']:.0f} tok/s")
+        del ncopies
+
     # ---- dominant kernel: the MFMA gate/up grouped GEMM over predecoded split bitmaps that the step runs,
     # one launch per layer copy, replayed from a graph on its own stream and timed there with HIP events
     x16, logits = main_res["x16"], main_res["logits"]
@@ -276,6 +297,7 @@ def main():
         "sweep": sweep,
         "prefill": prefill,
         "packed4_backbones": packed4,
+        "ns_compensation": ns_line,
     }
     print(json.dumps(line), flush=True)
 

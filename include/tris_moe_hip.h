@@ -352,13 +352,42 @@ typedef struct tris_ns_payload {
  * comp[r] = fp16(C1_e . fp16(C2_e . x_grouped[r])) for the rows r of every segment (e = its expert):
  * replaces grouped_ns_compensation_forward (TriSMoE_cuda_kernel.cu:1208-2145) and, with accumulate != 0,
  * the caller's out.add_(compensation) (qlinear_cuda.py:2322-2334): out[r] = fp16(out[r] + comp[r]);
- * with accumulate == 0, out = comp.  x_grouped fp16 [batch, in]; hidden: fp16 workspace
- * [batch, max_ns_rank] (no initial contents); out fp16 [batch, out].  Exact fp16 weights, fp32 sums.
+ * with accumulate == 0, out = comp.  x_grouped fp16 [batch, in] (16-byte aligned, in % 8 == 0); out fp16
+ * [batch, out].  The scale and zero point of element c come from group c / group_size (C2) and
+ * j / min(rank_e, group_size) (C1).  workspace: device scratch of
+ * tris_grouped_ns_workspace_bytes(batch, num_segments, in, max_ns_rank) bytes (fp32 split-K partial sums
+ * of C2 . x, added in a fixed order; no initial contents).  Exact fp16 weights, fp32 sums, fp16 between
+ * the two products.  Calls sharing a workspace on different streams must not overlap.
  */
 int tris_grouped_ns_compensation_forward(const uint16_t* x_grouped, int32_t batch, const int32_t* expert_ids,
                                          const int32_t* segment_offsets, int32_t num_segments,
-                                         const tris_ns_payload* ns, uint16_t* hidden, uint16_t* out,
-                                         int32_t accumulate, void* stream);
+                                         const tris_ns_payload* ns, void* workspace, int64_t workspace_bytes,
+                                         uint16_t* out, int32_t accumulate, void* stream);
+
+/* Workspace size for tris_grouped_ns_compensation_forward (no reference counterpart). */
+int64_t tris_grouped_ns_workspace_bytes(int32_t batch, int32_t num_segments, int32_t infeatures,
+                                        int32_t max_ns_rank);
+
+/*
+ * Two payloads over the same input rows and routing in one pair of launches: the gate and up
+ * projections' compensation terms, which the reference computes with two
+ * grouped_ns_compensation_forward calls on the same x_grouped (qlinear_cuda.py:2322-2334, once per
+ * projection).  ns_a and ns_b share infeatures; out_a / out_b [batch, out] as out above.  Input rows:
+ * with row_index NULL, x is x_grouped [batch, in]; else grouped row r is x[row_index[r]] of x fp16
+ * [x_rows, in], row_index int64 [batch] (the route's grouped_token_indices: the gather
+ * x.index_select(0, grouped_token_indices) done inside; an index outside [0, x_rows) reads row 0).
+ * workspace: tris_grouped_ns_pair_workspace_bytes(...) bytes.
+ */
+int tris_grouped_ns_compensation_pair_forward(const uint16_t* x, int32_t x_rows, const int64_t* row_index,
+                                              int32_t batch, const int32_t* expert_ids,
+                                              const int32_t* segment_offsets, int32_t num_segments,
+                                              const tris_ns_payload* ns_a, const tris_ns_payload* ns_b,
+                                              void* workspace, int64_t workspace_bytes, uint16_t* out_a,
+                                              uint16_t* out_b, int32_t accumulate, void* stream);
+
+/* Workspace size for tris_grouped_ns_compensation_pair_forward (no reference counterpart). */
+int64_t tris_grouped_ns_pair_workspace_bytes(int32_t batch, int32_t num_segments, int32_t infeatures,
+                                             int32_t max_ns_rank_a, int32_t max_ns_rank_b);
 
 /*
  * Routing-weighted combine: replaces final.index_add_(0, grouped_token_indices,
@@ -381,6 +410,26 @@ int tris_moe_combine(const uint16_t* expert_out, const int32_t* inverse_perm, co
  * tris_grouped_swiglu_forward_block_gr_predecoded.
  */
 int tris_swiglu_mul(const uint16_t* gate, const uint16_t* up, int64_t count, uint16_t* out, void* stream);
+
+/*
+ * tris_swiglu_mul after the null-space compensation of each projection: out = act_fn(fp16(gate + comp_gate))
+ * * fp16(up + comp_up), the reference's out.add_(compensation) on each GEMM output (qlinear_cuda.py:2322-2334)
+ * followed by act_fn(w1(x)) * w3(x) (modeling_mixtral.py:496), in one pass.  comp_gate / comp_up: fp16
+ * like gate, or NULL for no term.  Lets the compensation be computed beside the GEMMs (no reference
+ * counterpart as one call).
+ */
+int tris_swiglu_mul_compensated(const uint16_t* gate, const uint16_t* up, const uint16_t* comp_gate,
+                                const uint16_t* comp_up, int64_t count, uint16_t* out, void* stream);
+
+/*
+ * tris_moe_combine with expert_out[r] replaced by fp16(expert_out[r] + expert_comp[r]): the down
+ * projection's out.add_(compensation) (qlinear_cuda.py:2322-2334) folded into the combine.  expert_comp:
+ * fp16 [R, hidden] like expert_out (16-byte aligned when hidden % 8 == 0), or NULL (no reference
+ * counterpart as one call).
+ */
+int tris_moe_combine_compensated(const uint16_t* expert_out, const uint16_t* expert_comp, const int32_t* inverse_perm,
+                                 const uint16_t* weights, const uint16_t* shared, int32_t tokens, int32_t top_k,
+                                 int32_t hidden, uint16_t* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -7,7 +7,10 @@
 // reference) are gathered through the inverse route permutation, summed in
 // fp32 together with an optional unrouted shared-expert output, and rounded
 // once to bf16.  One thread produces 8 consecutive features; reads are
-// 16-byte vector loads.
+// 16-byte vector loads.  The compensated variants first add a null-space
+// compensation term to each expert output row (fp16(out + comp), the
+// reference's out.add_(compensation), qlinear_cuda.py:2322-2334), so that the
+// term computed beside the grouped GEMM joins it without a launch of its own.
 #include "tris_common.h"
 
 namespace tris {
@@ -19,7 +22,11 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+// fp16(a + b) for fp16 bit patterns: the exact sum rounded once, as torch's fp16 add_.
+__device__ __forceinline__ uint16_t f16_add_bits(uint16_t a, uint16_t b) { return f2h_bits(h2f(a) + h2f(b)); }
+
 __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __restrict__ expert_out,
+                                                          const uint16_t* __restrict__ expert_comp,
                                                           const int32_t* __restrict__ inverse_perm,
                                                           const uint16_t* __restrict__ weights,
                                                           const uint16_t* __restrict__ shared, int tokens, int top_k,
@@ -42,6 +49,18 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
 #pragma unroll
       for (int u = 0; u < 8; ++u) v[u] = (h0 + u < hidden) ? src[u] : 0;
     }
+    if (expert_comp != nullptr) {
+      const uint16_t* csrc = expert_comp + static_cast<int64_t>(row) * hidden + h0;
+      uint16_t c[8];
+      if (vec) {
+        *reinterpret_cast<uint4*>(c) = *reinterpret_cast<const uint4*>(csrc);
+      } else {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) c[u] = (h0 + u < hidden) ? csrc[u] : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = f16_add_bits(v[u], c[u]);
+    }
 #pragma unroll
     for (int u = 0; u < 8; ++u) acc[u] += __half2float(__hmul(__ushort_as_half(v[u]), w));
   }
@@ -59,62 +78,121 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
   }
 }
 
-// out = act_fn(gate) * up, 8 consecutive elements per thread (16-byte loads when aligned).
+// One element of act_fn(gate') * up' with gate' = fp16(gate + comp_gate), up' = fp16(up + comp_up) where a
+// compensation is given.
+__device__ __forceinline__ uint16_t swiglu_comp_bits(uint16_t g, uint16_t u, const uint16_t* cg, const uint16_t* cu,
+                                                     int64_t i) {
+  if (cg != nullptr) g = f16_add_bits(g, cg[i]);
+  if (cu != nullptr) u = f16_add_bits(u, cu[i]);
+  return swiglu_bits(g, u);
+}
+
+// 8 fp16 values of a 16-byte-aligned tensor, or zeros for a missing one.
+__device__ __forceinline__ void load8(const uint16_t* p, int64_t i0, uint32_t w[4]) {
+  if (p == nullptr) {
+    w[0] = w[1] = w[2] = w[3] = 0u;
+    return;
+  }
+  const uint4 v = *reinterpret_cast<const uint4*>(p + i0);
+  w[0] = v.x;
+  w[1] = v.y;
+  w[2] = v.z;
+  w[3] = v.w;
+}
+
+// out = act_fn(gate) * up, 8 consecutive elements per thread (16-byte loads when aligned); with comp_gate /
+// comp_up, the compensation is added to each operand first.
 __global__ __launch_bounds__(256) void swiglu_mul_kernel(const uint16_t* __restrict__ gate,
-                                                         const uint16_t* __restrict__ up, int64_t count,
+                                                         const uint16_t* __restrict__ up,
+                                                         const uint16_t* __restrict__ comp_gate,
+                                                         const uint16_t* __restrict__ comp_up, int64_t count,
                                                          uint16_t* __restrict__ out) {
   const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
   if (i0 >= count) return;
   if (i0 + 8 <= count) {
-    const uint4 gv = *reinterpret_cast<const uint4*>(gate + i0);
-    const uint4 uv = *reinterpret_cast<const uint4*>(up + i0);
-    const uint32_t g[4] = {gv.x, gv.y, gv.z, gv.w};
-    const uint32_t u[4] = {uv.x, uv.y, uv.z, uv.w};
+    uint32_t g[4], u[4], cg[4], cu[4];
+    load8(gate, i0, g);
+    load8(up, i0, u);
+    load8(comp_gate, i0, cg);
+    load8(comp_up, i0, cu);
     uint32_t o[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const uint32_t lo = swiglu_bits(static_cast<uint16_t>(g[k]), static_cast<uint16_t>(u[k]));
-      const uint32_t hi = swiglu_bits(static_cast<uint16_t>(g[k] >> 16), static_cast<uint16_t>(u[k] >> 16));
-      o[k] = lo | (hi << 16);
+      uint16_t gl = static_cast<uint16_t>(g[k]), gh = static_cast<uint16_t>(g[k] >> 16);
+      uint16_t ul = static_cast<uint16_t>(u[k]), uh = static_cast<uint16_t>(u[k] >> 16);
+      if (comp_gate != nullptr) {
+        gl = f16_add_bits(gl, static_cast<uint16_t>(cg[k]));
+        gh = f16_add_bits(gh, static_cast<uint16_t>(cg[k] >> 16));
+      }
+      if (comp_up != nullptr) {
+        ul = f16_add_bits(ul, static_cast<uint16_t>(cu[k]));
+        uh = f16_add_bits(uh, static_cast<uint16_t>(cu[k] >> 16));
+      }
+      o[k] = static_cast<uint32_t>(swiglu_bits(gl, ul)) | (static_cast<uint32_t>(swiglu_bits(gh, uh)) << 16);
     }
     *reinterpret_cast<uint4*>(out + i0) = make_uint4(o[0], o[1], o[2], o[3]);
     return;
   }
-  for (int64_t i = i0; i < count; ++i) out[i] = swiglu_bits(gate[i], up[i]);
+  for (int64_t i = i0; i < count; ++i) out[i] = swiglu_comp_bits(gate[i], up[i], comp_gate, comp_up, i);
 }
 
 }  // namespace tris
 
 using namespace tris;
 
-extern "C" int tris_swiglu_mul(const uint16_t* gate, const uint16_t* up, int64_t count, uint16_t* out, void* stream) {
-  TRIS_REQUIRE(count >= 0, "tris_swiglu_mul: negative count");
+static int swiglu_launch(const char* who, const uint16_t* gate, const uint16_t* up, const uint16_t* comp_gate,
+                         const uint16_t* comp_up, int64_t count, uint16_t* out, void* stream) {
+  TRIS_REQUIRE(count >= 0, "%s: negative count", who);
   if (count == 0) return TRIS_OK;
-  TRIS_REQUIRE(gate && up && out, "tris_swiglu_mul: null pointer");
-  TRIS_REQUIRE(reinterpret_cast<uintptr_t>(gate) % 16 == 0 && reinterpret_cast<uintptr_t>(up) % 16 == 0 &&
-                   reinterpret_cast<uintptr_t>(out) % 16 == 0,
-               "tris_swiglu_mul: tensors must be 16-byte aligned");
+  TRIS_REQUIRE(gate && up && out, "%s: null pointer", who);
+  const auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  TRIS_REQUIRE(a16(gate) && a16(up) && a16(out) && a16(comp_gate) && a16(comp_up), "%s: tensors must be 16-byte aligned",
+               who);
   const int64_t threads = 256;
   const int64_t blocks = (count + 8 * threads - 1) / (8 * threads);
-  TRIS_REQUIRE(blocks <= 2147483647LL, "tris_swiglu_mul: too many elements");
+  TRIS_REQUIRE(blocks <= 2147483647LL, "%s: too many elements", who);
   hipLaunchKernelGGL(swiglu_mul_kernel, dim3(static_cast<unsigned>(blocks)), dim3(threads), 0,
-                     static_cast<hipStream_t>(stream), gate, up, count, out);
-  return check_launch("swiglu_mul_kernel");
+                     static_cast<hipStream_t>(stream), gate, up, comp_gate, comp_up, count, out);
+  return check_launch(who);
+}
+
+extern "C" int tris_swiglu_mul(const uint16_t* gate, const uint16_t* up, int64_t count, uint16_t* out, void* stream) {
+  return swiglu_launch("tris_swiglu_mul", gate, up, nullptr, nullptr, count, out, stream);
+}
+
+extern "C" int tris_swiglu_mul_compensated(const uint16_t* gate, const uint16_t* up, const uint16_t* comp_gate,
+                                           const uint16_t* comp_up, int64_t count, uint16_t* out, void* stream) {
+  return swiglu_launch("tris_swiglu_mul_compensated", gate, up, comp_gate, comp_up, count, out, stream);
+}
+
+static int combine_launch(const char* who, const uint16_t* expert_out, const uint16_t* expert_comp,
+                          const int32_t* inverse_perm, const uint16_t* weights, const uint16_t* shared, int32_t tokens,
+                          int32_t top_k, int32_t hidden, uint16_t* out, void* stream) {
+  TRIS_REQUIRE(tokens >= 0 && top_k >= 0 && hidden >= 0, "%s: negative shape", who);
+  if (tokens == 0 || hidden == 0) return TRIS_OK;
+  TRIS_REQUIRE(out != nullptr && (top_k == 0 || (expert_out && inverse_perm && weights)), "%s: null pointer", who);
+  TRIS_REQUIRE(tokens <= 65535, "%s: too many tokens per launch (%d)", who, tokens);
+  TRIS_REQUIRE(hidden % 8 != 0 || (reinterpret_cast<uintptr_t>(expert_out) % 16 == 0 &&
+                                   reinterpret_cast<uintptr_t>(expert_comp) % 16 == 0),
+               "%s: expert_out and expert_comp must be 16-byte aligned", who);
+  const int threads = 256;
+  dim3 grid(ceil_div(ceil_div(hidden, 8), threads), tokens);
+  hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(threads), 0, static_cast<hipStream_t>(stream), expert_out,
+                     expert_comp, inverse_perm, weights, shared, tokens, top_k, hidden, out);
+  return check_launch(who);
 }
 
 extern "C" int tris_moe_combine(const uint16_t* expert_out, const int32_t* inverse_perm, const uint16_t* weights,
                                 const uint16_t* shared, int32_t tokens, int32_t top_k, int32_t hidden,
                                 uint16_t* out, void* stream) {
-  TRIS_REQUIRE(tokens >= 0 && top_k >= 0 && hidden >= 0, "tris_moe_combine: negative shape");
-  if (tokens == 0 || hidden == 0) return TRIS_OK;
-  TRIS_REQUIRE(out != nullptr && (top_k == 0 || (expert_out && inverse_perm && weights)),
-               "tris_moe_combine: null pointer");
-  TRIS_REQUIRE(tokens <= 65535, "tris_moe_combine: too many tokens per launch (%d)", tokens);
-  TRIS_REQUIRE(hidden % 8 != 0 || reinterpret_cast<uintptr_t>(expert_out) % 16 == 0,
-               "tris_moe_combine: expert_out must be 16-byte aligned");
-  const int threads = 256;
-  dim3 grid(ceil_div(ceil_div(hidden, 8), threads), tokens);
-  hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(threads), 0, static_cast<hipStream_t>(stream), expert_out,
-                     inverse_perm, weights, shared, tokens, top_k, hidden, out);
-  return check_launch("moe_combine_kernel");
+  return combine_launch("tris_moe_combine", expert_out, nullptr, inverse_perm, weights, shared, tokens, top_k, hidden,
+                        out, stream);
+}
+
+extern "C" int tris_moe_combine_compensated(const uint16_t* expert_out, const uint16_t* expert_comp,
+                                            const int32_t* inverse_perm, const uint16_t* weights,
+                                            const uint16_t* shared, int32_t tokens, int32_t top_k, int32_t hidden,
+                                            uint16_t* out, void* stream) {
+  return combine_launch("tris_moe_combine_compensated", expert_out, expert_comp, inverse_perm, weights, shared, tokens,
+                        top_k, hidden, out, stream);
 }

@@ -784,11 +784,78 @@ def ns_compensation_apply_(out: torch.Tensor, x_grouped: torch.Tensor, expert_id
     batch = int(x_grouped.size(0))
     if out.size(0) != batch or out.size(1) != st.outfeatures:
         raise RuntimeError("null-space compensation: out must be [batch, outfeatures]")
-    hidden = torch.empty((batch, max(st.max_ns_rank, 1)), dtype=torch.float16, device=dev)
-    _lib.check(_lib.load().tris_grouped_ns_compensation_forward(
-        _ptr(x_grouped), batch, _ptr(expert_ids), _ptr(segment_offsets), int(expert_ids.numel()), ctypes.byref(st),
-        _ptr(hidden), _ptr(out), int(bool(accumulate)), _stream(x_grouped)), "tris_grouped_ns_compensation_forward")
+    x_grouped = _aligned16(x_grouped)
+    lib = _lib.load()
+    nseg = int(expert_ids.numel())
+    ws = ns_workspace(dev, int(lib.tris_grouped_ns_workspace_bytes(batch, nseg, st.infeatures, st.max_ns_rank)))
+    _lib.check(lib.tris_grouped_ns_compensation_forward(
+        _ptr(x_grouped), batch, _ptr(expert_ids), _ptr(segment_offsets), nseg, ctypes.byref(st), _ptr(ws),
+        int(ws.numel()), _ptr(out), int(bool(accumulate)), _stream(x_grouped)), "tris_grouped_ns_compensation_forward")
     return out
+
+
+_NS_WORKSPACES: dict = {}
+
+
+def ns_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-device scratch for the null-space compensation's split-K partial sums, apart from the backbone's
+    (the layer runs the down projection's compensation on a second stream beside the backbone).  Calls on
+    one device share it, so they must not overlap on different streams."""
+    key = (device.type, device.index)
+    ws = _NS_WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _NS_WORKSPACES[key] = ws
+    return ws
+
+
+def _aligned16(x: torch.Tensor) -> torch.Tensor:
+    """x itself when its data starts on a 16-byte boundary (the kernels' vector loads), else a copy."""
+    return x if x.data_ptr() % 16 == 0 else x.clone()
+
+
+def ns_compensation_pair_apply_(out_a, out_b, x: torch.Tensor, expert_ids: torch.Tensor,
+                                segment_offsets: torch.Tensor, ns_a, ns_b, accumulate: bool = True,
+                                row_index: torch.Tensor | None = None) -> tuple:
+    """ns_compensation_apply_ for two payloads over the same rows (the gate and up projections) in one pair
+    of launches; the same values as two single calls.  A payload given as None (and its out) is skipped.
+    With row_index (int64 [batch], the route's grouped_token_indices), x is the ungrouped input [T, in] and
+    grouped row r reads x[row_index[r]]: the gather x.index_select(0, grouped_token_indices) of
+    qlinear_cuda.py:2322-2334 done inside the kernel."""
+    if ns_a is None or ns_b is None:
+        x_g = x if row_index is None else x.index_select(0, row_index)
+        for o, ns in ((out_a, ns_a), (out_b, ns_b)):
+            if ns is not None:
+                ns_compensation_apply_(o, x_g, expert_ids, segment_offsets, ns, accumulate)
+        return out_a, out_b
+    _check_cuda("x", x, torch.float16, 2)
+    dev = x.device
+    _check_cuda("out_a", out_a, torch.float16, 2, dev)
+    _check_cuda("out_b", out_b, torch.float16, 2, dev)
+    _check_cuda("expert_ids", expert_ids, torch.int32, 1, dev)
+    _check_cuda("segment_offsets", segment_offsets, torch.int32, 1, dev)
+    batch = int(out_a.size(0))
+    if row_index is not None:
+        _check_cuda("row_index", row_index, torch.int64, 1, dev)
+        if int(row_index.numel()) != batch:
+            raise RuntimeError("row_index must hold one input row per grouped row")
+    elif int(x.size(0)) != batch:
+        raise RuntimeError("null-space compensation: x_grouped must have one row per output row")
+    in_f = int(x.size(1))
+    sa, sb = _ns_struct(ns_a, in_f, dev), _ns_struct(ns_b, in_f, dev)
+    for o, st in ((out_a, sa), (out_b, sb)):
+        if o.size(0) != batch or o.size(1) != st.outfeatures:
+            raise RuntimeError("null-space compensation: out must be [batch, outfeatures]")
+    x = _aligned16(x)
+    lib = _lib.load()
+    nseg = int(expert_ids.numel())
+    ws = ns_workspace(dev, int(lib.tris_grouped_ns_pair_workspace_bytes(batch, nseg, in_f, sa.max_ns_rank,
+                                                                        sb.max_ns_rank)))
+    _lib.check(lib.tris_grouped_ns_compensation_pair_forward(
+        _ptr(x), int(x.size(0)), _ptr(row_index), batch, _ptr(expert_ids), _ptr(segment_offsets), nseg,
+        ctypes.byref(sa), ctypes.byref(sb), _ptr(ws), int(ws.numel()), _ptr(out_a), _ptr(out_b),
+        int(bool(accumulate)), _stream(x)), "tris_grouped_ns_compensation_pair_forward")
+    return out_a, out_b
 
 
 def grouped_ns_compensation_forward(x_grouped, expert_ids, segment_offsets, problem_offsets, total_problem_tiles,
@@ -809,10 +876,16 @@ def grouped_ns_compensation_forward(x_grouped, expert_ids, segment_offsets, prob
 
 
 def moe_combine(expert_out: torch.Tensor, inverse_perm: torch.Tensor, weights: torch.Tensor,
-                shared: torch.Tensor | None = None) -> torch.Tensor:
-    """bf16 [T, H] = sum_s fp16(expert_out[inverse_perm[t, s]] * weights[t, s]) (+ shared), fp32-accumulated."""
+                shared: torch.Tensor | None = None, expert_comp: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16 [T, H] = sum_s fp16(expert_out[inverse_perm[t, s]] * weights[t, s]) (+ shared), fp32-accumulated.
+    With expert_comp (fp16, the shape of expert_out), each expert row is fp16(expert_out + expert_comp) first:
+    the down projection's null-space compensation (qlinear_cuda.py:2322-2334) folded into the combine."""
     _check_cuda("expert_out", expert_out, torch.float16, 2)
     dev = expert_out.device
+    if expert_comp is not None:
+        _check_cuda("expert_comp", expert_comp, torch.float16, 2, dev)
+        if expert_comp.shape != expert_out.shape:
+            raise RuntimeError("expert_comp must have the shape of expert_out")
     _check_cuda("weights", weights, torch.float16, 2, dev)
     _check_cuda("inverse_perm", inverse_perm, torch.int32, 1, dev)
     tokens, top_k = int(weights.size(0)), int(weights.size(1))
@@ -824,24 +897,43 @@ def moe_combine(expert_out: torch.Tensor, inverse_perm: torch.Tensor, weights: t
         if tuple(shared.shape) != (tokens, hidden):
             raise RuntimeError("shared must be [tokens, hidden]")
     out = torch.empty((tokens, hidden), dtype=torch.bfloat16, device=dev)
-    _lib.check(_lib.load().tris_moe_combine(_ptr(expert_out), _ptr(inverse_perm), _ptr(weights), _ptr(shared), tokens,
-                                            top_k, hidden, _ptr(out), _stream(expert_out)), "tris_moe_combine")
+    if expert_comp is None:
+        _lib.check(_lib.load().tris_moe_combine(_ptr(expert_out), _ptr(inverse_perm), _ptr(weights), _ptr(shared),
+                                                tokens, top_k, hidden, _ptr(out), _stream(expert_out)),
+                   "tris_moe_combine")
+    else:
+        _lib.check(_lib.load().tris_moe_combine_compensated(
+            _ptr(expert_out), _ptr(expert_comp), _ptr(inverse_perm), _ptr(weights), _ptr(shared), tokens, top_k,
+            hidden, _ptr(out), _stream(expert_out)), "tris_moe_combine_compensated")
     return out
 
 
-def swiglu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """fp16 act_fn(gate) * up (modeling_mixtral.py:496): SiLU in fp32 rounded to fp16, then the fp16 product."""
+def swiglu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None,
+               comp_gate: torch.Tensor | None = None, comp_up: torch.Tensor | None = None) -> torch.Tensor:
+    """fp16 act_fn(gate) * up (modeling_mixtral.py:496): SiLU in fp32 rounded to fp16, then the fp16 product.
+    With comp_gate / comp_up, each operand first takes its null-space compensation, fp16(gate + comp_gate)
+    (out.add_(compensation), qlinear_cuda.py:2322-2334)."""
     _check_cuda("gate", gate, torch.float16, None)
     _check_cuda("up", up, torch.float16, None, gate.device)
     if gate.shape != up.shape:
         raise RuntimeError("gate and up must have the same shape")
+    for name, c in (("comp_gate", comp_gate), ("comp_up", comp_up)):
+        if c is not None:
+            _check_cuda(name, c, torch.float16, None, gate.device)
+            if c.shape != gate.shape:
+                raise RuntimeError(f"{name} must have the shape of gate")
     if out is None:
         out = torch.empty_like(gate)
     _check_cuda("out", out, torch.float16, None, gate.device)
     if out.shape != gate.shape:
         raise RuntimeError("out must have the shape of gate")
-    _lib.check(_lib.load().tris_swiglu_mul(_ptr(gate), _ptr(up), gate.numel(), _ptr(out), _stream(gate)),
-               "tris_swiglu_mul")
+    if comp_gate is None and comp_up is None:
+        _lib.check(_lib.load().tris_swiglu_mul(_ptr(gate), _ptr(up), gate.numel(), _ptr(out), _stream(gate)),
+                   "tris_swiglu_mul")
+    else:
+        _lib.check(_lib.load().tris_swiglu_mul_compensated(_ptr(gate), _ptr(up), _ptr(comp_gate), _ptr(comp_up),
+                                                           gate.numel(), _ptr(out), _stream(gate)),
+                   "tris_swiglu_mul_compensated")
     return out
 
 

@@ -109,10 +109,7 @@ def _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, ou
         pu["q_gmap_gr_offsets"], pu["q_gmap_gr_meta"], pu["c_map"], pu["g_idx"], pu["col_pack3"], pu["row_pack3"],
         pu["output_scale"], bool(pu["has_output_scale"]), pu["bias"] if pu["has_bias"] else empty, uniform)
     if ns["gate"] is not None or ns["up"] is not None:
-        x_g = x16.index_select(0, gti)
-        for out, key in ((g_out, "gate"), (u_out, "up")):
-            if ns[key] is not None:
-                ext.ns_compensation_apply_(out, x_g, expert_ids, seg, ns[key])
+        ext.ns_compensation_pair_apply_(g_out, u_out, x16, expert_ids, seg, ns["gate"], ns["up"], row_index=gti)
     mlp = F.silu(g_out) * u_out
     hid_d = shared_projection(mlp, backbones["down"])
     d_out = ext.compact3_tris_precomputed_grouped_forward_block_gr(
@@ -136,12 +133,12 @@ def _ns_payloads(payloads: dict) -> dict:
     return out
 
 
-def _combine(x16, d_out, route, w16, output_dtype, shared_expert):
+def _combine(x16, d_out, route, w16, output_dtype, shared_expert, d_comp=None):
     shared = None
     if shared_expert is not None:
         wg, wu, wd = shared_expert
         shared = F.linear(F.silu(F.linear(x16, wg)) * F.linear(x16, wu), wd).contiguous()
-    out = ext.moe_combine(d_out, route["inverse_perm"], w16, shared)
+    out = ext.moe_combine(d_out, route["inverse_perm"], w16, shared, expert_comp=d_comp)
     return out if output_dtype == torch.bfloat16 else out.to(output_dtype)
 
 
@@ -154,9 +151,10 @@ def _predecode_buffer(p, slots, device):
 _SIDE_STREAMS: dict = {}
 
 
-def _side_stream(device: torch.device) -> torch.cuda.Stream:
-    """A second stream per device (default priority) for work that overlaps the main chain."""
-    key = device.index if device.index is not None else torch.cuda.current_device()
+def _side_stream(device: torch.device, which: int = 0) -> torch.cuda.Stream:
+    """Extra streams per device (default priority) for work that overlaps the main chain: 0 for the
+    bitmap decodes and the down compensation, 1 for the gate/up compensation."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(), which)
     if key not in _SIDE_STREAMS:
         _SIDE_STREAMS[key] = torch.cuda.Stream(device=device)
     return _SIDE_STREAMS[key]
@@ -167,6 +165,10 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
 # decode shape: 17.6 vs 18.9 us at 2 rows, 49.7 vs 42.3 us at 32 rows).
 FUSED_SWIGLU_MAX_ROWS = 4
 
+# The down projection's null-space compensation runs on the side stream beside the down backbone and GEMM
+# (True) or on the caller's stream after the GEMM (False).
+NS_DOWN_BESIDE_GEMM = True
+
 
 def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype, shared_expert):
     """Uniform-group payloads without output scale or bias: GR-decode every routed expert's split
@@ -174,7 +176,13 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     (TriSMoE_cuda.cpp:855-889, 922-974).  Active experts come first in the padded route, so
     min(num_experts, R) segments cover every routed row and the later segments are empty.  The
     decodes depend only on the route, so they run on a side stream while the gate/up backbones
-    run on the caller's stream."""
+    run on the caller's stream.
+
+    Null-space compensation terms (qlinear_cuda.py:2322-2334) are computed apart from the GEMM outputs and
+    joined later, with the same fp16 adds: gate/up's on a stream of their own from the routed inputs
+    (read through the route's token indices), beside the decodes and the backbones, and added inside
+    act_fn(g) * u; the down projection's on the side stream beside the down backbone and GEMM, and added
+    inside the combine."""
     slots = min(num_experts, R)
     eid = route["expert_ids"][:slots]
     seg = route["segment_offsets"][: slots + 1]
@@ -187,6 +195,19 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     main = torch.cuda.current_stream(dev)
     side = _side_stream(dev)
     side.wait_stream(main)
+    n_mlp = int(pg["qweight1"].size(2))
+    comp_g = comp_u = None
+    ns_side = None
+    if ns["gate"] is not None or ns["up"] is not None:
+        # the gate/up compensation terms from the routed inputs, beside the decodes and the backbones; the
+        # buffers belong to the caller's stream, which waits for this one before reading or freeing them
+        comp_g = torch.empty((R, n_mlp), dtype=torch.float16, device=dev) if ns["gate"] is not None else None
+        comp_u = torch.empty((R, n_mlp), dtype=torch.float16, device=dev) if ns["up"] is not None else None
+        ns_side = _side_stream(dev, 1)
+        ns_side.wait_stream(main)
+        with torch.cuda.stream(ns_side):
+            ext.ns_compensation_pair_apply_(comp_g, comp_u, x16, eid, seg, ns["gate"], ns["up"], accumulate=False,
+                                            row_index=route["grouped_token_indices"])
 
     # one launch for the three projections (the persistent GEMMs assume the whole GPU, so nothing runs
     # beside them)
@@ -199,11 +220,12 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     hid_g, hid_u = shared_projection_pair(x16, backbones["gate"], backbones["up"],
                                             row_index=route["grouped_token_indices"])
     main.wait_stream(side)
+    if ns_side is not None:
+        main.wait_stream(ns_side)
     names = ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx", "col_pack3", "row_pack3")
     # every routed row lies in a segment, so the outputs need no zero fill
-    n_mlp = int(pg["qweight1"].size(2))
     mlp = torch.empty((R, n_mlp), dtype=torch.float16, device=dev)
-    if R <= FUSED_SWIGLU_MAX_ROWS and ns["gate"] is None and ns["up"] is None:
+    if R <= FUSED_SWIGLU_MAX_ROWS and comp_g is None and comp_u is None:
         # few rows: the gate/up GEMM with act_fn(g) * u in its epilogue (one launch)
         ext.compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded(
             hid_g, hid_u, eid, seg, prob, tile_bound, decoded["gate"], *[pg[k] for k in names], decoded["up"],
@@ -216,20 +238,26 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
         ext.compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
             hid_g, hid_u, eid, seg, prob, tile_bound, decoded["gate"], *[pg[k] for k in names], decoded["up"],
             *[pu[k] for k in names], True, out_a=g, out_b=u)
-        if ns["gate"] is not None or ns["up"] is not None:
-            # the compensation C1 . (C2 . x) joins each projection before act_fn (qlinear_cuda.py:2322-2334)
-            x_g = x16.index_select(0, route["grouped_token_indices"])
-            for out, key in ((g, "gate"), (u, "up")):
-                if ns[key] is not None:
-                    ext.ns_compensation_apply_(out, x_g, eid, seg, ns[key])
-        ext.swiglu_mul(g, u, out=mlp)
+        # g + comp_g and u + comp_u (fp16 adds) inside act_fn(g) * u
+        ext.swiglu_mul(g, u, out=mlp, comp_gate=comp_g, comp_up=comp_u)
+    n_out = int(pd["qweight1"].size(2))
+    comp_d = None
+    if ns["down"] is not None and NS_DOWN_BESIDE_GEMM:
+        # the down compensation beside the down backbone and GEMM; its buffer belongs to the caller's stream,
+        # which waits for the side stream before reading or freeing it
+        comp_d = torch.empty((R, n_out), dtype=torch.float16, device=dev)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            ext.ns_compensation_apply_(comp_d, mlp, eid, seg, ns["down"], accumulate=False)
     hid_d = shared_projection(mlp, backbones["down"])
-    d_out = torch.empty((R, int(pd["qweight1"].size(2))), dtype=torch.float16, device=dev)
+    d_out = torch.empty((R, n_out), dtype=torch.float16, device=dev)
     ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
         hid_d, eid, seg, prob, tile_bound, decoded["down"], *[pd[k] for k in names], True, out=d_out)
-    if ns["down"] is not None:
+    if comp_d is not None:
+        main.wait_stream(side)
+    elif ns["down"] is not None:
         ext.ns_compensation_apply_(d_out, mlp, eid, seg, ns["down"])
-    return _combine(x16, d_out, route, w16, output_dtype, shared_expert)
+    return _combine(x16, d_out, route, w16, output_dtype, shared_expert, d_comp=comp_d)
 
 
 class TrisSparseMoeBlock(nn.Module):

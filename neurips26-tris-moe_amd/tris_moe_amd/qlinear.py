@@ -441,8 +441,9 @@ def run_grouped_structured_expert_pair_forward(payload_or_modules_a, payload_or_
             pb["qweight1"], pb["qweight2_sparse"], pb["qweight2_sparse_prefix"], pb["q_gmap_gr_words"],
             pb["q_gmap_gr_offsets"], pb["q_gmap_gr_meta"], pb["c_map"], pb["g_idx"], pb["col_pack3"],
             pb["row_pack3"], pb["output_scale"], scale_b, bias_b, uniform)
-    _apply_ns(out_a, x_grouped, route, ns_a)
-    _apply_ns(out_b, x_grouped, route, ns_b)
+    if ns_a is not None or ns_b is not None:
+        ext.ns_compensation_pair_apply_(out_a, out_b, x_grouped.contiguous(), route["expert_ids"],
+                                        route["segment_offsets"], ns_a, ns_b)
     gexp = route["grouped_expert_ids"].to(dtype=torch.long)
     if defer_a:
         out_a.add_(pa["bias"].index_select(0, gexp))

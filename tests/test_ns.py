@@ -77,17 +77,22 @@ def _dev_ns(ns, dev):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("accumulate", [False, True])
-def test_compensation_kernel_matches_oracle(tris, oracle_mod, cuda, accumulate):
+@pytest.mark.parametrize("accumulate,infeatures,outfeatures,group_size", [
+    (False, 512, 320, 128), (True, 512, 320, 128), (True, 1000, 200, 128), (False, 14336, 264, 128),
+    (True, 512, 320, 20)])
+def test_compensation_kernel_matches_oracle(tris, oracle_mod, cuda, accumulate, infeatures, outfeatures, group_size):
     """Ragged segments, an empty segment, a segment routed to no expert, a rank-0 expert and a rank above
-    one C2 workgroup (64): comp (or out + comp) within tolerance of the oracle, untouched rows exact."""
+    one C2 workgroup (64): comp (or out + comp) within tolerance of the oracle, untouched rows exact.  The
+    input widths split C2 into 2 slices of 256 columns, 4 slices (the last 232 columns: a partial chunk) and 19
+    slices of 768 columns (the last 512).  Group size 20 puts group boundaries inside packed words of C2 and
+    (ranks 24 and 72) of C1: the scale and zero point are taken per element there."""
     from test_gpu_parity import assert_close, note
 
-    note(f"ns compensation accumulate={accumulate}")
+    note(f"ns compensation accumulate={accumulate} in={infeatures} out={outfeatures} gs={group_size}")
     ext = tris["ext"]
     rng = np.random.default_rng(7)
-    E, infeatures, outfeatures = 5, 512, 320
-    ns = synthetic.make_ns_payload(rng, E, infeatures, outfeatures, [16, 0, 72, 8, 24], group_size=128,
+    E = 5
+    ns = synthetic.make_ns_payload(rng, E, infeatures, outfeatures, [16, 0, 72, 8, 24], group_size=group_size,
                                    magnitude=0.05)
     ids = np.asarray([2, 0, 1, -1, 4, 3], np.int32)
     lens = [37, 5, 9, 4, 0, 17]
@@ -112,6 +117,49 @@ def test_compensation_kernel_matches_oracle(tris, oracle_mod, cuda, accumulate):
         t(x), t(ids), t(offs), t(offs), 0, *[dns[k] for k in ext.NS_PAYLOAD_TENSORS], dns["max_ns_rank"],
         dns["group_size"])
     assert_close(api.cpu().numpy(), comp, "grouped_ns_compensation_forward")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_compensation_pair_matches_single_calls(tris, oracle_mod, cuda, accumulate):
+    """The gate/up pair launch: payloads of different ranks and output widths (one of them with a rank-0
+    expert routed) give the bits of two single calls, within tolerance of the oracle; reading the rows
+    through a token index gives the bits of reading a gathered copy."""
+    from test_gpu_parity import assert_close, note
+
+    note(f"ns compensation pair accumulate={accumulate}")
+    ext = tris["ext"]
+    rng = np.random.default_rng(11)
+    E, infeatures = 4, 768
+    ns_a = synthetic.make_ns_payload(rng, E, infeatures, 384, [8, 40, 0, 16], group_size=128, magnitude=0.05)
+    ns_b = synthetic.make_ns_payload(rng, E, infeatures, 640, [96, 8, 24, 0], group_size=128, magnitude=0.05)
+    ids = np.asarray([1, 3, 0, 2], np.int32)
+    offs = np.concatenate([[0], np.cumsum([3, 21, 1, 6])]).astype(np.int32)
+    R = int(offs[-1])
+    x = (rng.standard_normal((R, infeatures)) * 1.5).astype(np.float16)
+    base_a = rng.standard_normal((R, 384)).astype(np.float16)
+    base_b = rng.standard_normal((R, 640)).astype(np.float16)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    da, db = _dev_ns(ns_a, cuda), _dev_ns(ns_b, cuda)
+    pa, pb = t(base_a).clone(), t(base_b).clone()
+    ext.ns_compensation_pair_apply_(pa, pb, t(x), t(ids), t(offs), da, db, accumulate=accumulate)
+    sa, sb = t(base_a).clone(), t(base_b).clone()
+    ext.ns_compensation_apply_(sa, t(x), t(ids), t(offs), da, accumulate=accumulate)
+    ext.ns_compensation_apply_(sb, t(x), t(ids), t(offs), db, accumulate=accumulate)
+    np.testing.assert_array_equal(pa.cpu().numpy(), sa.cpu().numpy())
+    np.testing.assert_array_equal(pb.cpu().numpy(), sb.cpu().numpy())
+    # the rows read through a token index (the route's grouped_token_indices) instead of a gathered copy
+    tok = rng.permutation(np.arange(R) % 11).astype(np.int64)
+    xt = (rng.standard_normal((11, infeatures)) * 1.5).astype(np.float16)
+    ia, ib = t(base_a).clone(), t(base_b).clone()
+    ext.ns_compensation_pair_apply_(ia, ib, t(xt), t(ids), t(offs), da, db, accumulate=accumulate, row_index=t(tok))
+    ga, gb = t(base_a).clone(), t(base_b).clone()
+    ext.ns_compensation_pair_apply_(ga, gb, t(xt[tok]), t(ids), t(offs), da, db, accumulate=accumulate)
+    np.testing.assert_array_equal(ia.cpu().numpy(), ga.cpu().numpy())
+    np.testing.assert_array_equal(ib.cpu().numpy(), gb.cpu().numpy())
+    for got, ns, base in ((pa, ns_a, base_a), (pb, ns_b, base_b)):
+        comp = oracle_mod.ns_compensation(x, ns, ids, offs)
+        assert_close(got.cpu().numpy(), oracle_mod.f16_add(base, comp) if accumulate else comp, "ns pair")
 
 
 @pytest.mark.gpu
@@ -149,3 +197,36 @@ def test_layer_with_ns_compensation(tris, oracle_mod, cuda, tokens):
     # magnitudes make C1 . C2 dominate the layer and its bf16 rounding)
     assert np.abs(want - without).max() > 0.02
     assert_close(out, oracle_mod.bf16_round(want), f"layer with ns T={tokens}")
+    # the exact (in-kernel decode) expert path applies the terms in place instead: same result
+    logits = torch.from_numpy(inp["router_logits"]).to(cuda)
+    fused = tris["moe"].grouped_moe_forward_from_logits(
+        x.to(torch.float16), logits, spec.top_k, spec.renormalize, payloads, backbones, spec.num_experts,
+        torch.bfloat16, expert_path="fused").float().cpu().numpy()
+    assert_close(fused, oracle_mod.bf16_round(want), f"layer with ns T={tokens} (fused path)")
+
+
+@pytest.mark.gpu
+def test_swiglu_and_combine_take_the_compensation(tris, cuda):
+    """The compensated act_fn(g) * u and combine give the bits of the plain kernels on fp16(out + comp),
+    the reference's out.add_(compensation) (qlinear_cuda.py:2322-2334) done first; ragged element counts
+    and a missing term too."""
+    from test_gpu_parity import note
+
+    note("compensated swiglu / combine")
+    ext = tris["ext"]
+    gen = torch.Generator(device="cpu").manual_seed(5)
+    rnd = lambda *s: (torch.randn(*s, generator=gen) * 3).half().to(cuda)
+    add = lambda a, b: (a.float() + b.float()).half()
+    for shape in ((37, 1536), (5, 1003)):
+        g, u, cg, cu = rnd(*shape), rnd(*shape), rnd(*shape), rnd(*shape)
+        got = ext.swiglu_mul(g, u, comp_gate=cg, comp_up=cu)
+        assert torch.equal(got, ext.swiglu_mul(add(g, cg), add(u, cu)))
+        got = ext.swiglu_mul(g, u, comp_gate=None, comp_up=cu)
+        assert torch.equal(got, ext.swiglu_mul(g, add(u, cu)))
+    tokens, k = 9, 2
+    for hidden in (1024, 1001):
+        d, c = rnd(tokens * k, hidden), rnd(tokens * k, hidden)
+        perm = torch.randperm(tokens * k, generator=gen).to(torch.int32).to(cuda)
+        w = torch.rand(tokens, k, generator=gen).half().to(cuda)
+        got = ext.moe_combine(d, perm, w, expert_comp=c)
+        assert torch.equal(got, ext.moe_combine(add(d, c), perm, w))
