@@ -40,8 +40,9 @@ constexpr int kNsC1Batch = 4;                            // C1 rank words loaded
 constexpr int kNsC1Slices = 16;                          // C2 partial sums per hidden element loaded together
 constexpr int kNsMaxRank = 512;                          // hidden columns staged for C1 (fp32 in LDS)
 constexpr int kNsTargetWgs = 512;                        // C2 workgroups aimed for
-constexpr int kNsMaxSlices = 64;
+constexpr int kNsMaxSlices = 16;                         // = kNsC1Slices: C1 loads every partial sum at once
 static_assert(kNsC2Units * kNsC2Threads * 8 == kNsRows * kNsC2Chunk, "x staging covers the tile");
+static_assert(kNsMaxSlices <= kNsC1Slices, "C1 loads every slice's partial sum in one batch");
 
 struct NsArgs {
   const uint16_t* x;          // [batch, in] (or [*, in] rows picked by row_index), rows 16-byte aligned
@@ -161,6 +162,37 @@ __device__ __forceinline__ void ns_weights8(uint32_t word, int z, float s, float
   for (int m = 0; m < 8; ++m) w[m] = ns_weight(static_cast<int>((word >> (4 * m)) & 0xFu), z, s);
 }
 
+// One C2 pass's operands in registers: this thread's packed words with their zero words and scale bits,
+// and its 16-byte units of the x tile.
+struct NsC2Pass {
+  uint32_t wd[kNsC2Words], zw[kNsC2Words];
+  uint16_t sb[kNsC2Words];
+  uint4 xv[kNsC2Units];
+};
+
+// Loads the pass at input column c0 (cc columns): every address valid (clamped), all in flight together.
+__device__ __forceinline__ void ns_c2_load(NsC2Pass& p, const int32_t* __restrict__ qw, const int32_t* __restrict__ qz,
+                                           const uint16_t* __restrict__ qs, int total_rank, int total_rank_words,
+                                           int gs, int groups, int kp, int c0, int cc,
+                                           const uint16_t* __restrict__ x, const int64_t* xrow, int in_f) {
+#pragma unroll
+  for (int i = 0; i < kNsC2Words; ++i) {
+    const int w = kp + i * kNsC2Parts;  // word of the chunk
+    const int c = c0 + (w * 8 < cc ? w * 8 : 0);
+    int g = c / gs;
+    g = g < groups ? g : groups - 1;
+    p.wd[i] = static_cast<uint32_t>(qw[static_cast<int64_t>(c >> 3) * total_rank]);
+    p.zw[i] = static_cast<uint32_t>(qz[static_cast<int64_t>(g) * total_rank_words]);
+    p.sb[i] = qs[static_cast<int64_t>(g) * total_rank];
+  }
+#pragma unroll
+  for (int i = 0; i < kNsC2Units; ++i) {
+    const int cu = (static_cast<int>(threadIdx.x) + i * kNsC2Threads) % (kNsC2Chunk / 8);
+    const int cl = cu * 8 < cc ? cu * 8 : 0;
+    p.xv[i] = *reinterpret_cast<const uint4*>(x + xrow[i] * in_f + c0 + cl);
+  }
+}
+
 __global__ __launch_bounds__(kNsC2Threads) void ns_c2_kernel(NsArgs a) {
   __shared__ float xs[kNsRows][kNsC2Chunk];
   __shared__ float part[kNsC2Parts - 1][kNsRows][kNsC2Ranks];
@@ -203,40 +235,36 @@ __global__ __launch_bounds__(kNsC2Threads) void ns_c2_kernel(NsArgs a) {
   for (int r = 0; r < kNsRows; ++r) acc[r] = 0.0f;
   const int cbeg = slice * a.slice_cols;
   const int cend = (cbeg + a.slice_cols) < in_f ? (cbeg + a.slice_cols) : in_f;
+  // the operands of the first pass; each pass then loads the next one's before computing its own
+  NsC2Pass cur;
+  if (cbeg < cend)
+    ns_c2_load(cur, qw, qz, qs, ns.total_rank, ns.total_rank_words, gs, groups, kp, cbeg,
+               (cend - cbeg) < kNsC2Chunk ? (cend - cbeg) : kNsC2Chunk, a.x, xrow, in_f);
   for (int c0 = cbeg; c0 < cend; c0 += kNsC2Chunk) {
     const int cc = (cend - c0) < kNsC2Chunk ? (cend - c0) : kNsC2Chunk;  // a multiple of 8
-    // the weights of this pass and the x tile: every load at a valid (clamped) address, all in flight together
-    uint32_t wd[kNsC2Words], zw[kNsC2Words];
-    uint16_t sb[kNsC2Words];
-#pragma unroll
-    for (int i = 0; i < kNsC2Words; ++i) {
-      const int p = kp + i * kNsC2Parts;  // word of the chunk
-      const int c = c0 + (p * 8 < cc ? p * 8 : 0);
-      int g = c / gs;
-      g = g < groups ? g : groups - 1;
-      wd[i] = static_cast<uint32_t>(qw[static_cast<int64_t>(c >> 3) * ns.total_rank]);
-      zw[i] = static_cast<uint32_t>(qz[static_cast<int64_t>(g) * ns.total_rank_words]);
-      sb[i] = qs[static_cast<int64_t>(g) * ns.total_rank];
-    }
-    uint4 xv[kNsC2Units];
-#pragma unroll
-    for (int i = 0; i < kNsC2Units; ++i) {
-      const int cu = (static_cast<int>(threadIdx.x) + i * kNsC2Threads) % (kNsC2Chunk / 8);
-      const int cl = cu * 8 < cc ? cu * 8 : 0;
-      xv[i] = *reinterpret_cast<const uint4*>(a.x + xrow[i] * in_f + c0 + cl);
-    }
 #pragma unroll
     for (int i = 0; i < kNsC2Units; ++i) {
       const int u = threadIdx.x + i * kNsC2Threads;
       const int r = u / (kNsC2Chunk / 8), cu = u % (kNsC2Chunk / 8);
       if (r < rc) {
         const bool v = cu * 8 < cc;
-        const uint32_t h[4] = {v ? xv[i].x : 0u, v ? xv[i].y : 0u, v ? xv[i].z : 0u, v ? xv[i].w : 0u};
+        const uint4 xv = cur.xv[i];
+        const uint32_t h[4] = {v ? xv.x : 0u, v ? xv.y : 0u, v ? xv.z : 0u, v ? xv.w : 0u};
         float4* d = reinterpret_cast<float4*>(&xs[r][cu * 8]);
         d[0] = make_float4(h2f(h[0] & 0xFFFFu), h2f(h[0] >> 16), h2f(h[1] & 0xFFFFu), h2f(h[1] >> 16));
         d[1] = make_float4(h2f(h[2] & 0xFFFFu), h2f(h[2] >> 16), h2f(h[3] & 0xFFFFu), h2f(h[3] >> 16));
       }
     }
+    const bool more = c0 + kNsC2Chunk < cend;  // uniform
+    NsC2Pass nxt;
+    if (more) {
+      const int c1 = c0 + kNsC2Chunk;
+      ns_c2_load(nxt, qw, qz, qs, ns.total_rank, ns.total_rank_words, gs, groups, kp, c1,
+                 (cend - c1) < kNsC2Chunk ? (cend - c1) : kNsC2Chunk, a.x, xrow, in_f);
+    }
+    const uint32_t* wd = cur.wd;
+    const uint32_t* zw = cur.zw;
+    const uint16_t* sb = cur.sb;
     __syncthreads();
     if (jv) {
 #pragma unroll
@@ -283,6 +311,7 @@ __global__ __launch_bounds__(kNsC2Threads) void ns_c2_kernel(NsArgs a) {
       }
     }
     __syncthreads();
+    if (more) cur = nxt;
   }
   if (kp > 0) {
 #pragma unroll
@@ -372,20 +401,25 @@ __global__ __launch_bounds__(kNsC1Cols) void ns_c1_kernel(NsArgs a) {
 #pragma unroll
     for (int r = 0; r < kNsRows; ++r) prev[r] = out[static_cast<int64_t>(row0 + (r < rc ? r : 0)) * out_f + nc];
   }
-  if (has0) {
+  if (has0) {  // a.slices <= kNsC1Slices: every partial sum is in t0
     float v = 0.0f;
 #pragma unroll
     for (int k = 0; k < kNsC1Slices; ++k) {
       if (k < a.slices) v += t0[k];
     }
-    for (int sl = kNsC1Slices; sl < a.slices; ++sl) v += src0[sl * sstride];
     hs[hr0][hj0] = h2f(f2h_bits(v));  // the hidden tensor's fp16 value (F.linear(x, c2))
   }
   for (int idx = threadIdx.x + kNsC1Cols; idx < nst; idx += kNsC1Cols) {  // tiles of more rows or ranks
     const int r = idx / rank, j = idx % rank;
     const float* src = part + static_cast<int64_t>(row0 + r) * ns.max_ns_rank + j;
+    float t[kNsC1Slices];
+#pragma unroll
+    for (int k = 0; k < kNsC1Slices; ++k) t[k] = src[(k < a.slices ? k : a.slices - 1) * sstride];
     float v = 0.0f;
-    for (int sl = 0; sl < a.slices; ++sl) v += src[sl * sstride];
+#pragma unroll
+    for (int k = 0; k < kNsC1Slices; ++k) {
+      if (k < a.slices) v += t[k];
+    }
     hs[r][j] = h2f(f2h_bits(v));
   }
   if (static_cast<int>(threadIdx.x) < rc * 8) {  // the last word's padding columns: zero, not stale LDS

@@ -51,6 +51,34 @@ def test_shared_c2_blocks(oracle_mod):
     assert not np.array_equal(m0[1], m1[1])
 
 
+def test_oracle_is_the_reference_fallback(oracle_mod):
+    """oracle.ns_compensation against the reference's own fallback, F.linear(F.linear(x_seg, c2), c1) on fp16
+    tensors (qlinear_cuda.py:1943-1946), run by torch on the CPU per segment: bit-identical, including
+    a segment with no expert and a rank-0 expert.  The same data without the fp16 rounding of the hidden
+    row (a plausible slip) does not match, so the check sees that rounding."""
+    import torch.nn.functional as F
+
+    rng = np.random.default_rng(3)
+    ns = synthetic.make_ns_payload(rng, 4, 96, 40, [8, 0, 24, 5], group_size=32, magnitude=0.05)
+    ids = np.asarray([2, 0, 3, -1, 1], np.int32)
+    offs = np.concatenate([[0], np.cumsum([6, 3, 4, 2, 3])]).astype(np.int32)
+    x = (rng.standard_normal((18, 96)) * 1.5).astype(np.float16)
+    got = oracle_mod.ns_compensation(x, ns, ids, offs)
+    want = np.zeros_like(got)
+    unrounded = np.zeros_like(got)
+    for s, e in enumerate(ids):
+        lo, hi = int(offs[s]), int(offs[s + 1])
+        m = oracle_mod.ns_expert_matrices(ns, int(e)) if 0 <= e < 4 else None
+        if m is None:
+            continue
+        c2, c1 = (torch.from_numpy(a) for a in m)
+        want[lo:hi] = F.linear(F.linear(torch.from_numpy(x[lo:hi]), c2), c1).numpy()
+        h32 = F.linear(torch.from_numpy(x[lo:hi]).float(), c2.float())
+        unrounded[lo:hi] = F.linear(h32, c1.float()).half().numpy()
+    np.testing.assert_array_equal(got, want)
+    assert not np.array_equal(unrounded, want)
+
+
 def test_out_of_range_slices_are_rejected():
     rng = np.random.default_rng(4)
     ns = synthetic.make_ns_payload(rng, 3, 64, 32, [8, 16, 8], group_size=32)
@@ -83,8 +111,9 @@ def _dev_ns(ns, dev):
 def test_compensation_kernel_matches_oracle(tris, oracle_mod, cuda, accumulate, infeatures, outfeatures, group_size):
     """Ragged segments, an empty segment, a segment routed to no expert, a rank-0 expert and a rank above
     one C2 workgroup (64): comp (or out + comp) within tolerance of the oracle, untouched rows exact.  The
-    input widths split C2 into 2 slices of 256 columns, 4 slices (the last 232 columns: a partial chunk) and 19
-    slices of 768 columns (the last 512).  Group size 20 puts group boundaries inside packed words of C2 and
+    input widths split C2 into 2 slices of 256 columns, 4 slices (the last 232 columns: a partial chunk) and 14
+    slices of 1024 columns (4 passes each, the next one's loads issued before the current one's
+    products).  Group size 20 puts group boundaries inside packed words of C2 and
     (ranks 24 and 72) of C1: the scale and zero point are taken per element there."""
     from test_gpu_parity import assert_close, note
 
