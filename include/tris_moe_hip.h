@@ -385,6 +385,17 @@ int tris_grouped_ns_compensation_pair_forward(const uint16_t* x, int32_t x_rows,
                                               void* workspace, int64_t workspace_bytes, uint16_t* out_a,
                                               uint16_t* out_b, int32_t accumulate, void* stream);
 
+/*
+ * The C1 half alone, on a given hidden: replaces grouped_ns_c1_forward (TriSMoE_cuda.cpp:423-455,
+ * kernel.cu:8526-8674; called by run_grouped_ns_c1_forward, qlinear_cuda.py:1964-2025, when every expert
+ * shares one cached C2 projection).  comp[r] = fp16(C1_e . hidden[r][0:rank_e]) for the rows of each
+ * segment, with accumulate as in tris_grouped_ns_compensation_forward.  hidden fp16 [batch, max_ns_rank];
+ * only the C1 fields of ns are read (the C2 pointers may be NULL).
+ */
+int tris_grouped_ns_c1_forward(const uint16_t* hidden, int32_t batch, const int32_t* expert_ids,
+                               const int32_t* segment_offsets, int32_t num_segments, const tris_ns_payload* ns,
+                               uint16_t* out, int32_t accumulate, void* stream);
+
 /* Workspace size for tris_grouped_ns_compensation_pair_forward (no reference counterpart). */
 int64_t tris_grouped_ns_pair_workspace_bytes(int32_t batch, int32_t num_segments, int32_t infeatures,
                                              int32_t max_ns_rank_a, int32_t max_ns_rank_b);

@@ -58,6 +58,7 @@ struct NsArgs {
   int accumulate;
   tris_ns_payload ns[2];
   float* part[2];  // [slices][batch][max_ns_rank] fp32 partial sums of C2 . x, per payload
+  const uint16_t* hidden16;  // C1 only: fp16 hidden [batch, max_ns_rank] given instead of the partial sums
   uint16_t* out[2];
 };
 
@@ -390,10 +391,16 @@ __global__ __launch_bounds__(kNsC1Cols) void ns_c1_kernel(NsArgs a) {
   const int nst = rc * rank;
   const bool has0 = static_cast<int>(threadIdx.x) < nst;
   const int hr0 = has0 ? static_cast<int>(threadIdx.x) / rank : 0, hj0 = has0 ? static_cast<int>(threadIdx.x) % rank : 0;
-  const float* src0 = part + static_cast<int64_t>(row0 + hr0) * ns.max_ns_rank + hj0;
+  const int64_t hoff0 = static_cast<int64_t>(row0 + hr0) * ns.max_ns_rank + hj0;
+  const bool given = a.hidden16 != nullptr;  // uniform
   float t0[kNsC1Slices];
+  uint32_t hraw0 = 0;
+  if (given) {
+    hraw0 = a.hidden16[hoff0];
+  } else {
 #pragma unroll
-  for (int k = 0; k < kNsC1Slices; ++k) t0[k] = src0[(k < a.slices ? k : a.slices - 1) * sstride];
+    for (int k = 0; k < kNsC1Slices; ++k) t0[k] = part[hoff0 + (k < a.slices ? k : a.slices - 1) * sstride];
+  }
   NsC1Batch cur;
   ns_c1_load(cur, qw, qz, qs, 0, words, egs, eg, out_f, qzc);
   uint32_t prev[kNsRows];  // one register per row: no packing, hence no wait, until the final add
@@ -402,15 +409,23 @@ __global__ __launch_bounds__(kNsC1Cols) void ns_c1_kernel(NsArgs a) {
     for (int r = 0; r < kNsRows; ++r) prev[r] = out[static_cast<int64_t>(row0 + (r < rc ? r : 0)) * out_f + nc];
   }
   if (has0) {  // a.slices <= kNsC1Slices: every partial sum is in t0
-    float v = 0.0f;
+    if (given) {
+      hs[hr0][hj0] = h2f(static_cast<uint16_t>(hraw0));
+    } else {
+      float v = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kNsC1Slices; ++k) {
-      if (k < a.slices) v += t0[k];
+      for (int k = 0; k < kNsC1Slices; ++k) {
+        if (k < a.slices) v += t0[k];
+      }
+      hs[hr0][hj0] = h2f(f2h_bits(v));  // the hidden tensor's fp16 value (F.linear(x, c2))
     }
-    hs[hr0][hj0] = h2f(f2h_bits(v));  // the hidden tensor's fp16 value (F.linear(x, c2))
   }
   for (int idx = threadIdx.x + kNsC1Cols; idx < nst; idx += kNsC1Cols) {  // tiles of more rows or ranks
     const int r = idx / rank, j = idx % rank;
+    if (given) {
+      hs[r][j] = h2f(a.hidden16[static_cast<int64_t>(row0 + r) * ns.max_ns_rank + j]);
+      continue;
+    }
     const float* src = part + static_cast<int64_t>(row0 + r) * ns.max_ns_rank + j;
     float t[kNsC1Slices];
 #pragma unroll
@@ -604,9 +619,51 @@ static int ns_forward(const char* who, const uint16_t* x, int32_t x_rows, const 
   return check_launch(who);
 }
 
+// The C1 half of a payload (what tris_grouped_ns_c1_forward reads).
+static int check_ns_c1(const tris_ns_payload* ns, const char* who) {
+  TRIS_REQUIRE(ns != nullptr, "%s: null payload", who);
+  TRIS_REQUIRE(ns->num_experts >= 0 && ns->outfeatures >= 0 && ns->max_ns_rank >= 0, "%s: negative shape", who);
+  TRIS_REQUIRE(ns->max_ns_rank <= kNsMaxRank, "%s: max_ns_rank %d exceeds %d", who, ns->max_ns_rank, kNsMaxRank);
+  if (ns->max_ns_rank > 0) {
+    TRIS_REQUIRE(ns->group_size > 0, "%s: group_size must be positive", who);
+    TRIS_REQUIRE(ns->ns_rank_per_expert && ns->ns_c1_rank_word_offsets && ns->ns_c1_group_offsets &&
+                     ns->ns_c1_qweight && ns->ns_c1_qzeros && ns->ns_c1_scales,
+                 "%s: null C1 tensor", who);
+  }
+  return TRIS_OK;
+}
+
 }  // namespace tris
 
 using namespace tris;
+
+extern "C" int tris_grouped_ns_c1_forward(const uint16_t* hidden, int32_t batch, const int32_t* expert_ids,
+                                          const int32_t* segment_offsets, int32_t num_segments,
+                                          const tris_ns_payload* ns, uint16_t* out, int32_t accumulate,
+                                          void* stream) {
+  const char* who = "tris_grouped_ns_c1_forward";
+  int rc = check_ns_c1(ns, who);
+  if (rc) return rc;
+  TRIS_REQUIRE(batch >= 0 && num_segments >= 0, "%s: negative batch or segment count", who);
+  if (batch == 0 || num_segments == 0 || ns->outfeatures == 0) return TRIS_OK;
+  TRIS_REQUIRE(expert_ids != nullptr && segment_offsets != nullptr && out != nullptr, "%s: null pointer", who);
+  if (ns->max_ns_rank == 0 && accumulate) return TRIS_OK;
+  TRIS_REQUIRE(ns->max_ns_rank == 0 || hidden != nullptr, "%s: null hidden", who);
+  NsArgs a{};
+  a.expert_ids = expert_ids;
+  a.segment_offsets = segment_offsets;
+  a.num_segments = num_segments;
+  a.batch = batch;
+  a.accumulate = accumulate != 0;
+  a.slices = 1;
+  a.c1_blocks = ceil_div(ns->outfeatures, kNsC1Cols);
+  a.ns[0] = a.ns[1] = *ns;
+  a.hidden16 = hidden;
+  a.out[0] = a.out[1] = out;
+  hipLaunchKernelGGL(ns_c1_kernel, dim3(ns_tiles(batch, num_segments), a.c1_blocks), dim3(kNsC1Cols), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch(who);
+}
 
 extern "C" int64_t tris_grouped_ns_workspace_bytes(int32_t batch, int32_t num_segments, int32_t infeatures,
                                                    int32_t max_ns_rank) {

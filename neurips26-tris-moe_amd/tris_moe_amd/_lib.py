@@ -146,6 +146,7 @@ SIGNATURES = {
     "tris_grouped_ns_compensation_pair_forward": (ctypes.c_int, [_P, _I32, _P, _I32, _P, _P, _I32, _PNS, _PNS, _P, _I64,
                                                                  _P, _P, _I32, _P]),
     "tris_grouped_ns_pair_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32, _I32]),
+    "tris_grouped_ns_c1_forward": (ctypes.c_int, [_P, _I32, _P, _P, _I32, _PNS, _P, _I32, _P]),
 }
 
 _lib = None

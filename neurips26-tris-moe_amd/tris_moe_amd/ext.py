@@ -875,6 +875,70 @@ def grouped_ns_compensation_forward(x_grouped, expert_ids, segment_offsets, prob
     return ns_compensation_apply_(out, x_grouped, expert_ids, segment_offsets, ns, accumulate=False)
 
 
+def grouped_ns_compensation_fused_decode_forward(x_grouped, expert_ids, segment_offsets, problem_offsets,
+                                                 total_problem_tiles, ns_rank_per_expert, ns_c2_rank_offsets,
+                                                 ns_c2_rank_word_offsets, ns_c1_rank_word_offsets,
+                                                 ns_c1_group_offsets, ns_c2_qweight, ns_c2_qzeros, ns_c2_scales,
+                                                 ns_c1_qweight, ns_c1_qzeros, ns_c1_scales, max_ns_rank: int,
+                                                 group_size: int) -> torch.Tensor:
+    """The extension's grouped_ns_compensation_fused_decode_forward (TriSMoE_cuda.cpp:456-496,
+    kernel.cu:8676-8776): the same compensation as grouped_ns_compensation_forward, which the reference
+    computes with one fused launch at decode.  Here both names run the decode-shaped split-K kernels."""
+    return grouped_ns_compensation_forward(
+        x_grouped, expert_ids, segment_offsets, problem_offsets, total_problem_tiles, ns_rank_per_expert,
+        ns_c2_rank_offsets, ns_c2_rank_word_offsets, ns_c1_rank_word_offsets, ns_c1_group_offsets, ns_c2_qweight,
+        ns_c2_qzeros, ns_c2_scales, ns_c1_qweight, ns_c1_qzeros, ns_c1_scales, max_ns_rank, group_size,
+        decode_phase=True)
+
+
+def _ns_c1_struct(ns: dict, device):
+    for k in ("ns_rank_per_expert", "ns_c1_rank_word_offsets", "ns_c1_group_offsets"):
+        _check_cuda(k, ns[k], torch.int32, 1, device)
+    for k in ("ns_c1_qweight", "ns_c1_qzeros"):
+        _check_cuda(k, ns[k], torch.int32, 2, device)
+    _check_cuda("ns_c1_scales", ns["ns_c1_scales"], torch.float16, 2, device)
+    E = int(ns["ns_rank_per_expert"].numel())
+    if any(int(ns[k].numel()) != E for k in ("ns_c1_rank_word_offsets", "ns_c1_group_offsets")):
+        raise RuntimeError("grouped NS C1 offset tensor length mismatch")
+    out_f = int(ns["ns_c1_qweight"].size(1))
+    if int(ns["ns_c1_scales"].size(1)) != out_f or int(ns["ns_c1_qzeros"].size(1)) != (out_f + 7) // 8:
+        raise RuntimeError("ns_c1 payload shapes do not match")
+    # the C2 fields stay NULL / 0: the C1-only entry does not read them
+    return _lib.TrisNsPayload(
+        ns_rank_per_expert=_ptr(ns["ns_rank_per_expert"]), ns_c1_rank_word_offsets=_ptr(ns["ns_c1_rank_word_offsets"]),
+        ns_c1_group_offsets=_ptr(ns["ns_c1_group_offsets"]), ns_c1_qweight=_ptr(ns["ns_c1_qweight"]),
+        ns_c1_qzeros=_ptr(ns["ns_c1_qzeros"]), ns_c1_scales=_ptr(ns["ns_c1_scales"]), num_experts=E,
+        outfeatures=out_f, max_ns_rank=int(ns["max_ns_rank"]), group_size=int(ns["group_size"]))
+
+
+def grouped_ns_c1_forward(hidden, expert_ids, segment_offsets, problem_offsets, total_problem_tiles,
+                          ns_rank_per_expert, ns_c1_rank_word_offsets, ns_c1_group_offsets, ns_c1_qweight,
+                          ns_c1_qzeros, ns_c1_scales, max_ns_rank: int, group_size: int,
+                          decode_phase: bool = False) -> torch.Tensor:
+    """The extension's grouped_ns_c1_forward (TriSMoE_cuda.cpp:423-455, kernel.cu:8526-8674): fp16
+    [batch, out] = C1_e . hidden[r][0:rank_e] per routed row, for a hidden [batch, max_ns_rank] computed
+    elsewhere (a C2 projection shared by every expert, qlinear_cuda.py:1952-2025).  Rows outside every
+    segment are zero, as the reference's torch::zeros output."""
+    _check_cuda("hidden", hidden, torch.float16, 2)
+    dev = hidden.device
+    _check_cuda("expert_ids", expert_ids, torch.int32, 1, dev)
+    _check_cuda("segment_offsets", segment_offsets, torch.int32, 1, dev)
+    if int(hidden.size(1)) != int(max_ns_rank):
+        raise RuntimeError("hidden rank mismatch for grouped NS C1 forward")
+    if int(segment_offsets.numel()) != int(expert_ids.numel()) + 1:
+        raise RuntimeError("segment_offsets length mismatch")
+    ns = {"ns_rank_per_expert": ns_rank_per_expert, "ns_c1_rank_word_offsets": ns_c1_rank_word_offsets,
+          "ns_c1_group_offsets": ns_c1_group_offsets, "ns_c1_qweight": ns_c1_qweight, "ns_c1_qzeros": ns_c1_qzeros,
+          "ns_c1_scales": ns_c1_scales, "max_ns_rank": int(max_ns_rank), "group_size": int(group_size)}
+    st = _ns_c1_struct(ns, dev)
+    batch = int(hidden.size(0))
+    out = torch.zeros((batch, st.outfeatures), dtype=torch.float16, device=dev)
+    _lib.check(_lib.load().tris_grouped_ns_c1_forward(
+        _ptr(hidden), batch, _ptr(expert_ids), _ptr(segment_offsets), int(expert_ids.numel()), ctypes.byref(st),
+        _ptr(out), 0, _stream(hidden)), "tris_grouped_ns_c1_forward")
+    return out
+
+
 def moe_combine(expert_out: torch.Tensor, inverse_perm: torch.Tensor, weights: torch.Tensor,
                 shared: torch.Tensor | None = None, expert_comp: torch.Tensor | None = None) -> torch.Tensor:
     """bf16 [T, H] = sum_s fp16(expert_out[inverse_perm[t, s]] * weights[t, s]) (+ shared), fp32-accumulated.

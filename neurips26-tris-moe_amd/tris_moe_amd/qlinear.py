@@ -10,14 +10,21 @@ Mirrors, for the grouped block-GR expert path:
 * ``ExpertSharedMatrix`` + ``QuantLinear`` in expert_compact3 mode (mode 5):
   ``compute_shared_hidden`` (``:4454-4502``), ``forward_from_precomputed_hidden``
   (``:4504-4560``), ``can_precompute_shared`` (``:4451``), block-GR packing
-  ``_pack_block_gr_gmap_tensor`` (``:3793-3859``).
+  ``_pack_block_gr_gmap_tensor`` (``:3793-3859``);
+* ``PackedQuantMatrix4bit`` (``:2637-2786``), the 4-bit packed backbone;
+* matrix-mode null-space compensation (``ns_mode == 2``) as a grouped payload:
+  ``build_grouped_ns_compensation_payload`` (``:1734-1872``, here
+  ``build_grouped_ns_payload``), ``run_grouped_ns_compensation_forward``
+  (``:2028-2128``), ``run_grouped_ns_c1_forward`` (``:1964-2025``) and the
+  ``ns_payload`` arguments of the structured forwards.
 
 Differences that are deliberate: no CPU/dequant fallback (a missing HIP
 library raises ``TrisExtensionUnavailable``); the route's segment order within
 an expert is the stable flat order; the launch policy is this library's
 (fused GR decode for decode-sized segments, predecode + predecoded GEMM when
 segments are long), with no split-K since each workgroup covers all of K.
-Matrix-mode null-space compensation (``ns_mode == 2``) is not provided.
+Null-space compensation comes from grouped payload dicts only; module lists
+carry vector-mode input scales (``expert_input_scale``), not matrices.
 """
 from __future__ import annotations
 
@@ -336,6 +343,48 @@ def _resolve_ns_payload(ns_payload):
 def _apply_ns(out, x_grouped, route, ns):
     if ns is not None:
         ext.ns_compensation_apply_(out, x_grouped.contiguous(), route["expert_ids"], route["segment_offsets"], ns)
+
+
+def _ns_route_inputs_ok(t: torch.Tensor, route) -> bool:
+    if route is None or t.device.type != "cuda" or t.dtype != torch.float16 or t.dim() != 2:
+        return False
+    gexp = route.get("grouped_expert_ids")
+    return gexp is not None and gexp.numel() == t.size(0)
+
+
+def run_grouped_ns_compensation_forward(payload_or_modules, x_grouped: torch.Tensor, grouped_route_or_segment_lengths,
+                                        expert_modules=None, expert_ids=None, prefer_fused_decode: bool = False):
+    """qlinear_cuda.py:2028-2128: the grouped compensation C1_e . fp16(C2_e . x) per routed row as a new
+    fp16 [R, out] tensor, or None when the inputs are outside the kernel contract or there is no
+    matrix-mode payload (module lists carry none in this build).  prefer_fused_decode selects the
+    reference's fused decode kernel there; the result is the same, and here one path serves both."""
+    route = _coerce_grouped_route(grouped_route_or_segment_lengths, x_grouped.device, expert_ids=expert_ids)
+    if not _ns_route_inputs_ok(x_grouped, route):
+        return None
+    ns = _resolve_ns_payload(payload_or_modules)
+    if ns is None:
+        return None
+    out = torch.empty((x_grouped.size(0), int(ns["ns_c1_scales"].size(1))), dtype=torch.float16,
+                      device=x_grouped.device)
+    return ext.ns_compensation_apply_(out, x_grouped.contiguous(), route["expert_ids"], route["segment_offsets"], ns,
+                                      accumulate=False)
+
+
+def run_grouped_ns_c1_forward(payload_or_modules, hidden_grouped: torch.Tensor, grouped_route_or_segment_lengths,
+                              expert_modules=None, expert_ids=None):
+    """qlinear_cuda.py:1964-2025: C1_e . hidden[r][0:rank_e] per routed row for a hidden [R, max_ns_rank]
+    computed elsewhere (the shared C2 projection), as a new fp16 [R, out] tensor, or None as above."""
+    route = _coerce_grouped_route(grouped_route_or_segment_lengths, hidden_grouped.device, expert_ids=expert_ids)
+    if not _ns_route_inputs_ok(hidden_grouped, route):
+        return None
+    ns = _resolve_ns_payload(payload_or_modules)
+    if ns is None:
+        return None
+    return ext.grouped_ns_c1_forward(
+        hidden_grouped.contiguous(), route["expert_ids"], route["segment_offsets"], route["problem_offsets"],
+        _route_total_problem_tiles_host(route), ns["ns_rank_per_expert"], ns["ns_c1_rank_word_offsets"],
+        ns["ns_c1_group_offsets"], ns["ns_c1_qweight"], ns["ns_c1_qzeros"], ns["ns_c1_scales"], int(ns["max_ns_rank"]),
+        int(ns["group_size"]))
 
 
 def run_grouped_structured_expert_forward(payload_or_modules, hidden_grouped: torch.Tensor, x_grouped: torch.Tensor,

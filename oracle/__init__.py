@@ -515,6 +515,24 @@ def ns_compensation(x_grouped, ns: dict, expert_ids, segment_offsets) -> np.ndar
     return out
 
 
+def ns_c1(hidden, ns: dict, expert_ids, segment_offsets) -> np.ndarray:
+    """fp16 [R, out] = F.linear(hidden_seg[:, :rank_e], C1_e) per segment for a given fp16 hidden
+    [R, max_ns_rank]: grouped_ns_c1_forward (kernel.cu:8526-8674, the C1 kernels at :1398-1592), used when
+    every expert shares one cached C2 projection (qlinear_cuda.py:1952-2025).  Rows of segments with no
+    expert or rank 0 are zero."""
+    h = np.asarray(hidden, dtype=np.float16)
+    out = np.zeros((h.shape[0], int(ns["outfeatures"])), dtype=np.float16)
+    seg = np.asarray(segment_offsets)
+    for s, e in enumerate(np.asarray(expert_ids)):
+        lo, hi = int(seg[s]), int(seg[s + 1])
+        if hi <= lo or e < 0 or e >= len(ns["ns_rank_per_expert"]):
+            continue
+        m = ns_expert_matrices(ns, int(e))
+        if m is not None:
+            out[lo:hi] = linear_f16(h[lo:hi, :m[1].shape[1]], m[1])
+    return out
+
+
 def bf16_round(x) -> np.ndarray:
     """fp32 -> bf16 (round to nearest even) -> fp32, for comparing bf16 outputs."""
     u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)

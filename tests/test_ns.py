@@ -79,6 +79,23 @@ def test_oracle_is_the_reference_fallback(oracle_mod):
     assert not np.array_equal(unrounded, want)
 
 
+def test_oracle_c1_is_the_second_half(oracle_mod):
+    """oracle.ns_c1 on the hidden fp16(C2_e . x) of each row gives ns_compensation(x) bit for bit, whatever the
+    hidden holds past each expert's rank (large values there: reading them would show)."""
+    rng = np.random.default_rng(9)
+    ns = synthetic.make_ns_payload(rng, 4, 64, 48, [8, 0, 24, 5], group_size=16, magnitude=0.05)
+    ids = np.asarray([3, 1, 0, -1, 2], np.int32)
+    offs = np.concatenate([[0], np.cumsum([2, 3, 6, 1, 4])]).astype(np.int32)
+    x = (rng.standard_normal((16, 64)) * 1.5).astype(np.float16)
+    hidden = np.full((16, int(ns["max_ns_rank"])), 300.0, np.float16)
+    for s, e in enumerate(ids):
+        lo, hi = int(offs[s]), int(offs[s + 1])
+        m = oracle_mod.ns_expert_matrices(ns, int(e)) if 0 <= e < 4 else None
+        if m is not None:
+            hidden[lo:hi, :m[0].shape[0]] = oracle_mod.linear_f16(x[lo:hi], m[0])
+    np.testing.assert_array_equal(oracle_mod.ns_c1(hidden, ns, ids, offs), oracle_mod.ns_compensation(x, ns, ids, offs))
+
+
 def test_out_of_range_slices_are_rejected():
     rng = np.random.default_rng(4)
     ns = synthetic.make_ns_payload(rng, 3, 64, 32, [8, 16, 8], group_size=32)
@@ -232,6 +249,50 @@ def test_layer_with_ns_compensation(tris, oracle_mod, cuda, tokens):
         x.to(torch.float16), logits, spec.top_k, spec.renormalize, payloads, backbones, spec.num_experts,
         torch.bfloat16, expert_path="fused").float().cpu().numpy()
     assert_close(fused, oracle_mod.bf16_round(want), f"layer with ns T={tokens} (fused path)")
+
+
+@pytest.mark.gpu
+def test_c1_only_and_runner_mirrors(tris, oracle_mod, cuda):
+    """grouped_ns_c1_forward on a given hidden (values past each expert's rank set large: never read), the
+    fused-decode binding, and the reference's runner functions run_grouped_ns_compensation_forward /
+    run_grouped_ns_c1_forward, against the oracle (rows outside every segment stay zero)."""
+    from test_gpu_parity import assert_close, note
+
+    note("ns c1-only and runner mirrors")
+    ext, ql = tris["ext"], tris["qlinear"]
+    rng = np.random.default_rng(12)
+    E, infeatures, outfeatures = 4, 384, 200
+    ns = synthetic.make_ns_payload(rng, E, infeatures, outfeatures, [8, 40, 0, 16], group_size=32, magnitude=0.05)
+    ids = np.asarray([1, 3, 0, 2], np.int32)
+    offs = np.concatenate([[0], np.cumsum([5, 0, 19, 3])]).astype(np.int32)
+    R = int(offs[-1])
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    dns = _dev_ns(ns, cuda)
+    hidden = (rng.standard_normal((R, int(ns["max_ns_rank"]))) * 2).astype(np.float16)
+    for s, e in enumerate(ids):
+        hidden[offs[s]:offs[s + 1], int(ns["ns_rank_per_expert"][e]):] = 1000.0
+    got = ext.grouped_ns_c1_forward(t(hidden), t(ids), t(offs), t(offs), 0, dns["ns_rank_per_expert"],
+                                    dns["ns_c1_rank_word_offsets"], dns["ns_c1_group_offsets"], dns["ns_c1_qweight"],
+                                    dns["ns_c1_qzeros"], dns["ns_c1_scales"], dns["max_ns_rank"], dns["group_size"])
+    assert_close(got.cpu().numpy(), oracle_mod.ns_c1(hidden, ns, ids, offs), "grouped_ns_c1_forward")
+    x = (rng.standard_normal((R, infeatures)) * 1.5).astype(np.float16)
+    comp = oracle_mod.ns_compensation(x, ns, ids, offs)
+    args = [dns[k] for k in ext.NS_PAYLOAD_TENSORS] + [dns["max_ns_rank"], dns["group_size"]]
+    plain = ext.grouped_ns_compensation_forward(t(x), t(ids), t(offs), t(offs), 0, *args)
+    fused = ext.grouped_ns_compensation_fused_decode_forward(t(x), t(ids), t(offs), t(offs), 0, *args)
+    assert torch.equal(plain, fused)
+    sel =torch.from_numpy(np.repeat(ids, np.diff(offs)).astype(np.int64)).reshape(-1, 1).to(cuda)
+    route = ql.build_grouped_route(sel, E)
+    order = route["expert_ids"].cpu().numpy()
+    # the route lists experts ascending: the same rows regrouped, so compare per expert
+    xr = np.concatenate([x[offs[list(ids).index(e)]:offs[list(ids).index(e) + 1]] for e in order])
+    hr = np.concatenate([hidden[offs[list(ids).index(e)]:offs[list(ids).index(e) + 1]] for e in order])
+    seg = route["segment_offsets"].cpu().numpy()
+    comp_r = ql.run_grouped_ns_compensation_forward(dns, t(xr), route)
+    assert_close(comp_r.cpu().numpy(), oracle_mod.ns_compensation(xr, ns, order, seg), "run_grouped_ns_compensation_forward")
+    c1_r = ql.run_grouped_ns_c1_forward(dns, t(hr), route)
+    assert_close(c1_r.cpu().numpy(), oracle_mod.ns_c1(hr, ns, order, seg), "run_grouped_ns_c1_forward")
+    assert ql.run_grouped_ns_compensation_forward(dns, t(xr).float(), route) is None   # outside the contract
 
 
 @pytest.mark.gpu
