@@ -401,6 +401,37 @@ int64_t tris_grouped_ns_pair_workspace_bytes(int32_t batch, int32_t num_segments
                                              int32_t max_ns_rank_a, int32_t max_ns_rank_b);
 
 /*
+ * Non-expert compact3 linear: replaces compact3_linear_forward (TriSMoE_cuda.cpp:497-563,
+ * kernel.cu:10781-11191, kernels :2146-3130) for block-GR payloads.  The module's matrix is a one-expert
+ * payload (num_experts == 1, rank = in_features); output[b][n] = fp16((sum_k x'[b][k] * W[n][k] (+
+ * addend[b][n])) (* output_scale[n]) (+ bias[n])) with x' = fp16(input * input_scale) per column when
+ * input_scale is given (__hmul), else input.  input fp16 [batch, rank]; addend fp32 [batch, out] or NULL
+ * (the module's null-space term C1 . (C2 . x), which the reference adds to the fp32 accumulator before
+ * the output scale); output fp16 [batch, out] (every row written).  The exact-weight VALU kernel over one
+ * segment of all rows.
+ */
+int tris_compact3_linear_forward(const uint16_t* input, int32_t batch, const tris_compact3_payload* payload,
+                                 const uint16_t* input_scale, const float* addend, uint16_t* output, void* stream);
+
+/*
+ * Two non-expert compact3 linears on the same input in one launch (no scale, no bias): replaces
+ * compact3_dual_linear_forward (TriSMoE_cuda.cpp:641-700, kernel.cu:11192-11456; the reference returns
+ * them stacked [2, batch, out]).  The same bits as two tris_compact3_linear_forward calls.
+ */
+int tris_compact3_dual_linear_forward(const uint16_t* input, int32_t batch, const tris_compact3_payload* payload_a,
+                                      const tris_compact3_payload* payload_b, uint16_t* output_a, uint16_t* output_b,
+                                      void* stream);
+
+/*
+ * output[b][n] = sum_k input[b][k] * weight[n][k] in fp32, no rounding; input fp16 (input_f16) or fp32
+ * (input_f32, exactly one non-NULL), weight fp16 [out, in].  The non-expert linear's null-space term
+ * C1 . (C2 . x) from the dequantised packed matrices, kept in fp32 as the reference's kernel does
+ * (kernel.cu:2252-2316).  No reference counterpart as a call.
+ */
+int tris_dense_linear_f32(const uint16_t* input_f16, const float* input_f32, int32_t batch, int32_t in_features,
+                          const uint16_t* weight, int32_t out_features, float* output, void* stream);
+
+/*
  * Routing-weighted combine: replaces final.index_add_(0, grouped_token_indices,
  * (down_out * routing).to(output_dtype)) (modeling_mixtral.py:529-536).
  * out[t, :] = bf16( sum_s fp16(expert_out[inverse_perm[t*top_k+s], :] * weights[t, s])

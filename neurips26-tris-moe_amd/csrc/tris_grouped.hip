@@ -33,14 +33,17 @@ struct ProjArgs {
   uint16_t* out;            // [batch, N]
   const int32_t* decoded;   // predecoded words [num_segments, nblk, 128] (predecoded variant)
   tris_compact3_payload p;
+  const uint16_t* input_scale;  // fp16 [rank] or NULL: the activation is fp16(hidden * input_scale) per column
+  const float* addend;          // fp32 [batch, N] or NULL: added to the sum before the output scale
 };
 
 struct GroupedArgs {
   ProjArgs proj[2];
   const int32_t* expert_ids;
-  const int32_t* segment_offsets;
+  const int32_t* segment_offsets;  // NULL: one segment of all batch rows, expert 0 (a non-expert linear)
   int num_segments;
   int row_tile;
+  int batch;
 };
 
 // Map workgroup tile index -> (segment, first row, row count) with row_tile
@@ -143,14 +146,20 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GroupedArgs 
   if (n0 >= N) return;  // uniform over the workgroup, before any barrier
 
   int s = 0, row0 = 0, rc = 0;
-  if (!map_row_tile(a.segment_offsets, a.num_segments, blockIdx.y, a.row_tile, &s, &row0, &rc)) return;
+  if (a.segment_offsets == nullptr) {  // uniform: every row in one segment of expert 0
+    row0 = static_cast<int>(blockIdx.y) * a.row_tile;
+    if (row0 >= a.batch) return;
+    rc = (a.batch - row0) < a.row_tile ? (a.batch - row0) : a.row_tile;
+  } else if (!map_row_tile(a.segment_offsets, a.num_segments, blockIdx.y, a.row_tile, &s, &row0, &rc)) {
+    return;
+  }
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
   const int lane = tid % kWave;
   const int n = n0 + lane;
   const bool nv = n < N;
-  const int e = a.expert_ids[s];
+  const int e = a.segment_offsets == nullptr ? 0 : a.expert_ids[s];
   uint16_t* out = pa.out;
 
   // Negative slots give zero rows (the reference's expert_valid); ids past the
@@ -199,7 +208,9 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GroupedArgs 
       const int r = idx / (kGemmWaves * kTileK);
       const int j = idx % (kGemmWaves * kTileK);
       const int k = kchunk + j;
-      xs[r][j] = k < rank ? h2f(hid[static_cast<int64_t>(row0 + r) * rank + k]) : 0.0f;
+      float xv = k < rank ? h2f(hid[static_cast<int64_t>(row0 + r) * rank + k]) : 0.0f;
+      if (pa.input_scale != nullptr && k < rank) xv = h2f(f2h_bits(xv * h2f(pa.input_scale[k])));  // __hmul
+      xs[r][j] = xv;
     }
     __syncthreads();
     const int kb = kc + wave;
@@ -293,6 +304,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GroupedArgs 
     for (int r = 0; r < MT; ++r) {
       if (r < rc) {
         float v = acc[r] + red[0][r][lane] + red[1][r][lane] + red[2][r][lane];
+        if (pa.addend != nullptr) v += pa.addend[static_cast<int64_t>(row0 + r) * N + n];
         if (p.has_output_scale) v = v * scale;
         if (p.has_bias) v = v + bias;
         out[static_cast<int64_t>(row0 + r) * N + n] = f2h_bits(v);
@@ -424,6 +436,7 @@ int launch_grouped(const uint16_t* hidden_a, const uint16_t* hidden_b, int batch
   args.segment_offsets = segment_offsets;
   args.num_segments = num_segments;
   args.row_tile = kGemmRows;
+  args.batch = batch;
   dim3 grid(ceil_div(max_n, kTileOut), static_cast<unsigned>(tiles), nproj);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (predecoded) {
@@ -442,6 +455,47 @@ int launch_grouped(const uint16_t* hidden_a, const uint16_t* hidden_b, int batch
   return check_launch(who);
 }
 
+// A non-expert linear (or two sharing the input): the exact kernel over one segment of all rows with each
+// payload's single expert, an optional per-column input scale and fp32 addend per projection.
+int launch_linear(const uint16_t* input, int batch, const tris_compact3_payload* pa, const tris_compact3_payload* pb,
+                  const uint16_t* input_scale, const float* addend, uint16_t* out_a, uint16_t* out_b, void* stream,
+                  const char* who) {
+  const int nproj = pb ? 2 : 1;
+  TRIS_REQUIRE(batch >= 0, "%s: negative batch", who);
+  for (int i = 0; i < nproj; ++i) {
+    const tris_compact3_payload* p = i ? pb : pa;
+    int rc = check_payload(p, true, who);
+    if (rc) return rc;
+    TRIS_REQUIRE(p->num_experts == 1, "%s: a non-expert payload holds one matrix (num_experts %d)", who,
+                 p->num_experts);
+    TRIS_REQUIRE(p->q_gmap_gr_offsets != nullptr, "%s: block-GR split bitmaps required", who);
+  }
+  TRIS_REQUIRE(!pb || pb->rank == pa->rank, "%s: the pair's ranks differ", who);
+  if (batch == 0 || pa->rank == 0) return TRIS_OK;
+  TRIS_REQUIRE(input && out_a && (!pb || out_b), "%s: null pointer", who);
+  int max_n = 0;
+  for (int i = 0; i < nproj; ++i) {
+    const tris_compact3_payload* p = i ? pb : pa;
+    max_n = p->outfeatures > max_n ? p->outfeatures : max_n;
+  }
+  if (max_n == 0) return TRIS_OK;
+  GroupedArgs args{};
+  args.proj[0] = ProjArgs{input, out_a, nullptr, *pa, input_scale, addend};
+  if (pb) args.proj[1] = ProjArgs{input, out_b, nullptr, *pb, nullptr, nullptr};
+  args.segment_offsets = nullptr;
+  args.num_segments = 1;
+  args.row_tile = kGemmRows;
+  args.batch = batch;
+  dim3 grid(ceil_div(max_n, kTileOut), ceil_div(batch, kGemmRows), nproj);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pb) {
+    hipLaunchKernelGGL((grouped_gemm_kernel<false, 2>), grid, dim3(kGemmThreads), 0, s, args);
+  } else {
+    hipLaunchKernelGGL((grouped_gemm_kernel<false, 1>), grid, dim3(kGemmThreads), 0, s, args);
+  }
+  return check_launch(who);
+}
+
 int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int batch, const int32_t* expert_ids,
                         const int32_t* segment_offsets, int num_segments, const int32_t* decoded_a,
                         const int32_t* decoded_b, const tris_compact3_payload* pa, const tris_compact3_payload* pb,
@@ -451,6 +505,21 @@ bool grouped_mfma_supported(const tris_compact3_payload* p, const uint16_t* hidd
 }  // namespace tris
 
 using namespace tris;
+
+extern "C" int tris_compact3_linear_forward(const uint16_t* input, int32_t batch, const tris_compact3_payload* payload,
+                                            const uint16_t* input_scale, const float* addend, uint16_t* output,
+                                            void* stream) {
+  return launch_linear(input, batch, payload, nullptr, input_scale, addend, output, nullptr, stream,
+                       "tris_compact3_linear_forward");
+}
+
+extern "C" int tris_compact3_dual_linear_forward(const uint16_t* input, int32_t batch,
+                                                 const tris_compact3_payload* payload_a,
+                                                 const tris_compact3_payload* payload_b, uint16_t* output_a,
+                                                 uint16_t* output_b, void* stream) {
+  return launch_linear(input, batch, payload_a, payload_b, nullptr, nullptr, output_a, output_b, stream,
+                       "tris_compact3_dual_linear_forward");
+}
 
 extern "C" int tris_grouped_forward_block_gr(const uint16_t* hidden, int32_t batch, const int32_t* expert_ids,
                                              const int32_t* segment_offsets, const int32_t* problem_offsets,

@@ -619,6 +619,32 @@ static int ns_forward(const char* who, const uint16_t* x, int32_t x_rows, const 
   return check_launch(who);
 }
 
+// out[b][n] = sum_k in[b][k] * W[n][k] in fp32 with no rounding (in fp16 or fp32, W fp16 [N, K]): the
+// non-expert linear's null-space term, whose C2 product stays in fp32 and whose C1 product joins the fp32
+// accumulator (kernel.cu:2252-2316).  One wavefront per output, lanes striding K (coalesced), a fixed
+// butterfly reduction (deterministic).
+__global__ __launch_bounds__(256) void dense_linear_f32_kernel(const uint16_t* __restrict__ in16,
+                                                               const float* __restrict__ in32, int batch, int K,
+                                                               const uint16_t* __restrict__ w, int N,
+                                                               float* __restrict__ out) {
+  const int64_t o = static_cast<int64_t>(blockIdx.x) * (blockDim.x / 64) + threadIdx.x / 64;
+  if (o >= static_cast<int64_t>(batch) * N) return;  // uniform over the wavefront
+  const int lane = threadIdx.x % 64;
+  const int b = static_cast<int>(o / N), n = static_cast<int>(o % N);
+  const uint16_t* wr = w + static_cast<int64_t>(n) * K;
+  float v = 0.0f;
+  if (in32 != nullptr) {
+    const float* xr = in32 + static_cast<int64_t>(b) * K;
+    for (int k = lane; k < K; k += 64) v += xr[k] * h2f(wr[k]);
+  } else {
+    const uint16_t* xr = in16 + static_cast<int64_t>(b) * K;
+    for (int k = lane; k < K; k += 64) v += h2f(xr[k]) * h2f(wr[k]);
+  }
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d);
+  if (lane == 0) out[o] = v;
+}
+
 // The C1 half of a payload (what tris_grouped_ns_c1_forward reads).
 static int check_ns_c1(const tris_ns_payload* ns, const char* who) {
   TRIS_REQUIRE(ns != nullptr, "%s: null payload", who);
@@ -636,6 +662,24 @@ static int check_ns_c1(const tris_ns_payload* ns, const char* who) {
 }  // namespace tris
 
 using namespace tris;
+
+extern "C" int tris_dense_linear_f32(const uint16_t* input_f16, const float* input_f32, int32_t batch,
+                                     int32_t in_features, const uint16_t* weight, int32_t out_features, float* output,
+                                     void* stream) {
+  const char* who = "tris_dense_linear_f32";
+  TRIS_REQUIRE(batch >= 0 && in_features >= 0 && out_features >= 0, "%s: negative shape", who);
+  if (batch == 0 || out_features == 0) return TRIS_OK;
+  TRIS_REQUIRE((input_f16 == nullptr) != (input_f32 == nullptr), "%s: give exactly one of the fp16 / fp32 inputs",
+               who);
+  TRIS_REQUIRE(output != nullptr && (in_features == 0 || weight != nullptr), "%s: null pointer", who);
+  const int64_t outs = static_cast<int64_t>(batch) * out_features;
+  const int64_t blocks = (outs + 3) / 4;
+  TRIS_REQUIRE(blocks <= 2147483647LL, "%s: too many outputs", who);
+  hipLaunchKernelGGL(dense_linear_f32_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), input_f16, input_f32, batch, in_features, weight, out_features,
+                     output);
+  return check_launch(who);
+}
 
 extern "C" int tris_grouped_ns_c1_forward(const uint16_t* hidden, int32_t batch, const int32_t* expert_ids,
                                           const int32_t* segment_offsets, int32_t num_segments,

@@ -147,6 +147,9 @@ SIGNATURES = {
                                                                  _P, _P, _I32, _P]),
     "tris_grouped_ns_pair_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32, _I32]),
     "tris_grouped_ns_c1_forward": (ctypes.c_int, [_P, _I32, _P, _P, _I32, _PNS, _P, _I32, _P]),
+    "tris_compact3_linear_forward": (ctypes.c_int, [_P, _I32, _PAY, _P, _P, _P, _P]),
+    "tris_compact3_dual_linear_forward": (ctypes.c_int, [_P, _I32, _PAY, _PAY, _P, _P, _P]),
+    "tris_dense_linear_f32": (ctypes.c_int, [_P, _P, _I32, _I32, _P, _I32, _P, _P]),
 }
 
 _lib = None

@@ -1,7 +1,7 @@
 """Drop-in for the reference's native module ``autogptq_TriS_cuda`` on the grouped expert path.
 
 Every function keeps the pybind name, argument order and defaults of
-``TriSMoE_cuda.cpp:1138-1430`` for the grouped block-GR path and returns
+``TriSMoE_cuda.cpp:1138-1430`` for the block-GR paths and returns
 freshly allocated torch tensors exactly as the reference does, but computes
 through the gfx950 HIP kernels of libtris_moe_hip.so (C ABI, via ctypes).
 Argument contracts mirror the reference's ``CHECK_*`` / ``TORCH_CHECK``
@@ -9,11 +9,13 @@ macros (``TriSMoE_cuda_kernel.cu:49-54``, ``:9789-9842``) and raise
 ``RuntimeError`` like them.  All work is enqueued on torch's current stream of
 the input's device.
 
-The non-expert compact3 linears (``compact3_linear_forward``,
-``compact3_qkv_linear_forward``, ``compact3_dual_linear_forward``) are outside
-this library's scope; they exist so that the reference's ABI probe
-(``qlinear_cuda.py:14-37``) accepts the module, and raise RuntimeError, which
-the reference's callers treat as "kernel unavailable".
+Besides the grouped expert entry points, the module has the 4-bit packed
+backbone (``packed4_linear_forward``), the grouped null-space compensation
+(``grouped_ns_*``) and the non-expert compact3 linears
+(``compact3_linear_forward``, ``compact3_qkv_linear_forward``,
+``compact3_dual_linear_forward``) for block-GR payloads; a sparse split-bitmap
+payload raises RuntimeError, which the reference's callers treat as "kernel
+unavailable" (convert it to block-GR at load).
 """
 from __future__ import annotations
 
@@ -498,18 +500,6 @@ def compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded_hybrid(
         col_pack3_b, row_pack3_b, use_uniform_k64_groups)
 
 
-def _out_of_scope(name):
-    def fn(*args, **kwargs):
-        raise RuntimeError(f"{name}: non-expert compact3 linears are not provided by the TriS-MoE HIP library")
-    fn.__name__ = name
-    return fn
-
-
-compact3_linear_forward = _out_of_scope("compact3_linear_forward")
-compact3_qkv_linear_forward = _out_of_scope("compact3_qkv_linear_forward")
-compact3_dual_linear_forward = _out_of_scope("compact3_dual_linear_forward")
-
-
 # ---------------------------------------------- verification / helper entry points
 def compact3_dequant(payload_tensors: dict, rank: int, expert_ids: torch.Tensor, use_uniform_k64_groups=False):
     """Dense fp16 weights [num, N, rank] of the listed experts (GPU verification kernel)."""
@@ -936,6 +926,166 @@ def grouped_ns_c1_forward(hidden, expert_ids, segment_offsets, problem_offsets, 
     _lib.check(_lib.load().tris_grouped_ns_c1_forward(
         _ptr(hidden), batch, _ptr(expert_ids), _ptr(segment_offsets), int(expert_ids.numel()), ctypes.byref(st),
         _ptr(out), 0, _stream(hidden)), "tris_grouped_ns_c1_forward")
+    return out
+
+
+# ----------------------------------------------------------------- non-expert compact3 linears
+def _is_block_gr(q_gmap_gr_offsets, q_gmap_gr_meta, rank: int, outfeatures: int) -> bool:
+    """The reference's format test (kernel.cu:10841-10842): block-GR when the offsets / meta lengths match
+    the block grid, else the sparse split-bitmap form."""
+    nblk = _num_gr_blocks((rank + 31) // 32, outfeatures)
+    return (q_gmap_gr_offsets is not None and int(q_gmap_gr_offsets.numel()) == nblk + 1
+            and q_gmap_gr_meta is not None and int(q_gmap_gr_meta.numel()) == nblk)
+
+
+def _linear_struct(rank, qweight1, qweight2_sparse, qweight2_sparse_prefix, q_gmap_gr_words, q_gmap_gr_offsets,
+                   q_gmap_gr_meta, c_map, g_idx, col_pack3, row_pack3, output_scale, has_output_scale, bias, has_bias,
+                   device, who):
+    """A non-expert module's tensors (2-D / 1-D) as a one-expert payload descriptor: views, no copies."""
+    outfeatures = int(qweight1.size(1))
+    if not _is_block_gr(q_gmap_gr_offsets, q_gmap_gr_meta, rank, outfeatures):
+        raise RuntimeError(f"{who}: sparse split-bitmap payloads are not accepted; convert them to block-GR at load "
+                           "(checkpoint.sparse_gmap_to_dense + gr_encode, as GroupedCheckpoint does)")
+    one = lambda t: t.unsqueeze(0) if t is not None else None
+    g2 = g_idx.reshape(1, -1)
+    uniform = bool(torch.equal(g2[:, (torch.arange(rank, device=g2.device) // 64) * 64], g2)) if rank else True
+    return make_payload_struct(rank, one(qweight1), one(qweight2_sparse), one(qweight2_sparse_prefix),
+                               one(q_gmap_gr_words), one(q_gmap_gr_offsets), one(q_gmap_gr_meta), one(c_map), g2,
+                               one(col_pack3), one(row_pack3), one(output_scale) if has_output_scale else output_scale,
+                               has_output_scale, one(bias) if has_bias else bias, has_bias, uniform, device, True, who)
+
+
+def _ns_linear_addend(x16, ns_c1_qweight, ns_c1_qzeros, ns_c1_scales, ns_c1_g_idx, ns_c2_qweight, ns_c2_qzeros,
+                      ns_c2_scales, ns_c2_g_idx, outfeatures: int) -> torch.Tensor:
+    """fp32 [batch, out] = C1 . (C2 . x) with no rounding between or after, from the exactly dequantised
+    packed matrices: the non-expert kernel's null-space term (kernel.cu:2252-2316), which joins the fp32
+    accumulator before the output scale."""
+    rank = int(x16.size(1))
+    ns_rank = int(ns_c2_qweight.size(1))
+    c2 = packed4_dequant(Packed4Matrix(ns_c2_qweight, ns_c2_qzeros, ns_c2_scales, ns_c2_g_idx, ns_rank, rank,
+                                       uniform_group_size(ns_c2_g_idx)))
+    c1 = packed4_dequant(Packed4Matrix(ns_c1_qweight, ns_c1_qzeros, ns_c1_scales, ns_c1_g_idx, outfeatures, ns_rank,
+                                       uniform_group_size(ns_c1_g_idx)))
+    batch = int(x16.size(0))
+    lib = _lib.load()
+    hidden = torch.empty((batch, ns_rank), dtype=torch.float32, device=x16.device)
+    _lib.check(lib.tris_dense_linear_f32(_ptr(x16), None, batch, rank, _ptr(c2), ns_rank, _ptr(hidden), _stream(x16)),
+               "tris_dense_linear_f32")
+    addend = torch.empty((batch, outfeatures), dtype=torch.float32, device=x16.device)
+    _lib.check(lib.tris_dense_linear_f32(None, _ptr(hidden), batch, ns_rank, _ptr(c1), outfeatures, _ptr(addend),
+                                         _stream(x16)), "tris_dense_linear_f32")
+    return addend
+
+
+def compact3_linear_forward(input, qweight1, qweight2_sparse, qweight2_sparse_prefix, q_gmap_sparse,
+                            q_gmap_sparse_prefix, q_gmap_gr_words, q_gmap_gr_offsets, q_gmap_gr_meta, c_map, g_idx,
+                            col_pack3, row_pack3, input_scale, output_scale, bias, has_input_scale: bool,
+                            has_output_scale: bool, has_bias: bool, ns_c1_qweight, ns_c1_qzeros, ns_c1_scales,
+                            ns_c1_g_idx, ns_c2_qweight, ns_c2_qzeros, ns_c2_scales, ns_c2_g_idx, has_ns_matrix: bool,
+                            split_k_slices: int = 1, request_prefill_tensor_core: bool = False,
+                            use_uniform_k64_groups: bool = False) -> torch.Tensor:
+    """The extension's compact3_linear_forward (TriSMoE_cuda.cpp:497-563, kernel.cu:10781-11191): fp16
+    [batch, out] = fp16((x' . W^T + ns) * output_scale + bias) for one non-expert compact3 matrix, x' the
+    input times input_scale per column (fp16), ns the matrix-mode null-space term in fp32.  Block-GR payloads;
+    split_k_slices, request_prefill_tensor_core and use_uniform_k64_groups are the reference's launch hints
+    (one exact kernel serves every shape here)."""
+    who = "compact3_linear_forward"
+    _check_cuda("input", input, torch.float16, 2)
+    dev = input.device
+    rank = int(input.size(1))
+    if int(g_idx.numel()) != rank:
+        raise RuntimeError(f"{who}: g_idx rank mismatch")
+    outfeatures = int(qweight1.size(1))
+    st = _linear_struct(rank, qweight1, qweight2_sparse, qweight2_sparse_prefix, q_gmap_gr_words, q_gmap_gr_offsets,
+                        q_gmap_gr_meta, c_map, g_idx, col_pack3, row_pack3, output_scale, has_output_scale, bias,
+                        has_bias, dev, who)
+    batch = int(input.size(0))
+    out = torch.zeros((batch, outfeatures), dtype=torch.float16, device=dev)
+    if batch == 0 or rank == 0 or outfeatures == 0:
+        return out
+    scale = None
+    if has_input_scale:
+        _check_cuda("input_scale", input_scale, torch.float16, 1, dev)
+        if int(input_scale.numel()) != rank:
+            raise RuntimeError(f"{who}: input_scale length mismatch")
+        scale = input_scale
+    addend = None
+    if has_ns_matrix:
+        addend = _ns_linear_addend(input, ns_c1_qweight, ns_c1_qzeros, ns_c1_scales, ns_c1_g_idx, ns_c2_qweight,
+                                   ns_c2_qzeros, ns_c2_scales, ns_c2_g_idx, outfeatures)
+    _lib.check(_lib.load().tris_compact3_linear_forward(_ptr(input), batch, ctypes.byref(st), _ptr(scale),
+                                                        _ptr(addend), _ptr(out), _stream(input)), who)
+    return out
+
+
+def compact3_dual_linear_forward(input, a_qweight1, a_qweight2_sparse, a_qweight2_sparse_prefix, a_gmap_gr_words,
+                                 a_gmap_gr_offsets, a_gmap_gr_meta, a_c_map, a_g_idx, a_col_pack3, a_row_pack3,
+                                 b_qweight1, b_qweight2_sparse, b_qweight2_sparse_prefix, b_gmap_gr_words,
+                                 b_gmap_gr_offsets, b_gmap_gr_meta, b_c_map, b_g_idx, b_col_pack3, b_row_pack3,
+                                 split_k_slices: int = 1, use_uniform_k64_groups: bool = False) -> torch.Tensor:
+    """The extension's compact3_dual_linear_forward (TriSMoE_cuda.cpp:641-700, kernel.cu:11192-11456): two
+    non-expert matrices of the same shape on one input (a shared expert's gate and up), no scale or bias;
+    returns them stacked, fp16 [2, batch, out], from one launch."""
+    who = "compact3_dual_linear_forward"
+    _check_cuda("input", input, torch.float16, 2)
+    dev = input.device
+    rank = int(input.size(1))
+    outfeatures = int(a_qweight1.size(1))
+    if int(b_qweight1.size(1)) != outfeatures:
+        raise RuntimeError(f"{who}: the two projections' output widths differ")
+    sa = _linear_struct(rank, a_qweight1, a_qweight2_sparse, a_qweight2_sparse_prefix, a_gmap_gr_words,
+                        a_gmap_gr_offsets, a_gmap_gr_meta, a_c_map, a_g_idx, a_col_pack3, a_row_pack3, None, False,
+                        None, False, dev, who)
+    sb = _linear_struct(rank, b_qweight1, b_qweight2_sparse, b_qweight2_sparse_prefix, b_gmap_gr_words,
+                        b_gmap_gr_offsets, b_gmap_gr_meta, b_c_map, b_g_idx, b_col_pack3, b_row_pack3, None, False,
+                        None, False, dev, who)
+    batch = int(input.size(0))
+    out = torch.zeros((2, batch, outfeatures), dtype=torch.float16, device=dev)
+    if batch == 0 or rank == 0 or outfeatures == 0:
+        return out
+    _lib.check(_lib.load().tris_compact3_dual_linear_forward(_ptr(input), batch, ctypes.byref(sa), ctypes.byref(sb),
+                                                             _ptr(out[0]), _ptr(out[1]), _stream(input)), who)
+    return out
+
+
+def compact3_qkv_linear_forward(input, q_qweight1, q_qweight2_sparse, q_qweight2_sparse_prefix, q_gmap_gr_words,
+                                q_gmap_gr_offsets, q_gmap_gr_meta, q_c_map, q_g_idx, q_col_pack3, q_row_pack3, q_bias,
+                                k_qweight1, k_qweight2_sparse, k_qweight2_sparse_prefix, k_gmap_gr_words,
+                                k_gmap_gr_offsets, k_gmap_gr_meta, k_c_map, k_g_idx, k_col_pack3, k_row_pack3, k_bias,
+                                v_qweight1, v_qweight2_sparse, v_qweight2_sparse_prefix, v_gmap_gr_words,
+                                v_gmap_gr_offsets, v_gmap_gr_meta, v_c_map, v_g_idx, v_col_pack3, v_row_pack3, v_bias,
+                                split_k_slices: int = 1, use_uniform_k64_groups: bool = False) -> torch.Tensor:
+    """The extension's compact3_qkv_linear_forward (TriSMoE_cuda.cpp:564-640, kernel.cu:11457-11740): the
+    attention Q / K / V projections of one input, each fp16((x . W^T) + bias), stacked fp16 [3, batch, out]
+    (equal output widths).  Q and K share one launch, V takes a second."""
+    who = "compact3_qkv_linear_forward"
+    _check_cuda("input", input, torch.float16, 2)
+    dev = input.device
+    rank = int(input.size(1))
+    outfeatures = int(q_qweight1.size(1))
+    if int(k_qweight1.size(1)) != outfeatures or int(v_qweight1.size(1)) != outfeatures:
+        raise RuntimeError(f"{who}: Q, K and V must have the same output width")
+    structs = []
+    for (qw1, qw2, qw2p, grw, gro, grm, cmap, gidx, colp, rowp, b) in (
+            (q_qweight1, q_qweight2_sparse, q_qweight2_sparse_prefix, q_gmap_gr_words, q_gmap_gr_offsets,
+             q_gmap_gr_meta, q_c_map, q_g_idx, q_col_pack3, q_row_pack3, q_bias),
+            (k_qweight1, k_qweight2_sparse, k_qweight2_sparse_prefix, k_gmap_gr_words, k_gmap_gr_offsets,
+             k_gmap_gr_meta, k_c_map, k_g_idx, k_col_pack3, k_row_pack3, k_bias),
+            (v_qweight1, v_qweight2_sparse, v_qweight2_sparse_prefix, v_gmap_gr_words, v_gmap_gr_offsets,
+             v_gmap_gr_meta, v_c_map, v_g_idx, v_col_pack3, v_row_pack3, v_bias)):
+        has_bias = b is not None and b.numel() > 0
+        structs.append(_linear_struct(rank, qw1, qw2, qw2p, grw, gro, grm, cmap, gidx, colp, rowp, None, False, b,
+                                      has_bias, dev, who))
+    batch = int(input.size(0))
+    out = torch.zeros((3, batch, outfeatures), dtype=torch.float16, device=dev)
+    if batch == 0 or rank == 0 or outfeatures == 0:
+        return out
+    lib = _lib.load()
+    _lib.check(lib.tris_compact3_dual_linear_forward(_ptr(input), batch, ctypes.byref(structs[0]),
+                                                     ctypes.byref(structs[1]), _ptr(out[0]), _ptr(out[1]),
+                                                     _stream(input)), who)
+    _lib.check(lib.tris_compact3_linear_forward(_ptr(input), batch, ctypes.byref(structs[2]), None, None, _ptr(out[2]),
+                                                _stream(input)), who)
     return out
 
 

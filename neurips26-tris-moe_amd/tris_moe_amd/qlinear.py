@@ -12,6 +12,9 @@ Mirrors, for the grouped block-GR expert path:
   (``:4504-4560``), ``can_precompute_shared`` (``:4451``), block-GR packing
   ``_pack_block_gr_gmap_tensor`` (``:3793-3859``);
 * ``PackedQuantMatrix4bit`` (``:2637-2786``), the 4-bit packed backbone;
+* the non-expert compact3 linear (``QuantLinear`` mode 4, ``:4238-4360``, here
+  ``Compact3Linear``) and its fused launches ``run_compact3_qkv_block_gr_forward``
+  (``:915-1002``) and ``run_compact3_shared_expert_gate_up_forward`` (``:1005-1098``);
 * matrix-mode null-space compensation (``ns_mode == 2``) as a grouped payload:
   ``build_grouped_ns_compensation_payload`` (``:1734-1872``, here
   ``build_grouped_ns_payload``), ``run_grouped_ns_compensation_forward``
@@ -783,6 +786,126 @@ class QuantLinear(nn.Module):
     def forward(self, x: torch.Tensor):
         hidden = self.compute_shared_hidden(x)
         return self.forward_from_precomputed_hidden(hidden, x)
+
+
+# ------------------------------------------------------------------ non-expert compact3 linears
+COMPACT3_MODULE_KEYS = ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "q_gmap_gr_words",
+                        "q_gmap_gr_offsets", "q_gmap_gr_meta", "c_map", "g_idx", "col_pack3", "row_pack3")
+
+
+class Compact3Linear(nn.Module):
+    """A non-expert compact3 linear (the reference's QuantLinear in compact3 mode 4, qlinear_cuda.py:4238-4360):
+    y = fp16((x' . W^T + C1 . (C2 . x)) * output_scale + bias) with W the block-GR compact3 matrix over the
+    full input width, x' = fp16(x * input_scale) when an input scale is set, the null-space term when packed
+    C1 / C2 matrices are set.  Attention projections and dense (shared-expert) MLPs use it."""
+
+    def __init__(self, infeatures: int, outfeatures: int):
+        super().__init__()
+        self.infeatures = int(infeatures)
+        self.outfeatures = int(outfeatures)
+        self._mode_host = 4
+        self._ns_mode_host = 0
+        for key in COMPACT3_MODULE_KEYS:
+            self.register_buffer(key, torch.empty(0, dtype=torch.int64 if key.endswith("pack3") else torch.int32))
+        self.register_buffer("input_scale", None)
+        self.register_buffer("output_scale", None)
+        self.register_buffer("bias", None)
+        self.ns_c1 = None
+        self.ns_c2 = None
+
+    def load_tensors(self, tensors: dict):
+        """Set the packed buffers from host arrays or tensors (the module's checkpoint keys); optional
+        input_scale, output_scale, bias, and ns_c1 / ns_c2 as pack_4bit dicts (qweight, qzeros, scales, g_idx)."""
+        conv = lambda v, dt: v.to(dtype=dt) if isinstance(v, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(v)).to(dt)
+        for key in COMPACT3_MODULE_KEYS:
+            setattr(self, key, conv(tensors[key], torch.int64 if key.endswith("pack3") else torch.int32))
+        for key in ("input_scale", "output_scale", "bias"):
+            if tensors.get(key) is not None:
+                setattr(self, key, conv(tensors[key], torch.float16))
+        for key in ("ns_c1", "ns_c2"):
+            if tensors.get(key) is not None:
+                setattr(self, key, {k: conv(v, torch.float16 if k == "scales" else torch.int32)
+                                    for k, v in tensors[key].items()})
+        self._ns_mode_host = 2 if self.ns_c1 is not None and self.ns_c2 is not None else 0
+        return self
+
+    def _apply(self, fn, *args, **kwargs):
+        super()._apply(fn, *args, **kwargs)
+        for key in ("ns_c1", "ns_c2"):
+            d = getattr(self, key)
+            if d is not None:
+                setattr(self, key, {k: fn(v) for k, v in d.items()})
+        return self
+
+    def _compact3_k64_groups_uniform(self) -> bool:
+        g = self.g_idx.reshape(1, -1)
+        rank = int(g.size(1))
+        return bool(torch.equal(g[:, (torch.arange(rank, device=g.device) // 64) * 64], g)) if rank else True
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        shape = x.shape[:-1] + (self.outfeatures,)
+        x2 = x.reshape(-1, self.infeatures).to(torch.float16).contiguous()
+        empty = x2.new_empty((0,))
+        ns = self._ns_mode_host == 2
+        c1, c2 = (self.ns_c1, self.ns_c2) if ns else ({}, {})
+        y = ext.compact3_linear_forward(
+            x2, *[getattr(self, key) for key in COMPACT3_MODULE_KEYS[:3]], empty, empty,
+            *[getattr(self, key) for key in COMPACT3_MODULE_KEYS[3:]],
+            self.input_scale if self.input_scale is not None else empty,
+            self.output_scale if self.output_scale is not None else empty,
+            self.bias if self.bias is not None else empty,
+            self.input_scale is not None, self.output_scale is not None, self.bias is not None,
+            *[c1.get(k, empty) for k in ("qweight", "qzeros", "scales", "g_idx")],
+            *[c2.get(k, empty) for k in ("qweight", "qzeros", "scales", "g_idx")], ns, 1, False,
+            self._compact3_k64_groups_uniform())
+        return y.reshape(shape)
+
+
+def _plain_compact3(module, outfeatures=None, allow_bias=False) -> bool:
+    """The fused Q/K/V and gate/up launches take modules without scales or a null-space term
+    (qlinear_cuda.py:873-912)."""
+    return (isinstance(module, Compact3Linear) and module._ns_mode_host == 0 and module.input_scale is None
+            and module.output_scale is None and (allow_bias or module.bias is None)
+            and (outfeatures is None or module.outfeatures == outfeatures))
+
+
+def run_compact3_qkv_block_gr_forward(q_proj, k_proj, v_proj, hidden_states: torch.Tensor):
+    """qlinear_cuda.py:915-1002: (q, k, v) of one input through the fused Q/K/V binding, or None when the
+    modules or the input fall outside it (the caller then runs the three modules)."""
+    if hidden_states.device.type != "cuda" or hidden_states.dtype != torch.float16:
+        return None
+    if hidden_states.shape[-1] != getattr(q_proj, "infeatures", None):
+        return None
+    n = getattr(q_proj, "outfeatures", None)
+    if not all(_plain_compact3(m, n, allow_bias=True) for m in (q_proj, k_proj, v_proj)):
+        return None
+    shape = hidden_states.shape[:-1] + (n,)
+    x = hidden_states.reshape(-1, hidden_states.shape[-1]).contiguous()
+    empty = x.new_empty((0,))
+    args = []
+    for m in (q_proj, k_proj, v_proj):
+        args += [getattr(m, key) for key in COMPACT3_MODULE_KEYS] + [m.bias if m.bias is not None else empty]
+    fused = ext.compact3_qkv_linear_forward(x, *args, 1, all(m._compact3_k64_groups_uniform()
+                                                            for m in (q_proj, k_proj, v_proj)))
+    return tuple(fused[i].reshape(shape) for i in range(3))
+
+
+def run_compact3_shared_expert_gate_up_forward(gate_proj, up_proj, hidden_states: torch.Tensor):
+    """qlinear_cuda.py:1005-1098: (gate, up) of one input through the dual binding, or None as above."""
+    if hidden_states.device.type != "cuda" or hidden_states.dtype != torch.float16:
+        return None
+    if hidden_states.shape[-1] != getattr(gate_proj, "infeatures", None):
+        return None
+    n = getattr(gate_proj, "outfeatures", None)
+    if not (_plain_compact3(gate_proj, n) and _plain_compact3(up_proj, n)):
+        return None
+    shape = hidden_states.shape[:-1] + (n,)
+    x = hidden_states.reshape(-1, hidden_states.shape[-1]).contiguous()
+    fused = ext.compact3_dual_linear_forward(x, *[getattr(gate_proj, k) for k in COMPACT3_MODULE_KEYS],
+                                             *[getattr(up_proj, k) for k in COMPACT3_MODULE_KEYS], 1,
+                                             gate_proj._compact3_k64_groups_uniform()
+                                             and up_proj._compact3_k64_groups_uniform())
+    return fused[0].reshape(shape), fused[1].reshape(shape)
 
 
 def build_grouped_precomputed_payload(modules, device, dtype):

@@ -341,6 +341,34 @@ def grouped_forward(payload: dict, hidden, expert_ids, segment_offsets, uniform_
     return out
 
 
+def module_as_payload(module: dict) -> dict:
+    """A non-expert module's tensors (no expert dimension) as a one-expert stacked payload."""
+    out = {}
+    for k, v in module.items():
+        out[k] = v[None] if isinstance(v, np.ndarray) else v
+    return out
+
+
+def compact3_linear(x, module: dict, input_scale=None, output_scale=None, bias=None, ns_c2=None, ns_c1=None,
+                    uniform_k64_groups: bool | None = None) -> np.ndarray:
+    """compact3_linear_forward (kernel.cu:2146-2331 arithmetic, host 10781-11191): fp16 [batch, out] =
+    fp16((x' . W^T + C1 . (C2 . x)) * output_scale + bias), x' = fp16(x * input_scale) per column (__hmul)
+    when given, the null-space term from the raw x in fp32 with no rounding, every sum in fp32 and one
+    rounding at the end.  ns_c2 fp16 [ns_rank, in], ns_c1 fp16 [out, ns_rank] (dense, dequantised)."""
+    x = np.asarray(x, dtype=np.float16)
+    w = dequant_grouped_expert(module_as_payload(module), 0, uniform_k64_groups).astype(np.float32)
+    xs = f16_mul(x, np.asarray(input_scale, dtype=np.float16)[None, :]) if input_scale is not None else x
+    acc = xs.astype(np.float32) @ w.T
+    if ns_c2 is not None:
+        h = x.astype(np.float32) @ np.asarray(ns_c2, dtype=np.float16).astype(np.float32).T
+        acc = acc + h @ np.asarray(ns_c1, dtype=np.float16).astype(np.float32).T
+    if output_scale is not None:
+        acc = acc * np.asarray(output_scale, dtype=np.float16).astype(np.float32)[None, :]
+    if bias is not None:
+        acc = acc + np.asarray(bias, dtype=np.float16).astype(np.float32)[None, :]
+    return acc.astype(np.float16)
+
+
 # ------------------------------------------------------------------ route
 def build_route(selected_experts, num_experts: int, m_tile: int = 4) -> dict:
     """TriSMoE_cuda.cpp:741-793.  The permutation is the stable argsort of the

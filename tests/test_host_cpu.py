@@ -57,8 +57,10 @@ def test_ext_module_passes_reference_abi_probe(tris):
     assert ext.TRIS_COMPACT3_KERNEL_ABI_VERSION == 2
     for name in required:
         assert callable(getattr(ext, name)), name
-    with pytest.raises(RuntimeError):
-        ext.compact3_linear_forward()
+    import torch
+
+    with pytest.raises(RuntimeError):   # a CPU input is outside the kernel contract, as the reference's CHECK_CUDA
+        ext.compact3_linear_forward(*([torch.zeros((2, 2), dtype=torch.float16)] * 28))
 
 
 def test_c_abi_argument_errors_without_gpu(tris):
