@@ -6,16 +6,20 @@
 // through an optional row index.
 //
 // Shape: out[T, rank] = x[T, in] . SV[rank, in]^T with fp16 inputs and fp32
-// accumulation.  One workgroup = 4 wavefronts computes a 16-token x 16-row
-// output tile over one K slice; wavefront w takes a contiguous quarter of the
-// slice and issues its 16-byte operand loads in batches of kBbBatch 32-wide K
-// steps before the v_mfma_f32_16x16x32_f16, and the four partial tiles are
-// added in LDS in wavefront order.  The slice count is chosen so that a decode
+// accumulation.  One workgroup = 4 wavefronts computes up to 4 16-token x
+// 16-row output tiles over one K slice, so each SV operand load feeds every
+// token tile (SV is read once per row tile and slice); wavefront w takes a
+// contiguous quarter of the slice and issues its 16-byte operand loads in
+// batches of 4 or 8 32-wide K steps (the last batch predicated) before the
+// v_mfma_f32_16x16x32_f16, and the four partial tiles are added in LDS in
+// wavefront order.  The slice count is chosen so that a decode
 // launch has a few hundred workgroups (latency, not MFMA, bounds this
 // projection at decode).  With one slice the workgroup writes fp16; otherwise
 // it writes fp32 partial tiles to the caller's workspace and
 // backbone_reduce_kernel adds the slices in slice order and rounds once, so
-// results are deterministic and no workgroups communicate inside a kernel.
+// results are deterministic and no workgroups communicate inside a kernel (an
+// in-kernel last-arriver reduction needs device-scope release fences, which
+// write back the L2 on this GPU: measured far slower than the extra launch).
 // blockIdx.z selects one of up to two projections of the same rows (a gate/up
 // pair in one launch).
 //
@@ -69,9 +73,13 @@ __device__ __forceinline__ f16x8 load8_vec(const uint16_t* __restrict__ src, int
   return v;
 }
 
-// grid = (row tiles, token tiles * slices, projections)
+// grid = (row tiles, token-tile groups * slices, projections).  A workgroup covers TT token tiles of 16
+// rows, so each SV operand load feeds TT MFMAs (SV, the bytes that bound the projection, is read once per
+// row tile and slice however many tokens there are, up to 16 * TT); B K steps of loads are in flight per
+// wavefront, the last batch of a slice predicated (zero operands past its end).
+template <int TT, int B>
 __global__ __launch_bounds__(kBbThreads) void backbone_kernel(BackboneArgs a) {
-  __shared__ f32x4 red[kBbWaves - 1][kWave];
+  __shared__ f32x4 red[kBbWaves - 1][TT][kWave];
   const int q = blockIdx.z;
   const BackboneProj& pj = a.proj[q];
   const int tid = threadIdx.x;
@@ -79,86 +87,103 @@ __global__ __launch_bounds__(kBbThreads) void backbone_kernel(BackboneArgs a) {
   const int lane = tid % kWave;
   const int r0 = blockIdx.x * 16;
   const int slice = blockIdx.y % a.slices;
-  const int t0 = (blockIdx.y / a.slices) * 16;
+  const int tg0 = (blockIdx.y / a.slices) * TT;  // first token tile of the group
   const int i = lane % 16;
   const int kg = lane / 16;
 
-  const int t = t0 + i;
-  const bool t_valid = t < a.tokens;
-  int64_t xrow = 0;
-  if (t_valid) xrow = a.row_index != nullptr ? a.row_index[t] : t;
-  const uint16_t* xsrc = a.x + xrow * a.in_features;
+  bool t_valid[TT];
+  const uint16_t* xsrc[TT];
+#pragma unroll
+  for (int j = 0; j < TT; ++j) {
+    const int t = (tg0 + j) * 16 + i;
+    t_valid[j] = t < a.tokens;
+    int64_t xrow = 0;
+    if (t_valid[j]) xrow = a.row_index != nullptr ? a.row_index[t] : t;
+    xsrc[j] = a.x + xrow * a.in_features;
+  }
   const int r = r0 + i;
   const bool r_valid = r < a.rank;
   const uint16_t* ssrc = pj.sv + static_cast<int64_t>(r_valid ? r : 0) * a.in_features;
   const bool scaled = a.in_scale != nullptr;
   const bool vec = (a.in_features % 8) == 0;
 
-  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4 acc[TT];
+#pragma unroll
+  for (int j = 0; j < TT; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const int kper = a.slice_k / kBbWaves;
   const int kbeg0 = slice * a.slice_k + wave * kper;
   const int kbeg = kbeg0 < a.in_features ? kbeg0 : a.in_features;
   const int kend = (kbeg0 + kper) < a.in_features ? (kbeg0 + kper) : a.in_features;
-  int k0 = kbeg;
   if (vec) {
-    for (; k0 + kBbBatch * kBbKStep <= kend; k0 += kBbBatch * kBbKStep) {
-      f16x8 av[kBbBatch], bv[kBbBatch];
+    // every k is a multiple of 8 and so is kend: a 16-byte run is inside the slice iff k < kend
+    for (int k0 = kbeg; k0 < kend; k0 += B * kBbKStep) {
+      f16x8 bv[B], av[TT][B];
 #pragma unroll
-      for (int u = 0; u < kBbBatch; ++u) {
+      for (int u = 0; u < B; ++u) {
         const int k = k0 + u * kBbKStep + kg * 8;
-        av[u] = load8_vec(xsrc, k, t_valid);
-        bv[u] = load8_vec(ssrc, k, r_valid);
+        const bool kv = k < kend;
+        bv[u] = load8_vec(ssrc, k, r_valid && kv);
+#pragma unroll
+        for (int j = 0; j < TT; ++j) av[j][u] = load8_vec(xsrc[j], k, t_valid[j] && kv);
       }
       if (scaled) {
 #pragma unroll
-        for (int u = 0; u < kBbBatch; ++u) {
-          av[u] = av[u] * load8_vec(a.in_scale, k0 + u * kBbKStep + kg * 8, true);  // fp16 products, as x * ns_col
+        for (int u = 0; u < B; ++u) {
+          const int k = k0 + u * kBbKStep + kg * 8;
+          const f16x8 sc = load8_vec(a.in_scale, k, k < kend);
+#pragma unroll
+          for (int j = 0; j < TT; ++j) av[j][u] = av[j][u] * sc;  // fp16 products, as x * ns_col
         }
       }
 #pragma unroll
-      for (int u = 0; u < kBbBatch; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[u], bv[u], acc, 0, 0, 0);
+      for (int u = 0; u < B; ++u) {
+#pragma unroll
+        for (int j = 0; j < TT; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[j][u], bv[u], acc[j], 0, 0, 0);
+      }
+    }
+  } else {
+    // rows not a multiple of 8 columns: element-wise loads
+    for (int k0 = kbeg; k0 < kend; k0 += kBbKStep) {
+      const int k = k0 + kg * 8;
+      const f16x8 bv = load8_tail(ssrc, k, kend, r_valid);
+      const f16x8 sc = scaled ? load8_tail(a.in_scale, k, kend, true) : f16x8{1, 1, 1, 1, 1, 1, 1, 1};
+#pragma unroll
+      for (int j = 0; j < TT; ++j) {
+        f16x8 av = load8_tail(xsrc[j], k, kend, t_valid[j]);
+        if (scaled) av = av * sc;
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[j], 0, 0, 0);
+      }
     }
   }
-  // remaining steps: 16-byte loads for whole runs of 8 columns, element-wise at the end of a row
-  for (; k0 < kend; k0 += kBbKStep) {
-    const int k = k0 + kg * 8;
-    f16x8 av, bv;
-    if (vec && k + 8 <= kend) {
-      av = load8_vec(xsrc, k, t_valid);
-      bv = load8_vec(ssrc, k, r_valid);
-      if (scaled) av = av * load8_vec(a.in_scale, k, true);
-    } else {
-      av = load8_tail(xsrc, k, kend, t_valid);
-      bv = load8_tail(ssrc, k, kend, r_valid);
-      if (scaled) av = av * load8_tail(a.in_scale, k, kend, true);
-    }
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
+  if (wave > 0) {
+#pragma unroll
+    for (int j = 0; j < TT; ++j) red[wave - 1][j][lane] = acc[j];
   }
-  if (wave > 0) red[wave - 1][lane] = acc;
   __syncthreads();
-  if (wave != 0) return;
-#pragma unroll
-  for (int w = 0; w < kBbWaves - 1; ++w) acc += red[w][lane];
-  // acc[v] = out[t0 + 4*kg + v][r0 + i]
   const int col = r0 + i;
-  if (col >= a.rank) return;
-  if (a.slices == 1) {
+  if (wave == 0) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int tt = t0 + 4 * kg + v;
-      if (tt < a.tokens) pj.out[static_cast<int64_t>(tt) * a.rank + col] = f2h_bits(acc[v]);
+    for (int j = 0; j < TT; ++j) {
+#pragma unroll
+      for (int w = 0; w < kBbWaves - 1; ++w) acc[j] += red[w][j][lane];
+      // acc[j][v] = out[t0 + 4*kg + v][r0 + i], t0 the tile's first token
+      const int t0 = (tg0 + j) * 16;
+      float* part = a.partials + (static_cast<int64_t>(q) * a.slices + slice) * a.tokens * a.rank;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int tt = t0 + 4 * kg + v;
+        if (tt < a.tokens && col < a.rank) {
+          if (a.slices == 1) {
+            pj.out[static_cast<int64_t>(tt) * a.rank + col] = f2h_bits(acc[j][v]);
+          } else {
+            part[static_cast<int64_t>(tt) * a.rank + col] = acc[j][v];
+          }
+        }
+      }
     }
-    return;
-  }
-  float* part = a.partials + (static_cast<int64_t>(q) * a.slices + slice) * a.tokens * a.rank;
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int tt = t0 + 4 * kg + v;
-    if (tt < a.tokens) part[static_cast<int64_t>(tt) * a.rank + col] = acc[v];
   }
 }
 
-// out[q][t][r] = fp16(sum over slices s = 0, 1, ... of partials[q][s][t][r]); blockIdx.y = q.
 __global__ __launch_bounds__(256) void backbone_reduce_kernel(BackboneArgs a) {
   const int64_t count = static_cast<int64_t>(a.tokens) * a.rank;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -185,9 +210,16 @@ __global__ __launch_bounds__(256) void fill_zero_u16_kernel(uint16_t* __restrict
 // most one slice per kBbWaves*kBbKStep columns and kBbMaxSlices in all.  The
 // count does not depend on how many projections share the launch, so a pair
 // gives the same bits as two single calls.
+// Token tiles per workgroup: all of them up to 4 (one SV read per row tile and slice).
+static int backbone_token_group(int tokens) {
+  const int tiles = ceil_div(tokens > 0 ? tokens : 1, 16);
+  return tiles < 4 ? tiles : 4;
+}
+
 int backbone_slices(int tokens, int in_features, int rank) {
   if (tokens <= 0 || in_features <= 0 || rank <= 0) return 1;
-  const int64_t tiles = static_cast<int64_t>(ceil_div(tokens, 16)) * ceil_div(rank, 16);
+  const int64_t tiles =
+      static_cast<int64_t>(ceil_div(ceil_div(tokens, 16), backbone_token_group(tokens))) * ceil_div(rank, 16);
   int64_t slices = (kBbTargetWgs + tiles - 1) / tiles;
   const int64_t max_by_k = ceil_div(in_features, kBbWaves * kBbKStep);
   if (slices > max_by_k) slices = max_by_k;
@@ -226,9 +258,10 @@ int launch_backbone(const uint16_t* x, int tokens, int in_features, const int64_
   TRIS_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
                "%s: workspace of %lld bytes needed, %lld given", who, static_cast<long long>(need),
                static_cast<long long>(workspace_bytes));
-  const int token_tiles = ceil_div(tokens, 16);
+  const int tt = backbone_token_group(tokens);
+  const int token_groups = ceil_div(ceil_div(tokens, 16), tt);
   const int row_tiles = ceil_div(rank, 16);
-  TRIS_REQUIRE(static_cast<int64_t>(token_tiles) * slices <= 65535, "%s: too many tokens", who);
+  TRIS_REQUIRE(static_cast<int64_t>(token_groups) * slices <= 65535, "%s: too many tokens", who);
   BackboneArgs args{};
   args.x = x;
   args.row_index = row_index;
@@ -241,7 +274,13 @@ int launch_backbone(const uint16_t* x, int tokens, int in_features, const int64_
   args.rank = rank;
   args.slices = slices;
   args.slice_k = ceil_div(ceil_div(in_features, slices), kBbWaves * kBbKStep) * kBbWaves * kBbKStep;
-  hipLaunchKernelGGL(backbone_kernel, dim3(row_tiles, token_tiles * slices, nproj), dim3(kBbThreads), 0, s, args);
+  const dim3 grid(row_tiles, token_groups * slices, nproj);
+  switch (tt) {
+    case 1: hipLaunchKernelGGL((backbone_kernel<1, 8>), grid, dim3(kBbThreads), 0, s, args); break;
+    case 2: hipLaunchKernelGGL((backbone_kernel<2, 8>), grid, dim3(kBbThreads), 0, s, args); break;
+    case 3: hipLaunchKernelGGL((backbone_kernel<3, 4>), grid, dim3(kBbThreads), 0, s, args); break;
+    default: hipLaunchKernelGGL((backbone_kernel<4, 4>), grid, dim3(kBbThreads), 0, s, args); break;
+  }
   int rc = check_launch(who);
   if (rc || slices == 1) return rc;
   const int64_t count = static_cast<int64_t>(tokens) * rank;

@@ -545,10 +545,11 @@ def test_run_grouped_structured_api(tris, oracle_mod, cuda):
 
 # ------------------------------------------------------------------ backbone
 @pytest.mark.parametrize("tokens,in_f,rank", [(1, 4096, 512), (16, 4096, 512), (5, 14336, 512), (37, 2048, 256),
-                                              (4, 1000, 100), (300, 4096, 512)])
+                                              (4, 1000, 100), (64, 4096, 512), (70, 1001, 48), (300, 4096, 512)])
 def test_backbone_matches_fp32(tris, cuda, tokens, in_f, rank):
-    """Decode-sized inputs run the split-K MFMA kernel; from ext.BACKBONE_LIBRARY_MIN_ROWS rows (the last
-    case, and its gathered rows) the library GEMM."""
+    """Decode-sized inputs run the split-K MFMA kernel (1 to 4 token tiles per workgroup: 37 tokens are 3,
+    64 are 4, 70 are a group of 4 and a partial one; 1001 columns take the element-wise loads); from
+    ext.BACKBONE_LIBRARY_MIN_ROWS rows (the last case, and its gathered rows) the library GEMM."""
     note(f"backbone T={tokens} in={in_f} rank={rank}")
     rng = np.random.default_rng(tokens + in_f)
     x = rng.standard_normal((tokens, in_f)).astype(np.float16)
