@@ -663,8 +663,11 @@ __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, i
 // Along a run the units compute from one weight buffer while the next tile's weight words are copied into
 // the other.  With more than one 512-column chunk (rank > 512) the chunk data is restaged per tile and
 // nothing is prefetched.
+// At most 128 VGPRs for one unit (no spills: checked with -Rpass-analysis=kernel-resource-usage), so four
+// wavefronts per SIMD fit: more workgroups resident to cover the weight-load latency of each tile.
 template <int kUnits>
-__global__ __launch_bounds__(kUnits * kMfThreads) void grouped_mfma_kernel(MfmaArgs a) {
+__global__ __launch_bounds__(kUnits * kMfThreads) __attribute__((amdgpu_waves_per_eu(4 / kUnits, 8)))
+void grouped_mfma_kernel(MfmaArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char mf_lds[];
   const int unit = kUnits == 2 ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kMfThreads) : 0;
   const int utid = static_cast<int>(threadIdx.x) % kMfThreads;
@@ -1329,10 +1332,10 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
   const int lds = mf_lds_bytes(units, args.xs_rows, args.lds_groups);
   const int lds_total = lds + mf_static_lds_bytes(units);
   TRIS_REQUIRE(lds_total <= 160 * 1024, "%s: LDS request %d exceeds a CU", who, lds_total);
-  // Workgroups: as many as the GPU holds at once (LDS and about 160 VGPRs per lane, 3 wavefronts per
-  // SIMD, bound them), shared by the projections of an unfused pair.
+  // Workgroups: as many as the GPU holds at once (LDS and the kernel's 128 VGPRs per lane, 4 wavefronts
+  // per SIMD for one unit, bound them), shared by the projections of an unfused pair.
   int wgs_per_cu = (160 * 1024) / lds_total;
-  const int by_regs = 3 / units;
+  const int by_regs = units == 1 ? 4 : 1;
   wgs_per_cu = wgs_per_cu < by_regs ? wgs_per_cu : by_regs;
   wgs_per_cu = wgs_per_cu > 0 ? wgs_per_cu : 1;
   int wgs = (kMfCus * wgs_per_cu) / nproj;
