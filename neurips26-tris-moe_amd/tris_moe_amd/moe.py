@@ -210,7 +210,7 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
                                             row_index=route["grouped_token_indices"])
 
     # one launch for the three projections (the persistent GEMMs assume the whole GPU, so nothing runs
-    # beside them)
+    # beside them; two launches, the down bitmaps on either stream, measured slower)
     with torch.cuda.stream(side):
         order = (("gate", pg), ("up", pu), ("down", pd))
         ext.grouped_block_gr_predecode_multi(
