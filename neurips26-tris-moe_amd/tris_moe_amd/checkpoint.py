@@ -396,6 +396,47 @@ class GroupedCheckpoint:
         return {proj: {k: (v.numpy() if isinstance(v, torch.Tensor) else v) for k, v in p.items()}
                 for proj, p in layer.items() if proj in GROUPED_PRECOMPUTED_KEYS}
 
+    def load_compact3_linear(self, prefix: str, device):
+        """A non-expert compact3 linear (the reference's QuantLinear in mode 4: attention projections,
+        dense or shared-expert MLPs) from its state-dict keys ``{prefix}.qweight1`` ... ``{prefix}.row_pack3``,
+        as a ``qlinear.Compact3Linear`` on ``device``.  A sparse split bitmap (``q_gmap_sparse`` +
+        prefix) is converted to block-GR here; ``ns_mode == 1`` brings the input / output scales
+        ``ns_vector_col`` / ``ns_vector_row`` and packed ``ns_c1_quant`` / ``ns_c2_quant`` matrices the
+        null-space term, as the reference's forward uses them (qlinear_cuda.py:4238-4360, 3998-4022)."""
+        from .packing import num_gr_blocks
+        from .qlinear import COMPACT3_MODULE_KEYS, Compact3Linear
+
+        get = lambda name: self._f.get_tensor(f"{prefix}.{name}") if f"{prefix}.{name}" in self._keys else None
+        t = {k: get(k) for k in COMPACT3_MODULE_KEYS}
+        rank = int(t["g_idx"].numel())
+        n = int(t["qweight1"].size(1))
+        gro, grm = t.get("q_gmap_gr_offsets"), t.get("q_gmap_gr_meta")
+        if gro is None or grm is None or int(grm.numel()) != num_gr_blocks(rank, n):
+            sparse, sprefix = get("q_gmap_sparse"), get("q_gmap_sparse_prefix")
+            if sparse is None or sprefix is None:
+                raise KeyError(f"{self.path}: {prefix} has neither block-GR nor sparse split bitmaps")
+            one = {"q_gmap_sparse": sparse[None], "q_gmap_sparse_prefix": sprefix[None], "c_map": t["c_map"][None],
+                   "g_idx": t["g_idx"][None], "qweight1": t["qweight1"][None]}
+            gr = _to_block_gr(one)
+            for k in ("q_gmap_gr_words", "q_gmap_gr_offsets", "q_gmap_gr_meta"):
+                t[k] = torch.as_tensor(gr[k])[0]
+        extras = {}
+        ns_mode = get("ns_mode")
+        if ns_mode is not None and int(ns_mode.reshape(-1)[0]) == 1:
+            extras["input_scale"] = get("ns_vector_col")
+            extras["output_scale"] = get("ns_vector_row")
+        bias = get("bias")
+        if bias is not None and bias.numel() > 0:
+            extras["bias"] = bias
+        for key in ("ns_c1", "ns_c2"):
+            q = {name: get(f"{key}_quant.{name}") for name in ("qweight", "qzeros", "scales", "g_idx")}
+            if all(v is not None and v.numel() > 0 for v in q.values()):
+                extras[key] = q
+        if ("ns_c1" in extras) != ("ns_c2" in extras):
+            extras.pop("ns_c1", None)
+            extras.pop("ns_c2", None)
+        return Compact3Linear(rank, n).load_tensors(dict(t, **extras)).to(device)
+
     def load_backbones(self, layer_idx: int, device) -> dict:
         from .qlinear import PackedQuantMatrix4bit
 

@@ -196,3 +196,86 @@ def test_checkpoint_layer_runs_like_memory(tris, cuda, tmp_path):
                                                 TINY.num_experts, torch.bfloat16)
         torch.cuda.synchronize()
         assert torch.equal(a.view(torch.int16), b.view(torch.int16)), lp
+
+
+def _mode4_tensors(tris, rng, n=96, rank=128, sparse_form=False):
+    """A non-expert compact3 module's state-dict tensors (QuantLinear mode 4), block-GR or sparse split
+    bitmaps, with ns_mode 1 scales and packed null-space matrices."""
+    from tris_moe_amd.packing import pack_4bit, pack_bool_matrix, pack_sparse_bool_matrix, sparse_prefix
+
+    syn, ext = tris["synthetic"], tris["ext"]
+    col_norm = rng.random(rank).astype(np.float32) + 0.5
+    proj = syn.make_projection(rng, 1, n, rank, 0.15, col_norm, ext.gr_encode)
+    t = {k: np.ascontiguousarray(proj[k][0]) for k in ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix",
+                                                       "c_map", "g_idx", "col_pack3", "row_pack3")}
+    sal = ((t["c_map"].astype(np.uint32)[np.arange(rank) // 32] >> (np.arange(rank) % 32).astype(np.uint32)) & 1
+           ).astype(bool)
+    dense = (rng.random((n, rank)) < 0.2) & ~sal[None, :]
+    words, offsets, meta = ext.gr_encode(pack_bool_matrix(dense))
+    if sparse_form:
+        t["q_gmap_sparse"] = pack_sparse_bool_matrix(dense, ~sal)
+        t["q_gmap_sparse_prefix"] = sparse_prefix(~sal)
+    else:
+        t.update(q_gmap_gr_words=words, q_gmap_gr_offsets=offsets, q_gmap_gr_meta=meta)
+    t["ns_mode"] = np.asarray([1], np.int32)
+    t["ns_vector_col"] = (rng.random(rank) + 0.5).astype(np.float16)
+    t["ns_vector_row"] = (rng.random(n) + 0.5).astype(np.float16)
+    t["bias"] = rng.standard_normal(n).astype(np.float16)
+    for key, mat, gs in (("ns_c2", rng.standard_normal((16, rank)), 32), ("ns_c1", rng.standard_normal((n, 16)), 16)):
+        for name, v in pack_4bit(mat.astype(np.float32) * 0.05, gs).items():
+            t[f"{key}_quant.{name}"] = v
+    return t, (words, offsets, meta)
+
+
+def test_compact3_linear_module_loads(tris, tmp_path):
+    """load_compact3_linear: a mode-4 module's keys, block-GR or sparse split bitmaps (converted to the words
+    this build's encoder gives), with its ns_mode 1 scales, bias and packed null-space matrices."""
+    from safetensors.torch import save_file
+
+    rng = np.random.default_rng(4)
+    for sparse_form in (False, True):
+        t, (words, offsets, meta) = _mode4_tensors(tris, rng, sparse_form=sparse_form)
+        path = str(tmp_path / f"m4_{int(sparse_form)}.safetensors")
+        save_file({f"model.layers.0.self_attn.q_proj.{k}": torch.from_numpy(np.ascontiguousarray(v))
+                   for k, v in t.items()}, path)
+        m = ck.GroupedCheckpoint(path).load_compact3_linear("model.layers.0.self_attn.q_proj", "cpu")
+        np.testing.assert_array_equal(m.q_gmap_gr_offsets.numpy(), offsets)
+        np.testing.assert_array_equal(m.q_gmap_gr_meta.numpy(), meta)
+        np.testing.assert_array_equal(m.q_gmap_gr_words.numpy()[: words.size], words)
+        np.testing.assert_array_equal(m.input_scale.numpy(), t["ns_vector_col"])
+        np.testing.assert_array_equal(m.output_scale.numpy(), t["ns_vector_row"])
+        assert m._ns_mode_host == 2 and m.ns_c1["qweight"].shape == t["ns_c1_quant.qweight"].shape
+
+
+@pytest.mark.gpu
+def test_compact3_linear_from_checkpoint_runs(tris, oracle_mod, cuda, tmp_path):
+    """A mode-4 module loaded from a sparse-form checkpoint computes what the same module built from the
+    block-GR tensors computes (bit for bit), within tolerance of the oracle."""
+    from safetensors.torch import save_file
+    from test_gpu_parity import assert_close, note
+
+    note("compact3 linear from checkpoint")
+    rng = np.random.default_rng(6)
+    t, _ = _mode4_tensors(tris, rng, sparse_form=True)
+    path = str(tmp_path / "m4.safetensors")
+    save_file({f"mlp.shared_expert.gate_proj.{k}": torch.from_numpy(np.ascontiguousarray(v)) for k, v in t.items()},
+              path)
+    loaded = ck.GroupedCheckpoint(path).load_compact3_linear("mlp.shared_expert.gate_proj", cuda)
+    rng2 = np.random.default_rng(6)
+    tb, _ = _mode4_tensors(tris, rng2, sparse_form=False)
+    direct = tris["qlinear"].Compact3Linear(128, 96).load_tensors(dict(
+        {k: tb[k] for k in tris["qlinear"].COMPACT3_MODULE_KEYS}, input_scale=tb["ns_vector_col"],
+        output_scale=tb["ns_vector_row"], bias=tb["bias"],
+        ns_c1={n: tb[f"ns_c1_quant.{n}"] for n in ("qweight", "qzeros", "scales", "g_idx")},
+        ns_c2={n: tb[f"ns_c2_quant.{n}"] for n in ("qweight", "qzeros", "scales", "g_idx")})).to(cuda)
+    x = torch.from_numpy((np.random.default_rng(8).standard_normal((5, 128)) * 1.5).astype(np.float16)).to(cuda)
+    y = loaded(x)
+    assert torch.equal(y, direct(x))
+    c2 = oracle_mod.packed4_dequant(tb["ns_c2_quant.qweight"], tb["ns_c2_quant.qzeros"], tb["ns_c2_quant.scales"],
+                                    tb["ns_c2_quant.g_idx"], 16, 128)
+    c1 = oracle_mod.packed4_dequant(tb["ns_c1_quant.qweight"], tb["ns_c1_quant.qzeros"], tb["ns_c1_quant.scales"],
+                                    tb["ns_c1_quant.g_idx"], 96, 16)
+    module = {k: tb[k] for k in tris["qlinear"].COMPACT3_MODULE_KEYS}
+    want = oracle_mod.compact3_linear(x.cpu().numpy(), module, tb["ns_vector_col"], tb["ns_vector_row"], tb["bias"],
+                                      c2, c1)
+    assert_close(y.cpu().numpy(), want, "compact3 linear from checkpoint")
