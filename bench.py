@@ -76,7 +76,7 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
-                          "(multi-GPU sharding is design-only, see DESIGN.md)"}))
+                          "(sharding across GPUs is designed, not built)"}))
         sys.exit(2)
     import numpy as np
     import torch
