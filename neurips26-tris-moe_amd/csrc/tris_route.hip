@@ -155,14 +155,15 @@ constexpr int kRouteMaxTopK = 16;
 // Softmax of one token's logits (fp32, max-subtracted, summed in expert order) and its top-k by
 // probability with ties to the lower expert id (a stable descending sort, as the oracle's argsort):
 // bp[j] / be[j] for j < top_k, most probable first.
+template <int K>
 __device__ __forceinline__ void route_token_topk(const float* __restrict__ row, int num_experts, int top_k,
-                                                 float bp[kRouteMaxTopK], int be[kRouteMaxTopK]) {
+                                                 float bp[K], int be[K]) {
   float m = row[0];
   for (int e = 1; e < num_experts; ++e) m = fmaxf(m, row[e]);
   float sum = 0.0f;
   for (int e = 0; e < num_experts; ++e) sum += expf(row[e] - m);
 #pragma unroll
-  for (int j = 0; j < kRouteMaxTopK; ++j) {
+  for (int j = 0; j < K; ++j) {
     bp[j] = -1.0f;
     be[j] = -1;
   }
@@ -174,7 +175,7 @@ __device__ __forceinline__ void route_token_topk(const float* __restrict__ row, 
       int ce = e;
       bool shifting = false;  // once placed, every later entry moves down one
 #pragma unroll
-      for (int j = 0; j < kRouteMaxTopK; ++j) {
+      for (int j = 0; j < K; ++j) {
         if (j < top_k && (shifting || be[j] < 0 || cp > bp[j])) {
           const float tp = bp[j];
           const int te = be[j];
@@ -190,10 +191,11 @@ __device__ __forceinline__ void route_token_topk(const float* __restrict__ row, 
 }
 
 // The routing weight of pick j: renormalised over the k picks (summed in pick order) or not.
-__device__ __forceinline__ float route_pick_weight(const float bp[kRouteMaxTopK], int top_k, int renormalize, int j) {
+template <int K>
+__device__ __forceinline__ float route_pick_weight(const float bp[K], int top_k, int renormalize, int j) {
   float denom = 0.0f;
 #pragma unroll
-  for (int q = 0; q < kRouteMaxTopK; ++q) {
+  for (int q = 0; q < K; ++q) {
     if (q < top_k) denom += bp[q];
   }
   return renormalize ? bp[j] / denom : bp[j];
@@ -206,6 +208,7 @@ constexpr int kRouteWaveMax = 64;  // routed rows and experts of the one-wavefro
 // num_experts counts its expert by ballots, and prefix sums over lanes give the compacted active
 // experts and their segment / problem offsets; entry i's place in its segment is the number of
 // earlier entries of its expert.  The same outputs as route_topk_small_kernel.
+template <int K>
 __global__ __launch_bounds__(kWave) void route_topk_wave_kernel(
     const float* __restrict__ logits, int tokens, int num_experts, int top_k, int renormalize, int m_tile,
     uint16_t* __restrict__ weights16, float* __restrict__ weights32, int64_t* __restrict__ selected,
@@ -232,19 +235,19 @@ __global__ __launch_bounds__(kWave) void route_topk_wave_kernel(
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
-  float bp[kRouteMaxTopK];
-  int be[kRouteMaxTopK];
+  float bp[K];
+  int be[K];
 #pragma unroll
-  for (int j = 0; j < kRouteMaxTopK; ++j) {
+  for (int j = 0; j < K; ++j) {
     bp[j] = -1.0f;
     be[j] = -1;
   }
   if (lane < tokens) {
-    route_token_topk(lg + lane * num_experts, num_experts, top_k, bp, be);
+    route_token_topk<K>(lg + lane * num_experts, num_experts, top_k, bp, be);
 #pragma unroll
-    for (int j = 0; j < kRouteMaxTopK; ++j) {
+    for (int j = 0; j < K; ++j) {
       if (j < top_k) {
-        const float w = route_pick_weight(bp, top_k, renormalize, j);
+        const float w = route_pick_weight<K>(bp, top_k, renormalize, j);
         const int i = lane * top_k + j;
         if (selected != nullptr) selected[i] = be[j];
         weights16[i] = f2h_bits(w);
@@ -258,7 +261,7 @@ __global__ __launch_bounds__(kWave) void route_topk_wave_kernel(
     const int t = lane / top_k;
     const int jj = lane - t * top_k;
 #pragma unroll
-    for (int j = 0; j < kRouteMaxTopK; ++j) {
+    for (int j = 0; j < K; ++j) {
       const int v = __shfl(be[j], t < kWave ? t : 0);
       if (j < top_k && j == jj && lane < total) sel_i = v;
     }
@@ -340,11 +343,11 @@ __global__ __launch_bounds__(kRouteThreads) void route_topk_small_kernel(
   for (int t = tid; t < tokens; t += kRouteThreads) {
     float bp[kRouteMaxTopK];
     int be[kRouteMaxTopK];
-    route_token_topk(logits + static_cast<int64_t>(t) * num_experts, num_experts, top_k, bp, be);
+    route_token_topk<kRouteMaxTopK>(logits + static_cast<int64_t>(t) * num_experts, num_experts, top_k, bp, be);
 #pragma unroll
     for (int j = 0; j < kRouteMaxTopK; ++j) {
       if (j < top_k) {
-        const float w = route_pick_weight(bp, top_k, renormalize, j);
+        const float w = route_pick_weight<kRouteMaxTopK>(bp, top_k, renormalize, j);
         const int i = t * top_k + j;
         sel[i] = static_cast<int16_t>(be[j]);
         if (selected != nullptr) selected[i] = be[j];
@@ -481,8 +484,10 @@ extern "C" int tris_route_topk_grouped(const float* router_logits, int32_t num_t
                                    grouped_slots && grouped_expert_ids),
                "%s: null pointer", who);
   if (static_cast<int64_t>(num_tokens) * top_k <= kRouteWaveMax && num_experts <= kRouteWaveMax) {
-    hipLaunchKernelGGL(route_topk_wave_kernel, dim3(1), dim3(kWave), 0, static_cast<hipStream_t>(stream),
-                       router_logits, num_tokens, num_experts, top_k, renormalize, m_tile, routing_weights_f16,
+    // the pick lists are sized to top_k's bucket: shorter unrolled insertion chains and less code to fetch
+    auto* kernel = top_k <= 2 ? route_topk_wave_kernel<2> : top_k <= 8 ? route_topk_wave_kernel<8>
+                                                                        : route_topk_wave_kernel<kRouteMaxTopK>;
+    hipLaunchKernelGGL(kernel, dim3(1), dim3(kWave), 0, static_cast<hipStream_t>(stream), router_logits, num_tokens, num_experts, top_k, renormalize, m_tile, routing_weights_f16,
                        routing_weights_f32, selected_experts, perm, grouped_token_indices, grouped_slots,
                        grouped_expert_ids, expert_ids, segment_offsets, problem_offsets, counts, inverse_perm);
     return check_launch(who);
