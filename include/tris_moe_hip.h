@@ -102,7 +102,11 @@ int64_t tris_gr_encode(const int32_t* packed, int32_t packed_rows, int32_t outfe
  *   problem_offsets    int32 [num_experts+1] prefix of ceil(len/m_tile), rest = total
  *   counts             int32 [2] = {num_active, total_problem_tiles}
  *   inverse_perm       int32 [R] or NULL: grouped row of flat slot t*top_k + s
- * Expert ids outside [0, num_experts) are an error reported through counts[0] = -1.
+ * Expert ids outside [0, num_experts) are an error reported through counts[0] = -1 (no host
+ * synchronisation); the route stays memory-safe for callers that do not check it: the valid entries keep
+ * their segments, and the invalid ones fill grouped rows [segment_offsets[num_experts], R) in flat order
+ * with their own token index and slot, grouped_expert_ids -1 and inverse_perm -1 (no segment covers them,
+ * and tris_moe_combine skips them).
  */
 int tris_build_grouped_route(const int64_t* selected_experts, int32_t num_tokens, int32_t top_k,
                              int32_t num_experts, int32_t m_tile, int64_t* perm,
@@ -262,13 +266,15 @@ int tris_backbone_linear(const uint16_t* x, int32_t tokens, int32_t in_features,
 
 /* Two backbone projections of the same gathered rows in one launch (no
  * reference counterpart: batches the gate and up compute_shared_hidden calls
- * of a grouped SwiGLU layer, modeling_mixtral.py:467-476, without in_scale).
- * out_a = x[row_index] . sv_a^T, out_b = x[row_index] . sv_b^T, as two calls
- * of tris_backbone_linear would give.  workspace: see
- * tris_backbone_pair_workspace_bytes. */
+ * of a grouped SwiGLU layer, modeling_mixtral.py:467-476, each with its own
+ * ns_mode == 1 input scale, qlinear_cuda.py:4477-4480).
+ * out_a = fp16(x[row_index] * in_scale_a) . sv_a^T, out_b likewise with
+ * in_scale_b (either scale may be NULL), as two calls of tris_backbone_linear
+ * would give.  workspace: see tris_backbone_pair_workspace_bytes. */
 int tris_backbone_linear_pair(const uint16_t* x, int32_t tokens, int32_t in_features, const int64_t* row_index,
-                              const uint16_t* sv_a, const uint16_t* sv_b, int32_t rank, uint16_t* out_a,
-                              uint16_t* out_b, void* workspace, int64_t workspace_bytes, void* stream);
+                              const uint16_t* sv_a, const uint16_t* sv_b, int32_t rank, const uint16_t* in_scale_a,
+                              const uint16_t* in_scale_b, uint16_t* out_a, uint16_t* out_b, void* workspace,
+                              int64_t workspace_bytes, void* stream);
 
 /* Workspace sizes for tris_backbone_linear / _pair (no reference counterpart:
  * cuBLAS owns its workspace). */
@@ -308,12 +314,12 @@ int tris_packed4_backbone_linear(const uint16_t* x, int32_t tokens, const int64_
                                  const tris_packed4_matrix* w, const uint16_t* in_scale, uint16_t* out,
                                  void* workspace, int64_t workspace_bytes, void* stream);
 
-/* Gate and up packed backbones of the same rows in one launch (no reference counterpart; see
- * tris_backbone_linear_pair).  Workspace: tris_backbone_pair_workspace_bytes. */
+/* Gate and up packed backbones of the same rows in one launch, each with its own input scale or NULL
+ * (no reference counterpart; see tris_backbone_linear_pair).  Workspace: tris_backbone_pair_workspace_bytes. */
 int tris_packed4_backbone_linear_pair(const uint16_t* x, int32_t tokens, const int64_t* row_index,
                                       const tris_packed4_matrix* wa, const tris_packed4_matrix* wb,
-                                      uint16_t* out_a, uint16_t* out_b, void* workspace,
-                                      int64_t workspace_bytes, void* stream);
+                                      const uint16_t* in_scale_a, const uint16_t* in_scale_b, uint16_t* out_a,
+                                      uint16_t* out_b, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Matrix-mode null-space compensation payload of one projection (build_grouped_ns_compensation_payload,
@@ -437,7 +443,8 @@ int tris_dense_linear_f32(const uint16_t* input_f16, const float* input_f32, int
  * out[t, :] = bf16( sum_s fp16(expert_out[inverse_perm[t*top_k+s], :] * weights[t, s])
  *                   (+ shared[t, :]) ), summed in fp32 and rounded once.
  * expert_out fp16 [R, hidden] (16-byte aligned when hidden % 8 == 0);
- * inverse_perm int32 [tokens*top_k]; weights fp16 [tokens, top_k];
+ * inverse_perm int32 [tokens*top_k] (entries < 0 are skipped: picks the route left out); weights fp16
+ * [tokens, top_k];
  * shared fp16 [tokens, hidden] or NULL; out bf16 [tokens, hidden].
  */
 int tris_moe_combine(const uint16_t* expert_out, const int32_t* inverse_perm, const uint16_t* weights,

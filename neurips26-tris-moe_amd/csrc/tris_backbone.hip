@@ -41,12 +41,12 @@ constexpr int kBbMaxSlices = 32;
 struct BackboneProj {
   const uint16_t* sv;
   uint16_t* out;
+  const uint16_t* in_scale;  // fp16 [in] per-column input scale of this projection, or null
 };
 
 struct BackboneArgs {
   const uint16_t* x;
   const int64_t* row_index;
-  const uint16_t* in_scale;
   BackboneProj proj[2];
   float* partials;  // [nproj][slices][tokens][rank] when slices > 1
   int tokens;
@@ -104,7 +104,8 @@ __global__ __launch_bounds__(kBbThreads) void backbone_kernel(BackboneArgs a) {
   const int r = r0 + i;
   const bool r_valid = r < a.rank;
   const uint16_t* ssrc = pj.sv + static_cast<int64_t>(r_valid ? r : 0) * a.in_features;
-  const bool scaled = a.in_scale != nullptr;
+  const uint16_t* in_scale = pj.in_scale;
+  const bool scaled = in_scale != nullptr;
   const bool vec = (a.in_features % 8) == 0;
 
   f32x4 acc[TT];
@@ -130,7 +131,7 @@ __global__ __launch_bounds__(kBbThreads) void backbone_kernel(BackboneArgs a) {
 #pragma unroll
         for (int u = 0; u < B; ++u) {
           const int k = k0 + u * kBbKStep + kg * 8;
-          const f16x8 sc = load8_vec(a.in_scale, k, k < kend);
+          const f16x8 sc = load8_vec(in_scale, k, k < kend);
 #pragma unroll
           for (int j = 0; j < TT; ++j) av[j][u] = av[j][u] * sc;  // fp16 products, as x * ns_col
         }
@@ -146,7 +147,7 @@ __global__ __launch_bounds__(kBbThreads) void backbone_kernel(BackboneArgs a) {
     for (int k0 = kbeg; k0 < kend; k0 += kBbKStep) {
       const int k = k0 + kg * 8;
       const f16x8 bv = load8_tail(ssrc, k, kend, r_valid);
-      const f16x8 sc = scaled ? load8_tail(a.in_scale, k, kend, true) : f16x8{1, 1, 1, 1, 1, 1, 1, 1};
+      const f16x8 sc = scaled ? load8_tail(in_scale, k, kend, true) : f16x8{1, 1, 1, 1, 1, 1, 1, 1};
 #pragma unroll
       for (int j = 0; j < TT; ++j) {
         f16x8 av = load8_tail(xsrc[j], k, kend, t_valid[j]);
@@ -233,8 +234,9 @@ int64_t backbone_workspace_bytes(int tokens, int in_features, int rank, int npro
 }
 
 int launch_backbone(const uint16_t* x, int tokens, int in_features, const int64_t* row_index, const uint16_t* sv_a,
-                    const uint16_t* sv_b, int rank, const uint16_t* in_scale, uint16_t* out_a, uint16_t* out_b,
-                    void* workspace, int64_t workspace_bytes, void* stream, const char* who) {
+                    const uint16_t* sv_b, int rank, const uint16_t* in_scale_a, const uint16_t* in_scale_b,
+                    uint16_t* out_a, uint16_t* out_b, void* workspace, int64_t workspace_bytes, void* stream,
+                    const char* who) {
   TRIS_REQUIRE(tokens >= 0 && in_features >= 0 && rank >= 0, "%s: negative shape", who);
   if (tokens == 0 || rank == 0) return TRIS_OK;
   TRIS_REQUIRE(out_a != nullptr && (sv_b == nullptr || out_b != nullptr), "%s: null output", who);
@@ -251,7 +253,8 @@ int launch_backbone(const uint16_t* x, int tokens, int in_features, const int64_
   TRIS_REQUIRE(x && sv_a, "%s: null input", who);
   TRIS_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(sv_a) % 16 == 0 &&
                    (sv_b == nullptr || reinterpret_cast<uintptr_t>(sv_b) % 16 == 0) &&
-                   (in_scale == nullptr || reinterpret_cast<uintptr_t>(in_scale) % 16 == 0),
+                   reinterpret_cast<uintptr_t>(in_scale_a) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(in_scale_b) % 16 == 0,
                "%s: x, sv and in_scale must be 16-byte aligned", who);
   const int slices = backbone_slices(tokens, in_features, rank);
   const int64_t need = backbone_workspace_bytes(tokens, in_features, rank, nproj);
@@ -265,9 +268,8 @@ int launch_backbone(const uint16_t* x, int tokens, int in_features, const int64_
   BackboneArgs args{};
   args.x = x;
   args.row_index = row_index;
-  args.in_scale = in_scale;
-  args.proj[0] = BackboneProj{sv_a, out_a};
-  args.proj[1] = BackboneProj{sv_b, out_b};
+  args.proj[0] = BackboneProj{sv_a, out_a, in_scale_a};
+  args.proj[1] = BackboneProj{sv_b, out_b, in_scale_b};
   args.partials = static_cast<float*>(workspace);
   args.tokens = tokens;
   args.in_features = in_features;
@@ -353,7 +355,8 @@ __global__ __launch_bounds__(kBbThreads) void packed4_backbone_kernel(Packed4Arg
   const int r = r0 + i;
   const bool r_valid = r < a.rank;
   const int rr = r_valid ? r : 0;
-  const bool scaled = a.in_scale != nullptr;
+  const uint16_t* in_scale = a.proj[q].in_scale;
+  const bool scaled = in_scale != nullptr;
   const bool vec = (a.in_features % 8) == 0;
   const uint32_t zshift = 4u * static_cast<uint32_t>(rr & 7);
 
@@ -392,7 +395,7 @@ __global__ __launch_bounds__(kBbThreads) void packed4_backbone_kernel(Packed4Arg
       if (scaled) {
 #pragma unroll
         for (int u = 0; u < kBbBatch; ++u) {
-          av[u] = av[u] * load8_vec(a.in_scale, k0 + u * kBbKStep + kg * 8, true);  // fp16 products, as x * ns_col
+          av[u] = av[u] * load8_vec(in_scale, k0 + u * kBbKStep + kg * 8, true);  // fp16 products, as x * ns_col
         }
       }
 #pragma unroll
@@ -404,10 +407,10 @@ __global__ __launch_bounds__(kBbThreads) void packed4_backbone_kernel(Packed4Arg
     f16x8 av;
     if (vec && k + 8 <= kend) {
       av = load8_vec(xsrc, k, t_valid);
-      if (scaled) av = av * load8_vec(a.in_scale, k, true);
+      if (scaled) av = av * load8_vec(in_scale, k, true);
     } else {
       av = load8_tail(xsrc, k, kend, t_valid);  // columns past the end read 0, so their weights do not count
-      if (scaled) av = av * load8_tail(a.in_scale, k, kend, true);
+      if (scaled) av = av * load8_tail(in_scale, k, kend, true);
     }
     const f16x8 bv = k < kend ? weights(k) : f16x8{};
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
@@ -487,8 +490,9 @@ static int check_packed4(const tris_packed4_matrix* w, bool fused, const char* w
 }
 
 int launch_packed4_backbone(const uint16_t* x, int tokens, const int64_t* row_index, const tris_packed4_matrix* wa,
-                            const tris_packed4_matrix* wb, const uint16_t* in_scale, uint16_t* out_a, uint16_t* out_b,
-                            void* workspace, int64_t workspace_bytes, void* stream, const char* who) {
+                            const tris_packed4_matrix* wb, const uint16_t* in_scale_a, const uint16_t* in_scale_b,
+                            uint16_t* out_a, uint16_t* out_b, void* workspace, int64_t workspace_bytes, void* stream,
+                            const char* who) {
   int rc = check_packed4(wa, true, who);
   if (rc) return rc;
   if (wb) {
@@ -512,8 +516,8 @@ int launch_packed4_backbone(const uint16_t* x, int tokens, const int64_t* row_in
     return check_launch("fill_zero_u16_kernel");
   }
   TRIS_REQUIRE(x != nullptr, "%s: null input", who);
-  TRIS_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
-                   (in_scale == nullptr || reinterpret_cast<uintptr_t>(in_scale) % 16 == 0),
+  TRIS_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(in_scale_a) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(in_scale_b) % 16 == 0,
                "%s: x and in_scale must be 16-byte aligned", who);
   const int slices = backbone_slices(tokens, in_features, rank);
   const int64_t need = backbone_workspace_bytes(tokens, in_features, rank, nproj);
@@ -527,9 +531,8 @@ int launch_packed4_backbone(const uint16_t* x, int tokens, const int64_t* row_in
   BackboneArgs& args = pa.base;
   args.x = x;
   args.row_index = row_index;
-  args.in_scale = in_scale;
-  args.proj[0] = BackboneProj{nullptr, out_a};
-  args.proj[1] = BackboneProj{nullptr, out_b};
+  args.proj[0] = BackboneProj{nullptr, out_a, in_scale_a};
+  args.proj[1] = BackboneProj{nullptr, out_b, in_scale_b};
   args.partials = static_cast<float*>(workspace);
   args.tokens = tokens;
   args.in_features = in_features;
@@ -570,17 +573,18 @@ extern "C" int64_t tris_backbone_pair_workspace_bytes(int32_t tokens, int32_t in
 extern "C" int tris_backbone_linear(const uint16_t* x, int32_t tokens, int32_t in_features, const int64_t* row_index,
                                     const uint16_t* sv, int32_t rank, const uint16_t* in_scale, uint16_t* out,
                                     void* workspace, int64_t workspace_bytes, void* stream) {
-  return launch_backbone(x, tokens, in_features, row_index, sv, nullptr, rank, in_scale, out, nullptr, workspace,
-                         workspace_bytes, stream, "tris_backbone_linear");
+  return launch_backbone(x, tokens, in_features, row_index, sv, nullptr, rank, in_scale, nullptr, out, nullptr,
+                         workspace, workspace_bytes, stream, "tris_backbone_linear");
 }
 
 extern "C" int tris_backbone_linear_pair(const uint16_t* x, int32_t tokens, int32_t in_features,
                                          const int64_t* row_index, const uint16_t* sv_a, const uint16_t* sv_b,
-                                         int32_t rank, uint16_t* out_a, uint16_t* out_b, void* workspace,
-                                         int64_t workspace_bytes, void* stream) {
+                                         int32_t rank, const uint16_t* in_scale_a, const uint16_t* in_scale_b,
+                                         uint16_t* out_a, uint16_t* out_b, void* workspace, int64_t workspace_bytes,
+                                         void* stream) {
   TRIS_REQUIRE(sv_b != nullptr, "tris_backbone_linear_pair: null sv_b");
-  return launch_backbone(x, tokens, in_features, row_index, sv_a, sv_b, rank, nullptr, out_a, out_b, workspace,
-                         workspace_bytes, stream, "tris_backbone_linear_pair");
+  return launch_backbone(x, tokens, in_features, row_index, sv_a, sv_b, rank, in_scale_a, in_scale_b, out_a, out_b,
+                         workspace, workspace_bytes, stream, "tris_backbone_linear_pair");
 }
 
 extern "C" int tris_packed4_dequant(const tris_packed4_matrix* w, uint16_t* out, void* stream) {
@@ -597,15 +601,16 @@ extern "C" int tris_packed4_dequant(const tris_packed4_matrix* w, uint16_t* out,
 extern "C" int tris_packed4_backbone_linear(const uint16_t* x, int32_t tokens, const int64_t* row_index,
                                             const tris_packed4_matrix* w, const uint16_t* in_scale, uint16_t* out,
                                             void* workspace, int64_t workspace_bytes, void* stream) {
-  return launch_packed4_backbone(x, tokens, row_index, w, nullptr, in_scale, out, nullptr, workspace, workspace_bytes,
-                                 stream, "tris_packed4_backbone_linear");
+  return launch_packed4_backbone(x, tokens, row_index, w, nullptr, in_scale, nullptr, out, nullptr, workspace,
+                                 workspace_bytes, stream, "tris_packed4_backbone_linear");
 }
 
 extern "C" int tris_packed4_backbone_linear_pair(const uint16_t* x, int32_t tokens, const int64_t* row_index,
                                                  const tris_packed4_matrix* wa, const tris_packed4_matrix* wb,
+                                                 const uint16_t* in_scale_a, const uint16_t* in_scale_b,
                                                  uint16_t* out_a, uint16_t* out_b, void* workspace,
                                                  int64_t workspace_bytes, void* stream) {
   TRIS_REQUIRE(wb != nullptr, "tris_packed4_backbone_linear_pair: null second matrix");
-  return launch_packed4_backbone(x, tokens, row_index, wa, wb, nullptr, out_a, out_b, workspace, workspace_bytes,
-                                 stream, "tris_packed4_backbone_linear_pair");
+  return launch_packed4_backbone(x, tokens, row_index, wa, wb, in_scale_a, in_scale_b, out_a, out_b, workspace,
+                                 workspace_bytes, stream, "tris_packed4_backbone_linear_pair");
 }

@@ -30,17 +30,18 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
                                                           const int32_t* __restrict__ inverse_perm,
                                                           const uint16_t* __restrict__ weights,
                                                           const uint16_t* __restrict__ shared, int tokens, int top_k,
-                                                          int hidden, uint16_t* __restrict__ out) {
-  const int t = blockIdx.y;
-  const int h0 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
+                                                          int hidden, int hblocks, uint16_t* __restrict__ out) {
+  const int t = static_cast<int>(blockIdx.x) / hblocks;
+  const int h0 = ((static_cast<int>(blockIdx.x) - t * hblocks) * static_cast<int>(blockDim.x) + threadIdx.x) * 8;
   if (t >= tokens || h0 >= hidden) return;
   const bool vec = (hidden % 8) == 0;
   float acc[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u) acc[u] = 0.0f;
   for (int s = 0; s < top_k; ++s) {
-    const int row = inverse_perm[t * top_k + s];
-    const __half w = __ushort_as_half(weights[t * top_k + s]);
+    const int row = inverse_perm[static_cast<int64_t>(t) * top_k + s];
+    if (row < 0) continue;  // a pick the route left out (expert id outside [0, num_experts))
+    const __half w = __ushort_as_half(weights[static_cast<int64_t>(t) * top_k + s]);
     const uint16_t* src = expert_out + static_cast<int64_t>(row) * hidden + h0;
     uint16_t v[8];
     if (vec) {
@@ -171,14 +172,16 @@ static int combine_launch(const char* who, const uint16_t* expert_out, const uin
   TRIS_REQUIRE(tokens >= 0 && top_k >= 0 && hidden >= 0, "%s: negative shape", who);
   if (tokens == 0 || hidden == 0) return TRIS_OK;
   TRIS_REQUIRE(out != nullptr && (top_k == 0 || (expert_out && inverse_perm && weights)), "%s: null pointer", who);
-  TRIS_REQUIRE(tokens <= 65535, "%s: too many tokens per launch (%d)", who, tokens);
   TRIS_REQUIRE(hidden % 8 != 0 || (reinterpret_cast<uintptr_t>(expert_out) % 16 == 0 &&
                                    reinterpret_cast<uintptr_t>(expert_comp) % 16 == 0),
                "%s: expert_out and expert_comp must be 16-byte aligned", who);
   const int threads = 256;
-  dim3 grid(ceil_div(ceil_div(hidden, 8), threads), tokens);
-  hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(threads), 0, static_cast<hipStream_t>(stream), expert_out,
-                     expert_comp, inverse_perm, weights, shared, tokens, top_k, hidden, out);
+  const int hblocks = ceil_div(ceil_div(hidden, 8), threads);
+  const int64_t blocks = static_cast<int64_t>(hblocks) * tokens;  // token-major, one dimension (no 65535 limit)
+  TRIS_REQUIRE(blocks <= 2147483647LL, "%s: too many tokens (%d)", who, tokens);
+  hipLaunchKernelGGL(moe_combine_kernel, dim3(static_cast<unsigned>(blocks)), dim3(threads), 0,
+                     static_cast<hipStream_t>(stream), expert_out, expert_comp, inverse_perm, weights, shared, tokens,
+                     top_k, hidden, hblocks, out);
   return check_launch(who);
 }
 

@@ -92,12 +92,10 @@ __global__ __launch_bounds__(kRouteThreads) void route_histogram_kernel(
     problem_offsets[j] = tiles_total;
   }
   if (tid == 0) {
+    // An id outside [0, num_experts) is reported here; the valid entries keep their segments and the
+    // scatter's last workgroup places the invalid ones after them (see route_scatter_kernel).
     counts[0] = bad ? -1 : num_active;
-    counts[1] = bad ? 0 : tiles_total;
-  }
-  if (bad) {
-    // Leave no active expert so the scatter writes nothing.
-    for (int j = tid; j < num_experts; j += kRouteThreads) expert_ids[j] = -1;
+    counts[1] = tiles_total;
   }
 }
 
@@ -107,24 +105,35 @@ constexpr int kScatterWaves = kScatterThreads / kWave;
 // One workgroup per segment slot: the flattened expert ids are scanned in chunks of kScatterThreads, each
 // chunk's hits of this expert placed in flat order (ballot within a wave, wave totals through LDS), so a
 // segment's entries keep the order of the flat index as in a stable sort.
+// Workgroup num_experts places the entries whose id lies outside [0, num_experts) (counts[0] == -1) after
+// every segment, in flat order, with their own token index and slot, grouped expert id -1 and inverse_perm
+// -1: every grouped row then holds a valid token index (the backbone's row gather stays in bounds), no
+// segment covers those rows, and the combine skips them.
 __global__ __launch_bounds__(kScatterThreads) void route_scatter_kernel(
     const int64_t* __restrict__ selected, int total, int top_k, int num_experts, const int32_t* __restrict__ expert_ids,
-    const int32_t* __restrict__ segment_offsets, int64_t* __restrict__ perm, int64_t* __restrict__ token_idx,
-    int64_t* __restrict__ slots, int32_t* __restrict__ grouped_expert_ids, int32_t* __restrict__ inverse_perm) {
+    const int32_t* __restrict__ segment_offsets, const int32_t* __restrict__ counts, int64_t* __restrict__ perm,
+    int64_t* __restrict__ token_idx, int64_t* __restrict__ slots, int32_t* __restrict__ grouped_expert_ids,
+    int32_t* __restrict__ inverse_perm) {
   __shared__ int wave_hits[2][kScatterWaves];
   const int seg = blockIdx.x;
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
   const int lane = tid % kWave;
-  if (seg >= num_experts) return;
-  const int e = expert_ids[seg];
-  if (e < 0) return;  // the whole workgroup: an inactive slot
-  int pos = segment_offsets[seg];
+  if (seg > num_experts) return;
+  const bool invalid_slot = seg == num_experts;
+  if (invalid_slot && counts[0] >= 0) return;  // every id was valid
+  const int e = invalid_slot ? -1 : expert_ids[seg];
+  if (!invalid_slot && e < 0) return;  // the whole workgroup: an inactive slot
+  int pos = segment_offsets[seg];      // [num_experts]: the end of the valid rows
   const uint64_t lower = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   int buf = 0;
   for (int c = 0; c < total; c += kScatterThreads) {
     const int i = c + tid;
-    const bool hit = i < total && selected[i] == e;
+    bool hit = false;
+    if (i < total) {
+      const int64_t si = selected[i];
+      hit = invalid_slot ? (si < 0 || si >= num_experts) : si == e;
+    }
     const uint64_t mask = __ballot(hit);
     if (lane == 0) wave_hits[buf][wave] = __popcll(mask);
     __syncthreads();  // (two buffers: the next chunk's writes do not race this chunk's reads)
@@ -141,7 +150,7 @@ __global__ __launch_bounds__(kScatterThreads) void route_scatter_kernel(
       token_idx[dst] = i / top_k;
       slots[dst] = i % top_k;
       grouped_expert_ids[dst] = e;
-      if (inverse_perm != nullptr) inverse_perm[i] = dst;
+      if (inverse_perm != nullptr) inverse_perm[i] = invalid_slot ? -1 : dst;
     }
     pos += chunk;
     buf ^= 1;
@@ -455,10 +464,10 @@ extern "C" int tris_build_grouped_route(const int64_t* selected_experts, int32_t
                      counts);
   int rc = check_launch("route_histogram_kernel");
   if (rc) return rc;
-  if (total == 0 || num_experts == 0) return TRIS_OK;
-  hipLaunchKernelGGL(route_scatter_kernel, dim3(num_experts), dim3(kScatterThreads), 0, s,
-                     selected_experts, static_cast<int>(total), top_k, num_experts, expert_ids, segment_offsets, perm,
-                     grouped_token_indices, grouped_slots, grouped_expert_ids, inverse_perm);
+  if (total == 0) return TRIS_OK;
+  hipLaunchKernelGGL(route_scatter_kernel, dim3(num_experts + 1), dim3(kScatterThreads), 0, s,
+                     selected_experts, static_cast<int>(total), top_k, num_experts, expert_ids, segment_offsets, counts,
+                     perm, grouped_token_indices, grouped_slots, grouped_expert_ids, inverse_perm);
   return check_launch("route_scatter_kernel");
 }
 

@@ -131,7 +131,7 @@ SIGNATURES = {
     "tris_compact3_dequant": (ctypes.c_int, [_PAY, _P, _I32, _P, _P]),
     "tris_gr_decode_dense": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _P, _I32, _I32, _I32, _P, _P]),
     "tris_backbone_linear": (ctypes.c_int, [_P, _I32, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P]),
-    "tris_backbone_linear_pair": (ctypes.c_int, [_P, _I32, _I32, _P, _P, _P, _I32, _P, _P, _P, _I64, _P]),
+    "tris_backbone_linear_pair": (ctypes.c_int, [_P, _I32, _I32, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _I64, _P]),
     "tris_backbone_pair_workspace_bytes": (_I64, [_I32, _I32, _I32]),
     "tris_backbone_workspace_bytes": (_I64, [_I32, _I32, _I32]),
     "tris_moe_combine": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _P, _P]),
@@ -140,7 +140,7 @@ SIGNATURES = {
     "tris_swiglu_mul_compensated": (ctypes.c_int, [_P, _P, _P, _P, _I64, _P, _P]),
     "tris_packed4_dequant": (ctypes.c_int, [_P4, _P, _P]),
     "tris_packed4_backbone_linear": (ctypes.c_int, [_P, _I32, _P, _P4, _P, _P, _P, _I64, _P]),
-    "tris_packed4_backbone_linear_pair": (ctypes.c_int, [_P, _I32, _P, _P4, _P4, _P, _P, _P, _I64, _P]),
+    "tris_packed4_backbone_linear_pair": (ctypes.c_int, [_P, _I32, _P, _P4, _P4, _P, _P, _P, _P, _P, _I64, _P]),
     "tris_grouped_ns_compensation_forward": (ctypes.c_int, [_P, _I32, _P, _P, _I32, _PNS, _P, _I64, _P, _I32, _P]),
     "tris_grouped_ns_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32]),
     "tris_grouped_ns_compensation_pair_forward": (ctypes.c_int, [_P, _I32, _P, _I32, _P, _P, _I32, _PNS, _PNS, _P, _I64,

@@ -43,6 +43,9 @@ SCALAR_NAMES = frozenset({"is_compact3", "compact3_use_block_gr", "has_output_sc
                           "infeatures", "outfeatures", "group_size"})
 BOOL_NAMES = frozenset({"is_compact3", "compact3_use_block_gr", "has_output_scale", "has_bias"})
 PROJ_MODULE = {"gate": "gate_proj", "up": "up_proj", "down": "down_proj"}
+# Expert module of each projection under a MoE block's ``experts.{e}`` (grouped_payload_sidecar.py:467-495):
+# Mixtral's w1 / w3 / w2, else gate_proj / up_proj / down_proj.
+EXPERT_MODULE = {"mixtral": {"gate": "w1", "up": "w3", "down": "w2"}, "other": PROJ_MODULE}
 PACKED4_NAMES = ("qweight", "qzeros", "scales", "g_idx", "rows", "cols")
 MARKER = ".grouped_payload."
 
@@ -69,6 +72,12 @@ def split_payload_tensor_name(name: str):
 def moe_layer_prefix(layer_idx: int, family: str = "mixtral") -> str:
     """The MoE block of decoder layer i (grouped_payload_sidecar.py:54-80)."""
     return f"model.layers.{layer_idx}.block_sparse_moe" if family == "mixtral" else f"model.layers.{layer_idx}.mlp"
+
+
+def expert_module_prefix(layer_prefix: str, expert: int, proj: str) -> str:
+    """The state-dict prefix of one expert's projection module under a MoE block."""
+    family = "mixtral" if layer_prefix.endswith("block_sparse_moe") else "other"
+    return f"{layer_prefix}.experts.{expert}.{EXPERT_MODULE[family][proj]}"
 
 
 def shared_bank_prefix(layer_idx: int, proj: str) -> str:
@@ -124,14 +133,21 @@ def backbone_tensors(layer_idx: int, proj: str, backbone) -> dict:
 
 
 def save_grouped_checkpoint(path: str, layers: list, family: str = "mixtral", backbones: list | None = None,
-                            metadata: dict | None = None) -> str:
+                            metadata: dict | None = None, input_scales: list | None = None) -> str:
     """Write decoder layers' grouped payloads (``layers[i] = {"gate": payload, "up": ..., "down": ...}``,
     host arrays) and optionally their shared backbones (``backbones[i] = {proj: SV or packed payload}``) in the
-    reference's key scheme, with the sidecar metadata (:542-557)."""
+    reference's key scheme, with the sidecar metadata (:542-557).  ``input_scales[i] = {proj: fp16 [in]}``
+    writes experts[0]'s ``mode`` (5), ``ns_mode`` (1) and ``expert_input_scale`` for those projections, the
+    per-expert state a deployment-only checkpoint keeps (grouped_payload_sidecar.py:38-46)."""
     from safetensors.torch import save_file
 
     tensors = {}
     for i, layer in enumerate(layers):
+        for proj, scale in ((input_scales[i] or {}) if input_scales is not None else {}).items():
+            prefix = expert_module_prefix(moe_layer_prefix(i, family), 0, proj)
+            tensors[f"{prefix}.mode"] = torch.tensor([5], dtype=torch.int32)
+            tensors[f"{prefix}.ns_mode"] = torch.tensor([1], dtype=torch.int32)
+            tensors[f"{prefix}.expert_input_scale"] = encode_payload_tensor(np.asarray(scale, dtype=np.float16))
         for key in GROUPED_PRECOMPUTED_KEYS:
             tensors.update(payload_tensors(moe_layer_prefix(i, family), key, layer[key]))
             if layer.get(f"{key}_ns") is not None:
@@ -437,10 +453,39 @@ class GroupedCheckpoint:
             extras.pop("ns_c2", None)
         return Compact3Linear(rank, n).load_tensors(dict(t, **extras)).to(device)
 
-    def load_backbones(self, layer_idx: int, device) -> dict:
+    def load_input_scales(self, layer_prefix: str, device) -> dict:
+        """``{proj}_in_scale`` for the projections whose experts[0] module has ``ns_mode == 1``: the fp16 [in]
+        vector compute_shared_hidden multiplies the backbone input by (``expert_input_scale`` for expert_compact3
+        modules, mode 5; ``ns_vector_col`` otherwise, qlinear_cuda.py:3918-3923, 4477-4480).  The grouped
+        forward projects every expert's input through experts[0] (modeling_mixtral.py:469-470, 497), so only
+        expert 0's scale is read.  Raises ValueError when ns_mode is 1 and the scale is missing."""
+        out = {}
+        for proj in GROUPED_PRECOMPUTED_KEYS:
+            prefix = expert_module_prefix(layer_prefix, 0, proj)
+            key = f"{prefix}.ns_mode"
+            if key not in self._keys or int(self._f.get_tensor(key).reshape(-1)[0]) != 1:
+                continue
+            mode_key = f"{prefix}.mode"
+            mode = int(self._f.get_tensor(mode_key).reshape(-1)[0]) if mode_key in self._keys else 5
+            name = f"{prefix}.expert_input_scale" if mode == 5 else f"{prefix}.ns_vector_col"
+            if name not in self._keys or self._f.get_tensor(name).numel() == 0:
+                raise ValueError(f"{self.path}: {prefix} has ns_mode 1 but no {name.rsplit('.', 1)[1]}")
+            out[f"{proj}_in_scale"] = self._f.get_tensor(name).to(device=device, dtype=torch.float16).contiguous()
+        return out
+
+    def load_backbones(self, layer_idx: int, device, layer_prefix: str | None = None) -> dict:
+        """The layer's shared backbones {gate, up, down}, plus ``{proj}_in_scale`` entries for the projections
+        that scale their input (``load_input_scales`` of ``layer_prefix``, by default the layer's Mixtral or
+        OLMoE block, whichever the checkpoint holds)."""
         from .qlinear import PackedQuantMatrix4bit
 
         out = {}
+        if layer_prefix is None:
+            cands = [moe_layer_prefix(layer_idx, f) for f in ("mixtral", "other")]
+            held = [c for c in cands if any(k.startswith(c + ".") for k in self._keys)]
+            layer_prefix = held[0] if held else None
+        if layer_prefix is not None:
+            out.update(self.load_input_scales(layer_prefix, device))
         for proj in GROUPED_PRECOMPUTED_KEYS:
             prefix = shared_bank_prefix(layer_idx, proj)
             quant = {n: f"{prefix}.shared_sv_quant.{n}" for n in PACKED4_NAMES}

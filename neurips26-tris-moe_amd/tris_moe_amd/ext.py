@@ -551,15 +551,20 @@ def backbone_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 BACKBONE_LIBRARY_MIN_ROWS = 256
 
 
-def _backbone_library(x, svs, in_scale, row_index):
-    if row_index is not None and x.size(0) < row_index.numel():
-        # more routed rows than tokens (top-k > 1): project each token once, then gather the projected rows
-        xs = x * in_scale if in_scale is not None else x
-        return [torch.nn.functional.linear(xs, sv).index_select(0, row_index) for sv in svs]
-    xs = x.index_select(0, row_index) if row_index is not None else x
-    if in_scale is not None:
-        xs = xs * in_scale  # fp16 products, as x * ns_col
-    return [torch.nn.functional.linear(xs, sv) for sv in svs]
+def _backbone_library(x, svs, in_scales, row_index):
+    """One library GEMM per projection; in_scales: one fp16 input scale (or None) per projection."""
+    outs = []
+    for sv, sc in zip(svs, in_scales):
+        if row_index is not None and x.size(0) < row_index.numel():
+            # more routed rows than tokens (top-k > 1): project each token once, then gather the projected rows
+            xs = x * sc if sc is not None else x
+            outs.append(torch.nn.functional.linear(xs, sv).index_select(0, row_index))
+            continue
+        xs = x.index_select(0, row_index) if row_index is not None else x
+        if sc is not None:
+            xs = xs * sc  # fp16 products, as x * ns_col
+        outs.append(torch.nn.functional.linear(xs, sv))
+    return outs
 
 
 def backbone_linear(x: torch.Tensor, sv: torch.Tensor, in_scale: torch.Tensor | None = None,
@@ -576,7 +581,7 @@ def backbone_linear(x: torch.Tensor, sv: torch.Tensor, in_scale: torch.Tensor | 
         _check_cuda("in_scale", in_scale, torch.float16, 1, x.device)
     rank, in_f = int(sv.size(0)), int(sv.size(1))
     if tokens >= BACKBONE_LIBRARY_MIN_ROWS:
-        return _backbone_library(x, (sv,), in_scale, row_index)[0]
+        return _backbone_library(x, (sv,), (in_scale,), row_index)[0]
     out = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
     lib = _lib.load()
     ws = backbone_workspace(x.device, int(lib.tris_backbone_workspace_bytes(tokens, in_f, rank)))
@@ -586,8 +591,10 @@ def backbone_linear(x: torch.Tensor, sv: torch.Tensor, in_scale: torch.Tensor | 
 
 
 def backbone_linear_pair(x: torch.Tensor, sv_a: torch.Tensor, sv_b: torch.Tensor,
-                         row_index: torch.Tensor | None = None):
-    """(x[row_index] @ sv_a^T, x[row_index] @ sv_b^T) in one launch: the gate and up backbones."""
+                         row_index: torch.Tensor | None = None, in_scale_a: torch.Tensor | None = None,
+                         in_scale_b: torch.Tensor | None = None):
+    """(fp16(x[row_index] * in_scale_a) @ sv_a^T, fp16(x[row_index] * in_scale_b) @ sv_b^T) in one launch: the
+    gate and up backbones, each with its own ns_mode == 1 input scale (or None)."""
     _check_cuda("x", x, torch.float16, 2)
     _check_cuda("shared_sv_a", sv_a, torch.float16, 2, x.device)
     _check_cuda("shared_sv_b", sv_b, torch.float16, 2, x.device)
@@ -596,16 +603,22 @@ def backbone_linear_pair(x: torch.Tensor, sv_a: torch.Tensor, sv_b: torch.Tensor
     tokens = int(row_index.numel()) if row_index is not None else int(x.size(0))
     if row_index is not None:
         _check_cuda("row_index", row_index, torch.int64, 1, x.device)
+    for name, sc in (("in_scale_a", in_scale_a), ("in_scale_b", in_scale_b)):
+        if sc is not None:
+            _check_cuda(name, sc, torch.float16, 1, x.device)
+            if sc.numel() != x.size(1):
+                raise RuntimeError(f"{name} must hold in_features values")
     rank, in_f = int(sv_a.size(0)), int(sv_a.size(1))
     if tokens >= BACKBONE_LIBRARY_MIN_ROWS:
-        out_a, out_b = _backbone_library(x, (sv_a, sv_b), None, row_index)
+        out_a, out_b = _backbone_library(x, (sv_a, sv_b), (in_scale_a, in_scale_b), row_index)
         return out_a, out_b
     out_a = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
     out_b = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
     lib = _lib.load()
     ws = backbone_workspace(x.device, int(lib.tris_backbone_pair_workspace_bytes(tokens, in_f, rank)))
     _lib.check(lib.tris_backbone_linear_pair(_ptr(x), tokens, in_f, _ptr(row_index), _ptr(sv_a), _ptr(sv_b), rank,
-                                             _ptr(out_a), _ptr(out_b), _ptr(ws), int(ws.numel()), _stream(x)),
+                                             _ptr(in_scale_a), _ptr(in_scale_b), _ptr(out_a), _ptr(out_b), _ptr(ws),
+                                             int(ws.numel()), _stream(x)),
                "tris_backbone_linear_pair")
     return out_a, out_b
 
@@ -693,8 +706,10 @@ def packed4_backbone_linear(x: torch.Tensor, m: Packed4Matrix, in_scale: torch.T
 
 
 def packed4_backbone_linear_pair(x: torch.Tensor, ma: Packed4Matrix, mb: Packed4Matrix,
-                                 row_index: torch.Tensor | None = None):
-    """The gate and up packed backbones of the same rows in one launch (same bits as two single calls)."""
+                                 row_index: torch.Tensor | None = None, in_scale_a: torch.Tensor | None = None,
+                                 in_scale_b: torch.Tensor | None = None):
+    """The gate and up packed backbones of the same rows in one launch, each with its own input scale (or None);
+    the same bits as two single calls."""
     _check_cuda("x", x, torch.float16, 2)
     _check_packed4(ma, x.device)
     _check_packed4(mb, x.device)
@@ -703,14 +718,19 @@ def packed4_backbone_linear_pair(x: torch.Tensor, ma: Packed4Matrix, mb: Packed4
     tokens = int(row_index.numel()) if row_index is not None else int(x.size(0))
     if row_index is not None:
         _check_cuda("row_index", row_index, torch.int64, 1, x.device)
+    for name, sc in (("in_scale_a", in_scale_a), ("in_scale_b", in_scale_b)):
+        if sc is not None:
+            _check_cuda(name, sc, torch.float16, 1, x.device)
+            if sc.numel() != x.size(1):
+                raise RuntimeError(f"{name} must hold in_features values")
     out_a = torch.empty((tokens, ma.rows), dtype=torch.float16, device=x.device)
     out_b = torch.empty((tokens, mb.rows), dtype=torch.float16, device=x.device)
     lib = _lib.load()
     ws = backbone_workspace(x.device, int(lib.tris_backbone_pair_workspace_bytes(tokens, ma.cols, ma.rows)))
     sa, sb = ma.c_struct(), mb.c_struct()
     _lib.check(lib.tris_packed4_backbone_linear_pair(_ptr(x), tokens, _ptr(row_index), ctypes.byref(sa),
-                                                     ctypes.byref(sb), _ptr(out_a), _ptr(out_b), _ptr(ws),
-                                                     int(ws.numel()), _stream(x)),
+                                                     ctypes.byref(sb), _ptr(in_scale_a), _ptr(in_scale_b),
+                                                     _ptr(out_a), _ptr(out_b), _ptr(ws), int(ws.numel()), _stream(x)),
                "tris_packed4_backbone_linear_pair")
     return out_a, out_b
 

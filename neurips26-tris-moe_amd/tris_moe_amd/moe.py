@@ -40,7 +40,10 @@ def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, select
 
     x16 fp16 [T, H]; routing_weights [T, k] (cast to fp16 as in modeling_mixtral.py:555);
     selected_experts int64 [T, k]; payloads {gate, up, down} device payload dicts;
-    backbones {gate, up, down}: fp16 SV [rank, in] or qlinear.PackedQuantMatrix4bit.  payloads may also hold
+    backbones {gate, up, down}: fp16 SV [rank, in] or qlinear.PackedQuantMatrix4bit, and optionally
+    {gate,up,down}_in_scale: the fp16 [in] expert_input_scale of experts[0]'s projection when its ns_mode is 1
+    (compute_shared_hidden multiplies the backbone input by it, qlinear_cuda.py:4477-4480; the grouped
+    forward projects every expert through experts[0], modeling_mixtral.py:469-470, 497).  payloads may also hold
     matrix-mode null-space payloads under gate_ns / up_ns / down_ns (``qlinear.build_grouped_ns_payload``
     format on the device).  Returns [T, H] in output_dtype.
 
@@ -98,7 +101,9 @@ def _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, ou
     if predecodable and expert_path != "fused":
         return _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype,
                                        shared_expert)
-    hid_g, hid_u = shared_projection_pair(x16, backbones["gate"], backbones["up"], row_index=gti)
+    sc = _in_scales(backbones)
+    hid_g, hid_u = shared_projection_pair(x16, backbones["gate"], backbones["up"], row_index=gti,
+                                          in_scale_a=sc["gate"], in_scale_b=sc["up"])
     empty = x16.new_empty((0, 0))
     g_out, u_out = ext.compact3_tris_precomputed_grouped_dual_forward_block_gr(
         hid_g, hid_u, expert_ids, seg, prob, tile_bound,
@@ -111,7 +116,7 @@ def _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, ou
     if ns["gate"] is not None or ns["up"] is not None:
         ext.ns_compensation_pair_apply_(g_out, u_out, x16, expert_ids, seg, ns["gate"], ns["up"], row_index=gti)
     mlp = F.silu(g_out) * u_out
-    hid_d = shared_projection(mlp, backbones["down"])
+    hid_d = shared_projection(mlp, backbones["down"], in_scale=sc["down"])
     d_out = ext.compact3_tris_precomputed_grouped_forward_block_gr(
         hid_d, expert_ids, seg, prob, tile_bound,
         pd["qweight1"], pd["qweight2_sparse"], pd["qweight2_sparse_prefix"], pd["q_gmap_gr_words"],
@@ -121,6 +126,11 @@ def _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, ou
     if ns["down"] is not None:
         ext.ns_compensation_apply_(d_out, mlp, expert_ids, seg, ns["down"])
     return _combine(x16, d_out, route, w16, output_dtype, shared_expert)
+
+
+def _in_scales(backbones: dict) -> dict:
+    """The backbone input scales of the layer (None where absent)."""
+    return {key: backbones.get(f"{key}_in_scale") for key in ("gate", "up", "down")}
 
 
 def _ns_payloads(payloads: dict) -> dict:
@@ -217,8 +227,10 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
             [(bufs[name], p["q_gmap_gr_words"], p["q_gmap_gr_offsets"], p["q_gmap_gr_meta"], int(p["qweight1"].size(1)),
               int(p["qweight1"].size(2))) for name, p in order], eid)
         decoded = bufs
+    sc = _in_scales(backbones)
     hid_g, hid_u = shared_projection_pair(x16, backbones["gate"], backbones["up"],
-                                            row_index=route["grouped_token_indices"])
+                                          row_index=route["grouped_token_indices"], in_scale_a=sc["gate"],
+                                          in_scale_b=sc["up"])
     main.wait_stream(side)
     if ns_side is not None:
         main.wait_stream(ns_side)
@@ -249,7 +261,7 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
         side.wait_stream(main)
         with torch.cuda.stream(side):
             ext.ns_compensation_apply_(comp_d, mlp, eid, seg, ns["down"], accumulate=False)
-    hid_d = shared_projection(mlp, backbones["down"])
+    hid_d = shared_projection(mlp, backbones["down"], in_scale=sc["down"])
     d_out = torch.empty((R, n_out), dtype=torch.float16, device=dev)
     ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
         hid_d, eid, seg, prob, tile_bound, decoded["down"], *[pd[k] for k in names], True, out=d_out)
@@ -261,18 +273,21 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
 
 
 class TrisSparseMoeBlock(nn.Module):
-    """Grouped-expert sparse MoE block (MixtralSparseMoeBlock / OlmoeSparseMoeBlock shape)."""
+    """Grouped-expert sparse MoE block (MixtralSparseMoeBlock / OlmoeSparseMoeBlock shape).  The router
+    ``gate`` is an nn.Linear in the model dtype (``router_dtype``, bf16 by default), as the reference's
+    block keeps it; its logits go through an fp32 softmax (modeling_mixtral.py:546-549)."""
 
     def __init__(self, hidden_size: int, num_experts: int, top_k: int, payloads: dict, backbones: dict,
-                 router_weight: torch.Tensor | None = None, renormalize: bool = True, shared_expert=None):
+                 router_weight: torch.Tensor | None = None, renormalize: bool = True, shared_expert=None,
+                 router_dtype: torch.dtype = torch.bfloat16):
         super().__init__()
         self.hidden_dim = hidden_size
         self.num_experts = num_experts
         self.top_k = top_k
         self.renormalize = renormalize
-        self.gate = nn.Linear(hidden_size, num_experts, bias=False)
+        self.gate = nn.Linear(hidden_size, num_experts, bias=False, dtype=router_dtype)
         if router_weight is not None:
-            self.gate.weight.data = router_weight
+            self.gate.weight.data = router_weight.to(router_dtype)
         self.payloads = payloads
         self.backbones = backbones
         self.shared_expert = shared_expert
@@ -288,8 +303,10 @@ class TrisSparseMoeBlock(nn.Module):
                                                output_dtype, self.shared_expert)
 
     def forward(self, hidden_states: torch.Tensor):
+        """modeling_mixtral.py:539-608: hidden_states [B, S, H] (bf16 or fp16) -> (out [B, S, H] in the input
+        dtype, router_logits [B*S, E] in the router's dtype)."""
         batch, seq, hidden = hidden_states.shape
-        flat = hidden_states.view(-1, hidden)
-        router_logits = self.gate(flat)
+        flat = hidden_states.reshape(-1, hidden)
+        router_logits = self.gate(flat.to(self.gate.weight.dtype))
         out = self.forward_routed(flat, router_logits)
         return out.reshape(batch, seq, hidden), router_logits

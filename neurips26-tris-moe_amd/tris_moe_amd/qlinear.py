@@ -649,18 +649,22 @@ def shared_projection(x: torch.Tensor, sv, in_scale: torch.Tensor | None = None,
     return ext.backbone_linear(x, sv, in_scale=in_scale, row_index=row_index)
 
 
-def shared_projection_pair(x: torch.Tensor, sv_a, sv_b, row_index: torch.Tensor | None = None):
-    """Gate and up backbones of the same rows: one launch for two fp16 matrices or two fused-capable packed
-    matrices of one shape, else two projections."""
+def shared_projection_pair(x: torch.Tensor, sv_a, sv_b, row_index: torch.Tensor | None = None,
+                           in_scale_a: torch.Tensor | None = None, in_scale_b: torch.Tensor | None = None):
+    """Gate and up backbones of the same rows, each with its own ns_mode == 1 input scale (or None): one launch
+    for two fp16 matrices or two fused-capable packed matrices of one shape, else two projections."""
     tokens = int(row_index.numel()) if row_index is not None else int(x.size(0))
     if isinstance(sv_a, torch.Tensor) and isinstance(sv_b, torch.Tensor):
-        return ext.backbone_linear_pair(x, sv_a, sv_b, row_index=row_index)
+        return ext.backbone_linear_pair(x, sv_a, sv_b, row_index=row_index, in_scale_a=in_scale_a,
+                                        in_scale_b=in_scale_b)
     if (isinstance(sv_a, PackedQuantMatrix4bit) and isinstance(sv_b, PackedQuantMatrix4bit)
             and sv_a.fused_ok(tokens) and sv_b.fused_ok(tokens) and sv_a.group_size == sv_b.group_size
             and (sv_a._rows_host, sv_a._cols_host) == (sv_b._rows_host, sv_b._cols_host)
             and sv_a.scales.shape == sv_b.scales.shape):
-        return ext.packed4_backbone_linear_pair(x, sv_a.matrix(), sv_b.matrix(), row_index=row_index)
-    return (shared_projection(x, sv_a, row_index=row_index), shared_projection(x, sv_b, row_index=row_index))
+        return ext.packed4_backbone_linear_pair(x, sv_a.matrix(), sv_b.matrix(), row_index=row_index,
+                                                in_scale_a=in_scale_a, in_scale_b=in_scale_b)
+    return (shared_projection(x, sv_a, in_scale=in_scale_a, row_index=row_index),
+            shared_projection(x, sv_b, in_scale=in_scale_b, row_index=row_index))
 
 
 class ExpertSharedMatrix(nn.Module):

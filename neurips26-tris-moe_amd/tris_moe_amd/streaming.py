@@ -158,6 +158,7 @@ class GroupedPayloadStreamer:
         self._ready = [torch.cuda.Event() for _ in range(num_slots)]
         self._done = [torch.cuda.Event() for _ in range(num_slots)]
         self._used = [False] * num_slots
+        self._held = [False] * num_slots     # acquired and not yet released: the slot must not be refilled
         self._owner = [-1] * num_slots       # layer held (or being copied) by each slot
         self._where = {}                      # layer -> slot
         self._next = 0
@@ -171,15 +172,22 @@ class GroupedPayloadStreamer:
         return self.layouts[i].nbytes
 
     def prefetch(self, i: int) -> int:
-        """Queue layer i's copy into a slot (no-op when it is already resident); returns the slot."""
+        """Queue layer i's copy into a slot (no-op when it is already resident); returns the slot.  The slots are
+        taken round-robin, skipping slots whose layer is acquired and not yet released (kernels queued on it may
+        still read it); RuntimeError when every slot is held."""
         if not 0 <= i < self.num_layers:
             raise IndexError(f"layer {i} out of range")
         self.stats["prefetches"] += 1
         if i in self._where:
             self.stats["hits"] += 1
             return self._where[i]
-        s = self._next
-        self._next = (self._next + 1) % self.num_slots
+        for _ in range(self.num_slots):
+            s = self._next
+            self._next = (self._next + 1) % self.num_slots
+            if not self._held[s]:
+                break
+        else:
+            raise RuntimeError(f"prefetch of layer {i}: every slot holds an acquired layer (release one first)")
         old = self._owner[s]
         if old >= 0:
             del self._where[old]
@@ -203,6 +211,7 @@ class GroupedPayloadStreamer:
             s = self.prefetch(i)
         stream = stream if stream is not None else torch.cuda.current_stream(self.device)
         stream.wait_event(self._ready[s])
+        self._held[s] = True
         # the slot's memory is used by `stream` (caching allocator bookkeeping for the views)
         self.slots[s].record_stream(stream)
         payloads, backbones = unpack_views(self.layouts[i], self.slots[s])
@@ -218,13 +227,17 @@ class GroupedPayloadStreamer:
         stream = stream if stream is not None else torch.cuda.current_stream(self.device)
         self._done[s].record(stream)
         self._used[s] = True
+        self._held[s] = False
 
 
 def streamed_forward(streamer: GroupedPayloadStreamer, x16: torch.Tensor, router_logits: list, top_k: int,
-                     renormalize: bool, num_experts: int, backbones: list | None = None):
-    """Run the layers in order, each layer's input the previous layer's output (fp16), prefetching layer
-    i + 1 while layer i computes.  ``router_logits[i]``: the [T, E] fp32 logits of layer i;
-    ``backbones[i]``: resident backbones when the blobs do not carry them.  Returns the last output (bf16)."""
+                     renormalize: bool, num_experts: int, backbones: list | None = None,
+                     outputs: list | None = None, residual: bool = False, inputs: list | None = None):
+    """Run the layers in order, prefetching layer i + 1 while layer i computes.  Layer i + 1's input is layer
+    i's output (fp16), or with ``residual`` the residual stream fp16(x_i + out_i) that a decoder stack feeds
+    its next layer (keeps activations O(1) across many layers).  ``router_logits[i]``: the [T, E] fp32 logits
+    of layer i; ``backbones[i]``: resident backbones when the blobs do not carry them; ``outputs`` /
+    ``inputs``: lists that receive every layer's output (bf16) / input (fp16).  Returns the last output."""
     from . import moe
 
     n = streamer.num_layers
@@ -236,8 +249,12 @@ def streamed_forward(streamer: GroupedPayloadStreamer, x16: torch.Tensor, router
         payloads, bb = streamer.acquire(i)
         if bb is None:
             bb = backbones[i]
+        if inputs is not None:
+            inputs.append(x16)
         out = moe.grouped_moe_forward_from_logits(x16, router_logits[i], top_k, renormalize, payloads, bb,
                                                   num_experts, torch.bfloat16)
         streamer.release(i)
-        x16 = out.to(torch.float16)
+        if outputs is not None:
+            outputs.append(out)
+        x16 = (x16.float() + out.float()).to(torch.float16) if residual else out.to(torch.float16)
     return out

@@ -17,9 +17,15 @@ reference checkout):
   ``TriSMoE_cuda_kernel.cu:665-774`` (per-weight formula) and ``:830-853``
   (row-pack group selection); agrees with the CPU fallback
   ``qlinear_cuda.py:4200-4236`` for finite scale products.
-* Grouped GEMM + epilogue (numpy, fp32 accumulation of the exact fp16 weights):
-  ``TriSMoE_cuda_kernel.cu:4500-4681`` (segment kernel arithmetic and
-  epilogue), segment search ``:3874-3904``.
+* Grouped GEMM + epilogue (numpy, the exact fp16 weights; sums accumulated in
+  float64, i.e. the exact product sum rounded once where the reference's
+  fp32 accumulation rounds on the way): ``TriSMoE_cuda_kernel.cu:4500-4681``
+  (segment kernel arithmetic and epilogue), segment search ``:3874-3904``.
+  The layer's backbone projections (``linear_f16``) accumulate the same way.
+  Two fp32-accumulating evaluations of the Mixtral decode layer that differ
+  only in summation order already differ by rel-L2 ~8e-4 on the bf16 output
+  (fp16 intermediates and the bf16 output flip by whole ulps at rounding
+  boundaries), so the checker is the exact sum, not one more fp32 order.
 * Route metadata (numpy): ``TriSMoE_cuda.cpp:741-793`` /
   ``qlinear_cuda.py:1301-1378``.
 * MoE block (numpy): ``modeling_mixtral.py:406-608`` (grouped forward) and
@@ -313,8 +319,8 @@ def dequant_grouped_expert(payload: dict, e: int, uniform_k64_groups: bool | Non
 # --------------------------------------------------------- grouped GEMM
 def grouped_forward(payload: dict, hidden, expert_ids, segment_offsets, uniform_k64_groups: bool | None = None,
                     weight_cache: dict | None = None) -> np.ndarray:
-    """out[R, N] fp16: per segment, fp32-accumulated hidden @ W_e^T, then the
-    reference epilogue fp16(acc * scale + bias) (TriSMoE_cuda_kernel.cu:4662-4680).
+    """out[R, N] fp16: per segment, hidden @ W_e^T (exact sums, held in fp32 as the kernel's accumulator),
+    then the reference epilogue fp16(acc * scale + bias) in fp32 (TriSMoE_cuda_kernel.cu:4662-4680).
     Segments with a negative expert slot produce zeros."""
     hidden = np.asarray(hidden, dtype=np.float16)
     n = int(payload["qweight1"].shape[2])
@@ -332,7 +338,7 @@ def grouped_forward(payload: dict, hidden, expert_ids, segment_offsets, uniform_
             continue
         if e not in cache:
             cache[e] = dequant_grouped_expert(payload, int(e), uniform_k64_groups).astype(np.float32)
-        acc = hidden[r0:r1].astype(np.float32) @ cache[e].T
+        acc = (hidden[r0:r1].astype(ACC) @ cache[e].astype(ACC).T).astype(np.float32)
         if has_scale:
             acc = acc * np.asarray(payload["output_scale"][e], dtype=np.float16).astype(np.float32)[None, :]
         if has_bias:
@@ -403,9 +409,14 @@ def silu_f16(x) -> np.ndarray:
     return (x32 / (1.0 + np.exp(-x32))).astype(np.float16)
 
 
+# Accumulation type of the layer's GEMMs (linear_f16, grouped_forward): float64 holds every fp16 x fp16
+# product exactly and sums of up to 2^29 of them without a rounding that can reach an fp16 ulp.
+ACC = np.float64
+
+
 def linear_f16(x, w) -> np.ndarray:
-    """fp16 F.linear with fp32 accumulation: fp16(x @ w^T)."""
-    return (np.asarray(x, dtype=np.float16).astype(np.float32) @ np.asarray(w, dtype=np.float16).astype(np.float32).T).astype(np.float16)
+    """fp16 F.linear of the exact product sums: fp16(x @ w^T), one rounding."""
+    return (np.asarray(x, dtype=np.float16).astype(ACC) @ np.asarray(w, dtype=np.float16).astype(ACC).T).astype(np.float16)
 
 
 def route_topk(router_logits, top_k: int, renormalize: bool = True):
@@ -420,8 +431,32 @@ def route_topk(router_logits, top_k: int, renormalize: bool = True):
     return w.astype(np.float32), idx.astype(np.int64)
 
 
+def dequant_experts(payloads: dict, experts, workers: int = 1) -> dict:
+    """Weight caches {proj: {e: fp32 [N, K]}} of the given experts for every projection, the per-expert GR
+    decode and exact fp16 dequant of the reference CPU path (qlinear_cuda.py:4532-4547 re-dequantises on
+    every call), spread over `workers` threads (the C decoder and numpy's array loops release the GIL)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    units = [(p, int(e)) for p in payloads for e in experts]
+
+    def one(unit):
+        p, e = unit
+        return p, e, dequant_grouped_expert(payloads[p], e).astype(np.float32)
+
+    caches = {p: {} for p in payloads}
+    if workers <= 1:
+        results = [one(u) for u in units]
+    else:
+        with ThreadPoolExecutor(max_workers=workers) as pool:
+            results = list(pool.map(one, units))
+    for p, e, w in results:
+        caches[p][e] = w
+    return caches
+
+
 def moe_layer(x_f16, routing_weights, selected_experts, payloads: dict, backbones: dict, num_experts: int,
-              shared_expert=None, weight_caches: dict | None = None, ns_payloads: dict | None = None) -> np.ndarray:
+              shared_expert=None, weight_caches: dict | None = None, ns_payloads: dict | None = None,
+              input_scales: dict | None = None) -> np.ndarray:
     """Grouped MoE block (modeling_mixtral.py:406-537) with fp16 tensors between
     stages and fp32 accumulation inside every product; returns fp32 [T, H]
     (the caller rounds to the output dtype).
@@ -430,6 +465,9 @@ def moe_layer(x_f16, routing_weights, selected_experts, payloads: dict, backbone
     matching fp16 shared matrices SV [rank, in].  routing_weights are cast to
     fp16 as the reference does (modeling_mixtral.py:555).  shared_expert, if
     given, is (w_gate [I,H], w_up [I,H], w_down [H,I]) fp16 added unrouted.
+    input_scales: {gate, up, down} -> fp16 [in] or absent: the ns_mode == 1 input
+    scale of experts[0]'s projection, an fp16 product with the backbone input
+    before F.linear (qlinear_cuda.py:4477-4480, modeling_mixtral.py:469-470, 497).
     """
     caches = weight_caches if weight_caches is not None else {"gate": {}, "up": {}, "down": {}}
     x = np.asarray(x_f16, dtype=np.float16)
@@ -439,8 +477,14 @@ def moe_layer(x_f16, routing_weights, selected_experts, payloads: dict, backbone
     gsl = route["grouped_slots"]
     rw16 = np.asarray(routing_weights, dtype=np.float32).astype(np.float16)
     x_g = x[gti]
-    hid_g = linear_f16(x, backbones["gate"])[gti]
-    hid_u = linear_f16(x, backbones["up"])[gti]
+    scales = input_scales or {}
+
+    def scaled(v, proj):
+        sc = scales.get(proj)
+        return v if sc is None else f16_mul(v, np.asarray(sc, dtype=np.float16)[None, :])
+
+    hid_g = linear_f16(scaled(x, "gate"), backbones["gate"])[gti]
+    hid_u = linear_f16(scaled(x, "up"), backbones["up"])[gti]
     g_out = grouped_forward(payloads["gate"], hid_g, route["expert_ids"], route["segment_offsets"], weight_cache=caches["gate"])
     u_out = grouped_forward(payloads["up"], hid_u, route["expert_ids"], route["segment_offsets"], weight_cache=caches["up"])
     ns_payloads = ns_payloads or {}
@@ -450,7 +494,7 @@ def moe_layer(x_f16, routing_weights, selected_experts, payloads: dict, backbone
     if ns_payloads.get("up") is not None:
         u_out = f16_add(u_out, ns_compensation(x_g, ns_payloads["up"], route["expert_ids"], route["segment_offsets"]))
     mlp = (silu_f16(g_out).astype(np.float32) * u_out.astype(np.float32)).astype(np.float16)
-    hid_d = linear_f16(mlp, backbones["down"])
+    hid_d = linear_f16(scaled(mlp, "down"), backbones["down"])
     d_out = grouped_forward(payloads["down"], hid_d, route["expert_ids"], route["segment_offsets"], weight_cache=caches["down"])
     if ns_payloads.get("down") is not None:
         d_out = f16_add(d_out, ns_compensation(mlp, ns_payloads["down"], route["expert_ids"], route["segment_offsets"]))

@@ -12,7 +12,14 @@ from tris_moe_amd.configs import MoELayerSpec
 TINY = MoELayerSpec("tiny", hidden=256, num_experts=4, intermediate=384, top_k=2, rank=128, tokens=(3,))
 
 
-def _save(tris, tmp_path, n=2, packed_down=False, family="mixtral"):
+def _input_scales(n):
+    """ns_mode 1 input scales for layer 1's gate and down projections (layer 0 has none)."""
+    rng = np.random.default_rng(77)
+    return [None] + [{"gate": rng.uniform(0.5, 1.5, TINY.hidden).astype(np.float16),
+                      "down": rng.uniform(0.5, 1.5, TINY.intermediate).astype(np.float16)}] * (n - 1)
+
+
+def _save(tris, tmp_path, n=2, packed_down=False, family="mixtral", input_scales=None):
     layers = [tris["synthetic"].make_layer(TINY, 100 + i, tris["ext"].gr_encode) for i in range(n)]
     bbs = []
     for L in layers:
@@ -23,7 +30,7 @@ def _save(tris, tmp_path, n=2, packed_down=False, family="mixtral"):
         bbs.append(bb)
     path = str(tmp_path / ck.GROUPED_PAYLOAD_SIDECAR_BASENAME)
     ck.save_grouped_checkpoint(path, [{p: L[p] for p in ck.GROUPED_PRECOMPUTED_KEYS} for L in layers], family,
-                               bbs, metadata={"model": "tiny"})
+                               bbs, metadata={"model": "tiny"}, input_scales=input_scales)
     return path, layers, bbs
 
 
@@ -162,6 +169,34 @@ def test_null_space_payloads_round_trip(tris, tmp_path):
         c.load_layer("model.layers.0.block_sparse_moe", "cpu")
 
 
+@pytest.mark.parametrize("family", ["mixtral", "olmoe"])
+def test_input_scales_round_trip(tris, tmp_path, family):
+    """experts[0]'s ns_mode / expert_input_scale (the per-expert state a deployment-only checkpoint keeps,
+    grouped_payload_sidecar.py:38-46) load as the layer's backbone input scales; ns_mode 1 without a scale is
+    an error."""
+    from safetensors.torch import save_file
+
+    scales = _input_scales(2)
+    path, _, _ = _save(tris, tmp_path, input_scales=scales, family=family)
+    c = ck.GroupedCheckpoint(path)
+    mod = {"mixtral": ("w1", "w2"), "olmoe": ("gate_proj", "down_proj")}[family]
+    lp1 = ck.moe_layer_prefix(1, family)
+    assert f"{lp1}.experts.0.{mod[0]}.expert_input_scale" in c.keys()
+    assert f"{lp1}.experts.0.{mod[1]}.ns_mode" in c.keys()
+    bb0, bb1 = c.load_backbones(0, "cpu"), c.load_backbones(1, "cpu")
+    assert not any(k.endswith("_in_scale") for k in bb0)
+    assert sorted(k for k in bb1 if k.endswith("_in_scale")) == ["down_in_scale", "gate_in_scale"]
+    for proj in ("gate", "down"):
+        got = bb1[f"{proj}_in_scale"]
+        assert got.dtype == torch.float16 and np.array_equal(got.numpy().view(np.uint16), scales[1][proj].view(np.uint16))
+    # ns_mode 1 with the scale missing
+    bad = {k: c._f.get_tensor(k) for k in c.keys() if not k.endswith("expert_input_scale")}
+    path2 = str(tmp_path / "bad.safetensors")
+    save_file(bad, path2)
+    with pytest.raises(ValueError, match="ns_mode 1"):
+        ck.GroupedCheckpoint(path2).load_backbones(1, "cpu")
+
+
 def test_incomplete_checkpoint_is_reported(tris, tmp_path):
     from safetensors.torch import save_file
 
@@ -174,11 +209,13 @@ def test_incomplete_checkpoint_is_reported(tris, tmp_path):
 
 
 @pytest.mark.gpu
-def test_checkpoint_layer_runs_like_memory(tris, cuda, tmp_path):
-    """Two layers loaded from a checkpoint (one with a packed down backbone) give the bits of the same layers
-    built from the in-memory payloads."""
+def test_checkpoint_layer_runs_like_memory(tris, oracle_mod, cuda, tmp_path):
+    """Two layers loaded from a checkpoint (packed down backbones; layer 1 with ns_mode 1 input scales on its
+    gate and down projections) match the oracle layer, and give the bits of the same layers built from the
+    in-memory payloads."""
     print("checkpoint layer", flush=True)
-    path, layers, bbs = _save(tris, tmp_path, packed_down=True)
+    scales = _input_scales(2)
+    path, layers, bbs = _save(tris, tmp_path, packed_down=True, input_scales=scales)
     c = ck.GroupedCheckpoint(path)
     ql, moe = tris["qlinear"], tris["moe"]
     rng = np.random.default_rng(5)
@@ -190,12 +227,27 @@ def test_checkpoint_layer_runs_like_memory(tris, cuda, tmp_path):
         mem = {p: ql.payload_to_device(layers[i][p], cuda) for p in ck.GROUPED_PRECOMPUTED_KEYS}
         mbb = {p: torch.from_numpy(bbs[i][p]).to(cuda) for p in ("gate", "up")}
         mbb["down"] = ql.PackedQuantMatrix4bit().set_from_payload(bbs[i]["down"]).to(cuda)
+        for proj, sc in (scales[i] or {}).items():
+            mbb[f"{proj}_in_scale"] = torch.from_numpy(sc).to(cuda)
         a = moe.grouped_moe_forward_from_logits(x16, logits, TINY.top_k, TINY.renormalize, loaded, lbb,
                                                 TINY.num_experts, torch.bfloat16)
         b = moe.grouped_moe_forward_from_logits(x16, logits, TINY.top_k, TINY.renormalize, mem, mbb,
                                                 TINY.num_experts, torch.bfloat16)
         torch.cuda.synchronize()
         assert torch.equal(a.view(torch.int16), b.view(torch.int16)), lp
+        # the oracle layer on the host copies (the packed down backbone dequantised by the oracle)
+        pk = bbs[i]["down"]
+        down_sv = oracle_mod.packed4_dequant(pk["qweight"], pk["qzeros"], pk["scales"], pk["g_idx"], int(pk["rows"]),
+                                             int(pk["cols"]))
+        w, sel = oracle_mod.route_topk(logits.cpu().numpy(), TINY.top_k, TINY.renormalize)
+        want = oracle_mod.bf16_round(oracle_mod.moe_layer(
+            x16.cpu().numpy(), w, sel, {p: layers[i][p] for p in ck.GROUPED_PRECOMPUTED_KEYS},
+            {"gate": bbs[i]["gate"], "up": bbs[i]["up"], "down": down_sv}, TINY.num_experts,
+            input_scales=scales[i]))
+        got = a.float().cpu().numpy().astype(np.float64)
+        err = got - want
+        rel = float(np.linalg.norm(err) / np.linalg.norm(want))
+        assert float(np.abs(err).max()) <= 2e-2 and rel <= 1e-3, (lp, rel)
 
 
 def _mode4_tensors(tris, rng, n=96, rank=128, sparse_form=False):

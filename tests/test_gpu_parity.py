@@ -244,19 +244,28 @@ def test_route_matches_oracle(tris, oracle_mod, cuda, t, k, e):
     assert int(got["total_problem_tiles"][0]) == want["total_problem_tiles"]
 
 
-@pytest.mark.parametrize("t,k,e", [(1, 2, 8), (16, 2, 8), (32, 2, 64), (8, 8, 60), (4, 16, 16), (3, 1, 64),
-                                   (16, 8, 64), (33, 2, 8), (7, 8, 256), (256, 8, 128)])
-def test_route_topk_fused_matches_oracle(tris, oracle_mod, cuda, t, k, e):
+ROUTE_TOPK_CASES = [(t, k, e, True) for t, k, e in [(1, 2, 8), (16, 2, 8), (32, 2, 64), (8, 8, 60), (4, 16, 16),
+                                                    (3, 1, 64), (16, 8, 64), (33, 2, 8), (7, 8, 256), (256, 8, 128)]]
+# top_k below its pick-list bucket on the one-wavefront router (buckets of 2, 8 and 16 picks), both weightings;
+# and the workgroup router without renormalisation (OLMoE's default)
+ROUTE_TOPK_CASES += [(t, k, e, rn) for t, k, e in [(8, 4, 32), (4, 6, 60), (2, 12, 64), (5, 3, 16), (16, 8, 64)]
+                     for rn in (False, True)]
+ROUTE_TOPK_CASES += [(16, 8, 128, False), (64, 2, 8, False)]
+
+
+@pytest.mark.parametrize("t,k,e,renorm", ROUTE_TOPK_CASES)
+def test_route_topk_fused_matches_oracle(tris, oracle_mod, cuda, t, k, e, renorm):
     """Fused softmax / top-k / route: the selection and the route are exactly the oracle's
     (stable argsort of the fp32 softmax), weights within one fp16 ulp.  Up to 64 routed rows and 64
-    experts one wavefront does it (the first six cases, at its limits); otherwise one workgroup."""
-    note(f"route topk fused t={t} k={k} e={e}")
-    rng = np.random.default_rng(t * 100 + e)
+    experts one wavefront does it (pick lists of 2, 8 or 16 entries, the smallest that holds top_k);
+    otherwise one workgroup."""
+    note(f"route topk fused t={t} k={k} e={e} renorm={renorm}")
+    rng = np.random.default_rng(t * 100 + e + k)
     logits = rng.standard_normal((t, e)).astype(np.float32)
     if t > 1:
         logits[1, : min(e, 4)] = 0.25  # exact ties among the top experts
-    w, sel = oracle_mod.route_topk(logits, k, True)
-    r = tris["ext"].route_topk_grouped(torch.from_numpy(logits).to(cuda), k, True, 4)
+    w, sel = oracle_mod.route_topk(logits, k, renorm)
+    r = tris["ext"].route_topk_grouped(torch.from_numpy(logits).to(cuda), k, renorm, 4)
     np.testing.assert_array_equal(r["selected_experts"].cpu().numpy(), sel)
     want = oracle_mod.build_route(sel, e, 4)
     for key in ("perm", "grouped_token_indices", "grouped_slots"):
@@ -282,6 +291,55 @@ def test_route_rejects_bad_expert_ids(tris, cuda):
     sel = torch.tensor([[0, 9]], dtype=torch.int64, device=cuda)
     with pytest.raises(RuntimeError):
         tris["qlinear"].build_grouped_route(sel, 8)
+
+
+@pytest.mark.parametrize("t,k,e", [(6, 2, 8), (40, 4, 16)])
+def test_route_device_bad_ids_stay_in_bounds(tris, oracle_mod, cuda, t, k, e):
+    """The no-sync route with expert ids outside [0, E): counts[0] = -1; the valid picks are routed as the
+    oracle routes them alone; the invalid ones fill the rows after every segment in flat order with their own
+    token index and slot, grouped expert id -1 and inverse_perm -1; the combine skips them."""
+    note(f"route bad ids device t={t} k={k} e={e}")
+    rng = np.random.default_rng(t + k)
+    sel = np.stack([rng.choice(e, size=k, replace=False) for _ in range(t)]).astype(np.int64)
+    bad = rng.random(sel.shape) < 0.2
+    bad[0, 0] = True
+    sel[bad] = np.where(rng.random(int(bad.sum())) < 0.5, -1, e + 3)
+    r = tris["ext"].build_grouped_route_device(torch.from_numpy(sel).to(cuda), e, 4)
+    flat = sel.reshape(-1)
+    valid = (flat >= 0) & (flat < e)
+    nv = int(valid.sum())
+    assert int(r["counts"][0]) == -1
+    # valid picks: a stable sort by expert, as the oracle's route of the valid entries alone
+    order = np.argsort(np.where(valid, flat, e), kind="stable")[:nv]
+    perm = r["perm"].cpu().numpy()
+    np.testing.assert_array_equal(perm[:nv], order)
+    gexp = r["grouped_expert_ids"].cpu().numpy()
+    np.testing.assert_array_equal(gexp[:nv], flat[order])
+    ids = sorted(set(flat[valid].tolist()))
+    np.testing.assert_array_equal(r["expert_ids"].cpu().numpy()[: len(ids)], ids)
+    segs = r["segment_offsets"].cpu().numpy()
+    counts = [int((flat[valid] == i).sum()) for i in ids]
+    np.testing.assert_array_equal(segs[: len(ids) + 1], np.concatenate([[0], np.cumsum(counts)]))
+    assert (segs[len(ids):] == nv).all()
+    # invalid picks: the tail rows, flat order
+    tail = np.nonzero(~valid)[0]
+    np.testing.assert_array_equal(perm[nv:], tail)
+    np.testing.assert_array_equal(r["grouped_token_indices"].cpu().numpy(), perm // k)
+    np.testing.assert_array_equal(r["grouped_slots"].cpu().numpy(), perm % k)
+    assert (gexp[nv:] == -1).all()
+    inv = r["inverse_perm"].cpu().numpy()
+    assert (inv[~valid] == -1).all()
+    np.testing.assert_array_equal(perm[inv[valid]], np.nonzero(valid)[0])
+    # the combine adds only the valid picks
+    hidden = 64
+    eo = torch.from_numpy(rng.standard_normal((t * k, hidden)).astype(np.float16)).to(cuda)
+    wts = torch.from_numpy(rng.uniform(0.1, 1.0, (t, k)).astype(np.float16)).to(cuda)
+    out = tris["ext"].moe_combine(eo, r["inverse_perm"], wts, None).float().cpu().numpy()
+    eon, wn = eo.cpu().numpy().astype(np.float32), wts.cpu().numpy()
+    want = np.zeros((t, hidden), np.float32)
+    for i in np.nonzero(valid)[0]:
+        want[i // k] += (eon[inv[i]] * np.float32(wn[i // k, i % k])).astype(np.float16).astype(np.float32)
+    np.testing.assert_allclose(out, oracle_mod.bf16_round(want), rtol=0, atol=0)
 
 
 # ----------------------------------------------------------- grouped GEMM
@@ -575,11 +633,15 @@ def test_backbone_matches_fp32(tris, cuda, tokens, in_f, rank):
 
 
 # --------------------------------------------------------------------- layer
-def _run_layer(tris, oracle_mod, cuda, spec, tokens, seed, expert_path="auto"):
+def _run_layer(tris, oracle_mod, cuda, spec, tokens, seed, expert_path="auto", steps=None):
+    """The layer on `steps` independent batches of `tokens` (each its own forward call), outputs and oracle
+    outputs concatenated.  Single-token cases take four steps: the bf16 output of one token is 4096 values, and
+    rel-L2 over so few is dominated by a handful of whole-ulp flips that any fp32-accumulating evaluation makes
+    (measured: two fp32 orders of the oracle itself differ by up to 1.2e-3 on one token, ~8e-4 on average)."""
     syn = tris["synthetic"]
     ql = tris["qlinear"]
+    steps = steps if steps is not None else (4 if tokens == 1 else 1)
     layer = syn.make_layer(spec, seed, tris["ext"].gr_encode)
-    inp = syn.make_inputs(spec, tokens, seed + 1, layer["outlier_idx"])
     payloads = {p: ql.payload_to_device(layer[p], cuda) for p in ("gate", "up", "down")}
     backbones = {p: torch.from_numpy(layer["backbones"][p]).to(cuda) for p in ("gate", "up", "down")}
     shared = None
@@ -587,18 +649,25 @@ def _run_layer(tris, oracle_mod, cuda, spec, tokens, seed, expert_path="auto"):
         shared = tuple(torch.from_numpy(w).to(cuda) for w in layer["shared_expert"])
     block = tris["moe"].TrisSparseMoeBlock(spec.hidden, spec.num_experts, spec.top_k, payloads, backbones,
                                            renormalize=spec.renormalize, shared_expert=shared)
-    x = torch.from_numpy(inp["x"]).to(cuda).to(torch.bfloat16)
-    logits = torch.from_numpy(inp["router_logits"]).to(cuda)
-    if expert_path == "auto":
-        out = block.forward_routed(x, logits).float().cpu().numpy()
-    else:
-        wt, st = tris["moe"].route_topk(logits, spec.top_k, spec.renormalize)
-        out = tris["moe"].grouped_moe_forward(x.to(torch.float16), wt, st, payloads, backbones, spec.num_experts,
-                                              torch.bfloat16, shared, expert_path=expert_path).float().cpu().numpy()
-    w, sel = oracle_mod.route_topk(inp["router_logits"], spec.top_k, spec.renormalize)
-    want = oracle_mod.moe_layer(inp["x"].astype(np.float16), w, sel, {p: layer[p] for p in ("gate", "up", "down")},
-                                layer["backbones"], spec.num_experts, layer.get("shared_expert"))
-    return out, oracle_mod.bf16_round(want)
+    caches = {"gate": {}, "up": {}, "down": {}}
+    outs, wants = [], []
+    for i in range(steps):
+        inp = syn.make_inputs(spec, tokens, seed + 1 + i, layer["outlier_idx"])
+        x = torch.from_numpy(inp["x"]).to(cuda).to(torch.bfloat16)
+        logits = torch.from_numpy(inp["router_logits"]).to(cuda)
+        if expert_path == "auto":
+            out = block.forward_routed(x, logits).float().cpu().numpy()
+        else:
+            wt, st = tris["moe"].route_topk(logits, spec.top_k, spec.renormalize)
+            out = tris["moe"].grouped_moe_forward(x.to(torch.float16), wt, st, payloads, backbones, spec.num_experts,
+                                                  torch.bfloat16, shared, expert_path=expert_path).float().cpu().numpy()
+        w, sel = oracle_mod.route_topk(inp["router_logits"], spec.top_k, spec.renormalize)
+        want = oracle_mod.moe_layer(inp["x"].astype(np.float16), w, sel, {p: layer[p] for p in ("gate", "up", "down")},
+                                    layer["backbones"], spec.num_experts, layer.get("shared_expert"),
+                                    weight_caches=caches)
+        outs.append(out)
+        wants.append(oracle_mod.bf16_round(want))
+    return np.concatenate(outs), np.concatenate(wants)
 
 
 def test_layer_olmoe_c0(tris, oracle_mod, cuda):
@@ -618,10 +687,11 @@ def test_layer_mixtral_c1_decode(tris, oracle_mod, cuda, tokens, path):
     assert_close(out, want, f"C1 layer T={tokens} {path}")
 
 
-@pytest.mark.parametrize("tokens", [160, 512])
+@pytest.mark.parametrize("tokens", [160, 512, 2048])
 def test_layer_mixtral_prefill_shape(tris, oracle_mod, cuda, tokens):
-    """C2's layer shape at 160 tokens (320 routed rows: multi-tile segments, the row-tile MFMA kernel) and
-    512 tokens (about 128 rows per expert: the weight-stationary kernel), with the library GEMM for the
+    """C2's layer shape at 160 tokens (320 routed rows: multi-tile segments, the row-tile MFMA kernel),
+    512 tokens (about 128 rows per expert: the weight-stationary kernel) and C2 itself (2048 tokens, N(0, 1)
+    router logits: the histogram / scatter route over 4096 routed rows), with the library GEMM for the
     backbones."""
     from tris_moe_amd.configs import C2_MIXTRAL_PREFILL
 
@@ -630,9 +700,12 @@ def test_layer_mixtral_prefill_shape(tris, oracle_mod, cuda, tokens):
     assert_close(out, want, f"C2-shape layer T={tokens}")
 
 
-def test_layer_a3b_c3_with_shared_expert(tris, oracle_mod, cuda):
+@pytest.mark.parametrize("tokens", [1, 32, 1024])
+def test_layer_a3b_c3_with_shared_expert(tris, oracle_mod, cuda, tokens):
+    """C3: 256 experts, top-8, an always-on fp16 shared expert, N(0, 1.5) router
+    logits, at its three batches (1024 tokens: 8192 routed rows over nearly every expert)."""
     from tris_moe_amd.configs import C3_A3B
 
-    note("layer C3 A3B T=32")
-    out, want = _run_layer(tris, oracle_mod, cuda, C3_A3B, 32, 3000)
-    assert_close(out, want, "C3 layer")
+    note(f"layer C3 A3B T={tokens}")
+    out, want = _run_layer(tris, oracle_mod, cuda, C3_A3B, tokens, 3000 + tokens)
+    assert_close(out, want, f"C3 layer T={tokens}")

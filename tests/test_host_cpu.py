@@ -76,8 +76,8 @@ def test_c_abi_argument_errors_without_gpu(tris):
     assert lib.tris_backbone_workspace_bytes(4096, 64, 512) == 0  # one slice: no scratch
     rc = lib.tris_backbone_linear(None, 2, 4096, None, None, 512, None, ctypes.c_void_p(16), None, 0, None)
     assert rc == -1 and b"null input" in lib.tris_last_error()
-    rc = lib.tris_backbone_linear_pair(None, 2, 4096, None, ctypes.c_void_p(16), None, 512, ctypes.c_void_p(16),
-                                       ctypes.c_void_p(16), None, 0, None)
+    rc = lib.tris_backbone_linear_pair(None, 2, 4096, None, ctypes.c_void_p(16), None, 512, None, None,
+                                       ctypes.c_void_p(16), ctypes.c_void_p(16), None, 0, None)
     assert rc == -1 and b"null sv_b" in lib.tris_last_error()
 
 
@@ -284,3 +284,34 @@ def test_oracle_layer_against_float64(oracle_mod, tris):
     err = out - ref
     assert np.abs(err).max() < 2e-2
     assert np.linalg.norm(err) / np.linalg.norm(ref) < 1e-3
+
+
+def test_oracle_layer_input_scales(oracle_mod, tris):
+    """The oracle's ns_mode == 1 backbone input scales (qlinear_cuda.py:4477-4480): unit scales change nothing;
+    power-of-two scales (exact fp16 products) give the bits of the layer whose backbone columns carry the same
+    factors, so the scale sits on the input columns of the named projection; a scale on up instead of gate
+    changes the output."""
+    from tris_moe_amd.configs import MoELayerSpec
+
+    spec = MoELayerSpec("tiny", hidden=256, num_experts=4, intermediate=384, top_k=2, rank=128, tokens=(5,))
+    syn = tris["synthetic"]
+    layer = syn.make_layer(spec, 9, oracle_mod.gr_encode)
+    inp = syn.make_inputs(spec, 5, 10, layer["outlier_idx"])
+    w, sel = oracle_mod.route_topk(inp["router_logits"], spec.top_k, spec.renormalize)
+    x16 = inp["x"].astype(np.float16)
+    pl = {p: layer[p] for p in ("gate", "up", "down")}
+    bb = layer["backbones"]
+    plain = oracle_mod.moe_layer(x16, w, sel, pl, bb, spec.num_experts)
+    ones = {"gate": np.ones(spec.hidden, np.float16), "down": np.ones(spec.intermediate, np.float16)}
+    assert np.array_equal(oracle_mod.moe_layer(x16, w, sel, pl, bb, spec.num_experts, input_scales=ones), plain)
+    rng = np.random.default_rng(3)
+    p2 = {"gate": np.exp2(rng.integers(-2, 3, spec.hidden)).astype(np.float16),
+          "down": np.exp2(rng.integers(-2, 3, spec.intermediate)).astype(np.float16)}
+    scaled = oracle_mod.moe_layer(x16, w, sel, pl, bb, spec.num_experts, input_scales=p2)
+    bb2 = dict(bb, gate=(bb["gate"] * p2["gate"][None, :]).astype(np.float16),
+               down=(bb["down"] * p2["down"][None, :]).astype(np.float16))
+    assert np.array_equal(scaled, oracle_mod.moe_layer(x16, w, sel, pl, bb2, spec.num_experts))
+    assert not np.array_equal(scaled, plain)
+    on_up = oracle_mod.moe_layer(x16, w, sel, pl, bb, spec.num_experts, input_scales={"up": p2["gate"]})
+    assert not np.array_equal(on_up, oracle_mod.moe_layer(x16, w, sel, pl, bb, spec.num_experts,
+                                                           input_scales={"gate": p2["gate"]}))

@@ -112,3 +112,98 @@ def test_streamer_keeps_resident_layers(tris, cuda):
     torch.cuda.synchronize()
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     assert st.stats["copies"] == 2 and st.stats["hits"] == 2
+
+
+def _oracle_layer_check(oracle_mod, layer, x16, logits, got, spec, what):
+    """One streamed layer's output against the oracle layer on the same input (the chain's fp16 input)."""
+    w, sel = oracle_mod.route_topk(logits.cpu().numpy(), spec.top_k, spec.renormalize)
+    want = oracle_mod.bf16_round(oracle_mod.moe_layer(
+        x16.cpu().numpy(), w, sel, {p: layer[p] for p in streaming.PROJECTIONS}, layer["backbones"],
+        spec.num_experts, weight_caches=layer.setdefault("_oracle_cache", {"gate": {}, "up": {}, "down": {}})))
+    err = got.float().cpu().numpy().astype(np.float64) - want
+    max_abs = float(np.abs(err).max())
+    rel = float(np.linalg.norm(err) / np.linalg.norm(want))
+    assert max_abs <= 2e-2 and rel <= 1e-3, f"{what}: max_abs={max_abs:.3g} rel_l2={rel:.3g}"
+
+
+def _chain_against_oracle(oracle_mod, st, layers, x16, logits, spec, what, backbones=None):
+    """The streamed chain with the residual stream (so activations stay O(1) over the layers: without it they
+    shrink towards fp16 underflow); each layer's output against the oracle layer on that layer's input."""
+    outs, ins = [], []
+    streaming.streamed_forward(st, x16, logits, spec.top_k, spec.renormalize, spec.num_experts,
+                               backbones=backbones, outputs=outs, inputs=ins, residual=True)
+    torch.cuda.synchronize()
+    assert len(outs) == len(layers) == len(ins)
+    assert torch.equal(ins[0], x16)
+    for i, out in enumerate(outs):
+        assert float(out.float().abs().max()) > 6.2e-5, f"{what} layer {i}: output in the fp16 subnormal range"
+        _oracle_layer_check(oracle_mod, layers[i], ins[i], logits[i], out, spec, f"{what} layer {i}")
+        if i + 1 < len(ins):
+            assert torch.equal(ins[i + 1], (ins[i].float() + out.float()).to(torch.float16))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("slots,with_backbones", [(2, True), (1, False)])
+def test_streamed_chain_matches_oracle(tris, oracle_mod, cuda, slots, with_backbones):
+    """Every layer of a five-layer streamed chain against the oracle layer on the same input."""
+    print(f"streamed chain vs oracle slots={slots} backbones={with_backbones}", flush=True)
+    layers = _layers(tris, 5, seed0=700)
+    rng = np.random.default_rng(13)
+    T = 3
+    x16 = torch.from_numpy(rng.standard_normal((T, TINY.hidden)).astype(np.float16)).to(cuda)
+    logits = [torch.from_numpy(rng.standard_normal((T, TINY.num_experts)).astype(np.float32)).to(cuda) for _ in layers]
+    host = [{p: l[p] for p in streaming.PROJECTIONS} for l in layers]
+    st = streaming.GroupedPayloadStreamer(host, cuda, num_slots=slots,
+                                          backbones=[l["backbones"] for l in layers] if with_backbones else None)
+    resident_bb = None
+    if not with_backbones:
+        resident_bb = [{p: torch.from_numpy(l["backbones"][p]).to(cuda) for p in streaming.PROJECTIONS} for l in layers]
+    _chain_against_oracle(oracle_mod, st, layers, x16, logits, TINY, f"slots={slots}", backbones=resident_bb)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("p", [0.05, 0.15, 0.30])
+def test_streamed_mixtral_layers_match_oracle(tris, oracle_mod, cuda, p):
+    """C4 at its real layer shape: Mixtral-8x7B MoE layers (hidden 4096, 8 experts,
+    intermediate 14336, rank 512) at decode T = 8 with split-bitmap density p, streamed from pinned host memory
+    through two device slots (layers A, B, A: a slot mix-up changes the weights), every layer's output against
+    the oracle layer on the same input."""
+    from tris_moe_amd.configs import C4_STREAMING as SPEC
+
+    print(f"C4 streamed Mixtral layers p={p}", flush=True)
+    ext, syn = tris["ext"], tris["synthetic"]
+    a = syn.make_layer(SPEC, 4100, ext.gr_encode, gmap_p=p)
+    b = syn.make_layer(SPEC, 4200, ext.gr_encode, gmap_p=p)
+    layers = [a, b, a]
+    T = SPEC.tokens[0]
+    inp = syn.make_inputs(SPEC, T, 4300, a["outlier_idx"])
+    x16 = torch.from_numpy(inp["x"]).to(cuda).to(torch.bfloat16).to(torch.float16)
+    rng = np.random.default_rng(int(p * 100))
+    logits = [torch.from_numpy(rng.standard_normal((T, SPEC.num_experts)).astype(np.float32)).to(cuda)
+              for _ in layers]
+    host = [{q: l[q] for q in streaming.PROJECTIONS} for l in layers]
+    st = streaming.GroupedPayloadStreamer(host, cuda, num_slots=2, backbones=[l["backbones"] for l in layers])
+    _chain_against_oracle(oracle_mod, st, layers, x16, logits, SPEC, f"C4 p={p}")
+    assert st.stats["copies"] == 3 and st.stats["slot_reuses"] == 1
+
+
+@pytest.mark.gpu
+def test_prefetch_never_refills_an_acquired_slot(tris, cuda):
+    """A slot whose layer is acquired and not released is skipped by prefetch (its kernels may still read it);
+    with every slot held, prefetch raises."""
+    print("streamer held slots", flush=True)
+    layers = _layers(tris, 3, seed0=950)
+    host = [{p: l[p] for p in streaming.PROJECTIONS} for l in layers]
+    st = streaming.GroupedPayloadStreamer(host, cuda, num_slots=2)
+    st.prefetch(0)
+    st.acquire(0)
+    st.prefetch(1)
+    st.prefetch(2)        # round-robin would take slot 0 (layer 0, held): it takes slot 1 instead
+    assert st._where.get(0) == 0 and st._where.get(2) == 1 and 1 not in st._where
+    st.acquire(2)
+    with pytest.raises(RuntimeError, match="every slot"):
+        st.prefetch(1)
+    st.release(0)
+    assert st.prefetch(1) == 0
+    st.release(2)
+    torch.cuda.synchronize()
