@@ -276,6 +276,23 @@ int tris_backbone_linear_pair(const uint16_t* x, int32_t tokens, int32_t in_feat
                               const uint16_t* in_scale_b, uint16_t* out_a, uint16_t* out_b, void* workspace,
                               int64_t workspace_bytes, void* stream);
 
+/*
+ * tris_backbone_linear with no workspace argument and no allocation (no reference counterpart: for
+ * callers that cannot allocate, such as code under HIP graph capture or tight serving loops).  The split-K
+ * partial sums live in a file-scope device array of tris_backbone_noalloc_scratch_bytes() bytes (4 MiB,
+ * held by every GPU the library runs on until the process ends); its address is looked up once per device
+ * on the first call.  Every call on one GPU shares that GPU's array: calls that overlap on one GPU (on
+ * different streams, or from different threads) race.  Each launch writes every partial sum it reads, so
+ * no clearing is needed.  Shapes whose partial sums exceed the array are rejected with TRIS_ERR_INVALID.
+ * Same arguments and results (bit for bit) as tris_backbone_linear otherwise.
+ */
+int tris_backbone_linear_noalloc(const uint16_t* x, int32_t tokens, int32_t in_features, const int64_t* row_index,
+                                 const uint16_t* sv, int32_t rank, const uint16_t* in_scale, uint16_t* out,
+                                 void* stream);
+
+/* Size of the static scratch array of tris_backbone_linear_noalloc, in bytes. */
+int64_t tris_backbone_noalloc_scratch_bytes(void);
+
 /* Workspace sizes for tris_backbone_linear / _pair (no reference counterpart:
  * cuBLAS owns its workspace). */
 int64_t tris_backbone_pair_workspace_bytes(int32_t tokens, int32_t in_features, int32_t rank);

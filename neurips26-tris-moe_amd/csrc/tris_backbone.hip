@@ -24,6 +24,8 @@
 // pair in one launch).
 //
 // At decode (T <= 16) the projection is HBM-bound on SV (2*rank*in bytes).
+#include <mutex>
+
 #include "tris_common.h"
 
 namespace tris {
@@ -575,6 +577,62 @@ extern "C" int tris_backbone_linear(const uint16_t* x, int32_t tokens, int32_t i
                                     void* workspace, int64_t workspace_bytes, void* stream) {
   return launch_backbone(x, tokens, in_features, row_index, sv, nullptr, rank, in_scale, nullptr, out, nullptr,
                          workspace, workspace_bytes, stream, "tris_backbone_linear");
+}
+
+// ---- tris_backbone_linear_noalloc: the split-K partial sums in a file-scope device array instead of a
+// caller workspace, for callers that cannot allocate (code under HIP graph capture, tight serving loops).
+// The partial sums need slices * tokens * rank * 4 bytes; the slice count aims at kBbTargetWgs workgroups,
+// which keeps that at most about 32768 * 64 bytes (2 MiB) for every shape, so 4 MiB is never exceeded in
+// practice.  Every launch writes every partial sum it reads, so the array needs no clearing between calls.
+constexpr int64_t kNoAllocScratchBytes = 4ll << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mutex;
+static void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up once per device (each GPU holds its own copy of the
+// array at its own address; host code never passes the array's name itself to a kernel).
+static int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) {
+    set_error("tris_backbone_linear_noalloc: hipGetDevice: %s", hipGetErrorString(err));
+    return TRIS_ERR_HIP;
+  }
+  TRIS_REQUIRE(dev >= 0 && dev < kMaxDevices, "tris_backbone_linear_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr) {
+      set_error("tris_backbone_linear_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(err));
+      return TRIS_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return TRIS_OK;
+}
+
+extern "C" int64_t tris_backbone_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int tris_backbone_linear_noalloc(const uint16_t* x, int32_t tokens, int32_t in_features,
+                                           const int64_t* row_index, const uint16_t* sv, int32_t rank,
+                                           const uint16_t* in_scale, uint16_t* out, void* stream) {
+  TRIS_REQUIRE(tokens >= 0 && in_features >= 0 && rank >= 0, "tris_backbone_linear_noalloc: negative shape");
+  const int64_t need = backbone_workspace_bytes(tokens, in_features, rank, 1);
+  TRIS_REQUIRE(need <= kNoAllocScratchBytes,
+               "tris_backbone_linear_noalloc: %d tokens x %d rank need %lld bytes of scratch, the static buffer "
+               "holds %lld (use tris_backbone_linear with a workspace)",
+               tokens, rank, static_cast<long long>(need), static_cast<long long>(kNoAllocScratchBytes));
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_address(&ws);
+    if (rc) return rc;
+  }
+  return launch_backbone(x, tokens, in_features, row_index, sv, nullptr, rank, in_scale, nullptr, out, nullptr, ws,
+                         need, stream, "tris_backbone_linear_noalloc");
 }
 
 extern "C" int tris_backbone_linear_pair(const uint16_t* x, int32_t tokens, int32_t in_features,
