@@ -158,6 +158,38 @@ int tris_grouped_dual_forward_block_gr(const uint16_t* hidden_a, const uint16_t*
                                        uint16_t* output_b, void* stream);
 
 /*
+ * Grouped expert GEMM for decode-sized row tiles with the block-GR split bitmap decoded inside the kernel, on
+ * MFMA: the reference's compact3_tris_precomputed_grouped_forward_block_gr (TriSMoE_cuda.cpp:1018-1063) for
+ * rows gathered through an index (no reference counterpart as one call: the reference gathers with
+ * index_select first, modeling_mixtral.py:475-476).  output[r, n] = fp16(sum_k hidden[row(r), k] * W_e[n, k]
+ * (* output_scale[e, n]) (+ bias[e, n])) for every row r of segment s, e = expert_ids[s] (e outside
+ * [0, num_experts): zero rows); row(r) = row_index[r] when row_index is given (an index outside
+ * [0, hidden_rows) reads row 0), else r.  hidden fp16 [hidden_rows, rank], 16-byte aligned; output fp16
+ * [batch, N]: rows inside segments are written, others untouched.  The payload needs the GR stream, uniform
+ * 64-column groups and rank a multiple of 256 up to 512 (else TRIS_ERR_INVALID).  Rows are taken in tiles of
+ * 16 per segment, so the kernel suits decode (few rows per segment); prefill-sized segments belong to the
+ * predecoded MFMA entries.
+ */
+int tris_grouped_decode_forward_block_gr(const uint16_t* hidden, const int64_t* row_index, int32_t hidden_rows,
+                                         int32_t batch, const int32_t* expert_ids, const int32_t* segment_offsets,
+                                         int32_t num_segments, const tris_compact3_payload* payload, uint16_t* output,
+                                         void* stream);
+
+/*
+ * Gate and up projections of the same routed rows in one launch with in-kernel GR decode: replaces
+ * compact3_tris_precomputed_grouped_dual_forward_block_gr (TriSMoE_cuda.cpp:1065-1136) for decode-sized row
+ * tiles.  swiglu == 0: output_a / output_b receive the two projections as tris_grouped_decode_forward_block_gr
+ * would; swiglu != 0: output_a receives fp16(fp16(silu(g)) * u) of the two fp16 outputs (act_fn(gate_out) *
+ * up_out, modeling_mixtral.py:496) and output_b is not used.  Both payloads must have one shape.
+ */
+int tris_grouped_decode_pair_forward_block_gr(const uint16_t* hidden_a, const uint16_t* hidden_b,
+                                              const int64_t* row_index, int32_t hidden_rows, int32_t batch,
+                                              const int32_t* expert_ids, const int32_t* segment_offsets,
+                                              int32_t num_segments, const tris_compact3_payload* payload_a,
+                                              const tris_compact3_payload* payload_b, uint16_t* output_a,
+                                              uint16_t* output_b, int32_t swiglu, void* stream);
+
+/*
  * Decode every GR block of the listed experts: replaces
  * compact3_tris_precomputed_grouped_block_gr_predecode (TriSMoE_cuda.cpp:836-853,
  * kernel.cu:4683-4718, host :8980-9029).  decoded int32 [num_active, nblk, 128];

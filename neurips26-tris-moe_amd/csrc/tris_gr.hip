@@ -5,9 +5,9 @@
 // thread 0.  Here a workgroup builds the byte decode table in LDS once, then
 // every group of S lanes decodes one block (tris_gr_span.h), so a 256-lane
 // workgroup decodes 256/S blocks at once; the decoded words leave LDS as
-// coalesced stores.  Work per block does not depend on S; more lanes per block
-// shorten each lane's serial span (latency), fewer cut the shuffle steps, so S
-// is chosen from the block count.
+// coalesced stores.  Work per block hardly depends on S; more lanes per block
+// shorten each lane's walk (latency), fewer cut the scan steps, so S is chosen
+// from the block count.
 #include "tris_gr_span.h"
 #include "tris_moe_hip.h"
 
@@ -38,7 +38,7 @@ template <int S>
 __global__ __launch_bounds__(kSpanThreads) void gr_decode_span_kernel(GrJobs jobs, const int32_t* __restrict__ expert_ids) {
   constexpr int kBlocksPerWg = kSpanThreads / S;
   __shared__ GrTables tab;
-  __shared__ uint32_t outb[kBlocksPerWg][kGrWords];
+  __shared__ uint32_t outb[kBlocksPerWg][kGrBlockStride];
   const GrJob& jb = jobs.job[blockIdx.z];
   const int slot = blockIdx.y;
   const int block0 = blockIdx.x * kBlocksPerWg;
@@ -55,14 +55,18 @@ __global__ __launch_bounds__(kSpanThreads) void gr_decode_span_kernel(GrJobs job
                   evalid ? jb.offsets + static_cast<int64_t>(expert) * (nblk + 1) : nullptr,
                   evalid ? jb.meta + static_cast<int64_t>(expert) * nblk : nullptr, block, evalid && block < nblk, j);
   gr_tables_to_lds(&tab);
-  for (int idx = tid; idx < kBlocksPerWg * kGrWords; idx += kSpanThreads) outb[idx / kGrWords][idx % kGrWords] = 0u;
+  for (int idx = tid; idx < kBlocksPerWg * kGrBlockStride; idx += kSpanThreads) {
+    outb[idx / kGrBlockStride][idx % kGrBlockStride] = 0u;
+  }
   __syncthreads();
-  gr_decode_block_group<S>(sp, &tab, outb[g], j);
+  gr_decode_block_group<S>(sp, &tab, outb[g] + kGrPadFront, j);
   __syncthreads();
   if (jb.dense_rows == 0) {
     int32_t* dst = jb.out + (static_cast<int64_t>(slot) * nblk + block0) * kGrWords;
     for (int idx = tid; idx < kBlocksPerWg * kGrWords; idx += kSpanThreads) {
-      if (block0 + idx / kGrWords < nblk) dst[idx] = static_cast<int32_t>(outb[idx / kGrWords][idx % kGrWords]);
+      if (block0 + idx / kGrWords < nblk) {
+        dst[idx] = static_cast<int32_t>(outb[idx / kGrWords][kGrPadFront + idx % kGrWords]);
+      }
     }
   } else {
     int32_t* dst = jb.out + static_cast<int64_t>(slot) * jb.dense_rows * jb.dense_cols;
@@ -73,7 +77,7 @@ __global__ __launch_bounds__(kSpanThreads) void gr_decode_span_kernel(GrJobs job
       const int row = (b / jb.num_out_blocks) * kGrPackedRows + w / kTileOut;
       const int col = (b % jb.num_out_blocks) * kTileOut + w % kTileOut;
       if (row < jb.dense_rows && col < jb.dense_cols) {
-        dst[static_cast<int64_t>(row) * jb.dense_cols + col] = static_cast<int32_t>(outb[idx / kGrWords][w]);
+        dst[static_cast<int64_t>(row) * jb.dense_cols + col] = static_cast<int32_t>(outb[idx / kGrWords][kGrPadFront + w]);
       }
     }
   }
@@ -105,14 +109,10 @@ int launch_gr_jobs(const GrJobs& jobs, int num_jobs, const int32_t* expert_ids, 
   TRIS_REQUIRE(expert_ids != nullptr, "%s: null expert ids", who);
   TRIS_REQUIRE(num_slots <= 65535, "%s: too many experts (%d)", who, num_slots);
   // lanes per block: more lanes shorten each block's walk, fewer spread the per-workgroup table copy
-  // over more blocks (measured on MI355X at the Mixtral shapes: 8192 blocks S = 32 14.1 us vs S = 8
-  // 19.7 us; 32768 blocks S = 16 30.7 us vs S = 8 36.0 us and S = 32 36.1 us)
-  const int S = total > 65536 ? 8 : (total > 8192 ? 16 : 32);
+  // over more blocks
+  const int S = total > 8192 ? 16 : 32;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (S == 8) {
-    hipLaunchKernelGGL((gr_decode_span_kernel<8>), dim3(ceil_div(max_nblk, kSpanThreads / 8), num_slots, num_jobs),
-                       dim3(kSpanThreads), 0, s, jobs, expert_ids);
-  } else if (S == 16) {
+  if (S == 16) {
     hipLaunchKernelGGL((gr_decode_span_kernel<16>), dim3(ceil_div(max_nblk, kSpanThreads / 16), num_slots, num_jobs),
                        dim3(kSpanThreads), 0, s, jobs, expert_ids);
   } else {

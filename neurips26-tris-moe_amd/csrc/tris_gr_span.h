@@ -11,37 +11,49 @@
 // Decoding state at any bit is s in [0, k]: 0 = reading unary bits, s > 0 =
 // s remainder bits still to read.  For k in {1, 2, 3} two tables describe one
 // byte of stream:
-//   step[k][byte]    four 16-bit slots, slot s = the transition from entry
-//                    state s: s' | n << 2 | dF << 6 (n codewords completed,
-//                    dF added to F); slots above k are the identity;
-//   mask[k][s][byte] the completed ones as a bit mask, bit i = a one at
-//                    F(byte start) - 1 + i (a codeword entered mid-remainder
-//                    whose last bits are zero ends at bit 0).
-// Because step is indexed by the byte alone, following all k + 1 entry states
-// through a span costs table reads that do not wait on each other.  Each lane
-// of the block's group of S lanes:
-//   A. runs its span from every entry state, giving per entry state the exit
-//      state, the F advance and the completed-codeword count;
-//   B. learns its true entry state by chaining the exit states of the lanes
-//      before it, and its starting F by a segmented prefix sum;
-//   C. runs its span again from the true state, OR-ing the decoded ones into
-//      the block's 128-word LDS bitmap.
-// k = 0 streams are the bitmap itself (each codeword is run zeros then a one)
-// and are copied.  Raw blocks are copied.  k >= 4, streams longer than 128
-// words (the encoder stores those raw), and any stream whose completed
-// codewords do not equal one_count or reach past bit 4095, are decoded by the
-// group's first lane with the reference's serial rules, so every input
-// decodes as the reference decodes it.
+//   next[k][byte]       four 4-bit fields, field s = 4 * (state after the
+//                       byte from entry state s); identity above k;
+//   entry[k][s][byte]   the completed ones as a bit mask (bits 0..40, bit i =
+//                       a one at F(byte start) - 1 + i; a codeword entered
+//                       mid-remainder whose last bits are zero ends at bit 0),
+//                       the F advance (bits 41..47) and the number of
+//                       completed codewords (bits 57..60).
+// Each lane of the block's group of S lanes:
+//   A. reads next[] for every byte of its span (loads that do not wait on
+//      each other) and composes them into its exit-state map;
+//   B. learns its true entry state from a log-step scan that composes the
+//      maps of the lanes before it;
+//   C. walks its bytes from the true state with one bit-field extract per
+//      byte, so every entry[] load is independent of the others, sums the F
+//      advances and codeword counts (a packed segmented prefix sum gives its
+//      starting F and the block's count), and ORs each byte's mask into the
+//      block's LDS bitmap at its F.
+// The bitmap has a zero pad word before it and three after it: a one at a
+// position past 4095 lands in the back pads (the reference stops there), and
+// the decode falls back to the serial rules.  k = 0 streams are the bitmap
+// itself (each codeword is run zeros then a one) and are copied.  Raw blocks
+// are copied.  k >= 4, streams longer than 128 words (the encoder stores
+// those raw), and any stream whose completed codewords do not equal one_count
+// or reach past bit 4095, are decoded by the group's first lane with the
+// reference's serial rules, so every input decodes as the reference decodes
+// it.
 #pragma once
 
 #include "tris_common.h"
 
 namespace tris {
 
-constexpr int kGrStepEntries = 3 * 256;            // k = 1, 2, 3; byte
-constexpr int kGrMaskEntries = (2 + 3 + 4) * 256;  // k = 1, 2, 3; s in [0, k]; byte
+constexpr int kGrEntryStates = 2 + 3 + 4;                     // k = 1, 2, 3; s in [0, k]
+constexpr int kGrEntries = kGrEntryStates * 256 + 1;             // + one all-zero entry
+constexpr uint32_t kGrZeroEntryOffset = kGrEntryStates * 256 * 8;  // byte offset of the zero entry
+constexpr uint32_t kGrIdentityNext = 0xC840u;                    // field s = 4 * s
 
-__host__ __device__ constexpr int gr_mask_base(int k) { return k == 1 ? 0 : (k == 2 ? 512 : 1280); }
+// Decoded-block layout in LDS: a pad word, the 128 bitmap words, three pad words.
+constexpr int kGrPadFront = 1;
+constexpr int kGrPadBack = 3;
+constexpr int kGrBlockStride = kGrPadFront + kGrWords + kGrPadBack;
+
+__host__ __device__ constexpr int gr_entry_base(int k) { return k == 1 ? 0 : (k == 2 ? 512 : 1280); }
 
 struct GrByteStep {
   uint32_t state;
@@ -78,25 +90,26 @@ __host__ __device__ constexpr GrByteStep gr_byte_step(int k, int st, int byte) {
 }
 
 struct alignas(16) GrTables {
-  uint64_t step[kGrStepEntries];
-  uint64_t mask[kGrMaskEntries];
+  uint64_t entry[kGrEntries + 1];  // (k, s, byte); then the zero entry and one pad entry
+  uint16_t next[3 * 256];          // (k, byte)
 };
 
 constexpr GrTables gr_make_tables() {
   GrTables t{};
   for (int k = 1; k <= 3; ++k) {
     for (int byte = 0; byte < 256; ++byte) {
-      uint64_t packed = 0;
+      uint32_t fields = 0;
       for (int s = 0; s < 4; ++s) {
-        uint64_t slot = static_cast<uint64_t>(s);
+        uint32_t nx = static_cast<uint32_t>(s);
         if (s <= k) {
           const GrByteStep r = gr_byte_step(k, s, byte);
-          slot = r.state | (r.count << 2) | (r.advance << 6);
-          t.mask[gr_mask_base(k) + s * 256 + byte] = r.mask;
+          nx = r.state;
+          t.entry[gr_entry_base(k) + s * 256 + byte] =
+              r.mask | (static_cast<uint64_t>(r.advance) << 41) | (static_cast<uint64_t>(r.count) << 57);
         }
-        packed |= slot << (16 * s);
+        fields |= (4u * nx) << (4 * s);
       }
-      t.step[(k - 1) * 256 + byte] = packed;
+      t.next[(k - 1) * 256 + byte] = static_cast<uint16_t>(fields);
     }
   }
   return t;
@@ -104,6 +117,7 @@ constexpr GrTables gr_make_tables() {
 
 __constant__ GrTables kGrTables = gr_make_tables();
 constexpr int kGrTableVec4 = static_cast<int>(sizeof(GrTables) / 16);
+static_assert(sizeof(GrTables) % 16 == 0, "GrTables is copied as 16-byte vectors");
 
 // Copy the tables into LDS (all threads of the workgroup; a barrier must follow).
 __device__ inline void gr_tables_to_lds(GrTables* dst) {
@@ -139,20 +153,58 @@ __device__ inline void gr_serial_decode(const int32_t* __restrict__ payload, int
   }
 }
 
-// Segmented (groups of S lanes) inclusive prefix sum.
-template <int S>
-__device__ __forceinline__ int group_incl_sum(int v, int j) {
-#pragma unroll
-  for (int d = 1; d < S; d <<= 1) {
-    const int u = __shfl_up(v, d);
-    if (j >= d) v += u;
-  }
+// Group scans over S = 16 or 32 lanes (one or two DPP rows of a wavefront) with DPP row shifts and the
+// row-15 broadcast: register moves between lanes, no LDS round trips.  Lanes whose source lies outside their
+// row take `identity`.  Every lane of a group must be active.
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t identity, uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(static_cast<int>(identity), static_cast<int>(v), Ctrl, RowMask, 0xF, false));
+}
+
+// Inclusive scan: op(own, earlier) combines a lane's value with the combined value of lanes before it.
+template <int S, typename Op>
+__device__ __forceinline__ uint32_t group_scan(uint32_t v, uint32_t identity, Op op) {
+  static_assert(S == 16 || S == 32, "DPP group scans span one or two rows");
+  v = op(v, dpp_mov<0x111, 0xF>(identity, v));  // row_shr:1
+  v = op(v, dpp_mov<0x112, 0xF>(identity, v));  // row_shr:2
+  v = op(v, dpp_mov<0x114, 0xF>(identity, v));  // row_shr:4
+  v = op(v, dpp_mov<0x118, 0xF>(identity, v));  // row_shr:8
+  if constexpr (S == 32) v = op(v, dpp_mov<0x142, 0xA>(identity, v));  // row_bcast:15 into rows 1 and 3
   return v;
 }
 
 template <int S>
-__device__ __forceinline__ int group_last(int v) {
-  return __shfl(v, (static_cast<int>(__lane_id()) / S) * S + S - 1);
+__device__ __forceinline__ uint32_t group_incl_sum(uint32_t v) {
+  return group_scan<S>(v, 0u, [](uint32_t own, uint32_t earlier) { return own + earlier; });
+}
+
+// The value of the group's last lane, in every lane of the group.
+template <int S>
+__device__ __forceinline__ uint32_t group_last(uint32_t v) {
+  static_assert(S == 16 || S == 32, "groups of 16 or 32 lanes");
+  const int g = static_cast<int>(__lane_id()) / S;
+  if constexpr (S == 32) {
+    const uint32_t a = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 31));
+    const uint32_t b = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+    return g == 0 ? a : b;
+  } else {
+    const uint32_t a = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 15));
+    const uint32_t b = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 31));
+    const uint32_t c = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 47));
+    const uint32_t d = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+    return g == 0 ? a : (g == 1 ? b : (g == 2 ? c : d));
+  }
+}
+
+// Composition of 4-state maps in the next[] field encoding (field s = 4 * image of s): first `earlier`, then
+// `own`.
+__device__ __forceinline__ uint32_t gr_map_compose(uint32_t own, uint32_t earlier) {
+  const uint32_t n0 = __builtin_amdgcn_ubfe(own, earlier & 15u, 4);
+  const uint32_t n1 = __builtin_amdgcn_ubfe(own, (earlier >> 4) & 15u, 4);
+  const uint32_t n2 = __builtin_amdgcn_ubfe(own, (earlier >> 8) & 15u, 4);
+  const uint32_t n3 = __builtin_amdgcn_ubfe(own, (earlier >> 12) & 15u, 4);
+  return n0 | (n1 << 4) | (n2 << 8) | (n3 << 12);
 }
 
 // One block's stream as seen by lane j of its group: the block header and the
@@ -200,12 +252,15 @@ __device__ __forceinline__ void gr_span_load(GrSpan<S>& sp, const int32_t* __res
 
 // Decode one block by the S lanes of a group (j = lane within the group; all S
 // lanes of the group call together, groups of a wave may decode different
-// blocks).  out: the block's 128-word LDS bitmap, already zero and visible to
-// the wave.  A wave-level LDS sync must follow before out is read.
+// blocks).  out: the block's 128-word LDS bitmap with kGrPadFront words before
+// it and kGrPadBack after it, all zero and visible to the wave.  A wave-level
+// LDS sync must follow before out is read; the pads are left dirty.
 template <int S>
 __device__ inline void gr_decode_block_group(const GrSpan<S>& sp, const GrTables* __restrict__ tab, uint32_t* out,
                                              int j) {
+  static_assert(S == 16 || S == 32, "span decoder groups are 16 or 32 lanes");
   constexpr int kMaxWords = GrSpan<S>::kMaxWords;
+  constexpr int kBytes = 4 * kMaxWords;
   const int wc = sp.word_count;
   if (wc <= 0) return;
   const int k = sp.meta & kMetaKMask;
@@ -225,10 +280,10 @@ __device__ inline void gr_decode_block_group(const GrSpan<S>& sp, const GrTables
   bool serial = k > 3 || wc > kGrWords;
   if (!serial && k == 0) {
     // The stream is the bitmap; it decodes as itself iff it holds exactly one_count ones.
-    int ones = 0;
+    uint32_t ones = 0u;
 #pragma unroll
-    for (int i = 0; i < kMaxWords; ++i) ones += __popc(sp.w[i]);
-    serial = group_last<S>(group_incl_sum<S>(ones, j)) != one_count;
+    for (int i = 0; i < kMaxWords; ++i) ones += static_cast<uint32_t>(__popc(sp.w[i]));
+    serial = static_cast<int>(group_last<S>(group_incl_sum<S>(ones))) != one_count;
     if (!serial) {
 #pragma unroll
       for (int i = 0; i < kMaxWords; ++i) {
@@ -236,113 +291,80 @@ __device__ inline void gr_decode_block_group(const GrSpan<S>& sp, const GrTables
       }
     }
   } else if (!serial) {
-    const uint64_t* step = tab->step + (k - 1) * 256;
-    const uint64_t* mtab = tab->mask + gr_mask_base(k);
-    // ---- A: every entry state through the span
-    uint32_t cur[4] = {0u, 1u, 2u, 3u};
-    int df[4] = {0, 0, 0, 0};
-    int nc[4] = {0, 0, 0, 0};
+    const uint16_t* __restrict__ nxt = tab->next + (k - 1) * 256;
+    const char* __restrict__ ent = reinterpret_cast<const char*>(tab->entry + gr_entry_base(k));
+    const int nbytes = 4 * sp.nw;
+    // ---- A: next-state fields of every byte, composed from every entry state
+    uint32_t nsv[kBytes];
+    uint32_t c0 = 0u, c1 = 4u, c2 = 8u, c3 = 12u;
 #pragma unroll
-    for (int i = 0; i < kMaxWords; ++i) {
-      if (i < sp.nw) {
-        const uint32_t word = sp.w[i];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const uint64_t t = step[(word >> (8 * b)) & 0xFFu];
-#pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            const uint32_t slot = static_cast<uint32_t>(t >> (cur[s] << 4));
-            cur[s] = slot & 3u;
-            nc[s] += static_cast<int>((slot >> 2) & 15u);
-            df[s] += static_cast<int>((slot >> 6) & 127u);
-          }
-        }
-      }
+    for (int i = 0; i < kBytes; ++i) {
+      const uint32_t byte = (sp.w[i / 4] >> (8 * (i % 4))) & 0xFFu;
+      const uint32_t e = nxt[byte];
+      nsv[i] = i < nbytes ? e : kGrIdentityNext;
+      c0 = __builtin_amdgcn_ubfe(nsv[i], c0, 4);
+      c1 = __builtin_amdgcn_ubfe(nsv[i], c1, 4);
+      c2 = __builtin_amdgcn_ubfe(nsv[i], c2, 4);
+      c3 = __builtin_amdgcn_ubfe(nsv[i], c3, 4);
     }
-    const int exit_map = static_cast<int>(cur[0] | (cur[1] << 2) | (cur[2] << 4) | (cur[3] << 6));
-    // ---- B: true entry state (chain over the group), then prefix sums
-    int entry = 0;
+    // ---- B: the map of lanes 0..j, then the previous lane's (wave_shr:1) applied to state 0
+    const uint32_t map = group_scan<S>(c0 | (c1 << 4) | (c2 << 8) | (c3 << 12), kGrIdentityNext, gr_map_compose);
+    const uint32_t prev_map = dpp_mov<0x138, 0xF>(kGrIdentityNext, map);
+    uint32_t st = j == 0 ? 0u : (prev_map & 15u);  // 4 * true entry state
+    // ---- C: entries along the true path; F advance and codeword count, packed adv | count << 16
+    uint32_t mlo[kBytes], mhi[kBytes];
+    uint32_t packed = 0u;
 #pragma unroll
-    for (int t = 1; t < S; ++t) {
-      const int prev_entry = __shfl_up(entry, 1);
-      const int prev_map = __shfl_up(exit_map, 1);
-      if (j == t) entry = (prev_map >> (2 * prev_entry)) & 3;
+    for (int i = 0; i < kBytes; ++i) {
+      const uint32_t byte = (sp.w[i / 4] >> (8 * (i % 4))) & 0xFFu;
+      const uint32_t off = i < nbytes ? (st << 9) + (byte << 3) : kGrZeroEntryOffset - gr_entry_base(k) * 8u;
+      st = __builtin_amdgcn_ubfe(nsv[i], st, 4);
+      const uint2 e = *reinterpret_cast<const uint2*>(ent + off);
+      mlo[i] = e.x;
+      mhi[i] = e.y;
+      packed += e.y >> 9;
     }
-    int my_df = df[0], my_nc = nc[0];
-#pragma unroll
-    for (int s = 1; s < 4; ++s) {
-      if (entry == s) {
-        my_df = df[s];
-        my_nc = nc[s];
-      }
-    }
-    const int incl_df = group_incl_sum<S>(my_df, j);
-    const int total_nc = group_last<S>(group_incl_sum<S>(my_nc, j));
-    // Completed codewords must number one_count: then they are exactly the
-    // reference's first one_count codewords, and whatever follows is padding.
-    serial = total_nc != one_count;
+    const uint32_t incl = group_incl_sum<S>(packed);
+    const int total = static_cast<int>(group_last<S>(incl) >> 16);
+    serial = total != one_count;
     if (!serial) {
-      // ---- C: emission from the true entry state
-      int pos = incl_df - my_df - 1;  // F at the span start, minus 1: mask bit 0's position
-      uint32_t state = static_cast<uint32_t>(entry);
-      uint32_t acc0 = 0u, acc1 = 0u, acc2 = 0u;  // bitmap words [aw, aw + 3)
-      int aw = pos >> 5;                         // -1 only at the block start
-      bool overflow = false;
+      // bit position + 32 of the lane's first mask bit 0 (F at the span start - 1, biased past the front pad)
+      uint32_t posb = ((incl - packed) & 0xFFFFu) + 31u;
+      uint32_t* base = out - kGrPadFront;
+      // OR a mask (< 2^64) whose bit 0 is at posb - 32 into the bitmap; word 129 and up are the back pads,
+      // where only positions past 4095 land
+      const auto emit = [&](uint64_t m, bool third) {
+        const uint32_t rel = posb & 31u;
+        const uint32_t widx = (posb >> 5) < 129u ? (posb >> 5) : 129u;
+        const uint64_t v = m << rel;
+        atomicOr(&base[widx], static_cast<uint32_t>(v));
+        atomicOr(&base[widx + 1], static_cast<uint32_t>(v >> 32));
+        if (third) atomicOr(&base[widx + 2], static_cast<uint32_t>((m >> 32) << rel >> 32));
+      };
+      if (k <= 2) {
+        // k <= 2: a byte's mask is below 2^25 and its advance at most 32, so two bytes fit one 64-bit mask
 #pragma unroll
-      for (int i = 0; i < kMaxWords; ++i) {
-        if (i < sp.nw) {
-          const uint32_t word = sp.w[i];
+        for (int i = 0; i < kBytes; i += 2) {
+          const uint32_t a0 = __builtin_amdgcn_ubfe(mhi[i], 9, 7);
+          const uint64_t m = (static_cast<uint64_t>(mhi[i] & 0x1FFu) << 32 | mlo[i]) |
+                             (static_cast<uint64_t>(mlo[i + 1]) << a0);
+          emit(m, true);
+          posb += a0 + __builtin_amdgcn_ubfe(mhi[i + 1], 9, 7);
+        }
+      } else {
 #pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            const uint32_t byte = (word >> (8 * b)) & 0xFFu;
-            const uint64_t mask = mtab[(state << 8) | byte];
-            const uint32_t slot = static_cast<uint32_t>(step[byte] >> (state << 4));
-            state = slot & 3u;
-            // 0 <= rel < 32 and mask bits < 41 keep every bit inside the 3-word window
-            const int rel = pos - (aw << 5);
-            const uint64_t lo = mask << rel;
-            const uint32_t hi = rel == 0 ? 0u : static_cast<uint32_t>(mask >> (64 - rel));
-            acc0 |= static_cast<uint32_t>(lo);
-            acc1 |= static_cast<uint32_t>(lo >> 32);
-            acc2 |= hi;
-            pos += static_cast<int>((slot >> 6) & 127u);
-            // advance <= 64 moves pos by at most two words; words below pos are final
-#pragma unroll
-            for (int f = 0; f < 2; ++f) {
-              if (pos - (aw << 5) >= 32) {
-                if (acc0 != 0u) {
-                  if (aw >= 0 && aw < kGrWords) {
-                    atomicOr(&out[aw], acc0);
-                  } else {
-                    overflow = true;
-                  }
-                }
-                acc0 = acc1;
-                acc1 = acc2;
-                acc2 = 0u;
-                ++aw;
-              }
-            }
-          }
+        for (int i = 0; i < kBytes; ++i) {
+          emit(static_cast<uint64_t>(mhi[i] & 0x1FFu) << 32 | mlo[i], true);
+          posb += __builtin_amdgcn_ubfe(mhi[i], 9, 7);
         }
       }
-      const uint32_t rest[3] = {acc0, acc1, acc2};
-#pragma unroll
-      for (int i = 0; i < 3; ++i) {
-        if (rest[i] != 0u) {
-          if (aw + i >= 0 && aw + i < kGrWords) {
-            atomicOr(&out[aw + i], rest[i]);
-          } else {
-            overflow = true;
-          }
-        }
-      }
-      // A one at position >= 4096: the reference stops there (and drops later
-      // ones); fall back to its serial rules.
-      const uint64_t any_overflow = __ballot(overflow);
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      const uint32_t pad = j < kGrPadBack ? out[kGrWords + j] : 0u;
+      const uint64_t hit = __ballot(pad != 0u);
       const uint64_t group_mask = (S == 64 ? ~0ull : ((1ull << S) - 1ull))
                                   << ((static_cast<int>(__lane_id()) / S) * S);
-      serial = (any_overflow & group_mask) != 0ull;
+      serial = (hit & group_mask) != 0ull;
       if (serial) {
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();

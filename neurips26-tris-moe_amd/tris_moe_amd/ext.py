@@ -501,6 +501,76 @@ def compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded_hybrid(
 
 
 # ---------------------------------------------- verification / helper entry points
+# ------------------------------------------------------------------ in-kernel-decode MFMA GEMMs (decode sizes)
+def decode_payload_ok(p: dict) -> bool:
+    """The payload suits the decode kernels: the GR stream, uniform 64-column groups, no sparse-only form, and
+    rank a multiple of 256 up to 512."""
+    rank = int(p["g_idx"].size(1))
+    return bool(p.get("_compact3_k64_groups_uniform", False)) and rank % 256 == 0 and 0 < rank <= 512 and \
+        p.get("q_gmap_gr_words") is not None
+
+
+def _decode_struct(p: dict, device):
+    rank = int(p["g_idx"].size(1))
+    bias = p["bias"] if p.get("has_bias") else None
+    return make_payload_struct(rank, p["qweight1"], p["qweight2_sparse"], p["qweight2_sparse_prefix"],
+                               p["q_gmap_gr_words"], p["q_gmap_gr_offsets"], p["q_gmap_gr_meta"], p["c_map"],
+                               p["g_idx"], p["col_pack3"], p["row_pack3"], p["output_scale"],
+                               bool(p.get("has_output_scale", False)), bias, bool(p.get("has_bias", False)),
+                               bool(p.get("_compact3_k64_groups_uniform", False)), device, who="decode payload")
+
+
+def _decode_route_args(hidden, expert_ids, segment_offsets, row_index, batch):
+    dev = hidden.device
+    _check_cuda("hidden", hidden, torch.float16, 2, dev)
+    _check_cuda("expert_ids", expert_ids, torch.int32, 1, dev)
+    _check_cuda("segment_offsets", segment_offsets, torch.int32, 1, dev)
+    if segment_offsets.numel() != expert_ids.numel() + 1:
+        raise RuntimeError("segment_offsets must hold segments + 1 entries")
+    if row_index is not None:
+        _check_cuda("row_index", row_index, torch.int64, 1, dev)
+        if row_index.numel() != batch:
+            raise RuntimeError("row_index must hold one entry per grouped row")
+    elif int(hidden.size(0)) != batch:
+        raise RuntimeError("without row_index hidden must hold one row per grouped row")
+
+
+def grouped_decode_forward(hidden: torch.Tensor, payload: dict, expert_ids: torch.Tensor,
+                           segment_offsets: torch.Tensor, batch: int, row_index: torch.Tensor | None = None,
+                           out: torch.Tensor | None = None) -> torch.Tensor:
+    """tris_grouped_decode_forward_block_gr: fp16 [batch, N] of the grouped rows (rows outside every segment
+    left as they are in ``out``)."""
+    _decode_route_args(hidden, expert_ids, segment_offsets, row_index, batch)
+    st = _decode_struct(payload, hidden.device)
+    out = _out_buffer(out, batch, st.outfeatures, hidden.device)
+    _lib.check(_lib.load().tris_grouped_decode_forward_block_gr(
+        _ptr(hidden), _ptr(row_index), int(hidden.size(0)), batch, _ptr(expert_ids), _ptr(segment_offsets),
+        int(expert_ids.numel()), ctypes.byref(st), _ptr(out), _stream(hidden)), "tris_grouped_decode_forward_block_gr")
+    return out
+
+
+def grouped_decode_pair_forward(hidden_a: torch.Tensor, hidden_b: torch.Tensor, payload_a: dict, payload_b: dict,
+                                expert_ids: torch.Tensor, segment_offsets: torch.Tensor, batch: int,
+                                row_index: torch.Tensor | None = None, swiglu: bool = False, out_a=None, out_b=None):
+    """tris_grouped_decode_pair_forward_block_gr: (out_a, out_b) fp16 [batch, N], or with swiglu one output
+    fp16(silu(g) * u)."""
+    _decode_route_args(hidden_a, expert_ids, segment_offsets, row_index, batch)
+    _check_cuda("hidden_b", hidden_b, torch.float16, 2, hidden_a.device)
+    if hidden_b.shape != hidden_a.shape:
+        raise RuntimeError("hidden_a and hidden_b must have one shape")
+    sa = _decode_struct(payload_a, hidden_a.device)
+    sb = _decode_struct(payload_b, hidden_a.device)
+    out_a = _out_buffer(out_a, batch, sa.outfeatures, hidden_a.device)
+    if not swiglu:
+        out_b = _out_buffer(out_b, batch, sb.outfeatures, hidden_a.device)
+    _lib.check(_lib.load().tris_grouped_decode_pair_forward_block_gr(
+        _ptr(hidden_a), _ptr(hidden_b), _ptr(row_index), int(hidden_a.size(0)), batch, _ptr(expert_ids),
+        _ptr(segment_offsets), int(expert_ids.numel()), ctypes.byref(sa), ctypes.byref(sb), _ptr(out_a),
+        _ptr(out_b) if not swiglu else None, int(bool(swiglu)), _stream(hidden_a)),
+        "tris_grouped_decode_pair_forward_block_gr")
+    return out_a if swiglu else (out_a, out_b)
+
+
 def compact3_dequant(payload_tensors: dict, rank: int, expert_ids: torch.Tensor, use_uniform_k64_groups=False):
     """Dense fp16 weights [num, N, rank] of the listed experts (GPU verification kernel)."""
     dev = expert_ids.device
