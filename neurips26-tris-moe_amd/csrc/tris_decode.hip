@@ -44,7 +44,7 @@ constexpr int kDcMaxBlocks = kDcMaxPrw / 2;     // GR blocks per wavefront and i
 constexpr int kDcSalWin = 32;                   // salient columns per MFMA window
 constexpr int kDcSpan = 32;                     // span decoder lanes per block
 constexpr int kDcStrips = kTileOut / 16;        // 16-column strips of an output tile
-constexpr int kDcWgsPerCu = 1;                  // > 128 VGPRs: one 8-wavefront workgroup per CU
+constexpr int kDcWgsPerCu = 2;                  // <= 128 VGPRs and < 80 KB of LDS: two workgroups per CU
 
 enum DcMode { kDcSingle = 0, kDcPair = 1, kDcSwiglu = 2 };
 
@@ -88,10 +88,27 @@ struct DcArgs {
   int mode;
 };
 
+// A wavefront's per-item operands, loaded into LDS while its GR blocks are decoded: for every tile column,
+// the sign words of the wavefront's packed rows, the row scales of each 64-column K tile's group (d | nd << 16
+// and 0 | 1 << 16), and the two qweight2_sparse rows of the slice's first salient window.
+struct DcStage {
+  uint32_t qw[kDcMaxPrw][kTileOut];
+  uint32_t rdn[kDcMaxBlocks][kTileOut];
+  uint32_t r01[kDcMaxBlocks][kTileOut];
+  uint32_t q2[2][kTileOut];
+};
+
 constexpr uint32_t kDcRsrcWord3 = 0x00020000;  // raw buffer resource, gfx9 family
 
+// Every caller passes wave-uniform values; reading them back from the first lane lets the compiler keep the
+// resource in scalar registers (a resource it cannot prove uniform costs a waterfall loop per load).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t dc_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kDcRsrcWord3);
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(a)));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32)));
+  const int n = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
+  void* ub = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(ub, 0, n, kDcRsrcWord3);
 }
 // Raw buffer loads: an offset at or past the buffer's size reads 0 without touching memory.
 __device__ __forceinline__ uint32_t dc_load32(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
@@ -105,6 +122,16 @@ __device__ __forceinline__ uint4 dc_load128(__amdgpu_buffer_rsrc_t r, uint32_t v
   const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0u, 0);
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
+
+// Buffer loads straight into LDS: lane l's 4 (16) bytes land at dst + 4l (16l); dst is wave-uniform.  An
+// offset past the buffer writes 0.  The wavefront waits for them (vmcnt) before reading dst.
+__device__ __forceinline__ void dc_dma32(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 4, voff, 0, 0, 0);
+}
+__device__ __forceinline__ void dc_dma128(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, 0, 0, 0);
+}
+constexpr int kDcVmcnt0 = 0x0F70;  // s_waitcnt vmcnt(0), other counters untouched
 
 __device__ __forceinline__ f16x2 dc_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
 __device__ __forceinline__ uint32_t dc_u32(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
@@ -304,11 +331,21 @@ __device__ inline void dc_zero_rows(uint16_t* out, int N, int row0, int rc, int 
   }
 }
 
-__global__ __launch_bounds__(kDcThreads) void grouped_decode_kernel(DcArgs a) {
+// Workgroup barrier ordering LDS only: outstanding global loads and stores stay in flight across it (a full
+// __syncthreads waits for them).
+__device__ __forceinline__ void dc_lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__global__ __launch_bounds__(kDcThreads) __attribute__((amdgpu_waves_per_eu(kDcWgsPerCu * kDcWaves / 4))) void
+grouped_decode_kernel(DcArgs a) {
   __shared__ GrTables tab;
   __shared__ DcLuts lut;
   __shared__ __attribute__((aligned(16))) uint32_t bitmap[kDcWaves][kDcMaxBlocks][kGrBlockStride];
-  __shared__ float red[kDcWaves][kDcRows][kTileOut];  // partial tiles; first the wavefront's salient table
+  // per wavefront, in turn: the item's stage (decode to salient), its salient table, its partial tile
+  __shared__ __attribute__((aligned(16))) float red[kDcWaves][kDcRows][kTileOut];
   __shared__ __attribute__((aligned(16))) uint16_t cols[2][2][kDcMaxPrw * kDcUnitWaves * 32];  // [unit][d / nd][k]
 
   gr_tables_to_lds(&tab);
@@ -319,14 +356,16 @@ __global__ __launch_bounds__(kDcThreads) void grouped_decode_kernel(DcArgs a) {
   }
   __syncthreads();
 
-  const int tid = static_cast<int>(threadIdx.x);
+  int tid = static_cast<int>(threadIdx.x);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int unit = wave / kDcUnitWaves;
   const int wu = wave % kDcUnitWaves;  // K slice of the wavefront within its unit
-  const int lane = tid % kWave;
-  const int i16 = lane % 16;
-  const int kg = lane / 16;
-  const int utid = tid % (kDcUnitWaves * kWave);
+  // lane-derived values; recomputed from an opaque copy of the thread index at each item, so the compiler
+  // rebuilds the addresses that derive from them inside the loop instead of holding them in registers
+  int lane = tid % kWave;
+  int i16 = lane % 16;
+  int kg = lane / 16;
+  int utid = tid % (kDcUnitWaves * kWave);
   const bool two_proj = a.mode != kDcSingle;
   const DcProj& pj = a.proj[two_proj ? unit : 0];
   const tris_compact3_payload& p = pj.p;
@@ -342,25 +381,23 @@ __global__ __launch_bounds__(kDcThreads) void grouped_decode_kernel(DcArgs a) {
   const int row_tiles = dc_count_tiles(a.segment_offsets, a.num_segments);
   const int64_t total = static_cast<int64_t>(row_tiles) * nob_items;
   const int W = static_cast<int>(gridDim.x);
-  const int64_t it0 = total * blockIdx.x / W;
-  const int64_t it1 = total * (blockIdx.x + 1) / W;
+  const int it0 = static_cast<int>(total * blockIdx.x / W);
+  const int it1 = static_cast<int>(total * (blockIdx.x + 1) / W);
 
   DcExpert X;
   X.e = -1;
   uint32_t* bm = &bitmap[wave][0][0];
-  uint16_t* sal_tab = reinterpret_cast<uint16_t*>(&red[wave][0][0]);  // [64 columns][kDcSalWin]
-  const uint32_t kshift = 8u * static_cast<uint32_t>(kg);
+  DcStage& stg = *reinterpret_cast<DcStage*>(&red[wave][0][0]);
+  uint32_t kshift = 8u * static_cast<uint32_t>(kg);
   int cur_rt = -1, s = 0, row0 = 0, rc = 0, e = -1;
-  f16x8 av[kDcMaxPrw];  // A operand: row i16 of the row tile, columns 32j + 8kg .. + 8 of the slice
-  f16x8 asal;           // salient A operand of the first window
   // the activations (wave-uniform resource); hoff: byte offset of the lane's row (0xFFFFFFF0: none)
   const __amdgpu_buffer_rsrc_t r_h =
       dc_rsrc(pj.hidden, static_cast<uint32_t>(static_cast<int64_t>(a.hidden_rows) * rank * 2));
   uint32_t hoff = 0xFFFFFFF0u;
 
   // GR blocks of the wavefront: block gb (lane group lane / 32) covers packed rows wu*prw + 2gb, + 1
-  const int gb = lane / kDcSpan;
-  const int gj = lane % kDcSpan;
+  int gb = lane / kDcSpan;
+  int gj = lane % kDcSpan;
 
   // An item's GR block as the span decoder sees it (header, then the lane's span words); the next item's is
   // loaded while this one is decoded and computed.
@@ -368,22 +405,29 @@ __global__ __launch_bounds__(kDcThreads) void grouped_decode_kernel(DcArgs a) {
     int begin, word_count, meta, w0, nw;  // begin: the block's first word
     uint32_t w[GrSpan<kDcSpan>::kMaxWords];
   };
-  auto item_ob = [&](int64_t it) {
-    const int obi = static_cast<int>(it % nob_items);
-    return two_proj ? obi : 2 * obi + unit;
-  };
-  auto gr_header = [&](int64_t it, ItemGr& G) {
-    const int ob = item_ob(it);
-    const bool v = ob < nob && gb < nblk_w;
-    const int b = v ? (wu * nblk_w + gb) * nob + ob : 0;
-    const int32_t* offs = p.q_gmap_gr_offsets + static_cast<int64_t>(e) * (nblk + 1);
-    const int begin = offs[b];
+  // item index within its row tile -> the unit's output tile
+  auto item_ob = [&](int obi) { return two_proj ? obi : 2 * obi + unit; };
+  // GR header and span loads go through buffer resources over expert e's arrays and are issued whether or
+  // not their item exists: an offset past the buffer reads 0 without touching memory, and no branch makes the
+  // compiler wait for a load before its value is used.  The resources are rebuilt from the wave-uniform
+  // expert id where they are used, so they stay in scalar registers.
+  auto gr_header = [&](int obi, bool valid, ItemGr& G) {
+    const __amdgpu_buffer_rsrc_t r_offs =
+        dc_rsrc(p.q_gmap_gr_offsets + static_cast<int64_t>(e) * (nblk + 1), static_cast<uint32_t>(nblk + 1) * 4u);
+    const __amdgpu_buffer_rsrc_t r_meta =
+        dc_rsrc(p.q_gmap_gr_meta + static_cast<int64_t>(e) * nblk, static_cast<uint32_t>(nblk) * 4u);
+    const int ob = item_ob(obi);
+    const bool v = valid && ob < nob && gb < nblk_w;
+    const uint32_t off = v ? static_cast<uint32_t>((wu * nblk_w + gb) * nob + ob) * 4u : 0xFFFFFFF0u;
+    const int begin = static_cast<int>(dc_load32(r_offs, off));
+    const int end = static_cast<int>(dc_load32(r_offs, off + 4u));
     G.begin = begin;
-    G.word_count = v ? offs[b + 1] - begin : 0;
-    G.meta = v ? p.q_gmap_gr_meta[static_cast<int64_t>(e) * nblk + b] : 0;
+    G.word_count = end - begin;
+    G.meta = static_cast<int>(dc_load32(r_meta, off));
   };
   auto gr_words = [&](ItemGr& G) {
-    const int32_t* words = p.q_gmap_gr_words + static_cast<int64_t>(e) * p.gr_words_stride + G.begin;
+    const __amdgpu_buffer_rsrc_t r_words = dc_rsrc(p.q_gmap_gr_words + static_cast<int64_t>(e) * p.gr_words_stride,
+                                                   static_cast<uint32_t>(p.gr_words_stride) * 4u);
     const int wc = G.word_count;
     int w0 = 0, nw = 0;
     if (wc > 0 && wc <= kGrWords) {
@@ -395,13 +439,31 @@ __global__ __launch_bounds__(kDcThreads) void grouped_decode_kernel(DcArgs a) {
     G.w0 = w0;
     G.nw = nw;
 #pragma unroll
-    for (int i = 0; i < GrSpan<kDcSpan>::kMaxWords; ++i) G.w[i] = i < nw ? static_cast<uint32_t>(words[w0 + i]) : 0u;
+    for (int i = 0; i < GrSpan<kDcSpan>::kMaxWords; ++i) {
+      G.w[i] = dc_load32(r_words, i < nw ? static_cast<uint32_t>(G.begin + w0 + i) * 4u : 0xFFFFFFF0u);
+    }
   };
 
   ItemGr cur, nxt;
   bool have_next = false;
-  for (int64_t it = it0; it < it1; ++it) {
-    const int rt = static_cast<int>(it / nob_items);
+  // the current item's row tile and index within it, carried from item to item (no division per item)
+  int rt = it0 / nob_items;
+  int obi = it0 - rt * nob_items;
+  const auto advance = [&]() {
+    if (++obi == nob_items) {
+      obi = 0;
+      ++rt;
+    }
+  };
+  for (int it = it0; it < it1; ++it, advance()) {
+    asm volatile("" : "+v"(tid));
+    lane = tid % kWave;
+    i16 = lane % 16;
+    kg = lane / 16;
+    utid = tid % (kDcUnitWaves * kWave);
+    kshift = 8u * static_cast<uint32_t>(kg);
+    gb = lane / kDcSpan;
+    gj = lane % kDcSpan;
     if (rt != cur_rt) {
       cur_rt = rt;
       have_next = false;
@@ -414,7 +476,7 @@ __global__ __launch_bounds__(kDcThreads) void grouped_decode_kernel(DcArgs a) {
         if (X.e != e) {
           dc_load_expert(p, e, wu, prw, X);
           dc_stage_columns(p, e, utid, cols[unit][0], cols[unit][1]);
-          __syncthreads();
+          dc_lds_barrier();
         }
         // A operand rows of this row tile (rows past rc read zero)
         hoff = 0xFFFFFFF0u;
@@ -423,15 +485,13 @@ __global__ __launch_bounds__(kDcThreads) void grouped_decode_kernel(DcArgs a) {
           if (hrow < 0 || hrow >= a.hidden_rows) hrow = 0;
           hoff = static_cast<uint32_t>(hrow * rank * 2);
         }
-#pragma unroll
-        for (int j = 0; j < kDcMaxPrw; ++j) {
-          const uint32_t off = hoff + static_cast<uint32_t>((wu * prw + j) * 32 + 8 * kg) * 2u;
-          av[j] = __builtin_bit_cast(f16x8, dc_load128(r_h, j < prw && hoff != 0xFFFFFFF0u ? off : 0xFFFFFFF0u));
-        }
-        asal = dc_sal_a(X, r_h, hoff, wu * prw * 32, 0, kg);
       }
     }
-    const int ob = item_ob(it);
+    // wave-uniform tile state (loop-carried values the compiler cannot prove uniform otherwise)
+    e = __builtin_amdgcn_readfirstlane(e);
+    row0 = __builtin_amdgcn_readfirstlane(row0);
+    rc = __builtin_amdgcn_readfirstlane(rc);
+    const int ob = item_ob(obi);
     const int n0 = ob * kTileOut;
     const bool unit_active = ob < nob;
     uint16_t* out = pj.out;
@@ -443,12 +503,50 @@ __global__ __launch_bounds__(kDcThreads) void grouped_decode_kernel(DcArgs a) {
     if (have_next) {
       cur = nxt;
     } else {
-      gr_header(it, cur);
+      gr_header(obi, true, cur);
       gr_words(cur);
     }
+    // the item's sign words, row scales and salient words into the wavefront's stage (landing during the decode)
+    const int nsal = X.nsal;
+    const int q2rows = p.qweight2_sparse_rows;
+    {
+      const __amdgpu_buffer_rsrc_t r_q1 =
+          dc_rsrc(p.qweight1 + static_cast<int64_t>(e) * packed_rows * N, static_cast<uint32_t>(packed_rows) * N * 4u);
+      const __amdgpu_buffer_rsrc_t r_rs = dc_rsrc(p.row_pack3 + static_cast<int64_t>(e) * N * p.num_groups,
+                                                  static_cast<uint32_t>(N) * p.num_groups * 8u);
+      const int nl = n0 + lane;
+      const bool lv = unit_active && nl < N;
+      if ((N & 3) == 0) {
+        // lane (row lane / 16, columns 4 (lane % 16) ..): whole 16-byte chunks, none straddling N
+        const int q = lane / 16;
+        const int n = n0 + 4 * (lane % 16);
+        dc_dma128(r_q1, &stg.qw[0][0],
+                  unit_active && q < prw && n < N ? static_cast<uint32_t>((wu * prw + q) * N + n) * 4u : 0xFFFFFFF0u);
+      } else {
+#pragma unroll
+        for (int j = 0; j < kDcMaxPrw; ++j) {
+          dc_dma32(r_q1, &stg.qw[j][0], lv && j < prw ? static_cast<uint32_t>((wu * prw + j) * N + nl) * 4u : 0xFFFFFFF0u);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < kDcMaxBlocks; ++t) {
+        const int g = X.grp[t];
+        const uint32_t off = lv && g >= 0 ? static_cast<uint32_t>(nl * p.num_groups + g) * 8u : 0xFFFFFFF0u;
+        dc_dma32(r_rs, &stg.rdn[t][0], off == 0xFFFFFFF0u ? off : off + 4u);
+        if (nsal > 0) dc_dma32(r_rs, &stg.r01[t][0], off);
+      }
+      if (nsal > 0) {
+        const __amdgpu_buffer_rsrc_t r_q2 = dc_rsrc(p.qweight2_sparse + static_cast<int64_t>(e) * q2rows * N,
+                                                    static_cast<uint32_t>(q2rows) * N * 4u);
+        const int sr0 = X.sbase >> 5;
+        dc_dma32(r_q2, &stg.q2[0][0], lv && sr0 < q2rows ? static_cast<uint32_t>(sr0 * N + nl) * 4u : 0xFFFFFFF0u);
+        dc_dma32(r_q2, &stg.q2[1][0], lv && sr0 + 1 < q2rows ? static_cast<uint32_t>((sr0 + 1) * N + nl) * 4u : 0xFFFFFFF0u);
+      }
+    }
     // the next item of the same row tile: its block header now, its words after this decode
-    have_next = it + 1 < it1 && (it + 1) / nob_items == rt;
-    if (have_next) gr_header(it + 1, nxt);
+    const int obi_next = obi + 1 < nob_items ? obi + 1 : 0;
+    have_next = it + 1 < it1 && obi_next != 0;
+    gr_header(obi_next, have_next, nxt);
 
     // ---- decode the wavefront's blocks into its LDS bitmap
     {
@@ -469,54 +567,19 @@ __global__ __launch_bounds__(kDcThreads) void grouped_decode_kernel(DcArgs a) {
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
       __builtin_amdgcn_wave_barrier();
     }
-    if (have_next) gr_words(nxt);
+    // the stage has landed (and the next item's header, issued before the decode)
+    __builtin_amdgcn_s_waitcnt(kDcVmcnt0);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    gr_words(nxt);
 
-    // sign words and row scales of the lane's column of every strip (MFMA layout), issued once the decode is done
-    const __amdgpu_buffer_rsrc_t r_q1 =
-        dc_rsrc(p.qweight1 + static_cast<int64_t>(e) * packed_rows * N, static_cast<uint32_t>(packed_rows) * N * 4u);
-    const __amdgpu_buffer_rsrc_t r_rs = dc_rsrc(p.row_pack3 + static_cast<int64_t>(e) * N * p.num_groups,
-                                                static_cast<uint32_t>(N) * p.num_groups * 8u);
-    uint32_t qw[kDcMaxPrw][kDcStrips];
-    uint32_t rs[kDcMaxBlocks][kDcStrips];
+    // ---- main MFMA pass: per packed row of the slice, every strip.  A operand: row i16 of the row tile,
+    // columns 32j + 8kg .. + 8 of the slice, read here each item (the row tile's activations stay in cache)
+    f16x8 av[kDcMaxPrw];
 #pragma unroll
-    for (int st = 0; st < kDcStrips; ++st) {
-      const int n = n0 + 16 * st + i16;
-      const bool nv = unit_active && n < N;
-#pragma unroll
-      for (int j = 0; j < kDcMaxPrw; ++j) {
-        qw[j][st] = dc_load32(r_q1, nv && j < prw ? static_cast<uint32_t>((wu * prw + j) * N + n) * 4u : 0xFFFFFFF0u);
-      }
-#pragma unroll
-      for (int t = 0; t < kDcMaxBlocks; ++t) {
-        const int g = X.grp[t];
-        rs[t][st] = dc_load64(r_rs, nv && g >= 0 ? static_cast<uint32_t>(n * p.num_groups + g) * 8u : 0xFFFFFFF0u).y;
-      }
+    for (int j = 0; j < kDcMaxPrw; ++j) {
+      const uint32_t off = hoff + static_cast<uint32_t>((wu * prw + j) * 32 + 8 * kg) * 2u;
+      av[j] = __builtin_bit_cast(f16x8, dc_load128(r_h, j < prw && hoff != 0xFFFFFFF0u ? off : 0xFFFFFFF0u));
     }
-
-    // ---- salient loads (sign words, row scales, first-window qweight2_sparse words of tile column `lane`)
-    const int nsal = X.nsal;
-    const int q2rows = p.qweight2_sparse_rows;
-    const __amdgpu_buffer_rsrc_t r_q2 = dc_rsrc(p.qweight2_sparse + static_cast<int64_t>(e) * q2rows * N,
-                                                static_cast<uint32_t>(q2rows) * N * 4u);
-    uint32_t q1c[kDcMaxPrw], r01[kDcMaxBlocks], q2a = 0u, q2b = 0u;
-    const int nc = n0 + lane;
-    const bool cv = unit_active && nc < N;
-    if (nsal > 0) {
-#pragma unroll
-      for (int j = 0; j < kDcMaxPrw; ++j) {
-        q1c[j] = dc_load32(r_q1, cv && j < prw ? static_cast<uint32_t>((wu * prw + j) * N + nc) * 4u : 0xFFFFFFF0u);
-      }
-#pragma unroll
-      for (int t = 0; t < kDcMaxBlocks; ++t) {
-        const int g = X.grp[t];
-        r01[t] = dc_load64(r_rs, cv && g >= 0 ? static_cast<uint32_t>(nc * p.num_groups + g) * 8u : 0xFFFFFFF0u).x;
-      }
-      const int r0 = X.sbase >> 5;
-      q2a = dc_load32(r_q2, cv && r0 < q2rows ? static_cast<uint32_t>(r0 * N + nc) * 4u : 0xFFFFFFF0u);
-      q2b = dc_load32(r_q2, cv && r0 + 1 < q2rows ? static_cast<uint32_t>((r0 + 1) * N + nc) * 4u : 0xFFFFFFF0u);
-    }
-
-    // ---- main MFMA pass: per packed row of the slice, every strip
     f32x4 acc[kDcStrips];
 #pragma unroll
     for (int st = 0; st < kDcStrips; ++st) acc[st] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -534,10 +597,10 @@ __global__ __launch_bounds__(kDcThreads) void grouped_decode_kernel(DcArgs a) {
 #pragma unroll
         for (int st = 0; st < kDcStrips; ++st) {
           const uint32_t gw = bm[t * kGrBlockStride + kGrPadFront + (j & 1) * kTileOut + 16 * st + i16];
-          const uint32_t r = rs[t][st];
+          const uint32_t r = stg.rdn[t][16 * st + i16];
           const uint32_t rd2 = (r & 0xFFFFu) * 0x00010001u;
           const uint32_t rn2 = (r >> 16) * 0x00010001u;
-          const f16x8 bv = dc_b_operand(&lut, qw[j][st], gw, kshift, cd, cn, rd2, rn2);
+          const f16x8 bv = dc_b_operand(&lut, stg.qw[j][16 * st + i16], gw, kshift, cd, cn, rd2, rn2);
           acc[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[j], bv, acc[st], 0, 0, 0);
         }
       }
@@ -545,6 +608,17 @@ __global__ __launch_bounds__(kDcThreads) void grouped_decode_kernel(DcArgs a) {
 
     // ---- salient columns: table of exact weights (lane = tile column), then one MFMA per strip and window
     if (nsal > 0) {
+      uint16_t* sal_tab = reinterpret_cast<uint16_t*>(&red[wave][0][0]);  // [64 columns][kDcSalWin]
+      const int nc = n0 + lane;
+      const bool cv = unit_active && nc < N;
+      const __amdgpu_buffer_rsrc_t r_q2 = dc_rsrc(p.qweight2_sparse + static_cast<int64_t>(e) * q2rows * N,
+                                                  static_cast<uint32_t>(q2rows) * N * 4u);
+      uint32_t q1c[kDcMaxPrw];
+#pragma unroll
+      for (int j = 0; j < kDcMaxPrw; ++j) q1c[j] = stg.qw[j][lane];
+      const uint32_t r01[2] = {stg.r01[0][lane], stg.r01[kDcMaxBlocks - 1][lane]};
+      uint32_t q2a = stg.q2[0][lane], q2b = stg.q2[1][lane];
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // the table overwrites the stage
       const int nwin = (nsal + kDcSalWin - 1) / kDcSalWin;
       uint4* trow = reinterpret_cast<uint4*>(&sal_tab[lane * kDcSalWin]);
       for (int w = 0; w < nwin; ++w) {
@@ -575,7 +649,7 @@ __global__ __launch_bounds__(kDcThreads) void grouped_decode_kernel(DcArgs a) {
         }
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
-        const f16x8 as = w == 0 ? asal : dc_sal_a(X, r_h, hoff, wu * prw * 32, w, kg);
+        const f16x8 as = dc_sal_a(X, r_h, hoff, wu * prw * 32, w, kg);
 #pragma unroll
         for (int st = 0; st < kDcStrips; ++st) {
           const f16x8 bs = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(
@@ -596,7 +670,7 @@ __global__ __launch_bounds__(kDcThreads) void grouped_decode_kernel(DcArgs a) {
         if (r < rc) red[wave][r][16 * st + i16] = acc[st][v];
       }
     }
-    __syncthreads();
+    dc_lds_barrier();
     if (a.mode == kDcSwiglu) {
       // both units' tile: out = fp16(silu(g) * u) with g, u each through its projection's epilogue
       const tris_compact3_payload& pg = a.proj[0].p;
@@ -635,7 +709,7 @@ __global__ __launch_bounds__(kDcThreads) void grouped_decode_kernel(DcArgs a) {
         out[static_cast<int64_t>(row0 + r) * N + n] = f2h_bits(v);
       }
     }
-    __syncthreads();  // the next item rewrites the partial tiles and salient tables
+    dc_lds_barrier();  // the next item's stage overwrites the partial tiles
   }
 }
 

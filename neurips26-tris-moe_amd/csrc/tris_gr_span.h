@@ -295,35 +295,36 @@ __device__ inline void gr_decode_block_group(const GrSpan<S>& sp, const GrTables
     const char* __restrict__ ent = reinterpret_cast<const char*>(tab->entry + gr_entry_base(k));
     const int nbytes = 4 * sp.nw;
     // ---- A: next-state fields of every byte, composed from every entry state
-    uint32_t nsv[kBytes];
+    const auto next_fields = [&](int i) {
+      const uint32_t byte = (sp.w[i / 4] >> (8 * (i % 4))) & 0xFFu;
+      const uint32_t e = nxt[byte];
+      return i < nbytes ? e : kGrIdentityNext;
+    };
     uint32_t c0 = 0u, c1 = 4u, c2 = 8u, c3 = 12u;
 #pragma unroll
     for (int i = 0; i < kBytes; ++i) {
-      const uint32_t byte = (sp.w[i / 4] >> (8 * (i % 4))) & 0xFFu;
-      const uint32_t e = nxt[byte];
-      nsv[i] = i < nbytes ? e : kGrIdentityNext;
-      c0 = __builtin_amdgcn_ubfe(nsv[i], c0, 4);
-      c1 = __builtin_amdgcn_ubfe(nsv[i], c1, 4);
-      c2 = __builtin_amdgcn_ubfe(nsv[i], c2, 4);
-      c3 = __builtin_amdgcn_ubfe(nsv[i], c3, 4);
+      const uint32_t f = next_fields(i);
+      c0 = __builtin_amdgcn_ubfe(f, c0, 4);
+      c1 = __builtin_amdgcn_ubfe(f, c1, 4);
+      c2 = __builtin_amdgcn_ubfe(f, c2, 4);
+      c3 = __builtin_amdgcn_ubfe(f, c3, 4);
     }
     // ---- B: the map of lanes 0..j, then the previous lane's (wave_shr:1) applied to state 0
     const uint32_t map = group_scan<S>(c0 | (c1 << 4) | (c2 << 8) | (c3 << 12), kGrIdentityNext, gr_map_compose);
     const uint32_t prev_map = dpp_mov<0x138, 0xF>(kGrIdentityNext, map);
     uint32_t st = j == 0 ? 0u : (prev_map & 15u);  // 4 * true entry state
-    // ---- C: entries along the true path; F advance and codeword count, packed adv | count << 16
-    uint32_t mlo[kBytes], mhi[kBytes];
+    // ---- C: entries along the true path (the next-state fields read again); F advance and codeword count
+    // (packed adv | count << 16) from their high words, the masks read again for the emission
+    uint32_t off[kBytes];
     uint32_t packed = 0u;
 #pragma unroll
     for (int i = 0; i < kBytes; ++i) {
       const uint32_t byte = (sp.w[i / 4] >> (8 * (i % 4))) & 0xFFu;
-      const uint32_t off = i < nbytes ? (st << 9) + (byte << 3) : kGrZeroEntryOffset - gr_entry_base(k) * 8u;
-      st = __builtin_amdgcn_ubfe(nsv[i], st, 4);
-      const uint2 e = *reinterpret_cast<const uint2*>(ent + off);
-      mlo[i] = e.x;
-      mhi[i] = e.y;
-      packed += e.y >> 9;
+      off[i] = i < nbytes ? (st << 9) + (byte << 3) : kGrZeroEntryOffset - gr_entry_base(k) * 8u;
+      st = __builtin_amdgcn_ubfe(next_fields(i), st, 4);
+      packed += *reinterpret_cast<const uint32_t*>(ent + off[i] + 4) >> 9;
     }
+    asm volatile("" ::: "memory");  // the emission reads the entries again rather than keeping 16 of them live
     const uint32_t incl = group_incl_sum<S>(packed);
     const int total = static_cast<int>(group_last<S>(incl) >> 16);
     serial = total != one_count;
@@ -333,29 +334,30 @@ __device__ inline void gr_decode_block_group(const GrSpan<S>& sp, const GrTables
       uint32_t* base = out - kGrPadFront;
       // OR a mask (< 2^64) whose bit 0 is at posb - 32 into the bitmap; word 129 and up are the back pads,
       // where only positions past 4095 land
-      const auto emit = [&](uint64_t m, bool third) {
+      const auto emit = [&](uint64_t m) {
         const uint32_t rel = posb & 31u;
         const uint32_t widx = (posb >> 5) < 129u ? (posb >> 5) : 129u;
         const uint64_t v = m << rel;
         atomicOr(&base[widx], static_cast<uint32_t>(v));
         atomicOr(&base[widx + 1], static_cast<uint32_t>(v >> 32));
-        if (third) atomicOr(&base[widx + 2], static_cast<uint32_t>((m >> 32) << rel >> 32));
+        atomicOr(&base[widx + 2], static_cast<uint32_t>((m >> 32) << rel >> 32));
       };
       if (k <= 2) {
         // k <= 2: a byte's mask is below 2^25 and its advance at most 32, so two bytes fit one 64-bit mask
 #pragma unroll
         for (int i = 0; i < kBytes; i += 2) {
-          const uint32_t a0 = __builtin_amdgcn_ubfe(mhi[i], 9, 7);
-          const uint64_t m = (static_cast<uint64_t>(mhi[i] & 0x1FFu) << 32 | mlo[i]) |
-                             (static_cast<uint64_t>(mlo[i + 1]) << a0);
-          emit(m, true);
-          posb += a0 + __builtin_amdgcn_ubfe(mhi[i + 1], 9, 7);
+          const uint2 e0 = *reinterpret_cast<const uint2*>(ent + off[i]);
+          const uint2 e1 = *reinterpret_cast<const uint2*>(ent + off[i + 1]);
+          const uint32_t a0 = __builtin_amdgcn_ubfe(e0.y, 9, 7);
+          emit(static_cast<uint64_t>(e0.x) | (static_cast<uint64_t>(e1.x) << a0));
+          posb += a0 + __builtin_amdgcn_ubfe(e1.y, 9, 7);
         }
       } else {
 #pragma unroll
         for (int i = 0; i < kBytes; ++i) {
-          emit(static_cast<uint64_t>(mhi[i] & 0x1FFu) << 32 | mlo[i], true);
-          posb += __builtin_amdgcn_ubfe(mhi[i], 9, 7);
+          const uint2 e = *reinterpret_cast<const uint2*>(ent + off[i]);
+          emit(static_cast<uint64_t>(e.y & 0x1FFu) << 32 | e.x);
+          posb += __builtin_amdgcn_ubfe(e.y, 9, 7);
         }
       }
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
