@@ -44,6 +44,8 @@ constexpr int kDcMaxBlocks = kDcMaxPrw / 2;     // GR blocks per wavefront and i
 constexpr int kDcSalWin = 32;                   // salient columns per MFMA window
 constexpr int kDcSpan = 32;                     // span decoder lanes per block
 constexpr int kDcStrips = kTileOut / 16;        // 16-column strips of an output tile
+constexpr int kDcRedStride = kTileOut + 4;      // partial-tile row stride: the four row groups of an MFMA
+                                                // result land in different LDS banks
 constexpr int kDcWgsPerCu = 2;                  // <= 128 VGPRs and < 80 KB of LDS: two workgroups per CU
 
 enum DcMode { kDcSingle = 0, kDcPair = 1, kDcSwiglu = 2 };
@@ -323,6 +325,15 @@ __device__ inline void dc_stage_columns(const tris_compact3_payload& p, int e, i
   }
 }
 
+static_assert(sizeof(DcStage) <= sizeof(float) * kDcRows * kDcRedStride &&
+                  sizeof(uint16_t) * kTileOut * kDcSalWin <= sizeof(float) * kDcRows * kDcRedStride,
+              "the stage and the salient table share a wavefront's partial-tile slot");
+
+// Salient table [64 tile columns][kDcSalWin slots] of fp16 weights.  The four 16-byte chunks of column c's
+// row are stored XOR-swizzled by c / 4, so a 16-lane phase of the MFMA operand read, and the zeroing of the
+// rows, touch 16 different bank groups.
+__device__ __forceinline__ int dc_sal_index(int c, int q) { return c * kDcSalWin + ((((q >> 3) ^ (c >> 2)) & 3) << 3) + (q & 7); }
+
 // Zero output for the rows of an item routed to no expert.
 __device__ inline void dc_zero_rows(uint16_t* out, int N, int row0, int rc, int n0, int utid) {
   for (int idx = utid; idx < rc * kTileOut; idx += kDcUnitWaves * kWave) {
@@ -345,7 +356,7 @@ grouped_decode_kernel(DcArgs a) {
   __shared__ DcLuts lut;
   __shared__ __attribute__((aligned(16))) uint32_t bitmap[kDcWaves][kDcMaxBlocks][kGrBlockStride];
   // per wavefront, in turn: the item's stage (decode to salient), its salient table, its partial tile
-  __shared__ __attribute__((aligned(16))) float red[kDcWaves][kDcRows][kTileOut];
+  __shared__ __attribute__((aligned(16))) float red[kDcWaves][kDcRows][kDcRedStride];
   __shared__ __attribute__((aligned(16))) uint16_t cols[2][2][kDcMaxPrw * kDcUnitWaves * 32];  // [unit][d / nd][k]
 
   gr_tables_to_lds(&tab);
@@ -645,7 +656,7 @@ grouped_decode_kernel(DcArgs a) {
           const uint32_t neg = ((~(w1 >> (k & 31)) & 1u) << 15) | ((~(q2 >> (sidx & 31)) & 1u) << 31);
           const f16x2 t = dc_h2(dc_u32(dc_h2(c01) * dc_h2(rr)) ^ neg);
           const _Float16 sum = t[0] + t[1];
-          sal_tab[lane * kDcSalWin + q] = __builtin_bit_cast(uint16_t, sum);
+          sal_tab[dc_sal_index(lane, q)] = __builtin_bit_cast(uint16_t, sum);
         }
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -653,7 +664,7 @@ grouped_decode_kernel(DcArgs a) {
 #pragma unroll
         for (int st = 0; st < kDcStrips; ++st) {
           const f16x8 bs = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(
-                                                          &sal_tab[(16 * st + i16) * kDcSalWin + 8 * kg]));
+                                                          &sal_tab[dc_sal_index(16 * st + i16, 8 * kg)]));
           acc[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as, bs, acc[st], 0, 0, 0);
         }
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");

@@ -14,6 +14,7 @@
 namespace tris {
 
 constexpr int kSpanThreads = 256;
+constexpr int kSpanWgTarget = 1024;  // persistent workgroups per launch (four per CU)
 
 // One projection's stream; jobs of one launch share the routed expert list.
 struct GrJob {
@@ -33,7 +34,9 @@ struct GrJobs {
   GrJob job[TRIS_MAX_PREDECODE_JOBS];
 };
 
-// grid = (ceil(max nblk / blocks per workgroup), slots, jobs)
+// grid = (workgroups per (slot, job), slots, jobs).  Persistent over block batches: a workgroup copies the
+// tables once, then decodes batches blockIdx.x, blockIdx.x + gridDim.x, ... of kSpanThreads / S blocks,
+// loading the next batch's block headers and span words while it decodes the current one.
 template <int S>
 __global__ __launch_bounds__(kSpanThreads) void gr_decode_span_kernel(GrJobs jobs, const int32_t* __restrict__ expert_ids) {
   constexpr int kBlocksPerWg = kSpanThreads / S;
@@ -41,45 +44,52 @@ __global__ __launch_bounds__(kSpanThreads) void gr_decode_span_kernel(GrJobs job
   __shared__ uint32_t outb[kBlocksPerWg][kGrBlockStride];
   const GrJob& jb = jobs.job[blockIdx.z];
   const int slot = blockIdx.y;
-  const int block0 = blockIdx.x * kBlocksPerWg;
-  if (block0 >= jb.nblk) return;  // uniform over the workgroup
   const int nblk = jb.nblk;
+  if (static_cast<int>(blockIdx.x) * kBlocksPerWg >= nblk) return;  // uniform over the workgroup
   const int tid = threadIdx.x;
   const int g = tid / S;
   const int j = tid % S;
-  const int block = block0 + g;
   const int expert = expert_ids[slot];
   const bool evalid = expert >= 0 && expert < jb.num_experts;
+  const int32_t* words = evalid ? jb.words + static_cast<int64_t>(expert) * jb.words_stride : nullptr;
+  const int32_t* offsets = evalid ? jb.offsets + static_cast<int64_t>(expert) * (nblk + 1) : nullptr;
+  const int32_t* meta = evalid ? jb.meta + static_cast<int64_t>(expert) * nblk : nullptr;
+  const int stride = static_cast<int>(gridDim.x) * kBlocksPerWg;
+  int block0 = blockIdx.x * kBlocksPerWg;
   GrSpan<S> sp;
-  gr_span_load<S>(sp, evalid ? jb.words + static_cast<int64_t>(expert) * jb.words_stride : nullptr,
-                  evalid ? jb.offsets + static_cast<int64_t>(expert) * (nblk + 1) : nullptr,
-                  evalid ? jb.meta + static_cast<int64_t>(expert) * nblk : nullptr, block, evalid && block < nblk, j);
+  gr_span_load<S>(sp, words, offsets, meta, block0 + g, evalid && block0 + g < nblk, j);
   gr_tables_to_lds(&tab);
-  for (int idx = tid; idx < kBlocksPerWg * kGrBlockStride; idx += kSpanThreads) {
-    outb[idx / kGrBlockStride][idx % kGrBlockStride] = 0u;
-  }
-  __syncthreads();
-  gr_decode_block_group<S>(sp, &tab, outb[g] + kGrPadFront, j);
-  __syncthreads();
-  if (jb.dense_rows == 0) {
-    int32_t* dst = jb.out + (static_cast<int64_t>(slot) * nblk + block0) * kGrWords;
-    for (int idx = tid; idx < kBlocksPerWg * kGrWords; idx += kSpanThreads) {
-      if (block0 + idx / kGrWords < nblk) {
-        dst[idx] = static_cast<int32_t>(outb[idx / kGrWords][kGrPadFront + idx % kGrWords]);
+  for (; block0 < nblk; block0 += stride) {
+    for (int idx = tid; idx < kBlocksPerWg * kGrBlockStride; idx += kSpanThreads) {
+      outb[idx / kGrBlockStride][idx % kGrBlockStride] = 0u;
+    }
+    __syncthreads();
+    const GrSpan<S> cur = sp;
+    const int next0 = block0 + stride;
+    gr_span_load<S>(sp, words, offsets, meta, next0 + g, evalid && next0 + g < nblk, j);
+    gr_decode_block_group<S>(cur, &tab, outb[g] + kGrPadFront, j);
+    __syncthreads();
+    if (jb.dense_rows == 0) {
+      int32_t* dst = jb.out + (static_cast<int64_t>(slot) * nblk + block0) * kGrWords;
+      for (int idx = tid; idx < kBlocksPerWg * kGrWords; idx += kSpanThreads) {
+        if (block0 + idx / kGrWords < nblk) {
+          dst[idx] = static_cast<int32_t>(outb[idx / kGrWords][kGrPadFront + idx % kGrWords]);
+        }
+      }
+    } else {
+      int32_t* dst = jb.out + static_cast<int64_t>(slot) * jb.dense_rows * jb.dense_cols;
+      for (int idx = tid; idx < kBlocksPerWg * kGrWords; idx += kSpanThreads) {
+        const int b = block0 + idx / kGrWords;
+        if (b >= nblk) continue;
+        const int w = idx % kGrWords;
+        const int row = (b / jb.num_out_blocks) * kGrPackedRows + w / kTileOut;
+        const int col = (b % jb.num_out_blocks) * kTileOut + w % kTileOut;
+        if (row < jb.dense_rows && col < jb.dense_cols) {
+          dst[static_cast<int64_t>(row) * jb.dense_cols + col] = static_cast<int32_t>(outb[idx / kGrWords][kGrPadFront + w]);
+        }
       }
     }
-  } else {
-    int32_t* dst = jb.out + static_cast<int64_t>(slot) * jb.dense_rows * jb.dense_cols;
-    for (int idx = tid; idx < kBlocksPerWg * kGrWords; idx += kSpanThreads) {
-      const int b = block0 + idx / kGrWords;
-      if (b >= nblk) continue;
-      const int w = idx % kGrWords;
-      const int row = (b / jb.num_out_blocks) * kGrPackedRows + w / kTileOut;
-      const int col = (b % jb.num_out_blocks) * kTileOut + w % kTileOut;
-      if (row < jb.dense_rows && col < jb.dense_cols) {
-        dst[static_cast<int64_t>(row) * jb.dense_cols + col] = static_cast<int32_t>(outb[idx / kGrWords][kGrPadFront + w]);
-      }
-    }
+    __syncthreads();  // the next batch zeroes and rewrites outb
   }
 }
 
@@ -111,13 +121,18 @@ int launch_gr_jobs(const GrJobs& jobs, int num_jobs, const int32_t* expert_ids, 
   // lanes per block: more lanes shorten each block's walk, fewer spread the per-workgroup table copy
   // over more blocks
   const int S = total > 8192 ? 16 : 32;
+  const int per_wg = kSpanThreads / S;
+  // persistent workgroups: about kSpanWgTarget in all, each copying the tables once
+  const int wanted = ceil_div(max_nblk, per_wg);
+  const int share = ceil_div(kSpanWgTarget, num_slots * num_jobs);
+  const int gx = wanted < share ? wanted : (share < 1 ? 1 : share);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (S == 16) {
-    hipLaunchKernelGGL((gr_decode_span_kernel<16>), dim3(ceil_div(max_nblk, kSpanThreads / 16), num_slots, num_jobs),
-                       dim3(kSpanThreads), 0, s, jobs, expert_ids);
+    hipLaunchKernelGGL((gr_decode_span_kernel<16>), dim3(gx, num_slots, num_jobs), dim3(kSpanThreads), 0, s, jobs,
+                       expert_ids);
   } else {
-    hipLaunchKernelGGL((gr_decode_span_kernel<32>), dim3(ceil_div(max_nblk, kSpanThreads / 32), num_slots, num_jobs),
-                       dim3(kSpanThreads), 0, s, jobs, expert_ids);
+    hipLaunchKernelGGL((gr_decode_span_kernel<32>), dim3(gx, num_slots, num_jobs), dim3(kSpanThreads), 0, s, jobs,
+                       expert_ids);
   }
   return check_launch(who);
 }

@@ -197,6 +197,19 @@ __device__ __forceinline__ uint32_t group_last(uint32_t v) {
   }
 }
 
+// The largest span (in words) of the wavefront's groups: their first lanes hold the longest spans.  Read from
+// those lanes whatever branch their groups took, so it is wave-uniform and only ever too large.
+template <int S>
+__device__ __forceinline__ int wave_max_words(int nw) {
+  int m = __builtin_amdgcn_readlane(nw, 0);
+#pragma unroll
+  for (int g = 1; g < kWave / S; ++g) {
+    const int v = __builtin_amdgcn_readlane(nw, g * S);
+    m = v > m ? v : m;
+  }
+  return m;
+}
+
 // Composition of 4-state maps in the next[] field encoding (field s = 4 * image of s): first `earlier`, then
 // `own`.
 __device__ __forceinline__ uint32_t gr_map_compose(uint32_t own, uint32_t earlier) {
@@ -294,6 +307,8 @@ __device__ inline void gr_decode_block_group(const GrSpan<S>& sp, const GrTables
     const uint16_t* __restrict__ nxt = tab->next + (k - 1) * 256;
     const char* __restrict__ ent = reinterpret_cast<const char*>(tab->entry + gr_entry_base(k));
     const int nbytes = 4 * sp.nw;
+    // words any lane of the wavefront holds (a group's first lane holds the most): the walks stop there
+    const int maxw = wave_max_words<S>(sp.nw);
     // ---- A: next-state fields of every byte, composed from every entry state
     const auto next_fields = [&](int i) {
       const uint32_t byte = (sp.w[i / 4] >> (8 * (i % 4))) & 0xFFu;
@@ -303,11 +318,13 @@ __device__ inline void gr_decode_block_group(const GrSpan<S>& sp, const GrTables
     uint32_t c0 = 0u, c1 = 4u, c2 = 8u, c3 = 12u;
 #pragma unroll
     for (int i = 0; i < kBytes; ++i) {
-      const uint32_t f = next_fields(i);
-      c0 = __builtin_amdgcn_ubfe(f, c0, 4);
-      c1 = __builtin_amdgcn_ubfe(f, c1, 4);
-      c2 = __builtin_amdgcn_ubfe(f, c2, 4);
-      c3 = __builtin_amdgcn_ubfe(f, c3, 4);
+      if (i / 4 < maxw) {
+        const uint32_t f = next_fields(i);
+        c0 = __builtin_amdgcn_ubfe(f, c0, 4);
+        c1 = __builtin_amdgcn_ubfe(f, c1, 4);
+        c2 = __builtin_amdgcn_ubfe(f, c2, 4);
+        c3 = __builtin_amdgcn_ubfe(f, c3, 4);
+      }
     }
     // ---- B: the map of lanes 0..j, then the previous lane's (wave_shr:1) applied to state 0
     const uint32_t map = group_scan<S>(c0 | (c1 << 4) | (c2 << 8) | (c3 << 12), kGrIdentityNext, gr_map_compose);
@@ -319,10 +336,12 @@ __device__ inline void gr_decode_block_group(const GrSpan<S>& sp, const GrTables
     uint32_t packed = 0u;
 #pragma unroll
     for (int i = 0; i < kBytes; ++i) {
-      const uint32_t byte = (sp.w[i / 4] >> (8 * (i % 4))) & 0xFFu;
-      off[i] = i < nbytes ? (st << 9) + (byte << 3) : kGrZeroEntryOffset - gr_entry_base(k) * 8u;
-      st = __builtin_amdgcn_ubfe(next_fields(i), st, 4);
-      packed += *reinterpret_cast<const uint32_t*>(ent + off[i] + 4) >> 9;
+      if (i / 4 < maxw) {
+        const uint32_t byte = (sp.w[i / 4] >> (8 * (i % 4))) & 0xFFu;
+        off[i] = i < nbytes ? (st << 9) + (byte << 3) : kGrZeroEntryOffset - gr_entry_base(k) * 8u;
+        st = __builtin_amdgcn_ubfe(next_fields(i), st, 4);
+        packed += *reinterpret_cast<const uint32_t*>(ent + off[i] + 4) >> 9;
+      }
     }
     asm volatile("" ::: "memory");  // the emission reads the entries again rather than keeping 16 of them live
     const uint32_t incl = group_incl_sum<S>(packed);
@@ -346,18 +365,22 @@ __device__ inline void gr_decode_block_group(const GrSpan<S>& sp, const GrTables
         // k <= 2: a byte's mask is below 2^25 and its advance at most 32, so two bytes fit one 64-bit mask
 #pragma unroll
         for (int i = 0; i < kBytes; i += 2) {
-          const uint2 e0 = *reinterpret_cast<const uint2*>(ent + off[i]);
-          const uint2 e1 = *reinterpret_cast<const uint2*>(ent + off[i + 1]);
-          const uint32_t a0 = __builtin_amdgcn_ubfe(e0.y, 9, 7);
-          emit(static_cast<uint64_t>(e0.x) | (static_cast<uint64_t>(e1.x) << a0));
-          posb += a0 + __builtin_amdgcn_ubfe(e1.y, 9, 7);
+          if (i / 4 < maxw) {
+            const uint2 e0 = *reinterpret_cast<const uint2*>(ent + off[i]);
+            const uint2 e1 = *reinterpret_cast<const uint2*>(ent + off[i + 1]);
+            const uint32_t a0 = __builtin_amdgcn_ubfe(e0.y, 9, 7);
+            emit(static_cast<uint64_t>(e0.x) | (static_cast<uint64_t>(e1.x) << a0));
+            posb += a0 + __builtin_amdgcn_ubfe(e1.y, 9, 7);
+          }
         }
       } else {
 #pragma unroll
         for (int i = 0; i < kBytes; ++i) {
-          const uint2 e = *reinterpret_cast<const uint2*>(ent + off[i]);
-          emit(static_cast<uint64_t>(e.y & 0x1FFu) << 32 | e.x);
-          posb += __builtin_amdgcn_ubfe(e.y, 9, 7);
+          if (i / 4 < maxw) {
+            const uint2 e = *reinterpret_cast<const uint2*>(ent + off[i]);
+            emit(static_cast<uint64_t>(e.y & 0x1FFu) << 32 | e.x);
+            posb += __builtin_amdgcn_ubfe(e.y, 9, 7);
+          }
         }
       }
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");

@@ -256,8 +256,15 @@ struct MfTileBuf {     // one output tile's weight words
 
 constexpr uint32_t kBufferWord3 = 0x00020000;  // raw buffer resource, gfx9 family
 
+// Every caller passes wave-uniform values; reading them back from the first lane lets the compiler keep the
+// resource in scalar registers (a resource it cannot prove uniform costs a waterfall loop per load).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufferWord3);
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(a)));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32)));
+  const int n = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
+  void* ub = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(ub, 0, n, kBufferWord3);
 }
 // Raw buffer loads: voffset at or past the buffer size returns 0 without a memory access.
 __device__ __forceinline__ uint32_t bload32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {

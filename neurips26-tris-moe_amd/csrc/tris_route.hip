@@ -199,6 +199,60 @@ __device__ __forceinline__ void route_token_topk(const float* __restrict__ row, 
   }
 }
 
+// One token's softmax and top-k by a whole wavefront (the same picks, in the same order, as route_token_topk):
+// coalesced reads of the logits, the max and the exp-sum reduced across lanes, then top_k rounds, each taking
+// the largest probability strictly below the previous pick in (probability, lower expert first) order.  The
+// picks depend only on the logits (exp is monotone and every probability shares the max and the sum); the
+// sum's order differs from the serial one, so a probability can differ in its last bit.
+template <int K>
+__device__ __forceinline__ void route_token_topk_wave(const float* __restrict__ row, int num_experts, int top_k,
+                                                      float bp[K], int be[K]) {
+  const int lane = static_cast<int>(__lane_id());
+  float m = -INFINITY;
+  for (int e = lane; e < num_experts; e += kWave) m = fmaxf(m, row[e]);
+#pragma unroll
+  for (int d = kWave / 2; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
+  float sum = 0.0f;
+  for (int e = lane; e < num_experts; e += kWave) sum += expf(row[e] - m);
+#pragma unroll
+  for (int d = kWave / 2; d >= 1; d >>= 1) sum += __shfl_xor(sum, d);
+  float lp = INFINITY;  // the previous pick
+  int le = -1;
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    bp[j] = -1.0f;
+    be[j] = -1;
+    if (j < top_k) {
+      float cp = -1.0f;
+      int ce = num_experts;  // none
+      for (int e = lane; e < num_experts; e += kWave) {
+        const float pe = expf(row[e] - m) / sum;
+        const bool below = pe < lp || (pe == lp && e > le);
+        const bool better = pe > cp || (pe == cp && e < ce);
+        if (below && better) {
+          cp = pe;
+          ce = e;
+        }
+      }
+#pragma unroll
+      for (int d = kWave / 2; d >= 1; d >>= 1) {
+        const float op = __shfl_xor(cp, d);
+        const int oe = __shfl_xor(ce, d);
+        if (op > cp || (op == cp && oe < ce)) {
+          cp = op;
+          ce = oe;
+        }
+      }
+      if (ce < num_experts) {
+        bp[j] = cp;
+        be[j] = ce;
+        lp = cp;
+        le = ce;
+      }
+    }
+  }
+}
+
 // The routing weight of pick j: renormalised over the k picks (summed in pick order) or not.
 template <int K>
 __device__ __forceinline__ float route_pick_weight(const float bp[K], int top_k, int renormalize, int j) {
@@ -348,21 +402,29 @@ __global__ __launch_bounds__(kRouteThreads) void route_topk_small_kernel(
   const int total = tokens * top_k;
   for (int e = tid; e < num_experts; e += kRouteThreads) cnt[e] = 0;
   __syncthreads();
-  // ---- softmax and top-k, one token per thread
-  for (int t = tid; t < tokens; t += kRouteThreads) {
-    float bp[kRouteMaxTopK];
-    int be[kRouteMaxTopK];
-    route_token_topk<kRouteMaxTopK>(logits + static_cast<int64_t>(t) * num_experts, num_experts, top_k, bp, be);
+  // ---- softmax and top-k, one wavefront per token
+  {
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
+    for (int t = wave; t < tokens; t += kRouteThreads / kWave) {
+      float bp[kRouteMaxTopK];
+      int be[kRouteMaxTopK];
+      route_token_topk_wave<kRouteMaxTopK>(logits + static_cast<int64_t>(t) * num_experts, num_experts, top_k, bp,
+                                           be);
+      if (lane < top_k) {
+        // lane j writes pick j
 #pragma unroll
-    for (int j = 0; j < kRouteMaxTopK; ++j) {
-      if (j < top_k) {
-        const float w = route_pick_weight<kRouteMaxTopK>(bp, top_k, renormalize, j);
-        const int i = t * top_k + j;
-        sel[i] = static_cast<int16_t>(be[j]);
-        if (selected != nullptr) selected[i] = be[j];
-        weights16[i] = f2h_bits(w);
-        if (weights32 != nullptr) weights32[i] = w;
-        atomicAdd(&cnt[be[j]], 1);
+        for (int j = 0; j < kRouteMaxTopK; ++j) {
+          if (j == lane) {
+            const float w = route_pick_weight<kRouteMaxTopK>(bp, top_k, renormalize, j);
+            const int i = t * top_k + j;
+            sel[i] = static_cast<int16_t>(be[j]);
+            if (selected != nullptr) selected[i] = be[j];
+            weights16[i] = f2h_bits(w);
+            if (weights32 != nullptr) weights32[i] = w;
+            if (be[j] >= 0) atomicAdd(&cnt[be[j]], 1);
+          }
+        }
       }
     }
   }

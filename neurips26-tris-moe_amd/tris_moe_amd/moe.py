@@ -49,7 +49,8 @@ def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, select
 
     expert_path: "predecoded" decodes the split bitmaps once per projection and runs the MFMA
     grouped GEMMs (needs uniform 64-column groups and no output scale or bias); "fused" decodes
-    inside the exact grouped GEMM; "auto" takes "predecoded" whenever the payloads allow it."""
+    inside the grouped GEMMs (the in-kernel-decode MFMA kernels when every payload suits them,
+    ext.decode_payload_ok); "auto" takes "predecoded" whenever the payloads allow it."""
     T, H = int(x16.size(0)), int(x16.size(1))
     k = int(selected_experts.size(1))
     if T * k == 0:
@@ -101,6 +102,9 @@ def _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, ou
     if predecodable and expert_path != "fused":
         return _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype,
                                        shared_expert)
+    if all(ext.decode_payload_ok(p) for p in (pg, pu, pd)):
+        return _decode_fused_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype,
+                                         shared_expert)
     sc = _in_scales(backbones)
     hid_g, hid_u = shared_projection_pair(x16, backbones["gate"], backbones["up"], row_index=gti,
                                           in_scale_a=sc["gate"], in_scale_b=sc["up"])
@@ -185,8 +189,7 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     bitmaps once per projection (TriSMoE_cuda.cpp:836-853), then run the predecoded grouped GEMMs
     (TriSMoE_cuda.cpp:855-889, 922-974).  Active experts come first in the padded route, so
     min(num_experts, R) segments cover every routed row and the later segments are empty.  The
-    decodes depend only on the route, so they run on a side stream while the gate/up backbones
-    run on the caller's stream.
+    decodes depend only on the route and run in one launch ahead of the gate/up backbones.
 
     Null-space compensation terms (qlinear_cuda.py:2322-2334) are computed apart from the GEMM outputs and
     joined later, with the same fp16 adds: gate/up's on a stream of their own from the routed inputs
@@ -204,7 +207,6 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     bufs = {name: _predecode_buffer(p, slots, dev) for name, p in (("gate", pg), ("up", pu), ("down", pd))}
     main = torch.cuda.current_stream(dev)
     side = _side_stream(dev)
-    side.wait_stream(main)
     n_mlp = int(pg["qweight1"].size(2))
     comp_g = comp_u = None
     ns_side = None
@@ -219,19 +221,18 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
             ext.ns_compensation_pair_apply_(comp_g, comp_u, x16, eid, seg, ns["gate"], ns["up"], accumulate=False,
                                             row_index=route["grouped_token_indices"])
 
-    # one launch for the three projections (the persistent GEMMs assume the whole GPU, so nothing runs
-    # beside them; two launches, the down bitmaps on either stream, measured slower)
-    with torch.cuda.stream(side):
-        order = (("gate", pg), ("up", pu), ("down", pd))
-        ext.grouped_block_gr_predecode_multi(
-            [(bufs[name], p["q_gmap_gr_words"], p["q_gmap_gr_offsets"], p["q_gmap_gr_meta"], int(p["qweight1"].size(1)),
-              int(p["qweight1"].size(2))) for name, p in order], eid)
-        decoded = bufs
+    # one launch for the three projections, on the caller's stream: beside the backbones it takes the CUs
+    # first and delays them, and the join costs more than the overlap saves (measured on MI355X at the
+    # Mixtral decode shape)
+    order = (("gate", pg), ("up", pu), ("down", pd))
+    ext.grouped_block_gr_predecode_multi(
+        [(bufs[name], p["q_gmap_gr_words"], p["q_gmap_gr_offsets"], p["q_gmap_gr_meta"], int(p["qweight1"].size(1)),
+          int(p["qweight1"].size(2))) for name, p in order], eid)
+    decoded = bufs
     sc = _in_scales(backbones)
     hid_g, hid_u = shared_projection_pair(x16, backbones["gate"], backbones["up"],
                                           row_index=route["grouped_token_indices"], in_scale_a=sc["gate"],
                                           in_scale_b=sc["up"])
-    main.wait_stream(side)
     if ns_side is not None:
         main.wait_stream(ns_side)
     names = ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx", "col_pack3", "row_pack3")
@@ -270,6 +271,39 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     elif ns["down"] is not None:
         ext.ns_compensation_apply_(d_out, mlp, eid, seg, ns["down"])
     return _combine(x16, d_out, route, w16, output_dtype, shared_expert, d_comp=comp_d)
+
+
+def _decode_fused_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype, shared_expert):
+    """The GR split bitmaps decoded inside the grouped GEMMs (the reference's fused decode path,
+    TriSMoE_cuda_kernel.cu:5382-5586): gate and up in one launch with act_fn(g) * u in its epilogue, read through
+    the route's token indices from per-token backbone outputs (every routed row of a token has the same shared
+    hidden, modeling_mixtral.py:467-476), then the down GEMM over the routed rows.  Output scale and bias, and
+    null-space compensation terms, are applied as in the predecoded path."""
+    slots = min(num_experts, R)
+    eid = route["expert_ids"][:slots]
+    seg = route["segment_offsets"][: slots + 1]
+    gti = route["grouped_token_indices"]
+    pg, pu, pd = payloads["gate"], payloads["up"], payloads["down"]
+    ns = _ns_payloads(payloads)
+    sc = _in_scales(backbones)
+    hid_g, hid_u = shared_projection_pair(x16, backbones["gate"], backbones["up"], in_scale_a=sc["gate"],
+                                          in_scale_b=sc["up"])
+    if ns["gate"] is None and ns["up"] is None:
+        mlp = ext.grouped_decode_pair_forward(hid_g, hid_u, pg, pu, eid, seg, R, row_index=gti, swiglu=True)
+    else:
+        g, u = ext.grouped_decode_pair_forward(hid_g, hid_u, pg, pu, eid, seg, R, row_index=gti)
+        n_mlp = int(g.size(1))
+        dev = x16.device
+        comp_g = torch.empty((R, n_mlp), dtype=torch.float16, device=dev) if ns["gate"] is not None else None
+        comp_u = torch.empty((R, n_mlp), dtype=torch.float16, device=dev) if ns["up"] is not None else None
+        ext.ns_compensation_pair_apply_(comp_g, comp_u, x16, eid, seg, ns["gate"], ns["up"], accumulate=False,
+                                        row_index=gti)
+        mlp = ext.swiglu_mul(g, u, comp_gate=comp_g, comp_up=comp_u)
+    hid_d = shared_projection(mlp, backbones["down"], in_scale=sc["down"])
+    d_out = ext.grouped_decode_forward(hid_d, pd, eid, seg, R)
+    if ns["down"] is not None:
+        ext.ns_compensation_apply_(d_out, mlp, eid, seg, ns["down"])
+    return _combine(x16, d_out, route, w16, output_dtype, shared_expert)
 
 
 class TrisSparseMoeBlock(nn.Module):
