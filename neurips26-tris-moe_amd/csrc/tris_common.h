@@ -53,6 +53,62 @@ __device__ __forceinline__ uint32_t low_mask(int bits) {
   return bits >= 32 ? 0xFFFFFFFFu : ((1u << bits) - 1u);
 }
 
+// DPP lane move (register to register, no LDS round trip): lanes whose source lies outside their row, or
+// whose row is masked off by RowMask, take `identity`.  Every lane of the wavefront must be active.
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t identity, uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(static_cast<int>(identity), static_cast<int>(v), Ctrl, RowMask, 0xF, false));
+}
+
+// Inclusive scan over the 64 lanes of a wavefront (all active): row shifts within each row of 16, then the
+// row-15 and row-31 broadcasts carry the row totals forward.  op(own, earlier) combines a lane's value with
+// the combined value of the lanes before it; the tree is fixed, so every run combines in the same order.
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, uint32_t identity, Op op) {
+  v = op(v, dpp_mov<0x111, 0xF>(identity, v));  // row_shr:1
+  v = op(v, dpp_mov<0x112, 0xF>(identity, v));  // row_shr:2
+  v = op(v, dpp_mov<0x114, 0xF>(identity, v));  // row_shr:4
+  v = op(v, dpp_mov<0x118, 0xF>(identity, v));  // row_shr:8
+  v = op(v, dpp_mov<0x142, 0xA>(identity, v));  // row_bcast:15 into rows 1 and 3
+  v = op(v, dpp_mov<0x143, 0xC>(identity, v));  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
+__device__ __forceinline__ int wave_incl_sum_i32(int v) {
+  return static_cast<int>(
+      wave_incl_scan(static_cast<uint32_t>(v), 0u, [](uint32_t own, uint32_t earlier) { return own + earlier; }));
+}
+
+// The wave-uniform maximum of int keys whose maximum is known to be >= 0 (every lane active): row maxima by
+// DPP row shifts (a lane whose source lies outside its row takes 0, which cannot exceed that maximum), then
+// the four rows' last lanes combined in scalar registers.
+__device__ __forceinline__ int wave_max_nonneg_i32(int v) {
+  v = max(v, static_cast<int>(dpp_mov<0x111, 0xF>(0u, static_cast<uint32_t>(v))));  // row_shr:1
+  v = max(v, static_cast<int>(dpp_mov<0x112, 0xF>(0u, static_cast<uint32_t>(v))));  // row_shr:2
+  v = max(v, static_cast<int>(dpp_mov<0x114, 0xF>(0u, static_cast<uint32_t>(v))));  // row_shr:4
+  v = max(v, static_cast<int>(dpp_mov<0x118, 0xF>(0u, static_cast<uint32_t>(v))));  // row_shr:8
+  const int a = __builtin_amdgcn_readlane(v, 15);
+  const int b = __builtin_amdgcn_readlane(v, 31);
+  const int c = __builtin_amdgcn_readlane(v, 47);
+  const int d = __builtin_amdgcn_readlane(v, 63);
+  return max(max(a, b), max(c, d));
+}
+
+// Wave-uniform reductions (the scan's last lane, read into a scalar register).
+__device__ __forceinline__ float wave_max_f32(float v) {
+  const uint32_t r = wave_incl_scan(__float_as_uint(v), __float_as_uint(-INFINITY), [](uint32_t own, uint32_t e) {
+    return __float_as_uint(fmaxf(__uint_as_float(own), __uint_as_float(e)));
+  });
+  return __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(r), kWave - 1)));
+}
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  const uint32_t r = wave_incl_scan(__float_as_uint(v), 0u, [](uint32_t own, uint32_t e) {
+    return __float_as_uint(__uint_as_float(own) + __uint_as_float(e));
+  });
+  return __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(r), kWave - 1)));
+}
+
 // Host-side error reporting shared by every C-ABI entry point.
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);

@@ -14,7 +14,7 @@
 namespace tris {
 
 constexpr int kSpanThreads = 256;
-constexpr int kSpanWgTarget = 1024;  // persistent workgroups per launch (four per CU)
+constexpr int kSpanWgTarget = 1024;  // persistent workgroups per launch: at most four per CU
 
 // One projection's stream; jobs of one launch share the routed expert list.
 struct GrJob {
@@ -34,41 +34,83 @@ struct GrJobs {
   GrJob job[TRIS_MAX_PREDECODE_JOBS];
 };
 
-// grid = (workgroups per (slot, job), slots, jobs).  Persistent over block batches: a workgroup copies the
-// tables once, then decodes batches blockIdx.x, blockIdx.x + gridDim.x, ... of kSpanThreads / S blocks,
-// loading the next batch's block headers and span words while it decodes the current one.
+// Work items: (job, slot, batch of kSpanThreads / S blocks), job-major, then slot, then batch.  The grid is
+// persistent over them: a workgroup copies the tables and the slots' expert ids to LDS once, then takes items
+// blockIdx.x, blockIdx.x + gridDim.x, ...; the next item's block headers are loaded before the current item
+// is decoded and its span words after, so their latency overlaps the decode.
+struct GrWork {
+  int num_jobs;
+  int num_slots;
+  int first[TRIS_MAX_PREDECODE_JOBS + 1];  // first item of each job; first[num_jobs] = all items
+};
+
+constexpr int kSpanLdsSlots = 1024;  // expert ids staged in LDS (later slots read from memory)
+
 template <int S>
-__global__ __launch_bounds__(kSpanThreads) void gr_decode_span_kernel(GrJobs jobs, const int32_t* __restrict__ expert_ids) {
+struct GrItem {
+  int q, slot, block0;
+  GrSpan<S> sp;
+};
+
+// Item w's job, slot and first block, and its block headers (an empty item past the last).
+template <int S>
+__device__ __forceinline__ void gr_item_header(const GrJobs& jobs, const GrWork& wk, const int32_t* __restrict__ eids,
+                                               const int32_t* __restrict__ expert_ids, int w, int g, GrItem<S>& it) {
+  constexpr int kBlocksPerWg = kSpanThreads / S;
+  const bool exists = w < wk.first[wk.num_jobs];
+  const int wv = exists ? w : 0;
+  int q = 0;
+#pragma unroll
+  for (int i = 1; i < TRIS_MAX_PREDECODE_JOBS; ++i) q += (i < wk.num_jobs && wv >= wk.first[i]) ? 1 : 0;
+  const GrJob& jb = jobs.job[q];
+  const int nblk = jb.nblk;
+  const int batches = ceil_div(nblk, kBlocksPerWg);
+  const int local = wv - wk.first[q];
+  it.q = q;
+  it.slot = local / batches;
+  it.block0 = (local - it.slot * batches) * kBlocksPerWg;
+  const int expert = it.slot < kSpanLdsSlots ? eids[it.slot] : expert_ids[it.slot];
+  const bool ev = exists && expert >= 0 && expert < jb.num_experts;
+  const int ex = ev ? expert : 0;
+  gr_span_header<S>(it.sp, jb.words + static_cast<int64_t>(ex) * jb.words_stride,
+                    jb.offsets + static_cast<int64_t>(ex) * (nblk + 1), jb.meta + static_cast<int64_t>(ex) * nblk,
+                    it.block0 + g, ev && it.block0 + g < nblk, expert_ids);
+}
+
+template <int S>
+__global__ __launch_bounds__(kSpanThreads) void gr_decode_span_kernel(GrJobs jobs, GrWork wk,
+                                                                      const int32_t* __restrict__ expert_ids) {
   constexpr int kBlocksPerWg = kSpanThreads / S;
   __shared__ GrTables tab;
   __shared__ uint32_t outb[kBlocksPerWg][kGrBlockStride];
-  const GrJob& jb = jobs.job[blockIdx.z];
-  const int slot = blockIdx.y;
-  const int nblk = jb.nblk;
-  if (static_cast<int>(blockIdx.x) * kBlocksPerWg >= nblk) return;  // uniform over the workgroup
+  __shared__ int32_t eids[kSpanLdsSlots];
+  const int total = wk.first[wk.num_jobs];
+  int w = blockIdx.x;
+  if (w >= total) return;  // uniform over the workgroup
   const int tid = threadIdx.x;
   const int g = tid / S;
   const int j = tid % S;
-  const int expert = expert_ids[slot];
-  const bool evalid = expert >= 0 && expert < jb.num_experts;
-  const int32_t* words = evalid ? jb.words + static_cast<int64_t>(expert) * jb.words_stride : nullptr;
-  const int32_t* offsets = evalid ? jb.offsets + static_cast<int64_t>(expert) * (nblk + 1) : nullptr;
-  const int32_t* meta = evalid ? jb.meta + static_cast<int64_t>(expert) * nblk : nullptr;
-  const int stride = static_cast<int>(gridDim.x) * kBlocksPerWg;
-  int block0 = blockIdx.x * kBlocksPerWg;
-  GrSpan<S> sp;
-  gr_span_load<S>(sp, words, offsets, meta, block0 + g, evalid && block0 + g < nblk, j);
+  const int nl = wk.num_slots < kSpanLdsSlots ? wk.num_slots : kSpanLdsSlots;
+  for (int i = tid; i < nl; i += kSpanThreads) eids[i] = expert_ids[i];
   gr_tables_to_lds(&tab);
-  for (; block0 < nblk; block0 += stride) {
+  __syncthreads();
+  GrItem<S> cur;
+  gr_item_header<S>(jobs, wk, eids, expert_ids, w, g, cur);
+  gr_span_words<S>(cur.sp, j);
+  for (; w < total; w += gridDim.x) {
     for (int idx = tid; idx < kBlocksPerWg * kGrBlockStride; idx += kSpanThreads) {
       outb[idx / kGrBlockStride][idx % kGrBlockStride] = 0u;
     }
     __syncthreads();
-    const GrSpan<S> cur = sp;
-    const int next0 = block0 + stride;
-    gr_span_load<S>(sp, words, offsets, meta, next0 + g, evalid && next0 + g < nblk, j);
-    gr_decode_block_group<S>(cur, &tab, outb[g] + kGrPadFront, j);
+    GrItem<S> nx;
+    gr_item_header<S>(jobs, wk, eids, expert_ids, w + static_cast<int>(gridDim.x), g, nx);
+    gr_decode_block_group<S>(cur.sp, &tab, outb[g] + kGrPadFront, j);
+    gr_span_words<S>(nx.sp, j);
     __syncthreads();
+    const GrJob& jb = jobs.job[cur.q];
+    const int nblk = jb.nblk;
+    const int block0 = cur.block0;
+    const int slot = cur.slot;
     if (jb.dense_rows == 0) {
       int32_t* dst = jb.out + (static_cast<int64_t>(slot) * nblk + block0) * kGrWords;
       for (int idx = tid; idx < kBlocksPerWg * kGrWords; idx += kSpanThreads) {
@@ -81,15 +123,16 @@ __global__ __launch_bounds__(kSpanThreads) void gr_decode_span_kernel(GrJobs job
       for (int idx = tid; idx < kBlocksPerWg * kGrWords; idx += kSpanThreads) {
         const int b = block0 + idx / kGrWords;
         if (b >= nblk) continue;
-        const int w = idx % kGrWords;
-        const int row = (b / jb.num_out_blocks) * kGrPackedRows + w / kTileOut;
-        const int col = (b % jb.num_out_blocks) * kTileOut + w % kTileOut;
+        const int wd = idx % kGrWords;
+        const int row = (b / jb.num_out_blocks) * kGrPackedRows + wd / kTileOut;
+        const int col = (b % jb.num_out_blocks) * kTileOut + wd % kTileOut;
         if (row < jb.dense_rows && col < jb.dense_cols) {
-          dst[static_cast<int64_t>(row) * jb.dense_cols + col] = static_cast<int32_t>(outb[idx / kGrWords][kGrPadFront + w]);
+          dst[static_cast<int64_t>(row) * jb.dense_cols + col] = static_cast<int32_t>(outb[idx / kGrWords][kGrPadFront + wd]);
         }
       }
     }
-    __syncthreads();  // the next batch zeroes and rewrites outb
+    cur = nx;
+    __syncthreads();  // the next item zeroes and rewrites outb
   }
 }
 
@@ -122,17 +165,26 @@ int launch_gr_jobs(const GrJobs& jobs, int num_jobs, const int32_t* expert_ids, 
   // over more blocks
   const int S = total > 8192 ? 16 : 32;
   const int per_wg = kSpanThreads / S;
-  // persistent workgroups: about kSpanWgTarget in all, each copying the tables once
-  const int wanted = ceil_div(max_nblk, per_wg);
-  const int share = ceil_div(kSpanWgTarget, num_slots * num_jobs);
-  const int gx = wanted < share ? wanted : (share < 1 ? 1 : share);
+  GrWork wk{};
+  wk.num_jobs = num_jobs;
+  wk.num_slots = num_slots;
+  int64_t items = 0;
+  for (int q = 0; q < num_jobs; ++q) {
+    wk.first[q] = static_cast<int>(items);
+    items += static_cast<int64_t>(num_slots) * ceil_div(jobs.job[q].nblk, per_wg);
+  }
+  TRIS_REQUIRE(items < (1LL << 30), "%s: too many blocks", who);
+  for (int q = num_jobs; q <= TRIS_MAX_PREDECODE_JOBS; ++q) wk.first[q] = static_cast<int>(items);
+  // persistent workgroups: one per item up to kSpanWgTarget (four per CU, all resident), so every item that can
+  // run at once does; past that each takes several
+  int64_t grid = items < kSpanWgTarget ? items : kSpanWgTarget;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (S == 16) {
-    hipLaunchKernelGGL((gr_decode_span_kernel<16>), dim3(gx, num_slots, num_jobs), dim3(kSpanThreads), 0, s, jobs,
-                       expert_ids);
+    hipLaunchKernelGGL((gr_decode_span_kernel<16>), dim3(static_cast<unsigned>(grid)), dim3(kSpanThreads), 0, s, jobs,
+                       wk, expert_ids);
   } else {
-    hipLaunchKernelGGL((gr_decode_span_kernel<32>), dim3(gx, num_slots, num_jobs), dim3(kSpanThreads), 0, s, jobs,
-                       expert_ids);
+    hipLaunchKernelGGL((gr_decode_span_kernel<32>), dim3(static_cast<unsigned>(grid)), dim3(kSpanThreads), 0, s, jobs,
+                       wk, expert_ids);
   }
   return check_launch(who);
 }

@@ -154,13 +154,8 @@ __device__ inline void gr_serial_decode(const int32_t* __restrict__ payload, int
 }
 
 // Group scans over S = 16 or 32 lanes (one or two DPP rows of a wavefront) with DPP row shifts and the
-// row-15 broadcast: register moves between lanes, no LDS round trips.  Lanes whose source lies outside their
-// row take `identity`.  Every lane of a group must be active.
-template <int Ctrl, int RowMask>
-__device__ __forceinline__ uint32_t dpp_mov(uint32_t identity, uint32_t v) {
-  return static_cast<uint32_t>(
-      __builtin_amdgcn_update_dpp(static_cast<int>(identity), static_cast<int>(v), Ctrl, RowMask, 0xF, false));
-}
+// row-15 broadcast (dpp_mov): register moves between lanes, no LDS round trips.  Every lane of a group must
+// be active.
 
 // Inclusive scan: op(own, earlier) combines a lane's value with the combined value of lanes before it.
 template <int S, typename Op>
@@ -233,23 +228,29 @@ struct GrSpan {
   uint32_t w[kMaxWords];
 };
 
-// Read the block header and the lane's span words.  Loads are issued together
-// so their latencies overlap.
+// The block header (stream start, word count, meta) of block_idx, or an empty block when !valid.  The loads are
+// issued without a branch (an invalid block reads `dummy`, any readable word), so nothing waits for them until
+// the header is used.
 template <int S>
-__device__ __forceinline__ void gr_span_load(GrSpan<S>& sp, const int32_t* __restrict__ words,
-                                             const int32_t* __restrict__ offsets, const int32_t* __restrict__ meta,
-                                             int block_idx, bool valid, int j) {
-  sp.payload = nullptr;
-  sp.word_count = 0;
-  sp.meta = 0;
+__device__ __forceinline__ void gr_span_header(GrSpan<S>& sp, const int32_t* __restrict__ words,
+                                               const int32_t* __restrict__ offsets, const int32_t* __restrict__ meta,
+                                               int block_idx, bool valid, const int32_t* __restrict__ dummy) {
+  valid = valid && words != nullptr && offsets != nullptr && meta != nullptr;
+  const int32_t* o = valid ? offsets + block_idx : dummy;
+  const int32_t* m = valid ? meta + block_idx : dummy;
+  const int begin = o[0];
+  const int end = o[valid ? 1 : 0];
+  const int mv = m[0];
+  sp.payload = valid ? words + begin : nullptr;
+  sp.word_count = valid ? end - begin : 0;
+  sp.meta = valid ? mv : 0;
   sp.w0 = 0;
   sp.nw = 0;
-  if (valid && words != nullptr && offsets != nullptr && meta != nullptr) {
-    const int begin = offsets[block_idx];
-    sp.word_count = offsets[block_idx + 1] - begin;
-    sp.meta = meta[block_idx];
-    sp.payload = words + begin;
-  }
+}
+
+// The lane's span words of a block whose header is loaded.
+template <int S>
+__device__ __forceinline__ void gr_span_words(GrSpan<S>& sp, int j) {
   const int wc = sp.word_count;
   if (wc > 0 && wc <= kGrWords) {
     const int span = (wc + S - 1) / S;

@@ -615,10 +615,18 @@ def backbone_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
-# From this many rows on the backbone is a plain dense GEMM better served by the library GEMM (hipBLASLt
-# through F.linear, as the reference's compute_shared_hidden, qlinear_cuda.py:4454-4502); below it, the
-# decode-shaped split-K MFMA kernel of tris_backbone_linear.
+# From this many rows on, and with more than BACKBONE_LIBRARY_MIN_ELEMS activation elements (rows x
+# in_features), the backbone is a plain dense GEMM better served by the library GEMM (hipBLASLt through
+# F.linear, as the reference's compute_shared_hidden, qlinear_cuda.py:4454-4502); otherwise the decode-shaped
+# split-K MFMA kernel of tris_backbone_linear.  Measured on MI355X (kernel vs library, us): in 2048 pair at
+# 256 rows 12.7 vs 16.4; in 512 at 256 rows 7.3 vs 16.7, at 512 rows 8.1 vs 5.4; in 4096 pair at 256 rows
+# 25.3 vs 18.0; in 14336 at 128 rows 23.0 vs 14.6.
 BACKBONE_LIBRARY_MIN_ROWS = 256
+BACKBONE_LIBRARY_MIN_ELEMS = 1 << 19
+
+
+def _backbone_use_library(rows: int, in_features: int) -> bool:
+    return rows >= BACKBONE_LIBRARY_MIN_ROWS and rows * in_features > BACKBONE_LIBRARY_MIN_ELEMS
 
 
 def _backbone_library(x, svs, in_scales, row_index):
@@ -650,7 +658,7 @@ def backbone_linear(x: torch.Tensor, sv: torch.Tensor, in_scale: torch.Tensor | 
     if in_scale is not None:
         _check_cuda("in_scale", in_scale, torch.float16, 1, x.device)
     rank, in_f = int(sv.size(0)), int(sv.size(1))
-    if tokens >= BACKBONE_LIBRARY_MIN_ROWS:
+    if _backbone_use_library(tokens, in_f):
         return _backbone_library(x, (sv,), (in_scale,), row_index)[0]
     out = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
     lib = _lib.load()
@@ -679,7 +687,7 @@ def backbone_linear_pair(x: torch.Tensor, sv_a: torch.Tensor, sv_b: torch.Tensor
             if sc.numel() != x.size(1):
                 raise RuntimeError(f"{name} must hold in_features values")
     rank, in_f = int(sv_a.size(0)), int(sv_a.size(1))
-    if tokens >= BACKBONE_LIBRARY_MIN_ROWS:
+    if _backbone_use_library(tokens, in_f):
         out_a, out_b = _backbone_library(x, (sv_a, sv_b), (in_scale_a, in_scale_b), row_index)
         return out_a, out_b
     out_a = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)

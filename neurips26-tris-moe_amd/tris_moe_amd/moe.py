@@ -150,8 +150,11 @@ def _ns_payloads(payloads: dict) -> dict:
 def _combine(x16, d_out, route, w16, output_dtype, shared_expert, d_comp=None):
     shared = None
     if shared_expert is not None:
+        # the always-on fp16 expert down(act_fn(gate x) * up x): gate and up in one backbone launch, SiLU and
+        # the product in fp16 as F.silu(g) * u, then the down projection
         wg, wu, wd = shared_expert
-        shared = F.linear(F.silu(F.linear(x16, wg)) * F.linear(x16, wu), wd).contiguous()
+        g, u = ext.backbone_linear_pair(x16, wg, wu)
+        shared = ext.backbone_linear(ext.swiglu_mul(g, u), wd)
     out = ext.moe_combine(d_out, route["inverse_perm"], w16, shared, expert_comp=d_comp)
     return out if output_dtype == torch.bfloat16 else out.to(output_dtype)
 
