@@ -199,58 +199,79 @@ __device__ __forceinline__ void route_token_topk(const float* __restrict__ row, 
   }
 }
 
-// One token's softmax and top-k by a whole wavefront (the same picks, in the same order, as route_token_topk):
-// coalesced reads of the logits, the max and the exp-sum reduced across lanes, then top_k rounds, each taking
-// the largest probability strictly below the previous pick in (probability, lower expert first) order.  The
-// picks depend only on the logits (exp is monotone and every probability shares the max and the sum); the
-// sum's order differs from the serial one, so a probability can differ in its last bit.
-template <int K>
-__device__ __forceinline__ void route_token_topk_wave(const float* __restrict__ row, int num_experts, int top_k,
-                                                      float bp[K], int be[K]) {
+// One token's softmax and top-k by a whole wavefront (wave-uniform call, every lane active): the same picks,
+// in the same order, as route_token_topk.  Lane l holds experts l + 64 q (q < P) in registers; the max and
+// the exp-sum are wave reductions (a fixed DPP tree: the serial sum's order differs, so a probability can
+// differ from route_token_topk's in its last bit; the picks compare those probabilities as the oracle's
+// argsort does).  Then top_k rounds, each the wave maximum of the probabilities not yet picked and, by
+// ballots over q, the lowest expert holding it (ties to the lower expert id); the owner clears its slot.
+// A NaN probability (NaN or infinite logits) counts as 0, so every round finds an expert in range.
+// Lane j < top_k returns pick j: its expert and its weight, renormalised over the picks (summed in pick
+// order) or not.
+// The logits of one token for route_token_wave: lane l takes experts l + 64 q.
+template <int P>
+__device__ __forceinline__ void route_load_logits(const float* __restrict__ row, int num_experts, float (&pv)[P]) {
   const int lane = static_cast<int>(__lane_id());
-  float m = -INFINITY;
-  for (int e = lane; e < num_experts; e += kWave) m = fmaxf(m, row[e]);
 #pragma unroll
-  for (int d = kWave / 2; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
-  float sum = 0.0f;
-  for (int e = lane; e < num_experts; e += kWave) sum += expf(row[e] - m);
+  for (int q = 0; q < P; ++q) {
+    const int e = lane + kWave * q;
+    pv[q] = e < num_experts ? row[e] : -INFINITY;
+  }
+}
+
+// pv: the lane's logits (route_load_logits).
+template <int P>
+__device__ __forceinline__ void route_token_wave(float (&pv)[P], int num_experts, int top_k, int renormalize,
+                                                 int& pick_e, float& pick_w) {
+  const int lane = static_cast<int>(__lane_id());
+  float lm = pv[0];
 #pragma unroll
-  for (int d = kWave / 2; d >= 1; d >>= 1) sum += __shfl_xor(sum, d);
-  float lp = INFINITY;  // the previous pick
-  int le = -1;
+  for (int q = 1; q < P; ++q) lm = fmaxf(lm, pv[q]);
+  const float m = wave_max_f32(lm);
+  float ls = 0.0f;
 #pragma unroll
-  for (int j = 0; j < K; ++j) {
-    bp[j] = -1.0f;
-    be[j] = -1;
-    if (j < top_k) {
-      float cp = -1.0f;
-      int ce = num_experts;  // none
-      for (int e = lane; e < num_experts; e += kWave) {
-        const float pe = expf(row[e] - m) / sum;
-        const bool below = pe < lp || (pe == lp && e > le);
-        const bool better = pe > cp || (pe == cp && e < ce);
-        if (below && better) {
-          cp = pe;
-          ce = e;
-        }
-      }
+  for (int q = 0; q < P; ++q) {
+    if (lane + kWave * q < num_experts) ls += expf(pv[q] - m);
+  }
+  const float sum = wave_sum_f32(ls);
+  // Probabilities as int keys: a non-negative float's bits order as a signed int, and every key in range
+  // is >= 0, so the -1.0f of an expert out of range or already picked sorts below them all.
+  int kv[P];
 #pragma unroll
-      for (int d = kWave / 2; d >= 1; d >>= 1) {
-        const float op = __shfl_xor(cp, d);
-        const int oe = __shfl_xor(ce, d);
-        if (op > cp || (op == cp && oe < ce)) {
-          cp = op;
-          ce = oe;
-        }
-      }
-      if (ce < num_experts) {
-        bp[j] = cp;
-        be[j] = ce;
-        lp = cp;
-        le = ce;
+  for (int q = 0; q < P; ++q) {
+    const float p = expf(pv[q] - m) / sum;
+    kv[q] = __float_as_int(lane + kWave * q < num_experts ? (p == p ? p : 0.0f) : -1.0f);
+  }
+  float denom = 0.0f, my_p = 0.0f;
+  int my_e = -1;
+  for (int j = 0; j < top_k; ++j) {
+    int lmax = kv[0];
+#pragma unroll
+    for (int q = 1; q < P; ++q) lmax = max(lmax, kv[q]);
+    const int best = wave_max_nonneg_i32(lmax);  // an unpicked expert in range remains (top_k <= num_experts)
+    int e = 0;
+    bool found = false;
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      const uint64_t hit = __ballot(kv[q] == best);
+      if (!found && hit != 0) {
+        e = kWave * q + __ffsll(static_cast<unsigned long long>(hit)) - 1;
+        found = true;
       }
     }
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      if (q == (e >> 6) && lane == (e & (kWave - 1))) kv[q] = __float_as_int(-1.0f);
+    }
+    const float bp = __int_as_float(best);
+    if (lane == j) {
+      my_p = bp;
+      my_e = e;
+    }
+    denom += bp;
   }
+  pick_e = my_e;
+  pick_w = renormalize ? my_p / denom : my_p;
 }
 
 // The routing weight of pick j: renormalised over the k picks (summed in pick order) or not.
@@ -264,10 +285,12 @@ __device__ __forceinline__ float route_pick_weight(const float bp[K], int top_k,
   return renormalize ? bp[j] / denom : bp[j];
 }
 
-constexpr int kRouteWaveMax = 64;  // routed rows and experts of the one-wavefront router
+constexpr int kRouteWaveMaxRows = 64;     // routed rows of the one-wavefront router
+constexpr int kRouteLaneMaxExperts = 8;   // its experts: a lane routes a token alone
 
-// One wavefront, no barriers, for at most 64 routed rows and 64 experts: lane t < tokens takes token
-// t's softmax and top-k; lane i < tokens * top_k then holds routed entry i (expert sel_i); lane e <
+// One wavefront, no barriers, for at most 64 routed rows and 8 experts: lane t < tokens takes token t's
+// softmax and top-k (a short serial chain over few experts); lane i < tokens * top_k then holds routed
+// entry i (expert sel_i); lane e <
 // num_experts counts its expert by ballots, and prefix sums over lanes give the compacted active
 // experts and their segment / problem offsets; entry i's place in its segment is the number of
 // earlier entries of its expert.  The same outputs as route_topk_small_kernel.
@@ -278,7 +301,7 @@ __global__ __launch_bounds__(kWave) void route_topk_wave_kernel(
     int64_t* __restrict__ perm, int64_t* __restrict__ token_idx, int64_t* __restrict__ slots,
     int32_t* __restrict__ grouped_expert_ids, int32_t* __restrict__ expert_ids, int32_t* __restrict__ segment_offsets,
     int32_t* __restrict__ problem_offsets, int32_t* __restrict__ counts, int32_t* __restrict__ inverse_perm) {
-  __shared__ float lg[kRouteWaveMax * kRouteWaveMax];  // the logits, [tokens][num_experts]
+  __shared__ float lg[kRouteWaveMaxRows * kRouteLaneMaxExperts];  // the logits, [tokens][num_experts]
   const int lane = static_cast<int>(threadIdx.x);
   const int total = tokens * top_k;
   // every load in flight at once (coalesced), then each token reads its row from LDS
@@ -380,99 +403,95 @@ __global__ __launch_bounds__(kWave) void route_topk_wave_kernel(
   }
 }
 
-// One workgroup: per token softmax (fp32, max-subtracted, summed in expert
-// order), top-k by probability with ties to the lower expert id (a stable
-// descending sort, as the oracle's argsort), optional renormalisation over the
-// k picks (summed in pick order), fp16 weights; then the histogram, scan and
-// padded outputs of route_histogram_kernel and a stable scatter in which each
-// routed entry counts the earlier entries of its expert.
+// One workgroup, one launch: per token softmax and top-k (route_token_wave, one wavefront per token: P
+// experts per lane, P * 64 >= num_experts) with optional renormalisation over the k picks and fp16 weights;
+// then the histogram and scan of route_histogram_kernel (thread e owns expert e: wave scans by DPP, one LDS
+// exchange of the wave totals) and a stable scatter.  A token's picks are distinct experts, so an entry's
+// place in its expert's segment is the number of earlier tokens that picked the expert: tokens go in chunks
+// of 64, each expert's tokens of the chunk marked in a 64-bit mask, the segment bases advanced by the
+// masks' popcounts after each chunk.
+template <int P>
 __global__ __launch_bounds__(kRouteThreads) void route_topk_small_kernel(
     const float* __restrict__ logits, int tokens, int num_experts, int top_k, int renormalize, int m_tile,
     uint16_t* __restrict__ weights16, float* __restrict__ weights32, int64_t* __restrict__ selected,
     int64_t* __restrict__ perm, int64_t* __restrict__ token_idx, int64_t* __restrict__ slots,
     int32_t* __restrict__ grouped_expert_ids, int32_t* __restrict__ expert_ids, int32_t* __restrict__ segment_offsets,
     int32_t* __restrict__ problem_offsets, int32_t* __restrict__ counts, int32_t* __restrict__ inverse_perm) {
+  static_assert(kRouteSmallMaxExperts == kRouteThreads, "thread e owns expert e");
+  static_assert(kRouteMaxTopK * kWave <= kRouteThreads, "a chunk of 64 tokens' entries fits the workgroup");
+  constexpr int kWaves = kRouteThreads / kWave;
   __shared__ int16_t sel[kRouteSmallMaxRows];
   __shared__ int cnt[kRouteSmallMaxExperts];
-  __shared__ int seg_of[kRouteSmallMaxExperts];  // first row of each expert's segment
-  __shared__ int scan_active[kRouteThreads];
-  __shared__ int scan_rows[kRouteThreads];
-  __shared__ int scan_tiles[kRouteThreads];
+  __shared__ int seg_of[kRouteSmallMaxExperts];                   // segment base of each expert's next tokens
+  __shared__ unsigned long long tok_bits[kRouteSmallMaxExperts];  // the chunk's tokens that picked expert e
+  __shared__ int wave_tot[3][kWaves];
   const int tid = threadIdx.x;
-  const int total = tokens * top_k;
-  for (int e = tid; e < num_experts; e += kRouteThreads) cnt[e] = 0;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int e = tid;
+  if (e < num_experts) {
+    cnt[e] = 0;
+    tok_bits[e] = 0ull;
+  }
   __syncthreads();
-  // ---- softmax and top-k, one wavefront per token
-  {
-    const int wave = tid / kWave;
-    const int lane = tid % kWave;
-    for (int t = wave; t < tokens; t += kRouteThreads / kWave) {
-      float bp[kRouteMaxTopK];
-      int be[kRouteMaxTopK];
-      route_token_topk_wave<kRouteMaxTopK>(logits + static_cast<int64_t>(t) * num_experts, num_experts, top_k, bp,
-                                           be);
-      if (lane < top_k) {
-        // lane j writes pick j
+  // ---- softmax and top-k, one wavefront per token; lane j writes pick j.  The wave's next token's logits
+  // are loaded while this one is routed.
+  float nxt[P];
+  if (wave < tokens) route_load_logits<P>(logits + static_cast<int64_t>(wave) * num_experts, num_experts, nxt);
+  for (int t = wave; t < tokens; t += kWaves) {
+    float pv[P];
 #pragma unroll
-        for (int j = 0; j < kRouteMaxTopK; ++j) {
-          if (j == lane) {
-            const float w = route_pick_weight<kRouteMaxTopK>(bp, top_k, renormalize, j);
-            const int i = t * top_k + j;
-            sel[i] = static_cast<int16_t>(be[j]);
-            if (selected != nullptr) selected[i] = be[j];
-            weights16[i] = f2h_bits(w);
-            if (weights32 != nullptr) weights32[i] = w;
-            if (be[j] >= 0) atomicAdd(&cnt[be[j]], 1);
-          }
-        }
-      }
+    for (int q = 0; q < P; ++q) pv[q] = nxt[q];
+    if (t + kWaves < tokens) {
+      route_load_logits<P>(logits + static_cast<int64_t>(t + kWaves) * num_experts, num_experts, nxt);
+    }
+    int pe;
+    float pw;
+    route_token_wave<P>(pv, num_experts, top_k, renormalize, pe, pw);
+    if (lane < top_k) {
+      const int i = t * top_k + lane;
+      sel[i] = static_cast<int16_t>(pe);
+      if (selected != nullptr) selected[i] = pe;
+      weights16[i] = f2h_bits(pw);
+      if (weights32 != nullptr) weights32[i] = pw;
+      atomicAdd(&cnt[pe], 1);
     }
   }
   __syncthreads();
   // ---- per-expert counts -> compacted active experts, segment and problem offsets
-  const int chunk = (num_experts + kRouteThreads - 1) / kRouteThreads;
-  const int e0 = tid * chunk;
-  const int e1 = (e0 + chunk) < num_experts ? (e0 + chunk) : num_experts;
-  int na = 0, nr = 0, nt = 0;
-  for (int e = e0; e < e1; ++e) {
-    const int c = cnt[e];
-    if (c > 0) {
-      ++na;
-      nr += c;
-      nt += (c + m_tile - 1) / m_tile;
-    }
+  const int c = e < num_experts ? cnt[e] : 0;
+  const bool act = c > 0;
+  const int tiles = act ? (c + m_tile - 1) / m_tile : 0;
+  const uint64_t amask = __ballot(act);
+  const uint64_t lower = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+  const int rows_incl = wave_incl_sum_i32(c);
+  const int tiles_incl = wave_incl_sum_i32(tiles);
+  if (lane == kWave - 1) {
+    wave_tot[0][wave] = __popcll(amask);
+    wave_tot[1][wave] = rows_incl;
+    wave_tot[2][wave] = tiles_incl;
   }
-  scan_active[tid] = na;
-  scan_rows[tid] = nr;
-  scan_tiles[tid] = nt;
   __syncthreads();
-  for (int d = 1; d < kRouteThreads; d <<= 1) {
-    const int va = tid >= d ? scan_active[tid - d] : 0;
-    const int vr = tid >= d ? scan_rows[tid - d] : 0;
-    const int vt = tid >= d ? scan_tiles[tid - d] : 0;
-    __syncthreads();
-    scan_active[tid] += va;
-    scan_rows[tid] += vr;
-    scan_tiles[tid] += vt;
-    __syncthreads();
-  }
-  const int num_active = scan_active[kRouteThreads - 1];
-  const int rows_total = scan_rows[kRouteThreads - 1];
-  const int tiles_total = scan_tiles[kRouteThreads - 1];
-  int a = scan_active[tid] - na;
-  int r = scan_rows[tid] - nr;
-  int tt = scan_tiles[tid] - nt;
-  for (int e = e0; e < e1; ++e) {
-    const int c = cnt[e];
-    seg_of[e] = r;
-    if (c > 0) {
-      expert_ids[a] = e;
-      segment_offsets[a] = r;
-      problem_offsets[a] = tt;
-      ++a;
-      r += c;
-      tt += (c + m_tile - 1) / m_tile;
+  int a0 = 0, r0 = 0, t0 = 0, num_active = 0, rows_total = 0, tiles_total = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int x = wave_tot[0][w], y = wave_tot[1][w], z = wave_tot[2][w];
+    if (w < wave) {
+      a0 += x;
+      r0 += y;
+      t0 += z;
     }
+    num_active += x;
+    rows_total += y;
+    tiles_total += z;
+  }
+  const int seg = r0 + rows_incl - c;
+  if (e < num_experts) seg_of[e] = seg;
+  if (act) {
+    const int a = a0 + __popcll(amask & lower);
+    expert_ids[a] = e;
+    segment_offsets[a] = seg;
+    problem_offsets[a] = t0 + tiles_incl - tiles;
   }
   for (int j = num_active + tid; j < num_experts; j += kRouteThreads) expert_ids[j] = -1;
   for (int j = num_active + tid; j <= num_experts; j += kRouteThreads) {
@@ -484,17 +503,29 @@ __global__ __launch_bounds__(kRouteThreads) void route_topk_small_kernel(
     counts[1] = tiles_total;
   }
   __syncthreads();
-  // ---- stable scatter: an entry's place in its segment = earlier entries of the same expert
-  for (int i = tid; i < total; i += kRouteThreads) {
-    const int e = sel[i];
-    int before = 0;
-    for (int q = 0; q < i; ++q) before += sel[q] == e ? 1 : 0;
-    const int dst = seg_of[e] + before;
-    perm[dst] = i;
-    token_idx[dst] = i / top_k;
-    slots[dst] = i % top_k;
-    grouped_expert_ids[dst] = e;
-    if (inverse_perm != nullptr) inverse_perm[i] = dst;
+  // ---- stable scatter, 64 tokens at a time: thread u takes entry chunk * 64 * top_k + u
+  for (int tc = 0; tc < tokens; tc += kWave) {
+    const int i = tc * top_k + tid;
+    const int t = i / top_k;
+    const bool mine = tid < kWave * top_k && t < tokens;
+    const int ex = mine ? sel[i] : 0;
+    const uint64_t bit = 1ull << (mine ? t - tc : 0);
+    if (mine) atomicOr(&tok_bits[ex], static_cast<unsigned long long>(bit));
+    __syncthreads();
+    if (mine) {
+      const int dst = seg_of[ex] + __popcll(tok_bits[ex] & (bit - 1ull));
+      perm[dst] = i;
+      token_idx[dst] = t;
+      slots[dst] = i - t * top_k;
+      grouped_expert_ids[dst] = ex;
+      if (inverse_perm != nullptr) inverse_perm[i] = dst;
+    }
+    __syncthreads();
+    if (e < num_experts) {
+      seg_of[e] += __popcll(tok_bits[e]);
+      tok_bits[e] = 0ull;
+    }
+    __syncthreads();
   }
 }
 
@@ -554,7 +585,7 @@ extern "C" int tris_route_topk_grouped(const float* router_logits, int32_t num_t
   TRIS_REQUIRE(num_tokens == 0 || (router_logits && routing_weights_f16 && perm && grouped_token_indices &&
                                    grouped_slots && grouped_expert_ids),
                "%s: null pointer", who);
-  if (static_cast<int64_t>(num_tokens) * top_k <= kRouteWaveMax && num_experts <= kRouteWaveMax) {
+  if (static_cast<int64_t>(num_tokens) * top_k <= kRouteWaveMaxRows && num_experts <= kRouteLaneMaxExperts) {
     // the pick lists are sized to top_k's bucket: shorter unrolled insertion chains and less code to fetch
     auto* kernel = top_k <= 2 ? route_topk_wave_kernel<2> : top_k <= 8 ? route_topk_wave_kernel<8>
                                                                         : route_topk_wave_kernel<kRouteMaxTopK>;
@@ -563,7 +594,15 @@ extern "C" int tris_route_topk_grouped(const float* router_logits, int32_t num_t
                        grouped_expert_ids, expert_ids, segment_offsets, problem_offsets, counts, inverse_perm);
     return check_launch(who);
   }
-  hipLaunchKernelGGL(route_topk_small_kernel, dim3(1), dim3(kRouteThreads), 0, static_cast<hipStream_t>(stream),
+  // experts per lane: the smallest of 1, 2, 4, 8, 16 that covers num_experts (a shorter register file of
+  // probabilities and fewer ballots per pick)
+  const int per_lane = ceil_div(num_experts, kWave);
+  auto* small = per_lane <= 1   ? route_topk_small_kernel<1>
+                : per_lane <= 2 ? route_topk_small_kernel<2>
+                : per_lane <= 4 ? route_topk_small_kernel<4>
+                : per_lane <= 8 ? route_topk_small_kernel<8>
+                                : route_topk_small_kernel<kRouteSmallMaxExperts / kWave>;
+  hipLaunchKernelGGL(small, dim3(1), dim3(kRouteThreads), 0, static_cast<hipStream_t>(stream),
                      router_logits, num_tokens, num_experts, top_k, renormalize, m_tile, routing_weights_f16,
                      routing_weights_f32, selected_experts, perm, grouped_token_indices, grouped_slots,
                      grouped_expert_ids, expert_ids, segment_offsets, problem_offsets, counts, inverse_perm);

@@ -247,18 +247,23 @@ def test_route_matches_oracle(tris, oracle_mod, cuda, t, k, e):
 ROUTE_TOPK_CASES = [(t, k, e, True) for t, k, e in [(1, 2, 8), (16, 2, 8), (32, 2, 64), (8, 8, 60), (4, 16, 16),
                                                     (3, 1, 64), (16, 8, 64), (33, 2, 8), (7, 8, 256), (256, 8, 128)]]
 # top_k below its pick-list bucket on the one-wavefront router (buckets of 2, 8 and 16 picks), both weightings;
-# and the workgroup router without renormalisation (OLMoE's default)
-ROUTE_TOPK_CASES += [(t, k, e, rn) for t, k, e in [(8, 4, 32), (4, 6, 60), (2, 12, 64), (5, 3, 16), (16, 8, 64)]
+# the same top_k on the workgroup router; and the workgroup router without renormalisation (OLMoE's default)
+ROUTE_TOPK_CASES += [(t, k, e, rn) for t, k, e in [(8, 4, 16), (4, 6, 12), (2, 12, 16), (5, 3, 16), (8, 4, 32),
+                                                   (4, 6, 60), (2, 12, 64), (16, 8, 64)]
                      for rn in (False, True)]
 ROUTE_TOPK_CASES += [(16, 8, 128, False), (64, 2, 8, False)]
+# the workgroup router's expert-per-lane buckets (1, 2, 4, 8, 16 experts a lane), its largest shapes (2048
+# routed rows, 1024 experts) and many 64-token scatter chunks
+ROUTE_TOPK_CASES += [(t, k, e, True) for t, k, e in [(100, 3, 200), (40, 8, 512), (32, 8, 1024), (128, 16, 1024),
+                                                     (2048, 1, 64), (1000, 2, 100), (9, 8, 60)]]
 
 
 @pytest.mark.parametrize("t,k,e,renorm", ROUTE_TOPK_CASES)
 def test_route_topk_fused_matches_oracle(tris, oracle_mod, cuda, t, k, e, renorm):
     """Fused softmax / top-k / route: the selection and the route are exactly the oracle's
-    (stable argsort of the fp32 softmax), weights within one fp16 ulp.  Up to 64 routed rows and 64
+    (stable argsort of the fp32 softmax), weights within one fp16 ulp.  Up to 64 routed rows and 8
     experts one wavefront does it (pick lists of 2, 8 or 16 entries, the smallest that holds top_k);
-    otherwise one workgroup."""
+    otherwise one workgroup (one wavefront per token, 1, 2, 4, 8 or 16 experts a lane)."""
     note(f"route topk fused t={t} k={k} e={e} renorm={renorm}")
     rng = np.random.default_rng(t * 100 + e + k)
     logits = rng.standard_normal((t, e)).astype(np.float32)
@@ -607,7 +612,8 @@ def test_run_grouped_structured_api(tris, oracle_mod, cuda):
 def test_backbone_matches_fp32(tris, cuda, tokens, in_f, rank):
     """Decode-sized inputs run the split-K MFMA kernel (1 to 4 token tiles per workgroup: 37 tokens are 3,
     64 are 4, 70 are a group of 4 and a partial one; 1001 columns take the element-wise loads); from
-    ext.BACKBONE_LIBRARY_MIN_ROWS rows (the last case, and its gathered rows) the library GEMM."""
+    ext.BACKBONE_LIBRARY_MIN_ROWS rows and ext.BACKBONE_LIBRARY_MIN_ELEMS activation elements (the last
+    case, and its gathered rows) the library GEMM."""
     note(f"backbone T={tokens} in={in_f} rank={rank}")
     rng = np.random.default_rng(tokens + in_f)
     x = rng.standard_normal((tokens, in_f)).astype(np.float16)
