@@ -222,6 +222,53 @@ int tris_grouped_block_gr_predecode_multi(const tris_gr_predecode_job* jobs, int
                                           const int32_t* expert_ids, int32_t num_active, void* stream);
 
 /*
+ * One or two fp16 backbone projections of the same token rows, as tris_backbone_linear_pair takes them
+ * (row_index NULL): out_a = fp16(x * in_scale_a) . sv_a^T [tokens, rank], out_b likewise (sv_b NULL: one
+ * projection); workspace of tris_backbone_pair_workspace_bytes(tokens, in_features, rank) bytes.
+ */
+typedef struct tris_backbone_pair_job {
+  const uint16_t* x;           /* fp16 [tokens, in_features], 16-byte aligned */
+  int32_t tokens;
+  int32_t in_features;
+  const uint16_t* sv_a;        /* fp16 [rank, in_features] */
+  const uint16_t* sv_b;        /* fp16 [rank, in_features] or NULL */
+  int32_t rank;
+  const uint16_t* in_scale_a;  /* fp16 [in_features] or NULL */
+  const uint16_t* in_scale_b;
+  uint16_t* out_a;             /* fp16 [tokens, rank] */
+  uint16_t* out_b;
+  void* workspace;
+  int64_t workspace_bytes;
+} tris_backbone_pair_job;
+
+/*
+ * The router of tris_route_topk_grouped and the gate/up backbone projections of the same tokens in one
+ * launch (no reference counterpart: the router, modeling_mixtral.py:548-555, and compute_shared_hidden,
+ * qlinear_cuda.py:4454-4502, do not depend on each other, so one launch runs both).  The route outputs are
+ * tris_route_topk_grouped's and the backbone outputs tris_backbone_linear_pair's (row_index NULL), bit
+ * for bit.  bb->tokens == num_tokens <= 64.  When the projection is split over K and defer_reduce != 0,
+ * the partial sums stay in bb->workspace and out_a / out_b are written by a later
+ * tris_grouped_block_gr_predecode_multi_reduce with the same job; otherwise a second launch reduces them.
+ */
+int tris_route_topk_backbone(const float* router_logits, int32_t num_tokens, int32_t num_experts, int32_t top_k,
+                             int32_t renormalize, int32_t m_tile, uint16_t* routing_weights_f16,
+                             float* routing_weights_f32, int64_t* selected_experts, int64_t* perm,
+                             int64_t* grouped_token_indices, int64_t* grouped_slots, int32_t* grouped_expert_ids,
+                             int32_t* expert_ids, int32_t* segment_offsets, int32_t* problem_offsets,
+                             int32_t* counts, int32_t* inverse_perm, const tris_backbone_pair_job* bb,
+                             int32_t defer_reduce, void* stream);
+
+/*
+ * tris_grouped_block_gr_predecode_multi with the deferred slice reduction of a tris_route_topk_backbone
+ * launch (defer_reduce != 0, the same job) in the same launch (no reference counterpart: the two do not
+ * depend on each other).  bb NULL: the plain predecode.  The backbone outputs are the bits
+ * tris_backbone_linear_pair writes.
+ */
+int tris_grouped_block_gr_predecode_multi_reduce(const tris_gr_predecode_job* jobs, int32_t num_jobs,
+                                                 const int32_t* expert_ids, int32_t num_active,
+                                                 const tris_backbone_pair_job* bb, void* stream);
+
+/*
  * Grouped GEMM reading predecoded split bitmaps: replaces
  * compact3_tris_precomputed_grouped_forward_block_gr_predecoded (TriSMoE_cuda.cpp:855-889,
  * kernel.cu:4720-4885).  decoded is indexed by segment (the predecode of
@@ -258,6 +305,28 @@ int tris_grouped_swiglu_forward_block_gr_predecoded(
     const int32_t* segment_offsets, const int32_t* problem_offsets, int32_t num_segments, int64_t total_problem_tiles,
     const int32_t* decoded_gate, const int32_t* decoded_up, const tris_compact3_payload* payload_gate,
     const tris_compact3_payload* payload_up, uint16_t* output, void* stream);
+
+/*
+ * The dual and SwiGLU predecoded entries above with the routed rows gathered from per-token activations
+ * (no reference counterpart: fuses the row gather of the reference's grouped forward,
+ * modeling_mixtral.py:467-470, where the shared backbone output is indexed by the route's token indices,
+ * into the GEMM's activation staging).  Grouped row r reads hidden row row_index[r] of hidden_* fp16
+ * [hidden_rows, rank]; row_index is the route's int64 grouped_token_indices [batch].  An index outside
+ * [0, hidden_rows) reads zeros.  Requires the MFMA kernel's payload conditions (uniform 64-column groups,
+ * rank % 64 == 0, 16-byte aligned rows) and hidden_rows * rank * 2 < 2 GiB, else TRIS_ERR_INVALID.
+ * problem_offsets is not needed (the kernels map their tiles from segment_offsets).
+ */
+int tris_grouped_dual_forward_block_gr_predecoded_rows(
+    const uint16_t* hidden_a, const uint16_t* hidden_b, const int64_t* row_index, int32_t hidden_rows, int32_t batch,
+    const int32_t* expert_ids, const int32_t* segment_offsets, int32_t num_segments, int64_t total_problem_tiles,
+    const int32_t* decoded_a, const int32_t* decoded_b, const tris_compact3_payload* payload_a,
+    const tris_compact3_payload* payload_b, uint16_t* output_a, uint16_t* output_b, void* stream);
+int tris_grouped_swiglu_forward_block_gr_predecoded_rows(
+    const uint16_t* hidden_gate, const uint16_t* hidden_up, const int64_t* row_index, int32_t hidden_rows,
+    int32_t batch, const int32_t* expert_ids, const int32_t* segment_offsets, int32_t num_segments,
+    int64_t total_problem_tiles, const int32_t* decoded_gate, const int32_t* decoded_up,
+    const tris_compact3_payload* payload_gate, const tris_compact3_payload* payload_up, uint16_t* output,
+    void* stream);
 
 /*
  * Dequantise the listed experts to dense fp16 weights [num, N, rank]

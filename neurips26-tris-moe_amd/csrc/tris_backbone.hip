@@ -26,182 +26,18 @@
 // At decode (T <= 16) the projection is HBM-bound on SV (2*rank*in bytes).
 #include <mutex>
 
-#include "tris_common.h"
+#include "tris_backbone.h"
 
 namespace tris {
 
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-constexpr int kBbWaves = 4;
-constexpr int kBbThreads = kBbWaves * kWave;
-constexpr int kBbKStep = 32;
-constexpr int kBbBatch = 8;          // K steps of loads in flight per wavefront
-constexpr int kBbTargetWgs = 512;    // aim for this many workgroups per launch
-constexpr int kBbMaxSlices = 32;
-
-struct BackboneProj {
-  const uint16_t* sv;
-  uint16_t* out;
-  const uint16_t* in_scale;  // fp16 [in] per-column input scale of this projection, or null
-};
-
-struct BackboneArgs {
-  const uint16_t* x;
-  const int64_t* row_index;
-  BackboneProj proj[2];
-  float* partials;  // [nproj][slices][tokens][rank] when slices > 1
-  int tokens;
-  int in_features;
-  int rank;
-  int slices;
-  int slice_k;  // K columns per slice (a multiple of kBbWaves * kBbKStep)
-};
-
-__device__ __forceinline__ f16x8 load8_tail(const uint16_t* __restrict__ src, int k, int limit, bool valid) {
-  f16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-  if (valid) {
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if (k + u < limit) v[u] = __builtin_bit_cast(_Float16, src[k + u]);
-    }
-  }
-  return v;
-}
-
-__device__ __forceinline__ f16x8 load8_vec(const uint16_t* __restrict__ src, int k, bool valid) {
-  f16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-  if (valid) v = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(src + k));
-  return v;
-}
-
-// grid = (row tiles, token-tile groups * slices, projections).  A workgroup covers TT token tiles of 16
-// rows, so each SV operand load feeds TT MFMAs (SV, the bytes that bound the projection, is read once per
-// row tile and slice however many tokens there are, up to 16 * TT); B K steps of loads are in flight per
-// wavefront, the last batch of a slice predicated (zero operands past its end).
 template <int TT, int B>
 __global__ __launch_bounds__(kBbThreads) void backbone_kernel(BackboneArgs a) {
   __shared__ f32x4 red[kBbWaves - 1][TT][kWave];
-  const int q = blockIdx.z;
-  const BackboneProj& pj = a.proj[q];
-  const int tid = threadIdx.x;
-  const int wave = tid / kWave;
-  const int lane = tid % kWave;
-  const int r0 = blockIdx.x * 16;
-  const int slice = blockIdx.y % a.slices;
-  const int tg0 = (blockIdx.y / a.slices) * TT;  // first token tile of the group
-  const int i = lane % 16;
-  const int kg = lane / 16;
-
-  bool t_valid[TT];
-  const uint16_t* xsrc[TT];
-#pragma unroll
-  for (int j = 0; j < TT; ++j) {
-    const int t = (tg0 + j) * 16 + i;
-    t_valid[j] = t < a.tokens;
-    int64_t xrow = 0;
-    if (t_valid[j]) xrow = a.row_index != nullptr ? a.row_index[t] : t;
-    xsrc[j] = a.x + xrow * a.in_features;
-  }
-  const int r = r0 + i;
-  const bool r_valid = r < a.rank;
-  const uint16_t* ssrc = pj.sv + static_cast<int64_t>(r_valid ? r : 0) * a.in_features;
-  const uint16_t* in_scale = pj.in_scale;
-  const bool scaled = in_scale != nullptr;
-  const bool vec = (a.in_features % 8) == 0;
-
-  f32x4 acc[TT];
-#pragma unroll
-  for (int j = 0; j < TT; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  const int kper = a.slice_k / kBbWaves;
-  const int kbeg0 = slice * a.slice_k + wave * kper;
-  const int kbeg = kbeg0 < a.in_features ? kbeg0 : a.in_features;
-  const int kend = (kbeg0 + kper) < a.in_features ? (kbeg0 + kper) : a.in_features;
-  if (vec) {
-    // every k is a multiple of 8 and so is kend: a 16-byte run is inside the slice iff k < kend
-    for (int k0 = kbeg; k0 < kend; k0 += B * kBbKStep) {
-      f16x8 bv[B], av[TT][B];
-#pragma unroll
-      for (int u = 0; u < B; ++u) {
-        const int k = k0 + u * kBbKStep + kg * 8;
-        const bool kv = k < kend;
-        bv[u] = load8_vec(ssrc, k, r_valid && kv);
-#pragma unroll
-        for (int j = 0; j < TT; ++j) av[j][u] = load8_vec(xsrc[j], k, t_valid[j] && kv);
-      }
-      if (scaled) {
-#pragma unroll
-        for (int u = 0; u < B; ++u) {
-          const int k = k0 + u * kBbKStep + kg * 8;
-          const f16x8 sc = load8_vec(in_scale, k, k < kend);
-#pragma unroll
-          for (int j = 0; j < TT; ++j) av[j][u] = av[j][u] * sc;  // fp16 products, as x * ns_col
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < B; ++u) {
-#pragma unroll
-        for (int j = 0; j < TT; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[j][u], bv[u], acc[j], 0, 0, 0);
-      }
-    }
-  } else {
-    // rows not a multiple of 8 columns: element-wise loads
-    for (int k0 = kbeg; k0 < kend; k0 += kBbKStep) {
-      const int k = k0 + kg * 8;
-      const f16x8 bv = load8_tail(ssrc, k, kend, r_valid);
-      const f16x8 sc = scaled ? load8_tail(in_scale, k, kend, true) : f16x8{1, 1, 1, 1, 1, 1, 1, 1};
-#pragma unroll
-      for (int j = 0; j < TT; ++j) {
-        f16x8 av = load8_tail(xsrc[j], k, kend, t_valid[j]);
-        if (scaled) av = av * sc;
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[j], 0, 0, 0);
-      }
-    }
-  }
-  if (wave > 0) {
-#pragma unroll
-    for (int j = 0; j < TT; ++j) red[wave - 1][j][lane] = acc[j];
-  }
-  __syncthreads();
-  const int col = r0 + i;
-  if (wave == 0) {
-#pragma unroll
-    for (int j = 0; j < TT; ++j) {
-#pragma unroll
-      for (int w = 0; w < kBbWaves - 1; ++w) acc[j] += red[w][j][lane];
-      // acc[j][v] = out[t0 + 4*kg + v][r0 + i], t0 the tile's first token
-      const int t0 = (tg0 + j) * 16;
-      float* part = a.partials + (static_cast<int64_t>(q) * a.slices + slice) * a.tokens * a.rank;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int tt = t0 + 4 * kg + v;
-        if (tt < a.tokens && col < a.rank) {
-          if (a.slices == 1) {
-            pj.out[static_cast<int64_t>(tt) * a.rank + col] = f2h_bits(acc[j][v]);
-          } else {
-            part[static_cast<int64_t>(tt) * a.rank + col] = acc[j][v];
-          }
-        }
-      }
-    }
-  }
+  backbone_block<TT, B>(a, true, blockIdx.x, blockIdx.y, blockIdx.z, threadIdx.x, red);
 }
 
 __global__ __launch_bounds__(256) void backbone_reduce_kernel(BackboneArgs a) {
-  const int64_t count = static_cast<int64_t>(a.tokens) * a.rank;
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (idx >= count) return;
-  const int q = blockIdx.y;
-  const float* src = a.partials + static_cast<int64_t>(q) * a.slices * count + idx;
-  float v[kBbMaxSlices];
-#pragma unroll
-  for (int s = 0; s < kBbMaxSlices; ++s) v[s] = s < a.slices ? src[s * count] : 0.0f;  // loads in flight together
-  float sum = 0.0f;
-#pragma unroll
-  for (int s = 0; s < kBbMaxSlices; ++s) {
-    if (s < a.slices) sum += v[s];
-  }
-  a.proj[q].out[idx] = f2h_bits(sum);
+  backbone_reduce_at(a, static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x, blockIdx.y);
 }
 
 __global__ __launch_bounds__(256) void fill_zero_u16_kernel(uint16_t* __restrict__ out, int64_t count) {
@@ -235,6 +71,51 @@ int64_t backbone_workspace_bytes(int tokens, int in_features, int rank, int npro
   return slices > 1 ? static_cast<int64_t>(nproj) * slices * tokens * rank * 4 : 0;
 }
 
+BackbonePlan backbone_plan(int tokens, int in_features, int rank) {
+  BackbonePlan p{};
+  p.slices = backbone_slices(tokens, in_features, rank);
+  p.tt = backbone_token_group(tokens);
+  p.token_groups = ceil_div(ceil_div(tokens, 16), p.tt);
+  p.row_tiles = ceil_div(rank, 16);
+  p.slice_k = ceil_div(ceil_div(in_features, p.slices), kBbWaves * kBbKStep) * kBbWaves * kBbKStep;
+  return p;
+}
+
+int backbone_prepare(const uint16_t* x, int tokens, int in_features, const int64_t* row_index, const uint16_t* sv_a,
+                     const uint16_t* sv_b, int rank, const uint16_t* in_scale_a, const uint16_t* in_scale_b,
+                     uint16_t* out_a, uint16_t* out_b, void* workspace, int64_t workspace_bytes, BackboneArgs* args,
+                     BackbonePlan* plan, const char* who) {
+  TRIS_REQUIRE(tokens > 0 && in_features > 0 && rank > 0, "%s: empty projection", who);
+  TRIS_REQUIRE(out_a != nullptr && (sv_b == nullptr || out_b != nullptr), "%s: null output", who);
+  TRIS_REQUIRE(x && sv_a, "%s: null input", who);
+  TRIS_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(sv_a) % 16 == 0 &&
+                   (sv_b == nullptr || reinterpret_cast<uintptr_t>(sv_b) % 16 == 0) &&
+                   reinterpret_cast<uintptr_t>(in_scale_a) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(in_scale_b) % 16 == 0,
+               "%s: x, sv and in_scale must be 16-byte aligned", who);
+  const int nproj = sv_b != nullptr ? 2 : 1;
+  const BackbonePlan pl = backbone_plan(tokens, in_features, rank);
+  const int64_t need = backbone_workspace_bytes(tokens, in_features, rank, nproj);
+  TRIS_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+               "%s: workspace of %lld bytes needed, %lld given", who, static_cast<long long>(need),
+               static_cast<long long>(workspace_bytes));
+  TRIS_REQUIRE(static_cast<int64_t>(pl.token_groups) * pl.slices <= 65535, "%s: too many tokens", who);
+  BackboneArgs a{};
+  a.x = x;
+  a.row_index = row_index;
+  a.proj[0] = BackboneProj{sv_a, out_a, in_scale_a};
+  a.proj[1] = BackboneProj{sv_b, out_b, in_scale_b};
+  a.partials = static_cast<float*>(workspace);
+  a.tokens = tokens;
+  a.in_features = in_features;
+  a.rank = rank;
+  a.slices = pl.slices;
+  a.slice_k = pl.slice_k;
+  *args = a;
+  *plan = pl;
+  return TRIS_OK;
+}
+
 int launch_backbone(const uint16_t* x, int tokens, int in_features, const int64_t* row_index, const uint16_t* sv_a,
                     const uint16_t* sv_b, int rank, const uint16_t* in_scale_a, const uint16_t* in_scale_b,
                     uint16_t* out_a, uint16_t* out_b, void* workspace, int64_t workspace_bytes, void* stream,
@@ -252,42 +133,25 @@ int launch_backbone(const uint16_t* x, int tokens, int in_features, const int64_
     }
     return check_launch("fill_zero_u16_kernel");
   }
-  TRIS_REQUIRE(x && sv_a, "%s: null input", who);
-  TRIS_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(sv_a) % 16 == 0 &&
-                   (sv_b == nullptr || reinterpret_cast<uintptr_t>(sv_b) % 16 == 0) &&
-                   reinterpret_cast<uintptr_t>(in_scale_a) % 16 == 0 &&
-                   reinterpret_cast<uintptr_t>(in_scale_b) % 16 == 0,
-               "%s: x, sv and in_scale must be 16-byte aligned", who);
-  const int slices = backbone_slices(tokens, in_features, rank);
-  const int64_t need = backbone_workspace_bytes(tokens, in_features, rank, nproj);
-  TRIS_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
-               "%s: workspace of %lld bytes needed, %lld given", who, static_cast<long long>(need),
-               static_cast<long long>(workspace_bytes));
-  const int tt = backbone_token_group(tokens);
-  const int token_groups = ceil_div(ceil_div(tokens, 16), tt);
-  const int row_tiles = ceil_div(rank, 16);
-  TRIS_REQUIRE(static_cast<int64_t>(token_groups) * slices <= 65535, "%s: too many tokens", who);
-  BackboneArgs args{};
-  args.x = x;
-  args.row_index = row_index;
-  args.proj[0] = BackboneProj{sv_a, out_a, in_scale_a};
-  args.proj[1] = BackboneProj{sv_b, out_b, in_scale_b};
-  args.partials = static_cast<float*>(workspace);
-  args.tokens = tokens;
-  args.in_features = in_features;
-  args.rank = rank;
-  args.slices = slices;
-  args.slice_k = ceil_div(ceil_div(in_features, slices), kBbWaves * kBbKStep) * kBbWaves * kBbKStep;
-  const dim3 grid(row_tiles, token_groups * slices, nproj);
-  switch (tt) {
+  BackboneArgs args;
+  BackbonePlan pl;
+  int rc = backbone_prepare(x, tokens, in_features, row_index, sv_a, sv_b, rank, in_scale_a, in_scale_b, out_a, out_b,
+                            workspace, workspace_bytes, &args, &pl, who);
+  if (rc) return rc;
+  const dim3 grid(pl.row_tiles, pl.token_groups * pl.slices, nproj);
+  switch (pl.tt) {
     case 1: hipLaunchKernelGGL((backbone_kernel<1, 8>), grid, dim3(kBbThreads), 0, s, args); break;
     case 2: hipLaunchKernelGGL((backbone_kernel<2, 8>), grid, dim3(kBbThreads), 0, s, args); break;
     case 3: hipLaunchKernelGGL((backbone_kernel<3, 4>), grid, dim3(kBbThreads), 0, s, args); break;
     default: hipLaunchKernelGGL((backbone_kernel<4, 4>), grid, dim3(kBbThreads), 0, s, args); break;
   }
-  int rc = check_launch(who);
-  if (rc || slices == 1) return rc;
-  const int64_t count = static_cast<int64_t>(tokens) * rank;
+  rc = check_launch(who);
+  if (rc || pl.slices == 1) return rc;
+  return launch_backbone_reduce(args, nproj, s, who);
+}
+
+int launch_backbone_reduce(const BackboneArgs& args, int nproj, hipStream_t s, const char* who) {
+  const int64_t count = static_cast<int64_t>(args.tokens) * args.rank;
   hipLaunchKernelGGL(backbone_reduce_kernel, dim3(static_cast<unsigned>((count + 255) / 256), nproj), dim3(256), 0, s,
                      args);
   return check_launch(who);

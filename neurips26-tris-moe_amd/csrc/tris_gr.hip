@@ -8,6 +8,7 @@
 // coalesced stores.  Work per block hardly depends on S; more lanes per block
 // shorten each lane's walk (latency), fewer cut the scan steps, so S is chosen
 // from the block count.
+#include "tris_backbone.h"
 #include "tris_gr_span.h"
 #include "tris_moe_hip.h"
 
@@ -42,6 +43,14 @@ struct GrWork {
   int num_jobs;
   int num_slots;
   int first[TRIS_MAX_PREDECODE_JOBS + 1];  // first item of each job; first[num_jobs] = all items
+  int decode_wgs;  // workgroups that decode; any after them reduce a backbone's slices (GrReduce)
+};
+
+// A backbone projection's slice reduction run by the workgroups past the decoders (independent work in the
+// same launch): blocks_per_proj workgroups of kSpanThreads output elements for each of nproj projections.
+struct GrReduce {
+  BackboneArgs bb;
+  int blocks_per_proj;
 };
 
 constexpr int kSpanLdsSlots = 1024;  // expert ids staged in LDS (later slots read from memory)
@@ -79,8 +88,15 @@ __device__ __forceinline__ void gr_item_header(const GrJobs& jobs, const GrWork&
 
 template <int S>
 __global__ __launch_bounds__(kSpanThreads) void gr_decode_span_kernel(GrJobs jobs, GrWork wk,
-                                                                      const int32_t* __restrict__ expert_ids) {
+                                                                      const int32_t* __restrict__ expert_ids,
+                                                                      GrReduce red) {
   constexpr int kBlocksPerWg = kSpanThreads / S;
+  if (static_cast<int>(blockIdx.x) >= wk.decode_wgs) {
+    const int rb = static_cast<int>(blockIdx.x) - wk.decode_wgs;
+    const int q = rb / red.blocks_per_proj;
+    backbone_reduce_at(red.bb, static_cast<int64_t>(rb % red.blocks_per_proj) * kSpanThreads + threadIdx.x, q);
+    return;
+  }
   __shared__ GrTables tab;
   __shared__ uint32_t outb[kBlocksPerWg][kGrBlockStride];
   __shared__ int32_t eids[kSpanLdsSlots];
@@ -97,13 +113,13 @@ __global__ __launch_bounds__(kSpanThreads) void gr_decode_span_kernel(GrJobs job
   GrItem<S> cur;
   gr_item_header<S>(jobs, wk, eids, expert_ids, w, g, cur);
   gr_span_words<S>(cur.sp, j);
-  for (; w < total; w += gridDim.x) {
+  for (; w < total; w += wk.decode_wgs) {
     for (int idx = tid; idx < kBlocksPerWg * kGrBlockStride; idx += kSpanThreads) {
       outb[idx / kGrBlockStride][idx % kGrBlockStride] = 0u;
     }
     __syncthreads();
     GrItem<S> nx;
-    gr_item_header<S>(jobs, wk, eids, expert_ids, w + static_cast<int>(gridDim.x), g, nx);
+    gr_item_header<S>(jobs, wk, eids, expert_ids, w + wk.decode_wgs, g, nx);
     gr_decode_block_group<S>(cur.sp, &tab, outb[g] + kGrPadFront, j);
     gr_span_words<S>(nx.sp, j);
     __syncthreads();
@@ -150,15 +166,19 @@ int make_gr_job(GrJob* job, int32_t* out, const int32_t* words, const int32_t* o
   return TRIS_OK;
 }
 
+// reduce: a backbone launch's deferred slice reduction to run in the same launch (or null).
 int launch_gr_jobs(const GrJobs& jobs, int num_jobs, const int32_t* expert_ids, int num_slots, void* stream,
-                   const char* who) {
+                   const char* who, const BackboneArgs* reduce = nullptr, int reduce_nproj = 0) {
   int max_nblk = 0;
   int64_t total = 0;
   for (int q = 0; q < num_jobs; ++q) {
     max_nblk = jobs.job[q].nblk > max_nblk ? jobs.job[q].nblk : max_nblk;
     total += static_cast<int64_t>(jobs.job[q].nblk) * num_slots;
   }
-  if (num_slots == 0 || max_nblk == 0) return TRIS_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (num_slots == 0 || max_nblk == 0) {
+    return reduce != nullptr ? launch_backbone_reduce(*reduce, reduce_nproj, s, who) : TRIS_OK;
+  }
   TRIS_REQUIRE(expert_ids != nullptr, "%s: null expert ids", who);
   TRIS_REQUIRE(num_slots <= 65535, "%s: too many experts (%d)", who, num_slots);
   // lanes per block: more lanes shorten each block's walk, fewer spread the per-workgroup table copy
@@ -177,14 +197,24 @@ int launch_gr_jobs(const GrJobs& jobs, int num_jobs, const int32_t* expert_ids, 
   for (int q = num_jobs; q <= TRIS_MAX_PREDECODE_JOBS; ++q) wk.first[q] = static_cast<int>(items);
   // persistent workgroups: one per item up to kSpanWgTarget (four per CU, all resident), so every item that can
   // run at once does; past that each takes several
-  int64_t grid = items < kSpanWgTarget ? items : kSpanWgTarget;
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t grid = items < kSpanWgTarget ? items : kSpanWgTarget;
+  wk.decode_wgs = static_cast<int>(grid);
+  GrReduce red{};
+  int64_t reduce_wgs = 0;
+  if (reduce != nullptr) {
+    red.bb = *reduce;
+    const int64_t per_proj = (static_cast<int64_t>(reduce->tokens) * reduce->rank + kSpanThreads - 1) / kSpanThreads;
+    TRIS_REQUIRE(per_proj < (1LL << 30), "%s: backbone reduction too large", who);
+    red.blocks_per_proj = static_cast<int>(per_proj);
+    reduce_wgs = per_proj * reduce_nproj;
+  }
+  red.blocks_per_proj = red.blocks_per_proj > 0 ? red.blocks_per_proj : 1;
+  TRIS_REQUIRE(grid + reduce_wgs < (1LL << 31), "%s: too many workgroups", who);
+  const dim3 g3(static_cast<unsigned>(grid + reduce_wgs));
   if (S == 16) {
-    hipLaunchKernelGGL((gr_decode_span_kernel<16>), dim3(static_cast<unsigned>(grid)), dim3(kSpanThreads), 0, s, jobs,
-                       wk, expert_ids);
+    hipLaunchKernelGGL((gr_decode_span_kernel<16>), g3, dim3(kSpanThreads), 0, s, jobs, wk, expert_ids, red);
   } else {
-    hipLaunchKernelGGL((gr_decode_span_kernel<32>), dim3(static_cast<unsigned>(grid)), dim3(kSpanThreads), 0, s, jobs,
-                       wk, expert_ids);
+    hipLaunchKernelGGL((gr_decode_span_kernel<32>), g3, dim3(kSpanThreads), 0, s, jobs, wk, expert_ids, red);
   }
   return check_launch(who);
 }
@@ -222,6 +252,34 @@ extern "C" int tris_grouped_block_gr_predecode_multi(const tris_gr_predecode_job
     if (rc) return rc;
   }
   return launch_gr_jobs(g, num_jobs, expert_ids, num_active, stream, who);
+}
+
+extern "C" int tris_grouped_block_gr_predecode_multi_reduce(const tris_gr_predecode_job* jobs, int32_t num_jobs,
+                                                            const int32_t* expert_ids, int32_t num_active,
+                                                            const tris_backbone_pair_job* bb, void* stream) {
+  const char* who = "tris_grouped_block_gr_predecode_multi_reduce";
+  TRIS_REQUIRE(num_active >= 0, "%s: negative size", who);
+  TRIS_REQUIRE(num_jobs >= 0 && num_jobs <= TRIS_MAX_PREDECODE_JOBS, "%s: %d jobs (at most %d)", who, num_jobs,
+               TRIS_MAX_PREDECODE_JOBS);
+  TRIS_REQUIRE(num_jobs == 0 || jobs != nullptr, "%s: null jobs", who);
+  GrJobs g{};
+  for (int q = 0; q < num_jobs; ++q) {
+    const tris_gr_predecode_job& j = jobs[q];
+    int rc = make_gr_job(&g.job[q], j.decoded, j.q_gmap_gr_words, j.q_gmap_gr_offsets, j.q_gmap_gr_meta,
+                         j.num_experts, j.words_stride, j.packed_rows, j.outfeatures, false, who);
+    if (rc) return rc;
+  }
+  if (bb == nullptr || bb->tokens == 0 || bb->rank == 0) {
+    return launch_gr_jobs(g, num_jobs, expert_ids, num_active, stream, who);
+  }
+  BackboneArgs ba;
+  BackbonePlan pl;
+  int rc = backbone_prepare(bb->x, bb->tokens, bb->in_features, nullptr, bb->sv_a, bb->sv_b, bb->rank,
+                            bb->in_scale_a, bb->in_scale_b, bb->out_a, bb->out_b, bb->workspace, bb->workspace_bytes,
+                            &ba, &pl, who);
+  if (rc) return rc;
+  if (pl.slices == 1) return launch_gr_jobs(g, num_jobs, expert_ids, num_active, stream, who);  // nothing deferred
+  return launch_gr_jobs(g, num_jobs, expert_ids, num_active, stream, who, &ba, bb->sv_b != nullptr ? 2 : 1);
 }
 
 extern "C" int tris_gr_decode_dense(const int32_t* q_gmap_gr_words, const int32_t* q_gmap_gr_offsets,

@@ -499,7 +499,8 @@ int launch_linear(const uint16_t* input, int batch, const tris_compact3_payload*
 int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int batch, const int32_t* expert_ids,
                         const int32_t* segment_offsets, int num_segments, const int32_t* decoded_a,
                         const int32_t* decoded_b, const tris_compact3_payload* pa, const tris_compact3_payload* pb,
-                        uint16_t* out_a, uint16_t* out_b, bool swiglu, void* stream, const char* who);
+                        uint16_t* out_a, uint16_t* out_b, bool swiglu, void* stream, const char* who,
+                        const int64_t* row_index = nullptr, int hidden_rows = 0);
 bool grouped_mfma_supported(const tris_compact3_payload* p, const uint16_t* hidden);
 
 }  // namespace tris
@@ -568,14 +569,16 @@ extern "C" int tris_grouped_forward_block_gr_predecoded(const uint16_t* hidden, 
                         "tris_grouped_forward_block_gr_predecoded");
 }
 
-extern "C" int tris_grouped_dual_forward_block_gr_predecoded(
-    const uint16_t* hidden_a, const uint16_t* hidden_b, int32_t batch, const int32_t* expert_ids,
-    const int32_t* segment_offsets, const int32_t* problem_offsets, int32_t num_segments, int64_t total_problem_tiles,
-    const int32_t* decoded_a, const int32_t* decoded_b, const tris_compact3_payload* payload_a,
-    const tris_compact3_payload* payload_b, uint16_t* output_a, uint16_t* output_b, void* stream) {
-  (void)problem_offsets;
+// The dual predecoded GEMM; row_index (or null) gathers the activation rows from hidden_rows rows.  The
+// exact VALU kernel (payloads outside the MFMA kernel's conditions) reads ungathered rows only.
+static int dual_predecoded(const uint16_t* hidden_a, const uint16_t* hidden_b, const int64_t* row_index,
+                           int32_t hidden_rows, int32_t batch, const int32_t* expert_ids,
+                           const int32_t* segment_offsets, int32_t num_segments, int64_t total_problem_tiles,
+                           const int32_t* decoded_a, const int32_t* decoded_b, const tris_compact3_payload* payload_a,
+                           const tris_compact3_payload* payload_b, uint16_t* output_a, uint16_t* output_b,
+                           void* stream, const char* who) {
   if (payload_a == nullptr || payload_b == nullptr) {
-    set_error("tris_grouped_dual_forward_block_gr_predecoded: null payload");
+    set_error("%s: null payload", who);
     return TRIS_ERR_INVALID;
   }
   tris_compact3_payload pa = *payload_a;
@@ -584,14 +587,57 @@ extern "C" int tris_grouped_dual_forward_block_gr_predecoded(
   pa.has_bias = pb.has_bias = 0;
   if (grouped_mfma_supported(&pa, hidden_a) && grouped_mfma_supported(&pb, hidden_b)) {
     if (total_problem_tiles <= 0) return TRIS_OK;
-    TRIS_REQUIRE(pa.num_experts == pb.num_experts, "tris_grouped_dual_forward_block_gr_predecoded: expert count mismatch");
+    TRIS_REQUIRE(pa.num_experts == pb.num_experts, "%s: expert count mismatch", who);
     return launch_grouped_mfma(hidden_a, hidden_b, batch, expert_ids, segment_offsets, num_segments, decoded_a,
-                               decoded_b, &pa, &pb, output_a, output_b, false, stream,
-                               "tris_grouped_dual_forward_block_gr_predecoded");
+                               decoded_b, &pa, &pb, output_a, output_b, false, stream, who, row_index, hidden_rows);
   }
+  TRIS_REQUIRE(row_index == nullptr, "%s: gathered rows need the MFMA kernel's payload conditions", who);
   return launch_grouped(hidden_a, hidden_b, batch, expert_ids, segment_offsets, num_segments, total_problem_tiles,
-                        decoded_a, decoded_b, &pa, &pb, output_a, output_b, true, stream,
-                        "tris_grouped_dual_forward_block_gr_predecoded");
+                        decoded_a, decoded_b, &pa, &pb, output_a, output_b, true, stream, who);
+}
+
+static int swiglu_predecoded(const uint16_t* hidden_gate, const uint16_t* hidden_up, const int64_t* row_index,
+                             int32_t hidden_rows, int32_t batch, const int32_t* expert_ids,
+                             const int32_t* segment_offsets, int32_t num_segments, int64_t total_problem_tiles,
+                             const int32_t* decoded_gate, const int32_t* decoded_up,
+                             const tris_compact3_payload* payload_gate, const tris_compact3_payload* payload_up,
+                             uint16_t* output, void* stream, const char* who) {
+  if (payload_gate == nullptr || payload_up == nullptr) {
+    set_error("%s: null payload", who);
+    return TRIS_ERR_INVALID;
+  }
+  tris_compact3_payload pg = *payload_gate;
+  tris_compact3_payload pu = *payload_up;
+  pg.has_output_scale = pu.has_output_scale = 0;
+  pg.has_bias = pu.has_bias = 0;
+  TRIS_REQUIRE(grouped_mfma_supported(&pg, hidden_gate) && grouped_mfma_supported(&pu, hidden_up),
+               "%s: needs uniform 64-column groups, rank %% 64 == 0 and 16-byte aligned hidden rows", who);
+  if (total_problem_tiles <= 0) return TRIS_OK;
+  return launch_grouped_mfma(hidden_gate, hidden_up, batch, expert_ids, segment_offsets, num_segments, decoded_gate,
+                             decoded_up, &pg, &pu, output, nullptr, true, stream, who, row_index, hidden_rows);
+}
+
+extern "C" int tris_grouped_dual_forward_block_gr_predecoded(
+    const uint16_t* hidden_a, const uint16_t* hidden_b, int32_t batch, const int32_t* expert_ids,
+    const int32_t* segment_offsets, const int32_t* problem_offsets, int32_t num_segments, int64_t total_problem_tiles,
+    const int32_t* decoded_a, const int32_t* decoded_b, const tris_compact3_payload* payload_a,
+    const tris_compact3_payload* payload_b, uint16_t* output_a, uint16_t* output_b, void* stream) {
+  (void)problem_offsets;
+  return dual_predecoded(hidden_a, hidden_b, nullptr, 0, batch, expert_ids, segment_offsets, num_segments,
+                         total_problem_tiles, decoded_a, decoded_b, payload_a, payload_b, output_a, output_b, stream,
+                         "tris_grouped_dual_forward_block_gr_predecoded");
+}
+
+extern "C" int tris_grouped_dual_forward_block_gr_predecoded_rows(
+    const uint16_t* hidden_a, const uint16_t* hidden_b, const int64_t* row_index, int32_t hidden_rows, int32_t batch,
+    const int32_t* expert_ids, const int32_t* segment_offsets, int32_t num_segments, int64_t total_problem_tiles,
+    const int32_t* decoded_a, const int32_t* decoded_b, const tris_compact3_payload* payload_a,
+    const tris_compact3_payload* payload_b, uint16_t* output_a, uint16_t* output_b, void* stream) {
+  const char* who = "tris_grouped_dual_forward_block_gr_predecoded_rows";
+  TRIS_REQUIRE(row_index != nullptr || batch == 0, "%s: null row_index", who);
+  return dual_predecoded(hidden_a, hidden_b, row_index, hidden_rows, batch, expert_ids, segment_offsets, num_segments,
+                         total_problem_tiles, decoded_a, decoded_b, payload_a, payload_b, output_a, output_b, stream,
+                         who);
 }
 
 extern "C" int tris_grouped_swiglu_forward_block_gr_predecoded(
@@ -600,21 +646,22 @@ extern "C" int tris_grouped_swiglu_forward_block_gr_predecoded(
     const int32_t* decoded_gate, const int32_t* decoded_up, const tris_compact3_payload* payload_gate,
     const tris_compact3_payload* payload_up, uint16_t* output, void* stream) {
   (void)problem_offsets;
-  if (payload_gate == nullptr || payload_up == nullptr) {
-    set_error("tris_grouped_swiglu_forward_block_gr_predecoded: null payload");
-    return TRIS_ERR_INVALID;
-  }
-  tris_compact3_payload pg = *payload_gate;
-  tris_compact3_payload pu = *payload_up;
-  pg.has_output_scale = pu.has_output_scale = 0;
-  pg.has_bias = pu.has_bias = 0;
-  TRIS_REQUIRE(grouped_mfma_supported(&pg, hidden_gate) && grouped_mfma_supported(&pu, hidden_up),
-               "tris_grouped_swiglu_forward_block_gr_predecoded: needs uniform 64-column groups, rank %% 64 == 0 "
-               "and 16-byte aligned hidden rows");
-  if (total_problem_tiles <= 0) return TRIS_OK;
-  return launch_grouped_mfma(hidden_gate, hidden_up, batch, expert_ids, segment_offsets, num_segments, decoded_gate,
-                             decoded_up, &pg, &pu, output, nullptr, true, stream,
-                             "tris_grouped_swiglu_forward_block_gr_predecoded");
+  return swiglu_predecoded(hidden_gate, hidden_up, nullptr, 0, batch, expert_ids, segment_offsets, num_segments,
+                           total_problem_tiles, decoded_gate, decoded_up, payload_gate, payload_up, output, stream,
+                           "tris_grouped_swiglu_forward_block_gr_predecoded");
+}
+
+extern "C" int tris_grouped_swiglu_forward_block_gr_predecoded_rows(
+    const uint16_t* hidden_gate, const uint16_t* hidden_up, const int64_t* row_index, int32_t hidden_rows,
+    int32_t batch, const int32_t* expert_ids, const int32_t* segment_offsets, int32_t num_segments,
+    int64_t total_problem_tiles, const int32_t* decoded_gate, const int32_t* decoded_up,
+    const tris_compact3_payload* payload_gate, const tris_compact3_payload* payload_up, uint16_t* output,
+    void* stream) {
+  const char* who = "tris_grouped_swiglu_forward_block_gr_predecoded_rows";
+  TRIS_REQUIRE(row_index != nullptr || batch == 0, "%s: null row_index", who);
+  return swiglu_predecoded(hidden_gate, hidden_up, row_index, hidden_rows, batch, expert_ids, segment_offsets,
+                           num_segments, total_problem_tiles, decoded_gate, decoded_up, payload_gate, payload_up,
+                           output, stream, who);
 }
 
 extern "C" int tris_compact3_dequant(const tris_compact3_payload* payload, const int32_t* expert_ids, int32_t num,

@@ -52,10 +52,12 @@ constexpr int kMfSalWin = 32;             // salient columns per MFMA pass
 constexpr int kMfSalStride = kMfSalWin + 8;
 
 struct MfmaProj {
-  const uint16_t* hidden;  // [batch, rank]
-  uint16_t* out;           // [batch, N]
-  const int32_t* decoded;  // [num_segments, nblk, 128]
+  const uint16_t* hidden;     // [batch, rank], or [hidden_rows, rank] read through row_index
+  uint16_t* out;              // [batch, N]
+  const int32_t* decoded;     // [num_segments, nblk, 128]
   tris_compact3_payload p;
+  const int64_t* row_index;   // null, or [batch]: segment row r reads hidden row row_index[r]
+  int hidden_rows;
 };
 
 struct MfmaArgs {
@@ -266,6 +268,32 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   void* ub = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
   return __builtin_amdgcn_make_buffer_rsrc(ub, 0, n, kBufferWord3);
 }
+
+// Byte offset of 8 activation columns [c, c + 8) of segment row row0 + r (r < rc), or `oob` (an offset
+// past the buffer: the load reads zeros) for rows outside the tile, columns past the rank and gathered
+// rows whose index lies outside [0, hidden_rows).  With a row index the buffer resource covers all of
+// hidden; without, it starts at row row0.  r is wave-uniform, so the index load is one scalar load.
+__device__ __forceinline__ uint32_t mf_hidden_voff(const MfmaProj& pa, int row0, int r, int rc, int c, int rank,
+                                                   uint32_t oob) {
+  if (r >= rc || c >= rank) return oob;
+  int64_t src = r;
+  if (pa.row_index != nullptr) {
+    src = pa.row_index[row0 + r];
+    if (src < 0 || src >= pa.hidden_rows) return oob;
+  }
+  return static_cast<uint32_t>(src * rank + c) * 2u;
+}
+
+// The activation buffer resource of rows [row0, row0 + rc) and its size (the offset that reads zeros).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t mf_hidden_rsrc(const MfmaProj& pa, int row0, int rc, int rank,
+                                                                 uint32_t* bytes) {
+  if (pa.row_index != nullptr) {
+    *bytes = static_cast<uint32_t>(pa.hidden_rows) * rank * 2u;
+    return make_rsrc(pa.hidden, *bytes);
+  }
+  *bytes = static_cast<uint32_t>(rc) * rank * 2u;
+  return make_rsrc(pa.hidden + static_cast<int64_t>(row0) * rank, *bytes);
+}
 // Raw buffer loads: voffset at or past the buffer size returns 0 without a memory access.
 __device__ __forceinline__ uint32_t bload32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
@@ -309,9 +337,9 @@ __device__ __forceinline__ void mf_chunk_issue(const MfmaProj& pa, int e, int ro
   const int packed_rows = rank / 32;  // rank % 64 == 0
   const int pr0 = kc / 32;
   const int npr = (packed_rows - pr0) < kMfPR ? (packed_rows - pr0) : kMfPR;
-  const uint32_t hid_bytes = static_cast<uint32_t>(rc) * rank * 2u;
+  uint32_t hid_bytes;
+  const __amdgpu_buffer_rsrc_t r_hid = mf_hidden_rsrc(pa, row0, rc, rank, &hid_bytes);
   const uint32_t col_bytes = static_cast<uint32_t>(rank) * 8u;
-  const __amdgpu_buffer_rsrc_t r_hid = make_rsrc(pa.hidden + static_cast<int64_t>(row0) * rank, hid_bytes);
   const __amdgpu_buffer_rsrc_t r_col = make_rsrc(p.col_pack3 + static_cast<int64_t>(e) * rank, col_bytes);
   const int32_t* cmap_e = p.c_map + static_cast<int64_t>(e) * packed_rows;
   const int32_t* q2p_e = p.qweight2_sparse_prefix + static_cast<int64_t>(e) * (packed_rows + 1);
@@ -319,9 +347,7 @@ __device__ __forceinline__ void mf_chunk_issue(const MfmaProj& pa, int e, int ro
 #pragma unroll
   for (int h = 0; h < kMfRuns; ++h) {
     const int r = 4 * h + wave;
-    const int c = lane * 8;
-    const uint32_t voff = (r < rc && kc + c < rank) ? static_cast<uint32_t>(r * rank + kc + c) * 2u : hid_bytes;
-    R.xv[h] = bload128(r_hid, voff, 0u);
+    R.xv[h] = bload128(r_hid, mf_hidden_voff(pa, row0, r, rc, kc + lane * 8, rank, hid_bytes), 0u);
   }
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -888,14 +914,12 @@ __device__ __forceinline__ void ws_x_issue(const MfmaProj& pa, int row0, int rc,
   const int rank = pa.p.rank;
   const int wave = utid / kWave;
   const int lane = utid % kWave;
-  const uint32_t hid_bytes = static_cast<uint32_t>(rc) * rank * 2u;
-  const __amdgpu_buffer_rsrc_t r_hid = make_rsrc(pa.hidden + static_cast<int64_t>(row0) * rank, hid_bytes);
+  uint32_t hid_bytes;
+  const __amdgpu_buffer_rsrc_t r_hid = mf_hidden_rsrc(pa, row0, rc, rank, &hid_bytes);
 #pragma unroll
   for (int h = 0; h < kMfRuns; ++h) {
     const int r = 4 * h + wave;
-    const int c = lane * 8;
-    const uint32_t voff = (r < rc && c < rank) ? static_cast<uint32_t>(r * rank + c) * 2u : hid_bytes;
-    X.xv[h] = bload128(r_hid, voff, 0u);
+    X.xv[h] = bload128(r_hid, mf_hidden_voff(pa, row0, r, rc, lane * 8, rank, hid_bytes), 0u);
   }
 }
 
@@ -1298,8 +1322,10 @@ static bool ws_fits(const tris_compact3_payload* p) {
 int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int batch, const int32_t* expert_ids,
                         const int32_t* segment_offsets, int num_segments, const int32_t* decoded_a,
                         const int32_t* decoded_b, const tris_compact3_payload* pa, const tris_compact3_payload* pb,
-                        uint16_t* out_a, uint16_t* out_b, bool swiglu, void* stream, const char* who) {
+                        uint16_t* out_a, uint16_t* out_b, bool swiglu, void* stream, const char* who,
+                        const int64_t* row_index, int hidden_rows) {
   TRIS_REQUIRE(batch >= 0 && num_segments >= 0, "%s: negative batch or segment count", who);
+  TRIS_REQUIRE(row_index == nullptr || hidden_rows >= 0, "%s: negative hidden row count", who);
   int rc = check_payload(pa, false, who);
   if (rc) return rc;
   if (pb) {
@@ -1319,9 +1345,15 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
   TRIS_REQUIRE(!swiglu || (pa->outfeatures == pb->outfeatures && pa->num_experts == pb->num_experts &&
                            pa->rank == pb->rank),
                "%s: gate and up projections differ in shape", who);
+  if (row_index != nullptr) {
+    // gathered rows: one 32-bit buffer offset spans every hidden row
+    const int64_t bytes = static_cast<int64_t>(hidden_rows) * (pb && pb->rank > pa->rank ? pb->rank : pa->rank) * 2;
+    TRIS_REQUIRE(bytes < (int64_t{1} << 31), "%s: %d hidden rows exceed the 2 GiB activation limit", who,
+                 hidden_rows);
+  }
   MfmaArgs args{};
-  args.proj[0] = MfmaProj{hidden_a, out_a, decoded_a, *pa};
-  if (pb) args.proj[1] = MfmaProj{hidden_b, out_b, decoded_b, *pb};
+  args.proj[0] = MfmaProj{hidden_a, out_a, decoded_a, *pa, row_index, hidden_rows};
+  if (pb) args.proj[1] = MfmaProj{hidden_b, out_b, decoded_b, *pb, row_index, hidden_rows};
   args.expert_ids = expert_ids;
   args.segment_offsets = segment_offsets;
   args.num_segments = num_segments;

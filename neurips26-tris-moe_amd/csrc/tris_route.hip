@@ -14,7 +14,7 @@
 // For decode-sized batches route_topk_small_kernel does the router softmax
 // and top-k (modeling_mixtral.py:548-555) and all of the above in one
 // workgroup and one launch.
-#include "tris_common.h"
+#include "tris_backbone.h"
 
 namespace tris {
 
@@ -161,6 +161,33 @@ constexpr int kRouteSmallMaxRows = 2048;    // tokens * top_k
 constexpr int kRouteSmallMaxExperts = 1024;
 constexpr int kRouteMaxTopK = 16;
 
+// The fused router's arguments (tris_route_topk_grouped's outputs, see the header).
+struct RouteArgs {
+  const float* logits;
+  int tokens, num_experts, top_k, renormalize, m_tile;
+  uint16_t* weights16;
+  float* weights32;
+  int64_t* selected;
+  int64_t* perm;
+  int64_t* token_idx;
+  int64_t* slots;
+  int32_t* grouped_expert_ids;
+  int32_t* expert_ids;
+  int32_t* segment_offsets;
+  int32_t* problem_offsets;
+  int32_t* counts;
+  int32_t* inverse_perm;
+};
+
+// LDS of the one-workgroup router.
+struct RouteSmem {
+  int16_t sel[kRouteSmallMaxRows];
+  int cnt[kRouteSmallMaxExperts];
+  int seg_of[kRouteSmallMaxExperts];                   // segment base of each expert's next tokens
+  unsigned long long tok_bits[kRouteSmallMaxExperts];  // the chunk's tokens that picked expert e
+  int wave_tot[3][kRouteThreads / kWave];
+};
+
 // Softmax of one token's logits (fp32, max-subtracted, summed in expert order) and its top-k by
 // probability with ties to the lower expert id (a stable descending sort, as the oracle's argsort):
 // bp[j] / be[j] for j < top_k, most probable first.
@@ -207,7 +234,11 @@ __device__ __forceinline__ void route_token_topk(const float* __restrict__ row, 
 // ballots over q, the lowest expert holding it (ties to the lower expert id); the owner clears its slot.
 // A NaN probability (NaN or infinite logits) counts as 0, so every round finds an expert in range.
 // Lane j < top_k returns pick j: its expert and its weight, renormalised over the picks (summed in pick
-// order) or not.
+// order) or not.  pv: the lane's logits (route_load_logits).
+template <int P>
+__device__ __forceinline__ void route_token_wave(float (&pv)[P], int num_experts, int top_k, int renormalize,
+                                                 int& pick_e, float& pick_w);
+
 // The logits of one token for route_token_wave: lane l takes experts l + 64 q.
 template <int P>
 __device__ __forceinline__ void route_load_logits(const float* __restrict__ row, int num_experts, float (&pv)[P]) {
@@ -219,7 +250,6 @@ __device__ __forceinline__ void route_load_logits(const float* __restrict__ row,
   }
 }
 
-// pv: the lane's logits (route_load_logits).
 template <int P>
 __device__ __forceinline__ void route_token_wave(float (&pv)[P], int num_experts, int top_k, int renormalize,
                                                  int& pick_e, float& pick_w) {
@@ -294,15 +324,26 @@ constexpr int kRouteLaneMaxExperts = 8;   // its experts: a lane routes a token 
 // num_experts counts its expert by ballots, and prefix sums over lanes give the compacted active
 // experts and their segment / problem offsets; entry i's place in its segment is the number of
 // earlier entries of its expert.  The same outputs as route_topk_small_kernel.
+// Run by the first wavefront of a workgroup (lane = thread index < 64); lg: LDS for the logits,
+// kRouteWaveMaxRows * kRouteLaneMaxExperts floats.
 template <int K>
-__global__ __launch_bounds__(kWave) void route_topk_wave_kernel(
-    const float* __restrict__ logits, int tokens, int num_experts, int top_k, int renormalize, int m_tile,
-    uint16_t* __restrict__ weights16, float* __restrict__ weights32, int64_t* __restrict__ selected,
-    int64_t* __restrict__ perm, int64_t* __restrict__ token_idx, int64_t* __restrict__ slots,
-    int32_t* __restrict__ grouped_expert_ids, int32_t* __restrict__ expert_ids, int32_t* __restrict__ segment_offsets,
-    int32_t* __restrict__ problem_offsets, int32_t* __restrict__ counts, int32_t* __restrict__ inverse_perm) {
-  __shared__ float lg[kRouteWaveMaxRows * kRouteLaneMaxExperts];  // the logits, [tokens][num_experts]
-  const int lane = static_cast<int>(threadIdx.x);
+__device__ __forceinline__ void route_wave_body(const RouteArgs& ra, float* lg, int lane) {
+  const float* __restrict__ logits = ra.logits;
+  const int tokens = ra.tokens, num_experts = ra.num_experts, top_k = ra.top_k, renormalize = ra.renormalize;
+  const int m_tile = ra.m_tile;
+  uint16_t* __restrict__ weights16 = ra.weights16;
+  float* __restrict__ weights32 = ra.weights32;
+  int64_t* __restrict__ selected = ra.selected;
+  int64_t* __restrict__ perm = ra.perm;
+  int64_t* __restrict__ token_idx = ra.token_idx;
+  int64_t* __restrict__ slots = ra.slots;
+  int32_t* __restrict__ grouped_expert_ids = ra.grouped_expert_ids;
+  int32_t* __restrict__ expert_ids = ra.expert_ids;
+  int32_t* __restrict__ segment_offsets = ra.segment_offsets;
+  int32_t* __restrict__ problem_offsets = ra.problem_offsets;
+  int32_t* __restrict__ counts = ra.counts;
+  int32_t* __restrict__ inverse_perm = ra.inverse_perm;
+
   const int total = tokens * top_k;
   // every load in flight at once (coalesced), then each token reads its row from LDS
   const int nlog = tokens * num_experts;
@@ -410,22 +451,33 @@ __global__ __launch_bounds__(kWave) void route_topk_wave_kernel(
 // place in its expert's segment is the number of earlier tokens that picked the expert: tokens go in chunks
 // of 64, each expert's tokens of the chunk marked in a 64-bit mask, the segment bases advanced by the
 // masks' popcounts after each chunk.
+// Run by a whole workgroup of kRouteThreads threads (tid = thread index), with its LDS in sm.
 template <int P>
-__global__ __launch_bounds__(kRouteThreads) void route_topk_small_kernel(
-    const float* __restrict__ logits, int tokens, int num_experts, int top_k, int renormalize, int m_tile,
-    uint16_t* __restrict__ weights16, float* __restrict__ weights32, int64_t* __restrict__ selected,
-    int64_t* __restrict__ perm, int64_t* __restrict__ token_idx, int64_t* __restrict__ slots,
-    int32_t* __restrict__ grouped_expert_ids, int32_t* __restrict__ expert_ids, int32_t* __restrict__ segment_offsets,
-    int32_t* __restrict__ problem_offsets, int32_t* __restrict__ counts, int32_t* __restrict__ inverse_perm) {
+__device__ __forceinline__ void route_small_body(const RouteArgs& ra, RouteSmem& sm, int tid) {
   static_assert(kRouteSmallMaxExperts == kRouteThreads, "thread e owns expert e");
   static_assert(kRouteMaxTopK * kWave <= kRouteThreads, "a chunk of 64 tokens' entries fits the workgroup");
   constexpr int kWaves = kRouteThreads / kWave;
-  __shared__ int16_t sel[kRouteSmallMaxRows];
-  __shared__ int cnt[kRouteSmallMaxExperts];
-  __shared__ int seg_of[kRouteSmallMaxExperts];                   // segment base of each expert's next tokens
-  __shared__ unsigned long long tok_bits[kRouteSmallMaxExperts];  // the chunk's tokens that picked expert e
-  __shared__ int wave_tot[3][kWaves];
-  const int tid = threadIdx.x;
+  const float* __restrict__ logits = ra.logits;
+  const int tokens = ra.tokens, num_experts = ra.num_experts, top_k = ra.top_k, renormalize = ra.renormalize;
+  const int m_tile = ra.m_tile;
+  uint16_t* __restrict__ weights16 = ra.weights16;
+  float* __restrict__ weights32 = ra.weights32;
+  int64_t* __restrict__ selected = ra.selected;
+  int64_t* __restrict__ perm = ra.perm;
+  int64_t* __restrict__ token_idx = ra.token_idx;
+  int64_t* __restrict__ slots = ra.slots;
+  int32_t* __restrict__ grouped_expert_ids = ra.grouped_expert_ids;
+  int32_t* __restrict__ expert_ids = ra.expert_ids;
+  int32_t* __restrict__ segment_offsets = ra.segment_offsets;
+  int32_t* __restrict__ problem_offsets = ra.problem_offsets;
+  int32_t* __restrict__ counts = ra.counts;
+  int32_t* __restrict__ inverse_perm = ra.inverse_perm;
+  int16_t* sel = sm.sel;
+  int* cnt = sm.cnt;
+  int* seg_of = sm.seg_of;
+  unsigned long long* tok_bits = sm.tok_bits;
+  int (*wave_tot)[kRouteThreads / kWave] = sm.wave_tot;
+
   const int wave = tid / kWave;
   const int lane = tid % kWave;
   const int e = tid;
@@ -529,6 +581,80 @@ __global__ __launch_bounds__(kRouteThreads) void route_topk_small_kernel(
   }
 }
 
+template <int K>
+__global__ __launch_bounds__(kWave) void route_topk_wave_kernel(RouteArgs ra) {
+  __shared__ float lg[kRouteWaveMaxRows * kRouteLaneMaxExperts];  // the logits, [tokens][num_experts]
+  route_wave_body<K>(ra, lg, static_cast<int>(threadIdx.x));
+}
+
+template <int P>
+__global__ __launch_bounds__(kRouteThreads) void route_topk_small_kernel(RouteArgs ra) {
+  __shared__ RouteSmem sm;
+  route_small_body<P>(ra, sm, static_cast<int>(threadIdx.x));
+}
+
+// Router variants: the one-wavefront router with pick lists of 2, 8 or 16 entries (the smallest that holds
+// top_k: shorter unrolled insertion chains), or the workgroup router with 1, 2, 4, 8 or 16 experts a lane
+// (the smallest that covers num_experts: fewer registers of probabilities and ballots per pick).
+enum RouteKind : int {
+  kRouteWave2, kRouteWave8, kRouteWave16, kRouteSmall1, kRouteSmall2, kRouteSmall4, kRouteSmall8, kRouteSmall16
+};
+
+static int route_variant(int tokens, int num_experts, int top_k) {
+  if (static_cast<int64_t>(tokens) * top_k <= kRouteWaveMaxRows && num_experts <= kRouteLaneMaxExperts) {
+    return top_k <= 2 ? kRouteWave2 : top_k <= 8 ? kRouteWave8 : kRouteWave16;
+  }
+  const int per_lane = ceil_div(num_experts, kWave);
+  return per_lane <= 1   ? kRouteSmall1
+         : per_lane <= 2 ? kRouteSmall2
+         : per_lane <= 4 ? kRouteSmall4
+         : per_lane <= 8 ? kRouteSmall8
+                         : kRouteSmall16;
+}
+
+// The router in a workgroup of kRouteThreads threads (the one-wavefront variants use its first wavefront).
+__device__ __forceinline__ void route_dispatch(const RouteArgs& ra, int kind, RouteSmem& sm, float* lg, int tid) {
+  switch (kind) {
+    case kRouteWave2: if (tid < kWave) route_wave_body<2>(ra, lg, tid); break;
+    case kRouteWave8: if (tid < kWave) route_wave_body<8>(ra, lg, tid); break;
+    case kRouteWave16: if (tid < kWave) route_wave_body<kRouteMaxTopK>(ra, lg, tid); break;
+    case kRouteSmall1: route_small_body<1>(ra, sm, tid); break;
+    case kRouteSmall2: route_small_body<2>(ra, sm, tid); break;
+    case kRouteSmall4: route_small_body<4>(ra, sm, tid); break;
+    case kRouteSmall8: route_small_body<8>(ra, sm, tid); break;
+    default: route_small_body<kRouteSmallMaxExperts / kWave>(ra, sm, tid); break;
+  }
+}
+
+// The router and the shared backbone projection of the same tokens in one launch (they do not depend on
+// each other): workgroup 0 routes; every other workgroup runs kRbSub blocks of the backbone's grid
+// (backbone_block, 256 threads each, sharing the workgroup's one barrier).  The two roles never share a
+// workgroup, so their LDS is one union.
+constexpr int kRbSub = kRouteThreads / kBbThreads;
+
+template <int TT>
+union RouteBackboneSmem {
+  RouteSmem r;
+  float lg[kRouteWaveMaxRows * kRouteLaneMaxExperts];
+  f32x4 red[kRbSub][kBbWaves - 1][TT][kWave];
+};
+
+template <int TT, int B>
+__global__ __launch_bounds__(kRouteThreads) void route_backbone_kernel(RouteArgs ra, int kind, BackboneArgs ba,
+                                                                      int bb_blocks, int gx, int gy) {
+  __shared__ RouteBackboneSmem<TT> sm;
+  const int tid = static_cast<int>(threadIdx.x);
+  if (blockIdx.x == 0) {
+    route_dispatch(ra, kind, sm.r, sm.lg, tid);
+    return;
+  }
+  const int sub = tid / kBbThreads;
+  const int vb = (static_cast<int>(blockIdx.x) - 1) * kRbSub + sub;
+  const bool active = vb < bb_blocks;
+  const int v = active ? vb : 0;
+  backbone_block<TT, B>(ba, active, v % gx, (v / gx) % gy, v / (gx * gy), tid % kBbThreads, sm.red[sub]);
+}
+
 }  // namespace tris
 
 using namespace tris;
@@ -564,14 +690,13 @@ extern "C" int tris_build_grouped_route(const int64_t* selected_experts, int32_t
   return check_launch("route_scatter_kernel");
 }
 
-extern "C" int tris_route_topk_grouped(const float* router_logits, int32_t num_tokens, int32_t num_experts,
-                                       int32_t top_k, int32_t renormalize, int32_t m_tile,
-                                       uint16_t* routing_weights_f16, float* routing_weights_f32,
-                                       int64_t* selected_experts, int64_t* perm, int64_t* grouped_token_indices,
-                                       int64_t* grouped_slots, int32_t* grouped_expert_ids, int32_t* expert_ids,
-                                       int32_t* segment_offsets, int32_t* problem_offsets, int32_t* counts,
-                                       int32_t* inverse_perm, void* stream) {
-  const char* who = "tris_route_topk_grouped";
+// Validates tris_route_topk_grouped's arguments and fills ra.
+static int route_prepare(const float* router_logits, int32_t num_tokens, int32_t num_experts, int32_t top_k,
+                         int32_t renormalize, int32_t m_tile, uint16_t* routing_weights_f16, float* routing_weights_f32,
+                         int64_t* selected_experts, int64_t* perm, int64_t* grouped_token_indices,
+                         int64_t* grouped_slots, int32_t* grouped_expert_ids, int32_t* expert_ids,
+                         int32_t* segment_offsets, int32_t* problem_offsets, int32_t* counts, int32_t* inverse_perm,
+                         RouteArgs* ra, const char* who) {
   TRIS_REQUIRE(num_tokens >= 0 && num_experts > 0 && top_k > 0, "%s: bad shape", who);
   TRIS_REQUIRE(top_k <= num_experts && top_k <= kRouteMaxTopK, "%s: top_k %d (at most %d and num_experts)", who,
                top_k, kRouteMaxTopK);
@@ -585,26 +710,105 @@ extern "C" int tris_route_topk_grouped(const float* router_logits, int32_t num_t
   TRIS_REQUIRE(num_tokens == 0 || (router_logits && routing_weights_f16 && perm && grouped_token_indices &&
                                    grouped_slots && grouped_expert_ids),
                "%s: null pointer", who);
-  if (static_cast<int64_t>(num_tokens) * top_k <= kRouteWaveMaxRows && num_experts <= kRouteLaneMaxExperts) {
-    // the pick lists are sized to top_k's bucket: shorter unrolled insertion chains and less code to fetch
-    auto* kernel = top_k <= 2 ? route_topk_wave_kernel<2> : top_k <= 8 ? route_topk_wave_kernel<8>
-                                                                        : route_topk_wave_kernel<kRouteMaxTopK>;
-    hipLaunchKernelGGL(kernel, dim3(1), dim3(kWave), 0, static_cast<hipStream_t>(stream), router_logits, num_tokens, num_experts, top_k, renormalize, m_tile, routing_weights_f16,
-                       routing_weights_f32, selected_experts, perm, grouped_token_indices, grouped_slots,
-                       grouped_expert_ids, expert_ids, segment_offsets, problem_offsets, counts, inverse_perm);
-    return check_launch(who);
+  *ra = RouteArgs{router_logits, num_tokens, num_experts, top_k, renormalize, m_tile, routing_weights_f16,
+                  routing_weights_f32, selected_experts, perm, grouped_token_indices, grouped_slots,
+                  grouped_expert_ids, expert_ids, segment_offsets, problem_offsets, counts, inverse_perm};
+  return TRIS_OK;
+}
+
+static int launch_route(const RouteArgs& ra, hipStream_t s, const char* who) {
+  switch (route_variant(ra.tokens, ra.num_experts, ra.top_k)) {
+    case kRouteWave2: hipLaunchKernelGGL((route_topk_wave_kernel<2>), dim3(1), dim3(kWave), 0, s, ra); break;
+    case kRouteWave8: hipLaunchKernelGGL((route_topk_wave_kernel<8>), dim3(1), dim3(kWave), 0, s, ra); break;
+    case kRouteWave16:
+      hipLaunchKernelGGL((route_topk_wave_kernel<kRouteMaxTopK>), dim3(1), dim3(kWave), 0, s, ra);
+      break;
+    case kRouteSmall1: hipLaunchKernelGGL((route_topk_small_kernel<1>), dim3(1), dim3(kRouteThreads), 0, s, ra); break;
+    case kRouteSmall2: hipLaunchKernelGGL((route_topk_small_kernel<2>), dim3(1), dim3(kRouteThreads), 0, s, ra); break;
+    case kRouteSmall4: hipLaunchKernelGGL((route_topk_small_kernel<4>), dim3(1), dim3(kRouteThreads), 0, s, ra); break;
+    case kRouteSmall8: hipLaunchKernelGGL((route_topk_small_kernel<8>), dim3(1), dim3(kRouteThreads), 0, s, ra); break;
+    default:
+      hipLaunchKernelGGL((route_topk_small_kernel<kRouteSmallMaxExperts / kWave>), dim3(1), dim3(kRouteThreads), 0, s,
+                         ra);
+      break;
   }
-  // experts per lane: the smallest of 1, 2, 4, 8, 16 that covers num_experts (a shorter register file of
-  // probabilities and fewer ballots per pick)
-  const int per_lane = ceil_div(num_experts, kWave);
-  auto* small = per_lane <= 1   ? route_topk_small_kernel<1>
-                : per_lane <= 2 ? route_topk_small_kernel<2>
-                : per_lane <= 4 ? route_topk_small_kernel<4>
-                : per_lane <= 8 ? route_topk_small_kernel<8>
-                                : route_topk_small_kernel<kRouteSmallMaxExperts / kWave>;
-  hipLaunchKernelGGL(small, dim3(1), dim3(kRouteThreads), 0, static_cast<hipStream_t>(stream),
-                     router_logits, num_tokens, num_experts, top_k, renormalize, m_tile, routing_weights_f16,
-                     routing_weights_f32, selected_experts, perm, grouped_token_indices, grouped_slots,
-                     grouped_expert_ids, expert_ids, segment_offsets, problem_offsets, counts, inverse_perm);
   return check_launch(who);
+}
+
+extern "C" int tris_route_topk_grouped(const float* router_logits, int32_t num_tokens, int32_t num_experts,
+                                       int32_t top_k, int32_t renormalize, int32_t m_tile,
+                                       uint16_t* routing_weights_f16, float* routing_weights_f32,
+                                       int64_t* selected_experts, int64_t* perm, int64_t* grouped_token_indices,
+                                       int64_t* grouped_slots, int32_t* grouped_expert_ids, int32_t* expert_ids,
+                                       int32_t* segment_offsets, int32_t* problem_offsets, int32_t* counts,
+                                       int32_t* inverse_perm, void* stream) {
+  const char* who = "tris_route_topk_grouped";
+  RouteArgs ra;
+  int rc = route_prepare(router_logits, num_tokens, num_experts, top_k, renormalize, m_tile, routing_weights_f16,
+                         routing_weights_f32, selected_experts, perm, grouped_token_indices, grouped_slots,
+                         grouped_expert_ids, expert_ids, segment_offsets, problem_offsets, counts, inverse_perm, &ra,
+                         who);
+  if (rc) return rc;
+  return launch_route(ra, static_cast<hipStream_t>(stream), who);
+}
+
+// Backbone token tiles per workgroup in the merged launch: the 1024-thread workgroup caps the kernel at 128
+// VGPRs, which the 8-step load batches fit with one token tile only.
+constexpr int kRbMaxTokens = 64;
+
+extern "C" int tris_route_topk_backbone(const float* router_logits, int32_t num_tokens, int32_t num_experts,
+                                        int32_t top_k, int32_t renormalize, int32_t m_tile,
+                                        uint16_t* routing_weights_f16, float* routing_weights_f32,
+                                        int64_t* selected_experts, int64_t* perm, int64_t* grouped_token_indices,
+                                        int64_t* grouped_slots, int32_t* grouped_expert_ids, int32_t* expert_ids,
+                                        int32_t* segment_offsets, int32_t* problem_offsets, int32_t* counts,
+                                        int32_t* inverse_perm, const tris_backbone_pair_job* bb,
+                                        int32_t defer_reduce, void* stream) {
+  const char* who = "tris_route_topk_backbone";
+  RouteArgs ra;
+  int rc = route_prepare(router_logits, num_tokens, num_experts, top_k, renormalize, m_tile, routing_weights_f16,
+                         routing_weights_f32, selected_experts, perm, grouped_token_indices, grouped_slots,
+                         grouped_expert_ids, expert_ids, segment_offsets, problem_offsets, counts, inverse_perm, &ra,
+                         who);
+  if (rc) return rc;
+  TRIS_REQUIRE(bb != nullptr, "%s: null backbone job", who);
+  TRIS_REQUIRE(bb->tokens == num_tokens, "%s: the backbone's %d tokens differ from the router's %d", who, bb->tokens,
+               num_tokens);
+  TRIS_REQUIRE(num_tokens <= kRbMaxTokens, "%s: %d tokens exceed the merged launch's %d", who, num_tokens,
+               kRbMaxTokens);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (num_tokens == 0) return TRIS_OK;
+  BackboneArgs ba;
+  BackbonePlan pl;
+  rc = backbone_prepare(bb->x, bb->tokens, bb->in_features, nullptr, bb->sv_a, bb->sv_b, bb->rank, bb->in_scale_a,
+                        bb->in_scale_b, bb->out_a, bb->out_b, bb->workspace, bb->workspace_bytes, &ba, &pl, who);
+  if (rc) return rc;
+  const int nproj = bb->sv_b != nullptr ? 2 : 1;
+  const int gx = pl.row_tiles;
+  const int gy = pl.token_groups * pl.slices;
+  const int64_t blocks = static_cast<int64_t>(gx) * gy * nproj;
+  TRIS_REQUIRE(blocks < (int64_t{1} << 28), "%s: backbone grid too large", who);
+  const dim3 grid(static_cast<unsigned>(1 + ceil_div(static_cast<int>(blocks), kRbSub)));
+  const int kind = route_variant(num_tokens, num_experts, top_k);
+  switch (pl.tt) {
+    case 1:
+      hipLaunchKernelGGL((route_backbone_kernel<1, 8>), grid, dim3(kRouteThreads), 0, s, ra, kind, ba,
+                         static_cast<int>(blocks), gx, gy);
+      break;
+    case 2:
+      hipLaunchKernelGGL((route_backbone_kernel<2, 4>), grid, dim3(kRouteThreads), 0, s, ra, kind, ba,
+                         static_cast<int>(blocks), gx, gy);
+      break;
+    case 3:
+      hipLaunchKernelGGL((route_backbone_kernel<3, 4>), grid, dim3(kRouteThreads), 0, s, ra, kind, ba,
+                         static_cast<int>(blocks), gx, gy);
+      break;
+    default:
+      hipLaunchKernelGGL((route_backbone_kernel<4, 4>), grid, dim3(kRouteThreads), 0, s, ra, kind, ba,
+                         static_cast<int>(blocks), gx, gy);
+      break;
+  }
+  rc = check_launch(who);
+  if (rc || pl.slices == 1 || defer_reduce) return rc;
+  return launch_backbone_reduce(ba, nproj, s, who);
 }

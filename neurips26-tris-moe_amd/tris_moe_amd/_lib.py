@@ -64,6 +64,25 @@ class TrisPredecodeJob(ctypes.Structure):
     ]
 
 
+class TrisBackbonePairJob(ctypes.Structure):
+    """Mirror of struct tris_backbone_pair_job."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("tokens", ctypes.c_int32),
+        ("in_features", ctypes.c_int32),
+        ("sv_a", ctypes.c_void_p),
+        ("sv_b", ctypes.c_void_p),
+        ("rank", ctypes.c_int32),
+        ("in_scale_a", ctypes.c_void_p),
+        ("in_scale_b", ctypes.c_void_p),
+        ("out_a", ctypes.c_void_p),
+        ("out_b", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_int64),
+    ]
+
+
 class TrisPacked4(ctypes.Structure):
     """Mirror of struct tris_packed4_matrix."""
 
@@ -126,11 +145,19 @@ SIGNATURES = {
     "tris_grouped_dual_forward_block_gr": (ctypes.c_int, [_P, _P, _I32, _P, _P, _P, _I32, _I64, _PAY, _PAY, _P, _P, _P]),
     "tris_grouped_block_gr_predecode": (ctypes.c_int, [_P, _P, _I32, _P, _P, _P, _I32, _I32, _I32, _I32, _P]),
     "tris_grouped_block_gr_predecode_multi": (ctypes.c_int, [ctypes.POINTER(TrisPredecodeJob), _I32, _P, _I32, _P]),
+    "tris_grouped_block_gr_predecode_multi_reduce": (
+        ctypes.c_int, [ctypes.POINTER(TrisPredecodeJob), _I32, _P, _I32, ctypes.POINTER(TrisBackbonePairJob), _P]),
+    "tris_route_topk_backbone": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                                 _P, _P, _P, ctypes.POINTER(TrisBackbonePairJob), _I32, _P]),
     "tris_grouped_forward_block_gr_predecoded": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I32, _I64, _P, _PAY, _P, _P]),
     "tris_grouped_dual_forward_block_gr_predecoded": (
         ctypes.c_int, [_P, _P, _I32, _P, _P, _P, _I32, _I64, _P, _P, _PAY, _PAY, _P, _P, _P]),
     "tris_grouped_swiglu_forward_block_gr_predecoded": (
         ctypes.c_int, [_P, _P, _I32, _P, _P, _P, _I32, _I64, _P, _P, _PAY, _PAY, _P, _P]),
+    "tris_grouped_dual_forward_block_gr_predecoded_rows": (
+        ctypes.c_int, [_P, _P, _P, _I32, _I32, _P, _P, _I32, _I64, _P, _P, _PAY, _PAY, _P, _P, _P]),
+    "tris_grouped_swiglu_forward_block_gr_predecoded_rows": (
+        ctypes.c_int, [_P, _P, _P, _I32, _I32, _P, _P, _I32, _I64, _P, _P, _PAY, _PAY, _P, _P]),
     "tris_compact3_dequant": (ctypes.c_int, [_PAY, _P, _I32, _P, _P]),
     "tris_gr_decode_dense": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _P, _I32, _I32, _I32, _P, _P]),
     "tris_backbone_linear": (ctypes.c_int, [_P, _I32, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P]),

@@ -223,17 +223,14 @@ ROUTE_TOPK_MAX_EXPERTS = 1024
 ROUTE_TOPK_MAX_K = 16
 
 
-def route_topk_grouped(router_logits: torch.Tensor, top_k: int, renormalize: bool, m_tile: int = 4) -> dict:
-    """Router softmax / top-k / renormalisation (modeling_mixtral.py:548-555) and the padded grouped
-    route in one launch, for decode-sized batches (an extension; see build_grouped_route_device).
-    Returns the route dict plus routing_weights_f16 [T, k], routing_weights [T, k] fp32 and
-    selected_experts [T, k] int64."""
+def _route_topk_outputs(router_logits: torch.Tensor, top_k: int, who: str):
+    """Validated logits and the fused router's output tensors: (logits, dict of outputs)."""
     _check_cuda("router_logits", router_logits, torch.float32, 2)
     logits = router_logits.contiguous()
     t, e = int(logits.size(0)), int(logits.size(1))
     k = int(top_k)
     if t * k > ROUTE_TOPK_MAX_ROWS or e > ROUTE_TOPK_MAX_EXPERTS or k > ROUTE_TOPK_MAX_K or k > e or k <= 0:
-        raise RuntimeError("route_topk_grouped: batch outside the one-workgroup limits")
+        raise RuntimeError(f"{who}: batch outside the one-workgroup limits")
     dev = logits.device
     r = t * k
     long_opts = dict(device=dev, dtype=torch.int64)
@@ -250,13 +247,104 @@ def route_topk_grouped(router_logits: torch.Tensor, top_k: int, renormalize: boo
     prob = torch.empty(e + 1, **int_opts)
     counts = torch.empty(2, **int_opts)
     inv = torch.empty(r, **int_opts)
-    _lib.check(_lib.load().tris_route_topk_grouped(
-        _ptr(logits), t, e, k, int(bool(renormalize)), int(m_tile), _ptr(w16), _ptr(w32), _ptr(sel), _ptr(perm),
-        _ptr(gti), _ptr(gsl), _ptr(gexp), _ptr(expert_ids), _ptr(seg), _ptr(prob), _ptr(counts), _ptr(inv),
-        _stream(logits)), "route_topk_grouped")
-    return {"perm": perm, "grouped_token_indices": gti, "grouped_slots": gsl, "grouped_expert_ids": gexp,
-            "expert_ids": expert_ids, "segment_offsets": seg, "problem_offsets": prob, "counts": counts,
-            "inverse_perm": inv, "routing_weights_f16": w16, "routing_weights": w32, "selected_experts": sel}
+    return logits, {"perm": perm, "grouped_token_indices": gti, "grouped_slots": gsl, "grouped_expert_ids": gexp,
+                    "expert_ids": expert_ids, "segment_offsets": seg, "problem_offsets": prob, "counts": counts,
+                    "inverse_perm": inv, "routing_weights_f16": w16, "routing_weights": w32,
+                    "selected_experts": sel}
+
+
+def _route_topk_args(logits, out, top_k, renormalize, m_tile):
+    t, e = int(logits.size(0)), int(logits.size(1))
+    return (_ptr(logits), t, e, int(top_k), int(bool(renormalize)), int(m_tile), _ptr(out["routing_weights_f16"]),
+            _ptr(out["routing_weights"]), _ptr(out["selected_experts"]), _ptr(out["perm"]),
+            _ptr(out["grouped_token_indices"]), _ptr(out["grouped_slots"]), _ptr(out["grouped_expert_ids"]),
+            _ptr(out["expert_ids"]), _ptr(out["segment_offsets"]), _ptr(out["problem_offsets"]),
+            _ptr(out["counts"]), _ptr(out["inverse_perm"]))
+
+
+def route_topk_grouped(router_logits: torch.Tensor, top_k: int, renormalize: bool, m_tile: int = 4) -> dict:
+    """Router softmax / top-k / renormalisation (modeling_mixtral.py:548-555) and the padded grouped
+    route in one launch, for decode-sized batches (an extension; see build_grouped_route_device).
+    Returns the route dict plus routing_weights_f16 [T, k], routing_weights [T, k] fp32 and
+    selected_experts [T, k] int64."""
+    logits, out = _route_topk_outputs(router_logits, top_k, "route_topk_grouped")
+    _lib.check(_lib.load().tris_route_topk_grouped(*_route_topk_args(logits, out, top_k, renormalize, m_tile),
+                                                   _stream(logits)), "route_topk_grouped")
+    return out
+
+
+ROUTE_BACKBONE_MAX_TOKENS = 64  # tokens of tris_route_topk_backbone
+_DEFERRED_WORKSPACES: dict = {}
+
+
+class BackbonePending:
+    """Gate/up backbone outputs launched beside the router (route_topk_backbone_pair) whose split-K slice
+    reduction may still be outstanding: pass it as ``backbone`` to grouped_block_gr_predecode_multi (or to
+    finish_backbone) on the same stream before out_a / out_b are read."""
+
+    __slots__ = ("job", "out_a", "out_b", "keep")
+
+    def __init__(self, job, out_a, out_b, keep):
+        self.job, self.out_a, self.out_b, self.keep = job, out_a, out_b, keep
+
+
+def route_topk_backbone_ok(x: torch.Tensor, sv_a, sv_b, in_scale_a=None, in_scale_b=None) -> bool:
+    """True when route_topk_backbone_pair can run this backbone pair: fp16 SV matrices of one shape over x's
+    columns, 16-byte aligned, at most ROUTE_BACKBONE_MAX_TOKENS tokens."""
+    if not (isinstance(sv_a, torch.Tensor) and isinstance(sv_b, torch.Tensor)):
+        return False
+    if x.dtype != torch.float16 or x.dim() != 2 or not x.is_contiguous() or x.data_ptr() % 16:
+        return False
+    if int(x.size(0)) > ROUTE_BACKBONE_MAX_TOKENS or int(x.size(0)) == 0:
+        return False
+    for sv in (sv_a, sv_b):
+        if (sv.dtype != torch.float16 or sv.dim() != 2 or not sv.is_contiguous() or sv.data_ptr() % 16
+                or sv.device != x.device):
+            return False
+    if sv_a.shape != sv_b.shape or int(sv_a.size(1)) != int(x.size(1)) or int(x.size(1)) == 0:
+        return False
+    for sc in (in_scale_a, in_scale_b):
+        if sc is not None and (sc.dtype != torch.float16 or sc.numel() != x.size(1) or not sc.is_contiguous()
+                               or sc.data_ptr() % 16):
+            return False
+    return True
+
+
+def route_topk_backbone_pair(router_logits: torch.Tensor, top_k: int, renormalize: bool, m_tile: int,
+                             x: torch.Tensor, sv_a: torch.Tensor, sv_b: torch.Tensor,
+                             in_scale_a: torch.Tensor | None = None, in_scale_b: torch.Tensor | None = None):
+    """route_topk_grouped and the gate/up backbones of the same tokens (backbone_linear_pair without a row
+    index) in one launch (tris_route_topk_backbone, an extension).  Returns (route dict, BackbonePending): the
+    backbone's split-K reduction is left for the predecode launch."""
+    if not route_topk_backbone_ok(x, sv_a, sv_b, in_scale_a, in_scale_b):
+        raise RuntimeError("route_topk_backbone_pair: backbone pair outside the merged launch's conditions")
+    logits, out = _route_topk_outputs(router_logits, top_k, "route_topk_backbone_pair")
+    if int(x.size(0)) != int(logits.size(0)):
+        raise RuntimeError("route_topk_backbone_pair: x and router_logits differ in tokens")
+    tokens, in_f, rank = int(x.size(0)), int(x.size(1)), int(sv_a.size(0))
+    out_a = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
+    out_b = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
+    lib = _lib.load()
+    nbytes = int(lib.tris_backbone_pair_workspace_bytes(tokens, in_f, rank))
+    # a buffer of its own: the partial sums must survive until the predecode launch reduces them
+    key = (x.device.type, x.device.index)
+    ws = _DEFERRED_WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=x.device)
+        _DEFERRED_WORKSPACES[key] = ws
+    job = _lib.TrisBackbonePairJob(_ptr(x), tokens, in_f, _ptr(sv_a), _ptr(sv_b), rank, _ptr(in_scale_a),
+                                   _ptr(in_scale_b), _ptr(out_a), _ptr(out_b), _ptr(ws), int(ws.numel()))
+    _lib.check(lib.tris_route_topk_backbone(*_route_topk_args(logits, out, top_k, renormalize, m_tile),
+                                            ctypes.byref(job), 1, _stream(logits)), "route_topk_backbone_pair")
+    return out, BackbonePending(job, out_a, out_b, (x, sv_a, sv_b, in_scale_a, in_scale_b, ws))
+
+
+def finish_backbone(pending: BackbonePending):
+    """Run a BackbonePending's outstanding reduction alone (when no predecode launch follows); returns
+    (out_a, out_b)."""
+    _lib.check(_lib.load().tris_grouped_block_gr_predecode_multi_reduce(
+        None, 0, None, 0, ctypes.byref(pending.job), _stream(pending.out_a)), "finish_backbone")
+    return pending.out_a, pending.out_b
 
 
 # ----------------------------------------------------------- grouped GEMMs
@@ -340,11 +428,13 @@ def compact3_tris_precomputed_grouped_block_gr_predecode(decoded_q_gmap_words, e
     return decoded_q_gmap_words
 
 
-def grouped_block_gr_predecode_multi(jobs, expert_ids):
+def grouped_block_gr_predecode_multi(jobs, expert_ids, backbone: BackbonePending | None = None):
     """Predecode several projections' GR streams for the same routed experts in one launch (an
     extension batching TriSMoE_cuda.cpp:836-853).  jobs: sequence of (decoded_buffer,
     q_gmap_gr_words, q_gmap_gr_offsets, q_gmap_gr_meta, packed_rows, outfeatures); each buffer is
-    filled as compact3_tris_precomputed_grouped_block_gr_predecode would fill it and returned."""
+    filled as compact3_tris_precomputed_grouped_block_gr_predecode would fill it and returned.
+    ``backbone``: a BackbonePending whose slice reduction runs in the same launch
+    (tris_grouped_block_gr_predecode_multi_reduce)."""
     if len(jobs) > _lib.MAX_PREDECODE_JOBS:
         raise RuntimeError(f"at most {_lib.MAX_PREDECODE_JOBS} predecode jobs per launch")
     _check_cuda("expert_ids", expert_ids, torch.int32, 1)
@@ -367,6 +457,11 @@ def grouped_block_gr_predecode_multi(jobs, expert_ids):
         keep.append(words)
         arr[q] = _lib.TrisPredecodeJob(_ptr(buf), _ptr(words), _ptr(offsets), _ptr(meta), int(offsets.size(0)),
                                        int(words.size(1)), int(packed_rows), int(outfeatures))
+    if backbone is not None:
+        _lib.check(_lib.load().tris_grouped_block_gr_predecode_multi_reduce(
+            arr, len(jobs), _ptr(expert_ids), num_active, ctypes.byref(backbone.job), _stream(expert_ids)),
+            "grouped_block_gr_predecode_multi")
+        return [j[0] for j in jobs]
     _lib.check(_lib.load().tris_grouped_block_gr_predecode_multi(arr, len(jobs), _ptr(expert_ids), num_active,
                                                                  _stream(expert_ids)),
                "grouped_block_gr_predecode_multi")
@@ -405,6 +500,17 @@ def _out_buffer(out, rows, cols, device):
     return out
 
 
+def _gather_rows(row_index, hidden_a, hidden_b):
+    """Grouped row count: hidden's rows, or row_index's length when the rows are gathered (then both
+    hidden tensors must hold the same rows)."""
+    if row_index is None:
+        return int(hidden_a.size(0))
+    _check_cuda("row_index", row_index, torch.int64, 1, hidden_a.device)
+    if int(hidden_b.size(0)) != int(hidden_a.size(0)):
+        raise RuntimeError("gathered hidden_a and hidden_b must have the same rows")
+    return int(row_index.size(0))
+
+
 def _check_predecoded(decoded, expert_ids, pay, device):
     _check_cuda("decoded_q_gmap_words", decoded, torch.int32, None, device)
     nblk = _num_gr_blocks((pay.rank + 31) // 32, pay.outfeatures)
@@ -416,10 +522,15 @@ def compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
         hidden_a, hidden_b, expert_ids, segment_offsets, problem_offsets, total_problem_tiles,
         decoded_q_gmap_words_a, qweight1_a, qweight2_sparse_a, qweight2_sparse_prefix_a, c_map_a, g_idx_a,
         col_pack3_a, row_pack3_a, decoded_q_gmap_words_b, qweight1_b, qweight2_sparse_b, qweight2_sparse_prefix_b,
-        c_map_b, g_idx_b, col_pack3_b, row_pack3_b, use_uniform_k64_groups=False, out_a=None, out_b=None):
-    """TriSMoE_cuda.cpp:922-974.  ``out_a`` / ``out_b`` as ``out`` of the single-projection call."""
+        c_map_b, g_idx_b, col_pack3_b, row_pack3_b, use_uniform_k64_groups=False, out_a=None, out_b=None,
+        row_index=None):
+    """TriSMoE_cuda.cpp:922-974.  ``out_a`` / ``out_b`` as ``out`` of the single-projection call.
+    ``row_index``: optional int64 [batch] (the route's grouped_token_indices): grouped row r reads row
+    row_index[r] of per-token hidden_a / hidden_b (tris_grouped_dual_forward_block_gr_predecoded_rows, an
+    extension; the MFMA kernel's payload conditions apply)."""
     _check_route(hidden_a, expert_ids, segment_offsets, problem_offsets)
     _check_cuda("hidden_b", hidden_b, torch.float16, 2, hidden_a.device)
+    batch = _gather_rows(row_index, hidden_a, hidden_b)
     total = _host_tiles(total_problem_tiles)
     pa = make_payload_struct(int(hidden_a.size(1)), qweight1_a, qweight2_sparse_a, qweight2_sparse_prefix_a, None,
                              None, None, c_map_a, g_idx_a, col_pack3_a, row_pack3_a, None, False, None, False,
@@ -429,8 +540,15 @@ def compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
                              use_uniform_k64_groups, hidden_a.device, need_gr=False, who="grouped payload b")
     _check_predecoded(decoded_q_gmap_words_a, expert_ids, pa, hidden_a.device)
     _check_predecoded(decoded_q_gmap_words_b, expert_ids, pb, hidden_a.device)
-    out_a = _out_buffer(out_a, hidden_a.size(0), pa.outfeatures, hidden_a.device)
-    out_b = _out_buffer(out_b, hidden_b.size(0), pb.outfeatures, hidden_a.device)
+    out_a = _out_buffer(out_a, batch, pa.outfeatures, hidden_a.device)
+    out_b = _out_buffer(out_b, batch, pb.outfeatures, hidden_a.device)
+    if row_index is not None:
+        _lib.check(_lib.load().tris_grouped_dual_forward_block_gr_predecoded_rows(
+            _ptr(hidden_a), _ptr(hidden_b), _ptr(row_index), int(hidden_a.size(0)), batch, _ptr(expert_ids),
+            _ptr(segment_offsets), int(expert_ids.size(0)), total, _ptr(decoded_q_gmap_words_a),
+            _ptr(decoded_q_gmap_words_b), ctypes.byref(pa), ctypes.byref(pb), _ptr(out_a), _ptr(out_b),
+            _stream(hidden_a)), "compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded")
+        return [out_a, out_b]
     _lib.check(_lib.load().tris_grouped_dual_forward_block_gr_predecoded(
         _ptr(hidden_a), _ptr(hidden_b), int(hidden_a.size(0)), _ptr(expert_ids), _ptr(segment_offsets),
         _ptr(problem_offsets), int(expert_ids.size(0)), total, _ptr(decoded_q_gmap_words_a),
@@ -443,12 +561,13 @@ def compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded(
         hidden_gate, hidden_up, expert_ids, segment_offsets, problem_offsets, total_problem_tiles,
         decoded_q_gmap_words_gate, qweight1_gate, qweight2_sparse_gate, qweight2_sparse_prefix_gate, c_map_gate,
         g_idx_gate, col_pack3_gate, row_pack3_gate, decoded_q_gmap_words_up, qweight1_up, qweight2_sparse_up,
-        qweight2_sparse_prefix_up, c_map_up, g_idx_up, col_pack3_up, row_pack3_up, out=None):
+        qweight2_sparse_prefix_up, c_map_up, g_idx_up, col_pack3_up, row_pack3_up, out=None, row_index=None):
     """fp16(silu(gate) * up) of the dual predecoded GEMM (TriSMoE_cuda.cpp:922-974) fused with the
     SwiGLU product of modeling_mixtral.py:496 (an extension with no reference entry point; needs
-    uniform 64-column groups)."""
+    uniform 64-column groups).  ``row_index`` as in the dual call."""
     _check_route(hidden_gate, expert_ids, segment_offsets, problem_offsets)
     _check_cuda("hidden_up", hidden_up, torch.float16, 2, hidden_gate.device)
+    batch = _gather_rows(row_index, hidden_gate, hidden_up)
     total = _host_tiles(total_problem_tiles)
     pg = make_payload_struct(int(hidden_gate.size(1)), qweight1_gate, qweight2_sparse_gate,
                              qweight2_sparse_prefix_gate, None, None, None, c_map_gate, g_idx_gate, col_pack3_gate,
@@ -459,7 +578,14 @@ def compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded(
                              False, True, hidden_gate.device, need_gr=False, who="up payload")
     _check_predecoded(decoded_q_gmap_words_gate, expert_ids, pg, hidden_gate.device)
     _check_predecoded(decoded_q_gmap_words_up, expert_ids, pu, hidden_gate.device)
-    out = _out_buffer(out, hidden_gate.size(0), pg.outfeatures, hidden_gate.device)
+    out = _out_buffer(out, batch, pg.outfeatures, hidden_gate.device)
+    if row_index is not None:
+        _lib.check(_lib.load().tris_grouped_swiglu_forward_block_gr_predecoded_rows(
+            _ptr(hidden_gate), _ptr(hidden_up), _ptr(row_index), int(hidden_gate.size(0)), batch, _ptr(expert_ids),
+            _ptr(segment_offsets), int(expert_ids.size(0)), total, _ptr(decoded_q_gmap_words_gate),
+            _ptr(decoded_q_gmap_words_up), ctypes.byref(pg), ctypes.byref(pu), _ptr(out), _stream(hidden_gate)),
+            "compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded")
+        return out
     _lib.check(_lib.load().tris_grouped_swiglu_forward_block_gr_predecoded(
         _ptr(hidden_gate), _ptr(hidden_up), int(hidden_gate.size(0)), _ptr(expert_ids), _ptr(segment_offsets),
         _ptr(problem_offsets), int(expert_ids.size(0)), total, _ptr(decoded_q_gmap_words_gate),
@@ -508,6 +634,24 @@ def decode_payload_ok(p: dict) -> bool:
     rank = int(p["g_idx"].size(1))
     return bool(p.get("_compact3_k64_groups_uniform", False)) and rank % 256 == 0 and 0 < rank <= 512 and \
         p.get("q_gmap_gr_words") is not None
+
+
+MFMA_MAX_GROUPS = 8  # row-scale groups the MFMA kernel stages whole per output tile
+
+
+def mfma_payload_ok(p: dict) -> bool:
+    """The payload suits the predecoded MFMA kernel (the one that can gather its rows through a row index):
+    uniform 64-column groups, rank a multiple of 64, at most MFMA_MAX_GROUPS groups and 32-bit buffer offsets
+    per expert."""
+    rank = int(p["g_idx"].size(1))
+    n = int(p["qweight1"].size(2))
+    groups = int(p["row_pack3"].size(2))
+    packed_rows = (rank + 31) // 32
+    limit = 1 << 31
+    return (bool(p.get("_compact3_k64_groups_uniform", False)) and rank > 0 and rank % 64 == 0
+            and 1 <= groups <= MFMA_MAX_GROUPS and packed_rows * n * 4 < limit
+            and int(p["qweight2_sparse"].size(1)) * n * 4 < limit and n * groups * 8 < limit
+            and ((packed_rows + 1) // 2) * ((n + 63) // 64) * 128 * 4 < limit)
 
 
 def _decode_struct(p: dict, device):

@@ -66,12 +66,27 @@ def grouped_moe_forward_from_logits(x16: torch.Tensor, router_logits: torch.Tens
                                     output_dtype=torch.bfloat16, shared_expert=None,
                                     expert_path: str = "auto") -> torch.Tensor:
     """The layer from router logits: softmax / top-k / renormalisation / route in one kernel when the
-    batch is decode-sized (tris_route_topk_grouped), else route_topk + the two-kernel route."""
+    batch is decode-sized (tris_route_topk_grouped), else route_topk + the two-kernel route.  On the
+    predecoded path with fp16 gate/up backbones and at most ext.ROUTE_BACKBONE_MAX_TOKENS tokens, the
+    gate/up backbones of the tokens run in the router's launch (tris_route_topk_backbone), their split-K
+    reduction in the predecode's, and the grouped GEMMs gather their rows through the route's token
+    indices (the backbone values equal those of the gathered rows up to the split-K summation order: the
+    slice count follows the row count)."""
     T, H = int(x16.size(0)), int(x16.size(1))
     if T * top_k == 0:
         return torch.zeros((T, H), dtype=output_dtype, device=x16.device)
     if (router_logits.dtype == torch.float32 and T * top_k <= ext.ROUTE_TOPK_MAX_ROWS
             and num_experts <= ext.ROUTE_TOPK_MAX_EXPERTS and top_k <= ext.ROUTE_TOPK_MAX_K):
+        sc = _in_scales(backbones)
+        if (expert_path != "fused" and _predecodable(payloads)
+                and ext.mfma_payload_ok(payloads["gate"]) and ext.mfma_payload_ok(payloads["up"])
+                and ext.route_topk_backbone_ok(x16, backbones["gate"], backbones["up"], sc["gate"], sc["up"])):
+            route, pending = ext.route_topk_backbone_pair(router_logits, top_k, renormalize, GROUPED_SEGMENT_M_TILE,
+                                                          x16, backbones["gate"], backbones["up"],
+                                                          in_scale_a=sc["gate"], in_scale_b=sc["up"])
+            return _forward_with_route(x16, route["routing_weights_f16"], route, top_k, payloads, backbones,
+                                       num_experts, output_dtype, shared_expert, expert_path,
+                                       backbone_pending=pending)
         route = ext.route_topk_grouped(router_logits, top_k, renormalize, GROUPED_SEGMENT_M_TILE)
         return _forward_with_route(x16, route["routing_weights_f16"], route, top_k, payloads, backbones,
                                    num_experts, output_dtype, shared_expert, expert_path)
@@ -80,8 +95,15 @@ def grouped_moe_forward_from_logits(x16: torch.Tensor, router_logits: torch.Tens
                                shared_expert, expert_path)
 
 
+def _predecodable(payloads: dict) -> bool:
+    """Every projection has uniform 64-column groups and no output scale or bias (the predecoded path)."""
+    pg, pu, pd = payloads["gate"], payloads["up"], payloads["down"]
+    return all(bool(p.get("_compact3_k64_groups_uniform", False)) for p in (pg, pu, pd)) and not any(
+        bool(p["has_output_scale"]) or bool(p["has_bias"]) for p in (pg, pu, pd))
+
+
 def _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, output_dtype, shared_expert,
-                        expert_path):
+                        expert_path, backbone_pending=None):
     if expert_path not in ("auto", "fused", "predecoded"):
         raise ValueError(f"unknown expert_path {expert_path!r}")
     T = int(x16.size(0))
@@ -95,13 +117,14 @@ def _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, ou
     pg, pu, pd = payloads["gate"], payloads["up"], payloads["down"]
     ns = _ns_payloads(payloads)
     uniform = bool(pg.get("_compact3_k64_groups_uniform", False) and pu.get("_compact3_k64_groups_uniform", False))
-    predecodable = uniform and bool(pd.get("_compact3_k64_groups_uniform", False)) and not any(
-        bool(p["has_output_scale"]) or bool(p["has_bias"]) for p in (pg, pu, pd))
+    predecodable = _predecodable(payloads)
     if expert_path == "predecoded" and not predecodable:
         raise RuntimeError("the predecoded expert path needs uniform 64-column groups and no output scale or bias")
     if predecodable and expert_path != "fused":
         return _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype,
-                                       shared_expert)
+                                       shared_expert, backbone_pending=backbone_pending)
+    if backbone_pending is not None:
+        raise RuntimeError("a backbone launched beside the router needs the predecoded expert path")
     if all(ext.decode_payload_ok(p) for p in (pg, pu, pd)):
         return _decode_fused_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype,
                                          shared_expert)
@@ -187,7 +210,8 @@ FUSED_SWIGLU_MAX_ROWS = 4
 NS_DOWN_BESIDE_GEMM = True
 
 
-def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype, shared_expert):
+def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype, shared_expert,
+                            backbone_pending=None):
     """Uniform-group payloads without output scale or bias: GR-decode every routed expert's split
     bitmaps once per projection (TriSMoE_cuda.cpp:836-853), then run the predecoded grouped GEMMs
     (TriSMoE_cuda.cpp:855-889, 922-974).  Active experts come first in the padded route, so
@@ -198,7 +222,11 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     joined later, with the same fp16 adds: gate/up's on a stream of their own from the routed inputs
     (read through the route's token indices), beside the decodes and the backbones, and added inside
     act_fn(g) * u; the down projection's on the side stream beside the down backbone and GEMM, and added
-    inside the combine."""
+    inside the combine.
+
+    backbone_pending: the gate/up backbones of the tokens launched beside the router (ext.BackbonePending);
+    their split-K reduction runs in the predecode's launch and the gate/up GEMMs gather their rows through
+    the route's token indices."""
     slots = min(num_experts, R)
     eid = route["expert_ids"][:slots]
     seg = route["segment_offsets"][: slots + 1]
@@ -228,14 +256,20 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     # first and delays them, and the join costs more than the overlap saves (measured on MI355X at the
     # Mixtral decode shape)
     order = (("gate", pg), ("up", pu), ("down", pd))
-    ext.grouped_block_gr_predecode_multi(
-        [(bufs[name], p["q_gmap_gr_words"], p["q_gmap_gr_offsets"], p["q_gmap_gr_meta"], int(p["qweight1"].size(1)),
-          int(p["qweight1"].size(2))) for name, p in order], eid)
+    pre_jobs = [(bufs[name], p["q_gmap_gr_words"], p["q_gmap_gr_offsets"], p["q_gmap_gr_meta"],
+                 int(p["qweight1"].size(1)), int(p["qweight1"].size(2))) for name, p in order]
     decoded = bufs
     sc = _in_scales(backbones)
-    hid_g, hid_u = shared_projection_pair(x16, backbones["gate"], backbones["up"],
-                                          row_index=route["grouped_token_indices"], in_scale_a=sc["gate"],
-                                          in_scale_b=sc["up"])
+    if backbone_pending is not None:
+        ext.grouped_block_gr_predecode_multi(pre_jobs, eid, backbone=backbone_pending)
+        hid_g, hid_u = backbone_pending.out_a, backbone_pending.out_b
+        gather = route["grouped_token_indices"]
+    else:
+        ext.grouped_block_gr_predecode_multi(pre_jobs, eid)
+        hid_g, hid_u = shared_projection_pair(x16, backbones["gate"], backbones["up"],
+                                              row_index=route["grouped_token_indices"], in_scale_a=sc["gate"],
+                                              in_scale_b=sc["up"])
+        gather = None
     if ns_side is not None:
         main.wait_stream(ns_side)
     names = ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx", "col_pack3", "row_pack3")
@@ -245,7 +279,7 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
         # few rows: the gate/up GEMM with act_fn(g) * u in its epilogue (one launch)
         ext.compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded(
             hid_g, hid_u, eid, seg, prob, tile_bound, decoded["gate"], *[pg[k] for k in names], decoded["up"],
-            *[pu[k] for k in names], out=mlp)
+            *[pu[k] for k in names], out=mlp, row_index=gather)
     else:
         # more rows: gate and up in separate workgroups (more of them resident per CU), then act_fn(g) * u;
         # the same bits as the fused epilogue
@@ -253,7 +287,7 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
         u = torch.empty((R, n_mlp), dtype=torch.float16, device=dev)
         ext.compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
             hid_g, hid_u, eid, seg, prob, tile_bound, decoded["gate"], *[pg[k] for k in names], decoded["up"],
-            *[pu[k] for k in names], True, out_a=g, out_b=u)
+            *[pu[k] for k in names], True, out_a=g, out_b=u, row_index=gather)
         # g + comp_g and u + comp_u (fp16 adds) inside act_fn(g) * u
         ext.swiglu_mul(g, u, out=mlp, comp_gate=comp_g, comp_up=comp_u)
     n_out = int(pd["qweight1"].size(2))

@@ -1,0 +1,226 @@
+"""Launches that carry independent work of the decode step together, against the separate calls they
+replace: the router with the gate/up backbones of the same tokens (tris_route_topk_backbone), the backbone's
+split-K slice reduction inside the predecode launch (tris_grouped_block_gr_predecode_multi_reduce), and the
+predecoded dual / SwiGLU GEMMs gathering their activation rows through a row index (the *_rows entries, on
+the decode kernel and on the weight-stationary prefill kernel).  Each gives the bits of the calls it
+replaces; the gathered GEMMs are also checked against the oracle."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+REL_L2 = 1e-3
+ROUTE_KEYS = ("perm", "grouped_token_indices", "grouped_slots", "grouped_expert_ids", "expert_ids", "segment_offsets",
+              "problem_offsets", "counts", "inverse_perm", "routing_weights_f16", "routing_weights",
+              "selected_experts")
+NAMES = ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx", "col_pack3", "row_pack3")
+
+
+def note(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def assert_close(got, want, what):
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    assert np.isfinite(got).all(), what
+    err = got - want
+    max_abs = float(np.abs(err).max()) if err.size else 0.0
+    denom = float(np.linalg.norm(want))
+    rel = float(np.linalg.norm(err)) / denom if denom > 0 else float(np.linalg.norm(err))
+    assert max_abs <= MAX_ABS and rel <= REL_L2, f"{what}: max_abs={max_abs:.3g} rel_l2={rel:.3g}"
+
+
+def t_i32(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(dev)
+
+
+def make_projection(tris, seed, E, n, k, p=0.15):
+    syn = tris["synthetic"]
+    rng = syn.rng_for(seed)
+    return syn.make_projection(rng, E, n, k, p, rng.random(k) + 0.5, tris["ext"].gr_encode)
+
+
+def backbone_inputs(seed, tokens, in_f, rank, scales, dev):
+    rng = np.random.default_rng(seed)
+    x = torch.from_numpy(rng.standard_normal((tokens, in_f)).astype(np.float16)).to(dev)
+    sv_a = torch.from_numpy((rng.standard_normal((rank, in_f)) * 0.05).astype(np.float16)).to(dev)
+    sv_b = torch.from_numpy((rng.standard_normal((rank, in_f)) * 0.05).astype(np.float16)).to(dev)
+    sa = sb = None
+    if scales:
+        sa = torch.from_numpy(rng.uniform(0.5, 1.5, in_f).astype(np.float16)).to(dev)
+        sb = torch.from_numpy(rng.uniform(0.5, 1.5, in_f).astype(np.float16)).to(dev)
+    return x, sv_a, sv_b, sa, sb
+
+
+ROUTE_BB_CASES = [
+    # tokens, experts, top_k, renormalize, in_features, rank, input scales
+    (1, 8, 2, True, 4096, 512, False),     # Mixtral decode: one-wavefront router, 16 slices
+    (16, 8, 2, True, 4096, 512, True),     # with ns_mode 1 input scales
+    (16, 64, 8, False, 2048, 256, False),  # workgroup router, one expert a lane
+    (20, 60, 4, True, 1024, 128, False),   # two token tiles per backbone workgroup
+    (40, 256, 8, True, 520, 64, True),     # three token tiles, four experts a lane
+    (64, 128, 8, True, 4096, 512, False),  # four token tiles: the merged launch's token limit
+    (7, 16, 3, True, 100, 64, False),      # columns not a multiple of 8 (element loads)
+    (5, 8, 2, True, 128, 128, False),      # one slice: the outputs are written in the launch itself
+]
+
+
+@pytest.mark.parametrize("case", ROUTE_BB_CASES, ids=lambda c: "T{}E{}k{}in{}r{}".format(c[0], c[1], c[2], c[4], c[5]))
+def test_route_topk_backbone_matches_separate_launches(tris, cuda, case):
+    t, e, k, renorm, in_f, rank, scales = case
+    note(f"route+backbone T={t} E={e} k={k} in={in_f} rank={rank}")
+    ext = tris["ext"]
+    rng = np.random.default_rng(t * 7 + e)
+    logits = torch.from_numpy(rng.standard_normal((t, e)).astype(np.float32)).to(cuda)
+    x, sv_a, sv_b, sa, sb = backbone_inputs(t + in_f, t, in_f, rank, scales, cuda)
+    want_route = ext.route_topk_grouped(logits, k, renorm, 4)
+    want_a, want_b = ext.backbone_linear_pair(x, sv_a, sv_b, in_scale_a=sa, in_scale_b=sb)
+    assert ext.route_topk_backbone_ok(x, sv_a, sv_b, sa, sb)
+    route, pending = ext.route_topk_backbone_pair(logits, k, renorm, 4, x, sv_a, sv_b, in_scale_a=sa, in_scale_b=sb)
+    got_a, got_b = ext.finish_backbone(pending)
+    for key in ROUTE_KEYS:
+        assert torch.equal(route[key], want_route[key]), key
+    assert torch.equal(got_a, want_a) and torch.equal(got_b, want_b)
+
+
+def test_route_topk_backbone_rejects_what_it_cannot_run(tris, cuda):
+    note("route+backbone limits")
+    ext = tris["ext"]
+    x, sv_a, sv_b, _, _ = backbone_inputs(3, 65, 256, 64, False, cuda)
+    assert not ext.route_topk_backbone_ok(x, sv_a, sv_b)  # more tokens than the merged launch takes
+    logits = torch.zeros((65, 8), dtype=torch.float32, device=cuda)
+    with pytest.raises(RuntimeError):
+        ext.route_topk_backbone_pair(logits, 2, True, 4, x, sv_a, sv_b)
+    x2, sa2, sb2, _, _ = backbone_inputs(4, 4, 256, 64, False, cuda)
+    assert not ext.route_topk_backbone_ok(x2, sa2, sb2[:, :128])  # shapes differ
+
+
+@pytest.mark.parametrize("tokens", [1, 16])
+def test_predecode_with_backbone_reduction(tris, oracle_mod, cuda, tokens):
+    """The predecode launch that also reduces a deferred backbone: the decoded bitmaps are the plain
+    predecode's and the backbone outputs tris_backbone_linear_pair's."""
+    note(f"predecode + backbone reduction T={tokens}")
+    ext = tris["ext"]
+    E, n, k = 4, 320, 256
+    payloads = [make_projection(tris, 71 + i, E, n, k) for i in range(2)]
+    dev_p = [tris["qlinear"].payload_to_device(p, cuda) for p in payloads]
+    eid = t_i32(np.asarray([2, 0, -1], dtype=np.int32), cuda)  # a padded (inactive) slot
+    nblk = tris["synthetic"].packing.num_gr_blocks(k, n)
+
+    def jobs():
+        out = []
+        for d in dev_p:
+            buf = torch.full((3, nblk, 128), -7, dtype=torch.int32, device=cuda)
+            out.append((buf, d["q_gmap_gr_words"], d["q_gmap_gr_offsets"], d["q_gmap_gr_meta"], k // 32, n))
+        return out
+
+    want_dec = ext.grouped_block_gr_predecode_multi(jobs(), eid)
+    rng = np.random.default_rng(tokens)
+    logits = torch.from_numpy(rng.standard_normal((tokens, 8)).astype(np.float32)).to(cuda)
+    x, sv_a, sv_b, sa, sb = backbone_inputs(tokens, tokens, 4096, 512, True, cuda)
+    want_a, want_b = ext.backbone_linear_pair(x, sv_a, sv_b, in_scale_a=sa, in_scale_b=sb)
+    _, pending = ext.route_topk_backbone_pair(logits, 2, True, 4, x, sv_a, sv_b, in_scale_a=sa, in_scale_b=sb)
+    got_dec = ext.grouped_block_gr_predecode_multi(jobs(), eid, backbone=pending)
+    for g, w in zip(got_dec, want_dec):
+        assert torch.equal(g[:2], w[:2])
+    assert torch.equal(pending.out_a, want_a) and torch.equal(pending.out_b, want_b)
+    # the decoded bitmaps are the oracle's
+    p0 = payloads[0]
+    want0 = oracle_mod.gr_predecode(p0["q_gmap_gr_words"], p0["q_gmap_gr_offsets"], p0["q_gmap_gr_meta"],
+                                    np.asarray([2, 0], dtype=np.int32), nblk)
+    np.testing.assert_array_equal(got_dec[0][:2].cpu().numpy(), want0)
+
+
+def gathered_inputs(rng, tokens, rows, k, dev):
+    ha = (rng.standard_normal((tokens, k)) * 1.5).astype(np.float16)
+    hb = (rng.standard_normal((tokens, k)) * 1.5).astype(np.float16)
+    ridx = rng.integers(0, tokens, rows).astype(np.int64)
+    ridx[min(3, rows - 1)] = -1      # indices outside [0, tokens) read zero rows
+    ridx[rows // 2] = tokens
+    valid = (ridx >= 0) & (ridx < tokens)
+    ga = np.where(valid[:, None], ha[np.clip(ridx, 0, tokens - 1)], np.float16(0))
+    gb = np.where(valid[:, None], hb[np.clip(ridx, 0, tokens - 1)], np.float16(0))
+    to = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    return to(ha), to(hb), to(ridx), to(ga), to(gb), ga, gb
+
+
+@pytest.mark.parametrize("lengths", [[2, 37, 0, 5], [300, 0, 200, 90]], ids=["decode", "prefill-ws"])
+def test_gathered_predecoded_gemms_match_materialised_rows(tris, oracle_mod, cuda, lengths):
+    """Grouped row r reads hidden[row_index[r]]: the dual and SwiGLU outputs equal the calls on the
+    materialised rows bit for bit (on the decode kernel, and on the weight-stationary kernel for long
+    segments), and the oracle's within tolerance."""
+    note(f"gathered dual/swiglu segments={lengths}")
+    ext = tris["ext"]
+    E, n, k = 4, 320, 256
+    pa, pb = make_projection(tris, 81, E, n, k), make_projection(tris, 82, E, n, k)
+    da, db = (tris["qlinear"].payload_to_device(p, cuda) for p in (pa, pb))
+    ids = np.asarray([e for e in range(E) if lengths[e] > 0], dtype=np.int32)
+    offs = np.concatenate([[0], np.cumsum([lengths[e] for e in ids])]).astype(np.int32)
+    prob = np.concatenate([[0], np.cumsum((np.diff(offs) + 3) // 4)]).astype(np.int32)
+    rows = int(offs[-1])
+    rng = np.random.default_rng(rows)
+    ha, hb, ridx, ga, gb, ga_np, gb_np = gathered_inputs(rng, max(8, rows // 3), rows, k, cuda)
+    args = (t_i32(ids, cuda), t_i32(offs, cuda), t_i32(prob, cuda), torch.tensor([int(prob[-1])]))
+    nblk = tris["synthetic"].packing.num_gr_blocks(k, n)
+    dec = []
+    for d in (da, db):
+        buf = torch.empty((ids.size, nblk, 128), dtype=torch.int32, device=cuda)
+        dec.append(ext.compact3_tris_precomputed_grouped_block_gr_predecode(
+            buf, t_i32(ids, cuda), d["q_gmap_gr_words"], d["q_gmap_gr_offsets"], d["q_gmap_gr_meta"], k // 32, n))
+    pa_args = [da[x] for x in NAMES]
+    pb_args = [db[x] for x in NAMES]
+    want = ext.compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
+        ga, gb, *args, dec[0], *pa_args, dec[1], *pb_args, True)
+    got = ext.compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
+        ha, hb, *args, dec[0], *pa_args, dec[1], *pb_args, True, row_index=ridx)
+    assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+    assert_close(got[0].cpu().numpy(), oracle_mod.grouped_forward(pa, ga_np, ids, offs, True), "gathered gate")
+    sw_want = ext.compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded(
+        ga, gb, *args, dec[0], *pa_args, dec[1], *pb_args)
+    sw_got = ext.compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded(
+        ha, hb, *args, dec[0], *pa_args, dec[1], *pb_args, row_index=ridx)
+    assert torch.equal(sw_got, sw_want)
+
+
+@pytest.mark.parametrize("tokens", [1, 16, 64])
+def test_layer_with_router_backbone_launch_matches_oracle(tris, oracle_mod, cuda, tokens, monkeypatch):
+    """The Mixtral-shaped layer from router logits takes the merged launches (router + gate/up backbones,
+    predecode + backbone reduction, gathered GEMMs) up to 64 tokens: its output is the oracle's within the
+    layer tolerance."""
+    from tris_moe_amd.configs import C1_MIXTRAL_DECODE as spec
+
+    note(f"layer router+backbone T={tokens}")
+    ext, moe, syn, ql = tris["ext"], tris["moe"], tris["synthetic"], tris["qlinear"]
+    calls = []
+    merged = ext.route_topk_backbone_pair
+
+    def counting(*a, **kw):
+        calls.append(1)
+        return merged(*a, **kw)
+
+    monkeypatch.setattr(ext, "route_topk_backbone_pair", counting)
+    layer = syn.make_layer(spec, 5000 + tokens, ext.gr_encode)
+    payloads = {p: ql.payload_to_device(layer[p], cuda) for p in ("gate", "up", "down")}
+    backbones = {p: torch.from_numpy(layer["backbones"][p]).to(cuda) for p in ("gate", "up", "down")}
+    caches = {"gate": {}, "up": {}, "down": {}}
+    outs, wants = [], []
+    for i in range(4 if tokens == 1 else 1):
+        inp = syn.make_inputs(spec, tokens, 5001 + tokens + i, layer["outlier_idx"])
+        x16 = torch.from_numpy(inp["x"].astype(np.float16)).to(cuda)
+        logits = torch.from_numpy(inp["router_logits"]).to(cuda)
+        out = moe.grouped_moe_forward_from_logits(x16, logits, spec.top_k, spec.renormalize, payloads, backbones,
+                                                  spec.num_experts, torch.bfloat16)
+        w, sel = oracle_mod.route_topk(inp["router_logits"], spec.top_k, spec.renormalize)
+        want = oracle_mod.moe_layer(inp["x"].astype(np.float16), w, sel, {p: layer[p] for p in ("gate", "up", "down")},
+                                    layer["backbones"], spec.num_experts, None, weight_caches=caches)
+        outs.append(out.float().cpu().numpy())
+        wants.append(oracle_mod.bf16_round(want))
+    assert calls, "the layer did not take the router + backbone launch"
+    assert_close(np.concatenate(outs), np.concatenate(wants), f"layer T={tokens}")
