@@ -208,8 +208,8 @@ constexpr int kMfRuns = kMfRows * (kMfChunk / 8) / kMfThreads;  // activation ru
 // arrays (double buffering): the copies of the next tile into one overlap the compute from the other,
 // and being distinct objects lets the compiler see that the compute's LDS reads do not wait for them.
 struct MfUnitLayout {
-  int xs, cds, cns, col_sal, sal_col, meta;  // chunk
-  int r01t, ws, bytes;
+  int xs, cds, cns, col_sal, sal_col, sal_cp, meta;  // chunk
+  int r01t, bytes;
 };
 
 __host__ __device__ inline int mf_take(int* o, int b) {
@@ -226,10 +226,10 @@ __host__ __device__ inline MfUnitLayout mf_unit_layout(int rows, int groups) {
   L.cns = mf_take(&o, kMfChunk * 2);
   L.col_sal = mf_take(&o, kMfChunk * 4);
   L.sal_col = mf_take(&o, kMfChunk * 2);
+  L.sal_cp = mf_take(&o, kMfChunk * 4);
   L.meta = mf_take(&o, 16 * 4);
   (void)groups;
   L.r01t = mf_take(&o, kMfTiles * kTileOut * 4);
-  L.ws = mf_take(&o, kMfWaves * 16 * kMfSalStride * 2);
   L.bytes = o;
   return L;
 }
@@ -248,6 +248,7 @@ struct MfChunk {       // a unit's staged chunk
   uint16_t* cns;       // C_nd, staged column order (0 for salient columns)
   uint32_t* col_sal;   // C0 | C1 << 16, natural order
   uint16_t* sal_col;   // chunk column of the chunk's q-th salient column
+  uint32_t* sal_cp;    // C0 | C1 << 16 of the chunk's q-th salient column
   int32_t* meta;       // [t < 8] group of K tile t (-1: none); [8] first salient index; [9] end
 };
 struct MfTileBuf {     // one output tile's weight words
@@ -407,7 +408,11 @@ __device__ __forceinline__ void mf_chunk_write(const MfmaProj& pa, int rc, int k
     ch.cds[pj] = sal ? static_cast<uint16_t>(0) : static_cast<uint16_t>(R.cpv[h] >> 32);
     ch.cns[pj] = sal ? static_cast<uint16_t>(0) : static_cast<uint16_t>(R.cpv[h] >> 48);
     ch.col_sal[j] = static_cast<uint32_t>(R.cpv[h]);
-    if (sal) ch.sal_col[R.q2t[h] - R.sbase0 + __popc(cm & ((1u << bit) - 1u))] = static_cast<uint16_t>(j);
+    if (sal) {
+      const int q = R.q2t[h] - R.sbase0 + __popc(cm & ((1u << bit) - 1u));
+      ch.sal_col[q] = static_cast<uint16_t>(j);
+      ch.sal_cp[q] = static_cast<uint32_t>(R.cpv[h]);
+    }
   }
   if (utid >= 64 && utid < 72) {
     const bool tv = kc + (utid - 64) * kTileK < rank && R.mv >= 0 && R.mv < G;
@@ -544,6 +549,46 @@ __device__ __forceinline__ void mf_salient_weights(const MfChunk& ch, const MfTi
   for (int u = 0; u < kMfSalWin / 4; ++u) ws[wave][i16][4 * u + kg] = wv[u];
 }
 
+// Both MFMA operands of salient window [w0, w0 + wn) of the chunk, built in registers: lane (i16, kg) takes
+// window slots 8 kg .. 8 kg + 7 (zero past wn); bv holds the exact fp16 weights of its column tc,
+// w = fp16(+-fp16(C0 * R0) +- fp16(C1 * R1)) (both products in one packed multiply), and av its activation
+// row xr at those slots' columns.  Slot data (columns and C0 | C1) are read 8 at a time in slot order; only
+// the qweight1 sign word and the row scales depend on the column.  q2w: the lane's qweight2_sparse words of
+// rows q2b and q2b + 1 (a window spans at most two).
+__device__ __forceinline__ void mf_salient_operands(const MfChunk& ch, const MfTileBuf& tb, const uint32_t* r01t,
+                                                    const uint16_t* xr, int tc, int kg, int sbase0, int w0, int wn,
+                                                    int q2b, const uint32_t q2w[2], f16x8& av, f16x8& bv) {
+  const int s0 = w0 + 8 * kg;  // a multiple of 8: the slot vectors are 16-byte aligned
+  const uint4 cv = *reinterpret_cast<const uint4*>(&ch.sal_col[s0]);
+  const uint32_t cw[4] = {cv.x, cv.y, cv.z, cv.w};
+  uint32_t wb[4] = {0u, 0u, 0u, 0u}, ab[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {  // four slots at a time: fewer registers live
+    const uint4 cpv = *reinterpret_cast<const uint4*>(&ch.sal_cp[s0 + 4 * half]);
+    const uint32_t cps[4] = {cpv.x, cpv.y, cpv.z, cpv.w};
+#pragma unroll
+    for (int uu = 0; uu < 4; ++uu) {
+      const int u = 4 * half + uu;
+      const bool v = 8 * kg + u < wn;
+      const int c = v ? static_cast<int>((cw[u / 2] >> (16 * (u & 1))) & 0xFFFFu) : 0;  // chunk column
+      const uint32_t w1 = tb.q1[(c >> 5) * kMfQ1Stride + tc];
+      const uint32_t rr = r01t[(c >> 6) * kTileOut + tc];
+      const int sidx = sbase0 + s0 + u;  // qweight2_sparse index
+      const uint32_t q2 = ((sidx >> 5) - q2b) == 0 ? q2w[0] : q2w[1];
+      // sign bits: positive where the qweight1 / qweight2 bit is set
+      const uint32_t neg = ((~(w1 >> (c & 31)) & 1u) << 15) | ((~(q2 >> (sidx & 31)) & 1u) << 31);
+      const f16x2 t = __builtin_bit_cast(f16x2, f16x2_as_u32(u32_as_f16x2(cps[uu]) * u32_as_f16x2(rr)) ^ neg);
+      const _Float16 w = t[0] + t[1];
+      const uint32_t wbits = v ? static_cast<uint32_t>(__builtin_bit_cast(uint16_t, w)) : 0u;
+      const uint32_t abits = v ? static_cast<uint32_t>(xr[(c & ~31) + mf_perm32(c & 31)]) : 0u;
+      wb[u / 2] |= wbits << (16 * (u & 1));
+      ab[u / 2] |= abits << (16 * (u & 1));
+    }
+  }
+  av = __builtin_bit_cast(f16x8, make_uint4(ab[0], ab[1], ab[2], ab[3]));
+  bv = __builtin_bit_cast(f16x8, make_uint4(wb[0], wb[1], wb[2], wb[3]));
+}
+
 // The lane's qweight2_sparse words of the chunk's first salient window (a window of kMfSalWin salient
 // columns spans at most two qweight2_sparse rows), for output column n.  Issued before the next tile's
 // LDS copies so that waiting for them does not wait for the copies.
@@ -566,7 +611,7 @@ __device__ __forceinline__ void mf_q2_issue(const MfmaProj& pa, int e, int n, co
 
 __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, int n0, int xrow, int utid,
                                             const MfChunk& ch, const MfTileBuf& tb, uint32_t* r01t,
-                                            uint16_t (*ws)[16][kMfSalStride], const uint32_t q2w0[2], f32x4 acc) {
+                                            const uint32_t q2w0[2], f32x4 acc) {
   const tris_compact3_payload& p = pa.p;
   const int N = p.outfeatures;
   const int rank = p.rank;
@@ -598,8 +643,8 @@ __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, i
   // j + 1 are issued before row j is computed.
   const uint32_t rot = static_cast<uint32_t>(kg - 1) & 31u;  // rotate right: bit kg + 4m -> 4m + 1
   const uint32_t shl = static_cast<uint32_t>(3 - kg);        // shift left:   bit kg + 4m -> 4m + 3
-  // row scales of each K tile's group for this column: R_d | R_nd << 16, and R0 | R1 << 16 into the
-  // wave's salient table (only this wave reads its columns' entries)
+  // row scales of each K tile's group for this column: R_d | R_nd << 16, and R0 | R1 << 16 into r01t
+  // (only this wave reads its columns' entries)
   uint32_t rdn[kMfTiles];
 #pragma unroll
   for (int t = 0; t < kMfTiles; ++t) {
@@ -644,11 +689,7 @@ __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, i
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();  // r01t written
 
-  // ---- salient columns, kMfSalWin at a time.  Lane group kg writes the exact fp16 weights of its
-  // column for window slots kg, kg + 4, ... into ws (every slot, zero past the window's end, with no
-  // per-slot branch so the LDS reads overlap): w = fp16(+-fp16(C0 * R0) +- fp16(C1 * R1)), both
-  // products in one packed multiply.  Then the wave multiplies the activations gathered at those
-  // columns by ws on MFMA.
+  // ---- salient columns, kMfSalWin at a time: both operands in registers (mf_salient_operands), one MFMA
   for (int w0 = 0; w0 < num_sal; w0 += kMfSalWin) {
     const int wn = (num_sal - w0) < kMfSalWin ? (num_sal - w0) : kMfSalWin;
     const int q2b = (sbase0 + w0) >> 5;  // qweight2_sparse row of the window's first salient column
@@ -659,29 +700,9 @@ __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, i
         q2w[h] = bload32(r_q2, rv ? v_q2 : q2_bytes, static_cast<uint32_t>(rv ? q2b + h : 0) * N * 4u);
       }
     }
-    mf_salient_weights(ch, tb, r01t, tc, kg, wave, i16, sbase0, w0, wn, q2b, q2w, ws);
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    uint32_t ap[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int q0 = 8 * kg + 2 * i;
-      uint32_t lo = 0u, hi = 0u;
-      if (q0 < wn) {
-        const int c = ch.sal_col[w0 + q0];
-        lo = xr[(c & ~31) + mf_perm32(c & 31)];
-      }
-      if (q0 + 1 < wn) {
-        const int c = ch.sal_col[w0 + q0 + 1];
-        hi = xr[(c & ~31) + mf_perm32(c & 31)];
-      }
-      ap[i] = lo | (hi << 16);
-    }
-    const f16x8 av = __builtin_bit_cast(f16x8, make_uint4(ap[0], ap[1], ap[2], ap[3]));
-    const f16x8 bv = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&ws[wave][i16][8 * kg]));
+    f16x8 av, bv;
+    mf_salient_operands(ch, tb, r01t, xr, tc, kg, sbase0, w0, wn, q2b, q2w, av, bv);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
   }
   return acc;
 }
@@ -753,8 +774,8 @@ void grouped_mfma_kernel(MfmaArgs a) {
   tb1.q1 = &mf_tb1[unit][kMfTbQ1];
   tb1.gw = &mf_tb1[unit][kMfTbGw];
   tb1.rs = &mf_tb1[unit][kMfTbRs];
+  ch.sal_cp = reinterpret_cast<uint32_t*>(base + L.sal_cp);
   uint32_t* r01t = reinterpret_cast<uint32_t*>(base + L.r01t);
-  auto ws = reinterpret_cast<uint16_t (*)[16][kMfSalStride]>(base + L.ws);
   float* exch = reinterpret_cast<float*>(mf_lds + kUnits * L.bytes);
   // A operand row of this lane: rows >= rc hold stale values and only feed output rows that are not stored
   const int i16 = lane % 16;
@@ -811,7 +832,7 @@ void grouped_mfma_kernel(MfmaArgs a) {
         __syncthreads();
         mf_q2_issue(pa, e, n, ch, q2w);
       }
-      acc = mf_compute(pa, e, kc, ob * kTileOut, xrow, utid, ch, cur, r01t, ws, q2w, acc);
+      acc = mf_compute(pa, e, kc, ob * kTileOut, xrow, utid, ch, cur, r01t, q2w, acc);
     }
 
     const bool nv = n < N;
@@ -882,7 +903,7 @@ constexpr int kWsXDepth = TRIS_WS_XDEPTH;  // row tiles of activations in flight
 static_assert(kWsXDepth == 1 || kWsXDepth == 2, "activation prefetch depth is 1 or 2");
 
 struct MfWsLayout {  // per unit, byte offsets into dynamic LDS
-  int xs[2], cds, cns, col_sal, sal_col, meta, r01t, ws, bytes;
+  int xs[2], cds, cns, col_sal, sal_col, sal_cp, meta, r01t, ws, bytes;
 };
 
 __host__ __device__ inline MfWsLayout mf_ws_layout() {
@@ -894,6 +915,7 @@ __host__ __device__ inline MfWsLayout mf_ws_layout() {
   L.cns = mf_take(&o, kMfChunk * 2);
   L.col_sal = mf_take(&o, kMfChunk * 4);
   L.sal_col = mf_take(&o, kMfChunk * 2);
+  L.sal_cp = mf_take(&o, kMfChunk * 4);
   L.meta = mf_take(&o, 16 * 4);
   L.r01t = mf_take(&o, kMfTiles * kTileOut * 4);
   L.ws = mf_take(&o, kMfWaves * 16 * kMfSalStride * 2);
@@ -1009,6 +1031,7 @@ __global__ __launch_bounds__(kUnits * kMfThreads) void grouped_mfma_ws_kernel(Mf
   ch.cns = reinterpret_cast<uint16_t*>(lbase + L.cns);
   ch.col_sal = reinterpret_cast<uint32_t*>(lbase + L.col_sal);
   ch.sal_col = reinterpret_cast<uint16_t*>(lbase + L.sal_col);
+  ch.sal_cp = reinterpret_cast<uint32_t*>(lbase + L.sal_cp);
   ch.meta = reinterpret_cast<int32_t*>(lbase + L.meta);
   uint16_t* const xsb0 = reinterpret_cast<uint16_t*>(lbase + L.xs[0]);
   uint16_t* const xsb1 = reinterpret_cast<uint16_t*>(lbase + L.xs[1]);
