@@ -208,7 +208,7 @@ constexpr int kMfRuns = kMfRows * (kMfChunk / 8) / kMfThreads;  // activation ru
 // arrays (double buffering): the copies of the next tile into one overlap the compute from the other,
 // and being distinct objects lets the compiler see that the compute's LDS reads do not wait for them.
 struct MfUnitLayout {
-  int xs, cds, cns, col_sal, sal_col, sal_cp, meta;  // chunk
+  int xs, cds, cns, col_sal, sal_col, sal_xi, sal_cp, meta;  // chunk
   int r01t, bytes;
 };
 
@@ -226,6 +226,7 @@ __host__ __device__ inline MfUnitLayout mf_unit_layout(int rows, int groups) {
   L.cns = mf_take(&o, kMfChunk * 2);
   L.col_sal = mf_take(&o, kMfChunk * 4);
   L.sal_col = mf_take(&o, kMfChunk * 2);
+  L.sal_xi = mf_take(&o, kMfChunk * 2);
   L.sal_cp = mf_take(&o, kMfChunk * 4);
   L.meta = mf_take(&o, 16 * 4);
   (void)groups;
@@ -248,7 +249,8 @@ struct MfChunk {       // a unit's staged chunk
   uint16_t* cns;       // C_nd, staged column order (0 for salient columns)
   uint32_t* col_sal;   // C0 | C1 << 16, natural order
   uint16_t* sal_col;   // chunk column of the chunk's q-th salient column
-  uint32_t* sal_cp;    // C0 | C1 << 16 of the chunk's q-th salient column
+  uint16_t* sal_xi;    // its position in the staged (permuted) column order
+  uint32_t* sal_cp;    // its C0 | C1 << 16
   int32_t* meta;       // [t < 8] group of K tile t (-1: none); [8] first salient index; [9] end
 };
 struct MfTileBuf {     // one output tile's weight words
@@ -411,6 +413,7 @@ __device__ __forceinline__ void mf_chunk_write(const MfmaProj& pa, int rc, int k
     if (sal) {
       const int q = R.q2t[h] - R.sbase0 + __popc(cm & ((1u << bit) - 1u));
       ch.sal_col[q] = static_cast<uint16_t>(j);
+      ch.sal_xi[q] = static_cast<uint16_t>((j & ~31) + mf_perm32(j & 31));
       ch.sal_cp[q] = static_cast<uint32_t>(R.cpv[h]);
     }
   }
@@ -552,37 +555,51 @@ __device__ __forceinline__ void mf_salient_weights(const MfChunk& ch, const MfTi
 // Both MFMA operands of salient window [w0, w0 + wn) of the chunk, built in registers: lane (i16, kg) takes
 // window slots 8 kg .. 8 kg + 7 (zero past wn); bv holds the exact fp16 weights of its column tc,
 // w = fp16(+-fp16(C0 * R0) +- fp16(C1 * R1)) (both products in one packed multiply), and av its activation
-// row xr at those slots' columns.  Slot data (columns and C0 | C1) are read 8 at a time in slot order; only
-// the qweight1 sign word and the row scales depend on the column.  q2w: the lane's qweight2_sparse words of
-// rows q2b and q2b + 1 (a window spans at most two).
+// row xr at those slots' columns.  Slot data (columns, staged positions and C0 | C1) are read 8 at a time in
+// slot order; only the qweight1 sign word, the row scales and the activation depend on the column.  q2w: the
+// lane's qweight2_sparse words of rows q2b = (sbase0 + w0) / 32 and q2b + 1 (a window spans at most two).
 __device__ __forceinline__ void mf_salient_operands(const MfChunk& ch, const MfTileBuf& tb, const uint32_t* r01t,
                                                     const uint16_t* xr, int tc, int kg, int sbase0, int w0, int wn,
                                                     int q2b, const uint32_t q2w[2], f16x8& av, f16x8& bv) {
   const int s0 = w0 + 8 * kg;  // a multiple of 8: the slot vectors are 16-byte aligned
   const uint4 cv = *reinterpret_cast<const uint4*>(&ch.sal_col[s0]);
+  const uint4 xv = *reinterpret_cast<const uint4*>(&ch.sal_xi[s0]);
   const uint32_t cw[4] = {cv.x, cv.y, cv.z, cv.w};
+  const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+  // Every slot reads its operands (slots past wn at column 0, in range) and is masked after; all 24
+  // column-dependent reads are issued before any is used, so their latencies overlap.
+  int col[8];
+  uint32_t w1v[8], rrv[8], av8[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const uint32_t keep = 8 * kg + u < wn ? 0xFFFFu : 0u;
+    const uint32_t sh = 16u * static_cast<uint32_t>(u & 1);
+    col[u] = static_cast<int>((cw[u / 2] >> sh) & keep);  // chunk column (0 past wn)
+    const int xi = static_cast<int>((xw[u / 2] >> sh) & keep);
+    w1v[u] = tb.q1[(col[u] >> 5) * kMfQ1Stride + tc];
+    rrv[u] = r01t[(col[u] >> 6) * kTileOut + tc];
+    av8[u] = xr[xi];
+  }
+  // qweight2_sparse sign bits of the 8 slots: bit u of q2bits (the slots' indices span at most two words)
+  const int off = ((sbase0 + w0) & 31) + 8 * kg;  // slot 0's bit within q2w[0] | q2w[1] << 32, <= 55
+  const uint64_t q2bits = ((static_cast<uint64_t>(q2w[1]) << 32) | q2w[0]) >> off;
   uint32_t wb[4] = {0u, 0u, 0u, 0u}, ab[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {  // four slots at a time: fewer registers live
+  for (int half = 0; half < 2; ++half) {
     const uint4 cpv = *reinterpret_cast<const uint4*>(&ch.sal_cp[s0 + 4 * half]);
     const uint32_t cps[4] = {cpv.x, cpv.y, cpv.z, cpv.w};
 #pragma unroll
     for (int uu = 0; uu < 4; ++uu) {
       const int u = 4 * half + uu;
-      const bool v = 8 * kg + u < wn;
-      const int c = v ? static_cast<int>((cw[u / 2] >> (16 * (u & 1))) & 0xFFFFu) : 0;  // chunk column
-      const uint32_t w1 = tb.q1[(c >> 5) * kMfQ1Stride + tc];
-      const uint32_t rr = r01t[(c >> 6) * kTileOut + tc];
-      const int sidx = sbase0 + s0 + u;  // qweight2_sparse index
-      const uint32_t q2 = ((sidx >> 5) - q2b) == 0 ? q2w[0] : q2w[1];
+      const uint32_t keep = 8 * kg + u < wn ? 0xFFFFu : 0u;
+      const uint32_t sh = 16u * static_cast<uint32_t>(u & 1);
       // sign bits: positive where the qweight1 / qweight2 bit is set
-      const uint32_t neg = ((~(w1 >> (c & 31)) & 1u) << 15) | ((~(q2 >> (sidx & 31)) & 1u) << 31);
-      const f16x2 t = __builtin_bit_cast(f16x2, f16x2_as_u32(u32_as_f16x2(cps[uu]) * u32_as_f16x2(rr)) ^ neg);
+      const uint32_t neg = ((~(w1v[u] >> (col[u] & 31)) & 1u) << 15) |
+                           ((~static_cast<uint32_t>(q2bits >> u) & 1u) << 31);
+      const f16x2 t = __builtin_bit_cast(f16x2, f16x2_as_u32(u32_as_f16x2(cps[uu]) * u32_as_f16x2(rrv[u])) ^ neg);
       const _Float16 w = t[0] + t[1];
-      const uint32_t wbits = v ? static_cast<uint32_t>(__builtin_bit_cast(uint16_t, w)) : 0u;
-      const uint32_t abits = v ? static_cast<uint32_t>(xr[(c & ~31) + mf_perm32(c & 31)]) : 0u;
-      wb[u / 2] |= wbits << (16 * (u & 1));
-      ab[u / 2] |= abits << (16 * (u & 1));
+      wb[u / 2] |= (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, w)) & keep) << sh;
+      ab[u / 2] |= (av8[u] & keep) << sh;
     }
   }
   av = __builtin_bit_cast(f16x8, make_uint4(ab[0], ab[1], ab[2], ab[3]));
@@ -774,6 +791,7 @@ void grouped_mfma_kernel(MfmaArgs a) {
   tb1.q1 = &mf_tb1[unit][kMfTbQ1];
   tb1.gw = &mf_tb1[unit][kMfTbGw];
   tb1.rs = &mf_tb1[unit][kMfTbRs];
+  ch.sal_xi = reinterpret_cast<uint16_t*>(base + L.sal_xi);
   ch.sal_cp = reinterpret_cast<uint32_t*>(base + L.sal_cp);
   uint32_t* r01t = reinterpret_cast<uint32_t*>(base + L.r01t);
   float* exch = reinterpret_cast<float*>(mf_lds + kUnits * L.bytes);
@@ -903,7 +921,7 @@ constexpr int kWsXDepth = TRIS_WS_XDEPTH;  // row tiles of activations in flight
 static_assert(kWsXDepth == 1 || kWsXDepth == 2, "activation prefetch depth is 1 or 2");
 
 struct MfWsLayout {  // per unit, byte offsets into dynamic LDS
-  int xs[2], cds, cns, col_sal, sal_col, sal_cp, meta, r01t, ws, bytes;
+  int xs[2], cds, cns, col_sal, sal_col, sal_xi, sal_cp, meta, r01t, ws, bytes;
 };
 
 __host__ __device__ inline MfWsLayout mf_ws_layout() {
@@ -915,6 +933,7 @@ __host__ __device__ inline MfWsLayout mf_ws_layout() {
   L.cns = mf_take(&o, kMfChunk * 2);
   L.col_sal = mf_take(&o, kMfChunk * 4);
   L.sal_col = mf_take(&o, kMfChunk * 2);
+  L.sal_xi = mf_take(&o, kMfChunk * 2);
   L.sal_cp = mf_take(&o, kMfChunk * 4);
   L.meta = mf_take(&o, 16 * 4);
   L.r01t = mf_take(&o, kMfTiles * kTileOut * 4);
@@ -1031,6 +1050,7 @@ __global__ __launch_bounds__(kUnits * kMfThreads) void grouped_mfma_ws_kernel(Mf
   ch.cns = reinterpret_cast<uint16_t*>(lbase + L.cns);
   ch.col_sal = reinterpret_cast<uint32_t*>(lbase + L.col_sal);
   ch.sal_col = reinterpret_cast<uint16_t*>(lbase + L.sal_col);
+  ch.sal_xi = reinterpret_cast<uint16_t*>(lbase + L.sal_xi);
   ch.sal_cp = reinterpret_cast<uint32_t*>(lbase + L.sal_cp);
   ch.meta = reinterpret_cast<int32_t*>(lbase + L.meta);
   uint16_t* const xsb0 = reinterpret_cast<uint16_t*>(lbase + L.xs[0]);
