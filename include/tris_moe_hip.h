@@ -400,6 +400,21 @@ int64_t tris_backbone_pair_workspace_bytes(int32_t tokens, int32_t in_features, 
 int64_t tris_backbone_workspace_bytes(int32_t tokens, int32_t in_features, int32_t rank);
 
 /*
+ * The down projection's shared backbone with the SwiGLU product of its input fused (no reference
+ * counterpart: act_fn(gate_out) * up_out of modeling_mixtral.py:496 formed inside compute_shared_hidden's
+ * projection, qlinear_cuda.py:4454-4502, so the product never reaches HBM).  in[r][k] =
+ * fp16(fp16(silu(gate[r][k])) * up[r][k]), the bits tris_swiglu_mul writes, times in_scale[k] (an fp16
+ * product, the ns_mode == 1 input scale) when in_scale is not NULL; out fp16 [rows, rank] = in . sv^T with
+ * fp32 accumulation, split over K and the slices added in fixed order (deterministic).  gate, up fp16
+ * [rows, in_features], sv fp16 [rank, in_features]; rows <= 64, in_features a multiple of 32, 16-byte aligned
+ * pointers (else TRIS_ERR_INVALID); workspace of tris_backbone_swiglu_workspace_bytes(rows, in_features, rank).
+ */
+int tris_backbone_swiglu_linear(const uint16_t* gate, const uint16_t* up, int32_t rows, int32_t in_features,
+                                const uint16_t* sv, int32_t rank, const uint16_t* in_scale, uint16_t* out,
+                                void* workspace, int64_t workspace_bytes, void* stream);
+int64_t tris_backbone_swiglu_workspace_bytes(int32_t rows, int32_t in_features, int32_t rank);
+
+/*
  * 4-bit packed backbone matrix (PackedQuantMatrix4bit buffers, qlinear_cuda.py:2637-2786):
  * SV[r][c] = fp16((q - z) * s) with q = nibble c % 8 (bits 4*(c%8)) of qweight[c / 8][r],
  * z = nibble r % 8 of qzeros[g][r / 8] plus one, s = scales[g][r], g = g_idx[c]

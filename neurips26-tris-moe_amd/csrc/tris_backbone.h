@@ -15,7 +15,8 @@ constexpr int kBbThreads = kBbWaves * kWave;
 constexpr int kBbKStep = 32;
 constexpr int kBbBatch = 8;          // K steps of loads in flight per wavefront
 constexpr int kBbTargetWgs = 512;    // aim for this many workgroups per launch
-constexpr int kBbMaxSlices = 32;
+constexpr int kBbMaxSlices = 32;        // slices of backbone_kernel
+constexpr int kBbReduceMaxSlices = 64;  // slices backbone_reduce_at adds (backbone_swiglu_kernel uses up to 64)
 
 struct BackboneProj {
   const uint16_t* sv;
@@ -172,12 +173,12 @@ __device__ __forceinline__ void backbone_reduce_at(const BackboneArgs& a, int64_
   const int64_t count = static_cast<int64_t>(a.tokens) * a.rank;
   if (idx >= count) return;
   const float* src = a.partials + static_cast<int64_t>(q) * a.slices * count + idx;
-  float v[kBbMaxSlices];
+  float v[kBbReduceMaxSlices];
 #pragma unroll
-  for (int s = 0; s < kBbMaxSlices; ++s) v[s] = s < a.slices ? src[s * count] : 0.0f;  // loads in flight together
+  for (int s = 0; s < kBbReduceMaxSlices; ++s) v[s] = s < a.slices ? src[s * count] : 0.0f;  // loads in flight together
   float sum = 0.0f;
 #pragma unroll
-  for (int s = 0; s < kBbMaxSlices; ++s) {
+  for (int s = 0; s < kBbReduceMaxSlices; ++s) {
     if (s < a.slices) sum += v[s];
   }
   a.proj[q].out[idx] = f2h_bits(sum);

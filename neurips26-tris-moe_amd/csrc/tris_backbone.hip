@@ -158,6 +158,139 @@ int launch_backbone_reduce(const BackboneArgs& args, int nproj, hipStream_t s, c
 }
 
 // ---------------------------------------------------------------------------------------------------------
+// Down-projection backbone with the SwiGLU product fused into its operand staging:
+// in[r][k] = fp16(fp16(silu(g[r][k])) * u[r][k]) (act_fn(gate) * up, modeling_mixtral.py:496, as swiglu_bits),
+// times in_scale[k] as an fp16 product when given, and hidden = in . SV^T.  Workgroup (cg, slice) covers rank
+// columns [128 cg, 128 cg + 128) over one K slice for every row (at most kSgMaxRowTiles 16-row tiles): it
+// forms the slice's product once in LDS (each of the rank's column groups forms it: rank / 128 times in all,
+// not once per 16-column tile), then wavefront w of kSgWaves multiplies it by columns [128 cg + 16 w, + 16)
+// (one MFMA column tile).  A slice is at most kSgSteps K steps, whose SV loads are all issued before the
+// product is formed.  Slices write fp32 partial tiles that backbone_reduce_kernel adds in slice order.
+constexpr int kSgCols = 128;
+constexpr int kSgWaves = kSgCols / 16;
+constexpr int kSgThreads = kSgWaves * kWave;
+constexpr int kSgMaxRowTiles = 4;
+constexpr int kSgSteps = 8;                       // K steps of 32 per slice at most
+constexpr int kSgTargetWgs = 256;
+constexpr int kSgVecIters = 4;                    // product vectors (8 columns) a thread forms per batch
+
+struct SwigluBackboneArgs {
+  const uint16_t* g;         // [rows, in_features]
+  const uint16_t* u;         // [rows, in_features]
+  const uint16_t* sv;        // [rank, in_features]
+  const uint16_t* in_scale;  // [in_features] or null
+  uint16_t* out;             // [rows, rank] (written directly when slices == 1)
+  float* partials;           // [slices][rows][rank]
+  int rows, in_features, rank, slices, slice_k;
+};
+
+template <int TT>
+__global__ __launch_bounds__(kSgThreads) void backbone_swiglu_kernel(SwigluBackboneArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t sg_in[];  // [TT * 16][slice_k + 8]
+  const int cg = blockIdx.x;
+  const int slice = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int i16 = lane % 16;
+  const int kg = lane / 16;
+  const int stride = a.slice_k + 8;
+  const int k0 = slice * a.slice_k;
+  const int kn = (a.in_features - k0) < a.slice_k ? (a.in_features - k0) : a.slice_k;  // a multiple of 32
+  const int steps = kn / 32;
+  // SV operands of the whole slice (the wave's column tile), in flight while the product is formed
+  const int col = cg * kSgCols + 16 * wave + i16;
+  f16x8 bq[kSgSteps];
+  {
+    const bool cv = col < a.rank;
+    const uint16_t* src = a.sv + static_cast<int64_t>(cv ? col : 0) * a.in_features + k0 + 8 * kg;
+#pragma unroll
+    for (int j = 0; j < kSgSteps; ++j) bq[j] = load8_vec(src, 32 * j, cv && j < steps);
+  }
+  // the product of the slice for every row (rows past a.rows are zero), kSgVecIters vectors a thread per batch
+  const int v8 = kn / 8;
+  const int nvec = TT * 16 * v8;
+  for (int v0 = 0; v0 < nvec; v0 += kSgVecIters * kSgThreads) {
+    uint4 gv[kSgVecIters], uv[kSgVecIters], sc[kSgVecIters];
+#pragma unroll
+    for (int i = 0; i < kSgVecIters; ++i) {
+      const int v = v0 + i * kSgThreads + tid;
+      const int r = v / v8;
+      const int c = k0 + (v % v8) * 8;
+      const bool ok = v < nvec && r < a.rows;
+      const int64_t o = static_cast<int64_t>(ok ? r : 0) * a.in_features + (ok ? c : 0);
+      gv[i] = ok ? *reinterpret_cast<const uint4*>(a.g + o) : make_uint4(0u, 0u, 0u, 0u);
+      uv[i] = ok ? *reinterpret_cast<const uint4*>(a.u + o) : make_uint4(0u, 0u, 0u, 0u);
+      sc[i] = (a.in_scale != nullptr && ok) ? *reinterpret_cast<const uint4*>(a.in_scale + c)
+                                            : make_uint4(0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u);
+    }
+#pragma unroll
+    for (int i = 0; i < kSgVecIters; ++i) {
+      const int v = v0 + i * kSgThreads + tid;
+      if (v >= nvec) continue;
+      const int r = v / v8;
+      const int c = (v % v8) * 8;
+      const uint32_t gw[4] = {gv[i].x, gv[i].y, gv[i].z, gv[i].w};
+      const uint32_t uw[4] = {uv[i].x, uv[i].y, uv[i].z, uv[i].w};
+      const uint32_t sw[4] = {sc[i].x, sc[i].y, sc[i].z, sc[i].w};
+      uint32_t pw[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const uint32_t lo = swiglu_bits(static_cast<uint16_t>(gw[h]), static_cast<uint16_t>(uw[h]));
+        const uint32_t hi = swiglu_bits(static_cast<uint16_t>(gw[h] >> 16), static_cast<uint16_t>(uw[h] >> 16));
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        // fp16 products with the input scale (1.0 without one), as the backbone's x * ns_col
+        pw[h] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, lo | (hi << 16)) * __builtin_bit_cast(h2, sw[h]));
+      }
+      *reinterpret_cast<uint4*>(&sg_in[r * stride + c]) = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+    }
+  }
+  __syncthreads();
+  f32x4 acc[TT];
+#pragma unroll
+  for (int rt = 0; rt < TT; ++rt) acc[rt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < kSgSteps; ++j) {
+    if (j < steps) {  // uniform
+#pragma unroll
+      for (int rt = 0; rt < TT; ++rt) {
+        const f16x8 av = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&sg_in[(16 * rt + i16) * stride + 32 * j + 8 * kg]));
+        acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bq[j], acc[rt], 0, 0, 0);
+      }
+    }
+  }
+  // acc[rt][v] = hidden[16 rt + 4 kg + v][128 cg + 16 w + i16]
+  if (col < a.rank) {
+#pragma unroll
+    for (int rt = 0; rt < TT; ++rt) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int r = 16 * rt + 4 * kg + v;
+        if (r >= a.rows) continue;
+        if (a.slices == 1) {
+          a.out[static_cast<int64_t>(r) * a.rank + col] = f2h_bits(acc[rt][v]);
+        } else {
+          a.partials[(static_cast<int64_t>(slice) * a.rows + r) * a.rank + col] = acc[rt][v];
+        }
+      }
+    }
+  }
+}
+
+// Slices of backbone_swiglu_kernel: about kSgTargetWgs workgroups, at most kSgSteps K steps and
+// kBbReduceMaxSlices slices; returns the slice width in columns (a multiple of 32) and sets *slices.
+static int swiglu_backbone_slice_k(int in_features, int rank, int* slices) {
+  const int groups = ceil_div(rank, kSgCols);
+  int s = ceil_div(kSgTargetWgs, groups);
+  s = s < kBbReduceMaxSlices ? s : kBbReduceMaxSlices;
+  const int min_slices = ceil_div(in_features, kSgSteps * 32);
+  s = s > min_slices ? s : min_slices;
+  const int slice_k = ceil_div(ceil_div(in_features, s), 32) * 32;
+  *slices = ceil_div(in_features, slice_k);
+  return slice_k;
+}
+
+// ---------------------------------------------------------------------------------------------------------
 // 4-bit packed backbone (PackedQuantMatrix4bit, qlinear_cuda.py:2637-2786): SV[r][c] =
 // fp16((q[c][r] - z[g][r]) * s[g][r]) with q the nibble c % 8 of qweight[c / 8][r], z = nibble r % 8 of
 // qzeros[g][r / 8] plus one, s = scales[g][r], g = g_idx[c] (the reference's dequantize, :2761-2786).
@@ -507,6 +640,56 @@ extern "C" int tris_backbone_linear_pair(const uint16_t* x, int32_t tokens, int3
   TRIS_REQUIRE(sv_b != nullptr, "tris_backbone_linear_pair: null sv_b");
   return launch_backbone(x, tokens, in_features, row_index, sv_a, sv_b, rank, in_scale_a, in_scale_b, out_a, out_b,
                          workspace, workspace_bytes, stream, "tris_backbone_linear_pair");
+}
+
+extern "C" int64_t tris_backbone_swiglu_workspace_bytes(int32_t rows, int32_t in_features, int32_t rank) {
+  if (rows <= 0 || in_features <= 0 || rank <= 0) return 0;
+  int slices = 1;
+  swiglu_backbone_slice_k(in_features, rank, &slices);
+  return slices > 1 ? static_cast<int64_t>(slices) * rows * rank * 4 : 0;
+}
+
+extern "C" int tris_backbone_swiglu_linear(const uint16_t* gate, const uint16_t* up, int32_t rows, int32_t in_features,
+                                           const uint16_t* sv, int32_t rank, const uint16_t* in_scale, uint16_t* out,
+                                           void* workspace, int64_t workspace_bytes, void* stream) {
+  const char* who = "tris_backbone_swiglu_linear";
+  TRIS_REQUIRE(rows >= 0 && in_features >= 0 && rank >= 0, "%s: negative shape", who);
+  if (rows == 0 || rank == 0) return TRIS_OK;
+  TRIS_REQUIRE(rows <= kSgMaxRowTiles * 16, "%s: %d rows exceed %d", who, rows, kSgMaxRowTiles * 16);
+  TRIS_REQUIRE(in_features > 0 && in_features % 32 == 0, "%s: in_features %d must be a positive multiple of 32", who,
+               in_features);
+  TRIS_REQUIRE(gate && up && sv && out, "%s: null pointer", who);
+  TRIS_REQUIRE(reinterpret_cast<uintptr_t>(gate) % 16 == 0 && reinterpret_cast<uintptr_t>(up) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(sv) % 16 == 0 && reinterpret_cast<uintptr_t>(in_scale) % 16 == 0,
+               "%s: gate, up, sv and in_scale must be 16-byte aligned", who);
+  int slices = 1;
+  const int slice_k = swiglu_backbone_slice_k(in_features, rank, &slices);
+  const int64_t need = tris_backbone_swiglu_workspace_bytes(rows, in_features, rank);
+  TRIS_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+               "%s: workspace of %lld bytes needed, %lld given", who, static_cast<long long>(need),
+               static_cast<long long>(workspace_bytes));
+  SwigluBackboneArgs a{gate, up, sv, in_scale, out, static_cast<float*>(workspace), rows, in_features, rank, slices,
+                       slice_k};
+  const int tt = ceil_div(rows, 16);
+  const size_t lds = static_cast<size_t>(tt) * 16 * (slice_k + 8) * 2;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(ceil_div(rank, kSgCols), slices);
+  switch (tt) {
+    case 1: hipLaunchKernelGGL((backbone_swiglu_kernel<1>), grid, dim3(kSgThreads), lds, s, a); break;
+    case 2: hipLaunchKernelGGL((backbone_swiglu_kernel<2>), grid, dim3(kSgThreads), lds, s, a); break;
+    case 3: hipLaunchKernelGGL((backbone_swiglu_kernel<3>), grid, dim3(kSgThreads), lds, s, a); break;
+    default: hipLaunchKernelGGL((backbone_swiglu_kernel<4>), grid, dim3(kSgThreads), lds, s, a); break;
+  }
+  int rc = check_launch(who);
+  if (rc || slices == 1) return rc;
+  BackboneArgs ra{};
+  ra.proj[0].out = out;
+  ra.partials = static_cast<float*>(workspace);
+  ra.tokens = rows;
+  ra.in_features = in_features;
+  ra.rank = rank;
+  ra.slices = slices;
+  return launch_backbone_reduce(ra, 1, s, who);
 }
 
 extern "C" int tris_packed4_dequant(const tris_packed4_matrix* w, uint16_t* out, void* stream) {

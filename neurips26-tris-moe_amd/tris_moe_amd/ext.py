@@ -845,6 +845,44 @@ def backbone_linear_pair(x: torch.Tensor, sv_a: torch.Tensor, sv_b: torch.Tensor
     return out_a, out_b
 
 
+SWIGLU_BACKBONE_MAX_ROWS = 64  # rows of tris_backbone_swiglu_linear
+
+
+def backbone_swiglu_ok(gate: torch.Tensor, sv, in_scale: torch.Tensor | None = None) -> bool:
+    """True when backbone_swiglu_linear can run: an fp16 SV matrix, at most SWIGLU_BACKBONE_MAX_ROWS rows, a
+    multiple of 32 columns and 16-byte aligned contiguous tensors."""
+    if not isinstance(sv, torch.Tensor) or sv.dtype != torch.float16 or sv.dim() != 2 or not sv.is_contiguous():
+        return False
+    if gate.dim() != 2 or int(gate.size(0)) > SWIGLU_BACKBONE_MAX_ROWS or int(gate.size(1)) % 32 != 0:
+        return False
+    if int(sv.size(1)) != int(gate.size(1)) or sv.data_ptr() % 16 or gate.data_ptr() % 16:
+        return False
+    return in_scale is None or (in_scale.dtype == torch.float16 and in_scale.numel() == gate.size(1)
+                                and in_scale.is_contiguous() and in_scale.data_ptr() % 16 == 0)
+
+
+def backbone_swiglu_linear(gate: torch.Tensor, up: torch.Tensor, sv: torch.Tensor,
+                           in_scale: torch.Tensor | None = None) -> torch.Tensor:
+    """fp16(act_fn(gate) * up [* in_scale]) @ sv^T in one projection with the product formed in its operand
+    staging (tris_backbone_swiglu_linear, an extension): the down backbone of a SwiGLU layer without the
+    intermediate tensor.  The product is swiglu_mul's, bit for bit."""
+    _check_cuda("gate", gate, torch.float16, 2)
+    _check_cuda("up", up, torch.float16, 2, gate.device)
+    _check_cuda("shared_sv", sv, torch.float16, 2, gate.device)
+    if up.shape != gate.shape or int(sv.size(1)) != int(gate.size(1)):
+        raise RuntimeError("backbone_swiglu_linear: shape mismatch")
+    if in_scale is not None:
+        _check_cuda("in_scale", in_scale, torch.float16, 1, gate.device)
+    rows, in_f, rank = int(gate.size(0)), int(gate.size(1)), int(sv.size(0))
+    out = torch.empty((rows, rank), dtype=torch.float16, device=gate.device)
+    lib = _lib.load()
+    ws = backbone_workspace(gate.device, int(lib.tris_backbone_swiglu_workspace_bytes(rows, in_f, rank)))
+    _lib.check(lib.tris_backbone_swiglu_linear(_ptr(gate), _ptr(up), rows, in_f, _ptr(sv), rank, _ptr(in_scale),
+                                               _ptr(out), _ptr(ws), int(ws.numel()), _stream(gate)),
+               "tris_backbone_swiglu_linear")
+    return out
+
+
 # ----------------------------------------------------------------------------------------- 4-bit backbone
 class Packed4Matrix:
     """Device tensors of one 4-bit packed matrix (PackedQuantMatrix4bit buffers, qlinear_cuda.py:2637-2786):

@@ -275,6 +275,7 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     names = ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx", "col_pack3", "row_pack3")
     # every routed row lies in a segment, so the outputs need no zero fill
     mlp = torch.empty((R, n_mlp), dtype=torch.float16, device=dev)
+    hid_d = None
     if R <= FUSED_SWIGLU_MAX_ROWS and comp_g is None and comp_u is None:
         # few rows: the gate/up GEMM with act_fn(g) * u in its epilogue (one launch)
         ext.compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded(
@@ -288,8 +289,13 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
         ext.compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
             hid_g, hid_u, eid, seg, prob, tile_bound, decoded["gate"], *[pg[k] for k in names], decoded["up"],
             *[pu[k] for k in names], True, out_a=g, out_b=u, row_index=gather)
-        # g + comp_g and u + comp_u (fp16 adds) inside act_fn(g) * u
-        ext.swiglu_mul(g, u, out=mlp, comp_gate=comp_g, comp_up=comp_u)
+        if (comp_g is None and comp_u is None and ns["down"] is None
+                and ext.backbone_swiglu_ok(g, backbones["down"], sc["down"])):
+            # act_fn(g) * u formed inside the down backbone (nothing else reads the product)
+            hid_d = ext.backbone_swiglu_linear(g, u, backbones["down"], in_scale=sc["down"])
+        else:
+            # g + comp_g and u + comp_u (fp16 adds) inside act_fn(g) * u
+            ext.swiglu_mul(g, u, out=mlp, comp_gate=comp_g, comp_up=comp_u)
     n_out = int(pd["qweight1"].size(2))
     comp_d = None
     if ns["down"] is not None and NS_DOWN_BESIDE_GEMM:
@@ -299,7 +305,8 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
         side.wait_stream(main)
         with torch.cuda.stream(side):
             ext.ns_compensation_apply_(comp_d, mlp, eid, seg, ns["down"], accumulate=False)
-    hid_d = shared_projection(mlp, backbones["down"], in_scale=sc["down"])
+    if hid_d is None:
+        hid_d = shared_projection(mlp, backbones["down"], in_scale=sc["down"])
     d_out = torch.empty((R, n_out), dtype=torch.float16, device=dev)
     ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
         hid_d, eid, seg, prob, tile_bound, decoded["down"], *[pd[k] for k in names], True, out=d_out)

@@ -224,3 +224,44 @@ def test_layer_with_router_backbone_launch_matches_oracle(tris, oracle_mod, cuda
         wants.append(oracle_mod.bf16_round(want))
     assert calls, "the layer did not take the router + backbone launch"
     assert_close(np.concatenate(outs), np.concatenate(wants), f"layer T={tokens}")
+
+
+@pytest.mark.parametrize("rows,scaled", [(1, False), (16, True), (33, False), (64, True)])
+def test_backbone_swiglu_product_is_exact(tris, cuda, rows, scaled):
+    """With SV the identity, the fused down backbone returns its operand: the product fp16(silu(g) * u)
+    (times the input scale) must be swiglu_mul's bits (one product per output, nothing rounds twice)."""
+    note(f"backbone swiglu identity rows={rows} scaled={scaled}")
+    ext = tris["ext"]
+    n = 256
+    rng = np.random.default_rng(rows)
+    g = torch.from_numpy((rng.standard_normal((rows, n)) * 3).astype(np.float16)).to(cuda)
+    u = torch.from_numpy((rng.standard_normal((rows, n)) * 3).astype(np.float16)).to(cuda)
+    sc = torch.from_numpy(rng.uniform(0.5, 1.5, n).astype(np.float16)).to(cuda) if scaled else None
+    eye = torch.eye(n, dtype=torch.float16, device=cuda)
+    got = ext.backbone_swiglu_linear(g, u, eye, in_scale=sc)
+    want = ext.swiglu_mul(g, u)
+    if sc is not None:
+        want = want * sc  # fp16 product, as the kernel's
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("rows,in_f,rank", [(32, 14336, 512), (16, 1024, 256), (64, 512, 128), (7, 4096, 64)])
+def test_backbone_swiglu_matches_unfused(tris, cuda, rows, in_f, rank):
+    """The fused down backbone against swiglu_mul followed by backbone_linear (the split over K differs, so the
+    fp32 sums agree within rounding) and against an fp32 reference."""
+    note(f"backbone swiglu rows={rows} in={in_f} rank={rank}")
+    ext = tris["ext"]
+    rng = np.random.default_rng(in_f + rows)
+    g = torch.from_numpy(rng.standard_normal((rows, in_f)).astype(np.float16)).to(cuda)
+    u = torch.from_numpy(rng.standard_normal((rows, in_f)).astype(np.float16)).to(cuda)
+    sv = torch.from_numpy((rng.standard_normal((rank, in_f)) * 0.02).astype(np.float16)).to(cuda)
+    sc = torch.from_numpy(rng.uniform(0.5, 1.5, in_f).astype(np.float16)).to(cuda)
+    assert ext.backbone_swiglu_ok(g, sv, sc)
+    got = ext.backbone_swiglu_linear(g, u, sv, in_scale=sc)
+    mlp = ext.swiglu_mul(g, u)
+    unfused = ext.backbone_linear(mlp, sv, in_scale=sc)
+    ref = ((mlp * sc).float() @ sv.float().t()).cpu().numpy()
+    assert_close(got.float().cpu().numpy(), ref, "fused vs fp32")
+    assert_close(got.float().cpu().numpy(), unfused.float().cpu().numpy(), "fused vs unfused")
+    again = ext.backbone_swiglu_linear(g, u, sv, in_scale=sc)
+    assert torch.equal(got, again)  # slices added in fixed order
