@@ -208,8 +208,8 @@ constexpr int kMfRuns = kMfRows * (kMfChunk / 8) / kMfThreads;  // activation ru
 // arrays (double buffering): the copies of the next tile into one overlap the compute from the other,
 // and being distinct objects lets the compiler see that the compute's LDS reads do not wait for them.
 struct MfUnitLayout {
-  int xs, cds, cns, col_sal, sal_col, sal_xi, sal_cp, meta;  // chunk
-  int r01t, bytes;
+  int xs, cds, cns, sal_w, sal_xo, sal_cp, meta;  // chunk
+  int bytes;
 };
 
 __host__ __device__ inline int mf_take(int* o, int b) {
@@ -224,13 +224,11 @@ __host__ __device__ inline MfUnitLayout mf_unit_layout(int rows, int groups) {
   L.xs = mf_take(&o, rows * kMfXStride * 2);
   L.cds = mf_take(&o, kMfChunk * 2);
   L.cns = mf_take(&o, kMfChunk * 2);
-  L.col_sal = mf_take(&o, kMfChunk * 4);
-  L.sal_col = mf_take(&o, kMfChunk * 2);
-  L.sal_xi = mf_take(&o, kMfChunk * 2);
+  L.sal_w = mf_take(&o, kMfChunk * 4);
+  L.sal_xo = mf_take(&o, kMfChunk * 2);
   L.sal_cp = mf_take(&o, kMfChunk * 4);
   L.meta = mf_take(&o, 16 * 4);
   (void)groups;
-  L.r01t = mf_take(&o, kMfTiles * kTileOut * 4);
   L.bytes = o;
   return L;
 }
@@ -244,13 +242,20 @@ __host__ __device__ inline int mf_lds_bytes(int units, int rows, int groups) {
 constexpr int mf_static_lds_bytes(int units) { return units * 2 * kMfTbWords * 4; }
 
 struct MfChunk {       // a unit's staged chunk
-  uint16_t* xs;        // [rows][kMfXStride] activations, staged column order
+  uint16_t* xs;        // [rows][kMfXStride] activations, staged column order; column kMfChunk is zero (decode)
   uint16_t* cds;       // C_d, staged column order (0 for salient columns)
   uint16_t* cns;       // C_nd, staged column order (0 for salient columns)
+  // Weight-stationary kernel (natural column order):
   uint32_t* col_sal;   // C0 | C1 << 16, natural order
   uint16_t* sal_col;   // chunk column of the chunk's q-th salient column
-  uint16_t* sal_xi;    // its position in the staged (permuted) column order
-  uint32_t* sal_cp;    // its C0 | C1 << 16
+  // Decode kernel, per salient slot q (slots past the chunk's salient count, up to the next multiple of
+  // kMfSalWin, read as zero weights and zero activations):
+  uint32_t* sal_w;     // bits 0-4: (column - 15) mod 32, the right rotation that puts the column's qweight1 bit
+                       // at bit 15; bits 8-15: byte offset of its group's R0 | R1 in a column's row-scale block;
+                       // bits 16-31: byte offset of its packed row in the staged qweight1 words
+  uint16_t* sal_xo;    // byte offset of its activation in a staged row (the zero column for padding slots)
+  uint32_t* sal_cp;    // C0 | C1 << 16 with both signs flipped (decode), or as stored (weight-stationary)
+  uint16_t* sal_xi;    // weight-stationary: its position in the staged column order
   int32_t* meta;       // [t < 8] group of K tile t (-1: none); [8] first salient index; [9] end
 };
 struct MfTileBuf {     // one output tile's weight words
@@ -323,7 +328,9 @@ struct MfRegs {
   uint64_t cpv[2];    // col_pack3 of columns kc + utid, kc + utid + 256
   uint32_t cmt[2];    // their salient words
   int q2t[2];         // their packed rows' salient prefix
+  int gt[2];          // their groups (g_idx), -1 past the rank
   int sbase0;         // salient prefix at the chunk's first packed row
+  int send;           // salient prefix at the chunk's end
   int32_t mv;         // metadata word (see mf_chunk_issue)
 };
 
@@ -360,8 +367,10 @@ __device__ __forceinline__ void mf_chunk_issue(const MfmaProj& pa, int e, int ro
     R.cpv[h] = bload64(r_col, kv ? static_cast<uint32_t>(k) * 8u : col_bytes, 0u);
     R.cmt[h] = static_cast<uint32_t>(cmap_e[pr]);
     R.q2t[h] = q2p_e[pr];
+    R.gt[h] = kv ? gidx_e[k] : -1;
   }
   R.sbase0 = q2p_e[pr0];
+  R.send = q2p_e[pr0 + npr];
   // metadata: utid 64..71 -> group of K tile utid - 64; 72 / 73 -> salient prefix at the chunk's
   // start / end
   const int32_t* mp = q2p_e + pr0;
@@ -409,13 +418,35 @@ __device__ __forceinline__ void mf_chunk_write(const MfmaProj& pa, int rc, int k
     const bool sal = k < rank && ((cm >> bit) & 1u);
     ch.cds[pj] = sal ? static_cast<uint16_t>(0) : static_cast<uint16_t>(R.cpv[h] >> 32);
     ch.cns[pj] = sal ? static_cast<uint16_t>(0) : static_cast<uint16_t>(R.cpv[h] >> 48);
-    ch.col_sal[j] = static_cast<uint32_t>(R.cpv[h]);
+    if (natural) ch.col_sal[j] = static_cast<uint32_t>(R.cpv[h]);
     if (sal) {
       const int q = R.q2t[h] - R.sbase0 + __popc(cm & ((1u << bit) - 1u));
-      ch.sal_col[q] = static_cast<uint16_t>(j);
-      ch.sal_xi[q] = static_cast<uint16_t>((j & ~31) + mf_perm32(j & 31));
-      ch.sal_cp[q] = static_cast<uint32_t>(R.cpv[h]);
+      if (natural) {
+        ch.sal_col[q] = static_cast<uint16_t>(j);
+        ch.sal_xi[q] = static_cast<uint16_t>((j & ~31) + mf_perm32(j & 31));
+        ch.sal_cp[q] = static_cast<uint32_t>(R.cpv[h]);
+      } else {
+        // the column's group as the main pass takes it (uniform 64-column groups); an invalid group gives
+        // zero factors, as a K tile without a group does
+        const bool gv = R.gt[h] >= 0 && R.gt[h] < G;
+        ch.sal_w[q] = (static_cast<uint32_t>((j >> 5) * kMfQ1Stride * 4) << 16) |
+                      (static_cast<uint32_t>((gv ? R.gt[h] : 0) * 8) << 8) | (static_cast<uint32_t>(bit - 15) & 31u);
+        ch.sal_xo[q] = static_cast<uint16_t>(pj * 2);
+        ch.sal_cp[q] = (gv ? static_cast<uint32_t>(R.cpv[h]) : 0u) ^ 0x80008000u;
+      }
     }
+  }
+  if (!natural) {
+    // padding slots up to the last window's end read the zero activation column with zero factors
+    const int nsal = R.send - R.sbase0;
+    const int q = nsal + utid;
+    if (utid < kMfSalWin && q < ((nsal + kMfSalWin - 1) & ~(kMfSalWin - 1))) {
+      ch.sal_w[q] = 0u;
+      ch.sal_xo[q] = static_cast<uint16_t>(kMfChunk * 2);
+      ch.sal_cp[q] = 0x80008000u;
+    }
+    // the zero column (and its neighbour, so that row 0 holds an aligned zero word)
+    if (utid < rc) *reinterpret_cast<uint32_t*>(&ch.xs[utid * kMfXStride + kMfChunk]) = 0u;
   }
   if (utid >= 64 && utid < 72) {
     const bool tv = kc + (utid - 64) * kTileK < rank && R.mv >= 0 && R.mv < G;
@@ -552,55 +583,54 @@ __device__ __forceinline__ void mf_salient_weights(const MfChunk& ch, const MfTi
   for (int u = 0; u < kMfSalWin / 4; ++u) ws[wave][i16][4 * u + kg] = wv[u];
 }
 
-// Both MFMA operands of salient window [w0, w0 + wn) of the chunk, built in registers: lane (i16, kg) takes
-// window slots 8 kg .. 8 kg + 7 (zero past wn); bv holds the exact fp16 weights of its column tc,
-// w = fp16(+-fp16(C0 * R0) +- fp16(C1 * R1)) (both products in one packed multiply), and av its activation
-// row xr at those slots' columns.  Slot data (columns, staged positions and C0 | C1) are read 8 at a time in
-// slot order; only the qweight1 sign word, the row scales and the activation depend on the column.  q2w: the
-// lane's qweight2_sparse words of rows q2b = (sbase0 + w0) / 32 and q2b + 1 (a window spans at most two).
-__device__ __forceinline__ void mf_salient_operands(const MfChunk& ch, const MfTileBuf& tb, const uint32_t* r01t,
-                                                    const uint16_t* xr, int tc, int kg, int sbase0, int w0, int wn,
-                                                    int q2b, const uint32_t q2w[2], f16x8& av, f16x8& bv) {
+// Both MFMA operands of the salient window starting at slot w0, built in registers: lane (i16, kg) takes window
+// slots 8 kg .. 8 kg + 7.  bv holds the exact fp16 weights of its column, w = fp16(+-fp16(C0 * R0) +-
+// fp16(C1 * R1)) (both products in one packed multiply), and av its activation row xr at those slots'
+// columns.  The staged slot words carry every column-dependent offset, so a slot costs three LDS reads (its
+// qweight1 word, its group's R0 | R1, its activation) and no masking: padding slots read zero factors and the
+// zero activation column.  q1_lane / rs_lane: the byte offsets of the lane's column in the staged qweight1 rows
+// and in the row-scale block; q2w: the lane's qweight2_sparse words of rows (sbase0 + w0) / 32 and the next
+// (a window spans at most two), q2off = (sbase0 + w0) % 32 + 8 kg the bit of slot 0 in q2w[0] | q2w[1] << 32.
+__device__ __forceinline__ void mf_salient_operands(const MfChunk& ch, const MfTileBuf& tb, const uint16_t* xr,
+                                                    uint32_t q1_lane, uint32_t rs_lane, int kg, int w0, int q2off,
+                                                    const uint32_t q2w[2], f16x8& av, f16x8& bv) {
   const int s0 = w0 + 8 * kg;  // a multiple of 8: the slot vectors are 16-byte aligned
-  const uint4 cv = *reinterpret_cast<const uint4*>(&ch.sal_col[s0]);
-  const uint4 xv = *reinterpret_cast<const uint4*>(&ch.sal_xi[s0]);
-  const uint32_t cw[4] = {cv.x, cv.y, cv.z, cv.w};
-  const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-  // Every slot reads its operands (slots past wn at column 0, in range) and is masked after; all 24
-  // column-dependent reads are issued before any is used, so their latencies overlap.
-  int col[8];
-  uint32_t w1v[8], rrv[8], av8[8];
+  const uint4 swa = *reinterpret_cast<const uint4*>(&ch.sal_w[s0]);
+  const uint4 swb = *reinterpret_cast<const uint4*>(&ch.sal_w[s0 + 4]);
+  const uint4 xov = *reinterpret_cast<const uint4*>(&ch.sal_xo[s0]);
+  const uint32_t sw[8] = {swa.x, swa.y, swa.z, swa.w, swb.x, swb.y, swb.z, swb.w};
+  const uint32_t xo[4] = {xov.x, xov.y, xov.z, xov.w};
+  const unsigned char* q1b = reinterpret_cast<const unsigned char*>(tb.q1) + q1_lane;
+  const unsigned char* rsb = reinterpret_cast<const unsigned char*>(tb.rs) + rs_lane;
+  const unsigned char* xb = reinterpret_cast<const unsigned char*>(xr);
+  uint32_t w1v[8], rrv[8], a16[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {  // all 24 reads issued before any is used
+    w1v[u] = *reinterpret_cast<const uint32_t*>(q1b + (sw[u] >> 16));
+    rrv[u] = *reinterpret_cast<const uint32_t*>(rsb + ((sw[u] >> 8) & 0xFFu));
+    a16[u] = *reinterpret_cast<const uint16_t*>(xb + ((xo[u / 2] >> (16 * (u & 1))) & 0xFFFFu));
+  }
+  const uint4 cpa = *reinterpret_cast<const uint4*>(&ch.sal_cp[s0]);
+  const uint4 cpb = *reinterpret_cast<const uint4*>(&ch.sal_cp[s0 + 4]);
+  const uint32_t cp[8] = {cpa.x, cpa.y, cpa.z, cpa.w, cpb.x, cpb.y, cpb.z, cpb.w};
+  // qweight2_sparse bits of the 8 slots: bit u of q2lo
+  const uint32_t q2lo = static_cast<uint32_t>(((static_cast<uint64_t>(q2w[1]) << 32) | q2w[0]) >> q2off);
+  uint32_t t[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
-    const uint32_t keep = 8 * kg + u < wn ? 0xFFFFu : 0u;
-    const uint32_t sh = 16u * static_cast<uint32_t>(u & 1);
-    col[u] = static_cast<int>((cw[u / 2] >> sh) & keep);  // chunk column (0 past wn)
-    const int xi = static_cast<int>((xw[u / 2] >> sh) & keep);
-    w1v[u] = tb.q1[(col[u] >> 5) * kMfQ1Stride + tc];
-    rrv[u] = r01t[(col[u] >> 6) * kTileOut + tc];
-    av8[u] = xr[xi];
+    // staged factors have both signs flipped; flip back where the qweight1 (bit 15) / qweight2 (bit 31) bit is
+    // set (the positive weights)
+    const uint32_t rot = __builtin_amdgcn_alignbit(w1v[u], w1v[u], sw[u]);  // column's bit at bit 15
+    const uint32_t pos = (rot & 0x8000u) | ((q2lo << (31 - u)) & 0x80000000u);
+    t[u] = f16x2_as_u32(u32_as_f16x2(cp[u]) * u32_as_f16x2(rrv[u])) ^ pos;
   }
-  // qweight2_sparse sign bits of the 8 slots: bit u of q2bits (the slots' indices span at most two words)
-  const int off = ((sbase0 + w0) & 31) + 8 * kg;  // slot 0's bit within q2w[0] | q2w[1] << 32, <= 55
-  const uint64_t q2bits = ((static_cast<uint64_t>(q2w[1]) << 32) | q2w[0]) >> off;
-  uint32_t wb[4] = {0u, 0u, 0u, 0u}, ab[4] = {0u, 0u, 0u, 0u};
+  uint32_t wb[4], ab[4];
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    const uint4 cpv = *reinterpret_cast<const uint4*>(&ch.sal_cp[s0 + 4 * half]);
-    const uint32_t cps[4] = {cpv.x, cpv.y, cpv.z, cpv.w};
-#pragma unroll
-    for (int uu = 0; uu < 4; ++uu) {
-      const int u = 4 * half + uu;
-      const uint32_t keep = 8 * kg + u < wn ? 0xFFFFu : 0u;
-      const uint32_t sh = 16u * static_cast<uint32_t>(u & 1);
-      // sign bits: positive where the qweight1 / qweight2 bit is set
-      const uint32_t neg = ((~(w1v[u] >> (col[u] & 31)) & 1u) << 15) |
-                           ((~static_cast<uint32_t>(q2bits >> u) & 1u) << 31);
-      const f16x2 t = __builtin_bit_cast(f16x2, f16x2_as_u32(u32_as_f16x2(cps[uu]) * u32_as_f16x2(rrv[u])) ^ neg);
-      const _Float16 w = t[0] + t[1];
-      wb[u / 2] |= (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, w)) & keep) << sh;
-      ab[u / 2] |= (av8[u] & keep) << sh;
-    }
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = __builtin_amdgcn_perm(t[2 * i + 1], t[2 * i], 0x05040100u);  // the C0 R0 terms
+    const uint32_t hi = __builtin_amdgcn_perm(t[2 * i + 1], t[2 * i], 0x07060302u);  // the C1 R1 terms
+    wb[i] = f16x2_as_u32(u32_as_f16x2(lo) + u32_as_f16x2(hi));
+    ab[i] = a16[2 * i] | (a16[2 * i + 1] << 16);
   }
   av = __builtin_bit_cast(f16x8, make_uint4(ab[0], ab[1], ab[2], ab[3]));
   bv = __builtin_bit_cast(f16x8, make_uint4(wb[0], wb[1], wb[2], wb[3]));
@@ -609,11 +639,31 @@ __device__ __forceinline__ void mf_salient_operands(const MfChunk& ch, const MfT
 // The lane's qweight2_sparse words of the chunk's first salient window (a window of kMfSalWin salient
 // columns spans at most two qweight2_sparse rows), for output column n.  Issued before the next tile's
 // LDS copies so that waiting for them does not wait for the copies.
-__device__ __forceinline__ void mf_q2_issue(const MfmaProj& pa, int e, int n, const MfChunk& ch, uint32_t q2w[2]) {
+// A staged chunk's metadata in scalar registers: the group of each K tile (-1: none), the chunk's first
+// salient index and its salient count.  One LDS round trip.
+struct MfChunkMeta {
+  int g[kMfTiles];
+  int sbase0, num_sal;
+};
+__device__ __forceinline__ MfChunkMeta mf_chunk_meta(const MfChunk& ch) {
+  const int4 m0 = *reinterpret_cast<const int4*>(&ch.meta[0]);
+  const int4 m1 = *reinterpret_cast<const int4*>(&ch.meta[4]);
+  const int4 m2 = *reinterpret_cast<const int4*>(&ch.meta[8]);
+  const int gv[kMfTiles] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+  MfChunkMeta m;
+#pragma unroll
+  for (int t = 0; t < kMfTiles; ++t) m.g[t] = __builtin_amdgcn_readfirstlane(gv[t]);
+  m.sbase0 = __builtin_amdgcn_readfirstlane(m2.x);
+  m.num_sal = __builtin_amdgcn_readfirstlane(m2.y) - m.sbase0;
+  return m;
+}
+
+__device__ __forceinline__ void mf_q2_issue(const MfmaProj& pa, int e, int n, const MfChunkMeta& cm,
+                                            uint32_t q2w[2]) {
   const tris_compact3_payload& p = pa.p;
   const int N = p.outfeatures;
-  const int sbase0 = __builtin_amdgcn_readfirstlane(ch.meta[8]);
-  const int num_sal = __builtin_amdgcn_readfirstlane(ch.meta[9]) - sbase0;
+  const int sbase0 = cm.sbase0;
+  const int num_sal = cm.num_sal;
   const int q2rows = p.qweight2_sparse_rows;
   const uint32_t q2_bytes = static_cast<uint32_t>(q2rows) * N * 4u;
   const __amdgpu_buffer_rsrc_t r_q2 = make_rsrc(p.qweight2_sparse + static_cast<int64_t>(e) * q2rows * N, q2_bytes);
@@ -627,7 +677,7 @@ __device__ __forceinline__ void mf_q2_issue(const MfmaProj& pa, int e, int n, co
 }
 
 __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, int n0, int xrow, int utid,
-                                            const MfChunk& ch, const MfTileBuf& tb, uint32_t* r01t,
+                                            const MfChunk& ch, const MfChunkMeta& cm, const MfTileBuf& tb,
                                             const uint32_t q2w0[2], f32x4 acc) {
   const tris_compact3_payload& p = pa.p;
   const int N = p.outfeatures;
@@ -645,8 +695,8 @@ __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, i
   const uint16_t* xr = ch.xs + xrow * kMfXStride;
 
   // salient columns of the chunk; the first window's qweight2_sparse words come in q2w0
-  const int sbase0 = __builtin_amdgcn_readfirstlane(ch.meta[8]);
-  const int num_sal = __builtin_amdgcn_readfirstlane(ch.meta[9]) - sbase0;
+  const int sbase0 = cm.sbase0;
+  const int num_sal = cm.num_sal;
   const int q2rows = p.qweight2_sparse_rows;
   const uint32_t q2_bytes = static_cast<uint32_t>(q2rows) * N * 4u;
   const __amdgpu_buffer_rsrc_t r_q2 =
@@ -660,15 +710,17 @@ __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, i
   // j + 1 are issued before row j is computed.
   const uint32_t rot = static_cast<uint32_t>(kg - 1) & 31u;  // rotate right: bit kg + 4m -> 4m + 1
   const uint32_t shl = static_cast<uint32_t>(3 - kg);        // shift left:   bit kg + 4m -> 4m + 3
-  // row scales of each K tile's group for this column: R_d | R_nd << 16, and R0 | R1 << 16 into r01t
-  // (only this wave reads its columns' entries)
+  // the lane's column in the row-scale block [64 columns][G][R0 | R1, R_d | R_nd]
+  const uint32_t rs_lane = static_cast<uint32_t>(tc * G * 8);
+  const unsigned char* rsb = reinterpret_cast<const unsigned char*>(tb.rs) + rs_lane;
+  // R_d | R_nd << 16 of each K tile's group for this column; a tile without a group reads the staged zero
+  // word, so the reads do not wait on each other
+  const uint32_t* zero_word = reinterpret_cast<const uint32_t*>(ch.xs + kMfChunk);
   uint32_t rdn[kMfTiles];
 #pragma unroll
   for (int t = 0; t < kMfTiles; ++t) {
-    const int g = __builtin_amdgcn_readfirstlane(ch.meta[t]);
-    const int gi = (tc * G + (g >= 0 ? g : 0)) * 2;
-    rdn[t] = g >= 0 ? tb.rs[gi + 1] : 0u;
-    if ((t & 3) == kg) r01t[t * kTileOut + tc] = g >= 0 ? tb.rs[gi] : 0u;
+    const int g = cm.g[t];
+    rdn[t] = *(g >= 0 ? reinterpret_cast<const uint32_t*>(rsb + g * 8 + 4) : zero_word);
   }
   struct Row {
     uint32_t qw, gw;
@@ -703,12 +755,9 @@ __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, i
       if (j < npr) row_mfma(load_row(j), rdn[j / 2]);  // uniform
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();  // r01t written
 
   // ---- salient columns, kMfSalWin at a time: both operands in registers (mf_salient_operands), one MFMA
   for (int w0 = 0; w0 < num_sal; w0 += kMfSalWin) {
-    const int wn = (num_sal - w0) < kMfSalWin ? (num_sal - w0) : kMfSalWin;
     const int q2b = (sbase0 + w0) >> 5;  // qweight2_sparse row of the window's first salient column
     if (w0 > 0) {
 #pragma unroll
@@ -718,7 +767,8 @@ __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, i
       }
     }
     f16x8 av, bv;
-    mf_salient_operands(ch, tb, r01t, xr, tc, kg, sbase0, w0, wn, q2b, q2w, av, bv);
+    mf_salient_operands(ch, tb, xr, static_cast<uint32_t>(tc * 4), rs_lane, kg, w0,
+                        ((sbase0 + w0) & 31) + 8 * kg, q2w, av, bv);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
   }
   return acc;
@@ -779,8 +829,12 @@ void grouped_mfma_kernel(MfmaArgs a) {
   ch.xs = reinterpret_cast<uint16_t*>(base + L.xs);
   ch.cds = reinterpret_cast<uint16_t*>(base + L.cds);
   ch.cns = reinterpret_cast<uint16_t*>(base + L.cns);
-  ch.col_sal = reinterpret_cast<uint32_t*>(base + L.col_sal);
-  ch.sal_col = reinterpret_cast<uint16_t*>(base + L.sal_col);
+  ch.col_sal = nullptr;
+  ch.sal_col = nullptr;
+  ch.sal_xi = nullptr;
+  ch.sal_w = reinterpret_cast<uint32_t*>(base + L.sal_w);
+  ch.sal_xo = reinterpret_cast<uint16_t*>(base + L.sal_xo);
+  ch.sal_cp = reinterpret_cast<uint32_t*>(base + L.sal_cp);
   ch.meta = reinterpret_cast<int32_t*>(base + L.meta);
   __shared__ __attribute__((aligned(16))) uint32_t mf_tb0[kUnits][kMfTbWords];
   __shared__ __attribute__((aligned(16))) uint32_t mf_tb1[kUnits][kMfTbWords];
@@ -791,9 +845,6 @@ void grouped_mfma_kernel(MfmaArgs a) {
   tb1.q1 = &mf_tb1[unit][kMfTbQ1];
   tb1.gw = &mf_tb1[unit][kMfTbGw];
   tb1.rs = &mf_tb1[unit][kMfTbRs];
-  ch.sal_xi = reinterpret_cast<uint16_t*>(base + L.sal_xi);
-  ch.sal_cp = reinterpret_cast<uint32_t*>(base + L.sal_cp);
-  uint32_t* r01t = reinterpret_cast<uint32_t*>(base + L.r01t);
   float* exch = reinterpret_cast<float*>(mf_lds + kUnits * L.bytes);
   // A operand row of this lane: rows >= rc hold stale values and only feed output rows that are not stored
   const int i16 = lane % 16;
@@ -836,7 +887,8 @@ void grouped_mfma_kernel(MfmaArgs a) {
   auto tile = [&](int ob, const MfTileBuf& cur, const MfTileBuf& nxt) {
     const int n = ob * kTileOut + 16 * (utid / kWave) + i16;
     uint32_t q2w[2];
-    mf_q2_issue(pa, e, n, ch, q2w);
+    MfChunkMeta cm = mf_chunk_meta(ch);
+    mf_q2_issue(pa, e, n, cm, q2w);
     if (one_chunk && ob + 1 < ob_end) mf_tile_issue(pa, s, e, 0, ob + 1, utid, nxt);  // prefetch
     f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     for (int kc = 0; kc < rank; kc += kMfChunk) {
@@ -848,9 +900,10 @@ void grouped_mfma_kernel(MfmaArgs a) {
         mf_chunk_write(pa, rc, kc, utid, ch, regs);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        mf_q2_issue(pa, e, n, ch, q2w);
+        cm = mf_chunk_meta(ch);
+        mf_q2_issue(pa, e, n, cm, q2w);
       }
-      acc = mf_compute(pa, e, kc, ob * kTileOut, xrow, utid, ch, cur, r01t, q2w, acc);
+      acc = mf_compute(pa, e, kc, ob * kTileOut, xrow, utid, ch, cm, cur, q2w, acc);
     }
 
     const bool nv = n < N;
@@ -1052,6 +1105,8 @@ __global__ __launch_bounds__(kUnits * kMfThreads) void grouped_mfma_ws_kernel(Mf
   ch.sal_col = reinterpret_cast<uint16_t*>(lbase + L.sal_col);
   ch.sal_xi = reinterpret_cast<uint16_t*>(lbase + L.sal_xi);
   ch.sal_cp = reinterpret_cast<uint32_t*>(lbase + L.sal_cp);
+  ch.sal_w = nullptr;
+  ch.sal_xo = nullptr;
   ch.meta = reinterpret_cast<int32_t*>(lbase + L.meta);
   uint16_t* const xsb0 = reinterpret_cast<uint16_t*>(lbase + L.xs[0]);
   uint16_t* const xsb1 = reinterpret_cast<uint16_t*>(lbase + L.xs[1]);
