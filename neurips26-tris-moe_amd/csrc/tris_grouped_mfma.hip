@@ -65,8 +65,6 @@ struct MfmaArgs {
   const int32_t* expert_ids;
   const int32_t* segment_offsets;
   int num_segments;
-  int xs_rows;       // activation rows staged per tile: min(16, batch)
-  int lds_groups;    // row-scale groups the LDS layout is sized for (max over the projections)
 };
 
 // Position of column k (0..31) of a packed row in the staged order: lane group
@@ -200,46 +198,24 @@ constexpr int kMfTbRs = kMfTbGw + kMfPR * kTileOut;
 constexpr int kMfTbWords = kMfTbRs + kTileOut * kMfMaxGroups * 2;
 static_assert(kMfTbGw % 4 == 0 && kMfTbRs % 4 == 0, "tile buffer pieces must be 16-byte aligned");
 constexpr int kMfCus = 256;  // MI355X compute units
+// per wavefront and copy buffer: qweight1 and split words of 16 columns, their row-scale block and a zero word
+constexpr int kMfWAllocBytes = (2 * (kMfChunk / 32) * 16 + 16 * kMfMaxGroups * 2 + 4) * 4;
 constexpr int kMfRuns = kMfRows * (kMfChunk / 8) / kMfThreads;  // activation runs per thread of a unit
 
-// Dynamic LDS of one unit (4 wavefronts computing one projection): the chunk's activations and column
-// data (shared by every output tile the workgroup walks), the salient row-scale table and the salient
-// weight table.  Byte offsets, 16-byte aligned pieces.  The per-tile weight words live in two static
-// arrays (double buffering): the copies of the next tile into one overlap the compute from the other,
-// and being distinct objects lets the compiler see that the compute's LDS reads do not wait for them.
-struct MfUnitLayout {
-  int xs, cds, cns, sal_w, sal_xo, sal_cp, meta;  // chunk
-  int bytes;
-};
+constexpr int kMfExchBytes = kMfThreads * 4 * 4;  // SwiGLU: the up unit's accumulators for the gate unit
 
+// Bump allocation of 16-byte aligned pieces (byte offsets into dynamic LDS).
 __host__ __device__ inline int mf_take(int* o, int b) {
   const int at = *o;
   *o += (b + 15) & ~15;
   return at;
 }
 
-__host__ __device__ inline MfUnitLayout mf_unit_layout(int rows, int groups) {
-  MfUnitLayout L;
-  int o = 0;
-  L.xs = mf_take(&o, rows * kMfXStride * 2);
-  L.cds = mf_take(&o, kMfChunk * 2);
-  L.cns = mf_take(&o, kMfChunk * 2);
-  L.sal_w = mf_take(&o, kMfChunk * 4);
-  L.sal_xo = mf_take(&o, kMfChunk * 2);
-  L.sal_cp = mf_take(&o, kMfChunk * 4);
-  L.meta = mf_take(&o, 16 * 4);
-  (void)groups;
-  L.bytes = o;
-  return L;
+// Static LDS of the decode kernel with `units` units and `rows` staged activation rows (as declared there).
+constexpr int mf_static_lds_bytes(int units, int rows) {
+  return units * (rows * kMfXStride * 2 + kMfChunk * (2 + 2 + 4 + 2 + 4) + 16 * 4 + 2 * kMfWaves * kMfWAllocBytes) +
+         (units == 2 ? kMfExchBytes : 16);
 }
-
-constexpr int kMfExchBytes = kMfThreads * 4 * 4;  // SwiGLU: the up unit's accumulators for the gate unit
-
-// Dynamic LDS of a workgroup with `units` units, and its static (tile buffer) LDS.
-__host__ __device__ inline int mf_lds_bytes(int units, int rows, int groups) {
-  return units * mf_unit_layout(rows, groups).bytes + (units == 2 ? kMfExchBytes : 0);
-}
-constexpr int mf_static_lds_bytes(int units) { return units * 2 * kMfTbWords * 4; }
 
 struct MfChunk {       // a unit's staged chunk
   uint16_t* xs;        // [rows][kMfXStride] activations, staged column order; column kMfChunk is zero (decode)
@@ -252,7 +228,7 @@ struct MfChunk {       // a unit's staged chunk
   // kMfSalWin, read as zero weights and zero activations):
   uint32_t* sal_w;     // bits 0-4: (column - 15) mod 32, the right rotation that puts the column's qweight1 bit
                        // at bit 15; bits 8-15: byte offset of its group's R0 | R1 in a column's row-scale block;
-                       // bits 16-31: byte offset of its packed row in the staged qweight1 words
+                       // bits 16-31: byte offset of its packed row in a wavefront's qweight1 words
   uint16_t* sal_xo;    // byte offset of its activation in a staged row (the zero column for padding slots)
   uint32_t* sal_cp;    // C0 | C1 << 16 with both signs flipped (decode), or as stored (weight-stationary)
   uint16_t* sal_xi;    // weight-stationary: its position in the staged column order
@@ -262,6 +238,25 @@ struct MfTileBuf {     // one output tile's weight words
   uint32_t* q1;        // [kMfPR][kMfQ1Stride] qweight1 words of the tile's 64 columns
   uint32_t* gw;        // [kMfPR][64] predecoded split words
   uint32_t* rs;        // [64][G][2] row_pack3: R0 | R1 << 16, R_d | R_nd << 16
+};
+
+// Decode kernel: each wavefront copies only the weight words of its own 16 output columns, so no other
+// wavefront waits for them.  Per wavefront and buffer: qweight1 [kMfPR][16], split words [kMfPR][16] and the
+// row-scale block [16 columns][kMfMaxGroups][2]; every piece is a whole number of 64-lane copies, so a tile
+// always takes kMfWDma copies (a fixed count lets each wavefront wait for exactly its own).
+constexpr int kMfWCols = 16;
+constexpr int kMfWq1 = 0;
+constexpr int kMfWgw = kMfPR * kMfWCols;
+constexpr int kMfWrs = 2 * kMfPR * kMfWCols;
+constexpr int kMfWWords = kMfWrs + kMfWCols * kMfMaxGroups * 2;
+constexpr int kMfWDma = kMfWWords / kWave;
+constexpr int kMfWAlloc = kMfWWords + 4;  // + a zero word that no copy writes (read for K tiles without a group)
+static_assert(kMfWWords % kWave == 0 && kMfWgw % kWave == 0 && kMfWrs % kWave == 0, "whole 64-lane copies");
+struct MfWaveBuf {     // one wavefront's copy of its 16 columns' words
+  uint32_t* q1;        // [kMfPR][16]
+  uint32_t* gw;        // [kMfPR][16]
+  uint32_t* rs;        // [16][G][2]
+  uint32_t* zero;      // a word that holds 0
 };
 
 constexpr uint32_t kBufferWord3 = 0x00020000;  // raw buffer resource, gfx9 family
@@ -320,6 +315,14 @@ __device__ __forceinline__ void dma32(__amdgpu_buffer_rsrc_t r, void* dst, uint3
 }
 __device__ __forceinline__ void dma128(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
+}
+
+// s_waitcnt on the vector memory counter alone (gfx9 encoding: vmcnt in bits 3:0 and 15:14; the export and LDS
+// counters left at their maxima): wait until at most N vector memory operations are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
 // Register-staged loads of a unit's chunk, held between issue and write.
@@ -429,7 +432,7 @@ __device__ __forceinline__ void mf_chunk_write(const MfmaProj& pa, int rc, int k
         // the column's group as the main pass takes it (uniform 64-column groups); an invalid group gives
         // zero factors, as a K tile without a group does
         const bool gv = R.gt[h] >= 0 && R.gt[h] < G;
-        ch.sal_w[q] = (static_cast<uint32_t>((j >> 5) * kMfQ1Stride * 4) << 16) |
+        ch.sal_w[q] = (static_cast<uint32_t>((j >> 5) * kMfWCols * 4) << 16) |
                       (static_cast<uint32_t>((gv ? R.gt[h] : 0) * 8) << 8) | (static_cast<uint32_t>(bit - 15) & 31u);
         ch.sal_xo[q] = static_cast<uint16_t>(pj * 2);
         ch.sal_cp[q] = (gv ? static_cast<uint32_t>(R.cpv[h]) : 0u) ^ 0x80008000u;
@@ -495,6 +498,61 @@ __device__ __forceinline__ void mf_tile_issue(const MfmaProj& pa, int s, int e, 
   const int kb = ceil_div(kTileOut * G * 8, 1024);  // <= 4 KiB (G <= kMfMaxGroups)
   for (int b = wave; b < kb; b += kMfWaves) {
     dma128(r_rs, reinterpret_cast<unsigned char*>(tb.rs) + b * 1024, static_cast<uint32_t>(b * 1024 + lane * 16), 0u);
+  }
+}
+
+// Per-lane byte offsets of a wavefront's copies for chunk kc, output tile 0 (mf_wave_tile_issue adds the tile):
+// lane l copies packed row pr0 + 4 i + l / 16 (copy i adds whole rows), column 16 wave + l % 16.
+struct MfWaveOffsets {
+  uint32_t q1;   // into the expert's qweight1 [packed rows][N]
+  uint32_t dec;  // into the segment's predecoded blocks [packed rows / 2][tiles][128]
+};
+__device__ __forceinline__ MfWaveOffsets mf_wave_offsets(const MfmaProj& pa, int kc, int wave, int lane) {
+  const tris_compact3_payload& p = pa.p;
+  const int N = p.outfeatures;
+  const int nob = ceil_div(N, kTileOut);
+  const uint32_t pr = static_cast<uint32_t>(kc / 32 + lane / kMfWCols);
+  const uint32_t c = static_cast<uint32_t>(kMfWCols * wave + lane % kMfWCols);
+  MfWaveOffsets o;
+  o.q1 = (pr * N + c) * 4u;
+  o.dec = ((pr >> 1) * nob * kGrWords + (pr & 1u) * kTileOut + c) * 4u;
+  return o;
+}
+
+// The wavefront's LDS copies of its 16 columns of output tile ob for chunk kc: qweight1 and split words of the
+// chunk's packed rows (lane l of copy i: packed row 4 i + l / 16, column l % 16) and the columns' row-scale block.
+// Always kMfWDma copies.  Nothing is masked: every offset is checked against its buffer's size (past it reads
+// zeros), and what lies inside it but past the chunk's rows or past column N (the next row's words, the next
+// tile's block) only feeds packed rows the compute skips or output columns that are not stored.  So ob may be
+// one past the last tile (a prefetch with nothing to fetch).
+__device__ __forceinline__ void mf_wave_tile_issue(const MfmaProj& pa, int s, int e, int ob, const MfWaveOffsets& o,
+                                                   int lane, int wave, const MfWaveBuf& wb) {
+  const tris_compact3_payload& p = pa.p;
+  const int N = p.outfeatures;
+  const int G = p.num_groups;
+  const int packed_rows = p.rank / 32;
+  const int nob = ceil_div(N, kTileOut);
+  const int nblk = (packed_rows / 2) * nob;
+  const uint32_t q1_bytes = static_cast<uint32_t>(packed_rows) * N * 4u;
+  const uint32_t dec_bytes = static_cast<uint32_t>(nblk) * kGrWords * 4u;
+  const __amdgpu_buffer_rsrc_t r_q1 = make_rsrc(p.qweight1 + static_cast<int64_t>(e) * packed_rows * N, q1_bytes);
+  const __amdgpu_buffer_rsrc_t r_dec =
+      make_rsrc(pa.decoded + static_cast<int64_t>(s) * nblk * kGrWords, dec_bytes);
+#pragma unroll
+  for (int i = 0; i < kMfPR / 4; ++i) {
+    dma32(r_q1, wb.q1 + i * kWave, o.q1 + static_cast<uint32_t>(4 * i * N + ob * kTileOut) * 4u, 0u);
+    dma32(r_dec, wb.gw + i * kWave, o.dec + static_cast<uint32_t>((2 * i * nob + ob) * kGrWords) * 4u, 0u);
+  }
+  // row_pack3[e][n0 .. n0 + 15][0 .. G - 1] is one contiguous run of 16 G pairs; the copies past it read the next
+  // columns' words (unused) or zeros past the expert
+  const int n0 = ob * kTileOut + kMfWCols * wave;
+  const int ncols = N - n0;
+  const uint32_t rs_bytes = ncols > 0 ? static_cast<uint32_t>(ncols) * G * 8u : 0u;
+  const __amdgpu_buffer_rsrc_t r_rs =
+      make_rsrc(p.row_pack3 + (static_cast<int64_t>(e) * N + (ncols > 0 ? n0 : 0)) * G, rs_bytes);
+#pragma unroll
+  for (int i = 0; i < kMfWCols * kMfMaxGroups * 2 / kWave; ++i) {
+    dma32(r_rs, wb.rs + i * kWave, static_cast<uint32_t>(i * kWave + lane) * 4u, 0u);
   }
 }
 
@@ -588,10 +646,10 @@ __device__ __forceinline__ void mf_salient_weights(const MfChunk& ch, const MfTi
 // fp16(C1 * R1)) (both products in one packed multiply), and av its activation row xr at those slots'
 // columns.  The staged slot words carry every column-dependent offset, so a slot costs three LDS reads (its
 // qweight1 word, its group's R0 | R1, its activation) and no masking: padding slots read zero factors and the
-// zero activation column.  q1_lane / rs_lane: the byte offsets of the lane's column in the staged qweight1 rows
-// and in the row-scale block; q2w: the lane's qweight2_sparse words of rows (sbase0 + w0) / 32 and the next
+// zero activation column.  q1_lane / rs_lane: the byte offsets of the lane's column in the wavefront's qweight1
+// rows and in its row-scale block; q2w: the lane's qweight2_sparse words of rows (sbase0 + w0) / 32 and the next
 // (a window spans at most two), q2off = (sbase0 + w0) % 32 + 8 kg the bit of slot 0 in q2w[0] | q2w[1] << 32.
-__device__ __forceinline__ void mf_salient_operands(const MfChunk& ch, const MfTileBuf& tb, const uint16_t* xr,
+__device__ __forceinline__ void mf_salient_operands(const MfChunk& ch, const MfWaveBuf& tb, const uint16_t* xr,
                                                     uint32_t q1_lane, uint32_t rs_lane, int kg, int w0, int q2off,
                                                     const uint32_t q2w[2], f16x8& av, f16x8& bv) {
   const int s0 = w0 + 8 * kg;  // a multiple of 8: the slot vectors are 16-byte aligned
@@ -677,7 +735,7 @@ __device__ __forceinline__ void mf_q2_issue(const MfmaProj& pa, int e, int n, co
 }
 
 __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, int n0, int xrow, int utid,
-                                            const MfChunk& ch, const MfChunkMeta& cm, const MfTileBuf& tb,
+                                            const MfChunk& ch, const MfChunkMeta& cm, const MfWaveBuf& tb,
                                             const uint32_t q2w0[2], f32x4 acc) {
   const tris_compact3_payload& p = pa.p;
   const int N = p.outfeatures;
@@ -702,7 +760,6 @@ __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, i
   const __amdgpu_buffer_rsrc_t r_q2 =
       make_rsrc(p.qweight2_sparse + static_cast<int64_t>(e) * q2rows * N, q2_bytes);
   const uint32_t v_q2 = n < N ? static_cast<uint32_t>(n) * 4u : q2_bytes;
-  uint32_t q2w[2] = {q2w0[0], q2w0[1]};
 
   // ---- MFMA over the chunk's packed rows (salient columns have zero factors here).  Per packed row
   // the lane builds the nibble selectors of its 8 columns k = kg + 4m: bit 1 = this term is used,
@@ -710,17 +767,19 @@ __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, i
   // j + 1 are issued before row j is computed.
   const uint32_t rot = static_cast<uint32_t>(kg - 1) & 31u;  // rotate right: bit kg + 4m -> 4m + 1
   const uint32_t shl = static_cast<uint32_t>(3 - kg);        // shift left:   bit kg + 4m -> 4m + 3
-  // the lane's column in the row-scale block [64 columns][G][R0 | R1, R_d | R_nd]
-  const uint32_t rs_lane = static_cast<uint32_t>(tc * G * 8);
-  const unsigned char* rsb = reinterpret_cast<const unsigned char*>(tb.rs) + rs_lane;
-  // R_d | R_nd << 16 of each K tile's group for this column; a tile without a group reads the staged zero
-  // word, so the reads do not wait on each other
-  const uint32_t* zero_word = reinterpret_cast<const uint32_t*>(ch.xs + kMfChunk);
+  // the lane's column in the wavefront's row-scale block [16 columns][G][R0 | R1, R_d | R_nd]
+  const uint32_t rs_lane = static_cast<uint32_t>(i16 * G * 8);
+  // R_d | R_nd << 16 of each K tile's group for this column; a tile without a group reads the buffer's zero
+  // word.  The offsets are selected, not the pointers, so every read is known to address this buffer and
+  // need not wait for copies into the other.
   uint32_t rdn[kMfTiles];
+  const uint32_t zero_off = static_cast<uint32_t>(reinterpret_cast<const unsigned char*>(tb.zero) -
+                                                  reinterpret_cast<const unsigned char*>(tb.rs));
 #pragma unroll
   for (int t = 0; t < kMfTiles; ++t) {
     const int g = cm.g[t];
-    rdn[t] = *(g >= 0 ? reinterpret_cast<const uint32_t*>(rsb + g * 8 + 4) : zero_word);
+    const uint32_t off = g >= 0 ? rs_lane + static_cast<uint32_t>(g) * 8u + 4u : zero_off;
+    rdn[t] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const unsigned char*>(tb.rs) + off);
   }
   struct Row {
     uint32_t qw, gw;
@@ -729,8 +788,8 @@ __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, i
   auto load_row = [&](int j) {
     Row r;
     const int kl = j * 32 + 8 * kg;
-    r.qw = tb.q1[j * kMfQ1Stride + tc];
-    r.gw = tb.gw[j * kTileOut + tc];
+    r.qw = tb.q1[j * kMfWCols + i16];
+    r.gw = tb.gw[j * kMfWCols + i16];
     r.av = *reinterpret_cast<const uint4*>(&xr[kl]);
     r.cd = *reinterpret_cast<const uint4*>(&ch.cds[kl]);
     r.cn = *reinterpret_cast<const uint4*>(&ch.cns[kl]);
@@ -756,18 +815,25 @@ __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, i
     }
   }
 
-  // ---- salient columns, kMfSalWin at a time: both operands in registers (mf_salient_operands), one MFMA
-  for (int w0 = 0; w0 < num_sal; w0 += kMfSalWin) {
+  // ---- salient columns, kMfSalWin at a time: both operands in registers (mf_salient_operands), one MFMA.
+  // The first window uses the words loaded with the tile (no copy of them is made, so nothing waits for them
+  // before the window); later windows load their own.
+  if (num_sal > 0) {
+    f16x8 av, bv;
+    mf_salient_operands(ch, tb, xr, static_cast<uint32_t>(i16 * 4), rs_lane, kg, 0, (sbase0 & 31) + 8 * kg, q2w0, av,
+                        bv);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
+  }
+  for (int w0 = kMfSalWin; w0 < num_sal; w0 += kMfSalWin) {
     const int q2b = (sbase0 + w0) >> 5;  // qweight2_sparse row of the window's first salient column
-    if (w0 > 0) {
+    uint32_t q2w[2];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const bool rv = q2b + h < q2rows;
-        q2w[h] = bload32(r_q2, rv ? v_q2 : q2_bytes, static_cast<uint32_t>(rv ? q2b + h : 0) * N * 4u);
-      }
+    for (int h = 0; h < 2; ++h) {
+      const bool rv = q2b + h < q2rows;
+      q2w[h] = bload32(r_q2, rv ? v_q2 : q2_bytes, static_cast<uint32_t>(rv ? q2b + h : 0) * N * 4u);
     }
     f16x8 av, bv;
-    mf_salient_operands(ch, tb, xr, static_cast<uint32_t>(tc * 4), rs_lane, kg, w0,
+    mf_salient_operands(ch, tb, xr, static_cast<uint32_t>(i16 * 4), rs_lane, kg, w0,
                         ((sbase0 + w0) & 31) + 8 * kg, q2w, av, bv);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
   }
@@ -784,12 +850,16 @@ __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, i
 // Along a run the units compute from one weight buffer while the next tile's weight words are copied into
 // the other.  With more than one 512-column chunk (rank > 512) the chunk data is restaged per tile and
 // nothing is prefetched.
-// At most 128 VGPRs for one unit (no spills: checked with -Rpass-analysis=kernel-resource-usage), so four
-// wavefronts per SIMD fit: more workgroups resident to cover the weight-load latency of each tile.
-template <int kUnits>
-__global__ __launch_bounds__(kUnits * kMfThreads) __attribute__((amdgpu_waves_per_eu(4 / kUnits, 8)))
+// Registers are capped at what the LDS lets reside anyway: one unit with 4 staged rows fits four workgroups per CU
+// (128 VGPRs), with 16 rows three.
+// Every LDS array is a static object of its own (kRows activation rows staged: 4 when the batch has at most 4
+// rows, else 16).  The compiler then tells the arrays apart from the copy buffers, and an LDS read waits only
+// for copies into the buffer it reads; a read from dynamic LDS would wait for every copy in flight, the
+// prefetch included.
+template <int kUnits, int kRows>
+__global__ __launch_bounds__(kUnits * kMfThreads)
+__attribute__((amdgpu_waves_per_eu(kUnits == 2 ? 2 : (kRows == kMfRows ? 3 : 4), 8)))
 void grouped_mfma_kernel(MfmaArgs a) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char mf_lds[];
   const int unit = kUnits == 2 ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kMfThreads) : 0;
   const int utid = static_cast<int>(threadIdx.x) % kMfThreads;
   const MfmaProj& pa = a.proj[kUnits == 2 ? unit : blockIdx.z];
@@ -823,32 +893,42 @@ void grouped_mfma_kernel(MfmaArgs a) {
   }
   const int lane = utid % kWave;
   uint16_t* out = kUnits == 2 ? a.proj[0].out : pa.out;
-  const MfUnitLayout L = mf_unit_layout(a.xs_rows, a.lds_groups);
-  unsigned char* base = mf_lds + unit * L.bytes;
+  __shared__ __attribute__((aligned(16))) uint16_t mf_xs[kUnits][kRows * kMfXStride];
+  __shared__ __attribute__((aligned(16))) uint16_t mf_cds[kUnits][kMfChunk];
+  __shared__ __attribute__((aligned(16))) uint16_t mf_cns[kUnits][kMfChunk];
+  __shared__ __attribute__((aligned(16))) uint32_t mf_salw[kUnits][kMfChunk];
+  __shared__ __attribute__((aligned(16))) uint16_t mf_salxo[kUnits][kMfChunk];
+  __shared__ __attribute__((aligned(16))) uint32_t mf_salcp[kUnits][kMfChunk];
+  __shared__ __attribute__((aligned(16))) int32_t mf_meta[kUnits][16];
+  __shared__ __attribute__((aligned(16))) float mf_exch[kUnits == 2 ? kMfThreads * 4 : 4];
   MfChunk ch;
-  ch.xs = reinterpret_cast<uint16_t*>(base + L.xs);
-  ch.cds = reinterpret_cast<uint16_t*>(base + L.cds);
-  ch.cns = reinterpret_cast<uint16_t*>(base + L.cns);
+  ch.xs = &mf_xs[unit][0];
+  ch.cds = &mf_cds[unit][0];
+  ch.cns = &mf_cns[unit][0];
   ch.col_sal = nullptr;
   ch.sal_col = nullptr;
   ch.sal_xi = nullptr;
-  ch.sal_w = reinterpret_cast<uint32_t*>(base + L.sal_w);
-  ch.sal_xo = reinterpret_cast<uint16_t*>(base + L.sal_xo);
-  ch.sal_cp = reinterpret_cast<uint32_t*>(base + L.sal_cp);
-  ch.meta = reinterpret_cast<int32_t*>(base + L.meta);
-  __shared__ __attribute__((aligned(16))) uint32_t mf_tb0[kUnits][kMfTbWords];
-  __shared__ __attribute__((aligned(16))) uint32_t mf_tb1[kUnits][kMfTbWords];
-  MfTileBuf tb0, tb1;
-  tb0.q1 = &mf_tb0[unit][kMfTbQ1];
-  tb0.gw = &mf_tb0[unit][kMfTbGw];
-  tb0.rs = &mf_tb0[unit][kMfTbRs];
-  tb1.q1 = &mf_tb1[unit][kMfTbQ1];
-  tb1.gw = &mf_tb1[unit][kMfTbGw];
-  tb1.rs = &mf_tb1[unit][kMfTbRs];
-  float* exch = reinterpret_cast<float*>(mf_lds + kUnits * L.bytes);
+  ch.sal_w = &mf_salw[unit][0];
+  ch.sal_xo = &mf_salxo[unit][0];
+  ch.sal_cp = &mf_salcp[unit][0];
+  ch.meta = &mf_meta[unit][0];
+  // each wavefront's two copy buffers (two objects, so reads of one do not wait for copies into the other)
+  __shared__ __attribute__((aligned(16))) uint32_t mf_wb0[kUnits * kMfWaves][kMfWAlloc];
+  __shared__ __attribute__((aligned(16))) uint32_t mf_wb1[kUnits * kMfWaves][kMfWAlloc];
+  const int wave = __builtin_amdgcn_readfirstlane(utid / kWave);
+  const int wslot = unit * kMfWaves + wave;
+  const MfWaveBuf tb0{&mf_wb0[wslot][kMfWq1], &mf_wb0[wslot][kMfWgw], &mf_wb0[wslot][kMfWrs],
+                      &mf_wb0[wslot][kMfWWords]};
+  const MfWaveBuf tb1{&mf_wb1[wslot][kMfWq1], &mf_wb1[wslot][kMfWgw], &mf_wb1[wslot][kMfWrs],
+                      &mf_wb1[wslot][kMfWWords]};
+  if (lane == 0) {  // the zero words (the first row tile's barrier orders these writes before any read)
+    *tb0.zero = 0u;
+    *tb1.zero = 0u;
+  }
+  float* exch = mf_exch;
   // A operand row of this lane: rows >= rc hold stale values and only feed output rows that are not stored
   const int i16 = lane % 16;
-  const int xrow = i16 < a.xs_rows ? i16 : a.xs_rows - 1;
+  const int xrow = i16 < kRows ? i16 : kRows - 1;
   const int rank = p.rank;
   const bool one_chunk = rank <= kMfChunk;
   const int kg = lane / 16;
@@ -873,39 +953,74 @@ void grouped_mfma_kernel(MfmaArgs a) {
     continue;
   }
   if (rt != rt_first) __syncthreads();  // the previous row tile's LDS readers are done
+  const MfWaveOffsets wo = mf_wave_offsets(pa, 0, wave, lane);
   {  // chunk 0 and the first tile's weights
     MfRegs regs;
-    mf_tile_issue(pa, s, e, 0, ob_begin, utid, tb0);
+    mf_wave_tile_issue(pa, s, e, ob_begin, wo, lane, wave, tb0);
     mf_chunk_issue(pa, e, row0, rc, 0, utid, regs);
     mf_chunk_write(pa, rc, 0, utid, ch, regs);
     __builtin_amdgcn_s_waitcnt(0);  // LDS copies landed (all counters zero)
     __syncthreads();
   }
-  // One output tile, computed from `cur`; with one chunk the next tile's words are copied into `nxt`
-  // meanwhile.  Called with the two static buffers in alternation, so every instance knows which
-  // object it reads and which it fills.
-  auto tile = [&](int ob, const MfTileBuf& cur, const MfTileBuf& nxt) {
-    const int n = ob * kTileOut + 16 * (utid / kWave) + i16;
-    uint32_t q2w[2];
-    MfChunkMeta cm = mf_chunk_meta(ch);
-    mf_q2_issue(pa, e, n, cm, q2w);
-    if (one_chunk && ob + 1 < ob_end) mf_tile_issue(pa, s, e, 0, ob + 1, utid, nxt);  // prefetch
+  // One output tile, computed from `cur`; with one chunk each wavefront copies its columns of the next tile
+  // into `nxt` meanwhile.  Called with the two buffers in alternation, so every instance knows which object it
+  // reads and which it fills.  With one chunk and one unit the wavefronts do not wait for each other, and a
+  // tile's four output stores are issued by the next tile (or after the last), once that tile has issued its
+  // own loads and copies: nothing then waits for a store that has just been issued.  Each tile issues, after
+  // the copies of `cur` (the previous tile's prefetch), at least its two qweight2_sparse loads, its prefetch
+  // and the previous tile's stores, so waiting until no more than those are outstanding leaves `cur`'s copies
+  // landed (vector memory operations complete in issue order).  The first tile of a row tile finds its copies
+  // landed already.
+  constexpr int kAfterCopies = 2 + kMfWDma + (kUnits == 1 ? 4 : 0);
+  // one unit: the last tile's outputs (fp16 pairs of rows 4 kg .. 4 kg + 3) and the tile they belong to
+  uint32_t held01 = 0u, held23 = 0u;
+  int held_ob = -1;
+  const uint32_t out_bytes = static_cast<uint32_t>(rc) * N * 2u;
+  const __amdgpu_buffer_rsrc_t r_out = make_rsrc(out + static_cast<int64_t>(row0) * N, out_bytes);
+  auto store_held = [&]() {
+    const int hn = held_ob * kTileOut + 16 * wave + i16;
+    const uint32_t hv[4] = {held01 & 0xFFFFu, held01 >> 16, held23 & 0xFFFFu, held23 >> 16};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int r = 4 * kg + v;
+      __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(hv[v]), r_out,
+                                            hn < N && r < rc ? static_cast<uint32_t>(r * N + hn) * 2u : out_bytes,
+                                            0u, 0);
+    }
+  };
+  auto tile = [&](int ob, const MfWaveBuf& cur, const MfWaveBuf& nxt) {
+    const int n = ob * kTileOut + 16 * wave + i16;
     f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int kc = 0; kc < rank; kc += kMfChunk) {
-      if (!one_chunk && (ob > ob_begin || kc > 0)) {
-        __syncthreads();  // the previous chunk's readers are done
-        MfRegs regs;
-        mf_tile_issue(pa, s, e, kc, ob, utid, cur);
-        mf_chunk_issue(pa, e, row0, rc, kc, utid, regs);
-        mf_chunk_write(pa, rc, kc, utid, ch, regs);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        cm = mf_chunk_meta(ch);
+    // (the two cases keep separate qweight2_sparse words: a variable shared by both would be copied at their join,
+    // and the copy waits for the loads)
+    if (one_chunk) {
+      const MfChunkMeta cm = mf_chunk_meta(ch);
+      uint32_t q2w[2];
+      mf_q2_issue(pa, e, n, cm, q2w);
+      mf_wave_tile_issue(pa, s, e, ob + 1, wo, lane, wave, nxt);  // prefetch
+      if (kUnits == 1 && held_ob >= 0) store_held();  // the previous tile's outputs (wave-uniform condition)
+      wait_vmcnt<kAfterCopies>();  // this wavefront's copies into `cur` landed
+      acc = mf_compute(pa, e, 0, ob * kTileOut, xrow, utid, ch, cm, cur, q2w, acc);
+    } else {
+      for (int kc = 0; kc < rank; kc += kMfChunk) {
+        if (ob > ob_begin || kc > 0) {
+          __syncthreads();  // the previous chunk's readers are done
+          MfRegs regs;
+          mf_wave_tile_issue(pa, s, e, ob, mf_wave_offsets(pa, kc, wave, lane), lane, wave, cur);
+          mf_chunk_issue(pa, e, row0, rc, kc, utid, regs);
+          mf_chunk_write(pa, rc, kc, utid, ch, regs);
+          __builtin_amdgcn_s_waitcnt(0);
+          __syncthreads();
+        }
+        const MfChunkMeta cm = mf_chunk_meta(ch);
+        uint32_t q2w[2];
         mf_q2_issue(pa, e, n, cm, q2w);
+        acc = mf_compute(pa, e, kc, ob * kTileOut, xrow, utid, ch, cm, cur, q2w, acc);
       }
-      acc = mf_compute(pa, e, kc, ob * kTileOut, xrow, utid, ch, cm, cur, q2w, acc);
     }
 
+    // stores through a buffer resource over the tile's rows: rows past rc and columns past N go past its end and
+    // are dropped, so every lane issues all four
     const bool nv = n < N;
     if (kUnits == 2) {
       if (unit == 1) *reinterpret_cast<f32x4*>(&exch[utid * 4]) = acc;
@@ -915,33 +1030,38 @@ void grouped_mfma_kernel(MfmaArgs a) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int r = 4 * kg + v;
-          if (!nv || r >= rc) continue;
           // g and u rounded to fp16 as the two outputs would be
-          out[static_cast<int64_t>(row0 + r) * N + n] = swiglu_bits(f2h_bits(acc[v]), f2h_bits(up[v]));
+          __builtin_amdgcn_raw_buffer_store_b16(swiglu_bits(f2h_bits(acc[v]), f2h_bits(up[v])), r_out,
+                                                nv && r < rc ? static_cast<uint32_t>(r * N + n) * 2u : out_bytes,
+                                                0u, 0);
         }
       }
+      __syncthreads();  // exch is rewritten by the next tile
     } else {
       const float scale = (nv && p.has_output_scale) ? h2f(p.output_scale[static_cast<int64_t>(e) * N + n]) : 1.0f;
       const float bias = (nv && p.has_bias) ? h2f(p.bias[static_cast<int64_t>(e) * N + n]) : 0.0f;
+      uint32_t hv[4];
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int r = 4 * kg + v;
-        if (!nv || r >= rc) continue;
         float x = acc[v];
         if (p.has_output_scale) x = x * scale;
         if (p.has_bias) x = x + bias;
-        out[static_cast<int64_t>(row0 + r) * N + n] = f2h_bits(x);
+        hv[v] = f2h_bits(x);
       }
-    }
-    if (one_chunk) {
-      __builtin_amdgcn_s_waitcnt(0);  // the next tile's copies landed
-      __syncthreads();                // and every reader of this tile's buffer (and exch) is done
+      held01 = hv[0] | (hv[1] << 16);
+      held23 = hv[2] | (hv[3] << 16);
+      held_ob = ob;
+      if (!one_chunk) {
+        store_held();
+        held_ob = -1;
+      }
     }
   };
   for (int ob = ob_begin; ob < ob_end; ob += 2) {
     tile(ob, tb0, tb1);
     if (ob + 1 < ob_end) tile(ob + 1, tb1, tb0);
   }
+  if (kUnits == 1 && held_ob >= 0) store_held();  // the row tile's last outputs
   }  // row tiles
 }
 
@@ -1362,14 +1482,12 @@ __global__ __launch_bounds__(kUnits * kMfThreads) void grouped_mfma_ws_kernel(Mf
 int check_payload(const tris_compact3_payload* p, bool need_gr, const char* who);
 
 static bool allow_mfma_lds(const void* kernel, int bytes) {
-  // dynamic LDS granted so far per kernel (the four instantiations of the two kernels)
-  static const void* kernels[4] = {reinterpret_cast<const void*>(&grouped_mfma_kernel<1>),
-                                   reinterpret_cast<const void*>(&grouped_mfma_kernel<2>),
-                                   reinterpret_cast<const void*>(&grouped_mfma_ws_kernel<1, kWsSub>),
+  // dynamic LDS granted so far per kernel (the weight-stationary kernel's two instantiations)
+  static const void* kernels[2] = {reinterpret_cast<const void*>(&grouped_mfma_ws_kernel<1, kWsSub>),
                                    reinterpret_cast<const void*>(&grouped_mfma_ws_kernel<2, kWsSub>)};
-  static int granted[4] = {0, 0, 0, 0};
+  static int granted[2] = {0, 0};
   int which = 0;
-  while (which < 3 && kernels[which] != kernel) ++which;
+  while (which < 1 && kernels[which] != kernel) ++which;
   if (bytes <= granted[which]) return true;
   // Raising the dynamic LDS limit is not a stream operation, so it is safe while a caller captures a graph.
   if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
@@ -1455,9 +1573,6 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
   args.expert_ids = expert_ids;
   args.segment_offsets = segment_offsets;
   args.num_segments = num_segments;
-  args.xs_rows = batch < kMfRows ? batch : kMfRows;
-  args.lds_groups = pa->num_groups;
-  if (pb && pb->num_groups > args.lds_groups) args.lds_groups = pb->num_groups;
   const int units = swiglu ? 2 : 1;
   const int nproj = (pb && !swiglu) ? 2 : 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -1466,8 +1581,8 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
       ws_fits(pa) && (!pb || ws_fits(pb))) {
     return launch_grouped_mfma_ws(args, units, nproj, max_n, s, who);
   }
-  const int lds = mf_lds_bytes(units, args.xs_rows, args.lds_groups);
-  const int lds_total = lds + mf_static_lds_bytes(units);
+  const int rows = batch <= 4 ? 4 : kMfRows;  // staged activation rows: a row tile has at most min(16, batch)
+  const int lds_total = mf_static_lds_bytes(units, rows);
   TRIS_REQUIRE(lds_total <= 160 * 1024, "%s: LDS request %d exceeds a CU", who, lds_total);
   // Workgroups: as many as the GPU holds at once (LDS and the kernel's 128 VGPRs per lane, 4 wavefronts
   // per SIMD for one unit, bound them), shared by the projections of an unfused pair.
@@ -1482,13 +1597,17 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
   if (pairs < wgs) wgs = static_cast<int>(pairs);
   const dim3 grid(wgs > 0 ? wgs : 1, 1, nproj);
   if (swiglu) {
-    TRIS_REQUIRE(allow_mfma_lds(reinterpret_cast<const void*>(&grouped_mfma_kernel<2>), lds), "%s: %s", who,
-                 "cannot raise the kernel's dynamic LDS limit");
-    hipLaunchKernelGGL((grouped_mfma_kernel<2>), grid, dim3(2 * kMfThreads), lds, s, args);
+    if (rows == 4) {
+      hipLaunchKernelGGL((grouped_mfma_kernel<2, 4>), grid, dim3(2 * kMfThreads), 0, s, args);
+    } else {
+      hipLaunchKernelGGL((grouped_mfma_kernel<2, kMfRows>), grid, dim3(2 * kMfThreads), 0, s, args);
+    }
   } else {
-    TRIS_REQUIRE(allow_mfma_lds(reinterpret_cast<const void*>(&grouped_mfma_kernel<1>), lds), "%s: %s", who,
-                 "cannot raise the kernel's dynamic LDS limit");
-    hipLaunchKernelGGL((grouped_mfma_kernel<1>), grid, dim3(kMfThreads), lds, s, args);
+    if (rows == 4) {
+      hipLaunchKernelGGL((grouped_mfma_kernel<1, 4>), grid, dim3(kMfThreads), 0, s, args);
+    } else {
+      hipLaunchKernelGGL((grouped_mfma_kernel<1, kMfRows>), grid, dim3(kMfThreads), 0, s, args);
+    }
   }
   return check_launch(who);
 }
