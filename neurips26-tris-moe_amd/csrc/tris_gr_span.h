@@ -310,38 +310,52 @@ __device__ inline void gr_decode_block_group(const GrSpan<S>& sp, const GrTables
     const int nbytes = 4 * sp.nw;
     // words any lane of the wavefront holds (a group's first lane holds the most): the walks stop there
     const int maxw = wave_max_words<S>(sp.nw);
-    // ---- A: next-state fields of every byte, composed from every entry state
-    const auto next_fields = [&](int i) {
-      const uint32_t byte = (sp.w[i / 4] >> (8 * (i % 4))) & 0xFFu;
-      const uint32_t e = nxt[byte];
-      return i < nbytes ? e : kGrIdentityNext;
-    };
+    // Each phase walks the span a word at a time under a wave-uniform guard, and issues a word's four table
+    // reads together before any is used: one LDS round trip per word, not per byte.
+    // ---- A: next-state fields of every byte (kept for C), composed from every entry state
+    uint32_t f[kBytes];
     uint32_t c0 = 0u, c1 = 4u, c2 = 8u, c3 = 12u;
 #pragma unroll
-    for (int i = 0; i < kBytes; ++i) {
-      if (i / 4 < maxw) {
-        const uint32_t f = next_fields(i);
-        c0 = __builtin_amdgcn_ubfe(f, c0, 4);
-        c1 = __builtin_amdgcn_ubfe(f, c1, 4);
-        c2 = __builtin_amdgcn_ubfe(f, c2, 4);
-        c3 = __builtin_amdgcn_ubfe(f, c3, 4);
+    for (int wd = 0; wd < kMaxWords; ++wd) {
+      if (wd < maxw) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const int i = 4 * wd + b;
+          const uint32_t e = nxt[(sp.w[wd] >> (8 * b)) & 0xFFu];
+          f[i] = i < nbytes ? e : kGrIdentityNext;
+        }
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const uint32_t fi = f[4 * wd + b];
+          c0 = __builtin_amdgcn_ubfe(fi, c0, 4);
+          c1 = __builtin_amdgcn_ubfe(fi, c1, 4);
+          c2 = __builtin_amdgcn_ubfe(fi, c2, 4);
+          c3 = __builtin_amdgcn_ubfe(fi, c3, 4);
+        }
       }
     }
     // ---- B: the map of lanes 0..j, then the previous lane's (wave_shr:1) applied to state 0
     const uint32_t map = group_scan<S>(c0 | (c1 << 4) | (c2 << 8) | (c3 << 12), kGrIdentityNext, gr_map_compose);
     const uint32_t prev_map = dpp_mov<0x138, 0xF>(kGrIdentityNext, map);
     uint32_t st = j == 0 ? 0u : (prev_map & 15u);  // 4 * true entry state
-    // ---- C: entries along the true path (the next-state fields read again); F advance and codeword count
+    // ---- C: entries along the true path (the state chain runs on A's fields); F advance and codeword count
     // (packed adv | count << 16) from their high words, the masks read again for the emission
     uint32_t off[kBytes];
     uint32_t packed = 0u;
 #pragma unroll
-    for (int i = 0; i < kBytes; ++i) {
-      if (i / 4 < maxw) {
-        const uint32_t byte = (sp.w[i / 4] >> (8 * (i % 4))) & 0xFFu;
-        off[i] = i < nbytes ? (st << 9) + (byte << 3) : kGrZeroEntryOffset - gr_entry_base(k) * 8u;
-        st = __builtin_amdgcn_ubfe(next_fields(i), st, 4);
-        packed += *reinterpret_cast<const uint32_t*>(ent + off[i] + 4) >> 9;
+    for (int wd = 0; wd < kMaxWords; ++wd) {
+      if (wd < maxw) {
+        uint32_t hi[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const int i = 4 * wd + b;
+          const uint32_t byte = (sp.w[wd] >> (8 * b)) & 0xFFu;
+          off[i] = i < nbytes ? (st << 9) + (byte << 3) : kGrZeroEntryOffset - gr_entry_base(k) * 8u;
+          st = __builtin_amdgcn_ubfe(f[i], st, 4);
+          hi[b] = *reinterpret_cast<const uint32_t*>(ent + off[i] + 4);
+        }
+#pragma unroll
+        for (int b = 0; b < 4; ++b) packed += hi[b] >> 9;
       }
     }
     asm volatile("" ::: "memory");  // the emission reads the entries again rather than keeping 16 of them live
@@ -365,22 +379,31 @@ __device__ inline void gr_decode_block_group(const GrSpan<S>& sp, const GrTables
       if (k <= 2) {
         // k <= 2: a byte's mask is below 2^25 and its advance at most 32, so two bytes fit one 64-bit mask
 #pragma unroll
-        for (int i = 0; i < kBytes; i += 2) {
-          if (i / 4 < maxw) {
-            const uint2 e0 = *reinterpret_cast<const uint2*>(ent + off[i]);
-            const uint2 e1 = *reinterpret_cast<const uint2*>(ent + off[i + 1]);
-            const uint32_t a0 = __builtin_amdgcn_ubfe(e0.y, 9, 7);
-            emit(static_cast<uint64_t>(e0.x) | (static_cast<uint64_t>(e1.x) << a0));
-            posb += a0 + __builtin_amdgcn_ubfe(e1.y, 9, 7);
+        for (int wd = 0; wd < kMaxWords; ++wd) {
+          if (wd < maxw) {
+            uint2 e[4];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) e[b] = *reinterpret_cast<const uint2*>(ent + off[4 * wd + b]);
+#pragma unroll
+            for (int b = 0; b < 4; b += 2) {
+              const uint32_t a0 = __builtin_amdgcn_ubfe(e[b].y, 9, 7);
+              emit(static_cast<uint64_t>(e[b].x) | (static_cast<uint64_t>(e[b + 1].x) << a0));
+              posb += a0 + __builtin_amdgcn_ubfe(e[b + 1].y, 9, 7);
+            }
           }
         }
       } else {
 #pragma unroll
-        for (int i = 0; i < kBytes; ++i) {
-          if (i / 4 < maxw) {
-            const uint2 e = *reinterpret_cast<const uint2*>(ent + off[i]);
-            emit(static_cast<uint64_t>(e.y & 0x1FFu) << 32 | e.x);
-            posb += __builtin_amdgcn_ubfe(e.y, 9, 7);
+        for (int wd = 0; wd < kMaxWords; ++wd) {
+          if (wd < maxw) {
+            uint2 e[4];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) e[b] = *reinterpret_cast<const uint2*>(ent + off[4 * wd + b]);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+              emit(static_cast<uint64_t>(e[b].y & 0x1FFu) << 32 | e[b].x);
+              posb += __builtin_amdgcn_ubfe(e[b].y, 9, 7);
+            }
           }
         }
       }
