@@ -198,8 +198,14 @@ constexpr int kMfTbRs = kMfTbGw + kMfPR * kTileOut;
 constexpr int kMfTbWords = kMfTbRs + kTileOut * kMfMaxGroups * 2;
 static_assert(kMfTbGw % 4 == 0 && kMfTbRs % 4 == 0, "tile buffer pieces must be 16-byte aligned");
 constexpr int kMfCus = 256;  // MI355X compute units
+// Decode kernel: row-scale groups and salient slots per chunk its LDS holds; the compact variant (at most 4
+// groups and 64 salient columns per expert) fits four workgroups per CU.
+constexpr int mf_groups_cap(bool compact) { return compact ? 4 : kMfMaxGroups; }
+constexpr int mf_sal_slots(bool compact) { return compact ? 64 : kMfChunk; }
 // per wavefront and copy buffer: qweight1 and split words of 16 columns, their row-scale block and a zero word
-constexpr int kMfWAllocBytes = (2 * (kMfChunk / 32) * 16 + 16 * kMfMaxGroups * 2 + 4) * 4;
+constexpr int mf_wave_alloc_bytes(bool compact) {
+  return (2 * (kMfChunk / 32) * 16 + 16 * mf_groups_cap(compact) * 2 + 4) * 4;
+}
 constexpr int kMfRuns = kMfRows * (kMfChunk / 8) / kMfThreads;  // activation runs per thread of a unit
 
 constexpr int kMfExchBytes = kMfThreads * 4 * 4;  // SwiGLU: the up unit's accumulators for the gate unit
@@ -212,8 +218,9 @@ __host__ __device__ inline int mf_take(int* o, int b) {
 }
 
 // Static LDS of the decode kernel with `units` units and `rows` staged activation rows (as declared there).
-constexpr int mf_static_lds_bytes(int units, int rows) {
-  return units * (rows * kMfXStride * 2 + kMfChunk * (2 + 2 + 4 + 2 + 4) + 16 * 4 + 2 * kMfWaves * kMfWAllocBytes) +
+constexpr int mf_static_lds_bytes(int units, int rows, bool compact) {
+  return units * (rows * kMfXStride * 2 + kMfChunk * (2 + 2) + mf_sal_slots(compact) * (4 + 2 + 4) + 16 * 4 +
+                  2 * kMfWaves * mf_wave_alloc_bytes(compact)) +
          (units == 2 ? kMfExchBytes : 16);
 }
 
@@ -248,10 +255,16 @@ constexpr int kMfWCols = 16;
 constexpr int kMfWq1 = 0;
 constexpr int kMfWgw = kMfPR * kMfWCols;
 constexpr int kMfWrs = 2 * kMfPR * kMfWCols;
-constexpr int kMfWWords = kMfWrs + kMfWCols * kMfMaxGroups * 2;
-constexpr int kMfWDma = kMfWWords / kWave;
-constexpr int kMfWAlloc = kMfWWords + 4;  // + a zero word that no copy writes (read for K tiles without a group)
-static_assert(kMfWWords % kWave == 0 && kMfWgw % kWave == 0 && kMfWrs % kWave == 0, "whole 64-lane copies");
+template <bool kCompact>
+struct MfWaveWords {
+  static constexpr int kRsCopies = kMfWCols * mf_groups_cap(kCompact) * 2 / kWave;
+  static constexpr int kWords = kMfWrs + kRsCopies * kWave;
+  static constexpr int kDma = kWords / kWave;
+  static constexpr int kAlloc = kWords + 4;  // + a zero word that no copy writes (read for K tiles without a group)
+  static_assert(kMfWCols * mf_groups_cap(kCompact) * 2 % kWave == 0 && kMfWgw % kWave == 0 && kMfWrs % kWave == 0,
+                "whole 64-lane copies");
+  static_assert(kAlloc * 4 == mf_wave_alloc_bytes(kCompact), "LDS accounting");
+};
 struct MfWaveBuf {     // one wavefront's copy of its 16 columns' words
   uint32_t* q1;        // [kMfPR][16]
   uint32_t* gw;        // [kMfPR][16]
@@ -389,7 +402,7 @@ __device__ __forceinline__ void mf_chunk_issue(const MfmaProj& pa, int e, int ro
 // Write a unit's register-staged chunk to LDS (waits for those loads).  Salient columns get zero
 // C_d / C_nd, so the main pass gives them zero weights whatever their selector bits.
 __device__ __forceinline__ void mf_chunk_write(const MfmaProj& pa, int rc, int kc, int utid, const MfChunk& ch,
-                                               const MfRegs& R, bool natural = false) {
+                                               const MfRegs& R, bool natural = false, int sal_cap = kMfChunk) {
   const tris_compact3_payload& p = pa.p;
   const int rank = p.rank;
   const int G = p.num_groups;
@@ -428,7 +441,7 @@ __device__ __forceinline__ void mf_chunk_write(const MfmaProj& pa, int rc, int k
         ch.sal_col[q] = static_cast<uint16_t>(j);
         ch.sal_xi[q] = static_cast<uint16_t>((j & ~31) + mf_perm32(j & 31));
         ch.sal_cp[q] = static_cast<uint32_t>(R.cpv[h]);
-      } else {
+      } else if (q >= 0 && q < sal_cap) {
         // the column's group as the main pass takes it (uniform 64-column groups); an invalid group gives
         // zero factors, as a K tile without a group does
         const bool gv = R.gt[h] >= 0 && R.gt[h] < G;
@@ -443,7 +456,7 @@ __device__ __forceinline__ void mf_chunk_write(const MfmaProj& pa, int rc, int k
     // padding slots up to the last window's end read the zero activation column with zero factors
     const int nsal = R.send - R.sbase0;
     const int q = nsal + utid;
-    if (utid < kMfSalWin && q < ((nsal + kMfSalWin - 1) & ~(kMfSalWin - 1))) {
+    if (utid < kMfSalWin && q >= 0 && q < sal_cap && q < ((nsal + kMfSalWin - 1) & ~(kMfSalWin - 1))) {
       ch.sal_w[q] = 0u;
       ch.sal_xo[q] = static_cast<uint16_t>(kMfChunk * 2);
       ch.sal_cp[q] = 0x80008000u;
@@ -521,10 +534,11 @@ __device__ __forceinline__ MfWaveOffsets mf_wave_offsets(const MfmaProj& pa, int
 
 // The wavefront's LDS copies of its 16 columns of output tile ob for chunk kc: qweight1 and split words of the
 // chunk's packed rows (lane l of copy i: packed row 4 i + l / 16, column l % 16) and the columns' row-scale block.
-// Always kMfWDma copies.  Nothing is masked: every offset is checked against its buffer's size (past it reads
+// Always MfWaveWords<kCompact>::kDma copies.  Nothing is masked: every offset is checked against its buffer's size (past it reads
 // zeros), and what lies inside it but past the chunk's rows or past column N (the next row's words, the next
 // tile's block) only feeds packed rows the compute skips or output columns that are not stored.  So ob may be
 // one past the last tile (a prefetch with nothing to fetch).
+template <bool kCompact>
 __device__ __forceinline__ void mf_wave_tile_issue(const MfmaProj& pa, int s, int e, int ob, const MfWaveOffsets& o,
                                                    int lane, int wave, const MfWaveBuf& wb) {
   const tris_compact3_payload& p = pa.p;
@@ -551,7 +565,7 @@ __device__ __forceinline__ void mf_wave_tile_issue(const MfmaProj& pa, int s, in
   const __amdgpu_buffer_rsrc_t r_rs =
       make_rsrc(p.row_pack3 + (static_cast<int64_t>(e) * N + (ncols > 0 ? n0 : 0)) * G, rs_bytes);
 #pragma unroll
-  for (int i = 0; i < kMfWCols * kMfMaxGroups * 2 / kWave; ++i) {
+  for (int i = 0; i < MfWaveWords<kCompact>::kRsCopies; ++i) {
     dma32(r_rs, wb.rs + i * kWave, static_cast<uint32_t>(i * kWave + lane) * 4u, 0u);
   }
 }
@@ -856,10 +870,12 @@ __device__ __forceinline__ f32x4 mf_compute(const MfmaProj& pa, int e, int kc, i
 // rows, else 16).  The compiler then tells the arrays apart from the copy buffers, and an LDS read waits only
 // for copies into the buffer it reads; a read from dynamic LDS would wait for every copy in flight, the
 // prefetch included.
-template <int kUnits, int kRows>
+template <int kUnits, int kRows, bool kCompact>
 __global__ __launch_bounds__(kUnits * kMfThreads)
-__attribute__((amdgpu_waves_per_eu(kUnits == 2 ? 2 : (kRows == kMfRows ? 3 : 4), 8)))
+__attribute__((amdgpu_waves_per_eu(kUnits == 2 ? 2 : (kRows == kMfRows && !kCompact ? 3 : 4), 8)))
 void grouped_mfma_kernel(MfmaArgs a) {
+  using WW = MfWaveWords<kCompact>;
+  constexpr int kSal = mf_sal_slots(kCompact);
   const int unit = kUnits == 2 ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kMfThreads) : 0;
   const int utid = static_cast<int>(threadIdx.x) % kMfThreads;
   const MfmaProj& pa = a.proj[kUnits == 2 ? unit : blockIdx.z];
@@ -896,9 +912,9 @@ void grouped_mfma_kernel(MfmaArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t mf_xs[kUnits][kRows * kMfXStride];
   __shared__ __attribute__((aligned(16))) uint16_t mf_cds[kUnits][kMfChunk];
   __shared__ __attribute__((aligned(16))) uint16_t mf_cns[kUnits][kMfChunk];
-  __shared__ __attribute__((aligned(16))) uint32_t mf_salw[kUnits][kMfChunk];
-  __shared__ __attribute__((aligned(16))) uint16_t mf_salxo[kUnits][kMfChunk];
-  __shared__ __attribute__((aligned(16))) uint32_t mf_salcp[kUnits][kMfChunk];
+  __shared__ __attribute__((aligned(16))) uint32_t mf_salw[kUnits][kSal];
+  __shared__ __attribute__((aligned(16))) uint16_t mf_salxo[kUnits][kSal];
+  __shared__ __attribute__((aligned(16))) uint32_t mf_salcp[kUnits][kSal];
   __shared__ __attribute__((aligned(16))) int32_t mf_meta[kUnits][16];
   __shared__ __attribute__((aligned(16))) float mf_exch[kUnits == 2 ? kMfThreads * 4 : 4];
   MfChunk ch;
@@ -913,14 +929,14 @@ void grouped_mfma_kernel(MfmaArgs a) {
   ch.sal_cp = &mf_salcp[unit][0];
   ch.meta = &mf_meta[unit][0];
   // each wavefront's two copy buffers (two objects, so reads of one do not wait for copies into the other)
-  __shared__ __attribute__((aligned(16))) uint32_t mf_wb0[kUnits * kMfWaves][kMfWAlloc];
-  __shared__ __attribute__((aligned(16))) uint32_t mf_wb1[kUnits * kMfWaves][kMfWAlloc];
+  __shared__ __attribute__((aligned(16))) uint32_t mf_wb0[kUnits * kMfWaves][WW::kAlloc];
+  __shared__ __attribute__((aligned(16))) uint32_t mf_wb1[kUnits * kMfWaves][WW::kAlloc];
   const int wave = __builtin_amdgcn_readfirstlane(utid / kWave);
   const int wslot = unit * kMfWaves + wave;
   const MfWaveBuf tb0{&mf_wb0[wslot][kMfWq1], &mf_wb0[wslot][kMfWgw], &mf_wb0[wslot][kMfWrs],
-                      &mf_wb0[wslot][kMfWWords]};
+                      &mf_wb0[wslot][WW::kWords]};
   const MfWaveBuf tb1{&mf_wb1[wslot][kMfWq1], &mf_wb1[wslot][kMfWgw], &mf_wb1[wslot][kMfWrs],
-                      &mf_wb1[wslot][kMfWWords]};
+                      &mf_wb1[wslot][WW::kWords]};
   if (lane == 0) {  // the zero words (the first row tile's barrier orders these writes before any read)
     *tb0.zero = 0u;
     *tb1.zero = 0u;
@@ -956,9 +972,9 @@ void grouped_mfma_kernel(MfmaArgs a) {
   const MfWaveOffsets wo = mf_wave_offsets(pa, 0, wave, lane);
   {  // chunk 0 and the first tile's weights
     MfRegs regs;
-    mf_wave_tile_issue(pa, s, e, ob_begin, wo, lane, wave, tb0);
+    mf_wave_tile_issue<kCompact>(pa, s, e, ob_begin, wo, lane, wave, tb0);
     mf_chunk_issue(pa, e, row0, rc, 0, utid, regs);
-    mf_chunk_write(pa, rc, 0, utid, ch, regs);
+    mf_chunk_write(pa, rc, 0, utid, ch, regs, false, kSal);
     __builtin_amdgcn_s_waitcnt(0);  // LDS copies landed (all counters zero)
     __syncthreads();
   }
@@ -971,7 +987,14 @@ void grouped_mfma_kernel(MfmaArgs a) {
   // and the previous tile's stores, so waiting until no more than those are outstanding leaves `cur`'s copies
   // landed (vector memory operations complete in issue order).  The first tile of a row tile finds its copies
   // landed already.
-  constexpr int kAfterCopies = 2 + kMfWDma + (kUnits == 1 ? 4 : 0);
+  constexpr int kAfterCopies = 2 + WW::kDma + (kUnits == 1 ? 4 : 0);
+  // the staged chunk's metadata, its salient count held to the slots staged (a payload whose prefix counts
+  // disagree with its salient map reads no slot past them)
+  const auto chunk_meta = [&]() {
+    MfChunkMeta m = mf_chunk_meta(ch);
+    m.num_sal = m.num_sal < 0 ? 0 : (m.num_sal < kSal ? m.num_sal : kSal);
+    return m;
+  };
   // one unit: the last tile's outputs (fp16 pairs of rows 4 kg .. 4 kg + 3) and the tile they belong to
   uint32_t held01 = 0u, held23 = 0u;
   int held_ob = -1;
@@ -994,10 +1017,10 @@ void grouped_mfma_kernel(MfmaArgs a) {
     // (the two cases keep separate qweight2_sparse words: a variable shared by both would be copied at their join,
     // and the copy waits for the loads)
     if (one_chunk) {
-      const MfChunkMeta cm = mf_chunk_meta(ch);
+      const MfChunkMeta cm = chunk_meta();
       uint32_t q2w[2];
       mf_q2_issue(pa, e, n, cm, q2w);
-      mf_wave_tile_issue(pa, s, e, ob + 1, wo, lane, wave, nxt);  // prefetch
+      mf_wave_tile_issue<kCompact>(pa, s, e, ob + 1, wo, lane, wave, nxt);  // prefetch
       if (kUnits == 1 && held_ob >= 0) store_held();  // the previous tile's outputs (wave-uniform condition)
       wait_vmcnt<kAfterCopies>();  // this wavefront's copies into `cur` landed
       acc = mf_compute(pa, e, 0, ob * kTileOut, xrow, utid, ch, cm, cur, q2w, acc);
@@ -1006,13 +1029,13 @@ void grouped_mfma_kernel(MfmaArgs a) {
         if (ob > ob_begin || kc > 0) {
           __syncthreads();  // the previous chunk's readers are done
           MfRegs regs;
-          mf_wave_tile_issue(pa, s, e, ob, mf_wave_offsets(pa, kc, wave, lane), lane, wave, cur);
+          mf_wave_tile_issue<kCompact>(pa, s, e, ob, mf_wave_offsets(pa, kc, wave, lane), lane, wave, cur);
           mf_chunk_issue(pa, e, row0, rc, kc, utid, regs);
-          mf_chunk_write(pa, rc, kc, utid, ch, regs);
+          mf_chunk_write(pa, rc, kc, utid, ch, regs, false, kSal);
           __builtin_amdgcn_s_waitcnt(0);
           __syncthreads();
         }
-        const MfChunkMeta cm = mf_chunk_meta(ch);
+        const MfChunkMeta cm = chunk_meta();
         uint32_t q2w[2];
         mf_q2_issue(pa, e, n, cm, q2w);
         acc = mf_compute(pa, e, kc, ob * kTileOut, xrow, utid, ch, cm, cur, q2w, acc);
@@ -1582,7 +1605,16 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
     return launch_grouped_mfma_ws(args, units, nproj, max_n, s, who);
   }
   const int rows = batch <= 4 ? 4 : kMfRows;  // staged activation rows: a row tile has at most min(16, batch)
-  const int lds_total = mf_static_lds_bytes(units, rows);
+  // the compact LDS layout (four workgroups per CU): at most 4 row-scale groups and 64 salient columns per expert,
+  // and rank <= 256, where a tile's work is short enough that the fourth workgroup's latency hiding pays (at
+  // rank 512 the 128-register cap and the coarser tile split cost more: measured on MI355X, OLMoE T=16 77 -> 73 us,
+  // Mixtral T=16 92.9 -> 95.5 us)
+  const auto compact_ok = [](const tris_compact3_payload* p) {
+    return p->num_groups <= mf_groups_cap(true) && p->qweight2_sparse_rows * kMfSalWin <= mf_sal_slots(true) &&
+           p->rank <= kMfChunk / 2;
+  };
+  const bool compact = compact_ok(pa) && (!pb || compact_ok(pb));
+  const int lds_total = mf_static_lds_bytes(units, rows, compact);
   TRIS_REQUIRE(lds_total <= 160 * 1024, "%s: LDS request %d exceeds a CU", who, lds_total);
   // Workgroups: as many as the GPU holds at once (LDS and the kernel's 128 VGPRs per lane, 4 wavefronts
   // per SIMD for one unit, bound them), shared by the projections of an unfused pair.
@@ -1596,19 +1628,22 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
       (static_cast<int64_t>(batch) / kMfRows + (num_segments < batch ? num_segments : batch)) * ceil_div(max_n, kTileOut);
   if (pairs < wgs) wgs = static_cast<int>(pairs);
   const dim3 grid(wgs > 0 ? wgs : 1, 1, nproj);
+  const dim3 block(units * kMfThreads);
+#define TRIS_MF_LAUNCH(U, ROWS, C) hipLaunchKernelGGL((grouped_mfma_kernel<U, ROWS, C>), grid, block, 0, s, args)
   if (swiglu) {
     if (rows == 4) {
-      hipLaunchKernelGGL((grouped_mfma_kernel<2, 4>), grid, dim3(2 * kMfThreads), 0, s, args);
+      if (compact) TRIS_MF_LAUNCH(2, 4, true); else TRIS_MF_LAUNCH(2, 4, false);
     } else {
-      hipLaunchKernelGGL((grouped_mfma_kernel<2, kMfRows>), grid, dim3(2 * kMfThreads), 0, s, args);
+      if (compact) TRIS_MF_LAUNCH(2, kMfRows, true); else TRIS_MF_LAUNCH(2, kMfRows, false);
     }
   } else {
     if (rows == 4) {
-      hipLaunchKernelGGL((grouped_mfma_kernel<1, 4>), grid, dim3(kMfThreads), 0, s, args);
+      if (compact) TRIS_MF_LAUNCH(1, 4, true); else TRIS_MF_LAUNCH(1, 4, false);
     } else {
-      hipLaunchKernelGGL((grouped_mfma_kernel<1, kMfRows>), grid, dim3(kMfThreads), 0, s, args);
+      if (compact) TRIS_MF_LAUNCH(1, kMfRows, true); else TRIS_MF_LAUNCH(1, kMfRows, false);
     }
   }
+#undef TRIS_MF_LAUNCH
   return check_launch(who);
 }
 
