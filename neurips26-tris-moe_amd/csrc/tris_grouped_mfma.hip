@@ -536,11 +536,13 @@ __device__ __forceinline__ MfWaveOffsets mf_wave_offsets(const MfmaProj& pa, int
 // chunk's packed rows (lane l of copy i: packed row 4 i + l / 16, column l % 16) and the columns' row-scale block.
 // Always MfWaveWords<kCompact>::kDma copies.  Nothing is masked: every offset is checked against its buffer's size (past it reads
 // zeros), and what lies inside it but past the chunk's rows or past column N (the next row's words, the next
-// tile's block) only feeds packed rows the compute skips or output columns that are not stored.  So ob may be
-// one past the last tile (a prefetch with nothing to fetch).
+// tile's block) only feeds packed rows the compute skips or output columns that are not stored.  valid = false
+// (a prefetch with no tile to fetch, wave-uniform) empties the buffer ranges, so every copy reads zeros without a
+// memory access: a workgroup does not fetch the tile after its run, which another workgroup reads (likely through
+// another XCD's L2).
 template <bool kCompact>
 __device__ __forceinline__ void mf_wave_tile_issue(const MfmaProj& pa, int s, int e, int ob, const MfWaveOffsets& o,
-                                                   int lane, int wave, const MfWaveBuf& wb) {
+                                                   int lane, int wave, const MfWaveBuf& wb, bool valid = true) {
   const tris_compact3_payload& p = pa.p;
   const int N = p.outfeatures;
   const int G = p.num_groups;
@@ -549,24 +551,27 @@ __device__ __forceinline__ void mf_wave_tile_issue(const MfmaProj& pa, int s, in
   const int nblk = (packed_rows / 2) * nob;
   const uint32_t q1_bytes = static_cast<uint32_t>(packed_rows) * N * 4u;
   const uint32_t dec_bytes = static_cast<uint32_t>(nblk) * kGrWords * 4u;
-  const __amdgpu_buffer_rsrc_t r_q1 = make_rsrc(p.qweight1 + static_cast<int64_t>(e) * packed_rows * N, q1_bytes);
+  const __amdgpu_buffer_rsrc_t r_q1 =
+      make_rsrc(p.qweight1 + static_cast<int64_t>(e) * packed_rows * N, valid ? q1_bytes : 0u);
   const __amdgpu_buffer_rsrc_t r_dec =
-      make_rsrc(pa.decoded + static_cast<int64_t>(s) * nblk * kGrWords, dec_bytes);
+      make_rsrc(pa.decoded + static_cast<int64_t>(s) * nblk * kGrWords, valid ? dec_bytes : 0u);
 #pragma unroll
   for (int i = 0; i < kMfPR / 4; ++i) {
     dma32(r_q1, wb.q1 + i * kWave, o.q1 + static_cast<uint32_t>(4 * i * N + ob * kTileOut) * 4u, 0u);
     dma32(r_dec, wb.gw + i * kWave, o.dec + static_cast<uint32_t>((2 * i * nob + ob) * kGrWords) * 4u, 0u);
   }
-  // row_pack3[e][n0 .. n0 + 15][0 .. G - 1] is one contiguous run of 16 G pairs; the copies past it read the next
-  // columns' words (unused) or zeros past the expert
+  // row_pack3[e][n0 .. n0 + 15][0 .. G - 1] is one contiguous run of 16 G pairs (32 G words); a lane past it reads
+  // zeros without a memory access (an offset past the buffer), as do columns past the expert
   const int n0 = ob * kTileOut + kMfWCols * wave;
-  const int ncols = N - n0;
+  const int ncols = valid ? N - n0 : 0;
   const uint32_t rs_bytes = ncols > 0 ? static_cast<uint32_t>(ncols) * G * 8u : 0u;
   const __amdgpu_buffer_rsrc_t r_rs =
       make_rsrc(p.row_pack3 + (static_cast<int64_t>(e) * N + (ncols > 0 ? n0 : 0)) * G, rs_bytes);
+  const int rs_words = kMfWCols * 2 * G;
 #pragma unroll
   for (int i = 0; i < MfWaveWords<kCompact>::kRsCopies; ++i) {
-    dma32(r_rs, wb.rs + i * kWave, static_cast<uint32_t>(i * kWave + lane) * 4u, 0u);
+    const int w = i * kWave + lane;
+    dma32(r_rs, wb.rs + i * kWave, w < rs_words ? static_cast<uint32_t>(w) * 4u : rs_bytes, 0u);
   }
 }
 
@@ -1020,7 +1025,7 @@ void grouped_mfma_kernel(MfmaArgs a) {
       const MfChunkMeta cm = chunk_meta();
       uint32_t q2w[2];
       mf_q2_issue(pa, e, n, cm, q2w);
-      mf_wave_tile_issue<kCompact>(pa, s, e, ob + 1, wo, lane, wave, nxt);  // prefetch
+      mf_wave_tile_issue<kCompact>(pa, s, e, ob + 1, wo, lane, wave, nxt, ob + 1 < ob_end);  // prefetch
       if (kUnits == 1 && held_ob >= 0) store_held();  // the previous tile's outputs (wave-uniform condition)
       wait_vmcnt<kAfterCopies>();  // this wavefront's copies into `cur` landed
       acc = mf_compute(pa, e, 0, ob * kTileOut, xrow, utid, ch, cm, cur, q2w, acc);
