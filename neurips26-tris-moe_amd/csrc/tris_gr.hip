@@ -15,7 +15,8 @@
 namespace tris {
 
 constexpr int kSpanThreads = 256;
-constexpr int kSpanWgTarget = 1024;  // persistent workgroups per launch: at most four per CU
+constexpr int kSpanWaves = kSpanThreads / kWave;
+constexpr int kSpanWgTarget = 1280;  // persistent workgroups per launch: five per CU (LDS and VGPRs allow five)
 
 // One projection's stream; jobs of one launch share the routed expert list.
 struct GrJob {
@@ -35,10 +36,12 @@ struct GrJobs {
   GrJob job[TRIS_MAX_PREDECODE_JOBS];
 };
 
-// Work items: (job, slot, batch of kSpanThreads / S blocks), job-major, then slot, then batch.  The grid is
-// persistent over them: a workgroup copies the tables and the slots' expert ids to LDS once, then takes items
-// blockIdx.x, blockIdx.x + gridDim.x, ...; the next item's block headers are loaded before the current item
-// is decoded and its span words after, so their latency overlaps the decode.
+// Work items: (job, slot, batch of kWave / S blocks), job-major, then slot, then batch; an item is one
+// wavefront's.  The grid is persistent over them: a workgroup copies the tables and the slots' expert ids to
+// LDS once, then each wavefront takes items on its own (no workgroup barrier after the copy): it zeroes its
+// blocks' LDS bitmaps, decodes them and stores them with 16-byte stores.  The next item's block headers are
+// loaded before the current item is decoded and its span words after, so their latency overlaps the decode;
+// the first item's headers are loaded before the table copy.
 struct GrWork {
   int num_jobs;
   int num_slots;
@@ -53,7 +56,7 @@ struct GrReduce {
   int blocks_per_proj;
 };
 
-constexpr int kSpanLdsSlots = 1024;  // expert ids staged in LDS (later slots read from memory)
+constexpr int kSpanLdsSlots = 256;  // expert ids staged in LDS (later slots read from memory)
 
 template <int S>
 struct GrItem {
@@ -65,7 +68,7 @@ struct GrItem {
 template <int S>
 __device__ __forceinline__ void gr_item_header(const GrJobs& jobs, const GrWork& wk, const int32_t* __restrict__ eids,
                                                const int32_t* __restrict__ expert_ids, int w, int g, GrItem<S>& it) {
-  constexpr int kBlocksPerWg = kSpanThreads / S;
+  constexpr int kBlocksPerItem = kWave / S;
   const bool exists = w < wk.first[wk.num_jobs];
   const int wv = exists ? w : 0;
   int q = 0;
@@ -73,11 +76,11 @@ __device__ __forceinline__ void gr_item_header(const GrJobs& jobs, const GrWork&
   for (int i = 1; i < TRIS_MAX_PREDECODE_JOBS; ++i) q += (i < wk.num_jobs && wv >= wk.first[i]) ? 1 : 0;
   const GrJob& jb = jobs.job[q];
   const int nblk = jb.nblk;
-  const int batches = ceil_div(nblk, kBlocksPerWg);
+  const int batches = ceil_div(nblk, kBlocksPerItem);
   const int local = wv - wk.first[q];
   it.q = q;
   it.slot = local / batches;
-  it.block0 = (local - it.slot * batches) * kBlocksPerWg;
+  it.block0 = (local - it.slot * batches) * kBlocksPerItem;
   const int expert = it.slot < kSpanLdsSlots ? eids[it.slot] : expert_ids[it.slot];
   const bool ev = exists && expert >= 0 && expert < jb.num_experts;
   const int ex = ev ? expert : 0;
@@ -90,7 +93,9 @@ template <int S>
 __global__ __launch_bounds__(kSpanThreads) void gr_decode_span_kernel(GrJobs jobs, GrWork wk,
                                                                       const int32_t* __restrict__ expert_ids,
                                                                       GrReduce red) {
-  constexpr int kBlocksPerWg = kSpanThreads / S;
+  constexpr int kBlocksPerItem = kWave / S;
+  constexpr int kItemVec4 = kBlocksPerItem * kGrWords / 4;
+  static_assert(kGrBlockStride % 4 == 0 && kGrPadFront % 4 == 0, "16-byte aligned block bitmaps");
   if (static_cast<int>(blockIdx.x) >= wk.decode_wgs) {
     const int rb = static_cast<int>(blockIdx.x) - wk.decode_wgs;
     const int q = rb / red.blocks_per_proj;
@@ -98,57 +103,67 @@ __global__ __launch_bounds__(kSpanThreads) void gr_decode_span_kernel(GrJobs job
     return;
   }
   __shared__ GrTables tab;
-  __shared__ uint32_t outb[kBlocksPerWg][kGrBlockStride];
+  __shared__ __attribute__((aligned(16))) uint32_t outb[kSpanWaves][kBlocksPerItem * kGrBlockStride];
   __shared__ int32_t eids[kSpanLdsSlots];
   const int total = wk.first[wk.num_jobs];
-  int w = blockIdx.x;
-  if (w >= total) return;  // uniform over the workgroup
   const int tid = threadIdx.x;
-  const int g = tid / S;
-  const int j = tid % S;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int g = lane / S;
+  const int j = lane % S;
+  const int stride = wk.decode_wgs * kSpanWaves;
+  int w = static_cast<int>(blockIdx.x) * kSpanWaves + wave;
+  GrItem<S> cur;
+  gr_item_header<S>(jobs, wk, expert_ids, expert_ids, w, g, cur);  // in flight during the copies below
   const int nl = wk.num_slots < kSpanLdsSlots ? wk.num_slots : kSpanLdsSlots;
   for (int i = tid; i < nl; i += kSpanThreads) eids[i] = expert_ids[i];
   gr_tables_to_lds(&tab);
-  __syncthreads();
-  GrItem<S> cur;
-  gr_item_header<S>(jobs, wk, eids, expert_ids, w, g, cur);
   gr_span_words<S>(cur.sp, j);
-  for (; w < total; w += wk.decode_wgs) {
-    for (int idx = tid; idx < kBlocksPerWg * kGrBlockStride; idx += kSpanThreads) {
-      outb[idx / kGrBlockStride][idx % kGrBlockStride] = 0u;
-    }
-    __syncthreads();
+  __syncthreads();
+  uint32_t* ob = outb[wave];
+  for (; w < total; w += stride) {
+    uint4* z = reinterpret_cast<uint4*>(ob);
+    for (int q = lane; q < kBlocksPerItem * kGrBlockStride / 4; q += kWave) z[q] = make_uint4(0u, 0u, 0u, 0u);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
     GrItem<S> nx;
-    gr_item_header<S>(jobs, wk, eids, expert_ids, w + wk.decode_wgs, g, nx);
-    gr_decode_block_group<S>(cur.sp, &tab, outb[g] + kGrPadFront, j);
+    gr_item_header<S>(jobs, wk, eids, expert_ids, w + stride, g, nx);
+    gr_decode_block_group<S>(cur.sp, &tab, ob + g * kGrBlockStride + kGrPadFront, j);
     gr_span_words<S>(nx.sp, j);
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
     const GrJob& jb = jobs.job[cur.q];
     const int nblk = jb.nblk;
     const int block0 = cur.block0;
     const int slot = cur.slot;
     if (jb.dense_rows == 0) {
-      int32_t* dst = jb.out + (static_cast<int64_t>(slot) * nblk + block0) * kGrWords;
-      for (int idx = tid; idx < kBlocksPerWg * kGrWords; idx += kSpanThreads) {
-        if (block0 + idx / kGrWords < nblk) {
-          dst[idx] = static_cast<int32_t>(outb[idx / kGrWords][kGrPadFront + idx % kGrWords]);
+      // the item's blocks are consecutive in [slot][block][128]: one contiguous run of 16-byte stores
+      uint4* dst = reinterpret_cast<uint4*>(jb.out + (static_cast<int64_t>(slot) * nblk + block0) * kGrWords);
+#pragma unroll
+      for (int q = lane; q < kItemVec4; q += kWave) {
+        const int b = q / (kGrWords / 4);
+        if (block0 + b < nblk) {
+          dst[q] = *reinterpret_cast<const uint4*>(ob + b * kGrBlockStride + kGrPadFront + 4 * (q % (kGrWords / 4)));
         }
       }
     } else {
       int32_t* dst = jb.out + static_cast<int64_t>(slot) * jb.dense_rows * jb.dense_cols;
-      for (int idx = tid; idx < kBlocksPerWg * kGrWords; idx += kSpanThreads) {
+      for (int idx = lane; idx < kBlocksPerItem * kGrWords; idx += kWave) {
         const int b = block0 + idx / kGrWords;
         if (b >= nblk) continue;
         const int wd = idx % kGrWords;
         const int row = (b / jb.num_out_blocks) * kGrPackedRows + wd / kTileOut;
         const int col = (b % jb.num_out_blocks) * kTileOut + wd % kTileOut;
         if (row < jb.dense_rows && col < jb.dense_cols) {
-          dst[static_cast<int64_t>(row) * jb.dense_cols + col] = static_cast<int32_t>(outb[idx / kGrWords][kGrPadFront + wd]);
+          dst[static_cast<int64_t>(row) * jb.dense_cols + col] =
+              static_cast<int32_t>(ob[(idx / kGrWords) * kGrBlockStride + kGrPadFront + wd]);
         }
       }
     }
     cur = nx;
-    __syncthreads();  // the next item zeroes and rewrites outb
+    // the stores' LDS reads come before the next item's zeroing in this wavefront's LDS order
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -184,20 +199,21 @@ int launch_gr_jobs(const GrJobs& jobs, int num_jobs, const int32_t* expert_ids, 
   // lanes per block: more lanes shorten each block's walk, fewer spread the per-workgroup table copy
   // over more blocks
   const int S = total > 8192 ? 16 : 32;
-  const int per_wg = kSpanThreads / S;
+  const int per_item = kWave / S;
   GrWork wk{};
   wk.num_jobs = num_jobs;
   wk.num_slots = num_slots;
   int64_t items = 0;
   for (int q = 0; q < num_jobs; ++q) {
     wk.first[q] = static_cast<int>(items);
-    items += static_cast<int64_t>(num_slots) * ceil_div(jobs.job[q].nblk, per_wg);
+    items += static_cast<int64_t>(num_slots) * ceil_div(jobs.job[q].nblk, per_item);
   }
   TRIS_REQUIRE(items < (1LL << 30), "%s: too many blocks", who);
   for (int q = num_jobs; q <= TRIS_MAX_PREDECODE_JOBS; ++q) wk.first[q] = static_cast<int>(items);
-  // persistent workgroups: one per item up to kSpanWgTarget (four per CU, all resident), so every item that can
-  // run at once does; past that each takes several
-  const int64_t grid = items < kSpanWgTarget ? items : kSpanWgTarget;
+  // persistent workgroups: one wavefront per item up to kSpanWgTarget workgroups (all resident), so every item
+  // that can run at once does; past that each wavefront takes several
+  const int64_t wgs = (items + kSpanWaves - 1) / kSpanWaves;
+  const int64_t grid = wgs < kSpanWgTarget ? wgs : kSpanWgTarget;
   wk.decode_wgs = static_cast<int>(grid);
   GrReduce red{};
   int64_t reduce_wgs = 0;

@@ -11,24 +11,30 @@
 // Decoding state at any bit is s in [0, k]: 0 = reading unary bits, s > 0 =
 // s remainder bits still to read.  For k in {1, 2, 3} two tables describe one
 // byte of stream:
-//   next[k][byte]       four 4-bit fields, field s = 4 * (state after the
-//                       byte from entry state s); identity above k;
-//   entry[k][s][byte]   the completed ones as a bit mask (bits 0..40, bit i =
-//                       a one at F(byte start) - 1 + i; a codeword entered
-//                       mid-remainder whose last bits are zero ends at bit 0),
-//                       the F advance (bits 41..47) and the number of
-//                       completed codewords (bits 57..60).
+//   next[k][byte]       four bytes, byte s = the state after the byte from
+//                       entry state s (identity above k).  A map of states in
+//                       this form is a v_perm_b32 selector: composing maps,
+//                       and stepping a state held in all four bytes, is one
+//                       v_perm_b32;
+//   entry[k][s][byte]   64 bits: the low word holds bits 0..31 of the
+//                       completed ones' bit mask (bit i = a one at
+//                       F(byte start) - 1 + i; a codeword entered
+//                       mid-remainder whose last bits are zero ends at bit 0);
+//                       the high word holds the F advance (bits 0..6), the
+//                       number of completed codewords (bits 12..15) and mask
+//                       bits 32..40 (bits 23..31), so a lane's sum of high
+//                       words holds its advance and count sums in bits 0..20.
 // Each lane of the block's group of S lanes:
 //   A. reads next[] for every byte of its span (loads that do not wait on
 //      each other) and composes them into its exit-state map;
 //   B. learns its true entry state from a log-step scan that composes the
 //      maps of the lanes before it;
-//   C. walks its bytes from the true state with one bit-field extract per
-//      byte, so every entry[] load is independent of the others, sums the F
-//      advances and codeword counts (a packed segmented prefix sum gives its
-//      starting F and the block's count), and ORs each byte's mask into the
-//      block's LDS bitmap at its F.
-// The bitmap has a zero pad word before it and three after it: a one at a
+//   C. walks its bytes from the true state with one v_perm_b32 per byte, so
+//      every entry[] load is independent of the others, sums the F advances
+//      and codeword counts (a packed segmented prefix sum gives its starting F
+//      and the block's count), and ORs each byte's mask into the block's LDS
+//      bitmap at its F.
+// The bitmap has zero pad words before and after it: a one at a
 // position past 4095 lands in the back pads (the reference stops there), and
 // the decode falls back to the serial rules.  k = 0 streams are the bitmap
 // itself (each codeword is run zeros then a one) and are copied.  Raw blocks
@@ -46,11 +52,13 @@ namespace tris {
 constexpr int kGrEntryStates = 2 + 3 + 4;                     // k = 1, 2, 3; s in [0, k]
 constexpr int kGrEntries = kGrEntryStates * 256 + 1;             // + one all-zero entry
 constexpr uint32_t kGrZeroEntryOffset = kGrEntryStates * 256 * 8;  // byte offset of the zero entry
-constexpr uint32_t kGrIdentityNext = 0xC840u;                    // field s = 4 * s
+constexpr uint32_t kGrIdentityNext = 0x03020100u;               // byte s = s
 
-// Decoded-block layout in LDS: a pad word, the 128 bitmap words, three pad words.
-constexpr int kGrPadFront = 1;
-constexpr int kGrPadBack = 3;
+// Decoded-block layout in LDS: four pad words, the 128 bitmap words, eight pad words.  The emission writes the
+// word before the bitmap and up to three words after it.  Rows stay 16-byte aligned, and the 140-word stride
+// puts the bitmaps of neighbouring blocks 12 banks apart.
+constexpr int kGrPadFront = 4;
+constexpr int kGrPadBack = 8;
 constexpr int kGrBlockStride = kGrPadFront + kGrWords + kGrPadBack;
 
 __host__ __device__ constexpr int gr_entry_base(int k) { return k == 1 ? 0 : (k == 2 ? 512 : 1280); }
@@ -91,7 +99,7 @@ __host__ __device__ constexpr GrByteStep gr_byte_step(int k, int st, int byte) {
 
 struct alignas(16) GrTables {
   uint64_t entry[kGrEntries + 1];  // (k, s, byte); then the zero entry and one pad entry
-  uint16_t next[3 * 256];          // (k, byte)
+  uint32_t next[3 * 256];          // (k, byte)
 };
 
 constexpr GrTables gr_make_tables() {
@@ -104,12 +112,12 @@ constexpr GrTables gr_make_tables() {
         if (s <= k) {
           const GrByteStep r = gr_byte_step(k, s, byte);
           nx = r.state;
-          t.entry[gr_entry_base(k) + s * 256 + byte] =
-              r.mask | (static_cast<uint64_t>(r.advance) << 41) | (static_cast<uint64_t>(r.count) << 57);
+          const uint32_t hi = r.advance | (r.count << 12) | (static_cast<uint32_t>(r.mask >> 32) << 23);
+          t.entry[gr_entry_base(k) + s * 256 + byte] = (r.mask & 0xFFFFFFFFull) | (static_cast<uint64_t>(hi) << 32);
         }
-        fields |= (4u * nx) << (4 * s);
+        fields |= nx << (8 * s);
       }
-      t.next[(k - 1) * 256 + byte] = static_cast<uint16_t>(fields);
+      t.next[(k - 1) * 256 + byte] = fields;
     }
   }
   return t;
@@ -205,14 +213,10 @@ __device__ __forceinline__ int wave_max_words(int nw) {
   return m;
 }
 
-// Composition of 4-state maps in the next[] field encoding (field s = 4 * image of s): first `earlier`, then
-// `own`.
+// Composition of 4-state maps in the next[] byte encoding (byte s = image of s): first `earlier`, then `own`.
+// Byte s of the result is byte earlier[s] of own, i.e. v_perm_b32 with `earlier` as the selector.
 __device__ __forceinline__ uint32_t gr_map_compose(uint32_t own, uint32_t earlier) {
-  const uint32_t n0 = __builtin_amdgcn_ubfe(own, earlier & 15u, 4);
-  const uint32_t n1 = __builtin_amdgcn_ubfe(own, (earlier >> 4) & 15u, 4);
-  const uint32_t n2 = __builtin_amdgcn_ubfe(own, (earlier >> 8) & 15u, 4);
-  const uint32_t n3 = __builtin_amdgcn_ubfe(own, (earlier >> 12) & 15u, 4);
-  return n0 | (n1 << 4) | (n2 << 8) | (n3 << 12);
+  return __builtin_amdgcn_perm(own, own, earlier);
 }
 
 // One block's stream as seen by lane j of its group: the block header and the
@@ -305,43 +309,38 @@ __device__ inline void gr_decode_block_group(const GrSpan<S>& sp, const GrTables
       }
     }
   } else if (!serial) {
-    const uint16_t* __restrict__ nxt = tab->next + (k - 1) * 256;
-    const char* __restrict__ ent = reinterpret_cast<const char*>(tab->entry + gr_entry_base(k));
+    const uint32_t* __restrict__ nxt = tab->next + (k - 1) * 256;
+    const char* __restrict__ ent = reinterpret_cast<const char*>(tab->entry);
+    const uint32_t kbase = static_cast<uint32_t>(gr_entry_base(k)) * 8u;  // byte offset of k's entries
     const int nbytes = 4 * sp.nw;
     // words any lane of the wavefront holds (a group's first lane holds the most): the walks stop there
     const int maxw = wave_max_words<S>(sp.nw);
     // Each phase walks the span a word at a time under a wave-uniform guard, and issues a word's four table
     // reads together before any is used: one LDS round trip per word, not per byte.
-    // ---- A: next-state fields of every byte (kept for C), composed from every entry state
+    // ---- A: next-state maps of every byte (kept for C), composed over the lane's words (the words past its
+    // span leave the map as it is; C does not use their maps)
     uint32_t f[kBytes];
-    uint32_t c0 = 0u, c1 = 4u, c2 = 8u, c3 = 12u;
+    uint32_t c = kGrIdentityNext;
 #pragma unroll
     for (int wd = 0; wd < kMaxWords; ++wd) {
       if (wd < maxw) {
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const int i = 4 * wd + b;
-          const uint32_t e = nxt[(sp.w[wd] >> (8 * b)) & 0xFFu];
-          f[i] = i < nbytes ? e : kGrIdentityNext;
-        }
+        for (int b = 0; b < 4; ++b) f[4 * wd + b] = nxt[(sp.w[wd] >> (8 * b)) & 0xFFu];
+        uint32_t cw = c;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const uint32_t fi = f[4 * wd + b];
-          c0 = __builtin_amdgcn_ubfe(fi, c0, 4);
-          c1 = __builtin_amdgcn_ubfe(fi, c1, 4);
-          c2 = __builtin_amdgcn_ubfe(fi, c2, 4);
-          c3 = __builtin_amdgcn_ubfe(fi, c3, 4);
-        }
+        for (int b = 0; b < 4; ++b) cw = gr_map_compose(f[4 * wd + b], cw);
+        c = wd < sp.nw ? cw : c;
       }
     }
     // ---- B: the map of lanes 0..j, then the previous lane's (wave_shr:1) applied to state 0
-    const uint32_t map = group_scan<S>(c0 | (c1 << 4) | (c2 << 8) | (c3 << 12), kGrIdentityNext, gr_map_compose);
+    const uint32_t map = group_scan<S>(c, kGrIdentityNext, gr_map_compose);
     const uint32_t prev_map = dpp_mov<0x138, 0xF>(kGrIdentityNext, map);
-    uint32_t st = j == 0 ? 0u : (prev_map & 15u);  // 4 * true entry state
-    // ---- C: entries along the true path (the state chain runs on A's fields); F advance and codeword count
-    // (packed adv | count << 16) from their high words, the masks read again for the emission
+    // the true entry state in all four bytes (a selector that steps it through a byte's map)
+    uint32_t st = j == 0 ? 0u : __builtin_amdgcn_perm(prev_map, prev_map, 0u);
+    // ---- C: entries along the true path (the state chain runs on A's maps); F advance and codeword count
+    // sums from their high words, the masks read again for the emission
     uint32_t off[kBytes];
-    uint32_t packed = 0u;
+    uint32_t hisum = 0u;
 #pragma unroll
     for (int wd = 0; wd < kMaxWords; ++wd) {
       if (wd < maxw) {
@@ -349,23 +348,26 @@ __device__ inline void gr_decode_block_group(const GrSpan<S>& sp, const GrTables
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
           const int i = 4 * wd + b;
-          const uint32_t byte = (sp.w[wd] >> (8 * b)) & 0xFFu;
-          off[i] = i < nbytes ? (st << 9) + (byte << 3) : kGrZeroEntryOffset - gr_entry_base(k) * 8u;
-          st = __builtin_amdgcn_ubfe(f[i], st, 4);
+          // entry index state * 256 + byte: the word's byte b into bits 0..7, the state into bits 8..15
+          const uint32_t idx = __builtin_amdgcn_perm(st, sp.w[wd], 0x0C0C0400u | static_cast<uint32_t>(b));
+          off[i] = i < nbytes ? (idx << 3) + kbase : kGrZeroEntryOffset;
+          st = __builtin_amdgcn_perm(f[i], f[i], st);
           hi[b] = *reinterpret_cast<const uint32_t*>(ent + off[i] + 4);
         }
 #pragma unroll
-        for (int b = 0; b < 4; ++b) packed += hi[b] >> 9;
+        for (int b = 0; b < 4; ++b) hisum += hi[b];
       }
     }
     asm volatile("" ::: "memory");  // the emission reads the entries again rather than keeping 16 of them live
+    // advance sum (< 2^12) and count sum (< 2^9) of the lane, repacked as adv | count << 16 for the group sums
+    const uint32_t packed = (hisum & 0xFFFu) | (((hisum >> 12) & 0x1FFu) << 16);
     const uint32_t incl = group_incl_sum<S>(packed);
     const int total = static_cast<int>(group_last<S>(incl) >> 16);
     serial = total != one_count;
     if (!serial) {
       // bit position + 32 of the lane's first mask bit 0 (F at the span start - 1, biased past the front pad)
       uint32_t posb = ((incl - packed) & 0xFFFFu) + 31u;
-      uint32_t* base = out - kGrPadFront;
+      uint32_t* base = out - 1;
       // OR a mask (< 2^64) whose bit 0 is at posb - 32 into the bitmap; word 129 and up are the back pads,
       // where only positions past 4095 land
       const auto emit = [&](uint64_t m) {
@@ -386,9 +388,9 @@ __device__ inline void gr_decode_block_group(const GrSpan<S>& sp, const GrTables
             for (int b = 0; b < 4; ++b) e[b] = *reinterpret_cast<const uint2*>(ent + off[4 * wd + b]);
 #pragma unroll
             for (int b = 0; b < 4; b += 2) {
-              const uint32_t a0 = __builtin_amdgcn_ubfe(e[b].y, 9, 7);
+              const uint32_t a0 = e[b].y & 0x7Fu;
               emit(static_cast<uint64_t>(e[b].x) | (static_cast<uint64_t>(e[b + 1].x) << a0));
-              posb += a0 + __builtin_amdgcn_ubfe(e[b + 1].y, 9, 7);
+              posb += a0 + (e[b + 1].y & 0x7Fu);
             }
           }
         }
@@ -401,15 +403,15 @@ __device__ inline void gr_decode_block_group(const GrSpan<S>& sp, const GrTables
             for (int b = 0; b < 4; ++b) e[b] = *reinterpret_cast<const uint2*>(ent + off[4 * wd + b]);
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
-              emit(static_cast<uint64_t>(e[b].y & 0x1FFu) << 32 | e[b].x);
-              posb += __builtin_amdgcn_ubfe(e[b].y, 9, 7);
+              emit(static_cast<uint64_t>(e[b].y >> 23) << 32 | e[b].x);
+              posb += e[b].y & 0x7Fu;
             }
           }
         }
       }
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
       __builtin_amdgcn_wave_barrier();
-      const uint32_t pad = j < kGrPadBack ? out[kGrWords + j] : 0u;
+      const uint32_t pad = j < 3 ? out[kGrWords + j] : 0u;
       const uint64_t hit = __ballot(pad != 0u);
       const uint64_t group_mask = (S == 64 ? ~0ull : ((1ull << S) - 1ull))
                                   << ((static_cast<int>(__lane_id()) / S) * S);
