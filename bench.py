@@ -25,6 +25,7 @@ dequant + fp32 GEMMs, every host core) on the same layer.  The other configs
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import statistics
@@ -56,6 +57,10 @@ def parse_args():
     ap.add_argument("--cpu-baseline", type=int, default=1)
     ap.add_argument("--cpu-reps", type=int, default=20, help="timed CPU-baseline repetitions (median reported)")
     ap.add_argument("--configs", default="c0,c3,c4", help="other configs measured into their keys ('' for none)")
+    ap.add_argument("--gmap-p", type=float, default=None, help="split-bitmap density of the reported C1 line "
+                    "(default: the config's 0.15)")
+    ap.add_argument("--density-sweep", default="0.05,0.3",
+                    help="split-bitmap densities p at which the C1 step is also measured, into 'gmap_density'")
     ap.add_argument("--stream-layers", type=int, default=32)
     ap.add_argument("--prefill", type=int, default=2048, help="C2 prefill tokens measured into 'prefill' (0: none)")
     ap.add_argument("--packed4", type=int, default=1,
@@ -104,8 +109,10 @@ def main():
         print(json.dumps(streaming_bench(args, dev)), flush=True)
         return
     t0 = time.time()
+    if args.gmap_p is not None:
+        SPEC = dataclasses.replace(SPEC, gmap_p=args.gmap_p)
     layer = synthetic.make_layer(SPEC, args.seed, ext.gr_encode)
-    log(f"synthetic C1 layer generated in {time.time() - t0:.1f}s")
+    log(f"synthetic C1 layer generated in {time.time() - t0:.1f}s (p = {SPEC.gmap_p:g})")
     lb = LayerBench(SPEC, layer, args.layers, dev)
     if args.profile_kernel:
         profile_dominant_kernel(args, lb)
@@ -128,6 +135,17 @@ def main():
     roofline = dominant_kernel_roofline(args, lb, main_res)
     log(f"dominant kernel {roofline['kernel']}: {roofline['kernel_us']:.1f} us/launch, "
         f"{roofline['achieved']:.0f} GB/s on compressed bytes (frac {roofline['frac']:.3f})")
+
+    density = {}
+    for p in [float(v) for v in args.density_sweep.split(",") if v.strip()]:
+        if p == SPEC.gmap_p:
+            continue
+        dl = synthetic.make_layer(SPEC, args.seed, ext.gr_encode, gmap_p=p)
+        db = LayerBench(SPEC, dl, args.layers, dev)
+        r = db.measure(args.tokens, max(args.steps // 2, 2 * args.layers), args.warmup, args.seed + args.tokens)
+        db.release()
+        density[f"p{p:g}"] = summary(r)
+        log(f"C1 T={args.tokens} at p={p:g}: {r['ms_per_step'] * 1e3:.1f} us/step, {r['tokens_per_s']:.0f} tok/s")
 
     packed4 = packed4_bench(args, lb) if args.packed4 else None
     ns_line = ns_bench(args, lb) if args.ns else None
@@ -171,6 +189,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "sweep": sweep,
+        "gmap_density": density,
         "prefill": prefill,
         "packed4_backbones": packed4,
         "ns_compensation": ns_line,

@@ -353,6 +353,7 @@ __device__ __forceinline__ void dc_lds_barrier() {
 __global__ __launch_bounds__(kDcThreads) __attribute__((amdgpu_waves_per_eu(kDcWgsPerCu * kDcWaves / 4))) void
 grouped_decode_kernel(DcArgs a) {
   __shared__ GrTables tab;
+  __shared__ GrTables4 tab4;
   __shared__ DcLuts lut;
   __shared__ __attribute__((aligned(16))) uint32_t bitmap[kDcWaves][kDcMaxBlocks][kGrBlockStride];
   // per wavefront, in turn: the item's stage (decode to salient), its salient table, its partial tile
@@ -360,6 +361,7 @@ grouped_decode_kernel(DcArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t cols[2][2][kDcMaxPrw * kDcUnitWaves * 32];  // [unit][d / nd][k]
 
   gr_tables_to_lds(&tab);
+  gr_tables4_to_lds(&tab4);
   {
     const uint4* src = reinterpret_cast<const uint4*>(&kDcLuts);
     uint4* dst = reinterpret_cast<uint4*>(&lut);
@@ -574,7 +576,7 @@ grouped_decode_kernel(DcArgs a) {
       for (int q = lane; q < kDcMaxBlocks * kGrBlockStride / 4; q += kWave) z[q] = make_uint4(0u, 0u, 0u, 0u);
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
       __builtin_amdgcn_wave_barrier();
-      gr_decode_block_group<kDcSpan>(sp, &tab, bm + gb * kGrBlockStride + kGrPadFront, gj);
+      gr_decode_block_group<kDcSpan>(sp, &tab, bm + gb * kGrBlockStride + kGrPadFront, gj, &tab4);
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
       __builtin_amdgcn_wave_barrier();
     }

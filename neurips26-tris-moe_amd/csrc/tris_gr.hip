@@ -90,7 +90,7 @@ __device__ __forceinline__ void gr_item_header(const GrJobs& jobs, const GrWork&
 }
 
 template <int S>
-__global__ __launch_bounds__(kSpanThreads) void gr_decode_span_kernel(GrJobs jobs, GrWork wk,
+__global__ __launch_bounds__(kSpanThreads) __attribute__((amdgpu_waves_per_eu(5))) void gr_decode_span_kernel(GrJobs jobs, GrWork wk,
                                                                       const int32_t* __restrict__ expert_ids,
                                                                       GrReduce red) {
   constexpr int kBlocksPerItem = kWave / S;
@@ -103,6 +103,7 @@ __global__ __launch_bounds__(kSpanThreads) void gr_decode_span_kernel(GrJobs job
     return;
   }
   __shared__ GrTables tab;
+  __shared__ GrTables4 tab4;
   __shared__ __attribute__((aligned(16))) uint32_t outb[kSpanWaves][kBlocksPerItem * kGrBlockStride];
   __shared__ int32_t eids[kSpanLdsSlots];
   const int total = wk.first[wk.num_jobs];
@@ -118,6 +119,7 @@ __global__ __launch_bounds__(kSpanThreads) void gr_decode_span_kernel(GrJobs job
   const int nl = wk.num_slots < kSpanLdsSlots ? wk.num_slots : kSpanLdsSlots;
   for (int i = tid; i < nl; i += kSpanThreads) eids[i] = expert_ids[i];
   gr_tables_to_lds(&tab);
+  gr_tables4_to_lds(&tab4);
   gr_span_words<S>(cur.sp, j);
   __syncthreads();
   uint32_t* ob = outb[wave];
@@ -128,7 +130,7 @@ __global__ __launch_bounds__(kSpanThreads) void gr_decode_span_kernel(GrJobs job
     __builtin_amdgcn_wave_barrier();
     GrItem<S> nx;
     gr_item_header<S>(jobs, wk, eids, expert_ids, w + stride, g, nx);
-    gr_decode_block_group<S>(cur.sp, &tab, ob + g * kGrBlockStride + kGrPadFront, j);
+    gr_decode_block_group<S>(cur.sp, &tab, ob + g * kGrBlockStride + kGrPadFront, j, &tab4);
     gr_span_words<S>(nx.sp, j);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();

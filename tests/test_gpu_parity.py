@@ -132,11 +132,89 @@ def test_gr_decode_malformed_streams_follow_reference(tris, oracle_mod, cuda, k)
     np.testing.assert_array_equal(got.cpu().numpy(), want)
 
 
+def rice_completions(words, k: int) -> int:
+    """Codewords (a 1 after any zeros, then k bits) completed within a Rice(k) stream read LSB first, k >= 1."""
+    bits = np.unpackbits(np.asarray(words, dtype=np.int32).view(np.uint8), bitorder="little")
+    count, state = 0, 0
+    for b in bits.tolist():
+        if state == 0:
+            state = k if b else 0
+        else:
+            state -= 1
+            count += state == 0
+    return count
+
+
+@pytest.mark.parametrize("k", [3, 4, 5, 6, 7])
+def test_gr_decode_large_rice_parameter(tris, oracle_mod, cuda, k):
+    """Rice k in [3, 7] (split maps sparser than p ~ 0.12) decode in parallel through the nibble tables: forced-k
+    encodings of sparse, very sparse and clustered bitmaps (and denser ones, which the encoder stores raw at this
+    k) decode bit-exactly through the predecode and dense entries."""
+    note(f"gr large k={k}")
+    rng = np.random.default_rng(700 + k)
+    rows, n = 16, 448
+    denses = [random_bitmap(rng, rows, n, p) for p in (0.003, 0.01, 0.03, 0.06, 0.12)]
+    denses.append(structured_bitmap("sparse_long_runs", rows, n, rng))
+    coded = [oracle_mod.gr_encode(d, k, k) for d in denses]
+    width = max(1, max(c[0].size for c in coded))
+    words = np.zeros((len(denses), width), dtype=np.int32)
+    for e, c in enumerate(coded):
+        words[e, : c[0].size] = c[0]
+    offsets = np.stack([c[1] for c in coded])
+    meta = np.stack([c[2] for c in coded])
+    assert ((meta & 15) == k).any()
+    ids = np.array([5, 0, 3, 1, 4, 2, 0], dtype=np.int32)
+    nblk = (rows // 2) * (n // 64)
+    want = oracle_mod.gr_predecode(words, offsets, meta, ids, nblk)
+    buf = torch.empty((ids.size, nblk, 128), dtype=torch.int32, device=cuda)
+    got = tris["ext"].compact3_tris_precomputed_grouped_block_gr_predecode(
+        buf, t_i32(ids, cuda), t_i32(words, cuda), t_i32(offsets, cuda), t_i32(meta, cuda), rows, n)
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
+    dense = tris["ext"].gr_decode_dense(t_i32(words, cuda), t_i32(offsets, cuda), t_i32(meta, cuda),
+                                        t_i32(ids, cuda), rows, n).cpu().numpy()
+    for i, e in enumerate(ids):
+        np.testing.assert_array_equal(dense[i], denses[e])
+
+
+@pytest.mark.parametrize("k", [3, 4, 5, 6, 7])
+def test_gr_decode_large_rice_parameter_count_matching_streams(tris, oracle_mod, cuda, k):
+    """Arbitrary streams whose one_count equals their completed codewords, which the parallel k >= 3 path accepts:
+    positions run past bit 4095 (dropped, where the reference stops), unary runs and remainders cross words and
+    lanes, long zero runs; one_count one above or below its count takes the serial rules.  Expected: the
+    oracle's restatement of the reference decoder."""
+    note(f"gr large k={k} count-matching")
+    rng = np.random.default_rng(900 + k)
+    nblk = 24
+    words, offsets, meta = [], [0], []
+    for b in range(nblk):
+        nw = int(rng.integers(1, 129))
+        w = rng.integers(-2**31, 2**31, size=nw, dtype=np.int64).astype(np.int32)
+        if b % 4 == 1:
+            w = (w & np.int32(0x01010101)).astype(np.int32)  # long unary runs
+        elif b % 4 == 2:
+            w = (w & np.int32(0x11111111)).astype(np.int32)
+        elif b % 4 == 3:
+            w[rng.random(nw) < 0.5] = 0  # whole zero words between codewords
+        ones = rice_completions(w, k) + (0, 0, 0, 1, -1, 0)[b % 6]
+        words.extend(w.tolist())
+        offsets.append(len(words))
+        meta.append(k | (max(ones, 0) << 8))
+    words_a = np.asarray(words, dtype=np.int32)[None]
+    offsets_a = np.asarray(offsets, dtype=np.int32)[None]
+    meta_a = np.asarray(meta, dtype=np.int32)[None]
+    packed_rows, n = 2 * 4, 64 * 6  # 4 k-blocks x 6 out-blocks = 24 blocks
+    want = oracle_mod.gr_predecode(words_a, offsets_a, meta_a, np.array([0]), nblk)
+    assert want.any()
+    buf = torch.zeros((1, nblk, 128), dtype=torch.int32, device=cuda)
+    got = tris["ext"].compact3_tris_precomputed_grouped_block_gr_predecode(
+        buf, t_i32([0], cuda), t_i32(words_a, cuda), t_i32(offsets_a, cuda), t_i32(meta_a, cuda), packed_rows, n)
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
+
+
 @pytest.mark.parametrize("experts,packed_rows,n", [(1, 64, 3200), (3, 128, 2048), (2, 128, 14336), (5, 128, 14336)],
                          ids=["1600blk", "6144blk", "28672blk", "71680blk"])
 def test_predecode_large_grids(tris, oracle_mod, cuda, experts, packed_rows, n):
-    """Block counts that select each lanes-per-block width of the decoder (32 lanes up to 8192 blocks,
-    16 up to 65536, 8 above)."""
+    """Block counts that select each lanes-per-block width of the decoder (32 lanes up to 8192 blocks, 16 above)."""
     note(f"predecode large E={experts} rows={packed_rows} n={n}")
     rng = np.random.default_rng(packed_rows + n + experts)
     denses = [random_bitmap(rng, packed_rows, n, (0.15, 0.02, 0.5, 0.3, 0.08)[i]) for i in range(experts)]
@@ -152,6 +230,25 @@ def test_predecode_large_grids(tris, oracle_mod, cuda, experts, packed_rows, n):
                                         t_i32(ids, cuda), packed_rows, n).cpu().numpy()
     for i, e in enumerate(ids):
         np.testing.assert_array_equal(dense[i], denses[e])
+
+
+def test_predecode_large_grid_sparse_maps(tris, oracle_mod, cuda):
+    """16 lanes per block (over 8192 blocks) on sparse maps: Rice k = 3 streams of 52-76 words (spans of up to 5
+    words a lane), k = 4 and 5, mixed with k = 2 and 1 blocks in one launch."""
+    note("predecode large grid sparse maps")
+    rng = np.random.default_rng(31)
+    packed_rows, n = 64, 14336
+    ps = (0.1, 0.12, 0.05, 0.03, 0.2, 0.08)
+    denses = [random_bitmap(rng, packed_rows, n, p) for p in ps]
+    words, offsets, meta = stacked_gr(oracle_mod, denses)
+    assert {3, 4, 5} <= set(np.unique(meta & 15).tolist())
+    ids = np.array([0, 1, 2, 3, 4, 5], dtype=np.int32)
+    nblk = (packed_rows // 2) * (n // 64)
+    want = oracle_mod.gr_predecode(words, offsets, meta, ids, nblk)
+    buf = torch.empty((ids.size, nblk, 128), dtype=torch.int32, device=cuda)
+    got = tris["ext"].compact3_tris_precomputed_grouped_block_gr_predecode(
+        buf, t_i32(ids, cuda), t_i32(words, cuda), t_i32(offsets, cuda), t_i32(meta, cuda), packed_rows, n)
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
 
 
 def test_predecode_multi_matches_single_calls(tris, oracle_mod, cuda):
