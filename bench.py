@@ -59,6 +59,8 @@ def parse_args():
     ap.add_argument("--configs", default="c0,c3,c4", help="other configs measured into their keys ('' for none)")
     ap.add_argument("--gmap-p", type=float, default=None, help="split-bitmap density of the reported C1 line "
                     "(default: the config's 0.15)")
+    ap.add_argument("--expert-path", default="auto", choices=("auto", "predecoded", "fused"),
+                    help="expert GEMM path of the reported C1 line (moe.grouped_moe_forward's expert_path)")
     ap.add_argument("--density-sweep", default="0.05,0.3",
                     help="split-bitmap densities p at which the C1 step is also measured, into 'gmap_density'")
     ap.add_argument("--stream-layers", type=int, default=32)
@@ -114,6 +116,7 @@ def main():
     layer = synthetic.make_layer(SPEC, args.seed, ext.gr_encode)
     log(f"synthetic C1 layer generated in {time.time() - t0:.1f}s (p = {SPEC.gmap_p:g})")
     lb = LayerBench(SPEC, layer, args.layers, dev)
+    lb.expert_path = args.expert_path
     if args.profile_kernel:
         profile_dominant_kernel(args, lb)
         return
@@ -185,6 +188,7 @@ def main():
                    "rank": SPEC.rank, "gmap_p": SPEC.gmap_p, "tokens": args.tokens,
                    "active_experts": main_res["active_experts"], "step_bytes": int(main_res["step_bytes"]),
                    "expert_bytes": int(main_res["expert_bytes"]), "layer_copies": args.layers,
+                   "expert_path": args.expert_path,
                    "graph": f"one HIP graph of {args.layers} steps (one per layer copy), replayed"},
         "roofline": roofline,
         "cpu_baseline": cpu,
@@ -215,6 +219,7 @@ class LayerBench:
         from tris_moe_amd import qlinear
 
         self.spec, self.layer, self.dev = spec, layer, dev
+        self.expert_path = "auto"
         base_pl = {p: qlinear.payload_to_device(layer[p], dev) for p in PROJS}
         base_bb = backbones if backbones is not None else {p: torch.from_numpy(layer["backbones"][p]).to(dev)
                                                             for p in PROJS}
@@ -277,7 +282,8 @@ class LayerBench:
             pl, bb = cps[i % len(cps)]
             sh = self.shared[i % len(self.shared)] if self.shared is not None else None
             return moe.grouped_moe_forward_from_logits(x16, logits, spec.top_k, spec.renormalize, pl, bb,
-                                                       spec.num_experts, torch.bfloat16, shared_expert=sh)
+                                                       spec.num_experts, torch.bfloat16, shared_expert=sh,
+                                                       expert_path=self.expert_path)
 
         for i in range(max(warmup, 1)):
             step(i)

@@ -148,6 +148,21 @@ int tris_grouped_forward_block_gr(const uint16_t* hidden, int32_t batch, const i
                                   int32_t num_segments, int64_t total_problem_tiles,
                                   const tris_compact3_payload* payload, uint16_t* output, void* stream);
 
+/*
+ * Sparse split-bitmap variant: replaces compact3_tris_precomputed_grouped_forward (TriSMoE_cuda.cpp:795-832,
+ * bound at :1263; host kernel.cu:8777-8975, kernels :3908-4498, split-bit lookups :619-637), the payload
+ * format of TRIS_COMPACT3_BLOCK_GR=0 checkpoints.  q_gmap_sparse int32 [E, q_gmap_sparse_rows, N]: the j-th
+ * non-salient column of an expert (k order) has its split bits in row j / 32, bit j % 32;
+ * q_gmap_sparse_prefix int32 [E, ceil(K/32)+1]: the non-salient columns before each packed row.  The
+ * payload's q_gmap_gr_* are not read.  As in the reference's sparse kernels, output_scale is always applied
+ * (has_output_scale is ignored) and bias when has_bias.
+ */
+int tris_grouped_forward_sparse(const uint16_t* hidden, int32_t batch, const int32_t* expert_ids,
+                                const int32_t* segment_offsets, const int32_t* problem_offsets, int32_t num_segments,
+                                int64_t total_problem_tiles, const tris_compact3_payload* payload,
+                                const int32_t* q_gmap_sparse, const int32_t* q_gmap_sparse_prefix,
+                                int32_t q_gmap_sparse_rows, uint16_t* output, void* stream);
+
 /* Gate/up pair in one launch: replaces compact3_tris_precomputed_grouped_dual_forward_block_gr
  * (TriSMoE_cuda.cpp:1065-1136, kernel.cu:10214-10779). */
 int tris_grouped_dual_forward_block_gr(const uint16_t* hidden_a, const uint16_t* hidden_b, int32_t batch,

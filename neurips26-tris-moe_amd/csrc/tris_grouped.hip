@@ -28,6 +28,20 @@ constexpr int kGemmWaves = 4;
 constexpr int kGemmThreads = kGemmWaves * kWave;
 constexpr int kGemmRows = 16;  // MT: rows per workgroup tile
 
+// Where the kernel takes each packed row's split bits from.
+constexpr int kGmapGr = 0;          // the payload's block-GR stream, decoded in the kernel
+constexpr int kGmapPredecoded = 1;  // predecoded words [num_segments, nblk, 128]
+constexpr int kGmapSparse = 2;      // the sparse form: non-salient columns only, compacted (SparseGmap)
+
+// Split bitmap in the sparse form (TRIS_COMPACT3_BLOCK_GR=0 payloads): the j-th non-salient column of an expert
+// (k order) is bit j % 32 of row j / 32 of words [E, rows, N]; prefix [E, packed_rows + 1] counts the
+// non-salient columns before each packed row.
+struct SparseGmap {
+  const int32_t* words;
+  const int32_t* prefix;
+  int rows;
+};
+
 struct ProjArgs {
   const uint16_t* hidden;   // [batch, rank]
   uint16_t* out;            // [batch, N]
@@ -35,6 +49,7 @@ struct ProjArgs {
   tris_compact3_payload p;
   const uint16_t* input_scale;  // fp16 [rank] or NULL: the activation is fp16(hidden * input_scale) per column
   const float* addend;          // fp32 [batch, N] or NULL: added to the sum before the output scale
+  SparseGmap sparse;            // the sparse variant's split bitmap
 };
 
 struct GroupedArgs {
@@ -130,9 +145,33 @@ __device__ __forceinline__ uint32_t dense_qweight2_word(const int32_t* __restric
   return dense;
 }
 
-// kNumProj (1 or 2) only separates the single and gate/up-pair launches in
-// profiles; the pair selects its projection by blockIdx.z.
-template <bool kPredecoded, int kNumProj>
+// Split bits of packed row pr for column n from the sparse form (the reference looks each bit up,
+// kernel.cu:619-637: index prefix[pr] + the column's rank among the row's non-salient columns).  The row's
+// non-salient bits are one run of the column's sparse stream, read from at most two words; a zero is then
+// inserted at each salient column (c_map is per row, so the loop is uniform across the wavefront).  Reads past
+// the stream give zeros.
+__device__ __forceinline__ uint32_t sparse_gmap_word(const int32_t* __restrict__ words,
+                                                     const int32_t* __restrict__ prefix, int rows, uint32_t cmap_word,
+                                                     int pr, int n, int N, bool nv) {
+  const int j0 = prefix[pr];
+  const int r0 = j0 >> 5;
+  if (!nv || cmap_word == 0xFFFFFFFFu || j0 < 0 || r0 >= rows) return 0u;
+  const uint32_t lo = static_cast<uint32_t>(words[static_cast<int64_t>(r0) * N + n]);
+  const uint32_t hi = r0 + 1 < rows ? static_cast<uint32_t>(words[static_cast<int64_t>(r0 + 1) * N + n]) : 0u;
+  const uint32_t sh = static_cast<uint32_t>(j0) & 31u;
+  uint32_t d = sh == 0u ? lo : ((lo >> sh) | (hi << (32u - sh)));
+  uint32_t pending = cmap_word;
+  while (pending != 0u) {
+    const uint32_t below = (1u << __builtin_ctz(pending)) - 1u;
+    d = (d & below) | ((d & ~below) << 1);
+    pending &= pending - 1u;
+  }
+  return d;
+}
+
+// kSrc: kGmapGr, kGmapPredecoded or kGmapSparse.  kNumProj (1 or 2) only separates the single and gate/up-pair
+// launches in profiles; the pair selects its projection by blockIdx.z.
+template <int kSrc, int kNumProj>
 __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GroupedArgs a) {
   constexpr int MT = kGemmRows;
   __shared__ float xs[MT][kGemmWaves * kTileK];
@@ -189,12 +228,18 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GroupedArgs 
   const int32_t* grw_e = nullptr;
   const int32_t* gro_e = nullptr;
   const int32_t* grm_e = nullptr;
-  if (!kPredecoded && p.q_gmap_gr_offsets != nullptr) {
+  if (kSrc == kGmapGr && p.q_gmap_gr_offsets != nullptr) {
     grw_e = p.q_gmap_gr_words + static_cast<int64_t>(e) * p.gr_words_stride;
     gro_e = p.q_gmap_gr_offsets + static_cast<int64_t>(e) * (nblk + 1);
     grm_e = p.q_gmap_gr_meta + static_cast<int64_t>(e) * nblk;
   }
-  const int32_t* dec_s = kPredecoded ? pa.decoded + static_cast<int64_t>(s) * nblk * kGrWords : nullptr;
+  const int32_t* dec_s = kSrc == kGmapPredecoded ? pa.decoded + static_cast<int64_t>(s) * nblk * kGrWords : nullptr;
+  const int32_t* gs_e = nullptr;
+  const int32_t* gsp_e = nullptr;
+  if (kSrc == kGmapSparse) {
+    gs_e = pa.sparse.words + static_cast<int64_t>(e) * pa.sparse.rows * N;
+    gsp_e = pa.sparse.prefix + static_cast<int64_t>(e) * (packed_rows + 1);
+  }
   const uint16_t* hid = pa.hidden;
 
   float acc[MT];
@@ -217,10 +262,18 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GroupedArgs 
     if (kb >= nkb) continue;
 
     uint32_t gwords[kGrPackedRows];
-    if (kPredecoded) {
+    if (kSrc == kGmapPredecoded) {
       const int32_t* src = dec_s + static_cast<int64_t>(kb * nob + ob) * kGrWords;
       gwords[0] = static_cast<uint32_t>(src[lane]);
       gwords[1] = static_cast<uint32_t>(src[kWave + lane]);
+    } else if (kSrc == kGmapSparse) {
+#pragma unroll
+      for (int lpr = 0; lpr < kGrPackedRows; ++lpr) {
+        const int pr = kb * kGrPackedRows + lpr;
+        gwords[lpr] = pr < packed_rows ? sparse_gmap_word(gs_e, gsp_e, pa.sparse.rows,
+                                                          static_cast<uint32_t>(cmap_e[pr]), pr, n, N, nv)
+                                       : 0u;
+      }
     } else {
       gr_decode_block_wave(grw_e, gro_e, grm_e, kb * nob + ob, gm[wave]);
       gwords[0] = gm[wave][lane];
@@ -401,17 +454,26 @@ int64_t row_tile_bound(int batch, int num_segments, int64_t total_problem_tiles,
   return total_problem_tiles < bound ? total_problem_tiles : bound;
 }
 
+// src: kGmapGr, kGmapPredecoded (decoded_a/b) or kGmapSparse (sparse: one projection).
 int launch_grouped(const uint16_t* hidden_a, const uint16_t* hidden_b, int batch, const int32_t* expert_ids,
                    const int32_t* segment_offsets, int num_segments, int64_t total_problem_tiles,
                    const int32_t* decoded_a, const int32_t* decoded_b, const tris_compact3_payload* pa,
-                   const tris_compact3_payload* pb, uint16_t* out_a, uint16_t* out_b, bool predecoded,
-                   void* stream, const char* who) {
+                   const tris_compact3_payload* pb, uint16_t* out_a, uint16_t* out_b, int src,
+                   void* stream, const char* who, const SparseGmap* sparse = nullptr) {
   const int nproj = pb ? 2 : 1;
+  const bool predecoded = src == kGmapPredecoded;
   TRIS_REQUIRE(batch >= 0 && num_segments >= 0, "%s: negative batch or segment count", who);
-  int rc = check_payload(pa, !predecoded, who);
+  TRIS_REQUIRE(src != kGmapSparse || (sparse != nullptr && pb == nullptr), "%s: sparse bitmaps for one projection",
+               who);
+  int rc = check_payload(pa, src == kGmapGr, who);
   if (rc) return rc;
+  if (src == kGmapSparse && pa->num_experts > 0 && pa->rank > 0 && pa->outfeatures > 0) {
+    TRIS_REQUIRE(sparse->rows >= 0, "%s: negative q_gmap_sparse row count", who);
+    TRIS_REQUIRE(sparse->prefix != nullptr && (sparse->rows == 0 || sparse->words != nullptr),
+                 "%s: null q_gmap_sparse / q_gmap_sparse_prefix", who);
+  }
   if (pb) {
-    rc = check_payload(pb, !predecoded, who);
+    rc = check_payload(pb, src == kGmapGr, who);
     if (rc) return rc;
     TRIS_REQUIRE(pa->num_experts == pb->num_experts, "%s: expert count mismatch between the pair", who);
   }
@@ -431,6 +493,7 @@ int launch_grouped(const uint16_t* hidden_a, const uint16_t* hidden_b, int batch
   TRIS_REQUIRE(tiles <= 2147483647LL, "%s: too many tiles", who);
   GroupedArgs args{};
   args.proj[0] = ProjArgs{hidden_a, out_a, decoded_a, *pa};
+  if (sparse != nullptr) args.proj[0].sparse = *sparse;
   if (pb) args.proj[1] = ProjArgs{hidden_b, out_b, decoded_b, *pb};
   args.expert_ids = expert_ids;
   args.segment_offsets = segment_offsets;
@@ -439,17 +502,19 @@ int launch_grouped(const uint16_t* hidden_a, const uint16_t* hidden_b, int batch
   args.batch = batch;
   dim3 grid(ceil_div(max_n, kTileOut), static_cast<unsigned>(tiles), nproj);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (predecoded) {
+  if (src == kGmapSparse) {
+    hipLaunchKernelGGL((grouped_gemm_kernel<kGmapSparse, 1>), grid, dim3(kGemmThreads), 0, s, args);
+  } else if (predecoded) {
     if (pb) {
-      hipLaunchKernelGGL((grouped_gemm_kernel<true, 2>), grid, dim3(kGemmThreads), 0, s, args);
+      hipLaunchKernelGGL((grouped_gemm_kernel<kGmapPredecoded, 2>), grid, dim3(kGemmThreads), 0, s, args);
     } else {
-      hipLaunchKernelGGL((grouped_gemm_kernel<true, 1>), grid, dim3(kGemmThreads), 0, s, args);
+      hipLaunchKernelGGL((grouped_gemm_kernel<kGmapPredecoded, 1>), grid, dim3(kGemmThreads), 0, s, args);
     }
   } else {
     if (pb) {
-      hipLaunchKernelGGL((grouped_gemm_kernel<false, 2>), grid, dim3(kGemmThreads), 0, s, args);
+      hipLaunchKernelGGL((grouped_gemm_kernel<kGmapGr, 2>), grid, dim3(kGemmThreads), 0, s, args);
     } else {
-      hipLaunchKernelGGL((grouped_gemm_kernel<false, 1>), grid, dim3(kGemmThreads), 0, s, args);
+      hipLaunchKernelGGL((grouped_gemm_kernel<kGmapGr, 1>), grid, dim3(kGemmThreads), 0, s, args);
     }
   }
   return check_launch(who);
@@ -489,9 +554,9 @@ int launch_linear(const uint16_t* input, int batch, const tris_compact3_payload*
   dim3 grid(ceil_div(max_n, kTileOut), ceil_div(batch, kGemmRows), nproj);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (pb) {
-    hipLaunchKernelGGL((grouped_gemm_kernel<false, 2>), grid, dim3(kGemmThreads), 0, s, args);
+    hipLaunchKernelGGL((grouped_gemm_kernel<kGmapGr, 2>), grid, dim3(kGemmThreads), 0, s, args);
   } else {
-    hipLaunchKernelGGL((grouped_gemm_kernel<false, 1>), grid, dim3(kGemmThreads), 0, s, args);
+    hipLaunchKernelGGL((grouped_gemm_kernel<kGmapGr, 1>), grid, dim3(kGemmThreads), 0, s, args);
   }
   return check_launch(who);
 }
@@ -528,8 +593,30 @@ extern "C" int tris_grouped_forward_block_gr(const uint16_t* hidden, int32_t bat
                                              const tris_compact3_payload* payload, uint16_t* output, void* stream) {
   (void)problem_offsets;
   return launch_grouped(hidden, nullptr, batch, expert_ids, segment_offsets, num_segments, total_problem_tiles,
-                        nullptr, nullptr, payload, nullptr, output, nullptr, false, stream,
+                        nullptr, nullptr, payload, nullptr, output, nullptr, kGmapGr, stream,
                         "tris_grouped_forward_block_gr");
+}
+
+extern "C" int tris_grouped_forward_sparse(const uint16_t* hidden, int32_t batch, const int32_t* expert_ids,
+                                           const int32_t* segment_offsets, const int32_t* problem_offsets,
+                                           int32_t num_segments, int64_t total_problem_tiles,
+                                           const tris_compact3_payload* payload, const int32_t* q_gmap_sparse,
+                                           const int32_t* q_gmap_sparse_prefix, int32_t q_gmap_sparse_rows,
+                                           uint16_t* output, void* stream) {
+  (void)problem_offsets;
+  if (payload == nullptr) {
+    set_error("tris_grouped_forward_sparse: null payload");
+    return TRIS_ERR_INVALID;
+  }
+  tris_compact3_payload p = *payload;  // the reference's sparse kernels always apply the output scale
+  p.has_output_scale = 1;
+  p.q_gmap_gr_words = nullptr;
+  p.q_gmap_gr_offsets = nullptr;
+  p.q_gmap_gr_meta = nullptr;
+  const SparseGmap sg{q_gmap_sparse, q_gmap_sparse_prefix, q_gmap_sparse_rows};
+  return launch_grouped(hidden, nullptr, batch, expert_ids, segment_offsets, num_segments, total_problem_tiles,
+                        nullptr, nullptr, &p, nullptr, output, nullptr, kGmapSparse, stream,
+                        "tris_grouped_forward_sparse", &sg);
 }
 
 extern "C" int tris_grouped_dual_forward_block_gr(const uint16_t* hidden_a, const uint16_t* hidden_b, int32_t batch,
@@ -541,7 +628,7 @@ extern "C" int tris_grouped_dual_forward_block_gr(const uint16_t* hidden_a, cons
   (void)problem_offsets;
   TRIS_REQUIRE(payload_b != nullptr, "tris_grouped_dual_forward_block_gr: null payload_b");
   return launch_grouped(hidden_a, hidden_b, batch, expert_ids, segment_offsets, num_segments, total_problem_tiles,
-                        nullptr, nullptr, payload_a, payload_b, output_a, output_b, false, stream,
+                        nullptr, nullptr, payload_a, payload_b, output_a, output_b, kGmapGr, stream,
                         "tris_grouped_dual_forward_block_gr");
 }
 
@@ -565,7 +652,7 @@ extern "C" int tris_grouped_forward_block_gr_predecoded(const uint16_t* hidden, 
                                &p, nullptr, output, nullptr, false, stream, "tris_grouped_forward_block_gr_predecoded");
   }
   return launch_grouped(hidden, nullptr, batch, expert_ids, segment_offsets, num_segments, total_problem_tiles,
-                        decoded, nullptr, &p, nullptr, output, nullptr, true, stream,
+                        decoded, nullptr, &p, nullptr, output, nullptr, kGmapPredecoded, stream,
                         "tris_grouped_forward_block_gr_predecoded");
 }
 
@@ -593,7 +680,7 @@ static int dual_predecoded(const uint16_t* hidden_a, const uint16_t* hidden_b, c
   }
   TRIS_REQUIRE(row_index == nullptr, "%s: gathered rows need the MFMA kernel's payload conditions", who);
   return launch_grouped(hidden_a, hidden_b, batch, expert_ids, segment_offsets, num_segments, total_problem_tiles,
-                        decoded_a, decoded_b, &pa, &pb, output_a, output_b, true, stream, who);
+                        decoded_a, decoded_b, &pa, &pb, output_a, output_b, kGmapPredecoded, stream, who);
 }
 
 static int swiglu_predecoded(const uint16_t* hidden_gate, const uint16_t* hidden_up, const int64_t* row_index,

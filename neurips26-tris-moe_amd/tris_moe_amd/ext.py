@@ -369,6 +369,33 @@ def compact3_tris_precomputed_grouped_forward_block_gr(hidden, expert_ids, segme
     return out
 
 
+def compact3_tris_precomputed_grouped_forward(hidden, expert_ids, segment_offsets, problem_offsets,
+                                              total_problem_tiles, qweight1, qweight2_sparse, qweight2_sparse_prefix,
+                                              q_gmap_sparse, q_gmap_sparse_prefix, c_map, g_idx, col_pack3,
+                                              row_pack3, output_scale, bias, has_bias):
+    """TriSMoE_cuda.cpp:795-832 (sparse split bitmaps) -> tris_grouped_forward_sparse.  output_scale fp16 [E, N]
+    is always applied, as the reference's sparse kernels do (kernel.cu:4051-4064)."""
+    _check_route(hidden, expert_ids, segment_offsets, problem_offsets)
+    total = _host_tiles(total_problem_tiles)
+    rank = int(hidden.size(1))
+    _check_cuda("q_gmap_sparse", q_gmap_sparse, torch.int32, 3, hidden.device)
+    _check_cuda("q_gmap_sparse_prefix", q_gmap_sparse_prefix, torch.int32, 2, hidden.device)
+    pay = make_payload_struct(rank, qweight1, qweight2_sparse, qweight2_sparse_prefix, None, None, None, c_map, g_idx,
+                              col_pack3, row_pack3, output_scale, True, bias, has_bias, False, hidden.device,
+                              need_gr=False)
+    packed_rows = (rank + 31) // 32
+    if int(q_gmap_sparse.size(0)) != pay.num_experts or int(q_gmap_sparse.size(2)) != pay.outfeatures:
+        raise RuntimeError("compact3 grouped q_gmap_sparse shape mismatch")
+    if tuple(q_gmap_sparse_prefix.shape) != (pay.num_experts, packed_rows + 1):
+        raise RuntimeError("compact3 grouped q_gmap prefix mismatch")
+    out = torch.zeros((hidden.size(0), pay.outfeatures), dtype=torch.float16, device=hidden.device)
+    _lib.check(_lib.load().tris_grouped_forward_sparse(
+        _ptr(hidden), int(hidden.size(0)), _ptr(expert_ids), _ptr(segment_offsets), _ptr(problem_offsets),
+        int(expert_ids.size(0)), total, ctypes.byref(pay), _ptr(q_gmap_sparse), _ptr(q_gmap_sparse_prefix),
+        int(q_gmap_sparse.size(1)), _ptr(out), _stream(hidden)), "compact3_tris_precomputed_grouped_forward")
+    return out
+
+
 def compact3_tris_precomputed_grouped_dual_forward_block_gr(
         hidden_a, hidden_b, expert_ids, segment_offsets, problem_offsets, total_problem_tiles,
         qweight1_a, qweight2_sparse_a, qweight2_sparse_prefix_a, q_gmap_gr_words_a, q_gmap_gr_offsets_a,

@@ -95,11 +95,34 @@ def grouped_moe_forward_from_logits(x16: torch.Tensor, router_logits: torch.Tens
                                shared_expert, expert_path)
 
 
+def _sparse(p: dict) -> bool:
+    """The payload's split bitmaps are in the sparse form (compact3_use_block_gr false)."""
+    return "q_gmap_sparse" in p and not bool(p.get("compact3_use_block_gr", False))
+
+
 def _predecodable(payloads: dict) -> bool:
-    """Every projection has uniform 64-column groups and no output scale or bias (the predecoded path)."""
+    """Every projection has block-GR split bitmaps, uniform 64-column groups and no output scale or bias (the
+    predecoded path)."""
     pg, pu, pd = payloads["gate"], payloads["up"], payloads["down"]
-    return all(bool(p.get("_compact3_k64_groups_uniform", False)) for p in (pg, pu, pd)) and not any(
+    return all(bool(p.get("_compact3_k64_groups_uniform", False)) and not _sparse(p) for p in (pg, pu, pd)) and not any(
         bool(p["has_output_scale"]) or bool(p["has_bias"]) for p in (pg, pu, pd))
+
+
+def _grouped_projection(p: dict, hidden, expert_ids, seg, prob, tile_bound):
+    """One projection's grouped GEMM on the exact kernel: the sparse-form entry (output scale always applied, as
+    the reference's sparse kernels do) or the block-GR one."""
+    empty = hidden.new_empty((0, 0))
+    bias = p["bias"] if p["has_bias"] else empty
+    if _sparse(p):
+        return ext.compact3_tris_precomputed_grouped_forward(
+            hidden, expert_ids, seg, prob, tile_bound, p["qweight1"], p["qweight2_sparse"],
+            p["qweight2_sparse_prefix"], p["q_gmap_sparse"], p["q_gmap_sparse_prefix"], p["c_map"], p["g_idx"],
+            p["col_pack3"], p["row_pack3"], p["output_scale"], bias, bool(p["has_bias"]))
+    return ext.compact3_tris_precomputed_grouped_forward_block_gr(
+        hidden, expert_ids, seg, prob, tile_bound, p["qweight1"], p["qweight2_sparse"], p["qweight2_sparse_prefix"],
+        p["q_gmap_gr_words"], p["q_gmap_gr_offsets"], p["q_gmap_gr_meta"], p["c_map"], p["g_idx"], p["col_pack3"],
+        p["row_pack3"], p["output_scale"], bool(p["has_output_scale"]), bias, bool(p["has_bias"]),
+        bool(p.get("_compact3_k64_groups_uniform", False)))
 
 
 def _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, output_dtype, shared_expert,
@@ -125,31 +148,30 @@ def _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, ou
                                        shared_expert, backbone_pending=backbone_pending)
     if backbone_pending is not None:
         raise RuntimeError("a backbone launched beside the router needs the predecoded expert path")
-    if all(ext.decode_payload_ok(p) for p in (pg, pu, pd)):
+    if not any(_sparse(p) for p in (pg, pu, pd)) and all(ext.decode_payload_ok(p) for p in (pg, pu, pd)):
         return _decode_fused_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype,
                                          shared_expert)
     sc = _in_scales(backbones)
     hid_g, hid_u = shared_projection_pair(x16, backbones["gate"], backbones["up"], row_index=gti,
                                           in_scale_a=sc["gate"], in_scale_b=sc["up"])
     empty = x16.new_empty((0, 0))
-    g_out, u_out = ext.compact3_tris_precomputed_grouped_dual_forward_block_gr(
-        hid_g, hid_u, expert_ids, seg, prob, tile_bound,
-        pg["qweight1"], pg["qweight2_sparse"], pg["qweight2_sparse_prefix"], pg["q_gmap_gr_words"],
-        pg["q_gmap_gr_offsets"], pg["q_gmap_gr_meta"], pg["c_map"], pg["g_idx"], pg["col_pack3"], pg["row_pack3"],
-        pg["output_scale"], bool(pg["has_output_scale"]), pg["bias"] if pg["has_bias"] else empty,
-        pu["qweight1"], pu["qweight2_sparse"], pu["qweight2_sparse_prefix"], pu["q_gmap_gr_words"],
-        pu["q_gmap_gr_offsets"], pu["q_gmap_gr_meta"], pu["c_map"], pu["g_idx"], pu["col_pack3"], pu["row_pack3"],
-        pu["output_scale"], bool(pu["has_output_scale"]), pu["bias"] if pu["has_bias"] else empty, uniform)
+    if _sparse(pg) or _sparse(pu):
+        g_out = _grouped_projection(pg, hid_g, expert_ids, seg, prob, tile_bound)
+        u_out = _grouped_projection(pu, hid_u, expert_ids, seg, prob, tile_bound)
+    else:
+        g_out, u_out = ext.compact3_tris_precomputed_grouped_dual_forward_block_gr(
+            hid_g, hid_u, expert_ids, seg, prob, tile_bound,
+            pg["qweight1"], pg["qweight2_sparse"], pg["qweight2_sparse_prefix"], pg["q_gmap_gr_words"],
+            pg["q_gmap_gr_offsets"], pg["q_gmap_gr_meta"], pg["c_map"], pg["g_idx"], pg["col_pack3"], pg["row_pack3"],
+            pg["output_scale"], bool(pg["has_output_scale"]), pg["bias"] if pg["has_bias"] else empty,
+            pu["qweight1"], pu["qweight2_sparse"], pu["qweight2_sparse_prefix"], pu["q_gmap_gr_words"],
+            pu["q_gmap_gr_offsets"], pu["q_gmap_gr_meta"], pu["c_map"], pu["g_idx"], pu["col_pack3"], pu["row_pack3"],
+            pu["output_scale"], bool(pu["has_output_scale"]), pu["bias"] if pu["has_bias"] else empty, uniform)
     if ns["gate"] is not None or ns["up"] is not None:
         ext.ns_compensation_pair_apply_(g_out, u_out, x16, expert_ids, seg, ns["gate"], ns["up"], row_index=gti)
     mlp = F.silu(g_out) * u_out
     hid_d = shared_projection(mlp, backbones["down"], in_scale=sc["down"])
-    d_out = ext.compact3_tris_precomputed_grouped_forward_block_gr(
-        hid_d, expert_ids, seg, prob, tile_bound,
-        pd["qweight1"], pd["qweight2_sparse"], pd["qweight2_sparse_prefix"], pd["q_gmap_gr_words"],
-        pd["q_gmap_gr_offsets"], pd["q_gmap_gr_meta"], pd["c_map"], pd["g_idx"], pd["col_pack3"], pd["row_pack3"],
-        pd["output_scale"], bool(pd["has_output_scale"]), pd["bias"] if pd["has_bias"] else empty,
-        bool(pd["has_bias"]), bool(pd.get("_compact3_k64_groups_uniform", False)))
+    d_out = _grouped_projection(pd, hid_d, expert_ids, seg, prob, tile_bound)
     if ns["down"] is not None:
         ext.ns_compensation_apply_(d_out, mlp, expert_ids, seg, ns["down"])
     return _combine(x16, d_out, route, w16, output_dtype, shared_expert)

@@ -102,6 +102,12 @@ def _k64_uniform(payload: dict) -> bool:
     return bool(payload["_compact3_k64_groups_uniform"])
 
 
+def is_sparse_payload(payload: dict) -> bool:
+    """A payload whose split bitmaps are in the sparse form (compact3_use_block_gr false,
+    qlinear_cuda.py:1658-1676): only the sparse kernel entry runs it."""
+    return not bool(payload.get("compact3_use_block_gr", False))
+
+
 def resolve_grouped_precomputed_payload(payload_or_modules, device, dtype):
     """qlinear_cuda.py:1639-1682: validate a payload dict or stack it from modules."""
     if isinstance(payload_or_modules, dict):
@@ -111,12 +117,16 @@ def resolve_grouped_precomputed_payload(payload_or_modules, device, dtype):
                 return None
         if payload["qweight1"].device != torch.device(device) or payload["output_scale"].dtype != dtype:
             return None
-        if not payload["is_compact3"] or not payload.get("compact3_use_block_gr", False):
+        if not payload["is_compact3"]:
             return None
-        for key in ("qweight2_sparse", "qweight2_sparse_prefix", "q_gmap_gr_words", "q_gmap_gr_offsets",
-                    "q_gmap_gr_meta", "col_pack3", "row_pack3"):
-            if key not in payload:
-                return None
+        if payload.get("compact3_use_block_gr", False):
+            required = ("qweight2_sparse", "qweight2_sparse_prefix", "q_gmap_gr_words", "q_gmap_gr_offsets",
+                        "q_gmap_gr_meta", "col_pack3", "row_pack3")
+        else:  # the sparse split-bitmap form
+            required = ("qweight2_sparse", "qweight2_sparse_prefix", "q_gmap_sparse", "q_gmap_sparse_prefix",
+                        "col_pack3", "row_pack3")
+        if any(key not in payload for key in required):
+            return None
         payload["has_output_scale"] = _payload_has_output_scale(payload)
         _k64_uniform(payload)
         return payload
@@ -421,7 +431,13 @@ def run_grouped_structured_expert_forward(payload_or_modules, hidden_grouped: to
     total = _route_total_problem_tiles_host(route)
     uniform = _k64_uniform(payload)
     hidden_c = hidden_grouped.contiguous()
-    if _use_predecode(batch, int(route["expert_ids"].numel()), payload, has_scale, has_bias_arg):
+    if is_sparse_payload(payload):
+        out = ext.compact3_tris_precomputed_grouped_forward(
+            hidden_c, route["expert_ids"], route["segment_offsets"], route["problem_offsets"], total,
+            payload["qweight1"], payload["qweight2_sparse"], payload["qweight2_sparse_prefix"],
+            payload["q_gmap_sparse"], payload["q_gmap_sparse_prefix"], payload["c_map"], payload["g_idx"],
+            payload["col_pack3"], payload["row_pack3"], payload["output_scale"], bias_arg, has_bias_arg)
+    elif _use_predecode(batch, int(route["expert_ids"].numel()), payload, has_scale, has_bias_arg):
         decoded = _predecode(payload, route, rank, n)
         out = ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
             hidden_c, route["expert_ids"], route["segment_offsets"], route["problem_offsets"], total, decoded,
@@ -456,6 +472,13 @@ def run_grouped_structured_expert_pair_forward(payload_or_modules_a, payload_or_
     pb = resolve_grouped_precomputed_payload(payload_or_modules_b, hidden_b_grouped.device, hidden_b_grouped.dtype)
     if pa is None or pb is None:
         return None, None
+    if is_sparse_payload(pa) or is_sparse_payload(pb):
+        # no pair entry for sparse split bitmaps: one launch per projection (qlinear_cuda.py:2381-2411)
+        out_a = run_grouped_structured_expert_forward(pa, hidden_a_grouped, x_grouped, route, expert_modules_a,
+                                                      ns_payload=ns_payload_a)
+        out_b = run_grouped_structured_expert_forward(pb, hidden_b_grouped, x_grouped, route, expert_modules_b,
+                                                      ns_payload=ns_payload_b)
+        return out_a, out_b
     ns_a = _resolve_ns_payload(ns_payload_a)
     ns_b = _resolve_ns_payload(ns_payload_b)
     if expert_modules_a is None and not isinstance(payload_or_modules_a, dict):

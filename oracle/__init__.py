@@ -297,18 +297,54 @@ def dequant_compact3(qweight1, qweight2_sparse, qweight2_sparse_prefix, gmap_den
     return np.where(salient[None, :], w_sal, w_ns).astype(np.float16)
 
 
+def sparse_gmap_dense(q_gmap_sparse, q_gmap_sparse_prefix, c_map, rank: int) -> np.ndarray:
+    """Dense packed split bitmap [ceil(rank/32), N] of one expert from the sparse form (TRIS_COMPACT3_BLOCK_GR=0
+    payloads): get_sparse_inactive_bit (TriSMoE_cuda_kernel.cu:619-637) for every (k, n).  A salient column gives
+    0; non-salient column k reads bit j of its column's sparse stream, j = prefix[k/32] + (k%32 -
+    popc(c_map_word & low_mask(k%32))), in row j/32, bit j%32.  With a consistent prefix this is
+    restore_dense_packed_gmap_from_sparse (tools/rewrite_runtime_min_checkpoint.py:147-159)."""
+    words = np.asarray(q_gmap_sparse).astype(np.uint32)
+    if words.ndim != 2:
+        words = words.reshape(0, 0)
+    n = words.shape[1]
+    ks = np.arange(rank)
+    rows = ks >> 5
+    bits = (ks & 31).astype(np.uint32)
+    cmap_w = np.asarray(c_map).astype(np.uint32).ravel()
+    salient = ((cmap_w[rows] >> bits) & 1).astype(bool)
+    low = np.where(bits == 0, np.uint32(0), (np.uint32(1) << bits) - np.uint32(1)).astype(np.uint32)
+    popc = np.array([bin(int(v)).count("1") for v in cmap_w[rows] & low], dtype=np.int64)
+    j = np.asarray(q_gmap_sparse_prefix).astype(np.int64)[rows] + (bits.astype(np.int64) - popc)
+    dense = np.zeros((n, rank), dtype=bool)
+    ns_k = np.nonzero(~salient)[0]
+    if ns_k.size and words.shape[0]:
+        jr, jb = j[ns_k] >> 5, (j[ns_k] & 31).astype(np.uint32)
+        dense[:, ns_k] = ((words[jr, :] >> jb[:, None]) & 1).astype(bool).T
+    return pack_bool_matrix(dense)
+
+
 def expert_slice(payload: dict, e: int) -> dict:
     return {k: (v[e] if isinstance(v, np.ndarray) and v.ndim >= 1 and k != "__scalar__" else v) for k, v in payload.items()}
 
 
+def is_sparse_payload(payload: dict) -> bool:
+    """A payload in the sparse split-bitmap form (qlinear_cuda.py:1658-1676: compact3_use_block_gr false)."""
+    return "q_gmap_sparse" in payload and not bool(payload.get("compact3_use_block_gr", "q_gmap_gr_words" in payload))
+
+
 def dequant_grouped_expert(payload: dict, e: int, uniform_k64_groups: bool | None = None) -> np.ndarray:
-    """Decode the expert's GR bitmap and reconstruct its fp16 weights [N, rank]."""
+    """Decode the expert's split bitmap (GR stream, or the sparse form) and reconstruct its fp16 weights
+    [N, rank]."""
     rank = int(payload["g_idx"].shape[1])
     n = int(payload["qweight1"].shape[2])
     packed_rows = -(-rank // 32)
     nblk = num_gr_blocks(packed_rows, n)
-    gmap = gr_decode_dense(payload["q_gmap_gr_words"][e], payload["q_gmap_gr_offsets"][e][: nblk + 1],
-                           payload["q_gmap_gr_meta"][e][:nblk], packed_rows, n)
+    if is_sparse_payload(payload):
+        gmap = sparse_gmap_dense(payload["q_gmap_sparse"][e], payload["q_gmap_sparse_prefix"][e], payload["c_map"][e],
+                                 rank)
+    else:
+        gmap = gr_decode_dense(payload["q_gmap_gr_words"][e], payload["q_gmap_gr_offsets"][e][: nblk + 1],
+                               payload["q_gmap_gr_meta"][e][:nblk], packed_rows, n)
     if uniform_k64_groups is None:
         uniform_k64_groups = bool(payload.get("_compact3_k64_groups_uniform", False))
     return dequant_compact3(payload["qweight1"][e], payload["qweight2_sparse"][e], payload["qweight2_sparse_prefix"][e],
@@ -320,12 +356,14 @@ def dequant_grouped_expert(payload: dict, e: int, uniform_k64_groups: bool | Non
 def grouped_forward(payload: dict, hidden, expert_ids, segment_offsets, uniform_k64_groups: bool | None = None,
                     weight_cache: dict | None = None) -> np.ndarray:
     """out[R, N] fp16: per segment, hidden @ W_e^T (exact sums, held in fp32 as the kernel's accumulator),
-    then the reference epilogue fp16(acc * scale + bias) in fp32 (TriSMoE_cuda_kernel.cu:4662-4680).
+    then the reference epilogue fp16(acc * scale + bias) in fp32 (TriSMoE_cuda_kernel.cu:4662-4680; sparse-form
+    payloads :4051-4064, which scale unconditionally).
     Segments with a negative expert slot produce zeros."""
     hidden = np.asarray(hidden, dtype=np.float16)
     n = int(payload["qweight1"].shape[2])
     out = np.zeros((hidden.shape[0], n), dtype=np.float16)
-    has_scale = bool(payload.get("has_output_scale", False))
+    # the sparse-form kernels always apply the output scale (TriSMoE_cuda_kernel.cu:4051-4064)
+    has_scale = bool(payload.get("has_output_scale", False)) or is_sparse_payload(payload)
     has_bias = bool(payload.get("has_bias", False))
     seg = np.asarray(segment_offsets).astype(np.int64)
     cache = weight_cache if weight_cache is not None else {}
