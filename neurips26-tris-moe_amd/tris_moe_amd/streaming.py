@@ -5,7 +5,8 @@ streams only the sparse split bitmap of non-GR payloads into one reused workspac
 every tensor of a layer (gate, up and down payloads, optionally the backbones): a layer is one pinned host
 blob, copied with one asynchronous host-to-device transfer on a copy stream into one of ``num_slots`` device
 slots, so that the next layer's copy overlaps the current layer's kernels when a device budget keeps the
-model off the GPU.
+model off the GPU.  The reference's own mode, only the split bitmaps streamed (sparse or block-GR) and every
+other tensor resident, is ``split_bitmaps`` plus the streamer's ``resident`` argument.
 
 Ordering (as the reference's per-slot ready/done events, :1093-1134):
 
@@ -117,6 +118,24 @@ def unpack_views(layout: LayerLayout, buf: torch.Tensor) -> tuple[dict, dict | N
     return payloads, backbones
 
 
+# the split-bitmap tensors of a payload: what the reference's staging manager streams
+# (grouped_payload_sidecar.py:764-1146 streams q_gmap_sparse(+prefix)); for block-GR payloads their GR streams
+BITMAP_KEYS = frozenset({"q_gmap_sparse", "q_gmap_sparse_prefix", "q_gmap_gr_words", "q_gmap_gr_offsets",
+                         "q_gmap_gr_meta"})
+
+
+def split_bitmaps(layer: dict) -> tuple[dict, dict]:
+    """One layer's host payloads split into (split bitmaps, the rest): stream the first with
+    ``GroupedPayloadStreamer`` and keep the second resident (``resident=``), as the reference's staging
+    manager keeps every other payload tensor on the device."""
+    streamed, rest = {}, {}
+    for proj in PROJECTIONS:
+        pl = layer[proj]
+        streamed[proj] = {k: v for k, v in pl.items() if k in BITMAP_KEYS}
+        rest[proj] = {k: v for k, v in pl.items() if k not in BITMAP_KEYS}
+    return streamed, rest
+
+
 def _uniform_k64(g_idx: np.ndarray) -> bool:
     """Every 64-column K tile of every expert lies in one group (qlinear_cuda.py:364-381)."""
     rank = g_idx.shape[-1]
@@ -130,16 +149,22 @@ class GroupedPayloadStreamer:
 
     ``layers``: per layer ``{"gate": payload, "up": payload, "down": payload}`` with numpy arrays (the host
     format of ``synthetic.make_layer`` / the sidecar loader); ``backbones``: per layer ``{"gate": SV, "up": SV,
-    "down": SV}`` fp16 arrays to stream as well, or None to keep them out of the blob.
+    "down": SV}`` fp16 arrays to stream as well, or None to keep them out of the blob.  ``resident``: per layer
+    the same dicts of device tensors that stay on the GPU (``split_bitmaps`` and ``qlinear.payload_to_device``);
+    acquire merges them under the streamed tensors, so ``layers`` may hold only the split bitmaps.
     """
 
-    def __init__(self, layers: list, device, num_slots: int = 2, backbones: list | None = None):
+    def __init__(self, layers: list, device, num_slots: int = 2, backbones: list | None = None,
+                 resident: list | None = None):
         if num_slots < 1:
             raise ValueError("num_slots must be at least 1")
         if not layers:
             raise ValueError("no layers to stream")
         if backbones is not None and len(backbones) != len(layers):
             raise ValueError("one backbone dict per layer")
+        if resident is not None and len(resident) != len(layers):
+            raise ValueError("one resident payload dict per layer")
+        self.resident = resident
         self.device = torch.device(device)
         self.layouts = [layer_layout(layers[i], None if backbones is None else backbones[i]) for i in range(len(layers))]
         self.slot_bytes = max(l.nbytes for l in self.layouts)
@@ -151,8 +176,12 @@ class GroupedPayloadStreamer:
             pack_layer(layers[i], None if backbones is None else backbones[i], lay, blob.numpy())
             self.host.append(blob)
         # the uniform 64-column group proof is taken once on the host (a device check would synchronise)
-        self._uniform = [{p: _uniform_k64(np.asarray(layers[i][p]["g_idx"])) for p in PROJECTIONS}
-                         for i in range(len(layers))]
+        def g_idx(i, p):
+            if "g_idx" in layers[i][p]:
+                return np.asarray(layers[i][p]["g_idx"])
+            return resident[i][p]["g_idx"].cpu().numpy()
+
+        self._uniform = [{p: _uniform_k64(g_idx(i, p)) for p in PROJECTIONS} for i in range(len(layers))]
         self.slots = [torch.empty(self.slot_bytes, dtype=torch.uint8, device=self.device) for _ in range(num_slots)]
         self.copy_stream = torch.cuda.Stream(device=self.device)
         self._ready = [torch.cuda.Event() for _ in range(num_slots)]
@@ -215,6 +244,8 @@ class GroupedPayloadStreamer:
         # the slot's memory is used by `stream` (caching allocator bookkeeping for the views)
         self.slots[s].record_stream(stream)
         payloads, backbones = unpack_views(self.layouts[i], self.slots[s])
+        if self.resident is not None:
+            payloads = {p: {**self.resident[i][p], **payloads[p]} for p in PROJECTIONS}
         for p in PROJECTIONS:
             payloads[p]["_compact3_k64_groups_uniform"] = self._uniform[i][p]
         return payloads, backbones

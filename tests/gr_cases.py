@@ -67,3 +67,25 @@ def structured_bitmap(kind: str, packed_rows: int, n: int, rng) -> np.ndarray:
         idx = rng.choice(packed_rows * n, size=max(1, packed_rows * n // 97), replace=False)
         dense.reshape(-1)[idx] = np.uint32(1) << rng.integers(0, 32, idx.size).astype(np.uint32)
     return dense.view(np.int32)
+
+
+def to_sparse(oracle_mod, payload, rank):
+    """A block-GR synthetic payload (with its dense split bitmaps) in the sparse form the reference's
+    TRIS_COMPACT3_BLOCK_GR=0 exporters write (pack_utils.py:32-52): non-salient columns only, per-expert rows
+    zero padded to the largest."""
+    E = payload["qweight1"].shape[0]
+    n = payload["qweight1"].shape[2]
+    forms = []
+    for e in range(E):
+        sal = oracle_mod.unpack_bool_vector(payload["c_map"][e], rank)
+        dense = oracle_mod.unpack_bool_matrix(payload["gmap_dense"][e], rank)  # [N, K]
+        forms.append((oracle_mod.pack_sparse_bool_matrix(dense, ~sal), oracle_mod.sparse_prefix(~sal)))
+    rows = max(1, max(w.shape[0] for w, _ in forms))
+    words = np.zeros((E, rows, n), dtype=np.int32)
+    for e, (w, _) in enumerate(forms):
+        words[e, : w.shape[0]] = w
+    out = {k: v for k, v in payload.items() if not k.startswith("q_gmap_gr") and k != "gmap_dense"}
+    out["q_gmap_sparse"] = words
+    out["q_gmap_sparse_prefix"] = np.stack([pre for _, pre in forms]).astype(np.int32)
+    out["compact3_use_block_gr"] = False
+    return out

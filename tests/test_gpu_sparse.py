@@ -8,6 +8,8 @@ import numpy as np
 import pytest
 import torch
 
+from gr_cases import to_sparse
+
 pytestmark = pytest.mark.gpu
 
 MAX_ABS = 2e-2
@@ -29,28 +31,6 @@ def assert_close(got, want, what):
     denom = float(np.linalg.norm(want))
     rel = float(np.linalg.norm(err)) / denom if denom > 0 else float(np.linalg.norm(err))
     assert max_abs <= MAX_ABS and rel <= REL_L2, f"{what}: max_abs={max_abs:.3g} rel_l2={rel:.3g}"
-
-
-def to_sparse(oracle_mod, payload, rank):
-    """A block-GR synthetic payload (with its dense split bitmaps) in the sparse form the reference's
-    TRIS_COMPACT3_BLOCK_GR=0 exporters write (pack_utils.py:32-52): non-salient columns only, per-expert rows
-    zero padded to the largest."""
-    E = payload["qweight1"].shape[0]
-    n = payload["qweight1"].shape[2]
-    forms = []
-    for e in range(E):
-        sal = oracle_mod.unpack_bool_vector(payload["c_map"][e], rank)
-        dense = oracle_mod.unpack_bool_matrix(payload["gmap_dense"][e], rank)  # [N, K]
-        forms.append((oracle_mod.pack_sparse_bool_matrix(dense, ~sal), oracle_mod.sparse_prefix(~sal)))
-    rows = max(1, max(w.shape[0] for w, _ in forms))
-    words = np.zeros((E, rows, n), dtype=np.int32)
-    for e, (w, _) in enumerate(forms):
-        words[e, : w.shape[0]] = w
-    out = {k: v for k, v in payload.items() if not k.startswith("q_gmap_gr") and k != "gmap_dense"}
-    out["q_gmap_sparse"] = words
-    out["q_gmap_sparse_prefix"] = np.stack([pre for _, pre in forms]).astype(np.int32)
-    out["compact3_use_block_gr"] = False
-    return out
 
 
 def make_projection(tris, seed, E, n, k, p=0.15, salient_counts=None, scale=False, bias=False):

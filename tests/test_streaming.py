@@ -161,6 +161,63 @@ def test_streamed_chain_matches_oracle(tris, oracle_mod, cuda, slots, with_backb
     _chain_against_oracle(oracle_mod, st, layers, x16, logits, TINY, f"slots={slots}", backbones=resident_bb)
 
 
+def test_split_bitmaps_partition(tris):
+    """split_bitmaps: the split-bitmap tensors go to the streamed dicts, every other key stays resident, and the
+    bitmap-only blob round-trips."""
+    from gr_cases import to_sparse
+    import oracle
+
+    layer = tris["synthetic"].make_layer(TINY, 31, tris["ext"].gr_encode, keep_dense_gmap=True)
+    for form in ("block_gr", "sparse"):
+        host = {p: (to_sparse(oracle, layer[p], TINY.rank) if form == "sparse" else
+                    {k: v for k, v in layer[p].items() if k != "gmap_dense"}) for p in streaming.PROJECTIONS}
+        streamed, rest = streaming.split_bitmaps(host)
+        for p in streaming.PROJECTIONS:
+            assert set(streamed[p]) | set(rest[p]) == set(host[p]) and not set(streamed[p]) & set(rest[p])
+            want = {"q_gmap_sparse", "q_gmap_sparse_prefix"} if form == "sparse" else \
+                {"q_gmap_gr_words", "q_gmap_gr_offsets", "q_gmap_gr_meta"}
+            assert set(streamed[p]) == want
+        lay = streaming.layer_layout(streamed)
+        blob = np.zeros(lay.nbytes, dtype=np.uint8)
+        streaming.pack_layer(streamed, None, lay, blob)
+        views, bb = streaming.unpack_views(lay, torch.from_numpy(blob))
+        assert bb is None
+        for p in streaming.PROJECTIONS:
+            for k, v in streamed[p].items():
+                np.testing.assert_array_equal(views[p][k].numpy(), v)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("form", ["sparse", "block_gr"])
+def test_streamed_bitmaps_only_match_oracle(tris, oracle_mod, cuda, form):
+    """The reference's staging mode (grouped_payload_sidecar.py:764-1146): only the split bitmaps stream
+    through two slots, every other payload tensor and the backbones stay resident; sparse-form payloads
+    (the format that mode serves) and block-GR ones; every layer against the oracle."""
+    from gr_cases import to_sparse
+
+    print(f"streamed bitmaps only, {form}", flush=True)
+    q = tris["qlinear"]
+    raw = [tris["synthetic"].make_layer(TINY, 900 + i, tris["ext"].gr_encode, keep_dense_gmap=True)
+           for i in range(4)]
+    layers = []
+    for l in raw:
+        conv = {p: (to_sparse(oracle_mod, l[p], TINY.rank) if form == "sparse" else
+                    {k: v for k, v in l[p].items() if k != "gmap_dense"}) for p in streaming.PROJECTIONS}
+        conv["backbones"] = l["backbones"]
+        layers.append(conv)
+    split = [streaming.split_bitmaps(l) for l in layers]
+    resident = [{p: q.payload_to_device(rest[p], cuda) for p in streaming.PROJECTIONS} for _, rest in split]
+    st = streaming.GroupedPayloadStreamer([s for s, _ in split], cuda, num_slots=2, resident=resident)
+    rng = np.random.default_rng(17)
+    T = 3
+    x16 = torch.from_numpy(rng.standard_normal((T, TINY.hidden)).astype(np.float16)).to(cuda)
+    logits = [torch.from_numpy(rng.standard_normal((T, TINY.num_experts)).astype(np.float32)).to(cuda)
+              for _ in layers]
+    bb = [{p: torch.from_numpy(l["backbones"][p]).to(cuda) for p in streaming.PROJECTIONS} for l in layers]
+    _chain_against_oracle(oracle_mod, st, layers, x16, logits, TINY, f"bitmaps only {form}", backbones=bb)
+    assert st.stats["copies"] == len(layers)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("p", [0.05, 0.15, 0.30])
 def test_streamed_mixtral_layers_match_oracle(tris, oracle_mod, cuda, p):
