@@ -115,6 +115,18 @@ int tris_build_grouped_route(const int64_t* selected_experts, int32_t num_tokens
                              int32_t* problem_offsets, int32_t* counts, int32_t* inverse_perm, void* stream);
 
 /*
+ * Router softmax, top-k and optional renormalisation for any batch: replaces route_topk with the fp16 cast
+ * of the routing weights (modeling_mixtral.py:548-555: F.softmax(dtype=float), torch.topk, weights /
+ * weights.sum, .to(fp16)), one wavefront per token, picks in descending probability with ties to the lower
+ * expert, the renormalising sum added in pick order.  routing_weights_f32 may be NULL.  Outputs
+ * [num_tokens, top_k]; num_experts <= 1024, top_k <= 16.  For batches past tris_route_topk_grouped's limit;
+ * tris_build_grouped_route then builds the route from selected_experts.
+ */
+int tris_route_topk(const float* router_logits, int32_t num_tokens, int32_t num_experts, int32_t top_k,
+                    int32_t renormalize, uint16_t* routing_weights_f16, float* routing_weights_f32,
+                    int64_t* selected_experts, void* stream);
+
+/*
  * Router softmax + top-k fused with the grouped route for decode-sized batches
  * (no reference counterpart: fuses F.softmax(router_logits, dtype=float),
  * torch.topk, the optional renormalisation and the routing-weight cast of

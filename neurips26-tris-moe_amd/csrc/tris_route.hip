@@ -593,6 +593,39 @@ __global__ __launch_bounds__(kRouteThreads) void route_topk_small_kernel(RouteAr
   route_small_body<P>(ra, sm, static_cast<int>(threadIdx.x));
 }
 
+// Softmax / top-k / renormalisation only, for batches past the one-launch router: one wavefront per token
+// (route_token_wave, P experts a lane), tokens spread over the grid; the route is then built by
+// route_histogram_kernel and route_scatter_kernel.  Each wavefront loads its next token's logits while it
+// routes the current one.
+constexpr int kRouteTokThreads = 256;
+constexpr int kRouteTokWaves = kRouteTokThreads / kWave;
+
+template <int P>
+__global__ __launch_bounds__(kRouteTokThreads) void route_topk_tokens_kernel(RouteArgs ra) {
+  const int lane = static_cast<int>(threadIdx.x) % kWave;
+  const int stride = static_cast<int>(gridDim.x) * kRouteTokWaves;
+  int t = static_cast<int>(blockIdx.x) * kRouteTokWaves + static_cast<int>(threadIdx.x) / kWave;
+  float nxt[P];
+  if (t < ra.tokens) route_load_logits<P>(ra.logits + static_cast<int64_t>(t) * ra.num_experts, ra.num_experts, nxt);
+  for (; t < ra.tokens; t += stride) {
+    float pv[P];
+#pragma unroll
+    for (int q = 0; q < P; ++q) pv[q] = nxt[q];
+    if (t + stride < ra.tokens) {
+      route_load_logits<P>(ra.logits + static_cast<int64_t>(t + stride) * ra.num_experts, ra.num_experts, nxt);
+    }
+    int pe;
+    float pw;
+    route_token_wave<P>(pv, ra.num_experts, ra.top_k, ra.renormalize, pe, pw);
+    if (lane < ra.top_k) {
+      const int64_t i = static_cast<int64_t>(t) * ra.top_k + lane;
+      ra.selected[i] = pe;
+      ra.weights16[i] = f2h_bits(pw);
+      if (ra.weights32 != nullptr) ra.weights32[i] = pw;
+    }
+  }
+}
+
 // Router variants: the one-wavefront router with pick lists of 2, 8 or 16 entries (the smallest that holds
 // top_k: shorter unrolled insertion chains), or the workgroup router with 1, 2, 4, 8 or 16 experts a lane
 // (the smallest that covers num_experts: fewer registers of probabilities and ballots per pick).
@@ -750,6 +783,46 @@ extern "C" int tris_route_topk_grouped(const float* router_logits, int32_t num_t
                          who);
   if (rc) return rc;
   return launch_route(ra, static_cast<hipStream_t>(stream), who);
+}
+
+extern "C" int tris_route_topk(const float* router_logits, int32_t num_tokens, int32_t num_experts, int32_t top_k,
+                               int32_t renormalize, uint16_t* routing_weights_f16, float* routing_weights_f32,
+                               int64_t* selected_experts, void* stream) {
+  const char* who = "tris_route_topk";
+  TRIS_REQUIRE(num_tokens >= 0 && num_experts > 0 && top_k > 0, "%s: bad shape", who);
+  TRIS_REQUIRE(top_k <= num_experts && top_k <= kRouteMaxTopK, "%s: top_k %d (at most %d and num_experts)", who,
+               top_k, kRouteMaxTopK);
+  TRIS_REQUIRE(num_experts <= kRouteSmallMaxExperts, "%s: num_experts %d exceeds %d", who, num_experts,
+               kRouteSmallMaxExperts);
+  if (num_tokens == 0) return TRIS_OK;
+  TRIS_REQUIRE(router_logits && routing_weights_f16 && selected_experts, "%s: null pointer", who);
+  RouteArgs ra{};
+  ra.logits = router_logits;
+  ra.tokens = num_tokens;
+  ra.num_experts = num_experts;
+  ra.top_k = top_k;
+  ra.renormalize = renormalize;
+  ra.weights16 = routing_weights_f16;
+  ra.weights32 = routing_weights_f32;
+  ra.selected = selected_experts;
+  // every token's wavefront resident at once up to 8192 workgroups (32768 tokens), then a grid-stride loop
+  const int64_t wgs = (static_cast<int64_t>(num_tokens) + kRouteTokWaves - 1) / kRouteTokWaves;
+  const dim3 grid(static_cast<unsigned>(wgs < 8192 ? wgs : 8192));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int per_lane = ceil_div(num_experts, kWave);
+  if (per_lane <= 1) {
+    hipLaunchKernelGGL((route_topk_tokens_kernel<1>), grid, dim3(kRouteTokThreads), 0, s, ra);
+  } else if (per_lane <= 2) {
+    hipLaunchKernelGGL((route_topk_tokens_kernel<2>), grid, dim3(kRouteTokThreads), 0, s, ra);
+  } else if (per_lane <= 4) {
+    hipLaunchKernelGGL((route_topk_tokens_kernel<4>), grid, dim3(kRouteTokThreads), 0, s, ra);
+  } else if (per_lane <= 8) {
+    hipLaunchKernelGGL((route_topk_tokens_kernel<8>), grid, dim3(kRouteTokThreads), 0, s, ra);
+  } else {
+    hipLaunchKernelGGL((route_topk_tokens_kernel<kRouteSmallMaxExperts / kWave>), grid, dim3(kRouteTokThreads), 0, s,
+                       ra);
+  }
+  return check_launch(who);
 }
 
 // Backbone token tiles per workgroup in the merged launch: the 1024-thread workgroup caps the kernel at 128

@@ -139,6 +139,7 @@ SIGNATURES = {
     "tris_route_topk_grouped": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                                 _P, _P, _P, _P]),
     "tris_grouped_forward_block_gr": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I32, _I64, _PAY, _P, _P]),
+    "tris_route_topk": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _P, _P, _P, _P]),
     "tris_grouped_forward_sparse": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I32, _I64, _PAY, _P, _P, _I32, _P, _P]),
     "tris_grouped_decode_forward_block_gr": (ctypes.c_int, [_P, _P, _I32, _I32, _P, _P, _I32, _PAY, _P, _P]),
     "tris_grouped_decode_pair_forward_block_gr": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _P, _P, _I32, _PAY, _PAY,

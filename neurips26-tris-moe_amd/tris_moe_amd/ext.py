@@ -262,6 +262,34 @@ def _route_topk_args(logits, out, top_k, renormalize, m_tile):
             _ptr(out["counts"]), _ptr(out["inverse_perm"]))
 
 
+def route_topk_ok(router_logits: torch.Tensor, top_k: int) -> bool:
+    """tris_route_topk takes these logits: fp32 [T, E] on the GPU, E <= ROUTE_TOPK_MAX_EXPERTS, 0 < top_k <=
+    min(E, ROUTE_TOPK_MAX_K)."""
+    if not isinstance(router_logits, torch.Tensor) or router_logits.device.type != "cuda":
+        return False
+    if router_logits.dtype != torch.float32 or router_logits.dim() != 2:
+        return False
+    e = int(router_logits.size(1))
+    return 0 < top_k <= min(e, ROUTE_TOPK_MAX_K) and e <= ROUTE_TOPK_MAX_EXPERTS
+
+
+def route_topk(router_logits: torch.Tensor, top_k: int, renormalize: bool):
+    """Router softmax / top-k / renormalisation and the fp16 cast (modeling_mixtral.py:548-555) in one launch
+    for any batch (tris_route_topk).  Returns (routing_weights fp32 [T, k], selected_experts int64 [T, k],
+    routing_weights fp16 [T, k])."""
+    if not route_topk_ok(router_logits, top_k):
+        raise RuntimeError("route_topk: fp32 [tokens, experts] logits on the GPU, experts <= "
+                           f"{ROUTE_TOPK_MAX_EXPERTS}, 0 < top_k <= min(experts, {ROUTE_TOPK_MAX_K})")
+    logits = router_logits.contiguous()
+    t, e = int(logits.size(0)), int(logits.size(1))
+    w32 = torch.empty((t, top_k), dtype=torch.float32, device=logits.device)
+    w16 = torch.empty((t, top_k), dtype=torch.float16, device=logits.device)
+    sel = torch.empty((t, top_k), dtype=torch.int64, device=logits.device)
+    _lib.check(_lib.load().tris_route_topk(_ptr(logits), t, e, top_k, int(bool(renormalize)), _ptr(w16), _ptr(w32),
+                                           _ptr(sel), _stream(logits)), "route_topk")
+    return w32, sel, w16
+
+
 def route_topk_grouped(router_logits: torch.Tensor, top_k: int, renormalize: bool, m_tile: int = 4) -> dict:
     """Router softmax / top-k / renormalisation (modeling_mixtral.py:548-555) and the padded grouped
     route in one launch, for decode-sized batches (an extension; see build_grouped_route_device).

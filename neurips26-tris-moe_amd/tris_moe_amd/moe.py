@@ -66,7 +66,8 @@ def grouped_moe_forward_from_logits(x16: torch.Tensor, router_logits: torch.Tens
                                     output_dtype=torch.bfloat16, shared_expert=None,
                                     expert_path: str = "auto") -> torch.Tensor:
     """The layer from router logits: softmax / top-k / renormalisation / route in one kernel when the
-    batch is decode-sized (tris_route_topk_grouped), else route_topk + the two-kernel route.  On the
+    batch is decode-sized (tris_route_topk_grouped), else the token-parallel tris_route_topk (torch's
+    route_topk for logits it does not take) + the two-kernel route.  On the
     predecoded path with fp16 gate/up backbones and at most ext.ROUTE_BACKBONE_MAX_TOKENS tokens, the
     gate/up backbones of the tokens run in the router's launch (tris_route_topk_backbone), their split-K
     reduction in the predecode's, and the grouped GEMMs gather their rows through the route's token
@@ -90,7 +91,11 @@ def grouped_moe_forward_from_logits(x16: torch.Tensor, router_logits: torch.Tens
         route = ext.route_topk_grouped(router_logits, top_k, renormalize, GROUPED_SEGMENT_M_TILE)
         return _forward_with_route(x16, route["routing_weights_f16"], route, top_k, payloads, backbones,
                                    num_experts, output_dtype, shared_expert, expert_path)
-    weights, selected = route_topk(router_logits, top_k, renormalize)
+    if ext.route_topk_ok(router_logits, top_k):
+        # past the one-launch router: the token-parallel softmax / top-k, then the two-kernel route
+        _, selected, weights = ext.route_topk(router_logits, top_k, renormalize)
+    else:
+        weights, selected = route_topk(router_logits, top_k, renormalize)
     return grouped_moe_forward(x16, weights, selected, payloads, backbones, num_experts, output_dtype,
                                shared_expert, expert_path)
 

@@ -388,6 +388,33 @@ def test_route_topk_fused_matches_oracle(tris, oracle_mod, cuda, t, k, e, renorm
     np.testing.assert_array_equal(r["perm"].cpu().numpy()[inv], np.arange(t * k))
 
 
+@pytest.mark.parametrize("t,k,e,renorm", [(2048, 2, 8, True), (1024, 8, 256, True), (3000, 1, 64, False),
+                                          (100, 16, 1024, True), (5, 3, 7, False), (40000, 2, 8, True),
+                                          (257, 6, 60, False), (0, 2, 8, True)])
+def test_route_topk_tokens_matches_oracle(tris, oracle_mod, cuda, t, k, e, renorm):
+    """The token-parallel router (tris_route_topk, batches past the one-launch router: C2's 2048 tokens, C3's
+    1024 tokens x top 8 of 256): selection exactly the oracle's, ties to the lower expert, weights within one
+    fp16 ulp; 40000 tokens run the grid-stride loop; then the two-kernel route of its picks is the oracle's."""
+    note(f"route topk tokens t={t} k={k} e={e} renorm={renorm}")
+    rng = np.random.default_rng(t * 7 + e + k)
+    logits = (rng.standard_normal((t, e)) * 1.5).astype(np.float32)
+    if t > 3:
+        logits[1, : min(e, 4)] = 0.25  # exact ties among the top experts
+        logits[3, :] = -1.0            # every expert tied
+    w, sel = oracle_mod.route_topk(logits, k, renorm)
+    w32, got_sel, w16 = tris["ext"].route_topk(torch.from_numpy(logits).to(cuda), k, renorm)
+    np.testing.assert_array_equal(got_sel.cpu().numpy(), sel)
+    np.testing.assert_allclose(w32.cpu().numpy(), w, rtol=2e-6, atol=1e-7)
+    got16 = w16.cpu().numpy().view(np.int16).astype(np.int32)
+    want16 = w.astype(np.float16).view(np.int16).astype(np.int32)
+    assert got16.size == 0 or np.abs(got16 - want16).max() <= 1
+    if 0 < t <= 4096:
+        route = tris["ext"].build_grouped_route_device(got_sel, e, 4)
+        want = oracle_mod.build_route(sel, e, 4)
+        for key in ("perm", "grouped_token_indices"):
+            np.testing.assert_array_equal(route[key].cpu().numpy(), np.asarray(want[key]), err_msg=key)
+
+
 def test_route_rejects_bad_expert_ids(tris, cuda):
     note("route bad ids")
     sel = torch.tensor([[0, 9]], dtype=torch.int64, device=cuda)
