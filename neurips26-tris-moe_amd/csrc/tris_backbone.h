@@ -16,6 +16,15 @@ constexpr int kBbKStep = 32;
 constexpr int kBbBatch = 8;          // K steps of loads in flight per wavefront
 constexpr int kBbTargetWgs = 512;    // aim for this many workgroups per launch
 constexpr int kBbMaxSlices = 32;        // slices of backbone_kernel
+// the tiled GEMM for prefill-size batches (backbone_gemm_kernel, tris_backbone.hip)
+constexpr int kBgTile = 128;         // rows and rank columns of a workgroup tile
+constexpr int kBgK = 64;             // K columns per LDS stage
+constexpr int kBgStride = kBgK + 8;  // fp16 per staged row: 144-byte rows spread the 16-byte reads over banks
+constexpr int kBgThreads = 256;
+constexpr int kBgMinRows = 512;      // rows from which the entry points take it
+constexpr int kBgMinStages = 8;      // K stages per slice at least
+constexpr int kBgTargetWgs = 512;
+constexpr int kBgMaxSlices = 16;
 constexpr int kBbReduceMaxSlices = 64;  // slices backbone_reduce_at adds (backbone_swiglu_kernel uses up to 64)
 
 struct BackboneProj {
@@ -194,12 +203,13 @@ struct BackbonePlan {
   int slice_k;
 };
 BackbonePlan backbone_plan(int tokens, int in_features, int rank);
-int64_t backbone_workspace_bytes(int tokens, int in_features, int rank, int nproj);
+int64_t backbone_workspace_bytes(int tokens, int in_features, int rank, int nproj, bool use_gemm = true);
+bool backbone_gemm_fits(int tokens, int in_features, int rank);
 // Validates one launch's arguments (tokens, in_features and rank > 0) and fills args and plan.
 int backbone_prepare(const uint16_t* x, int tokens, int in_features, const int64_t* row_index, const uint16_t* sv_a,
                      const uint16_t* sv_b, int rank, const uint16_t* in_scale_a, const uint16_t* in_scale_b,
                      uint16_t* out_a, uint16_t* out_b, void* workspace, int64_t workspace_bytes, BackboneArgs* args,
-                     BackbonePlan* plan, const char* who);
+                     BackbonePlan* plan, const char* who, bool use_gemm = false);
 // The slice reduction of a launch that left its partial sums in args.partials (slices > 1).
 int launch_backbone_reduce(const BackboneArgs& args, int nproj, hipStream_t s, const char* who);
 

@@ -66,8 +66,17 @@ int backbone_slices(int tokens, int in_features, int rank) {
   return slices < 1 ? 1 : static_cast<int>(slices);
 }
 
-int64_t backbone_workspace_bytes(int tokens, int in_features, int rank, int nproj) {
-  const int slices = backbone_slices(tokens, in_features, rank);
+static int backbone_gemm_slices(int tokens, int in_features, int rank);
+
+// use_gemm: the entry may take the tiled GEMM for prefill-size batches (backbone_gemm_fits); the
+// no-allocation entry keeps the decode-shaped kernel, whose partial sums stay small.
+int64_t backbone_workspace_bytes(int tokens, int in_features, int rank, int nproj, bool use_gemm) {
+  int slices = backbone_slices(tokens, in_features, rank);
+  if (use_gemm && backbone_gemm_fits(tokens, in_features, rank)) {
+    const int s0 = backbone_gemm_slices(tokens, in_features, rank);
+    const int ks = ceil_div(in_features / kBgK, s0) * kBgK;
+    slices = ceil_div(in_features, ks);
+  }
   return slices > 1 ? static_cast<int64_t>(nproj) * slices * tokens * rank * 4 : 0;
 }
 
@@ -84,7 +93,7 @@ BackbonePlan backbone_plan(int tokens, int in_features, int rank) {
 int backbone_prepare(const uint16_t* x, int tokens, int in_features, const int64_t* row_index, const uint16_t* sv_a,
                      const uint16_t* sv_b, int rank, const uint16_t* in_scale_a, const uint16_t* in_scale_b,
                      uint16_t* out_a, uint16_t* out_b, void* workspace, int64_t workspace_bytes, BackboneArgs* args,
-                     BackbonePlan* plan, const char* who) {
+                     BackbonePlan* plan, const char* who, bool use_gemm) {
   TRIS_REQUIRE(tokens > 0 && in_features > 0 && rank > 0, "%s: empty projection", who);
   TRIS_REQUIRE(out_a != nullptr && (sv_b == nullptr || out_b != nullptr), "%s: null output", who);
   TRIS_REQUIRE(x && sv_a, "%s: null input", who);
@@ -95,11 +104,13 @@ int backbone_prepare(const uint16_t* x, int tokens, int in_features, const int64
                "%s: x, sv and in_scale must be 16-byte aligned", who);
   const int nproj = sv_b != nullptr ? 2 : 1;
   const BackbonePlan pl = backbone_plan(tokens, in_features, rank);
-  const int64_t need = backbone_workspace_bytes(tokens, in_features, rank, nproj);
+  const int64_t need = backbone_workspace_bytes(tokens, in_features, rank, nproj, use_gemm);
   TRIS_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
                "%s: workspace of %lld bytes needed, %lld given", who, static_cast<long long>(need),
                static_cast<long long>(workspace_bytes));
-  TRIS_REQUIRE(static_cast<int64_t>(pl.token_groups) * pl.slices <= 65535, "%s: too many tokens", who);
+  TRIS_REQUIRE((use_gemm && backbone_gemm_fits(tokens, in_features, rank)) ||
+                   static_cast<int64_t>(pl.token_groups) * pl.slices <= 65535,
+               "%s: too many tokens", who);
   BackboneArgs a{};
   a.x = x;
   a.row_index = row_index;
@@ -116,10 +127,175 @@ int backbone_prepare(const uint16_t* x, int tokens, int in_features, const int64
   return TRIS_OK;
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// Prefill-size backbone: a tiled split-K MFMA GEMM.  hidden = fp16(x[row] * in_scale) . SV^T; workgroup
+// (mt, nt, s + slices * q) computes the 128 x 128 tile (rows 128 mt.., rank columns 128 nt..) of projection
+// q over K slice s.  Its four wavefronts each own a 64 x 64 quadrant (4 x 4 tiles of v_mfma_f32_16x16x32_f16).
+// Per stage of 64 K columns every thread copies four 16-byte runs of the x tile (rows read through row_index,
+// scaled by in_scale as fp16 products) and four of the SV tile into LDS; the next stage's global loads are in
+// flight in registers while the current stage is multiplied (two LDS buffers, one barrier a stage).  Slices
+// write fp32 partial tiles that backbone_reduce_kernel adds in slice order; one slice writes fp16 directly.
+
+struct BgArgs {
+  BackboneArgs b;
+  int slices;
+  int ks;  // K columns per slice, a multiple of kBgK
+};
+
+bool backbone_gemm_fits(int tokens, int in_features, int rank) {
+  return tokens >= kBgMinRows && rank % kBgTile == 0 && in_features % kBgK == 0 && in_features > 0;
+}
+
+// The slice count depends on the shape only (not on the projection count), so a pair launch gives each
+// projection the bits of its single launch.
+static int backbone_gemm_slices(int tokens, int in_features, int rank) {
+  const int64_t tiles = static_cast<int64_t>(ceil_div(tokens, kBgTile)) * (rank / kBgTile);
+  int64_t s = (kBgTargetWgs + tiles - 1) / tiles;
+  const int64_t max_by_k = in_features / (kBgK * kBgMinStages);
+  s = s < max_by_k ? s : max_by_k;
+  s = s < kBgMaxSlices ? s : kBgMaxSlices;
+  return s < 1 ? 1 : static_cast<int>(s);
+}
+
+__global__ __launch_bounds__(kBgThreads, 2) void backbone_gemm_kernel(BgArgs g) {
+  __shared__ __attribute__((aligned(16))) uint16_t la[2][kBgTile * kBgStride];
+  __shared__ __attribute__((aligned(16))) uint16_t lb[2][kBgTile * kBgStride];
+  const BackboneArgs& a = g.b;
+  const int q = static_cast<int>(blockIdx.z) / g.slices;
+  const int sl = static_cast<int>(blockIdx.z) % g.slices;
+  const BackboneProj pj = q == 0 ? a.proj[0] : a.proj[1];  // selected, not indexed: no private copy of the args
+  const int tid = static_cast<int>(threadIdx.x);
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int i16 = lane & 15, kg = lane >> 4;
+  const int m0 = static_cast<int>(blockIdx.x) * kBgTile;
+  const int n0 = static_cast<int>(blockIdx.y) * kBgTile;
+  const int K = a.in_features;
+  const int kbeg = sl * g.ks;
+  const int kn = (K - kbeg) < g.ks ? (K - kbeg) : g.ks;  // > 0, a multiple of kBgK
+  const int nstage = kn / kBgK;
+  // copy slots: thread tid moves 16-byte runs c = tid + 256 i (i < 4): row c / 8, columns 8 (c % 8) .. + 8
+  const uint16_t* xsrc[4];
+  const uint16_t* ssrc[4];
+  bool xv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + kBgThreads * i;
+    const int row = c >> 3, col = (c & 7) * 8;
+    const int m = m0 + row;
+    xv[i] = m < a.tokens;
+    const int64_t xrow = xv[i] ? (a.row_index != nullptr ? a.row_index[m] : m) : 0;
+    xsrc[i] = a.x + xrow * K + kbeg + col;
+    ssrc[i] = pj.sv + static_cast<int64_t>(n0 + row) * K + kbeg + col;
+  }
+  const uint16_t* scale = pj.in_scale != nullptr ? pj.in_scale + kbeg + (tid & 7) * 8 : nullptr;
+  uint4 ra0, ra1, ra2, ra3, rb0, rb1, rb2, rb3;
+// the stage's 16-byte runs into registers (x scaled by in_scale as fp16 products, as x * ns_col)
+#define TRIS_BG_LOAD(ko)                                                                                     \
+  do {                                                                                                       \
+    ra0 = xv[0] ? *reinterpret_cast<const uint4*>(xsrc[0] + (ko)) : make_uint4(0u, 0u, 0u, 0u);               \
+    ra1 = xv[1] ? *reinterpret_cast<const uint4*>(xsrc[1] + (ko)) : make_uint4(0u, 0u, 0u, 0u);               \
+    ra2 = xv[2] ? *reinterpret_cast<const uint4*>(xsrc[2] + (ko)) : make_uint4(0u, 0u, 0u, 0u);               \
+    ra3 = xv[3] ? *reinterpret_cast<const uint4*>(xsrc[3] + (ko)) : make_uint4(0u, 0u, 0u, 0u);               \
+    rb0 = *reinterpret_cast<const uint4*>(ssrc[0] + (ko));                                                   \
+    rb1 = *reinterpret_cast<const uint4*>(ssrc[1] + (ko));                                                   \
+    rb2 = *reinterpret_cast<const uint4*>(ssrc[2] + (ko));                                                   \
+    rb3 = *reinterpret_cast<const uint4*>(ssrc[3] + (ko));                                                   \
+    if (scale != nullptr) {                                                                                  \
+      const f16x8 sc = *reinterpret_cast<const f16x8*>(scale + (ko));                                        \
+      ra0 = __builtin_bit_cast(uint4, __builtin_bit_cast(f16x8, ra0) * sc);                                  \
+      ra1 = __builtin_bit_cast(uint4, __builtin_bit_cast(f16x8, ra1) * sc);                                  \
+      ra2 = __builtin_bit_cast(uint4, __builtin_bit_cast(f16x8, ra2) * sc);                                  \
+      ra3 = __builtin_bit_cast(uint4, __builtin_bit_cast(f16x8, ra3) * sc);                                  \
+    }                                                                                                        \
+  } while (0)
+// run c = tid + 256 i sits at row c / 8 (32 i + tid / 8), columns 8 (tid % 8)
+#define TRIS_BG_STORE(buf)                                                                                   \
+  do {                                                                                                       \
+    const int o = (tid >> 3) * kBgStride + (tid & 7) * 8;                                                    \
+    *reinterpret_cast<uint4*>(&la[buf][o]) = ra0;                                                            \
+    *reinterpret_cast<uint4*>(&la[buf][o + 32 * kBgStride]) = ra1;                                           \
+    *reinterpret_cast<uint4*>(&la[buf][o + 64 * kBgStride]) = ra2;                                           \
+    *reinterpret_cast<uint4*>(&la[buf][o + 96 * kBgStride]) = ra3;                                           \
+    *reinterpret_cast<uint4*>(&lb[buf][o]) = rb0;                                                            \
+    *reinterpret_cast<uint4*>(&lb[buf][o + 32 * kBgStride]) = rb1;                                           \
+    *reinterpret_cast<uint4*>(&lb[buf][o + 64 * kBgStride]) = rb2;                                           \
+    *reinterpret_cast<uint4*>(&lb[buf][o + 96 * kBgStride]) = rb3;                                           \
+  } while (0)
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  TRIS_BG_LOAD(0);
+  TRIS_BG_STORE(0);
+  __syncthreads();
+  for (int st = 0; st < nstage; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < nstage) TRIS_BG_LOAD((st + 1) * kBgK);
+    const uint16_t* A = la[buf] + (wm * 64 + i16) * kBgStride + kg * 8;
+    const uint16_t* B = lb[buf] + (wn * 64 + i16) * kBgStride + kg * 8;
+#pragma unroll
+    for (int kk = 0; kk < kBgK / 32; ++kk) {
+      f16x8 av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = *reinterpret_cast<const f16x8*>(A + i * 16 * kBgStride + kk * 32);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = *reinterpret_cast<const f16x8*>(B + j * 16 * kBgStride + kk * 32);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
+      }
+    }
+    if (st + 1 < nstage) TRIS_BG_STORE(buf ^ 1);
+    __syncthreads();
+  }
+#undef TRIS_BG_LOAD
+#undef TRIS_BG_STORE
+  // acc[i][j][v] = hidden[m0 + 64 wm + 16 i + 4 kg + v][n0 + 64 wn + 16 j + i16]
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = m0 + wm * 64 + i * 16 + kg * 4 + v;
+      if (m >= a.tokens) continue;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = n0 + wn * 64 + j * 16 + i16;
+        if (g.slices == 1) {
+          pj.out[static_cast<int64_t>(m) * a.rank + n] = f2h_bits(acc[i][j][v]);
+        } else {
+          a.partials[((static_cast<int64_t>(q) * g.slices + sl) * a.tokens + m) * a.rank + n] = acc[i][j][v];
+        }
+      }
+    }
+  }
+}
+
+static int launch_backbone_gemm(const BackboneArgs& base, int nproj, hipStream_t s, const char* who) {
+  BgArgs g{};
+  g.b = base;
+  g.slices = backbone_gemm_slices(base.tokens, base.in_features, base.rank);
+  g.ks = ceil_div(base.in_features / kBgK, g.slices) * kBgK;
+  g.slices = ceil_div(base.in_features, g.ks);
+  g.b.slices = g.slices;
+  TRIS_REQUIRE(static_cast<int64_t>(g.slices) * nproj <= 65535 && ceil_div(base.tokens, kBgTile) <= 2147483647,
+               "%s: grid too large", who);
+  const dim3 grid(static_cast<unsigned>(ceil_div(base.tokens, kBgTile)), static_cast<unsigned>(base.rank / kBgTile),
+                  static_cast<unsigned>(g.slices * nproj));
+  hipLaunchKernelGGL(backbone_gemm_kernel, grid, dim3(kBgThreads), 0, s, g);
+  int rc = check_launch(who);
+  if (rc || g.slices == 1) return rc;
+  return launch_backbone_reduce(g.b, nproj, s, who);
+}
+
 int launch_backbone(const uint16_t* x, int tokens, int in_features, const int64_t* row_index, const uint16_t* sv_a,
                     const uint16_t* sv_b, int rank, const uint16_t* in_scale_a, const uint16_t* in_scale_b,
                     uint16_t* out_a, uint16_t* out_b, void* workspace, int64_t workspace_bytes, void* stream,
-                    const char* who) {
+                    const char* who, bool use_gemm = true) {
   TRIS_REQUIRE(tokens >= 0 && in_features >= 0 && rank >= 0, "%s: negative shape", who);
   if (tokens == 0 || rank == 0) return TRIS_OK;
   TRIS_REQUIRE(out_a != nullptr && (sv_b == nullptr || out_b != nullptr), "%s: null output", who);
@@ -136,8 +312,9 @@ int launch_backbone(const uint16_t* x, int tokens, int in_features, const int64_
   BackboneArgs args;
   BackbonePlan pl;
   int rc = backbone_prepare(x, tokens, in_features, row_index, sv_a, sv_b, rank, in_scale_a, in_scale_b, out_a, out_b,
-                            workspace, workspace_bytes, &args, &pl, who);
+                            workspace, workspace_bytes, &args, &pl, who, use_gemm);
   if (rc) return rc;
+  if (use_gemm && backbone_gemm_fits(tokens, in_features, rank)) return launch_backbone_gemm(args, nproj, s, who);
   const dim3 grid(pl.row_tiles, pl.token_groups * pl.slices, nproj);
   switch (pl.tt) {
     case 1: hipLaunchKernelGGL((backbone_kernel<1, 8>), grid, dim3(kBbThreads), 0, s, args); break;
@@ -618,7 +795,7 @@ extern "C" int tris_backbone_linear_noalloc(const uint16_t* x, int32_t tokens, i
                                            const int64_t* row_index, const uint16_t* sv, int32_t rank,
                                            const uint16_t* in_scale, uint16_t* out, void* stream) {
   TRIS_REQUIRE(tokens >= 0 && in_features >= 0 && rank >= 0, "tris_backbone_linear_noalloc: negative shape");
-  const int64_t need = backbone_workspace_bytes(tokens, in_features, rank, 1);
+  const int64_t need = backbone_workspace_bytes(tokens, in_features, rank, 1, false);
   TRIS_REQUIRE(need <= kNoAllocScratchBytes,
                "tris_backbone_linear_noalloc: %d tokens x %d rank need %lld bytes of scratch, the static buffer "
                "holds %lld (use tris_backbone_linear with a workspace)",
@@ -629,7 +806,7 @@ extern "C" int tris_backbone_linear_noalloc(const uint16_t* x, int32_t tokens, i
     if (rc) return rc;
   }
   return launch_backbone(x, tokens, in_features, row_index, sv, nullptr, rank, in_scale, nullptr, out, nullptr, ws,
-                         need, stream, "tris_backbone_linear_noalloc");
+                         need, stream, "tris_backbone_linear_noalloc", false);
 }
 
 extern "C" int tris_backbone_linear_pair(const uint16_t* x, int32_t tokens, int32_t in_features,

@@ -824,8 +824,20 @@ BACKBONE_LIBRARY_MIN_ROWS = 256
 BACKBONE_LIBRARY_MIN_ELEMS = 1 << 19
 
 
-def _backbone_use_library(rows: int, in_features: int) -> bool:
-    return rows >= BACKBONE_LIBRARY_MIN_ROWS and rows * in_features > BACKBONE_LIBRARY_MIN_ELEMS
+# Rows from which the Python layer sends a backbone with rank a multiple of 128 and in_features of 64 to
+# tris_backbone_linear[_pair], whose tiled split-K GEMM takes such shapes from 512 rows (C callers, which have no
+# library GEMM).  Measured on MI355X at the prefill shapes: 103 us for 4096 x 14336 -> 512 plus a 17 us slice
+# reduction, against the library GEMM's 91-103 us alone, so the layer keeps the library GEMM (this threshold off).
+BACKBONE_GEMM_MIN_ROWS = 1 << 30
+
+
+def _backbone_gemm_ok(rows: int, in_features: int, rank: int) -> bool:
+    return rows >= BACKBONE_GEMM_MIN_ROWS and rank % 128 == 0 and in_features % 64 == 0 and in_features > 0
+
+
+def _backbone_use_library(rows: int, in_features: int, rank: int = 0) -> bool:
+    return (rows >= BACKBONE_LIBRARY_MIN_ROWS and rows * in_features > BACKBONE_LIBRARY_MIN_ELEMS
+            and not _backbone_gemm_ok(rows, in_features, rank))
 
 
 def _backbone_library(x, svs, in_scales, row_index):
@@ -857,8 +869,11 @@ def backbone_linear(x: torch.Tensor, sv: torch.Tensor, in_scale: torch.Tensor | 
     if in_scale is not None:
         _check_cuda("in_scale", in_scale, torch.float16, 1, x.device)
     rank, in_f = int(sv.size(0)), int(sv.size(1))
-    if _backbone_use_library(tokens, in_f):
+    if _backbone_use_library(tokens, in_f, rank):
         return _backbone_library(x, (sv,), (in_scale,), row_index)[0]
+    if row_index is not None and x.size(0) < tokens and _backbone_gemm_ok(int(x.size(0)), in_f, rank):
+        # more routed rows than tokens: project each token once, then gather the projected rows
+        return backbone_linear(x, sv, in_scale=in_scale).index_select(0, row_index)
     out = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
     lib = _lib.load()
     ws = backbone_workspace(x.device, int(lib.tris_backbone_workspace_bytes(tokens, in_f, rank)))
@@ -886,9 +901,13 @@ def backbone_linear_pair(x: torch.Tensor, sv_a: torch.Tensor, sv_b: torch.Tensor
             if sc.numel() != x.size(1):
                 raise RuntimeError(f"{name} must hold in_features values")
     rank, in_f = int(sv_a.size(0)), int(sv_a.size(1))
-    if _backbone_use_library(tokens, in_f):
+    if _backbone_use_library(tokens, in_f, rank):
         out_a, out_b = _backbone_library(x, (sv_a, sv_b), (in_scale_a, in_scale_b), row_index)
         return out_a, out_b
+    if row_index is not None and x.size(0) < tokens and _backbone_gemm_ok(int(x.size(0)), in_f, rank):
+        # more routed rows than tokens: project each token once, then gather the projected rows
+        out_a, out_b = backbone_linear_pair(x, sv_a, sv_b, in_scale_a=in_scale_a, in_scale_b=in_scale_b)
+        return out_a.index_select(0, row_index), out_b.index_select(0, row_index)
     out_a = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
     out_b = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
     lib = _lib.load()
