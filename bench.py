@@ -189,7 +189,9 @@ def main():
                    "active_experts": main_res["active_experts"], "step_bytes": int(main_res["step_bytes"]),
                    "expert_bytes": int(main_res["expert_bytes"]), "layer_copies": args.layers,
                    "expert_path": args.expert_path,
-                   "graph": f"one HIP graph of {args.layers} steps (one per layer copy), replayed"},
+                   "graph": (f"one HIP graph of {args.layers} steps (one per layer copy), replayed"
+                             if main_res["steps"] % args.layers == 0 else
+                             f"one HIP graph of {main_res['steps']} steps cycling through the layer copies")},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "sweep": sweep,
@@ -288,18 +290,22 @@ class LayerBench:
         for i in range(max(warmup, 1)):
             step(i)
         torch.cuda.synchronize()
-        reps = max(1, -(-steps // len(cps)))
+        # exactly `steps` steps: one pass over the copies replayed steps / copies times, or, when the copies do
+        # not divide the step count, one pass of `steps` steps cycling through them
+        steps = max(1, steps)
+        per_run = len(cps) if steps % len(cps) == 0 else steps
+        reps = steps // per_run
         if graph:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                for i in range(len(cps)):
+                for i in range(per_run):
                     step(i)
             g.replay()
             torch.cuda.synchronize()
             run = g.replay
         else:
             def run():
-                for i in range(len(cps)):
+                for i in range(per_run):
                     step(i)
             run()
             torch.cuda.synchronize()
@@ -309,7 +315,7 @@ class LayerBench:
             run()
         end.record()
         torch.cuda.synchronize()
-        n = reps * len(cps)
+        n = reps * per_run
         ms = start.elapsed_time(end) / n
         sb, eb, active = self.step_bytes(logits, tokens, backbone_bytes)
         return {"tokens": tokens, "steps": n, "ms_per_step": ms, "tokens_per_s": tokens / (ms / 1e3),
