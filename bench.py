@@ -332,6 +332,7 @@ def config_bench(args, name, dev):
     t0 = time.time()
     layer = synthetic.make_layer(spec, args.seed, ext.gr_encode)
     lb = LayerBench(spec, layer, 8, dev)
+    lb.expert_path = args.expert_path
     log(f"{spec.name}: layer generated in {time.time() - t0:.1f}s")
     out = {"workload": f"{spec.name}_moe_layer", "hidden": spec.hidden, "experts": spec.num_experts,
            "intermediate": spec.intermediate, "top_k": spec.top_k, "rank": spec.rank,
