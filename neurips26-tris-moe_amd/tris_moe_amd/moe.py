@@ -232,6 +232,11 @@ def _side_stream(device: torch.device, which: int = 0) -> torch.cuda.Stream:
 # decode shape: 17.6 vs 18.9 us at 2 rows, 49.7 vs 42.3 us at 32 rows).
 FUSED_SWIGLU_MAX_ROWS = 4
 
+# From this mean of routed rows per segment the grouped GEMMs run weight-stationary, which stages
+# materialised rows faster than it gathers them through token indices (C2 prefill: 0.68 against 0.92 ms), so the
+# backbones project the routed rows there; below it the GEMMs gather (A3B T = 1024: 353 -> 339 us).
+WS_GATHER_MIN_ROWS_PER_SEGMENT = 64
+
 # The down projection's null-space compensation runs on the side stream beside the down backbone and GEMM
 # (True) or on the caller's stream after the GEMM (False).
 NS_DOWN_BESIDE_GEMM = True
@@ -290,6 +295,13 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     if backbone_pending is not None:
         ext.grouped_block_gr_predecode_multi(pre_jobs, eid, backbone=backbone_pending)
         hid_g, hid_u = backbone_pending.out_a, backbone_pending.out_b
+        gather = route["grouped_token_indices"]
+    elif ext.mfma_payload_ok(pg) and ext.mfma_payload_ok(pu) and R < WS_GATHER_MIN_ROWS_PER_SEGMENT * slots:
+        ext.grouped_block_gr_predecode_multi(pre_jobs, eid)
+        # the tokens' gate/up backbones; the decode-sized MFMA GEMMs read each routed row through its token index,
+        # so the projected rows are never gathered (T rows projected instead of T * top_k)
+        hid_g, hid_u = shared_projection_pair(x16, backbones["gate"], backbones["up"], in_scale_a=sc["gate"],
+                                              in_scale_b=sc["up"])
         gather = route["grouped_token_indices"]
     else:
         ext.grouped_block_gr_predecode_multi(pre_jobs, eid)
