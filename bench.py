@@ -14,7 +14,7 @@ copy (as a model's decode graph holds its layers), and the timed region
 replays it.
 
 Prints ONE JSON line.  ``value`` is MoE-layer tokens/s at T = 16; ``hbm_gbps``
-the step's algorithmic bytes (SURVEY.md 8(d): the active experts' compressed
+the step's algorithmic bytes (the active experts' compressed
 payload + backbones + layer input/output) / step time, ``step_roofline_frac``
 that over 8 TB/s; ``roofline`` is for the dominant kernel, timed live with HIP
 events on its own stream over the same algorithmic (compressed) bytes of the
@@ -254,7 +254,7 @@ class LayerBench:
         return x16, torch.from_numpy(inp["router_logits"]).to(self.dev)
 
     def step_bytes(self, logits, tokens, backbone_bytes=None):
-        """active experts' compressed payload + backbones + layer input and output
+        """Algorithmic bytes: active experts' compressed payload + backbones + layer input and output
         (+ the shared expert's fp16 weights)."""
         import numpy as np
 
@@ -416,7 +416,7 @@ def prefill_bench(args, lb):
 # ------------------------------------------------------------------------------------------ dominant kernel
 def gateup_kernel(lb, rows, active, hid_g, hid_u, eid, seg, prob):
     """The gate/up grouped GEMM the layer step runs at `rows` routed rows: returns (launch(copy index),
-    kernel name, compressed bytes per launch (SURVEY.md 8(d): the routed experts' gate and up payloads with
+    kernel name, compressed bytes per launch (the routed experts' gate and up payloads with
     their GR streams, the two backbone outputs read, the fp16 output(s) written), kind)."""
     import torch
 
@@ -506,7 +506,7 @@ def dominant_kernel_roofline(args, lb, main_res):
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(args.tokens, kind),
             "kernel": kname, "kernel_us": round(kernel_s * 1e6, 2), "bytes_per_launch": int(kbytes),
-            "bytes": "compressed (SURVEY.md 8(d)): routed experts' gate+up payloads incl. GR words, "
+            "bytes": "compressed: routed experts' gate+up payloads incl. GR words, "
                      "backbone outputs read, outputs written"}
 
 
