@@ -4,8 +4,10 @@
 Headline workload: one Mixtral-8x7B-shaped MoE layer
 at decode (hidden 4096, 8 experts, intermediate 14336, top-2, rank-512 fp16
 backbones, binarised compact3 experts with a block-GR split bitmap at
-p = 0.15), T = 16 tokens.  A step is one full layer forward from the router
-logits: fused softmax / top-k / route, the gate/up backbone pair, the grouped
+p = 0.15), T = 16 tokens.  A step is the whole block (TrisSparseMoeBlock.forward,
+modeling_mixtral.py:539-608) from the bf16 activations: the router Linear (its
+weight drawn so the logits are N(0, 1) as the config states), the bf16 -> fp16
+cast, fused softmax / top-k / route, the gate/up backbone pair, the grouped
 gate/up GEMM with the SwiGLU product, the down backbone, the grouped down GEMM
 and the weighted scatter-add.  Synthetic seeded data; the steps cycle through
 --layers identical-content layer copies resident in HBM (so weights come from
@@ -115,7 +117,7 @@ def main():
         SPEC = dataclasses.replace(SPEC, gmap_p=args.gmap_p)
     layer = synthetic.make_layer(SPEC, args.seed, ext.gr_encode)
     log(f"synthetic C1 layer generated in {time.time() - t0:.1f}s (p = {SPEC.gmap_p:g})")
-    lb = LayerBench(SPEC, layer, args.layers, dev)
+    lb = LayerBench(SPEC, layer, args.layers, dev, seed=args.seed)
     lb.expert_path = args.expert_path
     if args.profile_kernel:
         profile_dominant_kernel(args, lb)
@@ -144,7 +146,7 @@ def main():
         if p == SPEC.gmap_p:
             continue
         dl = synthetic.make_layer(SPEC, args.seed, ext.gr_encode, gmap_p=p)
-        db = LayerBench(SPEC, dl, args.layers, dev)
+        db = LayerBench(SPEC, dl, args.layers, dev, seed=args.seed)
         r = db.measure(args.tokens, max(args.steps // 2, 2 * args.layers), args.warmup, args.seed + args.tokens)
         db.release()
         density[f"p{p:g}"] = summary(r)
@@ -212,10 +214,26 @@ def summary(r):
     return out
 
 
-class LayerBench:
-    """One synthetic layer of a config with `copies` HBM-resident copies, and the decode-step timing."""
+def router_weight(spec, seed):
+    """The router Linear's weight [E, H] (bf16 values), drawn so that its logits on the synthetic activations
+    are N(0, router_std) as the config states: N(0, router_std^2 / E||x||^2) entries, E||x||^2 = H + the
+    outlier channels' extra variance."""
+    import numpy as np
 
-    def __init__(self, spec, layer, copies, dev, backbones=None):
+    from tris_moe_amd import synthetic
+
+    rng = np.random.default_rng(seed)
+    ex2 = spec.hidden + spec.outlier_channels * (spec.outlier_scale ** 2 - 1.0)
+    w = rng.standard_normal((spec.num_experts, spec.hidden), dtype=np.float32) * np.float32(spec.router_std / ex2 ** 0.5)
+    return synthetic.bf16_round(w)
+
+
+class LayerBench:
+    """One synthetic layer of a config with `copies` HBM-resident copies, and the decode-step timing.  A step is
+    the whole block, TrisSparseMoeBlock.forward: the router Linear on the bf16 activations, the bf16 -> fp16
+    cast of the kernel input, and the grouped layer to the bf16 output (modeling_mixtral.py:539-608)."""
+
+    def __init__(self, spec, layer, copies, dev, backbones=None, seed=0):
         import torch
 
         from tris_moe_amd import qlinear
@@ -230,32 +248,66 @@ class LayerBench:
         self.copies = [({p: clone(base_pl[p]) for p in PROJS}, {k: (v.clone() if isinstance(v, torch.Tensor) else v)
                                                                  for k, v in base_bb.items()})
                        for _ in range(copies)]
+        self.router_w = torch.from_numpy(router_weight(spec, seed + 77)).to(dev).to(torch.bfloat16)
+        self.routers = [self.router_w.clone() for _ in range(copies)]
         self.shared = None
         if "shared_expert" in layer:
-            self.shared = [tuple(torch.from_numpy(w).to(dev) for w in layer["shared_expert"]) for _ in range(copies)]
+            gate = torch.from_numpy(layer["shared_expert_gate"]).to(dev).to(torch.bfloat16)
+            self.shared = [tuple(torch.from_numpy(w).to(dev) for w in layer["shared_expert"]) + (gate.clone(),)
+                           for _ in range(copies)]
         torch.cuda.synchronize()
         log(f"{spec.name}: {copies} layer copies resident")
+
+    def copy_nbytes(self) -> int:
+        """Device bytes of one layer copy (payloads, backbones, router, shared expert)."""
+        import torch
+
+        pl, bb = self.copies[0]
+        n = sum(v.numel() * v.element_size() for p in PROJS for v in pl[p].values() if isinstance(v, torch.Tensor))
+        n += sum(v.numel() * v.element_size() for v in bb.values() if isinstance(v, torch.Tensor))
+        n += self.routers[0].numel() * 2
+        if self.shared is not None:
+            n += sum(w.numel() * w.element_size() for w in self.shared[0])
+        return n
 
     def release(self):
         import torch
 
         self.copies = None
         self.shared = None
+        self.routers = None
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
 
     def inputs(self, tokens, seed):
+        """The bf16 block input [T, H] and the router logits the block computes from it (fp32)."""
         import torch
+        import torch.nn.functional as F
 
         from tris_moe_amd import synthetic
 
         inp = synthetic.make_inputs(self.spec, tokens, seed, self.layer["outlier_idx"])
-        x16 = torch.from_numpy(inp["x"]).to(self.dev).to(torch.bfloat16).to(torch.float16)
-        return x16, torch.from_numpy(inp["router_logits"]).to(self.dev)
+        x = torch.from_numpy(inp["x"]).to(self.dev).to(torch.bfloat16)
+        logits = F.linear(x, self.router_w).float()
+        return x, logits
+
+    def block(self, i, copies=None):
+        """A TrisSparseMoeBlock over layer copy i's device tensors (no copies made)."""
+        from tris_moe_amd import moe
+
+        cps = self.copies if copies is None else copies
+        pl, bb = cps[i % len(cps)]
+        sh = self.shared[i % len(self.shared)] if self.shared is not None else None
+        spec = self.spec
+        blk = moe.TrisSparseMoeBlock(spec.hidden, spec.num_experts, spec.top_k, pl, bb, renormalize=spec.renormalize,
+                                     shared_expert=sh[:3] if sh is not None else None,
+                                     shared_expert_gate=sh[3] if sh is not None else None)
+        blk.gate.weight.data = self.routers[i % len(self.routers)]
+        return blk
 
     def step_bytes(self, logits, tokens, backbone_bytes=None):
         """Algorithmic bytes: active experts' compressed payload + backbones + layer input and output
-        (+ the shared expert's fp16 weights)."""
+        (+ the router weight, the shared expert's fp16 weights and its gate)."""
         import numpy as np
 
         from tris_moe_amd import moe, synthetic
@@ -266,26 +318,25 @@ class LayerBench:
         if backbone_bytes is None:
             backbone_bytes = sum(self.layer["backbones"][p].nbytes for p in PROJS)
         shared_bytes = sum(int(np.asarray(a).nbytes) for a in self.layer.get("shared_expert", ()))
-        act_bytes = 2 * tokens * self.spec.hidden * 2
+        if "shared_expert_gate" in self.layer:
+            shared_bytes += 2 * self.spec.hidden
+        act_bytes = 2 * tokens * self.spec.hidden * 2 + 2 * self.spec.num_experts * self.spec.hidden
         return expert_bytes + backbone_bytes + act_bytes + shared_bytes, expert_bytes, active
 
     def measure(self, tokens, steps, warmup, seed, copies=None, backbone_bytes=None, graph=True):
-        """Mean time of one layer step at `tokens`: steps cycle through the layer copies; one graph holds one
+        """Mean time of one block step at `tokens`: steps cycle through the layer copies; one graph holds one
         step per copy and is replayed ceil(steps / copies) times (graph=False: eager launches)."""
         import torch
 
-        from tris_moe_amd import moe
-
         cps = self.copies if copies is None else copies
-        spec = self.spec
-        x16, logits = self.inputs(tokens, seed)
+        x, logits = self.inputs(tokens, seed)
+        x3 = x.view(1, tokens, self.spec.hidden)
+        blocks = [self.block(i, cps) for i in range(len(cps))]
+        for b in blocks:
+            b.expert_path = self.expert_path
 
         def step(i):
-            pl, bb = cps[i % len(cps)]
-            sh = self.shared[i % len(self.shared)] if self.shared is not None else None
-            return moe.grouped_moe_forward_from_logits(x16, logits, spec.top_k, spec.renormalize, pl, bb,
-                                                       spec.num_experts, torch.bfloat16, shared_expert=sh,
-                                                       expert_path=self.expert_path)
+            return blocks[i % len(blocks)].forward(x3)[0]
 
         for i in range(max(warmup, 1)):
             step(i)
@@ -320,7 +371,8 @@ class LayerBench:
         sb, eb, active = self.step_bytes(logits, tokens, backbone_bytes)
         return {"tokens": tokens, "steps": n, "ms_per_step": ms, "tokens_per_s": tokens / (ms / 1e3),
                 "hbm_gbps": sb / (ms / 1e3) / 1e9, "step_bytes": sb, "expert_bytes": eb,
-                "active_experts": len(active), "x16": x16, "logits": logits, "active": active}
+                "active_experts": len(active), "x16": x.to(torch.float16), "x": x, "logits": logits,
+                "active": active}
 
 
 def config_bench(args, name, dev):
@@ -331,12 +383,16 @@ def config_bench(args, name, dev):
     spec = {"c0": C0_OLMOE, "c3": C3_A3B}[name]
     t0 = time.time()
     layer = synthetic.make_layer(spec, args.seed, ext.gr_encode)
-    lb = LayerBench(spec, layer, 8, dev)
+    # enough copies that their footprint (C0 about 22 MB, C3 about 70 MB each) exceeds the 256 MB last-level cache
+    copies = 16 if name == "c0" else 8
+    lb = LayerBench(spec, layer, copies, dev, seed=args.seed)
     lb.expert_path = args.expert_path
     log(f"{spec.name}: layer generated in {time.time() - t0:.1f}s")
     out = {"workload": f"{spec.name}_moe_layer", "hidden": spec.hidden, "experts": spec.num_experts,
            "intermediate": spec.intermediate, "top_k": spec.top_k, "rank": spec.rank,
-           "shared_expert_intermediate": spec.shared_expert_intermediate, "layer_copies": 8}
+           "shared_expert_intermediate": spec.shared_expert_intermediate,
+           "shared_expert_gate": "shared_expert_gate" in layer, "layer_copies": copies,
+           "layer_copy_bytes": int(lb.copy_nbytes())}
     for tok in spec.tokens:
         r = lb.measure(tok, 64 if tok <= 64 else 16, 3, args.seed + tok, graph=tok <= 64)
         out[f"T{tok}"] = summary(r)
@@ -524,8 +580,8 @@ def profile_dominant_kernel(args, lb):
     """Eager launches of the dominant kernel at the bench workload, for hardware-counter runs."""
     import torch
 
-    x16, logits = lb.inputs(args.tokens, args.seed + args.tokens)
-    launch, kname, nbytes, kind = _dominant_setup(lb, x16, logits)
+    x, logits = lb.inputs(args.tokens, args.seed + args.tokens)
+    launch, kname, nbytes, kind = _dominant_setup(lb, x.to(torch.float16), logits)
     for r in range(args.kernel_reps):
         launch(r % len(lb.copies))
     torch.cuda.synchronize()

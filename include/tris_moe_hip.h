@@ -411,8 +411,11 @@ int tris_backbone_linear_pair(const uint16_t* x, int32_t tokens, int32_t in_feat
  * held by every GPU the library runs on until the process ends); its address is looked up once per device
  * on the first call.  Every call on one GPU shares that GPU's array: calls that overlap on one GPU (on
  * different streams, or from different threads) race.  Each launch writes every partial sum it reads, so
- * no clearing is needed.  Shapes whose partial sums exceed the array are rejected with TRIS_ERR_INVALID.
- * Same arguments and results (bit for bit) as tris_backbone_linear otherwise.
+ * no clearing is needed.  It runs tris_backbone_linear's plan (the same kernel and split-K slice count), so
+ * every shape it accepts gives tris_backbone_linear's results bit for bit.  Shapes whose partial sums
+ * (tris_backbone_workspace_bytes) exceed the array are rejected with TRIS_ERR_INVALID: decode-sized batches
+ * always fit (below 4 MiB), prefill-size ones (512 rows on, rank a multiple of 128, in_features of 64) may
+ * not.
  */
 int tris_backbone_linear_noalloc(const uint16_t* x, int32_t tokens, int32_t in_features, const int64_t* row_index,
                                  const uint16_t* sv, int32_t rank, const uint16_t* in_scale, uint16_t* out,
@@ -639,6 +642,26 @@ int tris_swiglu_mul_compensated(const uint16_t* gate, const uint16_t* up, const 
 int tris_moe_combine_compensated(const uint16_t* expert_out, const uint16_t* expert_comp, const int32_t* inverse_perm,
                                  const uint16_t* weights, const uint16_t* shared, int32_t tokens, int32_t top_k,
                                  int32_t hidden, uint16_t* out, void* stream);
+
+/*
+ * The block's output with a gated shared expert: replaces the end of the Qwen MoE blocks' forward
+ * (modeling_qwen2_moe.py:815-818, modeling_qwen3_5_moe.py:186-188):
+ *   shared_expert_output = shared_expert(h).to(dt)
+ *   shared_expert_gate   = sigmoid(shared_expert_gate(h)).to(dt)      (Linear(hidden, 1, bias=False))
+ *   final = final + shared_expert_gate * shared_expert_output
+ * with final = the routed combine of tris_moe_combine_compensated in the output dtype dt (bf16 when
+ * out_bf16, else fp16).  Per token t and feature h, every step rounded to dt as torch rounds it:
+ *   g = dt(sigmoid(dt(shared_gate_input[t] . shared_gate_weight)))    (fp32 sum of exact products)
+ *   out[t, h] = dt(dt(routed[t, h]) + dt(g * dt(shared[t, h])))
+ * shared_gate_input [tokens, hidden] and shared_gate_weight [hidden] are in dt (the block's model dtype,
+ * as h and the gate Linear are); shared fp16 [tokens, hidden]; out dt [tokens, hidden].  With
+ * shared_gate_weight NULL the shared output (or none, with shared NULL) is added ungated before the one
+ * rounding, as tris_moe_combine does, in dt.  Tensors are 16-byte aligned when hidden % 8 == 0.
+ */
+int tris_moe_combine_gated(const uint16_t* expert_out, const uint16_t* expert_comp, const int32_t* inverse_perm,
+                           const uint16_t* weights, const uint16_t* shared, const uint16_t* shared_gate_input,
+                           const uint16_t* shared_gate_weight, int32_t tokens, int32_t top_k, int32_t hidden,
+                           int32_t out_bf16, uint16_t* out, void* stream);
 
 #ifdef __cplusplus
 }

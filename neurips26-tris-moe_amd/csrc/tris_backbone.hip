@@ -68,8 +68,7 @@ int backbone_slices(int tokens, int in_features, int rank) {
 
 static int backbone_gemm_slices(int tokens, int in_features, int rank);
 
-// use_gemm: the entry may take the tiled GEMM for prefill-size batches (backbone_gemm_fits); the
-// no-allocation entry keeps the decode-shaped kernel, whose partial sums stay small.
+// use_gemm: the entry may take the tiled GEMM for prefill-size batches (backbone_gemm_fits).
 int64_t backbone_workspace_bytes(int tokens, int in_features, int rank, int nproj, bool use_gemm) {
   int slices = backbone_slices(tokens, in_features, rank);
   if (use_gemm && backbone_gemm_fits(tokens, in_features, rank)) {
@@ -755,9 +754,12 @@ extern "C" int tris_backbone_linear(const uint16_t* x, int32_t tokens, int32_t i
 
 // ---- tris_backbone_linear_noalloc: the split-K partial sums in a file-scope device array instead of a
 // caller workspace, for callers that cannot allocate (code under HIP graph capture, tight serving loops).
-// The partial sums need slices * tokens * rank * 4 bytes; the slice count aims at kBbTargetWgs workgroups,
-// which keeps that at most about 32768 * 64 bytes (2 MiB) for every shape, so 4 MiB is never exceeded in
-// practice.  Every launch writes every partial sum it reads, so the array needs no clearing between calls.
+// It runs the workspace entry's plan (the same kernel and slice count for every shape, so the same bits).
+// The partial sums need slices * tokens * rank * 4 bytes.  On the decode-shaped kernel the slice count aims
+// at kBbTargetWgs workgroups of up to 64 x 16 outputs, which keeps that below 2 * 511 * 64 * 16 * 4 bytes
+// (just under 4 MiB) for every shape; the tiled GEMM of prefill-size batches (kBgMinRows rows on) can need
+// more, and such shapes are rejected.  Every launch writes every partial sum it reads, so the array needs no
+// clearing between calls.
 constexpr int64_t kNoAllocScratchBytes = 4ll << 20;
 static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
 
@@ -795,18 +797,19 @@ extern "C" int tris_backbone_linear_noalloc(const uint16_t* x, int32_t tokens, i
                                            const int64_t* row_index, const uint16_t* sv, int32_t rank,
                                            const uint16_t* in_scale, uint16_t* out, void* stream) {
   TRIS_REQUIRE(tokens >= 0 && in_features >= 0 && rank >= 0, "tris_backbone_linear_noalloc: negative shape");
-  const int64_t need = backbone_workspace_bytes(tokens, in_features, rank, 1, false);
+  const int64_t need = backbone_workspace_bytes(tokens, in_features, rank, 1, true);
   TRIS_REQUIRE(need <= kNoAllocScratchBytes,
-               "tris_backbone_linear_noalloc: %d tokens x %d rank need %lld bytes of scratch, the static buffer "
-               "holds %lld (use tris_backbone_linear with a workspace)",
-               tokens, rank, static_cast<long long>(need), static_cast<long long>(kNoAllocScratchBytes));
+               "tris_backbone_linear_noalloc: %d tokens x %d in x %d rank need %lld bytes of scratch, the static "
+               "buffer holds %lld (use tris_backbone_linear with a workspace)",
+               tokens, in_features, rank, static_cast<long long>(need),
+               static_cast<long long>(kNoAllocScratchBytes));
   void* ws = nullptr;
   if (need > 0) {
     const int rc = scratch_address(&ws);
     if (rc) return rc;
   }
   return launch_backbone(x, tokens, in_features, row_index, sv, nullptr, rank, in_scale, nullptr, out, nullptr, ws,
-                         need, stream, "tris_backbone_linear_noalloc", false);
+                         need, stream, "tris_backbone_linear_noalloc", true);
 }
 
 extern "C" int tris_backbone_linear_pair(const uint16_t* x, int32_t tokens, int32_t in_features,

@@ -6,12 +6,20 @@
 // Here each token's top-k contributions (fp16 products down_out * w, as in the
 // reference) are gathered through the inverse route permutation, summed in
 // fp32 together with an optional unrouted shared-expert output, and rounded
-// once to bf16.  One thread produces 8 consecutive features; reads are
-// 16-byte vector loads.  The compensated variants first add a null-space
-// compensation term to each expert output row (fp16(out + comp), the
-// reference's out.add_(compensation), qlinear_cuda.py:2322-2334), so that the
-// term computed beside the grouped GEMM joins it without a launch of its own.
+// once to the output dtype (bf16, or fp16 for fp16 models).  One thread
+// produces 8 consecutive features; reads are 16-byte vector loads.  The
+// compensated variants first add a null-space compensation term to each
+// expert output row (fp16(out + comp), the reference's out.add_(compensation),
+// qlinear_cuda.py:2322-2334), so that the term computed beside the grouped GEMM
+// joins it without a launch of its own.  The gated variant joins a shared
+// expert through its sigmoid gate, as the Qwen blocks do
+// (modeling_qwen2_moe.py:815-818, modeling_qwen3_5_moe.py:186-188).
 #include "tris_common.h"
+
+// Every fp16 / bf16 rounding written here is one the reference performs (each torch op rounds its result), so
+// the compiler may not fuse a rounded product into the following add: without this, fp16(a + fp16(g * s))
+// compiles to one v_fma_f16 and the product's rounding is lost.
+#pragma clang fp contract(off)
 
 namespace tris {
 
@@ -25,16 +33,71 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
 // fp16(a + b) for fp16 bit patterns: the exact sum rounded once, as torch's fp16 add_.
 __device__ __forceinline__ uint16_t f16_add_bits(uint16_t a, uint16_t b) { return f2h_bits(h2f(a) + h2f(b)); }
 
+// Model-dtype (bf16 or fp16) bit patterns <-> float: exact widening, round-to-nearest-even narrowing.
+template <bool kBf16>
+__device__ __forceinline__ float dt_to_f32(uint16_t b) {
+  return kBf16 ? __uint_as_float(static_cast<uint32_t>(b) << 16) : h2f(b);
+}
+template <bool kBf16>
+__device__ __forceinline__ uint16_t f32_to_dt(float f) {
+  return kBf16 ? f32_to_bf16_rne(f) : f2h_bits(f);
+}
+template <bool kBf16>
+__device__ __forceinline__ float round_dt(float f) {
+  return dt_to_f32<kBf16>(f32_to_dt<kBf16>(f));
+}
+
+// The routed combine, one token per hblocks workgroups of 256 threads, 8 features per thread.  kBf16: the
+// output (and, when kGated, the gate's input and weight) are bf16, else fp16.  kGated: the shared expert
+// joins through its gate, as the Qwen blocks add it (modeling_qwen2_moe.py:815-818,
+// modeling_qwen3_5_moe.py:186-188):
+//   final  = dt(routed)                                   the routed sum in the output dtype
+//   gate   = dt(sigmoid(dt(gate_in[t] . gate_w)))         the one-output gate Linear, then sigmoid
+//   out    = dt(final + dt(gate * dt(shared)))            shared_expert(h).to(dt), gated, added
+// Every workgroup of a token reduces the gate's dot product itself (fixed order: per-thread fp32 sums of
+// exact products, the wavefront sum, then the four wavefronts in order), so no launch or grid-wide step is
+// added.  Without kGated, the shared output (if any) is added to the fp32 routed sum before the one rounding.
+template <bool kBf16, bool kGated>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __restrict__ expert_out,
                                                           const uint16_t* __restrict__ expert_comp,
                                                           const int32_t* __restrict__ inverse_perm,
                                                           const uint16_t* __restrict__ weights,
-                                                          const uint16_t* __restrict__ shared, int tokens, int top_k,
+                                                          const uint16_t* __restrict__ shared,
+                                                          const uint16_t* __restrict__ gate_in,
+                                                          const uint16_t* __restrict__ gate_w, int tokens, int top_k,
                                                           int hidden, int hblocks, uint16_t* __restrict__ out) {
   const int t = static_cast<int>(blockIdx.x) / hblocks;
   const int h0 = ((static_cast<int>(blockIdx.x) - t * hblocks) * static_cast<int>(blockDim.x) + threadIdx.x) * 8;
-  if (t >= tokens || h0 >= hidden) return;
   const bool vec = (hidden % 8) == 0;
+  float gate = 0.0f;
+  if constexpr (kGated) {
+    // every thread of the workgroup takes part in the reduction (the early exit comes after it)
+    __shared__ float wave_part[4];
+    const uint16_t* xr = gate_in + static_cast<int64_t>(t) * hidden;
+    float s = 0.0f;
+    for (int h = static_cast<int>(threadIdx.x) * 8; h < hidden; h += static_cast<int>(blockDim.x) * 8) {
+      uint16_t xv[8], wv[8];
+      if (vec) {
+        *reinterpret_cast<uint4*>(xv) = *reinterpret_cast<const uint4*>(xr + h);
+        *reinterpret_cast<uint4*>(wv) = *reinterpret_cast<const uint4*>(gate_w + h);
+      } else {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          xv[u] = (h + u < hidden) ? xr[h + u] : 0;
+          wv[u] = (h + u < hidden) ? gate_w[h + u] : 0;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += dt_to_f32<kBf16>(xv[u]) * dt_to_f32<kBf16>(wv[u]);  // exact products
+    }
+    s = wave_sum_f32(s);
+    if ((threadIdx.x & (kWave - 1)) == 0) wave_part[threadIdx.x / kWave] = s;
+    __syncthreads();
+    const float dot = ((wave_part[0] + wave_part[1]) + wave_part[2]) + wave_part[3];
+    const float logit = round_dt<kBf16>(dot);
+    gate = round_dt<kBf16>(1.0f / (1.0f + expf(-logit)));
+  }
+  if (t >= tokens || h0 >= hidden) return;
   float acc[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u) acc[u] = 0.0f;
@@ -65,17 +128,19 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
 #pragma unroll
     for (int u = 0; u < 8; ++u) acc[u] += __half2float(__hmul(__ushort_as_half(v[u]), w));
   }
-  if (shared != nullptr) {
-    const uint16_t* src = shared + static_cast<int64_t>(t) * hidden + h0;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if (h0 + u < hidden) acc[u] += h2f(src[u]);
-    }
-  }
   uint16_t* dst = out + static_cast<int64_t>(t) * hidden + h0;
+  const uint16_t* ssrc = shared != nullptr ? shared + static_cast<int64_t>(t) * hidden + h0 : nullptr;
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
-    if (h0 + u < hidden) dst[u] = f32_to_bf16_rne(acc[u]);
+    if (h0 + u >= hidden) continue;
+    float v = acc[u];
+    if constexpr (kGated) {
+      const float sh = round_dt<kBf16>(h2f(ssrc[u]));
+      v = round_dt<kBf16>(v) + round_dt<kBf16>(gate * sh);
+    } else {
+      if (ssrc != nullptr) v += h2f(ssrc[u]);
+    }
+    dst[u] = f32_to_dt<kBf16>(v);
   }
 }
 
@@ -167,35 +232,64 @@ extern "C" int tris_swiglu_mul_compensated(const uint16_t* gate, const uint16_t*
 }
 
 static int combine_launch(const char* who, const uint16_t* expert_out, const uint16_t* expert_comp,
-                          const int32_t* inverse_perm, const uint16_t* weights, const uint16_t* shared, int32_t tokens,
-                          int32_t top_k, int32_t hidden, uint16_t* out, void* stream) {
+                          const int32_t* inverse_perm, const uint16_t* weights, const uint16_t* shared,
+                          const uint16_t* gate_in, const uint16_t* gate_w, int32_t tokens, int32_t top_k,
+                          int32_t hidden, bool out_bf16, uint16_t* out, void* stream) {
   TRIS_REQUIRE(tokens >= 0 && top_k >= 0 && hidden >= 0, "%s: negative shape", who);
   if (tokens == 0 || hidden == 0) return TRIS_OK;
   TRIS_REQUIRE(out != nullptr && (top_k == 0 || (expert_out && inverse_perm && weights)), "%s: null pointer", who);
-  TRIS_REQUIRE(hidden % 8 != 0 || (reinterpret_cast<uintptr_t>(expert_out) % 16 == 0 &&
-                                   reinterpret_cast<uintptr_t>(expert_comp) % 16 == 0),
+  const auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  TRIS_REQUIRE(hidden % 8 != 0 || (a16(expert_out) && a16(expert_comp)),
                "%s: expert_out and expert_comp must be 16-byte aligned", who);
+  const bool gated = gate_w != nullptr;
+  TRIS_REQUIRE(!gated || (shared != nullptr && gate_in != nullptr),
+               "%s: a shared-expert gate needs the shared output and the gate input", who);
+  TRIS_REQUIRE(!gated || hidden % 8 != 0 || (a16(gate_in) && a16(gate_w)),
+               "%s: gate input and weight must be 16-byte aligned", who);
   const int threads = 256;
   const int hblocks = ceil_div(ceil_div(hidden, 8), threads);
   const int64_t blocks = static_cast<int64_t>(hblocks) * tokens;  // token-major, one dimension (no 65535 limit)
   TRIS_REQUIRE(blocks <= 2147483647LL, "%s: too many tokens (%d)", who, tokens);
-  hipLaunchKernelGGL(moe_combine_kernel, dim3(static_cast<unsigned>(blocks)), dim3(threads), 0,
-                     static_cast<hipStream_t>(stream), expert_out, expert_comp, inverse_perm, weights, shared, tokens,
-                     top_k, hidden, hblocks, out);
+  const dim3 grid(static_cast<unsigned>(blocks));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (out_bf16) {
+    if (gated)
+      hipLaunchKernelGGL((moe_combine_kernel<true, true>), grid, dim3(threads), 0, st, expert_out, expert_comp,
+                         inverse_perm, weights, shared, gate_in, gate_w, tokens, top_k, hidden, hblocks, out);
+    else
+      hipLaunchKernelGGL((moe_combine_kernel<true, false>), grid, dim3(threads), 0, st, expert_out, expert_comp,
+                         inverse_perm, weights, shared, gate_in, gate_w, tokens, top_k, hidden, hblocks, out);
+  } else {
+    if (gated)
+      hipLaunchKernelGGL((moe_combine_kernel<false, true>), grid, dim3(threads), 0, st, expert_out, expert_comp,
+                         inverse_perm, weights, shared, gate_in, gate_w, tokens, top_k, hidden, hblocks, out);
+    else
+      hipLaunchKernelGGL((moe_combine_kernel<false, false>), grid, dim3(threads), 0, st, expert_out, expert_comp,
+                         inverse_perm, weights, shared, gate_in, gate_w, tokens, top_k, hidden, hblocks, out);
+  }
   return check_launch(who);
 }
 
 extern "C" int tris_moe_combine(const uint16_t* expert_out, const int32_t* inverse_perm, const uint16_t* weights,
                                 const uint16_t* shared, int32_t tokens, int32_t top_k, int32_t hidden,
                                 uint16_t* out, void* stream) {
-  return combine_launch("tris_moe_combine", expert_out, nullptr, inverse_perm, weights, shared, tokens, top_k, hidden,
-                        out, stream);
+  return combine_launch("tris_moe_combine", expert_out, nullptr, inverse_perm, weights, shared, nullptr, nullptr,
+                        tokens, top_k, hidden, true, out, stream);
 }
 
 extern "C" int tris_moe_combine_compensated(const uint16_t* expert_out, const uint16_t* expert_comp,
                                             const int32_t* inverse_perm, const uint16_t* weights,
                                             const uint16_t* shared, int32_t tokens, int32_t top_k, int32_t hidden,
                                             uint16_t* out, void* stream) {
-  return combine_launch("tris_moe_combine_compensated", expert_out, expert_comp, inverse_perm, weights, shared, tokens,
-                        top_k, hidden, out, stream);
+  return combine_launch("tris_moe_combine_compensated", expert_out, expert_comp, inverse_perm, weights, shared,
+                        nullptr, nullptr, tokens, top_k, hidden, true, out, stream);
+}
+
+extern "C" int tris_moe_combine_gated(const uint16_t* expert_out, const uint16_t* expert_comp,
+                                      const int32_t* inverse_perm, const uint16_t* weights, const uint16_t* shared,
+                                      const uint16_t* shared_gate_input, const uint16_t* shared_gate_weight,
+                                      int32_t tokens, int32_t top_k, int32_t hidden, int32_t out_bf16,
+                                      uint16_t* out, void* stream) {
+  return combine_launch("tris_moe_combine_gated", expert_out, expert_comp, inverse_perm, weights, shared,
+                        shared_gate_input, shared_gate_weight, tokens, top_k, hidden, out_bf16 != 0, out, stream);
 }

@@ -302,7 +302,6 @@ def route_topk_grouped(router_logits: torch.Tensor, top_k: int, renormalize: boo
 
 
 ROUTE_BACKBONE_MAX_TOKENS = 64  # tokens of tris_route_topk_backbone
-_DEFERRED_WORKSPACES: dict = {}
 
 
 class BackbonePending:
@@ -354,12 +353,10 @@ def route_topk_backbone_pair(router_logits: torch.Tensor, top_k: int, renormaliz
     out_b = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
     lib = _lib.load()
     nbytes = int(lib.tris_backbone_pair_workspace_bytes(tokens, in_f, rank))
-    # a buffer of its own: the partial sums must survive until the predecode launch reduces them
-    key = (x.device.type, x.device.index)
-    ws = _DEFERRED_WORKSPACES.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=x.device)
-        _DEFERRED_WORKSPACES[key] = ws
+    # a buffer of this call's own, held by the BackbonePending until the launch that reduces the partial sums
+    # has been enqueued (on this stream, so the allocator reuses it only after that launch): pending calls on
+    # other streams, or a second call before the first is reduced, each keep their own partial sums
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=x.device)
     job = _lib.TrisBackbonePairJob(_ptr(x), tokens, in_f, _ptr(sv_a), _ptr(sv_b), rank, _ptr(in_scale_a),
                                    _ptr(in_scale_b), _ptr(out_a), _ptr(out_b), _ptr(ws), int(ws.numel()))
     _lib.check(lib.tris_route_topk_backbone(*_route_topk_args(logits, out, top_k, renormalize, m_tile),
@@ -800,18 +797,11 @@ def gr_decode_dense(q_gmap_gr_words, q_gmap_gr_offsets, q_gmap_gr_meta, expert_i
     return out
 
 
-_WORKSPACES: dict = {}
-
-
 def backbone_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per-device scratch for the backbone's split-K partial sums (no initial contents needed;
-    calls on one device share it, so they must not overlap on different streams)."""
-    key = (device.type, device.index)
-    ws = _WORKSPACES.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
-        _WORKSPACES[key] = ws
-    return ws
+    """Scratch for one backbone call's split-K partial sums (no initial contents needed), taken from the
+    caching allocator on the current stream: calls on different streams (the shared expert runs beside the
+    routed path) never share it, and its reuse is ordered after the call's reduction on that stream."""
+    return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
 
 
 # From this many rows on, and with more than BACKBONE_LIBRARY_MIN_ELEMS activation elements (rows x
@@ -857,8 +847,9 @@ def _backbone_library(x, svs, in_scales, row_index):
 
 
 def backbone_linear(x: torch.Tensor, sv: torch.Tensor, in_scale: torch.Tensor | None = None,
-                    row_index: torch.Tensor | None = None) -> torch.Tensor:
-    """hidden = fp16(x[row_index] * in_scale) @ sv^T with fp32 accumulation (compute_shared_hidden)."""
+                    row_index: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """hidden = fp16(x[row_index] * in_scale) @ sv^T with fp32 accumulation (compute_shared_hidden).  out: an
+    fp16 [rows, rank] buffer to write (e.g. one owned by another stream), else a new tensor."""
     _check_cuda("x", x, torch.float16, 2)
     _check_cuda("shared_sv", sv, torch.float16, 2, x.device)
     if sv.size(1) != x.size(1):
@@ -869,12 +860,19 @@ def backbone_linear(x: torch.Tensor, sv: torch.Tensor, in_scale: torch.Tensor | 
     if in_scale is not None:
         _check_cuda("in_scale", in_scale, torch.float16, 1, x.device)
     rank, in_f = int(sv.size(0)), int(sv.size(1))
+    if out is not None:
+        _check_cuda("out", out, torch.float16, 2, x.device)
+        if tuple(out.shape) != (tokens, rank):
+            raise RuntimeError("backbone_linear: out must be [rows, rank]")
     if _backbone_use_library(tokens, in_f, rank):
-        return _backbone_library(x, (sv,), (in_scale,), row_index)[0]
+        res = _backbone_library(x, (sv,), (in_scale,), row_index)[0]
+        return res if out is None else out.copy_(res)
     if row_index is not None and x.size(0) < tokens and _backbone_gemm_ok(int(x.size(0)), in_f, rank):
         # more routed rows than tokens: project each token once, then gather the projected rows
-        return backbone_linear(x, sv, in_scale=in_scale).index_select(0, row_index)
-    out = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
+        res = backbone_linear(x, sv, in_scale=in_scale).index_select(0, row_index)
+        return res if out is None else out.copy_(res)
+    if out is None:
+        out = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
     lib = _lib.load()
     ws = backbone_workspace(x.device, int(lib.tris_backbone_workspace_bytes(tokens, in_f, rank)))
     _lib.check(lib.tris_backbone_linear(_ptr(x), tokens, in_f, _ptr(row_index), _ptr(sv), rank, _ptr(in_scale),
@@ -936,7 +934,7 @@ def backbone_swiglu_ok(gate: torch.Tensor, sv, in_scale: torch.Tensor | None = N
 
 
 def backbone_swiglu_linear(gate: torch.Tensor, up: torch.Tensor, sv: torch.Tensor,
-                           in_scale: torch.Tensor | None = None) -> torch.Tensor:
+                           in_scale: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """fp16(act_fn(gate) * up [* in_scale]) @ sv^T in one projection with the product formed in its operand
     staging (tris_backbone_swiglu_linear, an extension): the down backbone of a SwiGLU layer without the
     intermediate tensor.  The product is swiglu_mul's, bit for bit."""
@@ -948,7 +946,12 @@ def backbone_swiglu_linear(gate: torch.Tensor, up: torch.Tensor, sv: torch.Tenso
     if in_scale is not None:
         _check_cuda("in_scale", in_scale, torch.float16, 1, gate.device)
     rows, in_f, rank = int(gate.size(0)), int(gate.size(1)), int(sv.size(0))
-    out = torch.empty((rows, rank), dtype=torch.float16, device=gate.device)
+    if out is None:
+        out = torch.empty((rows, rank), dtype=torch.float16, device=gate.device)
+    else:
+        _check_cuda("out", out, torch.float16, 2, gate.device)
+        if tuple(out.shape) != (rows, rank):
+            raise RuntimeError("backbone_swiglu_linear: out must be [rows, rank]")
     lib = _lib.load()
     ws = backbone_workspace(gate.device, int(lib.tris_backbone_swiglu_workspace_bytes(rows, in_f, rank)))
     _lib.check(lib.tris_backbone_swiglu_linear(_ptr(gate), _ptr(up), rows, in_f, _ptr(sv), rank, _ptr(in_scale),
@@ -1138,19 +1141,11 @@ def ns_compensation_apply_(out: torch.Tensor, x_grouped: torch.Tensor, expert_id
     return out
 
 
-_NS_WORKSPACES: dict = {}
-
-
 def ns_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per-device scratch for the null-space compensation's split-K partial sums, apart from the backbone's
-    (the layer runs the down projection's compensation on a second stream beside the backbone).  Calls on
-    one device share it, so they must not overlap on different streams."""
-    key = (device.type, device.index)
-    ws = _NS_WORKSPACES.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
-        _NS_WORKSPACES[key] = ws
-    return ws
+    """Scratch for one null-space compensation call's split-K partial sums, from the caching allocator on the
+    current stream (the layer runs compensation terms on side streams beside the backbones), so concurrent
+    calls never share it."""
+    return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
 
 
 def _aligned16(x: torch.Tensor) -> torch.Tensor:
@@ -1444,12 +1439,22 @@ def compact3_qkv_linear_forward(input, q_qweight1, q_qweight2_sparse, q_qweight2
 
 
 def moe_combine(expert_out: torch.Tensor, inverse_perm: torch.Tensor, weights: torch.Tensor,
-                shared: torch.Tensor | None = None, expert_comp: torch.Tensor | None = None) -> torch.Tensor:
-    """bf16 [T, H] = sum_s fp16(expert_out[inverse_perm[t, s]] * weights[t, s]) (+ shared), fp32-accumulated.
-    With expert_comp (fp16, the shape of expert_out), each expert row is fp16(expert_out + expert_comp) first:
-    the down projection's null-space compensation (qlinear_cuda.py:2322-2334) folded into the combine."""
+                shared: torch.Tensor | None = None, expert_comp: torch.Tensor | None = None,
+                shared_gate_input: torch.Tensor | None = None, shared_gate_weight: torch.Tensor | None = None,
+                out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """out_dtype [T, H] = sum_s fp16(expert_out[inverse_perm[t, s]] * weights[t, s]) (+ shared), fp32-accumulated
+    and rounded once (out_dtype bf16 or fp16).  With expert_comp (fp16, the shape of expert_out), each expert row
+    is fp16(expert_out + expert_comp) first: the down projection's null-space compensation
+    (qlinear_cuda.py:2322-2334) folded into the combine.
+
+    With shared_gate_weight ([H] or [1, H], the one-output gate Linear of the Qwen blocks) the shared expert is
+    gated as modeling_qwen2_moe.py:815-818 / modeling_qwen3_5_moe.py:186-188 do it, every step in out_dtype:
+    out = dt(dt(routed) + dt(dt(sigmoid(dt(shared_gate_input . w))) * dt(shared))).  shared_gate_input [T, H]
+    and the weight are in out_dtype (the block's model dtype)."""
     _check_cuda("expert_out", expert_out, torch.float16, 2)
     dev = expert_out.device
+    if out_dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError("moe_combine: out_dtype must be bfloat16 or float16")
     if expert_comp is not None:
         _check_cuda("expert_comp", expert_comp, torch.float16, 2, dev)
         if expert_comp.shape != expert_out.shape:
@@ -1464,15 +1469,34 @@ def moe_combine(expert_out: torch.Tensor, inverse_perm: torch.Tensor, weights: t
         _check_cuda("shared", shared, torch.float16, 2, dev)
         if tuple(shared.shape) != (tokens, hidden):
             raise RuntimeError("shared must be [tokens, hidden]")
-    out = torch.empty((tokens, hidden), dtype=torch.bfloat16, device=dev)
-    if expert_comp is None:
-        _lib.check(_lib.load().tris_moe_combine(_ptr(expert_out), _ptr(inverse_perm), _ptr(weights), _ptr(shared),
-                                                tokens, top_k, hidden, _ptr(out), _stream(expert_out)),
-                   "tris_moe_combine")
-    else:
-        _lib.check(_lib.load().tris_moe_combine_compensated(
-            _ptr(expert_out), _ptr(expert_comp), _ptr(inverse_perm), _ptr(weights), _ptr(shared), tokens, top_k,
-            hidden, _ptr(out), _stream(expert_out)), "tris_moe_combine_compensated")
+    if shared_gate_weight is not None:
+        if shared is None or shared_gate_input is None:
+            raise RuntimeError("a shared-expert gate needs the shared output and the gate input")
+        _check_cuda("shared_gate_input", shared_gate_input, out_dtype, 2, dev)
+        if tuple(shared_gate_input.shape) != (tokens, hidden):
+            raise RuntimeError("shared_gate_input must be [tokens, hidden]")
+        if shared_gate_weight.numel() != hidden:
+            raise RuntimeError("shared_gate_weight must hold hidden values (Linear(hidden, 1))")
+        shared_gate_weight = shared_gate_weight.reshape(hidden)
+        _check_cuda("shared_gate_weight", shared_gate_weight, out_dtype, 1, dev)
+        if hidden % 8 == 0:
+            shared_gate_input = _aligned16(shared_gate_input)
+            shared_gate_weight = _aligned16(shared_gate_weight)
+    out = torch.empty((tokens, hidden), dtype=out_dtype, device=dev)
+    if shared_gate_weight is None and out_dtype == torch.bfloat16:
+        if expert_comp is None:
+            _lib.check(_lib.load().tris_moe_combine(_ptr(expert_out), _ptr(inverse_perm), _ptr(weights), _ptr(shared),
+                                                    tokens, top_k, hidden, _ptr(out), _stream(expert_out)),
+                       "tris_moe_combine")
+        else:
+            _lib.check(_lib.load().tris_moe_combine_compensated(
+                _ptr(expert_out), _ptr(expert_comp), _ptr(inverse_perm), _ptr(weights), _ptr(shared), tokens, top_k,
+                hidden, _ptr(out), _stream(expert_out)), "tris_moe_combine_compensated")
+        return out
+    _lib.check(_lib.load().tris_moe_combine_gated(
+        _ptr(expert_out), _ptr(expert_comp), _ptr(inverse_perm), _ptr(weights), _ptr(shared), _ptr(shared_gate_input),
+        _ptr(shared_gate_weight), tokens, top_k, hidden, int(out_dtype == torch.bfloat16), _ptr(out),
+        _stream(expert_out)), "tris_moe_combine_gated")
     return out
 
 

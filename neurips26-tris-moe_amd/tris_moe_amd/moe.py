@@ -7,7 +7,9 @@ optional renormalisation (Mixtral/Qwen always, OLMoE when ``norm_topk_prob``,
 (``:83-90``) -> grouped route -> shared backbones -> grouped gate/up pair ->
 SiLU * up -> down backbone -> grouped down -> routing-weighted scatter-add in
 the output dtype.  An optional always-on fp16 shared expert (A3B-class
-layers) is added unrouted.
+layers) runs on a stream of its own beside the routed path and joins in the
+combine, through its sigmoid gate when the layer has one, as the Qwen blocks
+add it (``modeling_qwen2_moe.py:815-818``, ``modeling_qwen3_5_moe.py:186-188``).
 
 ``grouped_moe_forward`` is the same computation with every size fixed by the
 input shape (route metadata padded to num_experts segments, launch bounds
@@ -35,7 +37,8 @@ def route_topk(router_logits: torch.Tensor, top_k: int, renormalize: bool):
 
 def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, selected_experts: torch.Tensor,
                         payloads: dict, backbones: dict, num_experts: int, output_dtype=torch.bfloat16,
-                        shared_expert=None, expert_path: str = "auto") -> torch.Tensor:
+                        shared_expert=None, expert_path: str = "auto", x_model: torch.Tensor | None = None
+                        ) -> torch.Tensor:
     """The grouped MoE layer on the HIP kernels with no host synchronisation.
 
     x16 fp16 [T, H]; routing_weights [T, k] (cast to fp16 as in modeling_mixtral.py:555);
@@ -47,6 +50,11 @@ def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, select
     matrix-mode null-space payloads under gate_ns / up_ns / down_ns (``qlinear.build_grouped_ns_payload``
     format on the device).  Returns [T, H] in output_dtype.
 
+    shared_expert: None, (w_gate [Is, H], w_up [Is, H], w_down [H, Is]) fp16 added ungated, or those plus the
+    shared-expert gate's weight ([1, H] or [H], the model dtype) as a fourth element: the Qwen blocks' gated
+    shared expert.  x_model: the block's input in the model dtype (the gate's input, as h in
+    modeling_qwen2_moe.py:817); x16 in the gate weight's dtype when None.
+
     expert_path: "predecoded" decodes the split bitmaps once per projection and runs the MFMA
     grouped GEMMs (needs uniform 64-column groups and no output scale or bias); "fused" decodes
     inside the grouped GEMMs (the in-kernel-decode MFMA kernels when every payload suits them,
@@ -55,16 +63,17 @@ def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, select
     k = int(selected_experts.size(1))
     if T * k == 0:
         return torch.zeros((T, H), dtype=output_dtype, device=x16.device)
+    shared = _shared_expert_begin(x16, shared_expert, x_model, output_dtype)
     route = ext.build_grouped_route_device(selected_experts, num_experts, GROUPED_SEGMENT_M_TILE)
     w16 = routing_weights.to(torch.float16).contiguous()
-    return _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, output_dtype, shared_expert,
+    return _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, output_dtype, shared,
                                expert_path)
 
 
 def grouped_moe_forward_from_logits(x16: torch.Tensor, router_logits: torch.Tensor, top_k: int, renormalize: bool,
                                     payloads: dict, backbones: dict, num_experts: int,
                                     output_dtype=torch.bfloat16, shared_expert=None,
-                                    expert_path: str = "auto") -> torch.Tensor:
+                                    expert_path: str = "auto", x_model: torch.Tensor | None = None) -> torch.Tensor:
     """The layer from router logits: softmax / top-k / renormalisation / route in one kernel when the
     batch is decode-sized (tris_route_topk_grouped), else the token-parallel tris_route_topk (torch's
     route_topk for logits it does not take) + the two-kernel route.  On the
@@ -72,10 +81,11 @@ def grouped_moe_forward_from_logits(x16: torch.Tensor, router_logits: torch.Tens
     gate/up backbones of the tokens run in the router's launch (tris_route_topk_backbone), their split-K
     reduction in the predecode's, and the grouped GEMMs gather their rows through the route's token
     indices (the backbone values equal those of the gathered rows up to the split-K summation order: the
-    slice count follows the row count)."""
+    slice count follows the row count).  shared_expert and x_model: as grouped_moe_forward."""
     T, H = int(x16.size(0)), int(x16.size(1))
     if T * top_k == 0:
         return torch.zeros((T, H), dtype=output_dtype, device=x16.device)
+    shared = _shared_expert_begin(x16, shared_expert, x_model, output_dtype)
     if (router_logits.dtype == torch.float32 and T * top_k <= ext.ROUTE_TOPK_MAX_ROWS
             and num_experts <= ext.ROUTE_TOPK_MAX_EXPERTS and top_k <= ext.ROUTE_TOPK_MAX_K):
         sc = _in_scales(backbones)
@@ -86,18 +96,20 @@ def grouped_moe_forward_from_logits(x16: torch.Tensor, router_logits: torch.Tens
                                                           x16, backbones["gate"], backbones["up"],
                                                           in_scale_a=sc["gate"], in_scale_b=sc["up"])
             return _forward_with_route(x16, route["routing_weights_f16"], route, top_k, payloads, backbones,
-                                       num_experts, output_dtype, shared_expert, expert_path,
+                                       num_experts, output_dtype, shared, expert_path,
                                        backbone_pending=pending)
         route = ext.route_topk_grouped(router_logits, top_k, renormalize, GROUPED_SEGMENT_M_TILE)
         return _forward_with_route(x16, route["routing_weights_f16"], route, top_k, payloads, backbones,
-                                   num_experts, output_dtype, shared_expert, expert_path)
+                                   num_experts, output_dtype, shared, expert_path)
     if ext.route_topk_ok(router_logits, top_k):
         # past the one-launch router: the token-parallel softmax / top-k, then the two-kernel route
         _, selected, weights = ext.route_topk(router_logits, top_k, renormalize)
     else:
         weights, selected = route_topk(router_logits, top_k, renormalize)
-    return grouped_moe_forward(x16, weights, selected, payloads, backbones, num_experts, output_dtype,
-                               shared_expert, expert_path)
+    route = ext.build_grouped_route_device(selected, num_experts, GROUPED_SEGMENT_M_TILE)
+    w16 = weights.to(torch.float16).contiguous()
+    return _forward_with_route(x16, w16, route, top_k, payloads, backbones, num_experts, output_dtype, shared,
+                               expert_path)
 
 
 def _sparse(p: dict) -> bool:
@@ -197,16 +209,72 @@ def _ns_payloads(payloads: dict) -> dict:
     return out
 
 
-def _combine(x16, d_out, route, w16, output_dtype, shared_expert, d_comp=None):
-    shared = None
-    if shared_expert is not None:
-        # the always-on fp16 expert down(act_fn(gate x) * up x): gate and up in one backbone launch, SiLU and
-        # the product in fp16 as F.silu(g) * u, then the down projection
-        wg, wu, wd = shared_expert
+class _SharedPending:
+    """The shared expert's fp16 output [T, H], computed on a side stream beside the routed path (the buffer
+    belongs to the caller's stream, which waits for the side stream before the combine reads it), and its gate
+    (the weight and its input, both in the combine's dtype) or None."""
+
+    __slots__ = ("out", "stream", "gate_weight", "gate_input")
+
+    def __init__(self, out, stream, gate_weight, gate_input):
+        self.out, self.stream, self.gate_weight, self.gate_input = out, stream, gate_weight, gate_input
+
+
+def _combine_dtype(output_dtype) -> torch.dtype:
+    """The dtype the combine writes: the output dtype when bf16 or fp16, else bf16 (then cast)."""
+    return output_dtype if output_dtype in (torch.bfloat16, torch.float16) else torch.bfloat16
+
+
+def _shared_expert_begin(x16, shared_expert, x_model=None, output_dtype=None):
+    """Start the always-on shared expert down(act_fn(gate x) * up x) on side stream 2: gate and up in one
+    backbone launch, then the down projection with act_fn(g) * u formed in its operand staging (or SiLU and
+    the product in fp16 as F.silu(g) * u, then the down projection), the reference's fp16 MLP.  Returns a
+    _SharedPending or None."""
+    if shared_expert is None:
+        return None
+    if isinstance(shared_expert, _SharedPending):
+        return shared_expert
+    if len(shared_expert) not in (3, 4):
+        raise RuntimeError("shared_expert must be (w_gate, w_up, w_down) or (w_gate, w_up, w_down, gate_weight)")
+    wg, wu, wd = shared_expert[:3]
+    gate_w = shared_expert[3] if len(shared_expert) == 4 else None
+    T, H = int(x16.size(0)), int(x16.size(1))
+    dev = x16.device
+    gate_in = None
+    if gate_w is not None:
+        cd = gate_w.dtype if gate_w.dtype in (torch.bfloat16, torch.float16) else torch.bfloat16
+        if output_dtype is not None:
+            cd = _combine_dtype(output_dtype)
+        gate_w = gate_w.reshape(-1).to(cd).contiguous()
+        src = x_model if x_model is not None else x16
+        gate_in = src.to(cd).contiguous()
+    main = torch.cuda.current_stream(dev)
+    out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    side = _side_stream(dev, 2)
+    side.wait_stream(main)
+    with torch.cuda.stream(side):
         g, u = ext.backbone_linear_pair(x16, wg, wu)
-        shared = ext.backbone_linear(ext.swiglu_mul(g, u), wd)
-    out = ext.moe_combine(d_out, route["inverse_perm"], w16, shared, expert_comp=d_comp)
-    return out if output_dtype == torch.bfloat16 else out.to(output_dtype)
+        if ext.backbone_swiglu_ok(g, wd):
+            ext.backbone_swiglu_linear(g, u, wd, out=out)
+        else:
+            ext.backbone_linear(ext.swiglu_mul(g, u), wd, out=out)
+    return _SharedPending(out, side, gate_w, gate_in)
+
+
+def _combine(x16, d_out, route, w16, output_dtype, shared, d_comp=None):
+    """The routed combine in the output dtype, with the shared expert's output (a _SharedPending, or shared
+    weights run here) joined ungated or through its gate."""
+    shared = _shared_expert_begin(x16, shared, output_dtype=output_dtype)
+    cd = _combine_dtype(output_dtype)
+    kw = {}
+    if shared is not None:
+        torch.cuda.current_stream(x16.device).wait_stream(shared.stream)
+        kw["shared"] = shared.out
+        if shared.gate_weight is not None:
+            kw["shared_gate_weight"] = shared.gate_weight.to(cd)
+            kw["shared_gate_input"] = shared.gate_input.to(cd)
+    out = ext.moe_combine(d_out, route["inverse_perm"], w16, expert_comp=d_comp, out_dtype=cd, **kw)
+    return out if output_dtype == cd else out.to(output_dtype)
 
 
 def _predecode_buffer(p, slots, device):
@@ -220,7 +288,7 @@ _SIDE_STREAMS: dict = {}
 
 def _side_stream(device: torch.device, which: int = 0) -> torch.cuda.Stream:
     """Extra streams per device (default priority) for work that overlaps the main chain: 0 for the
-    bitmap decodes and the down compensation, 1 for the gate/up compensation."""
+    bitmap decodes and the down compensation, 1 for the gate/up compensation, 2 for the shared expert."""
     key = (device.index if device.index is not None else torch.cuda.current_device(), which)
     if key not in _SIDE_STREAMS:
         _SIDE_STREAMS[key] = torch.cuda.Stream(device=device)
@@ -390,13 +458,19 @@ def _decode_fused_moe_forward(x16, w16, route, payloads, backbones, num_experts,
 
 
 class TrisSparseMoeBlock(nn.Module):
-    """Grouped-expert sparse MoE block (MixtralSparseMoeBlock / OlmoeSparseMoeBlock shape).  The router
-    ``gate`` is an nn.Linear in the model dtype (``router_dtype``, bf16 by default), as the reference's
-    block keeps it; its logits go through an fp32 softmax (modeling_mixtral.py:546-549)."""
+    """Grouped-expert sparse MoE block (MixtralSparseMoeBlock / OlmoeSparseMoeBlock / Qwen2MoeSparseMoeBlock
+    shape).  The router ``gate`` is an nn.Linear in the model dtype (``router_dtype``, bf16 by default), as the
+    reference's block keeps it; its logits go through an fp32 softmax (modeling_mixtral.py:546-549).
+
+    shared_expert: None or (w_gate [Is, H], w_up [Is, H], w_down [H, Is]) fp16, the always-on shared expert of
+    the Qwen-style blocks.  shared_expert_gate: its gate's weight ([1, H] or [H]); the block then holds
+    ``shared_expert_gate = nn.Linear(H, 1, bias=False)`` in the model dtype and adds
+    sigmoid(shared_expert_gate(h)) * shared_expert(h) in the output dtype, as modeling_qwen2_moe.py:815-818
+    and modeling_qwen3_5_moe.py:186-188 do.  Without it the shared expert is added ungated."""
 
     def __init__(self, hidden_size: int, num_experts: int, top_k: int, payloads: dict, backbones: dict,
                  router_weight: torch.Tensor | None = None, renormalize: bool = True, shared_expert=None,
-                 router_dtype: torch.dtype = torch.bfloat16):
+                 router_dtype: torch.dtype = torch.bfloat16, shared_expert_gate: torch.Tensor | None = None):
         super().__init__()
         self.hidden_dim = hidden_size
         self.num_experts = num_experts
@@ -407,7 +481,20 @@ class TrisSparseMoeBlock(nn.Module):
             self.gate.weight.data = router_weight.to(router_dtype)
         self.payloads = payloads
         self.backbones = backbones
-        self.shared_expert = shared_expert
+        self.expert_path = "auto"  # grouped_moe_forward's expert_path
+        self.shared_expert = tuple(shared_expert) if shared_expert is not None else None
+        self.shared_expert_gate = None
+        if shared_expert_gate is not None:
+            if self.shared_expert is None:
+                raise ValueError("shared_expert_gate needs a shared_expert")
+            self.shared_expert_gate = nn.Linear(hidden_size, 1, bias=False, dtype=router_dtype,
+                                                device=shared_expert_gate.device)
+            self.shared_expert_gate.weight.data = shared_expert_gate.reshape(1, hidden_size).to(router_dtype)
+
+    def _shared(self, model_dtype: torch.dtype):
+        if self.shared_expert is None or self.shared_expert_gate is None:
+            return self.shared_expert
+        return (*self.shared_expert, self.shared_expert_gate.weight.detach().to(model_dtype))
 
     def forward_routed(self, hidden_states: torch.Tensor, router_logits: torch.Tensor) -> torch.Tensor:
         """The block after the router: [T, H] activations and [T, E] logits -> [T, H]."""
@@ -417,7 +504,8 @@ class TrisSparseMoeBlock(nn.Module):
             raise RuntimeError("grouped expert kernels require CUDA float16/bfloat16 hidden states")
         return grouped_moe_forward_from_logits(x16.contiguous(), router_logits.float().contiguous(), self.top_k,
                                                self.renormalize, self.payloads, self.backbones, self.num_experts,
-                                               output_dtype, self.shared_expert)
+                                               output_dtype, self._shared(output_dtype),
+                                               expert_path=self.expert_path, x_model=hidden_states.contiguous())
 
     def forward(self, hidden_states: torch.Tensor):
         """modeling_mixtral.py:539-608: hidden_states [B, S, H] (bf16 or fp16) -> (out [B, S, H] in the input

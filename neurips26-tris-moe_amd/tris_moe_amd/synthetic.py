@@ -182,6 +182,9 @@ def make_layer(spec: MoELayerSpec, seed: int, encode, keep_dense_gmap: bool = Fa
         layer["shared_expert"] = tuple(
             (rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)).astype(np.float16)
             for shape in ((Is, H), (Is, H), (H, Is)))
+        # the shared expert's gate, Linear(H, 1, bias=False) in the model dtype (bf16 values as float32), as the
+        # Qwen blocks hold it (modeling_qwen2_moe.py:270, modeling_qwen3_5_moe.py:57)
+        layer["shared_expert_gate"] = bf16_round(rng.standard_normal(H, dtype=np.float32) * np.float32(0.02))
     return layer
 
 

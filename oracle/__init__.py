@@ -492,9 +492,43 @@ def dequant_experts(payloads: dict, experts, workers: int = 1) -> dict:
     return caches
 
 
+def round_dtype(x, dtype: str) -> np.ndarray:
+    """fp32 values rounded (RNE) to "bf16" or "fp16" and widened back to fp32."""
+    if dtype == "bf16":
+        return bf16_round(x)
+    if dtype == "fp16":
+        return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+    raise ValueError(f"unknown dtype {dtype!r}")
+
+
+def shared_expert_mlp(x_f16, shared_expert) -> np.ndarray:
+    """The always-on shared expert, an fp16 SwiGLU MLP down(act_fn(gate(x)) * up(x)) (HF Qwen2MoeMLP as the
+    Qwen blocks call it, modeling_qwen2_moe.py:117-123, 816; modeling_qwen3_5_moe.py:186): each F.linear an
+    fp16 rounding of the exact sum, act_fn(g) * u in fp16 as the routed experts' (modeling_mixtral.py:496).
+    shared_expert = (w_gate [Is, H], w_up [Is, H], w_down [H, Is]) fp16.  Returns fp16 [T, H]."""
+    wg, wu, wd = shared_expert[:3]
+    x = np.asarray(x_f16, dtype=np.float16)
+    sg = linear_f16(x, wg)
+    su = linear_f16(x, wu)
+    smlp = (silu_f16(sg).astype(np.float32) * su.astype(np.float32)).astype(np.float16)
+    return linear_f16(smlp, wd)
+
+
+def shared_expert_gate(x_model, gate_weight, dtype: str) -> np.ndarray:
+    """sigmoid(shared_expert_gate(h)).to(dtype) (modeling_qwen2_moe.py:817, modeling_qwen3_5_moe.py:187): the
+    one-output Linear in the model dtype (the exact sum rounded once), then the sigmoid in fp32 rounded to the
+    dtype, as torch evaluates both for bf16/fp16 tensors.  x_model [T, H] and gate_weight [H] (or [1, H]) hold
+    model-dtype values.  Returns fp32 [T, 1]."""
+    xm = np.asarray(x_model, dtype=np.float32).astype(np.float64)
+    w = np.asarray(gate_weight, dtype=np.float32).reshape(-1).astype(np.float64)
+    logit = round_dtype((xm @ w).astype(np.float32), dtype)
+    return round_dtype(np.float32(1.0) / (np.float32(1.0) + np.exp(-logit)), dtype)[:, None]
+
+
 def moe_layer(x_f16, routing_weights, selected_experts, payloads: dict, backbones: dict, num_experts: int,
               shared_expert=None, weight_caches: dict | None = None, ns_payloads: dict | None = None,
-              input_scales: dict | None = None) -> np.ndarray:
+              input_scales: dict | None = None, shared_gate=None, x_model=None,
+              out_dtype: str = "bf16") -> np.ndarray:
     """Grouped MoE block (modeling_mixtral.py:406-537) with fp16 tensors between
     stages and fp32 accumulation inside every product; returns fp32 [T, H]
     (the caller rounds to the output dtype).
@@ -502,7 +536,14 @@ def moe_layer(x_f16, routing_weights, selected_experts, payloads: dict, backbone
     payloads: {"gate","up","down"} stacked grouped payloads; backbones: the
     matching fp16 shared matrices SV [rank, in].  routing_weights are cast to
     fp16 as the reference does (modeling_mixtral.py:555).  shared_expert, if
-    given, is (w_gate [I,H], w_up [I,H], w_down [H,I]) fp16 added unrouted.
+    given, is (w_gate [I,H], w_up [I,H], w_down [H,I]) fp16 (shared_expert_mlp).
+    Without shared_gate it is added unrouted to the fp32 sum.  With shared_gate
+    (the weight [H] of the Qwen blocks' shared_expert_gate, model-dtype values) it
+    joins as modeling_qwen2_moe.py:815-818 / modeling_qwen3_5_moe.py:186-188 add
+    it, every tensor in out_dtype ("bf16" or "fp16", the block's model dtype):
+        final + sigmoid(shared_expert_gate(h)).to(dt) * shared_expert(h).to(dt)
+    with final the routed sum rounded to dt and the product rounded to dt (the
+    caller's rounding is the sum's); h = x_model (default: x_f16's values).
     input_scales: {gate, up, down} -> fp16 [in] or absent: the ns_mode == 1 input
     scale of experts[0]'s projection, an fp16 product with the backbone input
     before F.linear (qlinear_cuda.py:4477-4480, modeling_mixtral.py:469-470, 497).
@@ -541,11 +582,13 @@ def moe_layer(x_f16, routing_weights, selected_experts, payloads: dict, backbone
     np.add.at(out, gti, contrib.astype(np.float32))
     del x_g
     if shared_expert is not None:
-        wg, wu, wd = shared_expert
-        sg = linear_f16(x, wg)
-        su = linear_f16(x, wu)
-        smlp = (silu_f16(sg).astype(np.float32) * su.astype(np.float32)).astype(np.float16)
-        out = out + linear_f16(smlp, wd).astype(np.float32)
+        shared = shared_expert_mlp(x, shared_expert).astype(np.float32)
+        if shared_gate is None:
+            out = out + shared
+        else:
+            h = x.astype(np.float32) if x_model is None else np.asarray(x_model, dtype=np.float32)
+            g = shared_expert_gate(h, shared_gate, out_dtype)
+            out = round_dtype(out, out_dtype) + round_dtype(g * round_dtype(shared, out_dtype), out_dtype)
     return out
 
 

@@ -471,6 +471,44 @@ def test_route_device_bad_ids_stay_in_bounds(tris, oracle_mod, cuda, t, k, e):
     np.testing.assert_allclose(out, oracle_mod.bf16_round(want), rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("hidden", [100, 2048, 4096])
+def test_combine_gated_shared_expert(tris, oracle_mod, cuda, dtype, hidden):
+    """tris_moe_combine_gated against the oracle's gated join (oracle.shared_expert_gate, round_dtype): the
+    routed sum in the output dtype plus dt(gate * dt(shared)), the gate's dot product reduced inside each
+    workgroup (hidden 4096: two workgroups per token), a ragged hidden size (scalar loads), both dtypes; and
+    without the gate, the ungated sum rounded once to the dtype."""
+    note(f"combine gated {dtype} hidden={hidden}")
+    rng = np.random.default_rng(hidden + (1 if dtype == "bf16" else 2))
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    t, k = 5, 3
+    eo = rng.standard_normal((t * k, hidden)).astype(np.float16)
+    inv = rng.permutation(t * k).astype(np.int32)
+    wts = rng.uniform(0.1, 1.0, (t, k)).astype(np.float16)
+    sh = rng.standard_normal((t, hidden)).astype(np.float16)
+    x = torch.from_numpy(rng.standard_normal((t, hidden)).astype(np.float32)).to(tdt)
+    wg = torch.from_numpy((rng.standard_normal(hidden) * (1.0 / math.sqrt(hidden))).astype(np.float32)).to(tdt)
+    dev = lambda a: torch.from_numpy(a).to(cuda)
+    got = tris["ext"].moe_combine(dev(eo), dev(inv), dev(wts), dev(sh), shared_gate_input=x.to(cuda),
+                                  shared_gate_weight=wg.to(cuda), out_dtype=tdt)
+    assert got.dtype == tdt
+    routed = np.zeros((t, hidden), np.float32)
+    for i in range(t * k):
+        routed[i // k] += (eo[inv[i]].astype(np.float32) * np.float32(wts[i // k, i % k])).astype(
+            np.float16).astype(np.float32)
+    gate = oracle_mod.shared_expert_gate(x.float().numpy(), wg.float().numpy(), dtype)
+    assert 0.01 < gate.min() and gate.max() < 0.99  # the data keep the gate away from 0 and 1
+    rd = lambda v: oracle_mod.round_dtype(v, dtype)
+    want = rd(rd(routed) + rd(gate * rd(sh.astype(np.float32))))
+    out = got.float().cpu().numpy()
+    assert_close(out, want, f"gated combine {dtype} {hidden}")
+    # the gate's fp32 sum runs in another order than the oracle's float64 one: a rounding of the logit may
+    # differ near a tie, and then a whole token moves by an ulp; every other value is bit-exact
+    assert (out == want).mean() > 0.99
+    plain = tris["ext"].moe_combine(dev(eo), dev(inv), dev(wts), dev(sh), out_dtype=tdt).float().cpu().numpy()
+    np.testing.assert_array_equal(plain, rd(routed + sh.astype(np.float32)))
+
+
 # ----------------------------------------------------------- grouped GEMM
 def oracle_grouped(oracle_mod, payload, hidden, expert_ids, seg, uniform):
     return oracle_mod.grouped_forward(payload, hidden, expert_ids, seg, uniform)
@@ -780,11 +818,13 @@ def _run_layer(tris, oracle_mod, cuda, spec, tokens, seed, expert_path="auto", s
     layer = syn.make_layer(spec, seed, tris["ext"].gr_encode)
     payloads = {p: ql.payload_to_device(layer[p], cuda) for p in ("gate", "up", "down")}
     backbones = {p: torch.from_numpy(layer["backbones"][p]).to(cuda) for p in ("gate", "up", "down")}
-    shared = None
+    shared = gate_w = None
     if "shared_expert" in layer:
         shared = tuple(torch.from_numpy(w).to(cuda) for w in layer["shared_expert"])
+        gate_w = torch.from_numpy(layer["shared_expert_gate"]).to(cuda).to(torch.bfloat16)
     block = tris["moe"].TrisSparseMoeBlock(spec.hidden, spec.num_experts, spec.top_k, payloads, backbones,
-                                           renormalize=spec.renormalize, shared_expert=shared)
+                                           renormalize=spec.renormalize, shared_expert=shared,
+                                           shared_expert_gate=gate_w)
     caches = {"gate": {}, "up": {}, "down": {}}
     outs, wants = [], []
     for i in range(steps):
@@ -795,12 +835,15 @@ def _run_layer(tris, oracle_mod, cuda, spec, tokens, seed, expert_path="auto", s
             out = block.forward_routed(x, logits).float().cpu().numpy()
         else:
             wt, st = tris["moe"].route_topk(logits, spec.top_k, spec.renormalize)
+            sh = (*shared, gate_w) if shared is not None else None
             out = tris["moe"].grouped_moe_forward(x.to(torch.float16), wt, st, payloads, backbones, spec.num_experts,
-                                                  torch.bfloat16, shared, expert_path=expert_path).float().cpu().numpy()
+                                                  torch.bfloat16, sh, expert_path=expert_path,
+                                                  x_model=x).float().cpu().numpy()
         w, sel = oracle_mod.route_topk(inp["router_logits"], spec.top_k, spec.renormalize)
         want = oracle_mod.moe_layer(inp["x"].astype(np.float16), w, sel, {p: layer[p] for p in ("gate", "up", "down")},
                                     layer["backbones"], spec.num_experts, layer.get("shared_expert"),
-                                    weight_caches=caches)
+                                    weight_caches=caches, shared_gate=layer.get("shared_expert_gate"),
+                                    x_model=inp["x"], out_dtype="bf16")
         outs.append(out)
         wants.append(oracle_mod.bf16_round(want))
     return np.concatenate(outs), np.concatenate(wants)
@@ -838,8 +881,9 @@ def test_layer_mixtral_prefill_shape(tris, oracle_mod, cuda, tokens):
 
 @pytest.mark.parametrize("tokens", [1, 32, 1024])
 def test_layer_a3b_c3_with_shared_expert(tris, oracle_mod, cuda, tokens):
-    """C3: 256 experts, top-8, an always-on fp16 shared expert, N(0, 1.5) router
-    logits, at its three batches (1024 tokens: 8192 routed rows over nearly every expert)."""
+    """C3: 256 experts, top-8, an always-on fp16 shared expert joined through its
+    sigmoid gate (modeling_qwen2_moe.py:815-818), N(0, 1.5) router logits, at its three batches (1024 tokens:
+    8192 routed rows over nearly every expert)."""
     from tris_moe_amd.configs import C3_A3B
 
     note(f"layer C3 A3B T={tokens}")

@@ -286,6 +286,212 @@ def test_oracle_layer_against_float64(oracle_mod, tris):
     assert np.linalg.norm(err) / np.linalg.norm(ref) < 1e-3
 
 
+def _float64_layer(oracle_mod, layer, x16, w, sel, spec):
+    """The layer in float64 from the same exact fp16 weights, with no intermediate rounding."""
+    sv = {p: layer["backbones"][p].astype(np.float64) for p in ("gate", "up", "down")}
+    t_count = x16.shape[0]
+    ref = np.zeros((t_count, spec.hidden))
+    w16 = w.astype(np.float16).astype(np.float64)
+    for t in range(t_count):
+        for s in range(spec.top_k):
+            e = int(sel[t, s])
+            Wg = oracle_mod.dequant_grouped_expert(layer["gate"], e).astype(np.float64)
+            Wu = oracle_mod.dequant_grouped_expert(layer["up"], e).astype(np.float64)
+            Wd = oracle_mod.dequant_grouped_expert(layer["down"], e).astype(np.float64)
+            xv = x16[t].astype(np.float64)
+            g = Wg @ (sv["gate"] @ xv)
+            u = Wu @ (sv["up"] @ xv)
+            m = g / (1 + np.exp(-g)) * u
+            ref[t] += w16[t, s] * (Wd @ (sv["down"] @ m))
+    return ref
+
+
+def _float64_shared(x, shared_expert):
+    """down(silu(gate x) * up x) in float64 from the fp16 weights."""
+    wg, wu, wd = (np.asarray(m, dtype=np.float64) for m in shared_expert)
+    g = x @ wg.T
+    u = x @ wu.T
+    return ((g / (1 + np.exp(-g))) * u) @ wd.T
+
+
+def _within_layer_tolerance(out, ref, rel_l2=1e-3) -> bool:
+    err = out - ref
+    return bool(np.abs(err).max() < 2e-2 and np.linalg.norm(err) / np.linalg.norm(ref) < rel_l2)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_oracle_layer_shared_expert_against_float64(oracle_mod, tris, dtype):
+    """The oracle's shared-expert branch (the Qwen blocks' shared expert, modeling_qwen2_moe.py:815-818 and
+    modeling_qwen3_5_moe.py:186-188) against a float64 evaluation: y = routed + sigmoid(h . w_g) * down(silu(gate
+    h) * up h), with no intermediate rounding, and ungated y = routed + shared.  The gated branch rounds every
+    tensor to the model dtype as the reference does, so the bound is the dtype's: rel-L2 1e-3 for fp16, 5e-3 for
+    bf16 (bf16's own rounding of a value is ~1.6e-3 rel-L2).  Planted slips fail the same check by two orders
+    of magnitude: the shared expert's gate and up swapped, the gate dropped (ungated), the gate applied to the
+    routed part instead, and the gate's sigmoid left out.  The rounding order itself is pinned bit for bit by
+    the reference's expression run by torch (test_oracle_shared_expert_combination_is_the_reference_expression)."""
+    from tris_moe_amd.configs import MoELayerSpec
+
+    spec = MoELayerSpec("tiny", hidden=256, num_experts=4, intermediate=384, top_k=2, rank=128, tokens=(5,),
+                        shared_expert_intermediate=192)
+    syn = tris["synthetic"]
+    layer = syn.make_layer(spec, 21, oracle_mod.gr_encode)
+    assert layer["shared_expert_gate"].shape == (spec.hidden,)
+    inp = syn.make_inputs(spec, 5, 22, layer["outlier_idx"])
+    w, sel = oracle_mod.route_topk(inp["router_logits"], spec.top_k, spec.renormalize)
+    x16 = inp["x"].astype(np.float16)
+    pl = {p: layer[p] for p in ("gate", "up", "down")}
+    shared = layer["shared_expert"]
+    wgate = layer["shared_expert_gate"]
+    xm = inp["x"] if dtype == "bf16" else x16.astype(np.float32)   # the block input in the model dtype
+    routed = _float64_layer(oracle_mod, layer, x16, w, sel, spec)
+    s64 = _float64_shared(x16.astype(np.float64), shared)
+    g64 = 1.0 / (1.0 + np.exp(-(xm.astype(np.float64) @ wgate.astype(np.float64))))[:, None]
+    assert 0.05 < g64.min() and g64.max() < 0.95            # the gate matters on this data
+    assert np.linalg.norm(s64) > 0.3 * np.linalg.norm(routed)  # and so does the shared expert
+    tol = 5e-3 if dtype == "bf16" else 1e-3
+
+    def layer_out(sh, gate):
+        return oracle_mod.moe_layer(x16, w, sel, pl, layer["backbones"], spec.num_experts, sh, shared_gate=gate,
+                                    x_model=xm, out_dtype=dtype)
+
+    gated_ref = routed + g64 * s64
+    assert _within_layer_tolerance(layer_out(shared, wgate), gated_ref, tol)
+    assert _within_layer_tolerance(layer_out(shared, None), routed + s64)
+    # planted slips
+    assert not _within_layer_tolerance(layer_out((shared[1], shared[0], shared[2]), wgate), gated_ref, tol)
+    assert not _within_layer_tolerance(layer_out(shared, None), gated_ref, tol)
+    assert not _within_layer_tolerance(g64 * routed + s64, gated_ref, tol)
+    logit_only = routed + (xm.astype(np.float64) @ wgate.astype(np.float64))[:, None] * s64
+    assert not _within_layer_tolerance(logit_only, gated_ref, tol)
+    # the shared MLP reads the fp16 cast of the input, its own gate/up/down in that order
+    assert np.array_equal(oracle_mod.shared_expert_mlp(x16, shared), oracle_mod.linear_f16(
+        (oracle_mod.silu_f16(oracle_mod.linear_f16(x16, shared[0])).astype(np.float32)
+         * oracle_mod.linear_f16(x16, shared[1]).astype(np.float32)).astype(np.float16), shared[2]))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_oracle_shared_expert_combination_is_the_reference_expression(oracle_mod, tris, dtype):
+    """The gated join's rounding order: the reference's own lines (modeling_qwen2_moe.py:816-818)
+        shared_expert_output = shared_expert(h).to(dt); final = final + gate.to(dt) * shared_expert_output
+    executed by torch on the CPU in the model dtype, from the oracle's routed sum (rounded to dt as the
+    reference's index_add result is held), its fp16 shared output and its gate, give the oracle's output bits
+    after the caller's rounding."""
+    from tris_moe_amd.configs import MoELayerSpec
+
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    spec = MoELayerSpec("tiny", hidden=256, num_experts=4, intermediate=384, top_k=2, rank=128, tokens=(7,),
+                        shared_expert_intermediate=192)
+    syn = tris["synthetic"]
+    layer = syn.make_layer(spec, 31, oracle_mod.gr_encode)
+    inp = syn.make_inputs(spec, 7, 32, layer["outlier_idx"])
+    w, sel = oracle_mod.route_topk(inp["router_logits"], spec.top_k, spec.renormalize)
+    x16 = inp["x"].astype(np.float16)
+    xm = inp["x"] if dtype == "bf16" else x16.astype(np.float32)
+    pl = {p: layer[p] for p in ("gate", "up", "down")}
+    routed = oracle_mod.moe_layer(x16, w, sel, pl, layer["backbones"], spec.num_experts)
+    got = oracle_mod.round_dtype(oracle_mod.moe_layer(
+        x16, w, sel, pl, layer["backbones"], spec.num_experts, layer["shared_expert"],
+        shared_gate=layer["shared_expert_gate"], x_model=xm, out_dtype=dtype), dtype)
+    final = torch.from_numpy(routed).to(tdt)
+    shared_expert_output = torch.from_numpy(oracle_mod.shared_expert_mlp(x16, layer["shared_expert"])).to(tdt)
+    gate = torch.from_numpy(oracle_mod.shared_expert_gate(xm, layer["shared_expert_gate"], dtype)).to(tdt)
+    want = (final + gate * shared_expert_output).float().numpy()
+    np.testing.assert_array_equal(got, want)
+    # a slip in the order (the product kept in fp32, one rounding at the end) changes bits on this data
+    slip = (final.float() + gate.float() * shared_expert_output.float()).to(tdt).float().numpy()
+    assert not np.array_equal(slip, want)
+
+
+def test_oracle_shared_expert_gate_rounding(oracle_mod):
+    """shared_expert_gate's roundings against torch's CPU bf16/fp16 evaluation of the same module
+    (sigmoid(F.linear(h, w)).to(dt)): one rounding of the exact dot product, then the sigmoid rounded to dt."""
+    import torch.nn.functional as F
+
+    rng = np.random.default_rng(5)
+    for dt, tdt in (("bf16", torch.bfloat16), ("fp16", torch.float16)):
+        h = rng.standard_normal((64, 96)).astype(np.float32)
+        w = (rng.standard_normal(96) * 0.2).astype(np.float32)
+        ht = torch.from_numpy(h).to(tdt)
+        wt = torch.from_numpy(w).to(tdt)
+        h_v, w_v = ht.float().numpy(), wt.float().numpy()
+        got = oracle_mod.shared_expert_gate(h_v, w_v, dt)
+        # torch's CPU linear over bf16/fp16 sums in fp32 (an order that can differ from the exact sum by an
+        # fp32 ulp): compare through the same exact-sum rounding, then check the sigmoid stage on its output
+        logit = F.linear(ht.double(), wt.double().reshape(1, -1)).to(tdt)
+        want = torch.sigmoid(logit.float()).to(tdt).float().numpy()
+        np.testing.assert_array_equal(got, want)
+
+
+def test_oracle_grouped_forward_epilogue_is_the_composition(oracle_mod, tris):
+    """oracle.grouped_forward's output scale and bias epilogue (TriSMoE_cuda_kernel.cu:4662-4680; the sparse
+    form's kernels scale unconditionally, :4051-4064) against torch on the CPU: per segment,
+    fp16(F.linear(hidden, W_e) * scale_e + bias_e) in fp32, zeros for a negative expert slot.  Experts carry
+    distinct scales and biases over three segments; three plausible slips give other bits on this data: the
+    bias added before the scale, one expert's scale used for every segment, and the bias left out."""
+    import torch.nn.functional as F
+
+    rng = np.random.default_rng(7)
+    ext = tris["ext"]
+    E, n, k = 3, 96, 128
+    col_norm = rng.random(k).astype(np.float32) + 0.5
+    proj = dict(tris["synthetic"].make_projection(rng, E, n, k, 0.15, col_norm, ext.gr_encode, keep_dense_gmap=True))
+    proj["output_scale"] = (rng.random((E, n)) * 2 + 0.25).astype(np.float16)
+    proj["bias"] = rng.standard_normal((E, n)).astype(np.float16)
+    proj["has_output_scale"] = True
+    proj["has_bias"] = True
+    hidden = (rng.standard_normal((11, k)) * 2).astype(np.float16)
+    eids = np.asarray([2, 0, -1, 1], dtype=np.int32)
+    seg = np.asarray([0, 4, 7, 8, 11], dtype=np.int32)
+    got = oracle_mod.grouped_forward(proj, hidden, eids, seg)
+
+    def composition(bias_first=False, one_scale=False, no_bias=False):
+        out = torch.zeros((11, n), dtype=torch.float16)
+        for s, e in enumerate(eids.tolist()):
+            lo, hi = int(seg[s]), int(seg[s + 1])
+            if e < 0:
+                continue
+            wt = torch.from_numpy(oracle_mod.dequant_grouped_expert(proj, e)).double()
+            acc = F.linear(torch.from_numpy(hidden[lo:hi]).double(), wt).float()
+            sc = torch.from_numpy(proj["output_scale"][0 if one_scale else e]).float()
+            bi = torch.from_numpy(proj["bias"][e]).float()
+            if no_bias:
+                acc = acc * sc
+            elif bias_first:
+                acc = (acc + bi) * sc
+            else:
+                acc = acc * sc + bi
+            out[lo:hi] = acc.half()
+        return out.numpy()
+
+    want = composition()
+    np.testing.assert_array_equal(got, want)
+    assert not np.any(got[7:8])                                   # the negative slot's rows are zero
+    for slip in (dict(bias_first=True), dict(one_scale=True), dict(no_bias=True)):
+        assert not np.array_equal(composition(**slip), want), slip
+    # scale only, and bias only
+    only_scale = dict(proj, has_bias=False)
+    ws = oracle_mod.grouped_forward(only_scale, hidden, eids, seg)
+    np.testing.assert_array_equal(ws, composition(no_bias=True))
+    wb = oracle_mod.grouped_forward(dict(proj, has_output_scale=False), hidden, eids, seg)
+    plain = oracle_mod.grouped_forward(dict(proj, has_output_scale=False, has_bias=False), hidden, eids, seg)
+    for s, e in enumerate(eids.tolist()):
+        lo, hi = int(seg[s]), int(seg[s + 1])
+        if e < 0:
+            continue
+        acc = F.linear(torch.from_numpy(hidden[lo:hi]).double(),
+                       torch.from_numpy(oracle_mod.dequant_grouped_expert(proj, e)).double()).float()
+        np.testing.assert_array_equal(wb[lo:hi], (acc + torch.from_numpy(proj["bias"][e]).float()).half().numpy())
+        np.testing.assert_array_equal(plain[lo:hi], acc.half().numpy())
+    # the sparse form scales unconditionally (TriSMoE_cuda_kernel.cu:4051-4064): a sparse payload without the
+    # has_output_scale flag still applies the scale
+    from gr_cases import to_sparse
+
+    sparse = to_sparse(oracle_mod, proj, k)
+    sparse["has_output_scale"] = False
+    sparse["has_bias"] = False
+    np.testing.assert_array_equal(oracle_mod.grouped_forward(sparse, hidden, eids, seg), composition(no_bias=True))
+
+
 def test_oracle_layer_input_scales(oracle_mod, tris):
     """The oracle's ns_mode == 1 backbone input scales (qlinear_cuda.py:4477-4480): unit scales change nothing;
     power-of-two scales (exact fp16 products) give the bits of the layer whose backbone columns carry the same
