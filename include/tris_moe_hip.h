@@ -663,6 +663,21 @@ int tris_moe_combine_gated(const uint16_t* expert_out, const uint16_t* expert_co
                            const uint16_t* shared_gate_weight, int32_t tokens, int32_t top_k, int32_t hidden,
                            int32_t out_bf16, uint16_t* out, void* stream);
 
+/*
+ * The block's router Linear and the expert kernels' input cast in one launch: replaces router_logits =
+ * self.gate(hidden_states) (nn.Linear(hidden, num_experts, bias=False) in the model dtype) and the fp16 cast
+ * of the kernel input (modeling_mixtral.py:83-90, 546-553).  x [tokens, hidden] and router_weight
+ * [num_experts, hidden] in the model dtype (bf16 when model_bf16, else fp16).  Outputs:
+ *   router_logits [tokens, num_experts], model dtype: dt(sum_k x[t][k] * w[e][k]), the fp32 sum of the exact
+ *     products (on MFMA) rounded once, the block's second output;
+ *   logits_f32 [tokens, num_experts]: the same values widened (the softmax input, F.softmax(..., dtype=float));
+ *   x16 [tokens, hidden] fp16(x) (round to nearest even) when model_bf16 and x16 is not NULL.
+ * hidden a multiple of 8; x, router_weight and x16 16-byte aligned.  No reference counterpart as one call.
+ */
+int tris_router_linear(const uint16_t* x, const uint16_t* router_weight, int32_t tokens, int32_t hidden,
+                       int32_t num_experts, int32_t model_bf16, uint16_t* router_logits, float* logits_f32,
+                       uint16_t* x16, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -688,6 +688,215 @@ __global__ __launch_bounds__(kRouteThreads) void route_backbone_kernel(RouteArgs
   backbone_block<TT, B>(ba, active, v % gx, (v / gx) % gy, v / (gx * gy), tid % kBbThreads, sm.red[sub]);
 }
 
+// ---- The block's prologue: the router Linear and the expert kernels' input cast in one launch
+// (modeling_mixtral.py:546-553: router_logits = self.gate(hidden_states) in the model dtype; hidden_states
+// cast to fp16 for the quantised kernels, :83-90).  Workgroup (ex, ty) computes the 16 x 16 tile of logits of
+// tokens 16 ty.. and experts 16 ex.. on v_mfma_f32_16x16x32_{bf16,f16} (products exact in fp32, fp32 sums):
+// its 16 wavefronts split the hidden dimension, each with kRlBatch K steps of loads in flight, and wavefront 0
+// adds the others' partial tiles in wavefront order.  Each logit is rounded once to the model dtype and
+// written twice: in that dtype (the block's router_logits output) and widened to fp32 (the softmax input,
+// F.softmax(router_logits, dtype=float)).  The workgroups of the first expert tile also write fp16(x) of
+// their tokens from the very operands they load (bf16 -> fp32 -> fp16, round to nearest even, as torch's
+// .to(float16)), so the cast reads nothing more.
+constexpr int kRlWaves = 16;
+constexpr int kRlThreads = kRlWaves * kWave;
+constexpr int kRlBatch = 4;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ uint4 rl_load16(const uint16_t* __restrict__ p, bool valid) {
+  const uint4 v = *reinterpret_cast<const uint4*>(p);
+  return valid ? v : make_uint4(0u, 0u, 0u, 0u);
+}
+
+// Two bf16 (one word) -> two fp16 (one word), each rounded to nearest even.
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w) {
+  const float lo = __uint_as_float(w << 16);
+  const float hi = __uint_as_float(w & 0xFFFF0000u);
+  return static_cast<uint32_t>(f2h_bits(lo)) | (static_cast<uint32_t>(f2h_bits(hi)) << 16);
+}
+
+template <bool kBf16>
+__global__ __launch_bounds__(kRlThreads) void router_linear_kernel(const uint16_t* __restrict__ x,
+                                                                   const uint16_t* __restrict__ w, int tokens,
+                                                                   int hidden, int num_experts, int kper,
+                                                                   uint16_t* __restrict__ logits_out,
+                                                                   float* __restrict__ logits_f32,
+                                                                   uint16_t* __restrict__ x16) {
+  __shared__ f32x4 red[kRlWaves - 1][kWave];
+  const int tid = static_cast<int>(threadIdx.x);
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int i = lane % 16;
+  const int kg = lane / 16;
+  const int t = static_cast<int>(blockIdx.y) * 16 + i;  // token of this lane's A row
+  const int e = static_cast<int>(blockIdx.x) * 16 + i;  // expert of this lane's B column
+  const bool tv = t < tokens;
+  const bool ev = e < num_experts;
+  const uint16_t* xr = x + static_cast<int64_t>(tv ? t : 0) * hidden;
+  const uint16_t* wr = w + static_cast<int64_t>(ev ? e : 0) * hidden;
+  const bool cast = kBf16 && x16 != nullptr && blockIdx.x == 0 && tv;
+  uint16_t* cr = cast ? x16 + static_cast<int64_t>(t) * hidden : nullptr;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int kb = wave * kper;
+  const int ke = (kb + kper) < hidden ? (kb + kper) : hidden;
+  for (int k0 = kb; k0 < ke; k0 += kRlBatch * 32) {
+    uint4 av[kRlBatch], bv[kRlBatch];
+#pragma unroll
+    for (int u = 0; u < kRlBatch; ++u) {
+      const int k = k0 + u * 32 + kg * 8;
+      const bool kv = k < ke;  // hidden % 8 == 0: a 16-byte run lies inside the row iff it starts before ke
+      av[u] = rl_load16(xr + (kv ? k : 0), kv && tv);
+      bv[u] = rl_load16(wr + (kv ? k : 0), kv && ev);
+    }
+    if (cast) {
+#pragma unroll
+      for (int u = 0; u < kRlBatch; ++u) {
+        const int k = k0 + u * 32 + kg * 8;
+        if (k < ke) {
+          *reinterpret_cast<uint4*>(cr + k) = make_uint4(bf16x2_to_f16x2(av[u].x), bf16x2_to_f16x2(av[u].y),
+                                                         bf16x2_to_f16x2(av[u].z), bf16x2_to_f16x2(av[u].w));
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kRlBatch; ++u) {
+      if constexpr (kBf16) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av[u]),
+                                                      __builtin_bit_cast(bf16x8, bv[u]), acc, 0, 0, 0);
+      } else {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av[u]),
+                                                     __builtin_bit_cast(f16x8, bv[u]), acc, 0, 0, 0);
+      }
+    }
+  }
+  if (wave > 0) red[wave - 1][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int q = 0; q < kRlWaves - 1; ++q) acc += red[q][lane];
+  // acc[v] = logit of token 16 ty + 4 kg + v, expert e
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int tt = static_cast<int>(blockIdx.y) * 16 + 4 * kg + v;
+    if (tt < tokens && ev) {
+      uint16_t bits;
+      float val;
+      if constexpr (kBf16) {
+        uint32_t u = __float_as_uint(acc[v]);
+        if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu) != 0u) {
+          bits = static_cast<uint16_t>((u >> 16) | 0x40u);  // NaN stays NaN
+        } else {
+          u += 0x7FFFu + ((u >> 16) & 1u);
+          bits = static_cast<uint16_t>(u >> 16);
+        }
+        val = __uint_as_float(static_cast<uint32_t>(bits) << 16);
+      } else {
+        bits = f2h_bits(acc[v]);
+        val = h2f(bits);
+      }
+      const int64_t o = static_cast<int64_t>(tt) * num_experts + e;
+      logits_out[o] = bits;
+      logits_f32[o] = val;
+    }
+  }
+}
+
+// The same outputs for decode-sized batches, spread over many workgroups: workgroup (t, eg) computes token t's
+// logits of experts 8 eg .. 8 eg + 7 with VALU dot products.  Thread j takes the 16-byte runs j, j + 256, ...
+// of the row; all its loads (x and the 8 weight rows) are issued before any product, each thread sums its
+// products in fp32 in run order, the wavefronts reduce by a fixed DPP tree and wavefront 0 adds the four
+// wavefront sums in order.  The workgroups of expert group 0 write fp16(x) of their token.
+constexpr int kRlsThreads = 256;
+constexpr int kRlsExperts = 8;
+constexpr int kRlsMaxRuns = 4;  // 16-byte runs per thread held in registers: hidden <= 4 * 256 * 8 = 8192
+
+template <bool kBf16>
+__device__ __forceinline__ float rl_dt(uint32_t w, int half) {
+  const uint32_t b = half ? (w >> 16) : (w & 0xFFFFu);
+  return kBf16 ? __uint_as_float(b << 16) : h2f(static_cast<uint16_t>(b));
+}
+
+template <bool kBf16>
+__global__ __launch_bounds__(kRlsThreads) void router_linear_small_kernel(const uint16_t* __restrict__ x,
+                                                                          const uint16_t* __restrict__ w,
+                                                                          int hidden, int num_experts,
+                                                                          uint16_t* __restrict__ logits_out,
+                                                                          float* __restrict__ logits_f32,
+                                                                          uint16_t* __restrict__ x16) {
+  __shared__ float part[kRlsThreads / kWave][kRlsExperts];
+  const int tid = static_cast<int>(threadIdx.x);
+  const int t = static_cast<int>(blockIdx.x);
+  const int e0 = static_cast<int>(blockIdx.y) * kRlsExperts;
+  const int runs = hidden / 8;
+  const uint16_t* xr = x + static_cast<int64_t>(t) * hidden;
+  uint4 xv[kRlsMaxRuns], wv[kRlsMaxRuns][kRlsExperts];
+#pragma unroll
+  for (int m = 0; m < kRlsMaxRuns; ++m) {
+    const int c = tid + m * kRlsThreads;
+    const bool cv = c < runs;
+    xv[m] = rl_load16(xr + (cv ? c : 0) * 8, cv);
+#pragma unroll
+    for (int q = 0; q < kRlsExperts; ++q) {
+      const int e = e0 + q;
+      const bool v = cv && e < num_experts;
+      wv[m][q] = rl_load16(w + static_cast<int64_t>(e < num_experts ? e : 0) * hidden + (cv ? c : 0) * 8, v);
+    }
+  }
+  if (kBf16 && x16 != nullptr && blockIdx.y == 0) {
+#pragma unroll
+    for (int m = 0; m < kRlsMaxRuns; ++m) {
+      const int c = tid + m * kRlsThreads;
+      if (c < runs) {
+        *reinterpret_cast<uint4*>(x16 + static_cast<int64_t>(t) * hidden + c * 8) =
+            make_uint4(bf16x2_to_f16x2(xv[m].x), bf16x2_to_f16x2(xv[m].y), bf16x2_to_f16x2(xv[m].z),
+                       bf16x2_to_f16x2(xv[m].w));
+      }
+    }
+  }
+  float acc[kRlsExperts];
+#pragma unroll
+  for (int q = 0; q < kRlsExperts; ++q) acc[q] = 0.0f;
+#pragma unroll
+  for (int m = 0; m < kRlsMaxRuns; ++m) {
+    const uint32_t xs[4] = {xv[m].x, xv[m].y, xv[m].z, xv[m].w};
+#pragma unroll
+    for (int q = 0; q < kRlsExperts; ++q) {
+      const uint32_t ws[4] = {wv[m][q].x, wv[m][q].y, wv[m][q].z, wv[m][q].w};
+#pragma unroll
+      for (int h = 0; h < 8; ++h) acc[q] += rl_dt<kBf16>(xs[h / 2], h & 1) * rl_dt<kBf16>(ws[h / 2], h & 1);
+    }
+  }
+  const int wave = tid / kWave;
+#pragma unroll
+  for (int q = 0; q < kRlsExperts; ++q) {
+    const float v = wave_sum_f32(acc[q]);
+    if ((tid & (kWave - 1)) == 0) part[wave][q] = v;
+  }
+  __syncthreads();
+  if (tid < kRlsExperts && e0 + tid < num_experts) {
+    const float dot = ((part[0][tid] + part[1][tid]) + part[2][tid]) + part[3][tid];
+    uint16_t bits;
+    float val;
+    if constexpr (kBf16) {
+      uint32_t u = __float_as_uint(dot);
+      if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu) != 0u) {
+        bits = static_cast<uint16_t>((u >> 16) | 0x40u);
+      } else {
+        u += 0x7FFFu + ((u >> 16) & 1u);
+        bits = static_cast<uint16_t>(u >> 16);
+      }
+      val = __uint_as_float(static_cast<uint32_t>(bits) << 16);
+    } else {
+      bits = f2h_bits(dot);
+      val = h2f(bits);
+    }
+    const int64_t o = static_cast<int64_t>(t) * num_experts + e0 + tid;
+    logits_out[o] = bits;
+    logits_f32[o] = val;
+  }
+}
+
 }  // namespace tris
 
 using namespace tris;
@@ -884,4 +1093,44 @@ extern "C" int tris_route_topk_backbone(const float* router_logits, int32_t num_
   rc = check_launch(who);
   if (rc || pl.slices == 1 || defer_reduce) return rc;
   return launch_backbone_reduce(ba, nproj, s, who);
+}
+
+// Batches up to this many tokens take router_linear_small_kernel (its grid is tokens x expert groups).
+constexpr int kRlsMaxTokens = 128;
+
+extern "C" int tris_router_linear(const uint16_t* x, const uint16_t* router_weight, int32_t tokens, int32_t hidden,
+                                  int32_t num_experts, int32_t model_bf16, uint16_t* router_logits,
+                                  float* logits_f32, uint16_t* x16, void* stream) {
+  const char* who = "tris_router_linear";
+  TRIS_REQUIRE(tokens >= 0 && hidden > 0 && num_experts > 0, "%s: bad shape", who);
+  if (tokens == 0) return TRIS_OK;
+  TRIS_REQUIRE(x && router_weight && router_logits && logits_f32, "%s: null pointer", who);
+  TRIS_REQUIRE(hidden % 8 == 0, "%s: hidden %d must be a multiple of 8", who, hidden);
+  const auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  TRIS_REQUIRE(a16(x) && a16(router_weight) && a16(x16), "%s: x, the weight and x16 must be 16-byte aligned", who);
+  TRIS_REQUIRE(model_bf16 || x16 == nullptr, "%s: x16 is written only for a bf16 model (fp16 x is the input)", who);
+  TRIS_REQUIRE(ceil_div(tokens, 16) <= 65535, "%s: %d tokens exceed the grid", who, tokens);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (tokens <= kRlsMaxTokens && hidden <= kRlsMaxRuns * kRlsThreads * 8) {
+    // decode-sized: one workgroup per token and 8 experts
+    const dim3 g(static_cast<unsigned>(tokens), static_cast<unsigned>(ceil_div(num_experts, kRlsExperts)));
+    if (model_bf16) {
+      hipLaunchKernelGGL((router_linear_small_kernel<true>), g, dim3(kRlsThreads), 0, s, x, router_weight, hidden,
+                         num_experts, router_logits, logits_f32, x16);
+    } else {
+      hipLaunchKernelGGL((router_linear_small_kernel<false>), g, dim3(kRlsThreads), 0, s, x, router_weight, hidden,
+                         num_experts, router_logits, logits_f32, x16);
+    }
+    return check_launch(who);
+  }
+  const int kper = ceil_div(ceil_div(hidden, kRlWaves), 32) * 32;
+  const dim3 grid(static_cast<unsigned>(ceil_div(num_experts, 16)), static_cast<unsigned>(ceil_div(tokens, 16)));
+  if (model_bf16) {
+    hipLaunchKernelGGL((router_linear_kernel<true>), grid, dim3(kRlThreads), 0, s, x, router_weight, tokens, hidden,
+                       num_experts, kper, router_logits, logits_f32, x16);
+  } else {
+    hipLaunchKernelGGL((router_linear_kernel<false>), grid, dim3(kRlThreads), 0, s, x, router_weight, tokens, hidden,
+                       num_experts, kper, router_logits, logits_f32, x16);
+  }
+  return check_launch(who);
 }

@@ -172,6 +172,7 @@ SIGNATURES = {
     "tris_backbone_workspace_bytes": (_I64, [_I32, _I32, _I32]),
     "tris_moe_combine": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _P, _P]),
     "tris_moe_combine_compensated": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P]),
+    "tris_router_linear": (ctypes.c_int, [_P, _P, _I32, _I32, _I32, _I32, _P, _P, _P, _P]),
     "tris_moe_combine_gated": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _P, _P]),
     "tris_swiglu_mul": (ctypes.c_int, [_P, _P, _I64, _P, _P]),
     "tris_swiglu_mul_compensated": (ctypes.c_int, [_P, _P, _P, _P, _I64, _P, _P]),

@@ -1438,6 +1438,40 @@ def compact3_qkv_linear_forward(input, q_qweight1, q_qweight2_sparse, q_qweight2
     return out
 
 
+def router_linear_ok(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    """True when router_linear can run: x [T, H] and weight [E, H] CUDA tensors of one dtype (bf16 or fp16) on
+    one device, contiguous, H a multiple of 8, 16-byte aligned."""
+    if not (isinstance(x, torch.Tensor) and isinstance(weight, torch.Tensor)):
+        return False
+    if x.device.type != "cuda" or weight.device != x.device or x.dtype != weight.dtype:
+        return False
+    if x.dtype not in (torch.bfloat16, torch.float16) or x.dim() != 2 or weight.dim() != 2:
+        return False
+    if int(x.size(1)) != int(weight.size(1)) or int(x.size(1)) % 8 or int(x.size(0)) > 16 * 65535:
+        return False
+    return (x.is_contiguous() and weight.is_contiguous() and x.data_ptr() % 16 == 0
+            and weight.data_ptr() % 16 == 0)
+
+
+def router_linear(x: torch.Tensor, weight: torch.Tensor):
+    """The block's router Linear and the expert kernels' input cast in one launch (tris_router_linear):
+    returns (router_logits in x's dtype, the same logits as fp32, x16), router_logits = F.linear(x, weight)
+    rounded once from the fp32 sum of exact products (modeling_mixtral.py:546), x16 = x.to(float16) (x itself
+    when x is fp16)."""
+    if not router_linear_ok(x, weight):
+        raise RuntimeError("router_linear: x [T, H] and weight [E, H] must be contiguous bf16/fp16 CUDA tensors of "
+                           "one dtype, H a multiple of 8, 16-byte aligned")
+    tokens, hidden, experts = int(x.size(0)), int(x.size(1)), int(weight.size(0))
+    bf16 = x.dtype == torch.bfloat16
+    logits = torch.empty((tokens, experts), dtype=x.dtype, device=x.device)
+    logits32 = torch.empty((tokens, experts), dtype=torch.float32, device=x.device)
+    x16 = torch.empty((tokens, hidden), dtype=torch.float16, device=x.device) if bf16 else x
+    _lib.check(_lib.load().tris_router_linear(_ptr(x), _ptr(weight), tokens, hidden, experts, int(bf16), _ptr(logits),
+                                              _ptr(logits32), _ptr(x16) if bf16 else None, _stream(x)),
+               "tris_router_linear")
+    return logits, logits32, x16
+
+
 def moe_combine(expert_out: torch.Tensor, inverse_perm: torch.Tensor, weights: torch.Tensor,
                 shared: torch.Tensor | None = None, expert_comp: torch.Tensor | None = None,
                 shared_gate_input: torch.Tensor | None = None, shared_gate_weight: torch.Tensor | None = None,

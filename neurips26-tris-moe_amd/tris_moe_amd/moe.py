@@ -496,22 +496,33 @@ class TrisSparseMoeBlock(nn.Module):
             return self.shared_expert
         return (*self.shared_expert, self.shared_expert_gate.weight.detach().to(model_dtype))
 
-    def forward_routed(self, hidden_states: torch.Tensor, router_logits: torch.Tensor) -> torch.Tensor:
-        """The block after the router: [T, H] activations and [T, E] logits -> [T, H]."""
+    def forward_routed(self, hidden_states: torch.Tensor, router_logits: torch.Tensor,
+                       x16: torch.Tensor | None = None) -> torch.Tensor:
+        """The block after the router: [T, H] activations and [T, E] logits -> [T, H].  x16: the activations
+        already cast to fp16 (else cast here)."""
         output_dtype = hidden_states.dtype
-        x16 = hidden_states.to(torch.float16) if hidden_states.dtype == torch.bfloat16 else hidden_states
+        if x16 is None:
+            x16 = hidden_states.to(torch.float16) if hidden_states.dtype == torch.bfloat16 else hidden_states
         if x16.dtype != torch.float16 or x16.device.type != "cuda":
             raise RuntimeError("grouped expert kernels require CUDA float16/bfloat16 hidden states")
-        return grouped_moe_forward_from_logits(x16.contiguous(), router_logits.float().contiguous(), self.top_k,
+        logits = router_logits if router_logits.dtype == torch.float32 else router_logits.float()
+        return grouped_moe_forward_from_logits(x16.contiguous(), logits.contiguous(), self.top_k,
                                                self.renormalize, self.payloads, self.backbones, self.num_experts,
                                                output_dtype, self._shared(output_dtype),
                                                expert_path=self.expert_path, x_model=hidden_states.contiguous())
 
     def forward(self, hidden_states: torch.Tensor):
         """modeling_mixtral.py:539-608: hidden_states [B, S, H] (bf16 or fp16) -> (out [B, S, H] in the input
-        dtype, router_logits [B*S, E] in the router's dtype)."""
+        dtype, router_logits [B*S, E] in the router's dtype).  When the activations and the router share the
+        model dtype, the router Linear and the fp16 cast run as one launch (ext.router_linear); else the
+        Linear is torch's."""
         batch, seq, hidden = hidden_states.shape
         flat = hidden_states.reshape(-1, hidden)
-        router_logits = self.gate(flat.to(self.gate.weight.dtype))
-        out = self.forward_routed(flat, router_logits)
+        weight = self.gate.weight.detach()
+        if ext.router_linear_ok(flat, weight):
+            router_logits, logits32, x16 = ext.router_linear(flat, weight)
+            out = self.forward_routed(flat, logits32, x16=x16)
+        else:
+            router_logits = self.gate(flat.to(self.gate.weight.dtype))
+            out = self.forward_routed(flat, router_logits)
         return out.reshape(batch, seq, hidden), router_logits

@@ -457,6 +457,16 @@ def linear_f16(x, w) -> np.ndarray:
     return (np.asarray(x, dtype=np.float16).astype(ACC) @ np.asarray(w, dtype=np.float16).astype(ACC).T).astype(np.float16)
 
 
+def router_logits(x_model, router_weight, dtype: str = "bf16") -> np.ndarray:
+    """router_logits = self.gate(hidden_states) (modeling_mixtral.py:546, nn.Linear(hidden, num_experts,
+    bias=False) in the model dtype): the exact sum of x . w rounded once to the dtype ("bf16" or "fp16").  x_model
+    [T, H] and router_weight [E, H] hold model-dtype values.  Returns the rounded logits as fp32 [T, E] (the
+    values F.softmax(router_logits, dtype=float) reads)."""
+    xm = np.asarray(x_model, dtype=np.float32).astype(np.float64)
+    w = np.asarray(router_weight, dtype=np.float32).astype(np.float64)
+    return round_dtype((xm @ w.T).astype(np.float32), dtype)
+
+
 def route_topk(router_logits, top_k: int, renormalize: bool = True):
     """softmax(fp32) -> top-k -> optional renorm (modeling_mixtral.py:548-551)."""
     lg = np.asarray(router_logits, dtype=np.float32)

@@ -54,6 +54,16 @@ def stacked_gr(oracle_mod, denses):
     return words, np.stack([c[1] for c in coded]), np.stack([c[2] for c in coded])
 
 
+def ulps(got, want, dtype):
+    """|got - want| in units of the dtype's ulp at the larger magnitude (fp16 subnormals included)."""
+    m = np.maximum(np.abs(got), np.abs(want)).astype(np.float64)
+    if dtype == "fp16":
+        ulp = np.spacing(m.astype(np.float16)).astype(np.float64)
+    else:
+        ulp = np.exp2(np.floor(np.log2(np.maximum(m, 2.0 ** -126))) - 7)
+    return np.abs(got.astype(np.float64) - want.astype(np.float64)) / ulp
+
+
 # --------------------------------------------------------------- GR decode
 def test_gr_decode_known_answers(tris, oracle_mod, cuda):
     ext = tris["ext"]
@@ -469,6 +479,40 @@ def test_route_device_bad_ids_stay_in_bounds(tris, oracle_mod, cuda, t, k, e):
     for i in np.nonzero(valid)[0]:
         want[i // k] += (eon[inv[i]] * np.float32(wn[i // k, i % k])).astype(np.float16).astype(np.float32)
     np.testing.assert_allclose(out, oracle_mod.bf16_round(want), rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("tokens,hidden,experts", [(1, 4096, 8), (16, 4096, 8), (37, 2048, 256), (300, 1024, 60),
+                                                   (2048, 4096, 8)])
+def test_router_linear_matches_oracle(tris, oracle_mod, cuda, dtype, tokens, hidden, experts):
+    """tris_router_linear (the block's router Linear and fp16 input cast in one launch) against the oracle's
+    router_logits: the model-dtype logits equal the exact sum rounded once except where the fp32 summation
+    order decides a rounding tie (a tiny fraction, each one ulp), the fp32 logits are those values widened, and
+    x16 is torch's x.to(float16) bit for bit (bf16 model; an fp16 model passes x itself)."""
+    note(f"router linear {dtype} T={tokens} H={hidden} E={experts}")
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    rng = np.random.default_rng(tokens * 7 + experts)
+    x = torch.from_numpy(rng.standard_normal((tokens, hidden)).astype(np.float32) * 2).to(tdt).to(cuda)
+    w = torch.from_numpy((rng.standard_normal((experts, hidden)) / math.sqrt(hidden)).astype(np.float32)).to(tdt)
+    w = w.to(cuda)
+    logits, logits32, x16 = tris["ext"].router_linear(x, w)
+    assert logits.dtype == tdt and logits32.dtype == torch.float32 and x16.dtype == torch.float16
+    got = logits.float().cpu().numpy()
+    want = oracle_mod.router_logits(x.float().cpu().numpy(), w.float().cpu().numpy(), dtype)
+    eq = got == want
+    assert (~eq).sum() <= max(1, 0.002 * eq.size), f"{(~eq).sum()} of {eq.size} logits differ"
+    # one ulp of the dtype, or (a sum that cancels to a tiny value) a few fp32 ulps of its terms' magnitudes:
+    # any fp32 summation order is that far from the exact sum
+    l1 = np.abs(x.float().cpu().numpy()).astype(np.float64) @ np.abs(w.float().cpu().numpy()).astype(np.float64).T
+    d = ulps(got, want, dtype)
+    ok = (d <= 1) | (np.abs(got - want) <= 16 * 2.0 ** -24 * l1)
+    worst = np.unravel_index(np.argmax(np.where(ok, 0, d)), d.shape)
+    assert ok.all(), f"{d[worst]} ulps at {worst}: got {got[worst]!r} want {want[worst]!r}"
+    np.testing.assert_array_equal(logits32.cpu().numpy(), got)
+    if dtype == "bf16":
+        assert torch.equal(x16.view(torch.int16), x.to(torch.float16).view(torch.int16))
+    else:
+        assert x16.data_ptr() == x.data_ptr()
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])

@@ -422,6 +422,30 @@ def test_oracle_shared_expert_gate_rounding(oracle_mod):
         np.testing.assert_array_equal(got, want)
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_oracle_router_logits_against_torch_linear(oracle_mod, dtype):
+    """oracle.router_logits against torch's own CPU nn.Linear in the model dtype (self.gate(hidden_states),
+    modeling_mixtral.py:546), which sums in fp32 and rounds once: equal except where an fp32 summation order
+    decides a rounding tie (at most 0.2 % of the logits, each then one ulp apart); a plausible slip (the
+    weight's rows misread as columns of a transposed layout, i.e. x . w for the wrong expert) is far off."""
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    rng = np.random.default_rng(11)
+    x = torch.from_numpy(rng.standard_normal((64, 512)).astype(np.float32)).to(tdt)
+    w = torch.from_numpy((rng.standard_normal((16, 512)) * 0.05).astype(np.float32)).to(tdt)
+    got = oracle_mod.router_logits(x.float().numpy(), w.float().numpy(), dtype)
+    lin = torch.nn.Linear(512, 16, bias=False, dtype=tdt)
+    lin.weight.data = w
+    with torch.no_grad():
+        want = lin(x).float().numpy()
+    eq = got == want
+    assert eq.mean() > 0.998
+    rel_ulp = 2.0 ** (-7 if dtype == "bf16" else -10)  # one ulp is at most the larger |v| * 2^-(mantissa bits)
+    assert np.all(np.abs(got - want) <= np.maximum(np.abs(got), np.abs(want)) * rel_ulp)
+    assert got.dtype == np.float32 and np.array_equal(oracle_mod.round_dtype(got, dtype), got)
+    slip = oracle_mod.router_logits(x.float().numpy(), np.roll(w.float().numpy(), 1, axis=0), dtype)
+    assert np.abs(slip - want).max() > 0.1
+
+
 def test_oracle_grouped_forward_epilogue_is_the_composition(oracle_mod, tris):
     """oracle.grouped_forward's output scale and bias epilogue (TriSMoE_cuda_kernel.cu:4662-4680; the sparse
     form's kernels scale unconditionally, :4051-4064) against torch on the CPU: per segment,
