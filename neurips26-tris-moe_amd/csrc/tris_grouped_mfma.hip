@@ -893,7 +893,15 @@ void grouped_mfma_kernel(MfmaArgs a) {
   const int W = static_cast<int>(gridDim.x);
   const int w = static_cast<int>(blockIdx.x);
   int rt_first = w, rt_step = W, ob_lo = 0, ob_hi = nob;
-  if (R <= W) {
+  if (static_cast<int64_t>(R) * nob <= W) {
+    // at least one workgroup per (row tile, output tile): workgroup w takes pair w, and the idle ones are the
+    // last of the grid, so the busy ones are spread evenly over the CUs as the hardware deals them out
+    if (w >= R * nob) return;
+    rt_first = w / nob;
+    ob_lo = w - rt_first * nob;
+    ob_hi = ob_lo + 1;
+    rt_step = R;  // one row tile
+  } else if (R <= W) {
     const int per = W / R;
     const int extra = W % R;
     int sub, cnt;

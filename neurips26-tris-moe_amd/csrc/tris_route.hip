@@ -697,7 +697,8 @@ __global__ __launch_bounds__(kRouteThreads) void route_backbone_kernel(RouteArgs
 // written twice: in that dtype (the block's router_logits output) and widened to fp32 (the softmax input,
 // F.softmax(router_logits, dtype=float)).  The workgroups of the first expert tile also write fp16(x) of
 // their tokens from the very operands they load (bf16 -> fp32 -> fp16, round to nearest even, as torch's
-// .to(float16)), so the cast reads nothing more.
+// .to(float16)), so the cast reads nothing more.  Used for large batches and for rows wider than
+// router_linear_small_kernel holds.
 constexpr int kRlWaves = 16;
 constexpr int kRlThreads = kRlWaves * kWave;
 constexpr int kRlBatch = 4;
@@ -802,7 +803,8 @@ __global__ __launch_bounds__(kRlThreads) void router_linear_kernel(const uint16_
   }
 }
 
-// The same outputs for decode-sized batches, spread over many workgroups: workgroup (t, eg) computes token t's
+// The same outputs for batches up to kRlsMaxTokens (rows of up to 8192 columns), spread over many workgroups:
+// workgroup (t, eg) computes token t's
 // logits of experts 8 eg .. 8 eg + 7 with VALU dot products.  Thread j takes the 16-byte runs j, j + 256, ...
 // of the row; all its loads (x and the 8 weight rows) are issued before any product, each thread sums its
 // products in fp32 in run order, the wavefronts reduce by a fixed DPP tree and wavefront 0 adds the four
@@ -1095,8 +1097,8 @@ extern "C" int tris_route_topk_backbone(const float* router_logits, int32_t num_
   return launch_backbone_reduce(ba, nproj, s, who);
 }
 
-// Batches up to this many tokens take router_linear_small_kernel (its grid is tokens x expert groups).
-constexpr int kRlsMaxTokens = 128;
+// Batches up to this many tokens take router_linear_small_kernel.
+constexpr int kRlsMaxTokens = 512;
 
 extern "C" int tris_router_linear(const uint16_t* x, const uint16_t* router_weight, int32_t tokens, int32_t hidden,
                                   int32_t num_experts, int32_t model_bf16, uint16_t* router_logits,
@@ -1112,7 +1114,9 @@ extern "C" int tris_router_linear(const uint16_t* x, const uint16_t* router_weig
   TRIS_REQUIRE(ceil_div(tokens, 16) <= 65535, "%s: %d tokens exceed the grid", who, tokens);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (tokens <= kRlsMaxTokens && hidden <= kRlsMaxRuns * kRlsThreads * 8) {
-    // decode-sized: one workgroup per token and 8 experts
+    // one workgroup per token and 8 experts: T x E/8 workgroups spread small batches over the GPU (the MFMA
+    // tile kernel has T/16 of them: at T = 16, 11.7 against 5.7 us); for large batches each of them re-reading
+    // the 8 weight rows costs more (T = 2048: 19.6 against the tile kernel's 15.6 us)
     const dim3 g(static_cast<unsigned>(tokens), static_cast<unsigned>(ceil_div(num_experts, kRlsExperts)));
     if (model_bf16) {
       hipLaunchKernelGGL((router_linear_small_kernel<true>), g, dim3(kRlsThreads), 0, s, x, router_weight, hidden,

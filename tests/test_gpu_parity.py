@@ -483,10 +483,10 @@ def test_route_device_bad_ids_stay_in_bounds(tris, oracle_mod, cuda, t, k, e):
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
 @pytest.mark.parametrize("tokens,hidden,experts", [(1, 4096, 8), (16, 4096, 8), (37, 2048, 256), (300, 1024, 60),
-                                                   (2048, 4096, 8)])
+                                                   (2048, 4096, 8), (40, 8448, 12)])
 def test_router_linear_matches_oracle(tris, oracle_mod, cuda, dtype, tokens, hidden, experts):
-    """tris_router_linear (the block's router Linear and fp16 input cast in one launch) against the oracle's
-    router_logits: the model-dtype logits equal the exact sum rounded once except where the fp32 summation
+    """tris_router_linear (the block's router Linear and fp16 input cast in one launch; rows of more than 8192
+    columns take the MFMA tile kernel) against the oracle's router_logits: the model-dtype logits equal the exact sum rounded once except where the fp32 summation
     order decides a rounding tie (a tiny fraction, each one ulp), the fp32 logits are those values widened, and
     x16 is torch's x.to(float16) bit for bit (bf16 model; an fp16 model passes x itself)."""
     note(f"router linear {dtype} T={tokens} H={hidden} E={experts}")
