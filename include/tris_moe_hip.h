@@ -678,6 +678,42 @@ int tris_router_linear(const uint16_t* x, const uint16_t* router_weight, int32_t
                        int32_t num_experts, int32_t model_bf16, uint16_t* router_logits, float* logits_f32,
                        uint16_t* x16, void* stream);
 
+/*
+ * The block's first launch at decode: tris_router_linear (bf16 model) and the gate/up backbone projections of
+ * the same tokens side by side (no reference counterpart as one call: the router Linear and
+ * compute_shared_hidden, modeling_mixtral.py:546 and qlinear_cuda.py:4454-4502, do not depend on each
+ * other).  x [tokens, hidden] bf16; router_weight [num_experts, hidden] bf16; router_logits bf16 and logits_f32
+ * [tokens, num_experts] and x16 [tokens, hidden] as tris_router_linear writes them.  bb projects the same
+ * input: bb->x == x (its bf16 values converted to fp16 on load, the bits x16 holds), bb->tokens == tokens
+ * <= 64, bb->in_features == hidden.  When the projection is split over K its partial sums stay in
+ * bb->workspace for tris_route_predecode_multi_reduce (or tris_grouped_block_gr_predecode_multi_reduce) to
+ * add with the same job; the outputs then equal tris_backbone_linear_pair's on x16, bit for bit.
+ * hidden a multiple of 8 and at most 8192; 16-byte aligned pointers.
+ */
+int tris_router_backbone(const uint16_t* x, const uint16_t* router_weight, int32_t tokens, int32_t hidden,
+                         int32_t num_experts, uint16_t* router_logits, float* logits_f32, uint16_t* x16,
+                         const tris_backbone_pair_job* bb, void* stream);
+
+/*
+ * The decode route and the predecode of its experts' split bitmaps in one launch (no reference counterpart as
+ * one call: build_grouped_route with the router, TriSMoE_cuda.cpp:741-793 and modeling_mixtral.py:548-555,
+ * and the per-projection predecode, TriSMoE_cuda.cpp:836-853).  One workgroup writes the route outputs
+ * exactly as tris_route_topk_grouped does; every decode workgroup derives the routed experts from the same
+ * router_logits with the same selection, and fills the jobs' buffers as tris_grouped_block_gr_predecode_multi
+ * does for that route's expert_ids (num_slots = min(num_experts, num_tokens * top_k) slots, the active experts
+ * first).  bb (or NULL): a backbone job whose deferred partial sums are reduced in the same launch, as
+ * tris_grouped_block_gr_predecode_multi_reduce does.  The one-wavefront route only: num_tokens * top_k <= 64,
+ * num_experts <= 8.
+ */
+int tris_route_predecode_multi_reduce(const float* router_logits, int32_t num_tokens, int32_t num_experts,
+                                      int32_t top_k, int32_t renormalize, int32_t m_tile,
+                                      uint16_t* routing_weights_f16, float* routing_weights_f32,
+                                      int64_t* selected_experts, int64_t* perm, int64_t* grouped_token_indices,
+                                      int64_t* grouped_slots, int32_t* grouped_expert_ids, int32_t* expert_ids,
+                                      int32_t* segment_offsets, int32_t* problem_offsets, int32_t* counts,
+                                      int32_t* inverse_perm, const tris_gr_predecode_job* jobs, int32_t num_jobs,
+                                      int32_t num_slots, const tris_backbone_pair_job* bb, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

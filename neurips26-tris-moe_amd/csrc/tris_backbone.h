@@ -70,7 +70,26 @@ __device__ __forceinline__ f16x8 load8_vec(const uint16_t* __restrict__ src, int
 // backbone_block: the work of workgroup (bx, by, bz) of that grid done by kBbThreads threads (tid < kBbThreads),
 // with its LDS partial tiles in red.  It passes exactly one __syncthreads (also when !active, a grid slot with
 // no work), so several such blocks can share one larger workgroup.
-template <int TT, int B>
+// 8 bf16 (16 bytes) -> 8 fp16, each rounded to nearest even (torch's bf16 .to(float16)).
+__device__ __forceinline__ f16x8 bf16x8_to_f16x8(uint4 v) {
+  f16x8 r;
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    r[2 * i] = static_cast<_Float16>(__uint_as_float(w[i] << 16));
+    r[2 * i + 1] = static_cast<_Float16>(__uint_as_float(w[i] & 0xFFFF0000u));
+  }
+  return r;
+}
+
+__device__ __forceinline__ f16x8 load8_vec_bf16(const uint16_t* __restrict__ src, int k, bool valid) {
+  f16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (valid) v = bf16x8_to_f16x8(*reinterpret_cast<const uint4*>(src + k));
+  return v;
+}
+
+// kXBf16: a.x holds bf16 activations, converted to fp16 on load (in_features % 8 == 0: the vector path only).
+template <int TT, int B, bool kXBf16 = false>
 __device__ __forceinline__ void backbone_block(const BackboneArgs& a, bool active, int bx, int by, int bz, int tid,
                                                f32x4 (*red)[TT][kWave]) {
   const int q = bz;
@@ -117,7 +136,9 @@ __device__ __forceinline__ void backbone_block(const BackboneArgs& a, bool activ
         const bool kv = k < kend;
         bv[u] = load8_vec(ssrc, k, r_valid && kv);
 #pragma unroll
-        for (int j = 0; j < TT; ++j) av[j][u] = load8_vec(xsrc[j], k, t_valid[j] && kv);
+        for (int j = 0; j < TT; ++j) {
+          av[j][u] = kXBf16 ? load8_vec_bf16(xsrc[j], k, t_valid[j] && kv) : load8_vec(xsrc[j], k, t_valid[j] && kv);
+        }
       }
       if (scaled) {
 #pragma unroll

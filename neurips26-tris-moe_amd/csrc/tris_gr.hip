@@ -11,6 +11,7 @@
 #include "tris_backbone.h"
 #include "tris_gr_span.h"
 #include "tris_moe_hip.h"
+#include "tris_route.h"
 
 namespace tris {
 
@@ -47,6 +48,15 @@ struct GrWork {
   int num_slots;
   int first[TRIS_MAX_PREDECODE_JOBS + 1];  // first item of each job; first[num_jobs] = all items
   int decode_wgs;  // workgroups that decode; any after them reduce a backbone's slices (GrReduce)
+};
+
+// The decode route built in the same launch (tris_route_predecode_multi_reduce): workgroup 0 runs
+// route_wave_body, and every decode workgroup derives its slots' experts from the
+// same logits (route_active_experts) instead of reading expert_ids, which that workgroup is still writing.
+struct GrRoute {
+  RouteArgs ra;
+  int k_variant;  // the route_wave_body instance: 2, 8 or kRouteMaxTopK (by top_k, as tris_route_topk_grouped)
+  int wg;         // its workgroup index (0: the decoders follow it), or -1: no route in this launch
 };
 
 // A backbone projection's slice reduction run by the workgroups past the decoders (independent work in the
@@ -92,36 +102,82 @@ __device__ __forceinline__ void gr_item_header(const GrJobs& jobs, const GrWork&
 template <int S>
 __global__ __launch_bounds__(kSpanThreads) __attribute__((amdgpu_waves_per_eu(5))) void gr_decode_span_kernel(GrJobs jobs, GrWork wk,
                                                                       const int32_t* __restrict__ expert_ids,
-                                                                      GrReduce red) {
+                                                                      GrReduce red, GrRoute rt) {
   constexpr int kBlocksPerItem = kWave / S;
   constexpr int kItemVec4 = kBlocksPerItem * kGrWords / 4;
   static_assert(kGrBlockStride % 4 == 0 && kGrPadFront % 4 == 0, "16-byte aligned block bitmaps");
-  if (static_cast<int>(blockIdx.x) >= wk.decode_wgs) {
-    const int rb = static_cast<int>(blockIdx.x) - wk.decode_wgs;
-    const int q = rb / red.blocks_per_proj;
-    backbone_reduce_at(red.bb, static_cast<int64_t>(rb % red.blocks_per_proj) * kSpanThreads + threadIdx.x, q);
-    return;
-  }
+  static_assert(kSpanWaves * kBlocksPerItem * kGrBlockStride >= kRouteWaveMaxRows * kRouteLaneMaxExperts,
+                "the route workgroup's logits fit the decode buffers");
   __shared__ GrTables tab;
   __shared__ GrTables4 tab4;
   __shared__ __attribute__((aligned(16))) uint32_t outb[kSpanWaves][kBlocksPerItem * kGrBlockStride];
   __shared__ int32_t eids[kSpanLdsSlots];
-  const int total = wk.first[wk.num_jobs];
+  __shared__ int32_t weids[kSpanWaves][kRouteLaneMaxExperts];  // each wavefront's expert list (route in launch)
   const int tid = threadIdx.x;
-  const int wave = tid / kWave;
+  // with a route in the launch, workgroup 0 builds it (dispatched first, so its latency overlaps the decode)
+  // and the decode and reduce workgroups follow
+  const int bid = static_cast<int>(blockIdx.x) - (rt.wg >= 0 ? 1 : 0);
+  if (bid < 0 || bid >= wk.decode_wgs) {
+    if (bid < 0) {  // the route (its logits staged in the decode buffers' LDS)
+      float* lg = reinterpret_cast<float*>(&outb[0][0]);
+      if (tid < kWave) {
+        if (rt.k_variant == 2) route_wave_body<2>(rt.ra, lg, tid);
+        else if (rt.k_variant == 8) route_wave_body<8>(rt.ra, lg, tid);
+        else route_wave_body<kRouteMaxTopK>(rt.ra, lg, tid);
+      }
+      return;
+    }
+    const int rb = bid - wk.decode_wgs;
+    const int q = rb / red.blocks_per_proj;
+    backbone_reduce_at(red.bb, static_cast<int64_t>(rb % red.blocks_per_proj) * kSpanThreads + threadIdx.x, q);
+    return;
+  }
+  const int total = wk.first[wk.num_jobs];
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform: what it selects stays scalar
   const int lane = tid % kWave;
   const int g = lane / S;
   const int j = lane % S;
   const int stride = wk.decode_wgs * kSpanWaves;
-  int w = static_cast<int>(blockIdx.x) * kSpanWaves + wave;
+  int w = bid * kSpanWaves + wave;
   GrItem<S> cur;
-  gr_item_header<S>(jobs, wk, expert_ids, expert_ids, w, g, cur);  // in flight during the copies below
-  const int nl = wk.num_slots < kSpanLdsSlots ? wk.num_slots : kSpanLdsSlots;
-  for (int i = tid; i < nl; i += kSpanThreads) eids[i] = expert_ids[i];
-  gr_tables_to_lds(&tab);
-  gr_tables4_to_lds(&tab4);
-  gr_span_words<S>(cur.sp, j);
-  __syncthreads();
+  const int32_t* my_eids = eids;
+  if (rt.wg >= 0) {
+    // Each wavefront derives the slots' experts from the logits itself (the route workgroup writes expert_ids
+    // meanwhile): the logits staged in its own decode buffer (one coalesced read; the host bounds tokens x
+    // experts by that buffer), the router's selection on them, the list in its own LDS words.  Every slot of a
+    // decode route is listed (num_slots <= kRouteLaneMaxExperts), so expert_ids is never read.  Its first
+    // header is then in flight during the table copy, as without a route.
+    expert_ids = reinterpret_cast<const int32_t*>(rt.ra.logits);  // any readable word, for invalid headers
+    float* wl = reinterpret_cast<float*>(outb[wave]);
+    const int nlog = rt.ra.tokens * rt.ra.num_experts;
+    for (int i = lane; i < nlog; i += kWave) wl[i] = rt.ra.logits[i];
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    if (rt.k_variant == 2) {
+      route_active_experts<2>(wl, rt.ra.tokens, rt.ra.num_experts, rt.ra.top_k, lane, weids[wave], wk.num_slots);
+    } else if (rt.k_variant == 8) {
+      route_active_experts<8>(wl, rt.ra.tokens, rt.ra.num_experts, rt.ra.top_k, lane, weids[wave], wk.num_slots);
+    } else {
+      route_active_experts<kRouteMaxTopK>(wl, rt.ra.tokens, rt.ra.num_experts, rt.ra.top_k, lane, weids[wave],
+                                          wk.num_slots);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    my_eids = weids[wave];
+    gr_item_header<S>(jobs, wk, my_eids, expert_ids, w, g, cur);  // in flight during the copies below
+    gr_tables_to_lds(&tab);
+    gr_tables4_to_lds(&tab4);
+    gr_span_words<S>(cur.sp, j);
+    __syncthreads();
+  } else {
+    gr_item_header<S>(jobs, wk, expert_ids, expert_ids, w, g, cur);  // in flight during the copies below
+    const int nl = wk.num_slots < kSpanLdsSlots ? wk.num_slots : kSpanLdsSlots;
+    for (int i = tid; i < nl; i += kSpanThreads) eids[i] = expert_ids[i];
+    gr_tables_to_lds(&tab);
+    gr_tables4_to_lds(&tab4);
+    gr_span_words<S>(cur.sp, j);
+    __syncthreads();
+  }
   uint32_t* ob = outb[wave];
   for (; w < total; w += stride) {
     uint4* z = reinterpret_cast<uint4*>(ob);
@@ -129,7 +185,7 @@ __global__ __launch_bounds__(kSpanThreads) __attribute__((amdgpu_waves_per_eu(5)
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
     GrItem<S> nx;
-    gr_item_header<S>(jobs, wk, eids, expert_ids, w + stride, g, nx);
+    gr_item_header<S>(jobs, wk, my_eids, expert_ids, w + stride, g, nx);
     gr_decode_block_group<S>(cur.sp, &tab, ob + g * kGrBlockStride + kGrPadFront, j, &tab4);
     gr_span_words<S>(nx.sp, j);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -183,9 +239,11 @@ int make_gr_job(GrJob* job, int32_t* out, const int32_t* words, const int32_t* o
   return TRIS_OK;
 }
 
-// reduce: a backbone launch's deferred slice reduction to run in the same launch (or null).
+// reduce: a backbone launch's deferred slice reduction to run in the same launch (or null); route: the decode
+// route to build in the same launch (or null: expert_ids holds it already).
 int launch_gr_jobs(const GrJobs& jobs, int num_jobs, const int32_t* expert_ids, int num_slots, void* stream,
-                   const char* who, const BackboneArgs* reduce = nullptr, int reduce_nproj = 0) {
+                   const char* who, const BackboneArgs* reduce = nullptr, int reduce_nproj = 0,
+                   const GrRoute* route = nullptr) {
   int max_nblk = 0;
   int64_t total = 0;
   for (int q = 0; q < num_jobs; ++q) {
@@ -193,14 +251,21 @@ int launch_gr_jobs(const GrJobs& jobs, int num_jobs, const int32_t* expert_ids, 
     total += static_cast<int64_t>(jobs.job[q].nblk) * num_slots;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
+  TRIS_REQUIRE(route == nullptr || (num_slots <= kRouteLaneMaxExperts && max_nblk > 0),
+               "%s: a route in the predecode launch needs blocks to decode and at most %d slots", who,
+               kRouteLaneMaxExperts);
   if (num_slots == 0 || max_nblk == 0) {
     return reduce != nullptr ? launch_backbone_reduce(*reduce, reduce_nproj, s, who) : TRIS_OK;
   }
-  TRIS_REQUIRE(expert_ids != nullptr, "%s: null expert ids", who);
+  TRIS_REQUIRE(route != nullptr || expert_ids != nullptr, "%s: null expert ids", who);
   TRIS_REQUIRE(num_slots <= 65535, "%s: too many experts (%d)", who, num_slots);
   // lanes per block: more lanes shorten each block's walk, fewer spread the per-workgroup table copy
   // over more blocks
-  const int S = total > 8192 ? 16 : 32;
+  // with a route in the launch each wavefront stages the logits in its decode buffer (kWave / S blocks)
+  const int64_t route_floats = route != nullptr ? static_cast<int64_t>(route->ra.tokens) * route->ra.num_experts : 0;
+  const int S = (total > 8192 || route_floats > (kWave / 32) * kGrBlockStride) ? 16 : 32;
+  TRIS_REQUIRE(route_floats <= (kWave / 16) * kGrBlockStride, "%s: %lld router logits exceed a wavefront's buffer",
+               who, static_cast<long long>(route_floats));
   const int per_item = kWave / S;
   GrWork wk{};
   wk.num_jobs = num_jobs;
@@ -227,12 +292,19 @@ int launch_gr_jobs(const GrJobs& jobs, int num_jobs, const int32_t* expert_ids, 
     reduce_wgs = per_proj * reduce_nproj;
   }
   red.blocks_per_proj = red.blocks_per_proj > 0 ? red.blocks_per_proj : 1;
-  TRIS_REQUIRE(grid + reduce_wgs < (1LL << 31), "%s: too many workgroups", who);
-  const dim3 g3(static_cast<unsigned>(grid + reduce_wgs));
+  GrRoute rt{};
+  rt.wg = -1;
+  if (route != nullptr) {
+    rt = *route;
+    rt.wg = 0;
+  }
+  const int64_t all = grid + reduce_wgs + (route != nullptr ? 1 : 0);
+  TRIS_REQUIRE(all < (1LL << 31), "%s: too many workgroups", who);
+  const dim3 g3(static_cast<unsigned>(all));
   if (S == 16) {
-    hipLaunchKernelGGL((gr_decode_span_kernel<16>), g3, dim3(kSpanThreads), 0, s, jobs, wk, expert_ids, red);
+    hipLaunchKernelGGL((gr_decode_span_kernel<16>), g3, dim3(kSpanThreads), 0, s, jobs, wk, expert_ids, red, rt);
   } else {
-    hipLaunchKernelGGL((gr_decode_span_kernel<32>), g3, dim3(kSpanThreads), 0, s, jobs, wk, expert_ids, red);
+    hipLaunchKernelGGL((gr_decode_span_kernel<32>), g3, dim3(kSpanThreads), 0, s, jobs, wk, expert_ids, red, rt);
   }
   return check_launch(who);
 }
@@ -311,4 +383,51 @@ extern "C" int tris_gr_decode_dense(const int32_t* q_gmap_gr_words, const int32_
                        words_stride, packed_rows, outfeatures, true, who);
   if (rc) return rc;
   return launch_gr_jobs(jobs, 1, expert_ids, num, stream, who);
+}
+
+extern "C" int tris_route_predecode_multi_reduce(const float* router_logits, int32_t num_tokens, int32_t num_experts,
+                                                 int32_t top_k, int32_t renormalize, int32_t m_tile,
+                                                 uint16_t* routing_weights_f16, float* routing_weights_f32,
+                                                 int64_t* selected_experts, int64_t* perm,
+                                                 int64_t* grouped_token_indices, int64_t* grouped_slots,
+                                                 int32_t* grouped_expert_ids, int32_t* expert_ids,
+                                                 int32_t* segment_offsets, int32_t* problem_offsets, int32_t* counts,
+                                                 int32_t* inverse_perm, const tris_gr_predecode_job* jobs,
+                                                 int32_t num_jobs, int32_t num_slots, const tris_backbone_pair_job* bb,
+                                                 void* stream) {
+  const char* who = "tris_route_predecode_multi_reduce";
+  GrRoute route{};
+  int rc = route_prepare(router_logits, num_tokens, num_experts, top_k, renormalize, m_tile, routing_weights_f16,
+                         routing_weights_f32, selected_experts, perm, grouped_token_indices, grouped_slots,
+                         grouped_expert_ids, expert_ids, segment_offsets, problem_offsets, counts, inverse_perm,
+                         &route.ra, who);
+  if (rc) return rc;
+  TRIS_REQUIRE(num_tokens > 0 && static_cast<int64_t>(num_tokens) * top_k <= kRouteWaveMaxRows &&
+                   num_experts <= kRouteLaneMaxExperts,
+               "%s: the one-wavefront route takes at most %d routed rows and %d experts", who, kRouteWaveMaxRows,
+               kRouteLaneMaxExperts);
+  const int rows = num_tokens * top_k;
+  TRIS_REQUIRE(num_slots == (num_experts < rows ? num_experts : rows),
+               "%s: num_slots must be min(num_experts, tokens * top_k) = %d", who, num_experts < rows ? num_experts : rows);
+  route.k_variant = top_k <= 2 ? 2 : (top_k <= 8 ? 8 : kRouteMaxTopK);
+  TRIS_REQUIRE(num_jobs > 0 && num_jobs <= TRIS_MAX_PREDECODE_JOBS && jobs != nullptr, "%s: %d jobs (1 to %d)", who,
+               num_jobs, TRIS_MAX_PREDECODE_JOBS);
+  GrJobs g{};
+  for (int q = 0; q < num_jobs; ++q) {
+    const tris_gr_predecode_job& j = jobs[q];
+    rc = make_gr_job(&g.job[q], j.decoded, j.q_gmap_gr_words, j.q_gmap_gr_offsets, j.q_gmap_gr_meta, j.num_experts,
+                     j.words_stride, j.packed_rows, j.outfeatures, false, who);
+    if (rc) return rc;
+    TRIS_REQUIRE(g.job[q].nblk > 0, "%s: job %d has no blocks", who, q);
+  }
+  if (bb == nullptr || bb->tokens == 0 || bb->rank == 0) {
+    return launch_gr_jobs(g, num_jobs, nullptr, num_slots, stream, who, nullptr, 0, &route);
+  }
+  BackboneArgs ba;
+  BackbonePlan pl;
+  rc = backbone_prepare(bb->x, bb->tokens, bb->in_features, nullptr, bb->sv_a, bb->sv_b, bb->rank, bb->in_scale_a,
+                        bb->in_scale_b, bb->out_a, bb->out_b, bb->workspace, bb->workspace_bytes, &ba, &pl, who);
+  if (rc) return rc;
+  if (pl.slices == 1) return launch_gr_jobs(g, num_jobs, nullptr, num_slots, stream, who, nullptr, 0, &route);
+  return launch_gr_jobs(g, num_jobs, nullptr, num_slots, stream, who, &ba, bb->sv_b != nullptr ? 2 : 1, &route);
 }

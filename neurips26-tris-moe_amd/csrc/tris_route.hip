@@ -15,6 +15,7 @@
 // and top-k (modeling_mixtral.py:548-555) and all of the above in one
 // workgroup and one launch.
 #include "tris_backbone.h"
+#include "tris_route.h"
 
 namespace tris {
 
@@ -159,25 +160,6 @@ __global__ __launch_bounds__(kScatterThreads) void route_scatter_kernel(
 
 constexpr int kRouteSmallMaxRows = 2048;    // tokens * top_k
 constexpr int kRouteSmallMaxExperts = 1024;
-constexpr int kRouteMaxTopK = 16;
-
-// The fused router's arguments (tris_route_topk_grouped's outputs, see the header).
-struct RouteArgs {
-  const float* logits;
-  int tokens, num_experts, top_k, renormalize, m_tile;
-  uint16_t* weights16;
-  float* weights32;
-  int64_t* selected;
-  int64_t* perm;
-  int64_t* token_idx;
-  int64_t* slots;
-  int32_t* grouped_expert_ids;
-  int32_t* expert_ids;
-  int32_t* segment_offsets;
-  int32_t* problem_offsets;
-  int32_t* counts;
-  int32_t* inverse_perm;
-};
 
 // LDS of the one-workgroup router.
 struct RouteSmem {
@@ -187,44 +169,6 @@ struct RouteSmem {
   unsigned long long tok_bits[kRouteSmallMaxExperts];  // the chunk's tokens that picked expert e
   int wave_tot[3][kRouteThreads / kWave];
 };
-
-// Softmax of one token's logits (fp32, max-subtracted, summed in expert order) and its top-k by
-// probability with ties to the lower expert id (a stable descending sort, as the oracle's argsort):
-// bp[j] / be[j] for j < top_k, most probable first.
-template <int K>
-__device__ __forceinline__ void route_token_topk(const float* __restrict__ row, int num_experts, int top_k,
-                                                 float bp[K], int be[K]) {
-  float m = row[0];
-  for (int e = 1; e < num_experts; ++e) m = fmaxf(m, row[e]);
-  float sum = 0.0f;
-  for (int e = 0; e < num_experts; ++e) sum += expf(row[e] - m);
-#pragma unroll
-  for (int j = 0; j < K; ++j) {
-    bp[j] = -1.0f;
-    be[j] = -1;
-  }
-  for (int e = 0; e < num_experts; ++e) {
-    const float pe = expf(row[e] - m) / sum;
-    // insert after every kept entry with probability >= pe (earlier experts win ties)
-    if (pe > bp[top_k - 1] || be[top_k - 1] < 0) {
-      float cp = pe;
-      int ce = e;
-      bool shifting = false;  // once placed, every later entry moves down one
-#pragma unroll
-      for (int j = 0; j < K; ++j) {
-        if (j < top_k && (shifting || be[j] < 0 || cp > bp[j])) {
-          const float tp = bp[j];
-          const int te = be[j];
-          bp[j] = cp;
-          be[j] = ce;
-          cp = tp;
-          ce = te;
-          shifting = true;
-        }
-      }
-    }
-  }
-}
 
 // One token's softmax and top-k by a whole wavefront (wave-uniform call, every lane active): the same picks,
 // in the same order, as route_token_topk.  Lane l holds experts l + 64 q (q < P) in registers; the max and
@@ -302,146 +246,6 @@ __device__ __forceinline__ void route_token_wave(float (&pv)[P], int num_experts
   }
   pick_e = my_e;
   pick_w = renormalize ? my_p / denom : my_p;
-}
-
-// The routing weight of pick j: renormalised over the k picks (summed in pick order) or not.
-template <int K>
-__device__ __forceinline__ float route_pick_weight(const float bp[K], int top_k, int renormalize, int j) {
-  float denom = 0.0f;
-#pragma unroll
-  for (int q = 0; q < K; ++q) {
-    if (q < top_k) denom += bp[q];
-  }
-  return renormalize ? bp[j] / denom : bp[j];
-}
-
-constexpr int kRouteWaveMaxRows = 64;     // routed rows of the one-wavefront router
-constexpr int kRouteLaneMaxExperts = 8;   // its experts: a lane routes a token alone
-
-// One wavefront, no barriers, for at most 64 routed rows and 8 experts: lane t < tokens takes token t's
-// softmax and top-k (a short serial chain over few experts); lane i < tokens * top_k then holds routed
-// entry i (expert sel_i); lane e <
-// num_experts counts its expert by ballots, and prefix sums over lanes give the compacted active
-// experts and their segment / problem offsets; entry i's place in its segment is the number of
-// earlier entries of its expert.  The same outputs as route_topk_small_kernel.
-// Run by the first wavefront of a workgroup (lane = thread index < 64); lg: LDS for the logits,
-// kRouteWaveMaxRows * kRouteLaneMaxExperts floats.
-template <int K>
-__device__ __forceinline__ void route_wave_body(const RouteArgs& ra, float* lg, int lane) {
-  const float* __restrict__ logits = ra.logits;
-  const int tokens = ra.tokens, num_experts = ra.num_experts, top_k = ra.top_k, renormalize = ra.renormalize;
-  const int m_tile = ra.m_tile;
-  uint16_t* __restrict__ weights16 = ra.weights16;
-  float* __restrict__ weights32 = ra.weights32;
-  int64_t* __restrict__ selected = ra.selected;
-  int64_t* __restrict__ perm = ra.perm;
-  int64_t* __restrict__ token_idx = ra.token_idx;
-  int64_t* __restrict__ slots = ra.slots;
-  int32_t* __restrict__ grouped_expert_ids = ra.grouped_expert_ids;
-  int32_t* __restrict__ expert_ids = ra.expert_ids;
-  int32_t* __restrict__ segment_offsets = ra.segment_offsets;
-  int32_t* __restrict__ problem_offsets = ra.problem_offsets;
-  int32_t* __restrict__ counts = ra.counts;
-  int32_t* __restrict__ inverse_perm = ra.inverse_perm;
-
-  const int total = tokens * top_k;
-  // every load in flight at once (coalesced), then each token reads its row from LDS
-  const int nlog = tokens * num_experts;
-  for (int u0 = 0; u0 < nlog; u0 += 8 * kWave) {  // 8 loads per lane in flight per round
-    float v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int idx = u0 + u * kWave + lane;
-      v[u] = logits[idx < nlog ? idx : 0];
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int idx = u0 + u * kWave + lane;
-      if (idx < nlog) lg[idx] = v[u];
-    }
-  }
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  float bp[K];
-  int be[K];
-#pragma unroll
-  for (int j = 0; j < K; ++j) {
-    bp[j] = -1.0f;
-    be[j] = -1;
-  }
-  if (lane < tokens) {
-    route_token_topk<K>(lg + lane * num_experts, num_experts, top_k, bp, be);
-#pragma unroll
-    for (int j = 0; j < K; ++j) {
-      if (j < top_k) {
-        const float w = route_pick_weight<K>(bp, top_k, renormalize, j);
-        const int i = lane * top_k + j;
-        if (selected != nullptr) selected[i] = be[j];
-        weights16[i] = f2h_bits(w);
-        if (weights32 != nullptr) weights32[i] = w;
-      }
-    }
-  }
-  // entry i = t * top_k + j lives in lane t's be[j]
-  int sel_i = -1;
-  {
-    const int t = lane / top_k;
-    const int jj = lane - t * top_k;
-#pragma unroll
-    for (int j = 0; j < K; ++j) {
-      const int v = __shfl(be[j], t < kWave ? t : 0);
-      if (j < top_k && j == jj && lane < total) sel_i = v;
-    }
-  }
-  // per-expert counts (lane e) and each entry's earlier entries of its expert
-  int cnt = 0, before = 0;
-  const uint64_t lower = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
-  for (int e = 0; e < num_experts; ++e) {
-    const uint64_t mask = __ballot(sel_i == e);
-    if (lane == e) cnt = __popcll(mask);
-    if (sel_i == e) before = __popcll(mask & lower);
-  }
-  const bool act = lane < num_experts && cnt > 0;
-  const int tiles = act ? (cnt + m_tile - 1) / m_tile : 0;
-  const uint64_t amask = __ballot(act);
-  const int a = __popcll(amask & lower);  // index among active experts
-  int rows_incl = cnt, tiles_incl = tiles;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int vr = __shfl_up(rows_incl, d);
-    const int vt = __shfl_up(tiles_incl, d);
-    if (lane >= d) {
-      rows_incl += vr;
-      tiles_incl += vt;
-    }
-  }
-  const int num_active = __popcll(amask);
-  const int rows_total = __shfl(rows_incl, kWave - 1);
-  const int tiles_total = __shfl(tiles_incl, kWave - 1);
-  const int seg_start = rows_incl - cnt;  // first row of lane e's segment
-  if (act) {
-    expert_ids[a] = lane;
-    segment_offsets[a] = seg_start;
-    problem_offsets[a] = tiles_incl - tiles;
-  }
-  for (int j = num_active + lane; j < num_experts; j += kWave) expert_ids[j] = -1;
-  for (int j = num_active + lane; j <= num_experts; j += kWave) {
-    segment_offsets[j] = rows_total;
-    problem_offsets[j] = tiles_total;
-  }
-  if (lane == 0) {
-    counts[0] = num_active;
-    counts[1] = tiles_total;
-  }
-  const int seg_of = __shfl(seg_start, sel_i >= 0 ? sel_i : 0);
-  if (lane < total) {
-    const int dst = seg_of + before;
-    perm[dst] = lane;
-    token_idx[dst] = lane / top_k;
-    slots[dst] = lane % top_k;
-    grouped_expert_ids[dst] = sel_i;
-    if (inverse_perm != nullptr) inverse_perm[lane] = dst;
-  }
 }
 
 // One workgroup, one launch: per token softmax and top-k (route_token_wave, one wavefront per token: P
@@ -819,19 +623,17 @@ __device__ __forceinline__ float rl_dt(uint32_t w, int half) {
   return kBf16 ? __uint_as_float(b << 16) : h2f(static_cast<uint16_t>(b));
 }
 
+// Workgroup-part body of router_linear_small_kernel: item (t, eg) by kRlsThreads threads (tid < kRlsThreads),
+// with its wavefront sums in part.  It passes exactly one __syncthreads (also when !active), so several items
+// can share one larger workgroup.
 template <bool kBf16>
-__global__ __launch_bounds__(kRlsThreads) void router_linear_small_kernel(const uint16_t* __restrict__ x,
-                                                                          const uint16_t* __restrict__ w,
-                                                                          int hidden, int num_experts,
-                                                                          uint16_t* __restrict__ logits_out,
-                                                                          float* __restrict__ logits_f32,
-                                                                          uint16_t* __restrict__ x16) {
-  __shared__ float part[kRlsThreads / kWave][kRlsExperts];
-  const int tid = static_cast<int>(threadIdx.x);
-  const int t = static_cast<int>(blockIdx.x);
-  const int e0 = static_cast<int>(blockIdx.y) * kRlsExperts;
-  const int runs = hidden / 8;
-  const uint16_t* xr = x + static_cast<int64_t>(t) * hidden;
+__device__ __forceinline__ void router_linear_item(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                   int hidden, int num_experts, int t, int eg, bool active, int tid,
+                                                   float (*part)[kRlsExperts], uint16_t* __restrict__ logits_out,
+                                                   float* __restrict__ logits_f32, uint16_t* __restrict__ x16) {
+  const int e0 = eg * kRlsExperts;
+  const int runs = active ? hidden / 8 : 0;
+  const uint16_t* xr = x + static_cast<int64_t>(active ? t : 0) * hidden;
   uint4 xv[kRlsMaxRuns], wv[kRlsMaxRuns][kRlsExperts];
 #pragma unroll
   for (int m = 0; m < kRlsMaxRuns; ++m) {
@@ -845,7 +647,7 @@ __global__ __launch_bounds__(kRlsThreads) void router_linear_small_kernel(const 
       wv[m][q] = rl_load16(w + static_cast<int64_t>(e < num_experts ? e : 0) * hidden + (cv ? c : 0) * 8, v);
     }
   }
-  if (kBf16 && x16 != nullptr && blockIdx.y == 0) {
+  if (kBf16 && x16 != nullptr && eg == 0) {
 #pragma unroll
     for (int m = 0; m < kRlsMaxRuns; ++m) {
       const int c = tid + m * kRlsThreads;
@@ -876,7 +678,7 @@ __global__ __launch_bounds__(kRlsThreads) void router_linear_small_kernel(const 
     if ((tid & (kWave - 1)) == 0) part[wave][q] = v;
   }
   __syncthreads();
-  if (tid < kRlsExperts && e0 + tid < num_experts) {
+  if (active && tid < kRlsExperts && e0 + tid < num_experts) {
     const float dot = ((part[0][tid] + part[1][tid]) + part[2][tid]) + part[3][tid];
     uint16_t bits;
     float val;
@@ -897,6 +699,52 @@ __global__ __launch_bounds__(kRlsThreads) void router_linear_small_kernel(const 
     logits_out[o] = bits;
     logits_f32[o] = val;
   }
+}
+
+template <bool kBf16>
+__global__ __launch_bounds__(kRlsThreads) void router_linear_small_kernel(const uint16_t* __restrict__ x,
+                                                                          const uint16_t* __restrict__ w,
+                                                                          int hidden, int num_experts,
+                                                                          uint16_t* __restrict__ logits_out,
+                                                                          float* __restrict__ logits_f32,
+                                                                          uint16_t* __restrict__ x16) {
+  __shared__ float part[kRlsThreads / kWave][kRlsExperts];
+  router_linear_item<kBf16>(x, w, hidden, num_experts, static_cast<int>(blockIdx.x), static_cast<int>(blockIdx.y),
+                            true, static_cast<int>(threadIdx.x), part, logits_out, logits_f32, x16);
+}
+
+// The block's first launch at decode: the router Linear (router_linear_item) and the gate/up backbone
+// projections of the same tokens (backbone_block), which do not depend on each other, one item or block per
+// workgroup of kBbThreads threads (a 1024-thread workgroup would cap the router body's registers below what
+// its loads in flight hold).  The backbone reads the bf16 activations and converts them on load (the bits x16
+// holds), since x16 is written in this same launch.  Workgroups [0, rl_items) take the router items (t, eg),
+// t-major; the rest the backbone's grid.
+template <int TT>
+union RouterBackboneSmem {
+  float part[kRlsThreads / kWave][kRlsExperts];
+  f32x4 red[kBbWaves - 1][TT][kWave];
+};
+
+template <int TT, int B>
+__global__ __launch_bounds__(kBbThreads) void router_backbone_kernel(const uint16_t* __restrict__ x,
+                                                                    const uint16_t* __restrict__ w, int hidden,
+                                                                    int num_experts, int rl_items,
+                                                                    uint16_t* __restrict__ logits_out,
+                                                                    float* __restrict__ logits_f32,
+                                                                    uint16_t* __restrict__ x16, BackboneArgs ba,
+                                                                    int gx, int gy) {
+  static_assert(kRlsThreads == kBbThreads, "one router item or one backbone block per workgroup");
+  __shared__ RouterBackboneSmem<TT> sm;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int b = static_cast<int>(blockIdx.x);
+  if (b < rl_items) {
+    const int groups = ceil_div(num_experts, kRlsExperts);
+    router_linear_item<true>(x, w, hidden, num_experts, b / groups, b % groups, true, tid, sm.part, logits_out,
+                             logits_f32, x16);
+    return;
+  }
+  const int v = b - rl_items;
+  backbone_block<TT, B, true>(ba, true, v % gx, (v / gx) % gy, v / (gx * gy), tid, sm.red);
 }
 
 }  // namespace tris
@@ -935,7 +783,7 @@ extern "C" int tris_build_grouped_route(const int64_t* selected_experts, int32_t
 }
 
 // Validates tris_route_topk_grouped's arguments and fills ra.
-static int route_prepare(const float* router_logits, int32_t num_tokens, int32_t num_experts, int32_t top_k,
+int tris::route_prepare(const float* router_logits, int32_t num_tokens, int32_t num_experts, int32_t top_k,
                          int32_t renormalize, int32_t m_tile, uint16_t* routing_weights_f16, float* routing_weights_f32,
                          int64_t* selected_experts, int64_t* perm, int64_t* grouped_token_indices,
                          int64_t* grouped_slots, int32_t* grouped_expert_ids, int32_t* expert_ids,
@@ -1136,5 +984,44 @@ extern "C" int tris_router_linear(const uint16_t* x, const uint16_t* router_weig
     hipLaunchKernelGGL((router_linear_kernel<false>), grid, dim3(kRlThreads), 0, s, x, router_weight, tokens, hidden,
                        num_experts, kper, router_logits, logits_f32, x16);
   }
+  return check_launch(who);
+}
+
+extern "C" int tris_router_backbone(const uint16_t* x, const uint16_t* router_weight, int32_t tokens, int32_t hidden,
+                                    int32_t num_experts, uint16_t* router_logits, float* logits_f32, uint16_t* x16,
+                                    const tris_backbone_pair_job* bb, void* stream) {
+  const char* who = "tris_router_backbone";
+  TRIS_REQUIRE(tokens > 0 && hidden > 0 && num_experts > 0, "%s: bad shape", who);
+  TRIS_REQUIRE(x && router_weight && router_logits && logits_f32 && x16 && bb, "%s: null pointer", who);
+  TRIS_REQUIRE(hidden % 8 == 0 && hidden <= kRlsMaxRuns * kRlsThreads * 8,
+               "%s: hidden %d must be a multiple of 8 and at most %d", who, hidden, kRlsMaxRuns * kRlsThreads * 8);
+  const auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  TRIS_REQUIRE(a16(x) && a16(router_weight) && a16(x16), "%s: x, the weight and x16 must be 16-byte aligned", who);
+  TRIS_REQUIRE(bb->x == x && bb->tokens == tokens && bb->in_features == hidden,
+               "%s: the backbone job must project the router's input (job x == x, same tokens and columns)", who);
+  TRIS_REQUIRE(tokens <= kRbMaxTokens, "%s: %d tokens exceed the merged launch's %d", who, tokens, kRbMaxTokens);
+  BackboneArgs ba;
+  BackbonePlan pl;
+  int rc = backbone_prepare(bb->x, bb->tokens, bb->in_features, nullptr, bb->sv_a, bb->sv_b, bb->rank, bb->in_scale_a,
+                            bb->in_scale_b, bb->out_a, bb->out_b, bb->workspace, bb->workspace_bytes, &ba, &pl, who);
+  if (rc) return rc;
+  const int nproj = bb->sv_b != nullptr ? 2 : 1;
+  const int gx = pl.row_tiles;
+  const int gy = pl.token_groups * pl.slices;
+  const int64_t blocks = static_cast<int64_t>(gx) * gy * nproj;
+  TRIS_REQUIRE(blocks < (int64_t{1} << 28), "%s: backbone grid too large", who);
+  const int rl_items = tokens * ceil_div(num_experts, kRlsExperts);
+  const dim3 grid(static_cast<unsigned>(rl_items + blocks));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define TRIS_RB_LAUNCH(TT, B)                                                                                      \
+  hipLaunchKernelGGL((router_backbone_kernel<TT, B>), grid, dim3(kBbThreads), 0, s, x, router_weight, hidden,      \
+                     num_experts, rl_items, router_logits, logits_f32, x16, ba, gx, gy)
+  switch (pl.tt) {
+    case 1: TRIS_RB_LAUNCH(1, 8); break;
+    case 2: TRIS_RB_LAUNCH(2, 4); break;
+    case 3: TRIS_RB_LAUNCH(3, 4); break;
+    default: TRIS_RB_LAUNCH(4, 4); break;
+  }
+#undef TRIS_RB_LAUNCH
   return check_launch(who);
 }

@@ -364,6 +364,98 @@ def route_topk_backbone_pair(router_logits: torch.Tensor, top_k: int, renormaliz
     return out, BackbonePending(job, out_a, out_b, (x, sv_a, sv_b, in_scale_a, in_scale_b, ws))
 
 
+ROUTE_WAVE_MAX_ROWS = 64     # tokens * top_k of the one-wavefront route (tris_route_predecode_multi_reduce)
+ROUTE_WAVE_MAX_EXPERTS = 8
+ROUTER_BACKBONE_MAX_HIDDEN = 8192  # hidden of tris_router_backbone
+
+
+def router_backbone_ok(x: torch.Tensor, weight: torch.Tensor, sv_a, sv_b, in_scale_a=None, in_scale_b=None) -> bool:
+    """True when router_backbone_pair can run: bf16 activations and router weight (router_linear_ok), at most
+    ROUTE_BACKBONE_MAX_TOKENS tokens and ROUTER_BACKBONE_MAX_HIDDEN columns, and fp16 backbones of one shape over
+    x's columns (16-byte aligned, optional fp16 input scales)."""
+    if not router_linear_ok(x, weight) or x.dtype != torch.bfloat16:
+        return False
+    if int(x.size(0)) > ROUTE_BACKBONE_MAX_TOKENS or int(x.size(1)) > ROUTER_BACKBONE_MAX_HIDDEN:
+        return False
+    return route_topk_backbone_ok(x.view(torch.float16), sv_a, sv_b, in_scale_a, in_scale_b)
+
+
+def router_backbone_pair(x: torch.Tensor, weight: torch.Tensor, sv_a: torch.Tensor, sv_b: torch.Tensor,
+                         in_scale_a: torch.Tensor | None = None, in_scale_b: torch.Tensor | None = None):
+    """router_linear and the gate/up backbones of the same tokens in one launch (tris_router_backbone, an
+    extension): returns (router_logits bf16 [T, E], the logits as fp32, x16, BackbonePending).  The backbones
+    read x's bf16 values as fp16 (x16's bits); their split-K reduction is left for route_predecode_multi or
+    grouped_block_gr_predecode_multi (backbone=)."""
+    if not router_backbone_ok(x, weight, sv_a, sv_b, in_scale_a, in_scale_b):
+        raise RuntimeError("router_backbone_pair: inputs outside the merged launch's conditions")
+    tokens, hidden, experts, rank = int(x.size(0)), int(x.size(1)), int(weight.size(0)), int(sv_a.size(0))
+    dev = x.device
+    logits = torch.empty((tokens, experts), dtype=torch.bfloat16, device=dev)
+    logits32 = torch.empty((tokens, experts), dtype=torch.float32, device=dev)
+    x16 = torch.empty((tokens, hidden), dtype=torch.float16, device=dev)
+    out_a = torch.empty((tokens, rank), dtype=torch.float16, device=dev)
+    out_b = torch.empty((tokens, rank), dtype=torch.float16, device=dev)
+    lib = _lib.load()
+    nbytes = int(lib.tris_backbone_pair_workspace_bytes(tokens, hidden, rank))
+    # this call's own partial sums, held by the BackbonePending until the reducing launch is enqueued
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
+    job = _lib.TrisBackbonePairJob(_ptr(x), tokens, hidden, _ptr(sv_a), _ptr(sv_b), rank, _ptr(in_scale_a),
+                                   _ptr(in_scale_b), _ptr(out_a), _ptr(out_b), _ptr(ws), int(ws.numel()))
+    _lib.check(lib.tris_router_backbone(_ptr(x), _ptr(weight), tokens, hidden, experts, _ptr(logits), _ptr(logits32),
+                                        _ptr(x16), ctypes.byref(job), _stream(x)), "router_backbone_pair")
+    return logits, logits32, x16, BackbonePending(job, out_a, out_b, (x, weight, sv_a, sv_b, in_scale_a, in_scale_b,
+                                                                      ws, x16))
+
+
+def route_predecode_ok(router_logits: torch.Tensor, top_k: int) -> bool:
+    """The one-wavefront route of route_predecode_multi takes these fp32 [T, E] logits: T * top_k <= 64,
+    E <= 8."""
+    if not isinstance(router_logits, torch.Tensor) or router_logits.dim() != 2:
+        return False
+    t, e = int(router_logits.size(0)), int(router_logits.size(1))
+    return (router_logits.dtype == torch.float32 and 0 < t and 0 < top_k <= e and t * top_k <= ROUTE_WAVE_MAX_ROWS
+            and e <= ROUTE_WAVE_MAX_EXPERTS)
+
+
+def route_predecode_multi(router_logits: torch.Tensor, top_k: int, renormalize: bool, m_tile: int, jobs,
+                          backbone: BackbonePending | None = None) -> dict:
+    """route_topk_grouped and grouped_block_gr_predecode_multi of the same route in one launch
+    (tris_route_predecode_multi_reduce, an extension): jobs as grouped_block_gr_predecode_multi takes them, each
+    buffer [min(E, T * top_k), blocks, 128]; ``backbone``: a BackbonePending reduced in the same launch.
+    Returns the route dict of route_topk_grouped."""
+    if not route_predecode_ok(router_logits, top_k):
+        raise RuntimeError("route_predecode_multi: logits outside the one-wavefront route (T * top_k <= "
+                           f"{ROUTE_WAVE_MAX_ROWS}, E <= {ROUTE_WAVE_MAX_EXPERTS})")
+    if not 0 < len(jobs) <= _lib.MAX_PREDECODE_JOBS:
+        raise RuntimeError(f"route_predecode_multi: 1 to {_lib.MAX_PREDECODE_JOBS} predecode jobs")
+    logits, out = _route_topk_outputs(router_logits, top_k, "route_predecode_multi")
+    t, e = int(logits.size(0)), int(logits.size(1))
+    slots = min(e, t * int(top_k))
+    dev = logits.device
+    arr = (_lib.TrisPredecodeJob * len(jobs))()
+    keep = []
+    for q, (buf, words, offsets, meta, packed_rows, outfeatures) in enumerate(jobs):
+        _check_cuda("decoded_q_gmap_words", buf, torch.int32, None, dev)
+        _check_cuda("q_gmap_gr_words", words, torch.int32, 2, dev)
+        _check_cuda("q_gmap_gr_offsets", offsets, torch.int32, 2, dev)
+        _check_cuda("q_gmap_gr_meta", meta, torch.int32, 2, dev)
+        nblk = _num_gr_blocks(int(packed_rows), int(outfeatures))
+        if buf.numel() != slots * nblk * BLOCK_GR_WORDS_PER_BLOCK:
+            raise RuntimeError("decoded_q_gmap_words must hold [min(E, T * top_k), blocks, 128] words")
+        if int(offsets.size(1)) != nblk + 1 or int(meta.size(1)) != nblk:
+            raise RuntimeError("q_gmap_gr_offsets/meta shape mismatch")
+        if words.numel() == 0:
+            words = torch.zeros((max(int(offsets.size(0)), 1), 1), dtype=torch.int32, device=dev)
+        keep.append(words)
+        arr[q] = _lib.TrisPredecodeJob(_ptr(buf), _ptr(words), _ptr(offsets), _ptr(meta), int(offsets.size(0)),
+                                       int(words.size(1)), int(packed_rows), int(outfeatures))
+    bb = ctypes.byref(backbone.job) if backbone is not None else None
+    _lib.check(_lib.load().tris_route_predecode_multi_reduce(
+        *_route_topk_args(logits, out, top_k, renormalize, m_tile), arr, len(jobs), slots, bb, _stream(logits)),
+        "route_predecode_multi")
+    return out
+
+
 def finish_backbone(pending: BackbonePending):
     """Run a BackbonePending's outstanding reduction alone (when no predecode launch follows); returns
     (out_a, out_b)."""

@@ -311,7 +311,7 @@ NS_DOWN_BESIDE_GEMM = True
 
 
 def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype, shared_expert,
-                            backbone_pending=None):
+                            backbone_pending=None, predecoded=None):
     """Uniform-group payloads without output scale or bias: GR-decode every routed expert's split
     bitmaps once per projection (TriSMoE_cuda.cpp:836-853), then run the predecoded grouped GEMMs
     (TriSMoE_cuda.cpp:855-889, 922-974).  Active experts come first in the padded route, so
@@ -326,7 +326,8 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
 
     backbone_pending: the gate/up backbones of the tokens launched beside the router (ext.BackbonePending);
     their split-K reduction runs in the predecode's launch and the gate/up GEMMs gather their rows through
-    the route's token indices."""
+    the route's token indices.  predecoded: {gate, up, down} buffers already filled for this route (with the
+    backbone's reduction) by the launch that built it (ext.route_predecode_multi)."""
     slots = min(num_experts, R)
     eid = route["expert_ids"][:slots]
     seg = route["segment_offsets"][: slots + 1]
@@ -335,7 +336,10 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     pg, pu, pd = payloads["gate"], payloads["up"], payloads["down"]
     ns = _ns_payloads(payloads)
     dev = x16.device
-    bufs = {name: _predecode_buffer(p, slots, dev) for name, p in (("gate", pg), ("up", pu), ("down", pd))}
+    if predecoded is not None and (backbone_pending is None or any(v is not None for v in ns.values())):
+        raise RuntimeError("predecoded buffers come with the router-launched backbones and no null-space payloads")
+    bufs = predecoded if predecoded is not None else {
+        name: _predecode_buffer(p, slots, dev) for name, p in (("gate", pg), ("up", pu), ("down", pd))}
     main = torch.cuda.current_stream(dev)
     side = _side_stream(dev)
     n_mlp = int(pg["qweight1"].size(2))
@@ -360,7 +364,10 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
                  int(p["qweight1"].size(1)), int(p["qweight1"].size(2))) for name, p in order]
     decoded = bufs
     sc = _in_scales(backbones)
-    if backbone_pending is not None:
+    if predecoded is not None:
+        hid_g, hid_u = backbone_pending.out_a, backbone_pending.out_b
+        gather = route["grouped_token_indices"]
+    elif backbone_pending is not None:
         ext.grouped_block_gr_predecode_multi(pre_jobs, eid, backbone=backbone_pending)
         hid_g, hid_u = backbone_pending.out_a, backbone_pending.out_b
         gather = route["grouped_token_indices"]
@@ -457,6 +464,49 @@ def _decode_fused_moe_forward(x16, w16, route, payloads, backbones, num_experts,
     return _combine(x16, d_out, route, w16, output_dtype, shared_expert)
 
 
+def decode_prologue_ok(x: torch.Tensor, router_weight: torch.Tensor, top_k: int, num_experts: int, payloads: dict,
+                       backbones: dict, expert_path: str = "auto") -> bool:
+    """The block's decode step can start with ext.router_backbone_pair and route in its predecode's launch
+    (ext.route_predecode_multi): bf16 activations and router, the one-wavefront route (tokens * top_k <= 64, at
+    most 8 experts), the predecoded MFMA path with fp16 gate/up backbones, no null-space payloads."""
+    if expert_path == "fused" or x.dim() != 2:
+        return False
+    t = int(x.size(0))
+    if not (0 < t and t * top_k <= ext.ROUTE_WAVE_MAX_ROWS and num_experts <= ext.ROUTE_WAVE_MAX_EXPERTS):
+        return False
+    if not (_predecodable(payloads) and ext.mfma_payload_ok(payloads["gate"]) and ext.mfma_payload_ok(payloads["up"])):
+        return False
+    if any(v is not None for v in _ns_payloads(payloads).values()):
+        return False
+    sc = _in_scales(backbones)
+    return ext.router_backbone_ok(x, router_weight, backbones["gate"], backbones["up"], sc["gate"], sc["up"])
+
+
+def grouped_moe_decode_step(x: torch.Tensor, router_weight: torch.Tensor, top_k: int, renormalize: bool,
+                            payloads: dict, backbones: dict, num_experts: int, output_dtype=torch.bfloat16,
+                            shared_expert=None):
+    """The whole block at decode from its bf16 input (decode_prologue_ok): the router Linear, the fp16 cast and
+    the gate/up backbones in one launch, the route and the predecode (with the backbones' split-K reduction) in
+    the next, then the grouped GEMMs and the combine.  Returns (out [T, H] in output_dtype, router_logits bf16
+    [T, E]).  The same outputs as TrisSparseMoeBlock's other path, bit for bit."""
+    sc = _in_scales(backbones)
+    logits, logits32, x16, pending = ext.router_backbone_pair(x, router_weight, backbones["gate"], backbones["up"],
+                                                              in_scale_a=sc["gate"], in_scale_b=sc["up"])
+    T = int(x.size(0))
+    R = T * top_k
+    shared = _shared_expert_begin(x16, shared_expert, x, output_dtype)
+    slots = min(num_experts, R)
+    dev = x.device
+    order = (("gate", payloads["gate"]), ("up", payloads["up"]), ("down", payloads["down"]))
+    bufs = {name: _predecode_buffer(p, slots, dev) for name, p in order}
+    jobs = [(bufs[name], p["q_gmap_gr_words"], p["q_gmap_gr_offsets"], p["q_gmap_gr_meta"],
+             int(p["qweight1"].size(1)), int(p["qweight1"].size(2))) for name, p in order]
+    route = ext.route_predecode_multi(logits32, top_k, renormalize, GROUPED_SEGMENT_M_TILE, jobs, backbone=pending)
+    out = _predecoded_moe_forward(x16, route["routing_weights_f16"], route, payloads, backbones, num_experts, R,
+                                  output_dtype, shared, backbone_pending=pending, predecoded=bufs)
+    return out, logits
+
+
 class TrisSparseMoeBlock(nn.Module):
     """Grouped-expert sparse MoE block (MixtralSparseMoeBlock / OlmoeSparseMoeBlock / Qwen2MoeSparseMoeBlock
     shape).  The router ``gate`` is an nn.Linear in the model dtype (``router_dtype``, bf16 by default), as the
@@ -513,12 +563,18 @@ class TrisSparseMoeBlock(nn.Module):
 
     def forward(self, hidden_states: torch.Tensor):
         """modeling_mixtral.py:539-608: hidden_states [B, S, H] (bf16 or fp16) -> (out [B, S, H] in the input
-        dtype, router_logits [B*S, E] in the router's dtype).  When the activations and the router share the
-        model dtype, the router Linear and the fp16 cast run as one launch (ext.router_linear); else the
-        Linear is torch's."""
+        dtype, router_logits [B*S, E] in the router's dtype).  At decode (decode_prologue_ok) the block runs as
+        grouped_moe_decode_step; otherwise, when the activations and the router share the model dtype, the router
+        Linear and the fp16 cast run as one launch (ext.router_linear); else the Linear is torch's."""
         batch, seq, hidden = hidden_states.shape
         flat = hidden_states.reshape(-1, hidden)
         weight = self.gate.weight.detach()
+        if decode_prologue_ok(flat, weight, self.top_k, self.num_experts, self.payloads, self.backbones,
+                              self.expert_path):
+            out, router_logits = grouped_moe_decode_step(flat, weight, self.top_k, self.renormalize, self.payloads,
+                                                         self.backbones, self.num_experts, flat.dtype,
+                                                         self._shared(flat.dtype))
+            return out.reshape(batch, seq, hidden), router_logits
         if ext.router_linear_ok(flat, weight):
             router_logits, logits32, x16 = ext.router_linear(flat, weight)
             out = self.forward_routed(flat, logits32, x16=x16)

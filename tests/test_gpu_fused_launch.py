@@ -265,3 +265,86 @@ def test_backbone_swiglu_matches_unfused(tris, cuda, rows, in_f, rank):
     assert_close(got.float().cpu().numpy(), unfused.float().cpu().numpy(), "fused vs unfused")
     again = ext.backbone_swiglu_linear(g, u, sv, in_scale=sc)
     assert torch.equal(got, again)  # slices added in fixed order
+
+
+PROLOGUE_CASES = [
+    # tokens, experts, top_k, renormalize, hidden, rank, input scales
+    (1, 8, 2, True, 4096, 512, False),     # Mixtral decode
+    (16, 8, 2, True, 4096, 512, True),     # with ns_mode 1 input scales
+    (32, 8, 2, True, 2048, 256, False),    # 64 routed rows: the one-wavefront route's limit
+    (5, 6, 3, False, 1024, 128, False),    # fewer experts, three picks, no renormalisation
+    (3, 8, 2, True, 512, 128, False),      # one slice: the backbone writes its outputs in the first launch
+]
+
+
+@pytest.mark.parametrize("case", PROLOGUE_CASES, ids=lambda c: "T{}E{}k{}h{}r{}".format(c[0], c[1], c[2], c[4], c[5]))
+def test_router_backbone_and_route_predecode_match_separate_launches(tris, cuda, case):
+    """tris_router_backbone (the router Linear, the fp16 cast and the gate/up backbones in one launch) and
+    tris_route_predecode_multi_reduce (the route beside the predecode and the backbones' slice reduction) give
+    the bits of the launches they replace: tris_router_linear, tris_backbone_linear_pair on x16,
+    tris_route_topk_grouped and tris_grouped_block_gr_predecode_multi for its expert ids."""
+    t, e, k, renorm, hidden, rank, scales = case
+    note(f"router+backbone, route+predecode T={t} E={e} k={k} h={hidden} r={rank}")
+    ext = tris["ext"]
+    rng = np.random.default_rng(t * 11 + e)
+    x = torch.from_numpy(rng.standard_normal((t, hidden)).astype(np.float32)).to(torch.bfloat16).to(cuda)
+    w = torch.from_numpy((rng.standard_normal((e, hidden)) / np.sqrt(hidden)).astype(np.float32))
+    w = w.to(torch.bfloat16).to(cuda)
+    _, sv_a, sv_b, sa, sb = backbone_inputs(t + 100, t, hidden, rank, scales, cuda)
+    logits, logits32, x16, pending = ext.router_backbone_pair(x, w, sv_a, sv_b, in_scale_a=sa, in_scale_b=sb)
+    want_logits, want32, want_x16 = ext.router_linear(x, w)
+    assert torch.equal(logits.view(torch.int16), want_logits.view(torch.int16))
+    assert torch.equal(logits32, want32)
+    assert torch.equal(x16.view(torch.int16), want_x16.view(torch.int16))
+    # two projections (rank x packed rows) with blocks for every expert
+    projs = [make_projection(tris, 300 + i, e, n, kk) for i, (n, kk) in enumerate([(256, 128), (192, 256)])]
+    pays = [tris["qlinear"].payload_to_device(p, cuda) for p in projs]
+    slots = min(e, t * k)
+    jobs, bufs = [], []
+    for p in pays:
+        pr, n = int(p["qweight1"].size(1)), int(p["qweight1"].size(2))
+        nblk = ((pr + 1) // 2) * ((n + 63) // 64)
+        buf = torch.full((slots, nblk, 128), -7, dtype=torch.int32, device=cuda)
+        bufs.append(buf)
+        jobs.append((buf, p["q_gmap_gr_words"], p["q_gmap_gr_offsets"], p["q_gmap_gr_meta"], pr, n))
+    route = ext.route_predecode_multi(logits32, k, renorm, 4, jobs, backbone=pending)
+    want_route = ext.route_topk_grouped(want32, k, renorm, 4)
+    for key in ROUTE_KEYS:
+        assert torch.equal(route[key], want_route[key]), key
+    ref_bufs = [torch.full_like(b, -7) for b in bufs]
+    ref_jobs = [(rb,) + j[1:] for rb, j in zip(ref_bufs, jobs)]
+    ext.grouped_block_gr_predecode_multi(ref_jobs, want_route["expert_ids"][:slots])
+    for b, rb in zip(bufs, ref_bufs):
+        assert torch.equal(b, rb)
+    want_a, want_b = ext.backbone_linear_pair(want_x16, sv_a, sv_b, in_scale_a=sa, in_scale_b=sb)
+    assert torch.equal(pending.out_a.view(torch.int16), want_a.view(torch.int16))
+    assert torch.equal(pending.out_b.view(torch.int16), want_b.view(torch.int16))
+
+
+@pytest.mark.parametrize("tokens", [1, 4, 16])
+def test_block_decode_step_matches_unfused_block(tris, oracle_mod, cuda, tokens):
+    """TrisSparseMoeBlock.forward at decode (grouped_moe_decode_step: router Linear + backbones, then route +
+    predecode) against the same block with the step's other path (router_linear, then the route with the
+    backbones, then the predecode): the same output and router logits, bit for bit, on the C1 layer."""
+    from tris_moe_amd.configs import C1_MIXTRAL_DECODE as SPEC
+
+    note(f"block decode step T={tokens}")
+    syn, ql, moe = tris["synthetic"], tris["qlinear"], tris["moe"]
+    layer = syn.make_layer(SPEC, 6100 + tokens, tris["ext"].gr_encode)
+    payloads = {p: ql.payload_to_device(layer[p], cuda) for p in ("gate", "up", "down")}
+    backbones = {p: torch.from_numpy(layer["backbones"][p]).to(cuda) for p in ("gate", "up", "down")}
+    rng = np.random.default_rng(tokens)
+    router = torch.from_numpy((rng.standard_normal((SPEC.num_experts, SPEC.hidden)) * 0.015).astype(np.float32))
+    block = moe.TrisSparseMoeBlock(SPEC.hidden, SPEC.num_experts, SPEC.top_k, payloads, backbones,
+                                   router_weight=router.to(cuda))
+    inp = syn.make_inputs(SPEC, tokens, 6200 + tokens, layer["outlier_idx"])
+    h = torch.from_numpy(inp["x"]).to(cuda).to(torch.bfloat16)
+    flat = h.reshape(-1, SPEC.hidden)
+    assert moe.decode_prologue_ok(flat, block.gate.weight.detach(), SPEC.top_k, SPEC.num_experts, payloads,
+                                  backbones)
+    with torch.no_grad():
+        out, logits = block(h.reshape(1, tokens, SPEC.hidden))
+        lg, lg32, x16 = tris["ext"].router_linear(flat, block.gate.weight.detach())
+        want = block.forward_routed(flat, lg32, x16=x16)
+    assert torch.equal(logits.view(torch.int16), lg.view(torch.int16))
+    assert torch.equal(out.reshape(tokens, SPEC.hidden).view(torch.int16), want.view(torch.int16))
