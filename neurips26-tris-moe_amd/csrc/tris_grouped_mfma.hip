@@ -1102,18 +1102,20 @@ void grouped_mfma_kernel(MfmaArgs a) {
 }
 
 // ----------------------------------------------------------------------------------------------------
-// Weight-stationary variant for long segments (prefill).  A work item is (active segment, 64-column output
-// tile): the unit copies the tile's weight words, builds the exact B operands of its column over the whole
-// K (rank <= 512: 16 packed rows, 4 registers each, plus at most two 32-column salient windows) once, and
-// streams the segment's 16-row activation tiles through them: per row tile 16 + 2 MFMAs per wavefront,
-// with the next row tile's loads in flight meanwhile (two activation buffers).  kUnits == 2 runs the
-// gate and up projections of the same item side by side and writes fp16(silu(g) * u).
+// Weight-stationary variant for long segments (prefill).  A work item is (active segment, kSub 64-column
+// output tiles): the unit copies the tiles' weight words, builds the exact B operands of its columns over the
+// whole K (rank <= 512: 16 packed rows, 4 registers each per tile, plus at most two 32-column salient windows)
+// once, and streams the segment's 16-row activation tiles through them: per row tile and output tile 16 + 1
+// or 2 MFMAs per wavefront, with the next row tile's loads in flight meanwhile (two activation buffers).
+// Each A-operand read from LDS feeds kSub MFMAs: one 16 x 16 x 32 MFMA per kilobyte read would need 256 B
+// of LDS reads per clock on a CU (4 SIMDs), twice what the LDS delivers.  kUnits == 2 runs the gate and up
+// projections of the same item side by side and writes fp16(silu(g) * u).
 constexpr int kWsSalWindows = 2;  // salient columns per item <= 64
 constexpr int kWsMinRows = 64;    // mean rows per active segment from which the host picks this kernel
 #ifndef TRIS_WS_SUB
-#define TRIS_WS_SUB 1
+#define TRIS_WS_SUB 2
 #endif
-constexpr int kWsSub = TRIS_WS_SUB;  // output tiles per item
+constexpr int kWsSub = TRIS_WS_SUB;  // output tiles per item (2: one activation read feeds two MFMAs)
 #ifndef TRIS_WS_XSTRIDE
 #define TRIS_WS_XSTRIDE 528
 #endif
@@ -1187,9 +1189,11 @@ __device__ __forceinline__ void ws_x_write(int utid, uint16_t* xs, const WsX& X)
 
 // Work split: item (segment a, kSub output tiles from tile kSub * i) costs t_a + kWsBuildCost row tiles (t_a:
 // the segment's row tiles; building the B operands costs about kWsBuildCost of them).  Items are ordered
-// segment-major and the workgroup of virtual index v takes those whose cost prefix starts in
-// [v * total / W, (v + 1) * total / W): each lane works out the item range of its segment, so no item list
-// exists anywhere.  Virtual indices are XCD-major: the hardware places workgroup w on XCD w % 8, and each
+// segment-major, each item's build first and then its row tiles, and the workgroup of virtual index v takes
+// the row tiles whose cost position lies in [v * total / W, (v + 1) * total / W), building the B operands of
+// every item it touches: an item split between two workgroups is built twice, and every workgroup gets the
+// same cost to within one item's build.  Each lane works out the item and row range of its segment, so no
+// item list exists anywhere.  Virtual indices are XCD-major: the hardware places workgroup w on XCD w % 8, and each
 // XCD gets a contiguous share of the items, so its L2 holds the activations of about one segment instead
 // of every XCD streaming every segment.
 constexpr int kWsBuildCost = 2;
@@ -1206,7 +1210,8 @@ __device__ __forceinline__ int xcd_major_index(int w, int W) {
 // from LDS feeds kSub MFMAs (B operands: 16 packed rows x kSub x 4 registers).  Activations are staged in
 // natural column order (a plain copy) and the B operands built for it (mf_row_b_nat).
 template <int kUnits, int kSub>
-__global__ __launch_bounds__(kUnits * kMfThreads) void grouped_mfma_ws_kernel(MfmaArgs a) {
+__global__ __launch_bounds__(kUnits * kMfThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) void grouped_mfma_ws_kernel(
+    MfmaArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char mf_lds[];
   __shared__ __attribute__((aligned(16))) uint32_t ws_tb[kUnits][kSub][kMfTbWords];
   const int unit = kUnits == 2 ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kMfThreads) : 0;
@@ -1241,12 +1246,16 @@ __global__ __launch_bounds__(kUnits * kMfThreads) void grouped_mfma_ws_kernel(Mf
   const int64_t lo_w = vw * total / W;
   const int64_t hi_w = (vw + 1) * total / W;
   const int64_t base = static_cast<int64_t>(nit) * (incl - u);
-  int it_lo = 0, it_hi = 0;
+  // this workgroup's cost range relative to the segment's first item, clamped to the segment's cost; item it
+  // covers [it * u, (it + 1) * u), its row tile r sits at it * u + kWsBuildCost + r
+  int d0 = 0, d1 = 0, it_lo = 0, it_hi = 0;
   if (act) {
-    const int64_t d0 = lo_w - base, d1 = hi_w - base;
-    it_lo = d0 <= 0 ? 0 : static_cast<int>((d0 + u - 1) / u);
-    it_hi = d1 <= 0 ? 0 : static_cast<int>((d1 + u - 1) / u);
-    it_lo = it_lo < nit ? it_lo : nit;
+    const int64_t seg_cost = static_cast<int64_t>(nit) * u;
+    const int64_t e0 = lo_w - base, e1 = hi_w - base;
+    d0 = static_cast<int>(e0 < 0 ? 0 : (e0 > seg_cost ? seg_cost : e0));
+    d1 = static_cast<int>(e1 < 0 ? 0 : (e1 > seg_cost ? seg_cost : e1));
+    it_lo = d0 / u;  // first item with a row tile at or past d0
+    it_hi = d1 > kWsBuildCost ? (d1 - kWsBuildCost + u - 1) / u : 0;  // first item whose row tiles start at or past d1
     it_hi = it_hi < nit ? it_hi : nit;
   }
   uint64_t todo = __ballot(act && it_hi > it_lo);
@@ -1287,21 +1296,30 @@ __global__ __launch_bounds__(kUnits * kMfThreads) void grouped_mfma_ws_kernel(Mf
     const int e = __builtin_amdgcn_readfirstlane(__shfl(sc.ex, s));
     const int it0 = __builtin_amdgcn_readfirstlane(__shfl(it_lo, s));
     const int it1 = __builtin_amdgcn_readfirstlane(__shfl(it_hi, s));
+    const int sd0 = __builtin_amdgcn_readfirstlane(__shfl(d0, s));
+    const int sd1 = __builtin_amdgcn_readfirstlane(__shfl(d1, s));
     const int rows = seg_hi - seg_lo;
-    if (e < 0 || e >= p.num_experts) {  // rows routed to no expert: zero output
-      if (unit == 0) {
-        const int n_lo = it0 * kSub * kTileOut;
-        const int n_hi = (it1 * kSub * kTileOut) < N ? it1 * kSub * kTileOut : N;
-        const int span = n_hi - n_lo;
-        for (int idx = utid; idx < rows * span; idx += kMfThreads) {
-          out[static_cast<int64_t>(seg_lo + idx / span) * N + n_lo + idx % span] = 0;
-        }
-      }
-      continue;
-    }
     const int nrt = ceil_div(rows, kMfRows);
+    const int cu = nrt + kWsBuildCost;
+    const bool dead = e < 0 || e >= p.num_experts;  // rows routed to no expert: zero output
     for (int it = it0; it < it1; ++it) {
+      // this workgroup's row tiles of the item (never empty: see it_lo, it_hi)
+      const int r_lo = max(0, min(nrt, sd0 - it * cu - kWsBuildCost));
+      const int r_hi = max(0, min(nrt, sd1 - it * cu - kWsBuildCost));
       const int ob = it * kSub;
+      if (dead) {
+        if (unit == 0) {
+          const int n_lo = ob * kTileOut;
+          const int n_hi = ((ob + kSub) * kTileOut) < N ? (ob + kSub) * kTileOut : N;
+          const int span = n_hi - n_lo;
+          const int row_lo = seg_lo + r_lo * kMfRows;
+          const int nrow = min(seg_hi, seg_lo + r_hi * kMfRows) - row_lo;
+          for (int idx = utid; idx < nrow * span; idx += kMfThreads) {
+            out[static_cast<int64_t>(row_lo + idx / span) * N + n_lo + idx % span] = 0;
+          }
+        }
+        continue;
+      }
       __syncthreads();  // the previous item's LDS readers are done
 #pragma unroll
       for (int b = 0; b < kSub; ++b) {
@@ -1343,9 +1361,12 @@ __global__ __launch_bounds__(kUnits * kMfThreads) void grouped_mfma_ws_kernel(Mf
       // the first two row tiles' activations, in flight while the B operands are built; row tile rt's
       // registers are X[rt % 2], reloaded with row tile rt + 2 once staged
       WsX X0, X1;
-      ws_x_issue(pa, seg_lo, rows < kMfRows ? rows : kMfRows, utid, X0);
-      if (kWsXDepth == 2 && nrt > 1) {
-        ws_x_issue(pa, seg_lo + kMfRows, (rows - kMfRows) < kMfRows ? rows - kMfRows : kMfRows, utid, X1);
+      {
+        const int r0 = seg_lo + r_lo * kMfRows;
+        ws_x_issue(pa, r0, min(seg_hi - r0, kMfRows), utid, X0);
+        if (kWsXDepth == 2 && r_lo + 1 < r_hi) {
+          ws_x_issue(pa, r0 + kMfRows, min(seg_hi - r0 - kMfRows, kMfRows), utid, X1);
+        }
       }
 
       // columns of the salient activations of each window, two 16-bit offsets a word, in the A operand's slot
@@ -1420,7 +1441,7 @@ __global__ __launch_bounds__(kUnits * kMfThreads) void grouped_mfma_ws_kernel(Mf
         const int rc = (seg_hi - row0) < kMfRows ? (seg_hi - row0) : kMfRows;
         ws_x_write(utid, xs, X);
         __syncthreads();  // staged rows visible; the previous row tile's exch reads are done
-        if (rt + kWsXDepth < nrt) {  // depth 1: X0 is the only register set (both call sites pass it)
+        if (rt + kWsXDepth < r_hi) {  // depth 1: X0 is the only register set (both call sites pass it)
           const int r2 = row0 + kWsXDepth * kMfRows;
           ws_x_issue(pa, r2, (seg_hi - r2) < kMfRows ? (seg_hi - r2) : kMfRows, utid, X);
         }
@@ -1507,9 +1528,9 @@ __global__ __launch_bounds__(kUnits * kMfThreads) void grouped_mfma_ws_kernel(Mf
         }
       };
       // two activation buffers in alternation (distinct objects per call site)
-      for (int rt = 0; rt < nrt; rt += 2) {
+      for (int rt = r_lo; rt < r_hi; rt += 2) {
         row_tile(rt, xsb0, X0);
-        if (rt + 1 < nrt) row_tile(rt + 1, xsb1, kWsXDepth == 2 ? X1 : X0);
+        if (rt + 1 < r_hi) row_tile(rt + 1, xsb1, kWsXDepth == 2 ? X1 : X0);
       }
     }
   }
@@ -1537,8 +1558,8 @@ static bool allow_mfma_lds(const void* kernel, int bytes) {
 // Weight-stationary launch (long segments, one 512-column chunk, <= 64 salient columns per expert):
 // workgroups as the GPU holds at once (the occupancy the compiled kernel allows with this LDS), no more
 // than the items.
-static int launch_grouped_mfma_ws(const MfmaArgs& args, int units, int nproj, int max_n, hipStream_t s,
-                                  const char* who) {
+static int launch_grouped_mfma_ws(const MfmaArgs& args, int units, int nproj, int max_n, int batch,
+                                  hipStream_t s, const char* who) {
   const int lds = mf_ws_lds_bytes(units, kWsSub);
   const int lds_total = lds + units * kWsSub * kMfTbWords * 4;
   TRIS_REQUIRE(lds_total <= 160 * 1024, "%s: LDS request %d exceeds a CU", who, lds_total);
@@ -1556,8 +1577,13 @@ static int launch_grouped_mfma_ws(const MfmaArgs& args, int units, int nproj, in
     wgs_per_cu = nb > 0 ? nb : 1;
   }
   int wgs = (kMfCus * wgs_per_cu) / nproj;
+  // an upper bound of the work's cost in row tiles (each segment's last row tile may be partial, and every
+  // item has its build): workgroups past it would find no row tile
   const int64_t items = static_cast<int64_t>(args.num_segments) * ceil_div(ceil_div(max_n, kTileOut), kWsSub);
-  if (items < wgs) wgs = static_cast<int>(items);
+  const int64_t cost = static_cast<int64_t>(ceil_div(ceil_div(max_n, kTileOut), kWsSub)) *
+                           (ceil_div(batch, kMfRows) + args.num_segments) +
+                       items * kWsBuildCost;
+  if (cost < wgs) wgs = static_cast<int>(cost);
   const dim3 grid(wgs > 0 ? wgs : 1, 1, nproj);
   if (units == 2) {
     hipLaunchKernelGGL((grouped_mfma_ws_kernel<2, kWsSub>), grid, dim3(2 * kMfThreads), lds, s, args);
@@ -1615,7 +1641,7 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
   // long segments: keep each output tile's weights in registers and stream the segment's rows through them
   if (num_segments <= kWave && static_cast<int64_t>(batch) >= static_cast<int64_t>(kWsMinRows) * num_segments &&
       ws_fits(pa) && (!pb || ws_fits(pb))) {
-    return launch_grouped_mfma_ws(args, units, nproj, max_n, s, who);
+    return launch_grouped_mfma_ws(args, units, nproj, max_n, batch, s, who);
   }
   const int rows = batch <= 4 ? 4 : kMfRows;  // staged activation rows: a row tile has at most min(16, batch)
   // the compact LDS layout (four workgroups per CU): at most 4 row-scale groups and 64 salient columns per expert,
