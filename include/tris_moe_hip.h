@@ -404,6 +404,23 @@ int tris_backbone_linear_pair(const uint16_t* x, int32_t tokens, int32_t in_feat
                               const uint16_t* in_scale_b, uint16_t* out_a, uint16_t* out_b, void* workspace,
                               int64_t workspace_bytes, void* stream);
 
+/* The gate/up backbones of prefill-size batches written straight to the routed rows (no reference
+ * counterpart: the reference projects the gathered rows, compute_shared_hidden on x[perm],
+ * qlinear_cuda.py:4454-4502 with modeling_mixtral.py:467-476; this projects each token once and stores the
+ * result to every row the route sends it to, so the gather of the rows is never materialised).
+ * out_a[inverse_perm[t * top_k + j]] = fp16(x[t] * in_scale_a) . sv_a^T for every token t and slot j (slots
+ * holding -1 or a row >= out_rows are skipped; rows no slot names are left as they are), out_b likewise (sv_b
+ * NULL: one projection).  inverse_perm int32 [tokens * top_k] as tris_build_grouped_route writes it; out
+ * fp16 [out_rows, rank].  Needs tokens >= 512, rank a multiple of 128 and in_features a multiple of 32 (the
+ * tiled GEMM; else TRIS_ERR_INVALID); the values are the bits tris_backbone_linear_pair gives for the token
+ * rows.  workspace: tris_backbone_scatter_workspace_bytes(tokens, in_features, rank, 1 or 2). */
+int tris_backbone_linear_pair_scatter(const uint16_t* x, int32_t tokens, int32_t in_features, const uint16_t* sv_a,
+                                      const uint16_t* sv_b, int32_t rank, const uint16_t* in_scale_a,
+                                      const uint16_t* in_scale_b, const int32_t* inverse_perm, int32_t top_k,
+                                      int32_t out_rows, uint16_t* out_a, uint16_t* out_b, void* workspace,
+                                      int64_t workspace_bytes, void* stream);
+int64_t tris_backbone_scatter_workspace_bytes(int32_t tokens, int32_t in_features, int32_t rank, int32_t nproj);
+
 /*
  * tris_backbone_linear with no workspace argument and no allocation (no reference counterpart: for
  * callers that cannot allocate, such as code under HIP graph capture or tight serving loops).  The split-K
@@ -436,8 +453,9 @@ int64_t tris_backbone_workspace_bytes(int32_t tokens, int32_t in_features, int32
  * fp16(fp16(silu(gate[r][k])) * up[r][k]), the bits tris_swiglu_mul writes, times in_scale[k] (an fp16
  * product, the ns_mode == 1 input scale) when in_scale is not NULL; out fp16 [rows, rank] = in . sv^T with
  * fp32 accumulation, split over K and the slices added in fixed order (deterministic).  gate, up fp16
- * [rows, in_features], sv fp16 [rank, in_features]; rows <= 64, in_features a multiple of 32, 16-byte aligned
- * pointers (else TRIS_ERR_INVALID); workspace of tris_backbone_swiglu_workspace_bytes(rows, in_features, rank).
+ * [rows, in_features], sv fp16 [rank, in_features]; in_features a multiple of 32, and above 64 rows (the tiled
+ * prefill GEMM) rank a multiple of 128; 16-byte aligned pointers (else TRIS_ERR_INVALID); workspace of
+ * tris_backbone_swiglu_workspace_bytes(rows, in_features, rank).
  */
 int tris_backbone_swiglu_linear(const uint16_t* gate, const uint16_t* up, int32_t rows, int32_t in_features,
                                 const uint16_t* sv, int32_t rank, const uint16_t* in_scale, uint16_t* out,

@@ -17,13 +17,14 @@ constexpr int kBbBatch = 8;          // K steps of loads in flight per wavefront
 constexpr int kBbTargetWgs = 512;    // aim for this many workgroups per launch
 constexpr int kBbMaxSlices = 32;        // slices of backbone_kernel
 // the tiled GEMM for prefill-size batches (backbone_gemm_kernel, tris_backbone.hip)
-constexpr int kBgTile = 128;         // rows and rank columns of a workgroup tile
-constexpr int kBgK = 64;             // K columns per LDS stage
-constexpr int kBgStride = kBgK + 8;  // fp16 per staged row: 144-byte rows spread the 16-byte reads over banks
+constexpr int kBgM = 256;            // rows of a workgroup tile
+constexpr int kBgN = 128;            // rank columns of a workgroup tile
+constexpr int kBgK = 32;             // K columns per LDS stage
+constexpr int kBgStride = kBgK + 8;  // fp16 per staged row: 80-byte rows put a wavefront's 16-byte reads on distinct banks
 constexpr int kBgThreads = 256;
 constexpr int kBgMinRows = 512;      // rows from which the entry points take it
-constexpr int kBgMinStages = 8;      // K stages per slice at least
-constexpr int kBgTargetWgs = 512;
+constexpr int kBgMinStages = 16;     // K stages per slice at least
+constexpr int kBgTargetWgs = 512;    // two workgroups per CU
 constexpr int kBgMaxSlices = 16;
 constexpr int kBbReduceMaxSlices = 64;  // slices backbone_reduce_at adds (backbone_swiglu_kernel uses up to 64)
 

@@ -66,16 +66,12 @@ int backbone_slices(int tokens, int in_features, int rank) {
   return slices < 1 ? 1 : static_cast<int>(slices);
 }
 
-static int backbone_gemm_slices(int tokens, int in_features, int rank);
+static int backbone_gemm_slice_k(int tokens, int in_features, int rank, int* slices);
 
 // use_gemm: the entry may take the tiled GEMM for prefill-size batches (backbone_gemm_fits).
 int64_t backbone_workspace_bytes(int tokens, int in_features, int rank, int nproj, bool use_gemm) {
   int slices = backbone_slices(tokens, in_features, rank);
-  if (use_gemm && backbone_gemm_fits(tokens, in_features, rank)) {
-    const int s0 = backbone_gemm_slices(tokens, in_features, rank);
-    const int ks = ceil_div(in_features / kBgK, s0) * kBgK;
-    slices = ceil_div(in_features, ks);
-  }
+  if (use_gemm && backbone_gemm_fits(tokens, in_features, rank)) backbone_gemm_slice_k(tokens, in_features, rank, &slices);
   return slices > 1 ? static_cast<int64_t>(nproj) * slices * tokens * rank * 4 : 0;
 }
 
@@ -127,28 +123,34 @@ int backbone_prepare(const uint16_t* x, int tokens, int in_features, const int64
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// Prefill-size backbone: a tiled split-K MFMA GEMM.  hidden = fp16(x[row] * in_scale) . SV^T; workgroup
-// (mt, nt, s + slices * q) computes the 128 x 128 tile (rows 128 mt.., rank columns 128 nt..) of projection
-// q over K slice s.  Its four wavefronts each own a 64 x 64 quadrant (4 x 4 tiles of v_mfma_f32_16x16x32_f16).
-// Per stage of 64 K columns every thread copies four 16-byte runs of the x tile (rows read through row_index,
-// scaled by in_scale as fp16 products) and four of the SV tile into LDS; the next stage's global loads are in
-// flight in registers while the current stage is multiplied (two LDS buffers, one barrier a stage).  Slices
-// write fp32 partial tiles that backbone_reduce_kernel adds in slice order; one slice writes fp16 directly.
+// Prefill-size backbone: a tiled split-K MFMA GEMM, hidden[m][n] = sum_k a[m][k] SV[n][k] over one K slice, with
+// a[m][k] = fp16(x[row(m)][k] * in_scale[k]) (row(m) = row_index[m] when given).  A workgroup computes a
+// 256 x 128 tile (rows x rank columns) of one projection and slice;
+// its four wavefronts each own a 128 x 64 quadrant (8 x 4 tiles of v_mfma_f32_16x16x32_f16), so every 16-byte
+// LDS read feeds 4 or 8 MFMAs: per 32-column stage a CU (two workgroups) reads 96 KB and writes 48 KB of LDS
+// for 2 x 512 MFMA cycles per SIMD.  Stages are double-buffered in LDS (60 KB a workgroup) with one barrier a
+// stage; the global loads of the next kDepth stages are in flight in registers meanwhile.  Tiles are ordered
+// (projection, slice, row tile, column tile) and handed out XCD-major: the four column tiles of a row tile run
+// on one XCD, whose L2 then serves the row tile's activations to all four.  Slices write fp32 partial tiles
+// that backbone_reduce_kernel adds in slice order (one slice writes fp16 directly), so the result does not
+// depend on the launch shape beyond the slice count, which depends on the problem shape only.
 
 struct BgArgs {
-  BackboneArgs b;
-  int slices;
-  int ks;  // K columns per slice, a multiple of kBgK
+  BackboneArgs b;       // x (g for the SwiGLU form), row_index, proj[], partials, tokens, in_features, rank, slices
+  const uint16_t* x2;   // u for the SwiGLU form
+  int ks;               // K columns per slice, a multiple of kBgK
+  int m_tiles, n_tiles;
+  int direct;           // one slice and no scatter: the tile is written as fp16 to proj[].out
 };
 
 bool backbone_gemm_fits(int tokens, int in_features, int rank) {
-  return tokens >= kBgMinRows && rank % kBgTile == 0 && in_features % kBgK == 0 && in_features > 0;
+  return tokens >= kBgMinRows && rank % kBgN == 0 && rank > 0 && in_features % kBgK == 0 && in_features > 0;
 }
 
 // The slice count depends on the shape only (not on the projection count), so a pair launch gives each
 // projection the bits of its single launch.
 static int backbone_gemm_slices(int tokens, int in_features, int rank) {
-  const int64_t tiles = static_cast<int64_t>(ceil_div(tokens, kBgTile)) * (rank / kBgTile);
+  const int64_t tiles = static_cast<int64_t>(ceil_div(tokens, kBgM)) * (rank / kBgN);
   int64_t s = (kBgTargetWgs + tiles - 1) / tiles;
   const int64_t max_by_k = in_features / (kBgK * kBgMinStages);
   s = s < max_by_k ? s : max_by_k;
@@ -156,138 +158,387 @@ static int backbone_gemm_slices(int tokens, int in_features, int rank) {
   return s < 1 ? 1 : static_cast<int>(s);
 }
 
+static int backbone_gemm_slice_k(int tokens, int in_features, int rank, int* slices) {
+  const int s0 = backbone_gemm_slices(tokens, in_features, rank);
+  const int ks = ceil_div(in_features / kBgK, s0) * kBgK;
+  *slices = ceil_div(in_features, ks);
+  return ks;
+}
+
+constexpr int kXcdCount = 8;  // MI355X: workgroup w runs on XCD w % 8
+
+struct BgStage {
+  uint4 a[4];  // the x runs
+  uint4 b[2];  // the SV runs
+  uint4 sc;    // in_scale of the thread's 8 columns
+};
+
+template <int kDepth>
 __global__ __launch_bounds__(kBgThreads, 2) void backbone_gemm_kernel(BgArgs g) {
-  __shared__ __attribute__((aligned(16))) uint16_t la[2][kBgTile * kBgStride];
-  __shared__ __attribute__((aligned(16))) uint16_t lb[2][kBgTile * kBgStride];
+  __shared__ __attribute__((aligned(16))) uint16_t la0[kBgM * kBgStride];
+  __shared__ __attribute__((aligned(16))) uint16_t la1[kBgM * kBgStride];
+  __shared__ __attribute__((aligned(16))) uint16_t lb0[kBgN * kBgStride];
+  __shared__ __attribute__((aligned(16))) uint16_t lb1[kBgN * kBgStride];
   const BackboneArgs& a = g.b;
-  const int q = static_cast<int>(blockIdx.z) / g.slices;
-  const int sl = static_cast<int>(blockIdx.z) % g.slices;
-  const BackboneProj pj = q == 0 ? a.proj[0] : a.proj[1];  // selected, not indexed: no private copy of the args
   const int tid = static_cast<int>(threadIdx.x);
   const int wave = tid / kWave;
   const int lane = tid % kWave;
   const int wm = wave >> 1, wn = wave & 1;
   const int i16 = lane & 15, kg = lane >> 4;
-  const int m0 = static_cast<int>(blockIdx.x) * kBgTile;
-  const int n0 = static_cast<int>(blockIdx.y) * kBgTile;
+  // XCD-major virtual tile index, column tile fastest
+  int v;
+  {
+    const int w = static_cast<int>(blockIdx.x);
+    const int W = static_cast<int>(gridDim.x);
+    const int x = w % kXcdCount, q = W / kXcdCount, r = W % kXcdCount;
+    v = x * q + (x < r ? x : r) + w / kXcdCount;
+  }
+  const int nt = v % g.n_tiles;
+  v /= g.n_tiles;
+  const int mt = v % g.m_tiles;
+  v /= g.m_tiles;
+  const int sl = v % a.slices;
+  const int q = v / a.slices;
+  const BackboneProj pj = q == 0 ? a.proj[0] : a.proj[1];  // selected, not indexed: no private copy of the args
+  const int m0 = mt * kBgM;
+  const int n0 = nt * kBgN;
   const int K = a.in_features;
   const int kbeg = sl * g.ks;
   const int kn = (K - kbeg) < g.ks ? (K - kbeg) : g.ks;  // > 0, a multiple of kBgK
   const int nstage = kn / kBgK;
-  // copy slots: thread tid moves 16-byte runs c = tid + 256 i (i < 4): row c / 8, columns 8 (c % 8) .. + 8
+  // copy slots: run i of the thread is row (tid / 4) + 64 i of the tile, columns 8 (tid % 4) .. + 8 of the stage;
+  // rows past the batch read the batch's last row (their outputs are not written)
+  const int crow = tid >> 2, ccol = (tid & 3) * 8;
   const uint16_t* xsrc[4];
-  const uint16_t* ssrc[4];
-  bool xv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int c = tid + kBgThreads * i;
-    const int row = c >> 3, col = (c & 7) * 8;
-    const int m = m0 + row;
-    xv[i] = m < a.tokens;
-    const int64_t xrow = xv[i] ? (a.row_index != nullptr ? a.row_index[m] : m) : 0;
-    xsrc[i] = a.x + xrow * K + kbeg + col;
-    ssrc[i] = pj.sv + static_cast<int64_t>(n0 + row) * K + kbeg + col;
+    int m = m0 + crow + 64 * i;
+    m = m < a.tokens ? m : a.tokens - 1;
+    const int64_t xrow = a.row_index != nullptr ? a.row_index[m] : m;
+    xsrc[i] = a.x + xrow * K + kbeg + ccol;
   }
-  const uint16_t* scale = pj.in_scale != nullptr ? pj.in_scale + kbeg + (tid & 7) * 8 : nullptr;
-  uint4 ra0, ra1, ra2, ra3, rb0, rb1, rb2, rb3;
-// the stage's 16-byte runs into registers (x scaled by in_scale as fp16 products, as x * ns_col)
-#define TRIS_BG_LOAD(ko)                                                                                     \
-  do {                                                                                                       \
-    ra0 = xv[0] ? *reinterpret_cast<const uint4*>(xsrc[0] + (ko)) : make_uint4(0u, 0u, 0u, 0u);               \
-    ra1 = xv[1] ? *reinterpret_cast<const uint4*>(xsrc[1] + (ko)) : make_uint4(0u, 0u, 0u, 0u);               \
-    ra2 = xv[2] ? *reinterpret_cast<const uint4*>(xsrc[2] + (ko)) : make_uint4(0u, 0u, 0u, 0u);               \
-    ra3 = xv[3] ? *reinterpret_cast<const uint4*>(xsrc[3] + (ko)) : make_uint4(0u, 0u, 0u, 0u);               \
-    rb0 = *reinterpret_cast<const uint4*>(ssrc[0] + (ko));                                                   \
-    rb1 = *reinterpret_cast<const uint4*>(ssrc[1] + (ko));                                                   \
-    rb2 = *reinterpret_cast<const uint4*>(ssrc[2] + (ko));                                                   \
-    rb3 = *reinterpret_cast<const uint4*>(ssrc[3] + (ko));                                                   \
-    if (scale != nullptr) {                                                                                  \
-      const f16x8 sc = *reinterpret_cast<const f16x8*>(scale + (ko));                                        \
-      ra0 = __builtin_bit_cast(uint4, __builtin_bit_cast(f16x8, ra0) * sc);                                  \
-      ra1 = __builtin_bit_cast(uint4, __builtin_bit_cast(f16x8, ra1) * sc);                                  \
-      ra2 = __builtin_bit_cast(uint4, __builtin_bit_cast(f16x8, ra2) * sc);                                  \
-      ra3 = __builtin_bit_cast(uint4, __builtin_bit_cast(f16x8, ra3) * sc);                                  \
-    }                                                                                                        \
-  } while (0)
-// run c = tid + 256 i sits at row c / 8 (32 i + tid / 8), columns 8 (tid % 8)
-#define TRIS_BG_STORE(buf)                                                                                   \
-  do {                                                                                                       \
-    const int o = (tid >> 3) * kBgStride + (tid & 7) * 8;                                                    \
-    *reinterpret_cast<uint4*>(&la[buf][o]) = ra0;                                                            \
-    *reinterpret_cast<uint4*>(&la[buf][o + 32 * kBgStride]) = ra1;                                           \
-    *reinterpret_cast<uint4*>(&la[buf][o + 64 * kBgStride]) = ra2;                                           \
-    *reinterpret_cast<uint4*>(&la[buf][o + 96 * kBgStride]) = ra3;                                           \
-    *reinterpret_cast<uint4*>(&lb[buf][o]) = rb0;                                                            \
-    *reinterpret_cast<uint4*>(&lb[buf][o + 32 * kBgStride]) = rb1;                                           \
-    *reinterpret_cast<uint4*>(&lb[buf][o + 64 * kBgStride]) = rb2;                                           \
-    *reinterpret_cast<uint4*>(&lb[buf][o + 96 * kBgStride]) = rb3;                                           \
-  } while (0)
-  f32x4 acc[4][4];
+  const uint16_t* ssrc0 = pj.sv + static_cast<int64_t>(n0 + crow) * K + kbeg + ccol;
+  const uint16_t* ssrc1 = ssrc0 + static_cast<int64_t>(64) * K;
+  const uint16_t* scale = pj.in_scale != nullptr ? pj.in_scale + kbeg + ccol : nullptr;
+
+  auto issue = [&](int st, BgStage& R) {
+    const int ko = st * kBgK;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 4; ++i) R.a[i] = *reinterpret_cast<const uint4*>(xsrc[i] + ko);
+    R.b[0] = *reinterpret_cast<const uint4*>(ssrc0 + ko);
+    R.b[1] = *reinterpret_cast<const uint4*>(ssrc1 + ko);
+    R.sc = scale != nullptr ? *reinterpret_cast<const uint4*>(scale + ko)
+                            : make_uint4(0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u);
+  };
+  // the stage's operands into LDS: a = fp16(x * in_scale) (fp16 products; a scale of 1.0 is exact)
+  auto write = [&](const BgStage& R, uint16_t* la, uint16_t* lb) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const uint32_t sw[4] = {R.sc.x, R.sc.y, R.sc.z, R.sc.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t xw[4] = {R.a[i].x, R.a[i].y, R.a[i].z, R.a[i].w};
+      uint32_t pw[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        pw[h] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, xw[h]) * __builtin_bit_cast(h2, sw[h]));
+      }
+      *reinterpret_cast<uint4*>(&la[(crow + 64 * i) * kBgStride + ccol]) = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+    }
+    *reinterpret_cast<uint4*>(&lb[crow * kBgStride + ccol]) = R.b[0];
+    *reinterpret_cast<uint4*>(&lb[(crow + 64) * kBgStride + ccol]) = R.b[1];
+  };
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
-  TRIS_BG_LOAD(0);
-  TRIS_BG_STORE(0);
-  __syncthreads();
-  for (int st = 0; st < nstage; ++st) {
-    const int buf = st & 1;
-    if (st + 1 < nstage) TRIS_BG_LOAD((st + 1) * kBgK);
-    const uint16_t* A = la[buf] + (wm * 64 + i16) * kBgStride + kg * 8;
-    const uint16_t* B = lb[buf] + (wn * 64 + i16) * kBgStride + kg * 8;
+  auto compute = [&](const uint16_t* la, const uint16_t* lb) {
+    f16x8 bv[4];
 #pragma unroll
-    for (int kk = 0; kk < kBgK / 32; ++kk) {
-      f16x8 av[4], bv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = *reinterpret_cast<const f16x8*>(A + i * 16 * kBgStride + kk * 32);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = *reinterpret_cast<const f16x8*>(B + j * 16 * kBgStride + kk * 32);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
-      }
+    for (int j = 0; j < 4; ++j) {
+      bv[j] = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&lb[(64 * wn + 16 * j + i16) * kBgStride + 8 * kg]));
     }
-    if (st + 1 < nstage) TRIS_BG_STORE(buf ^ 1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const f16x8 av =
+          __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&la[(128 * wm + 16 * i + i16) * kBgStride + 8 * kg]));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  // stage st sits in buffer st % 2; register set R[kDepth == 2 ? st % 2 : 0] carries it from its loads to LDS
+  BgStage R0, R1;
+  issue(0, R0);
+  if (kDepth == 2 && nstage > 1) issue(1, R1);
+  write(R0, la0, lb0);
+  __syncthreads();
+  for (int st = 0; st < nstage; st += 2) {
+    if (kDepth == 1) {
+      if (st + 1 < nstage) issue(st + 1, R0);
+    } else if (st + 2 < nstage) {
+      issue(st + 2, R0);
+    }
+    compute(la0, lb0);
+    if (st + 1 < nstage) write(kDepth == 1 ? R0 : R1, la1, lb1);
     __syncthreads();
+    if (st + 1 < nstage) {
+      if (kDepth == 1) {
+        if (st + 2 < nstage) issue(st + 2, R0);
+      } else if (st + 3 < nstage) {
+        issue(st + 3, R1);
+      }
+      compute(la1, lb1);
+      if (st + 2 < nstage) write(R0, la0, lb0);
+      __syncthreads();
+    }
   }
-#undef TRIS_BG_LOAD
-#undef TRIS_BG_STORE
-  // acc[i][j][v] = hidden[m0 + 64 wm + 16 i + 4 kg + v][n0 + 64 wn + 16 j + i16]
+  // acc[i][j][v] = hidden[m0 + 128 wm + 16 i + 4 kg + v][n0 + 64 wn + 16 j + i16]
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 8; ++i) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int m = m0 + wm * 64 + i * 16 + kg * 4 + v;
+    for (int vv = 0; vv < 4; ++vv) {
+      const int m = m0 + wm * 128 + i * 16 + kg * 4 + vv;
       if (m >= a.tokens) continue;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int n = n0 + wn * 64 + j * 16 + i16;
-        if (g.slices == 1) {
-          pj.out[static_cast<int64_t>(m) * a.rank + n] = f2h_bits(acc[i][j][v]);
+        if (g.direct) {
+          pj.out[static_cast<int64_t>(m) * a.rank + n] = f2h_bits(acc[i][j][vv]);
         } else {
-          a.partials[((static_cast<int64_t>(q) * g.slices + sl) * a.tokens + m) * a.rank + n] = acc[i][j][v];
+          a.partials[((static_cast<int64_t>(q) * a.slices + sl) * a.tokens + m) * a.rank + n] = acc[i][j][vv];
         }
       }
     }
   }
 }
 
-static int launch_backbone_gemm(const BackboneArgs& base, int nproj, hipStream_t s, const char* who) {
+// The slice reduction of a token-row projection written to routed rows: element (t, n) of projection q is
+// added in slice order, rounded once and stored to row inverse_perm[t * top_k + j] of proj[q].out for every
+// slot j (the rows the route sends token t to; -1 and rows past out_rows are skipped).
+__global__ __launch_bounds__(256) void backbone_reduce_scatter_kernel(BackboneArgs a, const int32_t* __restrict__ inv,
+                                                                      int top_k, int out_rows) {
+  const int q = static_cast<int>(blockIdx.y);
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t count = static_cast<int64_t>(a.tokens) * a.rank;
+  if (idx >= count) return;
+  const float* src = a.partials + static_cast<int64_t>(q) * a.slices * count + idx;
+  float v[kBgMaxSlices];
+#pragma unroll
+  for (int sl = 0; sl < kBgMaxSlices; ++sl) v[sl] = sl < a.slices ? src[sl * count] : 0.0f;  // loads in flight together
+  float sum = 0.0f;
+#pragma unroll
+  for (int sl = 0; sl < kBgMaxSlices; ++sl) {
+    if (sl < a.slices) sum += v[sl];
+  }
+  const uint16_t h = f2h_bits(sum);
+  const int t = static_cast<int>(idx / a.rank);
+  const int n = static_cast<int>(idx - static_cast<int64_t>(t) * a.rank);
+  uint16_t* out = q == 0 ? a.proj[0].out : a.proj[1].out;
+  for (int j = 0; j < top_k; ++j) {
+    const int row = inv[static_cast<int64_t>(t) * top_k + j];
+    if (row >= 0 && row < out_rows) out[static_cast<int64_t>(row) * a.rank + n] = h;
+  }
+}
+
+// The SwiGLU form of the tiled GEMM with each product formed once: a workgroup of eight wavefronts covers a
+// 128 x 512 tile (rows x rank columns; wavefront (wm, wn) of 2 x 4 owns a 64 x 128 quadrant, 4 x 8 tiles of
+// v_mfma_f32_16x16x32_f16), so act_fn(g) * u of a row is formed by one workgroup per K slice, not by every
+// 128-column tile of the rank (the SiLU takes about 30 VALU per element, more than the MFMA time per element of
+// a 128-column tile).  Per 32-column stage a thread forms 8 products and copies four 16-byte SV runs; stages are
+// double-buffered in LDS (100 KB), one workgroup per CU.  Rank columns past the rank are computed on clamped SV
+// rows and not written.  Tiles are ordered (slice, row tile, column tile) and handed out XCD-major, so the
+// workgroups of one K slice share its SV rows through one L2.
+constexpr int kBwM = 128;
+constexpr int kBwN = 512;
+constexpr int kBwThreads = 512;
+constexpr int kBwTargetWgs = 256;
+
+static int backbone_wide_slice_k(int rows, int in_features, int rank, int* slices) {
+  const int64_t tiles = static_cast<int64_t>(ceil_div(rows, kBwM)) * ceil_div(rank, kBwN);
+  int64_t sl = (kBwTargetWgs + tiles - 1) / tiles;
+  const int64_t max_by_k = in_features / (kBgK * kBgMinStages);
+  sl = sl < max_by_k ? sl : max_by_k;
+  sl = sl < kBgMaxSlices ? sl : kBgMaxSlices;
+  sl = sl < 1 ? 1 : sl;
+  const int ks = ceil_div(in_features / kBgK, static_cast<int>(sl)) * kBgK;
+  *slices = ceil_div(in_features, ks);
+  return ks;
+}
+
+__global__ __launch_bounds__(kBwThreads, 1) void backbone_swiglu_gemm_kernel(BgArgs g) {
+  __shared__ __attribute__((aligned(16))) uint16_t la0[kBwM * kBgStride];
+  __shared__ __attribute__((aligned(16))) uint16_t la1[kBwM * kBgStride];
+  __shared__ __attribute__((aligned(16))) uint16_t lb0[kBwN * kBgStride];
+  __shared__ __attribute__((aligned(16))) uint16_t lb1[kBwN * kBgStride];
+  const BackboneArgs& a = g.b;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int i16 = lane & 15, kg = lane >> 4;
+  int v;
+  {
+    const int w = static_cast<int>(blockIdx.x);
+    const int W = static_cast<int>(gridDim.x);
+    const int x = w % kXcdCount, q = W / kXcdCount, r = W % kXcdCount;
+    v = x * q + (x < r ? x : r) + w / kXcdCount;
+  }
+  const int nt = v % g.n_tiles;
+  v /= g.n_tiles;
+  const int mt = v % g.m_tiles;
+  const int sl = v / g.m_tiles;
+  const BackboneProj& pj = a.proj[0];
+  const int m0 = mt * kBwM;
+  const int n0 = nt * kBwN;
+  const int K = a.in_features;
+  const int kbeg = sl * g.ks;
+  const int kn = (K - kbeg) < g.ks ? (K - kbeg) : g.ks;
+  const int nstage = kn / kBgK;
+  // copy slots: the thread's g/u run is row tid / 4 of the tile, its SV runs rows tid / 4 + 128 i, columns
+  // 8 (tid % 4) .. + 8 of the stage (rows past the batch or the rank read the last valid row)
+  const int crow = tid >> 2, ccol = (tid & 3) * 8;
+  int m = m0 + crow;
+  m = m < a.tokens ? m : a.tokens - 1;
+  const uint16_t* gsrc = a.x + static_cast<int64_t>(m) * K + kbeg + ccol;
+  const uint16_t* usrc = g.x2 + static_cast<int64_t>(m) * K + kbeg + ccol;
+  const uint16_t* ssrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int n = n0 + crow + 128 * i;
+    n = n < a.rank ? n : a.rank - 1;
+    ssrc[i] = pj.sv + static_cast<int64_t>(n) * K + kbeg + ccol;
+  }
+  const uint16_t* scale = pj.in_scale != nullptr ? pj.in_scale + kbeg + ccol : nullptr;
+  struct Regs {
+    uint4 g, u, b[4], sc;
+  };
+  auto issue = [&](int st, Regs& R) {
+    const int ko = st * kBgK;
+    R.g = *reinterpret_cast<const uint4*>(gsrc + ko);
+    R.u = *reinterpret_cast<const uint4*>(usrc + ko);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) R.b[i] = *reinterpret_cast<const uint4*>(ssrc[i] + ko);
+    R.sc = scale != nullptr ? *reinterpret_cast<const uint4*>(scale + ko)
+                            : make_uint4(0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u);
+  };
+  auto write = [&](const Regs& R, uint16_t* la, uint16_t* lb) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const uint32_t gw[4] = {R.g.x, R.g.y, R.g.z, R.g.w};
+    const uint32_t uw[4] = {R.u.x, R.u.y, R.u.z, R.u.w};
+    const uint32_t sw[4] = {R.sc.x, R.sc.y, R.sc.z, R.sc.w};
+    uint32_t pw[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const uint32_t lo = swiglu_bits(static_cast<uint16_t>(gw[h]), static_cast<uint16_t>(uw[h]));
+      const uint32_t hi = swiglu_bits(static_cast<uint16_t>(gw[h] >> 16), static_cast<uint16_t>(uw[h] >> 16));
+      pw[h] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, lo | (hi << 16)) * __builtin_bit_cast(h2, sw[h]));
+    }
+    *reinterpret_cast<uint4*>(&la[crow * kBgStride + ccol]) = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&lb[(crow + 128 * i) * kBgStride + ccol]) = R.b[i];
+  };
+  f32x4 acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  auto compute = [&](const uint16_t* la, const uint16_t* lb) {
+    f16x8 bv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      bv[j] = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&lb[(128 * wn + 16 * j + i16) * kBgStride + 8 * kg]));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f16x8 av =
+          __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&la[(64 * wm + 16 * i + i16) * kBgStride + 8 * kg]));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv[j], acc[i][j], 0, 0, 0);
+    }
+  };
+  Regs R0;
+  issue(0, R0);
+  write(R0, la0, lb0);
+  __syncthreads();
+  for (int st = 0; st < nstage; st += 2) {
+    if (st + 1 < nstage) issue(st + 1, R0);
+    compute(la0, lb0);
+    if (st + 1 < nstage) write(R0, la1, lb1);
+    __syncthreads();
+    if (st + 1 < nstage) {
+      if (st + 2 < nstage) issue(st + 2, R0);
+      compute(la1, lb1);
+      if (st + 2 < nstage) write(R0, la0, lb0);
+      __syncthreads();
+    }
+  }
+  // acc[i][j][vv] = hidden[m0 + 64 wm + 16 i + 4 kg + vv][n0 + 128 wn + 16 j + i16]
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int vv = 0; vv < 4; ++vv) {
+      const int mm = m0 + wm * 64 + i * 16 + kg * 4 + vv;
+      if (mm >= a.tokens) continue;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int n = n0 + wn * 128 + j * 16 + i16;
+        if (n >= a.rank) continue;
+        if (g.direct) {
+          pj.out[static_cast<int64_t>(mm) * a.rank + n] = f2h_bits(acc[i][j][vv]);
+        } else {
+          a.partials[(static_cast<int64_t>(sl) * a.tokens + mm) * a.rank + n] = acc[i][j][vv];
+        }
+      }
+    }
+  }
+}
+
+// base: g, proj[0] (sv, out, in_scale), partials, rows (tokens), in_features, rank.
+static int launch_backbone_swiglu_gemm(const BackboneArgs& base, const uint16_t* up, hipStream_t s, const char* who) {
   BgArgs g{};
   g.b = base;
-  g.slices = backbone_gemm_slices(base.tokens, base.in_features, base.rank);
-  g.ks = ceil_div(base.in_features / kBgK, g.slices) * kBgK;
-  g.slices = ceil_div(base.in_features, g.ks);
-  g.b.slices = g.slices;
-  TRIS_REQUIRE(static_cast<int64_t>(g.slices) * nproj <= 65535 && ceil_div(base.tokens, kBgTile) <= 2147483647,
-               "%s: grid too large", who);
-  const dim3 grid(static_cast<unsigned>(ceil_div(base.tokens, kBgTile)), static_cast<unsigned>(base.rank / kBgTile),
-                  static_cast<unsigned>(g.slices * nproj));
-  hipLaunchKernelGGL(backbone_gemm_kernel, grid, dim3(kBgThreads), 0, s, g);
+  g.x2 = up;
+  int slices = 1;
+  g.ks = backbone_wide_slice_k(base.tokens, base.in_features, base.rank, &slices);
+  g.b.slices = slices;
+  g.m_tiles = ceil_div(base.tokens, kBwM);
+  g.n_tiles = ceil_div(base.rank, kBwN);
+  g.direct = slices == 1;
+  const int64_t wgs = static_cast<int64_t>(g.m_tiles) * g.n_tiles * slices;
+  TRIS_REQUIRE(wgs <= 2147483647, "%s: grid too large", who);
+  hipLaunchKernelGGL(backbone_swiglu_gemm_kernel, dim3(static_cast<unsigned>(wgs)), dim3(kBwThreads), 0, s, g);
   int rc = check_launch(who);
-  if (rc || g.slices == 1) return rc;
+  if (rc || g.direct) return rc;
+  return launch_backbone_reduce(g.b, 1, s, who);
+}
+
+// base: x, row_index, proj[], partials, tokens, in_features, rank; slices are set here.
+// scatter (inverse_perm, top_k, out_rows): the token rows' projections go to their routed rows.
+static int launch_backbone_gemm(const BackboneArgs& base, int nproj, hipStream_t s, const char* who,
+                                const int32_t* scatter = nullptr, int top_k = 0, int out_rows = 0) {
+  BgArgs g{};
+  g.b = base;
+  int slices = 1;
+  g.ks = backbone_gemm_slice_k(base.tokens, base.in_features, base.rank, &slices);
+  g.b.slices = slices;
+  g.m_tiles = ceil_div(base.tokens, kBgM);
+  g.n_tiles = base.rank / kBgN;
+  g.direct = slices == 1 && scatter == nullptr;
+  const int64_t wgs = static_cast<int64_t>(g.m_tiles) * g.n_tiles * slices * nproj;
+  TRIS_REQUIRE(wgs <= 2147483647, "%s: grid too large", who);
+  const dim3 grid(static_cast<unsigned>(wgs));
+  hipLaunchKernelGGL((backbone_gemm_kernel<2>), grid, dim3(kBgThreads), 0, s, g);
+  int rc = check_launch(who);
+  if (rc || g.direct) return rc;
+  if (scatter != nullptr) {
+    const int64_t count = static_cast<int64_t>(base.tokens) * base.rank;
+    hipLaunchKernelGGL(backbone_reduce_scatter_kernel, dim3(static_cast<unsigned>((count + 255) / 256), nproj),
+                       dim3(256), 0, s, g.b, scatter, top_k, out_rows);
+    return check_launch(who);
+  }
   return launch_backbone_reduce(g.b, nproj, s, who);
 }
 
@@ -822,10 +1073,62 @@ extern "C" int tris_backbone_linear_pair(const uint16_t* x, int32_t tokens, int3
                          workspace, workspace_bytes, stream, "tris_backbone_linear_pair");
 }
 
+extern "C" int64_t tris_backbone_scatter_workspace_bytes(int32_t tokens, int32_t in_features, int32_t rank,
+                                                         int32_t nproj) {
+  if (tokens <= 0 || in_features <= 0 || rank <= 0 || nproj <= 0 || !backbone_gemm_fits(tokens, in_features, rank)) {
+    return 0;
+  }
+  int slices = 1;
+  backbone_gemm_slice_k(tokens, in_features, rank, &slices);
+  return static_cast<int64_t>(slices) * nproj * tokens * rank * 4;
+}
+
+extern "C" int tris_backbone_linear_pair_scatter(const uint16_t* x, int32_t tokens, int32_t in_features,
+                                                 const uint16_t* sv_a, const uint16_t* sv_b, int32_t rank,
+                                                 const uint16_t* in_scale_a, const uint16_t* in_scale_b,
+                                                 const int32_t* inverse_perm, int32_t top_k, int32_t out_rows,
+                                                 uint16_t* out_a, uint16_t* out_b, void* workspace,
+                                                 int64_t workspace_bytes, void* stream) {
+  const char* who = "tris_backbone_linear_pair_scatter";
+  TRIS_REQUIRE(tokens >= 0 && in_features >= 0 && rank >= 0 && top_k >= 0 && out_rows >= 0, "%s: negative shape",
+               who);
+  if (tokens == 0 || rank == 0 || top_k == 0 || out_rows == 0) return TRIS_OK;
+  TRIS_REQUIRE(backbone_gemm_fits(tokens, in_features, rank),
+               "%s: needs %d tokens or more, rank a multiple of %d and in_features a multiple of %d (got %d, %d, %d)",
+               who, kBgMinRows, kBgN, kBgK, tokens, rank, in_features);
+  TRIS_REQUIRE(x && sv_a && out_a && inverse_perm && (sv_b == nullptr || out_b != nullptr), "%s: null pointer", who);
+  TRIS_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(sv_a) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(sv_b) % 16 == 0 && reinterpret_cast<uintptr_t>(in_scale_a) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(in_scale_b) % 16 == 0,
+               "%s: x, sv and in_scale must be 16-byte aligned", who);
+  const int nproj = sv_b != nullptr ? 2 : 1;
+  const int64_t need = tris_backbone_scatter_workspace_bytes(tokens, in_features, rank, nproj);
+  TRIS_REQUIRE(workspace != nullptr && workspace_bytes >= need, "%s: workspace of %lld bytes needed, %lld given", who,
+               static_cast<long long>(need), static_cast<long long>(workspace_bytes));
+  BackboneArgs ga{};
+  ga.x = x;
+  ga.proj[0] = BackboneProj{sv_a, out_a, in_scale_a};
+  ga.proj[1] = BackboneProj{sv_b, out_b, in_scale_b};
+  ga.partials = static_cast<float*>(workspace);
+  ga.tokens = tokens;
+  ga.in_features = in_features;
+  ga.rank = rank;
+  return launch_backbone_gemm(ga, nproj, static_cast<hipStream_t>(stream), who, inverse_perm, top_k, out_rows);
+}
+
+// More than kSgMaxRowTiles 16-row tiles take the tiled GEMM with the product formed in its operand staging.
+static bool swiglu_backbone_gemm(int rows, int in_features, int rank) {
+  return rows > kSgMaxRowTiles * 16 && rank % kBgN == 0 && in_features % kBgK == 0;
+}
+
 extern "C" int64_t tris_backbone_swiglu_workspace_bytes(int32_t rows, int32_t in_features, int32_t rank) {
   if (rows <= 0 || in_features <= 0 || rank <= 0) return 0;
   int slices = 1;
-  swiglu_backbone_slice_k(in_features, rank, &slices);
+  if (swiglu_backbone_gemm(rows, in_features, rank)) {
+    backbone_wide_slice_k(rows, in_features, rank, &slices);
+  } else {
+    swiglu_backbone_slice_k(in_features, rank, &slices);
+  }
   return slices > 1 ? static_cast<int64_t>(slices) * rows * rank * 4 : 0;
 }
 
@@ -835,24 +1138,35 @@ extern "C" int tris_backbone_swiglu_linear(const uint16_t* gate, const uint16_t*
   const char* who = "tris_backbone_swiglu_linear";
   TRIS_REQUIRE(rows >= 0 && in_features >= 0 && rank >= 0, "%s: negative shape", who);
   if (rows == 0 || rank == 0) return TRIS_OK;
-  TRIS_REQUIRE(rows <= kSgMaxRowTiles * 16, "%s: %d rows exceed %d", who, rows, kSgMaxRowTiles * 16);
   TRIS_REQUIRE(in_features > 0 && in_features % 32 == 0, "%s: in_features %d must be a positive multiple of 32", who,
                in_features);
+  TRIS_REQUIRE(rows <= kSgMaxRowTiles * 16 || rank % kBgN == 0,
+               "%s: %d rows need a rank that is a multiple of %d (rank %d)", who, rows, kBgN, rank);
   TRIS_REQUIRE(gate && up && sv && out, "%s: null pointer", who);
   TRIS_REQUIRE(reinterpret_cast<uintptr_t>(gate) % 16 == 0 && reinterpret_cast<uintptr_t>(up) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(sv) % 16 == 0 && reinterpret_cast<uintptr_t>(in_scale) % 16 == 0,
                "%s: gate, up, sv and in_scale must be 16-byte aligned", who);
-  int slices = 1;
-  const int slice_k = swiglu_backbone_slice_k(in_features, rank, &slices);
   const int64_t need = tris_backbone_swiglu_workspace_bytes(rows, in_features, rank);
   TRIS_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
                "%s: workspace of %lld bytes needed, %lld given", who, static_cast<long long>(need),
                static_cast<long long>(workspace_bytes));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (swiglu_backbone_gemm(rows, in_features, rank)) {
+    BackboneArgs ga{};
+    ga.x = gate;
+    ga.proj[0] = BackboneProj{sv, out, in_scale};
+    ga.partials = static_cast<float*>(workspace);
+    ga.tokens = rows;
+    ga.in_features = in_features;
+    ga.rank = rank;
+    return launch_backbone_swiglu_gemm(ga, up, s, who);
+  }
+  int slices = 1;
+  const int slice_k = swiglu_backbone_slice_k(in_features, rank, &slices);
   SwigluBackboneArgs a{gate, up, sv, in_scale, out, static_cast<float*>(workspace), rows, in_features, rank, slices,
                        slice_k};
   const int tt = ceil_div(rows, 16);
   const size_t lds = static_cast<size_t>(tt) * 16 * (slice_k + 8) * 2;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(ceil_div(rank, kSgCols), slices);
   switch (tt) {
     case 1: hipLaunchKernelGGL((backbone_swiglu_kernel<1>), grid, dim3(kSgThreads), lds, s, a); break;

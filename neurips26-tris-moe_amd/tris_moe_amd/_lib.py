@@ -167,6 +167,9 @@ SIGNATURES = {
     "tris_backbone_pair_workspace_bytes": (_I64, [_I32, _I32, _I32]),
     "tris_backbone_swiglu_linear": (ctypes.c_int, [_P, _P, _I32, _I32, _P, _I32, _P, _P, _P, _I64, _P]),
     "tris_backbone_swiglu_workspace_bytes": (_I64, [_I32, _I32, _I32]),
+    "tris_backbone_linear_pair_scatter": (ctypes.c_int, [_P, _I32, _I32, _P, _P, _I32, _P, _P, _P, _I32, _I32, _P, _P,
+                                                          _P, _I64, _P]),
+    "tris_backbone_scatter_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32]),
     "tris_backbone_linear_noalloc": (ctypes.c_int, [_P, _I32, _I32, _P, _P, _I32, _P, _P, _P]),
     "tris_backbone_noalloc_scratch_bytes": (_I64, []),
     "tris_backbone_workspace_bytes": (_I64, [_I32, _I32, _I32]),

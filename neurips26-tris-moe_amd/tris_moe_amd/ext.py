@@ -906,15 +906,16 @@ BACKBONE_LIBRARY_MIN_ROWS = 256
 BACKBONE_LIBRARY_MIN_ELEMS = 1 << 19
 
 
-# Rows from which the Python layer sends a backbone with rank a multiple of 128 and in_features of 64 to
-# tris_backbone_linear[_pair], whose tiled split-K GEMM takes such shapes from 512 rows (C callers, which have no
-# library GEMM).  Measured on MI355X at the prefill shapes: 103 us for 4096 x 14336 -> 512 plus a 17 us slice
-# reduction, against the library GEMM's 91-103 us alone, so the layer keeps the library GEMM (this threshold off).
-BACKBONE_GEMM_MIN_ROWS = 1 << 30
+# Rows from which a backbone with rank a multiple of 128 and in_features of 32 goes to the tiled split-K GEMM of
+# tris_backbone_linear[_pair] (256 x 128 workgroup tiles) instead of the library GEMM.  Measured on MI355X at the
+# C2 prefill shapes: the gate/up pair over 2048 tokens 35 us (+ 15.6 us for the reduction that writes the routed
+# rows) against the library's 2 x 22 us plus two 5.5 us row gathers; 4096 x 14336 -> 512 91 us + 19.7 us against
+# 105.6 us.
+BACKBONE_GEMM_MIN_ROWS = 512
 
 
 def _backbone_gemm_ok(rows: int, in_features: int, rank: int) -> bool:
-    return rows >= BACKBONE_GEMM_MIN_ROWS and rank % 128 == 0 and in_features % 64 == 0 and in_features > 0
+    return rows >= BACKBONE_GEMM_MIN_ROWS and rank % 128 == 0 and rank > 0 and in_features % 32 == 0 and in_features > 0
 
 
 def _backbone_use_library(rows: int, in_features: int, rank: int = 0) -> bool:
@@ -1009,15 +1010,62 @@ def backbone_linear_pair(x: torch.Tensor, sv_a: torch.Tensor, sv_b: torch.Tensor
     return out_a, out_b
 
 
-SWIGLU_BACKBONE_MAX_ROWS = 64  # rows of tris_backbone_swiglu_linear
+def backbone_scatter_ok(tokens: int, sv_a, sv_b) -> bool:
+    """True when backbone_linear_pair_scatter can run: two fp16 SV matrices of one shape that the tiled GEMM takes
+    (tokens >= 512, rank a multiple of 128, in_features of 32)."""
+    if not all(isinstance(sv, torch.Tensor) and sv.dtype == torch.float16 and sv.dim() == 2 and sv.is_contiguous()
+               and sv.data_ptr() % 16 == 0 for sv in (sv_a, sv_b)):
+        return False
+    rank, in_f = int(sv_a.size(0)), int(sv_a.size(1))
+    return sv_a.shape == sv_b.shape and tokens >= 512 and rank % 128 == 0 and rank > 0 and in_f % 32 == 0 and in_f > 0
+
+
+def backbone_linear_pair_scatter(x: torch.Tensor, sv_a: torch.Tensor, sv_b: torch.Tensor, inverse_perm: torch.Tensor,
+                                 top_k: int, out_rows: int, in_scale_a: torch.Tensor | None = None,
+                                 in_scale_b: torch.Tensor | None = None):
+    """The gate and up backbones of the tokens x written to their routed rows (tris_backbone_linear_pair_scatter,
+    an extension): out[inverse_perm[t * top_k + j]] = fp16(x[t] * in_scale) @ sv^T, the rows the reference's
+    compute_shared_hidden gives for x[perm] (qlinear_cuda.py:4454-4502), with each token projected once and no
+    gathered copy of the rows.  Returns two fp16 [out_rows, rank] tensors (rows no slot names are unset)."""
+    _check_cuda("x", x, torch.float16, 2)
+    _check_cuda("shared_sv_a", sv_a, torch.float16, 2, x.device)
+    _check_cuda("shared_sv_b", sv_b, torch.float16, 2, x.device)
+    _check_cuda("inverse_perm", inverse_perm, torch.int32, 1, x.device)
+    if sv_a.shape != sv_b.shape or sv_a.size(1) != x.size(1):
+        raise RuntimeError("backbone pair shape mismatch")
+    tokens = int(x.size(0))
+    if inverse_perm.numel() != tokens * top_k:
+        raise RuntimeError("inverse_perm must hold tokens * top_k entries")
+    for name, sc in (("in_scale_a", in_scale_a), ("in_scale_b", in_scale_b)):
+        if sc is not None:
+            _check_cuda(name, sc, torch.float16, 1, x.device)
+            if sc.numel() != x.size(1):
+                raise RuntimeError(f"{name} must hold in_features values")
+    rank, in_f = int(sv_a.size(0)), int(sv_a.size(1))
+    out_a = torch.empty((out_rows, rank), dtype=torch.float16, device=x.device)
+    out_b = torch.empty((out_rows, rank), dtype=torch.float16, device=x.device)
+    lib = _lib.load()
+    ws = backbone_workspace(x.device, int(lib.tris_backbone_scatter_workspace_bytes(tokens, in_f, rank, 2)))
+    _lib.check(lib.tris_backbone_linear_pair_scatter(_ptr(x), tokens, in_f, _ptr(sv_a), _ptr(sv_b), rank,
+                                                     _ptr(in_scale_a), _ptr(in_scale_b), _ptr(inverse_perm), int(top_k),
+                                                     int(out_rows), _ptr(out_a), _ptr(out_b), _ptr(ws),
+                                                     int(ws.numel()), _stream(x)),
+               "tris_backbone_linear_pair_scatter")
+    return out_a, out_b
+
+
+SWIGLU_BACKBONE_MAX_ROWS = 64  # rows of tris_backbone_swiglu_linear's decode kernel; more take the tiled GEMM
 
 
 def backbone_swiglu_ok(gate: torch.Tensor, sv, in_scale: torch.Tensor | None = None) -> bool:
-    """True when backbone_swiglu_linear can run: an fp16 SV matrix, at most SWIGLU_BACKBONE_MAX_ROWS rows, a
-    multiple of 32 columns and 16-byte aligned contiguous tensors."""
+    """True when backbone_swiglu_linear can run: an fp16 SV matrix, a multiple of 32 columns, 16-byte aligned
+    contiguous tensors, and either at most SWIGLU_BACKBONE_MAX_ROWS rows or a rank that is a multiple of 128
+    (the tiled GEMM)."""
     if not isinstance(sv, torch.Tensor) or sv.dtype != torch.float16 or sv.dim() != 2 or not sv.is_contiguous():
         return False
-    if gate.dim() != 2 or int(gate.size(0)) > SWIGLU_BACKBONE_MAX_ROWS or int(gate.size(1)) % 32 != 0:
+    if gate.dim() != 2 or int(gate.size(1)) % 32 != 0:
+        return False
+    if int(gate.size(0)) > SWIGLU_BACKBONE_MAX_ROWS and int(sv.size(0)) % 128 != 0:
         return False
     if int(sv.size(1)) != int(gate.size(1)) or sv.data_ptr() % 16 or gate.data_ptr() % 16:
         return False

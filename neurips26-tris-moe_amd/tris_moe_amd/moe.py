@@ -380,17 +380,25 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
         gather = route["grouped_token_indices"]
     else:
         ext.grouped_block_gr_predecode_multi(pre_jobs, eid)
-        hid_g, hid_u = shared_projection_pair(x16, backbones["gate"], backbones["up"],
-                                              row_index=route["grouped_token_indices"], in_scale_a=sc["gate"],
-                                              in_scale_b=sc["up"])
+        tokens = int(x16.size(0))
+        if R % tokens == 0 and ext.backbone_scatter_ok(tokens, backbones["gate"], backbones["up"]):
+            # each token projected once and stored to the rows the route sends it to (no gathered copy)
+            hid_g, hid_u = ext.backbone_linear_pair_scatter(x16, backbones["gate"], backbones["up"],
+                                                            route["inverse_perm"], R // tokens, R,
+                                                            in_scale_a=sc["gate"], in_scale_b=sc["up"])
+        else:
+            hid_g, hid_u = shared_projection_pair(x16, backbones["gate"], backbones["up"],
+                                                  row_index=route["grouped_token_indices"], in_scale_a=sc["gate"],
+                                                  in_scale_b=sc["up"])
         gather = None
     if ns_side is not None:
         main.wait_stream(ns_side)
     names = ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix", "c_map", "g_idx", "col_pack3", "row_pack3")
     # every routed row lies in a segment, so the outputs need no zero fill
-    mlp = torch.empty((R, n_mlp), dtype=torch.float16, device=dev)
+    mlp = None
     hid_d = None
     if R <= FUSED_SWIGLU_MAX_ROWS and comp_g is None and comp_u is None:
+        mlp = torch.empty((R, n_mlp), dtype=torch.float16, device=dev)
         # few rows: the gate/up GEMM with act_fn(g) * u in its epilogue (one launch)
         ext.compact3_tris_precomputed_grouped_swiglu_forward_block_gr_predecoded(
             hid_g, hid_u, eid, seg, prob, tile_bound, decoded["gate"], *[pg[k] for k in names], decoded["up"],
@@ -409,6 +417,7 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
             hid_d = ext.backbone_swiglu_linear(g, u, backbones["down"], in_scale=sc["down"])
         else:
             # g + comp_g and u + comp_u (fp16 adds) inside act_fn(g) * u
+            mlp = torch.empty((R, n_mlp), dtype=torch.float16, device=dev)
             ext.swiglu_mul(g, u, out=mlp, comp_gate=comp_g, comp_up=comp_u)
     n_out = int(pd["qweight1"].size(2))
     comp_d = None

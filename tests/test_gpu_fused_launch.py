@@ -226,10 +226,11 @@ def test_layer_with_router_backbone_launch_matches_oracle(tris, oracle_mod, cuda
     assert_close(np.concatenate(outs), np.concatenate(wants), f"layer T={tokens}")
 
 
-@pytest.mark.parametrize("rows,scaled", [(1, False), (16, True), (33, False), (64, True)])
+@pytest.mark.parametrize("rows,scaled", [(1, False), (16, True), (33, False), (64, True), (100, True), (600, False)])
 def test_backbone_swiglu_product_is_exact(tris, cuda, rows, scaled):
     """With SV the identity, the fused down backbone returns its operand: the product fp16(silu(g) * u)
-    (times the input scale) must be swiglu_mul's bits (one product per output, nothing rounds twice)."""
+    (times the input scale) must be swiglu_mul's bits (one product per output, nothing rounds twice).  Above 64
+    rows the tiled GEMM forms the product in its operand staging."""
     note(f"backbone swiglu identity rows={rows} scaled={scaled}")
     ext = tris["ext"]
     n = 256
@@ -245,10 +246,12 @@ def test_backbone_swiglu_product_is_exact(tris, cuda, rows, scaled):
     assert torch.equal(got, want)
 
 
-@pytest.mark.parametrize("rows,in_f,rank", [(32, 14336, 512), (16, 1024, 256), (64, 512, 128), (7, 4096, 64)])
+@pytest.mark.parametrize("rows,in_f,rank", [(32, 14336, 512), (16, 1024, 256), (64, 512, 128), (7, 4096, 64),
+                                             (300, 2048, 256), (600, 14336, 512), (1000, 1056, 128)])
 def test_backbone_swiglu_matches_unfused(tris, cuda, rows, in_f, rank):
-    """The fused down backbone against swiglu_mul followed by backbone_linear (the split over K differs, so the
-    fp32 sums agree within rounding) and against an fp32 reference."""
+    """The fused down backbone against swiglu_mul followed by backbone_linear (below 512 rows the split over K
+    differs, so the fp32 sums agree within rounding; from 512 rows both run the tiled GEMM with the same slices
+    and give the same bits) and against an fp32 reference."""
     note(f"backbone swiglu rows={rows} in={in_f} rank={rank}")
     ext = tris["ext"]
     rng = np.random.default_rng(in_f + rows)
@@ -263,8 +266,39 @@ def test_backbone_swiglu_matches_unfused(tris, cuda, rows, in_f, rank):
     ref = ((mlp * sc).float() @ sv.float().t()).cpu().numpy()
     assert_close(got.float().cpu().numpy(), ref, "fused vs fp32")
     assert_close(got.float().cpu().numpy(), unfused.float().cpu().numpy(), "fused vs unfused")
+    if rows >= ext.BACKBONE_GEMM_MIN_ROWS:
+        assert torch.equal(got, unfused)
     again = ext.backbone_swiglu_linear(g, u, sv, in_scale=sc)
     assert torch.equal(got, again)  # slices added in fixed order
+
+
+@pytest.mark.parametrize("tokens,in_f,rank,top_k", [(512, 4096, 512, 2), (1024, 2048, 256, 8), (700, 1056, 128, 3)])
+def test_backbone_pair_scatter_matches_token_projection(tris, cuda, tokens, in_f, rank, top_k):
+    """The gate/up backbones written to routed rows: row inverse_perm[t, j] holds the pair's projection of token t
+    (the same tiled GEMM over the tokens, so the same bits), slots of -1 write nothing, and the rows equal the
+    fp32 product of the gathered rows within rounding."""
+    note(f"backbone pair scatter T={tokens} in={in_f} rank={rank} k={top_k}")
+    ext = tris["ext"]
+    rng = np.random.default_rng(tokens + in_f)
+    x = torch.from_numpy(rng.standard_normal((tokens, in_f)).astype(np.float16)).to(cuda)
+    sv_a = torch.from_numpy((rng.standard_normal((rank, in_f)) * 0.02).astype(np.float16)).to(cuda)
+    sv_b = torch.from_numpy((rng.standard_normal((rank, in_f)) * 0.02).astype(np.float16)).to(cuda)
+    sc = torch.from_numpy(rng.uniform(0.5, 1.5, in_f).astype(np.float16)).to(cuda)
+    R = tokens * top_k
+    inv = rng.permutation(R).astype(np.int32)
+    inv[rng.choice(R, 5, replace=False)] = -1  # slots routed nowhere
+    assert ext.backbone_scatter_ok(tokens, sv_a, sv_b)
+    out_a, out_b = ext.backbone_linear_pair_scatter(x, sv_a, sv_b, torch.from_numpy(inv).to(cuda), top_k, R,
+                                                    in_scale_b=sc)
+    ta, tb = ext.backbone_linear_pair(x, sv_a, sv_b, in_scale_b=sc)
+    slot_token = np.repeat(np.arange(tokens), top_k)
+    ok = inv >= 0
+    rows = torch.from_numpy(inv[ok].astype(np.int64)).to(cuda)
+    toks = torch.from_numpy(slot_token[ok]).to(cuda)
+    assert torch.equal(out_a.index_select(0, rows), ta.index_select(0, toks))
+    assert torch.equal(out_b.index_select(0, rows), tb.index_select(0, toks))
+    ref = ((x * sc).float() @ sv_b.float().t()).index_select(0, toks).cpu().numpy()
+    assert_close(out_b.index_select(0, rows).float().cpu().numpy(), ref, "scatter vs fp32")
 
 
 PROLOGUE_CASES = [

@@ -816,17 +816,17 @@ def test_run_grouped_structured_api(tris, oracle_mod, cuda):
 @pytest.mark.parametrize("tokens,in_f,rank", [(1, 4096, 512), (16, 4096, 512), (5, 14336, 512), (37, 2048, 256),
                                               (4, 1000, 100), (64, 4096, 512), (70, 1001, 48), (300, 4096, 512),
                                               (512, 4096, 512), (1000, 14336, 512), (2048, 4096, 512),
-                                              (600, 2048, 256), (4096, 512, 256), (700, 1000, 128)])
-def test_backbone_matches_fp32(tris, cuda, tokens, in_f, rank, monkeypatch):
+                                              (600, 2048, 256), (4096, 512, 256), (700, 1000, 128),
+                                              (520, 1056, 128), (513, 96, 256)])
+def test_backbone_matches_fp32(tris, cuda, tokens, in_f, rank):
     """Decode-sized inputs run the split-K MFMA kernel (1 to 4 token tiles per workgroup: 37 tokens are 3,
     64 are 4, 70 are a group of 4 and a partial one; 1001 columns take the element-wise loads); from
-    ext.BACKBONE_GEMM_MIN_ROWS rows with rank a multiple of 128 and in_features of 64 the tiled split-K GEMM
-    (partial 128-row tiles, 1 to 16 slices, one slice at K = 512); otherwise from ext.BACKBONE_LIBRARY_MIN_ROWS
-    rows and ext.BACKBONE_LIBRARY_MIN_ELEMS activation elements (300 x 4096, and 700 x 1000 columns) the
-    library GEMM.  Gathered rows past the token count project the tokens, then gather."""
+    ext.BACKBONE_GEMM_MIN_ROWS rows with rank a multiple of 128 and in_features of 32 the tiled split-K GEMM
+    (partial 256-row tiles, 1 to 16 slices, an odd stage count at K = 1056, one slice that writes fp16 directly
+    at K = 96 and K = 512); otherwise from ext.BACKBONE_LIBRARY_MIN_ROWS rows and ext.BACKBONE_LIBRARY_MIN_ELEMS
+    activation elements (300 x 4096, and 700 x 1000 columns) the library GEMM.  Gathered rows past the token
+    count project the tokens, then gather."""
     note(f"backbone T={tokens} in={in_f} rank={rank}")
-    # the layer keeps the library GEMM at these sizes; the test sends them to the C entry's tiled GEMM
-    monkeypatch.setattr(tris["ext"], "BACKBONE_GEMM_MIN_ROWS", 512)
     rng = np.random.default_rng(tokens + in_f)
     x = rng.standard_normal((tokens, in_f)).astype(np.float16)
     sv = (rng.standard_normal((rank, in_f)) * 0.02).astype(np.float16)
