@@ -314,40 +314,61 @@ __global__ __launch_bounds__(kBgThreads, 2) void backbone_gemm_kernel(BgArgs g) 
   }
 }
 
-// The slice reduction of a token-row projection written to routed rows: element (t, n) of projection q is
-// added in slice order, rounded once and stored to row inverse_perm[t * top_k + j] of proj[q].out for every
-// slot j (the rows the route sends token t to; -1 and rows past out_rows are skipped).
-__global__ __launch_bounds__(256) void backbone_reduce_scatter_kernel(BackboneArgs a, const int32_t* __restrict__ inv,
-                                                                      int top_k, int out_rows) {
+// The slice reductions of the tiled GEMMs (rank a multiple of 128): four neighbouring outputs a thread, each the
+// slices' partial sums added in slice order and rounded once (the bits of backbone_reduce_kernel), 16-byte loads.
+// With inv (the route's inverse_perm) element (t, n) of projection q is stored to row inv[t * top_k + j] of
+// proj[q].out for every slot j (the rows the route sends token t to; -1 and rows past out_rows are skipped).
+__global__ __launch_bounds__(256) void backbone_reduce4_kernel(BackboneArgs a, const int32_t* __restrict__ inv,
+                                                               int top_k, int out_rows) {
   const int q = static_cast<int>(blockIdx.y);
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t i4 = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
   const int64_t count = static_cast<int64_t>(a.tokens) * a.rank;
-  if (idx >= count) return;
-  const float* src = a.partials + static_cast<int64_t>(q) * a.slices * count + idx;
-  float v[kBgMaxSlices];
-#pragma unroll
-  for (int sl = 0; sl < kBgMaxSlices; ++sl) v[sl] = sl < a.slices ? src[sl * count] : 0.0f;  // loads in flight together
-  float sum = 0.0f;
+  if (i4 >= count) return;
+  const float* src = a.partials + static_cast<int64_t>(q) * a.slices * count + i4;
+  float4 v[kBgMaxSlices];
 #pragma unroll
   for (int sl = 0; sl < kBgMaxSlices; ++sl) {
-    if (sl < a.slices) sum += v[sl];
+    v[sl] = sl < a.slices ? *reinterpret_cast<const float4*>(src + sl * count) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  const uint16_t h = f2h_bits(sum);
-  const int t = static_cast<int>(idx / a.rank);
-  const int n = static_cast<int>(idx - static_cast<int64_t>(t) * a.rank);
+  float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int sl = 0; sl < kBgMaxSlices; ++sl) {
+    if (sl < a.slices) {
+      sum.x += v[sl].x;
+      sum.y += v[sl].y;
+      sum.z += v[sl].z;
+      sum.w += v[sl].w;
+    }
+  }
+  const uint2 h = make_uint2(static_cast<uint32_t>(f2h_bits(sum.x)) | (static_cast<uint32_t>(f2h_bits(sum.y)) << 16),
+                             static_cast<uint32_t>(f2h_bits(sum.z)) | (static_cast<uint32_t>(f2h_bits(sum.w)) << 16));
   uint16_t* out = q == 0 ? a.proj[0].out : a.proj[1].out;
+  if (inv == nullptr) {
+    *reinterpret_cast<uint2*>(out + i4) = h;
+    return;
+  }
+  const int t = static_cast<int>(i4 / a.rank);
+  const int n = static_cast<int>(i4 - static_cast<int64_t>(t) * a.rank);
   for (int j = 0; j < top_k; ++j) {
     const int row = inv[static_cast<int64_t>(t) * top_k + j];
-    if (row >= 0 && row < out_rows) out[static_cast<int64_t>(row) * a.rank + n] = h;
+    if (row >= 0 && row < out_rows) *reinterpret_cast<uint2*>(out + static_cast<int64_t>(row) * a.rank + n) = h;
   }
+}
+
+static int launch_backbone_reduce4(const BackboneArgs& args, int nproj, hipStream_t s, const char* who,
+                                   const int32_t* inv = nullptr, int top_k = 0, int out_rows = 0) {
+  const int64_t quads = static_cast<int64_t>(args.tokens) * args.rank / 4;
+  hipLaunchKernelGGL(backbone_reduce4_kernel, dim3(static_cast<unsigned>((quads + 255) / 256), nproj), dim3(256), 0,
+                     s, args, inv, top_k, out_rows);
+  return check_launch(who);
 }
 
 // The SwiGLU form of the tiled GEMM with each product formed once: a workgroup of eight wavefronts covers a
 // 128 x 512 tile (rows x rank columns; wavefront (wm, wn) of 2 x 4 owns a 64 x 128 quadrant, 4 x 8 tiles of
 // v_mfma_f32_16x16x32_f16), so act_fn(g) * u of a row is formed by one workgroup per K slice, not by every
-// 128-column tile of the rank (the SiLU takes about 30 VALU per element, more than the MFMA time per element of
-// a 128-column tile).  Per 32-column stage a thread forms 8 products and copies four 16-byte SV runs; stages are
-// double-buffered in LDS (100 KB), one workgroup per CU.  Rank columns past the rank are computed on clamped SV
+// 128-column tile of the rank (SiLU's exponential and reciprocal run at a quarter of the VALU rate).  Per
+// 32-column stage a thread forms 8 products and copies four 16-byte SV runs; stages are double-buffered in LDS
+// (100 KB, one workgroup per CU) and their global loads issued two stages ahead.  Rank columns past the rank are computed on clamped SV
 // rows and not written.  Tiles are ordered (slice, row tile, column tile) and handed out XCD-major, so the
 // workgroups of one K slice share its SV rows through one L2.
 constexpr int kBwM = 128;
@@ -459,17 +480,19 @@ __global__ __launch_bounds__(kBwThreads, 1) void backbone_swiglu_gemm_kernel(BgA
       for (int j = 0; j < 8; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv[j], acc[i][j], 0, 0, 0);
     }
   };
-  Regs R0;
+  // stage st sits in buffer st % 2; its loads were issued two stages ahead, into register set st % 2
+  Regs R0, R1;
   issue(0, R0);
+  if (nstage > 1) issue(1, R1);
   write(R0, la0, lb0);
   __syncthreads();
   for (int st = 0; st < nstage; st += 2) {
-    if (st + 1 < nstage) issue(st + 1, R0);
+    if (st + 2 < nstage) issue(st + 2, R0);
     compute(la0, lb0);
-    if (st + 1 < nstage) write(R0, la1, lb1);
+    if (st + 1 < nstage) write(R1, la1, lb1);
     __syncthreads();
     if (st + 1 < nstage) {
-      if (st + 2 < nstage) issue(st + 2, R0);
+      if (st + 3 < nstage) issue(st + 3, R1);
       compute(la1, lb1);
       if (st + 2 < nstage) write(R0, la0, lb0);
       __syncthreads();
@@ -512,7 +535,7 @@ static int launch_backbone_swiglu_gemm(const BackboneArgs& base, const uint16_t*
   hipLaunchKernelGGL(backbone_swiglu_gemm_kernel, dim3(static_cast<unsigned>(wgs)), dim3(kBwThreads), 0, s, g);
   int rc = check_launch(who);
   if (rc || g.direct) return rc;
-  return launch_backbone_reduce(g.b, 1, s, who);
+  return launch_backbone_reduce4(g.b, 1, s, who);
 }
 
 // base: x, row_index, proj[], partials, tokens, in_features, rank; slices are set here.
@@ -533,13 +556,7 @@ static int launch_backbone_gemm(const BackboneArgs& base, int nproj, hipStream_t
   hipLaunchKernelGGL((backbone_gemm_kernel<2>), grid, dim3(kBgThreads), 0, s, g);
   int rc = check_launch(who);
   if (rc || g.direct) return rc;
-  if (scatter != nullptr) {
-    const int64_t count = static_cast<int64_t>(base.tokens) * base.rank;
-    hipLaunchKernelGGL(backbone_reduce_scatter_kernel, dim3(static_cast<unsigned>((count + 255) / 256), nproj),
-                       dim3(256), 0, s, g.b, scatter, top_k, out_rows);
-    return check_launch(who);
-  }
-  return launch_backbone_reduce(g.b, nproj, s, who);
+  return launch_backbone_reduce4(g.b, nproj, s, who, scatter, top_k, out_rows);
 }
 
 int launch_backbone(const uint16_t* x, int tokens, int in_features, const int64_t* row_index, const uint16_t* sv_a,

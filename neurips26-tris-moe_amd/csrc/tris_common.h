@@ -42,11 +42,20 @@ __device__ __forceinline__ uint16_t hadd_bits(uint16_t a, uint16_t b) {
 }
 
 // The reference's gated activation act_fn(g) * u for fp16 g, u (modeling_mixtral.py:496): SiLU in fp32
-// rounded to fp16, then the fp16 product.
+// rounded to fp16, then the fp16 product.  silu(g) = g / (1 + e^-g) is evaluated with the hardware's base-2
+// exponential and reciprocal (e^x = 2^(x log2 e), v_exp_f32 and v_rcp_f32, about 1 ulp each): the fp32 value is
+// within a few tens of fp32 ulps of the correctly rounded quotient, so after the rounding to fp16 it is the
+// IEEE-division value or one fp16 ulp from it (inf, -inf, NaN and the overflow of e^-g give the same results:
+// -inf / inf is NaN, g / inf is -0).  The division sequence took about 30 VALU per element, which bounded the
+// prefill kernels that form the product in their operand staging.  The quotient is formed from |g| and takes g's
+// sign bit afterwards: the compiler turns a rounded fp16 product into v_fma_mix with a +0 addend, which would make
+// silu(-0) = -0 a +0.
 __device__ __forceinline__ uint16_t swiglu_bits(uint16_t g16, uint16_t u16) {
   const float g = h2f(g16);
-  const float sg = h2f(f2h_bits(g / (1.0f + expf(-g))));
-  return f2h_bits(sg * h2f(u16));
+  const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);  // e^-g
+  const uint16_t mag = f2h_bits(__builtin_fabsf(g) * __builtin_amdgcn_rcpf(1.0f + e));
+  const uint16_t sg = static_cast<uint16_t>(mag | (g16 & 0x8000u));
+  return f2h_bits(h2f(sg) * h2f(u16));
 }
 
 __device__ __forceinline__ uint32_t low_mask(int bits) {
