@@ -20,7 +20,15 @@ constexpr int kBbMaxSlices = 32;        // slices of backbone_kernel
 constexpr int kBgM = 256;            // rows of a workgroup tile
 constexpr int kBgN = 128;            // rank columns of a workgroup tile
 constexpr int kBgK = 32;             // K columns per LDS stage
-constexpr int kBgStride = kBgK + 8;  // fp16 per staged row: 80-byte rows put a wavefront's 16-byte reads on distinct banks
+constexpr int kBgStride = kBgK;      // fp16 per staged row (64 bytes, four 16-byte chunks; see bg_chunk)
+
+// LDS position (fp16 offset) of 16-byte chunk c (0..3) of staged row r: the chunks of a row are permuted by
+// f(r) = ((r >> 1) ^ (r >> 3)) & 3, so the 16 rows an MFMA operand read touches (one chunk each) and the four
+// rows x four chunks a wavefront's copy writes (16 lanes a pass) fall on distinct banks, for 32 banks and 8
+// lanes a pass as for 64 banks and 16 lanes.
+__device__ __forceinline__ int bg_chunk(int r, int c) {
+  return r * kBgStride + 8 * (c ^ (((r >> 1) ^ (r >> 3)) & 3));
+}
 constexpr int kBgThreads = 256;
 constexpr int kBgMinRows = 512;      // rows from which the entry points take it
 constexpr int kBgMinStages = 16;     // K stages per slice at least

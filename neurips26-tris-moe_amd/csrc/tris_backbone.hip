@@ -128,8 +128,8 @@ int backbone_prepare(const uint16_t* x, int tokens, int in_features, const int64
 // 256 x 128 tile (rows x rank columns) of one projection and slice;
 // its four wavefronts each own a 128 x 64 quadrant (8 x 4 tiles of v_mfma_f32_16x16x32_f16), so every 16-byte
 // LDS read feeds 4 or 8 MFMAs: per 32-column stage a CU (two workgroups) reads 96 KB and writes 48 KB of LDS
-// for 2 x 512 MFMA cycles per SIMD.  Stages are double-buffered in LDS (60 KB a workgroup) with one barrier a
-// stage; the global loads of the next kDepth stages are in flight in registers meanwhile.  Tiles are ordered
+// for 2 x 512 MFMA cycles per SIMD.  Stages are double-buffered in LDS (48 KB a workgroup) with one barrier a
+// stage; the global loads of the next two stages are in flight in registers meanwhile.  Tiles are ordered
 // (projection, slice, row tile, column tile) and handed out XCD-major: the four column tiles of a row tile run
 // on one XCD, whose L2 then serves the row tile's activations to all four.  Slices write fp32 partial tiles
 // that backbone_reduce_kernel adds in slice order (one slice writes fp16 directly), so the result does not
@@ -173,7 +173,6 @@ struct BgStage {
   uint4 sc;    // in_scale of the thread's 8 columns
 };
 
-template <int kDepth>
 __global__ __launch_bounds__(kBgThreads, 2) void backbone_gemm_kernel(BgArgs g) {
   __shared__ __attribute__((aligned(16))) uint16_t la0[kBgM * kBgStride];
   __shared__ __attribute__((aligned(16))) uint16_t la1[kBgM * kBgStride];
@@ -208,7 +207,7 @@ __global__ __launch_bounds__(kBgThreads, 2) void backbone_gemm_kernel(BgArgs g) 
   const int nstage = kn / kBgK;
   // copy slots: run i of the thread is row (tid / 4) + 64 i of the tile, columns 8 (tid % 4) .. + 8 of the stage;
   // rows past the batch read the batch's last row (their outputs are not written)
-  const int crow = tid >> 2, ccol = (tid & 3) * 8;
+  const int crow = tid >> 2, cchunk = tid & 3, ccol = cchunk * 8;
   const uint16_t* xsrc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -242,10 +241,10 @@ __global__ __launch_bounds__(kBgThreads, 2) void backbone_gemm_kernel(BgArgs g) 
       for (int h = 0; h < 4; ++h) {
         pw[h] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, xw[h]) * __builtin_bit_cast(h2, sw[h]));
       }
-      *reinterpret_cast<uint4*>(&la[(crow + 64 * i) * kBgStride + ccol]) = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+      *reinterpret_cast<uint4*>(&la[bg_chunk(crow + 64 * i, cchunk)]) = make_uint4(pw[0], pw[1], pw[2], pw[3]);
     }
-    *reinterpret_cast<uint4*>(&lb[crow * kBgStride + ccol]) = R.b[0];
-    *reinterpret_cast<uint4*>(&lb[(crow + 64) * kBgStride + ccol]) = R.b[1];
+    *reinterpret_cast<uint4*>(&lb[bg_chunk(crow, cchunk)]) = R.b[0];
+    *reinterpret_cast<uint4*>(&lb[bg_chunk(crow + 64, cchunk)]) = R.b[1];
   };
   f32x4 acc[8][4];
 #pragma unroll
@@ -257,40 +256,49 @@ __global__ __launch_bounds__(kBgThreads, 2) void backbone_gemm_kernel(BgArgs g) 
     f16x8 bv[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      bv[j] = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&lb[(64 * wn + 16 * j + i16) * kBgStride + 8 * kg]));
+      bv[j] = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&lb[bg_chunk(64 * wn + 16 * j + i16, kg)]));
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const f16x8 av =
-          __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&la[(128 * wm + 16 * i + i16) * kBgStride + 8 * kg]));
+          __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&la[bg_chunk(128 * wm + 16 * i + i16, kg)]));
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv[j], acc[i][j], 0, 0, 0);
     }
   };
 
-  // stage st sits in buffer st % 2; register set R[kDepth == 2 ? st % 2 : 0] carries it from its loads to LDS
+  // One stage: the MFMAs of the buffer in LDS, the LDS writes of the next stage (registers loaded a stage
+  // ago) into the other buffer and the global loads of the stage after it, interleaved so the matrix cores
+  // keep issuing while the copies move.  Stage indices past the slice are clamped (a re-read, never used),
+  // and the extra write lands in a buffer nobody reads before the next barrier.
+  auto half = [&](const uint16_t* la, const uint16_t* lb, const BgStage& Rw, uint16_t* law, uint16_t* lbw, int sti,
+                  BgStage& Ri) {
+    issue(sti, Ri);
+    compute(la, lb);
+    write(Rw, law, lbw);
+    __builtin_amdgcn_sched_group_barrier(0x020, 7, 0);  // the global loads first
+    __builtin_amdgcn_sched_group_barrier(0x100, 5, 0);  // B fragments and the first A fragment
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // the MFMAs of A fragment i
+      if (i < 7) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (i < 6) {
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+      }
+    }
+  };
+  // stage st sits in buffer st % 2; register set st % 2 carries it from its loads (two stages ahead) to LDS
   BgStage R0, R1;
   issue(0, R0);
-  if (kDepth == 2 && nstage > 1) issue(1, R1);
+  issue(nstage > 1 ? 1 : 0, R1);
   write(R0, la0, lb0);
   __syncthreads();
   for (int st = 0; st < nstage; st += 2) {
-    if (kDepth == 1) {
-      if (st + 1 < nstage) issue(st + 1, R0);
-    } else if (st + 2 < nstage) {
-      issue(st + 2, R0);
-    }
-    compute(la0, lb0);
-    if (st + 1 < nstage) write(kDepth == 1 ? R0 : R1, la1, lb1);
+    half(la0, lb0, R1, la1, lb1, st + 2 < nstage ? st + 2 : nstage - 1, R0);
     __syncthreads();
     if (st + 1 < nstage) {
-      if (kDepth == 1) {
-        if (st + 2 < nstage) issue(st + 2, R0);
-      } else if (st + 3 < nstage) {
-        issue(st + 3, R1);
-      }
-      compute(la1, lb1);
-      if (st + 2 < nstage) write(R0, la0, lb0);
+      half(la1, lb1, R0, la0, lb0, st + 3 < nstage ? st + 3 : nstage - 1, R1);
       __syncthreads();
     }
   }
@@ -368,7 +376,7 @@ static int launch_backbone_reduce4(const BackboneArgs& args, int nproj, hipStrea
 // v_mfma_f32_16x16x32_f16), so act_fn(g) * u of a row is formed by one workgroup per K slice, not by every
 // 128-column tile of the rank (SiLU's exponential and reciprocal run at a quarter of the VALU rate).  Per
 // 32-column stage a thread forms 8 products and copies four 16-byte SV runs; stages are double-buffered in LDS
-// (100 KB, one workgroup per CU) and their global loads issued two stages ahead.  Rank columns past the rank are computed on clamped SV
+// (80 KB, one workgroup per CU) and their global loads issued two stages ahead.  Rank columns past the rank are computed on clamped SV
 // rows and not written.  Tiles are ordered (slice, row tile, column tile) and handed out XCD-major, so the
 // workgroups of one K slice share its SV rows through one L2.
 constexpr int kBwM = 128;
@@ -419,7 +427,7 @@ __global__ __launch_bounds__(kBwThreads, 1) void backbone_swiglu_gemm_kernel(BgA
   const int nstage = kn / kBgK;
   // copy slots: the thread's g/u run is row tid / 4 of the tile, its SV runs rows tid / 4 + 128 i, columns
   // 8 (tid % 4) .. + 8 of the stage (rows past the batch or the rank read the last valid row)
-  const int crow = tid >> 2, ccol = (tid & 3) * 8;
+  const int crow = tid >> 2, cchunk = tid & 3, ccol = cchunk * 8;
   int m = m0 + crow;
   m = m < a.tokens ? m : a.tokens - 1;
   const uint16_t* gsrc = a.x + static_cast<int64_t>(m) * K + kbeg + ccol;
@@ -456,9 +464,9 @@ __global__ __launch_bounds__(kBwThreads, 1) void backbone_swiglu_gemm_kernel(BgA
       const uint32_t hi = swiglu_bits(static_cast<uint16_t>(gw[h] >> 16), static_cast<uint16_t>(uw[h] >> 16));
       pw[h] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, lo | (hi << 16)) * __builtin_bit_cast(h2, sw[h]));
     }
-    *reinterpret_cast<uint4*>(&la[crow * kBgStride + ccol]) = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+    *reinterpret_cast<uint4*>(&la[bg_chunk(crow, cchunk)]) = make_uint4(pw[0], pw[1], pw[2], pw[3]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&lb[(crow + 128 * i) * kBgStride + ccol]) = R.b[i];
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&lb[bg_chunk(crow + 128 * i, cchunk)]) = R.b[i];
   };
   f32x4 acc[4][8];
 #pragma unroll
@@ -470,31 +478,48 @@ __global__ __launch_bounds__(kBwThreads, 1) void backbone_swiglu_gemm_kernel(BgA
     f16x8 bv[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      bv[j] = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&lb[(128 * wn + 16 * j + i16) * kBgStride + 8 * kg]));
+      bv[j] = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&lb[bg_chunk(128 * wn + 16 * j + i16, kg)]));
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const f16x8 av =
-          __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&la[(64 * wm + 16 * i + i16) * kBgStride + 8 * kg]));
+          __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(&la[bg_chunk(64 * wm + 16 * i + i16, kg)]));
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv[j], acc[i][j], 0, 0, 0);
     }
   };
-  // stage st sits in buffer st % 2; its loads were issued two stages ahead, into register set st % 2
+  // one stage as in backbone_gemm_kernel: MFMAs, the next stage's SwiGLU products and LDS writes, and the global
+  // loads of the stage after it, interleaved
+  auto half = [&](const uint16_t* la, const uint16_t* lb, const Regs& Rw, uint16_t* law, uint16_t* lbw, int sti,
+                  Regs& Ri) {
+    issue(sti, Ri);
+    compute(la, lb);
+    write(Rw, law, lbw);
+    __builtin_amdgcn_sched_group_barrier(0x020, 7, 0);  // the global loads first
+    __builtin_amdgcn_sched_group_barrier(0x100, 9, 0);  // B fragments and the first A fragment
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // SwiGLU products
+      }
+      if (i < 3) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (i == 0) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+    }
+  };
+  // stage st sits in buffer st % 2; register set st % 2 carries it from its loads (two stages ahead) to LDS
   Regs R0, R1;
   issue(0, R0);
-  if (nstage > 1) issue(1, R1);
+  issue(nstage > 1 ? 1 : 0, R1);
   write(R0, la0, lb0);
   __syncthreads();
   for (int st = 0; st < nstage; st += 2) {
-    if (st + 2 < nstage) issue(st + 2, R0);
-    compute(la0, lb0);
-    if (st + 1 < nstage) write(R1, la1, lb1);
+    half(la0, lb0, R1, la1, lb1, st + 2 < nstage ? st + 2 : nstage - 1, R0);
     __syncthreads();
     if (st + 1 < nstage) {
-      if (st + 3 < nstage) issue(st + 3, R1);
-      compute(la1, lb1);
-      if (st + 2 < nstage) write(R0, la0, lb0);
+      half(la1, lb1, R0, la0, lb0, st + 3 < nstage ? st + 3 : nstage - 1, R1);
       __syncthreads();
     }
   }
@@ -553,7 +578,7 @@ static int launch_backbone_gemm(const BackboneArgs& base, int nproj, hipStream_t
   const int64_t wgs = static_cast<int64_t>(g.m_tiles) * g.n_tiles * slices * nproj;
   TRIS_REQUIRE(wgs <= 2147483647, "%s: grid too large", who);
   const dim3 grid(static_cast<unsigned>(wgs));
-  hipLaunchKernelGGL((backbone_gemm_kernel<2>), grid, dim3(kBgThreads), 0, s, g);
+  hipLaunchKernelGGL(backbone_gemm_kernel, grid, dim3(kBgThreads), 0, s, g);
   int rc = check_launch(who);
   if (rc || g.direct) return rc;
   return launch_backbone_reduce4(g.b, nproj, s, who, scatter, top_k, out_rows);
