@@ -14,6 +14,8 @@
 // joins it without a launch of its own.  The gated variant joins a shared
 // expert through its sigmoid gate, as the Qwen blocks do
 // (modeling_qwen2_moe.py:815-818, modeling_qwen3_5_moe.py:186-188).
+#include <type_traits>
+
 #include "tris_common.h"
 
 // Every fp16 / bf16 rounding written here is one the reference performs (each torch op rounds its result), so
@@ -57,7 +59,8 @@ __device__ __forceinline__ float round_dt(float f) {
 // Every workgroup of a token reduces the gate's dot product itself (fixed order: per-thread fp32 sums of
 // exact products, the wavefront sum, then the four wavefronts in order), so no launch or grid-wide step is
 // added.  Without kGated, the shared output (if any) is added to the fp32 routed sum before the one rounding.
-template <bool kBf16, bool kGated>
+// kK > 0: top_k == kK, every pick's row loaded together; kK == 0: any top_k, one pick at a time.
+template <bool kBf16, bool kGated, int kK>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __restrict__ expert_out,
                                                           const uint16_t* __restrict__ expert_comp,
                                                           const int32_t* __restrict__ inverse_perm,
@@ -101,12 +104,9 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
   float acc[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u) acc[u] = 0.0f;
-  for (int s = 0; s < top_k; ++s) {
-    const int row = inverse_perm[static_cast<int64_t>(t) * top_k + s];
-    if (row < 0) continue;  // a pick the route left out (expert id outside [0, num_experts))
-    const __half w = __ushort_as_half(weights[static_cast<int64_t>(t) * top_k + s]);
+  // one slot's rows (and compensation) at column h0 into v, c
+  auto load_row = [&](int row, uint16_t v[8], uint16_t c[8]) {
     const uint16_t* src = expert_out + static_cast<int64_t>(row) * hidden + h0;
-    uint16_t v[8];
     if (vec) {
       *reinterpret_cast<uint4*>(v) = *reinterpret_cast<const uint4*>(src);
     } else {
@@ -115,18 +115,49 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
     }
     if (expert_comp != nullptr) {
       const uint16_t* csrc = expert_comp + static_cast<int64_t>(row) * hidden + h0;
-      uint16_t c[8];
       if (vec) {
         *reinterpret_cast<uint4*>(c) = *reinterpret_cast<const uint4*>(csrc);
       } else {
 #pragma unroll
         for (int u = 0; u < 8; ++u) c[u] = (h0 + u < hidden) ? csrc[u] : 0;
       }
+    }
+  };
+  auto add_row = [&](uint16_t v[8], const uint16_t c[8], __half w) {
+    if (expert_comp != nullptr) {
 #pragma unroll
       for (int u = 0; u < 8; ++u) v[u] = f16_add_bits(v[u], c[u]);
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) acc[u] += __half2float(__hmul(__ushort_as_half(v[u]), w));
+  };
+  const int32_t* inv = inverse_perm + static_cast<int64_t>(t) * top_k;
+  const uint16_t* wts = weights + static_cast<int64_t>(t) * top_k;
+  if constexpr (kK > 0) {
+    // every pick's index and weight, then every pick's row, in flight together (a pick the route left out,
+    // index -1, reads row 0 and adds nothing); the sum keeps pick order
+    int rows[kK];
+    uint16_t wbits[kK];
+#pragma unroll
+    for (int s = 0; s < kK; ++s) {
+      rows[s] = inv[s];
+      wbits[s] = wts[s];
+    }
+    uint16_t v[kK][8], c[kK][8];
+#pragma unroll
+    for (int s = 0; s < kK; ++s) load_row(rows[s] >= 0 ? rows[s] : 0, v[s], c[s]);
+#pragma unroll
+    for (int s = 0; s < kK; ++s) {
+      if (rows[s] >= 0) add_row(v[s], c[s], __ushort_as_half(wbits[s]));
+    }
+  } else {
+    for (int s = 0; s < top_k; ++s) {
+      const int row = inv[s];
+      if (row < 0) continue;  // a pick the route left out (expert id outside [0, num_experts))
+      uint16_t v[8], c[8];
+      load_row(row, v, c);
+      add_row(v, c, __ushort_as_half(wts[s]));
+    }
   }
   uint16_t* dst = out + static_cast<int64_t>(t) * hidden + h0;
   const uint16_t* ssrc = shared != nullptr ? shared + static_cast<int64_t>(t) * hidden + h0 : nullptr;
@@ -252,20 +283,27 @@ static int combine_launch(const char* who, const uint16_t* expert_out, const uin
   TRIS_REQUIRE(blocks <= 2147483647LL, "%s: too many tokens (%d)", who, tokens);
   const dim3 grid(static_cast<unsigned>(blocks));
   const hipStream_t st = static_cast<hipStream_t>(stream);
+  const auto launch = [&](auto bf16_tag, auto gated_tag, auto k_tag) {
+    hipLaunchKernelGGL((moe_combine_kernel<decltype(bf16_tag)::value, decltype(gated_tag)::value,
+                                           decltype(k_tag)::value>),
+                       grid, dim3(threads), 0, st, expert_out, expert_comp, inverse_perm, weights, shared, gate_in,
+                       gate_w, tokens, top_k, hidden, hblocks, out);
+  };
+  const auto by_k = [&](auto bf16_tag, auto gated_tag) {
+    if (top_k == 2) {
+      launch(bf16_tag, gated_tag, std::integral_constant<int, 2>{});
+    } else if (top_k == 8) {
+      launch(bf16_tag, gated_tag, std::integral_constant<int, 8>{});
+    } else {
+      launch(bf16_tag, gated_tag, std::integral_constant<int, 0>{});
+    }
+  };
   if (out_bf16) {
-    if (gated)
-      hipLaunchKernelGGL((moe_combine_kernel<true, true>), grid, dim3(threads), 0, st, expert_out, expert_comp,
-                         inverse_perm, weights, shared, gate_in, gate_w, tokens, top_k, hidden, hblocks, out);
-    else
-      hipLaunchKernelGGL((moe_combine_kernel<true, false>), grid, dim3(threads), 0, st, expert_out, expert_comp,
-                         inverse_perm, weights, shared, gate_in, gate_w, tokens, top_k, hidden, hblocks, out);
+    if (gated) by_k(std::true_type{}, std::true_type{});
+    else by_k(std::true_type{}, std::false_type{});
   } else {
-    if (gated)
-      hipLaunchKernelGGL((moe_combine_kernel<false, true>), grid, dim3(threads), 0, st, expert_out, expert_comp,
-                         inverse_perm, weights, shared, gate_in, gate_w, tokens, top_k, hidden, hblocks, out);
-    else
-      hipLaunchKernelGGL((moe_combine_kernel<false, false>), grid, dim3(threads), 0, st, expert_out, expert_comp,
-                         inverse_perm, weights, shared, gate_in, gate_w, tokens, top_k, hidden, hblocks, out);
+    if (gated) by_k(std::false_type{}, std::true_type{});
+    else by_k(std::false_type{}, std::false_type{});
   }
   return check_launch(who);
 }

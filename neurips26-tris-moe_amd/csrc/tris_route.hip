@@ -505,7 +505,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_backbone_kernel(RouteArgs
 // router_linear_small_kernel holds.
 constexpr int kRlWaves = 16;
 constexpr int kRlThreads = kRlWaves * kWave;
-constexpr int kRlBatch = 4;
+constexpr int kRlBatch = 8;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
