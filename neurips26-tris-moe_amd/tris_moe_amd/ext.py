@@ -912,10 +912,23 @@ BACKBONE_LIBRARY_MIN_ELEMS = 1 << 19
 # rows) against the library's 2 x 22 us plus two 5.5 us row gathers; 4096 x 14336 -> 512 91 us + 19.7 us against
 # 105.6 us.
 BACKBONE_GEMM_MIN_ROWS = 512
+# Workgroups the tiled GEMM's launch must have to take a shape (it fills the GPU from 512; with few, long
+# workgroups, as for the A3B layer's short rows, the library GEMM is faster).
+BACKBONE_GEMM_MIN_WORKGROUPS = 256
+
+
+def _gemm_workgroups(rows: int, in_features: int, rank: int, tile_m: int = 256, tile_n: int = 128,
+                     target: int = 512) -> int:
+    """Workgroups of one projection of the tiled GEMM (backbone_gemm_slices / backbone_wide_slice_k in
+    tris_backbone.hip): row tiles x column tiles x K slices (at least 16 stages of 32 columns each, at most 16)."""
+    tiles = -(-rows // tile_m) * -(-rank // tile_n)
+    slices = max(1, min(-(-target // tiles), in_features // 512, 16))
+    return tiles * slices
 
 
 def _backbone_gemm_ok(rows: int, in_features: int, rank: int) -> bool:
-    return rows >= BACKBONE_GEMM_MIN_ROWS and rank % 128 == 0 and rank > 0 and in_features % 32 == 0 and in_features > 0
+    return (rows >= BACKBONE_GEMM_MIN_ROWS and rank % 128 == 0 and rank > 0 and in_features % 32 == 0
+            and in_features > 0 and _gemm_workgroups(rows, in_features, rank) >= BACKBONE_GEMM_MIN_WORKGROUPS)
 
 
 def _backbone_use_library(rows: int, in_features: int, rank: int = 0) -> bool:
@@ -1017,7 +1030,7 @@ def backbone_scatter_ok(tokens: int, sv_a, sv_b) -> bool:
                and sv.data_ptr() % 16 == 0 for sv in (sv_a, sv_b)):
         return False
     rank, in_f = int(sv_a.size(0)), int(sv_a.size(1))
-    return sv_a.shape == sv_b.shape and tokens >= 512 and rank % 128 == 0 and rank > 0 and in_f % 32 == 0 and in_f > 0
+    return sv_a.shape == sv_b.shape and _backbone_gemm_ok(tokens, in_f, rank)
 
 
 def backbone_linear_pair_scatter(x: torch.Tensor, sv_a: torch.Tensor, sv_b: torch.Tensor, inverse_perm: torch.Tensor,
@@ -1058,14 +1071,17 @@ SWIGLU_BACKBONE_MAX_ROWS = 64  # rows of tris_backbone_swiglu_linear's decode ke
 
 
 def backbone_swiglu_ok(gate: torch.Tensor, sv, in_scale: torch.Tensor | None = None) -> bool:
-    """True when backbone_swiglu_linear can run: an fp16 SV matrix, a multiple of 32 columns, 16-byte aligned
-    contiguous tensors, and either at most SWIGLU_BACKBONE_MAX_ROWS rows or a rank that is a multiple of 128
-    (the tiled GEMM)."""
+    """True when backbone_swiglu_linear should run: an fp16 SV matrix, a multiple of 32 columns, 16-byte aligned
+    contiguous tensors, and either at most SWIGLU_BACKBONE_MAX_ROWS rows or a prefill-size batch whose rank is a
+    multiple of 512 (the tiled GEMM's full-rank tiles; the C entry takes any rank of 128s above 64 rows)."""
     if not isinstance(sv, torch.Tensor) or sv.dtype != torch.float16 or sv.dim() != 2 or not sv.is_contiguous():
         return False
     if gate.dim() != 2 or int(gate.size(1)) % 32 != 0:
         return False
-    if int(gate.size(0)) > SWIGLU_BACKBONE_MAX_ROWS and int(sv.size(0)) % 128 != 0:
+    rows, in_f, rank = int(gate.size(0)), int(gate.size(1)), int(sv.size(0))
+    # above the decode kernel's rows, the tiled GEMM's 128 x 512 tiles: a rank of 512s and enough workgroups
+    if rows > SWIGLU_BACKBONE_MAX_ROWS and (rank % 512 != 0 or rows < BACKBONE_GEMM_MIN_ROWS or _gemm_workgroups(
+            rows, in_f, rank, tile_m=128, tile_n=512, target=256) < BACKBONE_GEMM_MIN_WORKGROUPS // 2):
         return False
     if int(sv.size(1)) != int(gate.size(1)) or sv.data_ptr() % 16 or gate.data_ptr() % 16:
         return False

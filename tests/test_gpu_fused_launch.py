@@ -248,18 +248,21 @@ def test_backbone_swiglu_product_is_exact(tris, cuda, rows, scaled):
 
 @pytest.mark.parametrize("rows,in_f,rank", [(32, 14336, 512), (16, 1024, 256), (64, 512, 128), (7, 4096, 64),
                                              (300, 2048, 256), (600, 14336, 512), (1000, 1056, 128)])
-def test_backbone_swiglu_matches_unfused(tris, cuda, rows, in_f, rank):
+def test_backbone_swiglu_matches_unfused(tris, cuda, rows, in_f, rank, monkeypatch):
     """The fused down backbone against swiglu_mul followed by backbone_linear (below 512 rows the split over K
     differs, so the fp32 sums agree within rounding; from 512 rows both run the tiled GEMM with the same slices
     and give the same bits) and against an fp32 reference."""
     note(f"backbone swiglu rows={rows} in={in_f} rank={rank}")
     ext = tris["ext"]
+    monkeypatch.setattr(ext, "BACKBONE_GEMM_MIN_WORKGROUPS", 1)  # every eligible shape to the tiled GEMMs
     rng = np.random.default_rng(in_f + rows)
     g = torch.from_numpy(rng.standard_normal((rows, in_f)).astype(np.float16)).to(cuda)
     u = torch.from_numpy(rng.standard_normal((rows, in_f)).astype(np.float16)).to(cuda)
     sv = torch.from_numpy((rng.standard_normal((rank, in_f)) * 0.02).astype(np.float16)).to(cuda)
     sc = torch.from_numpy(rng.uniform(0.5, 1.5, in_f).astype(np.float16)).to(cuda)
-    assert ext.backbone_swiglu_ok(g, sv, sc)
+    # the layer's policy takes the fused form up to 64 rows and, above, for ranks of 512s (full-rank GEMM
+    # tiles); the C entry takes any rank of 128s
+    assert ext.backbone_swiglu_ok(g, sv, sc) == (rows <= 64 or (rows >= 512 and rank % 512 == 0))
     got = ext.backbone_swiglu_linear(g, u, sv, in_scale=sc)
     mlp = ext.swiglu_mul(g, u)
     unfused = ext.backbone_linear(mlp, sv, in_scale=sc)
@@ -273,12 +276,13 @@ def test_backbone_swiglu_matches_unfused(tris, cuda, rows, in_f, rank):
 
 
 @pytest.mark.parametrize("tokens,in_f,rank,top_k", [(512, 4096, 512, 2), (1024, 2048, 256, 8), (700, 1056, 128, 3)])
-def test_backbone_pair_scatter_matches_token_projection(tris, cuda, tokens, in_f, rank, top_k):
+def test_backbone_pair_scatter_matches_token_projection(tris, cuda, tokens, in_f, rank, top_k, monkeypatch):
     """The gate/up backbones written to routed rows: row inverse_perm[t, j] holds the pair's projection of token t
     (the same tiled GEMM over the tokens, so the same bits), slots of -1 write nothing, and the rows equal the
     fp32 product of the gathered rows within rounding."""
     note(f"backbone pair scatter T={tokens} in={in_f} rank={rank} k={top_k}")
     ext = tris["ext"]
+    monkeypatch.setattr(ext, "BACKBONE_GEMM_MIN_WORKGROUPS", 1)
     rng = np.random.default_rng(tokens + in_f)
     x = torch.from_numpy(rng.standard_normal((tokens, in_f)).astype(np.float16)).to(cuda)
     sv_a = torch.from_numpy((rng.standard_normal((rank, in_f)) * 0.02).astype(np.float16)).to(cuda)

@@ -818,7 +818,7 @@ def test_run_grouped_structured_api(tris, oracle_mod, cuda):
                                               (512, 4096, 512), (1000, 14336, 512), (2048, 4096, 512),
                                               (600, 2048, 256), (4096, 512, 256), (700, 1000, 128),
                                               (520, 1056, 128), (513, 96, 256)])
-def test_backbone_matches_fp32(tris, cuda, tokens, in_f, rank):
+def test_backbone_matches_fp32(tris, cuda, tokens, in_f, rank, monkeypatch):
     """Decode-sized inputs run the split-K MFMA kernel (1 to 4 token tiles per workgroup: 37 tokens are 3,
     64 are 4, 70 are a group of 4 and a partial one; 1001 columns take the element-wise loads); from
     ext.BACKBONE_GEMM_MIN_ROWS rows with rank a multiple of 128 and in_features of 32 the tiled split-K GEMM
@@ -827,6 +827,8 @@ def test_backbone_matches_fp32(tris, cuda, tokens, in_f, rank):
     activation elements (300 x 4096, and 700 x 1000 columns) the library GEMM.  Gathered rows past the token
     count project the tokens, then gather."""
     note(f"backbone T={tokens} in={in_f} rank={rank}")
+    # the layer sends a shape to the tiled GEMM only when its launch fills the GPU; here every eligible shape goes
+    monkeypatch.setattr(tris["ext"], "BACKBONE_GEMM_MIN_WORKGROUPS", 1)
     rng = np.random.default_rng(tokens + in_f)
     x = rng.standard_normal((tokens, in_f)).astype(np.float16)
     sv = (rng.standard_normal((rank, in_f)) * 0.02).astype(np.float16)
