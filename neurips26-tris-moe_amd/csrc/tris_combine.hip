@@ -72,35 +72,9 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
   const int t = static_cast<int>(blockIdx.x) / hblocks;
   const int h0 = ((static_cast<int>(blockIdx.x) - t * hblocks) * static_cast<int>(blockDim.x) + threadIdx.x) * 8;
   const bool vec = (hidden % 8) == 0;
-  float gate = 0.0f;
-  if constexpr (kGated) {
-    // every thread of the workgroup takes part in the reduction (the early exit comes after it)
-    __shared__ float wave_part[4];
-    const uint16_t* xr = gate_in + static_cast<int64_t>(t) * hidden;
-    float s = 0.0f;
-    for (int h = static_cast<int>(threadIdx.x) * 8; h < hidden; h += static_cast<int>(blockDim.x) * 8) {
-      uint16_t xv[8], wv[8];
-      if (vec) {
-        *reinterpret_cast<uint4*>(xv) = *reinterpret_cast<const uint4*>(xr + h);
-        *reinterpret_cast<uint4*>(wv) = *reinterpret_cast<const uint4*>(gate_w + h);
-      } else {
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          xv[u] = (h + u < hidden) ? xr[h + u] : 0;
-          wv[u] = (h + u < hidden) ? gate_w[h + u] : 0;
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) s += dt_to_f32<kBf16>(xv[u]) * dt_to_f32<kBf16>(wv[u]);  // exact products
-    }
-    s = wave_sum_f32(s);
-    if ((threadIdx.x & (kWave - 1)) == 0) wave_part[threadIdx.x / kWave] = s;
-    __syncthreads();
-    const float dot = ((wave_part[0] + wave_part[1]) + wave_part[2]) + wave_part[3];
-    const float logit = round_dt<kBf16>(dot);
-    gate = round_dt<kBf16>(1.0f / (1.0f + expf(-logit)));
-  }
-  if (t >= tokens || h0 >= hidden) return;
+  // the routed rows first (their loads in flight while the gate's dot product is reduced), then the gate,
+  // in which every thread of the workgroup takes part, then the early exit
+  const bool valid = t < tokens && h0 < hidden;
   float acc[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u) acc[u] = 0.0f;
@@ -133,6 +107,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
   };
   const int32_t* inv = inverse_perm + static_cast<int64_t>(t) * top_k;
   const uint16_t* wts = weights + static_cast<int64_t>(t) * top_k;
+  if (valid) {
   if constexpr (kK > 0) {
     // every pick's index and weight, then every pick's row, in flight together (a pick the route left out,
     // index -1, reads row 0 and adds nothing); the sum keeps pick order
@@ -159,17 +134,56 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
       add_row(v, c, __ushort_as_half(wts[s]));
     }
   }
-  uint16_t* dst = out + static_cast<int64_t>(t) * hidden + h0;
+  }
+  // the shared expert's output at these columns, in flight with the gate's loads
+  uint16_t sh16[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   const uint16_t* ssrc = shared != nullptr ? shared + static_cast<int64_t>(t) * hidden + h0 : nullptr;
+  if (valid && ssrc != nullptr) {
+    if (vec) {
+      *reinterpret_cast<uint4*>(sh16) = *reinterpret_cast<const uint4*>(ssrc);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) sh16[u] = (h0 + u < hidden) ? ssrc[u] : 0;
+    }
+  }
+  float gate = 0.0f;
+  if constexpr (kGated) {
+    __shared__ float wave_part[4];
+    const uint16_t* xr = gate_in + static_cast<int64_t>(t) * hidden;
+    float s = 0.0f;
+    for (int h = static_cast<int>(threadIdx.x) * 8; h < hidden; h += static_cast<int>(blockDim.x) * 8) {
+      uint16_t xv[8], wv[8];
+      if (vec) {
+        *reinterpret_cast<uint4*>(xv) = *reinterpret_cast<const uint4*>(xr + h);
+        *reinterpret_cast<uint4*>(wv) = *reinterpret_cast<const uint4*>(gate_w + h);
+      } else {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          xv[u] = (h + u < hidden) ? xr[h + u] : 0;
+          wv[u] = (h + u < hidden) ? gate_w[h + u] : 0;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += dt_to_f32<kBf16>(xv[u]) * dt_to_f32<kBf16>(wv[u]);  // exact products
+    }
+    s = wave_sum_f32(s);
+    if ((threadIdx.x & (kWave - 1)) == 0) wave_part[threadIdx.x / kWave] = s;
+    __syncthreads();
+    const float dot = ((wave_part[0] + wave_part[1]) + wave_part[2]) + wave_part[3];
+    const float logit = round_dt<kBf16>(dot);
+    gate = round_dt<kBf16>(1.0f / (1.0f + expf(-logit)));
+  }
+  if (!valid) return;
+  uint16_t* dst = out + static_cast<int64_t>(t) * hidden + h0;
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     if (h0 + u >= hidden) continue;
     float v = acc[u];
     if constexpr (kGated) {
-      const float sh = round_dt<kBf16>(h2f(ssrc[u]));
+      const float sh = round_dt<kBf16>(h2f(sh16[u]));
       v = round_dt<kBf16>(v) + round_dt<kBf16>(gate * sh);
     } else {
-      if (ssrc != nullptr) v += h2f(ssrc[u]);
+      if (ssrc != nullptr) v += h2f(sh16[u]);
     }
     dst[u] = f32_to_dt<kBf16>(v);
   }
