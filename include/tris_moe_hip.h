@@ -453,7 +453,7 @@ int64_t tris_backbone_workspace_bytes(int32_t tokens, int32_t in_features, int32
  * fp16(fp16(silu(gate[r][k])) * up[r][k]), the bits tris_swiglu_mul writes, times in_scale[k] (an fp16
  * product, the ns_mode == 1 input scale) when in_scale is not NULL; out fp16 [rows, rank] = in . sv^T with
  * fp32 accumulation, split over K and the slices added in fixed order (deterministic).  gate, up fp16
- * [rows, in_features], sv fp16 [rank, in_features]; in_features a multiple of 32, and above 64 rows (the tiled
+ * [rows, in_features], sv fp16 [rank, in_features]; in_features a multiple of 32, and above 128 rows (the tiled
  * prefill GEMM) rank a multiple of 128; 16-byte aligned pointers (else TRIS_ERR_INVALID); workspace of
  * tris_backbone_swiglu_workspace_bytes(rows, in_features, rank).
  */

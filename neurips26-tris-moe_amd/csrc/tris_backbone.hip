@@ -638,7 +638,7 @@ int launch_backbone_reduce(const BackboneArgs& args, int nproj, hipStream_t s, c
 constexpr int kSgCols = 128;
 constexpr int kSgWaves = kSgCols / 16;
 constexpr int kSgThreads = kSgWaves * kWave;
-constexpr int kSgMaxRowTiles = 4;
+constexpr int kSgMaxRowTiles = 8;
 constexpr int kSgSteps = 8;                       // K steps of 32 per slice at most
 constexpr int kSgTargetWgs = 256;
 constexpr int kSgVecIters = 4;                    // product vectors (8 columns) a thread forms per batch
@@ -1214,7 +1214,11 @@ extern "C" int tris_backbone_swiglu_linear(const uint16_t* gate, const uint16_t*
     case 1: hipLaunchKernelGGL((backbone_swiglu_kernel<1>), grid, dim3(kSgThreads), lds, s, a); break;
     case 2: hipLaunchKernelGGL((backbone_swiglu_kernel<2>), grid, dim3(kSgThreads), lds, s, a); break;
     case 3: hipLaunchKernelGGL((backbone_swiglu_kernel<3>), grid, dim3(kSgThreads), lds, s, a); break;
-    default: hipLaunchKernelGGL((backbone_swiglu_kernel<4>), grid, dim3(kSgThreads), lds, s, a); break;
+    case 4: hipLaunchKernelGGL((backbone_swiglu_kernel<4>), grid, dim3(kSgThreads), lds, s, a); break;
+    case 5: hipLaunchKernelGGL((backbone_swiglu_kernel<5>), grid, dim3(kSgThreads), lds, s, a); break;
+    case 6: hipLaunchKernelGGL((backbone_swiglu_kernel<6>), grid, dim3(kSgThreads), lds, s, a); break;
+    case 7: hipLaunchKernelGGL((backbone_swiglu_kernel<7>), grid, dim3(kSgThreads), lds, s, a); break;
+    default: hipLaunchKernelGGL((backbone_swiglu_kernel<8>), grid, dim3(kSgThreads), lds, s, a); break;
   }
   int rc = check_launch(who);
   if (rc || slices == 1) return rc;

@@ -1067,13 +1067,13 @@ def backbone_linear_pair_scatter(x: torch.Tensor, sv_a: torch.Tensor, sv_b: torc
     return out_a, out_b
 
 
-SWIGLU_BACKBONE_MAX_ROWS = 64  # rows of tris_backbone_swiglu_linear's decode kernel; more take the tiled GEMM
+SWIGLU_BACKBONE_MAX_ROWS = 128  # rows of tris_backbone_swiglu_linear's decode kernel; more take the tiled GEMM
 
 
 def backbone_swiglu_ok(gate: torch.Tensor, sv, in_scale: torch.Tensor | None = None) -> bool:
     """True when backbone_swiglu_linear should run: an fp16 SV matrix, a multiple of 32 columns, 16-byte aligned
     contiguous tensors, and either at most SWIGLU_BACKBONE_MAX_ROWS rows or a prefill-size batch whose rank is a
-    multiple of 512 (the tiled GEMM's full-rank tiles; the C entry takes any rank of 128s above 64 rows)."""
+    multiple of 512 (the tiled GEMM's full-rank tiles; the C entry takes any rank of 128s above 128 rows)."""
     if not isinstance(sv, torch.Tensor) or sv.dtype != torch.float16 or sv.dim() != 2 or not sv.is_contiguous():
         return False
     if gate.dim() != 2 or int(gate.size(1)) % 32 != 0:

@@ -226,10 +226,11 @@ def test_layer_with_router_backbone_launch_matches_oracle(tris, oracle_mod, cuda
     assert_close(np.concatenate(outs), np.concatenate(wants), f"layer T={tokens}")
 
 
-@pytest.mark.parametrize("rows,scaled", [(1, False), (16, True), (33, False), (64, True), (100, True), (600, False)])
+@pytest.mark.parametrize("rows,scaled", [(1, False), (16, True), (33, False), (64, True), (100, True), (128, False),
+                                         (600, False)])
 def test_backbone_swiglu_product_is_exact(tris, cuda, rows, scaled):
     """With SV the identity, the fused down backbone returns its operand: the product fp16(silu(g) * u)
-    (times the input scale) must be swiglu_mul's bits (one product per output, nothing rounds twice).  Above 64
+    (times the input scale) must be swiglu_mul's bits (one product per output, nothing rounds twice).  Above 128
     rows the tiled GEMM forms the product in its operand staging."""
     note(f"backbone swiglu identity rows={rows} scaled={scaled}")
     ext = tris["ext"]
@@ -247,7 +248,7 @@ def test_backbone_swiglu_product_is_exact(tris, cuda, rows, scaled):
 
 
 @pytest.mark.parametrize("rows,in_f,rank", [(32, 14336, 512), (16, 1024, 256), (64, 512, 128), (7, 4096, 64),
-                                             (300, 2048, 256), (600, 14336, 512), (1000, 1056, 128)])
+                                             (128, 1024, 256), (300, 2048, 256), (600, 14336, 512), (1000, 1056, 128)])
 def test_backbone_swiglu_matches_unfused(tris, cuda, rows, in_f, rank, monkeypatch):
     """The fused down backbone against swiglu_mul followed by backbone_linear (below 512 rows the split over K
     differs, so the fp32 sums agree within rounding; from 512 rows both run the tiled GEMM with the same slices
@@ -260,9 +261,9 @@ def test_backbone_swiglu_matches_unfused(tris, cuda, rows, in_f, rank, monkeypat
     u = torch.from_numpy(rng.standard_normal((rows, in_f)).astype(np.float16)).to(cuda)
     sv = torch.from_numpy((rng.standard_normal((rank, in_f)) * 0.02).astype(np.float16)).to(cuda)
     sc = torch.from_numpy(rng.uniform(0.5, 1.5, in_f).astype(np.float16)).to(cuda)
-    # the layer's policy takes the fused form up to 64 rows and, above, for ranks of 512s (full-rank GEMM
+    # the layer's policy takes the fused form up to 128 rows and, above, for ranks of 512s (full-rank GEMM
     # tiles); the C entry takes any rank of 128s
-    assert ext.backbone_swiglu_ok(g, sv, sc) == (rows <= 64 or (rows >= 512 and rank % 512 == 0))
+    assert ext.backbone_swiglu_ok(g, sv, sc) == (rows <= 128 or (rows >= 512 and rank % 512 == 0))
     got = ext.backbone_swiglu_linear(g, u, sv, in_scale=sc)
     mlp = ext.swiglu_mul(g, u)
     unfused = ext.backbone_linear(mlp, sv, in_scale=sc)
