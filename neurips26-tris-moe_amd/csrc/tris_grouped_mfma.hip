@@ -1175,6 +1175,16 @@ __device__ __forceinline__ void ws_x_issue(const MfmaProj& pa, int row0, int rc,
   }
 }
 
+// The same for materialised rows (no row_index): r_seg covers the segment's rows, rel0 is row0's row within
+// it; rows past the segment read zeros through the resource's size, so no per-row test is needed.
+__device__ __forceinline__ void ws_x_issue_seg(__amdgpu_buffer_rsrc_t r_seg, int rel0, int rank, int utid, WsX& X) {
+  const int wave = utid / kWave;
+  const int lane = utid % kWave;
+  const uint32_t base = (static_cast<uint32_t>(rel0 + wave) * rank + lane * 8) * 2u;
+#pragma unroll
+  for (int h = 0; h < kMfRuns; ++h) X.xv[h] = bload128(r_seg, base + static_cast<uint32_t>(4 * h * rank) * 2u, 0u);
+}
+
 // Writes every staged row in natural column order (rows >= rc get the zeros their loads returned): one
 // 16-byte LDS write per run, a wave's 64 runs one contiguous kilobyte.
 __device__ __forceinline__ void ws_x_write(int utid, uint16_t* xs, const WsX& X) {
@@ -1358,16 +1368,29 @@ __global__ __launch_bounds__(kUnits * kMfThreads) __attribute__((amdgpu_waves_pe
           }
         }
       }
+      // materialised rows: one buffer resource over the segment's activations and one over its outputs (rows
+      // past the segment read zeros and drop their stores through the resources' sizes)
+      const bool seg_rows = pa.row_index == nullptr;
+      const __amdgpu_buffer_rsrc_t r_seg =
+          make_rsrc(pa.hidden + static_cast<int64_t>(seg_lo) * p.rank, static_cast<uint32_t>(rows) * p.rank * 2u);
+      const uint32_t out_bytes = static_cast<uint32_t>(rows) * N * 2u;
+      const __amdgpu_buffer_rsrc_t r_out = make_rsrc(out + static_cast<int64_t>(seg_lo) * N, out_bytes);
+      uint32_t ocol[kSub];  // byte offset of the lane's column in row 4 kg of the row tile, or past the outputs
+#pragma unroll
+      for (int b = 0; b < kSub; ++b) ocol[b] = nv[b] ? static_cast<uint32_t>(4 * kg * N + n[b]) * 2u : 0x80000000u;
+      auto x_issue = [&](int rt, WsX& X) {
+        const int r0 = seg_lo + rt * kMfRows;
+        if (seg_rows) {
+          ws_x_issue_seg(r_seg, rt * kMfRows, p.rank, utid, X);
+        } else {
+          ws_x_issue(pa, r0, min(seg_hi - r0, kMfRows), utid, X);
+        }
+      };
       // the first two row tiles' activations, in flight while the B operands are built; row tile rt's
       // registers are X[rt % 2], reloaded with row tile rt + 2 once staged
       WsX X0, X1;
-      {
-        const int r0 = seg_lo + r_lo * kMfRows;
-        ws_x_issue(pa, r0, min(seg_hi - r0, kMfRows), utid, X0);
-        if (kWsXDepth == 2 && r_lo + 1 < r_hi) {
-          ws_x_issue(pa, r0 + kMfRows, min(seg_hi - r0 - kMfRows, kMfRows), utid, X1);
-        }
-      }
+      x_issue(r_lo, X0);
+      if (kWsXDepth == 2 && r_lo + 1 < r_hi) x_issue(r_lo + 1, X1);
 
       // columns of the salient activations of each window, two 16-bit offsets a word, in the A operand's slot
       // order (padding slots point at the zero column kMfChunk)
@@ -1437,14 +1460,9 @@ __global__ __launch_bounds__(kUnits * kMfThreads) __attribute__((amdgpu_waves_pe
 
       // ---- the segment's row tiles through the stationary B operands
       auto row_tile = [&](int rt, uint16_t* xs, WsX& X) {
-        const int row0 = seg_lo + rt * kMfRows;
-        const int rc = (seg_hi - row0) < kMfRows ? (seg_hi - row0) : kMfRows;
         ws_x_write(utid, xs, X);
         __syncthreads();  // staged rows visible; the previous row tile's exch reads are done
-        if (rt + kWsXDepth < r_hi) {  // depth 1: X0 is the only register set (both call sites pass it)
-          const int r2 = row0 + kWsXDepth * kMfRows;
-          ws_x_issue(pa, r2, (seg_hi - r2) < kMfRows ? (seg_hi - r2) : kMfRows, utid, X);
-        }
+        if (rt + kWsXDepth < r_hi) x_issue(rt + kWsXDepth, X);  // depth 1: X0 is the only register set
         const uint16_t* xr = xs + i16 * kWsXStride;
         f32x4 acc[kSub];
 #pragma unroll
@@ -1509,10 +1527,8 @@ __global__ __launch_bounds__(kUnits * kMfThreads) __attribute__((amdgpu_waves_pe
               const f32x4 up = *reinterpret_cast<const f32x4*>(&exch[(b * kMfThreads + utid) * 4]);
 #pragma unroll
               for (int v = 0; v < 4; ++v) {
-                const int r = 4 * kg + v;
-                if (nv[b] && r < rc) {
-                  out[static_cast<int64_t>(row0 + r) * N + n[b]] = swiglu_bits(f2h_bits(acc[b][v]), f2h_bits(up[v]));
-                }
+                __builtin_amdgcn_raw_buffer_store_b16(swiglu_bits(f2h_bits(acc[b][v]), f2h_bits(up[v])), r_out,
+                                                      ocol[b] + static_cast<uint32_t>(rt * kMfRows + v) * N * 2u, 0u, 0);
               }
             }
           }
@@ -1521,8 +1537,8 @@ __global__ __launch_bounds__(kUnits * kMfThreads) __attribute__((amdgpu_waves_pe
           for (int b = 0; b < kSub; ++b) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-              const int r = 4 * kg + v;
-              if (nv[b] && r < rc) out[static_cast<int64_t>(row0 + r) * N + n[b]] = f2h_bits(acc[b][v]);
+              __builtin_amdgcn_raw_buffer_store_b16(f2h_bits(acc[b][v]), r_out,
+                                                    ocol[b] + static_cast<uint32_t>(rt * kMfRows + v) * N * 2u, 0u, 0);
             }
           }
         }
@@ -1639,8 +1655,10 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
   const int nproj = (pb && !swiglu) ? 2 : 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
   // long segments: keep each output tile's weights in registers and stream the segment's rows through them
+  // (its buffer resources address a segment's rows in 32-bit byte offsets: the whole batch must stay below 2 GiB)
   if (num_segments <= kWave && static_cast<int64_t>(batch) >= static_cast<int64_t>(kWsMinRows) * num_segments &&
-      ws_fits(pa) && (!pb || ws_fits(pb))) {
+      ws_fits(pa) && (!pb || ws_fits(pb)) && static_cast<int64_t>(batch) * max_n * 2 < (int64_t{1} << 31) &&
+      static_cast<int64_t>(batch) * kMfChunk * 2 < (int64_t{1} << 31)) {
     return launch_grouped_mfma_ws(args, units, nproj, max_n, batch, s, who);
   }
   const int rows = batch <= 4 ? 4 : kMfRows;  // staged activation rows: a row tile has at most min(16, batch)
