@@ -302,20 +302,38 @@ __global__ __launch_bounds__(kBgThreads, 2) void backbone_gemm_kernel(BgArgs g) 
       __syncthreads();
     }
   }
-  // acc[i][j][v] = hidden[m0 + 128 wm + 16 i + 4 kg + v][n0 + 64 wn + 16 j + i16]
+  // acc[i][j][v] = hidden[m0 + 128 wm + 16 i + 4 kg + v][n0 + 64 wn + 16 j + i16], stored through a buffer
+  // resource over the tile's rows (rows past the batch drop their stores through its size: no per-row test)
+  const int mrows = a.tokens - m0 < kBgM ? a.tokens - m0 : kBgM;
+  const uint32_t lane_off = static_cast<uint32_t>((wm * 128 + kg * 4) * a.rank + n0 + wn * 64 + i16);
+  if (g.direct) {
+    const __amdgpu_buffer_rsrc_t r =
+        make_rsrc(pj.out + static_cast<int64_t>(m0) * a.rank, static_cast<uint32_t>(mrows) * a.rank * 2u);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 8; ++i) {
 #pragma unroll
-    for (int vv = 0; vv < 4; ++vv) {
-      const int m = m0 + wm * 128 + i * 16 + kg * 4 + vv;
-      if (m >= a.tokens) continue;
+      for (int vv = 0; vv < 4; ++vv) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int n = n0 + wn * 64 + j * 16 + i16;
-        if (g.direct) {
-          pj.out[static_cast<int64_t>(m) * a.rank + n] = f2h_bits(acc[i][j][vv]);
-        } else {
-          a.partials[((static_cast<int64_t>(q) * a.slices + sl) * a.tokens + m) * a.rank + n] = acc[i][j][vv];
+        for (int j = 0; j < 4; ++j) {
+          __builtin_amdgcn_raw_buffer_store_b16(
+              f2h_bits(acc[i][j][vv]), r,
+              (lane_off + static_cast<uint32_t>((i * 16 + vv) * a.rank + j * 16)) * 2u, 0u, 0);
+        }
+      }
+    }
+  } else {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(
+        a.partials + ((static_cast<int64_t>(q) * a.slices + sl) * a.tokens + m0) * a.rank,
+        static_cast<uint32_t>(mrows) * a.rank * 4u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int vv = 0; vv < 4; ++vv) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          __builtin_amdgcn_raw_buffer_store_b32(
+              __float_as_uint(acc[i][j][vv]), r,
+              (lane_off + static_cast<uint32_t>((i * 16 + vv) * a.rank + j * 16)) * 4u, 0u, 0);
         }
       }
     }
@@ -523,21 +541,32 @@ __global__ __launch_bounds__(kBwThreads, 1) void backbone_swiglu_gemm_kernel(BgA
       __syncthreads();
     }
   }
-  // acc[i][j][vv] = hidden[m0 + 64 wm + 16 i + 4 kg + vv][n0 + 128 wn + 16 j + i16]
+  // acc[i][j][vv] = hidden[m0 + 64 wm + 16 i + 4 kg + vv][n0 + 128 wn + 16 j + i16], stored through a buffer
+  // resource over the tile's rows (rows past the batch drop their stores through its size); columns past the
+  // rank (a rank that is not a multiple of 512) get an offset past it
+  const int mrows = a.tokens - m0 < kBwM ? a.tokens - m0 : kBwM;
+  const uint32_t row_off = static_cast<uint32_t>((wm * 64 + kg * 4) * a.rank);
+  uint32_t col_off[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int n = n0 + wn * 128 + j * 16 + i16;
+    col_off[j] = n < a.rank ? static_cast<uint32_t>(n) : 0x10000000u;  // x 4 bytes stays below 2^32
+  }
+  const __amdgpu_buffer_rsrc_t r =
+      g.direct ? make_rsrc(pj.out + static_cast<int64_t>(m0) * a.rank, static_cast<uint32_t>(mrows) * a.rank * 2u)
+               : make_rsrc(a.partials + (static_cast<int64_t>(sl) * a.tokens + m0) * a.rank,
+                           static_cast<uint32_t>(mrows) * a.rank * 4u);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
     for (int vv = 0; vv < 4; ++vv) {
-      const int mm = m0 + wm * 64 + i * 16 + kg * 4 + vv;
-      if (mm >= a.tokens) continue;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int n = n0 + wn * 128 + j * 16 + i16;
-        if (n >= a.rank) continue;
+        const uint32_t e = row_off + static_cast<uint32_t>((i * 16 + vv) * a.rank) + col_off[j];
         if (g.direct) {
-          pj.out[static_cast<int64_t>(mm) * a.rank + n] = f2h_bits(acc[i][j][vv]);
+          __builtin_amdgcn_raw_buffer_store_b16(f2h_bits(acc[i][j][vv]), r, e * 2u, 0u, 0);
         } else {
-          a.partials[(static_cast<int64_t>(sl) * a.tokens + mm) * a.rank + n] = acc[i][j][vv];
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][vv]), r, e * 4u, 0u, 0);
         }
       }
     }

@@ -58,6 +58,21 @@ __device__ __forceinline__ uint16_t swiglu_bits(uint16_t g16, uint16_t u16) {
   return f2h_bits(h2f(sg) * h2f(u16));
 }
 
+constexpr uint32_t kBufferWord3 = 0x00020000;  // raw buffer resource, gfx9 family
+
+// A raw buffer resource over [base, base + bytes): loads at or past `bytes` read zeros and stores there are
+// dropped, without a memory access.  Every caller passes wave-uniform values; reading them back from the first
+// lane lets the compiler keep the resource in scalar registers (a resource it cannot prove uniform costs a
+// waterfall loop per access).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(a)));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32)));
+  const int n = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
+  void* ub = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(ub, 0, n, kBufferWord3);
+}
+
 __device__ __forceinline__ uint32_t low_mask(int bits) {
   return bits >= 32 ? 0xFFFFFFFFu : ((1u << bits) - 1u);
 }

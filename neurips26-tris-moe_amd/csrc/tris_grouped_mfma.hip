@@ -272,19 +272,6 @@ struct MfWaveBuf {     // one wavefront's copy of its 16 columns' words
   uint32_t* zero;      // a word that holds 0
 };
 
-constexpr uint32_t kBufferWord3 = 0x00020000;  // raw buffer resource, gfx9 family
-
-// Every caller passes wave-uniform values; reading them back from the first lane lets the compiler keep the
-// resource in scalar registers (a resource it cannot prove uniform costs a waterfall loop per load).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(a)));
-  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32)));
-  const int n = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
-  void* ub = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
-  return __builtin_amdgcn_make_buffer_rsrc(ub, 0, n, kBufferWord3);
-}
-
 // Byte offset of 8 activation columns [c, c + 8) of segment row row0 + r (r < rc), or `oob` (an offset
 // past the buffer: the load reads zeros) for rows outside the tile, columns past the rank and gathered
 // rows whose index lies outside [0, hidden_rows).  With a row index the buffer resource covers all of
