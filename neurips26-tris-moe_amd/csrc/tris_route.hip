@@ -2,15 +2,16 @@
 //
 // Replaces build_grouped_route (TriSMoE_cuda.cpp:741-793), which runs a torch
 // sort, bincount, nonzero and two cumsums and then copies the tile count to
-// the host.  Here two small kernels build the same metadata on the stream
-// with no host round trip:
-//   1. route_histogram_kernel (one workgroup): per-expert counts in LDS,
-//      a block scan over experts, compacted active expert ids,
-//      segment_offsets, problem_offsets and {num_active, total_tiles}.
-//   2. route_scatter_kernel (one workgroup per active expert): a stable
-//      counting-sort scatter; each workgroup scans the flattened expert ids in
-//      1024-element chunks and places its expert's entries in flat order using
-//      ballots, a popcount of the lower lanes and the wave totals in LDS.
+// the host.  Here one launch builds the same metadata on the stream with no
+// host round trip (route_group_scatter_kernel, one workgroup per segment
+// slot, each of which runs both steps):
+//   1. route_histogram_block: per-expert counts in LDS, a block scan over
+//      experts, compacted active expert ids, segment_offsets,
+//      problem_offsets and {num_active, total_tiles};
+//   2. route_scatter_block: a stable counting-sort scatter of the slot's
+//      expert; the workgroup scans the flattened expert ids in 1024-element
+//      chunks and places its entries in flat order using ballots, a popcount
+//      of the lower lanes and the wave totals in LDS.
 // For decode-sized batches route_topk_small_kernel does the router softmax
 // and top-k (modeling_mixtral.py:548-555) and all of the above in one
 // workgroup and one launch.
@@ -22,22 +23,32 @@ namespace tris {
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteMaxExperts = 16384;
 
-__global__ __launch_bounds__(kRouteThreads) void route_histogram_kernel(
-    const int64_t* __restrict__ selected, int total, int num_experts, int m_tile, int32_t* __restrict__ expert_ids,
-    int32_t* __restrict__ segment_offsets, int32_t* __restrict__ problem_offsets, int32_t* __restrict__ counts) {
-  extern __shared__ int cnt[];  // [num_experts]
+// The histogram of the flattened expert ids, the scan over experts and the compacted segments, by one
+// workgroup of kRouteThreads threads (cnt: num_experts ints of LDS).  With write_out the workgroup writes
+// expert_ids, segment_offsets, problem_offsets and counts; it always leaves, in *slot_e / *slot_pos, the expert
+// and first row of segment slot `seg` (-1 when the slot is inactive; for seg == num_experts, the end of the
+// valid rows) and in *bad whether an id lay outside [0, num_experts).
+__device__ __forceinline__ void route_histogram_block(const int64_t* __restrict__ selected, int total, int num_experts,
+                                                      int m_tile, int* cnt, bool write_out,
+                                                      int32_t* __restrict__ expert_ids,
+                                                      int32_t* __restrict__ segment_offsets,
+                                                      int32_t* __restrict__ problem_offsets,
+                                                      int32_t* __restrict__ counts, int seg, int* slot_e,
+                                                      int* slot_pos, int* bad) {
   __shared__ int scan_active[kRouteThreads];
   __shared__ int scan_rows[kRouteThreads];
   __shared__ int scan_tiles[kRouteThreads];
-  __shared__ int bad;
   const int tid = threadIdx.x;
   for (int e = tid; e < num_experts; e += kRouteThreads) cnt[e] = 0;
-  if (tid == 0) bad = 0;
+  if (tid == 0) {
+    *bad = 0;
+    *slot_e = -1;
+  }
   __syncthreads();
   for (int i = tid; i < total; i += kRouteThreads) {
     const int64_t e = selected[i];
     if (e < 0 || e >= num_experts) {
-      bad = 1;
+      *bad = 1;
     } else {
       atomicAdd(&cnt[e], 1);
     }
@@ -79,53 +90,66 @@ __global__ __launch_bounds__(kRouteThreads) void route_histogram_kernel(
   for (int e = e0; e < e1; ++e) {
     const int c = cnt[e];
     if (c > 0) {
-      expert_ids[a] = e;
-      segment_offsets[a] = r;
-      problem_offsets[a] = t;
+      if (write_out) {
+        expert_ids[a] = e;
+        segment_offsets[a] = r;
+        problem_offsets[a] = t;
+      }
+      if (a == seg) {
+        *slot_e = e;
+        *slot_pos = r;
+      }
       ++a;
       r += c;
       t += (c + m_tile - 1) / m_tile;
     }
   }
-  for (int j = num_active + tid; j < num_experts; j += kRouteThreads) expert_ids[j] = -1;
-  for (int j = num_active + tid; j <= num_experts; j += kRouteThreads) {
-    segment_offsets[j] = rows_total;
-    problem_offsets[j] = tiles_total;
+  if (tid == 0 && seg == num_experts) *slot_pos = rows_total;
+  if (write_out) {
+    for (int j = num_active + tid; j < num_experts; j += kRouteThreads) expert_ids[j] = -1;
+    for (int j = num_active + tid; j <= num_experts; j += kRouteThreads) {
+      segment_offsets[j] = rows_total;
+      problem_offsets[j] = tiles_total;
+    }
   }
-  if (tid == 0) {
+  __syncthreads();
+  if (write_out && tid == 0) {
     // An id outside [0, num_experts) is reported here; the valid entries keep their segments and the
-    // scatter's last workgroup places the invalid ones after them (see route_scatter_kernel).
-    counts[0] = bad ? -1 : num_active;
+    // scatter places the invalid ones after them (route_scatter_block).
+    counts[0] = *bad ? -1 : num_active;
     counts[1] = tiles_total;
   }
+}
+
+__global__ __launch_bounds__(kRouteThreads) void route_histogram_kernel(
+    const int64_t* __restrict__ selected, int total, int num_experts, int m_tile, int32_t* __restrict__ expert_ids,
+    int32_t* __restrict__ segment_offsets, int32_t* __restrict__ problem_offsets, int32_t* __restrict__ counts) {
+  extern __shared__ int cnt[];  // [num_experts]
+  __shared__ int slot_e, slot_pos, bad;
+  route_histogram_block(selected, total, num_experts, m_tile, cnt, true, expert_ids, segment_offsets, problem_offsets,
+                        counts, -1, &slot_e, &slot_pos, &bad);
 }
 
 constexpr int kScatterThreads = 1024;
 constexpr int kScatterWaves = kScatterThreads / kWave;
 
-// One workgroup per segment slot: the flattened expert ids are scanned in chunks of kScatterThreads, each
-// chunk's hits of this expert placed in flat order (ballot within a wave, wave totals through LDS), so a
-// segment's entries keep the order of the flat index as in a stable sort.
-// Workgroup num_experts places the entries whose id lies outside [0, num_experts) (counts[0] == -1) after
-// every segment, in flat order, with their own token index and slot, grouped expert id -1 and inverse_perm
-// -1: every grouped row then holds a valid token index (the backbone's row gather stays in bounds), no
-// segment covers those rows, and the combine skips them.
-__global__ __launch_bounds__(kScatterThreads) void route_scatter_kernel(
-    const int64_t* __restrict__ selected, int total, int top_k, int num_experts, const int32_t* __restrict__ expert_ids,
-    const int32_t* __restrict__ segment_offsets, const int32_t* __restrict__ counts, int64_t* __restrict__ perm,
-    int64_t* __restrict__ token_idx, int64_t* __restrict__ slots, int32_t* __restrict__ grouped_expert_ids,
-    int32_t* __restrict__ inverse_perm) {
+// The stable scatter of segment slot `seg` (expert e, first row pos) by one workgroup of kScatterThreads
+// threads: the flattened expert ids are scanned in chunks of kScatterThreads, each chunk's hits placed in flat
+// order (ballot within a wave, wave totals through LDS), so a segment's entries keep the order of the flat index
+// as in a stable sort.  Slot num_experts (e == -1) places the entries whose id lies outside [0, num_experts)
+// after every segment, in flat order, with their own token index and slot, grouped expert id -1 and
+// inverse_perm -1: every grouped row then holds a valid token index (the backbone's row gather stays in
+// bounds), no segment covers those rows, and the combine skips them.
+__device__ __forceinline__ void route_scatter_block(const int64_t* __restrict__ selected, int total, int top_k,
+                                                    int num_experts, int seg, int e, int pos,
+                                                    int64_t* __restrict__ perm, int64_t* __restrict__ token_idx,
+                                                    int64_t* __restrict__ slots, int32_t* __restrict__ grouped_expert_ids,
+                                                    int32_t* __restrict__ inverse_perm) {
   __shared__ int wave_hits[2][kScatterWaves];
-  const int seg = blockIdx.x;
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
   const int lane = tid % kWave;
-  if (seg > num_experts) return;
   const bool invalid_slot = seg == num_experts;
-  if (invalid_slot && counts[0] >= 0) return;  // every id was valid
-  const int e = invalid_slot ? -1 : expert_ids[seg];
-  if (!invalid_slot && e < 0) return;  // the whole workgroup: an inactive slot
-  int pos = segment_offsets[seg];      // [num_experts]: the end of the valid rows
   const uint64_t lower = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   int buf = 0;
   for (int c = 0; c < total; c += kScatterThreads) {
@@ -156,6 +180,27 @@ __global__ __launch_bounds__(kScatterThreads) void route_scatter_kernel(
     pos += chunk;
     buf ^= 1;
   }
+}
+
+// The whole route from the flattened ids in one launch: workgroup seg (one per segment slot, and one for the
+// invalid ids) builds the histogram and the segments itself (workgroup 0 also writes them out), then scatters
+// its slot's entries.  Every workgroup reads all ids: for prefill routes of a few thousand rows that costs
+// less than a second launch.
+static_assert(kScatterThreads == kRouteThreads, "the histogram and the scatter share the workgroup");
+__global__ __launch_bounds__(kScatterThreads) void route_group_scatter_kernel(
+    const int64_t* __restrict__ selected, int total, int top_k, int num_experts, int m_tile,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ segment_offsets, int32_t* __restrict__ problem_offsets,
+    int32_t* __restrict__ counts, int64_t* __restrict__ perm, int64_t* __restrict__ token_idx,
+    int64_t* __restrict__ slots, int32_t* __restrict__ grouped_expert_ids, int32_t* __restrict__ inverse_perm) {
+  extern __shared__ int cnt[];  // [num_experts]
+  __shared__ int slot_e, slot_pos, bad;
+  const int seg = blockIdx.x;
+  route_histogram_block(selected, total, num_experts, m_tile, cnt, seg == 0, expert_ids, segment_offsets,
+                        problem_offsets, counts, seg, &slot_e, &slot_pos, &bad);
+  const bool invalid_slot = seg == num_experts;
+  if (invalid_slot ? bad == 0 : slot_e < 0) return;  // every id valid / an inactive slot (the whole workgroup)
+  route_scatter_block(selected, total, top_k, num_experts, seg, invalid_slot ? -1 : slot_e, slot_pos, perm, token_idx,
+                      slots, grouped_expert_ids, inverse_perm);
 }
 
 constexpr int kRouteSmallMaxRows = 2048;    // tokens * top_k
@@ -399,7 +444,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_topk_small_kernel(RouteAr
 
 // Softmax / top-k / renormalisation only, for batches past the one-launch router: one wavefront per token
 // (route_token_wave, P experts a lane), tokens spread over the grid; the route is then built by
-// route_histogram_kernel and route_scatter_kernel.  Each wavefront loads its next token's logits while it
+// route_group_scatter_kernel.  Each wavefront loads its next token's logits while it
 // routes the current one.
 constexpr int kRouteTokThreads = 256;
 constexpr int kRouteTokWaves = kRouteTokThreads / kWave;
@@ -769,17 +814,17 @@ extern "C" int tris_build_grouped_route(const int64_t* selected_experts, int32_t
   TRIS_REQUIRE(total == 0 || (selected_experts && perm && grouped_token_indices && grouped_slots && grouped_expert_ids),
                "build_grouped_route: null pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(route_histogram_kernel, dim3(1), dim3(kRouteThreads),
-                     static_cast<size_t>(num_experts > 0 ? num_experts : 1) * sizeof(int), s, selected_experts,
-                     static_cast<int>(total), num_experts, m_tile, expert_ids, segment_offsets, problem_offsets,
-                     counts);
-  int rc = check_launch("route_histogram_kernel");
-  if (rc) return rc;
-  if (total == 0) return TRIS_OK;
-  hipLaunchKernelGGL(route_scatter_kernel, dim3(num_experts + 1), dim3(kScatterThreads), 0, s,
-                     selected_experts, static_cast<int>(total), top_k, num_experts, expert_ids, segment_offsets, counts,
-                     perm, grouped_token_indices, grouped_slots, grouped_expert_ids, inverse_perm);
-  return check_launch("route_scatter_kernel");
+  const size_t lds = static_cast<size_t>(num_experts > 0 ? num_experts : 1) * sizeof(int);
+  if (total == 0) {
+    hipLaunchKernelGGL(route_histogram_kernel, dim3(1), dim3(kRouteThreads), lds, s, selected_experts, 0,
+                       num_experts, m_tile, expert_ids, segment_offsets, problem_offsets, counts);
+    return check_launch("route_histogram_kernel");
+  }
+  hipLaunchKernelGGL(route_group_scatter_kernel, dim3(num_experts + 1), dim3(kScatterThreads), lds, s,
+                     selected_experts, static_cast<int>(total), top_k, num_experts, m_tile, expert_ids, segment_offsets,
+                     problem_offsets, counts, perm, grouped_token_indices, grouped_slots, grouped_expert_ids,
+                     inverse_perm);
+  return check_launch("route_group_scatter_kernel");
 }
 
 // Validates tris_route_topk_grouped's arguments and fills ra.
