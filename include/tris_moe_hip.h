@@ -720,7 +720,8 @@ int tris_router_backbone(const uint16_t* x, const uint16_t* router_weight, int32
  * router_logits with the same selection, and fills the jobs' buffers as tris_grouped_block_gr_predecode_multi
  * does for that route's expert_ids (num_slots = min(num_experts, num_tokens * top_k) slots, the active experts
  * first).  bb (or NULL): a backbone job whose deferred partial sums are reduced in the same launch, as
- * tris_grouped_block_gr_predecode_multi_reduce does.  The one-wavefront route only: num_tokens * top_k <= 64,
+ * tris_grouped_block_gr_predecode_multi_reduce does.  num_jobs may be 0 (jobs NULL): the route and bb's reduction
+ * alone, for GEMMs that decode the bitmaps themselves.  The one-wavefront route only: num_tokens * top_k <= 64,
  * num_experts <= 8.
  */
 int tris_route_predecode_multi_reduce(const float* router_logits, int32_t num_tokens, int32_t num_experts,

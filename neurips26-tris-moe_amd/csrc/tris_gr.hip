@@ -251,12 +251,12 @@ int launch_gr_jobs(const GrJobs& jobs, int num_jobs, const int32_t* expert_ids, 
     total += static_cast<int64_t>(jobs.job[q].nblk) * num_slots;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  TRIS_REQUIRE(route == nullptr || (num_slots <= kRouteLaneMaxExperts && max_nblk > 0),
-               "%s: a route in the predecode launch needs blocks to decode and at most %d slots", who,
-               kRouteLaneMaxExperts);
-  if (num_slots == 0 || max_nblk == 0) {
+  TRIS_REQUIRE(route == nullptr || num_slots <= kRouteLaneMaxExperts,
+               "%s: a route in the predecode launch takes at most %d slots", who, kRouteLaneMaxExperts);
+  if (route == nullptr && (num_slots == 0 || max_nblk == 0)) {
     return reduce != nullptr ? launch_backbone_reduce(*reduce, reduce_nproj, s, who) : TRIS_OK;
   }
+  if (max_nblk == 0) num_slots = 0;  // a route (and a reduction) with nothing to decode: no decode workgroups
   TRIS_REQUIRE(route != nullptr || expert_ids != nullptr, "%s: null expert ids", who);
   TRIS_REQUIRE(num_slots <= 65535, "%s: too many experts (%d)", who, num_slots);
   // lanes per block: more lanes shorten each block's walk, fewer spread the per-workgroup table copy
@@ -410,8 +410,8 @@ extern "C" int tris_route_predecode_multi_reduce(const float* router_logits, int
   TRIS_REQUIRE(num_slots == (num_experts < rows ? num_experts : rows),
                "%s: num_slots must be min(num_experts, tokens * top_k) = %d", who, num_experts < rows ? num_experts : rows);
   route.k_variant = top_k <= 2 ? 2 : (top_k <= 8 ? 8 : kRouteMaxTopK);
-  TRIS_REQUIRE(num_jobs > 0 && num_jobs <= TRIS_MAX_PREDECODE_JOBS && jobs != nullptr, "%s: %d jobs (1 to %d)", who,
-               num_jobs, TRIS_MAX_PREDECODE_JOBS);
+  TRIS_REQUIRE(num_jobs >= 0 && num_jobs <= TRIS_MAX_PREDECODE_JOBS && (num_jobs == 0 || jobs != nullptr),
+               "%s: %d jobs (0 to %d)", who, num_jobs, TRIS_MAX_PREDECODE_JOBS);
   GrJobs g{};
   for (int q = 0; q < num_jobs; ++q) {
     const tris_gr_predecode_job& j = jobs[q];

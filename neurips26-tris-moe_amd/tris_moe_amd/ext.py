@@ -421,13 +421,14 @@ def route_predecode_multi(router_logits: torch.Tensor, top_k: int, renormalize: 
                           backbone: BackbonePending | None = None) -> dict:
     """route_topk_grouped and grouped_block_gr_predecode_multi of the same route in one launch
     (tris_route_predecode_multi_reduce, an extension): jobs as grouped_block_gr_predecode_multi takes them, each
-    buffer [min(E, T * top_k), blocks, 128]; ``backbone``: a BackbonePending reduced in the same launch.
+    buffer [min(E, T * top_k), blocks, 128], or none (the route and the backbone's reduction alone, for the
+    GEMMs that decode the bitmaps themselves); ``backbone``: a BackbonePending reduced in the same launch.
     Returns the route dict of route_topk_grouped."""
     if not route_predecode_ok(router_logits, top_k):
         raise RuntimeError("route_predecode_multi: logits outside the one-wavefront route (T * top_k <= "
                            f"{ROUTE_WAVE_MAX_ROWS}, E <= {ROUTE_WAVE_MAX_EXPERTS})")
-    if not 0 < len(jobs) <= _lib.MAX_PREDECODE_JOBS:
-        raise RuntimeError(f"route_predecode_multi: 1 to {_lib.MAX_PREDECODE_JOBS} predecode jobs")
+    if not 0 <= len(jobs) <= _lib.MAX_PREDECODE_JOBS:
+        raise RuntimeError(f"route_predecode_multi: 0 to {_lib.MAX_PREDECODE_JOBS} predecode jobs")
     logits, out = _route_topk_outputs(router_logits, top_k, "route_predecode_multi")
     t, e = int(logits.size(0)), int(logits.size(1))
     slots = min(e, t * int(top_k))
@@ -451,7 +452,8 @@ def route_predecode_multi(router_logits: torch.Tensor, top_k: int, renormalize: 
                                        int(words.size(1)), int(packed_rows), int(outfeatures))
     bb = ctypes.byref(backbone.job) if backbone is not None else None
     _lib.check(_lib.load().tris_route_predecode_multi_reduce(
-        *_route_topk_args(logits, out, top_k, renormalize, m_tile), arr, len(jobs), slots, bb, _stream(logits)),
+        *_route_topk_args(logits, out, top_k, renormalize, m_tile), arr if jobs else None, len(jobs), slots, bb,
+        _stream(logits)),
         "route_predecode_multi")
     return out
 

@@ -440,12 +440,14 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     return _combine(x16, d_out, route, w16, output_dtype, shared_expert, d_comp=comp_d)
 
 
-def _decode_fused_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype, shared_expert):
+def _decode_fused_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype, shared_expert,
+                              hidden_pair=None):
     """The GR split bitmaps decoded inside the grouped GEMMs (the reference's fused decode path,
     TriSMoE_cuda_kernel.cu:5382-5586): gate and up in one launch with act_fn(g) * u in its epilogue, read through
     the route's token indices from per-token backbone outputs (every routed row of a token has the same shared
     hidden, modeling_mixtral.py:467-476), then the down GEMM over the routed rows.  Output scale and bias, and
-    null-space compensation terms, are applied as in the predecoded path."""
+    null-space compensation terms, are applied as in the predecoded path.  hidden_pair: the tokens' gate/up
+    backbone outputs already computed (the decode step's router launch), else they are projected here."""
     slots = min(num_experts, R)
     eid = route["expert_ids"][:slots]
     seg = route["segment_offsets"][: slots + 1]
@@ -453,21 +455,31 @@ def _decode_fused_moe_forward(x16, w16, route, payloads, backbones, num_experts,
     pg, pu, pd = payloads["gate"], payloads["up"], payloads["down"]
     ns = _ns_payloads(payloads)
     sc = _in_scales(backbones)
-    hid_g, hid_u = shared_projection_pair(x16, backbones["gate"], backbones["up"], in_scale_a=sc["gate"],
-                                          in_scale_b=sc["up"])
-    if ns["gate"] is None and ns["up"] is None:
-        mlp = ext.grouped_decode_pair_forward(hid_g, hid_u, pg, pu, eid, seg, R, row_index=gti, swiglu=True)
+    if hidden_pair is not None:
+        hid_g, hid_u = hidden_pair
     else:
-        g, u = ext.grouped_decode_pair_forward(hid_g, hid_u, pg, pu, eid, seg, R, row_index=gti)
-        n_mlp = int(g.size(1))
-        dev = x16.device
+        hid_g, hid_u = shared_projection_pair(x16, backbones["gate"], backbones["up"], in_scale_a=sc["gate"],
+                                              in_scale_b=sc["up"])
+    dev = x16.device
+    n_mlp = int(pg["qweight1"].size(2))
+    # every routed row lies in one of the min(E, R) segments, so the outputs need no zero fill
+    if ns["gate"] is None and ns["up"] is None:
+        mlp = ext.grouped_decode_pair_forward(hid_g, hid_u, pg, pu, eid, seg, R, row_index=gti, swiglu=True,
+                                              out_a=torch.empty((R, n_mlp), dtype=torch.float16, device=dev))
+    else:
+        g, u = ext.grouped_decode_pair_forward(
+            hid_g, hid_u, pg, pu, eid, seg, R, row_index=gti,
+            out_a=torch.empty((R, n_mlp), dtype=torch.float16, device=dev),
+            out_b=torch.empty((R, int(pu["qweight1"].size(2))), dtype=torch.float16, device=dev))
         comp_g = torch.empty((R, n_mlp), dtype=torch.float16, device=dev) if ns["gate"] is not None else None
         comp_u = torch.empty((R, n_mlp), dtype=torch.float16, device=dev) if ns["up"] is not None else None
         ext.ns_compensation_pair_apply_(comp_g, comp_u, x16, eid, seg, ns["gate"], ns["up"], accumulate=False,
                                         row_index=gti)
         mlp = ext.swiglu_mul(g, u, comp_gate=comp_g, comp_up=comp_u)
     hid_d = shared_projection(mlp, backbones["down"], in_scale=sc["down"])
-    d_out = ext.grouped_decode_forward(hid_d, pd, eid, seg, R)
+    d_out = ext.grouped_decode_forward(hid_d, pd, eid, seg, R,
+                                       out=torch.empty((R, int(pd["qweight1"].size(2))), dtype=torch.float16,
+                                                       device=dev))
     if ns["down"] is not None:
         ext.ns_compensation_apply_(d_out, mlp, eid, seg, ns["down"])
     return _combine(x16, d_out, route, w16, output_dtype, shared_expert)
@@ -477,13 +489,18 @@ def decode_prologue_ok(x: torch.Tensor, router_weight: torch.Tensor, top_k: int,
                        backbones: dict, expert_path: str = "auto") -> bool:
     """The block's decode step can start with ext.router_backbone_pair and route in its predecode's launch
     (ext.route_predecode_multi): bf16 activations and router, the one-wavefront route (tokens * top_k <= 64, at
-    most 8 experts), the predecoded MFMA path with fp16 gate/up backbones, no null-space payloads."""
-    if expert_path == "fused" or x.dim() != 2:
+    most 8 experts), fp16 gate/up backbones, no null-space payloads, and the expert path's payload conditions:
+    the predecoded MFMA path ("auto", "predecoded"), or the in-kernel-decode GEMMs ("fused")."""
+    if x.dim() != 2:
         return False
     t = int(x.size(0))
     if not (0 < t and t * top_k <= ext.ROUTE_WAVE_MAX_ROWS and num_experts <= ext.ROUTE_WAVE_MAX_EXPERTS):
         return False
-    if not (_predecodable(payloads) and ext.mfma_payload_ok(payloads["gate"]) and ext.mfma_payload_ok(payloads["up"])):
+    if expert_path == "fused":
+        if not all(not _sparse(p) and ext.decode_payload_ok(p) for p in payloads.values()):
+            return False
+    elif not (_predecodable(payloads) and ext.mfma_payload_ok(payloads["gate"])
+              and ext.mfma_payload_ok(payloads["up"])):
         return False
     if any(v is not None for v in _ns_payloads(payloads).values()):
         return False
@@ -493,17 +510,24 @@ def decode_prologue_ok(x: torch.Tensor, router_weight: torch.Tensor, top_k: int,
 
 def grouped_moe_decode_step(x: torch.Tensor, router_weight: torch.Tensor, top_k: int, renormalize: bool,
                             payloads: dict, backbones: dict, num_experts: int, output_dtype=torch.bfloat16,
-                            shared_expert=None):
+                            shared_expert=None, expert_path: str = "auto"):
     """The whole block at decode from its bf16 input (decode_prologue_ok): the router Linear, the fp16 cast and
     the gate/up backbones in one launch, the route and the predecode (with the backbones' split-K reduction) in
-    the next, then the grouped GEMMs and the combine.  Returns (out [T, H] in output_dtype, router_logits bf16
-    [T, E]).  The same outputs as TrisSparseMoeBlock's other path, bit for bit."""
+    the next, then the grouped GEMMs and the combine.  expert_path "fused": the route launch only reduces the
+    backbones, and the grouped GEMMs decode the split bitmaps themselves.  Returns (out [T, H] in output_dtype,
+    router_logits bf16 [T, E]).  The same outputs as TrisSparseMoeBlock's other path, bit for bit."""
     sc = _in_scales(backbones)
     logits, logits32, x16, pending = ext.router_backbone_pair(x, router_weight, backbones["gate"], backbones["up"],
                                                               in_scale_a=sc["gate"], in_scale_b=sc["up"])
     T = int(x.size(0))
     R = T * top_k
     shared = _shared_expert_begin(x16, shared_expert, x, output_dtype)
+    if expert_path == "fused":
+        # the route and the backbones' reduction in one launch, then the GEMMs that decode the bitmaps themselves
+        route = ext.route_predecode_multi(logits32, top_k, renormalize, GROUPED_SEGMENT_M_TILE, [], backbone=pending)
+        out = _decode_fused_moe_forward(x16, route["routing_weights_f16"], route, payloads, backbones, num_experts, R,
+                                        output_dtype, shared, hidden_pair=(pending.out_a, pending.out_b))
+        return out, logits
     slots = min(num_experts, R)
     dev = x.device
     order = (("gate", payloads["gate"]), ("up", payloads["up"]), ("down", payloads["down"]))
@@ -582,7 +606,7 @@ class TrisSparseMoeBlock(nn.Module):
                               self.expert_path):
             out, router_logits = grouped_moe_decode_step(flat, weight, self.top_k, self.renormalize, self.payloads,
                                                          self.backbones, self.num_experts, flat.dtype,
-                                                         self._shared(flat.dtype))
+                                                         self._shared(flat.dtype), expert_path=self.expert_path)
             return out.reshape(batch, seq, hidden), router_logits
         if ext.router_linear_ok(flat, weight):
             router_logits, logits32, x16 = ext.router_linear(flat, weight)

@@ -360,14 +360,16 @@ def test_router_backbone_and_route_predecode_match_separate_launches(tris, cuda,
     assert torch.equal(pending.out_b.view(torch.int16), want_b.view(torch.int16))
 
 
+@pytest.mark.parametrize("path", ["auto", "fused"])
 @pytest.mark.parametrize("tokens", [1, 4, 16])
-def test_block_decode_step_matches_unfused_block(tris, oracle_mod, cuda, tokens):
+def test_block_decode_step_matches_unfused_block(tris, oracle_mod, cuda, tokens, path):
     """TrisSparseMoeBlock.forward at decode (grouped_moe_decode_step: router Linear + backbones, then route +
-    predecode) against the same block with the step's other path (router_linear, then the route with the
-    backbones, then the predecode): the same output and router logits, bit for bit, on the C1 layer."""
+    predecode, or with the "fused" expert path route + backbone reduction and the in-kernel-decode GEMMs) against
+    the same block with the step's other path (router_linear, then the route, the backbones and the expert path's
+    GEMMs): the same output and router logits, bit for bit, on the C1 layer."""
     from tris_moe_amd.configs import C1_MIXTRAL_DECODE as SPEC
 
-    note(f"block decode step T={tokens}")
+    note(f"block decode step T={tokens} path={path}")
     syn, ql, moe = tris["synthetic"], tris["qlinear"], tris["moe"]
     layer = syn.make_layer(SPEC, 6100 + tokens, tris["ext"].gr_encode)
     payloads = {p: ql.payload_to_device(layer[p], cuda) for p in ("gate", "up", "down")}
@@ -376,11 +378,12 @@ def test_block_decode_step_matches_unfused_block(tris, oracle_mod, cuda, tokens)
     router = torch.from_numpy((rng.standard_normal((SPEC.num_experts, SPEC.hidden)) * 0.015).astype(np.float32))
     block = moe.TrisSparseMoeBlock(SPEC.hidden, SPEC.num_experts, SPEC.top_k, payloads, backbones,
                                    router_weight=router.to(cuda))
+    block.expert_path = path
     inp = syn.make_inputs(SPEC, tokens, 6200 + tokens, layer["outlier_idx"])
     h = torch.from_numpy(inp["x"]).to(cuda).to(torch.bfloat16)
     flat = h.reshape(-1, SPEC.hidden)
     assert moe.decode_prologue_ok(flat, block.gate.weight.detach(), SPEC.top_k, SPEC.num_experts, payloads,
-                                  backbones)
+                                  backbones, path)
     with torch.no_grad():
         out, logits = block(h.reshape(1, tokens, SPEC.hidden))
         lg, lg32, x16 = tris["ext"].router_linear(flat, block.gate.weight.detach())
