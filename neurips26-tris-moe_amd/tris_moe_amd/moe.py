@@ -226,7 +226,8 @@ def _combine_dtype(output_dtype) -> torch.dtype:
 
 
 def _shared_expert_begin(x16, shared_expert, x_model=None, output_dtype=None):
-    """Start the always-on shared expert down(act_fn(gate x) * up x) on side stream 2: gate and up in one
+    """Start the always-on shared expert down(act_fn(gate x) * up x) on side stream 2 (on the caller's stream
+    below SHARED_EXPERT_SIDE_STREAM_MIN_TOKENS tokens): gate and up in one
     backbone launch, then the down projection with act_fn(g) * u formed in its operand staging (or SiLU and
     the product in fp16 as F.silu(g) * u, then the down projection), the reference's fp16 MLP.  Returns a
     _SharedPending or None."""
@@ -250,8 +251,9 @@ def _shared_expert_begin(x16, shared_expert, x_model=None, output_dtype=None):
         gate_in = src.to(cd).contiguous()
     main = torch.cuda.current_stream(dev)
     out = torch.empty((T, H), dtype=torch.float16, device=dev)
-    side = _side_stream(dev, 2)
-    side.wait_stream(main)
+    side = _side_stream(dev, 2) if T >= SHARED_EXPERT_SIDE_STREAM_MIN_TOKENS else main
+    if side is not main:
+        side.wait_stream(main)
     with torch.cuda.stream(side):
         g, u = ext.backbone_linear_pair(x16, wg, wu)
         if ext.backbone_swiglu_ok(g, wd):
@@ -267,7 +269,7 @@ def _combine(x16, d_out, route, w16, output_dtype, shared, d_comp=None):
     shared = _shared_expert_begin(x16, shared, output_dtype=output_dtype)
     cd = _combine_dtype(output_dtype)
     kw = {}
-    if shared is not None:
+    if shared is not None and shared.stream != torch.cuda.current_stream(x16.device):
         torch.cuda.current_stream(x16.device).wait_stream(shared.stream)
         kw["shared"] = shared.out
         if shared.gate_weight is not None:
@@ -308,6 +310,16 @@ WS_GATHER_MIN_ROWS_PER_SEGMENT = 64
 # The down projection's null-space compensation runs on the side stream beside the down backbone and GEMM
 # (True) or on the caller's stream after the GEMM (False).
 NS_DOWN_BESIDE_GEMM = True
+
+# The gate/up null-space compensation runs on a side stream beside the decodes and backbones (True) or on the
+# caller's stream before them (False; measured on MI355X at the Mixtral decode shape, T = 16: 133.2 us beside,
+# 136.7 us before).
+NS_GATE_UP_BESIDE = True
+
+# From this many tokens the shared expert runs on a side stream beside the routed experts; below it on the
+# caller's stream, since a graph's cross-queue join costs more than the overlap saves there (measured on MI355X at
+# the A3B shape: T = 1 64.3 -> 59.0 us inline; T = 32 138 vs 139 us; T = 1024 339 vs 356 us).
+SHARED_EXPERT_SIDE_STREAM_MIN_TOKENS = 32
 
 
 def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype, shared_expert,
@@ -350,11 +362,14 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
         # buffers belong to the caller's stream, which waits for this one before reading or freeing them
         comp_g = torch.empty((R, n_mlp), dtype=torch.float16, device=dev) if ns["gate"] is not None else None
         comp_u = torch.empty((R, n_mlp), dtype=torch.float16, device=dev) if ns["up"] is not None else None
-        ns_side = _side_stream(dev, 1)
-        ns_side.wait_stream(main)
+        ns_side = _side_stream(dev, 1) if NS_GATE_UP_BESIDE else main
+        if ns_side is not main:
+            ns_side.wait_stream(main)
         with torch.cuda.stream(ns_side):
             ext.ns_compensation_pair_apply_(comp_g, comp_u, x16, eid, seg, ns["gate"], ns["up"], accumulate=False,
                                             row_index=route["grouped_token_indices"])
+        if ns_side is main:
+            ns_side = None
 
     # one launch for the three projections, on the caller's stream: beside the backbones it takes the CUs
     # first and delays them, and the join costs more than the overlap saves (measured on MI355X at the
