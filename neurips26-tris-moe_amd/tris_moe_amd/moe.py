@@ -269,8 +269,10 @@ def _combine(x16, d_out, route, w16, output_dtype, shared, d_comp=None):
     shared = _shared_expert_begin(x16, shared, output_dtype=output_dtype)
     cd = _combine_dtype(output_dtype)
     kw = {}
-    if shared is not None and shared.stream != torch.cuda.current_stream(x16.device):
-        torch.cuda.current_stream(x16.device).wait_stream(shared.stream)
+    if shared is not None:
+        main = torch.cuda.current_stream(x16.device)
+        if shared.stream != main:
+            main.wait_stream(shared.stream)
         kw["shared"] = shared.out
         if shared.gate_weight is not None:
             kw["shared_gate_weight"] = shared.gate_weight.to(cd)
