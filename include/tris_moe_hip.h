@@ -356,6 +356,20 @@ int tris_grouped_swiglu_forward_block_gr_predecoded_rows(
     void* stream);
 
 /*
+ * The predecoded grouped GEMM (one projection, or two as the dual entry point) over bitmaps decoded for every
+ * expert (no reference counterpart: TriSMoE_cuda.cpp:855-889 and 922-974 read one slot per routed segment).
+ * decoded_* [num_experts, blocks, 128] (tris_route_predecode_all_reduce): segment s reads slot expert_ids[s].
+ * row_index (or NULL) as in the _rows entry points.  hidden_b, decoded_b, payload_b and output_b are all NULL
+ * for one projection.  Requires the MFMA kernel's payload conditions (else TRIS_ERR_INVALID); no output scale
+ * or bias is applied.
+ */
+int tris_grouped_forward_block_gr_predecoded_experts(
+    const uint16_t* hidden_a, const uint16_t* hidden_b, const int64_t* row_index, int32_t hidden_rows, int32_t batch,
+    const int32_t* expert_ids, const int32_t* segment_offsets, int32_t num_segments, int64_t total_problem_tiles,
+    const int32_t* decoded_a, const int32_t* decoded_b, const tris_compact3_payload* payload_a,
+    const tris_compact3_payload* payload_b, uint16_t* output_a, uint16_t* output_b, void* stream);
+
+/*
  * Dequantise the listed experts to dense fp16 weights [num, N, rank]
  * (verification kernel; the product GEMMs never write weights).  Replaces the
  * reference's CPU dequant QuantLinear._dequantize_compact3_matrix
@@ -732,6 +746,23 @@ int tris_route_predecode_multi_reduce(const float* router_logits, int32_t num_to
                                       int32_t* segment_offsets, int32_t* problem_offsets, int32_t* counts,
                                       int32_t* inverse_perm, const tris_gr_predecode_job* jobs, int32_t num_jobs,
                                       int32_t num_slots, const tris_backbone_pair_job* bb, void* stream);
+
+/*
+ * tris_route_predecode_multi_reduce that decodes every expert's split bitmaps, slot e for expert e (no reference
+ * counterpart: the reference predecodes the routed experts, TriSMoE_cuda.cpp:836-853).  The decoders then need
+ * nothing from the route, so they start without reading the router logits; at decode batches that route rows to
+ * nearly every expert this costs little extra work.  The route outputs are tris_route_predecode_multi_reduce's;
+ * each job's buffer holds num_experts slots [num_experts, blocks, 128].  Read them with
+ * tris_grouped_forward_block_gr_predecoded_experts.
+ */
+int tris_route_predecode_all_reduce(const float* router_logits, int32_t num_tokens, int32_t num_experts,
+                                    int32_t top_k, int32_t renormalize, int32_t m_tile, uint16_t* routing_weights_f16,
+                                    float* routing_weights_f32, int64_t* selected_experts, int64_t* perm,
+                                    int64_t* grouped_token_indices, int64_t* grouped_slots,
+                                    int32_t* grouped_expert_ids, int32_t* expert_ids, int32_t* segment_offsets,
+                                    int32_t* problem_offsets, int32_t* counts, int32_t* inverse_perm,
+                                    const tris_gr_predecode_job* jobs, int32_t num_jobs,
+                                    const tris_backbone_pair_job* bb, void* stream);
 
 #ifdef __cplusplus
 }

@@ -26,6 +26,15 @@ constexpr int kWave = 64;
 
 __host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
+// Typed views of generic pointers for loads whose address space the compiler cannot infer (pointers taken from
+// a struct indexed at run time, or selected between two arrays).  A generic (flat) load counts in the LDS
+// counter as well as the vector-memory one, so each later wait for an LDS read would also wait for it: a global
+// load issued ahead of a computation on LDS must be a global_load to stay in flight across it.
+typedef const __attribute__((address_space(1))) int32_t gmem_i32;
+typedef const __attribute__((address_space(3))) int32_t lds_i32;
+__device__ __forceinline__ gmem_i32* as_gmem(const int32_t* p) { return (gmem_i32*)p; }
+__device__ __forceinline__ lds_i32* as_lds(const int32_t* p) { return (lds_i32*)p; }
+
 // fp16 bits <-> float, exact.
 __device__ __forceinline__ float h2f(uint16_t bits) {
   return __half2float(__ushort_as_half(bits));

@@ -47,7 +47,8 @@ struct GrWork {
   int num_jobs;
   int num_slots;
   int first[TRIS_MAX_PREDECODE_JOBS + 1];  // first item of each job; first[num_jobs] = all items
-  int decode_wgs;  // workgroups that decode; any after them reduce a backbone's slices (GrReduce)
+  int reduce_wgs;  // workgroups that reduce a backbone's slices (GrReduce), dispatched before the decoders
+  int decode_wgs;  // workgroups that decode, after them
 };
 
 // The decode route built in the same launch (tris_route_predecode_multi_reduce): workgroup 0 runs
@@ -57,6 +58,7 @@ struct GrRoute {
   RouteArgs ra;
   int k_variant;  // the route_wave_body instance: 2, 8 or kRouteMaxTopK (by top_k, as tris_route_topk_grouped)
   int wg;         // its workgroup index (0: the decoders follow it), or -1: no route in this launch
+  int decode_all;  // 1: the decoders take every expert, slot = expert id, and do not read the logits
 };
 
 // A backbone projection's slice reduction run by the workgroups past the decoders (independent work in the
@@ -74,7 +76,8 @@ struct GrItem {
   GrSpan<S> sp;
 };
 
-// Item w's job, slot and first block, and its block headers (an empty item past the last).
+// Item w's job, slot and first block, and its block headers (an empty item past the last).  eids: the slots'
+// expert ids in LDS (the first kSpanLdsSlots), or null: every id read from expert_ids.
 template <int S>
 __device__ __forceinline__ void gr_item_header(const GrJobs& jobs, const GrWork& wk, const int32_t* __restrict__ eids,
                                                const int32_t* __restrict__ expert_ids, int w, int g, GrItem<S>& it) {
@@ -91,7 +94,14 @@ __device__ __forceinline__ void gr_item_header(const GrJobs& jobs, const GrWork&
   it.q = q;
   it.slot = local / batches;
   it.block0 = (local - it.slot * batches) * kBlocksPerItem;
-  const int expert = it.slot < kSpanLdsSlots ? eids[it.slot] : expert_ids[it.slot];
+  // the slot is wave-uniform: one LDS read or one global load, not a load through a pointer selected
+  // between LDS and memory (a flat load, which each later LDS wait would wait for)
+  int expert;
+  if (eids != nullptr && it.slot < kSpanLdsSlots) {
+    expert = as_lds(eids)[it.slot];
+  } else {
+    expert = as_gmem(expert_ids)[it.slot];
+  }
   const bool ev = exists && expert >= 0 && expert < jb.num_experts;
   const int ex = ev ? expert : 0;
   gr_span_header<S>(it.sp, jb.words + static_cast<int64_t>(ex) * jb.words_stride,
@@ -114,11 +124,12 @@ __global__ __launch_bounds__(kSpanThreads) __attribute__((amdgpu_waves_per_eu(5)
   __shared__ int32_t eids[kSpanLdsSlots];
   __shared__ int32_t weids[kSpanWaves][kRouteLaneMaxExperts];  // each wavefront's expert list (route in launch)
   const int tid = threadIdx.x;
-  // with a route in the launch, workgroup 0 builds it (dispatched first, so its latency overlaps the decode)
-  // and the decode and reduce workgroups follow
-  const int bid = static_cast<int>(blockIdx.x) - (rt.wg >= 0 ? 1 : 0);
-  if (bid < 0 || bid >= wk.decode_wgs) {
-    if (bid < 0) {  // the route (its logits staged in the decode buffers' LDS)
+  // with a route in the launch, workgroup 0 builds it (dispatched first, so its latency overlaps the decode);
+  // the reduction workgroups follow, then the decoders (so the reductions are resident from the start, not
+  // queued behind a grid of decoders that fills every CU)
+  const int rbid = static_cast<int>(blockIdx.x) - (rt.wg >= 0 ? 1 : 0);
+  if (rbid < wk.reduce_wgs) {
+    if (rbid < 0) {  // the route (its logits staged in the decode buffers' LDS)
       float* lg = reinterpret_cast<float*>(&outb[0][0]);
       if (tid < kWave) {
         if (rt.k_variant == 2) route_wave_body<2>(rt.ra, lg, tid);
@@ -127,11 +138,11 @@ __global__ __launch_bounds__(kSpanThreads) __attribute__((amdgpu_waves_per_eu(5)
       }
       return;
     }
-    const int rb = bid - wk.decode_wgs;
-    const int q = rb / red.blocks_per_proj;
-    backbone_reduce_at(red.bb, static_cast<int64_t>(rb % red.blocks_per_proj) * kSpanThreads + threadIdx.x, q);
+    const int q = rbid / red.blocks_per_proj;
+    backbone_reduce_at(red.bb, static_cast<int64_t>(rbid % red.blocks_per_proj) * kSpanThreads + threadIdx.x, q);
     return;
   }
+  const int bid = rbid - wk.reduce_wgs;
   const int total = wk.first[wk.num_jobs];
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform: what it selects stays scalar
   const int lane = tid % kWave;
@@ -148,18 +159,23 @@ __global__ __launch_bounds__(kSpanThreads) __attribute__((amdgpu_waves_per_eu(5)
     // decode route is listed (num_slots <= kRouteLaneMaxExperts), so expert_ids is never read.  Its first
     // header is then in flight during the table copy, as without a route.
     expert_ids = reinterpret_cast<const int32_t*>(rt.ra.logits);  // any readable word, for invalid headers
-    float* wl = reinterpret_cast<float*>(outb[wave]);
-    const int nlog = rt.ra.tokens * rt.ra.num_experts;
-    for (int i = lane; i < nlog; i += kWave) wl[i] = rt.ra.logits[i];
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    if (rt.k_variant == 2) {
-      route_active_experts<2>(wl, rt.ra.tokens, rt.ra.num_experts, rt.ra.top_k, lane, weids[wave], wk.num_slots);
-    } else if (rt.k_variant == 8) {
-      route_active_experts<8>(wl, rt.ra.tokens, rt.ra.num_experts, rt.ra.top_k, lane, weids[wave], wk.num_slots);
+    if (rt.decode_all) {
+      // every expert in its own slot (num_slots = num_experts): nothing waits for the logits
+      for (int i = lane; i < wk.num_slots; i += kWave) weids[wave][i] = i;
     } else {
-      route_active_experts<kRouteMaxTopK>(wl, rt.ra.tokens, rt.ra.num_experts, rt.ra.top_k, lane, weids[wave],
-                                          wk.num_slots);
+      float* wl = reinterpret_cast<float*>(outb[wave]);
+      const int nlog = rt.ra.tokens * rt.ra.num_experts;
+      for (int i = lane; i < nlog; i += kWave) wl[i] = rt.ra.logits[i];
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      if (rt.k_variant == 2) {
+        route_active_experts<2>(wl, rt.ra.tokens, rt.ra.num_experts, rt.ra.top_k, lane, weids[wave], wk.num_slots);
+      } else if (rt.k_variant == 8) {
+        route_active_experts<8>(wl, rt.ra.tokens, rt.ra.num_experts, rt.ra.top_k, lane, weids[wave], wk.num_slots);
+      } else {
+        route_active_experts<kRouteMaxTopK>(wl, rt.ra.tokens, rt.ra.num_experts, rt.ra.top_k, lane, weids[wave],
+                                            wk.num_slots);
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -170,7 +186,7 @@ __global__ __launch_bounds__(kSpanThreads) __attribute__((amdgpu_waves_per_eu(5)
     gr_span_words<S>(cur.sp, j);
     __syncthreads();
   } else {
-    gr_item_header<S>(jobs, wk, expert_ids, expert_ids, w, g, cur);  // in flight during the copies below
+    gr_item_header<S>(jobs, wk, nullptr, expert_ids, w, g, cur);  // in flight during the copies below
     const int nl = wk.num_slots < kSpanLdsSlots ? wk.num_slots : kSpanLdsSlots;
     for (int i = tid; i < nl; i += kSpanThreads) eids[i] = expert_ids[i];
     gr_tables_to_lds(&tab);
@@ -277,11 +293,6 @@ int launch_gr_jobs(const GrJobs& jobs, int num_jobs, const int32_t* expert_ids, 
   }
   TRIS_REQUIRE(items < (1LL << 30), "%s: too many blocks", who);
   for (int q = num_jobs; q <= TRIS_MAX_PREDECODE_JOBS; ++q) wk.first[q] = static_cast<int>(items);
-  // persistent workgroups: one wavefront per item up to kSpanWgTarget workgroups (all resident), so every item
-  // that can run at once does; past that each wavefront takes several
-  const int64_t wgs = (items + kSpanWaves - 1) / kSpanWaves;
-  const int64_t grid = wgs < kSpanWgTarget ? wgs : kSpanWgTarget;
-  wk.decode_wgs = static_cast<int>(grid);
   GrReduce red{};
   int64_t reduce_wgs = 0;
   if (reduce != nullptr) {
@@ -292,6 +303,16 @@ int launch_gr_jobs(const GrJobs& jobs, int num_jobs, const int32_t* expert_ids, 
     reduce_wgs = per_proj * reduce_nproj;
   }
   red.blocks_per_proj = red.blocks_per_proj > 0 ? red.blocks_per_proj : 1;
+  TRIS_REQUIRE(reduce_wgs < (1LL << 30), "%s: too many reduction workgroups", who);
+  wk.reduce_wgs = static_cast<int>(reduce_wgs);
+  // persistent workgroups: one wavefront per item up to what is resident beside the route and reduction
+  // workgroups (kSpanWgTarget in all), so every item that can run at once does; past that each wavefront takes
+  // several
+  const int64_t wgs = (items + kSpanWaves - 1) / kSpanWaves;
+  const int64_t others = reduce_wgs + (route != nullptr ? 1 : 0);
+  const int64_t cap = kSpanWgTarget - others > kSpanWgTarget / 2 ? kSpanWgTarget - others : kSpanWgTarget / 2;
+  const int64_t grid = wgs < cap ? wgs : cap;
+  wk.decode_wgs = static_cast<int>(grid);
   GrRoute rt{};
   rt.wg = -1;
   if (route != nullptr) {
@@ -385,7 +406,7 @@ extern "C" int tris_gr_decode_dense(const int32_t* q_gmap_gr_words, const int32_
   return launch_gr_jobs(jobs, 1, expert_ids, num, stream, who);
 }
 
-extern "C" int tris_route_predecode_multi_reduce(const float* router_logits, int32_t num_tokens, int32_t num_experts,
+static int route_predecode(const float* router_logits, int32_t num_tokens, int32_t num_experts,
                                                  int32_t top_k, int32_t renormalize, int32_t m_tile,
                                                  uint16_t* routing_weights_f16, float* routing_weights_f32,
                                                  int64_t* selected_experts, int64_t* perm,
@@ -394,8 +415,7 @@ extern "C" int tris_route_predecode_multi_reduce(const float* router_logits, int
                                                  int32_t* segment_offsets, int32_t* problem_offsets, int32_t* counts,
                                                  int32_t* inverse_perm, const tris_gr_predecode_job* jobs,
                                                  int32_t num_jobs, int32_t num_slots, const tris_backbone_pair_job* bb,
-                                                 void* stream) {
-  const char* who = "tris_route_predecode_multi_reduce";
+                                                 void* stream, bool decode_all, const char* who) {
   GrRoute route{};
   int rc = route_prepare(router_logits, num_tokens, num_experts, top_k, renormalize, m_tile, routing_weights_f16,
                          routing_weights_f32, selected_experts, perm, grouped_token_indices, grouped_slots,
@@ -407,8 +427,14 @@ extern "C" int tris_route_predecode_multi_reduce(const float* router_logits, int
                "%s: the one-wavefront route takes at most %d routed rows and %d experts", who, kRouteWaveMaxRows,
                kRouteLaneMaxExperts);
   const int rows = num_tokens * top_k;
-  TRIS_REQUIRE(num_slots == (num_experts < rows ? num_experts : rows),
-               "%s: num_slots must be min(num_experts, tokens * top_k) = %d", who, num_experts < rows ? num_experts : rows);
+  if (decode_all) {
+    TRIS_REQUIRE(num_slots == num_experts, "%s: num_slots must be num_experts = %d", who, num_experts);
+  } else {
+    TRIS_REQUIRE(num_slots == (num_experts < rows ? num_experts : rows),
+                 "%s: num_slots must be min(num_experts, tokens * top_k) = %d", who,
+                 num_experts < rows ? num_experts : rows);
+  }
+  route.decode_all = decode_all ? 1 : 0;
   route.k_variant = top_k <= 2 ? 2 : (top_k <= 8 ? 8 : kRouteMaxTopK);
   TRIS_REQUIRE(num_jobs >= 0 && num_jobs <= TRIS_MAX_PREDECODE_JOBS && (num_jobs == 0 || jobs != nullptr),
                "%s: %d jobs (0 to %d)", who, num_jobs, TRIS_MAX_PREDECODE_JOBS);
@@ -430,4 +456,35 @@ extern "C" int tris_route_predecode_multi_reduce(const float* router_logits, int
   if (rc) return rc;
   if (pl.slices == 1) return launch_gr_jobs(g, num_jobs, nullptr, num_slots, stream, who, nullptr, 0, &route);
   return launch_gr_jobs(g, num_jobs, nullptr, num_slots, stream, who, &ba, bb->sv_b != nullptr ? 2 : 1, &route);
+}
+
+extern "C" int tris_route_predecode_multi_reduce(const float* router_logits, int32_t num_tokens, int32_t num_experts,
+                                                 int32_t top_k, int32_t renormalize, int32_t m_tile,
+                                                 uint16_t* routing_weights_f16, float* routing_weights_f32,
+                                                 int64_t* selected_experts, int64_t* perm,
+                                                 int64_t* grouped_token_indices, int64_t* grouped_slots,
+                                                 int32_t* grouped_expert_ids, int32_t* expert_ids,
+                                                 int32_t* segment_offsets, int32_t* problem_offsets, int32_t* counts,
+                                                 int32_t* inverse_perm, const tris_gr_predecode_job* jobs,
+                                                 int32_t num_jobs, int32_t num_slots, const tris_backbone_pair_job* bb,
+                                                 void* stream) {
+  return route_predecode(router_logits, num_tokens, num_experts, top_k, renormalize, m_tile, routing_weights_f16,
+                         routing_weights_f32, selected_experts, perm, grouped_token_indices, grouped_slots,
+                         grouped_expert_ids, expert_ids, segment_offsets, problem_offsets, counts, inverse_perm, jobs,
+                         num_jobs, num_slots, bb, stream, false, "tris_route_predecode_multi_reduce");
+}
+
+extern "C" int tris_route_predecode_all_reduce(const float* router_logits, int32_t num_tokens, int32_t num_experts,
+                                               int32_t top_k, int32_t renormalize, int32_t m_tile,
+                                               uint16_t* routing_weights_f16, float* routing_weights_f32,
+                                               int64_t* selected_experts, int64_t* perm,
+                                               int64_t* grouped_token_indices, int64_t* grouped_slots,
+                                               int32_t* grouped_expert_ids, int32_t* expert_ids,
+                                               int32_t* segment_offsets, int32_t* problem_offsets, int32_t* counts,
+                                               int32_t* inverse_perm, const tris_gr_predecode_job* jobs,
+                                               int32_t num_jobs, const tris_backbone_pair_job* bb, void* stream) {
+  return route_predecode(router_logits, num_tokens, num_experts, top_k, renormalize, m_tile, routing_weights_f16,
+                         routing_weights_f32, selected_experts, perm, grouped_token_indices, grouped_slots,
+                         grouped_expert_ids, expert_ids, segment_offsets, problem_offsets, counts, inverse_perm, jobs,
+                         num_jobs, num_experts, bb, stream, true, "tris_route_predecode_all_reduce");
 }

@@ -244,19 +244,20 @@ __device__ inline void gr_tables4_to_lds(GrTables4* dst) {
 __device__ inline void gr_serial_decode(const int32_t* __restrict__ payload, int word_count, int k, int one_count,
                                         uint32_t* out) {
   const int total_bits = word_count * 32;
+  gmem_i32* pl = as_gmem(payload);
   int bit_pos = 0;
   int flat_pos = 0;
   for (int one = 0; one < one_count; ++one) {
     int quotient = 0;
     while (bit_pos < total_bits) {
-      const uint32_t bit = (static_cast<uint32_t>(payload[bit_pos >> 5]) >> (bit_pos & 31)) & 1u;
+      const uint32_t bit = (static_cast<uint32_t>(pl[bit_pos >> 5]) >> (bit_pos & 31)) & 1u;
       ++bit_pos;
       if (bit != 0u) break;
       ++quotient;
     }
     int remainder = 0;
     for (int shift = 0; shift < k && bit_pos < total_bits; ++shift) {
-      remainder |= static_cast<int>((static_cast<uint32_t>(payload[bit_pos >> 5]) >> (bit_pos & 31)) & 1u) << shift;
+      remainder |= static_cast<int>((static_cast<uint32_t>(pl[bit_pos >> 5]) >> (bit_pos & 31)) & 1u) << shift;
       ++bit_pos;
     }
     flat_pos += (quotient << k) | remainder;
@@ -378,8 +379,8 @@ __device__ __forceinline__ void gr_span_header(GrSpan<S>& sp, const int32_t* __r
                                                const int32_t* __restrict__ offsets, const int32_t* __restrict__ meta,
                                                int block_idx, bool valid, const int32_t* __restrict__ dummy) {
   valid = valid && words != nullptr && offsets != nullptr && meta != nullptr;
-  const int32_t* o = valid ? offsets + block_idx : dummy;
-  const int32_t* m = valid ? meta + block_idx : dummy;
+  gmem_i32* o = as_gmem(valid ? offsets + block_idx : dummy);
+  gmem_i32* m = as_gmem(valid ? meta + block_idx : dummy);
   const int begin = o[0];
   const int end = o[valid ? 1 : 0];
   const int mv = m[0];
@@ -400,9 +401,10 @@ __device__ __forceinline__ void gr_span_words(GrSpan<S>& sp, int j) {
     const int rest = wc - sp.w0;
     sp.nw = rest < 0 ? 0 : (rest < span ? rest : span);
   }
+  gmem_i32* src = as_gmem(sp.payload);
 #pragma unroll
   for (int i = 0; i < GrSpan<S>::kMaxWords; ++i) {
-    sp.w[i] = i < sp.nw ? static_cast<uint32_t>(sp.payload[sp.w0 + i]) : 0u;
+    sp.w[i] = i < sp.nw ? static_cast<uint32_t>(src[sp.w0 + i]) : 0u;
   }
 }
 
@@ -428,7 +430,7 @@ __device__ inline void gr_decode_block_group(const GrSpan<S>& sp, const GrTables
         if (i < sp.nw) out[sp.w0 + i] = sp.w[i];
       }
     } else {
-      for (int w = j; w < kGrWords; w += S) out[w] = static_cast<uint32_t>(sp.payload[w]);
+      for (int w = j; w < kGrWords; w += S) out[w] = static_cast<uint32_t>(as_gmem(sp.payload)[w]);
     }
     return;
   }

@@ -565,7 +565,7 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
                         const int32_t* segment_offsets, int num_segments, const int32_t* decoded_a,
                         const int32_t* decoded_b, const tris_compact3_payload* pa, const tris_compact3_payload* pb,
                         uint16_t* out_a, uint16_t* out_b, bool swiglu, void* stream, const char* who,
-                        const int64_t* row_index = nullptr, int hidden_rows = 0);
+                        const int64_t* row_index = nullptr, int hidden_rows = 0, bool decoded_by_expert = false);
 bool grouped_mfma_supported(const tris_compact3_payload* p, const uint16_t* hidden);
 
 }  // namespace tris
@@ -749,6 +749,27 @@ extern "C" int tris_grouped_swiglu_forward_block_gr_predecoded_rows(
   return swiglu_predecoded(hidden_gate, hidden_up, row_index, hidden_rows, batch, expert_ids, segment_offsets,
                            num_segments, total_problem_tiles, decoded_gate, decoded_up, payload_gate, payload_up,
                            output, stream, who);
+}
+
+extern "C" int tris_grouped_forward_block_gr_predecoded_experts(
+    const uint16_t* hidden_a, const uint16_t* hidden_b, const int64_t* row_index, int32_t hidden_rows, int32_t batch,
+    const int32_t* expert_ids, const int32_t* segment_offsets, int32_t num_segments, int64_t total_problem_tiles,
+    const int32_t* decoded_a, const int32_t* decoded_b, const tris_compact3_payload* payload_a,
+    const tris_compact3_payload* payload_b, uint16_t* output_a, uint16_t* output_b, void* stream) {
+  const char* who = "tris_grouped_forward_block_gr_predecoded_experts";
+  TRIS_REQUIRE(payload_a != nullptr, "%s: null payload", who);
+  TRIS_REQUIRE((payload_b == nullptr) == (hidden_b == nullptr), "%s: hidden_b and payload_b go together", who);
+  tris_compact3_payload pa = *payload_a;
+  tris_compact3_payload pb = payload_b != nullptr ? *payload_b : tris_compact3_payload{};
+  pa.has_output_scale = pb.has_output_scale = 0;
+  pa.has_bias = pb.has_bias = 0;
+  TRIS_REQUIRE(grouped_mfma_supported(&pa, hidden_a) && (payload_b == nullptr || grouped_mfma_supported(&pb, hidden_b)),
+               "%s: needs uniform 64-column groups, rank %% 64 == 0 and 16-byte aligned hidden rows", who);
+  TRIS_REQUIRE(payload_b == nullptr || pa.num_experts == pb.num_experts, "%s: expert count mismatch", who);
+  if (total_problem_tiles <= 0) return TRIS_OK;
+  return launch_grouped_mfma(hidden_a, payload_b ? hidden_b : nullptr, batch, expert_ids, segment_offsets, num_segments,
+                             decoded_a, payload_b ? decoded_b : nullptr, &pa, payload_b ? &pb : nullptr, output_a,
+                             payload_b ? output_b : nullptr, false, stream, who, row_index, hidden_rows, true);
 }
 
 extern "C" int tris_compact3_dequant(const tris_compact3_payload* payload, const int32_t* expert_ids, int32_t num,

@@ -65,6 +65,7 @@ struct MfmaArgs {
   const int32_t* expert_ids;
   const int32_t* segment_offsets;
   int num_segments;
+  int decoded_by_expert;  // 0: decoded holds one slot per segment; 1: one per expert id (every expert decoded)
 };
 
 // Position of column k (0..31) of a packed row in the staged order: lane group
@@ -956,6 +957,7 @@ void grouped_mfma_kernel(MfmaArgs a) {
   row0 = __builtin_amdgcn_readfirstlane(row0);
   rc = __builtin_amdgcn_readfirstlane(rc);
   e = __builtin_amdgcn_readfirstlane(e);
+  const int ds = a.decoded_by_expert ? e : s;  // the decoded bitmaps' slot
   const int ob_begin = ob_lo;
   const int ob_end = ob_hi;
   if (e < 0 || e >= p.num_experts) {  // rows routed to no expert: zero output
@@ -972,7 +974,7 @@ void grouped_mfma_kernel(MfmaArgs a) {
   const MfWaveOffsets wo = mf_wave_offsets(pa, 0, wave, lane);
   {  // chunk 0 and the first tile's weights
     MfRegs regs;
-    mf_wave_tile_issue<kCompact>(pa, s, e, ob_begin, wo, lane, wave, tb0);
+    mf_wave_tile_issue<kCompact>(pa, ds, e, ob_begin, wo, lane, wave, tb0);
     mf_chunk_issue(pa, e, row0, rc, 0, utid, regs);
     mf_chunk_write(pa, rc, 0, utid, ch, regs, false, kSal);
     __builtin_amdgcn_s_waitcnt(0);  // LDS copies landed (all counters zero)
@@ -1020,7 +1022,7 @@ void grouped_mfma_kernel(MfmaArgs a) {
       const MfChunkMeta cm = chunk_meta();
       uint32_t q2w[2];
       mf_q2_issue(pa, e, n, cm, q2w);
-      mf_wave_tile_issue<kCompact>(pa, s, e, ob + 1, wo, lane, wave, nxt, ob + 1 < ob_end);  // prefetch
+      mf_wave_tile_issue<kCompact>(pa, ds, e, ob + 1, wo, lane, wave, nxt, ob + 1 < ob_end);  // prefetch
       if (kUnits == 1 && held_ob >= 0) store_held();  // the previous tile's outputs (wave-uniform condition)
       wait_vmcnt<kAfterCopies>();  // this wavefront's copies into `cur` landed
       acc = mf_compute(pa, e, 0, ob * kTileOut, xrow, utid, ch, cm, cur, q2w, acc);
@@ -1029,7 +1031,7 @@ void grouped_mfma_kernel(MfmaArgs a) {
         if (ob > ob_begin || kc > 0) {
           __syncthreads();  // the previous chunk's readers are done
           MfRegs regs;
-          mf_wave_tile_issue<kCompact>(pa, s, e, ob, mf_wave_offsets(pa, kc, wave, lane), lane, wave, cur);
+          mf_wave_tile_issue<kCompact>(pa, ds, e, ob, mf_wave_offsets(pa, kc, wave, lane), lane, wave, cur);
           mf_chunk_issue(pa, e, row0, rc, kc, utid, regs);
           mf_chunk_write(pa, rc, kc, utid, ch, regs, false, kSal);
           __builtin_amdgcn_s_waitcnt(0);
@@ -1320,7 +1322,7 @@ __global__ __launch_bounds__(kUnits * kMfThreads) __attribute__((amdgpu_waves_pe
       __syncthreads();  // the previous item's LDS readers are done
 #pragma unroll
       for (int b = 0; b < kSub; ++b) {
-        if (ob + b < nob) mf_tile_issue(pa, s, e, 0, ob + b, utid, tb[b]);  // uniform; copies into LDS only
+        if (ob + b < nob) mf_tile_issue(pa, a.decoded_by_expert ? e : s, e, 0, ob + b, utid, tb[b]);  // uniform
       }
       if (it == it0) {  // the segment's column data
         MfRegs regs;
@@ -1604,7 +1606,7 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
                         const int32_t* segment_offsets, int num_segments, const int32_t* decoded_a,
                         const int32_t* decoded_b, const tris_compact3_payload* pa, const tris_compact3_payload* pb,
                         uint16_t* out_a, uint16_t* out_b, bool swiglu, void* stream, const char* who,
-                        const int64_t* row_index, int hidden_rows) {
+                        const int64_t* row_index, int hidden_rows, bool decoded_by_expert) {
   TRIS_REQUIRE(batch >= 0 && num_segments >= 0, "%s: negative batch or segment count", who);
   TRIS_REQUIRE(row_index == nullptr || hidden_rows >= 0, "%s: negative hidden row count", who);
   int rc = check_payload(pa, false, who);
@@ -1638,6 +1640,7 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
   args.expert_ids = expert_ids;
   args.segment_offsets = segment_offsets;
   args.num_segments = num_segments;
+  args.decoded_by_expert = decoded_by_expert ? 1 : 0;
   const int units = swiglu ? 2 : 1;
   const int nproj = (pb && !swiglu) ? 2 : 1;
   hipStream_t s = static_cast<hipStream_t>(stream);

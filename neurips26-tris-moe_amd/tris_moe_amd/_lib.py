@@ -181,6 +181,11 @@ SIGNATURES = {
     "tris_route_predecode_multi_reduce": (
         ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                        ctypes.POINTER(TrisPredecodeJob), _I32, _I32, ctypes.POINTER(TrisBackbonePairJob), _P]),
+    "tris_route_predecode_all_reduce": (
+        ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                       ctypes.POINTER(TrisPredecodeJob), _I32, ctypes.POINTER(TrisBackbonePairJob), _P]),
+    "tris_grouped_forward_block_gr_predecoded_experts": (
+        ctypes.c_int, [_P, _P, _P, _I32, _I32, _P, _P, _I32, _I64, _P, _P, _PAY, _PAY, _P, _P, _P]),
     "tris_moe_combine_gated": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _P, _P]),
     "tris_swiglu_mul": (ctypes.c_int, [_P, _P, _I64, _P, _P]),
     "tris_swiglu_mul_compensated": (ctypes.c_int, [_P, _P, _P, _P, _I64, _P, _P]),

@@ -418,12 +418,13 @@ def route_predecode_ok(router_logits: torch.Tensor, top_k: int) -> bool:
 
 
 def route_predecode_multi(router_logits: torch.Tensor, top_k: int, renormalize: bool, m_tile: int, jobs,
-                          backbone: BackbonePending | None = None) -> dict:
+                          backbone: BackbonePending | None = None, decode_all: bool = False) -> dict:
     """route_topk_grouped and grouped_block_gr_predecode_multi of the same route in one launch
     (tris_route_predecode_multi_reduce, an extension): jobs as grouped_block_gr_predecode_multi takes them, each
     buffer [min(E, T * top_k), blocks, 128], or none (the route and the backbone's reduction alone, for the
     GEMMs that decode the bitmaps themselves); ``backbone``: a BackbonePending reduced in the same launch.
-    Returns the route dict of route_topk_grouped."""
+    decode_all: decode every expert into slot e for expert e (tris_route_predecode_all_reduce; buffers
+    [E, blocks, 128], read by the ``decoded_by_expert`` GEMMs).  Returns the route dict of route_topk_grouped."""
     if not route_predecode_ok(router_logits, top_k):
         raise RuntimeError("route_predecode_multi: logits outside the one-wavefront route (T * top_k <= "
                            f"{ROUTE_WAVE_MAX_ROWS}, E <= {ROUTE_WAVE_MAX_EXPERTS})")
@@ -431,7 +432,7 @@ def route_predecode_multi(router_logits: torch.Tensor, top_k: int, renormalize: 
         raise RuntimeError(f"route_predecode_multi: 0 to {_lib.MAX_PREDECODE_JOBS} predecode jobs")
     logits, out = _route_topk_outputs(router_logits, top_k, "route_predecode_multi")
     t, e = int(logits.size(0)), int(logits.size(1))
-    slots = min(e, t * int(top_k))
+    slots = e if decode_all else min(e, t * int(top_k))
     dev = logits.device
     arr = (_lib.TrisPredecodeJob * len(jobs))()
     keep = []
@@ -442,7 +443,8 @@ def route_predecode_multi(router_logits: torch.Tensor, top_k: int, renormalize: 
         _check_cuda("q_gmap_gr_meta", meta, torch.int32, 2, dev)
         nblk = _num_gr_blocks(int(packed_rows), int(outfeatures))
         if buf.numel() != slots * nblk * BLOCK_GR_WORDS_PER_BLOCK:
-            raise RuntimeError("decoded_q_gmap_words must hold [min(E, T * top_k), blocks, 128] words")
+            raise RuntimeError("decoded_q_gmap_words must hold [E, blocks, 128] words" if decode_all else
+                               "decoded_q_gmap_words must hold [min(E, T * top_k), blocks, 128] words")
         if int(offsets.size(1)) != nblk + 1 or int(meta.size(1)) != nblk:
             raise RuntimeError("q_gmap_gr_offsets/meta shape mismatch")
         if words.numel() == 0:
@@ -451,10 +453,15 @@ def route_predecode_multi(router_logits: torch.Tensor, top_k: int, renormalize: 
         arr[q] = _lib.TrisPredecodeJob(_ptr(buf), _ptr(words), _ptr(offsets), _ptr(meta), int(offsets.size(0)),
                                        int(words.size(1)), int(packed_rows), int(outfeatures))
     bb = ctypes.byref(backbone.job) if backbone is not None else None
-    _lib.check(_lib.load().tris_route_predecode_multi_reduce(
-        *_route_topk_args(logits, out, top_k, renormalize, m_tile), arr if jobs else None, len(jobs), slots, bb,
-        _stream(logits)),
-        "route_predecode_multi")
+    lib = _lib.load()
+    if decode_all:
+        _lib.check(lib.tris_route_predecode_all_reduce(
+            *_route_topk_args(logits, out, top_k, renormalize, m_tile), arr if jobs else None, len(jobs), bb,
+            _stream(logits)), "route_predecode_multi")
+    else:
+        _lib.check(lib.tris_route_predecode_multi_reduce(
+            *_route_topk_args(logits, out, top_k, renormalize, m_tile), arr if jobs else None, len(jobs), slots, bb,
+            _stream(logits)), "route_predecode_multi")
     return out
 
 
@@ -619,17 +626,24 @@ def compact3_tris_precomputed_grouped_forward_block_gr_predecoded(hidden, expert
                                                                   decoded_q_gmap_words, qweight1, qweight2_sparse,
                                                                   qweight2_sparse_prefix, c_map, g_idx, col_pack3,
                                                                   row_pack3, use_uniform_k64_groups=False,
-                                                                  out=None):
+                                                                  out=None, decoded_by_expert=False):
     """TriSMoE_cuda.cpp:855-889 (no output scale / bias, as the reference's NoScaleNoBias kernel).
     ``out``: optional [rows, N] fp16 buffer; rows outside every segment are left as they are
-    (the default buffer is zero-filled, as the reference's)."""
+    (the default buffer is zero-filled, as the reference's).  decoded_by_expert: the decoded bitmaps hold every
+    expert, slot e for expert e (tris_grouped_forward_block_gr_predecoded_experts, an extension)."""
     _check_route(hidden, expert_ids, segment_offsets, problem_offsets)
     total = _host_tiles(total_problem_tiles)
     pay = make_payload_struct(int(hidden.size(1)), qweight1, qweight2_sparse, qweight2_sparse_prefix, None, None,
                               None, c_map, g_idx, col_pack3, row_pack3, None, False, None, False,
                               use_uniform_k64_groups, hidden.device, need_gr=False)
-    _check_predecoded(decoded_q_gmap_words, expert_ids, pay, hidden.device)
+    _check_predecoded(decoded_q_gmap_words, expert_ids, pay, hidden.device, decoded_by_expert)
     out = _out_buffer(out, hidden.size(0), pay.outfeatures, hidden.device)
+    if decoded_by_expert:
+        _lib.check(_lib.load().tris_grouped_forward_block_gr_predecoded_experts(
+            _ptr(hidden), None, None, 0, int(hidden.size(0)), _ptr(expert_ids), _ptr(segment_offsets),
+            int(expert_ids.size(0)), total, _ptr(decoded_q_gmap_words), None, ctypes.byref(pay), None, _ptr(out), None,
+            _stream(hidden)), "compact3_tris_precomputed_grouped_forward_block_gr_predecoded")
+        return out
     _lib.check(_lib.load().tris_grouped_forward_block_gr_predecoded(
         _ptr(hidden), int(hidden.size(0)), _ptr(expert_ids), _ptr(segment_offsets), _ptr(problem_offsets),
         int(expert_ids.size(0)), total, _ptr(decoded_q_gmap_words), ctypes.byref(pay), _ptr(out), _stream(hidden)),
@@ -657,10 +671,13 @@ def _gather_rows(row_index, hidden_a, hidden_b):
     return int(row_index.size(0))
 
 
-def _check_predecoded(decoded, expert_ids, pay, device):
+def _check_predecoded(decoded, expert_ids, pay, device, by_expert=False):
     _check_cuda("decoded_q_gmap_words", decoded, torch.int32, None, device)
     nblk = _num_gr_blocks((pay.rank + 31) // 32, pay.outfeatures)
-    if decoded.numel() < int(expert_ids.size(0)) * nblk * BLOCK_GR_WORDS_PER_BLOCK:
+    if by_expert:
+        if decoded.numel() < int(pay.num_experts) * nblk * BLOCK_GR_WORDS_PER_BLOCK:
+            raise RuntimeError("decoded_q_gmap_words is smaller than [experts, blocks, 128]")
+    elif decoded.numel() < int(expert_ids.size(0)) * nblk * BLOCK_GR_WORDS_PER_BLOCK:
         raise RuntimeError("decoded_q_gmap_words is smaller than [segments, blocks, 128]")
 
 
@@ -669,11 +686,12 @@ def compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
         decoded_q_gmap_words_a, qweight1_a, qweight2_sparse_a, qweight2_sparse_prefix_a, c_map_a, g_idx_a,
         col_pack3_a, row_pack3_a, decoded_q_gmap_words_b, qweight1_b, qweight2_sparse_b, qweight2_sparse_prefix_b,
         c_map_b, g_idx_b, col_pack3_b, row_pack3_b, use_uniform_k64_groups=False, out_a=None, out_b=None,
-        row_index=None):
+        row_index=None, decoded_by_expert=False):
     """TriSMoE_cuda.cpp:922-974.  ``out_a`` / ``out_b`` as ``out`` of the single-projection call.
     ``row_index``: optional int64 [batch] (the route's grouped_token_indices): grouped row r reads row
     row_index[r] of per-token hidden_a / hidden_b (tris_grouped_dual_forward_block_gr_predecoded_rows, an
-    extension; the MFMA kernel's payload conditions apply)."""
+    extension; the MFMA kernel's payload conditions apply).  decoded_by_expert: as in the single-projection
+    call."""
     _check_route(hidden_a, expert_ids, segment_offsets, problem_offsets)
     _check_cuda("hidden_b", hidden_b, torch.float16, 2, hidden_a.device)
     batch = _gather_rows(row_index, hidden_a, hidden_b)
@@ -684,10 +702,17 @@ def compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
     pb = make_payload_struct(int(hidden_b.size(1)), qweight1_b, qweight2_sparse_b, qweight2_sparse_prefix_b, None,
                              None, None, c_map_b, g_idx_b, col_pack3_b, row_pack3_b, None, False, None, False,
                              use_uniform_k64_groups, hidden_a.device, need_gr=False, who="grouped payload b")
-    _check_predecoded(decoded_q_gmap_words_a, expert_ids, pa, hidden_a.device)
-    _check_predecoded(decoded_q_gmap_words_b, expert_ids, pb, hidden_a.device)
+    _check_predecoded(decoded_q_gmap_words_a, expert_ids, pa, hidden_a.device, decoded_by_expert)
+    _check_predecoded(decoded_q_gmap_words_b, expert_ids, pb, hidden_a.device, decoded_by_expert)
     out_a = _out_buffer(out_a, batch, pa.outfeatures, hidden_a.device)
     out_b = _out_buffer(out_b, batch, pb.outfeatures, hidden_a.device)
+    if decoded_by_expert:
+        _lib.check(_lib.load().tris_grouped_forward_block_gr_predecoded_experts(
+            _ptr(hidden_a), _ptr(hidden_b), _ptr(row_index), int(hidden_a.size(0)), batch, _ptr(expert_ids),
+            _ptr(segment_offsets), int(expert_ids.size(0)), total, _ptr(decoded_q_gmap_words_a),
+            _ptr(decoded_q_gmap_words_b), ctypes.byref(pa), ctypes.byref(pb), _ptr(out_a), _ptr(out_b),
+            _stream(hidden_a)), "compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded")
+        return [out_a, out_b]
     if row_index is not None:
         _lib.check(_lib.load().tris_grouped_dual_forward_block_gr_predecoded_rows(
             _ptr(hidden_a), _ptr(hidden_b), _ptr(row_index), int(hidden_a.size(0)), batch, _ptr(expert_ids),

@@ -318,6 +318,11 @@ NS_DOWN_BESIDE_GEMM = True
 # 136.7 us before).
 NS_GATE_UP_BESIDE = True
 
+# The decode step decodes every expert's split bitmaps (slot e for expert e) when the batch routes at least this
+# many rows per expert, so the predecode does not wait for the router's selection (at the Mixtral shape, T = 16
+# routes 32 rows over 8 experts and leaves an expert idle about once in 12 steps).
+DECODE_ALL_MIN_ROWS_PER_EXPERT = 4
+
 # From this many tokens the shared expert runs on a side stream beside the routed experts; below it on the
 # caller's stream, since a graph's cross-queue join costs more than the overlap saves there (measured on MI355X at
 # the A3B shape: T = 1 64.3 -> 59.0 us inline; T = 32 138 vs 139 us; T = 1024 339 vs 356 us).
@@ -325,7 +330,7 @@ SHARED_EXPERT_SIDE_STREAM_MIN_TOKENS = 32
 
 
 def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype, shared_expert,
-                            backbone_pending=None, predecoded=None):
+                            backbone_pending=None, predecoded=None, decoded_by_expert=False):
     """Uniform-group payloads without output scale or bias: GR-decode every routed expert's split
     bitmaps once per projection (TriSMoE_cuda.cpp:836-853), then run the predecoded grouped GEMMs
     (TriSMoE_cuda.cpp:855-889, 922-974).  Active experts come first in the padded route, so
@@ -341,7 +346,8 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     backbone_pending: the gate/up backbones of the tokens launched beside the router (ext.BackbonePending);
     their split-K reduction runs in the predecode's launch and the gate/up GEMMs gather their rows through
     the route's token indices.  predecoded: {gate, up, down} buffers already filled for this route (with the
-    backbone's reduction) by the launch that built it (ext.route_predecode_multi)."""
+    backbone's reduction) by the launch that built it (ext.route_predecode_multi); decoded_by_expert: they hold
+    every expert, slot e for expert e (its decode_all)."""
     slots = min(num_experts, R)
     eid = route["expert_ids"][:slots]
     seg = route["segment_offsets"][: slots + 1]
@@ -352,6 +358,9 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     dev = x16.device
     if predecoded is not None and (backbone_pending is None or any(v is not None for v in ns.values())):
         raise RuntimeError("predecoded buffers come with the router-launched backbones and no null-space payloads")
+    if decoded_by_expert and (predecoded is None or R <= FUSED_SWIGLU_MAX_ROWS):
+        raise RuntimeError("bitmaps decoded for every expert come from route_predecode_multi(decode_all=True), "
+                           f"above {FUSED_SWIGLU_MAX_ROWS} routed rows")
     bufs = predecoded if predecoded is not None else {
         name: _predecode_buffer(p, slots, dev) for name, p in (("gate", pg), ("up", pu), ("down", pd))}
     main = torch.cuda.current_stream(dev)
@@ -427,7 +436,7 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
         u = torch.empty((R, n_mlp), dtype=torch.float16, device=dev)
         ext.compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
             hid_g, hid_u, eid, seg, prob, tile_bound, decoded["gate"], *[pg[k] for k in names], decoded["up"],
-            *[pu[k] for k in names], True, out_a=g, out_b=u, row_index=gather)
+            *[pu[k] for k in names], True, out_a=g, out_b=u, row_index=gather, decoded_by_expert=decoded_by_expert)
         if (comp_g is None and comp_u is None and ns["down"] is None
                 and ext.backbone_swiglu_ok(g, backbones["down"], sc["down"])):
             # act_fn(g) * u formed inside the down backbone (nothing else reads the product)
@@ -449,7 +458,8 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
         hid_d = shared_projection(mlp, backbones["down"], in_scale=sc["down"])
     d_out = torch.empty((R, n_out), dtype=torch.float16, device=dev)
     ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
-        hid_d, eid, seg, prob, tile_bound, decoded["down"], *[pd[k] for k in names], True, out=d_out)
+        hid_d, eid, seg, prob, tile_bound, decoded["down"], *[pd[k] for k in names], True, out=d_out,
+        decoded_by_expert=decoded_by_expert)
     if comp_d is not None:
         main.wait_stream(side)
     elif ns["down"] is not None:
@@ -545,15 +555,20 @@ def grouped_moe_decode_step(x: torch.Tensor, router_weight: torch.Tensor, top_k:
         out = _decode_fused_moe_forward(x16, route["routing_weights_f16"], route, payloads, backbones, num_experts, R,
                                         output_dtype, shared, hidden_pair=(pending.out_a, pending.out_b))
         return out, logits
-    slots = min(num_experts, R)
+    # with rows enough to reach nearly every expert, every expert is decoded (slot e for expert e), so the decoders
+    # need nothing from the route and start without reading the logits
+    decode_all = R >= DECODE_ALL_MIN_ROWS_PER_EXPERT * num_experts and R > FUSED_SWIGLU_MAX_ROWS
+    slots = num_experts if decode_all else min(num_experts, R)
     dev = x.device
     order = (("gate", payloads["gate"]), ("up", payloads["up"]), ("down", payloads["down"]))
     bufs = {name: _predecode_buffer(p, slots, dev) for name, p in order}
     jobs = [(bufs[name], p["q_gmap_gr_words"], p["q_gmap_gr_offsets"], p["q_gmap_gr_meta"],
              int(p["qweight1"].size(1)), int(p["qweight1"].size(2))) for name, p in order]
-    route = ext.route_predecode_multi(logits32, top_k, renormalize, GROUPED_SEGMENT_M_TILE, jobs, backbone=pending)
+    route = ext.route_predecode_multi(logits32, top_k, renormalize, GROUPED_SEGMENT_M_TILE, jobs, backbone=pending,
+                                      decode_all=decode_all)
     out = _predecoded_moe_forward(x16, route["routing_weights_f16"], route, payloads, backbones, num_experts, R,
-                                  output_dtype, shared, backbone_pending=pending, predecoded=bufs)
+                                  output_dtype, shared, backbone_pending=pending, predecoded=bufs,
+                                  decoded_by_expert=decode_all)
     return out, logits
 
 

@@ -390,3 +390,74 @@ def test_block_decode_step_matches_unfused_block(tris, oracle_mod, cuda, tokens,
         want = block.forward_routed(flat, lg32, x16=x16)
     assert torch.equal(logits.view(torch.int16), lg.view(torch.int16))
     assert torch.equal(out.reshape(tokens, SPEC.hidden).view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("case", [(16, 8, 2), (3, 8, 2), (5, 6, 3)], ids=lambda c: "T{}E{}k{}".format(*c))
+def test_route_predecode_all_experts_matches_separate_launches(tris, cuda, case):
+    """tris_route_predecode_all_reduce (decode_all: every expert's bitmaps, slot e for expert e, with the route and
+    the backbones' reduction in the same launch) writes tris_route_topk_grouped's route and, in slot e,
+    tris_grouped_block_gr_predecode_multi's bitmaps of expert e, also for experts the route leaves idle (T = 3 and
+    5 route fewer rows than there are experts)."""
+    t, e, k = case
+    note(f"route+predecode of every expert T={t} E={e} k={k}")
+    ext = tris["ext"]
+    rng = np.random.default_rng(t * 13 + e)
+    hidden, rank = 512, 256
+    x = torch.from_numpy(rng.standard_normal((t, hidden)).astype(np.float32)).to(torch.bfloat16).to(cuda)
+    w = torch.from_numpy((rng.standard_normal((e, hidden)) / np.sqrt(hidden)).astype(np.float32))
+    w = w.to(torch.bfloat16).to(cuda)
+    _, sv_a, sv_b, sa, sb = backbone_inputs(t + 200, t, hidden, rank, False, cuda)
+    logits, logits32, x16, pending = ext.router_backbone_pair(x, w, sv_a, sv_b, in_scale_a=sa, in_scale_b=sb)
+    projs = [make_projection(tris, 400 + i, e, n, kk) for i, (n, kk) in enumerate([(256, 128), (192, 256)])]
+    pays = [tris["qlinear"].payload_to_device(p, cuda) for p in projs]
+    jobs, bufs = [], []
+    for p in pays:
+        pr, n = int(p["qweight1"].size(1)), int(p["qweight1"].size(2))
+        nblk = ((pr + 1) // 2) * ((n + 63) // 64)
+        buf = torch.full((e, nblk, 128), -7, dtype=torch.int32, device=cuda)
+        bufs.append(buf)
+        jobs.append((buf, p["q_gmap_gr_words"], p["q_gmap_gr_offsets"], p["q_gmap_gr_meta"], pr, n))
+    route = ext.route_predecode_multi(logits32, k, True, 4, jobs, backbone=pending, decode_all=True)
+    want_route = ext.route_topk_grouped(logits32, k, True, 4)
+    for key in ROUTE_KEYS:
+        assert torch.equal(route[key], want_route[key]), key
+    ref_bufs = [torch.full_like(b, -7) for b in bufs]
+    ext.grouped_block_gr_predecode_multi([(rb,) + j[1:] for rb, j in zip(ref_bufs, jobs)],
+                                         torch.arange(e, dtype=torch.int32, device=cuda))
+    for b, rb in zip(bufs, ref_bufs):
+        assert torch.equal(b, rb)
+    want_a, want_b = ext.backbone_linear_pair(x16, sv_a, sv_b, in_scale_a=sa, in_scale_b=sb)
+    assert torch.equal(pending.out_a.view(torch.int16), want_a.view(torch.int16))
+    assert torch.equal(pending.out_b.view(torch.int16), want_b.view(torch.int16))
+
+
+@pytest.mark.parametrize("tokens", [4, 16])
+def test_block_decode_step_decoding_every_expert_matches_unfused_block(tris, cuda, tokens, monkeypatch):
+    """The decode step with every expert's bitmaps decoded (moe.DECODE_ALL_MIN_ROWS_PER_EXPERT lowered to 1, so T = 4
+    takes it with 8 routed rows over 8 experts and some experts idle: segment s reads slot expert_ids[s], not s)
+    gives the unfused block's output and router logits bit for bit on the C1 layer."""
+    from tris_moe_amd.configs import C1_MIXTRAL_DECODE as SPEC
+
+    note(f"block decode step, every expert decoded, T={tokens}")
+    syn, ql, moe = tris["synthetic"], tris["qlinear"], tris["moe"]
+    monkeypatch.setattr(moe, "DECODE_ALL_MIN_ROWS_PER_EXPERT", 1)
+    layer = syn.make_layer(SPEC, 6300 + tokens, tris["ext"].gr_encode)
+    payloads = {p: ql.payload_to_device(layer[p], cuda) for p in ("gate", "up", "down")}
+    backbones = {p: torch.from_numpy(layer["backbones"][p]).to(cuda) for p in ("gate", "up", "down")}
+    rng = np.random.default_rng(tokens + 50)
+    router = torch.from_numpy((rng.standard_normal((SPEC.num_experts, SPEC.hidden)) * 0.015).astype(np.float32))
+    block = moe.TrisSparseMoeBlock(SPEC.hidden, SPEC.num_experts, SPEC.top_k, payloads, backbones,
+                                   router_weight=router.to(cuda))
+    inp = syn.make_inputs(SPEC, tokens, 6400 + tokens, layer["outlier_idx"])
+    h = torch.from_numpy(inp["x"]).to(cuda).to(torch.bfloat16)
+    flat = h.reshape(-1, SPEC.hidden)
+    with torch.no_grad():
+        lg, lg32, x16 = tris["ext"].router_linear(flat, block.gate.weight.detach())
+        # T = 4 routes 8 rows: with this seed some experts are idle, so segments and expert ids differ
+        active = torch.unique(torch.topk(lg32, SPEC.top_k, dim=1).indices)
+        out, logits = block(h.reshape(1, tokens, SPEC.hidden))
+        want = block.forward_routed(flat, lg32, x16=x16)
+    if tokens == 4:
+        assert int(active.numel()) < SPEC.num_experts, "the case needs an idle expert"
+    assert torch.equal(logits.view(torch.int16), lg.view(torch.int16))
+    assert torch.equal(out.reshape(tokens, SPEC.hidden).view(torch.int16), want.view(torch.int16))
