@@ -262,10 +262,16 @@ typedef struct tris_backbone_pair_job {
   int32_t rank;
   const uint16_t* in_scale_a;  /* fp16 [in_features] or NULL */
   const uint16_t* in_scale_b;
-  uint16_t* out_a;             /* fp16 [tokens, rank] */
+  uint16_t* out_a;             /* fp16 [tokens, rank], or [tokens, split] with a column split */
   uint16_t* out_b;
   void* workspace;
   int64_t workspace_bytes;
+  /* Column split (0: none).  With split in (0, rank) each projection is two stacked ones: out_a / out_b hold
+   * columns [0, split) as [tokens, split] and out_a_hi / out_b_hi columns [split, rank) as [tokens, rank - split]
+   * (the same values the whole projection gives in those columns).  Decode-size launches only. */
+  uint16_t* out_a_hi;
+  uint16_t* out_b_hi;
+  int32_t split;
 } tris_backbone_pair_job;
 
 /*
@@ -475,6 +481,19 @@ int tris_backbone_swiglu_linear(const uint16_t* gate, const uint16_t* up, int32_
                                 const uint16_t* sv, int32_t rank, const uint16_t* in_scale, uint16_t* out,
                                 void* workspace, int64_t workspace_bytes, void* stream);
 int64_t tris_backbone_swiglu_workspace_bytes(int32_t rows, int32_t in_features, int32_t rank);
+
+/*
+ * tris_backbone_swiglu_linear of two stacked projections with its output split by columns (no reference
+ * counterpart: it runs the routed experts' down backbone, compute_shared_hidden of qlinear_cuda.py:4454-4502, and
+ * the always-on shared expert's down projection, modeling_qwen2_moe.py:815-818, as one projection of the stacked
+ * weights over the stacked rows).  out fp16 [rows, split] gets columns [0, split), out_hi fp16
+ * [rows, rank - split] columns [split, rank), each the value the whole projection gives there.  0 < split < rank;
+ * at most 128 rows (the decode kernel; else TRIS_ERR_INVALID); workspace as tris_backbone_swiglu_linear's.
+ */
+int tris_backbone_swiglu_linear_split(const uint16_t* gate, const uint16_t* up, int32_t rows, int32_t in_features,
+                                      const uint16_t* sv, int32_t rank, const uint16_t* in_scale, uint16_t* out,
+                                      uint16_t* out_hi, int32_t split, void* workspace, int64_t workspace_bytes,
+                                      void* stream);
 
 /*
  * 4-bit packed backbone matrix (PackedQuantMatrix4bit buffers, qlinear_cuda.py:2637-2786):

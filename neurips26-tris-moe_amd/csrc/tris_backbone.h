@@ -40,7 +40,20 @@ struct BackboneProj {
   const uint16_t* sv;
   uint16_t* out;
   const uint16_t* in_scale;  // fp16 [in] per-column input scale of this projection, or null
+  // split > 0: the projection is two stacked ones; out holds columns [0, split) as [tokens, split] and out_hi
+  // columns [split, rank) as [tokens, rank - split]
+  uint16_t* out_hi;
+  int split;
 };
+
+// Stores output (row, col) of a projection of `rank` columns, through its column split.
+__device__ __forceinline__ void bb_store(const BackboneProj& pj, int rank, int64_t row, int col, uint16_t v) {
+  if (pj.split > 0 && col >= pj.split) {
+    pj.out_hi[row * (rank - pj.split) + (col - pj.split)] = v;
+  } else {
+    pj.out[row * (pj.split > 0 ? pj.split : rank) + col] = v;
+  }
+}
 
 struct BackboneArgs {
   const uint16_t* x;
@@ -197,7 +210,7 @@ __device__ __forceinline__ void backbone_block(const BackboneArgs& a, bool activ
         const int tt = t0 + 4 * kg + v;
         if (tt < a.tokens && col < a.rank) {
           if (a.slices == 1) {
-            pj.out[static_cast<int64_t>(tt) * a.rank + col] = f2h_bits(acc[j][v]);
+            bb_store(pj, a.rank, tt, col, f2h_bits(acc[j][v]));
           } else {
             part[static_cast<int64_t>(tt) * a.rank + col] = acc[j][v];
           }
@@ -220,7 +233,12 @@ __device__ __forceinline__ void backbone_reduce_at(const BackboneArgs& a, int64_
   for (int s = 0; s < kBbReduceMaxSlices; ++s) {
     if (s < a.slices) sum += v[s];
   }
-  a.proj[q].out[idx] = f2h_bits(sum);
+  const BackboneProj& pj = a.proj[q];
+  if (pj.split > 0) {
+    bb_store(pj, a.rank, idx / a.rank, static_cast<int>(idx % a.rank), f2h_bits(sum));
+  } else {
+    pj.out[idx] = f2h_bits(sum);
+  }
 }
 
 
@@ -242,5 +260,8 @@ int backbone_prepare(const uint16_t* x, int tokens, int in_features, const int64
                      BackbonePlan* plan, const char* who, bool use_gemm = false);
 // The slice reduction of a launch that left its partial sums in args.partials (slices > 1).
 int launch_backbone_reduce(const BackboneArgs& args, int nproj, hipStream_t s, const char* who);
+// backbone_prepare for a tris_backbone_pair_job, with its column split (decode-size launches only: the tiled
+// GEMM of prefill batches stores whole rows).
+int backbone_prepare_job(const tris_backbone_pair_job* bb, BackboneArgs* args, BackbonePlan* plan, const char* who);
 
 }  // namespace tris

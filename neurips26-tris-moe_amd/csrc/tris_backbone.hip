@@ -109,8 +109,8 @@ int backbone_prepare(const uint16_t* x, int tokens, int in_features, const int64
   BackboneArgs a{};
   a.x = x;
   a.row_index = row_index;
-  a.proj[0] = BackboneProj{sv_a, out_a, in_scale_a};
-  a.proj[1] = BackboneProj{sv_b, out_b, in_scale_b};
+  a.proj[0] = BackboneProj{sv_a, out_a, in_scale_a, nullptr, 0};
+  a.proj[1] = BackboneProj{sv_b, out_b, in_scale_b, nullptr, 0};
   a.partials = static_cast<float*>(workspace);
   a.tokens = tokens;
   a.in_features = in_features;
@@ -119,6 +119,24 @@ int backbone_prepare(const uint16_t* x, int tokens, int in_features, const int64
   a.slice_k = pl.slice_k;
   *args = a;
   *plan = pl;
+  return TRIS_OK;
+}
+
+int backbone_prepare_job(const tris_backbone_pair_job* bb, BackboneArgs* args, BackbonePlan* plan, const char* who) {
+  const int rc = backbone_prepare(bb->x, bb->tokens, bb->in_features, nullptr, bb->sv_a, bb->sv_b, bb->rank,
+                                  bb->in_scale_a, bb->in_scale_b, bb->out_a, bb->out_b, bb->workspace,
+                                  bb->workspace_bytes, args, plan, who);
+  if (rc) return rc;
+  TRIS_REQUIRE(bb->split >= 0 && bb->split < bb->rank, "%s: column split %d outside [0, %d)", who, bb->split,
+               bb->rank);
+  if (bb->split > 0) {
+    TRIS_REQUIRE(bb->out_a_hi != nullptr && (bb->sv_b == nullptr || bb->out_b_hi != nullptr),
+                 "%s: a column split needs out_a_hi (and out_b_hi for two projections)", who);
+    args->proj[0].out_hi = bb->out_a_hi;
+    args->proj[0].split = bb->split;
+    args->proj[1].out_hi = bb->out_b_hi;
+    args->proj[1].split = bb->sv_b != nullptr ? bb->split : 0;
+  }
   return TRIS_OK;
 }
 
@@ -677,9 +695,11 @@ struct SwigluBackboneArgs {
   const uint16_t* u;         // [rows, in_features]
   const uint16_t* sv;        // [rank, in_features]
   const uint16_t* in_scale;  // [in_features] or null
-  uint16_t* out;             // [rows, rank] (written directly when slices == 1)
+  uint16_t* out;             // [rows, rank] (written directly when slices == 1), or [rows, split] with a split
   float* partials;           // [slices][rows][rank]
   int rows, in_features, rank, slices, slice_k;
+  uint16_t* out_hi;          // with split > 0: columns [split, rank) as [rows, rank - split]
+  int split;
 };
 
 template <int TT>
@@ -766,7 +786,7 @@ __global__ __launch_bounds__(kSgThreads) void backbone_swiglu_kernel(SwigluBackb
         const int r = 16 * rt + 4 * kg + v;
         if (r >= a.rows) continue;
         if (a.slices == 1) {
-          a.out[static_cast<int64_t>(r) * a.rank + col] = f2h_bits(acc[rt][v]);
+          bb_store(BackboneProj{a.sv, a.out, a.in_scale, a.out_hi, a.split}, a.rank, r, col, f2h_bits(acc[rt][v]));
         } else {
           a.partials[(static_cast<int64_t>(slice) * a.rows + r) * a.rank + col] = acc[rt][v];
         }
@@ -1203,10 +1223,9 @@ extern "C" int64_t tris_backbone_swiglu_workspace_bytes(int32_t rows, int32_t in
   return slices > 1 ? static_cast<int64_t>(slices) * rows * rank * 4 : 0;
 }
 
-extern "C" int tris_backbone_swiglu_linear(const uint16_t* gate, const uint16_t* up, int32_t rows, int32_t in_features,
-                                           const uint16_t* sv, int32_t rank, const uint16_t* in_scale, uint16_t* out,
-                                           void* workspace, int64_t workspace_bytes, void* stream) {
-  const char* who = "tris_backbone_swiglu_linear";
+static int swiglu_linear(const uint16_t* gate, const uint16_t* up, int32_t rows, int32_t in_features,
+                         const uint16_t* sv, int32_t rank, const uint16_t* in_scale, uint16_t* out, uint16_t* out_hi,
+                         int32_t split, void* workspace, int64_t workspace_bytes, void* stream, const char* who) {
   TRIS_REQUIRE(rows >= 0 && in_features >= 0 && rank >= 0, "%s: negative shape", who);
   if (rows == 0 || rank == 0) return TRIS_OK;
   TRIS_REQUIRE(in_features > 0 && in_features % 32 == 0, "%s: in_features %d must be a positive multiple of 32", who,
@@ -1222,6 +1241,10 @@ extern "C" int tris_backbone_swiglu_linear(const uint16_t* gate, const uint16_t*
                "%s: workspace of %lld bytes needed, %lld given", who, static_cast<long long>(need),
                static_cast<long long>(workspace_bytes));
   hipStream_t s = static_cast<hipStream_t>(stream);
+  TRIS_REQUIRE(split >= 0 && split < rank && (split == 0 || out_hi != nullptr), "%s: column split %d of %d columns",
+               who, split, rank);
+  TRIS_REQUIRE(split == 0 || !swiglu_backbone_gemm(rows, in_features, rank),
+               "%s: a column split takes at most %d rows (the decode kernel)", who, kSgMaxRowTiles * 16);
   if (swiglu_backbone_gemm(rows, in_features, rank)) {
     BackboneArgs ga{};
     ga.x = gate;
@@ -1235,7 +1258,7 @@ extern "C" int tris_backbone_swiglu_linear(const uint16_t* gate, const uint16_t*
   int slices = 1;
   const int slice_k = swiglu_backbone_slice_k(in_features, rank, &slices);
   SwigluBackboneArgs a{gate, up, sv, in_scale, out, static_cast<float*>(workspace), rows, in_features, rank, slices,
-                       slice_k};
+                       slice_k, out_hi, split};
   const int tt = ceil_div(rows, 16);
   const size_t lds = static_cast<size_t>(tt) * 16 * (slice_k + 8) * 2;
   const dim3 grid(ceil_div(rank, kSgCols), slices);
@@ -1253,12 +1276,31 @@ extern "C" int tris_backbone_swiglu_linear(const uint16_t* gate, const uint16_t*
   if (rc || slices == 1) return rc;
   BackboneArgs ra{};
   ra.proj[0].out = out;
+  ra.proj[0].out_hi = out_hi;
+  ra.proj[0].split = split;
   ra.partials = static_cast<float*>(workspace);
   ra.tokens = rows;
   ra.in_features = in_features;
   ra.rank = rank;
   ra.slices = slices;
   return launch_backbone_reduce(ra, 1, s, who);
+}
+
+extern "C" int tris_backbone_swiglu_linear(const uint16_t* gate, const uint16_t* up, int32_t rows, int32_t in_features,
+                                           const uint16_t* sv, int32_t rank, const uint16_t* in_scale, uint16_t* out,
+                                           void* workspace, int64_t workspace_bytes, void* stream) {
+  return swiglu_linear(gate, up, rows, in_features, sv, rank, in_scale, out, nullptr, 0, workspace, workspace_bytes,
+                       stream, "tris_backbone_swiglu_linear");
+}
+
+extern "C" int tris_backbone_swiglu_linear_split(const uint16_t* gate, const uint16_t* up, int32_t rows,
+                                                 int32_t in_features, const uint16_t* sv, int32_t rank,
+                                                 const uint16_t* in_scale, uint16_t* out, uint16_t* out_hi,
+                                                 int32_t split, void* workspace, int64_t workspace_bytes,
+                                                 void* stream) {
+  TRIS_REQUIRE(split > 0, "tris_backbone_swiglu_linear_split: split %d must be positive", split);
+  return swiglu_linear(gate, up, rows, in_features, sv, rank, in_scale, out, out_hi, split, workspace,
+                       workspace_bytes, stream, "tris_backbone_swiglu_linear_split");
 }
 
 extern "C" int tris_packed4_dequant(const tris_packed4_matrix* w, uint16_t* out, void* stream) {

@@ -385,9 +385,7 @@ extern "C" int tris_grouped_block_gr_predecode_multi_reduce(const tris_gr_predec
   }
   BackboneArgs ba;
   BackbonePlan pl;
-  int rc = backbone_prepare(bb->x, bb->tokens, bb->in_features, nullptr, bb->sv_a, bb->sv_b, bb->rank,
-                            bb->in_scale_a, bb->in_scale_b, bb->out_a, bb->out_b, bb->workspace, bb->workspace_bytes,
-                            &ba, &pl, who);
+  int rc = backbone_prepare_job(bb, &ba, &pl, who);
   if (rc) return rc;
   if (pl.slices == 1) return launch_gr_jobs(g, num_jobs, expert_ids, num_active, stream, who);  // nothing deferred
   return launch_gr_jobs(g, num_jobs, expert_ids, num_active, stream, who, &ba, bb->sv_b != nullptr ? 2 : 1);
@@ -451,8 +449,7 @@ static int route_predecode(const float* router_logits, int32_t num_tokens, int32
   }
   BackboneArgs ba;
   BackbonePlan pl;
-  rc = backbone_prepare(bb->x, bb->tokens, bb->in_features, nullptr, bb->sv_a, bb->sv_b, bb->rank, bb->in_scale_a,
-                        bb->in_scale_b, bb->out_a, bb->out_b, bb->workspace, bb->workspace_bytes, &ba, &pl, who);
+  rc = backbone_prepare_job(bb, &ba, &pl, who);
   if (rc) return rc;
   if (pl.slices == 1) return launch_gr_jobs(g, num_jobs, nullptr, num_slots, stream, who, nullptr, 0, &route);
   return launch_gr_jobs(g, num_jobs, nullptr, num_slots, stream, who, &ba, bb->sv_b != nullptr ? 2 : 1, &route);

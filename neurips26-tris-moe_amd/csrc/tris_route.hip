@@ -957,8 +957,7 @@ extern "C" int tris_route_topk_backbone(const float* router_logits, int32_t num_
   if (num_tokens == 0) return TRIS_OK;
   BackboneArgs ba;
   BackbonePlan pl;
-  rc = backbone_prepare(bb->x, bb->tokens, bb->in_features, nullptr, bb->sv_a, bb->sv_b, bb->rank, bb->in_scale_a,
-                        bb->in_scale_b, bb->out_a, bb->out_b, bb->workspace, bb->workspace_bytes, &ba, &pl, who);
+  rc = backbone_prepare_job(bb, &ba, &pl, who);
   if (rc) return rc;
   const int nproj = bb->sv_b != nullptr ? 2 : 1;
   const int gx = pl.row_tiles;
@@ -1047,8 +1046,7 @@ extern "C" int tris_router_backbone(const uint16_t* x, const uint16_t* router_we
   TRIS_REQUIRE(tokens <= kRbMaxTokens, "%s: %d tokens exceed the merged launch's %d", who, tokens, kRbMaxTokens);
   BackboneArgs ba;
   BackbonePlan pl;
-  int rc = backbone_prepare(bb->x, bb->tokens, bb->in_features, nullptr, bb->sv_a, bb->sv_b, bb->rank, bb->in_scale_a,
-                            bb->in_scale_b, bb->out_a, bb->out_b, bb->workspace, bb->workspace_bytes, &ba, &pl, who);
+  int rc = backbone_prepare_job(bb, &ba, &pl, who);
   if (rc) return rc;
   const int nproj = bb->sv_b != nullptr ? 2 : 1;
   const int gx = pl.row_tiles;

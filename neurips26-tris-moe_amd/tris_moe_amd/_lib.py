@@ -80,6 +80,9 @@ class TrisBackbonePairJob(ctypes.Structure):
         ("out_b", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_int64),
+        ("out_a_hi", ctypes.c_void_p),
+        ("out_b_hi", ctypes.c_void_p),
+        ("split", ctypes.c_int32),
     ]
 
 
@@ -166,6 +169,8 @@ SIGNATURES = {
     "tris_backbone_linear_pair": (ctypes.c_int, [_P, _I32, _I32, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _I64, _P]),
     "tris_backbone_pair_workspace_bytes": (_I64, [_I32, _I32, _I32]),
     "tris_backbone_swiglu_linear": (ctypes.c_int, [_P, _P, _I32, _I32, _P, _I32, _P, _P, _P, _I64, _P]),
+    "tris_backbone_swiglu_linear_split": (ctypes.c_int, [_P, _P, _I32, _I32, _P, _I32, _P, _P, _P, _I32, _P, _I64,
+                                                         _P]),
     "tris_backbone_swiglu_workspace_bytes": (_I64, [_I32, _I32, _I32]),
     "tris_backbone_linear_pair_scatter": (ctypes.c_int, [_P, _I32, _I32, _P, _P, _I32, _P, _P, _P, _I32, _I32, _P, _P,
                                                           _P, _I64, _P]),

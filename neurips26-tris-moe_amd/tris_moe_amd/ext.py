@@ -339,18 +339,30 @@ def route_topk_backbone_ok(x: torch.Tensor, sv_a, sv_b, in_scale_a=None, in_scal
 
 def route_topk_backbone_pair(router_logits: torch.Tensor, top_k: int, renormalize: bool, m_tile: int,
                              x: torch.Tensor, sv_a: torch.Tensor, sv_b: torch.Tensor,
-                             in_scale_a: torch.Tensor | None = None, in_scale_b: torch.Tensor | None = None):
+                             in_scale_a: torch.Tensor | None = None, in_scale_b: torch.Tensor | None = None,
+                             split: int = 0, out_a_hi: torch.Tensor | None = None,
+                             out_b_hi: torch.Tensor | None = None):
     """route_topk_grouped and the gate/up backbones of the same tokens (backbone_linear_pair without a row
     index) in one launch (tris_route_topk_backbone, an extension).  Returns (route dict, BackbonePending): the
-    backbone's split-K reduction is left for the predecode launch."""
+    backbone's split-K reduction is left for the predecode launch.  split > 0: sv_a / sv_b are two stacked
+    projections each; the pending outputs hold columns [0, split) and out_a_hi / out_b_hi (fp16
+    [tokens, rank - split], given) receive columns [split, rank)."""
     if not route_topk_backbone_ok(x, sv_a, sv_b, in_scale_a, in_scale_b):
         raise RuntimeError("route_topk_backbone_pair: backbone pair outside the merged launch's conditions")
     logits, out = _route_topk_outputs(router_logits, top_k, "route_topk_backbone_pair")
     if int(x.size(0)) != int(logits.size(0)):
         raise RuntimeError("route_topk_backbone_pair: x and router_logits differ in tokens")
     tokens, in_f, rank = int(x.size(0)), int(x.size(1)), int(sv_a.size(0))
-    out_a = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
-    out_b = torch.empty((tokens, rank), dtype=torch.float16, device=x.device)
+    lo = split if split > 0 else rank
+    if split > 0:
+        if not 0 < split < rank:
+            raise RuntimeError("route_topk_backbone_pair: split outside (0, rank)")
+        for name, t in (("out_a_hi", out_a_hi), ("out_b_hi", out_b_hi)):
+            _check_cuda(name, t, torch.float16, 2, x.device)
+            if tuple(t.shape) != (tokens, rank - split) or not t.is_contiguous():
+                raise RuntimeError(f"route_topk_backbone_pair: {name} must be a contiguous [{tokens}, {rank - split}]")
+    out_a = torch.empty((tokens, lo), dtype=torch.float16, device=x.device)
+    out_b = torch.empty((tokens, lo), dtype=torch.float16, device=x.device)
     lib = _lib.load()
     nbytes = int(lib.tris_backbone_pair_workspace_bytes(tokens, in_f, rank))
     # a buffer of this call's own, held by the BackbonePending until the launch that reduces the partial sums
@@ -358,10 +370,12 @@ def route_topk_backbone_pair(router_logits: torch.Tensor, top_k: int, renormaliz
     # other streams, or a second call before the first is reduced, each keep their own partial sums
     ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=x.device)
     job = _lib.TrisBackbonePairJob(_ptr(x), tokens, in_f, _ptr(sv_a), _ptr(sv_b), rank, _ptr(in_scale_a),
-                                   _ptr(in_scale_b), _ptr(out_a), _ptr(out_b), _ptr(ws), int(ws.numel()))
+                                   _ptr(in_scale_b), _ptr(out_a), _ptr(out_b), _ptr(ws), int(ws.numel()),
+                                   _ptr(out_a_hi) if split > 0 else None, _ptr(out_b_hi) if split > 0 else None,
+                                   int(split))
     _lib.check(lib.tris_route_topk_backbone(*_route_topk_args(logits, out, top_k, renormalize, m_tile),
                                             ctypes.byref(job), 1, _stream(logits)), "route_topk_backbone_pair")
-    return out, BackbonePending(job, out_a, out_b, (x, sv_a, sv_b, in_scale_a, in_scale_b, ws))
+    return out, BackbonePending(job, out_a, out_b, (x, sv_a, sv_b, in_scale_a, in_scale_b, ws, out_a_hi, out_b_hi))
 
 
 ROUTE_WAVE_MAX_ROWS = 64     # tokens * top_k of the one-wavefront route (tris_route_predecode_multi_reduce)
@@ -1141,6 +1155,40 @@ def backbone_swiglu_linear(gate: torch.Tensor, up: torch.Tensor, sv: torch.Tenso
                                                _ptr(out), _ptr(ws), int(ws.numel()), _stream(gate)),
                "tris_backbone_swiglu_linear")
     return out
+
+
+def backbone_swiglu_linear_split(gate: torch.Tensor, up: torch.Tensor, sv: torch.Tensor, split: int,
+                                 in_scale: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                                 out_hi: torch.Tensor | None = None):
+    """backbone_swiglu_linear of two stacked projections, its output split by columns
+    (tris_backbone_swiglu_linear_split, an extension): returns (out [rows, split], out_hi [rows, rank - split]).
+    At most SWIGLU_BACKBONE_MAX_ROWS rows."""
+    _check_cuda("gate", gate, torch.float16, 2)
+    _check_cuda("up", up, torch.float16, 2, gate.device)
+    _check_cuda("shared_sv", sv, torch.float16, 2, gate.device)
+    if up.shape != gate.shape or int(sv.size(1)) != int(gate.size(1)):
+        raise RuntimeError("backbone_swiglu_linear_split: shape mismatch")
+    if in_scale is not None:
+        _check_cuda("in_scale", in_scale, torch.float16, 1, gate.device)
+    rows, in_f, rank = int(gate.size(0)), int(gate.size(1)), int(sv.size(0))
+    if not 0 < int(split) < rank:
+        raise RuntimeError("backbone_swiglu_linear_split: split outside (0, rank)")
+    bufs = []
+    for name, t, cols in (("out", out, int(split)), ("out_hi", out_hi, rank - int(split))):
+        if t is None:
+            t = torch.empty((rows, cols), dtype=torch.float16, device=gate.device)
+        else:
+            _check_cuda(name, t, torch.float16, 2, gate.device)
+            if tuple(t.shape) != (rows, cols) or not t.is_contiguous():
+                raise RuntimeError(f"backbone_swiglu_linear_split: {name} must be a contiguous [{rows}, {cols}]")
+        bufs.append(t)
+    lib = _lib.load()
+    ws = backbone_workspace(gate.device, int(lib.tris_backbone_swiglu_workspace_bytes(rows, in_f, rank)))
+    _lib.check(lib.tris_backbone_swiglu_linear_split(_ptr(gate), _ptr(up), rows, in_f, _ptr(sv), rank, _ptr(in_scale),
+                                                     _ptr(bufs[0]), _ptr(bufs[1]), int(split), _ptr(ws),
+                                                     int(ws.numel()), _stream(gate)),
+               "tris_backbone_swiglu_linear_split")
+    return bufs[0], bufs[1]
 
 
 # ----------------------------------------------------------------------------------------- 4-bit backbone

@@ -73,7 +73,8 @@ def grouped_moe_forward(x16: torch.Tensor, routing_weights: torch.Tensor, select
 def grouped_moe_forward_from_logits(x16: torch.Tensor, router_logits: torch.Tensor, top_k: int, renormalize: bool,
                                     payloads: dict, backbones: dict, num_experts: int,
                                     output_dtype=torch.bfloat16, shared_expert=None,
-                                    expert_path: str = "auto", x_model: torch.Tensor | None = None) -> torch.Tensor:
+                                    expert_path: str = "auto", x_model: torch.Tensor | None = None,
+                                    shared_stack: "SharedExpertStack | None" = None) -> torch.Tensor:
     """The layer from router logits: softmax / top-k / renormalisation / route in one kernel when the
     batch is decode-sized (tris_route_topk_grouped), else the token-parallel tris_route_topk (torch's
     route_topk for logits it does not take) + the two-kernel route.  On the
@@ -81,17 +82,31 @@ def grouped_moe_forward_from_logits(x16: torch.Tensor, router_logits: torch.Tens
     gate/up backbones of the tokens run in the router's launch (tris_route_topk_backbone), their split-K
     reduction in the predecode's, and the grouped GEMMs gather their rows through the route's token
     indices (the backbone values equal those of the gathered rows up to the split-K summation order: the
-    slice count follows the row count).  shared_expert and x_model: as grouped_moe_forward."""
+    slice count follows the row count).  shared_expert and x_model: as grouped_moe_forward.  shared_stack: the
+    shared expert's weights stacked under the routed backbones (SharedExpertStack); when the batch fits its
+    launches, the shared expert runs as their extra columns (_SharedFold) instead of four launches of its own."""
     T, H = int(x16.size(0)), int(x16.size(1))
     if T * top_k == 0:
         return torch.zeros((T, H), dtype=output_dtype, device=x16.device)
+    one_launch_router = (router_logits.dtype == torch.float32 and T * top_k <= ext.ROUTE_TOPK_MAX_ROWS
+                         and num_experts <= ext.ROUTE_TOPK_MAX_EXPERTS and top_k <= ext.ROUTE_TOPK_MAX_K)
+    sc = _in_scales(backbones)
+    router_backbone = (one_launch_router and expert_path != "fused" and _predecodable(payloads)
+                       and ext.mfma_payload_ok(payloads["gate"]) and ext.mfma_payload_ok(payloads["up"])
+                       and ext.route_topk_backbone_ok(x16, backbones["gate"], backbones["up"], sc["gate"], sc["up"]))
+    fold = None
+    if router_backbone and shared_stack is not None and shared_expert is not None:
+        fold = _SharedFold.make(shared_stack, shared_expert, x16, x_model, output_dtype, T * top_k, payloads,
+                                backbones)
+    if fold is not None:
+        route, pending = ext.route_topk_backbone_pair(router_logits, top_k, renormalize, GROUPED_SEGMENT_M_TILE, x16,
+                                                      shared_stack.gate, shared_stack.up, split=shared_stack.split_gu,
+                                                      out_a_hi=fold.g_all[T * top_k:], out_b_hi=fold.u_all[T * top_k:])
+        return _forward_with_route(x16, route["routing_weights_f16"], route, top_k, payloads, backbones, num_experts,
+                                   output_dtype, None, expert_path, backbone_pending=pending, shared_fold=fold)
     shared = _shared_expert_begin(x16, shared_expert, x_model, output_dtype)
-    if (router_logits.dtype == torch.float32 and T * top_k <= ext.ROUTE_TOPK_MAX_ROWS
-            and num_experts <= ext.ROUTE_TOPK_MAX_EXPERTS and top_k <= ext.ROUTE_TOPK_MAX_K):
-        sc = _in_scales(backbones)
-        if (expert_path != "fused" and _predecodable(payloads)
-                and ext.mfma_payload_ok(payloads["gate"]) and ext.mfma_payload_ok(payloads["up"])
-                and ext.route_topk_backbone_ok(x16, backbones["gate"], backbones["up"], sc["gate"], sc["up"])):
+    if one_launch_router:
+        if router_backbone:
             route, pending = ext.route_topk_backbone_pair(router_logits, top_k, renormalize, GROUPED_SEGMENT_M_TILE,
                                                           x16, backbones["gate"], backbones["up"],
                                                           in_scale_a=sc["gate"], in_scale_b=sc["up"])
@@ -143,7 +158,7 @@ def _grouped_projection(p: dict, hidden, expert_ids, seg, prob, tile_bound):
 
 
 def _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, output_dtype, shared_expert,
-                        expert_path, backbone_pending=None):
+                        expert_path, backbone_pending=None, shared_fold=None):
     if expert_path not in ("auto", "fused", "predecoded"):
         raise ValueError(f"unknown expert_path {expert_path!r}")
     T = int(x16.size(0))
@@ -162,8 +177,8 @@ def _forward_with_route(x16, w16, route, k, payloads, backbones, num_experts, ou
         raise RuntimeError("the predecoded expert path needs uniform 64-column groups and no output scale or bias")
     if predecodable and expert_path != "fused":
         return _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype,
-                                       shared_expert, backbone_pending=backbone_pending)
-    if backbone_pending is not None:
+                                       shared_expert, backbone_pending=backbone_pending, shared_fold=shared_fold)
+    if backbone_pending is not None or shared_fold is not None:
         raise RuntimeError("a backbone launched beside the router needs the predecoded expert path")
     if not any(_sparse(p) for p in (pg, pu, pd)) and all(ext.decode_payload_ok(p) for p in (pg, pu, pd)):
         return _decode_fused_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype,
@@ -220,6 +235,78 @@ class _SharedPending:
         self.out, self.stream, self.gate_weight, self.gate_input = out, stream, gate_weight, gate_input
 
 
+class SharedExpertStack:
+    """The always-on shared expert's fp16 weights stacked under the routed backbones, so its projections run as
+    extra columns of the routed path's launches: gate / up [rank + Is, H] (the routed gate or up backbone SV, then
+    the shared expert's weight) and down [rank_d + H, Is] (the routed down backbone, then the shared down weight).
+    Needs fp16 backbones without input scales and a shared intermediate size equal to the routed one (the shared
+    rows then stack under the routed rows of the down backbone's input)."""
+
+    __slots__ = ("gate", "up", "down", "split_gu", "split_d")
+
+    def __init__(self, backbones: dict, shared_expert):
+        wg, wu, wd = shared_expert[:3]
+        self.gate = torch.cat([backbones["gate"], wg]).contiguous()
+        self.up = torch.cat([backbones["up"], wu]).contiguous()
+        self.down = torch.cat([backbones["down"], wd]).contiguous()
+        self.split_gu = int(backbones["gate"].size(0))
+        self.split_d = int(backbones["down"].size(0))
+
+    @staticmethod
+    def ok(backbones: dict, shared_expert) -> bool:
+        if shared_expert is None or len(shared_expert) not in (3, 4):
+            return False
+        wg, wu, wd = shared_expert[:3]
+        svs = [backbones.get(k) for k in ("gate", "up", "down")]
+        if any(backbones.get(f"{k}_in_scale") is not None for k in ("gate", "up", "down")):
+            return False
+        ts = svs + [wg, wu, wd]
+        if not all(isinstance(t, torch.Tensor) and t.dtype == torch.float16 and t.dim() == 2 for t in ts):
+            return False
+        if len({t.device for t in ts}) != 1:
+            return False
+        sv_g, sv_u, sv_d = svs
+        # gate / up: one input width; down: the shared and routed intermediates agree
+        return (sv_g.shape == sv_u.shape and wg.shape == wu.shape and int(wg.size(1)) == int(sv_g.size(1))
+                and int(wd.size(1)) == int(wg.size(0)) == int(sv_d.size(1)))
+
+
+class _SharedFold:
+    """One step's shared expert as extra columns of the routed launches: the stacked gate and up rows (routed rows
+    first, then the T shared rows) that the dual GEMM and the gate/up backbone fill, and the gate of the combine."""
+
+    __slots__ = ("stack", "g_all", "u_all", "gate_weight", "gate_input")
+
+    @classmethod
+    def make(cls, stack, shared_expert, x16, x_model, output_dtype, R, payloads, backbones):
+        """The fold of this step, or None when the batch is outside the launches it rides in."""
+        T = int(x16.size(0))
+        n_mlp = int(payloads["gate"]["qweight1"].size(2))
+        inter = int(shared_expert[0].size(0))
+        if (T >= SHARED_EXPERT_SIDE_STREAM_MIN_TOKENS or R <= FUSED_SWIGLU_MAX_ROWS
+                or R + T > ext.SWIGLU_BACKBONE_MAX_ROWS or inter != n_mlp
+                or any(v is not None for v in _ns_payloads(payloads).values())):
+            return None
+        f = cls()
+        f.stack = stack
+        f.g_all = torch.empty((R + T, n_mlp), dtype=torch.float16, device=x16.device)
+        f.u_all = torch.empty((R + T, n_mlp), dtype=torch.float16, device=x16.device)
+        f.gate_weight, f.gate_input = _shared_gate_operands(shared_expert, x16, x_model, output_dtype)
+        return f
+
+
+def _shared_gate_operands(shared_expert, x16, x_model, output_dtype):
+    """The shared expert's gate weight and its input in the combine's dtype (None, None without a gate)."""
+    if len(shared_expert) != 4 or shared_expert[3] is None:
+        return None, None
+    gate_w = shared_expert[3]
+    cd = gate_w.dtype if gate_w.dtype in (torch.bfloat16, torch.float16) else torch.bfloat16
+    if output_dtype is not None:
+        cd = _combine_dtype(output_dtype)
+    src = x_model if x_model is not None else x16
+    return gate_w.reshape(-1).to(cd).contiguous(), src.to(cd).contiguous()
+
+
 def _combine_dtype(output_dtype) -> torch.dtype:
     """The dtype the combine writes: the output dtype when bf16 or fp16, else bf16 (then cast)."""
     return output_dtype if output_dtype in (torch.bfloat16, torch.float16) else torch.bfloat16
@@ -238,17 +325,9 @@ def _shared_expert_begin(x16, shared_expert, x_model=None, output_dtype=None):
     if len(shared_expert) not in (3, 4):
         raise RuntimeError("shared_expert must be (w_gate, w_up, w_down) or (w_gate, w_up, w_down, gate_weight)")
     wg, wu, wd = shared_expert[:3]
-    gate_w = shared_expert[3] if len(shared_expert) == 4 else None
     T, H = int(x16.size(0)), int(x16.size(1))
     dev = x16.device
-    gate_in = None
-    if gate_w is not None:
-        cd = gate_w.dtype if gate_w.dtype in (torch.bfloat16, torch.float16) else torch.bfloat16
-        if output_dtype is not None:
-            cd = _combine_dtype(output_dtype)
-        gate_w = gate_w.reshape(-1).to(cd).contiguous()
-        src = x_model if x_model is not None else x16
-        gate_in = src.to(cd).contiguous()
+    gate_w, gate_in = _shared_gate_operands(shared_expert, x16, x_model, output_dtype)
     main = torch.cuda.current_stream(dev)
     out = torch.empty((T, H), dtype=torch.float16, device=dev)
     side = _side_stream(dev, 2) if T >= SHARED_EXPERT_SIDE_STREAM_MIN_TOKENS else main
@@ -318,6 +397,11 @@ NS_DOWN_BESIDE_GEMM = True
 # 136.7 us before).
 NS_GATE_UP_BESIDE = True
 
+# The block runs its shared expert as extra columns of the routed launches when the batch fits them
+# (SharedExpertStack, _SharedFold; measured on MI355X at the A3B shape, T = 1: see the bench's c3 line); False
+# keeps its four launches of its own.
+FOLD_SHARED_EXPERT = True
+
 # The decode step decodes every expert's split bitmaps (slot e for expert e) when the batch routes at least this
 # many rows per expert, so the predecode does not wait for the router's selection (at the Mixtral shape, T = 16
 # routes 32 rows over 8 experts and leaves an expert idle about once in 12 steps).
@@ -330,7 +414,7 @@ SHARED_EXPERT_SIDE_STREAM_MIN_TOKENS = 32
 
 
 def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R, output_dtype, shared_expert,
-                            backbone_pending=None, predecoded=None, decoded_by_expert=False):
+                            backbone_pending=None, predecoded=None, decoded_by_expert=False, shared_fold=None):
     """Uniform-group payloads without output scale or bias: GR-decode every routed expert's split
     bitmaps once per projection (TriSMoE_cuda.cpp:836-853), then run the predecoded grouped GEMMs
     (TriSMoE_cuda.cpp:855-889, 922-974).  Active experts come first in the padded route, so
@@ -347,7 +431,9 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     their split-K reduction runs in the predecode's launch and the gate/up GEMMs gather their rows through
     the route's token indices.  predecoded: {gate, up, down} buffers already filled for this route (with the
     backbone's reduction) by the launch that built it (ext.route_predecode_multi); decoded_by_expert: they hold
-    every expert, slot e for expert e (its decode_all)."""
+    every expert, slot e for expert e (its decode_all).  shared_fold: the shared expert as extra columns of the
+    launches (_SharedFold): the gate/up backbones (launched beside the router) left its gate and up rows in
+    shared_fold.g_all / u_all below the routed rows, and the down backbone's launch computes its down projection."""
     slots = min(num_experts, R)
     eid = route["expert_ids"][:slots]
     seg = route["segment_offsets"][: slots + 1]
@@ -358,6 +444,10 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     dev = x16.device
     if predecoded is not None and (backbone_pending is None or any(v is not None for v in ns.values())):
         raise RuntimeError("predecoded buffers come with the router-launched backbones and no null-space payloads")
+    if shared_fold is not None and (backbone_pending is None or shared_expert is not None or R <= FUSED_SWIGLU_MAX_ROWS
+                                    or any(v is not None for v in ns.values())):
+        raise RuntimeError("a folded shared expert comes with the router-launched backbones, above "
+                           f"{FUSED_SWIGLU_MAX_ROWS} routed rows and without null-space payloads")
     if decoded_by_expert and (predecoded is None or R <= FUSED_SWIGLU_MAX_ROWS):
         raise RuntimeError("bitmaps decoded for every expert come from route_predecode_multi(decode_all=True), "
                            f"above {FUSED_SWIGLU_MAX_ROWS} routed rows")
@@ -432,12 +522,22 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     else:
         # more rows: gate and up in separate workgroups (more of them resident per CU), then act_fn(g) * u;
         # the same bits as the fused epilogue
-        g = torch.empty((R, n_mlp), dtype=torch.float16, device=dev)
-        u = torch.empty((R, n_mlp), dtype=torch.float16, device=dev)
+        if shared_fold is not None:  # the routed rows above the shared expert's in the stacked buffers
+            g, u = shared_fold.g_all[:R], shared_fold.u_all[:R]
+        else:
+            g = torch.empty((R, n_mlp), dtype=torch.float16, device=dev)
+            u = torch.empty((R, n_mlp), dtype=torch.float16, device=dev)
         ext.compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
             hid_g, hid_u, eid, seg, prob, tile_bound, decoded["gate"], *[pg[k] for k in names], decoded["up"],
             *[pu[k] for k in names], True, out_a=g, out_b=u, row_index=gather, decoded_by_expert=decoded_by_expert)
-        if (comp_g is None and comp_u is None and ns["down"] is None
+        if shared_fold is not None:
+            # one launch of the stacked down weights over the stacked rows: the routed rows' backbone in its first
+            # columns, the shared expert's down projection in the rest
+            hid_all, sh_all = ext.backbone_swiglu_linear_split(shared_fold.g_all, shared_fold.u_all,
+                                                               shared_fold.stack.down, shared_fold.stack.split_d)
+            hid_d = hid_all[:R]
+            shared_expert = _SharedPending(sh_all[R:], main, shared_fold.gate_weight, shared_fold.gate_input)
+        elif (comp_g is None and comp_u is None and ns["down"] is None
                 and ext.backbone_swiglu_ok(g, backbones["down"], sc["down"])):
             # act_fn(g) * u formed inside the down backbone (nothing else reads the product)
             hid_d = ext.backbone_swiglu_linear(g, u, backbones["down"], in_scale=sc["down"])
@@ -605,6 +705,10 @@ class TrisSparseMoeBlock(nn.Module):
             self.shared_expert_gate = nn.Linear(hidden_size, 1, bias=False, dtype=router_dtype,
                                                 device=shared_expert_gate.device)
             self.shared_expert_gate.weight.data = shared_expert_gate.reshape(1, hidden_size).to(router_dtype)
+        # the shared expert's weights stacked under the routed backbones (its projections then ride in the routed
+        # launches at decode batches)
+        self.shared_stack = (SharedExpertStack(backbones, self.shared_expert)
+                             if SharedExpertStack.ok(backbones, self.shared_expert) else None)
 
     def _shared(self, model_dtype: torch.dtype):
         if self.shared_expert is None or self.shared_expert_gate is None:
@@ -624,7 +728,8 @@ class TrisSparseMoeBlock(nn.Module):
         return grouped_moe_forward_from_logits(x16.contiguous(), logits.contiguous(), self.top_k,
                                                self.renormalize, self.payloads, self.backbones, self.num_experts,
                                                output_dtype, self._shared(output_dtype),
-                                               expert_path=self.expert_path, x_model=hidden_states.contiguous())
+                                               expert_path=self.expert_path, x_model=hidden_states.contiguous(),
+                                               shared_stack=self.shared_stack if FOLD_SHARED_EXPERT else None)
 
     def forward(self, hidden_states: torch.Tensor):
         """modeling_mixtral.py:539-608: hidden_states [B, S, H] (bf16 or fp16) -> (out [B, S, H] in the input

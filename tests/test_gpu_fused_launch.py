@@ -461,3 +461,44 @@ def test_block_decode_step_decoding_every_expert_matches_unfused_block(tris, cud
         assert int(active.numel()) < SPEC.num_experts, "the case needs an idle expert"
     assert torch.equal(logits.view(torch.int16), lg.view(torch.int16))
     assert torch.equal(out.reshape(tokens, SPEC.hidden).view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("tokens,in_f,rank,split", [(1, 2048, 768, 256), (3, 512, 320, 64), (24, 1024, 272, 144)])
+def test_backbone_column_split_matches_whole_projection(tris, cuda, tokens, in_f, rank, split):
+    """A gate/up backbone pair with a column split (two stacked projections, as the A3B block runs the routed
+    backbones and the shared expert's gate/up) writes the whole projection's columns [0, split) to out and
+    [split, rank) to out_hi, bit for bit: launched beside the router and reduced in the predecode launch."""
+    note(f"backbone column split T={tokens} in={in_f} rank={rank} split={split}")
+    ext = tris["ext"]
+    x, sv_a, sv_b, _, _ = backbone_inputs(tokens * 7 + split, tokens, in_f, rank, False, cuda)
+    logits = torch.from_numpy(np.random.default_rng(tokens).standard_normal((tokens, 16)).astype(np.float32)).to(cuda)
+    hi_a = torch.full((tokens, rank - split), float("nan"), dtype=torch.float16, device=cuda)
+    hi_b = torch.full_like(hi_a, float("nan"))
+    route, pend = ext.route_topk_backbone_pair(logits, 2, True, 4, x, sv_a, sv_b, split=split, out_a_hi=hi_a,
+                                               out_b_hi=hi_b)
+    ext.finish_backbone(pend)
+    _, whole = ext.route_topk_backbone_pair(logits, 2, True, 4, x, sv_a, sv_b)
+    ext.finish_backbone(whole)
+    for lo, hi, full in ((pend.out_a, hi_a, whole.out_a), (pend.out_b, hi_b, whole.out_b)):
+        assert torch.equal(lo.view(torch.int16), full[:, :split].contiguous().view(torch.int16))
+        assert torch.equal(hi.view(torch.int16), full[:, split:].contiguous().view(torch.int16))
+
+
+@pytest.mark.parametrize("rows,in_f,rank,split", [(9, 512, 2304, 256), (40, 1024, 640, 512), (128, 512, 384, 128)])
+def test_backbone_swiglu_column_split_matches_whole_projection(tris, cuda, rows, in_f, rank, split):
+    """tris_backbone_swiglu_linear_split (the routed down backbone and the shared expert's down projection as one
+    stacked projection) gives tris_backbone_swiglu_linear's columns [0, split) and [split, rank) bit for bit, and
+    rejects a split past the decode kernel's rows."""
+    note(f"swiglu backbone column split rows={rows} in={in_f} rank={rank} split={split}")
+    ext = tris["ext"]
+    rng = np.random.default_rng(rows + rank)
+    g = torch.from_numpy(rng.standard_normal((rows, in_f)).astype(np.float16)).to(cuda)
+    u = torch.from_numpy(rng.standard_normal((rows, in_f)).astype(np.float16)).to(cuda)
+    sv = torch.from_numpy((rng.standard_normal((rank, in_f)) * 0.05).astype(np.float16)).to(cuda)
+    lo, hi = ext.backbone_swiglu_linear_split(g, u, sv, split)
+    whole = ext.backbone_swiglu_linear(g, u, sv)
+    assert torch.equal(lo.view(torch.int16), whole[:, :split].contiguous().view(torch.int16))
+    assert torch.equal(hi.view(torch.int16), whole[:, split:].contiguous().view(torch.int16))
+    big = torch.zeros((ext.SWIGLU_BACKBONE_MAX_ROWS + 1, in_f), dtype=torch.float16, device=cuda)
+    with pytest.raises(RuntimeError, match="column split"):
+        ext.backbone_swiglu_linear_split(big, big, sv, split)

@@ -895,6 +895,17 @@ def _run_layer(tris, oracle_mod, cuda, spec, tokens, seed, expert_path="auto", s
     return np.concatenate(outs), np.concatenate(wants)
 
 
+def test_layer_a3b_c3_shared_expert_in_own_launches(tris, oracle_mod, cuda, monkeypatch):
+    """C3 at T = 1 with the shared expert in launches of its own (moe.FOLD_SHARED_EXPERT off): the path the block
+    takes when its weights do not stack; the default runs it as extra columns of the routed launches."""
+    from tris_moe_amd.configs import C3_A3B
+
+    note("layer C3 A3B T=1, shared expert unfolded")
+    monkeypatch.setattr(tris["moe"], "FOLD_SHARED_EXPERT", False)
+    out, want = _run_layer(tris, oracle_mod, cuda, C3_A3B, 1, 3001)
+    assert_close(out, want, "C3 layer T=1 (shared expert unfolded)")
+
+
 def test_layer_olmoe_c0(tris, oracle_mod, cuda):
     from tris_moe_amd.configs import C0_OLMOE
 

@@ -545,3 +545,31 @@ def test_oracle_layer_input_scales(oracle_mod, tris):
     on_up = oracle_mod.moe_layer(x16, w, sel, pl, bb, spec.num_experts, input_scales={"up": p2["gate"]})
     assert not np.array_equal(on_up, oracle_mod.moe_layer(x16, w, sel, pl, bb, spec.num_experts,
                                                            input_scales={"gate": p2["gate"]}))
+
+
+def test_shared_expert_stack_conditions_and_layout():
+    """SharedExpertStack (the A3B shared expert's weights under the routed backbones, run as extra columns of the
+    routed launches): built for fp16 backbones without input scales whose down input width is the shared
+    intermediate; the stacks hold the routed rows first, then the shared expert's, unchanged."""
+    import torch
+
+    from tris_moe_amd import moe
+
+    H, rank, rank_d, inter = 64, 32, 16, 48
+    g = torch.Generator().manual_seed(5)
+    mk = lambda *s: torch.randn(*s, generator=g).to(torch.float16)
+    backbones = {"gate": mk(rank, H), "up": mk(rank, H), "down": mk(rank_d, inter)}
+    shared = (mk(inter, H), mk(inter, H), mk(H, inter))
+    assert moe.SharedExpertStack.ok(backbones, shared)
+    assert moe.SharedExpertStack.ok(backbones, shared + (mk(1, H).to(torch.bfloat16),))
+    st = moe.SharedExpertStack(backbones, shared)
+    assert (st.split_gu, st.split_d) == (rank, rank_d)
+    assert torch.equal(st.gate[:rank], backbones["gate"]) and torch.equal(st.gate[rank:], shared[0])
+    assert torch.equal(st.up[:rank], backbones["up"]) and torch.equal(st.up[rank:], shared[1])
+    assert torch.equal(st.down[:rank_d], backbones["down"]) and torch.equal(st.down[rank_d:], shared[2])
+    assert tuple(st.down.shape) == (rank_d + H, inter)
+    # a shared intermediate other than the routed one (the down input widths differ), input scales, other dtypes
+    assert not moe.SharedExpertStack.ok({**backbones, "down": mk(rank_d, inter + 16)}, shared)
+    assert not moe.SharedExpertStack.ok({**backbones, "gate_in_scale": mk(H)}, shared)
+    assert not moe.SharedExpertStack.ok(backbones, (shared[0].float(), shared[1], shared[2]))
+    assert not moe.SharedExpertStack.ok(backbones, None)
