@@ -403,9 +403,11 @@ NS_GATE_UP_BESIDE = True
 FOLD_SHARED_EXPERT = True
 
 # The decode step decodes every expert's split bitmaps (slot e for expert e) when the batch routes at least this
-# many rows per expert, so the predecode does not wait for the router's selection (at the Mixtral shape, T = 16
-# routes 32 rows over 8 experts and leaves an expert idle about once in 12 steps).
-DECODE_ALL_MIN_ROWS_PER_EXPERT = 4
+# many rows per expert, so the predecode does not wait for the router's selection (measured on MI355X at the
+# Mixtral shape: T = 8, 16 rows over 8 experts, 92.4 -> 89.0 us; T = 4, 8 rows over ~5 experts, 78.8 against
+# 78.4 us, where decoding every expert is 1.6 times the blocks; T = 16 routes 32 rows and leaves an expert idle
+# about once in 12 steps).
+DECODE_ALL_MIN_ROWS_PER_EXPERT = 2
 
 # From this many tokens the shared expert runs on a side stream beside the routed experts; below it on the
 # caller's stream, since a graph's cross-queue join costs more than the overlap saves there (measured on MI355X at
