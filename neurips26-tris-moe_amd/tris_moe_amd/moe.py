@@ -101,7 +101,7 @@ def grouped_moe_forward_from_logits(x16: torch.Tensor, router_logits: torch.Tens
     if fold is not None:
         route, pending = ext.route_topk_backbone_pair(router_logits, top_k, renormalize, GROUPED_SEGMENT_M_TILE, x16,
                                                       shared_stack.gate, shared_stack.up, split=shared_stack.split_gu,
-                                                      out_a_hi=fold.g_all[T * top_k:], out_b_hi=fold.u_all[T * top_k:])
+                                                      out_a_hi=fold.g_s, out_b_hi=fold.u_s)
         return _forward_with_route(x16, route["routing_weights_f16"], route, top_k, payloads, backbones, num_experts,
                                    output_dtype, None, expert_path, backbone_pending=pending, shared_fold=fold)
     shared = _shared_expert_begin(x16, shared_expert, x_model, output_dtype)
@@ -272,10 +272,14 @@ class SharedExpertStack:
 
 
 class _SharedFold:
-    """One step's shared expert as extra columns of the routed launches: the stacked gate and up rows (routed rows
-    first, then the T shared rows) that the dual GEMM and the gate/up backbone fill, and the gate of the combine."""
+    """One step's shared expert as extra columns of the routed launches.  Its gate and up always ride in the gate/up
+    backbone launched beside the router (the stack's split projection).  With split_down, its rows stack under the
+    routed rows in g_all / u_all (the dual GEMM fills the first R rows, the backbone the last T) and one launch of
+    the stacked down weights projects both; otherwise (routed and shared rows together past the SwiGLU backbone's
+    128 rows) its gate and up land in g_s / u_s and its down projection runs apart, after the routed gate/up GEMM.
+    gate_weight / gate_input: the combine's gate operands (None without a gate)."""
 
-    __slots__ = ("stack", "g_all", "u_all", "gate_weight", "gate_input")
+    __slots__ = ("stack", "split_down", "g_all", "u_all", "g_s", "u_s", "wd", "gate_weight", "gate_input")
 
     @classmethod
     def make(cls, stack, shared_expert, x16, x_model, output_dtype, R, payloads, backbones):
@@ -283,16 +287,33 @@ class _SharedFold:
         T = int(x16.size(0))
         n_mlp = int(payloads["gate"]["qweight1"].size(2))
         inter = int(shared_expert[0].size(0))
-        if (T >= SHARED_EXPERT_SIDE_STREAM_MIN_TOKENS or R <= FUSED_SWIGLU_MAX_ROWS
-                or R + T > ext.SWIGLU_BACKBONE_MAX_ROWS or inter != n_mlp
-                or any(v is not None for v in _ns_payloads(payloads).values())):
+        if R <= FUSED_SWIGLU_MAX_ROWS or any(v is not None for v in _ns_payloads(payloads).values()):
             return None
         f = cls()
         f.stack = stack
-        f.g_all = torch.empty((R + T, n_mlp), dtype=torch.float16, device=x16.device)
-        f.u_all = torch.empty((R + T, n_mlp), dtype=torch.float16, device=x16.device)
+        f.wd = shared_expert[2]
+        f.split_down = R + T <= ext.SWIGLU_BACKBONE_MAX_ROWS and inter == n_mlp
+        dev = x16.device
+        if f.split_down:
+            f.g_all = torch.empty((R + T, n_mlp), dtype=torch.float16, device=dev)
+            f.u_all = torch.empty((R + T, n_mlp), dtype=torch.float16, device=dev)
+            f.g_s, f.u_s = f.g_all[R:], f.u_all[R:]
+        else:
+            f.g_all = f.u_all = None
+            f.g_s = torch.empty((T, inter), dtype=torch.float16, device=dev)
+            f.u_s = torch.empty((T, inter), dtype=torch.float16, device=dev)
         f.gate_weight, f.gate_input = _shared_gate_operands(shared_expert, x16, x_model, output_dtype)
         return f
+
+    def down_apart(self, main) -> "_SharedPending":
+        """The shared expert's down projection of act_fn(g) * u on its own rows (the fold without split_down), on
+        the caller's stream, as _shared_expert_begin runs it."""
+        out = torch.empty((int(self.g_s.size(0)), int(self.wd.size(0))), dtype=torch.float16, device=self.g_s.device)
+        if ext.backbone_swiglu_ok(self.g_s, self.wd):
+            ext.backbone_swiglu_linear(self.g_s, self.u_s, self.wd, out=out)
+        else:
+            ext.backbone_linear(ext.swiglu_mul(self.g_s, self.u_s), self.wd, out=out)
+        return _SharedPending(out, main, self.gate_weight, self.gate_input)
 
 
 def _shared_gate_operands(shared_expert, x16, x_model, output_dtype):
@@ -409,7 +430,8 @@ FOLD_SHARED_EXPERT = True
 # about once in 12 steps).
 DECODE_ALL_MIN_ROWS_PER_EXPERT = 2
 
-# From this many tokens the shared expert runs on a side stream beside the routed experts; below it on the
+# From this many tokens the shared expert, when it runs in launches of its own, runs on a side stream beside the
+# routed experts; below it on the
 # caller's stream, since a graph's cross-queue join costs more than the overlap saves there (measured on MI355X at
 # the A3B shape: T = 1 64.3 -> 59.0 us inline; T = 32 138 vs 139 us; T = 1024 339 vs 356 us).
 SHARED_EXPERT_SIDE_STREAM_MIN_TOKENS = 32
@@ -435,7 +457,8 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     backbone's reduction) by the launch that built it (ext.route_predecode_multi); decoded_by_expert: they hold
     every expert, slot e for expert e (its decode_all).  shared_fold: the shared expert as extra columns of the
     launches (_SharedFold): the gate/up backbones (launched beside the router) left its gate and up rows in
-    shared_fold.g_all / u_all below the routed rows, and the down backbone's launch computes its down projection."""
+    shared_fold.g_s / u_s, below the routed rows of g_all / u_all when the down backbone's launch computes its down
+    projection too (split_down); else its down projection runs apart after the routed gate/up GEMM."""
     slots = min(num_experts, R)
     eid = route["expert_ids"][:slots]
     seg = route["segment_offsets"][: slots + 1]
@@ -524,7 +547,7 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
     else:
         # more rows: gate and up in separate workgroups (more of them resident per CU), then act_fn(g) * u;
         # the same bits as the fused epilogue
-        if shared_fold is not None:  # the routed rows above the shared expert's in the stacked buffers
+        if shared_fold is not None and shared_fold.split_down:  # the routed rows above the shared expert's
             g, u = shared_fold.g_all[:R], shared_fold.u_all[:R]
         else:
             g = torch.empty((R, n_mlp), dtype=torch.float16, device=dev)
@@ -532,7 +555,9 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
         ext.compact3_tris_precomputed_grouped_dual_forward_block_gr_predecoded(
             hid_g, hid_u, eid, seg, prob, tile_bound, decoded["gate"], *[pg[k] for k in names], decoded["up"],
             *[pu[k] for k in names], True, out_a=g, out_b=u, row_index=gather, decoded_by_expert=decoded_by_expert)
-        if shared_fold is not None:
+        if shared_fold is not None and not shared_fold.split_down:
+            shared_expert = shared_fold.down_apart(main)
+        if shared_fold is not None and shared_fold.split_down:
             # one launch of the stacked down weights over the stacked rows: the routed rows' backbone in its first
             # columns, the shared expert's down projection in the rest
             hid_all, sh_all = ext.backbone_swiglu_linear_split(shared_fold.g_all, shared_fold.u_all,

@@ -906,6 +906,36 @@ def test_layer_a3b_c3_shared_expert_in_own_launches(tris, oracle_mod, cuda, monk
     assert_close(out, want, "C3 layer T=1 (shared expert unfolded)")
 
 
+@pytest.mark.parametrize("tokens", [1, 3, 20])
+def test_layer_ungated_shared_expert_in_routed_launches(tris, oracle_mod, cuda, tokens):
+    """A smaller A3B-shaped layer (1024 hidden, 32 experts, top-8) with an ungated shared expert (the three weights,
+    no gate: final + shared(h)), run through the block, so its shared expert rides in the routed launches
+    (SharedExpertStack: at T = 20, 160 routed rows, its down projection runs apart), against the oracle."""
+    from tris_moe_amd.configs import C3_A3B
+
+    spec = C3_A3B.with_(name="a3b_small", hidden=1024, num_experts=32)
+    note(f"layer with an ungated shared expert in the routed launches T={tokens}")
+    syn, ql, moe = tris["synthetic"], tris["qlinear"], tris["moe"]
+    layer = syn.make_layer(spec, 3300 + tokens, tris["ext"].gr_encode)
+    payloads = {p: ql.payload_to_device(layer[p], cuda) for p in ("gate", "up", "down")}
+    backbones = {p: torch.from_numpy(layer["backbones"][p]).to(cuda) for p in ("gate", "up", "down")}
+    shared = tuple(torch.from_numpy(w).to(cuda) for w in layer["shared_expert"])
+    block = moe.TrisSparseMoeBlock(spec.hidden, spec.num_experts, spec.top_k, payloads, backbones,
+                                   renormalize=spec.renormalize, shared_expert=shared)
+    assert block.shared_stack is not None
+    outs, wants = [], []
+    for i in range(4):
+        inp = syn.make_inputs(spec, tokens, 3400 + 10 * tokens + i, layer["outlier_idx"])
+        x = torch.from_numpy(inp["x"]).to(cuda).to(torch.bfloat16)
+        logits = torch.from_numpy(inp["router_logits"]).to(cuda)
+        outs.append(block.forward_routed(x, logits).float().cpu().numpy())
+        w, sel = oracle_mod.route_topk(inp["router_logits"], spec.top_k, spec.renormalize)
+        want = oracle_mod.moe_layer(inp["x"].astype(np.float16), w, sel, {p: layer[p] for p in ("gate", "up", "down")},
+                                    layer["backbones"], spec.num_experts, layer["shared_expert"], out_dtype="bf16")
+        wants.append(oracle_mod.bf16_round(want))
+    assert_close(np.concatenate(outs), np.concatenate(wants), f"ungated shared expert layer T={tokens}")
+
+
 def test_layer_olmoe_c0(tris, oracle_mod, cuda):
     from tris_moe_amd.configs import C0_OLMOE
 
