@@ -53,7 +53,9 @@ struct GrWork {
 
 // The decode route built in the same launch (tris_route_predecode_multi_reduce): workgroup 0 runs
 // route_wave_body, and every decode workgroup derives its slots' experts from the
-// same logits (route_active_experts) instead of reading expert_ids, which that workgroup is still writing.
+// same logits (route_active_experts) instead of reading expert_ids, which that workgroup is still writing; with
+// decode_all (tris_route_predecode_all_reduce) the decoders take every expert, slot e for expert e, and read
+// nothing the route writes.
 struct GrRoute {
   RouteArgs ra;
   int k_variant;  // the route_wave_body instance: 2, 8 or kRouteMaxTopK (by top_k, as tris_route_topk_grouped)
@@ -61,8 +63,9 @@ struct GrRoute {
   int decode_all;  // 1: the decoders take every expert, slot = expert id, and do not read the logits
 };
 
-// A backbone projection's slice reduction run by the workgroups past the decoders (independent work in the
-// same launch): blocks_per_proj workgroups of kSpanThreads output elements for each of nproj projections.
+// A backbone projection's slice reduction run by workgroups of the same launch, dispatched after the route's and
+// before the decoders (independent work): blocks_per_proj workgroups of kSpanThreads output elements for each of
+// nproj projections.
 struct GrReduce {
   BackboneArgs bb;
   int blocks_per_proj;

@@ -276,7 +276,8 @@ class _SharedFold:
     backbone launched beside the router (the stack's split projection).  With split_down, its rows stack under the
     routed rows in g_all / u_all (the dual GEMM fills the first R rows, the backbone the last T) and one launch of
     the stacked down weights projects both; otherwise (routed and shared rows together past the SwiGLU backbone's
-    128 rows) its gate and up land in g_s / u_s and its down projection runs apart, after the routed gate/up GEMM.
+    128 rows, or a shared intermediate other than the routed one) its gate and up land in g_s / u_s and its down
+    projection runs apart, after the routed gate/up GEMM.
     gate_weight / gate_input: the combine's gate operands (None without a gate)."""
 
     __slots__ = ("stack", "split_down", "g_all", "u_all", "g_s", "u_s", "wd", "gate_weight", "gate_input")
@@ -419,8 +420,8 @@ NS_DOWN_BESIDE_GEMM = True
 NS_GATE_UP_BESIDE = True
 
 # The block runs its shared expert as extra columns of the routed launches when the batch fits them
-# (SharedExpertStack, _SharedFold; measured on MI355X at the A3B shape, T = 1: see the bench's c3 line); False
-# keeps its four launches of its own.
+# (SharedExpertStack, _SharedFold; measured on MI355X at the A3B shape: T = 1 60.6 -> 48.9 us, T = 32 140.2 ->
+# 133.4 us); False keeps its four launches of its own.
 FOLD_SHARED_EXPERT = True
 
 # The decode step decodes every expert's split bitmaps (slot e for expert e) when the batch routes at least this
