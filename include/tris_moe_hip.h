@@ -376,6 +376,21 @@ int tris_grouped_forward_block_gr_predecoded_experts(
     const tris_compact3_payload* payload_b, uint16_t* output_a, uint16_t* output_b, void* stream);
 
 /*
+ * The predecoded grouped GEMM of one projection (TriSMoE_cuda.cpp:855-889) whose activation rows are taken from
+ * the fp32 split-K partial sums of the backbone that produced them (no reference counterpart: the reference
+ * projects the shared hidden with F.linear, qlinear_cuda.py:4454-4502, and reads it back).  partials
+ * [slices][batch][rank] as tris_backbone_linear_deferred leaves them; row r of the GEMM is fp16 of the slices'
+ * sum added in slice order, the bits tris_backbone_linear writes, so the output equals the predecoded GEMM over
+ * that projection's output bit for bit.  decoded: one slot per segment, or with decoded_by_expert != 0 one per
+ * expert (as tris_grouped_forward_block_gr_predecoded_experts).  Requires the MFMA kernel's payload conditions
+ * and rank <= 512 (else TRIS_ERR_INVALID); no output scale or bias is applied.
+ */
+int tris_grouped_forward_block_gr_predecoded_partials(
+    const float* partials, int32_t slices, int32_t batch, const int32_t* expert_ids, const int32_t* segment_offsets,
+    int32_t num_segments, int64_t total_problem_tiles, const int32_t* decoded, const tris_compact3_payload* payload,
+    uint16_t* output, int32_t decoded_by_expert, void* stream);
+
+/*
  * Dequantise the listed experts to dense fp16 weights [num, N, rank]
  * (verification kernel; the product GEMMs never write weights).  Replaces the
  * reference's CPU dequant QuantLinear._dequantize_compact3_matrix
@@ -411,6 +426,17 @@ int tris_gr_decode_dense(const int32_t* q_gmap_gr_words, const int32_t* q_gmap_g
 int tris_backbone_linear(const uint16_t* x, int32_t tokens, int32_t in_features, const int64_t* row_index,
                          const uint16_t* sv, int32_t rank, const uint16_t* in_scale, uint16_t* out,
                          void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * tris_backbone_linear with its split-K reduction left to the consumer (no reference counterpart; an extension of
+ * compute_shared_hidden, qlinear_cuda.py:4454-4502).  *slices is set to the plan's slice count: with one slice out
+ * holds the projection, as tris_backbone_linear writes it; with more, out is not written and workspace holds the
+ * fp32 partial sums [slices][tokens][rank] that tris_grouped_forward_block_gr_predecoded_partials adds.  Shapes
+ * that take the tiled GEMM (prefill-size batches) are rejected with TRIS_ERR_INVALID.
+ */
+int tris_backbone_linear_deferred(const uint16_t* x, int32_t tokens, int32_t in_features, const int64_t* row_index,
+                                  const uint16_t* sv, int32_t rank, const uint16_t* in_scale, uint16_t* out,
+                                  void* workspace, int64_t workspace_bytes, int32_t* slices, void* stream);
 
 /* Two backbone projections of the same gathered rows in one launch (no
  * reference counterpart: batches the gate and up compute_shared_hidden calls

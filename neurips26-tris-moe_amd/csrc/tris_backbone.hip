@@ -634,8 +634,9 @@ static int launch_backbone_gemm(const BackboneArgs& base, int nproj, hipStream_t
 int launch_backbone(const uint16_t* x, int tokens, int in_features, const int64_t* row_index, const uint16_t* sv_a,
                     const uint16_t* sv_b, int rank, const uint16_t* in_scale_a, const uint16_t* in_scale_b,
                     uint16_t* out_a, uint16_t* out_b, void* workspace, int64_t workspace_bytes, void* stream,
-                    const char* who, bool use_gemm = true) {
+                    const char* who, bool use_gemm = true, int32_t* deferred_slices = nullptr) {
   TRIS_REQUIRE(tokens >= 0 && in_features >= 0 && rank >= 0, "%s: negative shape", who);
+  if (deferred_slices != nullptr) *deferred_slices = 1;
   if (tokens == 0 || rank == 0) return TRIS_OK;
   TRIS_REQUIRE(out_a != nullptr && (sv_b == nullptr || out_b != nullptr), "%s: null output", who);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -653,7 +654,10 @@ int launch_backbone(const uint16_t* x, int tokens, int in_features, const int64_
   int rc = backbone_prepare(x, tokens, in_features, row_index, sv_a, sv_b, rank, in_scale_a, in_scale_b, out_a, out_b,
                             workspace, workspace_bytes, &args, &pl, who, use_gemm);
   if (rc) return rc;
-  if (use_gemm && backbone_gemm_fits(tokens, in_features, rank)) return launch_backbone_gemm(args, nproj, s, who);
+  const bool gemm = use_gemm && backbone_gemm_fits(tokens, in_features, rank);
+  TRIS_REQUIRE(deferred_slices == nullptr || !gemm,
+               "%s: %d rows take the tiled GEMM, whose reduction cannot be deferred", who, tokens);
+  if (gemm) return launch_backbone_gemm(args, nproj, s, who);
   const dim3 grid(pl.row_tiles, pl.token_groups * pl.slices, nproj);
   switch (pl.tt) {
     case 1: hipLaunchKernelGGL((backbone_kernel<1, 8>), grid, dim3(kBbThreads), 0, s, args); break;
@@ -663,6 +667,10 @@ int launch_backbone(const uint16_t* x, int tokens, int in_features, const int64_
   }
   rc = check_launch(who);
   if (rc || pl.slices == 1) return rc;
+  if (deferred_slices != nullptr) {  // the consumer adds the slices
+    *deferred_slices = pl.slices;
+    return TRIS_OK;
+  }
   return launch_backbone_reduce(args, nproj, s, who);
 }
 
@@ -1092,6 +1100,15 @@ extern "C" int tris_backbone_linear(const uint16_t* x, int32_t tokens, int32_t i
                                     void* workspace, int64_t workspace_bytes, void* stream) {
   return launch_backbone(x, tokens, in_features, row_index, sv, nullptr, rank, in_scale, nullptr, out, nullptr,
                          workspace, workspace_bytes, stream, "tris_backbone_linear");
+}
+
+extern "C" int tris_backbone_linear_deferred(const uint16_t* x, int32_t tokens, int32_t in_features,
+                                             const int64_t* row_index, const uint16_t* sv, int32_t rank,
+                                             const uint16_t* in_scale, uint16_t* out, void* workspace,
+                                             int64_t workspace_bytes, int32_t* slices, void* stream) {
+  TRIS_REQUIRE(slices != nullptr, "tris_backbone_linear_deferred: null slice count");
+  return launch_backbone(x, tokens, in_features, row_index, sv, nullptr, rank, in_scale, nullptr, out, nullptr,
+                         workspace, workspace_bytes, stream, "tris_backbone_linear_deferred", true, slices);
 }
 
 // ---- tris_backbone_linear_noalloc: the split-K partial sums in a file-scope device array instead of a

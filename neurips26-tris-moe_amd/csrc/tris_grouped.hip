@@ -565,7 +565,8 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
                         const int32_t* segment_offsets, int num_segments, const int32_t* decoded_a,
                         const int32_t* decoded_b, const tris_compact3_payload* pa, const tris_compact3_payload* pb,
                         uint16_t* out_a, uint16_t* out_b, bool swiglu, void* stream, const char* who,
-                        const int64_t* row_index = nullptr, int hidden_rows = 0, bool decoded_by_expert = false);
+                        const int64_t* row_index = nullptr, int hidden_rows = 0, bool decoded_by_expert = false,
+                        const float* partials = nullptr, int slices = 0);
 bool grouped_mfma_supported(const tris_compact3_payload* p, const uint16_t* hidden);
 
 }  // namespace tris
@@ -770,6 +771,24 @@ extern "C" int tris_grouped_forward_block_gr_predecoded_experts(
   return launch_grouped_mfma(hidden_a, payload_b ? hidden_b : nullptr, batch, expert_ids, segment_offsets, num_segments,
                              decoded_a, payload_b ? decoded_b : nullptr, &pa, payload_b ? &pb : nullptr, output_a,
                              payload_b ? output_b : nullptr, false, stream, who, row_index, hidden_rows, true);
+}
+
+extern "C" int tris_grouped_forward_block_gr_predecoded_partials(
+    const float* partials, int32_t slices, int32_t batch, const int32_t* expert_ids, const int32_t* segment_offsets,
+    int32_t num_segments, int64_t total_problem_tiles, const int32_t* decoded, const tris_compact3_payload* payload,
+    uint16_t* output, int32_t decoded_by_expert, void* stream) {
+  const char* who = "tris_grouped_forward_block_gr_predecoded_partials";
+  TRIS_REQUIRE(payload != nullptr && partials != nullptr, "%s: null payload or partial sums", who);
+  TRIS_REQUIRE(batch >= 0 && slices >= 1, "%s: negative batch or no slices", who);
+  tris_compact3_payload p = *payload;  // the predecoded kernels apply no scale or bias
+  p.has_output_scale = 0;
+  p.has_bias = 0;
+  TRIS_REQUIRE(grouped_mfma_supported(&p, reinterpret_cast<const uint16_t*>(partials)),
+               "%s: needs uniform 64-column groups, rank %% 64 == 0 and 16-byte aligned partial sums", who);
+  if (total_problem_tiles <= 0 || batch == 0) return TRIS_OK;
+  return launch_grouped_mfma(nullptr, nullptr, batch, expert_ids, segment_offsets, num_segments, decoded, nullptr, &p,
+                             nullptr, output, nullptr, false, stream, who, nullptr, batch, decoded_by_expert != 0,
+                             partials, slices);
 }
 
 extern "C" int tris_compact3_dequant(const tris_compact3_payload* payload, const int32_t* expert_ids, int32_t num,

@@ -57,7 +57,11 @@ struct MfmaProj {
   const int32_t* decoded;     // [num_segments, nblk, 128]
   tris_compact3_payload p;
   const int64_t* row_index;   // null, or [batch]: segment row r reads hidden row row_index[r]
-  int hidden_rows;
+  int hidden_rows;            // row_index's range, or with partials the rows of each slice
+  // null, or [slices][hidden_rows][rank] fp32 split-K partial sums of the backbone that produced the activations:
+  // hidden row r is then fp16(the slices' sum, added in slice order) and `hidden` is not read (rank <= kMfChunk)
+  const float* partials;
+  int slices;
 };
 
 struct MfmaArgs {
@@ -288,9 +292,15 @@ __device__ __forceinline__ uint32_t mf_hidden_voff(const MfmaProj& pa, int row0,
   return static_cast<uint32_t>(src * rank + c) * 2u;
 }
 
-// The activation buffer resource of rows [row0, row0 + rc) and its size (the offset that reads zeros).
+// The activation buffer resource of rows [row0, row0 + rc) and its size (the offset that reads zeros).  With
+// partial sums the activations are staged from them (mf_partials_stage): an empty resource, whose loads read zeros
+// without a memory access.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t mf_hidden_rsrc(const MfmaProj& pa, int row0, int rc, int rank,
                                                                  uint32_t* bytes) {
+  if (pa.partials != nullptr) {
+    *bytes = 0u;
+    return make_rsrc(pa.partials, 0u);
+  }
   if (pa.row_index != nullptr) {
     *bytes = static_cast<uint32_t>(pa.hidden_rows) * rank * 2u;
     return make_rsrc(pa.hidden, *bytes);
@@ -399,7 +409,7 @@ __device__ __forceinline__ void mf_chunk_write(const MfmaProj& pa, int rc, int k
 #pragma unroll
   for (int h = 0; h < kMfRuns; ++h) {
     const int r = 4 * h + wave;
-    if (r < rc) {  // wave-uniform
+    if (r < rc && pa.partials == nullptr) {  // wave-uniform; partial sums are staged by mf_partials_stage
       const int c = lane * 8;  // run start within the chunk (a multiple of 8)
       // columns c + b and c + b + 4 (b < 4) are neighbours in the staged order
       const uint32_t w[4] = {R.xv[h].x, R.xv[h].y, R.xv[h].z, R.xv[h].w};
@@ -457,6 +467,44 @@ __device__ __forceinline__ void mf_chunk_write(const MfmaProj& pa, int rc, int k
     ch.meta[utid - 64] = tv ? R.mv : -1;
   } else if (utid >= 72 && utid < 74) {
     ch.meta[8 + (utid - 72)] = R.mv;
+  }
+}
+
+// Activation rows [row0, row0 + rc) of the one chunk (rank <= kMfChunk) from the split-K partial sums of the backbone
+// that produced them: fp16 of the slices' sum added in slice order, the bits the backbone's own reduction
+// (backbone_reduce_at) writes.  Thread utid of the unit takes columns 2 utid and 2 utid + 1 of each row, with
+// kMfPartialBatch slices' loads in flight.
+constexpr int kMfPartialBatch = 16;
+__device__ __forceinline__ void mf_partials_stage(const MfmaProj& pa, int row0, int rc, int utid, const MfChunk& ch) {
+  const int rank = pa.p.rank;
+  const int c = 2 * utid;
+  const int slices = pa.slices;
+  const int prow = pa.hidden_rows;
+  const uint32_t bytes = static_cast<uint32_t>(slices) * static_cast<uint32_t>(prow) * rank * 4u;
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(pa.partials, bytes);
+  const int pos0 = (c & ~31) + mf_perm32(c & 31);
+  const int pos1 = ((c + 1) & ~31) + mf_perm32((c + 1) & 31);
+  for (int i = 0; i < rc; ++i) {  // uniform
+    float a0 = 0.0f, a1 = 0.0f;
+    for (int s0 = 0; s0 < slices; s0 += kMfPartialBatch) {
+      uint64_t v[kMfPartialBatch];
+#pragma unroll
+      for (int j = 0; j < kMfPartialBatch; ++j) {
+        const bool ok = s0 + j < slices && c < rank;
+        v[j] = bload64(r, ok ? static_cast<uint32_t>(((s0 + j) * prow + row0 + i) * rank + c) * 4u : bytes, 0u);
+      }
+#pragma unroll
+      for (int j = 0; j < kMfPartialBatch; ++j) {
+        if (s0 + j < slices) {
+          a0 += __uint_as_float(static_cast<uint32_t>(v[j]));
+          a1 += __uint_as_float(static_cast<uint32_t>(v[j] >> 32));
+        }
+      }
+    }
+    if (c < rank) {
+      ch.xs[i * kMfXStride + pos0] = f2h_bits(a0);
+      ch.xs[i * kMfXStride + pos1] = f2h_bits(a1);
+    }
   }
 }
 
@@ -977,6 +1025,7 @@ void grouped_mfma_kernel(MfmaArgs a) {
     mf_wave_tile_issue<kCompact>(pa, ds, e, ob_begin, wo, lane, wave, tb0);
     mf_chunk_issue(pa, e, row0, rc, 0, utid, regs);
     mf_chunk_write(pa, rc, 0, utid, ch, regs, false, kSal);
+    if (pa.partials != nullptr) mf_partials_stage(pa, row0, rc, utid, ch);  // one chunk (host-checked)
     __builtin_amdgcn_s_waitcnt(0);  // LDS copies landed (all counters zero)
     __syncthreads();
   }
@@ -1606,7 +1655,8 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
                         const int32_t* segment_offsets, int num_segments, const int32_t* decoded_a,
                         const int32_t* decoded_b, const tris_compact3_payload* pa, const tris_compact3_payload* pb,
                         uint16_t* out_a, uint16_t* out_b, bool swiglu, void* stream, const char* who,
-                        const int64_t* row_index, int hidden_rows, bool decoded_by_expert) {
+                        const int64_t* row_index, int hidden_rows, bool decoded_by_expert, const float* partials,
+                        int slices) {
   TRIS_REQUIRE(batch >= 0 && num_segments >= 0, "%s: negative batch or segment count", who);
   TRIS_REQUIRE(row_index == nullptr || hidden_rows >= 0, "%s: negative hidden row count", who);
   int rc = check_payload(pa, false, who);
@@ -1617,7 +1667,15 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
   }
   TRIS_REQUIRE(!swiglu || pb != nullptr, "%s: the fused SwiGLU needs two projections", who);
   if (batch == 0 || num_segments == 0) return TRIS_OK;
-  TRIS_REQUIRE(hidden_a && out_a && expert_ids && segment_offsets && decoded_a, "%s: null pointer", who);
+  TRIS_REQUIRE((hidden_a || partials) && out_a && expert_ids && segment_offsets && decoded_a, "%s: null pointer", who);
+  if (partials != nullptr) {
+    // one projection, one chunk, every slice's rows addressed by 32-bit buffer offsets
+    TRIS_REQUIRE(pb == nullptr && !swiglu && row_index == nullptr, "%s: partial sums feed one projection", who);
+    TRIS_REQUIRE(pa->rank <= kMfChunk, "%s: partial sums need rank <= %d (one chunk)", who, kMfChunk);
+    TRIS_REQUIRE(slices >= 1 && hidden_rows >= batch, "%s: bad partial-sum shape", who);
+    TRIS_REQUIRE(static_cast<int64_t>(slices) * hidden_rows * pa->rank * 4 < (int64_t{1} << 31),
+                 "%s: partial sums exceed the 2 GiB limit", who);
+  }
   TRIS_REQUIRE(!pb || (hidden_b && decoded_b && (swiglu || out_b)), "%s: null pointer (second projection)", who);
   int max_n = 0;
   for (int i = 0; i < (pb ? 2 : 1); ++i) {
@@ -1635,7 +1693,7 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
                  hidden_rows);
   }
   MfmaArgs args{};
-  args.proj[0] = MfmaProj{hidden_a, out_a, decoded_a, *pa, row_index, hidden_rows};
+  args.proj[0] = MfmaProj{hidden_a, out_a, decoded_a, *pa, row_index, hidden_rows, partials, slices};
   if (pb) args.proj[1] = MfmaProj{hidden_b, out_b, decoded_b, *pb, row_index, hidden_rows};
   args.expert_ids = expert_ids;
   args.segment_offsets = segment_offsets;
@@ -1646,7 +1704,8 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
   hipStream_t s = static_cast<hipStream_t>(stream);
   // long segments: keep each output tile's weights in registers and stream the segment's rows through them
   // (its buffer resources address a segment's rows in 32-bit byte offsets: the whole batch must stay below 2 GiB)
-  if (num_segments <= kWave && static_cast<int64_t>(batch) >= static_cast<int64_t>(kWsMinRows) * num_segments &&
+  if (partials == nullptr && num_segments <= kWave &&
+      static_cast<int64_t>(batch) >= static_cast<int64_t>(kWsMinRows) * num_segments &&
       ws_fits(pa) && (!pb || ws_fits(pb)) && static_cast<int64_t>(batch) * max_n * 2 < (int64_t{1} << 31) &&
       static_cast<int64_t>(batch) * kMfChunk * 2 < (int64_t{1} << 31)) {
     return launch_grouped_mfma_ws(args, units, nproj, max_n, batch, s, who);

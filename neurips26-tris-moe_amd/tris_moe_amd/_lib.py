@@ -166,6 +166,7 @@ SIGNATURES = {
     "tris_compact3_dequant": (ctypes.c_int, [_PAY, _P, _I32, _P, _P]),
     "tris_gr_decode_dense": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _P, _I32, _I32, _I32, _P, _P]),
     "tris_backbone_linear": (ctypes.c_int, [_P, _I32, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P]),
+    "tris_backbone_linear_deferred": (ctypes.c_int, [_P, _I32, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P, _P]),
     "tris_backbone_linear_pair": (ctypes.c_int, [_P, _I32, _I32, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _I64, _P]),
     "tris_backbone_pair_workspace_bytes": (_I64, [_I32, _I32, _I32]),
     "tris_backbone_swiglu_linear": (ctypes.c_int, [_P, _P, _I32, _I32, _P, _I32, _P, _P, _P, _I64, _P]),
@@ -191,6 +192,8 @@ SIGNATURES = {
                        ctypes.POINTER(TrisPredecodeJob), _I32, ctypes.POINTER(TrisBackbonePairJob), _P]),
     "tris_grouped_forward_block_gr_predecoded_experts": (
         ctypes.c_int, [_P, _P, _P, _I32, _I32, _P, _P, _I32, _I64, _P, _P, _PAY, _PAY, _P, _P, _P]),
+    "tris_grouped_forward_block_gr_predecoded_partials": (
+        ctypes.c_int, [_P, _I32, _I32, _P, _P, _I32, _I64, _P, _PAY, _P, _I32, _P]),
     "tris_moe_combine_gated": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _P, _P]),
     "tris_swiglu_mul": (ctypes.c_int, [_P, _P, _I64, _P, _P]),
     "tris_swiglu_mul_compensated": (ctypes.c_int, [_P, _P, _P, _P, _I64, _P, _P]),

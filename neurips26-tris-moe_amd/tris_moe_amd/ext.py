@@ -1027,6 +1027,86 @@ def backbone_linear(x: torch.Tensor, sv: torch.Tensor, in_scale: torch.Tensor | 
     return out
 
 
+class BackbonePartials:
+    """The fp32 split-K partial sums [slices, rows, rank] of a backbone projection whose reduction was left to its
+    consumer (backbone_linear_deferred): grouped_forward_block_gr_predecoded_partials takes them in place of the
+    projection's rows.  Holds the call's workspace until then."""
+
+    __slots__ = ("partials", "slices", "rows", "rank")
+
+    def __init__(self, partials: torch.Tensor, slices: int, rows: int, rank: int):
+        self.partials, self.slices, self.rows, self.rank = partials, slices, rows, rank
+
+
+# Rows up to which backbone_linear_deferred leaves the reduction to the consumer (decode batches; the tiled
+# GEMM's shapes start far above).
+BACKBONE_DEFERRED_MAX_ROWS = 64
+
+
+def backbone_linear_deferred(x: torch.Tensor, sv: torch.Tensor, in_scale: torch.Tensor | None = None):
+    """backbone_linear of x's rows with its split-K reduction left to the consumer (tris_backbone_linear_deferred,
+    an extension): a BackbonePartials when the plan splits K, else the fp16 [rows, rank] projection (also for
+    shapes past BACKBONE_DEFERRED_MAX_ROWS, which backbone_linear projects).  The partial sums' reduction gives
+    backbone_linear's bits."""
+    _check_cuda("x", x, torch.float16, 2)
+    _check_cuda("shared_sv", sv, torch.float16, 2, x.device)
+    if sv.size(1) != x.size(1):
+        raise RuntimeError("shared_sv in-features mismatch")
+    if in_scale is not None:
+        _check_cuda("in_scale", in_scale, torch.float16, 1, x.device)
+    rows, in_f, rank = int(x.size(0)), int(sv.size(1)), int(sv.size(0))
+    if rows == 0 or rows > BACKBONE_DEFERRED_MAX_ROWS or _backbone_use_library(rows, in_f, rank):
+        return backbone_linear(x, sv, in_scale=in_scale)
+    out = torch.empty((rows, rank), dtype=torch.float16, device=x.device)
+    lib = _lib.load()
+    ws = backbone_workspace(x.device, int(lib.tris_backbone_workspace_bytes(rows, in_f, rank)))
+    slices = ctypes.c_int32(0)
+    _lib.check(lib.tris_backbone_linear_deferred(_ptr(x), rows, in_f, None, _ptr(sv), rank, _ptr(in_scale), _ptr(out),
+                                                 _ptr(ws), int(ws.numel()), ctypes.byref(slices), _stream(x)),
+               "tris_backbone_linear_deferred")
+    n = int(slices.value)
+    if n <= 1:
+        return out
+    part = ws[: n * rows * rank * 4].view(torch.float32).view(n, rows, rank)
+    return BackbonePartials(part, n, rows, rank)
+
+
+def partials_gemm_ok(payload: dict) -> bool:
+    """True when grouped_forward_block_gr_predecoded_partials takes a projection's payload dict: rank <= 512, a
+    multiple of 64, and at most 8 row-scale groups (the MFMA kernel's staging of one chunk)."""
+    rank = int(payload["g_idx"].size(1))
+    return 0 < rank <= 512 and rank % 64 == 0 and int(payload["row_pack3"].size(2)) <= 8
+
+
+def grouped_forward_block_gr_predecoded_partials(hidden: BackbonePartials, expert_ids, segment_offsets,
+                                                 total_problem_tiles, decoded_q_gmap_words, qweight1,
+                                                 qweight2_sparse, qweight2_sparse_prefix, c_map, g_idx, col_pack3,
+                                                 row_pack3, use_uniform_k64_groups=True, out=None,
+                                                 decoded_by_expert=False):
+    """compact3_tris_precomputed_grouped_forward_block_gr_predecoded over the rows a deferred backbone projection
+    leaves as partial sums (tris_grouped_forward_block_gr_predecoded_partials, an extension): the GEMM's staging
+    adds the slices as backbone_linear's reduction would, so the output is that GEMM's over backbone_linear's
+    output, bit for bit, without the reduction's launch."""
+    if not isinstance(hidden, BackbonePartials):
+        raise RuntimeError("grouped_forward_block_gr_predecoded_partials: hidden must be a BackbonePartials")
+    dev = hidden.partials.device
+    _check_cuda("expert_ids", expert_ids, torch.int32, 1, dev)
+    _check_cuda("segment_offsets", segment_offsets, torch.int32, 1, dev)
+    if segment_offsets.size(0) != expert_ids.size(0) + 1:
+        raise RuntimeError("segment_offsets must be 1D [segments + 1]")
+    total = _host_tiles(total_problem_tiles)
+    pay = make_payload_struct(hidden.rank, qweight1, qweight2_sparse, qweight2_sparse_prefix, None, None, None,
+                              c_map, g_idx, col_pack3, row_pack3, None, False, None, False, use_uniform_k64_groups,
+                              dev, need_gr=False)
+    _check_predecoded(decoded_q_gmap_words, expert_ids, pay, dev, decoded_by_expert)
+    out = _out_buffer(out, hidden.rows, pay.outfeatures, dev)
+    _lib.check(_lib.load().tris_grouped_forward_block_gr_predecoded_partials(
+        _ptr(hidden.partials), hidden.slices, hidden.rows, _ptr(expert_ids), _ptr(segment_offsets),
+        int(expert_ids.size(0)), total, _ptr(decoded_q_gmap_words), ctypes.byref(pay), _ptr(out),
+        1 if decoded_by_expert else 0, _stream(hidden.partials)), "grouped_forward_block_gr_predecoded_partials")
+    return out
+
+
 def backbone_linear_pair(x: torch.Tensor, sv_a: torch.Tensor, sv_b: torch.Tensor,
                          row_index: torch.Tensor | None = None, in_scale_a: torch.Tensor | None = None,
                          in_scale_b: torch.Tensor | None = None):

@@ -424,6 +424,11 @@ NS_GATE_UP_BESIDE = True
 # 133.4 us); False keeps its four launches of its own.
 FOLD_SHARED_EXPERT = True
 
+# After the fused gate/up GEMM the down backbone's split-K partial sums go straight to the down GEMM, whose
+# staging adds them (ext.backbone_linear_deferred, ext.grouped_forward_block_gr_predecoded_partials): the same
+# bits without the reduction's launch.
+DOWN_PARTIALS_IN_GEMM = True
+
 # The decode step decodes every expert's split bitmaps (slot e for expert e) when the batch routes at least this
 # many rows per expert, so the predecode does not wait for the router's selection (measured on MI355X at the
 # Mixtral shape: T = 8, 16 rows over 8 experts, 92.4 -> 89.0 us; T = 4, 8 rows over ~5 experts, 78.8 against
@@ -583,11 +588,20 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
         with torch.cuda.stream(side):
             ext.ns_compensation_apply_(comp_d, mlp, eid, seg, ns["down"], accumulate=False)
     if hid_d is None:
-        hid_d = shared_projection(mlp, backbones["down"], in_scale=sc["down"])
+        if DOWN_PARTIALS_IN_GEMM and isinstance(backbones["down"], torch.Tensor) and ext.partials_gemm_ok(pd):
+            # the down backbone's split-K slices added by the down GEMM's staging (no reduction launch)
+            hid_d = ext.backbone_linear_deferred(mlp, backbones["down"], in_scale=sc["down"])
+        else:
+            hid_d = shared_projection(mlp, backbones["down"], in_scale=sc["down"])
     d_out = torch.empty((R, n_out), dtype=torch.float16, device=dev)
-    ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
-        hid_d, eid, seg, prob, tile_bound, decoded["down"], *[pd[k] for k in names], True, out=d_out,
-        decoded_by_expert=decoded_by_expert)
+    if isinstance(hid_d, ext.BackbonePartials):
+        ext.grouped_forward_block_gr_predecoded_partials(
+            hid_d, eid, seg, tile_bound, decoded["down"], *[pd[k] for k in names], True, out=d_out,
+            decoded_by_expert=decoded_by_expert)
+    else:
+        ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
+            hid_d, eid, seg, prob, tile_bound, decoded["down"], *[pd[k] for k in names], True, out=d_out,
+            decoded_by_expert=decoded_by_expert)
     if comp_d is not None:
         main.wait_stream(side)
     elif ns["down"] is not None:

@@ -502,3 +502,130 @@ def test_backbone_swiglu_column_split_matches_whole_projection(tris, cuda, rows,
     big = torch.zeros((ext.SWIGLU_BACKBONE_MAX_ROWS + 1, in_f), dtype=torch.float16, device=cuda)
     with pytest.raises(RuntimeError, match="column split"):
         ext.backbone_swiglu_linear_split(big, big, sv, split)
+
+
+PARTIAL_CASES = [
+    # rows per segment (expert id, rows), in_features, rank, outfeatures, input scale, every expert decoded
+    ([(3, 1), (6, 1)], 14336, 512, 256, False, False),   # Mixtral T = 1 down shape: 16 slices, one row a tile
+    ([(2, 4)], 4096, 512, 192, True, False),              # four rows in one segment, input scale
+    ([(0, 2), (5, 1)], 4096, 128, 128, False, True),      # 32 slices (two load batches), slots by expert id
+    ([(1, 2), (4, 2), (7, 1)], 1024, 256, 320, True, True),  # 8 slices
+    ([(5, 1)], 512, 64, 64, False, False),                # 4 slices
+]
+
+
+@pytest.mark.parametrize("case", PARTIAL_CASES,
+                         ids=lambda c: "R{}in{}r{}{}".format(sum(n for _, n in c[0]), c[1], c[2], "x" if c[5] else ""))
+def test_down_gemm_from_partial_sums_matches_reduced_backbone(tris, cuda, case):
+    """tris_backbone_linear_deferred leaves the split-K partial sums and
+    tris_grouped_forward_block_gr_predecoded_partials adds them in its staging: the output is the predecoded GEMM's
+    over tris_backbone_linear's rows, bit for bit (one and two batches of slices in flight, several rows in one
+    segment, slots per segment and per expert)."""
+    segs, in_f, rank, n, scaled, by_expert = case
+    R = sum(c for _, c in segs)
+    E = 8
+    note(f"down GEMM from partial sums R={R} in={in_f} rank={rank} N={n} by_expert={by_expert}")
+    ext, ql = tris["ext"], tris["qlinear"]
+    rng = np.random.default_rng(R * 31 + rank)
+    x = torch.from_numpy(rng.standard_normal((R, in_f)).astype(np.float16)).to(cuda)
+    sv = torch.from_numpy((rng.standard_normal((rank, in_f)) * 0.02).astype(np.float16)).to(cuda)
+    sc = torch.from_numpy(rng.uniform(0.5, 1.5, in_f).astype(np.float16)).to(cuda) if scaled else None
+    pay = ql.payload_to_device(make_projection(tris, 900 + rank, E, n, rank), cuda)
+    assert ext.partials_gemm_ok(pay)
+    eid = t_i32([e for e, _ in segs], cuda)
+    offs = np.concatenate([[0], np.cumsum([c for _, c in segs])])
+    seg = t_i32(offs, cuda)
+    prob = t_i32(np.concatenate([[0], np.cumsum([(c + 15) // 16 for _, c in segs])]), cuda)
+    tiles = int(sum((c + 15) // 16 for _, c in segs))
+    pr = int(pay["qweight1"].size(1))
+    nblk = ((pr + 1) // 2) * ((n + 63) // 64)
+    slots = E if by_expert else len(segs)
+    dec = torch.full((slots, nblk, 128), -7, dtype=torch.int32, device=cuda)
+    ids = torch.arange(E, dtype=torch.int32, device=cuda) if by_expert else eid
+    ext.grouped_block_gr_predecode_multi([(dec, pay["q_gmap_gr_words"], pay["q_gmap_gr_offsets"],
+                                           pay["q_gmap_gr_meta"], pr, n)], ids)
+    pend = ext.backbone_linear_deferred(x, sv, in_scale=sc)
+    assert isinstance(pend, ext.BackbonePartials) and pend.slices > 1
+    got = torch.full((R, n), float("nan"), dtype=torch.float16, device=cuda)
+    ext.grouped_forward_block_gr_predecoded_partials(pend, eid, seg, tiles, dec, *[pay[k] for k in NAMES], True,
+                                                     out=got, decoded_by_expert=by_expert)
+    hid = ext.backbone_linear(x, sv, in_scale=sc)
+    want = torch.full_like(got, float("nan"))
+    ext.compact3_tris_precomputed_grouped_forward_block_gr_predecoded(
+        hid, eid, seg, prob, tiles, dec, *[pay[k] for k in NAMES], True, out=want, decoded_by_expert=by_expert)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    # the partial sums themselves: their slice-order sum is tris_backbone_linear's output
+    acc = torch.zeros((R, rank), dtype=torch.float32, device=cuda)
+    for s in range(pend.slices):
+        acc = acc + pend.partials[s]
+    assert torch.equal(acc.to(torch.float16).view(torch.int16), hid.view(torch.int16))
+
+
+def test_deferred_backbone_entries_reject_unsupported_shapes(tris, cuda):
+    """One slice: backbone_linear_deferred returns the projection itself.  The C entries reject what they cannot
+    run with an error: a shape that takes the tiled GEMM (its reduction cannot be deferred) and partial sums for
+    a rank past one 512-column chunk."""
+    import ctypes
+
+    from tris_moe_amd import _lib as lib
+
+    ext = tris["ext"]
+    note("deferred backbone: one slice, rejected shapes")
+    rng = np.random.default_rng(5)
+    x = torch.from_numpy(rng.standard_normal((2, 128)).astype(np.float16)).to(cuda)
+    sv = torch.from_numpy((rng.standard_normal((128, 128)) * 0.05).astype(np.float16)).to(cuda)
+    one = ext.backbone_linear_deferred(x, sv)
+    assert isinstance(one, torch.Tensor)
+    assert torch.equal(one.view(torch.int16), ext.backbone_linear(x, sv).view(torch.int16))
+    L = lib.load()
+    tokens, in_f, rank = 512, 4096, 512
+    xs = torch.zeros((tokens, in_f), dtype=torch.float16, device=cuda)
+    svs = torch.zeros((rank, in_f), dtype=torch.float16, device=cuda)
+    out = torch.empty((tokens, rank), dtype=torch.float16, device=cuda)
+    nbytes = int(L.tris_backbone_workspace_bytes(tokens, in_f, rank))
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=cuda)
+    slices = ctypes.c_int32(-1)
+    rc = L.tris_backbone_linear_deferred(xs.data_ptr(), tokens, in_f, None, svs.data_ptr(), rank, None,
+                                         out.data_ptr(), ws.data_ptr(), int(ws.numel()), ctypes.byref(slices),
+                                         torch.cuda.current_stream().cuda_stream)
+    assert rc != 0 and b"tiled GEMM" in L.tris_last_error()
+    pay = tris["qlinear"].payload_to_device(make_projection(tris, 77, 2, 64, 576), cuda)
+    assert not ext.partials_gemm_ok(pay)
+    pstruct = ext.make_payload_struct(576, *[pay[k] for k in ("qweight1", "qweight2_sparse", "qweight2_sparse_prefix")],
+                                      None, None, None, *[pay[k] for k in ("c_map", "g_idx", "col_pack3", "row_pack3")],
+                                      None, False, None, False, True, cuda, need_gr=False)
+    part = torch.zeros((2, 1, 576), dtype=torch.float32, device=cuda)
+    dec = torch.zeros((1, 9 * 1, 128), dtype=torch.int32, device=cuda)
+    o = torch.empty((1, 64), dtype=torch.float16, device=cuda)
+    rc = L.tris_grouped_forward_block_gr_predecoded_partials(
+        part.data_ptr(), 2, 1, t_i32([0], cuda).data_ptr(), t_i32([0, 1], cuda).data_ptr(), 1, 1, dec.data_ptr(),
+        ctypes.byref(pstruct), o.data_ptr(), 0, torch.cuda.current_stream().cuda_stream)
+    assert rc != 0 and b"rank <= 512" in L.tris_last_error()
+
+
+@pytest.mark.parametrize("tokens", [1, 2])
+def test_block_down_partials_in_gemm_matches_reduced_backbone(tris, cuda, tokens, monkeypatch):
+    """The decode step at fused-SwiGLU batches with the down backbone's partial sums added by the down GEMM
+    (moe.DOWN_PARTIALS_IN_GEMM) gives the step with the reduction's own launch bit for bit, on the C1 layer."""
+    from tris_moe_amd.configs import C1_MIXTRAL_DECODE as SPEC
+
+    note(f"block decode step, down partial sums in the GEMM, T={tokens}")
+    syn, ql, moe = tris["synthetic"], tris["qlinear"], tris["moe"]
+    layer = syn.make_layer(SPEC, 6500 + tokens, tris["ext"].gr_encode)
+    payloads = {p: ql.payload_to_device(layer[p], cuda) for p in ("gate", "up", "down")}
+    backbones = {p: torch.from_numpy(layer["backbones"][p]).to(cuda) for p in ("gate", "up", "down")}
+    rng = np.random.default_rng(tokens + 70)
+    router = torch.from_numpy((rng.standard_normal((SPEC.num_experts, SPEC.hidden)) * 0.015).astype(np.float32))
+    block = moe.TrisSparseMoeBlock(SPEC.hidden, SPEC.num_experts, SPEC.top_k, payloads, backbones,
+                                   router_weight=router.to(cuda))
+    inp = syn.make_inputs(SPEC, tokens, 6600 + tokens, layer["outlier_idx"])
+    h = torch.from_numpy(inp["x"]).to(cuda).to(torch.bfloat16).reshape(1, tokens, SPEC.hidden)
+    assert tokens * SPEC.top_k <= moe.FUSED_SWIGLU_MAX_ROWS
+    with torch.no_grad():
+        monkeypatch.setattr(moe, "DOWN_PARTIALS_IN_GEMM", True)
+        got, lg_got = block(h)
+        monkeypatch.setattr(moe, "DOWN_PARTIALS_IN_GEMM", False)
+        want, lg_want = block(h)
+    assert torch.equal(lg_got.view(torch.int16), lg_want.view(torch.int16))
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
