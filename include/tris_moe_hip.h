@@ -391,6 +391,20 @@ int tris_grouped_forward_block_gr_predecoded_partials(
     uint16_t* output, int32_t decoded_by_expert, void* stream);
 
 /*
+ * tris_grouped_forward_block_gr_predecoded_partials for one token routed to two experts, with the routed combine
+ * (tris_moe_combine, modeling_mixtral.py:529-536) in the same launch (no reference counterpart): partials
+ * [slices][2][rank] are the two routed rows' down backbone, segments 0 and 1 one row each (a top-2 route of one
+ * token); inverse_perm [2] and routing_weights_f16 [2] are the route's.  out [1, N] in bf16 (out_bf16 != 0) or
+ * fp16 receives dt(fp16(y_r0 * w_r0) + fp16(y_r1 * w_r1)) with y the GEMM's rows rounded to fp16: tris_moe_combine's
+ * output over the GEMM's, bit for bit.  A route that is not one token on two valid experts gives zeros.
+ */
+int tris_grouped_forward_block_gr_predecoded_partials_combine(
+    const float* partials, int32_t slices, const int32_t* expert_ids, const int32_t* segment_offsets,
+    int64_t total_problem_tiles, const int32_t* decoded, const tris_compact3_payload* payload,
+    const int32_t* inverse_perm, const uint16_t* routing_weights_f16, int32_t out_bf16, uint16_t* out,
+    int32_t decoded_by_expert, void* stream);
+
+/*
  * Dequantise the listed experts to dense fp16 weights [num, N, rank]
  * (verification kernel; the product GEMMs never write weights).  Replaces the
  * reference's CPU dequant QuantLinear._dequantize_compact3_matrix

@@ -25,12 +25,6 @@
 
 namespace tris {
 
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu) != 0u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
-}
 
 // fp16(a + b) for fp16 bit patterns: the exact sum rounded once, as torch's fp16 add_.
 __device__ __forceinline__ uint16_t f16_add_bits(uint16_t a, uint16_t b) { return f2h_bits(h2f(a) + h2f(b)); }

@@ -42,6 +42,13 @@ __device__ __forceinline__ float h2f(uint16_t bits) {
 __device__ __forceinline__ uint16_t f2h_bits(float v) {
   return __half_as_ushort(__float2half(v));
 }
+// float -> bf16 bits, round to nearest even (NaN stays a quiet NaN), as torch's .to(bfloat16).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu) != 0u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
 // Correctly rounded fp16 product / sum (RNE), matching __hmul/__hadd.
 __device__ __forceinline__ uint16_t hmul_bits(uint16_t a, uint16_t b) {
   return __half_as_ushort(__hmul(__ushort_as_half(a), __ushort_as_half(b)));

@@ -566,7 +566,8 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
                         const int32_t* decoded_b, const tris_compact3_payload* pa, const tris_compact3_payload* pb,
                         uint16_t* out_a, uint16_t* out_b, bool swiglu, void* stream, const char* who,
                         const int64_t* row_index = nullptr, int hidden_rows = 0, bool decoded_by_expert = false,
-                        const float* partials = nullptr, int slices = 0);
+                        const float* partials = nullptr, int slices = 0, uint16_t* comb_out = nullptr,
+                        const int32_t* comb_inv = nullptr, const uint16_t* comb_w = nullptr, bool comb_bf16 = false);
 bool grouped_mfma_supported(const tris_compact3_payload* p, const uint16_t* hidden);
 
 }  // namespace tris
@@ -789,6 +790,26 @@ extern "C" int tris_grouped_forward_block_gr_predecoded_partials(
   return launch_grouped_mfma(nullptr, nullptr, batch, expert_ids, segment_offsets, num_segments, decoded, nullptr, &p,
                              nullptr, output, nullptr, false, stream, who, nullptr, batch, decoded_by_expert != 0,
                              partials, slices);
+}
+
+extern "C" int tris_grouped_forward_block_gr_predecoded_partials_combine(
+    const float* partials, int32_t slices, const int32_t* expert_ids, const int32_t* segment_offsets,
+    int64_t total_problem_tiles, const int32_t* decoded, const tris_compact3_payload* payload,
+    const int32_t* inverse_perm, const uint16_t* routing_weights_f16, int32_t out_bf16, uint16_t* out,
+    int32_t decoded_by_expert, void* stream) {
+  const char* who = "tris_grouped_forward_block_gr_predecoded_partials_combine";
+  TRIS_REQUIRE(payload != nullptr && partials != nullptr && out != nullptr, "%s: null payload, partial sums or output",
+               who);
+  TRIS_REQUIRE(slices >= 1, "%s: no slices", who);
+  tris_compact3_payload p = *payload;  // the predecoded kernels apply no scale or bias
+  p.has_output_scale = 0;
+  p.has_bias = 0;
+  TRIS_REQUIRE(grouped_mfma_supported(&p, reinterpret_cast<const uint16_t*>(partials)),
+               "%s: needs uniform 64-column groups, rank %% 64 == 0 and 16-byte aligned partial sums", who);
+  if (total_problem_tiles <= 0) return TRIS_OK;
+  return launch_grouped_mfma(nullptr, nullptr, 2, expert_ids, segment_offsets, 2, decoded, nullptr, &p, nullptr, out,
+                             nullptr, false, stream, who, nullptr, 2, decoded_by_expert != 0, partials, slices, out,
+                             inverse_perm, routing_weights_f16, out_bf16 != 0);
 }
 
 extern "C" int tris_compact3_dequant(const tris_compact3_payload* payload, const int32_t* expert_ids, int32_t num,

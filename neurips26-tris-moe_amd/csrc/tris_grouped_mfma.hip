@@ -70,6 +70,12 @@ struct MfmaArgs {
   const int32_t* segment_offsets;
   int num_segments;
   int decoded_by_expert;  // 0: decoded holds one slot per segment; 1: one per expert id (every expert decoded)
+  // One token's combine in the launch (two units, proj[1] == proj[0]; null: none): the token's two routed rows are
+  // row tiles 0 and 1, one a unit, and unit 0 writes dt(fp16(out_r0 * w_r0) + fp16(out_r1 * w_r1)) to comb_out.
+  uint16_t* comb_out;
+  const int32_t* comb_inv;  // inverse_perm [2]: the row of each pick
+  const uint16_t* comb_w;   // fp16 routing weights [2], by pick
+  int comb_bf16;            // comb_out is bf16 (else fp16)
 };
 
 // Position of column k (0..31) of a packed row in the staged order: lane group
@@ -926,20 +932,24 @@ void grouped_mfma_kernel(MfmaArgs a) {
   const MfSegScan sc = mf_scan_segments(a.segment_offsets, a.expert_ids, a.num_segments, kMfRows);
   const int R = __builtin_amdgcn_readfirstlane(sc.total);
   if (R == 0) return;  // no rows
+  // the one-token combine: the two units take row tiles 0 and 1 of the same output tiles, so the workgroups share
+  // out output tiles only
+  const bool comb = kUnits == 2 && a.comb_out != nullptr;
+  const int Rm = comb ? 1 : R;
   const int W = static_cast<int>(gridDim.x);
   const int w = static_cast<int>(blockIdx.x);
   int rt_first = w, rt_step = W, ob_lo = 0, ob_hi = nob;
-  if (static_cast<int64_t>(R) * nob <= W) {
+  if (static_cast<int64_t>(Rm) * nob <= W) {
     // at least one workgroup per (row tile, output tile): workgroup w takes pair w, and the idle ones are the
     // last of the grid, so the busy ones are spread evenly over the CUs as the hardware deals them out
-    if (w >= R * nob) return;
+    if (w >= Rm * nob) return;
     rt_first = w / nob;
     ob_lo = w - rt_first * nob;
     ob_hi = ob_lo + 1;
-    rt_step = R;  // one row tile
-  } else if (R <= W) {
-    const int per = W / R;
-    const int extra = W % R;
+    rt_step = Rm;  // one row tile
+  } else if (Rm <= W) {
+    const int per = W / Rm;
+    const int extra = W % Rm;
     int sub, cnt;
     if (w < extra * (per + 1)) {
       rt_first = w / (per + 1);
@@ -954,7 +964,28 @@ void grouped_mfma_kernel(MfmaArgs a) {
     if (sub >= cnt) return;  // more workgroups than output tiles for this row tile
     ob_lo = static_cast<int>(static_cast<int64_t>(sub) * nob / cnt);
     ob_hi = static_cast<int>(static_cast<int64_t>(sub + 1) * nob / cnt);
-    rt_step = R;  // one row tile
+    rt_step = Rm;  // one row tile
+  }
+  // the combine's weights by row (w_row[inverse_perm[s]] = w[s]); a route that is not one token on two experts,
+  // one row each, gets zero outputs (before any barrier, the same in both units)
+  uint16_t wr0 = 0, wr1 = 0;
+  if (comb) {
+    const int inv0 = a.comb_inv[0], inv1 = a.comb_inv[1];
+    bool ok = R == 2 && ((inv0 == 0 && inv1 == 1) || (inv0 == 1 && inv1 == 0));
+    for (int t = 0; t < 2 && ok; ++t) {
+      int cs = 0, cr0 = 0, crc = 0, ce = -1;
+      mf_map_scanned(sc, a.segment_offsets, a.expert_ids, a.num_segments, t, kMfRows, &cs, &cr0, &crc, &ce);
+      ce = __builtin_amdgcn_readfirstlane(ce);
+      ok = __builtin_amdgcn_readfirstlane(crc) == 1 && ce >= 0 && ce < p.num_experts;
+    }
+    if (!ok) {
+      if (unit == 0) {
+        for (int n = ob_lo * kTileOut + utid; n < ob_hi * kTileOut && n < N; n += kMfThreads) a.comb_out[n] = 0;
+      }
+      return;
+    }
+    wr0 = a.comb_w[inv0 == 0 ? 0 : 1];
+    wr1 = a.comb_w[inv0 == 0 ? 1 : 0];
   }
   const int lane = utid % kWave;
   uint16_t* out = kUnits == 2 ? a.proj[0].out : pa.out;
@@ -996,7 +1027,8 @@ void grouped_mfma_kernel(MfmaArgs a) {
   const bool one_chunk = rank <= kMfChunk;
   const int kg = lane / 16;
 
-  for (int rt = rt_first; rt < R; rt += rt_step) {
+  for (int rt_i = rt_first; rt_i < Rm; rt_i += rt_step) {
+  const int rt = comb ? unit : rt_i;  // the combine's units: row tiles 0 and 1
   int s = 0, row0 = 0, rc = 0, e = -1;
   mf_map_scanned(sc, a.segment_offsets, a.expert_ids, a.num_segments, rt, kMfRows, &s, &row0, &rc, &e);
   s = __builtin_amdgcn_readfirstlane(s);  // the mapping is the same in every lane
@@ -1016,7 +1048,7 @@ void grouped_mfma_kernel(MfmaArgs a) {
     }
     continue;
   }
-  if (rt != rt_first) __syncthreads();  // the previous row tile's LDS readers are done
+  if (rt_i != rt_first) __syncthreads();  // the previous row tile's LDS readers are done
   // A operand row of this lane: rows past rc feed output rows that are not stored, so they read row 0 (the same
   // LDS words as lane 0's rows: broadcast reads instead of bank conflicts; T = 16 gate/up launch 33.2 -> 32.5 us)
   const int xrow = i16 < rc ? i16 : 0;
@@ -1100,7 +1132,19 @@ void grouped_mfma_kernel(MfmaArgs a) {
     if (kUnits == 2) {
       if (unit == 1) *reinterpret_cast<f32x4*>(&exch[utid * 4]) = acc;
       __syncthreads();
-      if (unit == 0) {
+      if (unit == 0 && comb) {
+        // row 0 of each unit's tile (one row a tile): the combine of the token's two rows at column n, the products
+        // rounded to fp16 (the asm keeps them from being fused into the sum) and added in fp32 (two terms: the
+        // pick order does not matter), rounded once to the output dtype
+        if (kg == 0 && nv) {
+          const float up0 = exch[utid * 4];
+          uint16_t p0 = hmul_bits(f2h_bits(acc[0]), wr0);
+          uint16_t p1 = hmul_bits(f2h_bits(up0), wr1);
+          asm volatile("" : "+v"(p0), "+v"(p1));
+          const float y = h2f(p0) + h2f(p1);
+          a.comb_out[n] = a.comb_bf16 ? f32_to_bf16_rne(y) : f2h_bits(y);
+        }
+      } else if (unit == 0) {
         const f32x4 up = *reinterpret_cast<const f32x4*>(&exch[utid * 4]);
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
@@ -1657,7 +1701,8 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
                         const int32_t* decoded_b, const tris_compact3_payload* pa, const tris_compact3_payload* pb,
                         uint16_t* out_a, uint16_t* out_b, bool swiglu, void* stream, const char* who,
                         const int64_t* row_index, int hidden_rows, bool decoded_by_expert, const float* partials,
-                        int slices) {
+                        int slices, uint16_t* comb_out, const int32_t* comb_inv, const uint16_t* comb_w,
+                        bool comb_bf16) {
   TRIS_REQUIRE(batch >= 0 && num_segments >= 0, "%s: negative batch or segment count", who);
   TRIS_REQUIRE(row_index == nullptr || hidden_rows >= 0, "%s: negative hidden row count", who);
   int rc = check_payload(pa, false, who);
@@ -1669,6 +1714,12 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
   TRIS_REQUIRE(!swiglu || pb != nullptr, "%s: the fused SwiGLU needs two projections", who);
   if (batch == 0 || num_segments == 0) return TRIS_OK;
   TRIS_REQUIRE((hidden_a || partials) && out_a && expert_ids && segment_offsets && decoded_a, "%s: null pointer", who);
+  if (comb_out != nullptr) {
+    // one token routed to two experts: two rows, two segments, one projection
+    TRIS_REQUIRE(pb == nullptr && !swiglu && row_index == nullptr && comb_inv && comb_w,
+                 "%s: the one-token combine takes one projection and the route's picks", who);
+    TRIS_REQUIRE(batch == 2 && num_segments == 2, "%s: the one-token combine takes 2 rows in 2 segments", who);
+  }
   if (partials != nullptr) {
     // one projection, one chunk, every slice's rows addressed by 32-bit buffer offsets
     TRIS_REQUIRE(pb == nullptr && !swiglu && row_index == nullptr, "%s: partial sums feed one projection", who);
@@ -1700,7 +1751,14 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
   args.segment_offsets = segment_offsets;
   args.num_segments = num_segments;
   args.decoded_by_expert = decoded_by_expert ? 1 : 0;
-  const int units = swiglu ? 2 : 1;
+  if (comb_out != nullptr) {  // both units run the one projection, on row tiles 0 and 1
+    args.proj[1] = args.proj[0];
+    args.comb_out = comb_out;
+    args.comb_inv = comb_inv;
+    args.comb_w = comb_w;
+    args.comb_bf16 = comb_bf16 ? 1 : 0;
+  }
+  const int units = (swiglu || comb_out != nullptr) ? 2 : 1;
   const int nproj = (pb && !swiglu) ? 2 : 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
   // long segments: keep each output tile's weights in registers and stream the segment's rows through them
@@ -1734,10 +1792,11 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
   const int64_t pairs =
       (static_cast<int64_t>(batch) / kMfRows + (num_segments < batch ? num_segments : batch)) * ceil_div(max_n, kTileOut);
   if (pairs < wgs) wgs = static_cast<int>(pairs);
+  if (comb_out != nullptr && ceil_div(max_n, kTileOut) < wgs) wgs = ceil_div(max_n, kTileOut);  // output tiles only
   const dim3 grid(wgs > 0 ? wgs : 1, 1, nproj);
   const dim3 block(units * kMfThreads);
 #define TRIS_MF_LAUNCH(U, ROWS, C) hipLaunchKernelGGL((grouped_mfma_kernel<U, ROWS, C>), grid, block, 0, s, args)
-  if (swiglu) {
+  if (units == 2) {
     if (rows == 4) {
       if (compact) TRIS_MF_LAUNCH(2, 4, true); else TRIS_MF_LAUNCH(2, 4, false);
     } else {

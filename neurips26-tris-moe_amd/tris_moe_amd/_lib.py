@@ -194,6 +194,8 @@ SIGNATURES = {
         ctypes.c_int, [_P, _P, _P, _I32, _I32, _P, _P, _I32, _I64, _P, _P, _PAY, _PAY, _P, _P, _P]),
     "tris_grouped_forward_block_gr_predecoded_partials": (
         ctypes.c_int, [_P, _I32, _I32, _P, _P, _I32, _I64, _P, _PAY, _P, _I32, _P]),
+    "tris_grouped_forward_block_gr_predecoded_partials_combine": (
+        ctypes.c_int, [_P, _I32, _P, _P, _I64, _P, _PAY, _P, _P, _I32, _P, _I32, _P]),
     "tris_moe_combine_gated": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _P, _P]),
     "tris_swiglu_mul": (ctypes.c_int, [_P, _P, _I64, _P, _P]),
     "tris_swiglu_mul_compensated": (ctypes.c_int, [_P, _P, _P, _P, _I64, _P, _P]),

@@ -1107,6 +1107,43 @@ def grouped_forward_block_gr_predecoded_partials(hidden: BackbonePartials, exper
     return out
 
 
+def grouped_forward_block_gr_predecoded_partials_combine(hidden: BackbonePartials, expert_ids, segment_offsets,
+                                                         total_problem_tiles, decoded_q_gmap_words, qweight1,
+                                                         qweight2_sparse, qweight2_sparse_prefix, c_map, g_idx,
+                                                         col_pack3, row_pack3, inverse_perm, routing_weights_f16,
+                                                         out_dtype=torch.bfloat16, use_uniform_k64_groups=True,
+                                                         decoded_by_expert=False):
+    """grouped_forward_block_gr_predecoded_partials for one token routed to two experts with the routed combine in
+    the same launch (tris_grouped_forward_block_gr_predecoded_partials_combine, an extension): returns the token's
+    [1, N] output in out_dtype (bf16 or fp16), moe_combine's over the GEMM's rows bit for bit."""
+    if not isinstance(hidden, BackbonePartials) or hidden.rows != 2:
+        raise RuntimeError("the one-token combine takes the partial sums of 2 routed rows")
+    if out_dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError("out_dtype must be bfloat16 or float16")
+    dev = hidden.partials.device
+    _check_cuda("expert_ids", expert_ids, torch.int32, 1, dev)
+    _check_cuda("segment_offsets", segment_offsets, torch.int32, 1, dev)
+    _check_cuda("inverse_perm", inverse_perm, torch.int32, 1, dev)
+    _check_cuda("routing_weights_f16", routing_weights_f16, torch.float16, None, dev)
+    if int(expert_ids.numel()) != 2 or int(segment_offsets.numel()) != 3:
+        raise RuntimeError("the one-token combine takes 2 segments")
+    if int(inverse_perm.numel()) != 2 or int(routing_weights_f16.numel()) != 2:
+        raise RuntimeError("the one-token combine takes a top-2 route of one token")
+    total = _host_tiles(total_problem_tiles)
+    pay = make_payload_struct(hidden.rank, qweight1, qweight2_sparse, qweight2_sparse_prefix, None, None, None,
+                              c_map, g_idx, col_pack3, row_pack3, None, False, None, False, use_uniform_k64_groups,
+                              dev, need_gr=False)
+    _check_predecoded(decoded_q_gmap_words, expert_ids, pay, dev, decoded_by_expert)
+    out = torch.empty((1, pay.outfeatures), dtype=out_dtype, device=dev)
+    w16 = routing_weights_f16.contiguous()
+    _lib.check(_lib.load().tris_grouped_forward_block_gr_predecoded_partials_combine(
+        _ptr(hidden.partials), hidden.slices, _ptr(expert_ids), _ptr(segment_offsets), total,
+        _ptr(decoded_q_gmap_words), ctypes.byref(pay), _ptr(inverse_perm), _ptr(w16),
+        1 if out_dtype == torch.bfloat16 else 0, _ptr(out), 1 if decoded_by_expert else 0, _stream(hidden.partials)),
+        "grouped_forward_block_gr_predecoded_partials_combine")
+    return out
+
+
 def backbone_linear_pair(x: torch.Tensor, sv_a: torch.Tensor, sv_b: torch.Tensor,
                          row_index: torch.Tensor | None = None, in_scale_a: torch.Tensor | None = None,
                          in_scale_b: torch.Tensor | None = None):

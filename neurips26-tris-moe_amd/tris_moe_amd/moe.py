@@ -428,6 +428,9 @@ FOLD_SHARED_EXPERT = True
 # staging adds them (ext.backbone_linear_deferred, ext.grouped_forward_block_gr_predecoded_partials): the same
 # bits without the reduction's launch.
 DOWN_PARTIALS_IN_GEMM = True
+# One token on two experts (Mixtral at T = 1): the routed combine in the down GEMM's launch
+# (ext.grouped_forward_block_gr_predecoded_partials_combine), the combine launch's bits.
+COMBINE_IN_DOWN_GEMM = True
 
 # The decode step decodes every expert's split bitmaps (slot e for expert e) when the batch routes at least this
 # many rows per expert, so the predecode does not wait for the router's selection (measured on MI355X at the
@@ -593,6 +596,14 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
             hid_d = ext.backbone_linear_deferred(mlp, backbones["down"], in_scale=sc["down"])
         else:
             hid_d = shared_projection(mlp, backbones["down"], in_scale=sc["down"])
+    if (isinstance(hid_d, ext.BackbonePartials) and COMBINE_IN_DOWN_GEMM and int(x16.size(0)) == 1 and R == 2
+            and shared_expert is None and ns["down"] is None):
+        # one token on two experts: the routed combine in the down GEMM's launch (its two units take the two rows)
+        cd = _combine_dtype(output_dtype)
+        out = ext.grouped_forward_block_gr_predecoded_partials_combine(
+            hid_d, eid, seg, tile_bound, decoded["down"], *[pd[k] for k in names], route["inverse_perm"], w16,
+            out_dtype=cd, decoded_by_expert=decoded_by_expert)
+        return out if output_dtype == cd else out.to(output_dtype)
     d_out = torch.empty((R, n_out), dtype=torch.float16, device=dev)
     if isinstance(hid_d, ext.BackbonePartials):
         ext.grouped_forward_block_gr_predecoded_partials(

@@ -629,3 +629,93 @@ def test_block_down_partials_in_gemm_matches_reduced_backbone(tris, cuda, tokens
         want, lg_want = block(h)
     assert torch.equal(lg_got.view(torch.int16), lg_want.view(torch.int16))
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+COMBINE_CASES = [
+    # experts of the two segments, inverse_perm (pick -> row), output dtype, every expert decoded
+    ((3, 6), (0, 1), torch.bfloat16, False),
+    ((1, 7), (1, 0), torch.bfloat16, True),   # the first pick's expert holds the second row
+    ((0, 5), (1, 0), torch.float16, False),
+]
+
+
+@pytest.mark.parametrize("case", COMBINE_CASES, ids=lambda c: "e{}{}inv{}{}{}{}".format(
+    c[0][0], c[0][1], c[1][0], c[1][1], "bf16" if c[2] == torch.bfloat16 else "fp16", "x" if c[3] else ""))
+def test_down_gemm_with_one_token_combine_matches_combine_launch(tris, cuda, case):
+    """tris_grouped_forward_block_gr_predecoded_partials_combine (one token routed to two experts, the routed
+    combine in the down GEMM's launch) gives tris_moe_combine's output over the partial-sum down GEMM's rows, bit
+    for bit, in either pick order and output dtype."""
+    experts, inv, dt, by_expert = case
+    E, in_f, rank, n = 8, 14336, 512, 320
+    note(f"down GEMM with the one-token combine experts={experts} inv={inv} {dt} by_expert={by_expert}")
+    ext, ql = tris["ext"], tris["qlinear"]
+    rng = np.random.default_rng(sum(experts) * 11 + inv[0])
+    x = torch.from_numpy(rng.standard_normal((2, in_f)).astype(np.float16)).to(cuda)
+    sv = torch.from_numpy((rng.standard_normal((rank, in_f)) * 0.02).astype(np.float16)).to(cuda)
+    pay = ql.payload_to_device(make_projection(tris, 950 + experts[0], E, n, rank), cuda)
+    eid = t_i32(list(experts), cuda)
+    seg = t_i32([0, 1, 2], cuda)
+    pr = int(pay["qweight1"].size(1))
+    nblk = ((pr + 1) // 2) * ((n + 63) // 64)
+    dec = torch.full((E if by_expert else 2, nblk, 128), -7, dtype=torch.int32, device=cuda)
+    ids = torch.arange(E, dtype=torch.int32, device=cuda) if by_expert else eid
+    ext.grouped_block_gr_predecode_multi([(dec, pay["q_gmap_gr_words"], pay["q_gmap_gr_offsets"],
+                                           pay["q_gmap_gr_meta"], pr, n)], ids)
+    inverse_perm = t_i32(list(inv), cuda)
+    w16 = torch.from_numpy(rng.uniform(0.1, 0.9, (1, 2)).astype(np.float16)).to(cuda)
+    pend = ext.backbone_linear_deferred(x, sv)
+    assert isinstance(pend, ext.BackbonePartials)
+    got = ext.grouped_forward_block_gr_predecoded_partials_combine(
+        pend, eid, seg, 2, dec, *[pay[k] for k in NAMES], inverse_perm, w16, out_dtype=dt, decoded_by_expert=by_expert)
+    rows = torch.empty((2, n), dtype=torch.float16, device=cuda)
+    ext.grouped_forward_block_gr_predecoded_partials(pend, eid, seg, 2, dec, *[pay[k] for k in NAMES], True, out=rows,
+                                                     decoded_by_expert=by_expert)
+    want = ext.moe_combine(rows, inverse_perm, w16, out_dtype=dt)
+    torch.cuda.synchronize()
+    assert got.dtype == dt and tuple(got.shape) == (1, n)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_one_token_combine_rejects_other_routes_with_zeros(tris, cuda):
+    """A route that is not one token on two experts with one row each (here both rows in one segment) gives a zero
+    output row instead of reading past the route."""
+    ext, ql = tris["ext"], tris["qlinear"]
+    note("one-token combine: malformed route")
+    rng = np.random.default_rng(3)
+    x = torch.from_numpy(rng.standard_normal((2, 4096)).astype(np.float16)).to(cuda)
+    sv = torch.from_numpy((rng.standard_normal((512, 4096)) * 0.02).astype(np.float16)).to(cuda)
+    pay = ql.payload_to_device(make_projection(tris, 977, 4, 128, 512), cuda)
+    pr = int(pay["qweight1"].size(1))
+    dec = torch.zeros((2, ((pr + 1) // 2) * 2, 128), dtype=torch.int32, device=cuda)
+    pend = ext.backbone_linear_deferred(x, sv)
+    got = ext.grouped_forward_block_gr_predecoded_partials_combine(
+        pend, t_i32([1, 2], cuda), t_i32([0, 2, 2], cuda), 1, dec, *[pay[k] for k in NAMES], t_i32([0, 1], cuda),
+        torch.full((1, 2), 0.5, dtype=torch.float16, device=cuda))
+    torch.cuda.synchronize()
+    assert torch.equal(got, torch.zeros_like(got))
+
+
+def test_block_one_token_combine_in_down_gemm_matches_combine_launch(tris, cuda, monkeypatch):
+    """The decode step at T = 1 with the combine in the down GEMM's launch (moe.COMBINE_IN_DOWN_GEMM) gives the
+    step with the combine's own launch bit for bit, on the C1 layer."""
+    from tris_moe_amd.configs import C1_MIXTRAL_DECODE as SPEC
+
+    note("block decode step, one-token combine in the down GEMM")
+    syn, ql, moe = tris["synthetic"], tris["qlinear"], tris["moe"]
+    layer = syn.make_layer(SPEC, 6701, tris["ext"].gr_encode)
+    payloads = {p: ql.payload_to_device(layer[p], cuda) for p in ("gate", "up", "down")}
+    backbones = {p: torch.from_numpy(layer["backbones"][p]).to(cuda) for p in ("gate", "up", "down")}
+    rng = np.random.default_rng(71)
+    router = torch.from_numpy((rng.standard_normal((SPEC.num_experts, SPEC.hidden)) * 0.015).astype(np.float32))
+    block = moe.TrisSparseMoeBlock(SPEC.hidden, SPEC.num_experts, SPEC.top_k, payloads, backbones,
+                                   router_weight=router.to(cuda))
+    for seed in (6801, 6802, 6803):
+        inp = syn.make_inputs(SPEC, 1, seed, layer["outlier_idx"])
+        h = torch.from_numpy(inp["x"]).to(cuda).to(torch.bfloat16).reshape(1, 1, SPEC.hidden)
+        with torch.no_grad():
+            monkeypatch.setattr(moe, "COMBINE_IN_DOWN_GEMM", True)
+            got, lg_got = block(h)
+            monkeypatch.setattr(moe, "COMBINE_IN_DOWN_GEMM", False)
+            want, lg_want = block(h)
+        assert torch.equal(lg_got.view(torch.int16), lg_want.view(torch.int16))
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), seed
