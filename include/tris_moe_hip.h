@@ -513,9 +513,10 @@ int64_t tris_backbone_workspace_bytes(int32_t tokens, int32_t in_features, int32
  * fp16(fp16(silu(gate[r][k])) * up[r][k]), the bits tris_swiglu_mul writes, times in_scale[k] (an fp16
  * product, the ns_mode == 1 input scale) when in_scale is not NULL; out fp16 [rows, rank] = in . sv^T with
  * fp32 accumulation, split over K and the slices added in fixed order (deterministic).  gate, up fp16
- * [rows, in_features], sv fp16 [rank, in_features]; in_features a multiple of 32, and above 128 rows (the tiled
- * prefill GEMM) rank a multiple of 128; 16-byte aligned pointers (else TRIS_ERR_INVALID); workspace of
- * tris_backbone_swiglu_workspace_bytes(rows, in_features, rank).
+ * [rows, in_features], sv fp16 [rank, in_features]; in_features a multiple of 32; above 128 rows the decode kernel
+ * runs in row groups of 128 up to 512 rows for a rank that is not a multiple of 512, and otherwise the tiled
+ * prefill GEMM, which needs a rank that is a multiple of 128; 16-byte aligned pointers (else TRIS_ERR_INVALID);
+ * workspace of tris_backbone_swiglu_workspace_bytes(rows, in_features, rank).
  */
 int tris_backbone_swiglu_linear(const uint16_t* gate, const uint16_t* up, int32_t rows, int32_t in_features,
                                 const uint16_t* sv, int32_t rank, const uint16_t* in_scale, uint16_t* out,
@@ -528,7 +529,8 @@ int64_t tris_backbone_swiglu_workspace_bytes(int32_t rows, int32_t in_features, 
  * the always-on shared expert's down projection, modeling_qwen2_moe.py:815-818, as one projection of the stacked
  * weights over the stacked rows).  out fp16 [rows, split] gets columns [0, split), out_hi fp16
  * [rows, rank - split] columns [split, rank), each the value the whole projection gives there.  0 < split < rank;
- * at most 128 rows (the decode kernel; else TRIS_ERR_INVALID); workspace as tris_backbone_swiglu_linear's.
+ * the decode kernel only (at most 128 rows, or 512 for a rank that is not a multiple of 512; else TRIS_ERR_INVALID);
+ * workspace as tris_backbone_swiglu_linear's.
  */
 int tris_backbone_swiglu_linear_split(const uint16_t* gate, const uint16_t* up, int32_t rows, int32_t in_features,
                                       const uint16_t* sv, int32_t rank, const uint16_t* in_scale, uint16_t* out,

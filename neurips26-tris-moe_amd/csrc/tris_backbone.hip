@@ -693,7 +693,8 @@ int launch_backbone_reduce(const BackboneArgs& args, int nproj, hipStream_t s, c
 constexpr int kSgCols = 128;
 constexpr int kSgWaves = kSgCols / 16;
 constexpr int kSgThreads = kSgWaves * kWave;
-constexpr int kSgMaxRowTiles = 8;
+constexpr int kSgMaxRowTiles = 8;                 // row tiles a workgroup stages (its row group)
+constexpr int kSgMaxRowGroups = 4;                // row groups of one launch (blockIdx.z): at most 512 rows
 constexpr int kSgSteps = 8;                       // K steps of 32 per slice at most
 constexpr int kSgTargetWgs = 256;
 constexpr int kSgVecIters = 4;                    // product vectors (8 columns) a thread forms per batch
@@ -715,6 +716,7 @@ __global__ __launch_bounds__(kSgThreads) void backbone_swiglu_kernel(SwigluBackb
   extern __shared__ __attribute__((aligned(16))) uint16_t sg_in[];  // [TT * 16][slice_k + 8]
   const int cg = blockIdx.x;
   const int slice = blockIdx.y;
+  const int row0 = static_cast<int>(blockIdx.z) * TT * 16;  // the workgroup's row group
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
   const int lane = tid % kWave;
@@ -743,8 +745,8 @@ __global__ __launch_bounds__(kSgThreads) void backbone_swiglu_kernel(SwigluBackb
       const int v = v0 + i * kSgThreads + tid;
       const int r = v / v8;
       const int c = k0 + (v % v8) * 8;
-      const bool ok = v < nvec && r < a.rows;
-      const int64_t o = static_cast<int64_t>(ok ? r : 0) * a.in_features + (ok ? c : 0);
+      const bool ok = v < nvec && row0 + r < a.rows;
+      const int64_t o = static_cast<int64_t>(ok ? row0 + r : 0) * a.in_features + (ok ? c : 0);
       gv[i] = ok ? *reinterpret_cast<const uint4*>(a.g + o) : make_uint4(0u, 0u, 0u, 0u);
       uv[i] = ok ? *reinterpret_cast<const uint4*>(a.u + o) : make_uint4(0u, 0u, 0u, 0u);
       sc[i] = (a.in_scale != nullptr && ok) ? *reinterpret_cast<const uint4*>(a.in_scale + c)
@@ -785,13 +787,13 @@ __global__ __launch_bounds__(kSgThreads) void backbone_swiglu_kernel(SwigluBackb
       }
     }
   }
-  // acc[rt][v] = hidden[16 rt + 4 kg + v][128 cg + 16 w + i16]
+  // acc[rt][v] = hidden[row0 + 16 rt + 4 kg + v][128 cg + 16 w + i16]
   if (col < a.rank) {
 #pragma unroll
     for (int rt = 0; rt < TT; ++rt) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int r = 16 * rt + 4 * kg + v;
+        const int r = row0 + 16 * rt + 4 * kg + v;
         if (r >= a.rows) continue;
         if (a.slices == 1) {
           bb_store(BackboneProj{a.sv, a.out, a.in_scale, a.out_hi, a.split}, a.rank, r, col, f2h_bits(acc[rt][v]));
@@ -1225,8 +1227,12 @@ extern "C" int tris_backbone_linear_pair_scatter(const uint16_t* x, int32_t toke
 }
 
 // More than kSgMaxRowTiles 16-row tiles take the tiled GEMM with the product formed in its operand staging.
+// The tiled GEMM above one row group of the decode kernel, except for a rank that is not a multiple of 512 up to
+// kSgMaxRowGroups row groups (its 512-column tiles would be partial): the decode kernel's row groups there.
 static bool swiglu_backbone_gemm(int rows, int in_features, int rank) {
-  return rows > kSgMaxRowTiles * 16 && rank % kBgN == 0 && in_features % kBgK == 0;
+  if (rows <= kSgMaxRowTiles * 16) return false;
+  if (rank % 512 != 0 && rows <= kSgMaxRowGroups * kSgMaxRowTiles * 16) return false;
+  return rank % kBgN == 0 && in_features % kBgK == 0;
 }
 
 extern "C" int64_t tris_backbone_swiglu_workspace_bytes(int32_t rows, int32_t in_features, int32_t rank) {
@@ -1247,7 +1253,7 @@ static int swiglu_linear(const uint16_t* gate, const uint16_t* up, int32_t rows,
   if (rows == 0 || rank == 0) return TRIS_OK;
   TRIS_REQUIRE(in_features > 0 && in_features % 32 == 0, "%s: in_features %d must be a positive multiple of 32", who,
                in_features);
-  TRIS_REQUIRE(rows <= kSgMaxRowTiles * 16 || rank % kBgN == 0,
+  TRIS_REQUIRE(rows <= kSgMaxRowGroups * kSgMaxRowTiles * 16 || rank % kBgN == 0,
                "%s: %d rows need a rank that is a multiple of %d (rank %d)", who, rows, kBgN, rank);
   TRIS_REQUIRE(gate && up && sv && out, "%s: null pointer", who);
   TRIS_REQUIRE(reinterpret_cast<uintptr_t>(gate) % 16 == 0 && reinterpret_cast<uintptr_t>(up) % 16 == 0 &&
@@ -1261,7 +1267,7 @@ static int swiglu_linear(const uint16_t* gate, const uint16_t* up, int32_t rows,
   TRIS_REQUIRE(split >= 0 && split < rank && (split == 0 || out_hi != nullptr), "%s: column split %d of %d columns",
                who, split, rank);
   TRIS_REQUIRE(split == 0 || !swiglu_backbone_gemm(rows, in_features, rank),
-               "%s: a column split takes at most %d rows (the decode kernel)", who, kSgMaxRowTiles * 16);
+               "%s: a column split runs on the decode kernel, not on the tiled GEMM of %d rows", who, rows);
   if (swiglu_backbone_gemm(rows, in_features, rank)) {
     BackboneArgs ga{};
     ga.x = gate;
@@ -1276,9 +1282,12 @@ static int swiglu_linear(const uint16_t* gate, const uint16_t* up, int32_t rows,
   const int slice_k = swiglu_backbone_slice_k(in_features, rank, &slices);
   SwigluBackboneArgs a{gate, up, sv, in_scale, out, static_cast<float*>(workspace), rows, in_features, rank, slices,
                        slice_k, out_hi, split};
-  const int tt = ceil_div(rows, 16);
+  // past kSgMaxRowTiles row tiles, row groups of that many (blockIdx.z), each staging its own rows' product and
+  // reading the slice's SV again
+  const int tt = ceil_div(rows, 16) < kSgMaxRowTiles ? ceil_div(rows, 16) : kSgMaxRowTiles;
   const size_t lds = static_cast<size_t>(tt) * 16 * (slice_k + 8) * 2;
-  const dim3 grid(ceil_div(rank, kSgCols), slices);
+  TRIS_REQUIRE(lds <= 64 * 1024, "%s: %zu bytes of LDS for a %d-column slice", who, lds, slice_k);
+  const dim3 grid(ceil_div(rank, kSgCols), slices, ceil_div(rows, kSgMaxRowTiles * 16));
   switch (tt) {
     case 1: hipLaunchKernelGGL((backbone_swiglu_kernel<1>), grid, dim3(kSgThreads), lds, s, a); break;
     case 2: hipLaunchKernelGGL((backbone_swiglu_kernel<2>), grid, dim3(kSgThreads), lds, s, a); break;

@@ -1225,7 +1225,11 @@ def backbone_linear_pair_scatter(x: torch.Tensor, sv_a: torch.Tensor, sv_b: torc
     return out_a, out_b
 
 
-SWIGLU_BACKBONE_MAX_ROWS = 128  # rows of tris_backbone_swiglu_linear's decode kernel; more take the tiled GEMM
+SWIGLU_BACKBONE_MAX_ROWS = 128  # rows of one row group of tris_backbone_swiglu_linear's decode kernel
+# rows of its four row groups, for a rank that is not a multiple of 512 (a multiple takes the tiled GEMM above
+# SWIGLU_BACKBONE_MAX_ROWS); each group reads the projection again.  Measured on MI355X at the A3B shape (256
+# routed rows, in 512, rank 256): one launch in place of the SwiGLU product and a backbone launch
+SWIGLU_BACKBONE_GROUPED_MAX_ROWS = 512
 
 
 def backbone_swiglu_ok(gate: torch.Tensor, sv, in_scale: torch.Tensor | None = None) -> bool:
@@ -1237,9 +1241,12 @@ def backbone_swiglu_ok(gate: torch.Tensor, sv, in_scale: torch.Tensor | None = N
     if gate.dim() != 2 or int(gate.size(1)) % 32 != 0:
         return False
     rows, in_f, rank = int(gate.size(0)), int(gate.size(1)), int(sv.size(0))
-    # above the decode kernel's rows, the tiled GEMM's 128 x 512 tiles: a rank of 512s and enough workgroups
-    if rows > SWIGLU_BACKBONE_MAX_ROWS and (rank % 512 != 0 or rows < BACKBONE_GEMM_MIN_ROWS or _gemm_workgroups(
+    # above one row group of the decode kernel: a rank of 512s takes the tiled GEMM's 128 x 512 tiles (which need
+    # enough workgroups); any other rank, the decode kernel's row groups up to SWIGLU_BACKBONE_GROUPED_MAX_ROWS
+    if rows > SWIGLU_BACKBONE_MAX_ROWS and rank % 512 == 0 and (rows < BACKBONE_GEMM_MIN_ROWS or _gemm_workgroups(
             rows, in_f, rank, tile_m=128, tile_n=512, target=256) < BACKBONE_GEMM_MIN_WORKGROUPS // 2):
+        return False
+    if rows > SWIGLU_BACKBONE_GROUPED_MAX_ROWS and rank % 512 != 0:
         return False
     if int(sv.size(1)) != int(gate.size(1)) or sv.data_ptr() % 16 or gate.data_ptr() % 16:
         return False
@@ -1279,7 +1286,8 @@ def backbone_swiglu_linear_split(gate: torch.Tensor, up: torch.Tensor, sv: torch
                                  out_hi: torch.Tensor | None = None):
     """backbone_swiglu_linear of two stacked projections, its output split by columns
     (tris_backbone_swiglu_linear_split, an extension): returns (out [rows, split], out_hi [rows, rank - split]).
-    At most SWIGLU_BACKBONE_MAX_ROWS rows."""
+    On the decode kernel only: at most SWIGLU_BACKBONE_MAX_ROWS rows, or SWIGLU_BACKBONE_GROUPED_MAX_ROWS for a
+    rank that is not a multiple of 512."""
     _check_cuda("gate", gate, torch.float16, 2)
     _check_cuda("up", up, torch.float16, 2, gate.device)
     _check_cuda("shared_sv", sv, torch.float16, 2, gate.device)

@@ -227,11 +227,11 @@ def test_layer_with_router_backbone_launch_matches_oracle(tris, oracle_mod, cuda
 
 
 @pytest.mark.parametrize("rows,scaled", [(1, False), (16, True), (33, False), (64, True), (100, True), (128, False),
-                                         (600, False)])
+                                         (300, True), (600, False)])
 def test_backbone_swiglu_product_is_exact(tris, cuda, rows, scaled):
     """With SV the identity, the fused down backbone returns its operand: the product fp16(silu(g) * u)
-    (times the input scale) must be swiglu_mul's bits (one product per output, nothing rounds twice).  Above 128
-    rows the tiled GEMM forms the product in its operand staging."""
+    (times the input scale) must be swiglu_mul's bits (one product per output, nothing rounds twice).  At 300 rows
+    (rank 256) the decode kernel's three row groups form it, at 600 rows the tiled GEMM in its operand staging."""
     note(f"backbone swiglu identity rows={rows} scaled={scaled}")
     ext = tris["ext"]
     n = 256
@@ -248,7 +248,8 @@ def test_backbone_swiglu_product_is_exact(tris, cuda, rows, scaled):
 
 
 @pytest.mark.parametrize("rows,in_f,rank", [(32, 14336, 512), (16, 1024, 256), (64, 512, 128), (7, 4096, 64),
-                                             (128, 1024, 256), (300, 2048, 256), (600, 14336, 512), (1000, 1056, 128)])
+                                             (128, 1024, 256), (257, 512, 256), (300, 2048, 256), (512, 512, 192),
+                                             (600, 14336, 512), (1000, 1056, 128)])
 def test_backbone_swiglu_matches_unfused(tris, cuda, rows, in_f, rank, monkeypatch):
     """The fused down backbone against swiglu_mul followed by backbone_linear (below 512 rows the split over K
     differs, so the fp32 sums agree within rounding; from 512 rows both run the tiled GEMM with the same slices
@@ -261,17 +262,19 @@ def test_backbone_swiglu_matches_unfused(tris, cuda, rows, in_f, rank, monkeypat
     u = torch.from_numpy(rng.standard_normal((rows, in_f)).astype(np.float16)).to(cuda)
     sv = torch.from_numpy((rng.standard_normal((rank, in_f)) * 0.02).astype(np.float16)).to(cuda)
     sc = torch.from_numpy(rng.uniform(0.5, 1.5, in_f).astype(np.float16)).to(cuda)
-    # the layer's policy takes the fused form up to 128 rows and, above, for ranks of 512s (full-rank GEMM
-    # tiles); the C entry takes any rank of 128s
-    assert ext.backbone_swiglu_ok(g, sv, sc) == (rows <= 128 or (rows >= 512 and rank % 512 == 0))
+    # the layer's policy takes the fused form up to 128 rows, up to 512 rows for ranks that are not 512s (the decode
+    # kernel's row groups) and, from 512 rows, for ranks of 512s (full-rank GEMM tiles); the C entry takes any rank
+    # of 128s above
+    assert ext.backbone_swiglu_ok(g, sv, sc) == (rows <= 128 or (rows <= 512 and rank % 512 != 0)
+                                                 or (rows >= 512 and rank % 512 == 0))
     got = ext.backbone_swiglu_linear(g, u, sv, in_scale=sc)
     mlp = ext.swiglu_mul(g, u)
     unfused = ext.backbone_linear(mlp, sv, in_scale=sc)
     ref = ((mlp * sc).float() @ sv.float().t()).cpu().numpy()
     assert_close(got.float().cpu().numpy(), ref, "fused vs fp32")
     assert_close(got.float().cpu().numpy(), unfused.float().cpu().numpy(), "fused vs unfused")
-    if rows >= ext.BACKBONE_GEMM_MIN_ROWS:
-        assert torch.equal(got, unfused)
+    if rows >= ext.BACKBONE_GEMM_MIN_ROWS and (rank % 512 == 0 or rows > ext.SWIGLU_BACKBONE_GROUPED_MAX_ROWS):
+        assert torch.equal(got, unfused)  # both on the tiled GEMM
     again = ext.backbone_swiglu_linear(g, u, sv, in_scale=sc)
     assert torch.equal(got, again)  # slices added in fixed order
 
@@ -484,11 +487,12 @@ def test_backbone_column_split_matches_whole_projection(tris, cuda, tokens, in_f
         assert torch.equal(hi.view(torch.int16), full[:, split:].contiguous().view(torch.int16))
 
 
-@pytest.mark.parametrize("rows,in_f,rank,split", [(9, 512, 2304, 256), (40, 1024, 640, 512), (128, 512, 384, 128)])
+@pytest.mark.parametrize("rows,in_f,rank,split", [(9, 512, 2304, 256), (40, 1024, 640, 512), (128, 512, 384, 128),
+                                                   (288, 512, 2304, 256)])
 def test_backbone_swiglu_column_split_matches_whole_projection(tris, cuda, rows, in_f, rank, split):
     """tris_backbone_swiglu_linear_split (the routed down backbone and the shared expert's down projection as one
-    stacked projection) gives tris_backbone_swiglu_linear's columns [0, split) and [split, rank) bit for bit, and
-    rejects a split past the decode kernel's rows."""
+    stacked projection) gives tris_backbone_swiglu_linear's columns [0, split) and [split, rank) bit for bit (288
+    rows: three row groups of the decode kernel), and rejects a split on the tiled GEMM (513 rows)."""
     note(f"swiglu backbone column split rows={rows} in={in_f} rank={rank} split={split}")
     ext = tris["ext"]
     rng = np.random.default_rng(rows + rank)
@@ -499,7 +503,7 @@ def test_backbone_swiglu_column_split_matches_whole_projection(tris, cuda, rows,
     whole = ext.backbone_swiglu_linear(g, u, sv)
     assert torch.equal(lo.view(torch.int16), whole[:, :split].contiguous().view(torch.int16))
     assert torch.equal(hi.view(torch.int16), whole[:, split:].contiguous().view(torch.int16))
-    big = torch.zeros((ext.SWIGLU_BACKBONE_MAX_ROWS + 1, in_f), dtype=torch.float16, device=cuda)
+    big = torch.zeros((ext.SWIGLU_BACKBONE_GROUPED_MAX_ROWS + 1, in_f), dtype=torch.float16, device=cuda)
     with pytest.raises(RuntimeError, match="column split"):
         ext.backbone_swiglu_linear_split(big, big, sv, split)
 
