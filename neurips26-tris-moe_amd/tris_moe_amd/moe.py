@@ -293,7 +293,7 @@ class _SharedFold:
         f = cls()
         f.stack = stack
         f.wd = shared_expert[2]
-        f.split_down = R + T <= ext.SWIGLU_BACKBONE_MAX_ROWS and inter == n_mlp
+        f.split_down = R + T <= FOLD_SPLIT_DOWN_MAX_ROWS and inter == n_mlp
         dev = x16.device
         if f.split_down:
             f.g_all = torch.empty((R + T, n_mlp), dtype=torch.float16, device=dev)
@@ -428,6 +428,13 @@ FOLD_SHARED_EXPERT = True
 # staging adds them (ext.backbone_linear_deferred, ext.grouped_forward_block_gr_predecoded_partials): the same
 # bits without the reduction's launch.
 DOWN_PARTIALS_IN_GEMM = True
+# Stacked rows (routed + shared) up to which the folded shared expert's down projection runs as extra columns of the
+# routed down backbone's launch (tris_backbone_swiglu_linear_split); above, in launches of its own.  The decode
+# kernel's row groups would take up to 512, but the stacked product's unused quadrants (routed rows x the shared
+# columns) cost more than the two launches: measured on MI355X at the A3B shape, T = 32 134.5 against 133.8 us,
+# T = 48 156.1 against 152.5 us.
+FOLD_SPLIT_DOWN_MAX_ROWS = 128
+
 # One token on two experts (Mixtral at T = 1): the routed combine in the down GEMM's launch
 # (ext.grouped_forward_block_gr_predecoded_partials_combine), the combine launch's bits.
 COMBINE_IN_DOWN_GEMM = True
