@@ -14,7 +14,10 @@ constexpr int kBbWaves = 4;
 constexpr int kBbThreads = kBbWaves * kWave;
 constexpr int kBbKStep = 32;
 constexpr int kBbBatch = 8;          // K steps of loads in flight per wavefront
-constexpr int kBbTargetWgs = 512;    // aim for this many workgroups per launch
+constexpr int kBbTargetWgs = 256;    // aim for this many workgroups per launch (MI355X: 512 and 1024 were slower
+                                      // at the Mixtral decode shapes, 128 too at T <= 2)
+constexpr int kBbPacked4TargetWgs = 512;  // the 4-bit backbone, which dequantises in its loop (256: Mixtral T = 16
+                                          // step 108 -> 113 us)
 constexpr int kBbMaxSlices = 32;        // slices of backbone_kernel
 // the tiled GEMM for prefill-size batches (backbone_gemm_kernel, tris_backbone.hip)
 constexpr int kBgM = 256;            // rows of a workgroup tile
@@ -251,7 +254,8 @@ struct BackbonePlan {
   int slice_k;
 };
 BackbonePlan backbone_plan(int tokens, int in_features, int rank);
-int64_t backbone_workspace_bytes(int tokens, int in_features, int rank, int nproj, bool use_gemm = true);
+int64_t backbone_workspace_bytes(int tokens, int in_features, int rank, int nproj, bool use_gemm = true,
+                                 int target = kBbTargetWgs);
 bool backbone_gemm_fits(int tokens, int in_features, int rank);
 // Validates one launch's arguments (tokens, in_features and rank > 0) and fills args and plan.
 int backbone_prepare(const uint16_t* x, int tokens, int in_features, const int64_t* row_index, const uint16_t* sv_a,

@@ -55,11 +55,12 @@ static int backbone_token_group(int tokens) {
   return tiles < 4 ? tiles : 4;
 }
 
-int backbone_slices(int tokens, int in_features, int rank) {
+// target: the workgroups a launch aims at (kBbTargetWgs; the 4-bit backbone kBbPacked4TargetWgs).
+int backbone_slices(int tokens, int in_features, int rank, int target = kBbTargetWgs) {
   if (tokens <= 0 || in_features <= 0 || rank <= 0) return 1;
   const int64_t tiles =
       static_cast<int64_t>(ceil_div(ceil_div(tokens, 16), backbone_token_group(tokens))) * ceil_div(rank, 16);
-  int64_t slices = (kBbTargetWgs + tiles - 1) / tiles;
+  int64_t slices = (target + tiles - 1) / tiles;
   const int64_t max_by_k = ceil_div(in_features, kBbWaves * kBbKStep);
   if (slices > max_by_k) slices = max_by_k;
   if (slices > kBbMaxSlices) slices = kBbMaxSlices;
@@ -69,8 +70,8 @@ int backbone_slices(int tokens, int in_features, int rank) {
 static int backbone_gemm_slice_k(int tokens, int in_features, int rank, int* slices);
 
 // use_gemm: the entry may take the tiled GEMM for prefill-size batches (backbone_gemm_fits).
-int64_t backbone_workspace_bytes(int tokens, int in_features, int rank, int nproj, bool use_gemm) {
-  int slices = backbone_slices(tokens, in_features, rank);
+int64_t backbone_workspace_bytes(int tokens, int in_features, int rank, int nproj, bool use_gemm, int target) {
+  int slices = backbone_slices(tokens, in_features, rank, target);
   if (use_gemm && backbone_gemm_fits(tokens, in_features, rank)) backbone_gemm_slice_k(tokens, in_features, rank, &slices);
   return slices > 1 ? static_cast<int64_t>(nproj) * slices * tokens * rank * 4 : 0;
 }
@@ -1046,8 +1047,8 @@ int launch_packed4_backbone(const uint16_t* x, int tokens, const int64_t* row_in
   TRIS_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(in_scale_a) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(in_scale_b) % 16 == 0,
                "%s: x and in_scale must be 16-byte aligned", who);
-  const int slices = backbone_slices(tokens, in_features, rank);
-  const int64_t need = backbone_workspace_bytes(tokens, in_features, rank, nproj);
+  const int slices = backbone_slices(tokens, in_features, rank, kBbPacked4TargetWgs);
+  const int64_t need = backbone_workspace_bytes(tokens, in_features, rank, nproj, false, kBbPacked4TargetWgs);
   TRIS_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
                "%s: workspace of %lld bytes needed, %lld given", who, static_cast<long long>(need),
                static_cast<long long>(workspace_bytes));
@@ -1089,12 +1090,19 @@ int launch_packed4_backbone(const uint16_t* x, int tokens, const int64_t* row_in
 
 using namespace tris;
 
+// Enough for tris_backbone_linear[_pair] and for tris_packed4_backbone_linear[_pair], whose plan keeps more slices.
+static int64_t backbone_any_workspace_bytes(int tokens, int in_features, int rank, int nproj) {
+  const int64_t a = backbone_workspace_bytes(tokens, in_features, rank, nproj);
+  const int64_t b = backbone_workspace_bytes(tokens, in_features, rank, nproj, false, kBbPacked4TargetWgs);
+  return a > b ? a : b;
+}
+
 extern "C" int64_t tris_backbone_workspace_bytes(int32_t tokens, int32_t in_features, int32_t rank) {
-  return backbone_workspace_bytes(tokens, in_features, rank, 1);
+  return backbone_any_workspace_bytes(tokens, in_features, rank, 1);
 }
 
 extern "C" int64_t tris_backbone_pair_workspace_bytes(int32_t tokens, int32_t in_features, int32_t rank) {
-  return backbone_workspace_bytes(tokens, in_features, rank, 2);
+  return backbone_any_workspace_bytes(tokens, in_features, rank, 2);
 }
 
 extern "C" int tris_backbone_linear(const uint16_t* x, int32_t tokens, int32_t in_features, const int64_t* row_index,
@@ -1117,8 +1125,8 @@ extern "C" int tris_backbone_linear_deferred(const uint16_t* x, int32_t tokens, 
 // caller workspace, for callers that cannot allocate (code under HIP graph capture, tight serving loops).
 // It runs the workspace entry's plan (the same kernel and slice count for every shape, so the same bits).
 // The partial sums need slices * tokens * rank * 4 bytes.  On the decode-shaped kernel the slice count aims
-// at kBbTargetWgs workgroups of up to 64 x 16 outputs, which keeps that below 2 * 511 * 64 * 16 * 4 bytes
-// (just under 4 MiB) for every shape; the tiled GEMM of prefill-size batches (kBgMinRows rows on) can need
+// at kBbTargetWgs (256) workgroups of up to 64 x 16 outputs, which keeps that below 2 * 255 * 64 * 16 * 4 bytes
+// (about 2 MiB) for every shape; the tiled GEMM of prefill-size batches (kBgMinRows rows on) can need
 // more, and such shapes are rejected.  Every launch writes every partial sum it reads, so the array needs no
 // clearing between calls.
 constexpr int64_t kNoAllocScratchBytes = 4ll << 20;

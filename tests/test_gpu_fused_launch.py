@@ -61,7 +61,7 @@ def backbone_inputs(seed, tokens, in_f, rank, scales, dev):
 
 ROUTE_BB_CASES = [
     # tokens, experts, top_k, renormalize, in_features, rank, input scales
-    (1, 8, 2, True, 4096, 512, False),     # Mixtral decode: one-wavefront router, 16 slices
+    (1, 8, 2, True, 4096, 512, False),     # Mixtral decode: one-wavefront router, 8 slices
     (16, 8, 2, True, 4096, 512, True),     # with ns_mode 1 input scales
     (16, 64, 8, False, 2048, 256, False),  # workgroup router, one expert a lane
     (20, 60, 4, True, 1024, 128, False),   # two token tiles per backbone workgroup
@@ -510,7 +510,7 @@ def test_backbone_swiglu_column_split_matches_whole_projection(tris, cuda, rows,
 
 PARTIAL_CASES = [
     # rows per segment (expert id, rows), in_features, rank, outfeatures, input scale, every expert decoded
-    ([(3, 1), (6, 1)], 14336, 512, 256, False, False),   # Mixtral T = 1 down shape: 16 slices, one row a tile
+    ([(3, 1), (6, 1)], 14336, 512, 256, False, False),   # Mixtral T = 1 down shape: 8 slices, one row a tile
     ([(2, 4)], 4096, 512, 192, True, False),              # four rows in one segment, input scale
     ([(0, 2), (5, 1)], 4096, 128, 128, False, True),      # 32 slices (two load batches), slots by expert id
     ([(1, 2), (4, 2), (7, 1)], 1024, 256, 320, True, True),  # 8 slices
