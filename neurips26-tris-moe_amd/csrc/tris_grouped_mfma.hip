@@ -5,7 +5,8 @@
 // w[n,k] = s1 * fp16(C_j[k] * R_j[n,g]) with j = d if the split bit is set,
 // else nd, and s1 = +-1 from qweight1 (TriSMoE_cuda_kernel.cu:665-774); the
 // products are formed with packed fp16 multiplies (round to nearest even, as
-// __hmul).  The choice of j and the sign come from the bit planes as two
+// __hmul) on column factors staged negated (P_j = fp16(-C_j * R_j) = -fp16(C_j * R_j)
+// exactly).  The choice of j and the sign come from the bit planes as two
 // selector pairs sd, sn in {0, +1, -1}: w = fma(sd, P_d, sn * P_nd), exact
 // because one of the two terms is zero.  Salient columns (a few per cent,
 // w = fp16(+-fp16(C0*R0) +- fp16(C1*R1))) are zero in that operand and get
@@ -237,8 +238,8 @@ constexpr int mf_static_lds_bytes(int units, int rows, bool compact) {
 
 struct MfChunk {       // a unit's staged chunk
   uint16_t* xs;        // [rows][kMfXStride] activations, staged column order; column kMfChunk is zero (decode)
-  uint16_t* cds;       // C_d, staged column order (0 for salient columns)
-  uint16_t* cns;       // C_nd, staged column order (0 for salient columns)
+  uint16_t* cds;       // -C_d, staged column order (0 for salient columns)
+  uint16_t* cns;       // -C_nd, staged column order (0 for salient columns)
   // Weight-stationary kernel (natural column order):
   uint32_t* col_sal;   // C0 | C1 << 16, natural order
   uint16_t* sal_col;   // chunk column of the chunk's q-th salient column
@@ -436,8 +437,9 @@ __device__ __forceinline__ void mf_chunk_write(const MfmaProj& pa, int rc, int k
     const int bit = k & 31;
     const uint32_t cm = R.cmt[h];
     const bool sal = k < rank && ((cm >> bit) & 1u);
-    ch.cds[pj] = sal ? static_cast<uint16_t>(0) : static_cast<uint16_t>(R.cpv[h] >> 32);
-    ch.cns[pj] = sal ? static_cast<uint16_t>(0) : static_cast<uint16_t>(R.cpv[h] >> 48);
+    // staged negated (-C * R rounds to exactly -fp16(C * R)), so a set qweight1 bit is the selectors' sign bit
+    ch.cds[pj] = sal ? static_cast<uint16_t>(0) : static_cast<uint16_t>((R.cpv[h] >> 32) ^ 0x8000u);
+    ch.cns[pj] = sal ? static_cast<uint16_t>(0) : static_cast<uint16_t>((R.cpv[h] >> 48) ^ 0x8000u);
     if (natural) ch.col_sal[j] = static_cast<uint32_t>(R.cpv[h]);
     if (sal) {
       const int q = R.q2t[h] - R.sbase0 + __popc(cm & ((1u << bit) - 1u));
@@ -621,16 +623,17 @@ __device__ __forceinline__ void mf_wave_tile_issue(const MfmaProj& pa, int s, in
 // column n0 + 16 * wave + lane % 16 of x . W^T into acc.  xrow is the staged activation row this
 // lane's A operand reads.
 // Exact B operand of the lane's column for packed row j: the 8 weights k = kg + 4m.  Per packed row the
-// lane builds nibble selectors: bit 1 = this term is used, bit 3 = negative (shared by both terms; the
-// unused term is a signed zero); w = fma(sd, fp16(C_d * R_d), sn * fp16(C_nd * R_nd)).
+// lane builds nibble selectors: bit 1 = this term is used, bit 3 = the column's qweight1 bit (shared by both
+// terms; the unused term is a signed zero); with the staged factors negated, w = fma(sd, fp16(-C_d * R_d),
+// sn * fp16(-C_nd * R_nd)) is -fp16(C_j * R_j) where the bit is clear and +fp16(C_j * R_j) where it is set.
 __device__ __forceinline__ f16x8 mf_row_b(uint32_t qw, uint32_t gw, const uint4& cdv, const uint4& cnv, uint32_t rs2,
                                           uint32_t shl, uint32_t rot) {
   const f16x2 rd2 = u32_as_f16x2(__builtin_amdgcn_perm(rs2, rs2, 0x01000100u));
   const f16x2 rn2 = u32_as_f16x2(__builtin_amdgcn_perm(rs2, rs2, 0x03020302u));
   const uint32_t cd[4] = {cdv.x, cdv.y, cdv.z, cdv.w};
   const uint32_t cn[4] = {cnv.x, cnv.y, cnv.z, cnv.w};
-  const uint32_t neg3 = ~(qw << shl) & 0x88888888u;
-  const uint32_t sd = (__builtin_rotateright32(gw, rot) & 0x22222222u) | neg3;  // d term: fp4 +-1.0, else +-0
+  const uint32_t sgn3 = (qw << shl) & 0x88888888u;  // fp4 -1.0 on a negated factor where the bit is set
+  const uint32_t sd = (__builtin_rotateright32(gw, rot) & 0x22222222u) | sgn3;  // d term: fp4 +-1.0, else +-0
   const uint32_t sn = sd ^ 0x22222222u;                                        // nd term: the others
   uint32_t b[4];
 #pragma unroll
@@ -661,7 +664,7 @@ __device__ __forceinline__ f16x8 mf_row_b_nat(uint32_t qw, uint32_t gw, const ui
   const uint32_t cn[4] = {cnv.x, cnv.y, cnv.z, cnv.w};
   const uint32_t q4 = spread8(__builtin_amdgcn_ubfe(qw, 8u * kg, 8u));
   const uint32_t g4 = spread8(__builtin_amdgcn_ubfe(gw, 8u * kg, 8u));
-  const uint32_t sd = (g4 << 1) | ((q4 ^ 0x11111111u) << 3);  // d term: fp4 +-1.0, else +-0; bit 3 = negative
+  const uint32_t sd = (g4 << 1) | (q4 << 3);  // d term: fp4 +-1.0, else +-0; bit 3 = qweight1 (negated factors)
   const uint32_t sn = sd ^ 0x22222222u;                        // nd term: the others
   uint32_t b[4];
 #pragma unroll
