@@ -382,8 +382,9 @@ int tris_grouped_forward_block_gr_predecoded_experts(
  * [slices][batch][rank] as tris_backbone_linear_deferred leaves them; row r of the GEMM is fp16 of the slices'
  * sum added in slice order, the bits tris_backbone_linear writes, so the output equals the predecoded GEMM over
  * that projection's output bit for bit.  decoded: one slot per segment, or with decoded_by_expert != 0 one per
- * expert (as tris_grouped_forward_block_gr_predecoded_experts).  Requires the MFMA kernel's payload conditions
- * and rank <= 512 (else TRIS_ERR_INVALID); no output scale or bias is applied.
+ * expert (as tris_grouped_forward_block_gr_predecoded_experts).  Requires the MFMA kernel's payload conditions,
+ * rank <= 512 and batch <= 4 (the decode batches after the fused gate/up GEMM; else TRIS_ERR_INVALID); no output
+ * scale or bias is applied.
  */
 int tris_grouped_forward_block_gr_predecoded_partials(
     const float* partials, int32_t slices, int32_t batch, const int32_t* expert_ids, const int32_t* segment_offsets,

@@ -303,8 +303,8 @@ __device__ __forceinline__ uint32_t mf_hidden_voff(const MfmaProj& pa, int row0,
 // partial sums the activations are staged from them (mf_partials_stage): an empty resource, whose loads read zeros
 // without a memory access.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t mf_hidden_rsrc(const MfmaProj& pa, int row0, int rc, int rank,
-                                                                 uint32_t* bytes) {
-  if (pa.partials != nullptr) {
+                                                                 uint32_t* bytes, bool part = false) {
+  if (part) {
     *bytes = 0u;
     return make_rsrc(pa.partials, 0u);
   }
@@ -360,7 +360,7 @@ struct MfRegs {
 // branch around a load makes the compiler wait for it at the join); invalid lanes get an offset past
 // their buffer, which reads 0.
 __device__ __forceinline__ void mf_chunk_issue(const MfmaProj& pa, int e, int row0, int rc, int kc, int utid,
-                                               MfRegs& R) {
+                                               MfRegs& R, bool part = false) {
   const tris_compact3_payload& p = pa.p;
   const int rank = p.rank;
   const int wave = __builtin_amdgcn_readfirstlane(utid / kWave);  // wave-uniform
@@ -369,7 +369,7 @@ __device__ __forceinline__ void mf_chunk_issue(const MfmaProj& pa, int e, int ro
   const int pr0 = kc / 32;
   const int npr = (packed_rows - pr0) < kMfPR ? (packed_rows - pr0) : kMfPR;
   uint32_t hid_bytes;
-  const __amdgpu_buffer_rsrc_t r_hid = mf_hidden_rsrc(pa, row0, rc, rank, &hid_bytes);
+  const __amdgpu_buffer_rsrc_t r_hid = mf_hidden_rsrc(pa, row0, rc, rank, &hid_bytes, part);
   const uint32_t col_bytes = static_cast<uint32_t>(rank) * 8u;
   const __amdgpu_buffer_rsrc_t r_col = make_rsrc(p.col_pack3 + static_cast<int64_t>(e) * rank, col_bytes);
   const int32_t* cmap_e = p.c_map + static_cast<int64_t>(e) * packed_rows;
@@ -407,7 +407,8 @@ __device__ __forceinline__ void mf_chunk_issue(const MfmaProj& pa, int e, int ro
 // Write a unit's register-staged chunk to LDS (waits for those loads).  Salient columns get zero
 // C_d / C_nd, so the main pass gives them zero weights whatever their selector bits.
 __device__ __forceinline__ void mf_chunk_write(const MfmaProj& pa, int rc, int kc, int utid, const MfChunk& ch,
-                                               const MfRegs& R, bool natural = false, int sal_cap = kMfChunk) {
+                                               const MfRegs& R, bool natural = false, int sal_cap = kMfChunk,
+                                               bool part = false) {
   const tris_compact3_payload& p = pa.p;
   const int rank = p.rank;
   const int G = p.num_groups;
@@ -416,7 +417,7 @@ __device__ __forceinline__ void mf_chunk_write(const MfmaProj& pa, int rc, int k
 #pragma unroll
   for (int h = 0; h < kMfRuns; ++h) {
     const int r = 4 * h + wave;
-    if (r < rc && pa.partials == nullptr) {  // wave-uniform; partial sums are staged by mf_partials_stage
+    if (r < rc && !part) {  // wave-uniform; partial sums are staged by mf_partials_stage
       const int c = lane * 8;  // run start within the chunk (a multiple of 8)
       // columns c + b and c + b + 4 (b < 4) are neighbours in the staged order
       const uint32_t w[4] = {R.xv[h].x, R.xv[h].y, R.xv[h].z, R.xv[h].w};
@@ -1039,6 +1040,9 @@ void grouped_mfma_kernel(MfmaArgs a) {
   rc = __builtin_amdgcn_readfirstlane(rc);
   e = __builtin_amdgcn_readfirstlane(e);
   const int ds = a.decoded_by_expert ? e : s;  // the decoded bitmaps' slot
+  // activations from partial sums: only the 4-row instances carry that staging (the host sends at most 4 rows),
+  // so the others keep no register for it across their tile loop
+  const bool part = kRows == 4 && pa.partials != nullptr;
   const int ob_begin = ob_lo;
   const int ob_end = ob_hi;
   if (e < 0 || e >= p.num_experts) {  // rows routed to no expert: zero output
@@ -1059,9 +1063,9 @@ void grouped_mfma_kernel(MfmaArgs a) {
   {  // chunk 0 and the first tile's weights
     MfRegs regs;
     mf_wave_tile_issue<kCompact>(pa, ds, e, ob_begin, wo, lane, wave, tb0);
-    mf_chunk_issue(pa, e, row0, rc, 0, utid, regs);
-    mf_chunk_write(pa, rc, 0, utid, ch, regs, false, kSal);
-    if (pa.partials != nullptr) mf_partials_stage(pa, row0, rc, utid, ch);  // one chunk (host-checked)
+    mf_chunk_issue(pa, e, row0, rc, 0, utid, regs, part);
+    mf_chunk_write(pa, rc, 0, utid, ch, regs, false, kSal, part);
+    if (part) mf_partials_stage(pa, row0, rc, utid, ch);  // one chunk (host-checked)
     __builtin_amdgcn_s_waitcnt(0);  // LDS copies landed (all counters zero)
     __syncthreads();
   }
@@ -1728,6 +1732,7 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
     TRIS_REQUIRE(pb == nullptr && !swiglu && row_index == nullptr, "%s: partial sums feed one projection", who);
     TRIS_REQUIRE(pa->rank <= kMfChunk, "%s: partial sums need rank <= %d (one chunk)", who, kMfChunk);
     TRIS_REQUIRE(slices >= 1 && hidden_rows >= batch, "%s: bad partial-sum shape", who);
+    TRIS_REQUIRE(batch <= 4, "%s: partial sums take at most 4 rows (%d given)", who, batch);
     TRIS_REQUIRE(static_cast<int64_t>(slices) * hidden_rows * pa->rank * 4 < (int64_t{1} << 31),
                  "%s: partial sums exceed the 2 GiB limit", who);
   }

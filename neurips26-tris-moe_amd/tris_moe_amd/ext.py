@@ -1071,6 +1071,9 @@ def backbone_linear_deferred(x: torch.Tensor, sv: torch.Tensor, in_scale: torch.
     return BackbonePartials(part, n, rows, rank)
 
 
+PARTIALS_GEMM_MAX_ROWS = 4  # rows grouped_forward_block_gr_predecoded_partials takes (its 4-row kernel instances)
+
+
 def partials_gemm_ok(payload: dict) -> bool:
     """True when grouped_forward_block_gr_predecoded_partials takes a projection's payload dict: rank <= 512, a
     multiple of 64, and at most 8 row-scale groups (the MFMA kernel's staging of one chunk)."""
@@ -1089,6 +1092,8 @@ def grouped_forward_block_gr_predecoded_partials(hidden: BackbonePartials, exper
     output, bit for bit, without the reduction's launch."""
     if not isinstance(hidden, BackbonePartials):
         raise RuntimeError("grouped_forward_block_gr_predecoded_partials: hidden must be a BackbonePartials")
+    if hidden.rows > PARTIALS_GEMM_MAX_ROWS:
+        raise RuntimeError(f"grouped_forward_block_gr_predecoded_partials: at most {PARTIALS_GEMM_MAX_ROWS} rows")
     dev = hidden.partials.device
     _check_cuda("expert_ids", expert_ids, torch.int32, 1, dev)
     _check_cuda("segment_offsets", segment_offsets, torch.int32, 1, dev)

@@ -598,7 +598,8 @@ def _predecoded_moe_forward(x16, w16, route, payloads, backbones, num_experts, R
         with torch.cuda.stream(side):
             ext.ns_compensation_apply_(comp_d, mlp, eid, seg, ns["down"], accumulate=False)
     if hid_d is None:
-        if DOWN_PARTIALS_IN_GEMM and isinstance(backbones["down"], torch.Tensor) and ext.partials_gemm_ok(pd):
+        if (DOWN_PARTIALS_IN_GEMM and R <= ext.PARTIALS_GEMM_MAX_ROWS and isinstance(backbones["down"], torch.Tensor)
+                and ext.partials_gemm_ok(pd)):
             # the down backbone's split-K slices added by the down GEMM's staging (no reduction launch)
             hid_d = ext.backbone_linear_deferred(mlp, backbones["down"], in_scale=sc["down"])
         else:

@@ -513,7 +513,7 @@ PARTIAL_CASES = [
     ([(3, 1), (6, 1)], 14336, 512, 256, False, False),   # Mixtral T = 1 down shape: 8 slices, one row a tile
     ([(2, 4)], 4096, 512, 192, True, False),              # four rows in one segment, input scale
     ([(0, 2), (5, 1)], 4096, 128, 128, False, True),      # 32 slices (two load batches), slots by expert id
-    ([(1, 2), (4, 2), (7, 1)], 1024, 256, 320, True, True),  # 8 slices
+    ([(1, 2), (4, 1), (7, 1)], 1024, 256, 320, True, True),  # 3 segments, slots by expert id
     ([(5, 1)], 512, 64, 64, False, False),                # 4 slices
 ]
 
