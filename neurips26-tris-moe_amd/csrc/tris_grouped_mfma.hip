@@ -1164,16 +1164,10 @@ void grouped_mfma_kernel(MfmaArgs a) {
       }
       __syncthreads();  // exch is rewritten by the next tile
     } else {
-      const float scale = (nv && p.has_output_scale) ? h2f(p.output_scale[static_cast<int64_t>(e) * N + n]) : 1.0f;
-      const float bias = (nv && p.has_bias) ? h2f(p.bias[static_cast<int64_t>(e) * N + n]) : 0.0f;
+      // no output scale or bias here: the host sends none (launch_grouped_mfma rejects payloads with them)
       uint32_t hv[4];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        float x = acc[v];
-        if (p.has_output_scale) x = x * scale;
-        if (p.has_bias) x = x + bias;
-        hv[v] = f2h_bits(x);
-      }
+      for (int v = 0; v < 4; ++v) hv[v] = f2h_bits(acc[v]);
       held01 = hv[0] | (hv[1] << 16);
       held23 = hv[2] | (hv[3] << 16);
       held_ob = ob;
@@ -1719,6 +1713,8 @@ int launch_grouped_mfma(const uint16_t* hidden_a, const uint16_t* hidden_b, int 
     if (rc) return rc;
   }
   TRIS_REQUIRE(!swiglu || pb != nullptr, "%s: the fused SwiGLU needs two projections", who);
+  TRIS_REQUIRE(!pa->has_output_scale && !pa->has_bias && (!pb || (!pb->has_output_scale && !pb->has_bias)),
+               "%s: the MFMA GEMM applies no output scale or bias", who);
   if (batch == 0 || num_segments == 0) return TRIS_OK;
   TRIS_REQUIRE((hidden_a || partials) && out_a && expert_ids && segment_offsets && decoded_a, "%s: null pointer", who);
   if (comb_out != nullptr) {
